@@ -1,0 +1,442 @@
+// gx_api.hip - the C ABI of include/golem_hip.h: contexts, resident weights,
+// argument checking, and dispatch to the kernels.
+//
+// Misuse is reported with golem's own panic messages (nn/dot_q4_0.go:119,
+// nn/dot_q6_k.go:66-70, nn/batch.go:49-51, :75-77, :160-162,
+// nn/matrix.go:124, :137) so a shim can panic with them unchanged.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+
+#include "gx_internal.hpp"
+
+namespace {
+thread_local std::string g_error;
+}
+
+namespace gx {
+
+int fail(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_error = buf;
+    return code;
+}
+
+int check_launch(const char *what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+        return fail(GX_ERR_HIP, "%s: launch failed: %s", what, hipGetErrorString(e));
+    return GX_OK;
+}
+
+}  // namespace gx
+
+static int ok() {
+    g_error.clear();
+    return GX_OK;
+}
+
+static int use(gx_ctx *ctx) {
+    GX_CHECK(ctx != nullptr, "gx: no context");
+    GX_HIP(hipSetDevice(ctx->device));
+    return GX_OK;
+}
+
+extern "C" {
+
+const char *gx_last_error(void) { return g_error.c_str(); }
+
+int gx_init(int device, gx_ctx **out) {
+    GX_CHECK(out != nullptr, "gx: no place for the context");
+    int n = 0;
+    GX_HIP(hipGetDeviceCount(&n));
+    GX_CHECK(device >= 0 && device < n, "gx: device %d out of %d", device, n);
+    GX_HIP(hipSetDevice(device));
+    gx_ctx *ctx = new gx_ctx();
+    ctx->device = device;
+    ctx->stream = nullptr;
+    hipDeviceProp_t prop;
+    hipError_t e = hipGetDeviceProperties(&prop, device);
+    if (e != hipSuccess) {
+        delete ctx;
+        return gx::fail(GX_ERR_HIP, "hipGetDeviceProperties: %s", hipGetErrorString(e));
+    }
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        delete ctx;
+        return gx::fail(GX_ERR_UNSUPPORTED, "gx: built for gfx950, device %d is %s", device, prop.gcnArchName);
+    }
+    ctx->cu_count = prop.multiProcessorCount;
+    if (hipEventCreate(&ctx->t0) != hipSuccess || hipEventCreate(&ctx->t1) != hipSuccess) {
+        delete ctx;
+        return gx::fail(GX_ERR_HIP, "hipEventCreate failed");
+    }
+    *out = ctx;
+    return ok();
+}
+
+int gx_free(gx_ctx *ctx) {
+    if (ctx == nullptr)
+        return ok();
+    (void)hipSetDevice(ctx->device);
+    (void)hipEventDestroy(ctx->t0);
+    (void)hipEventDestroy(ctx->t1);
+    delete ctx;
+    return ok();
+}
+
+int gx_set_stream(gx_ctx *ctx, void *stream) {
+    if (int rc = use(ctx))
+        return rc;
+    ctx->stream = (hipStream_t)stream;
+    return ok();
+}
+
+int gx_sync(gx_ctx *ctx) {
+    if (int rc = use(ctx))
+        return rc;
+    GX_HIP(hipStreamSynchronize(ctx->stream));
+    return ok();
+}
+
+int gx_alloc(gx_ctx *ctx, size_t bytes, void **device) {
+    if (int rc = use(ctx))
+        return rc;
+    GX_CHECK(device != nullptr, "gx: no place for the pointer");
+    if (hipMalloc(device, bytes == 0 ? 1 : bytes) != hipSuccess)
+        return gx::fail(GX_ERR_NOMEM, "gx: cannot allocate %zu bytes", bytes);
+    return ok();
+}
+
+int gx_dealloc(gx_ctx *ctx, void *device) {
+    if (int rc = use(ctx))
+        return rc;
+    GX_HIP(hipFree(device));
+    return ok();
+}
+
+int gx_upload(gx_ctx *ctx, void *device, const void *host, size_t bytes) {
+    if (int rc = use(ctx))
+        return rc;
+    GX_HIP(hipMemcpyAsync(device, host, bytes, hipMemcpyHostToDevice, ctx->stream));
+    GX_HIP(hipStreamSynchronize(ctx->stream));
+    return ok();
+}
+
+int gx_download(gx_ctx *ctx, void *host, const void *device, size_t bytes) {
+    if (int rc = use(ctx))
+        return rc;
+    GX_HIP(hipMemcpyAsync(host, device, bytes, hipMemcpyDeviceToHost, ctx->stream));
+    GX_HIP(hipStreamSynchronize(ctx->stream));
+    return ok();
+}
+
+int gx_timer_start(gx_ctx *ctx) {
+    if (int rc = use(ctx))
+        return rc;
+    GX_HIP(hipEventRecord(ctx->t0, ctx->stream));
+    return ok();
+}
+
+int gx_timer_stop(gx_ctx *ctx, float *ms) {
+    if (int rc = use(ctx))
+        return rc;
+    GX_CHECK(ms != nullptr, "gx: no place for the time");
+    GX_HIP(hipEventRecord(ctx->t1, ctx->stream));
+    GX_HIP(hipEventSynchronize(ctx->t1));
+    GX_HIP(hipEventElapsedTime(ms, ctx->t0, ctx->t1));
+    return ok();
+}
+
+// ---- weights -------------------------------------------------------------
+
+static int weight_upload(gx_ctx *ctx, const void *data, size_t bytes, int on_device, int quant, int rows, int cols,
+                         int count, gx_weight **out) {
+    if (int rc = use(ctx))
+        return rc;
+    GX_CHECK(out != nullptr && data != nullptr, "gx: no weights");
+    GX_CHECK(rows > 0 && cols > 0 && count > 0, "nn: a matrix needs rows and columns");
+    size_t src_row = 0;
+    gx_weight w{};
+    w.ctx = ctx;
+    w.quant = quant;
+    w.rows = rows;
+    w.cols = cols;
+    w.count = count;
+    w.tiles = (rows + gx::kTileRows - 1) / gx::kTileRows;
+    switch (quant) {
+    case GX_Q4_0:
+        GX_CHECK(cols % gx::kQ4Block == 0, "nn: Q4_0 rows must be a multiple of the block size");
+        w.blocks = cols / gx::kQ4Block;
+        w.dchunks = (w.blocks + 7) / 8;
+        w.plane0_bytes = (size_t)w.tiles * w.blocks * gx::kTileRows * gx::kChunk;
+        w.matrix_bytes = w.plane0_bytes + (size_t)w.tiles * w.dchunks * gx::kTileRows * gx::kChunk;
+        src_row = (size_t)w.blocks * gx::kQ4BlockBytes;
+        break;
+    case GX_Q6_K:
+        GX_CHECK(cols % gx::kSuper == 0, "nn: Q6_K rows must be a multiple of the superblock size");
+        w.blocks = cols / gx::kSuper;
+        w.dchunks = (w.blocks + 7) / 8;
+        w.plane0_bytes = (size_t)w.tiles * w.blocks * gx::kQ6Chunks * gx::kTileRows * gx::kChunk;
+        w.matrix_bytes = w.plane0_bytes + (size_t)w.tiles * w.dchunks * gx::kTileRows * gx::kChunk;
+        src_row = (size_t)w.blocks * gx::kQ6BlockBytes;
+        break;
+    case GX_F32:
+        w.blocks = cols;
+        w.plane0_bytes = (size_t)rows * cols * 4;
+        w.matrix_bytes = w.plane0_bytes;
+        src_row = (size_t)cols * 4;
+        break;
+    default:
+        return gx::fail(GX_ERR_UNSUPPORTED, "nn: quant %d is not a matrix format this build multiplies", quant);
+    }
+    const size_t need = src_row * rows * count;
+    GX_CHECK(bytes >= need, "gx: %zu bytes given, a %dx%d matrix (x%d) needs %zu", bytes, rows, cols, count, need);
+
+    gx_weight *wp = new gx_weight(w);
+    if (hipMalloc(&wp->dev, wp->matrix_bytes * count) != hipSuccess) {
+        delete wp;
+        return gx::fail(GX_ERR_NOMEM, "gx: cannot allocate %zu bytes for weights", w.matrix_bytes * count);
+    }
+    int rc = GX_OK;
+    if (quant == GX_F32) {
+        hipError_t e = hipMemcpyAsync(wp->dev, data, need, on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,
+                                      ctx->stream);
+        if (e != hipSuccess)
+            rc = gx::fail(GX_ERR_HIP, "weight copy: %s", hipGetErrorString(e));
+    } else {
+        // Stage the GGUF bytes on the device and repack them there.
+        const uint8_t *src = (const uint8_t *)data;
+        uint8_t *staged = nullptr;
+        if (!on_device) {
+            if (hipMalloc(&staged, need) != hipSuccess) {
+                (void)hipFree(wp->dev);
+                delete wp;
+                return gx::fail(GX_ERR_NOMEM, "gx: cannot allocate %zu bytes to stage weights", need);
+            }
+            hipError_t e = hipMemcpyAsync(staged, data, need, hipMemcpyHostToDevice, ctx->stream);
+            if (e != hipSuccess)
+                rc = gx::fail(GX_ERR_HIP, "weight copy: %s", hipGetErrorString(e));
+            src = staged;
+        }
+        if (rc == GX_OK) {
+            hipError_t e = hipMemsetAsync(wp->dev, 0, wp->matrix_bytes * count, ctx->stream);
+            if (e != hipSuccess)
+                rc = gx::fail(GX_ERR_HIP, "weight clear: %s", hipGetErrorString(e));
+        }
+        if (rc == GX_OK)
+            rc = gx::launch_repack(ctx, src, wp);
+        if (staged) {
+            hipError_t e = hipStreamSynchronize(ctx->stream);
+            if (e != hipSuccess && rc == GX_OK)
+                rc = gx::fail(GX_ERR_HIP, "weight repack: %s", hipGetErrorString(e));
+            (void)hipFree(staged);
+        }
+    }
+    if (rc == GX_OK) {
+        hipError_t e = hipStreamSynchronize(ctx->stream);
+        if (e != hipSuccess)
+            rc = gx::fail(GX_ERR_HIP, "weight upload: %s", hipGetErrorString(e));
+    }
+    if (rc != GX_OK) {
+        (void)hipFree(wp->dev);
+        delete wp;
+        return rc;
+    }
+    *out = wp;
+    return ok();
+}
+
+int gx_weight_upload(gx_ctx *ctx, const void *data, size_t bytes, int on_device, int quant, int rows, int cols,
+                     gx_weight **out) {
+    return weight_upload(ctx, data, bytes, on_device, quant, rows, cols, 1, out);
+}
+
+int gx_weight_upload_stack(gx_ctx *ctx, const void *data, size_t bytes, int on_device, int quant, int rows,
+                           int cols, int count, gx_weight **out) {
+    return weight_upload(ctx, data, bytes, on_device, quant, rows, cols, count, out);
+}
+
+int gx_weight_free(gx_weight *w) {
+    if (w == nullptr)
+        return ok();
+    (void)hipSetDevice(w->ctx->device);
+    (void)hipFree(w->dev);
+    delete w;
+    return ok();
+}
+
+int gx_weight_info(const gx_weight *w, int *quant, int *rows, int *cols, int *count, size_t *device_bytes) {
+    GX_CHECK(w != nullptr, "gx: no weights");
+    if (quant)
+        *quant = w->quant;
+    if (rows)
+        *rows = w->rows;
+    if (cols)
+        *cols = w->cols;
+    if (count)
+        *count = w->count;
+    if (device_bytes)
+        *device_bytes = w->matrix_bytes * w->count;
+    return ok();
+}
+
+int gx_weight_rows(gx_ctx *ctx, const gx_weight *w, int expert, const int32_t *ids, int n, float *out) {
+    if (int rc = use(ctx))
+        return rc;
+    GX_CHECK(w != nullptr && ids != nullptr && out != nullptr, "gx: missing argument");
+    GX_CHECK(expert >= 0 && expert < w->count, "gx: expert %d out of %d", expert, w->count);
+    GX_CHECK(n >= 0, "gx: negative row count");
+    if (n == 0)
+        return ok();
+    if (int rc = gx::launch_rows(ctx, w, expert, ids, n, out))
+        return rc;
+    return ok();
+}
+
+// ---- activations ---------------------------------------------------------
+
+int gx_quantize_q8_0(gx_ctx *ctx, const float *x, int ldx, int M, int K, int8_t *q, float *scales, int32_t *qsum,
+                     float *corr) {
+    if (int rc = use(ctx))
+        return rc;
+    GX_CHECK(K % gx::kQ4Block == 0 && K > 0, "nn: activation length must be a multiple of the block size");
+    GX_CHECK(M >= 0 && ldx >= K, "gx: bad batch shape M=%d ldx=%d K=%d", M, ldx, K);
+    GX_CHECK(x && q && scales && qsum, "gx: missing argument");
+    if (M == 0)
+        return ok();
+    if (int rc = gx::launch_quantize_q8_0(ctx, x, ldx, M, K, q, scales, qsum, corr))
+        return rc;
+    return ok();
+}
+
+int gx_quantize_q8_k(gx_ctx *ctx, const float *x, int ldx, int M, int K, int8_t *q, float *kscales,
+                     int16_t *bsums) {
+    if (int rc = use(ctx))
+        return rc;
+    GX_CHECK(K % gx::kSuper == 0 && K > 0, "nn: the Q8_K form needs a multiple of the superblock size");
+    GX_CHECK(M >= 0 && ldx >= K, "gx: bad batch shape M=%d ldx=%d K=%d", M, ldx, K);
+    GX_CHECK(x && q && kscales && bsums, "gx: missing argument");
+    GX_CHECK(((uintptr_t)x & 15) == 0 && ldx % 4 == 0 && ((uintptr_t)q & 3) == 0,
+             "gx: the Q8_K quantiser needs x 16-byte aligned, ldx a multiple of 4 and q 4-byte aligned");
+    if (M == 0)
+        return ok();
+    if (int rc = gx::launch_quantize_q8_k(ctx, x, ldx, M, K, q, kscales, bsums))
+        return rc;
+    return ok();
+}
+
+// ---- products ------------------------------------------------------------
+
+static int check_product(const gx_weight *w, int quant, int M, int row_start, int row_end, const void *y, int ldy) {
+    GX_CHECK(w != nullptr, "gx: no weights");
+    GX_CHECK(w->quant == quant, "gx: a %s product was asked of a matrix of quant %d",
+             quant == GX_Q4_0 ? "Q4_0" : quant == GX_Q6_K ? "Q6_K" : "F32", w->quant);
+    GX_CHECK(M >= 0, "gx: negative batch");
+    GX_CHECK(row_start >= 0 && row_start <= row_end && row_end <= w->rows, "nn: rows [%d,%d) out of %d", row_start,
+             row_end, w->rows);
+    GX_CHECK(y != nullptr || M == 0, "gx: no output");
+    GX_CHECK(ldy >= row_end || M <= 1, "gx: ldy %d shorter than row %d", ldy, row_end);
+    return GX_OK;
+}
+
+static int q4_0_product(gx_ctx *ctx, const gx_weight *w, int expert, const int8_t *q, const float *scales,
+                        const int32_t *qsum, int M, int row_start, int row_end, const float *bias, float *y,
+                        int ldy) {
+    if (int rc = use(ctx))
+        return rc;
+    if (int rc = check_product(w, GX_Q4_0, M, row_start, row_end, y, ldy))
+        return rc;
+    GX_CHECK(expert >= 0 && expert < w->count, "gx: expert %d out of %d", expert, w->count);
+    GX_CHECK(q && scales && qsum, "nn: a Q4_0 product needs the activation in its Q8_0 form");
+    GX_CHECK(((uintptr_t)q & 15) == 0, "gx: q must be 16-byte aligned");
+    if (M == 0 || row_start == row_end)
+        return ok();
+    const uint8_t *mat = w->dev + (size_t)expert * w->matrix_bytes;
+    int rc = M <= 8 ? gx::launch_q4_0_matvec(ctx, w, mat, q, scales, qsum, M, row_start, row_end, bias, y, ldy)
+                    : gx::launch_q4_0_gemm(ctx, w, mat, q, scales, qsum, M, row_start, row_end, bias, y, ldy,
+                                           nullptr);
+    if (rc)
+        return rc;
+    return ok();
+}
+
+int gx_matmul_q4_0(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const float *scales, const int32_t *qsum,
+                   int M, int row_start, int row_end, const float *bias, float *y, int ldy) {
+    return q4_0_product(ctx, w, 0, q, scales, qsum, M, row_start, row_end, bias, y, ldy);
+}
+
+int gx_matmul_q4_0_expert(gx_ctx *ctx, const gx_weight *w, int expert, const int8_t *q, const float *scales,
+                          const int32_t *qsum, int M, int row_start, int row_end, float *y, int ldy) {
+    return q4_0_product(ctx, w, expert, q, scales, qsum, M, row_start, row_end, nullptr, y, ldy);
+}
+
+int gx_matmul_q6_k(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const float *kscales, const int16_t *bsums,
+                   int M, int row_start, int row_end, const float *bias, float *y, int ldy) {
+    if (int rc = use(ctx))
+        return rc;
+    if (int rc = check_product(w, GX_Q6_K, M, row_start, row_end, y, ldy))
+        return rc;
+    GX_CHECK(q && kscales && bsums, "nn: a Q6_K product needs the activation in its Q8_K form");
+    GX_CHECK(((uintptr_t)q & 15) == 0 && ((uintptr_t)bsums & 15) == 0, "gx: q and bsums must be 16-byte aligned");
+    if (M == 0 || row_start == row_end)
+        return ok();
+    if (int rc = gx::launch_q6_k_matvec(ctx, w, q, kscales, bsums, M, row_start, row_end, bias, y, ldy, nullptr))
+        return rc;
+    return ok();
+}
+
+int gx_matmul_f32(gx_ctx *ctx, const gx_weight *w, const float *x, int ldx, int M, int row_start, int row_end,
+                  float *y, int ldy) {
+    if (int rc = use(ctx))
+        return rc;
+    if (int rc = check_product(w, GX_F32, M, row_start, row_end, y, ldy))
+        return rc;
+    GX_CHECK(x != nullptr && ldx >= w->cols, "gx: bad activation");
+    if (M == 0 || row_start == row_end)
+        return ok();
+    if (int rc = gx::launch_f32_matvec(ctx, w, x, ldx, M, row_start, row_end, y, ldy))
+        return rc;
+    return ok();
+}
+
+int gx_q4_0_block_dots(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const int32_t *qsum, int M, int row_start,
+                       int row_end, int path, int32_t *out) {
+    if (int rc = use(ctx))
+        return rc;
+    if (int rc = check_product(w, GX_Q4_0, M, row_start, row_end, out, row_end))
+        return rc;
+    GX_CHECK(q && qsum, "gx: missing activation");
+    GX_CHECK(((uintptr_t)q & 15) == 0, "gx: q must be 16-byte aligned");
+    GX_CHECK(path == 0 || path == 1, "gx: path must be 0 (matrix-vector) or 1 (MFMA)");
+    if (M == 0 || row_start == row_end)
+        return ok();
+    int rc = path == 0 ? gx::launch_q4_0_block_dots_matvec(ctx, w, q, qsum, M, row_start, row_end, out)
+                       : gx::launch_q4_0_gemm(ctx, w, w->dev, q, nullptr, qsum, M, row_start, row_end, nullptr,
+                                              nullptr, 0, out);
+    if (rc)
+        return rc;
+    return ok();
+}
+
+int gx_q6_k_block_dots(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const int16_t *bsums, int M, int row_start,
+                       int row_end, int32_t *out) {
+    if (int rc = use(ctx))
+        return rc;
+    if (int rc = check_product(w, GX_Q6_K, M, row_start, row_end, out, row_end))
+        return rc;
+    GX_CHECK(q && bsums, "gx: missing activation");
+    GX_CHECK(((uintptr_t)q & 15) == 0 && ((uintptr_t)bsums & 15) == 0, "gx: q and bsums must be 16-byte aligned");
+    if (M == 0 || row_start == row_end)
+        return ok();
+    if (int rc = gx::launch_q6_k_matvec(ctx, w, q, nullptr, bsums, M, row_start, row_end, nullptr, nullptr, 0, out))
+        return rc;
+    return ok();
+}
+
+}  // extern "C"

@@ -1,0 +1,100 @@
+// gx_device.hpp - device helpers shared by the gfx950 kernels.
+#pragma once
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace gx {
+
+// fp16 -> fp32, exact (v_cvt_f32_f16; fp16 denormals are kept on gfx950).
+// The widening golem's halfToFloat does by hand (nn/dot_q4_0.go:21-43).
+__device__ __forceinline__ float half_bits_to_float(uint32_t h) {
+    return __half2float(__ushort_as_half((unsigned short)(h & 0xFFFFu)));
+}
+
+// fp32 -> fp16 bits, round to nearest even (v_cvt_f16_f32), golem's
+// floatToHalf (nn/half.go:8-38) on finite inputs.
+__device__ __forceinline__ uint32_t float_to_half_bits(float f) {
+    return (uint32_t)__half_as_ushort(__float2half_rn(f));
+}
+
+// The j-th of the eight fp16 values packed in a 16-byte chunk.
+__device__ __forceinline__ float chunk_half(const uint4 &c, int j) {
+    const uint32_t word = (j >> 1) == 0 ? c.x : (j >> 1) == 1 ? c.y : (j >> 1) == 2 ? c.z : c.w;
+    return half_bits_to_float((j & 1) ? (word >> 16) : word);
+}
+
+// golem's nearestInt (nn/batch.go:221-224): round half to even by adding
+// 1.5*2^23 and reading the low mantissa bits.
+__device__ __forceinline__ int32_t nearest_int(float f) {
+    const float s = f + 12582912.0f;
+    return (int32_t)(__float_as_uint(s) & 0x007fffffu) - 0x00400000;
+}
+
+// Four signed byte products added to c (v_dot4_i32_i8).
+__device__ __forceinline__ int32_t dot4(uint32_t a, uint32_t b, int32_t c) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+// The signed integer dot of one Q4_0 block against 32 int8 activations:
+// sum_j (n_j - 8) * q_j.  The nibble order is golem's (nn/dot_q4_0.go:5-8):
+// the low nibble of byte j is weight j, the high nibble weight j+16.  The
+// unsigned nibbles meet the activations in v_dot4 and the recentring is the
+// single term -8 * sum(q).
+__device__ __forceinline__ int32_t q4_0_block_isum(const uint4 &w, const int4 &a0, const int4 &a1, int32_t qsum) {
+    int32_t s = -8 * qsum;
+    s = dot4(w.x & 0x0F0F0F0Fu, (uint32_t)a0.x, s);
+    s = dot4(w.y & 0x0F0F0F0Fu, (uint32_t)a0.y, s);
+    s = dot4(w.z & 0x0F0F0F0Fu, (uint32_t)a0.z, s);
+    s = dot4(w.w & 0x0F0F0F0Fu, (uint32_t)a0.w, s);
+    s = dot4((w.x >> 4) & 0x0F0F0F0Fu, (uint32_t)a1.x, s);
+    s = dot4((w.y >> 4) & 0x0F0F0F0Fu, (uint32_t)a1.y, s);
+    s = dot4((w.z >> 4) & 0x0F0F0F0Fu, (uint32_t)a1.z, s);
+    s = dot4((w.w >> 4) & 0x0F0F0F0Fu, (uint32_t)a1.w, s);
+    return s;
+}
+
+// The integer of one Q6_K superblock against a Q8_K activation, golem's
+// sum - 32*shift (nn/dot_q6_k.go:31-51), restated group by group:
+// sum_g sc[g] * (sum_{k in g} q6_k * a_k - 32 * bsum[g]).  The 6-bit values
+// are assembled four bytes at a time from the ql/qh chunks.
+//   ql: 32 dwords (128 bytes), qh: 16 dwords (64 bytes), sc: 16 int8,
+//   a: 64 dwords (256 int8), bsum: 16 int16.
+__device__ __forceinline__ int32_t q6_k_block_isum(const uint32_t *ql, const uint32_t *qh, const uint4 &sc,
+                                                   const int4 *a, const int4 &bs0, const int4 &bs1) {
+    int32_t g[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++)
+        g[i] = 0;
+    const uint32_t *A = (const uint32_t *)a;
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const uint32_t L = ql[16 * h + k], L2 = ql[16 * h + 8 + k], H = qh[8 * h + k];
+            const uint32_t qa = (L & 0x0F0F0F0Fu) | ((H << 4) & 0x30303030u);
+            const uint32_t qb = (L2 & 0x0F0F0F0Fu) | ((H << 2) & 0x30303030u);
+            const uint32_t qc = ((L >> 4) & 0x0F0F0F0Fu) | (H & 0x30303030u);
+            const uint32_t qd = ((L2 >> 4) & 0x0F0F0F0Fu) | ((H >> 2) & 0x30303030u);
+            const int grp = k >> 2;
+            g[8 * h + 0 + grp] = dot4(qa, A[32 * h + k], g[8 * h + 0 + grp]);
+            g[8 * h + 2 + grp] = dot4(qb, A[32 * h + 8 + k], g[8 * h + 2 + grp]);
+            g[8 * h + 4 + grp] = dot4(qc, A[32 * h + 16 + k], g[8 * h + 4 + grp]);
+            g[8 * h + 6 + grp] = dot4(qd, A[32 * h + 24 + k], g[8 * h + 6 + grp]);
+        }
+    }
+    const uint32_t scw[4] = {sc.x, sc.y, sc.z, sc.w};
+    const uint32_t bsw[8] = {(uint32_t)bs0.x, (uint32_t)bs0.y, (uint32_t)bs0.z, (uint32_t)bs0.w,
+                             (uint32_t)bs1.x, (uint32_t)bs1.y, (uint32_t)bs1.z, (uint32_t)bs1.w};
+    int32_t isum = 0;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const int32_t s = (int32_t)(int8_t)(scw[i >> 2] >> (8 * (i & 3)));
+        const int32_t b = (int32_t)(int16_t)(bsw[i >> 1] >> (16 * (i & 1)));
+        isum += s * (g[i] - 32 * b);
+    }
+    return isum;
+}
+
+}  // namespace gx

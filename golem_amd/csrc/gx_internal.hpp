@@ -1,0 +1,97 @@
+// gx_internal.hpp - shared definitions of the gfx950 quantized-product library.
+//
+// Weight layout on the device ("R64").  A matrix's rows are cut into tiles of
+// 64 rows (the last tile padded with zero rows).  Within a tile every per-row
+// byte stream is cut into 16-byte chunks, and chunk j of the 64 rows is stored
+// as one contiguous kilobyte: chunk j of row r of tile t lives at
+//     plane + ((t * chunks_per_row + j) * 64 + r) * 16.
+// A wavefront whose lanes are 64 consecutive rows therefore reads 1 KiB of
+// contiguous memory with one 16-byte load per lane, and a lane that owns a row
+// walks that row's chunks 1 KiB apart.  The byte count equals the GGUF
+// layout's, apart from the padding rows and scale chunks.
+//
+//   Q4_0:  plane 0 = the 16 nibble bytes of each block (chunk j = block j),
+//          plane 1 = the fp16 block scales, 8 blocks per chunk.
+//   Q6_K:  plane 0 = per superblock 13 chunks: ql (8), qh (4), scales (1),
+//          plane 1 = the fp16 superblock scales, 8 superblocks per chunk.
+//   F32:   row-major floats, unchanged.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/golem_hip.h"
+
+namespace gx {
+
+constexpr int kTileRows = 64;
+constexpr int kChunk = 16;
+constexpr int kQ4Block = 32;      // nn/quant.go:50
+constexpr int kQ4BlockBytes = 18; // nn/quant.go:52
+constexpr int kSuper = 256;       // nn/quant.go:54
+constexpr int kQ6BlockBytes = 210;// nn/quant.go:56
+constexpr int kQ6Chunks = 13;     // ql 8 + qh 4 + scales 1
+// The blocks of one stretch: a row's products are summed within a stretch
+// first, then the stretch sums in order (the canonical order every Q4_0
+// kernel here follows).  Eight blocks is also one scale chunk.
+constexpr int kStretch = 8;
+
+int fail(int code, const char *fmt, ...);
+int check_launch(const char *what);
+
+}  // namespace gx
+
+struct gx_ctx {
+    int device;
+    hipStream_t stream;
+    hipEvent_t t0, t1;
+    int cu_count;
+};
+
+struct gx_weight {
+    gx_ctx *ctx;
+    int quant, rows, cols, count;
+    int tiles;           // ceil(rows / 64)
+    int blocks;          // Q4_0: cols/32; Q6_K: cols/256; F32: cols
+    int dchunks;         // ceil(blocks / 8)
+    size_t plane0_bytes; // per matrix
+    size_t matrix_bytes; // per matrix, both planes
+    uint8_t *dev;
+};
+
+#define GX_HIP(expr)                                                                          \
+    do {                                                                                      \
+        hipError_t e_ = (expr);                                                               \
+        if (e_ != hipSuccess)                                                                 \
+            return gx::fail(GX_ERR_HIP, "%s failed: %s", #expr, hipGetErrorString(e_));       \
+    } while (0)
+
+#define GX_CHECK(cond, ...)                                                                   \
+    do {                                                                                      \
+        if (!(cond))                                                                          \
+            return gx::fail(GX_ERR_INVALID, __VA_ARGS__);                                     \
+    } while (0)
+
+// ---- launchers implemented in the kernel files ---------------------------
+namespace gx {
+int launch_repack(gx_ctx *ctx, const uint8_t *src, gx_weight *w);
+int launch_rows(gx_ctx *ctx, const gx_weight *w, int expert, const int32_t *ids, int n, float *out);
+int launch_quantize_q8_0(gx_ctx *ctx, const float *x, int ldx, int M, int K, int8_t *q, float *scales,
+                         int32_t *qsum, float *corr);
+int launch_quantize_q8_k(gx_ctx *ctx, const float *x, int ldx, int M, int K, int8_t *q, float *kscales,
+                         int16_t *bsums);
+int launch_q4_0_matvec(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, const int8_t *q, const float *scales,
+                       const int32_t *qsum, int M, int row_start, int row_end, const float *bias, float *y,
+                       int ldy);
+int launch_q4_0_gemm(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, const int8_t *q, const float *scales,
+                     const int32_t *qsum, int M, int row_start, int row_end, const float *bias, float *y, int ldy,
+                     int32_t *dots);
+int launch_q4_0_block_dots_matvec(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const int32_t *qsum, int M,
+                                  int row_start, int row_end, int32_t *out);
+int launch_q6_k_matvec(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const float *kscales,
+                       const int16_t *bsums, int M, int row_start, int row_end, const float *bias, float *y,
+                       int ldy, int32_t *dots);
+int launch_f32_matvec(gx_ctx *ctx, const gx_weight *w, const float *x, int ldx, int M, int row_start, int row_end,
+                      float *y, int ldy);
+}  // namespace gx

@@ -1,0 +1,185 @@
+/*
+ * golem_hip.h - C ABI of the MI355X (gfx950) quantized linear-layer path.
+ *
+ * This is the boundary a cgo shim binds to replace golem's nn.Matrix /
+ * nn.Batch products (ThiraSoft/golem, package nn).  Every entry point takes
+ * plain pointers and sizes; no HIP or torch types cross it.  Pointers named
+ * "device" must point into device memory of the context's GPU (hipMalloc,
+ * gx_alloc, or a torch tensor's storage); "host" pointers are ordinary memory.
+ *
+ * Errors.  Every call returns GX_OK (0) or a status code, and leaves a message
+ * for gx_last_error() (thread-local).  Misuse that golem answers with a panic
+ * ("nn: ...") is GX_ERR_INVALID with the same wording, so a shim can panic
+ * with it unchanged.  Nothing falls back to a CPU path: a GPU failure is an
+ * error, never silent zeros.
+ *
+ * Streams.  All work of a context is enqueued on one stream (the null stream
+ * unless gx_set_stream chose another); calls return once it is enqueued.
+ * gx_sync waits for it.  A context is not meant to be driven by several host
+ * threads at once: golem serialises its parallel sections with a mutex
+ * (nn/parallel.go:163-191) and a shim does the same.
+ *
+ * Layouts on the device.
+ *   Q8_0 activations (golem's Batch.Q/Scales/Corr, nn/batch.go:17-27), one
+ *   token per row rather than golem's column interleave:
+ *     q      int8    [M][K]
+ *     scales float   [M][K/32]   the fp16-rounded scale, held as float
+ *     qsum   int32   [M][K/32]   sum of the block's 32 q values
+ *     corr   float   [M][K/32]   (8*scale)*float(qsum), golem's Corr (optional)
+ *   Q8_K activations (Batch.QK/KScales/BSums, nn/batch.go:29-32), same layout
+ *   as golem's:
+ *     q      int8    [M][K]
+ *     kscales float  [M][K/256]
+ *     bsums  int16   [M][K/16]
+ *   Outputs y are float [M][ldy]; a product over rows [row_start, row_end)
+ *   writes y[m*ldy + r] for r in that range and nothing else.
+ *   Weights are repacked on upload into a 64-row interleaved layout (see
+ *   gx_weight_upload); callers never address them directly.
+ */
+#ifndef GOLEM_HIP_H
+#define GOLEM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    GX_OK = 0,
+    GX_ERR_INVALID = 1,     /* misuse: golem panics with the same message */
+    GX_ERR_HIP = 2,         /* the HIP runtime reported an error */
+    GX_ERR_UNSUPPORTED = 3, /* a format or shape this build has no kernel for */
+    GX_ERR_NOMEM = 4        /* a device allocation failed */
+};
+
+/* Weight formats: the values of golem's nn.Quant (nn/quant.go:12-17). */
+enum { GX_F32 = 0, GX_BF16 = 1, GX_Q4_0 = 2, GX_Q6_K = 3 };
+
+typedef struct gx_ctx gx_ctx;
+typedef struct gx_weight gx_weight;
+
+/* ---- context --------------------------------------------------------- */
+
+/* The message of the last failing call on this thread ("" if none). */
+const char *gx_last_error(void);
+
+/* Opens a context on one GPU.  No counterpart in golem (it has no device);
+ * the shim calls it once where golem builds its worker pool
+ * (nn/parallel.go:59-72). */
+int gx_init(int device, gx_ctx **out);
+int gx_free(gx_ctx *ctx);
+
+/* Chooses the stream (a hipStream_t, or NULL for the null stream) the
+ * context enqueues on. */
+int gx_set_stream(gx_ctx *ctx, void *stream);
+/* Waits for everything enqueued on the context's stream. */
+int gx_sync(gx_ctx *ctx);
+
+/* Device memory for callers with no HIP runtime of their own (the cgo shim):
+ * allocate, free, and synchronous copies. */
+int gx_alloc(gx_ctx *ctx, size_t bytes, void **device);
+int gx_dealloc(gx_ctx *ctx, void *device);
+int gx_upload(gx_ctx *ctx, void *device, const void *host, size_t bytes);
+int gx_download(gx_ctx *ctx, void *host, const void *device, size_t bytes);
+
+/* Timing on the context's stream: gx_timer_start records an event,
+ * gx_timer_stop records another, waits for it and returns the milliseconds
+ * between the two. */
+int gx_timer_start(gx_ctx *ctx);
+int gx_timer_stop(gx_ctx *ctx, float *ms);
+
+/* ---- weights (nn.Matrix) -------------------------------------------- */
+
+/* Uploads one matrix of `rows` outputs by `cols` inputs, given in the GGUF
+ * block layout golem's Matrix.Data holds (nn/matrix.go:23-31): Q4_0 rows of
+ * cols/32 blocks of 18 bytes (nn/dot_q4_0.go:3-13), Q6_K rows of cols/256
+ * superblocks of 210 bytes (nn/dequant_q6_k.go:3-15), F32 row-major floats.
+ * `data` is host memory, or device memory when on_device is non-zero.  The
+ * quantized formats are repacked on the device into a 64-row interleaved
+ * layout of the same bytes (the role of Matrix.Repack, nn/matrix.go:40-46);
+ * the matrix stays resident until gx_weight_free.  Replaces Matrix{Data,
+ * Quant, Rows, Cols} plus Repack (nn/matrix.go:23-46).
+ * Errors as golem: cols not a multiple of 32 for Q4_0 (nn/dot_q4_0.go:119),
+ * of 256 for Q6_K (nn/dot_q6_k.go:66). */
+int gx_weight_upload(gx_ctx *ctx, const void *data, size_t bytes, int on_device, int quant, int rows, int cols,
+                     gx_weight **out);
+
+/* Uploads `count` matrices of the same shape stored back to back, as golem's
+ * gemma.ExpertStack (gemma/weights.go:59-72); expert i is the i-th matrix. */
+int gx_weight_upload_stack(gx_ctx *ctx, const void *data, size_t bytes, int on_device, int quant, int rows,
+                           int cols, int count, gx_weight **out);
+
+int gx_weight_free(gx_weight *w);
+
+/* Shape and the device bytes the resident copy occupies. */
+int gx_weight_info(const gx_weight *w, int *quant, int *rows, int *cols, int *count, size_t *device_bytes);
+
+/* Matrix.Row (nn/matrix.go:135-160): expands rows ids[0..n) of expert
+ * `expert` (0 for a single matrix) into out[n][cols] (device floats).  The
+ * embedding lookup of qwen/model.go:107-109 is this with n tokens. */
+int gx_weight_rows(gx_ctx *ctx, const gx_weight *w, int expert, const int32_t *ids_device, int n, float *out);
+
+/* ---- activations (nn.Batch) ------------------------------------------ */
+
+/* Batch.Quantize / QuantizeRange / QuantizeColumnRange (nn/batch.go:69-143)
+ * for M activations of K floats at x[m*ldx ...] (device).  corr may be NULL.
+ * K must be a multiple of 32 (nn/batch.go:49-51). */
+int gx_quantize_q8_0(gx_ctx *ctx, const float *x, int ldx, int M, int K, int8_t *q, float *scales, int32_t *qsum,
+                     float *corr);
+
+/* Batch.QuantizeK (nn/batch.go:159-213).  K must be a multiple of 256
+ * (nn/batch.go:160-162). */
+int gx_quantize_q8_k(gx_ctx *ctx, const float *x, int ldx, int M, int K, int8_t *q, float *kscales,
+                     int16_t *bsums);
+
+/* ---- products (Matrix.MatVec / MatVecBatch / MatVecRows) ------------ */
+
+/* y[m][r] = W[r] . x[m] (+ bias[r]) for the M activations of a Q8_0 batch and
+ * rows r in [row_start, row_end) of a Q4_0 matrix: Matrix.MatVecBatch and
+ * MatVecRows for Q4_0 (nn/matrix.go:78-104), and MatVecQ4_0
+ * (nn/dot_q4_0.go:117-124) when the range is all rows.  bias is NULL or
+ * rows floats (device).  M <= 8 runs the bandwidth-bound matrix-vector
+ * kernel; larger M runs the int8-MFMA product.  Both sum every row's blocks
+ * in the same order, so a column's result does not depend on M. */
+int gx_matmul_q4_0(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const float *scales, const int32_t *qsum,
+                   int M, int row_start, int row_end, const float *bias, float *y, int ldy);
+
+/* The same product with one expert of a stack (gemma's
+ * ExpertStack.At(expert).MatVecRows, gemma/moe.go:151-161). */
+int gx_matmul_q4_0_expert(gx_ctx *ctx, const gx_weight *w, int expert, const int8_t *q, const float *scales,
+                          const int32_t *qsum, int M, int row_start, int row_end, float *y, int ldy);
+
+/* y[m][r] = W[r] . x[m] (+ bias[r]) for a Q6_K matrix and a Q8_K batch:
+ * MatVecQ6_K and matVecQ6_KRows (nn/dot_q6_k.go:64-103), which include the
+ * two-column dotQ6_Kx2 (nn/dot_q6_k_amd64.go:14-20): one weight read serves
+ * all M <= 8 columns.  Bit-identical to golem's dotQ6_KGo. */
+int gx_matmul_q6_k(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const float *kscales, const int16_t *bsums,
+                   int M, int row_start, int row_end, const float *bias, float *y, int ldy);
+
+/* y[m][r] = DotF32(W[r], x[m]) for an F32 matrix (Matrix.rows' F32 case,
+ * nn/matrix.go:113-120), in the generic DotF32 order (nn/dot_f32.go:13-33):
+ * four interleaved accumulators, then (s0+s1)+(s2+s3). */
+int gx_matmul_f32(gx_ctx *ctx, const gx_weight *w, const float *x, int ldx, int M, int row_start, int row_end,
+                  float *y, int ldy);
+
+/* ---- per-block integers (parity instrumentation) --------------------- */
+
+/* The signed per-block integer each product uses, sum_j (n_j - 8) * q_j, for
+ * every (m, r, block): out[m][r - row_start][K/32] (device int32).  path 0 is
+ * the matrix-vector kernel's arithmetic, path 1 the MFMA product's.  golem's
+ * dotQ4_0Go accumulator (nn/dot_q4_0.go:58-63) is this plus 8*qsum. */
+int gx_q4_0_block_dots(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const int32_t *qsum, int M,
+                       int row_start, int row_end, int path, int32_t *out);
+
+/* dotQ6_KGo's per-superblock integer sum - 32*shift (nn/dot_q6_k.go:31-51)
+ * for every (m, r, superblock): out[m][r - row_start][K/256]. */
+int gx_q6_k_block_dots(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const int16_t *bsums, int M,
+                       int row_start, int row_end, int32_t *out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GOLEM_HIP_H */

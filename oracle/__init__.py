@@ -1,0 +1,324 @@
+"""Python handle on the oracle: golem's generic Go arithmetic restated in C
+(oracle/oracle.c), for checking the GPU path.
+
+TEST INFRASTRUCTURE ONLY: tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg are the only importers.  The product (golem_amd/) never
+imports it.
+
+Arrays are numpy; layouts are golem's nn.Batch (nn/batch.go:17-45):
+Q int8 [block][column][32], Scales/Corr [block][column], QK [column][width],
+KScales [column][width/256], BSums [column][width/16]; outputs [column][rows].
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+F32, BF16, Q4_0, Q6_K = 0, 1, 2, 3
+
+_lib = None
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def load():
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        from . import build
+        build.build(verbose=False)
+    lib = ctypes.CDLL(LIB_PATH)
+    I, F, V, S = ctypes.c_int, ctypes.c_float, ctypes.c_void_p, ctypes.c_size_t
+    sig = {
+        "orc_half_to_float": (F, [ctypes.c_uint16]),
+        "orc_float_to_half": (ctypes.c_uint16, [F]),
+        "orc_round_half": (F, [F]),
+        "orc_nearest_int": (ctypes.c_int32, [F]),
+        "orc_quantize_range": (I, [V, I, I, I, V, V, V, I, I]),
+        "orc_quantize_column_range": (None, [V, I, I, V, V, V, I, I, I]),
+        "orc_quantize_k": (I, [V, I, I, V, V, V]),
+        "orc_dot_q4_0_go": (None, [V, V, V, V, I, I, I, I, V]),
+        "orc_fold": (F, [V, F]),
+        "orc_mat_vec_q4_0_rows": (None, [V, V, V, V, I, I, I, V, I, I, I]),
+        "orc_dequantize_q4_0_row": (None, [V, I, V]),
+        "orc_packed_q4_0_bytes": (S, [I, I]),
+        "orc_pack_q4_0": (I, [V, I, I, V]),
+        "orc_dot_packed_q4_0_go": (None, [V, V, V, V, I, I, I, I, V]),
+        "orc_mat_vec_packed_q4_0_rows": (None, [V, V, V, V, I, I, I, V, I, I, I]),
+        "orc_q6_k_block_isum": (ctypes.c_int32, [V, V, V]),
+        "orc_q4_0_acc": (ctypes.c_int32, [V, V]),
+        "orc_dot_q6_k_go": (F, [V, V, V, V, I]),
+        "orc_mat_vec_q6_k_rows": (None, [V, V, V, V, I, I, I, V, I, I, I]),
+        "orc_dequantize_q6_k": (None, [V, I, V]),
+        "orc_dot_f32": (F, [V, V, I]),
+        "orc_matrix_rows": (I, [I, V, V, I, I, V, I, V, V, V, V, V, V, V, I, I, V, I, I, I]),
+        "orc_rms_norm_plain": (None, [V, I, V, F]),
+        "orc_gelu_table_build": (None, [V]),
+        "orc_gelu_table": (None, [V, I]),
+        "orc_expf": (F, [F]),
+        "orc_swiglu_range": (None, [V, V, I, I]),
+        "orc_softmax_in_place": (None, [V, I]),
+        "orc_axpy": (None, [V, V, I, F]),
+        "orc_choose_experts": (None, [V, I, I, V, V]),
+        "orc_route_one": (None, [V, I, V, V, I, I, F, V, V, V, V]),
+        "orc_expert_unit": (None, [V, V, V, I, I, V]),
+        "orc_expert_reduce": (None, [V, V, V, V, I, I, V]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+# ---- scalars --------------------------------------------------------------
+
+def half_to_float(h):
+    return load().orc_half_to_float(int(h))
+
+
+def float_to_half(f):
+    return load().orc_float_to_half(float(f))
+
+
+def nearest_int(f):
+    return load().orc_nearest_int(float(f))
+
+
+def expf(x):
+    return load().orc_expf(float(x))
+
+
+# ---- batches (nn.Batch) ---------------------------------------------------
+
+class Batch:
+    """golem's nn.Batch (nn/batch.go:17-66): F [size][width] float32 and the
+    Q8_0 form interleaved by column; QuantizeK adds the Q8_K form."""
+
+    def __init__(self, F):
+        F = np.ascontiguousarray(F, dtype=np.float32)
+        self.size, self.width = F.shape
+        if self.width % 32:
+            raise ValueError("nn: activation length must be a multiple of the block size")
+        self.stride = self.size
+        self.F = F
+        blocks = self.width // 32
+        self.Q = np.zeros(blocks * self.size * 32, dtype=np.int8)
+        self.Scales = np.zeros(blocks * self.size, dtype=np.float32)
+        self.Corr = np.zeros(blocks * self.size, dtype=np.float32)
+        self.QK = self.KScales = self.BSums = None
+
+    def quantize(self):
+        rc = load().orc_quantize_range(_p(self.F), self.width, self.size, self.stride, _p(self.Q),
+                                       _p(self.Scales), _p(self.Corr), 0, self.width)
+        assert rc == 0
+        return self
+
+    def quantize_k(self):
+        if self.width % 256:
+            raise ValueError("nn: the Q8_K form needs a multiple of the superblock size")
+        self.QK = np.zeros(self.size * self.width, dtype=np.int8)
+        self.KScales = np.zeros(self.size * self.width // 256, dtype=np.float32)
+        self.BSums = np.zeros(self.size * self.width // 16, dtype=np.int16)
+        rc = load().orc_quantize_k(_p(self.F), self.width, self.size, _p(self.QK), _p(self.KScales),
+                                   _p(self.BSums))
+        assert rc == 0
+        return self
+
+    # Views in the GPU's token-major layout.
+    def q_rows(self):
+        """Q as [size][width] (token-major)."""
+        b = self.width // 32
+        return self.Q.reshape(b, self.size, 32).transpose(1, 0, 2).reshape(self.size, self.width).copy()
+
+    def scales_rows(self):
+        b = self.width // 32
+        return self.Scales.reshape(b, self.size).T.copy()
+
+    def corr_rows(self):
+        b = self.width // 32
+        return self.Corr.reshape(b, self.size).T.copy()
+
+    def qsum_rows(self):
+        return self.q_rows().reshape(self.size, -1, 32).astype(np.int32).sum(axis=2).astype(np.int32)
+
+
+# ---- products -------------------------------------------------------------
+
+def mat_vec_q4_0_rows(w, batch, rows, start=0, end=None, ys=None):
+    """matVecQ4_0Rows with golem's generic kernels (row layout)."""
+    end = rows if end is None else end
+    if ys is None:
+        ys = np.full((batch.size, rows), np.nan, dtype=np.float32)
+    load().orc_mat_vec_q4_0_rows(_p(w), _p(batch.Q), _p(batch.Scales), _p(batch.Corr), batch.stride,
+                                 batch.size, batch.width, _p(ys), ys.shape[1], start, end)
+    return ys
+
+
+def pack_q4_0(w, rows, cols):
+    out = np.zeros(load().orc_packed_q4_0_bytes(rows, cols), dtype=np.uint8)
+    assert load().orc_pack_q4_0(_p(w), rows, cols, _p(out)) == 0
+    return out
+
+
+def mat_vec_packed_q4_0_rows(packed, batch, rows, start=0, end=None, ys=None):
+    end = rows if end is None else end
+    if ys is None:
+        ys = np.full((batch.size, rows), np.nan, dtype=np.float32)
+    load().orc_mat_vec_packed_q4_0_rows(_p(packed), _p(batch.Q), _p(batch.Scales), _p(batch.Corr),
+                                        batch.stride, batch.size, batch.width, _p(ys), ys.shape[1], start, end)
+    return ys
+
+
+def matrix_rows(quant, data, rows, cols, batch, start=0, end=None, packed=None, bias=None, ys=None):
+    """Matrix.rows (nn/matrix.go:94-131)."""
+    end = rows if end is None else end
+    if ys is None:
+        ys = np.full((batch.size, rows), np.nan, dtype=np.float32)
+    rc = load().orc_matrix_rows(quant, _p(data), _p(packed), rows, cols, _p(bias),
+                                0 if bias is None else len(bias), _p(batch.F), _p(batch.Q), _p(batch.Scales),
+                                _p(batch.Corr), _p(batch.QK), _p(batch.KScales), _p(batch.BSums), batch.stride,
+                                batch.size, _p(ys), ys.shape[1], start, end)
+    if rc != 0:
+        raise ValueError(f"nn: matrix_rows refused (status {rc})")
+    return ys
+
+
+def mat_vec_q6_k_rows(w, batch, rows, start=0, end=None, ys=None):
+    end = rows if end is None else end
+    if ys is None:
+        ys = np.full((batch.size, rows), np.nan, dtype=np.float32)
+    load().orc_mat_vec_q6_k_rows(_p(w), _p(batch.QK), _p(batch.KScales), _p(batch.BSums), batch.width,
+                                 batch.size, batch.width, _p(ys), ys.shape[1], start, end)
+    return ys
+
+
+def dequantize_q4_0_row(w_row, n):
+    out = np.zeros(n, dtype=np.float32)
+    load().orc_dequantize_q4_0_row(_p(np.ascontiguousarray(w_row)), n, _p(out))
+    return out
+
+
+def dequantize_q6_k(w_row, n):
+    out = np.zeros(n, dtype=np.float32)
+    load().orc_dequantize_q6_k(_p(np.ascontiguousarray(w_row)), n, _p(out))
+    return out
+
+
+def q4_0_block_acc(w, batch, rows):
+    """golem's per-block integer accumulator (unsigned nibbles) for every
+    (column, row, block): [size][rows][blocks] int32, computed in numpy from
+    the same bytes (the oracle's C loop states the same sum)."""
+    blocks = batch.width // 32
+    wb = w.reshape(rows, blocks, 18)
+    nib = wb[:, :, 2:]
+    lo = (nib & 0x0F).astype(np.int32)
+    hi = (nib >> 4).astype(np.int32)
+    wv = np.concatenate([lo, hi], axis=2)  # [rows][blocks][32]: weight j at index j
+    q = batch.q_rows().reshape(batch.size, blocks, 32).astype(np.int32)
+    return np.einsum("rbj,cbj->crb", wv, q, optimize=True).astype(np.int32)
+
+
+def q6_k_block_isum(w, batch, rows):
+    """dotQ6_KGo's per-superblock integer for every (column, row, superblock)
+    via the oracle's C restatement."""
+    nsb = batch.width // 256
+    lib = load()
+    out = np.zeros((batch.size, rows, nsb), dtype=np.int32)
+    wb = w.reshape(rows, nsb, 210)
+    for c in range(batch.size):
+        qk = batch.QK[c * batch.width:(c + 1) * batch.width]
+        bs = batch.BSums[c * batch.width // 16:(c + 1) * batch.width // 16]
+        for r in range(rows):
+            for b in range(nsb):
+                out[c, r, b] = lib.orc_q6_k_block_isum(_p(np.ascontiguousarray(wb[r, b])),
+                                                       _p(qk[b * 256:(b + 1) * 256]), _p(bs[b * 16:(b + 1) * 16]))
+    return out
+
+
+def dot_f32(a, b):
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    return load().orc_dot_f32(_p(a), _p(b), min(len(a), len(b)))
+
+
+def rms_norm_plain(x, gain=None, eps=1e-6):
+    x = np.array(x, dtype=np.float32)
+    g = None if gain is None else np.ascontiguousarray(gain, dtype=np.float32)
+    load().orc_rms_norm_plain(_p(x), len(x), _p(g), eps)
+    return x
+
+
+def gelu_table(x):
+    x = np.array(x, dtype=np.float32)
+    load().orc_gelu_table(_p(x), len(x))
+    return x
+
+
+def gelu_table_build():
+    t = np.zeros(1 << 16, dtype=np.float32)
+    load().orc_gelu_table_build(_p(t))
+    return t
+
+
+def softmax_in_place(x):
+    x = np.array(x, dtype=np.float32)
+    load().orc_softmax_in_place(_p(x), len(x))
+    return x
+
+
+def choose_experts(logits, used):
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    ids = np.zeros(used, dtype=np.int32)
+    weights = np.zeros(used, dtype=np.float32)
+    load().orc_choose_experts(_p(logits), len(logits), used, _p(ids), _p(weights))
+    return ids, weights
+
+
+def route_one(resid, router, used, eps=1e-6, router_scale=None):
+    resid = np.ascontiguousarray(resid, dtype=np.float32)
+    router = np.ascontiguousarray(router, dtype=np.float32)
+    experts, dim = router.shape
+    scratch = np.zeros(dim, dtype=np.float32)
+    logits = np.zeros(experts, dtype=np.float32)
+    ids = np.zeros(used, dtype=np.int32)
+    weights = np.zeros(used, dtype=np.float32)
+    rs = None if router_scale is None else np.ascontiguousarray(router_scale, dtype=np.float32)
+    load().orc_route_one(_p(resid), dim, _p(router), _p(rs), experts, used, eps, _p(scratch), _p(logits),
+                         _p(ids), _p(weights))
+    return logits, ids, weights
+
+
+def expert_unit(gate_up_w, down_w, x, dim, ffn):
+    partial = np.zeros(dim, dtype=np.float32)
+    load().orc_expert_unit(_p(np.ascontiguousarray(gate_up_w)), _p(np.ascontiguousarray(down_w)),
+                           _p(np.ascontiguousarray(x, dtype=np.float32)), dim, ffn, _p(partial))
+    return partial
+
+
+def expert_reduce(partials, ids, weights, dim, down_scale=None):
+    out = np.zeros(dim, dtype=np.float32)
+    ds = None if down_scale is None else np.ascontiguousarray(down_scale, dtype=np.float32)
+    load().orc_expert_reduce(_p(np.ascontiguousarray(partials, dtype=np.float32)),
+                             _p(np.ascontiguousarray(ids, dtype=np.int32)),
+                             _p(np.ascontiguousarray(weights, dtype=np.float32)), _p(ds), len(ids), dim, _p(out))
+    return out
+
+
+def compare_floats(got, want):
+    """golem's compareFloats (nn/quants_reference_test.go:96-120): the worst
+    absolute gap over RMS(want) + 1e-6.  Returns (relative, index)."""
+    got = np.asarray(got, dtype=np.float32).reshape(-1)
+    want = np.asarray(want, dtype=np.float32).reshape(-1)
+    assert got.shape == want.shape
+    scale = np.float32(np.sqrt(np.sum(want.astype(np.float64) ** 2) / len(want))) + np.float32(1e-6)
+    gaps = np.abs(got - want)
+    at = int(np.argmax(gaps))
+    return float(gaps[at] / scale), at

@@ -1,0 +1,171 @@
+"""The Q4_0 products against the oracle.
+
+Integers: every per-block sum the GPU uses equals golem's dotQ4_0Go
+accumulator minus 8*sum(q) (nn/dot_q4_0.go:58-63), for both the
+matrix-vector kernel and the MFMA product, bit for bit.
+Floats: golem's compareFloats bar (nn/quants_reference_test.go:96-120),
+max |got - want| / RMS(want) <= 1e-5, against both of golem's generic forms
+(row layout dotQ4_0Go and the 8-row packed dotPackedQ4_0Go) through
+Matrix.rows.  Determinism: a column's result is bit-identical whatever the
+batch (M = 1 .. 8 on the matrix-vector kernel, M > 8 on MFMA), golem's
+"batch == one at a time" (nn/dot_q4_0.go:143-146).
+"""
+import numpy as np
+import pytest
+
+from golem_amd import capi, synth
+from tests.gpu_util import log
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+
+
+def setup(dev, orc, rows, cols, M, seed):
+    g = synth.rng(seed)
+    w = synth.q4_0_weights(g, rows, cols)
+    x = synth.activations(g, M, cols)
+    b = orc.Batch(x).quantize()
+    wd = dev.weight(w, capi.Q4_0, rows, cols)
+    act = dev.quantize_q8_0(x, with_corr=False)
+    return w, b, wd, act
+
+
+def test_dequantized_rows_cover_every_half(dev, orc):
+    """Matrix.Row (dequantizeQ4_0Row, nn/matrix.go:175-190) bit for bit, over a
+    matrix whose block scales run through every finite fp16 pattern: pins the
+    device fp16 widening exhaustively."""
+    halves = np.array([h for h in range(1 << 16) if (h >> 10) & 0x1F != 0x1F], dtype=np.uint16)
+    cols = 256
+    blocks_per_row = cols // 32
+    rows = (len(halves) + blocks_per_row - 1) // blocks_per_row
+    g = synth.rng(1)
+    w = synth.q4_0_weights(g, rows, cols).reshape(-1, 18)
+    d = np.resize(halves, rows * blocks_per_row)
+    w[:, 0:2] = d.view(np.uint8).reshape(-1, 2)
+    w = w.reshape(-1)
+    wd = dev.weight(w, capi.Q4_0, rows, cols)
+    ids = np.arange(rows, dtype=np.int32)
+    got = dev.rows(wd, ids)
+    want = np.stack([orc.dequantize_q4_0_row(w[r * blocks_per_row * 18:(r + 1) * blocks_per_row * 18], cols)
+                     for r in range(rows)])
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("rows,cols,M", [(64, 256, 1), (200, 2560, 3), (96, 704, 9), (130, 2816, 40)])
+@pytest.mark.parametrize("path", [0, 1])
+def test_block_integers_bit_exact(dev, orc, rows, cols, M, path):
+    log(f"q4_0 block dots rows={rows} cols={cols} M={M} path={path}")
+    w, b, wd, act = setup(dev, orc, rows, cols, M, 100 + rows)
+    start, end = (0, rows) if rows < 100 else (5, rows - 3)
+    got = dev.q4_0_block_dots(wd, act, M, start, end, path)
+    acc = orc.q4_0_block_acc(w, b, rows)[:, start:end, :]
+    qsum = b.qsum_rows()[:, None, :]
+    np.testing.assert_array_equal(got, acc - 8 * qsum)
+
+
+def test_block_acc_oracle_agrees_with_c_loop(orc):
+    """The numpy per-block accumulator used above equals the oracle's C loop."""
+    g = synth.rng(5)
+    rows, cols = 3, 256
+    w = synth.q4_0_weights(g, rows, cols)
+    b = orc.Batch(synth.activations(g, 2, cols)).quantize()
+    acc = orc.q4_0_block_acc(w, b, rows)
+    q = b.q_rows()
+    wb = w.reshape(rows, cols // 32, 18)
+    import ctypes
+    lib = orc.load()
+    for c in range(2):
+        for r in range(rows):
+            for blk in range(cols // 32):
+                nib = np.ascontiguousarray(wb[r, blk, 2:])
+                qq = np.ascontiguousarray(q[c, blk * 32:(blk + 1) * 32])
+                v = lib.orc_q4_0_acc(nib.ctypes.data_as(ctypes.c_void_p), qq.ctypes.data_as(ctypes.c_void_p))
+                assert v == acc[c, r, blk]
+
+
+@pytest.mark.parametrize("rows,cols,M", [(9728, 2560, 1), (1024, 2560, 2), (2560, 9728, 1), (1408, 2816, 4),
+                                         (2816, 704, 8), (136, 4096, 5), (77, 256, 3)])
+def test_matvec_against_golem(dev, orc, rows, cols, M):
+    log(f"q4_0 matvec rows={rows} cols={cols} M={M}")
+    w, b, wd, act = setup(dev, orc, rows, cols, M, 200 + rows + M)
+    got = dev.get(dev.matmul_q4_0(wd, act, M))
+    row_form = orc.mat_vec_q4_0_rows(w, b, rows)
+    packed = orc.pack_q4_0(w, rows, cols)
+    packed_form = orc.matrix_rows(orc.Q4_0, w, rows, cols, b, packed=packed)
+    for c in range(M):
+        rel, at = orc.compare_floats(got[c], row_form[c])
+        assert rel <= TOL, f"column {c}: {rel:.3g} of RMS at row {at} (row layout)"
+        rel, at = orc.compare_floats(got[c], packed_form[c])
+        assert rel <= TOL, f"column {c}: {rel:.3g} of RMS at row {at} (packed)"
+
+
+@pytest.mark.parametrize("span", [(0, 130), (1, 129), (3, 11), (127, 130), (64, 128)])
+def test_row_ranges_and_bias(dev, orc, span):
+    """Only rows in [start, end) are written (pack_matvec_test.go:14 checks the
+    same with NaN sentinels), and the bias is added to those rows
+    (nn/matrix.go:126-130)."""
+    rows, cols, M = 130, 2080, 12
+    w, b, wd, act = setup(dev, orc, rows, cols, M, 300)
+    bias = synth.activations(synth.rng(301), 1, rows)[0]
+    start, end = span
+    for m in (1, 6, M):
+        log(f"range {span} M={m}")
+        bm = orc.Batch(b.F[:m]).quantize()
+        actm = dev.quantize_q8_0(b.F[:m], with_corr=False)
+        got = dev.get(dev.matmul_q4_0(wd, actm, m, start, end, bias=bias))
+        want = orc.matrix_rows(orc.Q4_0, w, rows, cols, bm, start, end, bias=bias)
+        assert np.all(np.isnan(got[:, :start])) and np.all(np.isnan(got[:, end:]))
+        assert not np.any(np.isnan(got[:, start:end]))
+        for c in range(m):
+            rel, at = orc.compare_floats(got[c, start:end], want[c, start:end])
+            assert rel <= TOL, f"column {c}: {rel:.3g} at {at}"
+
+
+@pytest.mark.parametrize("rows,cols", [(9728, 2560), (2560, 9728), (2816, 704), (200, 2816)])
+def test_batch_equals_one_at_a_time(dev, orc, rows, cols):
+    """Every column of a batch -- M in 1..8 on the matrix-vector kernel, larger
+    M on MFMA -- is bit-identical to the same column computed alone."""
+    M = 70
+    g = synth.rng(400 + rows)
+    w = synth.q4_0_weights(g, rows, cols)
+    x = synth.activations(g, M, cols)
+    wd = dev.weight(w, capi.Q4_0, rows, cols)
+    act = dev.quantize_q8_0(x, with_corr=False)
+    log(f"batch==alone rows={rows} cols={cols}")
+    whole = dev.get(dev.matmul_q4_0(wd, act, M))
+    for m in (1, 2, 3, 5, 8, 9, 33):
+        part = dev.get(dev.matmul_q4_0(wd, tuple(a[:m] for a in act[:3]), m))
+        np.testing.assert_array_equal(part.view(np.uint32), whole[:m].view(np.uint32))
+    for c in (0, 17, 69):
+        one = tuple(a[c:c + 1] for a in act[:3])
+        alone = dev.get(dev.matmul_q4_0(wd, one, 1))
+        np.testing.assert_array_equal(alone[0].view(np.uint32), whole[c].view(np.uint32))
+
+
+@pytest.mark.parametrize("M", [64, 512])
+def test_gemm_against_golem(dev, orc, M):
+    rows, cols = 9728, 2560
+    log(f"q4_0 gemm M={M}")
+    w, b, wd, act = setup(dev, orc, rows, cols, M, 500 + M)
+    got = dev.get(dev.matmul_q4_0(wd, act, M))
+    # The oracle on a sample of rows and columns (the whole product would take
+    # the scalar oracle minutes).
+    sel_rows = np.r_[0:64, 4000:4064, rows - 64:rows]
+    cols_sel = [0, 1, M // 2, M - 1]
+    sub = orc.Batch(b.F[cols_sel]).quantize()
+    wsub = w.reshape(rows, -1)[sel_rows].reshape(-1)
+    want = orc.mat_vec_q4_0_rows(wsub, sub, len(sel_rows))
+    for i, c in enumerate(cols_sel):
+        rel, at = orc.compare_floats(got[c, sel_rows], want[i])
+        assert rel <= TOL, f"column {c}: {rel:.3g} at {at}"
+
+
+def test_errors_are_golem_panics(dev):
+    g = synth.rng(9)
+    with pytest.raises(capi.GxError, match="multiple of the block size"):
+        dev.weight(synth.q4_0_weights(g, 4, 64), capi.Q4_0, 4, 48)
+    wd = dev.weight(synth.q4_0_weights(g, 4, 64), capi.Q4_0, 4, 64)
+    act = dev.quantize_q8_0(synth.activations(g, 1, 64), with_corr=False)
+    with pytest.raises(capi.GxError, match="out of"):
+        dev.matmul_q4_0(wd, act, 1, 0, 5)
