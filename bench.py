@@ -1,0 +1,236 @@
+"""Benchmark of golem's quantized linear-layer path on one MI355X.
+
+The headline workload is the benchmark's config 1: the Q6_K output head,
+151936 rows x 2560 inputs, batch 1.  One step is one pass of the path over
+one token: Q8_K-quantise the activation (Batch.QuantizeK) and run the Q6_K
+matrix-vector product (MatVecQ6_K) -- everything resident in HBM before the
+timed region.  `value` is algorithmic bytes per step (weights as stored +
+quantised activation + fp32 logits) over the step time, in GB/s.
+
+The weights rotate over two resident copies (640 MB together) so that no
+step finds the previous step's weights in the 256 MB Infinity Cache.
+
+Also reported, measured the same way with HIP events on the library's
+stream: config 0 (Q4_0 matvec 9728x2560, rotating over 20 copies = 281 MB)
+and config 2 (the Q4_0 x Q8_0 MFMA product at M = 64, 512, 2048).
+
+cpu_baseline: the oracle (golem's generic Go arithmetic restated in C,
+single-threaded) timed on this host over a bounded sample of config 1, and
+used at the same time to check the GPU's logits bit for bit.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, 8 TB/s
+INT8_PEAK_TOPS = 5000.0        # MI355X dense int8 MFMA, 5.0 POP/s
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--no-extra", action="store_true", help="skip the config 0 / config 2 measurements")
+    p.add_argument("--only", default="", help="profiling: run only this leg (c1, c0, c2) and exit")
+    return p.parse_args()
+
+
+def read_traffic(name):
+    """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE +
+    WRITE_SIZE, scaled by a copy kernel of known size), kept as a one-line
+    text summary under profiles/."""
+    path = os.path.join(ROOT, "profiles", name)
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":")[1].strip())
+    return None
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only; --gpus {args.gpus} is not supported by this build "
+              "(the path shards by output rows; see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from golem_amd import capi, synth
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    torch.cuda.init()
+    stream = torch.cuda.current_stream()
+    ctx = capi.Context(0, stream=stream.cuda_stream)
+    call = capi.call
+    vp = capi.vp
+
+    def dev(a):
+        return torch.from_numpy(np.ascontiguousarray(a).copy()).cuda()
+
+    # ---- config 1: Q6_K head, 151936 x 2560, M = 1, seed 1 ----------------
+    rows, cols = 151936, 2560
+    g = synth.rng(1)
+    w6 = synth.q6_k_weights(g, rows, cols)
+    x = synth.activations(g, 1, cols)
+    copies = [capi.Weight(ctx, w6, capi.Q6_K, rows, cols) for _ in range(2)]
+    xd = dev(x)
+    q = torch.empty((1, cols), dtype=torch.int8, device="cuda")
+    ks = torch.empty((1, cols // 256), dtype=torch.float32, device="cuda")
+    bs = torch.empty((1, cols // 16), dtype=torch.int16, device="cuda")
+    y = torch.empty((1, rows), dtype=torch.float32, device="cuda")
+    step_bytes = rows * (cols // 256) * 210 + cols + 4 * (cols // 256) + 2 * (cols // 16) + 4 * rows
+
+    def step(i):
+        call("gx_quantize_q8_k", ctx.ptr, vp(xd), cols, 1, cols, vp(q), vp(ks), vp(bs))
+        call("gx_matmul_q6_k", ctx.ptr, copies[i & 1].ptr, vp(q), vp(ks), vp(bs), 1, 0, rows, None, vp(y), rows)
+
+    if args.only in ("", "c1"):
+        for i in range(args.warmup):
+            step(i)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(args.steps):
+            step(i)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        ms_per_step = (t1 - t0) * 1e3 / args.steps
+        value = step_bytes / (ms_per_step * 1e-3) / 1e9
+
+        # The dominant kernel alone, timed with HIP events on the same stream.
+        reps = max(args.steps, 50)
+        ctx.timer_start()
+        for i in range(reps):
+            call("gx_matmul_q6_k", ctx.ptr, copies[i & 1].ptr, vp(q), vp(ks), vp(bs), 1, 0, rows, None, vp(y),
+                 rows)
+        kernel_ms = ctx.timer_stop() / reps
+        matvec_bytes = rows * (cols // 256) * 210 + cols + 4 * (cols // 256) + 2 * (cols // 16) + 4 * rows
+        achieved = matvec_bytes / (kernel_ms * 1e-3) / 1e9
+        if args.only == "c1":
+            print(json.dumps({"leg": "c1", "ms_per_step": ms_per_step, "kernel_ms": kernel_ms}))
+            return
+
+    # ---- config 0 and config 2 (secondary) --------------------------------
+    extra = {}
+    if not args.no_extra and args.only in ("", "c0", "c2"):
+        r0, c0 = 9728, 2560
+        g0 = synth.rng(0)
+        w0 = synth.q4_0_weights(g0, r0, c0)
+        x0 = synth.activations(g0, 1, c0)
+        if args.only in ("", "c0"):
+            n_copies = 20
+            w0s = [capi.Weight(ctx, w0, capi.Q4_0, r0, c0) for _ in range(n_copies)]
+            x0d = dev(x0)
+            q0 = torch.empty((1, c0), dtype=torch.int8, device="cuda")
+            s0 = torch.empty((1, c0 // 32), dtype=torch.float32, device="cuda")
+            qs0 = torch.empty((1, c0 // 32), dtype=torch.int32, device="cuda")
+            y0 = torch.empty((1, r0), dtype=torch.float32, device="cuda")
+            call("gx_quantize_q8_0", ctx.ptr, vp(x0d), c0, 1, c0, vp(q0), vp(s0), vp(qs0), None)
+            for i in range(20):
+                call("gx_matmul_q4_0", ctx.ptr, w0s[i % n_copies].ptr, vp(q0), vp(s0), vp(qs0), 1, 0, r0, None,
+                     vp(y0), r0)
+            reps = 400
+            ctx.timer_start()
+            for i in range(reps):
+                call("gx_matmul_q4_0", ctx.ptr, w0s[i % n_copies].ptr, vp(q0), vp(s0), vp(qs0), 1, 0, r0, None,
+                     vp(y0), r0)
+            ms0 = ctx.timer_stop() / reps
+            b0 = r0 * (c0 // 32) * 18 + c0 + 8 * (c0 // 32) + 4 * r0
+            extra["c0_q4_0_matvec"] = {"shape": [r0, c0], "M": 1, "kernel_us": round(ms0 * 1e3, 3),
+                                       "GB/s": round(b0 / (ms0 * 1e-3) / 1e9, 1),
+                                       "hbm_frac": round(b0 / (ms0 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                                       "bytes_per_launch": b0, "weight_copies": n_copies}
+            for w_ in w0s:
+                w_.free()
+            if args.only == "c0":
+                print(json.dumps(extra))
+                return
+        w0d = capi.Weight(ctx, w0, capi.Q4_0, r0, c0)
+        g2 = synth.rng(2)
+        for M in (64, 512, 2048):
+            x2 = synth.activations(g2, M, c0)
+            x2d = dev(x2)
+            q2 = torch.empty((M, c0), dtype=torch.int8, device="cuda")
+            s2 = torch.empty((M, c0 // 32), dtype=torch.float32, device="cuda")
+            qs2 = torch.empty((M, c0 // 32), dtype=torch.int32, device="cuda")
+            y2 = torch.empty((M, r0), dtype=torch.float32, device="cuda")
+            call("gx_quantize_q8_0", ctx.ptr, vp(x2d), c0, M, c0, vp(q2), vp(s2), vp(qs2), None)
+            for _ in range(5):
+                call("gx_matmul_q4_0", ctx.ptr, w0d.ptr, vp(q2), vp(s2), vp(qs2), M, 0, r0, None, vp(y2), r0)
+            reps = 50
+            ctx.timer_start()
+            for _ in range(reps):
+                call("gx_matmul_q4_0", ctx.ptr, w0d.ptr, vp(q2), vp(s2), vp(qs2), M, 0, r0, None, vp(y2), r0)
+            ms2 = ctx.timer_stop() / reps
+            ops = 2.0 * M * r0 * c0
+            tops = ops / (ms2 * 1e-3) / 1e12
+            by = r0 * (c0 // 32) * 18 + M * (c0 + 8 * (c0 // 32)) + 4 * M * r0
+            extra[f"c2_q4_0_gemm_m{M}"] = {"shape": [M, r0, c0], "kernel_us": round(ms2 * 1e3, 2),
+                                           "TOP/s": round(tops, 2), "int8_mfma_frac": round(tops / INT8_PEAK_TOPS, 4),
+                                           "GB/s": round(by / (ms2 * 1e-3) / 1e9, 1)}
+        w0d.free()
+        if args.only == "c2":
+            print(json.dumps(extra))
+            return
+
+    # ---- CPU baseline: the oracle on this host, and the check --------------
+    cpu = None
+    if not args.no_cpu:
+        import oracle
+        b = oracle.Batch(x).quantize_k()
+        passes = 3
+        t0 = time.perf_counter()
+        for _ in range(passes):
+            want = oracle.mat_vec_q6_k_rows(w6, b, rows)
+        t1 = time.perf_counter()
+        cpu_gbs = passes * step_bytes / (t1 - t0) / 1e9
+        step(0)  # recompute on copy 0 for the bit-for-bit check
+        torch.cuda.synchronize()
+        got = y.cpu().numpy()
+        exact = bool(np.array_equal(got.view(np.uint32), want.view(np.uint32)))
+        cpu = {"value": round(cpu_gbs, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+               "sample": f"{passes} full passes of config 1 (151936x2560 Q6_K, M=1) through the oracle's "
+                         f"dotQ6_KGo restatement, {t1 - t0:.2f} s",
+               "gpu_logits_bit_exact": exact}
+
+    traffic = read_traffic("q6_k_matvec_c1_traffic.txt")
+    out = {
+        "metric": "Q4_0/Q6_K matvec HBM GB/s (% of peak); decode tok/s, Qwen3-4B shape",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded PCG64; Q6_K weights and N(0,1) activations as config 1 specifies)",
+        "config": {"workload": "config 1: Q6_K output-head matvec 151936x2560, batch 1, Q8_K activation, "
+                               "quantise + product per step, weights rotating over 2 resident copies",
+                   "rows": rows, "cols": cols, "batch": 1, "seed": 1},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "kernel": "q6_k_matvec_kernel", "kernel_us": round(kernel_ms * 1e3, 3),
+                     "algorithmic_bytes_per_launch": matvec_bytes},
+        "cpu_baseline": cpu,
+        "configs": extra,
+    }
+    print(json.dumps(out))
+    for w_ in copies:
+        w_.free()
+    ctx.close()
+
+
+if __name__ == "__main__":
+    main()

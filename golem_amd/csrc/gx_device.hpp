@@ -59,17 +59,19 @@ __device__ __forceinline__ int32_t q4_0_block_isum(const uint4 &w, const int4 &a
 // sum - 32*shift (nn/dot_q6_k.go:31-51), restated group by group:
 // sum_g sc[g] * (sum_{k in g} q6_k * a_k - 32 * bsum[g]).  The 6-bit values
 // are assembled four bytes at a time from the ql/qh chunks.
-//   ql: 32 dwords (128 bytes), qh: 16 dwords (64 bytes), sc: 16 int8,
-//   a: 64 dwords (256 int8), bsum: 16 int16.
+//   ql: 32 dwords (128 bytes), qh: 16 dwords (64 bytes), sc: 16 int8 (per
+//   lane); a: 64 dwords (256 int8), bsum: 16 int16 (read where they lie, so a
+//   wavefront-uniform activation becomes scalar loads).
 __device__ __forceinline__ int32_t q6_k_block_isum(const uint32_t *ql, const uint32_t *qh, const uint4 &sc,
-                                                   const int4 *a, const int4 &bs0, const int4 &bs1) {
-    int32_t g[16];
-#pragma unroll
-    for (int i = 0; i < 16; i++)
-        g[i] = 0;
-    const uint32_t *A = (const uint32_t *)a;
+                                                   const uint32_t *__restrict__ A, const int16_t *__restrict__ bs) {
+    const uint32_t scw[4] = {sc.x, sc.y, sc.z, sc.w};
+    int32_t isum = 0;
 #pragma unroll
     for (int h = 0; h < 2; h++) {
+        int32_t g[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            g[i] = 0;
 #pragma unroll
         for (int k = 0; k < 8; k++) {
             const uint32_t L = ql[16 * h + k], L2 = ql[16 * h + 8 + k], H = qh[8 * h + k];
@@ -78,21 +80,17 @@ __device__ __forceinline__ int32_t q6_k_block_isum(const uint32_t *ql, const uin
             const uint32_t qc = ((L >> 4) & 0x0F0F0F0Fu) | (H & 0x30303030u);
             const uint32_t qd = ((L2 >> 4) & 0x0F0F0F0Fu) | ((H >> 2) & 0x30303030u);
             const int grp = k >> 2;
-            g[8 * h + 0 + grp] = dot4(qa, A[32 * h + k], g[8 * h + 0 + grp]);
-            g[8 * h + 2 + grp] = dot4(qb, A[32 * h + 8 + k], g[8 * h + 2 + grp]);
-            g[8 * h + 4 + grp] = dot4(qc, A[32 * h + 16 + k], g[8 * h + 4 + grp]);
-            g[8 * h + 6 + grp] = dot4(qd, A[32 * h + 24 + k], g[8 * h + 6 + grp]);
+            g[0 + grp] = dot4(qa, A[32 * h + k], g[0 + grp]);
+            g[2 + grp] = dot4(qb, A[32 * h + 8 + k], g[2 + grp]);
+            g[4 + grp] = dot4(qc, A[32 * h + 16 + k], g[4 + grp]);
+            g[6 + grp] = dot4(qd, A[32 * h + 24 + k], g[6 + grp]);
         }
-    }
-    const uint32_t scw[4] = {sc.x, sc.y, sc.z, sc.w};
-    const uint32_t bsw[8] = {(uint32_t)bs0.x, (uint32_t)bs0.y, (uint32_t)bs0.z, (uint32_t)bs0.w,
-                             (uint32_t)bs1.x, (uint32_t)bs1.y, (uint32_t)bs1.z, (uint32_t)bs1.w};
-    int32_t isum = 0;
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-        const int32_t s = (int32_t)(int8_t)(scw[i >> 2] >> (8 * (i & 3)));
-        const int32_t b = (int32_t)(int16_t)(bsw[i >> 1] >> (16 * (i & 1)));
-        isum += s * (g[i] - 32 * b);
+        for (int i = 0; i < 8; i++) {
+            const int gi = 8 * h + i;
+            const int32_t s = (int32_t)(int8_t)(scw[gi >> 2] >> (8 * (gi & 3)));
+            isum += s * (g[i] - 32 * (int32_t)bs[gi]);
+        }
     }
     return isum;
 }

@@ -14,70 +14,88 @@
 // golem sums the same integers with an unsigned nibble and a cancelling
 // correction term (nn/dot_q4_0.go:64-66); the two agree to rounding.
 //
-// Decomposition.  A workgroup owns RW consecutive rows and all stretches of
-// them; a lane is one (row, stretch-slot) pair.  Lanes of one slot read RW
-// consecutive rows' 16-byte chunks, which are contiguous in the R64 layout.
-// The stretch sums meet in LDS and one lane per row adds them in order.
+// Decomposition.  A workgroup owns one 64-row tile of the R64 layout; each
+// wavefront takes whole stretches, and a lane is one row of the tile.  The
+// wavefront's 16-byte loads of a stretch's chunks are 1 KiB contiguous, and
+// the activation of a stretch is the same for all 64 lanes, so it is read
+// with scalar loads into SGPRs and fed to v_dot4 from there: the vector
+// memory path carries weights only.  The stretch sums meet in LDS and one
+// wavefront adds them in order.
 #include "gx_device.hpp"
 #include "gx_internal.hpp"
 
 namespace gx {
 namespace {
 
-template <int RW, int NC>
+template <int NC>
 __global__ __launch_bounds__(1024) void q4_0_matvec_kernel(
     const uint8_t *__restrict__ W, size_t plane0_bytes, int B, int DC, const int8_t *__restrict__ q,
-    const float *__restrict__ scales, const int32_t *__restrict__ qsum, int K, int row_base, int row_start,
-    int row_end, const float *__restrict__ bias, float *__restrict__ y, int ldy, int nslots) {
-    extern __shared__ float part[];  // [S][NC][RW]
+    const float *__restrict__ scales, const int32_t *__restrict__ qsum, int K, int tile0, int row_start,
+    int row_end, const float *__restrict__ bias, float *__restrict__ y, int ldy) {
+    extern __shared__ float part[];  // [S][NC][64]
     const int S = (B + kStretch - 1) / kStretch;
-    const int tid = threadIdx.x;
-    const int r = tid % RW, slot = tid / RW;
-    const int row = row_base + blockIdx.x * RW + r;
-    const int tile = row >> 6, rr = row & 63;
-    const uint8_t *qs_row = W + ((size_t)tile * B * kTileRows + rr) * kChunk;
-    const uint8_t *d_row = W + plane0_bytes + ((size_t)tile * DC * kTileRows + rr) * kChunk;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nwaves = blockDim.x >> 6;
+    const int tile = tile0 + blockIdx.x;
+    const uint8_t *qs_row = W + ((size_t)tile * B * kTileRows + lane) * kChunk;
+    const uint8_t *d_row = W + plane0_bytes + ((size_t)tile * DC * kTileRows + lane) * kChunk;
 
-    if (slot < nslots) {
-        for (int s = slot; s < S; s += nslots) {
-            const int b0 = s * kStretch;
-            const int nb = min(kStretch, B - b0);
-            uint4 wq[kStretch];
+    for (int s = wave; s < S; s += nwaves) {
+        const int b0 = s * kStretch;
+        const int nb = min(kStretch, B - b0);
+        // Unconditional loads: past the last block a load repeats the last
+        // block (in bounds) and its product is skipped, so the compiler issues
+        // all nine loads back to back instead of one per guarded branch.
+        uint4 wq[kStretch];
 #pragma unroll
-            for (int j = 0; j < kStretch; j++)
-                if (j < nb)
-                    wq[j] = *(const uint4 *)(qs_row + (size_t)(b0 + j) * kTileRows * kChunk);
-            const uint4 dch = *(const uint4 *)(d_row + (size_t)s * kTileRows * kChunk);
-            float p[NC];
+        for (int j = 0; j < kStretch; j++)
+            wq[j] = *(const uint4 *)(qs_row + (size_t)min(b0 + j, B - 1) * kTileRows * kChunk);
+        const uint4 dch = *(const uint4 *)(d_row + (size_t)s * kTileRows * kChunk);
+        float p[NC];
 #pragma unroll
-            for (int c = 0; c < NC; c++)
-                p[c] = 0.0f;
+        for (int c = 0; c < NC; c++)
+            p[c] = 0.0f;
 #pragma unroll
-            for (int j = 0; j < kStretch; j++) {
-                if (j < nb) {
-                    const float dw = chunk_half(dch, j);
-                    const int b = b0 + j;
+        for (int c = 0; c < NC; c++) {
 #pragma unroll
-                    for (int c = 0; c < NC; c++) {
-                        const int4 *a = (const int4 *)(q + (size_t)c * K + (size_t)b * kQ4Block);
-                        const int32_t isum = q4_0_block_isum(wq[j], a[0], a[1], qsum[(size_t)c * B + b]);
-                        const float sc = dw * scales[(size_t)c * B + b];
+            for (int h = 0; h < 2; h++) {
+                // Four blocks' activation at a time, loaded before any use.
+                int4 a0[4], a1[4];
+                int32_t qs[4];
+                float sa[4];
+#pragma unroll
+                for (int jj = 0; jj < 4; jj++) {
+                    const int b = min(b0 + 4 * h + jj, B - 1);
+                    const int4 *a = (const int4 *)(q + (size_t)c * K + (size_t)b * kQ4Block);
+                    a0[jj] = a[0];
+                    a1[jj] = a[1];
+                    qs[jj] = qsum[(size_t)c * B + b];
+                    sa[jj] = scales[(size_t)c * B + b];
+                }
+#pragma unroll
+                for (int jj = 0; jj < 4; jj++) {
+                    const int j = 4 * h + jj;
+                    if (j < nb) {
+                        const int32_t isum = q4_0_block_isum(wq[j], a0[jj], a1[jj], qs[jj]);
+                        const float sc = chunk_half(dch, j) * sa[jj];
                         p[c] = fmaf((float)isum, sc, p[c]);
                     }
                 }
             }
-#pragma unroll
-            for (int c = 0; c < NC; c++)
-                part[(s * NC + c) * RW + r] = p[c];
         }
+#pragma unroll
+        for (int c = 0; c < NC; c++)
+            part[(s * NC + c) * kTileRows + lane] = p[c];
     }
     __syncthreads();
-    if (slot == 0 && row >= row_start && row < row_end) {
+    const int row = tile * kTileRows + lane;
+    if (wave == 0 && row >= row_start && row < row_end) {
 #pragma unroll
         for (int c = 0; c < NC; c++) {
             float acc = 0.0f;
             for (int s = 0; s < S; s++)
-                acc = acc + part[(s * NC + c) * RW + r];
+                acc = acc + part[(s * NC + c) * kTileRows + lane];
             if (bias)
                 acc = acc + bias[row];
             y[(size_t)c * ldy + row] = acc;
@@ -103,35 +121,20 @@ __global__ void q4_0_block_dots_kernel(const uint8_t *__restrict__ W, int B, con
     out[id] = q4_0_block_isum(w, a[0], a[1], qsum[(size_t)m * B + b]);
 }
 
-template <int RW, int NC>
-int launch_rw(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, const int8_t *q, const float *scales,
-              const int32_t *qsum, int row_start, int row_end, const float *bias, float *y, int ldy) {
-    const int B = w->blocks;
-    const int S = (B + kStretch - 1) / kStretch;
-    const int nslots = min(S, 1024 / RW);
-    const int threads = ((RW * nslots + 63) / 64) * 64;
-    const size_t lds = (size_t)S * NC * RW * sizeof(float);
-    GX_CHECK(lds <= 64 * 1024, "gx: a %d-input Q4_0 row is wider than this kernel's LDS", w->cols);
-    const int row_base = (row_start / RW) * RW;
-    const int grid = (row_end - row_base + RW - 1) / RW;
-    q4_0_matvec_kernel<RW, NC><<<grid, threads, lds, ctx->stream>>>(mat, w->plane0_bytes, B, w->dchunks, q, scales,
-                                                                     qsum, w->cols, row_base, row_start, row_end,
-                                                                     bias, y, ldy, nslots);
-    return check_launch("q4_0_matvec");
-}
-
 template <int NC>
 int launch_nc(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, const int8_t *q, const float *scales,
               const int32_t *qsum, int row_start, int row_end, const float *bias, float *y, int ldy) {
-    // Rows per workgroup: the widest that still gives every CU about two
-    // workgroups; narrower tiles spread a small matrix over more CUs.
-    const int rows = row_end - row_start;
-    const int want = 2 * ctx->cu_count;
-    if (rows / 32 >= want)
-        return launch_rw<32, NC>(ctx, w, mat, q, scales, qsum, row_start, row_end, bias, y, ldy);
-    if (rows / 16 >= want)
-        return launch_rw<16, NC>(ctx, w, mat, q, scales, qsum, row_start, row_end, bias, y, ldy);
-    return launch_rw<8, NC>(ctx, w, mat, q, scales, qsum, row_start, row_end, bias, y, ldy);
+    const int B = w->blocks;
+    const int S = (B + kStretch - 1) / kStretch;
+    const int waves = min(S, 16);
+    const size_t lds = (size_t)S * NC * kTileRows * sizeof(float);
+    GX_CHECK(lds <= 64 * 1024, "gx: a %d-input Q4_0 row is wider than this kernel's LDS", w->cols);
+    const int tile0 = row_start / kTileRows;
+    const int grid = (row_end + kTileRows - 1) / kTileRows - tile0;
+    q4_0_matvec_kernel<NC><<<grid, 64 * waves, lds, ctx->stream>>>(mat, w->plane0_bytes, B, w->dchunks, q, scales,
+                                                                   qsum, w->cols, tile0, row_start, row_end, bias, y,
+                                                                   ldy);
+    return check_launch("q4_0_matvec");
 }
 
 }  // namespace
@@ -140,9 +143,13 @@ int launch_q4_0_matvec(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, cons
                        const int32_t *qsum, int M, int row_start, int row_end, const float *bias, float *y,
                        int ldy) {
     // Columns in groups of 8, 4, 2, 1, each group reading the weights once;
-    // the per-column arithmetic is the same whatever the group.
+    // the per-column arithmetic is the same whatever the group.  Very wide
+    // rows keep the group narrow enough for the stretch sums to fit in LDS.
     int c = 0;
     const int K = w->cols, B = w->blocks;
+    const size_t per_column = (size_t)((B + kStretch - 1) / kStretch) * kTileRows * sizeof(float);
+    const int widest = per_column * 8 <= 64 * 1024 ? 8 : per_column * 4 <= 64 * 1024 ? 4
+                     : per_column * 2 <= 64 * 1024 ? 2 : 1;
     while (c < M) {
         const int left = M - c;
         const int8_t *qc = q + (size_t)c * K;
@@ -150,13 +157,13 @@ int launch_q4_0_matvec(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, cons
         const int32_t *qs = qsum + (size_t)c * B;
         float *yc = y + (size_t)c * ldy;
         int rc;
-        if (left >= 8) {
+        if (left >= 8 && widest >= 8) {
             rc = launch_nc<8>(ctx, w, mat, qc, sc, qs, row_start, row_end, bias, yc, ldy);
             c += 8;
-        } else if (left >= 4) {
+        } else if (left >= 4 && widest >= 4) {
             rc = launch_nc<4>(ctx, w, mat, qc, sc, qs, row_start, row_end, bias, yc, ldy);
             c += 4;
-        } else if (left >= 2) {
+        } else if (left >= 2 && widest >= 2) {
             rc = launch_nc<2>(ctx, w, mat, qc, sc, qs, row_start, row_end, bias, yc, ldy);
             c += 2;
         } else {

@@ -9,73 +9,69 @@
 // the weights, the role of dotQ6_Kx2 (nn/dot_q6_k_x2_amd64.s:64-154), and
 // give each column exactly its one-column result.
 //
-// Decomposition as the Q4_0 kernel: a workgroup owns RW rows, a lane one
-// (row, superblock-slot) pair; the superblock terms meet in LDS and one lane
-// per row adds them in order.
+// Decomposition as the Q4_0 kernel: a workgroup owns one 64-row tile, each
+// wavefront whole superblocks, a lane one row.  The activation of a
+// superblock is uniform across the wavefront and is read into SGPRs with
+// scalar loads; the superblock terms meet in LDS and one wavefront adds them
+// in order.
 #include "gx_device.hpp"
 #include "gx_internal.hpp"
 
 namespace gx {
 namespace {
 
-template <int RW, int NC>
+template <int NC>
 __global__ __launch_bounds__(1024) void q6_k_matvec_kernel(
     const uint8_t *__restrict__ W, size_t plane0_bytes, int B, int DC, const int8_t *__restrict__ q,
-    const float *__restrict__ kscales, const int16_t *__restrict__ bsums, int K, int row_base, int row_start,
-    int row_end, const float *__restrict__ bias, float *__restrict__ y, int ldy, int nslots,
-    int32_t *__restrict__ dots, int M) {
-    extern __shared__ float part[];  // [B][NC][RW]
-    const int tid = threadIdx.x;
-    const int r = tid % RW, slot = tid / RW;
-    const int row = row_base + blockIdx.x * RW + r;
-    const int tile = row >> 6, rr = row & 63;
-    const uint8_t *d_row = W + plane0_bytes + ((size_t)tile * DC * kTileRows + rr) * kChunk;
+    const float *__restrict__ kscales, const int16_t *__restrict__ bsums, int K, int tile0, int row_start,
+    int row_end, const float *__restrict__ bias, float *__restrict__ y, int ldy, int32_t *__restrict__ dots) {
+    extern __shared__ float part[];  // [B][NC][64]
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nwaves = blockDim.x >> 6;
+    const int tile = tile0 + blockIdx.x;
+    const int row = tile * kTileRows + lane;
+    const uint8_t *d_row = W + plane0_bytes + ((size_t)tile * DC * kTileRows + lane) * kChunk;
 
-    if (slot < nslots) {
-        for (int s = slot; s < B; s += nslots) {
-            const uint8_t *base = W + (((size_t)tile * B + s) * kQ6Chunks * kTileRows + rr) * kChunk;
-            uint32_t ql[32], qh[16];
+    for (int s = wave; s < B; s += nwaves) {
+        const uint8_t *base = W + (((size_t)tile * B + s) * kQ6Chunks * kTileRows + lane) * kChunk;
+        uint32_t ql[32], qh[16];
 #pragma unroll
-            for (int c = 0; c < 8; c++) {
-                const uint4 v = *(const uint4 *)(base + (size_t)c * kTileRows * kChunk);
-                ql[4 * c] = v.x, ql[4 * c + 1] = v.y, ql[4 * c + 2] = v.z, ql[4 * c + 3] = v.w;
-            }
+        for (int c = 0; c < 8; c++) {
+            const uint4 v = *(const uint4 *)(base + (size_t)c * kTileRows * kChunk);
+            ql[4 * c] = v.x, ql[4 * c + 1] = v.y, ql[4 * c + 2] = v.z, ql[4 * c + 3] = v.w;
+        }
 #pragma unroll
-            for (int c = 0; c < 4; c++) {
-                const uint4 v = *(const uint4 *)(base + (size_t)(8 + c) * kTileRows * kChunk);
-                qh[4 * c] = v.x, qh[4 * c + 1] = v.y, qh[4 * c + 2] = v.z, qh[4 * c + 3] = v.w;
-            }
-            const uint4 sc = *(const uint4 *)(base + (size_t)12 * kTileRows * kChunk);
-            const uint4 dch = *(const uint4 *)(d_row + (size_t)(s >> 3) * kTileRows * kChunk);
-            const float d = chunk_half(dch, s & 7);
+        for (int c = 0; c < 4; c++) {
+            const uint4 v = *(const uint4 *)(base + (size_t)(8 + c) * kTileRows * kChunk);
+            qh[4 * c] = v.x, qh[4 * c + 1] = v.y, qh[4 * c + 2] = v.z, qh[4 * c + 3] = v.w;
+        }
+        const uint4 sc = *(const uint4 *)(base + (size_t)12 * kTileRows * kChunk);
+        const float d = half_bits_to_float(*(const uint16_t *)(d_row + (size_t)(s >> 3) * kTileRows * kChunk +
+                                                              (size_t)(s & 7) * 2));
 #pragma unroll
-            for (int c = 0; c < NC; c++) {
-                const int4 *a = (const int4 *)(q + (size_t)c * K + (size_t)s * kSuper);
-                int4 av[16];
-#pragma unroll
-                for (int i = 0; i < 16; i++)
-                    av[i] = a[i];
-                const int4 *bsp = (const int4 *)(bsums + (size_t)c * (K / 16) + (size_t)s * 16);
-                const int32_t isum = q6_k_block_isum(ql, qh, sc, av, bsp[0], bsp[1]);
-                if (dots) {
-                    if (row >= row_start && row < row_end)
-                        dots[((size_t)c * (row_end - row_start) + (row - row_start)) * B + s] = isum;
-                } else {
-                    const float t0 = (float)isum * d;
-                    part[(s * NC + c) * RW + r] = t0 * kscales[(size_t)c * B + s];
-                }
+        for (int c = 0; c < NC; c++) {
+            const uint32_t *a = (const uint32_t *)(q + (size_t)c * K + (size_t)s * kSuper);
+            const int16_t *bs = bsums + (size_t)c * (K / 16) + (size_t)s * 16;
+            const int32_t isum = q6_k_block_isum(ql, qh, sc, a, bs);
+            if (dots) {
+                if (row >= row_start && row < row_end)
+                    dots[((size_t)c * (row_end - row_start) + (row - row_start)) * B + s] = isum;
+            } else {
+                const float t0 = (float)isum * d;
+                part[(s * NC + c) * kTileRows + lane] = t0 * kscales[(size_t)c * B + s];
             }
         }
     }
     if (dots)
         return;
     __syncthreads();
-    if (slot == 0 && row >= row_start && row < row_end) {
+    if (wave == 0 && row >= row_start && row < row_end) {
 #pragma unroll
         for (int c = 0; c < NC; c++) {
             float total = 0.0f;
             for (int s = 0; s < B; s++)
-                total = total + part[(s * NC + c) * RW + r];
+                total = total + part[(s * NC + c) * kTileRows + lane];
             if (bias)
                 total = total + bias[row];
             y[(size_t)c * ldy + row] = total;
@@ -83,32 +79,19 @@ __global__ __launch_bounds__(1024) void q6_k_matvec_kernel(
     }
 }
 
-template <int RW, int NC>
-int launch_rw(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const float *kscales, const int16_t *bsums,
-              int row_start, int row_end, const float *bias, float *y, int ldy, int32_t *dots) {
-    const int B = w->blocks;
-    const int nslots = min(B, 1024 / RW);
-    const int threads = ((RW * nslots + 63) / 64) * 64;
-    const size_t lds = dots ? 0 : (size_t)B * NC * RW * sizeof(float);
-    GX_CHECK(lds <= 64 * 1024, "gx: a %d-input Q6_K row is wider than this kernel's LDS", w->cols);
-    const int row_base = (row_start / RW) * RW;
-    const int grid = (row_end - row_base + RW - 1) / RW;
-    q6_k_matvec_kernel<RW, NC><<<grid, threads, lds, ctx->stream>>>(w->dev, w->plane0_bytes, B, w->dchunks, q,
-                                                                     kscales, bsums, w->cols, row_base, row_start,
-                                                                     row_end, bias, y, ldy, nslots, dots, NC);
-    return check_launch("q6_k_matvec");
-}
-
 template <int NC>
 int launch_nc(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const float *kscales, const int16_t *bsums,
               int row_start, int row_end, const float *bias, float *y, int ldy, int32_t *dots) {
-    const int rows = row_end - row_start;
-    const int want = 2 * ctx->cu_count;
-    if (rows / 32 >= want)
-        return launch_rw<32, NC>(ctx, w, q, kscales, bsums, row_start, row_end, bias, y, ldy, dots);
-    if (rows / 16 >= want)
-        return launch_rw<16, NC>(ctx, w, q, kscales, bsums, row_start, row_end, bias, y, ldy, dots);
-    return launch_rw<8, NC>(ctx, w, q, kscales, bsums, row_start, row_end, bias, y, ldy, dots);
+    const int B = w->blocks;
+    const int waves = min(B, 16);
+    const size_t lds = dots ? 0 : (size_t)B * NC * kTileRows * sizeof(float);
+    GX_CHECK(lds <= 64 * 1024, "gx: a %d-input Q6_K row is wider than this kernel's LDS", w->cols);
+    const int tile0 = row_start / kTileRows;
+    const int grid = (row_end + kTileRows - 1) / kTileRows - tile0;
+    q6_k_matvec_kernel<NC><<<grid, 64 * waves, lds, ctx->stream>>>(w->dev, w->plane0_bytes, B, w->dchunks, q,
+                                                                   kscales, bsums, w->cols, tile0, row_start,
+                                                                   row_end, bias, y, ldy, dots);
+    return check_launch("q6_k_matvec");
 }
 
 }  // namespace
