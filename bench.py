@@ -134,15 +134,15 @@ def main():
             s0 = torch.empty((1, c0 // 32), dtype=torch.float32, device="cuda")
             qs0 = torch.empty((1, c0 // 32), dtype=torch.int32, device="cuda")
             y0 = torch.empty((1, r0), dtype=torch.float32, device="cuda")
-            call("gx_quantize_q8_0", ctx.ptr, vp(x0d), c0, 1, c0, vp(q0), vp(s0), vp(qs0), None)
+            call("gx_quantize_q8_0", ctx.ptr, vp(x0d), c0, 1, c0, vp(q0), vp(s0), vp(qs0), None, None)
             for i in range(20):
-                call("gx_matmul_q4_0", ctx.ptr, w0s[i % n_copies].ptr, vp(q0), vp(s0), vp(qs0), 1, 0, r0, None,
-                     vp(y0), r0)
+                call("gx_matmul_q4_0", ctx.ptr, w0s[i % n_copies].ptr, vp(q0), vp(s0), vp(qs0), None, 1, 0, r0,
+                     None, vp(y0), r0)
             reps = 400
             ctx.timer_start()
             for i in range(reps):
-                call("gx_matmul_q4_0", ctx.ptr, w0s[i % n_copies].ptr, vp(q0), vp(s0), vp(qs0), 1, 0, r0, None,
-                     vp(y0), r0)
+                call("gx_matmul_q4_0", ctx.ptr, w0s[i % n_copies].ptr, vp(q0), vp(s0), vp(qs0), None, 1, 0, r0,
+                     None, vp(y0), r0)
             ms0 = ctx.timer_stop() / reps
             b0 = r0 * (c0 // 32) * 18 + c0 + 8 * (c0 // 32) + 4 * r0
             extra["c0_q4_0_matvec"] = {"shape": [r0, c0], "M": 1, "kernel_us": round(ms0 * 1e3, 3),
@@ -162,21 +162,26 @@ def main():
             q2 = torch.empty((M, c0), dtype=torch.int8, device="cuda")
             s2 = torch.empty((M, c0 // 32), dtype=torch.float32, device="cuda")
             qs2 = torch.empty((M, c0 // 32), dtype=torch.int32, device="cuda")
+            h2 = torch.empty((M, c0), dtype=torch.int16, device="cuda")
             y2 = torch.empty((M, r0), dtype=torch.float32, device="cuda")
-            call("gx_quantize_q8_0", ctx.ptr, vp(x2d), c0, M, c0, vp(q2), vp(s2), vp(qs2), None)
-            for _ in range(5):
-                call("gx_matmul_q4_0", ctx.ptr, w0d.ptr, vp(q2), vp(s2), vp(qs2), M, 0, r0, None, vp(y2), r0)
-            reps = 50
-            ctx.timer_start()
-            for _ in range(reps):
-                call("gx_matmul_q4_0", ctx.ptr, w0d.ptr, vp(q2), vp(s2), vp(qs2), M, 0, r0, None, vp(y2), r0)
-            ms2 = ctx.timer_stop() / reps
-            ops = 2.0 * M * r0 * c0
-            tops = ops / (ms2 * 1e-3) / 1e12
-            by = r0 * (c0 // 32) * 18 + M * (c0 + 8 * (c0 // 32)) + 4 * M * r0
-            extra[f"c2_q4_0_gemm_m{M}"] = {"shape": [M, r0, c0], "kernel_us": round(ms2 * 1e3, 2),
-                                           "TOP/s": round(tops, 2), "int8_mfma_frac": round(tops / INT8_PEAK_TOPS, 4),
-                                           "GB/s": round(by / (ms2 * 1e-3) / 1e9, 1)}
+            call("gx_quantize_q8_0", ctx.ptr, vp(x2d), c0, M, c0, vp(q2), vp(s2), vp(qs2), None, vp(h2))
+            # fp16-MFMA kernel (q16 given) and int8-MFMA kernel (q16 withheld)
+            for label, q16 in (("f16", h2), ("i8", None)):
+                for _ in range(5):
+                    call("gx_matmul_q4_0", ctx.ptr, w0d.ptr, vp(q2), vp(s2), vp(qs2), vp(q16), M, 0, r0, None,
+                         vp(y2), r0)
+                reps = 50
+                ctx.timer_start()
+                for _ in range(reps):
+                    call("gx_matmul_q4_0", ctx.ptr, w0d.ptr, vp(q2), vp(s2), vp(qs2), vp(q16), M, 0, r0, None,
+                         vp(y2), r0)
+                ms2 = ctx.timer_stop() / reps
+                ops = 2.0 * M * r0 * c0
+                tops = ops / (ms2 * 1e-3) / 1e12
+                by = r0 * (c0 // 32) * 18 + M * (c0 + 8 * (c0 // 32)) + 4 * M * r0
+                extra[f"c2_q4_0_gemm_m{M}_{label}"] = {
+                    "shape": [M, r0, c0], "kernel_us": round(ms2 * 1e3, 2), "TOP/s": round(tops, 2),
+                    "int8_mfma_frac": round(tops / INT8_PEAK_TOPS, 4), "GB/s": round(by / (ms2 * 1e-3) / 1e9, 1)}
         w0d.free()
         if args.only == "c2":
             print(json.dumps(extra))

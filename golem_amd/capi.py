@@ -47,13 +47,13 @@ _SIGNATURES = {
     "gx_weight_info": [_vp, ctypes.POINTER(_c_int), ctypes.POINTER(_c_int), ctypes.POINTER(_c_int),
                        ctypes.POINTER(_c_int), ctypes.POINTER(_c_size)],
     "gx_weight_rows": [_vp, _vp, _c_int, _vp, _c_int, _vp],
-    "gx_quantize_q8_0": [_vp, _vp, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp],
+    "gx_quantize_q8_0": [_vp, _vp, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _vp],
     "gx_quantize_q8_k": [_vp, _vp, _c_int, _c_int, _c_int, _vp, _vp, _vp],
-    "gx_matmul_q4_0": [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _vp, _c_int],
-    "gx_matmul_q4_0_expert": [_vp, _vp, _c_int, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _c_int],
+    "gx_matmul_q4_0": [_vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _vp, _c_int],
+    "gx_matmul_q4_0_expert": [_vp, _vp, _c_int, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _c_int],
     "gx_matmul_q6_k": [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _vp, _c_int],
     "gx_matmul_f32": [_vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _c_int],
-    "gx_q4_0_block_dots": [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp],
+    "gx_q4_0_block_dots": [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp],
     "gx_q6_k_block_dots": [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp],
 }
 _RESTYPE = {"gx_last_error": ctypes.c_char_p}

@@ -302,7 +302,7 @@ int gx_weight_rows(gx_ctx *ctx, const gx_weight *w, int expert, const int32_t *i
 // ---- activations ---------------------------------------------------------
 
 int gx_quantize_q8_0(gx_ctx *ctx, const float *x, int ldx, int M, int K, int8_t *q, float *scales, int32_t *qsum,
-                     float *corr) {
+                     float *corr, uint16_t *q16) {
     if (int rc = use(ctx))
         return rc;
     GX_CHECK(K % gx::kQ4Block == 0 && K > 0, "nn: activation length must be a multiple of the block size");
@@ -310,7 +310,7 @@ int gx_quantize_q8_0(gx_ctx *ctx, const float *x, int ldx, int M, int K, int8_t 
     GX_CHECK(x && q && scales && qsum, "gx: missing argument");
     if (M == 0)
         return ok();
-    if (int rc = gx::launch_quantize_q8_0(ctx, x, ldx, M, K, q, scales, qsum, corr))
+    if (int rc = gx::launch_quantize_q8_0(ctx, x, ldx, M, K, q, scales, qsum, corr, q16))
         return rc;
     return ok();
 }
@@ -346,8 +346,8 @@ static int check_product(const gx_weight *w, int quant, int M, int row_start, in
 }
 
 static int q4_0_product(gx_ctx *ctx, const gx_weight *w, int expert, const int8_t *q, const float *scales,
-                        const int32_t *qsum, int M, int row_start, int row_end, const float *bias, float *y,
-                        int ldy) {
+                        const int32_t *qsum, const uint16_t *q16, int M, int row_start, int row_end,
+                        const float *bias, float *y, int ldy) {
     if (int rc = use(ctx))
         return rc;
     if (int rc = check_product(w, GX_Q4_0, M, row_start, row_end, y, ldy))
@@ -358,22 +358,28 @@ static int q4_0_product(gx_ctx *ctx, const gx_weight *w, int expert, const int8_
     if (M == 0 || row_start == row_end)
         return ok();
     const uint8_t *mat = w->dev + (size_t)expert * w->matrix_bytes;
-    int rc = M <= 8 ? gx::launch_q4_0_matvec(ctx, w, mat, q, scales, qsum, M, row_start, row_end, bias, y, ldy)
-                    : gx::launch_q4_0_gemm(ctx, w, mat, q, scales, qsum, M, row_start, row_end, bias, y, ldy,
-                                           nullptr);
+    GX_CHECK(((uintptr_t)q16 & 15) == 0, "gx: q16 must be 16-byte aligned");
+    int rc;
+    if (M <= 8)
+        rc = gx::launch_q4_0_matvec(ctx, w, mat, q, scales, qsum, M, row_start, row_end, bias, y, ldy);
+    else if (q16)
+        rc = gx::launch_q4_0_gemm_f16(ctx, w, mat, q16, scales, M, row_start, row_end, bias, y, ldy, nullptr);
+    else
+        rc = gx::launch_q4_0_gemm(ctx, w, mat, q, scales, qsum, M, row_start, row_end, bias, y, ldy, nullptr);
     if (rc)
         return rc;
     return ok();
 }
 
 int gx_matmul_q4_0(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const float *scales, const int32_t *qsum,
-                   int M, int row_start, int row_end, const float *bias, float *y, int ldy) {
-    return q4_0_product(ctx, w, 0, q, scales, qsum, M, row_start, row_end, bias, y, ldy);
+                   const uint16_t *q16, int M, int row_start, int row_end, const float *bias, float *y, int ldy) {
+    return q4_0_product(ctx, w, 0, q, scales, qsum, q16, M, row_start, row_end, bias, y, ldy);
 }
 
 int gx_matmul_q4_0_expert(gx_ctx *ctx, const gx_weight *w, int expert, const int8_t *q, const float *scales,
-                          const int32_t *qsum, int M, int row_start, int row_end, float *y, int ldy) {
-    return q4_0_product(ctx, w, expert, q, scales, qsum, M, row_start, row_end, nullptr, y, ldy);
+                          const int32_t *qsum, const uint16_t *q16, int M, int row_start, int row_end, float *y,
+                          int ldy) {
+    return q4_0_product(ctx, w, expert, q, scales, qsum, q16, M, row_start, row_end, nullptr, y, ldy);
 }
 
 int gx_matmul_q6_k(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const float *kscales, const int16_t *bsums,
@@ -405,20 +411,25 @@ int gx_matmul_f32(gx_ctx *ctx, const gx_weight *w, const float *x, int ldx, int 
     return ok();
 }
 
-int gx_q4_0_block_dots(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const int32_t *qsum, int M, int row_start,
-                       int row_end, int path, int32_t *out) {
+int gx_q4_0_block_dots(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const int32_t *qsum, const uint16_t *q16,
+                       int M, int row_start, int row_end, int path, int32_t *out) {
     if (int rc = use(ctx))
         return rc;
     if (int rc = check_product(w, GX_Q4_0, M, row_start, row_end, out, row_end))
         return rc;
     GX_CHECK(q && qsum, "gx: missing activation");
     GX_CHECK(((uintptr_t)q & 15) == 0, "gx: q must be 16-byte aligned");
-    GX_CHECK(path == 0 || path == 1, "gx: path must be 0 (matrix-vector) or 1 (MFMA)");
+    GX_CHECK(path >= 0 && path <= 2, "gx: path must be 0 (matrix-vector), 1 (int8 MFMA) or 2 (fp16 MFMA)");
+    GX_CHECK(path != 2 || (q16 && ((uintptr_t)q16 & 15) == 0), "gx: path 2 needs a 16-byte aligned q16");
     if (M == 0 || row_start == row_end)
         return ok();
-    int rc = path == 0 ? gx::launch_q4_0_block_dots_matvec(ctx, w, q, qsum, M, row_start, row_end, out)
-                       : gx::launch_q4_0_gemm(ctx, w, w->dev, q, nullptr, qsum, M, row_start, row_end, nullptr,
-                                              nullptr, 0, out);
+    int rc;
+    if (path == 0)
+        rc = gx::launch_q4_0_block_dots_matvec(ctx, w, q, qsum, M, row_start, row_end, out);
+    else if (path == 1)
+        rc = gx::launch_q4_0_gemm(ctx, w, w->dev, q, nullptr, qsum, M, row_start, row_end, nullptr, nullptr, 0, out);
+    else
+        rc = gx::launch_q4_0_gemm_f16(ctx, w, w->dev, q16, nullptr, M, row_start, row_end, nullptr, nullptr, 0, out);
     if (rc)
         return rc;
     return ok();

@@ -10,11 +10,22 @@
 // (gx_q4_0.hip), stretch by stretch, so a token's result is bit-identical
 // whether it came through this kernel or that one.
 //
-// Tile: a workgroup of four wavefronts owns 64 rows (one R64 tile) x 64
-// tokens; each wavefront one 32x32 quarter.  The weights' nibbles are widened
-// to signed int8 in registers (n - 8); the activations are already int8.
-// The block scales of the tile's rows and tokens for one stretch are staged
-// in LDS as floats, double-buffered, one barrier per stretch.
+// The per-block epilogue is what bounds this product: every output element
+// needs float(isum) * (d_w * d_a) added to its sum, per block.  The scale
+// product d_w[i] * d_a[j] of a 32x32 tile is an outer product of two fp16
+// vectors (golem stores d_a, the Q8_0 scale, already rounded through fp16),
+// so it comes from the matrix core too: v_mfma_f32_32x32x8_f16 with the two
+// vectors in k = 0 and zeros elsewhere gives every product exactly (an
+// 11-bit by 11-bit product fits fp32).  The vector ALU is left with one
+// conversion and one fma per element per block.
+//
+// Tile: a workgroup of four wavefronts owns 64 rows (one R64 tile) x 128
+// tokens; each wavefront 32 rows x 64 tokens, i.e. two 32x32 MFMA tiles that
+// share the weight operand.  Half a stretch (4 blocks) of the tile's nibbles, its
+// tokens' int8 activations and both sides' scales are staged in LDS, double
+// buffered: the next stretch's global loads are in flight while this one's
+// MFMAs run.  The weights' nibbles are widened to signed int8 (n - 8) in
+// registers as they are read.
 #include "gx_device.hpp"
 #include "gx_internal.hpp"
 
@@ -23,111 +34,425 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
 
 // Nibbles 0..15 in each byte -> (n - 8) as int8: n + 120 stays below 256
 // without a carry, and flipping the top bit subtracts 128.
 __device__ __forceinline__ uint32_t widen_nibbles(uint32_t n) { return (n + 0x78787878u) ^ 0x80808080u; }
 
+// The signed weights of one block for this lane's k-half: g = 0 takes the
+// low nibbles (weights 0..15), g = 1 the high nibbles (weights 16..31).
+__device__ __forceinline__ v4i weight_operand(const uint4 &wq, uint32_t sh) {
+    v4i A;
+    A.x = (int)widen_nibbles((wq.x >> sh) & 0x0F0F0F0Fu);
+    A.y = (int)widen_nibbles((wq.y >> sh) & 0x0F0F0F0Fu);
+    A.z = (int)widen_nibbles((wq.z >> sh) & 0x0F0F0F0Fu);
+    A.w = (int)widen_nibbles((wq.w >> sh) & 0x0F0F0F0Fu);
+    return A;
+}
+
+// A 32x32x8 f16 operand holding the fp16 bits `h` at k = 0 (lanes 0..31,
+// element 0) and zeros everywhere else.
+__device__ __forceinline__ v4h k0_operand(uint32_t h, bool first_half) {
+    const uint2 bits = make_uint2(first_half ? (h & 0xFFFFu) : 0u, 0u);
+    return __builtin_bit_cast(v4h, bits);
+}
+
+// The fp16 bits of the j-th of the eight values packed in a chunk (j may be
+// a run-time index).
+__device__ __forceinline__ uint32_t chunk_half_bits(const uint4 &c, int j) {
+    const uint32_t lo = (j & 2) ? c.y : c.x, hi = (j & 2) ? c.w : c.z;
+    const uint32_t word = (j & 4) ? hi : lo;
+    return (j & 1) ? (word >> 16) : (word & 0xFFFFu);
+}
+
+// LDS layout of one pipeline stage: half a stretch, 4 blocks.
+constexpr int kStage = 4;                         // blocks per stage
+constexpr int kTokTile = 128;                     // tokens per workgroup
+constexpr int kActRow = kStage * kQ4Block + 16;   // one token's stage, padded (144 B)
+struct Stage {
+    uint8_t w[kStage][kTileRows][kChunk];         // nibbles, block-major, R64 order (4 KiB)
+    uint8_t a[kTokTile][kActRow];                 // int8 activations (18 KiB)
+    uint16_t dw[kStage][kTileRows];               // weight scales, fp16 bits
+    uint16_t da[kStage][kTokTile];                // activation scales, fp16 bits
+};
+
+// One thread's share of a stage: the global loads, then the writes into LDS.
+// Weights: chunk tid of the 256 (block tid / 64, row tid % 64).  Activations:
+// chunks c = tid + 256 k (k < 4) of the 1024 (token c / 8, 16-byte part
+// c % 8).  Weight scales: threads 0..63, the 8 bytes of row tid's chunk that
+// hold this stage's 4 blocks.  Activation scales: token tid / 2, blocks
+// 2 (tid % 2) .. + 2.  Indices past the matrix or the batch are clamped to
+// the last valid one (in bounds; such values are never used: a block past
+// the row gets weight scale 0, a token past the batch is not stored).
+struct Fetch {
+    v4u w, a[4];
+    unsigned dw0, dw1;
+    float da[2];
+};
+
 template <bool DOTS>
-__global__ __launch_bounds__(256) void q4_0_gemm_kernel(const uint8_t *__restrict__ W, size_t plane0_bytes, int B,
-                                                        int DC, const int8_t *__restrict__ q,
-                                                        const float *__restrict__ scales, int K, int M,
-                                                        int row_base, int row_start, int row_end,
-                                                        const float *__restrict__ bias, float *__restrict__ y,
-                                                        int ldy, int32_t *__restrict__ dots) {
-    __shared__ float sdw[2][kStretch][64];
-    __shared__ float sda[2][kStretch][64];
+__device__ __forceinline__ void fetch_stage(Fetch &f, const uint8_t *__restrict__ W, size_t plane0_bytes, int B,
+                                            int DC, const int8_t *__restrict__ q, const float *__restrict__ scales,
+                                            int K, int M, int tile, int m0, int h, int tid) {
+    const int b0 = h * kStage;
+    {
+        const int b = min(b0 + (tid >> 6), B - 1);
+        f.w = *(const v4u *)(W + (((size_t)tile * B + b) * kTileRows + (tid & 63)) * kChunk);
+    }
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int c = tid + 256 * k;
+        const int m = min(m0 + (c >> 3), M - 1);
+        const int b = min(b0 + ((c & 7) >> 1), B - 1);
+        f.a[k] = *(const v4u *)(q + (size_t)m * K + (size_t)b * kQ4Block + 16 * (c & 1));
+    }
+    if (!DOTS) {
+        if (tid < 64) {
+            const unsigned *chunk = (const unsigned *)(W + plane0_bytes +
+                                                       (((size_t)tile * DC + (b0 >> 3)) * kTileRows + tid) * kChunk);
+            f.dw0 = chunk[(b0 & 7) >> 1];
+            f.dw1 = chunk[((b0 & 7) >> 1) + 1];
+        }
+        const int m = min(m0 + (tid >> 1), M - 1);
+#pragma unroll
+        for (int k = 0; k < 2; k++)
+            f.da[k] = scales[(size_t)m * B + min(b0 + 2 * (tid & 1) + k, B - 1)];
+    }
+}
+
+template <bool DOTS>
+__device__ __forceinline__ void commit_stage(const Fetch &f, Stage &t, int nb, int tid) {
+    *(v4u *)t.w[tid >> 6][tid & 63] = f.w;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int c = tid + 256 * k;
+        *(v4u *)&t.a[c >> 3][(c & 7) * 16] = f.a[k];
+    }
+    if (!DOTS) {
+        if (tid < 64) {
+            const unsigned words[2] = {f.dw0, f.dw1};
+#pragma unroll
+            for (int j = 0; j < kStage; j++)  // a block past the row gets scale 0
+                t.dw[j][tid] = j < nb ? (uint16_t)(words[j >> 1] >> (16 * (j & 1))) : (uint16_t)0;
+        }
+#pragma unroll
+        for (int k = 0; k < 2; k++)
+            t.da[2 * (tid & 1) + k][tid >> 1] = (uint16_t)float_to_half_bits(f.da[k]);
+    }
+}
+
+template <bool DOTS>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) void q4_0_gemm_kernel(
+    const uint8_t *__restrict__ W, size_t plane0_bytes, int B, int DC, const int8_t *__restrict__ q,
+    const float *__restrict__ scales, int K, int M, int tile0, int row_start, int row_end,
+    const float *__restrict__ bias, float *__restrict__ y, int ldy, int32_t *__restrict__ dots) {
+    __shared__ Stage st[2];
     const int tid = threadIdx.x;
     const int lane = tid & 63, wv = tid >> 6;
-    const int n0 = row_base + blockIdx.x * 64;
-    const int m0 = blockIdx.y * 64;
-    const int nw = 32 * (wv & 1), mw = 32 * (wv >> 1);
+    const int tile = tile0 + blockIdx.x;
+    const int n0 = tile * kTileRows;
+    const int m0 = blockIdx.y * kTokTile;
+    const int nw = 32 * (wv & 1), mw = 64 * (wv >> 1);
     const int li = lane & 31, g = lane >> 5;
+    const uint32_t sh = 4u * g;
+    const int H = (B + kStage - 1) / kStage;  // stages; two make a stretch
+    const int nrows = row_end - row_start;
 
-    const int arow = n0 + nw + li;
-    const uint8_t *a_src = W + ((size_t)(arow >> 6) * B * kTileRows + (arow & 63)) * kChunk;
-    const int bm = m0 + mw + li;
-    const bool bvalid = bm < M;
-    const int8_t *b_src = q + (size_t)(bvalid ? bm : 0) * K + 16 * g;
-
-    float acc[16], tot[16];
+    v16f acc0, acc1, tot0, tot1;
 #pragma unroll
     for (int e = 0; e < 16; e++)
-        acc[e] = 0.0f, tot[e] = 0.0f;
+        acc0[e] = acc1[e] = tot0[e] = tot1[e] = 0.0f;
+    const v16i zero_i = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    const v16f zero_f = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    const int bm0 = m0 + mw + li, bm1 = bm0 + 32;
+    const bool v0 = bm0 < M, v1 = bm1 < M;
 
-    const int S = (B + kStretch - 1) / kStretch;
-    const int nrows = row_end - row_start;
-    for (int s = 0; s < S; s++) {
-        const int buf = s & 1;
-        const int b0 = s * kStretch;
-        const int nb = min(kStretch, B - b0);
-        if (!DOTS) {
-            if (tid < 64) {
-                const int n = n0 + tid;
-                const uint4 dch = *(const uint4 *)(W + plane0_bytes +
-                                                   (((size_t)(n >> 6) * DC + s) * kTileRows + (n & 63)) * kChunk);
-#pragma unroll
-                for (int j = 0; j < kStretch; j++)
-                    sdw[buf][j][tid] = chunk_half(dch, j);
-            } else if (tid < 128) {
-                const int m = m0 + tid - 64;
-#pragma unroll
-                for (int j = 0; j < kStretch; j++)
-                    sda[buf][j][tid - 64] = (m < M && j < nb) ? scales[(size_t)m * B + b0 + j] : 0.0f;
-            }
-            __syncthreads();
-        }
-        for (int j = 0; j < nb; j++) {
-            const int b = b0 + j;
-            const uint4 wq = *(const uint4 *)(a_src + (size_t)b * kTileRows * kChunk);
-            const uint32_t sh = 4 * g;
-            v4i A;
-            A.x = (int)widen_nibbles((wq.x >> sh) & 0x0F0F0F0Fu);
-            A.y = (int)widen_nibbles((wq.y >> sh) & 0x0F0F0F0Fu);
-            A.z = (int)widen_nibbles((wq.z >> sh) & 0x0F0F0F0Fu);
-            A.w = (int)widen_nibbles((wq.w >> sh) & 0x0F0F0F0Fu);
-            v4i Bv = {0, 0, 0, 0};
-            if (bvalid)
-                Bv = *(const v4i *)(b_src + (size_t)b * kQ4Block);
-            v16i C = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-            C = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, Bv, C, 0, 0, 0);
+    Fetch f;
+    fetch_stage<DOTS>(f, W, plane0_bytes, B, DC, q, scales, K, M, tile, m0, 0, tid);
+    commit_stage<DOTS>(f, st[0], min(kStage, B), tid);
+    __syncthreads();
+    for (int h = 0; h < H; h++) {
+        Stage &cur = st[h & 1];
+        if (h + 1 < H)  // in flight during this stage's arithmetic
+            fetch_stage<DOTS>(f, W, plane0_bytes, B, DC, q, scales, K, M, tile, m0, h + 1, tid);
+        const int nb = min(kStage, B - h * kStage);
+#pragma unroll 2
+        for (int j = 0; j < kStage; j++) {
+            const v4i A = weight_operand(*(const uint4 *)cur.w[j][nw + li], sh);
+            const v4i B0 = *(const v4i *)&cur.a[mw + li][j * kQ4Block + 16 * g];
+            const v4i B1 = *(const v4i *)&cur.a[mw + 32 + li][j * kQ4Block + 16 * g];
+            const v16i C0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B0, zero_i, 0, 0, 0);
+            const v16i C1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B1, zero_i, 0, 0, 0);
             if (DOTS) {
-                if (bvalid) {
+                if (j < nb) {
+                    const int b = h * kStage + j;
 #pragma unroll
                     for (int e = 0; e < 16; e++) {
                         const int n = n0 + nw + 8 * (e >> 2) + 4 * g + (e & 3);
-                        if (n >= row_start && n < row_end)
-                            dots[((size_t)bm * nrows + (n - row_start)) * B + b] = C[e];
+                        if (n >= row_start && n < row_end) {
+                            if (v0)
+                                dots[((size_t)bm0 * nrows + (n - row_start)) * B + b] = C0[e];
+                            if (v1)
+                                dots[((size_t)bm1 * nrows + (n - row_start)) * B + b] = C1[e];
+                        }
                     }
                 }
             } else {
-                const float da = sda[buf][j][mw + li];
+                // Past the last block the weight scale is 0: the product adds
+                // fma(c, 0, acc) == acc.
+                const v4h As = k0_operand(cur.dw[j][nw + li], g == 0);
+                const v16f S0 = __builtin_amdgcn_mfma_f32_32x32x8f16(As, k0_operand(cur.da[j][mw + li], g == 0),
+                                                                     zero_f, 0, 0, 0);
+                const v16f S1 = __builtin_amdgcn_mfma_f32_32x32x8f16(As, k0_operand(cur.da[j][mw + 32 + li], g == 0),
+                                                                     zero_f, 0, 0, 0);
 #pragma unroll
                 for (int e = 0; e < 16; e++) {
-                    const float dw = sdw[buf][j][nw + 8 * (e >> 2) + 4 * g + (e & 3)];
-                    const float sc = dw * da;
-                    acc[e] = fmaf((float)C[e], sc, acc[e]);
+                    acc0[e] = fmaf((float)C0[e], S0[e], acc0[e]);
+                    acc1[e] = fmaf((float)C1[e], S1[e], acc1[e]);
                 }
             }
         }
-        if (!DOTS) {
+        // A stretch is two stages: after the second (or the row's last stage)
+        // the stretch sum joins the total.
+        if (!DOTS && ((h & 1) || h + 1 == H)) {
 #pragma unroll
             for (int e = 0; e < 16; e++) {
-                tot[e] = tot[e] + acc[e];
-                acc[e] = 0.0f;
+                tot0[e] = tot0[e] + acc0[e];
+                tot1[e] = tot1[e] + acc1[e];
+                acc0[e] = 0.0f;
+                acc1[e] = 0.0f;
             }
         }
+        if (h + 1 < H)
+            commit_stage<DOTS>(f, st[(h + 1) & 1], min(kStage, B - (h + 1) * kStage), tid);
+        __syncthreads();
     }
-    if (DOTS || !bvalid)
+    if (DOTS)
         return;
 #pragma unroll
     for (int e = 0; e < 16; e++) {
         const int n = n0 + nw + 8 * (e >> 2) + 4 * g + (e & 3);
         if (n >= row_start && n < row_end) {
-            float v = tot[e];
-            if (bias)
-                v = v + bias[n];
-            y[(size_t)bm * ldy + n] = v;
+            const float bn = bias ? bias[n] : 0.0f;
+            if (v0)
+                y[(size_t)bm0 * ldy + n] = bias ? tot0[e] + bn : tot0[e];
+            if (v1)
+                y[(size_t)bm1 * ldy + n] = bias ? tot1[e] + bn : tot1[e];
+        }
+    }
+}
+
+// ---- the fp16 product ------------------------------------------------------
+//
+// The same contraction with the per-block integers taken by
+// v_mfma_f32_32x32x16_f16 from integer-valued fp16 operands: the weights
+// (n - 8) and the Q8_0 values q, both exact in fp16.  Every product and every
+// partial sum is an integer below 2^24 in magnitude, so the fp32 result is
+// the exact per-block integer, already a float: the epilogue is one fma per
+// element per block, where the int8 kernel needs a conversion and an fma.
+// The caller provides the activation's fp16 copy (the quantiser writes it);
+// the weights are widened to fp16 once per workgroup as a stage is staged.
+//
+// Tile: 64 rows x 128 tokens per workgroup; each wavefront 32 rows x 64
+// tokens (two 32x32 tiles sharing the weight operand).  Stage = 2 blocks,
+// double buffered in LDS: fp16 weights [2][64][40] (rows padded to 80 B),
+// fp16 activations [128][2*32 + 8] (144 B per token), both scales as fp16.
+constexpr int kF16Stage = 2;                       // blocks per stage
+constexpr int kF16Tok = 128;                       // tokens per workgroup
+constexpr int kWRow = 40;                          // halves per weight row (32 + pad)
+constexpr int kARow = kF16Stage * kQ4Block + 8;    // halves per token row (64 + pad)
+struct StageF16 {
+    uint16_t w[kF16Stage][kTileRows][kWRow];       // 10 KiB
+    uint16_t a[kF16Tok][kARow];                    // 18 KiB
+    uint16_t dw[kF16Stage][kTileRows];
+    uint16_t da[kF16Stage][kF16Tok];
+};
+
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
+
+// Four nibbles (one per byte, values 0..15) -> four fp16 values n - 8, as two
+// dwords.  0x64 above a byte makes the fp16 1024 + n; subtracting 1032 is
+// exact.
+__device__ __forceinline__ void nibbles_to_f16(uint32_t n, uint32_t &lo, uint32_t &hi) {
+    const uint32_t a = __builtin_amdgcn_perm(0x64646464u, n, 0x04010400u);
+    const uint32_t b = __builtin_amdgcn_perm(0x64646464u, n, 0x04030402u);
+    const v2h bias = {(_Float16)1032.0f, (_Float16)1032.0f};
+    lo = __builtin_bit_cast(uint32_t, __builtin_bit_cast(v2h, a) - bias);
+    hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(v2h, b) - bias);
+}
+
+// One thread's share of a stage.  Weights: threads 0..127, chunk tid (block
+// tid / 64, row tid % 64).  Activations: chunks c = tid + 256 k (k < 4) of the
+// 1024 (token c / 8, 16-byte part c % 8, i.e. block (c % 8) / 4).  Weight
+// scales: threads 128..191, one 4-byte word of row tid - 128's chunk.
+// Activation scales: token tid / 2, block tid % 2.  Indices past the matrix
+// or the batch are clamped (in bounds, never used).
+struct FetchF16 {
+    v4u w, a[4];
+    unsigned dw;
+    float da;
+};
+
+template <bool DOTS>
+__device__ __forceinline__ void fetch_stage_f16(FetchF16 &f, const uint8_t *__restrict__ W, size_t plane0_bytes,
+                                                int B, int DC, const uint16_t *__restrict__ q16,
+                                                const float *__restrict__ scales, int K, int M, int tile, int m0,
+                                                int h, int tid) {
+    const int b0 = h * kF16Stage;
+    if (tid < 128) {
+        const int b = min(b0 + (tid >> 6), B - 1);
+        f.w = *(const v4u *)(W + (((size_t)tile * B + b) * kTileRows + (tid & 63)) * kChunk);
+    }
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int c = tid + 256 * k;
+        const int m = min(m0 + (c >> 3), M - 1);
+        const int b = min(b0 + ((c & 7) >> 2), B - 1);
+        f.a[k] = *(const v4u *)(q16 + (size_t)m * K + (size_t)b * kQ4Block + 8 * (c & 3));
+    }
+    if (!DOTS) {
+        if (tid >= 128 && tid < 192) {
+            const unsigned *chunk = (const unsigned *)(W + plane0_bytes +
+                                                       (((size_t)tile * DC + (b0 >> 3)) * kTileRows + (tid - 128)) *
+                                                           kChunk);
+            f.dw = chunk[(b0 & 7) >> 1];  // blocks b0, b0 + 1 (b0 is even)
+        }
+        const int m = min(m0 + (tid >> 1), M - 1);
+        f.da = scales[(size_t)m * B + min(b0 + (tid & 1), B - 1)];
+    }
+}
+
+template <bool DOTS>
+__device__ __forceinline__ void commit_stage_f16(const FetchF16 &f, StageF16 &t, int nb, int tid) {
+    if (tid < 128) {  // widen one block row of nibbles to 32 fp16 weights in golem's order:
+                      // [0,16) from the low nibbles of bytes 0..15, [16,32) from the high.
+        const uint32_t words[4] = {f.w.x, f.w.y, f.w.z, f.w.w};
+        uint32_t out[16];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            nibbles_to_f16(words[k] & 0x0F0F0F0Fu, out[2 * k], out[2 * k + 1]);
+            nibbles_to_f16((words[k] >> 4) & 0x0F0F0F0Fu, out[8 + 2 * k], out[8 + 2 * k + 1]);
+        }
+        uint16_t *row = t.w[tid >> 6][tid & 63];
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+            *(v4u *)(row + 8 * k) = (v4u){out[4 * k], out[4 * k + 1], out[4 * k + 2], out[4 * k + 3]};
+    }
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int c = tid + 256 * k;
+        *(v4u *)&t.a[c >> 3][(c & 7) * 8] = f.a[k];
+    }
+    if (!DOTS) {
+        if (tid >= 128 && tid < 192) {  // a block past the row gets scale 0
+            t.dw[0][tid - 128] = (uint16_t)(f.dw & 0xFFFFu);
+            t.dw[1][tid - 128] = nb > 1 ? (uint16_t)(f.dw >> 16) : (uint16_t)0;
+        }
+        t.da[tid & 1][tid >> 1] = (uint16_t)float_to_half_bits(f.da);
+    }
+}
+
+template <bool DOTS>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) void q4_0_gemm_f16_kernel(
+    const uint8_t *__restrict__ W, size_t plane0_bytes, int B, int DC, const uint16_t *__restrict__ q16,
+    const float *__restrict__ scales, int K, int M, int tile0, int row_start, int row_end,
+    const float *__restrict__ bias, float *__restrict__ y, int ldy, int32_t *__restrict__ dots) {
+    __shared__ StageF16 st[2];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wv = tid >> 6;
+    const int tile = tile0 + blockIdx.x;
+    const int n0 = tile * kTileRows;
+    const int m0 = blockIdx.y * kF16Tok;
+    const int nw = 32 * (wv & 1), mw = 64 * (wv >> 1);
+    const int li = lane & 31, g = lane >> 5;
+    const int H = (B + kF16Stage - 1) / kF16Stage;  // stages; four make a stretch
+    const int nrows = row_end - row_start;
+
+    v16f acc0, acc1, tot0, tot1;
+#pragma unroll
+    for (int e = 0; e < 16; e++)
+        acc0[e] = acc1[e] = tot0[e] = tot1[e] = 0.0f;
+    const v16f zero_f = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    const int bm0 = m0 + mw + li, bm1 = bm0 + 32;
+    const bool v0 = bm0 < M, v1 = bm1 < M;
+
+    FetchF16 f;
+    fetch_stage_f16<DOTS>(f, W, plane0_bytes, B, DC, q16, scales, K, M, tile, m0, 0, tid);
+    commit_stage_f16<DOTS>(f, st[0], min(kF16Stage, B), tid);
+    __syncthreads();
+    for (int h = 0; h < H; h++) {
+        StageF16 &cur = st[h & 1];
+        if (h + 1 < H)  // in flight during this stage's arithmetic
+            fetch_stage_f16<DOTS>(f, W, plane0_bytes, B, DC, q16, scales, K, M, tile, m0, h + 1, tid);
+        const int nb = min(kF16Stage, B - h * kF16Stage);
+#pragma unroll
+        for (int j = 0; j < kF16Stage; j++) {
+            const v8h A0 = *(const v8h *)&cur.w[j][nw + li][8 * g];
+            const v8h A1 = *(const v8h *)&cur.w[j][nw + li][16 + 8 * g];
+            const v8h P0 = *(const v8h *)&cur.a[mw + li][j * kQ4Block + 8 * g];
+            const v8h P1 = *(const v8h *)&cur.a[mw + li][j * kQ4Block + 16 + 8 * g];
+            const v8h Q0 = *(const v8h *)&cur.a[mw + 32 + li][j * kQ4Block + 8 * g];
+            const v8h Q1 = *(const v8h *)&cur.a[mw + 32 + li][j * kQ4Block + 16 + 8 * g];
+            v16f D0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(A0, P0, zero_f, 0, 0, 0);
+            D0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(A1, P1, D0, 0, 0, 0);
+            v16f D1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(A0, Q0, zero_f, 0, 0, 0);
+            D1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(A1, Q1, D1, 0, 0, 0);
+            if (DOTS) {
+                if (j < nb) {
+                    const int b = h * kF16Stage + j;
+#pragma unroll
+                    for (int e = 0; e < 16; e++) {
+                        const int n = n0 + nw + 8 * (e >> 2) + 4 * g + (e & 3);
+                        if (n >= row_start && n < row_end) {
+                            if (v0)
+                                dots[((size_t)bm0 * nrows + (n - row_start)) * B + b] = (int32_t)D0[e];
+                            if (v1)
+                                dots[((size_t)bm1 * nrows + (n - row_start)) * B + b] = (int32_t)D1[e];
+                        }
+                    }
+                }
+            } else {
+                // Past the last block the weight scale is 0: fma(d, 0, acc) == acc.
+                const v4h As = k0_operand(cur.dw[j][nw + li], g == 0);
+                const v16f S0 = __builtin_amdgcn_mfma_f32_32x32x8f16(As, k0_operand(cur.da[j][mw + li], g == 0),
+                                                                     zero_f, 0, 0, 0);
+                const v16f S1 = __builtin_amdgcn_mfma_f32_32x32x8f16(As, k0_operand(cur.da[j][mw + 32 + li], g == 0),
+                                                                     zero_f, 0, 0, 0);
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    acc0[e] = fmaf(D0[e], S0[e], acc0[e]);
+                    acc1[e] = fmaf(D1[e], S1[e], acc1[e]);
+                }
+            }
+        }
+        if (!DOTS && ((h & 3) == 3 || h + 1 == H)) {  // a stretch is four stages
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                tot0[e] = tot0[e] + acc0[e];
+                tot1[e] = tot1[e] + acc1[e];
+                acc0[e] = 0.0f;
+                acc1[e] = 0.0f;
+            }
+        }
+        if (h + 1 < H)
+            commit_stage_f16<DOTS>(f, st[(h + 1) & 1], min(kF16Stage, B - (h + 1) * kF16Stage), tid);
+        __syncthreads();
+    }
+    if (DOTS)
+        return;
+#pragma unroll
+    for (int e = 0; e < 16; e++) {
+        const int n = n0 + nw + 8 * (e >> 2) + 4 * g + (e & 3);
+        if (n >= row_start && n < row_end) {
+            const float bn = bias ? bias[n] : 0.0f;
+            if (v0)
+                y[(size_t)bm0 * ldy + n] = bias ? tot0[e] + bn : tot0[e];
+            if (v1)
+                y[(size_t)bm1 * ldy + n] = bias ? tot1[e] + bn : tot1[e];
         }
     }
 }
@@ -138,17 +463,37 @@ int launch_q4_0_gemm(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, const 
                      const int32_t *qsum, int M, int row_start, int row_end, const float *bias, float *y, int ldy,
                      int32_t *dots) {
     (void)qsum;  // the widened weights are signed: no recentring term
-    const int row_base = (row_start / 64) * 64;
-    dim3 grid((row_end - row_base + 63) / 64, (M + 63) / 64);
+    const int tile0 = row_start / kTileRows;
+    dim3 grid((row_end + kTileRows - 1) / kTileRows - tile0, (M + kTokTile - 1) / kTokTile);
     if (dots)
         q4_0_gemm_kernel<true><<<grid, 256, 0, ctx->stream>>>(mat, w->plane0_bytes, w->blocks, w->dchunks, q, scales,
-                                                              w->cols, M, row_base, row_start, row_end, bias, y, ldy,
+                                                              w->cols, M, tile0, row_start, row_end, bias, y, ldy,
                                                               dots);
     else
         q4_0_gemm_kernel<false><<<grid, 256, 0, ctx->stream>>>(mat, w->plane0_bytes, w->blocks, w->dchunks, q,
-                                                               scales, w->cols, M, row_base, row_start, row_end,
-                                                               bias, y, ldy, dots);
+                                                               scales, w->cols, M, tile0, row_start, row_end, bias,
+                                                               y, ldy, dots);
     return check_launch("q4_0_gemm");
+}
+
+}  // namespace gx
+
+namespace gx {
+
+int launch_q4_0_gemm_f16(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, const uint16_t *q16,
+                         const float *scales, int M, int row_start, int row_end, const float *bias, float *y, int ldy,
+                         int32_t *dots) {
+    const int tile0 = row_start / kTileRows;
+    dim3 grid((row_end + kTileRows - 1) / kTileRows - tile0, (M + kF16Tok - 1) / kF16Tok);
+    if (dots)
+        q4_0_gemm_f16_kernel<true><<<grid, 256, 0, ctx->stream>>>(mat, w->plane0_bytes, w->blocks, w->dchunks, q16,
+                                                                  scales, w->cols, M, tile0, row_start, row_end, bias,
+                                                                  y, ldy, dots);
+    else
+        q4_0_gemm_f16_kernel<false><<<grid, 256, 0, ctx->stream>>>(mat, w->plane0_bytes, w->blocks, w->dchunks, q16,
+                                                                   scales, w->cols, M, tile0, row_start, row_end,
+                                                                   bias, y, ldy, dots);
+    return check_launch("q4_0_gemm_f16");
 }
 
 }  // namespace gx

@@ -78,7 +78,7 @@ namespace gx {
 int launch_repack(gx_ctx *ctx, const uint8_t *src, gx_weight *w);
 int launch_rows(gx_ctx *ctx, const gx_weight *w, int expert, const int32_t *ids, int n, float *out);
 int launch_quantize_q8_0(gx_ctx *ctx, const float *x, int ldx, int M, int K, int8_t *q, float *scales,
-                         int32_t *qsum, float *corr);
+                         int32_t *qsum, float *corr, uint16_t *q16);
 int launch_quantize_q8_k(gx_ctx *ctx, const float *x, int ldx, int M, int K, int8_t *q, float *kscales,
                          int16_t *bsums);
 int launch_q4_0_matvec(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, const int8_t *q, const float *scales,
@@ -87,6 +87,9 @@ int launch_q4_0_matvec(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, cons
 int launch_q4_0_gemm(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, const int8_t *q, const float *scales,
                      const int32_t *qsum, int M, int row_start, int row_end, const float *bias, float *y, int ldy,
                      int32_t *dots);
+int launch_q4_0_gemm_f16(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, const uint16_t *q16,
+                         const float *scales, int M, int row_start, int row_end, const float *bias, float *y, int ldy,
+                         int32_t *dots);
 int launch_q4_0_block_dots_matvec(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const int32_t *qsum, int M,
                                   int row_start, int row_end, int32_t *out);
 int launch_q6_k_matvec(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const float *kscales,

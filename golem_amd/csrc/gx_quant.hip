@@ -15,7 +15,8 @@ namespace {
 // x is [M][ldx]; q [M][K], scales/qsum/corr [M][K/32].
 __global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float *__restrict__ x, int ldx, int M, int K,
                                                             int8_t *__restrict__ q, float *__restrict__ scales,
-                                                            int32_t *__restrict__ qsum, float *__restrict__ corr) {
+                                                            int32_t *__restrict__ qsum, float *__restrict__ corr,
+                                                            uint16_t *__restrict__ q16) {
     const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     const size_t total = (size_t)M * K;
     // total is a multiple of 32 and blocks are 256 threads, so a 32-lane
@@ -32,6 +33,8 @@ __global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float *__restr
     const size_t index = (size_t)m * (K >> 5) + block;
     if (peak == 0.0f) {
         q[gid] = 0;
+        if (q16)
+            q16[gid] = 0;
         if ((k & 31) == 0) {
             scales[index] = 0.0f;
             qsum[index] = 0;
@@ -47,6 +50,8 @@ __global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float *__restr
     int32_t n = nearest_int(prod);
     n = n > 127 ? 127 : (n < -128 ? -128 : n);
     q[gid] = (int8_t)n;
+    if (q16)  // the same integer as fp16 (exact: |n| <= 128)
+        q16[gid] = float_to_half_bits((float)n);
     int32_t sum = n;
 #pragma unroll
     for (int off = 16; off > 0; off >>= 1)
@@ -129,11 +134,11 @@ __global__ __launch_bounds__(256) void quantize_q8_k_kernel(const float *__restr
 }  // namespace
 
 int launch_quantize_q8_0(gx_ctx *ctx, const float *x, int ldx, int M, int K, int8_t *q, float *scales, int32_t *qsum,
-                         float *corr) {
+                         float *corr, uint16_t *q16) {
     const size_t total = (size_t)M * K;
     const int threads = 256;
     quantize_q8_0_kernel<<<(unsigned)((total + threads - 1) / threads), threads, 0, ctx->stream>>>(
-        x, ldx, M, K, q, scales, qsum, corr);
+        x, ldx, M, K, q, scales, qsum, corr, q16);
     return check_launch("quantize_q8_0");
 }
 

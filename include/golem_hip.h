@@ -26,6 +26,7 @@
  *     scales float   [M][K/32]   the fp16-rounded scale, held as float
  *     qsum   int32   [M][K/32]   sum of the block's 32 q values
  *     corr   float   [M][K/32]   (8*scale)*float(qsum), golem's Corr (optional)
+ *     q16    fp16    [M][K]      the same q values as fp16 (optional; exact)
  *   Q8_K activations (Batch.QK/KScales/BSums, nn/batch.go:29-32), same layout
  *   as golem's:
  *     q      int8    [M][K]
@@ -124,10 +125,11 @@ int gx_weight_rows(gx_ctx *ctx, const gx_weight *w, int expert, const int32_t *i
 /* ---- activations (nn.Batch) ------------------------------------------ */
 
 /* Batch.Quantize / QuantizeRange / QuantizeColumnRange (nn/batch.go:69-143)
- * for M activations of K floats at x[m*ldx ...] (device).  corr may be NULL.
- * K must be a multiple of 32 (nn/batch.go:49-51). */
+ * for M activations of K floats at x[m*ldx ...] (device).  corr and q16 may
+ * be NULL; q16 (uint16 storage of fp16) is what the fp16-MFMA batch product
+ * reads.  K must be a multiple of 32 (nn/batch.go:49-51). */
 int gx_quantize_q8_0(gx_ctx *ctx, const float *x, int ldx, int M, int K, int8_t *q, float *scales, int32_t *qsum,
-                     float *corr);
+                     float *corr, uint16_t *q16);
 
 /* Batch.QuantizeK (nn/batch.go:159-213).  K must be a multiple of 256
  * (nn/batch.go:160-162). */
@@ -141,15 +143,18 @@ int gx_quantize_q8_k(gx_ctx *ctx, const float *x, int ldx, int M, int K, int8_t 
  * MatVecRows for Q4_0 (nn/matrix.go:78-104), and MatVecQ4_0
  * (nn/dot_q4_0.go:117-124) when the range is all rows.  bias is NULL or
  * rows floats (device).  M <= 8 runs the bandwidth-bound matrix-vector
- * kernel; larger M runs the int8-MFMA product.  Both sum every row's blocks
- * in the same order, so a column's result does not depend on M. */
+ * kernel; larger M runs an MFMA product: on fp16 MFMA when q16 is given,
+ * else on int8 MFMA.  All of them sum every row's blocks in the same order
+ * from the same exact per-block integers, so a column's result does not
+ * depend on M or on the kernel. */
 int gx_matmul_q4_0(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const float *scales, const int32_t *qsum,
-                   int M, int row_start, int row_end, const float *bias, float *y, int ldy);
+                   const uint16_t *q16, int M, int row_start, int row_end, const float *bias, float *y, int ldy);
 
 /* The same product with one expert of a stack (gemma's
  * ExpertStack.At(expert).MatVecRows, gemma/moe.go:151-161). */
 int gx_matmul_q4_0_expert(gx_ctx *ctx, const gx_weight *w, int expert, const int8_t *q, const float *scales,
-                          const int32_t *qsum, int M, int row_start, int row_end, float *y, int ldy);
+                          const int32_t *qsum, const uint16_t *q16, int M, int row_start, int row_end, float *y,
+                          int ldy);
 
 /* y[m][r] = W[r] . x[m] (+ bias[r]) for a Q6_K matrix and a Q8_K batch:
  * MatVecQ6_K and matVecQ6_KRows (nn/dot_q6_k.go:64-103), which include the
@@ -168,10 +173,11 @@ int gx_matmul_f32(gx_ctx *ctx, const gx_weight *w, const float *x, int ldx, int 
 
 /* The signed per-block integer each product uses, sum_j (n_j - 8) * q_j, for
  * every (m, r, block): out[m][r - row_start][K/32] (device int32).  path 0 is
- * the matrix-vector kernel's arithmetic, path 1 the MFMA product's.  golem's
- * dotQ4_0Go accumulator (nn/dot_q4_0.go:58-63) is this plus 8*qsum. */
-int gx_q4_0_block_dots(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const int32_t *qsum, int M,
-                       int row_start, int row_end, int path, int32_t *out);
+ * the matrix-vector kernel's arithmetic, path 1 the int8-MFMA product's,
+ * path 2 the fp16-MFMA product's (needs q16).  golem's dotQ4_0Go accumulator
+ * (nn/dot_q4_0.go:58-63) is this plus 8*qsum. */
+int gx_q4_0_block_dots(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const int32_t *qsum, const uint16_t *q16,
+                       int M, int row_start, int row_end, int path, int32_t *out);
 
 /* dotQ6_KGo's per-superblock integer sum - 32*shift (nn/dot_q6_k.go:31-51)
  * for every (m, r, superblock): out[m][r - row_start][K/256]. */

@@ -49,7 +49,8 @@ class Device:
     def weight(self, data, quant, rows, cols, count=1):
         return capi.Weight(self.ctx, np.ascontiguousarray(data), quant, rows, cols, count)
 
-    def quantize_q8_0(self, x, with_corr=True):
+    def quantize_q8_0(self, x, with_corr=True, with_q16=True):
+        """The Q8_0 form on the device: (q, scales, qsum, q16, corr)."""
         x = np.ascontiguousarray(x, dtype=np.float32)
         M, K = x.shape
         xd = self.put(x)
@@ -57,9 +58,10 @@ class Device:
         sc = self.empty((M, K // 32), np.float32)
         qs = self.empty((M, K // 32), np.int32)
         co = self.empty((M, K // 32), np.float32) if with_corr else None
+        q16 = self.empty((M, K), np.int16) if with_q16 else None
         capi.call("gx_quantize_q8_0", self.ctx.ptr, capi.vp(xd), K, M, K, capi.vp(q), capi.vp(sc), capi.vp(qs),
-                  capi.vp(co))
-        return q, sc, qs, co
+                  capi.vp(co), capi.vp(q16))
+        return q, sc, qs, q16, co
 
     def quantize_q8_k(self, x):
         x = np.ascontiguousarray(x, dtype=np.float32)
@@ -71,14 +73,16 @@ class Device:
         capi.call("gx_quantize_q8_k", self.ctx.ptr, capi.vp(xd), K, M, K, capi.vp(q), capi.vp(ks), capi.vp(bs))
         return q, ks, bs
 
-    def matmul_q4_0(self, w, act, M, start=0, end=None, bias=None, y=None):
-        q, sc, qs = act[:3]
+    def matmul_q4_0(self, w, act, M, start=0, end=None, bias=None, y=None, f16=True):
+        """act is quantize_q8_0's tuple (or its first four entries, sliced);
+        f16=False withholds q16 so that a batch runs the int8-MFMA kernel."""
+        q, sc, qs, q16 = act[:4]
         end = w.rows if end is None else end
         if y is None:
             y = self.full((M, w.rows), float("nan"))
         b = None if bias is None else self.put(np.asarray(bias, dtype=np.float32))
-        capi.call("gx_matmul_q4_0", self.ctx.ptr, w.ptr, capi.vp(q), capi.vp(sc), capi.vp(qs), M, start, end,
-                  capi.vp(b), capi.vp(y), y.shape[1])
+        capi.call("gx_matmul_q4_0", self.ctx.ptr, w.ptr, capi.vp(q), capi.vp(sc), capi.vp(qs),
+                  capi.vp(q16 if f16 else None), M, start, end, capi.vp(b), capi.vp(y), y.shape[1])
         return y
 
     def matmul_q6_k(self, w, act, M, start=0, end=None, bias=None, y=None):
@@ -92,10 +96,10 @@ class Device:
         return y
 
     def q4_0_block_dots(self, w, act, M, start, end, path):
-        q, sc, qs = act[:3]
+        q, sc, qs, q16 = act[:4]
         out = self.empty((M, end - start, w.cols // 32), np.int32)
-        capi.call("gx_q4_0_block_dots", self.ctx.ptr, w.ptr, capi.vp(q), capi.vp(qs), M, start, end, path,
-                  capi.vp(out))
+        capi.call("gx_q4_0_block_dots", self.ctx.ptr, w.ptr, capi.vp(q), capi.vp(qs), capi.vp(q16), M, start, end,
+                  path, capi.vp(out))
         return self.get(out)
 
     def q6_k_block_dots(self, w, act, M, start, end):

@@ -53,7 +53,7 @@ def test_dequantized_rows_cover_every_half(dev, orc):
 
 
 @pytest.mark.parametrize("rows,cols,M", [(64, 256, 1), (200, 2560, 3), (96, 704, 9), (130, 2816, 40)])
-@pytest.mark.parametrize("path", [0, 1])
+@pytest.mark.parametrize("path", [0, 1, 2])
 def test_block_integers_bit_exact(dev, orc, rows, cols, M, path):
     log(f"q4_0 block dots rows={rows} cols={cols} M={M} path={path}")
     w, b, wd, act = setup(dev, orc, rows, cols, M, 100 + rows)
@@ -122,33 +122,43 @@ def test_row_ranges_and_bias(dev, orc, span):
             assert rel <= TOL, f"column {c}: {rel:.3g} at {at}"
 
 
+@pytest.mark.parametrize("f16", [True, False])
 @pytest.mark.parametrize("rows,cols", [(9728, 2560), (2560, 9728), (2816, 704), (200, 2816)])
-def test_batch_equals_one_at_a_time(dev, orc, rows, cols):
+def test_batch_equals_one_at_a_time(dev, orc, rows, cols, f16):
     """Every column of a batch -- M in 1..8 on the matrix-vector kernel, larger
-    M on MFMA -- is bit-identical to the same column computed alone."""
+    M on the fp16-MFMA (f16) or int8-MFMA kernel -- is bit-identical to the
+    same column computed alone."""
     M = 70
     g = synth.rng(400 + rows)
     w = synth.q4_0_weights(g, rows, cols)
     x = synth.activations(g, M, cols)
+    # Scales that are fp16 subnormals, on both sides of the product: every
+    # 7th weight block and two tokens whose Q8_0 scales fall below 2^-14.
+    wb = w.reshape(-1, 18)
+    sub = g.integers(1, 0x400, size=len(wb[::7]), dtype=np.uint16)
+    wb[::7, 0:2] = sub.view(np.uint8).reshape(-1, 2)
+    x[5] *= np.float32(3e-6)
+    x[40] *= np.float32(1e-7)
     wd = dev.weight(w, capi.Q4_0, rows, cols)
     act = dev.quantize_q8_0(x, with_corr=False)
-    log(f"batch==alone rows={rows} cols={cols}")
-    whole = dev.get(dev.matmul_q4_0(wd, act, M))
+    log(f"batch==alone rows={rows} cols={cols} f16={f16}")
+    whole = dev.get(dev.matmul_q4_0(wd, act, M, f16=f16))
     for m in (1, 2, 3, 5, 8, 9, 33):
-        part = dev.get(dev.matmul_q4_0(wd, tuple(a[:m] for a in act[:3]), m))
+        part = dev.get(dev.matmul_q4_0(wd, tuple(a[:m] for a in act[:4]), m, f16=f16))
         np.testing.assert_array_equal(part.view(np.uint32), whole[:m].view(np.uint32))
     for c in (0, 17, 69):
-        one = tuple(a[c:c + 1] for a in act[:3])
+        one = tuple(a[c:c + 1] for a in act[:4])
         alone = dev.get(dev.matmul_q4_0(wd, one, 1))
         np.testing.assert_array_equal(alone[0].view(np.uint32), whole[c].view(np.uint32))
 
 
+@pytest.mark.parametrize("f16", [True, False])
 @pytest.mark.parametrize("M", [64, 512])
-def test_gemm_against_golem(dev, orc, M):
+def test_gemm_against_golem(dev, orc, M, f16):
     rows, cols = 9728, 2560
-    log(f"q4_0 gemm M={M}")
+    log(f"q4_0 gemm M={M} f16={f16}")
     w, b, wd, act = setup(dev, orc, rows, cols, M, 500 + M)
-    got = dev.get(dev.matmul_q4_0(wd, act, M))
+    got = dev.get(dev.matmul_q4_0(wd, act, M, f16=f16))
     # The oracle on a sample of rows and columns (the whole product would take
     # the scalar oracle minutes).
     sel_rows = np.r_[0:64, 4000:4064, rows - 64:rows]

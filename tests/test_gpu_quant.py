@@ -36,8 +36,9 @@ def test_q8_0_bit_exact(dev, orc, M, K):
     if M >= 6:
         x[:6] = edge_rows(K, 11)[:6, :K]
     b = orc.Batch(x).quantize()
-    q, sc, qs, co = dev.quantize_q8_0(x)
+    q, sc, qs, q16, co = dev.quantize_q8_0(x)
     np.testing.assert_array_equal(dev.get(q), b.q_rows())
+    np.testing.assert_array_equal(dev.get(q16).view(np.float16).astype(np.float32), b.q_rows().astype(np.float32))
     np.testing.assert_array_equal(dev.get(sc).view(np.uint32), b.scales_rows().view(np.uint32))
     np.testing.assert_array_equal(dev.get(qs), b.qsum_rows())
     np.testing.assert_array_equal(dev.get(co).view(np.uint32), b.corr_rows().view(np.uint32))
