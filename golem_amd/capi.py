@@ -55,6 +55,10 @@ _SIGNATURES = {
     "gx_matmul_f32": [_vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _c_int],
     "gx_q4_0_block_dots": [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp],
     "gx_q6_k_block_dots": [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp],
+    "gx_gelu_table": [_vp, _vp],
+    "gx_moe_workspace_bytes": [_c_int, _c_int, _c_int, _c_int, _c_int, ctypes.POINTER(_c_size)],
+    "gx_moe_route": [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, ctypes.c_float, _vp, _vp, _vp],
+    "gx_moe_experts": [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _vp, _vp, _c_int, _vp, _c_size],
 }
 _RESTYPE = {"gx_last_error": ctypes.c_char_p}
 

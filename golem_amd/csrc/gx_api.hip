@@ -76,6 +76,20 @@ int gx_init(int device, gx_ctx **out) {
         delete ctx;
         return gx::fail(GX_ERR_HIP, "hipEventCreate failed");
     }
+    if (hipMalloc(&ctx->gelu_table, 65536 * sizeof(float)) != hipSuccess) {
+        delete ctx;
+        return gx::fail(GX_ERR_NOMEM, "gx: cannot allocate the GELU table");
+    }
+    if (int rc = gx::launch_gelu_table(ctx, ctx->gelu_table)) {
+        (void)hipFree(ctx->gelu_table);
+        delete ctx;
+        return rc;
+    }
+    if (hipStreamSynchronize(ctx->stream) != hipSuccess) {
+        (void)hipFree(ctx->gelu_table);
+        delete ctx;
+        return gx::fail(GX_ERR_HIP, "gx: building the GELU table failed");
+    }
     *out = ctx;
     return ok();
 }
@@ -86,6 +100,7 @@ int gx_free(gx_ctx *ctx) {
     (void)hipSetDevice(ctx->device);
     (void)hipEventDestroy(ctx->t0);
     (void)hipEventDestroy(ctx->t1);
+    (void)hipFree(ctx->gelu_table);
     delete ctx;
     return ok();
 }
@@ -446,6 +461,64 @@ int gx_q6_k_block_dots(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const i
     if (M == 0 || row_start == row_end)
         return ok();
     if (int rc = gx::launch_q6_k_matvec(ctx, w, q, nullptr, bsums, M, row_start, row_end, nullptr, nullptr, 0, out))
+        return rc;
+    return ok();
+}
+
+// ---- mixture of experts --------------------------------------------------
+
+int gx_gelu_table(gx_ctx *ctx, float *out) {
+    if (int rc = use(ctx))
+        return rc;
+    GX_CHECK(out != nullptr, "gx: no output");
+    GX_HIP(hipMemcpyAsync(out, ctx->gelu_table, 65536 * sizeof(float), hipMemcpyDeviceToDevice, ctx->stream));
+    return ok();
+}
+
+int gx_moe_workspace_bytes(int M, int top_k, int dim, int ffn, int experts, size_t *bytes) {
+    GX_CHECK(bytes != nullptr, "gx: no place for the size");
+    GX_CHECK(M >= 0 && top_k > 0 && dim > 0 && ffn > 0 && experts > 0, "gx: bad mixture shape");
+    return gx::moe_workspace_bytes(M, top_k, dim, ffn, experts, bytes) == GX_OK ? ok() : GX_ERR_INVALID;
+}
+
+int gx_moe_route(gx_ctx *ctx, const gx_weight *router, const float *router_scale, const float *resid, int ldr, int M,
+                 int top_k, float eps, float *logits, int32_t *ids, float *weights) {
+    if (int rc = use(ctx))
+        return rc;
+    GX_CHECK(router != nullptr && router->quant == GX_F32 && router->count == 1, "gx: the router is an F32 matrix");
+    GX_CHECK(top_k > 0 && top_k <= router->rows && top_k <= 64, "gx: top_k %d out of range for %d experts", top_k,
+             router->rows);
+    GX_CHECK(M >= 0 && ldr >= router->cols, "gx: bad residual shape");
+    GX_CHECK(resid && logits && ids && weights, "gx: missing argument");
+    if (M == 0)
+        return ok();
+    if (int rc = gx::launch_moe_route(ctx, router, router_scale, resid, ldr, M, top_k, eps, logits, ids, weights))
+        return rc;
+    return ok();
+}
+
+int gx_moe_experts(gx_ctx *ctx, const gx_weight *gate_up, const gx_weight *down, const float *down_scale,
+                   const float *x, int ldx, int M, int top_k, const int32_t *ids, const float *weights, float *out,
+                   int ldo, void *workspace, size_t workspace_bytes) {
+    if (int rc = use(ctx))
+        return rc;
+    GX_CHECK(gate_up && down && gate_up->quant == GX_Q4_0 && down->quant == GX_Q4_0,
+             "gx: the expert stacks are Q4_0 matrices");
+    GX_CHECK(gate_up->count == down->count, "gx: %d gate_up experts but %d down experts", gate_up->count, down->count);
+    GX_CHECK(gate_up->rows == 2 * down->cols && down->rows == gate_up->cols,
+             "gx: gate_up is %dx%d and down %dx%d: want 2F x D and D x F", gate_up->rows, gate_up->cols, down->rows,
+             down->cols);
+    GX_CHECK(top_k > 0 && top_k <= gate_up->count, "gx: top_k %d out of range", top_k);
+    GX_CHECK(M >= 0 && ldx >= gate_up->cols && ldo >= gate_up->cols, "gx: bad batch shape");
+    GX_CHECK(x && ids && weights && out && workspace, "gx: missing argument");
+    GX_CHECK(((uintptr_t)workspace & 255) == 0, "gx: the workspace must be 256-byte aligned");
+    size_t need = 0;
+    gx::moe_workspace_bytes(M, top_k, gate_up->cols, down->cols, gate_up->count, &need);
+    GX_CHECK(workspace_bytes >= need, "gx: the workspace holds %zu bytes, %zu needed", workspace_bytes, need);
+    if (M == 0)
+        return ok();
+    if (int rc = gx::launch_moe_experts(ctx, gate_up, down, down_scale, x, ldx, M, top_k, ids, weights, out, ldo,
+                                        (uint8_t *)workspace, ctx->gelu_table))
         return rc;
     return ok();
 }

@@ -93,10 +93,17 @@ struct Fetch {
     float da[2];
 };
 
+// The activation rows a thread stages are fixed for the whole product: its
+// four chunks belong to tokens tid/8 + 32 k, its scales to token tid/2.  They
+// are resolved once (through the expert groups' gather list when grouped).
+struct Rows {
+    const int8_t *a[4];
+    const float *s;
+};
+
 template <bool DOTS>
 __device__ __forceinline__ void fetch_stage(Fetch &f, const uint8_t *__restrict__ W, size_t plane0_bytes, int B,
-                                            int DC, const int8_t *__restrict__ q, const float *__restrict__ scales,
-                                            int K, int M, int tile, int m0, int h, int tid) {
+                                            int DC, const Rows &rows, int tile, int h, int tid) {
     const int b0 = h * kStage;
     {
         const int b = min(b0 + (tid >> 6), B - 1);
@@ -105,9 +112,8 @@ __device__ __forceinline__ void fetch_stage(Fetch &f, const uint8_t *__restrict_
 #pragma unroll
     for (int k = 0; k < 4; k++) {
         const int c = tid + 256 * k;
-        const int m = min(m0 + (c >> 3), M - 1);
         const int b = min(b0 + ((c & 7) >> 1), B - 1);
-        f.a[k] = *(const v4u *)(q + (size_t)m * K + (size_t)b * kQ4Block + 16 * (c & 1));
+        f.a[k] = *(const v4u *)(rows.a[k] + (size_t)b * kQ4Block + 16 * (c & 1));
     }
     if (!DOTS) {
         if (tid < 64) {
@@ -116,12 +122,22 @@ __device__ __forceinline__ void fetch_stage(Fetch &f, const uint8_t *__restrict_
             f.dw0 = chunk[(b0 & 7) >> 1];
             f.dw1 = chunk[((b0 & 7) >> 1) + 1];
         }
-        const int m = min(m0 + (tid >> 1), M - 1);
 #pragma unroll
         for (int k = 0; k < 2; k++)
-            f.da[k] = scales[(size_t)m * B + min(b0 + 2 * (tid & 1) + k, B - 1)];
+            f.da[k] = rows.s[min(b0 + 2 * (tid & 1) + k, B - 1)];
     }
 }
+
+// A mixture-of-experts product runs grouped: workgroup row y of the grid is
+// work item y, {expert, first, count}, covering units sorted[first ..
+// first + count) of one expert (count 0: nothing to do).  Unit u reads
+// activation row u / act_div and writes output row u.
+struct Groups {
+    const int32_t *work;
+    const int32_t *sorted;
+    int act_div;
+    size_t matrix_bytes;
+};
 
 template <bool DOTS>
 __device__ __forceinline__ void commit_stage(const Fetch &f, Stage &t, int nb, int tid) {
@@ -144,22 +160,44 @@ __device__ __forceinline__ void commit_stage(const Fetch &f, Stage &t, int nb, i
     }
 }
 
-template <bool DOTS>
+template <bool DOTS, bool GROUPED>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) void q4_0_gemm_kernel(
     const uint8_t *__restrict__ W, size_t plane0_bytes, int B, int DC, const int8_t *__restrict__ q,
     const float *__restrict__ scales, int K, int M, int tile0, int row_start, int row_end,
-    const float *__restrict__ bias, float *__restrict__ y, int ldy, int32_t *__restrict__ dots) {
+    const float *__restrict__ bias, float *__restrict__ y, int ldy, int32_t *__restrict__ dots, Groups grp) {
     __shared__ Stage st[2];
     const int tid = threadIdx.x;
     const int lane = tid & 63, wv = tid >> 6;
     const int tile = tile0 + blockIdx.x;
     const int n0 = tile * kTileRows;
-    const int m0 = blockIdx.y * kTokTile;
     const int nw = 32 * (wv & 1), mw = 64 * (wv >> 1);
     const int li = lane & 31, g = lane >> 5;
     const uint32_t sh = 4u * g;
     const int H = (B + kStage - 1) / kStage;  // stages; two make a stretch
     const int nrows = row_end - row_start;
+
+    // Local token t of this workgroup -> activation row and output row.
+    int first = blockIdx.y * kTokTile, count = min(kTokTile, M - first);
+    if (GROUPED) {
+        const int *item = grp.work + 4 * blockIdx.y;
+        count = item[2];
+        if (count <= 0)
+            return;
+        W += (size_t)item[0] * grp.matrix_bytes;
+        first = item[1];
+    }
+    auto act_row = [&](int t) -> int {
+        t = min(t, count - 1);
+        return GROUPED ? grp.sorted[first + t] / grp.act_div : first + t;
+    };
+    auto out_row = [&](int t) -> int { return t < count ? (GROUPED ? grp.sorted[first + t] : first + t) : -1; };
+    Rows rows;
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+        rows.a[k] = q + (size_t)act_row((tid >> 3) + 32 * k) * K;
+    rows.s = DOTS ? nullptr : scales + (size_t)act_row(tid >> 1) * B;
+    const int bm0 = out_row(mw + li), bm1 = out_row(mw + 32 + li);
+    const bool v0 = bm0 >= 0, v1 = bm1 >= 0;
 
     v16f acc0, acc1, tot0, tot1;
 #pragma unroll
@@ -167,17 +205,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
         acc0[e] = acc1[e] = tot0[e] = tot1[e] = 0.0f;
     const v16i zero_i = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
     const v16f zero_f = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-    const int bm0 = m0 + mw + li, bm1 = bm0 + 32;
-    const bool v0 = bm0 < M, v1 = bm1 < M;
 
     Fetch f;
-    fetch_stage<DOTS>(f, W, plane0_bytes, B, DC, q, scales, K, M, tile, m0, 0, tid);
+    fetch_stage<DOTS>(f, W, plane0_bytes, B, DC, rows, tile, 0, tid);
     commit_stage<DOTS>(f, st[0], min(kStage, B), tid);
     __syncthreads();
     for (int h = 0; h < H; h++) {
         Stage &cur = st[h & 1];
         if (h + 1 < H)  // in flight during this stage's arithmetic
-            fetch_stage<DOTS>(f, W, plane0_bytes, B, DC, q, scales, K, M, tile, m0, h + 1, tid);
+            fetch_stage<DOTS>(f, W, plane0_bytes, B, DC, rows, tile, h + 1, tid);
         const int nb = min(kStage, B - h * kStage);
 #pragma unroll 2
         for (int j = 0; j < kStage; j++) {
@@ -465,15 +501,27 @@ int launch_q4_0_gemm(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, const 
     (void)qsum;  // the widened weights are signed: no recentring term
     const int tile0 = row_start / kTileRows;
     dim3 grid((row_end + kTileRows - 1) / kTileRows - tile0, (M + kTokTile - 1) / kTokTile);
+    const Groups none{nullptr, nullptr, 1, 0};
     if (dots)
-        q4_0_gemm_kernel<true><<<grid, 256, 0, ctx->stream>>>(mat, w->plane0_bytes, w->blocks, w->dchunks, q, scales,
-                                                              w->cols, M, tile0, row_start, row_end, bias, y, ldy,
-                                                              dots);
+        q4_0_gemm_kernel<true, false><<<grid, 256, 0, ctx->stream>>>(mat, w->plane0_bytes, w->blocks, w->dchunks, q,
+                                                                     scales, w->cols, M, tile0, row_start, row_end,
+                                                                     bias, y, ldy, dots, none);
     else
-        q4_0_gemm_kernel<false><<<grid, 256, 0, ctx->stream>>>(mat, w->plane0_bytes, w->blocks, w->dchunks, q,
-                                                               scales, w->cols, M, tile0, row_start, row_end, bias,
-                                                               y, ldy, dots);
+        q4_0_gemm_kernel<false, false><<<grid, 256, 0, ctx->stream>>>(mat, w->plane0_bytes, w->blocks, w->dchunks, q,
+                                                                      scales, w->cols, M, tile0, row_start, row_end,
+                                                                      bias, y, ldy, dots, none);
     return check_launch("q4_0_gemm");
+}
+
+int launch_q4_0_gemm_grouped(gx_ctx *ctx, const gx_weight *w, const int32_t *work, int max_items,
+                             const int32_t *sorted, int act_div, const int8_t *q, const float *scales, float *y,
+                             int ldy) {
+    dim3 grid(w->tiles, max_items);
+    const Groups grp{work, sorted, act_div, w->matrix_bytes};
+    q4_0_gemm_kernel<false, true><<<grid, 256, 0, ctx->stream>>>(w->dev, w->plane0_bytes, w->blocks, w->dchunks, q,
+                                                                 scales, w->cols, 0, 0, 0, w->rows, nullptr, y, ldy,
+                                                                 nullptr, grp);
+    return check_launch("q4_0_gemm_grouped");
 }
 
 }  // namespace gx

@@ -47,6 +47,7 @@ struct gx_ctx {
     hipStream_t stream;
     hipEvent_t t0, t1;
     int cu_count;
+    float *gelu_table;  // golem's 65536-entry GELU table, built on the device at init
 };
 
 struct gx_weight {
@@ -87,14 +88,26 @@ int launch_q4_0_matvec(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, cons
 int launch_q4_0_gemm(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, const int8_t *q, const float *scales,
                      const int32_t *qsum, int M, int row_start, int row_end, const float *bias, float *y, int ldy,
                      int32_t *dots);
+int launch_q4_0_gemm_grouped(gx_ctx *ctx, const gx_weight *w, const int32_t *work, int max_items,
+                             const int32_t *sorted, int act_div, const int8_t *q, const float *scales, float *y,
+                             int ldy);
 int launch_q4_0_gemm_f16(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, const uint16_t *q16,
                          const float *scales, int M, int row_start, int row_end, const float *bias, float *y, int ldy,
                          int32_t *dots);
+int launch_q4_0_matvec_units(gx_ctx *ctx, const gx_weight *w, const int32_t *unit_expert, int units, int act_div,
+                              const int8_t *q, const float *scales, const int32_t *qsum, float *y, int ldy);
 int launch_q4_0_block_dots_matvec(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const int32_t *qsum, int M,
                                   int row_start, int row_end, int32_t *out);
 int launch_q6_k_matvec(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const float *kscales,
                        const int16_t *bsums, int M, int row_start, int row_end, const float *bias, float *y,
                        int ldy, int32_t *dots);
+int moe_workspace_bytes(int M, int k, int D, int F, int E, size_t *bytes);
+int launch_gelu_table(gx_ctx *ctx, float *table);
+int launch_moe_route(gx_ctx *ctx, const gx_weight *router, const float *router_scale, const float *resid, int ldr,
+                     int M, int k, float eps, float *logits, int32_t *ids, float *weights);
+int launch_moe_experts(gx_ctx *ctx, const gx_weight *gate_up, const gx_weight *down, const float *down_scale,
+                       const float *x, int ldx, int M, int k, const int32_t *ids, const float *weights, float *out,
+                       int ldo, uint8_t *ws, const float *gelu_table);
 int launch_f32_matvec(gx_ctx *ctx, const gx_weight *w, const float *x, int ldx, int M, int row_start, int row_end,
                       float *y, int ldy);
 }  // namespace gx

@@ -27,17 +27,37 @@
 namespace gx {
 namespace {
 
-template <int NC>
+// With UNITS, blockIdx.y is a unit of a mixture-of-experts batch: unit u
+// multiplies expert unit_expert[u] of a stack (matrices matrix_bytes apart)
+// by activation row u / act_div, into output row u.
+template <int NC, bool UNITS>
 __global__ __launch_bounds__(1024) void q4_0_matvec_kernel(
     const uint8_t *__restrict__ W, size_t plane0_bytes, int B, int DC, const int8_t *__restrict__ q,
     const float *__restrict__ scales, const int32_t *__restrict__ qsum, int K, int tile0, int row_start,
-    int row_end, const float *__restrict__ bias, float *__restrict__ y, int ldy) {
+    int row_end, const float *__restrict__ bias, float *__restrict__ y, int ldy,
+    const int32_t *__restrict__ unit_expert, size_t matrix_bytes, int act_div, int experts) {
     extern __shared__ float part[];  // [S][NC][64]
     const int S = (B + kStretch - 1) / kStretch;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nwaves = blockDim.x >> 6;
     const int tile = tile0 + blockIdx.x;
+    if (UNITS) {
+        const int u = blockIdx.y;
+        const int e = unit_expert[u];
+        if (e < 0 || e >= experts) {  // an id out of range reads nothing and yields NaN
+            const int row = tile * kTileRows + lane;
+            if (threadIdx.x < 64 && row < row_end)
+                y[(size_t)u * ldy + row] = __builtin_nanf("");
+            return;
+        }
+        W += (size_t)e * matrix_bytes;
+        const int a = u / act_div;
+        q += (size_t)a * K;
+        scales += (size_t)a * B;
+        qsum += (size_t)a * B;
+        y += (size_t)u * ldy;
+    }
     const uint8_t *qs_row = W + ((size_t)tile * B * kTileRows + lane) * kChunk;
     const uint8_t *d_row = W + plane0_bytes + ((size_t)tile * DC * kTileRows + lane) * kChunk;
 
@@ -131,9 +151,9 @@ int launch_nc(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, const int8_t 
     GX_CHECK(lds <= 64 * 1024, "gx: a %d-input Q4_0 row is wider than this kernel's LDS", w->cols);
     const int tile0 = row_start / kTileRows;
     const int grid = (row_end + kTileRows - 1) / kTileRows - tile0;
-    q4_0_matvec_kernel<NC><<<grid, 64 * waves, lds, ctx->stream>>>(mat, w->plane0_bytes, B, w->dchunks, q, scales,
-                                                                   qsum, w->cols, tile0, row_start, row_end, bias, y,
-                                                                   ldy);
+    q4_0_matvec_kernel<NC, false><<<grid, 64 * waves, lds, ctx->stream>>>(
+        mat, w->plane0_bytes, B, w->dchunks, q, scales, qsum, w->cols, tile0, row_start, row_end, bias, y, ldy,
+        nullptr, 0, 1, 0);
     return check_launch("q4_0_matvec");
 }
 
@@ -174,6 +194,20 @@ int launch_q4_0_matvec(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, cons
             return rc;
     }
     return GX_OK;
+}
+
+int launch_q4_0_matvec_units(gx_ctx *ctx, const gx_weight *w, const int32_t *unit_expert, int units, int act_div,
+                              const int8_t *q, const float *scales, const int32_t *qsum, float *y, int ldy) {
+    const int B = w->blocks;
+    const int S = (B + kStretch - 1) / kStretch;
+    const int waves = min(S, 16);
+    const size_t lds = (size_t)S * kTileRows * sizeof(float);
+    GX_CHECK(lds <= 64 * 1024, "gx: a %d-input Q4_0 row is wider than this kernel's LDS", w->cols);
+    dim3 grid(w->tiles, units);
+    q4_0_matvec_kernel<1, true><<<grid, 64 * waves, lds, ctx->stream>>>(
+        w->dev, w->plane0_bytes, B, w->dchunks, q, scales, qsum, w->cols, 0, 0, w->rows, nullptr, y, ldy,
+        unit_expert, w->matrix_bytes, act_div, w->count);
+    return check_launch("q4_0_matvec_units");
 }
 
 int launch_q4_0_block_dots_matvec(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const int32_t *qsum, int M,

@@ -184,6 +184,41 @@ int gx_q4_0_block_dots(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const i
 int gx_q6_k_block_dots(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const int16_t *bsums, int M,
                        int row_start, int row_end, int32_t *out);
 
+/* ---- mixture of experts (gemma.ExpertFFN) ---------------------------- */
+
+/* golem's GELU table (nn/gelu_table.go:19-38), built on the device when the
+ * context opens: out receives 65536 floats (device), entry i for the fp16
+ * input with bits i. */
+int gx_gelu_table(gx_ctx *ctx, float *out);
+
+/* The device workspace gx_moe_experts needs for M positions of top_k
+ * experts, model width dim, expert width ffn, and `experts` experts. */
+int gx_moe_workspace_bytes(int M, int top_k, int dim, int ffn, int experts, size_t *bytes);
+
+/* Route (gemma/moe.go:34-53) and chooseExperts (:62-88) for M positions:
+ * resid[m*ldr ...] (device floats, dim = router->cols) is normalised by
+ * RMSNormPlain without a gain (eps), scaled by (1/sqrt(dim)) *
+ * router_scale[i] (router_scale may be NULL: ones), and multiplied by the F32
+ * router (experts x dim) in DotF32's generic order.  Outputs (device):
+ * logits [M][experts], ids [M][top_k], weights [M][top_k]. */
+int gx_moe_route(gx_ctx *ctx, const gx_weight *router, const float *router_scale, const float *resid, int ldr, int M,
+                 int top_k, float eps, float *logits, int32_t *ids, float *weights);
+
+/* The expert units and their weighted sum of ExpertFFN (gemma/moe.go:
+ * 112-180): for every position m and slot k, expert e = ids[m][k] of the
+ * stacks gate_up (2*ffn x dim per expert, gate rows first, as the fused
+ * tensor of gemma/README.md:276-278) and down (dim x ffn) computes
+ * Down[e] . Q8_0(GELUTable(gate) * up) with gate|up = GateUp[e] . Q8_0(x[m]);
+ * out[m] = sum_k (weights[m][k] * down_scale[e]) * that (down_scale may be
+ * NULL: ones).  Few positions run each unit as a matrix-vector product; more
+ * are sorted by expert and run as ragged MFMA batches, one per expert.  The
+ * workspace (device, 256-byte aligned, gx_moe_workspace_bytes) is the
+ * scratch golem keeps in its Scratch; no call allocates.  An id out of range
+ * makes its position's output NaN. */
+int gx_moe_experts(gx_ctx *ctx, const gx_weight *gate_up, const gx_weight *down, const float *down_scale,
+                   const float *x, int ldx, int M, int top_k, const int32_t *ids, const float *weights, float *out,
+                   int ldo, void *workspace, size_t workspace_bytes);
+
 #ifdef __cplusplus
 }
 #endif

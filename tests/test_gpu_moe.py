@@ -1,0 +1,175 @@
+"""The expert branch of golem's mixture of experts (gemma/moe.go:34-180)
+against the oracle.
+
+Selection: router logits bit for bit (golem's generic DotF32 order) and the
+chosen experts identical; the 8th/9th logit margin is logged, as
+gemma/moe_reference_test.go:117-136 does for its greedy ties.
+Outputs: within 2e-5 of RMS (the benchmark's bar for config 4), for the
+per-unit matrix-vector path (few positions) and the expert-grouped MFMA
+path (more positions); a position's output is bit-identical in either, the
+"batch == one at a time" of gemma/moe_test.go:164-201.
+"""
+import numpy as np
+import pytest
+
+from golem_amd import capi, synth
+from tests.gpu_util import log
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-5
+
+
+class Moe:
+    def __init__(self, dev, D, F, E, k, seed):
+        g = synth.rng(seed)
+        self.D, self.F, self.E, self.k = D, F, E, k
+        self.gate_up = synth.q4_0_weights(g, E * 2 * F, D)
+        self.down = synth.q4_0_weights(g, E * D, F)
+        self.router = (g.standard_normal((E, D)) * 0.02).astype(np.float32)
+        self.g = g
+        self.dev = dev
+        self.wgu = dev.weight(self.gate_up, capi.Q4_0, 2 * F, D, count=E)
+        self.wdn = dev.weight(self.down, capi.Q4_0, D, F, count=E)
+        self.wr = dev.weight(self.router, capi.F32, E, D)
+
+    def expert_bytes(self, stack, rows, cols, e):
+        n = rows * (cols // 32) * 18
+        return stack[e * n:(e + 1) * n]
+
+    def route(self, x):
+        dev = self.dev
+        M = x.shape[0]
+        xd = dev.put(x)
+        logits = dev.empty((M, self.E), np.float32)
+        ids = dev.empty((M, self.k), np.int32)
+        w = dev.empty((M, self.k), np.float32)
+        capi.call("gx_moe_route", dev.ctx.ptr, self.wr.ptr, None, capi.vp(xd), self.D, M, self.k,
+                  np.float32(1e-6), capi.vp(logits), capi.vp(ids), capi.vp(w))
+        return logits, ids, w
+
+    def experts(self, x, ids, w):
+        dev = self.dev
+        M = x.shape[0]
+        import ctypes
+        n = ctypes.c_size_t()
+        capi.call("gx_moe_workspace_bytes", M, self.k, self.D, self.F, self.E, ctypes.byref(n))
+        ws = dev.empty((n.value + 256,), np.uint8)
+        xd = dev.put(x)
+        out = dev.full((M, self.D), float("nan"))
+        capi.call("gx_moe_experts", dev.ctx.ptr, self.wgu.ptr, self.wdn.ptr, None, capi.vp(xd), self.D, M, self.k,
+                  capi.vp(ids), capi.vp(w), capi.vp(out), self.D, capi.vp(ws), n.value)
+        return out
+
+    def oracle(self, orc, x, ids, weights):
+        """ExpertFFN through the oracle for the given choices."""
+        out = np.zeros((x.shape[0], self.D), dtype=np.float32)
+        for t in range(x.shape[0]):
+            partials = np.stack([orc.expert_unit(self.expert_bytes(self.gate_up, 2 * self.F, self.D, e),
+                                                 self.expert_bytes(self.down, self.D, self.F, e), x[t], self.D,
+                                                 self.F) for e in ids[t]])
+            out[t] = orc.expert_reduce(partials, ids[t], weights[t], self.D)
+        return out
+
+
+def test_gelu_table_matches_oracle_exhaustively(dev, orc):
+    got = dev.empty((65536,), np.float32)
+    capi.call("gx_gelu_table", dev.ctx.ptr, capi.vp(got))
+    got = dev.get(got)
+    want = orc.gelu_table_build()
+    # every fp16 input that GELUTable can index: finite halves of magnitude < 10
+    h = np.arange(65536, dtype=np.uint16)
+    v = h.view(np.float16).astype(np.float32)
+    used = np.isfinite(v) & (np.abs(v) < 10)
+    assert np.array_equal(got[used].view(np.uint32), want[used].view(np.uint32))
+
+
+@pytest.mark.parametrize("D,E,k,M", [(2816, 128, 8, 6), (512, 16, 4, 3)])
+def test_route_bit_exact(dev, orc, D, E, k, M):
+    m = Moe.__new__(Moe)
+    g = synth.rng(40 + E)
+    m.D, m.E, m.k, m.dev = D, E, k, dev
+    m.router = (g.standard_normal((E, D)) * 0.02).astype(np.float32)
+    m.wr = dev.weight(m.router, capi.F32, E, D)
+    x = synth.activations(g, M, D)
+    x[1] *= 1e-3
+    logits, ids, w = m.route(x)
+    logits, ids, w = dev.get(logits), dev.get(ids), dev.get(w)
+    for t in range(M):
+        ol, oi, ow = orc.route_one(x[t], m.router, k)
+        np.testing.assert_array_equal(logits[t].view(np.uint32), ol.view(np.uint32))
+        np.testing.assert_array_equal(ids[t], oi)
+        np.testing.assert_allclose(w[t], ow, rtol=1e-6, atol=0)
+        srt = np.sort(ol)[::-1]
+        log(f"position {t}: experts {list(oi)}, k-th/next logit margin {srt[k - 1] - srt[k]:.3g}")
+
+
+def test_route_ties_go_to_lower_index(dev, orc):
+    """TestChooseExpertsIsStableInTies (gemma/moe_test.go:234-244) through the
+    device router: two identical router rows give identical logits, and the
+    lower index is chosen first."""
+    g = synth.rng(5)
+    D, E, k = 256, 8, 3
+    router = (g.standard_normal((E, D)) * 0.02).astype(np.float32)
+    router[5] = router[2]
+    router[2] *= 10
+    router[5] = router[2]
+    m = Moe.__new__(Moe)
+    m.D, m.E, m.k, m.dev = D, E, k, dev
+    m.router = router
+    m.wr = dev.weight(router, capi.F32, E, D)
+    x = (router[2] * 100)[None, :].astype(np.float32)  # experts 2 and 5 (equal rows) score highest
+    logits, ids, w = m.route(x)
+    logits, ids = dev.get(logits)[0], dev.get(ids)[0]
+    assert logits[2] == logits[5] and logits[2] > np.delete(logits, [2, 5]).max()
+    assert ids[0] == 2 and ids[1] == 5
+
+
+@pytest.mark.parametrize("M", [1, 2, 20])
+def test_experts_against_golem(dev, orc, M):
+    """Small shape: the matrix-vector path (M <= 4) and the grouped path."""
+    D, F, E, k = 512, 128, 16, 4
+    moe = Moe(dev, D, F, E, k, 50)
+    x = synth.activations(moe.g, M, D)
+    logits, ids, w = moe.route(x)
+    out = dev.get(moe.experts(x, ids, w))
+    want = moe.oracle(orc, x, dev.get(ids), dev.get(w))
+    for t in range(M):
+        rel, at = orc.compare_floats(out[t], want[t])
+        assert rel <= TOL, f"M={M} position {t}: {rel:.3g} of RMS at {at}"
+
+
+def test_config4_decode_and_prefill(dev, orc):
+    """Config 4's shape (hidden 2816, 128 experts of width 704, top 8): decode
+    of one position, and a 40-position batch grouped by expert, each checked
+    against golem through the oracle; the batch's positions are
+    bit-identical to the same positions alone."""
+    D, F, E, k = 2816, 704, 128, 8
+    moe = Moe(dev, D, F, E, k, 4)
+    M = 40
+    x = synth.activations(moe.g, M, D)
+    logits, ids, w = moe.route(x)
+    log("config 4: routed")
+    batch = dev.get(moe.experts(x, ids, w))
+    idh, wh = dev.get(ids), dev.get(w)
+    want = moe.oracle(orc, x[:3], idh[:3], wh[:3])
+    for t in range(3):
+        rel, at = orc.compare_floats(batch[t], want[t])
+        assert rel <= TOL, f"position {t}: {rel:.3g} of RMS at {at}"
+    for t in (0, 7, 39):
+        one = dev.get(moe.experts(x[t:t + 1], ids[t:t + 1], w[t:t + 1]))
+        np.testing.assert_array_equal(one[0].view(np.uint32), batch[t].view(np.uint32))
+    log("config 4: decode and grouped prefill agree")
+
+
+def test_bad_expert_id_poisons_its_position(dev):
+    D, F, E, k = 256, 64, 4, 2
+    moe = Moe(dev, D, F, E, k, 60)
+    for M in (1, 6):
+        x = synth.activations(moe.g, M, D)
+        ids = np.tile(np.array([0, 1], dtype=np.int32), (M, 1))
+        ids[0, 1] = 9  # out of range
+        w = np.full((M, k), 0.5, dtype=np.float32)
+        out = dev.get(moe.experts(x, dev.put(ids), dev.put(w)))
+        assert np.all(np.isnan(out[0]))
+        assert not np.any(np.isnan(out[1:]))
