@@ -40,7 +40,9 @@ def parse():
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-extra", action="store_true", help="skip the config 0 / config 2 measurements")
-    p.add_argument("--only", default="", help="profiling: run only this leg (c1, c0, c2) and exit")
+    p.add_argument("--only", default="",
+                   help="profiling: run only this leg (c1, c0, c2, c4) and exit; 'copy' runs the 256 MiB "
+                        "device copy that scales the FETCH_SIZE / WRITE_SIZE counters")
     return p.parse_args()
 
 
@@ -69,6 +71,18 @@ def main():
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     torch.cuda.init()
+    if args.only == "copy":
+        # A plain copy of known size: FETCH_SIZE / WRITE_SIZE per dispatch of
+        # it, against 256 MiB read and 256 MiB written, give the factors that
+        # turn those counters into bytes.
+        n = 256 << 20
+        a = torch.full((n // 4,), 1.0, dtype=torch.float32, device="cuda")
+        b = torch.empty_like(a)
+        for _ in range(5):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"leg": "copy", "bytes": n, "dispatches": 5}))
+        return
     stream = torch.cuda.current_stream()
     ctx = capi.Context(0, stream=stream.cuda_stream)
     call = capi.call

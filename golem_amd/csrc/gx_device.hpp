@@ -25,6 +25,15 @@ __device__ __forceinline__ float chunk_half(const uint4 &c, int j) {
     return half_bits_to_float((j & 1) ? (word >> 16) : word);
 }
 
+// A 16-byte load of weights that are streamed once per product: the
+// non-temporal hint keeps them from displacing the activations and outputs
+// in the caches (global_load ... nt).
+typedef unsigned v4u_stream __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 load_stream(const uint8_t *p) {
+    const v4u_stream v = __builtin_nontemporal_load((const v4u_stream *)p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 // golem's nearestInt (nn/batch.go:221-224): round half to even by adding
 // 1.5*2^23 and reading the low mantissa bits.
 __device__ __forceinline__ int32_t nearest_int(float f) {
@@ -60,10 +69,10 @@ __device__ __forceinline__ int32_t q4_0_block_isum(const uint4 &w, const int4 &a
 // sum_g sc[g] * (sum_{k in g} q6_k * a_k - 32 * bsum[g]).  The 6-bit values
 // are assembled four bytes at a time from the ql/qh chunks.
 //   ql: 32 dwords (128 bytes), qh: 16 dwords (64 bytes), sc: 16 int8 (per
-//   lane); a: 64 dwords (256 int8), bsum: 16 int16 (read where they lie, so a
-//   wavefront-uniform activation becomes scalar loads).
+//   lane); a: 64 dwords (256 int8), bsum: 8 dwords (16 int16), both read
+//   where they lie, so a wavefront-uniform activation becomes scalar loads.
 __device__ __forceinline__ int32_t q6_k_block_isum(const uint32_t *ql, const uint32_t *qh, const uint4 &sc,
-                                                   const uint32_t *__restrict__ A, const int16_t *__restrict__ bs) {
+                                                   const uint32_t *__restrict__ A, const uint32_t *__restrict__ bs) {
     const uint32_t scw[4] = {sc.x, sc.y, sc.z, sc.w};
     int32_t isum = 0;
 #pragma unroll
@@ -89,7 +98,8 @@ __device__ __forceinline__ int32_t q6_k_block_isum(const uint32_t *ql, const uin
         for (int i = 0; i < 8; i++) {
             const int gi = 8 * h + i;
             const int32_t s = (int32_t)(int8_t)(scw[gi >> 2] >> (8 * (gi & 3)));
-            isum += s * (g[i] - 32 * (int32_t)bs[gi]);
+            const int32_t b = (int32_t)(int16_t)(bs[gi >> 1] >> (16 * (gi & 1)));  // bsum pairs as words
+            isum += s * (g[i] - 32 * b);
         }
     }
     return isum;

@@ -70,7 +70,7 @@ __global__ __launch_bounds__(1024) void q4_0_matvec_kernel(
         uint4 wq[kStretch];
 #pragma unroll
         for (int j = 0; j < kStretch; j++)
-            wq[j] = *(const uint4 *)(qs_row + (size_t)min(b0 + j, B - 1) * kTileRows * kChunk);
+            wq[j] = load_stream(qs_row + (size_t)min(b0 + j, B - 1) * kTileRows * kChunk);
         const uint4 dch = *(const uint4 *)(d_row + (size_t)s * kTileRows * kChunk);
         float p[NC];
 #pragma unroll

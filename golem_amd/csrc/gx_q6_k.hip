@@ -38,21 +38,21 @@ __global__ __launch_bounds__(1024) void q6_k_matvec_kernel(
         uint32_t ql[32], qh[16];
 #pragma unroll
         for (int c = 0; c < 8; c++) {
-            const uint4 v = *(const uint4 *)(base + (size_t)c * kTileRows * kChunk);
+            const uint4 v = load_stream(base + (size_t)c * kTileRows * kChunk);
             ql[4 * c] = v.x, ql[4 * c + 1] = v.y, ql[4 * c + 2] = v.z, ql[4 * c + 3] = v.w;
         }
 #pragma unroll
         for (int c = 0; c < 4; c++) {
-            const uint4 v = *(const uint4 *)(base + (size_t)(8 + c) * kTileRows * kChunk);
+            const uint4 v = load_stream(base + (size_t)(8 + c) * kTileRows * kChunk);
             qh[4 * c] = v.x, qh[4 * c + 1] = v.y, qh[4 * c + 2] = v.z, qh[4 * c + 3] = v.w;
         }
-        const uint4 sc = *(const uint4 *)(base + (size_t)12 * kTileRows * kChunk);
+        const uint4 sc = load_stream(base + (size_t)12 * kTileRows * kChunk);
         const float d = half_bits_to_float(*(const uint16_t *)(d_row + (size_t)(s >> 3) * kTileRows * kChunk +
                                                               (size_t)(s & 7) * 2));
 #pragma unroll
         for (int c = 0; c < NC; c++) {
             const uint32_t *a = (const uint32_t *)(q + (size_t)c * K + (size_t)s * kSuper);
-            const int16_t *bs = bsums + (size_t)c * (K / 16) + (size_t)s * 16;
+            const uint32_t *bs = (const uint32_t *)(bsums + (size_t)c * (K / 16) + (size_t)s * 16);
             const int32_t isum = q6_k_block_isum(ql, qh, sc, a, bs);
             if (dots) {
                 if (row >= row_start && row < row_end)
