@@ -11,11 +11,14 @@ The weights rotate over two resident copies (640 MB together) so that no
 step finds the previous step's weights in the 256 MB Infinity Cache.
 
 Also reported, measured the same way with HIP events on the library's
-stream: config 0 (Q4_0 matvec 9728x2560, rotating over 20 copies = 281 MB)
-and config 2 (the Q4_0 x Q8_0 MFMA product at M = 64, 512, 2048).
+stream: config 0 (Q4_0 matvec 9728x2560, rotating over 20 copies = 281 MB),
+config 2 (the Q4_0 x Q8_0 MFMA product at M = 64, 512, 2048) and config 4
+(the Gemma-shaped MoE layer: route + experts, decode and a 256-position
+prefill).
 
-cpu_baseline: the oracle (golem's generic Go arithmetic restated in C,
-single-threaded) timed on this host over a bounded sample of config 1, and
+cpu_baseline: golem's x86 path -- its AVX2 kernels and worker pool, restated
+in C with intrinsics (oracle/cpu_avx2.c) -- timed on this host's allowed
+threads over a bounded sample of config 1 (and one thread beside it), and
 used at the same time to check the GPU's logits bit for bit.
 """
 import argparse
@@ -201,25 +204,17 @@ def main():
             print(json.dumps(extra))
             return
 
-    # ---- CPU baseline: the oracle on this host, and the check --------------
+    # ---- config 4: Gemma-shaped MoE layer (route + experts) ----------------
+    if not args.no_extra and args.only in ("", "c4"):
+        extra.update(bench_c4(ctx, torch, dev))
+        if args.only == "c4":
+            print(json.dumps(extra))
+            return
+
+    # ---- CPU baseline: golem's AVX2 path on this host's cores, and the check --
     cpu = None
     if not args.no_cpu:
-        import oracle
-        b = oracle.Batch(x).quantize_k()
-        passes = 3
-        t0 = time.perf_counter()
-        for _ in range(passes):
-            want = oracle.mat_vec_q6_k_rows(w6, b, rows)
-        t1 = time.perf_counter()
-        cpu_gbs = passes * step_bytes / (t1 - t0) / 1e9
-        step(0)  # recompute on copy 0 for the bit-for-bit check
-        torch.cuda.synchronize()
-        got = y.cpu().numpy()
-        exact = bool(np.array_equal(got.view(np.uint32), want.view(np.uint32)))
-        cpu = {"value": round(cpu_gbs, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-               "sample": f"{passes} full passes of config 1 (151936x2560 Q6_K, M=1) through the oracle's "
-                         f"dotQ6_KGo restatement, {t1 - t0:.2f} s",
-               "gpu_logits_bit_exact": exact}
+        cpu = cpu_baseline(w6, x, rows, cols, step_bytes, step, y, torch, args.no_extra)
 
     traffic = read_traffic("q6_k_matvec_c1_traffic.txt")
     out = {
@@ -249,6 +244,122 @@ def main():
     for w_ in copies:
         w_.free()
     ctx.close()
+
+
+def cpu_baseline(w6, x, rows, cols, step_bytes, step, y, torch, no_extra):
+    """golem's x86 path restated (oracle/cpu_avx2.c: dotQ6_KAVX2 and the
+    worker pool of nn/parallel.go) timed on this host: config 1 over two
+    rotating weight copies (640 MB, past the last-level cache) for ~10 s on
+    every allowed thread and ~3 s on one; the GPU's logits are checked bit for
+    bit against it.  Config 0 (Q4_0, dotQ4_0AVX2 under matVecQ4_0Rows) is
+    timed the same way for ~3 s."""
+    import oracle
+    threads = oracle.host_threads()
+    oracle.cpu_lib(threads)
+
+    def timed(fn, budget):
+        fn(0)
+        n, t0 = 0, time.perf_counter()
+        while True:
+            fn(n)
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= budget:
+                return n, el
+
+    b = oracle.Batch(x).quantize_k()
+    hw = [w6, w6.copy()]
+    yc = np.zeros((1, rows), dtype=np.float32)
+    n_all, t_all = timed(lambda i, th=threads: oracle.cpu_mat_vec_q6_k(hw[i & 1], b, rows, th, yc), 10.0)
+    n_one, t_one = timed(lambda i: oracle.cpu_mat_vec_q6_k(hw[i & 1], b, rows, 1, yc), 3.0)
+    oracle.cpu_mat_vec_q6_k(w6, b, rows, threads, yc)
+    step(0)  # recompute on copy 0 for the bit-for-bit check
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    exact = bool(np.array_equal(got.view(np.uint32), yc.view(np.uint32)))
+    out = {"value": round(n_all * step_bytes / t_all / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
+           "sample": f"{n_all} passes of config 1 (151936x2560 Q6_K, M=1) through golem's AVX2 Q6_K kernel and "
+                     f"worker pool restated in C, {threads} threads, 2 rotating weight copies, {t_all:.1f} s",
+           "one_thread_value": round(n_one * step_bytes / t_one / 1e9, 2),
+           "gpu_logits_bit_exact": exact}
+    if not no_extra:
+        from golem_amd import synth
+        r0, c0 = 9728, 2560
+        g0 = synth.rng(0)
+        w0 = synth.q4_0_weights(g0, r0, c0)
+        b0 = oracle.Batch(synth.activations(g0, 1, c0)).quantize()
+        h0 = [w0] + [w0.copy() for _ in range(19)]
+        y0 = np.zeros((1, r0), dtype=np.float32)
+        n0, t0 = timed(lambda i: oracle.cpu_mat_vec_q4_0(h0[i % 20], b0, r0, threads, y0), 3.0)
+        by0 = r0 * (c0 // 32) * 18 + c0 + 8 * (c0 // 32) + 4 * r0
+        out["c0_q4_0_matvec"] = {"GB/s": round(n0 * by0 / t0 / 1e9, 2), "us_per_pass": round(t0 / n0 * 1e6, 1),
+                                 "cores": threads, "passes": n0}
+    return out
+
+
+def bench_c4(ctx, torch, dev):
+    """Config 4: router (128 x 2816 fp32) + top-8 + 8 GELU-gated Q4_0 experts
+    per position (gate_up 1408 x 2816, down 2816 x 704), seed 4. Decode (one
+    position) and a 256-position prefill grouped by expert, each timed as
+    route + experts with HIP events. Two copies of the expert stacks (856 MB,
+    beyond the 256 MB last-level cache) alternate between steps, and decode
+    walks 64 different positions, so the experts a step reads are not cached."""
+    from golem_amd import capi, synth
+    import ctypes
+    call, vp = capi.call, capi.vp
+    D, F, E, k = 2816, 704, 128, 8
+    g = synth.rng(4)
+    router = (g.standard_normal((E, D)) * 0.02).astype(np.float32)
+    gate_up = synth.q4_0_weights(g, E * 2 * F, D)
+    down = synth.q4_0_weights(g, E * D, F)
+    wr = capi.Weight(ctx, router, capi.F32, E, D)
+    stacks = [(capi.Weight(ctx, gate_up, capi.Q4_0, 2 * F, D, count=E),
+               capi.Weight(ctx, down, capi.Q4_0, D, F, count=E)) for _ in range(2)]
+    expert_bytes = (2 * F * (D // 32) + D * (F // 32)) * 18
+    res = {}
+    for label, M, npos in (("decode", 1, 64), ("prefill256", 256, 2)):
+        xs = [dev(synth.activations(g, M, D)) for _ in range(npos)]
+        logits = torch.empty((M, E), dtype=torch.float32, device="cuda")
+        ids = torch.empty((M, k), dtype=torch.int32, device="cuda")
+        wts = torch.empty((M, k), dtype=torch.float32, device="cuda")
+        out = torch.empty((M, D), dtype=torch.float32, device="cuda")
+        n = ctypes.c_size_t()
+        call("gx_moe_workspace_bytes", M, k, D, F, E, ctypes.byref(n))
+        ws = torch.empty((n.value,), dtype=torch.uint8, device="cuda")
+
+        def step(i):
+            x = xs[i % npos]
+            gu, dn = stacks[i & 1]
+            call("gx_moe_route", ctx.ptr, wr.ptr, None, vp(x), D, M, k, np.float32(1e-6), vp(logits), vp(ids),
+                 vp(wts))
+            call("gx_moe_experts", ctx.ptr, gu.ptr, dn.ptr, None, vp(x), D, M, k, vp(ids), vp(wts), vp(out), D,
+                 vp(ws), n.value)
+
+        for i in range(6):
+            step(i)
+        torch.cuda.synchronize()
+        # distinct experts each position set reads, for the algorithmic bytes
+        touched = []
+        for i in range(npos):
+            step(i)
+            torch.cuda.synchronize()
+            touched.append(len(np.unique(ids.cpu().numpy())))
+        reps = 128 if M == 1 else 20
+        ctx.timer_start()
+        for i in range(reps):
+            step(i)
+        ms = ctx.timer_stop() / reps
+        mean_touched = float(np.mean(touched))
+        by = mean_touched * expert_bytes + E * D * 4 + M * D * 4 * 2
+        res[f"c4_moe_{label}"] = {
+            "M": M, "ms_per_layer": round(ms, 4), "positions_per_s": round(M / (ms * 1e-3), 1),
+            "experts_read": round(mean_touched, 2), "bytes_per_layer": int(by),
+            "GB/s": round(by / (ms * 1e-3) / 1e9, 1), "hbm_frac": round(by / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    wr.free()
+    for gu, dn in stacks:
+        gu.free()
+        dn.free()
+    return res
 
 
 if __name__ == "__main__":

@@ -21,8 +21,6 @@
 namespace gx {
 namespace {
 
-constexpr int kRouteThreads = 512;
-
 // golem's GELU table (nn/gelu_table.go:25-38): for every fp16 input,
 // fp16(float32(geluTanh(float64(input)))), held as float.
 __global__ void gelu_table_kernel(float *__restrict__ table) {
@@ -37,101 +35,248 @@ __global__ void gelu_table_kernel(float *__restrict__ table) {
     table[i] = half_bits_to_float(float_to_half_bits((float)g));
 }
 
-// Route for one position per workgroup.
-__global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(const float *__restrict__ router, int D, int E,
-                                                                  const float *__restrict__ router_scale,
-                                                                  const float *__restrict__ resid, int ldr, int k,
-                                                                  float eps, float *__restrict__ logits,
-                                                                  int32_t *__restrict__ ids,
-                                                                  float *__restrict__ weights) {
-    extern __shared__ float xr[];  // D floats, then E logits
-    __shared__ double part[kRouteThreads];
-    __shared__ float chains[kRouteThreads];
-    const int tid = threadIdx.x;
-    const int t = blockIdx.x;
-    const float *x = resid + (size_t)t * ldr;
-    float *lg = xr + D;
+// The router in two kernels.
+//
+// moe_logits_kernel<EW>: a workgroup holds EW router rows in LDS and computes
+// their logits for P = 64/EW positions; lane = (position, expert, chain).
+// DotF32 (nn/dot_f32.go:13-33) is four serial chains -- chain c adds the
+// products of elements c, c+4, c+8, ... in order -- that meet as
+// (s0 + s1) + (s2 + s3); each lane runs one chain in that order, so the
+// logits are golem's bits.  The normalised input reaches the chains in
+// 64-element chunks, double-buffered through LDS, so a chain step is two LDS
+// reads, a multiply and an add, and the global loads of the next chunk are in
+// flight meanwhile.
+//
+// RMSNormPlain (nn/ops.go:195-214) squares in float32 and sums in float64.
+// The sum is taken in a fixed tree: 512 partial sums, partial t holding
+// elements t, t+512, t+1024, ... in order, then halved pairwise (t + w for
+// w = 256 .. 1).  golem sums left to right; the two float64 sums differ by a
+// few units in the 53rd bit, below the float32 rounding of the mean except in
+// rare ties.
+constexpr int kLogitsThreads = 256;
+constexpr int kLogitsChunk = 64;     // inputs per chunk
+constexpr int kLogitsChunkPad = 68;  // chunk row stride in LDS (bank spread)
 
-    // RMSNormPlain (nn/ops.go:195-214): float32 squares summed in float64.
-    // The sum is taken in a fixed tree (each thread its elements in order,
-    // then pairwise), not golem's left-to-right loop; the two float64 sums
-    // differ by at most a few units in the 53rd bit, below the float32
-    // rounding of the mean except in rare ties.
-    double s = 0.0;
-    for (int i = tid; i < D; i += kRouteThreads) {
-        const float v = x[i];
-        const float sq = v * v;
-        s += (double)sq;
+constexpr int kLogitsDepth = 4;     // chunks fetched ahead
+
+// One thread's share of chunk k of the positions' inputs: XF4 float4.
+template <int P, int XF4>
+__device__ __forceinline__ void logits_fetch(const float *__restrict__ resid, int ldr, int M, int t0, int k,
+                                             float (&st)[XF4 * 4]) {
+    for (int f = 0; f < XF4; f++) {
+        const int idx = (int)threadIdx.x + f * kLogitsThreads;
+        const int t = min(t0 + (idx >> 4), M - 1);
+        const float4 v = *(const float4 *)(resid + (size_t)t * ldr + k * kLogitsChunk + 4 * (idx & 15));
+        st[4 * f + 0] = v.x;
+        st[4 * f + 1] = v.y;
+        st[4 * f + 2] = v.z;
+        st[4 * f + 3] = v.w;
     }
-    part[tid] = s;
+}
+
+// The same share, normalised (x * scale) * ((1/sqrt(D)) * RouterScale[i]),
+// into chunk k's LDS buffer.
+template <int P, int XF4>
+__device__ __forceinline__ void logits_put(const float (&st)[XF4 * 4], const float *scale,
+                                           const float *__restrict__ router_scale, float inv_sqrt_dim, int k,
+                                           float *xbuf) {
+    float *buf = xbuf + (k & 1) * P * kLogitsChunkPad;
+    for (int f = 0; f < XF4; f++) {
+        const int idx = (int)threadIdx.x + f * kLogitsThreads;
+        const int pp = idx >> 4, q = idx & 15;
+        const float sc = scale[pp];
+        const int i0 = k * kLogitsChunk + 4 * q;
+        for (int j = 0; j < 4; j++) {
+            const float normed = st[4 * f + j] * sc;
+            const float factor = inv_sqrt_dim * (router_scale ? router_scale[i0 + j] : 1.0f);
+            buf[pp * kLogitsChunkPad + 4 * q + j] = normed * factor;
+        }
+    }
+}
+
+__host__ __device__ constexpr int logits_row_stride(int D) { return (D + 63) / 64 * 64 + 8; }
+
+template <int EW>
+__global__ __launch_bounds__(kLogitsThreads) void moe_logits_kernel(const float *__restrict__ router, int D, int E,
+                                                                    const float *__restrict__ router_scale,
+                                                                    const float *__restrict__ resid, int ldr, int M,
+                                                                    float eps, float *__restrict__ logits) {
+    constexpr int P = 64 / EW;                          // positions per workgroup
+    constexpr int XF4 = P * kLogitsChunk / 4 / kLogitsThreads;  // float4 of a chunk per thread
+    extern __shared__ float lds[];
+    const int S = logits_row_stride(D);
+    float *rows = lds;                                  // [EW][S]
+    float *xbuf = rows + EW * S;                        // [2][P][kLogitsChunkPad]
+    float *scale = xbuf + 2 * P * kLogitsChunkPad;      // [P]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int e0 = blockIdx.x * EW, t0 = blockIdx.y * P;
+
+    // Router rows, every load issued at once (D % 64 == 0, checked on the host).
+    const int per_row = D / 4;
+    for (int i = tid; i < EW * per_row; i += kLogitsThreads) {
+        const int e = i / per_row, q = i - e * per_row;
+        const int row = min(e0 + e, E - 1);
+        const float4 v = *(const float4 *)(router + (size_t)row * D + 4 * q);
+        *(float4 *)(rows + e * S + 4 * q) = v;
+    }
+
+    // The norm's scale for each position, one wavefront per position.
+    for (int p = wave; p < P; p += kLogitsThreads / 64) {
+        const int t = t0 + p;
+        if (t >= M)
+            break;
+        const float *x = resid + (size_t)t * ldr;
+        double part[8];
+        for (int v = 0; v < 8; v++) {
+            double s = 0.0;
+            for (int i = lane + 64 * v; i < D; i += 512) {
+                const float xv = x[i];
+                const float sq = xv * xv;
+                s += (double)sq;
+            }
+            part[v] = s;
+        }
+        for (int v = 0; v < 4; v++)
+            part[v] = part[v] + part[v + 4];
+        for (int v = 0; v < 2; v++)
+            part[v] = part[v] + part[v + 2];
+        double s = part[0] + part[1];
+        for (int w = 32; w > 0; w >>= 1) {
+            const double o = __shfl_down(s, w, 64);
+            if (lane < w)
+                s = s + o;
+        }
+        if (lane == 0) {
+            const float mean = (float)(s / (double)D);
+            scale[p] = (float)(1.0 / sqrt((double)(mean + eps)));
+        }
+    }
     __syncthreads();
-    for (int w = kRouteThreads / 2; w > 0; w >>= 1) {
-        if (tid < w)
-            part[tid] = part[tid] + part[tid + w];
-        __syncthreads();
-    }
-    const float mean = (float)(part[0] / (double)D);
-    const float scale = (float)(1.0 / sqrt((double)(mean + eps)));
+
+    // The normalised input reaches LDS a chunk at a time; each thread carries
+    // XF4 groups of four inputs of a chunk, fetched kLogitsDepth chunks ahead
+    // into a ring of registers (the loop is unrolled by the ring's depth, so
+    // every ring index is a constant).
     const float inv_sqrt_dim = (float)(1.0 / sqrt((double)D));
-    for (int i = tid; i < D; i += kRouteThreads) {
-        const float normed = x[i] * scale;
-        const float factor = inv_sqrt_dim * (router_scale ? router_scale[i] : 1.0f);
-        xr[i] = normed * factor;
-    }
+    float stage[kLogitsDepth][XF4 * 4];
+    const int c = tid & 3, e = (tid >> 2) % EW, p = (tid >> 2) / EW;  // lane = (p, e, c)
+    const float *rrow = rows + e * S + c;
+    float acc = 0.0f;
+    const int chunks = D / kLogitsChunk;
+#pragma unroll
+    for (int u = 0; u < kLogitsDepth; u++)
+        if (u < chunks)
+            logits_fetch<P, XF4>(resid, ldr, M, t0, u, stage[u]);
+    logits_put<P, XF4>(stage[0], scale, router_scale, inv_sqrt_dim, 0, xbuf);
+    if (kLogitsDepth < chunks)
+        logits_fetch<P, XF4>(resid, ldr, M, t0, kLogitsDepth, stage[0]);
     __syncthreads();
-
-    // DotF32 (nn/dot_f32.go:13-33) for every expert: four lanes per expert
-    // run the four accumulators, elements past the last four go to the
-    // first, result (s0 + s1) + (s2 + s3).
-    const int whole = D & ~3;
-    for (int base = 0; base < 4 * E; base += kRouteThreads) {
-        const int id = base + tid;
-        const int e = id >> 2, c = id & 3;
-        float acc = 0.0f;
-        if (e < E) {
-            const float *row = router + (size_t)e * D;
-            for (int i = c; i < whole; i += 4) {
-                const float p = row[i] * xr[i];
-                acc = acc + p;
-            }
-            if (c == 0)
-                for (int i = whole; i < D; i++) {
-                    const float p = row[i] * xr[i];
-                    acc = acc + p;
+    for (int kb = 0; kb < chunks; kb += kLogitsDepth) {
+#pragma unroll
+        for (int u = 0; u < kLogitsDepth; u++) {
+            const int k = kb + u;
+            if (k < chunks) {
+                // chain steps over chunk k
+                const float *xr = xbuf + (k & 1) * P * kLogitsChunkPad + p * kLogitsChunkPad + c;
+                const float *rk = rrow + k * kLogitsChunk;
+                float a[16], b[16];
+                for (int j = 0; j < 16; j++) {
+                    a[j] = rk[4 * j];
+                    b[j] = xr[4 * j];
                 }
-        }
-        chains[tid] = acc;
-        __syncthreads();
-        if (e < E && c == 0) {
-            const float v = (chains[tid] + chains[tid + 1]) + (chains[tid + 2] + chains[tid + 3]);
-            lg[e] = v;
-            logits[(size_t)t * E + e] = v;
-        }
-        __syncthreads();
-    }
-
-    // chooseExperts (gemma/moe.go:62-88).
-    if (tid == 0) {
-        int32_t chosen[64];
-        for (int j = 0; j < k; j++) {
-            int best = -1;
-            for (int e = 0; e < E; e++) {
-                bool taken = false;
-                for (int i = 0; i < j; i++)
-                    taken |= chosen[i] == e;
-                if (taken)
-                    continue;
-                if (best < 0 || lg[e] > lg[best])
-                    best = e;
+                for (int j = 0; j < 16; j++) {
+                    const float prod = a[j] * b[j];
+                    acc = acc + prod;
+                }
+                // chunk k + 1 into the other buffer (last read at chunk k - 1),
+                // and its ring slot refilled with chunk k + 1 + depth
+                const int nu = (u + 1) % kLogitsDepth;  // a constant once unrolled
+                if (k + 1 < chunks) {
+                    logits_put<P, XF4>(stage[nu], scale, router_scale, inv_sqrt_dim, k + 1, xbuf);
+                    if (k + 1 + kLogitsDepth < chunks)
+                        logits_fetch<P, XF4>(resid, ldr, M, t0, k + 1 + kLogitsDepth, stage[nu]);
+                }
+                __syncthreads();
             }
-            chosen[j] = best;
-            ids[(size_t)t * k + j] = best;
         }
-        const float top = lg[chosen[0]];
+    }
+    const float s1 = __shfl_down(acc, 1, 64), s2 = __shfl_down(acc, 2, 64), s3 = __shfl_down(acc, 3, 64);
+    if (c == 0 && t0 + p < M && e0 + e < E)
+        logits[(size_t)(t0 + p) * E + e0 + e] = (acc + s1) + (s2 + s3);
+}
+
+// chooseExperts (gemma/moe.go:62-88) for one position per wavefront: k rounds
+// of argmax over the logits not yet chosen.  golem scans in index order and
+// replaces its best on a strictly greater logit, so ties go to the lower
+// index and a NaN is taken only when it is the first logit not yet chosen
+// (no comparison with it is ever true); the wavefront reduction keeps exactly
+// that rule.  Weights: exp(l - top) in float64, rounded to float32, summed in
+// slot order, divided by the sum.
+constexpr int kTopkMaxPerLane = 16;  // E <= 1024
+constexpr int kTopkMax = 64;         // k <= 64
+
+__global__ __launch_bounds__(64) void moe_topk_kernel(const float *__restrict__ logits, int E, int k,
+                                                      int32_t *__restrict__ ids, float *__restrict__ weights) {
+    __shared__ float chosen_l[kTopkMax];
+    __shared__ float wv[kTopkMax];
+    const int t = blockIdx.x, lane = threadIdx.x;
+    const float *lg = logits + (size_t)t * E;
+    float v[kTopkMaxPerLane];
+    unsigned taken = 0;  // bit j: logit lane + 64 j is chosen or absent
+#pragma unroll
+    for (int j = 0; j < kTopkMaxPerLane; j++) {
+        const int e = lane + 64 * j;
+        v[j] = e < E ? lg[e] : 0.0f;
+        taken |= (e >= E ? 1u : 0u) << j;
+    }
+    for (int round = 0; round < k; round++) {
+        // first index not yet chosen
+        int first = 0x7fffffff;
+        const unsigned open = ~taken & ((1u << kTopkMaxPerLane) - 1);
+        if (open)
+            first = lane + 64 * __builtin_ctz(open);
+        for (int w = 32; w > 0; w >>= 1)
+            first = min(first, __shfl_xor(first, w, 64));
+        const float fv = lg[first];
+        int best;
+        if (fv != fv) {
+            best = first;
+        } else {
+            // largest non-NaN value not yet chosen, lowest index among equals
+            float bv = 0.0f;
+            int bi = 0x7fffffff;
+#pragma unroll
+            for (int j = 0; j < kTopkMaxPerLane; j++) {
+                const int e = lane + 64 * j;
+                if (((taken >> j) & 1u) || v[j] != v[j])
+                    continue;
+                if (bi == 0x7fffffff || v[j] > bv || (v[j] == bv && e < bi)) {
+                    bv = v[j];
+                    bi = e;
+                }
+            }
+            for (int w = 32; w > 0; w >>= 1) {
+                const float ov = __shfl_xor(bv, w, 64);
+                const int oi = __shfl_xor(bi, w, 64);
+                if (oi != 0x7fffffff && (bi == 0x7fffffff || ov > bv || (ov == bv && oi < bi))) {
+                    bv = ov;
+                    bi = oi;
+                }
+            }
+            best = bi;
+        }
+        if ((best & 63) == lane)
+            taken |= 1u << (best >> 6);
+        if (lane == 0) {
+            ids[(size_t)t * k + round] = best;
+            chosen_l[round] = lg[best];
+        }
+    }
+    if (lane == 0) {
+        const float top = chosen_l[0];
         float total = 0.0f;
-        float wv[64];
         for (int j = 0; j < k; j++) {
-            wv[j] = (float)exp((double)(lg[chosen[j]] - top));
+            wv[j] = (float)exp((double)(chosen_l[j] - top));
             total += wv[j];
         }
         for (int j = 0; j < k; j++)
@@ -327,11 +472,33 @@ int launch_gelu_table(gx_ctx *ctx, float *table) {
 int launch_moe_route(gx_ctx *ctx, const gx_weight *router, const float *router_scale, const float *resid, int ldr,
                      int M, int k, float eps, float *logits, int32_t *ids, float *weights) {
     const int D = router->cols, E = router->rows;
-    const size_t lds = (size_t)(D + E) * sizeof(float);
-    GX_CHECK(lds <= 64 * 1024, "gx: a router of %d x %d does not fit this kernel's LDS", E, D);
-    moe_route_kernel<<<M, kRouteThreads, lds, ctx->stream>>>((const float *)router->dev, D, E, router_scale, resid,
-                                                             ldr, k, eps, logits, ids, weights);
-    return check_launch("moe_route");
+    GX_CHECK(D % kLogitsChunk == 0, "gx: the router's width %d is not a multiple of %d", D, kLogitsChunk);
+    GX_CHECK(E <= 64 * kTopkMaxPerLane, "gx: %d experts exceed the router's limit of %d", E, 64 * kTopkMaxPerLane);
+    GX_CHECK(k <= kTopkMax, "gx: top_k %d exceeds %d", k, kTopkMax);
+    GX_CHECK(((uintptr_t)resid & 15) == 0 && ldr % 4 == 0, "gx: resid must be 16-byte aligned with ldr %% 4 == 0");
+    // The most router rows per workgroup that fit the LDS.
+    const size_t fixed = sizeof(float) * (size_t)logits_row_stride(D);
+    auto lds = [&](int ew) {
+        const int P = 64 / ew;
+        return fixed * ew + sizeof(float) * (2 * (size_t)P * kLogitsChunkPad + P);
+    };
+    const int ew = lds(4) <= 64 * 1024 ? 4 : lds(2) <= 64 * 1024 ? 2 : 1;
+    GX_CHECK(lds(ew) <= 64 * 1024, "gx: a router of width %d does not fit the LDS", D);
+    const dim3 grid((unsigned)((E + ew - 1) / ew), (unsigned)((M + 64 / ew - 1) / (64 / ew)));
+    const float *rw = (const float *)router->dev;
+    if (ew == 4)
+        moe_logits_kernel<4><<<grid, kLogitsThreads, lds(4), ctx->stream>>>(rw, D, E, router_scale, resid, ldr, M,
+                                                                           eps, logits);
+    else if (ew == 2)
+        moe_logits_kernel<2><<<grid, kLogitsThreads, lds(2), ctx->stream>>>(rw, D, E, router_scale, resid, ldr, M,
+                                                                           eps, logits);
+    else
+        moe_logits_kernel<1><<<grid, kLogitsThreads, lds(1), ctx->stream>>>(rw, D, E, router_scale, resid, ldr, M,
+                                                                           eps, logits);
+    if (int rc = check_launch("moe_logits"))
+        return rc;
+    moe_topk_kernel<<<M, 64, 0, ctx->stream>>>(logits, E, k, ids, weights);
+    return check_launch("moe_topk");
 }
 
 int launch_moe_experts(gx_ctx *ctx, const gx_weight *gate_up, const gx_weight *down, const float *down_scale,

@@ -322,3 +322,79 @@ def compare_floats(got, want):
     gaps = np.abs(got - want)
     at = int(np.argmax(gaps))
     return float(gaps[at] / scale), at
+
+
+# ---- the CPU baseline: golem's AVX2 kernels and worker pool ----------------
+
+CPU_LIB_PATH = os.path.join(HERE, "libcpu_avx2.so")
+_cpu = None
+
+
+def host_has_avx2():
+    try:
+        flags = open("/proc/cpuinfo").read()
+    except OSError:
+        return False
+    return all(f" {f}" in flags for f in ("avx2", "fma", "f16c"))
+
+
+def host_threads():
+    """The threads the CPU baseline may use: OMP_NUM_THREADS when set (the GPU
+    host sets it to its per-GPU share of cores), else this process's CPUs."""
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    n = len(os.sched_getaffinity(0))
+    return min(int(env), n) if env.isdigit() and int(env) > 0 else n
+
+
+def cpu_lib(threads=None):
+    """libcpu_avx2.so with its pool started (once per process)."""
+    global _cpu
+    if _cpu is not None:
+        return _cpu
+    if not host_has_avx2():
+        raise RuntimeError("the CPU baseline needs AVX2, FMA and F16C")
+    if not os.path.exists(CPU_LIB_PATH):
+        from . import build
+        build.build(verbose=False)
+    lib = ctypes.CDLL(CPU_LIB_PATH)
+    I, F, V = ctypes.c_int, ctypes.c_float, ctypes.c_void_p
+    for name, (res, args) in {
+        "cpu_pool_init": (I, [I]),
+        "cpu_pool_threads": (I, []),
+        "cpu_mat_vec_q6_k": (I, [V, V, V, V, I, I, I, V, I, I]),
+        "cpu_mat_vec_q4_0": (I, [V, V, V, V, I, I, I, V, I, I]),
+        "cpu_dot_q4_0": (None, [V, V, V, V, I, I, I, I, V, I, I]),
+        "cpu_dot_q6_k": (F, [V, V, V, V, I]),
+    }.items():
+        fn = getattr(lib, name)
+        fn.restype, fn.argtypes = res, args
+    if lib.cpu_pool_init(threads or host_threads()) != 0:
+        raise RuntimeError("cpu_pool_init refused")
+    _cpu = lib
+    return lib
+
+
+def cpu_mat_vec_q6_k(w, batch, rows, threads, ys=None):
+    """MatVecQ6_K through golem's AVX2 kernel on at most `threads` threads."""
+    if ys is None:
+        ys = np.full((batch.size, rows), np.nan, dtype=np.float32)
+    rc = cpu_lib().cpu_mat_vec_q6_k(_p(w), _p(batch.QK), _p(batch.BSums), _p(batch.KScales), rows, batch.width,
+                                    batch.size, _p(ys), ys.shape[1], threads)
+    assert rc == 0
+    return ys
+
+
+def cpu_mat_vec_q4_0(w, batch, rows, threads, ys=None):
+    """MatVecQ4_0 (row layout) through golem's AVX2 x8/x4/x1 kernels."""
+    if ys is None:
+        ys = np.full((batch.size, rows), np.nan, dtype=np.float32)
+    rc = cpu_lib().cpu_mat_vec_q4_0(_p(w), _p(batch.Q), _p(batch.Scales), _p(batch.Corr), rows, batch.width,
+                                    batch.size, _p(ys), ys.shape[1], threads)
+    assert rc == 0
+    return ys
+
+
+def cpu_dot_q4_0(w_row, batch, block, column, n, state, mode, cols):
+    cpu_lib().cpu_dot_q4_0(_p(w_row), _p(batch.Q), _p(batch.Scales), _p(batch.Corr), batch.stride, block, column, n,
+                           _p(state), mode, cols)
+    return state

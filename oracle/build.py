@@ -12,21 +12,29 @@ import subprocess
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB = os.path.join(HERE, "liboracle.so")
+CPU_LIB = os.path.join(HERE, "libcpu_avx2.so")
+
+
+def _gcc(src, out, flags, verbose):
+    tmp = out + ".tmp"
+    cmd = ["gcc", "-O2", "-ffp-contract=off", "-fno-fast-math", "-fPIC", "-shared", "-Wall", *flags,
+           "-o", tmp, src, "-lm"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"build of {os.path.basename(src)} failed:\n{r.stderr}")
+    if r.stderr.strip() and verbose:
+        print(r.stderr)
+    os.replace(tmp, out)
+    if verbose:
+        print(f"built {out}")
 
 
 def build(verbose=True):
-    src = os.path.join(HERE, "oracle.c")
-    tmp = LIB + ".tmp"
-    cmd = ["gcc", "-O2", "-ffp-contract=off", "-fno-fast-math", "-fPIC", "-shared",
-           "-Wall", "-o", tmp, src, "-lm"]
-    r = subprocess.run(cmd, capture_output=True, text=True)
-    if r.returncode != 0:
-        raise RuntimeError(f"oracle build failed:\n{r.stderr}")
-    if r.stderr.strip() and verbose:
-        print(r.stderr)
-    os.replace(tmp, LIB)
-    if verbose:
-        print(f"built {LIB}")
+    """liboracle.so (generic restatement) and libcpu_avx2.so (golem's AVX2
+    kernels and worker pool, the CPU baseline; -mavx2 -mfma -mf16c, loaded
+    only on a host that has them)."""
+    _gcc(os.path.join(HERE, "oracle.c"), LIB, [], verbose)
+    _gcc(os.path.join(HERE, "cpu_avx2.c"), CPU_LIB, ["-mavx2", "-mfma", "-mf16c", "-pthread"], verbose)
     return LIB
 
 

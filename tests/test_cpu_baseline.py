@@ -1,0 +1,120 @@
+"""The CPU baseline (oracle/cpu_avx2.c: golem's AVX2 kernels and worker pool)
+against the generic restatement, on the bars golem's own tests set:
+
+- Q6_K: the AVX2 kernel is bit-identical to dotQ6_KGo (nn/dot_q6_k_test.go:51-75).
+- Q4_0: x1, x4 and x8 agree with dotQ4_0Go within 1e-3 relative + 1e-6
+  (nn/dot_q4_0_avx2_test.go:14-79); a row cut into two stretches gives exactly
+  the row done in one call (:81-130).  x1, x4 and x8 also agree with each other
+  bit for bit: the same per-column instructions, which golem relies on when a
+  batch finishes on the narrower kernels (nn/dot_q4_0.go:156-160).
+- The pool: any thread count gives the same bits (rows are independent; the
+  split never cuts a row).
+"""
+import numpy as np
+import pytest
+
+import oracle
+from golem_amd import synth
+
+pytestmark = pytest.mark.skipif(not oracle.host_has_avx2(), reason="no AVX2/FMA/F16C on this host")
+
+BEGIN, FINISH = 1, 2
+
+
+def portable(orc, w, b, column, n):
+    state = np.zeros(9, dtype=np.float32)
+    lib = orc.load()
+    lib.orc_dot_q4_0_go(orc._p(w), orc._p(b.Q), orc._p(b.Scales), orc._p(b.Corr), b.stride, 0, column, n,
+                        orc._p(state))
+    return np.float32(lib.orc_fold(orc._p(state), np.float32(state[8])))
+
+
+def golem_like_rows(g, n):
+    """A row as golem's AVX2 test draws it: random bytes, scale bytes kept to
+    sane fp16 magnitudes (high byte 0x30..0x33)."""
+    blocks = n // 32
+    w = g.integers(0, 256, size=blocks * 18, dtype=np.uint8)
+    w[0::18] = g.integers(0, 256, size=blocks, dtype=np.uint8)
+    w[1::18] = 0x30 + g.integers(0, 4, size=blocks, dtype=np.uint8)
+    return w
+
+
+@pytest.mark.parametrize("n", [32, 64, 256, 1536, 4096])
+@pytest.mark.parametrize("size", [1, 3, 4, 7, 8, 11, 16])
+def test_q4_0_kernels_against_portable(n, size):
+    g = synth.rng(7 + n + size)
+    w = golem_like_rows(g, n)
+    F = (g.random((size, n), dtype=np.float32) * 2 - 1).astype(np.float32)
+    b = oracle.Batch(F).quantize()
+    want = np.array([portable(oracle, w, b, c, n) for c in range(size)], dtype=np.float32)
+
+    def bar(got, c):
+        assert abs(float(got) - float(want[c])) <= 1e-3 * abs(float(want[c])) + 1e-6, (n, size, c, got, want[c])
+
+    one = np.zeros(size, dtype=np.float32)
+    for c in range(size):
+        st = np.zeros(72, dtype=np.float32)
+        oracle.cpu_dot_q4_0(w, b, 0, c, n, st, BEGIN | FINISH, 1)
+        one[c] = st[0]
+        bar(st[0], c)
+    for cols in (4, 8):
+        for c in range(0, size - cols + 1, cols):
+            st = np.zeros(72, dtype=np.float32)
+            oracle.cpu_dot_q4_0(w, b, 0, c, n, st, BEGIN | FINISH, cols)
+            for j in range(cols):
+                bar(st[j], c + j)
+            np.testing.assert_array_equal(st[:cols].view(np.uint32), one[c:c + cols].view(np.uint32))
+            if n >= 64 and (n // 2) % 32 == 0:
+                half = n // 2
+                split = np.zeros(72, dtype=np.float32)
+                oracle.cpu_dot_q4_0(w, b, 0, c, half, split, BEGIN, cols)
+                oracle.cpu_dot_q4_0(w[half // 32 * 18:], b, half // 32, c, n - half, split, FINISH, cols)
+                np.testing.assert_array_equal(split[:cols].view(np.uint32), st[:cols].view(np.uint32))
+
+
+@pytest.mark.parametrize("rows,cols,size", [(64, 2560, 1), (37, 3840, 3), (21, 512, 13)])
+def test_q4_0_mat_vec_tiled(rows, cols, size):
+    """matVecQ4_0Rows' stretches of 2048 and row tiles (K=2560 and 3840 take
+    the tiled branch, 3840 with a partial last stretch), against the generic
+    product, and independent of the thread count."""
+    g = synth.rng(rows + cols)
+    w = synth.q4_0_weights(g, rows, cols)
+    b = oracle.Batch(synth.activations(g, size, cols)).quantize()
+    want = oracle.mat_vec_q4_0_rows(w, b, rows)
+    got1 = oracle.cpu_mat_vec_q4_0(w, b, rows, 1)
+    gotn = oracle.cpu_mat_vec_q4_0(w, b, rows, oracle.host_threads())
+    np.testing.assert_array_equal(got1.view(np.uint32), gotn.view(np.uint32))
+    for c in range(size):
+        rel, at = oracle.compare_floats(got1[c], want[c])
+        assert rel <= 1e-3, (c, rel, at)
+
+
+@pytest.mark.parametrize("rows,cols,size", [(300, 2560, 1), (40, 512, 3)])
+def test_q6_k_bit_exact_against_portable(rows, cols, size):
+    g = synth.rng(cols + size)
+    w = synth.q6_k_weights(g, rows, cols)
+    x = synth.activations(g, size, cols)
+    x[0, :256] = 0.0                        # a zero superblock
+    b = oracle.Batch(x).quantize_k()
+    want = oracle.mat_vec_q6_k_rows(w, b, rows)
+    for threads in (1, oracle.host_threads()):
+        got = oracle.cpu_mat_vec_q6_k(w, b, rows, threads)
+        np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_q6_k_extreme_scales():
+    """Sub-scales at -64 and 63 and magnitudes at 0 and 63: the int16 pair sums
+    of VPMADDUBSW stay in range and the result stays bit-exact."""
+    g = synth.rng(99)
+    rows, cols = 8, 512
+    w = synth.q6_k_weights(g, rows, cols).reshape(rows * 2, 210)
+    w[0::2, 192:208] = np.uint8(0xC0)       # -64
+    w[1::2, 192:208] = np.uint8(63)
+    w[:4, :192] = 0xFF                       # magnitude 63 everywhere
+    w[4:8, :192] = 0x00                      # magnitude 0
+    w = w.reshape(-1)
+    x = np.full((1, cols), -1.0, dtype=np.float32)
+    x[0, ::3] = 1.0
+    b = oracle.Batch(x).quantize_k()
+    np.testing.assert_array_equal(oracle.cpu_mat_vec_q6_k(w, b, rows, 1).view(np.uint32),
+                                  oracle.mat_vec_q6_k_rows(w, b, rows).view(np.uint32))

@@ -125,6 +125,50 @@ def test_route_ties_go_to_lower_index(dev, orc):
     assert ids[0] == 2 and ids[1] == 5
 
 
+@pytest.mark.parametrize("D,E,k,M", [(4096, 10, 3, 33), (6144, 6, 2, 5), (256, 130, 8, 17)])
+def test_route_layouts_bit_exact(dev, orc, D, E, k, M):
+    """The router's other shapes: rows per workgroup 2 (D = 4096) and 1
+    (D = 6144) where four rows do not fit the LDS, an expert count that is not
+    a multiple of four, and positions spanning several workgroups."""
+    m = Moe.__new__(Moe)
+    g = synth.rng(D + E)
+    m.D, m.E, m.k, m.dev = D, E, k, dev
+    m.router = (g.standard_normal((E, D)) * 0.02).astype(np.float32)
+    m.wr = dev.weight(m.router, capi.F32, E, D)
+    x = synth.activations(g, M, D)
+    logits, ids, w = m.route(x)
+    logits, ids, w = dev.get(logits), dev.get(ids), dev.get(w)
+    for t in range(M):
+        ol, oi, ow = orc.route_one(x[t], m.router, k)
+        np.testing.assert_array_equal(logits[t].view(np.uint32), ol.view(np.uint32))
+        np.testing.assert_array_equal(ids[t], oi)
+        np.testing.assert_allclose(w[t], ow, rtol=1e-6, atol=0)
+
+
+def test_route_nan_logit_follows_golem_scan(dev, orc):
+    """chooseExperts scans in index order and replaces its best only on a
+    strictly greater logit, so a NaN logit is chosen exactly when it is the
+    first one not yet chosen: expert 0 (NaN) first, then the largest others."""
+    D, E, k = 256, 8, 3
+    g = synth.rng(8)
+    router = (g.standard_normal((E, D)) * 0.02).astype(np.float32)
+    router[0, 5] = np.nan
+    router[4, 7] = np.nan
+    m = Moe.__new__(Moe)
+    m.D, m.E, m.k, m.dev = D, E, k, dev
+    m.router = router
+    m.wr = dev.weight(router, capi.F32, E, D)
+    x = synth.activations(g, 2, D)
+    logits, ids, w = m.route(x)
+    logits, ids, w = dev.get(logits), dev.get(ids), dev.get(w)
+    for t in range(2):
+        ol, oi, ow = orc.route_one(x[t], router, k)
+        assert np.isnan(logits[t, 0]) and np.isnan(logits[t, 4])
+        assert oi[0] == 0 and 4 not in oi
+        np.testing.assert_array_equal(ids[t], oi)
+        assert np.all(np.isnan(w[t])) and np.all(np.isnan(ow))
+
+
 @pytest.mark.parametrize("M", [1, 2, 20])
 def test_experts_against_golem(dev, orc, M):
     """Small shape: the matrix-vector path (M <= 4) and the grouped path."""
