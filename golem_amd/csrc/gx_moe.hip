@@ -35,171 +35,265 @@ __global__ void gelu_table_kernel(float *__restrict__ table) {
     table[i] = half_bits_to_float(float_to_half_bits((float)g));
 }
 
-// The router in two kernels.
+// The router.
 //
-// moe_logits_kernel<EW>: a workgroup holds EW router rows in LDS and computes
-// their logits for P = 64/EW positions; lane = (position, expert, chain).
-// DotF32 (nn/dot_f32.go:13-33) is four serial chains -- chain c adds the
-// products of elements c, c+4, c+8, ... in order -- that meet as
-// (s0 + s1) + (s2 + s3); each lane runs one chain in that order, so the
-// logits are golem's bits.  The normalised input reaches the chains in
-// 64-element chunks, double-buffered through LDS, so a chain step is two LDS
-// reads, a multiply and an add, and the global loads of the next chunk are in
-// flight meanwhile.
-//
-// RMSNormPlain (nn/ops.go:195-214) squares in float32 and sums in float64.
-// The sum is taken in a fixed tree: 512 partial sums, partial t holding
+// Logits: DotF32 (nn/dot_f32.go:13-33) is four serial chains -- chain c adds
+// the products of elements c, c+4, c+8, ... in order -- that meet as
+// (s0 + s1) + (s2 + s3).  A lane runs one chain in that order, so the logits
+// are golem's bits.  RMSNormPlain (nn/ops.go:195-214) squares in float32 and
+// sums in float64, here in a fixed tree: 512 partial sums, partial t holding
 // elements t, t+512, t+1024, ... in order, then halved pairwise (t + w for
 // w = 256 .. 1).  golem sums left to right; the two float64 sums differ by a
 // few units in the 53rd bit, below the float32 rounding of the mean except in
-// rare ties.
+// rare ties.  The normalised input is (x * scale) * ((1/sqrt(D)) *
+// RouterScale[i]), as Route forms it (gemma/moe.go:34-53).
+//
+//   moe_logits_one_kernel: one workgroup per (expert, position); the row and
+//     the position's input sit in LDS, every load issued at once.  Few
+//     positions (decode), where the cost is latency.
+//   moe_logits_kernel<EW>: EW experts x 64/EW positions per workgroup; rows and
+//     inputs pass through LDS a 64-input chunk at a time, fetched from a ring
+//     of registers kLogitsDepth chunks ahead.  Many positions.
 constexpr int kLogitsThreads = 256;
 constexpr int kLogitsChunk = 64;     // inputs per chunk
 constexpr int kLogitsChunkPad = 68;  // chunk row stride in LDS (bank spread)
+constexpr int kLogitsDepth = 8;      // chunks fetched ahead
+constexpr int kLogitsOneMaxD = 7168; // row + input in LDS: 57 KB
+constexpr int kLogitsOneF4 = kLogitsOneMaxD / 4 / kLogitsThreads;
 
-constexpr int kLogitsDepth = 4;     // chunks fetched ahead
-
-// One thread's share of chunk k of the positions' inputs: XF4 float4.
-template <int P, int XF4>
-__device__ __forceinline__ void logits_fetch(const float *__restrict__ resid, int ldr, int M, int t0, int k,
-                                             float (&st)[XF4 * 4]) {
-    for (int f = 0; f < XF4; f++) {
-        const int idx = (int)threadIdx.x + f * kLogitsThreads;
-        const int t = min(t0 + (idx >> 4), M - 1);
-        const float4 v = *(const float4 *)(resid + (size_t)t * ldr + k * kLogitsChunk + 4 * (idx & 15));
-        st[4 * f + 0] = v.x;
-        st[4 * f + 1] = v.y;
-        st[4 * f + 2] = v.z;
-        st[4 * f + 3] = v.w;
-    }
-}
-
-// The same share, normalised (x * scale) * ((1/sqrt(D)) * RouterScale[i]),
-// into chunk k's LDS buffer.
-template <int P, int XF4>
-__device__ __forceinline__ void logits_put(const float (&st)[XF4 * 4], const float *scale,
-                                           const float *__restrict__ router_scale, float inv_sqrt_dim, int k,
-                                           float *xbuf) {
-    float *buf = xbuf + (k & 1) * P * kLogitsChunkPad;
-    for (int f = 0; f < XF4; f++) {
-        const int idx = (int)threadIdx.x + f * kLogitsThreads;
-        const int pp = idx >> 4, q = idx & 15;
-        const float sc = scale[pp];
-        const int i0 = k * kLogitsChunk + 4 * q;
-        for (int j = 0; j < 4; j++) {
-            const float normed = st[4 * f + j] * sc;
-            const float factor = inv_sqrt_dim * (router_scale ? router_scale[i0 + j] : 1.0f);
-            buf[pp * kLogitsChunkPad + 4 * q + j] = normed * factor;
+// Partial sums t and t + 256 of the norm's tree (this thread's pair), over
+// x[0, D) with x in LDS or global memory.  Elements are read 8 per partial
+// at a time; past D they read as element D - 1 and add 0.0, which leaves a
+// non-negative double unchanged.
+__device__ __forceinline__ void norm_partials(const float *x, int D, double &p0, double &p1) {
+    const int tid = threadIdx.x;
+    p0 = 0.0;
+    p1 = 0.0;
+    for (int base = 0; base < D; base += 8 * 512) {
+        float v0[8], v1[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            v0[u] = x[min(base + tid + 512 * u, D - 1)];
+            v1[u] = x[min(base + tid + 256 + 512 * u, D - 1)];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const float a = base + tid + 512 * u < D ? v0[u] : 0.0f;
+            const float b = base + tid + 256 + 512 * u < D ? v1[u] : 0.0f;
+            const float sa = a * a, sb = b * b;
+            p0 += (double)sa;
+            p1 += (double)sb;
         }
     }
 }
 
-__host__ __device__ constexpr int logits_row_stride(int D) { return (D + 63) / 64 * 64 + 8; }
+// The rest of the tree (w = 256 .. 1) across a 256-thread workgroup; the
+// result is valid in thread 0.  `red` is 256 doubles of LDS.
+__device__ __forceinline__ double norm_tree(double p0, double p1, double *red) {
+    const int tid = threadIdx.x;
+    double s = p0 + p1;  // w = 256
+    red[tid] = s;
+    __syncthreads();
+    if (tid < 128)
+        s = s + red[tid + 128];
+    __syncthreads();
+    if (tid < 128)
+        red[tid] = s;
+    __syncthreads();
+    if (tid < 64) {
+        s = s + red[tid + 64];
+        for (int w = 32; w > 0; w >>= 1) {
+            const double o = __shfl_down(s, w, 64);
+            if (tid < w)
+                s = s + o;
+        }
+    }
+    return s;
+}
+
+__device__ __forceinline__ float norm_scale(double sum, int D, float eps) {
+    const float mean = (float)(sum / (double)D);
+    return (float)(1.0 / sqrt((double)(mean + eps)));
+}
+
+__global__ __launch_bounds__(kLogitsThreads) void moe_logits_one_kernel(const float *__restrict__ router, int D,
+                                                                        int E, const float *__restrict__ router_scale,
+                                                                        const float *__restrict__ resid, int ldr,
+                                                                        float eps, float *__restrict__ logits) {
+    extern __shared__ float lds[];
+    float *row = lds, *xr = lds + D;
+    __shared__ double red[kLogitsThreads];
+    __shared__ float scale_sh;
+    const int tid = threadIdx.x, e = blockIdx.x, t = blockIdx.y;
+    const float *rg = router + (size_t)e * D;
+    const float *xg = resid + (size_t)t * ldr;
+    const int n4 = D / 4;
+    float4 rv[kLogitsOneF4 + 1], xv[kLogitsOneF4 + 1];
+#pragma unroll
+    for (int f = 0; f <= kLogitsOneF4; f++) {  // clamped: every load issued, no branch
+        const int q = min(tid + f * kLogitsThreads, n4 - 1);
+        rv[f] = *(const float4 *)(rg + 4 * q);
+        xv[f] = *(const float4 *)(xg + 4 * q);
+    }
+#pragma unroll
+    for (int f = 0; f <= kLogitsOneF4; f++) {
+        const int q = tid + f * kLogitsThreads;
+        if (q < n4) {
+            *(float4 *)(row + 4 * q) = rv[f];
+            *(float4 *)(xr + 4 * q) = xv[f];
+        }
+    }
+    __syncthreads();
+    double p0, p1;
+    norm_partials(xr, D, p0, p1);
+    const double sum = norm_tree(p0, p1, red);
+    if (tid == 0)
+        scale_sh = norm_scale(sum, D, eps);
+    __syncthreads();
+    const float sc = scale_sh;
+    const float inv_sqrt_dim = (float)(1.0 / sqrt((double)D));
+    for (int i = tid; i < D; i += kLogitsThreads) {
+        const float normed = xr[i] * sc;
+        const float factor = inv_sqrt_dim * (router_scale ? router_scale[i] : 1.0f);
+        xr[i] = normed * factor;
+    }
+    __syncthreads();
+    if (tid < 64) {
+        const int c = tid & 3;
+        float acc = 0.0f;
+        if (tid < 4) {
+            for (int i0 = c; i0 < D; i0 += 64) {  // D % 64 == 0: 16 steps per pass
+                float a[16], b[16];
+#pragma unroll
+                for (int j = 0; j < 16; j++) {
+                    a[j] = row[i0 + 4 * j];
+                    b[j] = xr[i0 + 4 * j];
+                }
+#pragma unroll
+                for (int j = 0; j < 16; j++) {
+                    const float prod = a[j] * b[j];
+                    acc = acc + prod;
+                }
+            }
+        }
+        const float s1 = __shfl_down(acc, 1, 64), s2 = __shfl_down(acc, 2, 64), s3 = __shfl_down(acc, 3, 64);
+        if (tid == 0)
+            logits[(size_t)t * E + e] = (acc + s1) + (s2 + s3);
+    }
+}
 
 template <int EW>
 __global__ __launch_bounds__(kLogitsThreads) void moe_logits_kernel(const float *__restrict__ router, int D, int E,
                                                                     const float *__restrict__ router_scale,
                                                                     const float *__restrict__ resid, int ldr, int M,
                                                                     float eps, float *__restrict__ logits) {
-    constexpr int P = 64 / EW;                          // positions per workgroup
-    constexpr int XF4 = P * kLogitsChunk / 4 / kLogitsThreads;  // float4 of a chunk per thread
-    extern __shared__ float lds[];
-    const int S = logits_row_stride(D);
-    float *rows = lds;                                  // [EW][S]
-    float *xbuf = rows + EW * S;                        // [2][P][kLogitsChunkPad]
-    float *scale = xbuf + 2 * P * kLogitsChunkPad;      // [P]
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    constexpr int P = 64 / EW;                       // positions per workgroup
+    constexpr int XF4 = P * 16 / kLogitsThreads;     // input float4 per thread per chunk
+    constexpr int RT = EW * 16;                      // threads holding a row float4 per chunk
+    constexpr int BUF = (EW + P) * kLogitsChunkPad;  // a chunk in LDS: rows, then inputs
+    __shared__ float buf[2 * BUF];
+    __shared__ float scale[P];
+    __shared__ double red[kLogitsThreads];
+    const int tid = threadIdx.x;
     const int e0 = blockIdx.x * EW, t0 = blockIdx.y * P;
 
-    // Router rows, every load issued at once (D % 64 == 0, checked on the host).
-    const int per_row = D / 4;
-    for (int i = tid; i < EW * per_row; i += kLogitsThreads) {
-        const int e = i / per_row, q = i - e * per_row;
-        const int row = min(e0 + e, E - 1);
-        const float4 v = *(const float4 *)(router + (size_t)row * D + 4 * q);
-        *(float4 *)(rows + e * S + 4 * q) = v;
+    // The norm's scale for each position, the workgroup together.
+    for (int p = 0; p < P && t0 + p < M; p++) {
+        double p0, p1;
+        norm_partials(resid + (size_t)(t0 + p) * ldr, D, p0, p1);
+        const double sum = norm_tree(p0, p1, red);
+        if (tid == 0)
+            scale[p] = norm_scale(sum, D, eps);
+        __syncthreads();
     }
 
-    // The norm's scale for each position, one wavefront per position.
-    for (int p = wave; p < P; p += kLogitsThreads / 64) {
-        const int t = t0 + p;
-        if (t >= M)
-            break;
-        const float *x = resid + (size_t)t * ldr;
-        double part[8];
-        for (int v = 0; v < 8; v++) {
-            double s = 0.0;
-            for (int i = lane + 64 * v; i < D; i += 512) {
-                const float xv = x[i];
-                const float sq = xv * xv;
-                s += (double)sq;
-            }
-            part[v] = s;
-        }
-        for (int v = 0; v < 4; v++)
-            part[v] = part[v] + part[v + 4];
-        for (int v = 0; v < 2; v++)
-            part[v] = part[v] + part[v + 2];
-        double s = part[0] + part[1];
-        for (int w = 32; w > 0; w >>= 1) {
-            const double o = __shfl_down(s, w, 64);
-            if (lane < w)
-                s = s + o;
-        }
-        if (lane == 0) {
-            const float mean = (float)(s / (double)D);
-            scale[p] = (float)(1.0 / sqrt((double)(mean + eps)));
-        }
-    }
-    __syncthreads();
-
-    // The normalised input reaches LDS a chunk at a time; each thread carries
-    // XF4 groups of four inputs of a chunk, fetched kLogitsDepth chunks ahead
-    // into a ring of registers (the loop is unrolled by the ring's depth, so
-    // every ring index is a constant).
     const float inv_sqrt_dim = (float)(1.0 / sqrt((double)D));
-    float stage[kLogitsDepth][XF4 * 4];
+    const int re = (tid % RT) >> 4, rq = tid & 15;  // this thread's row float4 of a chunk
+    const float *rsrc = router + (size_t)min(e0 + re, E - 1) * D + 4 * rq;
+    float xs[kLogitsDepth][XF4 * 4], rs[kLogitsDepth][4];
     const int c = tid & 3, e = (tid >> 2) % EW, p = (tid >> 2) / EW;  // lane = (p, e, c)
-    const float *rrow = rows + e * S + c;
     float acc = 0.0f;
     const int chunks = D / kLogitsChunk;
+
+#define GX_LOGITS_FETCH(k, slot)                                                                                     \
+    do {                                                                                                             \
+        for (int f = 0; f < XF4; f++) {                                                                              \
+            const int idx = tid + f * kLogitsThreads;                                                                \
+            const int tt = min(t0 + (idx >> 4), M - 1);                                                              \
+            const float4 v = *(const float4 *)(resid + (size_t)tt * ldr + (k) * kLogitsChunk + 4 * (idx & 15));     \
+            xs[slot][4 * f + 0] = v.x;                                                                               \
+            xs[slot][4 * f + 1] = v.y;                                                                               \
+            xs[slot][4 * f + 2] = v.z;                                                                               \
+            xs[slot][4 * f + 3] = v.w;                                                                               \
+        }                                                                                                            \
+        const float4 r = *(const float4 *)(rsrc + (k) * kLogitsChunk);                                               \
+        rs[slot][0] = r.x;                                                                                           \
+        rs[slot][1] = r.y;                                                                                           \
+        rs[slot][2] = r.z;                                                                                           \
+        rs[slot][3] = r.w;                                                                                           \
+    } while (0)
+
+#define GX_LOGITS_PUT(k, slot)                                                                                       \
+    do {                                                                                                             \
+        float *b = buf + ((k) & 1) * BUF;                                                                            \
+        if (tid < RT)                                                                                                \
+            for (int j = 0; j < 4; j++)                                                                              \
+                b[re * kLogitsChunkPad + 4 * rq + j] = rs[slot][j];                                                  \
+        float *bx = b + EW * kLogitsChunkPad;                                                                        \
+        for (int f = 0; f < XF4; f++) {                                                                              \
+            const int idx = tid + f * kLogitsThreads;                                                                \
+            const int pp = idx >> 4, q = idx & 15;                                                                   \
+            const float sc = scale[pp];                                                                              \
+            const int i0 = (k) * kLogitsChunk + 4 * q;                                                               \
+            for (int j = 0; j < 4; j++) {                                                                            \
+                const float normed = xs[slot][4 * f + j] * sc;                                                       \
+                const float factor = inv_sqrt_dim * (router_scale ? router_scale[i0 + j] : 1.0f);                    \
+                bx[pp * kLogitsChunkPad + 4 * q + j] = normed * factor;                                              \
+            }                                                                                                        \
+        }                                                                                                            \
+    } while (0)
+
 #pragma unroll
     for (int u = 0; u < kLogitsDepth; u++)
         if (u < chunks)
-            logits_fetch<P, XF4>(resid, ldr, M, t0, u, stage[u]);
-    logits_put<P, XF4>(stage[0], scale, router_scale, inv_sqrt_dim, 0, xbuf);
+            GX_LOGITS_FETCH(u, u);
+    GX_LOGITS_PUT(0, 0);
     if (kLogitsDepth < chunks)
-        logits_fetch<P, XF4>(resid, ldr, M, t0, kLogitsDepth, stage[0]);
+        GX_LOGITS_FETCH(kLogitsDepth, 0);
     __syncthreads();
     for (int kb = 0; kb < chunks; kb += kLogitsDepth) {
 #pragma unroll
         for (int u = 0; u < kLogitsDepth; u++) {
             const int k = kb + u;
             if (k < chunks) {
-                // chain steps over chunk k
-                const float *xr = xbuf + (k & 1) * P * kLogitsChunkPad + p * kLogitsChunkPad + c;
-                const float *rk = rrow + k * kLogitsChunk;
-                float a[16], b[16];
+                const float *b = buf + (k & 1) * BUF;
+                const float *rk = b + e * kLogitsChunkPad + c;
+                const float *xr = b + EW * kLogitsChunkPad + p * kLogitsChunkPad + c;
+                float av[16], bv[16];
+#pragma unroll
                 for (int j = 0; j < 16; j++) {
-                    a[j] = rk[4 * j];
-                    b[j] = xr[4 * j];
+                    av[j] = rk[4 * j];
+                    bv[j] = xr[4 * j];
                 }
+#pragma unroll
                 for (int j = 0; j < 16; j++) {
-                    const float prod = a[j] * b[j];
+                    const float prod = av[j] * bv[j];
                     acc = acc + prod;
                 }
-                // chunk k + 1 into the other buffer (last read at chunk k - 1),
-                // and its ring slot refilled with chunk k + 1 + depth
+                // chunk k + 1 into the other buffer (last read at chunk k - 1);
+                // its ring slot then takes chunk k + 1 + depth
                 const int nu = (u + 1) % kLogitsDepth;  // a constant once unrolled
                 if (k + 1 < chunks) {
-                    logits_put<P, XF4>(stage[nu], scale, router_scale, inv_sqrt_dim, k + 1, xbuf);
+                    GX_LOGITS_PUT(k + 1, nu);
                     if (k + 1 + kLogitsDepth < chunks)
-                        logits_fetch<P, XF4>(resid, ldr, M, t0, k + 1 + kLogitsDepth, stage[nu]);
+                        GX_LOGITS_FETCH(k + 1 + kLogitsDepth, nu);
                 }
                 __syncthreads();
             }
         }
     }
+#undef GX_LOGITS_FETCH
+#undef GX_LOGITS_PUT
     const float s1 = __shfl_down(acc, 1, 64), s2 = __shfl_down(acc, 2, 64), s3 = __shfl_down(acc, 3, 64);
     if (c == 0 && t0 + p < M && e0 + e < E)
         logits[(size_t)(t0 + p) * E + e0 + e] = (acc + s1) + (s2 + s3);
@@ -219,29 +313,39 @@ __global__ __launch_bounds__(64) void moe_topk_kernel(const float *__restrict__ 
                                                       int32_t *__restrict__ ids, float *__restrict__ weights) {
     __shared__ float chosen_l[kTopkMax];
     __shared__ float wv[kTopkMax];
+    __shared__ float lg[64 * kTopkMaxPerLane];
     const int t = blockIdx.x, lane = threadIdx.x;
-    const float *lg = logits + (size_t)t * E;
+    const float *lgg = logits + (size_t)t * E;
     float v[kTopkMaxPerLane];
     unsigned taken = 0;  // bit j: logit lane + 64 j is chosen or absent
 #pragma unroll
     for (int j = 0; j < kTopkMaxPerLane; j++) {
         const int e = lane + 64 * j;
-        v[j] = e < E ? lg[e] : 0.0f;
+        v[j] = lgg[min(e, E - 1)];
+        lg[e] = v[j];
         taken |= (e >= E ? 1u : 0u) << j;
     }
+    __syncthreads();
+    // A NaN logit is taken only as the first logit not yet chosen; without
+    // any, a round is a plain argmax (greater value, then lower index).
+    bool nan_here = false;
+#pragma unroll
+    for (int j = 0; j < kTopkMaxPerLane; j++)
+        nan_here |= lane + 64 * j < E && v[j] != v[j];
+    const bool any_nan = __any(nan_here);
     for (int round = 0; round < k; round++) {
-        // first index not yet chosen
-        int first = 0x7fffffff;
-        const unsigned open = ~taken & ((1u << kTopkMaxPerLane) - 1);
-        if (open)
-            first = lane + 64 * __builtin_ctz(open);
-        for (int w = 32; w > 0; w >>= 1)
-            first = min(first, __shfl_xor(first, w, 64));
-        const float fv = lg[first];
-        int best;
-        if (fv != fv) {
-            best = first;
-        } else {
+        int best = 0x7fffffff;
+        if (any_nan) {
+            int first = 0x7fffffff;
+            const unsigned open = ~taken & ((1u << kTopkMaxPerLane) - 1);
+            if (open)
+                first = lane + 64 * __builtin_ctz(open);
+            for (int w = 32; w > 0; w >>= 1)
+                first = min(first, __shfl_xor(first, w, 64));
+            if (lg[first] != lg[first])
+                best = first;
+        }
+        if (best == 0x7fffffff) {
             // largest non-NaN value not yet chosen, lowest index among equals
             float bv = 0.0f;
             int bi = 0x7fffffff;
@@ -250,7 +354,7 @@ __global__ __launch_bounds__(64) void moe_topk_kernel(const float *__restrict__ 
                 const int e = lane + 64 * j;
                 if (((taken >> j) & 1u) || v[j] != v[j])
                     continue;
-                if (bi == 0x7fffffff || v[j] > bv || (v[j] == bv && e < bi)) {
+                if (bi == 0x7fffffff || v[j] > bv) {  // e rises with j: equal values keep the lower index
                     bv = v[j];
                     bi = e;
                 }
@@ -272,16 +376,16 @@ __global__ __launch_bounds__(64) void moe_topk_kernel(const float *__restrict__ 
             chosen_l[round] = lg[best];
         }
     }
-    if (lane == 0) {
-        const float top = chosen_l[0];
-        float total = 0.0f;
-        for (int j = 0; j < k; j++) {
-            wv[j] = (float)exp((double)(chosen_l[j] - top));
-            total += wv[j];
-        }
-        for (int j = 0; j < k; j++)
-            weights[(size_t)t * k + j] = wv[j] / total;
-    }
+    __syncthreads();
+    // exp(l - top) in float64 for every slot at once; the sum in slot order.
+    if (lane < k)
+        wv[lane] = (float)exp((double)(chosen_l[lane] - chosen_l[0]));
+    __syncthreads();
+    float total = 0.0f;
+    for (int j = 0; j < k; j++)
+        total += wv[j];
+    if (lane < k)
+        weights[(size_t)t * k + lane] = wv[lane] / total;
 }
 
 // mid = GELUTable(gate) * up for one unit per workgroup row, then its Q8_0
@@ -476,25 +580,17 @@ int launch_moe_route(gx_ctx *ctx, const gx_weight *router, const float *router_s
     GX_CHECK(E <= 64 * kTopkMaxPerLane, "gx: %d experts exceed the router's limit of %d", E, 64 * kTopkMaxPerLane);
     GX_CHECK(k <= kTopkMax, "gx: top_k %d exceeds %d", k, kTopkMax);
     GX_CHECK(((uintptr_t)resid & 15) == 0 && ldr % 4 == 0, "gx: resid must be 16-byte aligned with ldr %% 4 == 0");
-    // The most router rows per workgroup that fit the LDS.
-    const size_t fixed = sizeof(float) * (size_t)logits_row_stride(D);
-    auto lds = [&](int ew) {
-        const int P = 64 / ew;
-        return fixed * ew + sizeof(float) * (2 * (size_t)P * kLogitsChunkPad + P);
-    };
-    const int ew = lds(4) <= 64 * 1024 ? 4 : lds(2) <= 64 * 1024 ? 2 : 1;
-    GX_CHECK(lds(ew) <= 64 * 1024, "gx: a router of width %d does not fit the LDS", D);
-    const dim3 grid((unsigned)((E + ew - 1) / ew), (unsigned)((M + 64 / ew - 1) / (64 / ew)));
     const float *rw = (const float *)router->dev;
-    if (ew == 4)
-        moe_logits_kernel<4><<<grid, kLogitsThreads, lds(4), ctx->stream>>>(rw, D, E, router_scale, resid, ldr, M,
-                                                                           eps, logits);
-    else if (ew == 2)
-        moe_logits_kernel<2><<<grid, kLogitsThreads, lds(2), ctx->stream>>>(rw, D, E, router_scale, resid, ldr, M,
-                                                                           eps, logits);
-    else
-        moe_logits_kernel<1><<<grid, kLogitsThreads, lds(1), ctx->stream>>>(rw, D, E, router_scale, resid, ldr, M,
-                                                                           eps, logits);
+    if (M <= 4 && D <= kLogitsOneMaxD) {
+        const size_t lds = 2 * sizeof(float) * (size_t)D;
+        moe_logits_one_kernel<<<dim3((unsigned)E, (unsigned)M), kLogitsThreads, lds, ctx->stream>>>(
+            rw, D, E, router_scale, resid, ldr, eps, logits);
+    } else {
+        constexpr int EW = 4, P = 64 / EW;
+        const dim3 grid((unsigned)((E + EW - 1) / EW), (unsigned)((M + P - 1) / P));
+        moe_logits_kernel<EW><<<grid, kLogitsThreads, 0, ctx->stream>>>(rw, D, E, router_scale, resid, ldr, M, eps,
+                                                                         logits);
+    }
     if (int rc = check_launch("moe_logits"))
         return rc;
     moe_topk_kernel<<<M, 64, 0, ctx->stream>>>(logits, E, k, ids, weights);

@@ -125,11 +125,14 @@ def test_route_ties_go_to_lower_index(dev, orc):
     assert ids[0] == 2 and ids[1] == 5
 
 
-@pytest.mark.parametrize("D,E,k,M", [(4096, 10, 3, 33), (6144, 6, 2, 5), (256, 130, 8, 17)])
+@pytest.mark.parametrize("D,E,k,M", [(4096, 10, 3, 33), (6144, 6, 2, 5), (6144, 6, 2, 3), (7168, 5, 2, 1),
+                                     (8192, 4, 2, 2), (256, 130, 8, 17)])
 def test_route_layouts_bit_exact(dev, orc, D, E, k, M):
-    """The router's other shapes: rows per workgroup 2 (D = 4096) and 1
-    (D = 6144) where four rows do not fit the LDS, an expert count that is not
-    a multiple of four, and positions spanning several workgroups."""
+    """The router's two logits kernels at their edges: one workgroup per
+    (expert, position) for up to four positions while the row and input fit
+    the LDS (D <= 7168), the streamed kernel otherwise (D = 8192 even at two
+    positions); an expert count that is not a multiple of four; positions
+    spanning several workgroups."""
     m = Moe.__new__(Moe)
     g = synth.rng(D + E)
     m.D, m.E, m.k, m.dev = D, E, k, dev
