@@ -46,6 +46,8 @@ def parse():
     p.add_argument("--only", default="",
                    help="profiling: run only this leg (c1, c0, c2, c4) and exit; 'copy' runs the 256 MiB "
                         "device copy that scales the FETCH_SIZE / WRITE_SIZE counters")
+    p.add_argument("--c2-m", type=int, default=0, help="profiling: config 2 at this M only")
+    p.add_argument("--c2-path", default="", help="profiling: config 2 on this kernel only (f16, i8)")
     return p.parse_args()
 
 
@@ -174,16 +176,20 @@ def main():
         w0d = capi.Weight(ctx, w0, capi.Q4_0, r0, c0)
         g2 = synth.rng(2)
         for M in (64, 512, 2048):
+            if args.c2_m and M != args.c2_m:
+                continue
             x2 = synth.activations(g2, M, c0)
             x2d = dev(x2)
             q2 = torch.empty((M, c0), dtype=torch.int8, device="cuda")
             s2 = torch.empty((M, c0 // 32), dtype=torch.float32, device="cuda")
             qs2 = torch.empty((M, c0 // 32), dtype=torch.int32, device="cuda")
-            h2 = torch.empty((M, c0), dtype=torch.int16, device="cuda")
+            h2 = torch.empty((capi.q16_elems(M, c0),), dtype=torch.int16, device="cuda")
             y2 = torch.empty((M, r0), dtype=torch.float32, device="cuda")
             call("gx_quantize_q8_0", ctx.ptr, vp(x2d), c0, M, c0, vp(q2), vp(s2), vp(qs2), None, vp(h2))
             # fp16-MFMA kernel (q16 given) and int8-MFMA kernel (q16 withheld)
             for label, q16 in (("f16", h2), ("i8", None)):
+                if args.c2_path and label != args.c2_path:
+                    continue
                 for _ in range(5):
                     call("gx_matmul_q4_0", ctx.ptr, w0d.ptr, vp(q2), vp(s2), vp(qs2), vp(q16), M, 0, r0, None,
                          vp(y2), r0)

@@ -10,6 +10,9 @@ Flags that matter for parity and safety:
                       golem's amd64 code does.
   -Xclang -target-feature -Xclang -packed-fp32-ops
                       no packed-fp32 VALU instructions in the device code.
+  -mllvm -amdgpu-mfma-vgpr-form
+                      MFMA results in ordinary VGPRs: the epilogue's fma reads
+                      them directly instead of copying each out of an AGPR.
 """
 import concurrent.futures
 import os
@@ -27,6 +30,7 @@ FLAGS = [
     "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
     "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wall", "-Wno-unused-function", "-Wno-unused-variable",
 ]
 

@@ -173,3 +173,9 @@ def vp(x):
     if hasattr(x, "data_ptr"):
         return ctypes.c_void_p(x.data_ptr())
     return ctypes.c_void_p(int(x))
+
+
+def q16_elems(M, K):
+    """Values in the fp16 copy of a Q8_0 batch (gx_quantize_q8_0's q16):
+    tokens padded to a multiple of 32."""
+    return (M + 31) // 32 * 32 * K

@@ -289,23 +289,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) voi
 // partial sum is an integer below 2^24 in magnitude, so the fp32 result is
 // the exact per-block integer, already a float: the epilogue is one fma per
 // element per block, where the int8 kernel needs a conversion and an fma.
-// The caller provides the activation's fp16 copy (the quantiser writes it);
-// the weights are widened to fp16 once per workgroup as a stage is staged.
 //
-// Tile: 64 rows x 128 tokens per workgroup; each wavefront 32 rows x 64
-// tokens (two 32x32 tiles sharing the weight operand).  Stage = 2 blocks,
-// double buffered in LDS: fp16 weights [2][64][40] (rows padded to 80 B),
-// fp16 activations [128][2*32 + 8] (144 B per token), both scales as fp16.
-constexpr int kF16Stage = 2;                       // blocks per stage
-constexpr int kF16Tok = 128;                       // tokens per workgroup
-constexpr int kWRow = 40;                          // halves per weight row (32 + pad)
-constexpr int kARow = kF16Stage * kQ4Block + 8;    // halves per token row (64 + pad)
-struct StageF16 {
-    uint16_t w[kF16Stage][kTileRows][kWRow];       // 10 KiB
-    uint16_t a[kF16Tok][kARow];                    // 18 KiB
-    uint16_t dw[kF16Stage][kTileRows];
-    uint16_t da[kF16Stage][kF16Tok];
-};
+// Tile: a workgroup owns 64 rows (one R64 tile) x 32*NWT tokens; wavefront w
+// owns the 64 rows x token group w (32 tokens): two 32x32 MFMA tiles sharing
+// the activation operand.  The rows' nibbles are widened to fp16 once per
+// workgroup into LDS, four blocks per stage, double buffered: the next
+// stage's nibbles are in flight while this one's MFMAs run.  Each wavefront
+// reads its activation operands straight from the panel-ordered fp16 copy
+// (q16_offset): one contiguous 1 KiB per operand, one block ahead.
+constexpr int kFStage = 4;   // blocks per stage
+constexpr int kFWRow = 40;   // halves per staged weight row (32 + pad: 80-byte rows)
 
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef _Float16 v2h __attribute__((ext_vector_type(2)));
@@ -321,175 +314,209 @@ __device__ __forceinline__ void nibbles_to_f16(uint32_t n, uint32_t &lo, uint32_
     hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(v2h, b) - bias);
 }
 
-// One thread's share of a stage.  Weights: threads 0..127, chunk tid (block
-// tid / 64, row tid % 64).  Activations: chunks c = tid + 256 k (k < 4) of the
-// 1024 (token c / 8, 16-byte part c % 8, i.e. block (c % 8) / 4).  Weight
-// scales: threads 128..191, one 4-byte word of row tid - 128's chunk.
-// Activation scales: token tid / 2, block tid % 2.  Indices past the matrix
-// or the batch are clamped (in bounds, never used).
-struct FetchF16 {
-    v4u w, a[4];
-    unsigned dw;
-    float da;
-};
-
-template <bool DOTS>
-__device__ __forceinline__ void fetch_stage_f16(FetchF16 &f, const uint8_t *__restrict__ W, size_t plane0_bytes,
-                                                int B, int DC, const uint16_t *__restrict__ q16,
-                                                const float *__restrict__ scales, int K, int M, int tile, int m0,
-                                                int h, int tid) {
-    const int b0 = h * kF16Stage;
-    if (tid < 128) {
-        const int b = min(b0 + (tid >> 6), B - 1);
-        f.w = *(const v4u *)(W + (((size_t)tile * B + b) * kTileRows + (tid & 63)) * kChunk);
-    }
+// One block row of nibbles (16 bytes) -> its 32 fp16 weights in golem's
+// order in LDS: [0,16) from the low nibbles of bytes 0..15, [16,32) from the
+// high nibbles.
+__device__ __forceinline__ void widen_row(const v4u &w, uint16_t *row) {
+    const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+    uint32_t out[16];
 #pragma unroll
     for (int k = 0; k < 4; k++) {
-        const int c = tid + 256 * k;
-        const int m = min(m0 + (c >> 3), M - 1);
-        const int b = min(b0 + ((c & 7) >> 2), B - 1);
-        f.a[k] = *(const v4u *)(q16 + (size_t)m * K + (size_t)b * kQ4Block + 8 * (c & 3));
+        nibbles_to_f16(words[k] & 0x0F0F0F0Fu, out[2 * k], out[2 * k + 1]);
+        nibbles_to_f16((words[k] >> 4) & 0x0F0F0F0Fu, out[8 + 2 * k], out[8 + 2 * k + 1]);
     }
-    if (!DOTS) {
-        if (tid >= 128 && tid < 192) {
-            const unsigned *chunk = (const unsigned *)(W + plane0_bytes +
-                                                       (((size_t)tile * DC + (b0 >> 3)) * kTileRows + (tid - 128)) *
-                                                           kChunk);
-            f.dw = chunk[(b0 & 7) >> 1];  // blocks b0, b0 + 1 (b0 is even)
-        }
-        const int m = min(m0 + (tid >> 1), M - 1);
-        f.da = scales[(size_t)m * B + min(b0 + (tid & 1), B - 1)];
-    }
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+        *(v4u *)(row + 8 * k) = (v4u){out[4 * k], out[4 * k + 1], out[4 * k + 2], out[4 * k + 3]};
 }
 
-template <bool DOTS>
-__device__ __forceinline__ void commit_stage_f16(const FetchF16 &f, StageF16 &t, int nb, int tid) {
-    if (tid < 128) {  // widen one block row of nibbles to 32 fp16 weights in golem's order:
-                      // [0,16) from the low nibbles of bytes 0..15, [16,32) from the high.
-        const uint32_t words[4] = {f.w.x, f.w.y, f.w.z, f.w.w};
-        uint32_t out[16];
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            nibbles_to_f16(words[k] & 0x0F0F0F0Fu, out[2 * k], out[2 * k + 1]);
-            nibbles_to_f16((words[k] >> 4) & 0x0F0F0F0Fu, out[8 + 2 * k], out[8 + 2 * k + 1]);
-        }
-        uint16_t *row = t.w[tid >> 6][tid & 63];
-#pragma unroll
-        for (int k = 0; k < 4; k++)
-            *(v4u *)(row + 8 * k) = (v4u){out[4 * k], out[4 * k + 1], out[4 * k + 2], out[4 * k + 3]};
-    }
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        const int c = tid + 256 * k;
-        *(v4u *)&t.a[c >> 3][(c & 7) * 8] = f.a[k];
-    }
-    if (!DOTS) {
-        if (tid >= 128 && tid < 192) {  // a block past the row gets scale 0
-            t.dw[0][tid - 128] = (uint16_t)(f.dw & 0xFFFFu);
-            t.dw[1][tid - 128] = nb > 1 ? (uint16_t)(f.dw >> 16) : (uint16_t)0;
-        }
-        t.da[tid & 1][tid >> 1] = (uint16_t)float_to_half_bits(f.da);
-    }
-}
-
-template <bool DOTS>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) void q4_0_gemm_f16_kernel(
+template <int NWT, bool DOTS>
+__global__ __launch_bounds__(64 * NWT) void q4_0_gemm_f16_kernel(
     const uint8_t *__restrict__ W, size_t plane0_bytes, int B, int DC, const uint16_t *__restrict__ q16,
-    const float *__restrict__ scales, int K, int M, int tile0, int row_start, int row_end,
-    const float *__restrict__ bias, float *__restrict__ y, int ldy, int32_t *__restrict__ dots) {
-    __shared__ StageF16 st[2];
+    const float *__restrict__ scales, int M, int tile0, int row_start, int row_end, const float *__restrict__ bias,
+    float *__restrict__ y, int ldy, int32_t *__restrict__ dots) {
+    constexpr int NT = 64 * NWT;
+    constexpr int RW = (kFStage * kTileRows + NT - 1) / NT;  // 16-byte nibble chunks per thread per stage
+    __shared__ __attribute__((aligned(16))) uint16_t wl[2][kFStage][kTileRows][kFWRow];
+    __shared__ uint16_t dwl[2][kFStage][kTileRows];
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wv = tid >> 6;
+    const int lane = tid & 63, wv = tid >> 6, li = lane & 31, g = lane >> 5;
     const int tile = tile0 + blockIdx.x;
     const int n0 = tile * kTileRows;
-    const int m0 = blockIdx.y * kF16Tok;
-    const int nw = 32 * (wv & 1), mw = 64 * (wv >> 1);
-    const int li = lane & 31, g = lane >> 5;
-    const int H = (B + kF16Stage - 1) / kF16Stage;  // stages; four make a stretch
+    const int Gn = (M + 31) / 32;
+    const int G = blockIdx.y * NWT + wv;  // this wavefront's token group
+    const int Gc = min(G, Gn - 1);
+    const int t = 32 * G + li;            // this lane's token
+    const float *srow = scales ? scales + (size_t)min(t, M - 1) * B : nullptr;
+    const uint16_t *panel = q16 + (size_t)Gc * B * 1024 + 8 * lane;  // + (2b + h) * 512
+    const int S = (B + kFStage - 1) / kFStage;
     const int nrows = row_end - row_start;
+
+    // Stage h's nibbles: chunk c (block c / 64, row c % 64) for c = tid + NT i;
+    // clamped past the last block (never used).  Scales: rows tid < 64, the
+    // 8 bytes of the row's scale chunk that hold the stage's 4 blocks.
+    v4u raw[RW];
+    uint2 sraw = make_uint2(0, 0);
+    auto fetch_w = [&](int h, v4u (&r)[RW], uint2 &sr) {
+#pragma unroll
+        for (int i = 0; i < RW; i++) {
+            const int c = min(tid + NT * i, kFStage * kTileRows - 1);
+            const int b = min(h * kFStage + (c >> 6), B - 1);
+            r[i] = *(const v4u *)(W + (((size_t)tile * B + b) * kTileRows + (c & 63)) * kChunk);
+        }
+        if (!DOTS && tid < kTileRows) {
+            const int b0 = h * kFStage;
+            sr = *(const uint2 *)(W + plane0_bytes + (((size_t)tile * DC + (b0 >> 3)) * kTileRows + tid) * kChunk +
+                                  2 * (b0 & 7));
+        }
+    };
+    auto commit_w = [&](int buf, const v4u (&r)[RW], const uint2 &sr) {
+#pragma unroll
+        for (int i = 0; i < RW; i++) {
+            const int c = tid + NT * i;
+            if (c < kFStage * kTileRows)
+                widen_row(r[i], wl[buf][c >> 6][c & 63]);
+        }
+        if (!DOTS && tid < kTileRows) {
+            dwl[buf][0][tid] = (uint16_t)(sr.x & 0xFFFFu);
+            dwl[buf][1][tid] = (uint16_t)(sr.x >> 16);
+            dwl[buf][2][tid] = (uint16_t)(sr.y & 0xFFFFu);
+            dwl[buf][3][tid] = (uint16_t)(sr.y >> 16);
+        }
+    };
 
     v16f acc0, acc1, tot0, tot1;
 #pragma unroll
     for (int e = 0; e < 16; e++)
         acc0[e] = acc1[e] = tot0[e] = tot1[e] = 0.0f;
     const v16f zero_f = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-    const int bm0 = m0 + mw + li, bm1 = bm0 + 32;
-    const bool v0 = bm0 < M, v1 = bm1 < M;
 
-    FetchF16 f;
-    fetch_stage_f16<DOTS>(f, W, plane0_bytes, B, DC, q16, scales, K, M, tile, m0, 0, tid);
-    commit_stage_f16<DOTS>(f, st[0], min(kF16Stage, B), tid);
+    // Activation operands a stage ahead, in two register sets that alternate
+    // by stage (the stage loop is unrolled by two, so each set's registers are
+    // fixed): slot j of a set holds block 4s + j's two panels and scale
+    // (clamped past the last block; never used there).
+    v8h PA0[kFStage], PA1[kFStage], PB0[kFStage], PB1[kFStage];
+    float dA[kFStage], dB[kFStage];
+#define GX_F16_LOAD_SET(P0, P1, DS, s)                                                                               \
+    do {                                                                                                             \
+        for (int j = 0; j < kFStage; j++) {                                                                          \
+            const int bn = min((s) * kFStage + j, B - 1);                                                            \
+            P0[j] = *(const v8h *)(panel + (size_t)(2 * bn) * 512);                                                  \
+            P1[j] = *(const v8h *)(panel + (size_t)(2 * bn + 1) * 512);                                              \
+            DS[j] = DOTS ? 0.0f : srow[bn];                                                                          \
+        }                                                                                                            \
+    } while (0)
+
+// One stage, software-pipelined across the two row tiles: tile 0's MFMAs for
+// block j, then tile 1's fmas for block j - 1 (results of the previous
+// block's MFMAs), then tile 1's MFMAs for block j, then tile 0's fmas for
+// block j -- each batch of fmas runs while an independent batch of MFMAs is
+// in the matrix core.  `pend` is the block whose tile-1 fmas are pending (-1:
+// none).
+#define GX_F16_FMA(D, SC, ACC, TOT, bb)                                                                              \
+    do {                                                                                                             \
+        for (int e = 0; e < 16; e++)                                                                                 \
+            ACC[e] = fmaf(D[e], SC[e], ACC[e]);                                                                      \
+        if (((bb) & (kStretch - 1)) == kStretch - 1 || (bb) == B - 1) { /* a stretch ends */                         \
+            for (int e = 0; e < 16; e++) {                                                                           \
+                TOT[e] = TOT[e] + ACC[e];                                                                            \
+                ACC[e] = 0.0f;                                                                                       \
+            }                                                                                                        \
+        }                                                                                                            \
+    } while (0)
+
+#define GX_F16_DOTS(D, roff, bb)                                                                                     \
+    do {                                                                                                             \
+        if (t < M) {                                                                                                 \
+            for (int e = 0; e < 16; e++) {                                                                           \
+                const int n = n0 + (roff) + 8 * (e >> 2) + 4 * g + (e & 3);                                          \
+                if (n >= row_start && n < row_end)                                                                   \
+                    dots[((size_t)t * nrows + (n - row_start)) * B + (bb)] = (int32_t)D[e];                          \
+            }                                                                                                        \
+        }                                                                                                            \
+    } while (0)
+
+#define GX_F16_STAGE(P0, P1, DS, h)                                                                                  \
+    do {                                                                                                             \
+        const int buf = (h) & 1;                                                                                     \
+        const int nb = min(kFStage, B - (h) * kFStage);                                                              \
+        for (int j = 0; j < kFStage; j++) {                                                                          \
+            if (j < nb) {                                                                                            \
+                const int b = (h) * kFStage + j;                                                                     \
+                const v4h Bs = k0_operand(float_to_half_bits(DS[j]), g == 0);                                        \
+                {                                                                                                    \
+                    const v8h A00 = *(const v8h *)&wl[buf][j][li][8 * g];                                            \
+                    const v8h A01 = *(const v8h *)&wl[buf][j][li][16 + 8 * g];                                       \
+                    D0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(A00, P0[j], zero_f, 0, 0, 0);                         \
+                    D0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(A01, P1[j], D0, 0, 0, 0);                            \
+                    if (!DOTS)                                                                                       \
+                        S0 = __builtin_amdgcn_mfma_f32_32x32x8f16(k0_operand(dwl[buf][j][li], g == 0), Bs, zero_f,  \
+                                                                  0, 0, 0);                                          \
+                }                                                                                                    \
+                if (!DOTS && pend >= 0)                                                                              \
+                    GX_F16_FMA(D1, S1, acc1, tot1, pend);                                                            \
+                {                                                                                                    \
+                    const v8h A10 = *(const v8h *)&wl[buf][j][32 + li][8 * g];                                       \
+                    const v8h A11 = *(const v8h *)&wl[buf][j][32 + li][16 + 8 * g];                                  \
+                    D1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(A10, P0[j], zero_f, 0, 0, 0);                         \
+                    D1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(A11, P1[j], D1, 0, 0, 0);                            \
+                    if (!DOTS)                                                                                       \
+                        S1 = __builtin_amdgcn_mfma_f32_32x32x8f16(k0_operand(dwl[buf][j][32 + li], g == 0), Bs,     \
+                                                                  zero_f, 0, 0, 0);                                  \
+                }                                                                                                    \
+                if (DOTS) {                                                                                          \
+                    GX_F16_DOTS(D0, 0, b);                                                                           \
+                    GX_F16_DOTS(D1, 32, b);                                                                          \
+                } else {                                                                                             \
+                    GX_F16_FMA(D0, S0, acc0, tot0, b);                                                               \
+                }                                                                                                    \
+                pend = b;                                                                                            \
+            }                                                                                                        \
+        }                                                                                                            \
+    } while (0)
+
+    v16f D0 = zero_f, D1 = zero_f, S0 = zero_f, S1 = zero_f;
+    int pend = -1;
+    fetch_w(0, raw, sraw);
+    GX_F16_LOAD_SET(PA0, PA1, dA, 0);
+    commit_w(0, raw, sraw);
     __syncthreads();
-    for (int h = 0; h < H; h++) {
-        StageF16 &cur = st[h & 1];
-        if (h + 1 < H)  // in flight during this stage's arithmetic
-            fetch_stage_f16<DOTS>(f, W, plane0_bytes, B, DC, q16, scales, K, M, tile, m0, h + 1, tid);
-        const int nb = min(kF16Stage, B - h * kF16Stage);
-#pragma unroll
-        for (int j = 0; j < kF16Stage; j++) {
-            const v8h A0 = *(const v8h *)&cur.w[j][nw + li][8 * g];
-            const v8h A1 = *(const v8h *)&cur.w[j][nw + li][16 + 8 * g];
-            const v8h P0 = *(const v8h *)&cur.a[mw + li][j * kQ4Block + 8 * g];
-            const v8h P1 = *(const v8h *)&cur.a[mw + li][j * kQ4Block + 16 + 8 * g];
-            const v8h Q0 = *(const v8h *)&cur.a[mw + 32 + li][j * kQ4Block + 8 * g];
-            const v8h Q1 = *(const v8h *)&cur.a[mw + 32 + li][j * kQ4Block + 16 + 8 * g];
-            v16f D0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(A0, P0, zero_f, 0, 0, 0);
-            D0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(A1, P1, D0, 0, 0, 0);
-            v16f D1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(A0, Q0, zero_f, 0, 0, 0);
-            D1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(A1, Q1, D1, 0, 0, 0);
-            if (DOTS) {
-                if (j < nb) {
-                    const int b = h * kF16Stage + j;
-#pragma unroll
-                    for (int e = 0; e < 16; e++) {
-                        const int n = n0 + nw + 8 * (e >> 2) + 4 * g + (e & 3);
-                        if (n >= row_start && n < row_end) {
-                            if (v0)
-                                dots[((size_t)bm0 * nrows + (n - row_start)) * B + b] = (int32_t)D0[e];
-                            if (v1)
-                                dots[((size_t)bm1 * nrows + (n - row_start)) * B + b] = (int32_t)D1[e];
-                        }
-                    }
-                }
-            } else {
-                // Past the last block the weight scale is 0: fma(d, 0, acc) == acc.
-                const v4h As = k0_operand(cur.dw[j][nw + li], g == 0);
-                const v16f S0 = __builtin_amdgcn_mfma_f32_32x32x8f16(As, k0_operand(cur.da[j][mw + li], g == 0),
-                                                                     zero_f, 0, 0, 0);
-                const v16f S1 = __builtin_amdgcn_mfma_f32_32x32x8f16(As, k0_operand(cur.da[j][mw + 32 + li], g == 0),
-                                                                     zero_f, 0, 0, 0);
-#pragma unroll
-                for (int e = 0; e < 16; e++) {
-                    acc0[e] = fmaf(D0[e], S0[e], acc0[e]);
-                    acc1[e] = fmaf(D1[e], S1[e], acc1[e]);
-                }
-            }
+    for (int h = 0; h < S; h += 2) {  // set A holds stage h
+        if (h + 1 < S) {  // in flight during this stage's arithmetic
+            fetch_w(h + 1, raw, sraw);
+            GX_F16_LOAD_SET(PB0, PB1, dB, h + 1);
         }
-        if (!DOTS && ((h & 3) == 3 || h + 1 == H)) {  // a stretch is four stages
-#pragma unroll
-            for (int e = 0; e < 16; e++) {
-                tot0[e] = tot0[e] + acc0[e];
-                tot1[e] = tot1[e] + acc1[e];
-                acc0[e] = 0.0f;
-                acc1[e] = 0.0f;
-            }
-        }
-        if (h + 1 < H)
-            commit_stage_f16<DOTS>(f, st[(h + 1) & 1], min(kF16Stage, B - (h + 1) * kF16Stage), tid);
+        GX_F16_STAGE(PA0, PA1, dA, h);
+        if (h + 1 >= S)
+            break;
+        commit_w((h + 1) & 1, raw, sraw);
         __syncthreads();
+        if (h + 2 < S) {
+            fetch_w(h + 2, raw, sraw);
+            GX_F16_LOAD_SET(PA0, PA1, dA, h + 2);
+        }
+        GX_F16_STAGE(PB0, PB1, dB, h + 1);
+        if (h + 2 < S) {
+            commit_w(h & 1, raw, sraw);
+            __syncthreads();
+        }
     }
-    if (DOTS)
+    if (!DOTS && pend >= 0)  // the last block's tile-1 fmas
+        GX_F16_FMA(D1, S1, acc1, tot1, pend);
+#undef GX_F16_LOAD_SET
+#undef GX_F16_STAGE
+#undef GX_F16_FMA
+#undef GX_F16_DOTS
+    if (DOTS || t >= M)
         return;
 #pragma unroll
     for (int e = 0; e < 16; e++) {
-        const int n = n0 + nw + 8 * (e >> 2) + 4 * g + (e & 3);
-        if (n >= row_start && n < row_end) {
-            const float bn = bias ? bias[n] : 0.0f;
-            if (v0)
-                y[(size_t)bm0 * ldy + n] = bias ? tot0[e] + bn : tot0[e];
-            if (v1)
-                y[(size_t)bm1 * ldy + n] = bias ? tot1[e] + bn : tot1[e];
-        }
+        const int r = 8 * (e >> 2) + 4 * g + (e & 3);
+        const int na = n0 + r, nb2 = n0 + 32 + r;
+        if (na >= row_start && na < row_end)
+            y[(size_t)t * ldy + na] = bias ? tot0[e] + bias[na] : tot0[e];
+        if (nb2 >= row_start && nb2 < row_end)
+            y[(size_t)t * ldy + nb2] = bias ? tot1[e] + bias[nb2] : tot1[e];
     }
 }
 
@@ -532,15 +559,28 @@ int launch_q4_0_gemm_f16(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, co
                          const float *scales, int M, int row_start, int row_end, const float *bias, float *y, int ldy,
                          int32_t *dots) {
     const int tile0 = row_start / kTileRows;
-    dim3 grid((row_end + kTileRows - 1) / kTileRows - tile0, (M + kF16Tok - 1) / kF16Tok);
-    if (dots)
-        q4_0_gemm_f16_kernel<true><<<grid, 256, 0, ctx->stream>>>(mat, w->plane0_bytes, w->blocks, w->dchunks, q16,
-                                                                  scales, w->cols, M, tile0, row_start, row_end, bias,
-                                                                  y, ldy, dots);
+    const unsigned tiles = (unsigned)((row_end + kTileRows - 1) / kTileRows - tile0);
+    const int groups = (M + 31) / 32;
+    // Token groups per workgroup: wider workgroups share the widening of the
+    // weights among more tokens; narrower ones keep more workgroups in flight.
+    const int nwt = groups <= 32 ? 2 : 4;
+    const dim3 grid(tiles, (unsigned)((groups + nwt - 1) / nwt));
+#define GX_F16_LAUNCH(N)                                                                                             \
+    do {                                                                                                             \
+        if (dots)                                                                                                    \
+            q4_0_gemm_f16_kernel<N, true><<<grid, 64 * N, 0, ctx->stream>>>(                                         \
+                mat, w->plane0_bytes, w->blocks, w->dchunks, q16, scales, M, tile0, row_start, row_end, bias, y, ldy, \
+                dots);                                                                                               \
+        else                                                                                                         \
+            q4_0_gemm_f16_kernel<N, false><<<grid, 64 * N, 0, ctx->stream>>>(                                        \
+                mat, w->plane0_bytes, w->blocks, w->dchunks, q16, scales, M, tile0, row_start, row_end, bias, y, ldy, \
+                dots);                                                                                               \
+    } while (0)
+    if (nwt == 2)
+        GX_F16_LAUNCH(2);
     else
-        q4_0_gemm_f16_kernel<false><<<grid, 256, 0, ctx->stream>>>(mat, w->plane0_bytes, w->blocks, w->dchunks, q16,
-                                                                   scales, w->cols, M, tile0, row_start, row_end,
-                                                                   bias, y, ldy, dots);
+        GX_F16_LAUNCH(4);
+#undef GX_F16_LAUNCH
     return check_launch("q4_0_gemm_f16");
 }
 

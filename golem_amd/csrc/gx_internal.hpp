@@ -37,6 +37,18 @@ constexpr int kQ6Chunks = 13;     // ql 8 + qh 4 + scales 1
 // kernel here follows).  Eight blocks is also one scale chunk.
 constexpr int kStretch = 8;
 
+// The fp16 copy of a Q8_0 activation (q16) is laid out in the operand order
+// of v_mfma_f32_32x32x16_f16: tokens in groups of 32, and for group G, block
+// b and k-half h (inputs 32b + 16h .. + 15) one 1 KiB panel in which lane
+// 32g + li of a wavefront finds, at 16 bytes per lane, token 32G + li's inputs
+// 32b + 16h + 8g .. + 7.  The buffer holds ceil(M/32)*32 tokens; tokens past
+// M are zero.
+__host__ __device__ inline size_t q16_offset(int t, int k, int blocks) {
+    const int G = t >> 5, li = t & 31, b = k >> 5, j = k & 31;
+    const int h = j >> 4, g = (j >> 3) & 1, e = j & 7;
+    return ((((size_t)G * blocks + b) * 2 + h) * 64 + 32 * g + li) * 8 + e;
+}
+
 int fail(int code, const char *fmt, ...);
 int check_launch(const char *what);
 

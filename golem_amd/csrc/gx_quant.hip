@@ -12,18 +12,23 @@ namespace gx {
 namespace {
 
 // One lane per element, 32 lanes per block: a wavefront quantises two blocks.
-// x is [M][ldx]; q [M][K], scales/qsum/corr [M][K/32].
-__global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float *__restrict__ x, int ldx, int M, int K,
-                                                            int8_t *__restrict__ q, float *__restrict__ scales,
-                                                            int32_t *__restrict__ qsum, float *__restrict__ corr,
-                                                            uint16_t *__restrict__ q16) {
+// x is [M][ldx]; q [M][K], scales/qsum/corr [M][K/32]; q16 in panel order
+// (q16_offset), over Mp = ceil(M/32)*32 tokens, the ones past M zero.
+__global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float *__restrict__ x, int ldx, int M, int Mp,
+                                                            int K, int8_t *__restrict__ q,
+                                                            float *__restrict__ scales, int32_t *__restrict__ qsum,
+                                                            float *__restrict__ corr, uint16_t *__restrict__ q16) {
     const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const size_t total = (size_t)M * K;
-    // total is a multiple of 32 and blocks are 256 threads, so a 32-lane
-    // group is either wholly inside or wholly outside the batch.
-    if (gid >= total)
+    // M*K and Mp*K are multiples of 32 and blocks are 256 threads, so a
+    // 32-lane group is wholly inside or wholly outside each range.
+    if (gid >= (size_t)(q16 ? Mp : M) * K)
         return;
     const int m = (int)(gid / K), k = (int)(gid % K);
+    const size_t o16 = q16 ? q16_offset(m, k, K >> 5) : 0;
+    if (m >= M) {  // padding tokens of the fp16 copy
+        q16[o16] = 0;
+        return;
+    }
     const float v = x[(size_t)m * ldx + k];
     float peak = fabsf(v);
 #pragma unroll
@@ -34,7 +39,7 @@ __global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float *__restr
     if (peak == 0.0f) {
         q[gid] = 0;
         if (q16)
-            q16[gid] = 0;
+            q16[o16] = 0;
         if ((k & 31) == 0) {
             scales[index] = 0.0f;
             qsum[index] = 0;
@@ -51,7 +56,7 @@ __global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float *__restr
     n = n > 127 ? 127 : (n < -128 ? -128 : n);
     q[gid] = (int8_t)n;
     if (q16)  // the same integer as fp16 (exact: |n| <= 128)
-        q16[gid] = float_to_half_bits((float)n);
+        q16[o16] = float_to_half_bits((float)n);
     int32_t sum = n;
 #pragma unroll
     for (int off = 16; off > 0; off >>= 1)
@@ -135,10 +140,11 @@ __global__ __launch_bounds__(256) void quantize_q8_k_kernel(const float *__restr
 
 int launch_quantize_q8_0(gx_ctx *ctx, const float *x, int ldx, int M, int K, int8_t *q, float *scales, int32_t *qsum,
                          float *corr, uint16_t *q16) {
-    const size_t total = (size_t)M * K;
+    const int Mp = (M + 31) / 32 * 32;
+    const size_t total = (size_t)(q16 ? Mp : M) * K;
     const int threads = 256;
     quantize_q8_0_kernel<<<(unsigned)((total + threads - 1) / threads), threads, 0, ctx->stream>>>(
-        x, ldx, M, K, q, scales, qsum, corr, q16);
+        x, ldx, M, Mp, K, q, scales, qsum, corr, q16);
     return check_launch("quantize_q8_0");
 }
 

@@ -26,7 +26,10 @@
  *     scales float   [M][K/32]   the fp16-rounded scale, held as float
  *     qsum   int32   [M][K/32]   sum of the block's 32 q values
  *     corr   float   [M][K/32]   (8*scale)*float(qsum), golem's Corr (optional)
- *     q16    fp16    [M][K]      the same q values as fp16 (optional; exact)
+ *     q16    fp16    the same q values as fp16 (optional; exact), in the
+ *                    operand order of the fp16 MFMA: ceil(M/32)*32*K values;
+ *                    token t's input k sits at q16_offset below; tokens past
+ *                    M are zero
  *   Q8_K activations (Batch.QK/KScales/BSums, nn/batch.go:29-32), same layout
  *   as golem's:
  *     q      int8    [M][K]
@@ -126,8 +129,12 @@ int gx_weight_rows(gx_ctx *ctx, const gx_weight *w, int expert, const int32_t *i
 
 /* Batch.Quantize / QuantizeRange / QuantizeColumnRange (nn/batch.go:69-143)
  * for M activations of K floats at x[m*ldx ...] (device).  corr and q16 may
- * be NULL; q16 (uint16 storage of fp16) is what the fp16-MFMA batch product
- * reads.  K must be a multiple of 32 (nn/batch.go:49-51). */
+ * be NULL; q16 (uint16 storage of fp16, ceil(M/32)*32*K values) is what the
+ * fp16-MFMA batch product reads.  In q16, token t's input k is at
+ *   ((((t/32)*(K/32) + k/32)*2 + (k%32)/16)*64 + 32*((k%16)/8) + t%32)*8 + k%8:
+ * tokens in groups of 32, and per group, block and half-block one 1 KiB
+ * panel holding each lane's 8 operand values contiguously.  K must be a
+ * multiple of 32 (nn/batch.go:49-51). */
 int gx_quantize_q8_0(gx_ctx *ctx, const float *x, int ldx, int M, int K, int8_t *q, float *scales, int32_t *qsum,
                      float *corr, uint16_t *q16);
 

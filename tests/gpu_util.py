@@ -58,7 +58,7 @@ class Device:
         sc = self.empty((M, K // 32), np.float32)
         qs = self.empty((M, K // 32), np.int32)
         co = self.empty((M, K // 32), np.float32) if with_corr else None
-        q16 = self.empty((M, K), np.int16) if with_q16 else None
+        q16 = self.empty((capi.q16_elems(M, K),), np.int16) if with_q16 else None
         capi.call("gx_quantize_q8_0", self.ctx.ptr, capi.vp(xd), K, M, K, capi.vp(q), capi.vp(sc), capi.vp(qs),
                   capi.vp(co), capi.vp(q16))
         return q, sc, qs, q16, co
@@ -114,3 +114,12 @@ class Device:
         out = self.empty((len(ids), w.cols), np.float32)
         capi.call("gx_weight_rows", self.ctx.ptr, w.ptr, expert, capi.vp(idd), len(ids), capi.vp(out))
         return self.get(out)
+
+
+def q16_rows(q16, M, K):
+    """The panel-ordered fp16 copy (gx_quantize_q8_0's q16) back to token rows
+    [ceil(M/32)*32][K], as float32."""
+    Mp = (M + 31) // 32 * 32
+    # [G][b][h][g][li][e] -> token 32G + li, input 32b + 16h + 8g + e
+    a = np.asarray(q16).view(np.float16).astype(np.float32).reshape(Mp // 32, K // 32, 2, 2, 32, 8)
+    return a.transpose(0, 4, 1, 2, 3, 5).reshape(Mp, K)

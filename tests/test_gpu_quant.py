@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 
 from golem_amd import synth
-from tests.gpu_util import log
+from tests.gpu_util import log, q16_rows
 
 pytestmark = pytest.mark.gpu
 
@@ -38,7 +38,9 @@ def test_q8_0_bit_exact(dev, orc, M, K):
     b = orc.Batch(x).quantize()
     q, sc, qs, q16, co = dev.quantize_q8_0(x)
     np.testing.assert_array_equal(dev.get(q), b.q_rows())
-    np.testing.assert_array_equal(dev.get(q16).view(np.float16).astype(np.float32), b.q_rows().astype(np.float32))
+    rows16 = q16_rows(dev.get(q16), M, K)
+    np.testing.assert_array_equal(rows16[:M], b.q_rows().astype(np.float32))
+    assert not np.any(rows16[M:]), "the fp16 copy's padding tokens are not zero"
     np.testing.assert_array_equal(dev.get(sc).view(np.uint32), b.scales_rows().view(np.uint32))
     np.testing.assert_array_equal(dev.get(qs), b.qsum_rows())
     np.testing.assert_array_equal(dev.get(co).view(np.uint32), b.corr_rows().view(np.uint32))
