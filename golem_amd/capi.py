@@ -59,6 +59,12 @@ _SIGNATURES = {
     "gx_moe_workspace_bytes": [_c_int, _c_int, _c_int, _c_int, _c_int, ctypes.POINTER(_c_size)],
     "gx_moe_route": [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, ctypes.c_float, _vp, _vp, _vp],
     "gx_moe_experts": [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _vp, _vp, _c_int, _vp, _c_size],
+    "gx_norm_quant": [_vp, _vp, _c_int, _vp, _c_int, _vp, _c_int, _c_int, ctypes.c_float, _vp, _c_int, _vp, _vp, _vp],
+    "gx_qwen_qk_rope": [_vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _vp, ctypes.c_float,
+                        _vp, _vp, _vp],
+    "gx_qwen_attention": [_vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _vp, _vp],
+    "gx_swiglu_quant": [_vp, _vp, _c_int, _c_int, _c_int, _vp, _vp, _vp],
+    "gx_argmax": [_vp, _vp, _c_int, _c_int, _c_int, _vp],
 }
 _RESTYPE = {"gx_last_error": ctypes.c_char_p}
 
@@ -167,7 +173,9 @@ class Weight:
 
 
 def vp(x):
-    """A device pointer argument from an int, a torch tensor or None."""
+    """A device pointer argument from an int, a torch tensor or None.  Only the
+    address is kept: the caller must hold the tensor until the work that uses
+    it has run."""
     if x is None:
         return None
     if hasattr(x, "data_ptr"):

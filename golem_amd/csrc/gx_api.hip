@@ -497,6 +497,82 @@ int gx_moe_route(gx_ctx *ctx, const gx_weight *router, const float *router_scale
     return ok();
 }
 
+int gx_norm_quant(gx_ctx *ctx, float *x, int ldx, const float *add, int lda, const float *gain, int M, int K,
+                  float eps, float *out, int ldo, int8_t *q, float *scales, int32_t *qsum) {
+    if (int rc = use(ctx))
+        return rc;
+    GX_CHECK(K > 0 && K % 32 == 0, "nn: activation length must be a multiple of the block size");
+    GX_CHECK(M >= 0 && ldx >= K && (!add || lda >= K) && (!out || ldo >= K), "gx: bad batch shape");
+    GX_CHECK(x && gain && (out || q) && (!q || (scales && qsum)), "gx: missing argument");
+    if (M == 0)
+        return ok();
+    if (int rc = gx::launch_qwen_norm_quant(ctx, x, ldx, add, lda, gain, M, K, eps, out, ldo, q, scales, qsum))
+        return rc;
+    return ok();
+}
+
+int gx_qwen_qk_rope(gx_ctx *ctx, const float *qkv, int ldqkv, int M, int heads, int kv_heads, int head_dim,
+                    const int32_t *positions, const float *q_norm, const float *k_norm, const float *rope_cos,
+                    const float *rope_sin, float eps, uint16_t *qh, uint16_t *kcache, uint16_t *vcache) {
+    if (int rc = use(ctx))
+        return rc;
+    GX_CHECK(heads > 0 && kv_heads > 0 && heads % kv_heads == 0, "gx: %d query heads over %d key-value heads", heads,
+             kv_heads);
+    GX_CHECK(M >= 0 && ldqkv >= (heads + 2 * kv_heads) * head_dim, "gx: bad batch shape");
+    GX_CHECK(qkv && positions && q_norm && k_norm && rope_cos && rope_sin && qh && kcache && vcache,
+             "gx: missing argument");
+    if (M == 0)
+        return ok();
+    if (int rc = gx::launch_qwen_qk_rope(ctx, qkv, ldqkv, M, heads, kv_heads, head_dim, positions, q_norm, k_norm,
+                                         rope_cos, rope_sin, eps, qh, kcache, vcache))
+        return rc;
+    return ok();
+}
+
+int gx_qwen_attention(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int kv_heads, int head_dim, int max_pos,
+                      const int32_t *positions, const uint16_t *kcache, const uint16_t *vcache, int8_t *q,
+                      float *scales, int32_t *qsum) {
+    if (int rc = use(ctx))
+        return rc;
+    GX_CHECK(heads > 0 && kv_heads > 0 && heads % kv_heads == 0, "gx: %d query heads over %d key-value heads", heads,
+             kv_heads);
+    GX_CHECK(M >= 0 && max_pos >= 0, "gx: bad batch shape");
+    GX_CHECK(qh && positions && kcache && vcache && q && scales && qsum, "gx: missing argument");
+    if (M == 0)
+        return ok();
+    // llama.cpp's 1/sqrt(head_dim), taken in float64 and rounded (qwen/attention.go:90-93)
+    const float scale = (float)(1.0 / sqrt((double)head_dim));
+    if (int rc = gx::launch_qwen_attention(ctx, qh, M, heads, kv_heads, head_dim, max_pos, positions, kcache, vcache,
+                                           scale, q, scales, qsum))
+        return rc;
+    return ok();
+}
+
+int gx_swiglu_quant(gx_ctx *ctx, const float *gu, int ldgu, int M, int ffn, int8_t *q, float *scales, int32_t *qsum) {
+    if (int rc = use(ctx))
+        return rc;
+    GX_CHECK(ffn > 0 && ffn % 32 == 0, "nn: activation length must be a multiple of the block size");
+    GX_CHECK(M >= 0 && ldgu >= 2 * ffn, "gx: bad batch shape");
+    GX_CHECK(gu && q && scales && qsum, "gx: missing argument");
+    if (M == 0)
+        return ok();
+    if (int rc = gx::launch_qwen_swiglu_quant(ctx, gu, ldgu, M, ffn, q, scales, qsum))
+        return rc;
+    return ok();
+}
+
+int gx_argmax(gx_ctx *ctx, const float *x, int ldx, int M, int n, int32_t *ids) {
+    if (int rc = use(ctx))
+        return rc;
+    GX_CHECK(M >= 0 && n > 0 && ldx >= n, "gx: bad shape");
+    GX_CHECK(x && ids, "gx: missing argument");
+    if (M == 0)
+        return ok();
+    if (int rc = gx::launch_argmax(ctx, x, ldx, M, n, ids))
+        return rc;
+    return ok();
+}
+
 int gx_moe_experts(gx_ctx *ctx, const gx_weight *gate_up, const gx_weight *down, const float *down_scale,
                    const float *x, int ldx, int M, int top_k, const int32_t *ids, const float *weights, float *out,
                    int ldo, void *workspace, size_t workspace_bytes) {

@@ -105,4 +105,94 @@ __device__ __forceinline__ int32_t q6_k_block_isum(const uint32_t *ql, const uin
     return isum;
 }
 
+// ---- RMSNormPlain's float64 sum (nn/ops.go:195-214) over 256 threads ------
+//
+// The squares are float32 products summed in float64 in a fixed tree: 512
+// partial sums, partial t holding elements t, t+512, t+1024, ... in order,
+// then halved pairwise (t + w for w = 256 .. 1).  golem sums left to right;
+// the two float64 sums differ by a few units in the 53rd bit, below the
+// float32 rounding of the mean except in rare ties.
+// Partial sums t and t + 256 of the norm's tree (this thread's pair), over
+// x[0, D) with x in LDS or global memory.  Elements are read 8 per partial
+// at a time; past D they read as element D - 1 and add 0.0, which leaves a
+// non-negative double unchanged.
+__device__ __forceinline__ void norm_partials(const float *x, int D, double &p0, double &p1) {
+    const int tid = threadIdx.x;
+    p0 = 0.0;
+    p1 = 0.0;
+    for (int base = 0; base < D; base += 8 * 512) {
+        float v0[8], v1[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            v0[u] = x[min(base + tid + 512 * u, D - 1)];
+            v1[u] = x[min(base + tid + 256 + 512 * u, D - 1)];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const float a = base + tid + 512 * u < D ? v0[u] : 0.0f;
+            const float b = base + tid + 256 + 512 * u < D ? v1[u] : 0.0f;
+            const float sa = a * a, sb = b * b;
+            p0 += (double)sa;
+            p1 += (double)sb;
+        }
+    }
+}
+
+// The rest of the tree (w = 256 .. 1) across a 256-thread workgroup; the
+// result is valid in thread 0.  `red` is 256 doubles of LDS.
+__device__ __forceinline__ double norm_tree(double p0, double p1, double *red) {
+    const int tid = threadIdx.x;
+    double s = p0 + p1;  // w = 256
+    red[tid] = s;
+    __syncthreads();
+    if (tid < 128)
+        s = s + red[tid + 128];
+    __syncthreads();
+    if (tid < 128)
+        red[tid] = s;
+    __syncthreads();
+    if (tid < 64) {
+        s = s + red[tid + 64];
+        for (int w = 32; w > 0; w >>= 1) {
+            const double o = __shfl_down(s, w, 64);
+            if (tid < w)
+                s = s + o;
+        }
+    }
+    return s;
+}
+
+__device__ __forceinline__ float norm_scale(double sum, int D, float eps) {
+    const float mean = (float)(sum / (double)D);
+    return (float)(1.0 / sqrt((double)(mean + eps)));
+}
+
+
+// Q8_0 of one element per lane of a 32-lane group (Batch.quantizeBlock,
+// nn/batch.go:109-143): returns q; the group's fp16-rounded scale and sum of
+// q come back in *stored and *sum (valid in every lane).
+__device__ __forceinline__ int32_t q8_0_lane(float v, float *stored, int32_t *sum) {
+    float peak = fabsf(v);
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1)
+        peak = fmaxf(peak, __shfl_xor(peak, off, 32));
+    if (peak == 0.0f) {
+        *stored = 0.0f;
+        *sum = 0;
+        return 0;
+    }
+    const float scale = __fdiv_rn(peak, 127.0f);
+    const float inverse = __fdiv_rn(127.0f, peak);
+    *stored = half_bits_to_float(float_to_half_bits(scale));
+    const float prod = v * inverse;
+    int32_t n = nearest_int(prod);
+    n = n > 127 ? 127 : (n < -128 ? -128 : n);
+    int32_t s = n;
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1)
+        s += __shfl_xor(s, off, 32);
+    *sum = s;
+    return n;
+}
+
 }  // namespace gx

@@ -120,6 +120,17 @@ int launch_moe_route(gx_ctx *ctx, const gx_weight *router, const float *router_s
 int launch_moe_experts(gx_ctx *ctx, const gx_weight *gate_up, const gx_weight *down, const float *down_scale,
                        const float *x, int ldx, int M, int k, const int32_t *ids, const float *weights, float *out,
                        int ldo, uint8_t *ws, const float *gelu_table);
+int launch_qwen_norm_quant(gx_ctx *ctx, float *x, int ldx, const float *add, int lda, const float *gain, int M, int K,
+                           float eps, float *out, int ldo, int8_t *q, float *scales, int32_t *qsum);
+int launch_qwen_qk_rope(gx_ctx *ctx, const float *qkv, int ldqkv, int M, int heads, int kv_heads, int hd,
+                        const int32_t *positions, const float *q_norm, const float *k_norm, const float *rope_cos,
+                        const float *rope_sin, float eps, uint16_t *qh, uint16_t *kcache, uint16_t *vcache);
+int launch_qwen_attention(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int kv_heads, int hd, int max_pos,
+                          const int32_t *positions, const uint16_t *kcache, const uint16_t *vcache, float scale,
+                          int8_t *q, float *scales, int32_t *qsum);
+int launch_qwen_swiglu_quant(gx_ctx *ctx, const float *gu, int ldgu, int M, int ffn, int8_t *q, float *scales,
+                             int32_t *qsum);
+int launch_argmax(gx_ctx *ctx, const float *x, int ldx, int M, int n, int32_t *out);
 int launch_f32_matvec(gx_ctx *ctx, const gx_weight *w, const float *x, int ldx, int M, int row_start, int row_end,
                       float *y, int ldy);
 }  // namespace gx

@@ -61,61 +61,6 @@ constexpr int kLogitsDepth = 8;      // chunks fetched ahead
 constexpr int kLogitsOneMaxD = 7168; // row + input in LDS: 57 KB
 constexpr int kLogitsOneF4 = kLogitsOneMaxD / 4 / kLogitsThreads;
 
-// Partial sums t and t + 256 of the norm's tree (this thread's pair), over
-// x[0, D) with x in LDS or global memory.  Elements are read 8 per partial
-// at a time; past D they read as element D - 1 and add 0.0, which leaves a
-// non-negative double unchanged.
-__device__ __forceinline__ void norm_partials(const float *x, int D, double &p0, double &p1) {
-    const int tid = threadIdx.x;
-    p0 = 0.0;
-    p1 = 0.0;
-    for (int base = 0; base < D; base += 8 * 512) {
-        float v0[8], v1[8];
-#pragma unroll
-        for (int u = 0; u < 8; u++) {
-            v0[u] = x[min(base + tid + 512 * u, D - 1)];
-            v1[u] = x[min(base + tid + 256 + 512 * u, D - 1)];
-        }
-#pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const float a = base + tid + 512 * u < D ? v0[u] : 0.0f;
-            const float b = base + tid + 256 + 512 * u < D ? v1[u] : 0.0f;
-            const float sa = a * a, sb = b * b;
-            p0 += (double)sa;
-            p1 += (double)sb;
-        }
-    }
-}
-
-// The rest of the tree (w = 256 .. 1) across a 256-thread workgroup; the
-// result is valid in thread 0.  `red` is 256 doubles of LDS.
-__device__ __forceinline__ double norm_tree(double p0, double p1, double *red) {
-    const int tid = threadIdx.x;
-    double s = p0 + p1;  // w = 256
-    red[tid] = s;
-    __syncthreads();
-    if (tid < 128)
-        s = s + red[tid + 128];
-    __syncthreads();
-    if (tid < 128)
-        red[tid] = s;
-    __syncthreads();
-    if (tid < 64) {
-        s = s + red[tid + 64];
-        for (int w = 32; w > 0; w >>= 1) {
-            const double o = __shfl_down(s, w, 64);
-            if (tid < w)
-                s = s + o;
-        }
-    }
-    return s;
-}
-
-__device__ __forceinline__ float norm_scale(double sum, int D, float eps) {
-    const float mean = (float)(sum / (double)D);
-    return (float)(1.0 / sqrt((double)(mean + eps)));
-}
-
 __global__ __launch_bounds__(kLogitsThreads) void moe_logits_one_kernel(const float *__restrict__ router, int D,
                                                                         int E, const float *__restrict__ router_scale,
                                                                         const float *__restrict__ resid, int ldr,

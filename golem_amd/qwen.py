@@ -1,0 +1,192 @@
+"""golem's Qwen3 dense decoder (qwen/) with every step on the device.
+
+qwen.Model.ForwardBatch (qwen/model.go:127-175) for M consecutive positions:
+the embedding rows (TokenEmbd.Row, a Q6_K dequantisation), then per block
+(qwen/block.go:32-102):
+
+    gx_norm_quant      x += previous FFN output; RMSNormPlain(attn_norm); Q8_0
+    gx_matmul_q4_0     Q, K and V, stacked by rows into one Q4_0 matrix
+    gx_qwen_qk_rope    head norms, RoPE, fp16 query, fp16 cache entries
+    gx_qwen_attention  scores, softmax, values; Q8_0 of the heads
+    gx_matmul_q4_0     O
+    gx_norm_quant      x += attention; RMSNormPlain(ffn_norm); Q8_0
+    gx_matmul_q4_0     Gate and Up, stacked by rows
+    gx_swiglu_quant    silu(gate) * up; Q8_0
+    gx_matmul_q4_0     Down
+
+and the final norm (the last block's residual folded in).  Logits
+(qwen/model.go:181-194) is QuantizeK plus the tied Q6_K head; greedy picks the
+largest logit, the lower id on ties.  Stacking Q/K/V and Gate/Up changes no
+result: every output row is its own product.
+
+Every kernel treats a position on its own, so a prompt read in one batch
+gives, bit for bit, what the same tokens give one at a time (golem's
+TestBatchAgreesWithOneAtATime, qwen/model_test.go:79).
+"""
+import math
+
+import numpy as np
+import torch
+
+from . import capi
+
+
+def rope_tables(dims, context, base):
+    """RoPETable.Prepare (nn/rope.go:33-59) for positions 0 .. context-1:
+    theta = pos * base^(-2i/dims) in float64, cos and sin rounded to float32,
+    through the C library's pow, cos and sin."""
+    half = dims // 2
+    cos = np.empty((context, half), np.float32)
+    sin = np.empty((context, half), np.float32)
+    freqs = [math.pow(base, -2 * float(i) / float(dims)) for i in range(half)]
+    for p in range(context):
+        for i in range(half):
+            theta = float(p) * freqs[i]
+            cos[p, i] = math.cos(theta)
+            sin[p, i] = math.sin(theta)
+    return cos, sin
+
+
+class _Q8:
+    """A Q8_0 batch on the device: q [M][K], scales and qsum [M][K/32]."""
+
+    def __init__(self, M, K):
+        self.q = torch.empty((M, K), dtype=torch.int8, device="cuda")
+        self.s = torch.empty((M, K // 32), dtype=torch.float32, device="cuda")
+        self.qs = torch.empty((M, K // 32), dtype=torch.int32, device="cuda")
+
+
+class QwenModel:
+    def __init__(self, ctx, cfg, weights, max_batch):
+        self.ctx, self.cfg, self.max_batch = ctx, cfg, max_batch
+        vp, call = capi.vp, capi.call
+        qd, kvd = cfg.heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim
+        self.qd, self.kvd = qd, kvd
+
+        def dev(a, dtype=torch.float32):
+            return torch.from_numpy(np.ascontiguousarray(a)).to(dtype).cuda()
+
+        self.blocks = []
+        for b in weights["blocks"]:
+            self.blocks.append({
+                "qkv": capi.Weight(ctx, np.concatenate([b["q"], b["k"], b["v"]]), capi.Q4_0, qd + 2 * kvd, cfg.dim),
+                "o": capi.Weight(ctx, b["o"], capi.Q4_0, cfg.dim, qd),
+                "gu": capi.Weight(ctx, np.concatenate([b["gate"], b["up"]]), capi.Q4_0, 2 * cfg.ffn, cfg.dim),
+                "down": capi.Weight(ctx, b["down"], capi.Q4_0, cfg.dim, cfg.ffn),
+                "attn_norm": dev(b["attn_norm"]), "ffn_norm": dev(b["ffn_norm"]),
+                "q_norm": dev(b["q_norm"]), "k_norm": dev(b["k_norm"]),
+            })
+        self.embd = capi.Weight(ctx, weights["token_embd"], capi.Q6_K, cfg.vocab, cfg.dim)
+        self.output_norm = dev(weights["output_norm"])
+        cos, sin = rope_tables(cfg.head_dim, cfg.max_context, cfg.rope_base)
+        self.rope_cos, self.rope_sin = dev(cos), dev(sin)
+        shape = (cfg.max_context, cfg.kv_heads, cfg.head_dim)
+        self.kc = [torch.zeros(shape, dtype=torch.int16, device="cuda") for _ in range(cfg.layers)]
+        self.vc = [torch.zeros(shape, dtype=torch.int16, device="cuda") for _ in range(cfg.layers)]
+
+        M = max_batch
+        self.xs = torch.empty((M, cfg.dim), dtype=torch.float32, device="cuda")
+        self.x8 = _Q8(M, cfg.dim)
+        self.qkv = torch.empty((M, qd + 2 * kvd), dtype=torch.float32, device="cuda")
+        self.qh = torch.empty((M, qd), dtype=torch.int16, device="cuda")
+        self.set8 = _Q8(M, qd)
+        self.attn = torch.empty((M, cfg.dim), dtype=torch.float32, device="cuda")
+        self.gu = torch.empty((M, 2 * cfg.ffn), dtype=torch.float32, device="cuda")
+        self.mid8 = _Q8(M, cfg.ffn)
+        self.ffn = torch.empty((M, cfg.dim), dtype=torch.float32, device="cuda")
+        self.hidden = torch.empty((M, cfg.dim), dtype=torch.float32, device="cuda")
+        self.positions = torch.empty((M,), dtype=torch.int32, device="cuda")
+        self.tokens = torch.empty((M,), dtype=torch.int32, device="cuda")
+        self.k8 = torch.empty((1, cfg.dim), dtype=torch.int8, device="cuda")
+        self.ks = torch.empty((1, cfg.dim // 256), dtype=torch.float32, device="cuda")
+        self.bs = torch.empty((1, cfg.dim // 16), dtype=torch.int16, device="cuda")
+        self.logit = torch.empty((1, cfg.vocab), dtype=torch.float32, device="cuda")
+        self.next_id = torch.empty((1,), dtype=torch.int32, device="cuda")
+        self._vp, self._call = vp, call
+
+    def reset(self):
+        """Forget the conversation (Model.Reset): the caches are cleared."""
+        for k, v in zip(self.kc, self.vc):
+            k.zero_()
+            v.zero_()
+
+    def _mm(self, w, act, M, y, ldy):
+        vp = self._vp
+        self._call("gx_matmul_q4_0", self.ctx.ptr, w.ptr, vp(act.q), vp(act.s), vp(act.qs), None, M, 0, w.rows,
+                   None, vp(y), ldy)
+
+    def forward(self, tokens, start_pos):
+        """ForwardBatch: tokens is a device int32 tensor of M ids (or a host
+        sequence, uploaded); returns the device hidden states [M][dim] after
+        the final norm (a view of reused storage)."""
+        cfg, vp, call, ctx = self.cfg, self._vp, self._call, self.ctx.ptr
+        if not torch.is_tensor(tokens):
+            tokens = torch.tensor(np.asarray(tokens, dtype=np.int32), device="cuda")
+        M = int(tokens.shape[0])
+        if M > self.max_batch or start_pos + M > cfg.max_context:
+            raise ValueError(f"qwen: {M} positions from {start_pos} exceed the batch {self.max_batch} "
+                             f"or the context {cfg.max_context}")
+        self.tokens[:M].copy_(tokens)
+        torch.arange(start_pos, start_pos + M, dtype=torch.int32, out=self.positions[:M])
+        call("gx_weight_rows", ctx, self.embd.ptr, 0, vp(self.tokens), M, vp(self.xs))
+        qd, kvd = self.qd, self.kvd
+        for i, b in enumerate(self.blocks):
+            add = None if i == 0 else vp(self.ffn)
+            call("gx_norm_quant", ctx, vp(self.xs), cfg.dim, add, cfg.dim, vp(b["attn_norm"]), M, cfg.dim,
+                 np.float32(cfg.eps), None, 0, vp(self.x8.q), vp(self.x8.s), vp(self.x8.qs))
+            self._mm(b["qkv"], self.x8, M, self.qkv, qd + 2 * kvd)
+            call("gx_qwen_qk_rope", ctx, vp(self.qkv), qd + 2 * kvd, M, cfg.heads, cfg.kv_heads, cfg.head_dim,
+                 vp(self.positions), vp(b["q_norm"]), vp(b["k_norm"]), vp(self.rope_cos), vp(self.rope_sin),
+                 np.float32(cfg.eps), vp(self.qh), vp(self.kc[i]), vp(self.vc[i]))
+            call("gx_qwen_attention", ctx, vp(self.qh), M, cfg.heads, cfg.kv_heads, cfg.head_dim,
+                 start_pos + M - 1, vp(self.positions), vp(self.kc[i]), vp(self.vc[i]), vp(self.set8.q),
+                 vp(self.set8.s), vp(self.set8.qs))
+            self._mm(b["o"], self.set8, M, self.attn, cfg.dim)
+            call("gx_norm_quant", ctx, vp(self.xs), cfg.dim, vp(self.attn), cfg.dim, vp(b["ffn_norm"]), M, cfg.dim,
+                 np.float32(cfg.eps), None, 0, vp(self.x8.q), vp(self.x8.s), vp(self.x8.qs))
+            self._mm(b["gu"], self.x8, M, self.gu, 2 * cfg.ffn)
+            call("gx_swiglu_quant", ctx, vp(self.gu), 2 * cfg.ffn, M, cfg.ffn, vp(self.mid8.q), vp(self.mid8.s),
+                 vp(self.mid8.qs))
+            self._mm(b["down"], self.mid8, M, self.ffn, cfg.dim)
+        call("gx_norm_quant", ctx, vp(self.xs), cfg.dim, vp(self.ffn), cfg.dim, vp(self.output_norm), M, cfg.dim,
+             np.float32(cfg.eps), vp(self.hidden), cfg.dim, None, None, None)
+        return self.hidden[:M]
+
+    def logits(self, row):
+        """Logits of hidden state `row` (of the last forward): QuantizeK and
+        the tied Q6_K head; the device logits [vocab] (reused storage)."""
+        cfg, vp, call, ctx = self.cfg, self._vp, self._call, self.ctx.ptr
+        h = self.hidden[row:row + 1]
+        call("gx_quantize_q8_k", ctx, vp(h), cfg.dim, 1, cfg.dim, vp(self.k8), vp(self.ks), vp(self.bs))
+        call("gx_matmul_q6_k", ctx, self.embd.ptr, vp(self.k8), vp(self.ks), vp(self.bs), 1, 0, cfg.vocab, None,
+             vp(self.logit), cfg.vocab)
+        return self.logit[0]
+
+    def next_token(self, row):
+        """The greedy id after hidden state `row`, left on the device."""
+        self.logits(row)
+        self._call("gx_argmax", self.ctx.ptr, self._vp(self.logit), self.cfg.vocab, 1, self.cfg.vocab,
+                   self._vp(self.next_id))
+        return self.next_id
+
+    def greedy(self, prompt, steps):
+        """The prompt in one batch, then `steps` greedy tokens, each fed back
+        from the device.  Returns the ids (host list)."""
+        self.reset()
+        self.forward(prompt, 0)
+        ids = []
+        tok = self.next_token(len(prompt) - 1)
+        pos = len(prompt)
+        for s in range(steps):
+            ids.append(tok.clone())
+            if s + 1 < steps:
+                self.forward(tok, pos)
+                tok = self.next_token(0)
+                pos += 1
+        return [int(t.item()) for t in ids]
+
+    def free(self):
+        for b in self.blocks:
+            for k in ("qkv", "o", "gu", "down"):
+                b[k].free()
+        self.embd.free()

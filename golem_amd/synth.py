@@ -22,14 +22,20 @@ def rng(seed):
     return np.random.Generator(np.random.PCG64(seed))
 
 
-def q4_0_weights(g, rows, cols, scale=0.02):
-    """GGUF Q4_0 bytes for a rows x cols matrix (uint8 array)."""
+def q4_0_weights(g, rows, cols, scale=0.02, symmetric=False):
+    """GGUF Q4_0 bytes for a rows x cols matrix (uint8 array).  symmetric draws
+    nibbles from 1..15 (weights -7..7, mean zero) instead of 0..15."""
     assert cols % 32 == 0
     blocks = rows * (cols // 32)
     out = np.empty((blocks, Q4_0_BLOCK_BYTES), dtype=np.uint8)
     d = (np.abs(g.standard_normal(blocks)) * scale).astype(np.float16)
     out[:, 0:2] = d.view(np.uint8).reshape(blocks, 2)
-    out[:, 2:] = g.integers(0, 256, size=(blocks, 16), dtype=np.uint8)
+    if symmetric:
+        lo = g.integers(1, 16, size=(blocks, 16), dtype=np.uint8)
+        hi = g.integers(1, 16, size=(blocks, 16), dtype=np.uint8)
+        out[:, 2:] = lo | (hi << 4)
+    else:
+        out[:, 2:] = g.integers(0, 256, size=(blocks, 16), dtype=np.uint8)
     return out.reshape(-1)
 
 
@@ -47,3 +53,54 @@ def q6_k_weights(g, rows, cols, scale=0.002):
 
 def activations(g, m, k):
     return g.standard_normal((m, k)).astype(np.float32)
+
+
+class QwenConfig:
+    """A Qwen3 dense decoder's geometry (golem's qwen.Config / BlockConfig,
+    qwen/config.go): every block alike, full-width NeoX RoPE."""
+
+    def __init__(self, dim, ffn, layers, heads, kv_heads, head_dim, vocab, max_context, rope_base=1e6, eps=1e-6):
+        self.dim, self.ffn, self.layers = dim, ffn, layers
+        self.heads, self.kv_heads, self.head_dim = heads, kv_heads, head_dim
+        self.vocab, self.max_context = vocab, max_context
+        self.rope_base, self.eps = rope_base, eps
+
+    def __repr__(self):
+        return (f"QwenConfig(dim={self.dim}, ffn={self.ffn}, layers={self.layers}, heads={self.heads}/"
+                f"{self.kv_heads}x{self.head_dim}, vocab={self.vocab}, ctx={self.max_context})")
+
+
+def qwen3_4b(max_context=640):
+    """Config 3: Qwen3-4B's shape (36 blocks, 2560 wide, FFN 9728, 32 query
+    and 8 key-value heads of 128, vocab 151936, RoPE base 1e6, eps 1e-6)."""
+    return QwenConfig(2560, 9728, 36, 32, 8, 128, 151936, max_context)
+
+
+def qwen_weights(cfg, seed, symmetric=False):
+    """Random weights of that shape, drawn as config 3 specifies: every linear
+    matrix Q4_0 as in config 0, the tied embedding / output head Q6_K as in
+    config 1, norms 1 + N(0, 0.02).  A dict of numpy arrays: matrices as GGUF
+    bytes (row-major), norms as float32.  symmetric: zero-mean Q4_0 nibbles
+    (config 3's nibbles have mean -0.5 after centring, which drives every
+    position towards the same token; tests use both)."""
+    g = rng(seed)
+
+    def norm(n):
+        return (1.0 + 0.02 * g.standard_normal(n)).astype(np.float32)
+
+    qd, kvd = cfg.heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim
+    blocks = []
+    for _ in range(cfg.layers):
+        blocks.append({
+            "attn_norm": norm(cfg.dim),
+            "q": q4_0_weights(g, qd, cfg.dim, symmetric=symmetric), "q_norm": norm(cfg.head_dim),
+            "k": q4_0_weights(g, kvd, cfg.dim, symmetric=symmetric), "k_norm": norm(cfg.head_dim),
+            "v": q4_0_weights(g, kvd, cfg.dim, symmetric=symmetric),
+            "o": q4_0_weights(g, cfg.dim, qd, symmetric=symmetric),
+            "ffn_norm": norm(cfg.dim),
+            "gate": q4_0_weights(g, cfg.ffn, cfg.dim, symmetric=symmetric),
+            "up": q4_0_weights(g, cfg.ffn, cfg.dim, symmetric=symmetric),
+            "down": q4_0_weights(g, cfg.dim, cfg.ffn, symmetric=symmetric),
+        })
+    return {"blocks": blocks, "output_norm": norm(cfg.dim),
+            "token_embd": q6_k_weights(g, cfg.vocab, cfg.dim)}

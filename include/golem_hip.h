@@ -226,6 +226,50 @@ int gx_moe_experts(gx_ctx *ctx, const gx_weight *gate_up, const gx_weight *down,
                    const float *x, int ldx, int M, int top_k, const int32_t *ids, const float *weights, float *out,
                    int ldo, void *workspace, size_t workspace_bytes);
 
+/* ---- the Qwen3 dense block around the products (qwen/) --------------- */
+
+/* x[m] += add[m] (add may be NULL: no residual), then RMSNormPlain(x[m], gain,
+ * eps) (nn/ops.go:195-214) into out[m] (optional) and its Q8_0 form into
+ * q/scales/qsum (optional): the two pre-norms of Block (qwen/block.go:45-52,
+ * 59-68, the residual of the previous half folded in) and the final norm
+ * (qwen/model.go:167-171).  x, add, out: device floats [M][ld*]; gain: K
+ * device floats; K a multiple of 32. */
+int gx_norm_quant(gx_ctx *ctx, float *x, int ldx, const float *add, int lda, const float *gain, int M, int K,
+                  float eps, float *out, int ldo, int8_t *q, float *scales, int32_t *qsum);
+
+/* The head-by-head part of Attention's projections (qwen/attention.go:57-84)
+ * for M positions: qkv[m] holds the Q (heads*head_dim), K and V
+ * (kv_heads*head_dim each) projections of position m.  Query heads are
+ * normed by q_norm, rotated (NeoX pairs, RoPETable.Apply, nn/rope.go:62-73)
+ * by rope_cos/rope_sin[positions[m]] ([context][head_dim/2] floats: golem's
+ * RoPETable.Prepare values) and rounded to fp16 into qh [M][heads*head_dim];
+ * key heads are normed by k_norm and rotated, and key and value are stored
+ * rounded to fp16 into the layer's caches kcache/vcache at
+ * [positions[m]][kv_head][head_dim] (LayerCache.Store, qwen/cache.go:52-60).
+ * All device pointers; positions: M int32. */
+int gx_qwen_qk_rope(gx_ctx *ctx, const float *qkv, int ldqkv, int M, int heads, int kv_heads, int head_dim,
+                    const int32_t *positions, const float *q_norm, const float *k_norm, const float *rope_cos,
+                    const float *rope_sin, float eps, uint16_t *qh, uint16_t *kcache, uint16_t *vcache);
+
+/* The attention proper (qwen/attention.go:86-124) for M positions: every
+ * query head of position m against the layer's cache over positions
+ * 0 .. positions[m] (max_pos bounds them all): scores (1/sqrt(head_dim)) *
+ * DotF32, SoftmaxInPlace, probabilities rounded to fp16, values summed by
+ * Axpy in position order; the heads' outputs [M][heads*head_dim] quantised to
+ * Q8_0 into q/scales/qsum for the output projection. */
+int gx_qwen_attention(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int kv_heads, int head_dim, int max_pos,
+                      const int32_t *positions, const uint16_t *kcache, const uint16_t *vcache, int8_t *q,
+                      float *scales, int32_t *qsum);
+
+/* SwiGLURange (nn/swiglu.go:77-82) and the Q8_0 of the result: gu[m] holds
+ * position m's gate (ffn floats) then up (ffn floats); q/scales/qsum receive
+ * Q8_0(silu(gate) * up) [M][ffn].  ffn a multiple of 32. */
+int gx_swiglu_quant(gx_ctx *ctx, const float *gu, int ldgu, int M, int ffn, int8_t *q, float *scales, int32_t *qsum);
+
+/* Greedy choice: ids[m] = the index of the largest of x[m][0..n), the lower
+ * index on ties (qwen/model_test.go:118-126). */
+int gx_argmax(gx_ctx *ctx, const float *x, int ldx, int M, int n, int32_t *ids);
+
 #ifdef __cplusplus
 }
 #endif

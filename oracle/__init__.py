@@ -57,6 +57,9 @@ def load():
         "orc_mat_vec_q6_k_rows": (None, [V, V, V, V, I, I, I, V, I, I, I]),
         "orc_dequantize_q6_k": (None, [V, I, V]),
         "orc_dot_f32": (F, [V, V, I]),
+        "orc_rope_prepare": (None, [I, I, ctypes.c_double, V, V]),
+        "orc_rope_apply": (None, [V, I, V, V]),
+        "orc_attend": (None, [V, V, V, I, I, I, I, F, V, V]),
         "orc_matrix_rows": (I, [I, V, V, I, I, V, I, V, V, V, V, V, V, V, I, I, V, I, I, I]),
         "orc_rms_norm_plain": (None, [V, I, V, F]),
         "orc_gelu_table_build": (None, [V]),

@@ -683,6 +683,53 @@ void orc_axpy(float *dst, const float *src, int n, float a)
         dst[i] += a * src[i];
 }
 
+/* ---- the Qwen3 decoder (qwen/) ------------------------------------------- */
+
+/* RoPETable.Prepare, nn/rope.go:33-59, without frequency factors:
+ * theta_i = position * base^(-2i/dims) in float64, cos and sin rounded to
+ * float32.  (glibc's pow, cos and sin stand in for Go's math package; they
+ * agree to about one unit in the last place of a float64, which rounds to the
+ * same float32 except in rare ties.) */
+void orc_rope_prepare(int dims, int position, double base, float *cos_out, float *sin_out)
+{
+    int half = dims / 2;
+    for (int i = 0; i < half; i++) {
+        double theta = (double)position * pow(base, -2 * (double)i / (double)dims);
+        cos_out[i] = (float)cos(theta);
+        sin_out[i] = (float)sin(theta);
+    }
+}
+
+/* RoPETable.Apply, nn/rope.go:62-73: element i pairs with i + dims/2 (NeoX). */
+void orc_rope_apply(float *vec, int dims, const float *c, const float *s)
+{
+    int half = dims / 2;
+    for (int i = 0; i < half; i++) {
+        float re = vec[i], im = vec[i + half];
+        vec[i] = re * c[i] - im * s[i];
+        vec[i + half] = re * s[i] + im * c[i];
+    }
+}
+
+/* One query head of one position, qwen/attention.go:96-124: against the first
+ * n positions of a layer cache (K, V as [position][kvheads][hd] floats, already
+ * rounded through fp16), scores = scale * DotF32(query, key), SoftmaxInPlace,
+ * every probability rounded through fp16, then dst = sum over positions in
+ * order of Axpy(value, probability) from zero.  scores holds n floats. */
+void orc_attend(const float *query, const float *K, const float *V, int kvheads, int hd, int kv, int n, float scale,
+                float *scores, float *dst)
+{
+    for (int p = 0; p < n; p++)
+        scores[p] = scale * orc_dot_f32(query, K + ((size_t)p * kvheads + kv) * hd, hd);
+    orc_softmax_in_place(scores, n);
+    for (int p = 0; p < n; p++)
+        scores[p] = orc_round_half(scores[p]);
+    for (int i = 0; i < hd; i++)
+        dst[i] = 0;
+    for (int p = 0; p < n; p++)
+        orc_axpy(dst, V + ((size_t)p * kvheads + kv) * hd, hd, scores[p]);
+}
+
 /* ---- mixture of experts ------------------------------------------------- */
 
 /* chooseExperts, gemma/moe.go:62-88: repeated argmax (strict >, ties to the

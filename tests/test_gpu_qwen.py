@@ -1,0 +1,250 @@
+"""golem's Qwen3 dense decoder (qwen/) on the device against the oracle's
+restatement of it (oracle/qwen.py).
+
+Kernel by kernel, on identical inputs, bit for bit: the residual add + norm +
+Q8_0 (Block's pre-norms), the head norms + RoPE + fp16 query and cache
+entries, the attention (scores, softmax, fp16 probabilities, values) with the
+Q8_0 of its heads, SwiGLU + Q8_0, the greedy argmax.
+
+The whole model, on small models of the same structure:
+- prefill: the hidden state after the final norm at every prompt position,
+  within 5e-2 of RMS (golem's compareFloats), every error logged, and the
+  last position's logits within 0.25 of RMS.  The
+  products differ from golem's by float rounding, which leaves a block's
+  output within 1e-6 of RMS.  But Q8_0 and the fp16 cache are discontinuous:
+  once in a while a value sits on a rounding boundary and moves by one step.
+  One such step in a head's output was seen to move 50 values of the next FFN
+  input and 1.1e-2 of RMS of that position's hidden state (every other
+  position staying at 1e-6); one in a cache entry reaches every later
+  position.  The kernels themselves are pinned bit for bit below; a wrong
+  index, head, rotation or residual moves every position by O(1).
+- greedy decode: token ids identical to golem's, top-1/top-2 margins logged
+  (qwen/model_test.go:118-126).
+- a prompt read in one batch is, bit for bit, the same tokens read one at a
+  time -- hidden states and cache entries (TestBatchAgreesWithOneAtATime,
+  qwen/model_test.go:79).
+
+The two geometries cover a head of 64 with two query heads per key-value head,
+and golem's real head of 128 with four per key-value head; each model is drawn
+with config 3's Q4_0 nibbles and with zero-mean ones.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from golem_amd import capi, synth
+from golem_amd.qwen import QwenModel, rope_tables
+from tests.gpu_util import log
+
+pytestmark = pytest.mark.gpu
+
+LOOSE = 5e-2
+LOGITS = 0.25  # the head spreads a hidden state's shift over 150k dot products
+
+CONFIGS = {
+    "hd64": synth.QwenConfig(256, 512, 2, 4, 2, 64, 1024, 48),
+    "hd128": synth.QwenConfig(512, 1024, 2, 8, 2, 128, 2048, 40),
+}
+
+
+def models(dev, name, symmetric):
+    from oracle.qwen import QwenOracle
+    cfg = CONFIGS[name]
+    w = synth.qwen_weights(cfg, 7 + len(name), symmetric=symmetric)
+    return cfg, QwenModel(dev.ctx, cfg, w, max_batch=16), QwenOracle(cfg, w)
+
+
+@pytest.mark.parametrize("symmetric", [False, True])
+@pytest.mark.parametrize("name", list(CONFIGS))
+def test_prefill_and_greedy_against_golem(dev, orc, name, symmetric):
+    cfg, model, oracle_model = models(dev, name, symmetric)
+    prompt = [int(t) for t in synth.rng(8).integers(0, cfg.vocab, 12)]
+    log(f"qwen {name} symmetric={symmetric}: prefill {len(prompt)}")
+    oracle_model.reset()
+    want = oracle_model.forward(prompt, 0)
+    model.reset()
+    got = dev.get(model.forward(prompt, 0))
+    rels = [orc.compare_floats(got[t], want[t])[0] for t in range(len(prompt))]
+    log(f"  hidden, of RMS per position: {[float('%.2g' % r) for r in rels]}")
+    assert max(rels) <= LOOSE, f"position {int(np.argmax(rels))}: {max(rels):.3g} of RMS"
+    lg = dev.get(model.logits(len(prompt) - 1))
+    rel, at = orc.compare_floats(lg, oracle_model.logits(want[-1]))
+    log(f"  last logits {rel:.3g} of RMS")
+    assert rel <= LOGITS, f"logits: {rel:.3g} of RMS at {at}"
+
+    steps = 6
+    ids, margins = oracle_model.greedy(prompt, steps)
+    got_ids = model.greedy(prompt, steps)
+    log(f"  greedy {got_ids} (golem {ids}); margins {np.round(margins, 3).tolist()}")
+    assert got_ids == ids
+    model.free()
+
+
+@pytest.mark.parametrize("name", list(CONFIGS))
+def test_batch_equals_one_at_a_time(dev, name):
+    cfg, model, _ = models(dev, name, True)
+    prompt = [int(t) for t in synth.rng(9).integers(0, cfg.vocab, 13)]
+    model.reset()
+    batch = dev.get(model.forward(prompt, 0)).copy()
+    kb = [k.cpu().numpy().copy() for k in model.kc]
+    vb = [v.cpu().numpy().copy() for v in model.vc]
+    model.reset()
+    alone = np.stack([dev.get(model.forward([t], i))[0].copy() for i, t in enumerate(prompt)])
+    np.testing.assert_array_equal(batch.view(np.uint32), alone.view(np.uint32))
+    for layer in range(cfg.layers):
+        np.testing.assert_array_equal(kb[layer], model.kc[layer].cpu().numpy())
+        np.testing.assert_array_equal(vb[layer], model.vc[layer].cpu().numpy())
+    model.free()
+
+
+def test_bad_shapes_are_refused(dev):
+    from golem_amd import capi
+    cfg, model, _ = models(dev, "hd64", False)
+    with pytest.raises(ValueError):
+        model.forward(list(range(17)), 0)  # wider than the batch it was built for
+    with pytest.raises(ValueError):
+        model.forward([1, 2], cfg.max_context - 1)  # past the context
+    with pytest.raises(capi.GxError):
+        capi.call("gx_swiglu_quant", dev.ctx.ptr, capi.vp(model.gu), 2 * cfg.ffn, 1, 100, capi.vp(model.mid8.q),
+                  capi.vp(model.mid8.s), capi.vp(model.mid8.qs))  # 100 is not a multiple of 32
+    model.free()
+
+
+# ---- kernel by kernel, bit for bit -------------------------------------------
+
+def test_norm_quant_bit_exact(dev, orc):
+    g = synth.rng(61)
+    M, K = 5, 2560
+    x = (g.standard_normal((M, K)) * 3).astype(np.float32)
+    add = g.standard_normal((M, K)).astype(np.float32)
+    gain = (1 + 0.02 * g.standard_normal(K)).astype(np.float32)
+    xd, ad, gd = dev.put(x), dev.put(add), dev.put(gain)
+    q = dev.empty((M, K), np.int8)
+    sc = dev.empty((M, K // 32), np.float32)
+    qs = dev.empty((M, K // 32), np.int32)
+    out = dev.empty((M, K), np.float32)
+    capi.call("gx_norm_quant", dev.ctx.ptr, capi.vp(xd), K, capi.vp(ad), K, capi.vp(gd), M, K, np.float32(1e-6),
+              capi.vp(out), K, capi.vp(q), capi.vp(sc), capi.vp(qs))
+    summed = x + add
+    np.testing.assert_array_equal(dev.get(xd).view(np.uint32), summed.view(np.uint32))
+    normed = np.stack([orc.rms_norm_plain(r, gain, 1e-6) for r in summed])
+    np.testing.assert_array_equal(dev.get(out).view(np.uint32), normed.view(np.uint32))
+    b = orc.Batch(normed).quantize()
+    np.testing.assert_array_equal(dev.get(q), b.q_rows())
+    np.testing.assert_array_equal(dev.get(sc).view(np.uint32), b.scales_rows().view(np.uint32))
+    np.testing.assert_array_equal(dev.get(qs), b.qsum_rows())
+
+
+@pytest.mark.parametrize("hd,heads,kv", [(128, 8, 2), (64, 4, 4)])
+def test_qk_rope_and_cache_bit_exact(dev, orc, hd, heads, kv):
+    g = synth.rng(62 + hd)
+    M, ctx_len = 6, 40
+    cos, sin = rope_tables(hd, ctx_len, 1e6)
+    lib = orc.load()
+    # the host tables are golem's RoPETable values through the same libm
+    c1, s1 = np.zeros(hd // 2, np.float32), np.zeros(hd // 2, np.float32)
+    lib.orc_rope_prepare(hd, 37, 1e6, orc._p(c1), orc._p(s1))
+    np.testing.assert_array_equal(cos[37], c1)
+    np.testing.assert_array_equal(sin[37], s1)
+    width = (heads + 2 * kv) * hd
+    qkv = (g.standard_normal((M, width)) * 4).astype(np.float32)
+    qn = (1 + 0.02 * g.standard_normal(hd)).astype(np.float32)
+    kn = (1 + 0.02 * g.standard_normal(hd)).astype(np.float32)
+    pos = np.array([0, 1, 5, 17, 38, 39], np.int32)
+    qh = dev.empty((M, heads * hd), np.int16)
+    kc = torch.zeros((ctx_len, kv, hd), dtype=torch.int16, device="cuda")
+    vc = torch.zeros((ctx_len, kv, hd), dtype=torch.int16, device="cuda")
+    # every input held by a name until the kernel has run (capi.vp keeps only the address)
+    ins = [dev.put(a) for a in (qkv, pos, qn, kn, cos, sin)]
+    capi.call("gx_qwen_qk_rope", dev.ctx.ptr, capi.vp(ins[0]), width, M, heads, kv, hd, capi.vp(ins[1]),
+              capi.vp(ins[2]), capi.vp(ins[3]), capi.vp(ins[4]), capi.vp(ins[5]), np.float32(1e-6), capi.vp(qh),
+              capi.vp(kc), capi.vp(vc))
+    got_q = dev.get(qh).view(np.float16).astype(np.float32)
+    got_k = kc.cpu().numpy().view(np.float16).astype(np.float32)
+    got_v = vc.cpu().numpy().view(np.float16).astype(np.float32)
+    for t in range(M):
+        lib.orc_rope_prepare(hd, int(pos[t]), 1e6, orc._p(c1), orc._p(s1))
+        for h in range(heads):
+            head = orc.rms_norm_plain(qkv[t, h * hd:(h + 1) * hd], qn, 1e-6)
+            lib.orc_rope_apply(orc._p(head), hd, orc._p(c1), orc._p(s1))
+            want = np.array([lib.orc_round_half(float(v)) for v in head], np.float32)
+            np.testing.assert_array_equal(got_q[t, h * hd:(h + 1) * hd].view(np.uint32), want.view(np.uint32))
+        for h in range(kv):
+            kh = orc.rms_norm_plain(qkv[t, (heads + h) * hd:(heads + h + 1) * hd], kn, 1e-6)
+            lib.orc_rope_apply(orc._p(kh), hd, orc._p(c1), orc._p(s1))
+            want_k = np.array([lib.orc_round_half(float(v)) for v in kh], np.float32)
+            vh = qkv[t, (heads + kv + h) * hd:(heads + kv + h + 1) * hd]
+            want_v = np.array([lib.orc_round_half(float(v)) for v in vh], np.float32)
+            np.testing.assert_array_equal(got_k[pos[t], h].view(np.uint32), want_k.view(np.uint32))
+            np.testing.assert_array_equal(got_v[pos[t], h].view(np.uint32), want_v.view(np.uint32))
+
+
+@pytest.mark.parametrize("hd,heads,kv,ctx_len", [(128, 8, 2, 70), (64, 4, 2, 300), (128, 32, 8, 640)])
+def test_attention_bit_exact(dev, orc, hd, heads, kv, ctx_len):
+    """Every query of a batch at its own position (the last sees the whole
+    cache): scores, softmax, fp16 probabilities, values, Q8_0 of the heads."""
+    g = synth.rng(63 + ctx_len)
+    pos = np.array([0, 1, ctx_len // 3, ctx_len - 2, ctx_len - 1], np.int32)
+    M = len(pos)
+    kcf = g.standard_normal((ctx_len, kv, hd)).astype(np.float16)
+    vcf = (g.standard_normal((ctx_len, kv, hd)) * 2).astype(np.float16)
+    qf = (g.standard_normal((M, heads * hd)) * 1.5).astype(np.float16)
+    q8 = dev.empty((M, heads * hd), np.int8)
+    sc = dev.empty((M, heads * hd // 32), np.float32)
+    qs = dev.empty((M, heads * hd // 32), np.int32)
+    ins = [dev.put(a) for a in (qf.view(np.int16), pos, kcf.view(np.int16), vcf.view(np.int16))]
+    capi.call("gx_qwen_attention", dev.ctx.ptr, capi.vp(ins[0]), M, heads, kv, hd, int(pos.max()), capi.vp(ins[1]),
+              capi.vp(ins[2]), capi.vp(ins[3]), capi.vp(q8), capi.vp(sc), capi.vp(qs))
+    lib = orc.load()
+    K32, V32 = np.ascontiguousarray(kcf.astype(np.float32)), np.ascontiguousarray(vcf.astype(np.float32))
+    scale = np.float32(1 / math.sqrt(float(hd)))
+    out = np.zeros((M, heads * hd), np.float32)
+    scores = np.zeros(ctx_len, np.float32)
+    for t in range(M):
+        for h in range(heads):
+            query = np.ascontiguousarray(qf[t, h * hd:(h + 1) * hd].astype(np.float32))
+            dst = np.zeros(hd, np.float32)
+            lib.orc_attend(orc._p(query), orc._p(K32), orc._p(V32), kv, hd, h // (heads // kv), int(pos[t]) + 1,
+                           scale, orc._p(scores), orc._p(dst))
+            out[t, h * hd:(h + 1) * hd] = dst
+    b = orc.Batch(out).quantize()
+    np.testing.assert_array_equal(dev.get(q8), b.q_rows())
+    np.testing.assert_array_equal(dev.get(sc).view(np.uint32), b.scales_rows().view(np.uint32))
+    np.testing.assert_array_equal(dev.get(qs), b.qsum_rows())
+
+
+def test_swiglu_quant_bit_exact(dev, orc):
+    g = synth.rng(64)
+    M, ffn = 3, 9728
+    gu = (g.standard_normal((M, 2 * ffn)) * 5).astype(np.float32)
+    gu[0, :8] = [0.0, -0.0, 90.0, -90.0, 1e-30, -1e-30, 87.5, -87.5]  # expf's range edges
+    q8 = dev.empty((M, ffn), np.int8)
+    sc = dev.empty((M, ffn // 32), np.float32)
+    qs = dev.empty((M, ffn // 32), np.int32)
+    gud = dev.put(gu)
+    capi.call("gx_swiglu_quant", dev.ctx.ptr, capi.vp(gud), 2 * ffn, M, ffn, capi.vp(q8), capi.vp(sc),
+              capi.vp(qs))
+    lib = orc.load()
+    mid = np.zeros((M, ffn), np.float32)
+    for t in range(M):
+        gate, up = np.ascontiguousarray(gu[t, :ffn]), np.ascontiguousarray(gu[t, ffn:])
+        lib.orc_swiglu_range(orc._p(gate), orc._p(up), 0, ffn)
+        mid[t] = gate
+    b = orc.Batch(mid).quantize()
+    np.testing.assert_array_equal(dev.get(q8), b.q_rows())
+    np.testing.assert_array_equal(dev.get(sc).view(np.uint32), b.scales_rows().view(np.uint32))
+
+
+def test_argmax_ties_to_lower_id(dev):
+    x = np.zeros((3, 151936), np.float32)
+    x[0, 77] = x[0, 150000] = 5.0
+    x[1, :] = -1.0
+    x[1, 151935] = 2.0
+    x[2, 1000] = np.nan
+    x[2, 9] = 3.0
+    ids = dev.empty((3,), np.int32)
+    xd = dev.put(x)
+    capi.call("gx_argmax", dev.ctx.ptr, capi.vp(xd), x.shape[1], 3, x.shape[1], capi.vp(ids))
+    assert dev.get(ids).tolist() == [77, 151935, 9]
