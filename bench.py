@@ -44,7 +44,7 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-extra", action="store_true", help="skip the config 0 / config 2 measurements")
     p.add_argument("--only", default="",
-                   help="profiling: run only this leg (c1, c0, c2, c4) and exit; 'copy' runs the 256 MiB "
+                   help="profiling: run only this leg (c1, c0, c2, c3, c4) and exit; 'copy' runs the 256 MiB "
                         "device copy that scales the FETCH_SIZE / WRITE_SIZE counters")
     p.add_argument("--c2-m", type=int, default=0, help="profiling: config 2 at this M only")
     p.add_argument("--c2-path", default="", help="profiling: config 2 on this kernel only (f16, i8)")
@@ -210,6 +210,13 @@ def main():
             print(json.dumps(extra))
             return
 
+    # ---- config 3: Qwen3-4B-shaped decoder, prefill 512 + 128 greedy steps ----
+    if not args.no_extra and args.only in ("", "c3"):
+        extra.update(bench_c3(ctx, torch))
+        if args.only == "c3":
+            print(json.dumps(extra))
+            return
+
     # ---- config 4: Gemma-shaped MoE layer (route + experts) ----------------
     if not args.no_extra and args.only in ("", "c4"):
         extra.update(bench_c4(ctx, torch, dev))
@@ -301,6 +308,62 @@ def cpu_baseline(w6, x, rows, cols, step_bytes, step, y, torch, no_extra):
         out["c0_q4_0_matvec"] = {"GB/s": round(n0 * by0 / t0 / 1e9, 2), "us_per_pass": round(t0 / n0 * 1e6, 1),
                                  "cores": threads, "passes": n0}
     return out
+
+
+def bench_c3(ctx, torch):
+    """Config 3: Qwen3-4B's shape (36 blocks, 2560 wide, FFN 9728, 32/8 heads of
+    128, vocab 151936) with random weights drawn as config 3 specifies (seed
+    3): a 512-token prompt of uniform random ids read in one batch, then 128
+    greedy tokens, each fed back from the device, with the fp16 cache growing
+    to 640.  Timed with HIP events: the prefill (through the first token) and
+    the 128 decode steps."""
+    from golem_amd import synth
+    from golem_amd.qwen import QwenModel
+    cfg = synth.qwen3_4b(640)
+    t0 = time.perf_counter()
+    w = synth.qwen_weights(cfg, 3)
+    model = QwenModel(ctx, cfg, w, max_batch=512)
+    del w
+    torch.cuda.synchronize()
+    setup_s = time.perf_counter() - t0
+    prompt = synth.rng(3).integers(0, cfg.vocab, 512).astype(np.int32)
+    model.reset()
+    model.forward(prompt[:16], 0)
+    model.next_token(15)
+    torch.cuda.synchronize()
+
+    model.reset()
+    ctx.timer_start()
+    model.forward(prompt, 0)
+    tok = model.next_token(len(prompt) - 1)
+    prefill_ms = ctx.timer_stop()
+    steps = 128
+    ids = [tok.clone()]
+    ctx.timer_start()
+    for s in range(steps - 1):
+        model.forward(tok, len(prompt) + s)
+        tok = model.next_token(0)
+        ids.append(tok.clone())
+    decode_ms = ctx.timer_stop()
+    ids = [int(t.item()) for t in ids]
+    q4 = lambda r, c: r * (c // 32) * 18
+    qd, kvd = cfg.heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim
+    layer_bytes = (q4(qd + 2 * kvd, cfg.dim) + q4(cfg.dim, qd) + q4(2 * cfg.ffn, cfg.dim) + q4(cfg.dim, cfg.ffn))
+    head_bytes = cfg.vocab * (cfg.dim // 256) * 210
+    mean_ctx = len(prompt) + steps / 2
+    kv_bytes = cfg.layers * mean_ctx * cfg.kv_heads * cfg.head_dim * 2 * 2
+    token_bytes = cfg.layers * layer_bytes + head_bytes + kv_bytes
+    per_tok = decode_ms / (steps - 1)
+    model.free()
+    return {"c3_qwen3_4b": {
+        "prefill_tokens": len(prompt), "prefill_ms": round(prefill_ms, 2),
+        "prefill_tok_per_s": round(len(prompt) / (prefill_ms * 1e-3), 1),
+        "decode_steps": steps, "decode_ms_per_token": round(per_tok, 3),
+        "decode_tok_per_s": round(1e3 / per_tok, 1),
+        "decode_bytes_per_token": int(token_bytes),
+        "decode_GB/s": round(token_bytes / (per_tok * 1e-3) / 1e9, 1),
+        "decode_hbm_frac": round(token_bytes / (per_tok * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "greedy_ids_head": ids[:8], "setup_s": round(setup_s, 1)}}
 
 
 def bench_c4(ctx, torch, dev):
