@@ -315,8 +315,9 @@ def bench_c3(ctx, torch):
     128, vocab 151936) with random weights drawn as config 3 specifies (seed
     3): a 512-token prompt of uniform random ids read in one batch, then 128
     greedy tokens, each fed back from the device, with the fp16 cache growing
-    to 640.  Timed with HIP events: the prefill (through the first token) and
-    the 128 decode steps."""
+    to 640; the decode steps are replays of one captured HIP graph.  Timed
+    with HIP events: the prefill (through the first token) and the 127 decode
+    steps after it."""
     from golem_amd import synth
     from golem_amd.qwen import QwenModel
     cfg = synth.qwen3_4b(640)
@@ -329,7 +330,10 @@ def bench_c3(ctx, torch):
     prompt = synth.rng(3).integers(0, cfg.vocab, 512).astype(np.int32)
     model.reset()
     model.forward(prompt[:16], 0)
-    model.next_token(15)
+    model.start_decode(model.next_token(15), 16)
+    model.capture_decode()
+    for _ in range(3):
+        model.graph.replay()
     torch.cuda.synchronize()
 
     model.reset()
@@ -338,14 +342,12 @@ def bench_c3(ctx, torch):
     tok = model.next_token(len(prompt) - 1)
     prefill_ms = ctx.timer_stop()
     steps = 128
-    ids = [tok.clone()]
     ctx.timer_start()
+    model.start_decode(tok, len(prompt))
     for s in range(steps - 1):
-        model.forward(tok, len(prompt) + s)
-        tok = model.next_token(0)
-        ids.append(tok.clone())
+        model.graph.replay()
     decode_ms = ctx.timer_stop()
-    ids = [int(t.item()) for t in ids]
+    ids = model.decoded(tok, len(prompt), steps)
     q4 = lambda r, c: r * (c // 32) * 18
     qd, kvd = cfg.heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim
     layer_bytes = (q4(qd + 2 * kvd, cfg.dim) + q4(cfg.dim, qd) + q4(2 * cfg.ffn, cfg.dim) + q4(cfg.dim, cfg.ffn))

@@ -61,8 +61,10 @@ _SIGNATURES = {
     "gx_moe_experts": [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _vp, _vp, _c_int, _vp, _c_size],
     "gx_norm_quant": [_vp, _vp, _c_int, _vp, _c_int, _vp, _c_int, _c_int, ctypes.c_float, _vp, _c_int, _vp, _vp, _vp],
     "gx_qwen_qk_rope": [_vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _vp, ctypes.c_float,
-                        _vp, _vp, _vp],
-    "gx_qwen_attention": [_vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _vp, _vp],
+                        _vp, _vp, _vp, _c_int],
+    "gx_qwen_attention_workspace_bytes": [_c_int, _c_int, _c_int, ctypes.POINTER(_c_size)],
+    "gx_qwen_attention": [_vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _c_int, _vp, _vp, _vp,
+                          _vp, _c_size],
     "gx_swiglu_quant": [_vp, _vp, _c_int, _c_int, _c_int, _vp, _vp, _vp],
     "gx_argmax": [_vp, _vp, _c_int, _c_int, _c_int, _vp],
 }
@@ -187,3 +189,11 @@ def q16_elems(M, K):
     """Values in the fp16 copy of a Q8_0 batch (gx_quantize_q8_0's q16):
     tokens padded to a multiple of 32."""
     return (M + 31) // 32 * 32 * K
+
+
+def size_out(name, *args):
+    """Calls an entry point whose last argument is a size_t out-parameter and
+    returns that size."""
+    n = _c_size(0)
+    call(name, *args, ctypes.byref(n))
+    return int(n.value)

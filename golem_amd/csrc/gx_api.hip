@@ -76,18 +76,23 @@ int gx_init(int device, gx_ctx **out) {
         delete ctx;
         return gx::fail(GX_ERR_HIP, "hipEventCreate failed");
     }
-    if (hipMalloc(&ctx->gelu_table, 65536 * sizeof(float)) != hipSuccess) {
+    ctx->gelu_table = nullptr;
+    auto undo = [ctx]() {
+        (void)hipFree(ctx->gelu_table);
+        (void)hipEventDestroy(ctx->t0);
+        (void)hipEventDestroy(ctx->t1);
         delete ctx;
+    };
+    if (hipMalloc(&ctx->gelu_table, 65536 * sizeof(float)) != hipSuccess) {
+        undo();
         return gx::fail(GX_ERR_NOMEM, "gx: cannot allocate the GELU table");
     }
     if (int rc = gx::launch_gelu_table(ctx, ctx->gelu_table)) {
-        (void)hipFree(ctx->gelu_table);
-        delete ctx;
+        undo();
         return rc;
     }
     if (hipStreamSynchronize(ctx->stream) != hipSuccess) {
-        (void)hipFree(ctx->gelu_table);
-        delete ctx;
+        undo();
         return gx::fail(GX_ERR_HIP, "gx: building the GELU table failed");
     }
     *out = ctx;
@@ -513,37 +518,49 @@ int gx_norm_quant(gx_ctx *ctx, float *x, int ldx, const float *add, int lda, con
 
 int gx_qwen_qk_rope(gx_ctx *ctx, const float *qkv, int ldqkv, int M, int heads, int kv_heads, int head_dim,
                     const int32_t *positions, const float *q_norm, const float *k_norm, const float *rope_cos,
-                    const float *rope_sin, float eps, uint16_t *qh, uint16_t *kcache, uint16_t *vcache) {
+                    const float *rope_sin, float eps, uint16_t *qh, uint16_t *kcache, uint16_t *vcache, int context) {
     if (int rc = use(ctx))
         return rc;
     GX_CHECK(heads > 0 && kv_heads > 0 && heads % kv_heads == 0, "gx: %d query heads over %d key-value heads", heads,
              kv_heads);
-    GX_CHECK(M >= 0 && ldqkv >= (heads + 2 * kv_heads) * head_dim, "gx: bad batch shape");
+    GX_CHECK(M >= 0 && ldqkv >= (heads + 2 * kv_heads) * head_dim && context > 0, "gx: bad batch shape");
     GX_CHECK(qkv && positions && q_norm && k_norm && rope_cos && rope_sin && qh && kcache && vcache,
              "gx: missing argument");
     if (M == 0)
         return ok();
     if (int rc = gx::launch_qwen_qk_rope(ctx, qkv, ldqkv, M, heads, kv_heads, head_dim, positions, q_norm, k_norm,
-                                         rope_cos, rope_sin, eps, qh, kcache, vcache))
+                                         rope_cos, rope_sin, eps, qh, kcache, vcache, context))
         return rc;
     return ok();
 }
 
+int gx_qwen_attention_workspace_bytes(int M, int heads, int max_pos, size_t *bytes) {
+    GX_CHECK(M >= 0 && heads > 0 && max_pos >= 0 && bytes, "gx: bad attention shape");
+    *bytes = gx::qwen_attention_workspace(M, heads, max_pos);
+    return ok();
+}
+
 int gx_qwen_attention(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int kv_heads, int head_dim, int max_pos,
-                      const int32_t *positions, const uint16_t *kcache, const uint16_t *vcache, int8_t *q,
-                      float *scales, int32_t *qsum) {
+                      const int32_t *positions, const uint16_t *kcache, const uint16_t *vcache, int context,
+                      int8_t *q, float *scales, int32_t *qsum, void *workspace, size_t workspace_bytes) {
     if (int rc = use(ctx))
         return rc;
     GX_CHECK(heads > 0 && kv_heads > 0 && heads % kv_heads == 0, "gx: %d query heads over %d key-value heads", heads,
              kv_heads);
     GX_CHECK(M >= 0 && max_pos >= 0, "gx: bad batch shape");
-    GX_CHECK(qh && positions && kcache && vcache && q && scales && qsum, "gx: missing argument");
+    GX_CHECK(context % 8 == 0 && max_pos < context, "gx: a cache of %d positions (a multiple of 8) cannot hold %d",
+             context, max_pos);
+    GX_CHECK(qh && positions && kcache && vcache && q && scales && qsum && workspace, "gx: missing argument");
+    GX_CHECK(((uintptr_t)vcache & 15) == 0, "gx: the value cache must be 16-byte aligned");
+    GX_CHECK(((uintptr_t)workspace & 255) == 0, "gx: the workspace must be 256-byte aligned");
     if (M == 0)
         return ok();
+    const size_t need = gx::qwen_attention_workspace(M, heads, max_pos);
+    GX_CHECK(workspace_bytes >= need, "gx: the workspace holds %zu bytes, %zu needed", workspace_bytes, need);
     // llama.cpp's 1/sqrt(head_dim), taken in float64 and rounded (qwen/attention.go:90-93)
     const float scale = (float)(1.0 / sqrt((double)head_dim));
     if (int rc = gx::launch_qwen_attention(ctx, qh, M, heads, kv_heads, head_dim, max_pos, positions, kcache, vcache,
-                                           scale, q, scales, qsum))
+                                           context, scale, q, scales, qsum, (uint8_t *)workspace))
         return rc;
     return ok();
 }

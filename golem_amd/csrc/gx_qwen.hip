@@ -136,7 +136,8 @@ constexpr int kHeadMax = 256;  // head_dim limit (two values per lane)
 // position's Q rows, then K rows, then V rows.  rope_cos/sin are [context][hd/2].
 // Query heads: normed, rotated, rounded to fp16 into qh [M][heads*hd].  Key-
 // value heads: the key normed and rotated, both rounded to fp16 into the
-// layer's caches at [pos][kvh][hd].
+// layer's caches: the key at [pos][kvh][hd], the value at [kvh][hd][pos] of a
+// cache of `context` positions.
 __global__ __launch_bounds__(64) void qwen_qk_rope_kernel(const float *__restrict__ qkv, int ldqkv, int heads,
                                                           int kv_heads, int hd, const int32_t *__restrict__ positions,
                                                           const float *__restrict__ q_norm,
@@ -144,7 +145,7 @@ __global__ __launch_bounds__(64) void qwen_qk_rope_kernel(const float *__restric
                                                           const float *__restrict__ rope_cos,
                                                           const float *__restrict__ rope_sin, float eps,
                                                           uint16_t *__restrict__ qh, uint16_t *__restrict__ kcache,
-                                                          uint16_t *__restrict__ vcache) {
+                                                          uint16_t *__restrict__ vcache, int context) {
     __shared__ float h[kHeadMax];
     __shared__ float sc_sh;
     const int lane = threadIdx.x, t = blockIdx.x, u = blockIdx.y;
@@ -179,229 +180,275 @@ __global__ __launch_bounds__(64) void qwen_qk_rope_kernel(const float *__restric
     }
     if (!is_q) {
         const float *vsrc = qkv + (size_t)t * ldqkv + (heads + kv_heads) * hd + (u - heads) * hd;
-        const size_t o = ((size_t)pos * kv_heads + (u - heads)) * hd;
+        uint16_t *vt = vcache + (size_t)(u - heads) * hd * context + pos;
         for (int i = lane; i < hd; i += 64)
-            vcache[o + i] = (uint16_t)float_to_half_bits(vsrc[i]);
+            vt[(size_t)i * context] = (uint16_t)float_to_half_bits(vsrc[i]);
     }
 }
 
-// grid (M, kv_heads), 256 threads: position t's G = heads / kv_heads query
-// heads that read key-value head kvh, against the layer's cache over
-// positions 0 .. positions[t] (n of them).  Per query head, in golem's order:
-// scores (scale * DotF32), SoftmaxInPlace (max; exp in float64; the sum taken
-// position by position by one thread; the division), probabilities rounded
-// to fp16, then dst = sum over positions in order of Axpy(value, probability)
-// -- G * hd independent chains, two per thread.  The key and value rows are
-// read once for the G heads.  Values pass through LDS in chunks of kAttnChunk
-// positions, fetched two chunks ahead.  The heads' outputs are quantised
-// (Q8_0) into q/scales/qsum at columns (kvh*G + g)*hd of a [M][heads*hd] batch.
-constexpr int kAttnThreads = 256;
-constexpr int kAttnChunk = 32;   // positions per value chunk
-constexpr int kAttnDepth = 3;    // value chunks in LDS (two in flight)
+// The attention proper runs as three passes over a workspace: scores
+// sc [M][heads][S] floats, the maximum of every 64-position tile
+// tmax [M][heads][S/64], probabilities prob [M][heads][S] fp16, where S is the
+// deepest visible prefix rounded up to 64.
+//   scores   a lane per cached position: scale * DotF32(query, key) in
+//            DotF32's four-chain order, and each tile's maximum
+//   softmax  a wavefront per (position, head): SoftmaxInPlace's maximum,
+//            exp in float64, the sum taken position by position, the
+//            division, the probability rounded through fp16
+//   values   Axpy in position order, a lane per (position, head, element),
+//            the value cache ([kv_heads][hd][context], positions contiguous)
+//            staged through LDS; Q8_0 of the heads
+// The query, keys, values and probabilities are all fp16 values, so each
+// product of two of them is exact in float32: a fused multiply-add then
+// rounds exactly as golem's multiply-then-add does (its one rounding is the
+// addition's), and the kernels use v_fma_mix, which takes the fp16 operands
+// as they are stored.
 
-template <int G, int HD>
-__global__ __launch_bounds__(kAttnThreads) void qwen_attention_kernel(const uint16_t *__restrict__ qh, int kv_heads,
-                                                                      const int32_t *__restrict__ positions,
-                                                                      const uint16_t *__restrict__ kcache,
-                                                                      const uint16_t *__restrict__ vcache,
-                                                                      float scale, int sstride,
-                                                                      int8_t *__restrict__ q,
-                                                                      float *__restrict__ scales,
-                                                                      int32_t *__restrict__ qsum) {
-    constexpr int hd = HD;
-    extern __shared__ float lds[];
-    float *query = lds;                                  // [G][hd]
-    float *scores = query + G * kHeadMax;                // [G][sstride]
-    uint16_t *vbuf = (uint16_t *)(scores + G * sstride); // [kAttnDepth][kAttnChunk][hd]
-    __shared__ float red[kAttnThreads / 64][G];
-    __shared__ float total[G];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int t = blockIdx.x, kvh = blockIdx.y;
-    const int heads = G * kv_heads, width = heads * hd;
-    const int n = positions[t] + 1;
-    for (int c = tid; c < G * hd; c += kAttnThreads) {
-        const int g = c / hd, i = c - g * hd;
-        query[g * kHeadMax + i] = half_bits_to_float(qh[(size_t)t * width + (kvh * G + g) * hd + i]);
-    }
-    __syncthreads();
+__device__ __forceinline__ float half_lo(uint32_t w) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xFFFFu));
+}
+__device__ __forceinline__ float half_hi(uint32_t w) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16)); }
 
-    // Scores: a thread per position; the key row is read once for the G heads.
-    float mx[G];
+constexpr int kTile = 64;  // positions per scores wavefront
+
+// grid (S/64 position tiles, heads/GH head groups, ceil(M/TT) token tiles),
+// one wavefront.  Lane = cached position p; its key row is held in registers
+// for the GH heads (of one key-value head) of the TT tokens, whose queries
+// are uniform across the wavefront (scalar loads).
+template <int HD>
+__global__ __launch_bounds__(64) void attn_scores_kernel(const uint16_t *__restrict__ qh, int M, int heads, int G,
+                                                         int GH, int TT, const int32_t *__restrict__ positions, int limit,
+                                                         const uint16_t *__restrict__ kcache, int kv_heads,
+                                                         float scale, int S, float *__restrict__ sc,
+                                                         float *__restrict__ tmax) {
+    const int lane = threadIdx.x, tile = blockIdx.x;
+    const int h0 = blockIdx.y * GH, t0 = blockIdx.z * TT;
+    const int kvh = h0 / G, tiles = S / kTile;
+    const int tn = min(TT, M - t0);
+    int last = -1;
+    for (int tt = 0; tt < tn; tt++)
+        last = max(last, min(positions[t0 + tt], limit - 1));
+    if (tile * kTile > last)
+        return;  // the whole wavefront: nothing visible here
+    const int p = tile * kTile + lane;
+    const v4u_stream *kr = (const v4u_stream *)(kcache + ((size_t)min(p, last) * kv_heads + kvh) * HD);
+    v4u_stream k[HD / 8];
 #pragma unroll
-    for (int g = 0; g < G; g++)
-        mx[g] = -INFINITY;
-    for (int p = tid; p < n; p += kAttnThreads) {
-        const uint16_t *key = kcache + ((size_t)p * kv_heads + kvh) * hd;
-        float s[G][4];
+    for (int i = 0; i < HD / 8; i++)
+        k[i] = kr[i];
+    for (int tt = 0; tt < tn; tt++) {
+        const int t = t0 + tt;
+        const int n = min(positions[t] + 1, limit);
+        if (tile * kTile >= n)
+            continue;
+        for (int j = 0; j < GH; j++) {
+            const int h = h0 + j;
+            const uint32_t *q = (const uint32_t *)(qh + ((size_t)t * heads + h) * HD);
+            float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;  // elements 4i, 4i+1, 4i+2, 4i+3
 #pragma unroll
-        for (int g = 0; g < G; g++)
-            s[g][0] = s[g][1] = s[g][2] = s[g][3] = 0.0f;
-        v4u_stream kr[hd / 8];  // the whole key row first
+            for (int i = 0; i < HD / 8; i++) {
+                const uint32_t kw[4] = {k[i].x, k[i].y, k[i].z, k[i].w};
 #pragma unroll
-        for (int i = 0; i < hd; i += 8)
-            kr[i / 8] = *(const v4u_stream *)(key + i);
-#pragma unroll
-        for (int i = 0; i < hd; i += 8) {
-            const v4u_stream kw = kr[i / 8];
-            const uint32_t w4[4] = {kw.x, kw.y, kw.z, kw.w};
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const float kv = half_bits_to_float((w4[j >> 1] >> (16 * (j & 1))) & 0xFFFFu);
-#pragma unroll
-                for (int g = 0; g < G; g++) {
-                    const float pr = query[g * kHeadMax + i + j] * kv;
-                    s[g][j & 3] = s[g][j & 3] + pr;
+                for (int w = 0; w < 4; w += 2) {
+                    const uint32_t qa = q[4 * i + w], qb = q[4 * i + w + 1];
+                    s0 = __builtin_fmaf(half_lo(qa), half_lo(kw[w]), s0);
+                    s1 = __builtin_fmaf(half_hi(qa), half_hi(kw[w]), s1);
+                    s2 = __builtin_fmaf(half_lo(qb), half_lo(kw[w + 1]), s2);
+                    s3 = __builtin_fmaf(half_hi(qb), half_hi(kw[w + 1]), s3);
                 }
             }
-        }
+            const float v = scale * ((s0 + s1) + (s2 + s3));
+            const size_t row = (size_t)t * heads + h;
+            if (p < n)
+                sc[row * S + p] = v;
+            float m = p < n ? v : -INFINITY;
 #pragma unroll
-        for (int g = 0; g < G; g++) {
-            const float dot = (s[g][0] + s[g][1]) + (s[g][2] + s[g][3]);
-            const float sc = scale * dot;
-            scores[g * sstride + p] = sc;
-            mx[g] = fmaxf(mx[g], sc);
+            for (int off = 32; off > 0; off >>= 1)
+                m = fmaxf(m, __shfl_xor(m, off, 64));
+            if (lane == 0)
+                tmax[row * tiles + tile] = m;
         }
     }
+}
+
+constexpr int kSoftChunk = 2048;  // exponentials per pass through LDS
+
+// Sum e[0 .. n) into `total` one value at a time, in order: two register sets
+// of 16 so that the next set's LDS reads overlap this set's additions.
+__device__ __forceinline__ float serial_sum(const float *e, int n, float total) {
+    int j = 0;
+    if (n >= 16) {
+        float a[16], b[16];
 #pragma unroll
-    for (int g = 0; g < G; g++) {
-        for (int off = 32; off > 0; off >>= 1)
-            mx[g] = fmaxf(mx[g], __shfl_xor(mx[g], off, 64));
+        for (int u = 0; u < 16; u++)
+            a[u] = e[u];
+        for (; j + 32 <= n; j += 32) {
+#pragma unroll
+            for (int u = 0; u < 16; u++)
+                b[u] = e[j + 16 + u];
+#pragma unroll
+            for (int u = 0; u < 16; u++)
+                total += a[u];
+#pragma unroll
+            for (int u = 0; u < 16; u++)
+                a[u] = e[min(j + 32 + u, n - 1)];
+#pragma unroll
+            for (int u = 0; u < 16; u++)
+                total += b[u];
+        }
+        if (j + 16 <= n) {
+#pragma unroll
+            for (int u = 0; u < 16; u++)
+                total += a[u];
+            j += 16;
+        }
+    }
+    for (; j < n; j++)
+        total += e[j];
+    return total;
+}
+
+// grid (heads, M), one wavefront: SoftmaxInPlace (nn/ops.go:59-73) of the
+// scores of (position t, head h), then RoundHalf of each probability.
+__global__ __launch_bounds__(64) void attn_softmax_kernel(int heads, const int32_t *__restrict__ positions, int limit,
+                                                          int S,
+                                                          float *__restrict__ sc, const float *__restrict__ tmax,
+                                                          uint16_t *__restrict__ prob) {
+    __shared__ float e[kSoftChunk];
+    __shared__ float total_sh;
+    const int lane = threadIdx.x, h = blockIdx.x, t = blockIdx.y;
+    const size_t row = (size_t)t * heads + h;
+    const int n = min(positions[t] + 1, limit), tiles = (n + kTile - 1) / kTile;
+    float m = -INFINITY;  // the maximum is exact in any order
+    for (int i = lane; i < tiles; i += 64)
+        m = fmaxf(m, tmax[row * (S / kTile) + i]);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1)
+        m = fmaxf(m, __shfl_xor(m, off, 64));
+    float *s = sc + row * S;
+    float total = 0.0f;  // lane 0's
+    for (int c0 = 0; c0 < n; c0 += kSoftChunk) {
+        const int cn = min(kSoftChunk, n - c0);
+        for (int j = lane; j < cn; j += 64) {
+            const float v = (float)exp((double)(s[c0 + j] - m));
+            e[j] = v;
+            if (n > kSoftChunk)
+                s[c0 + j] = v;  // kept for the division
+        }
+        __syncthreads();
         if (lane == 0)
-            red[wave][g] = mx[g];
+            total = serial_sum(e, cn, total);
+        __syncthreads();
     }
+    if (lane == 0)
+        total_sh = total;
     __syncthreads();
-#pragma unroll
-    for (int g = 0; g < G; g++) {
-        float m = red[0][g];
-        for (int w = 1; w < kAttnThreads / 64; w++)
-            m = fmaxf(m, red[w][g]);
-        for (int p = tid; p < n; p += kAttnThreads)
-            scores[g * sstride + p] = (float)exp((double)(scores[g * sstride + p] - m));
+    total = total_sh;
+    uint16_t *pr = prob + row * S;
+    if (n <= kSoftChunk) {
+        for (int j = lane; j < n; j += 64)
+            pr[j] = (uint16_t)float_to_half_bits(__fdiv_rn(e[j], total));
+    } else {
+        for (int j = lane; j < n; j += 64)
+            pr[j] = (uint16_t)float_to_half_bits(__fdiv_rn(s[j], total));
     }
-    __syncthreads();
-    if (tid < G) {  // SoftmaxInPlace's sum, position by position (read 16 at a time)
-        const float *e = scores + tid * sstride;
-        float sum = 0.0f;
-        int p = 0;
-        for (; p + 16 <= n; p += 16) {
-            float v[16];
-#pragma unroll
-            for (int j = 0; j < 16; j++)
-                v[j] = e[p + j];
-#pragma unroll
-            for (int j = 0; j < 16; j++)
-                sum += v[j];
-        }
-        for (; p < n; p++)
-            sum += e[p];
-        total[tid] = sum;
-    }
+}
 
-    // Value chunks: chunk k holds positions k*kAttnChunk ..; thread tid carries
-    // hd*kAttnChunk/(8*256) 16-byte pieces of a chunk.
-    const int pieces = hd * kAttnChunk / 8;  // uint4 per chunk
-    const int chunks = (n + kAttnChunk - 1) / kAttnChunk;
-    v4u_stream stage[2][2];  // up to two pieces per thread (hd <= 128), two chunks ahead
-#define GX_ATTN_FETCH(k, slot)                                                                                       \
-    do {                                                                                                             \
-        _Pragma("unroll") for (int r = 0; r < 2; r++) {                                                            \
-            const int pc = tid + r * kAttnThreads;                                                                   \
-            if (pc < pieces) {                                                                                       \
-                const int pp = (k) * kAttnChunk + pc / (hd / 8);                                                     \
-                const int col = (pc % (hd / 8)) * 8;                                                                 \
-                stage[slot][r] = *(const v4u_stream *)(vcache + ((size_t)min(pp, n - 1) * kv_heads + kvh) * hd + col); \
-            }                                                                                                        \
-        }                                                                                                            \
-    } while (0)
-#define GX_ATTN_PUT(k, slot)                                                                                         \
-    do {                                                                                                             \
-        uint16_t *vb = vbuf + (size_t)((k) % kAttnDepth) * kAttnChunk * hd;                                          \
-        _Pragma("unroll") for (int r = 0; r < 2; r++) {                                                            \
-            const int pc = tid + r * kAttnThreads;                                                                   \
-            if (pc < pieces)                                                                                         \
-                *(v4u_stream *)(vb + (pc / (hd / 8)) * hd + (pc % (hd / 8)) * 8) = stage[slot][r];                  \
-        }                                                                                                            \
-    } while (0)
-    GX_ATTN_FETCH(0, 0);
-    if (chunks > 1)
-        GX_ATTN_FETCH(1, 1);
-    GX_ATTN_PUT(0, 0);
-    __syncthreads();
-    // probabilities, rounded through fp16 (SoftmaxInPlace's division)
-#pragma unroll
-    for (int g = 0; g < G; g++)
-        for (int p = tid; p < n; p += kAttnThreads)
-            scores[g * sstride + p] = half_bits_to_float(float_to_half_bits(scores[g * sstride + p] / total[g]));
-    if (chunks > 1)
-        GX_ATTN_PUT(1, 1);
-    __syncthreads();
+constexpr int kValSlice = 32;    // elements of a head per workgroup: one Q8_0 block
+constexpr int kValChunk = 768;   // positions per pass through LDS
+constexpr int kValStride = kValChunk + 8;  // LDS row stride in halves (16 bytes of padding)
+constexpr int kValRegs = 24;     // value pieces a thread holds in flight
 
-    const int c0 = tid, c1 = tid + kAttnThreads;  // chains (head, element)
-    // a thread without a chain computes on head G - 1 (in bounds) and stores nothing
-    const int g0 = min(c0 / hd, G - 1), i0 = c0 - (c0 / hd) * hd;
-    const int g1 = min(c1 / hd, G - 1), i1 = c1 - (c1 / hd) * hd;
-    float d0 = 0.0f, d1 = 0.0f;
-#define GX_ATTN_CHUNK(k, slot)                                                                                       \
-    do {                                                                                                             \
-        if ((k) + 2 < chunks)                                                                                        \
-            GX_ATTN_FETCH((k) + 2, slot);                                                                            \
-        const uint16_t *vb = vbuf + (size_t)((k) % kAttnDepth) * kAttnChunk * hd;                                    \
-        const int p0 = (k) * kAttnChunk, pn = min(kAttnChunk, n - p0);                                               \
-        if (pn == kAttnChunk) { /* a whole chunk: reads first, then the two chains in order */                       \
-            for (int jb = 0; jb < kAttnChunk; jb += 8) {                                                             \
-                float a0[8], v0[8], a1[8], v1[8];                                                                    \
-                _Pragma("unroll") for (int j = 0; j < 8; j++) {                                                      \
-                    a0[j] = scores[g0 * sstride + p0 + jb + j];                                                      \
-                    v0[j] = half_bits_to_float(vb[(jb + j) * hd + i0]);                                              \
-                    a1[j] = scores[g1 * sstride + p0 + jb + j];                                                      \
-                    v1[j] = half_bits_to_float(vb[(jb + j) * hd + i1]);                                              \
-                }                                                                                                    \
-                _Pragma("unroll") for (int j = 0; j < 8; j++) {                                                      \
-                    const float m0 = a0[j] * v0[j];                                                                  \
-                    d0 = d0 + m0;                                                                                    \
-                    const float m1 = a1[j] * v1[j];                                                                  \
-                    d1 = d1 + m1;                                                                                    \
-                }                                                                                                    \
-            }                                                                                                        \
-        } else {                                                                                                     \
-            for (int j = 0; j < pn; j++) {                                                                           \
-                const float m0 = scores[g0 * sstride + p0 + j] * half_bits_to_float(vb[j * hd + i0]);                \
-                d0 = d0 + m0;                                                                                        \
-                const float m1 = scores[g1 * sstride + p0 + j] * half_bits_to_float(vb[j * hd + i1]);                \
-                d1 = d1 + m1;                                                                                        \
-            }                                                                                                        \
-        }                                                                                                            \
-        if ((k) + 2 < chunks) /* chunk k + 2 into the buffer chunk k - 1 used */                                     \
-            GX_ATTN_PUT((k) + 2, slot);                                                                              \
-        __syncthreads();                                                                                             \
-    } while (0)
-    // Chunk k's registers are slot k & 1; the loop runs two chunks a pass so
-    // that the slot is a constant.
-    for (int k = 0; k < chunks; k += 2) {
-        GX_ATTN_CHUNK(k, 0);
-        if (k + 1 < chunks)
-            GX_ATTN_CHUNK(k + 1, 1);
-    }
-#undef GX_ATTN_CHUNK
-#undef GX_ATTN_FETCH
-#undef GX_ATTN_PUT
-    // Q8_0 of the heads: consecutive chains are consecutive elements of one
-    // head (hd % 32 == 0), so a 32-lane group is one block.
-    const int B = width >> 5;
-    for (int r = 0; r < 2; r++) {
-        const int c = r == 0 ? c0 : c1;
-        if (r * kAttnThreads < G * hd) {  // uniform
-            if (c < G * hd) {             // whole 32-lane groups
-                float stored;
-                int32_t sm;
-                const int32_t nq = q8_0_lane(r == 0 ? d0 : d1, &stored, &sm);
-                const int col = (kvh * G + c / hd) * hd + (c % hd);
-                q[(size_t)t * width + col] = (int8_t)nq;
-                if ((col & 31) == 0) {
-                    scales[(size_t)t * B + (col >> 5)] = stored;
-                    qsum[(size_t)t * B + (col >> 5)] = sm;
+// grid (kv_heads * hd/32 slices, ceil(M/TT) token tiles), NT = TT*G*32
+// threads.  Thread (tt, g, d): chain of element d of the slice for query
+// head kvh*G + g of token t0 + tt, over positions 0 .. positions[t] in order:
+// acc = fma(p, v, acc) (Axpy, nn/kernel.go:221-233).  The slice's value rows
+// (32 rows of positions) and the TT*G probability rows pass through LDS a
+// chunk of kValChunk positions at a time; a 32-lane group's chains are one
+// Q8_0 block of the head outputs.
+template <int NT>
+__global__ __launch_bounds__(NT) void attn_values_kernel(int M, int heads, int G, int hd,
+                                                         const int32_t *__restrict__ positions, int limit,
+                                                         const uint16_t *__restrict__ vcache, int context,
+                                                         int kv_heads, int S, const uint16_t *__restrict__ prob,
+                                                         int8_t *__restrict__ q, float *__restrict__ scales,
+                                                         int32_t *__restrict__ qsum) {
+    constexpr int rows = NT / kValSlice;  // (tt, g) pairs
+    __shared__ __align__(16) uint16_t vs[kValSlice * kValStride];
+    __shared__ __align__(16) uint16_t ps[rows * kValStride];
+    const int tid = threadIdx.x;
+    const int slices = hd / kValSlice, TT = rows / G;
+    const int kvh = blockIdx.x / slices, d0 = (blockIdx.x - kvh * slices) * kValSlice;
+    const int t0 = blockIdx.y * TT, tn = min(TT, M - t0);
+    const int dd = tid % kValSlice, hg = tid / kValSlice;
+    const int tt = hg / G, g = hg - tt * G;
+    const bool live = tt < tn;
+    const int n = live ? min(positions[t0 + tt] + 1, limit) : 0;
+    int nmax = 0;
+    for (int i = 0; i < tn; i++)
+        nmax = max(nmax, min(positions[t0 + i] + 1, limit));
+    const uint16_t *vrow = vcache + ((size_t)kvh * hd + d0) * context;
+    float acc = 0.0f;
+    for (int c0 = 0; c0 < nmax; c0 += kValChunk) {
+        const int groups = (min(kValChunk, nmax - c0) + 7) / 8;  // 8-position pieces of a row
+        const int pieces = kValSlice * groups;
+        __syncthreads();  // the previous chunk's chains are done with the buffers
+        for (int base = 0; base < pieces; base += NT * kValRegs) {
+            v4u_stream r[kValRegs];
+#pragma unroll
+            for (int u = 0; u < kValRegs; u++) {
+                const int i = min(base + tid + u * NT, pieces - 1);
+                const int rr = i / groups, c = i - rr * groups;
+                r[u] = *(const v4u_stream *)(vrow + (size_t)rr * context + c0 + 8 * c);
+            }
+#pragma unroll
+            for (int u = 0; u < kValRegs; u++) {
+                const int i = base + tid + u * NT;
+                if (i < pieces) {
+                    const int rr = i / groups, c = i - rr * groups;
+                    *(v4u_stream *)(vs + rr * kValStride + 8 * c) = r[u];
                 }
             }
+        }
+        for (int i = tid; i < rows * groups; i += NT) {
+            const int rr = i / groups, c = i - rr * groups;
+            const int ttr = rr / G, hr = kvh * G + (rr - ttr * G);
+            v4u_stream v = {0u, 0u, 0u, 0u};
+            if (ttr < tn)
+                v = *(const v4u_stream *)(prob + ((size_t)(t0 + ttr) * heads + hr) * S + c0 + 8 * c);
+            *(v4u_stream *)(ps + rr * kValStride + 8 * c) = v;
+        }
+        __syncthreads();
+        const int ln = min(kValChunk, n - c0);  // this chain's positions in the chunk
+        const uint16_t *vr = vs + dd * kValStride, *pr = ps + hg * kValStride;
+        int j = 0;
+#pragma unroll 4
+        for (; j + 8 <= ln; j += 8) {
+            const v4u_stream vv = *(const v4u_stream *)(vr + j);
+            const v4u_stream pp = *(const v4u_stream *)(pr + j);
+            acc = __builtin_fmaf(half_lo(pp.x), half_lo(vv.x), acc);
+            acc = __builtin_fmaf(half_hi(pp.x), half_hi(vv.x), acc);
+            acc = __builtin_fmaf(half_lo(pp.y), half_lo(vv.y), acc);
+            acc = __builtin_fmaf(half_hi(pp.y), half_hi(vv.y), acc);
+            acc = __builtin_fmaf(half_lo(pp.z), half_lo(vv.z), acc);
+            acc = __builtin_fmaf(half_hi(pp.z), half_hi(vv.z), acc);
+            acc = __builtin_fmaf(half_lo(pp.w), half_lo(vv.w), acc);
+            acc = __builtin_fmaf(half_hi(pp.w), half_hi(vv.w), acc);
+        }
+        for (; j < ln; j++)
+            acc = __builtin_fmaf((float)__builtin_bit_cast(_Float16, pr[j]),
+                                 (float)__builtin_bit_cast(_Float16, vr[j]), acc);
+    }
+    float stored;
+    int32_t sm;
+    const int32_t nq = q8_0_lane(acc, &stored, &sm);
+    if (live) {
+        const int width = heads * hd, B = width >> 5;
+        const int t = t0 + tt, col = (kvh * G + g) * hd + d0 + dd;
+        q[(size_t)t * width + col] = (int8_t)nq;
+        if (dd == 0) {
+            scales[(size_t)t * B + (col >> 5)] = stored;
+            qsum[(size_t)t * B + (col >> 5)] = sm;
         }
     }
 }
@@ -515,52 +562,80 @@ int launch_qwen_norm_quant(gx_ctx *ctx, float *x, int ldx, const float *add, int
 
 int launch_qwen_qk_rope(gx_ctx *ctx, const float *qkv, int ldqkv, int M, int heads, int kv_heads, int hd,
                         const int32_t *positions, const float *q_norm, const float *k_norm, const float *rope_cos,
-                        const float *rope_sin, float eps, uint16_t *qh, uint16_t *kcache, uint16_t *vcache) {
+                        const float *rope_sin, float eps, uint16_t *qh, uint16_t *kcache, uint16_t *vcache,
+                        int context) {
     GX_CHECK(hd <= kHeadMax && hd % 2 == 0, "gx: head width %d unsupported (even, at most %d)", hd, kHeadMax);
     qwen_qk_rope_kernel<<<dim3((unsigned)M, (unsigned)(heads + kv_heads)), 64, 0, ctx->stream>>>(
-        qkv, ldqkv, heads, kv_heads, hd, positions, q_norm, k_norm, rope_cos, rope_sin, eps, qh, kcache, vcache);
+        qkv, ldqkv, heads, kv_heads, hd, positions, q_norm, k_norm, rope_cos, rope_sin, eps, qh, kcache, vcache,
+        context);
     return check_launch("qwen_qk_rope");
 }
 
+size_t qwen_attention_workspace(int M, int heads, int max_pos) {
+    const size_t S = ((size_t)max_pos + kTile) / kTile * kTile;
+    const size_t rows = (size_t)M * heads;
+    auto up = [](size_t b) { return (b + 255) / 256 * 256; };
+    return up(rows * S * sizeof(float)) + up(rows * (S / kTile) * sizeof(float)) + up(rows * S * sizeof(uint16_t));
+}
+
 int launch_qwen_attention(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int kv_heads, int hd, int max_pos,
-                          const int32_t *positions, const uint16_t *kcache, const uint16_t *vcache, float scale,
-                          int8_t *q, float *scales, int32_t *qsum) {
+                          const int32_t *positions, const uint16_t *kcache, const uint16_t *vcache, int context,
+                          float scale, int8_t *q, float *scales, int32_t *qsum, uint8_t *workspace) {
     const int G = heads / kv_heads;
-    GX_CHECK(hd <= 128 && hd % 32 == 0, "gx: attention supports head widths that are multiples of 32 up to 128");
+    GX_CHECK(hd == 32 || hd == 64 || hd == 96 || hd == 128, "gx: attention supports head widths 32, 64, 96 and 128");
     GX_CHECK(G == 1 || G == 2 || G == 4 || G == 8, "gx: %d query heads per key-value head unsupported", G);
-    GX_CHECK(G * hd <= 2 * kAttnThreads, "gx: %d query heads of %d per key-value head exceed the kernel's %d chains", G,
-             hd, 2 * kAttnThreads);
-    const int sstride = max_pos + 1;
-    const size_t lds = sizeof(float) * ((size_t)G * kHeadMax + (size_t)G * sstride) +
-                       sizeof(uint16_t) * (size_t)kAttnDepth * kAttnChunk * hd;
-    GX_CHECK(lds <= 64 * 1024, "gx: attention over %d positions with %d heads per group does not fit the LDS",
-             max_pos + 1, G);
-    const dim3 grid((unsigned)M, (unsigned)kv_heads);
-#define GX_ATTN_LAUNCH(GG, HH)                                                                                       \
-    qwen_attention_kernel<GG, HH><<<grid, kAttnThreads, lds, ctx->stream>>>(qh, kv_heads, positions, kcache, vcache,  \
-                                                                            scale, sstride, q, scales, qsum)
-#define GX_ATTN_LAUNCH_HD(GG)                                                                                        \
-    do {                                                                                                             \
-        if (hd == 32)                                                                                                \
-            GX_ATTN_LAUNCH(GG, 32);                                                                                  \
-        else if (hd == 64)                                                                                           \
-            GX_ATTN_LAUNCH(GG, 64);                                                                                  \
-        else if (hd == 96)                                                                                           \
-            GX_ATTN_LAUNCH(GG, 96);                                                                                  \
-        else                                                                                                         \
-            GX_ATTN_LAUNCH(GG, 128);                                                                                 \
-    } while (0)
-    if (G == 1)
-        GX_ATTN_LAUNCH_HD(1);
-    else if (G == 2)
-        GX_ATTN_LAUNCH_HD(2);
-    else if (G == 4)
-        GX_ATTN_LAUNCH_HD(4);
+    const int S = (max_pos + kTile) / kTile * kTile;
+    const int limit = max_pos + 1;  // positions beyond max_pos are read as max_pos
+    const size_t rows = (size_t)M * heads;
+    auto up = [](size_t b) { return (b + 255) / 256 * 256; };
+    float *sc = (float *)workspace;
+    float *tmax = (float *)(workspace + up(rows * S * sizeof(float)));
+    uint16_t *prob = (uint16_t *)(workspace + up(rows * S * sizeof(float)) + up(rows * (S / kTile) * sizeof(float)));
+
+    // Scores: decode spreads the heads of a group over wavefronts (the key
+    // rows are re-read from L2); a batch shares each key row among the group's
+    // heads and 8 tokens.
+    const int GH = M <= 4 ? 1 : G, TT = M <= 4 ? 1 : 8;
+    const dim3 sgrid((unsigned)(S / kTile), (unsigned)(heads / GH), (unsigned)((M + TT - 1) / TT));
+#define GX_SCORES(HH)                                                                                                \
+    attn_scores_kernel<HH><<<sgrid, 64, 0, ctx->stream>>>(qh, M, heads, G, GH, TT, positions, limit, kcache,       \
+                                                          kv_heads, scale, S, sc, tmax)
+    if (hd == 32)
+        GX_SCORES(32);
+    else if (hd == 64)
+        GX_SCORES(64);
+    else if (hd == 96)
+        GX_SCORES(96);
     else
-        GX_ATTN_LAUNCH_HD(8);
-#undef GX_ATTN_LAUNCH_HD
-#undef GX_ATTN_LAUNCH
-    return check_launch("qwen_attention");
+        GX_SCORES(128);
+#undef GX_SCORES
+    if (int rc = check_launch("qwen_attention scores"))
+        return rc;
+    attn_softmax_kernel<<<dim3((unsigned)heads, (unsigned)M), 64, 0, ctx->stream>>>(heads, positions, limit, S,
+                                                                                     sc, tmax, prob);
+    if (int rc = check_launch("qwen_attention softmax"))
+        return rc;
+    // Values: TT tokens of G heads per workgroup, 32 chains each (NT <= 256).
+    int NT = G * kValSlice;
+    while (NT < 128 && NT * 2 <= G * kValSlice * M)
+        NT *= 2;
+    if (M > 4 && NT < 256)
+        NT *= 2;
+    const int TT2 = NT / (G * kValSlice);
+    const dim3 vgrid((unsigned)(kv_heads * (hd / kValSlice)), (unsigned)((M + TT2 - 1) / TT2));
+#define GX_VALUES(N)                                                                                                 \
+    attn_values_kernel<N><<<vgrid, N, 0, ctx->stream>>>(M, heads, G, hd, positions, limit, vcache, context,         \
+                                                        kv_heads, S, prob, q, scales, qsum)
+    if (NT == 32)
+        GX_VALUES(32);
+    else if (NT == 64)
+        GX_VALUES(64);
+    else if (NT == 128)
+        GX_VALUES(128);
+    else
+        GX_VALUES(256);
+#undef GX_VALUES
+    return check_launch("qwen_attention values");
 }
 
 int launch_qwen_swiglu_quant(gx_ctx *ctx, const float *gu, int ldgu, int M, int ffn, int8_t *q, float *scales,

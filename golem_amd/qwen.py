@@ -22,7 +22,15 @@ result: every output row is its own product.
 Every kernel treats a position on its own, so a prompt read in one batch
 gives, bit for bit, what the same tokens give one at a time (golem's
 TestBatchAgreesWithOneAtATime, qwen/model_test.go:79).
+
+A decode step (one position) can be captured once into a HIP graph and
+replayed: the token and its position are read from the device (the previous
+step's argmax and a device counter), and the attention is launched for the
+whole cache (max_pos = context - 1; the kernels stop at each position's own
+prefix), so every replay runs the same launches.  A replay computes exactly
+what the eager step computes.
 """
+import ctypes
 import math
 
 import numpy as np
@@ -80,9 +88,12 @@ class QwenModel:
         self.output_norm = dev(weights["output_norm"])
         cos, sin = rope_tables(cfg.head_dim, cfg.max_context, cfg.rope_base)
         self.rope_cos, self.rope_sin = dev(cos), dev(sin)
-        shape = (cfg.max_context, cfg.kv_heads, cfg.head_dim)
-        self.kc = [torch.zeros(shape, dtype=torch.int16, device="cuda") for _ in range(cfg.layers)]
-        self.vc = [torch.zeros(shape, dtype=torch.int16, device="cuda") for _ in range(cfg.layers)]
+        # keys [context][kv_head][head_dim]; values transposed, [kv_head][head_dim][context]
+        self.context = (cfg.max_context + 7) // 8 * 8
+        kshape = (self.context, cfg.kv_heads, cfg.head_dim)
+        vshape = (cfg.kv_heads, cfg.head_dim, self.context)
+        self.kc = [torch.zeros(kshape, dtype=torch.int16, device="cuda") for _ in range(cfg.layers)]
+        self.vc = [torch.zeros(vshape, dtype=torch.int16, device="cuda") for _ in range(cfg.layers)]
 
         M = max_batch
         self.xs = torch.empty((M, cfg.dim), dtype=torch.float32, device="cuda")
@@ -102,6 +113,11 @@ class QwenModel:
         self.bs = torch.empty((1, cfg.dim // 16), dtype=torch.int16, device="cuda")
         self.logit = torch.empty((1, cfg.vocab), dtype=torch.float32, device="cuda")
         self.next_id = torch.empty((1,), dtype=torch.int32, device="cuda")
+        self.pos64 = torch.zeros((1,), dtype=torch.int64, device="cuda")  # the graph's position counter
+        self.history = torch.zeros((cfg.max_context + 1,), dtype=torch.int32, device="cuda")
+        self.graph = None
+        n = capi.size_out("gx_qwen_attention_workspace_bytes", M, cfg.heads, cfg.max_context - 1)
+        self.attn_ws = torch.empty((n + 255) // 256 * 256, dtype=torch.uint8, device="cuda")
         self._vp, self._call = vp, call
 
     def reset(self):
@@ -119,7 +135,7 @@ class QwenModel:
         """ForwardBatch: tokens is a device int32 tensor of M ids (or a host
         sequence, uploaded); returns the device hidden states [M][dim] after
         the final norm (a view of reused storage)."""
-        cfg, vp, call, ctx = self.cfg, self._vp, self._call, self.ctx.ptr
+        cfg = self.cfg
         if not torch.is_tensor(tokens):
             tokens = torch.tensor(np.asarray(tokens, dtype=np.int32), device="cuda")
         M = int(tokens.shape[0])
@@ -128,6 +144,13 @@ class QwenModel:
                              f"or the context {cfg.max_context}")
         self.tokens[:M].copy_(tokens)
         torch.arange(start_pos, start_pos + M, dtype=torch.int32, out=self.positions[:M])
+        self._blocks(M, start_pos + M - 1)
+        return self.hidden[:M]
+
+    def _blocks(self, M, max_pos):
+        """The embedding rows, every block and the final norm for the M tokens
+        and positions already in self.tokens / self.positions."""
+        cfg, vp, call, ctx = self.cfg, self._vp, self._call, self.ctx.ptr
         call("gx_weight_rows", ctx, self.embd.ptr, 0, vp(self.tokens), M, vp(self.xs))
         qd, kvd = self.qd, self.kvd
         for i, b in enumerate(self.blocks):
@@ -137,10 +160,10 @@ class QwenModel:
             self._mm(b["qkv"], self.x8, M, self.qkv, qd + 2 * kvd)
             call("gx_qwen_qk_rope", ctx, vp(self.qkv), qd + 2 * kvd, M, cfg.heads, cfg.kv_heads, cfg.head_dim,
                  vp(self.positions), vp(b["q_norm"]), vp(b["k_norm"]), vp(self.rope_cos), vp(self.rope_sin),
-                 np.float32(cfg.eps), vp(self.qh), vp(self.kc[i]), vp(self.vc[i]))
+                 np.float32(cfg.eps), vp(self.qh), vp(self.kc[i]), vp(self.vc[i]), self.context)
             call("gx_qwen_attention", ctx, vp(self.qh), M, cfg.heads, cfg.kv_heads, cfg.head_dim,
-                 start_pos + M - 1, vp(self.positions), vp(self.kc[i]), vp(self.vc[i]), vp(self.set8.q),
-                 vp(self.set8.s), vp(self.set8.qs))
+                 max_pos, vp(self.positions), vp(self.kc[i]), vp(self.vc[i]), self.context,
+                 vp(self.set8.q), vp(self.set8.s), vp(self.set8.qs), vp(self.attn_ws), self.attn_ws.numel())
             self._mm(b["o"], self.set8, M, self.attn, cfg.dim)
             call("gx_norm_quant", ctx, vp(self.xs), cfg.dim, vp(self.attn), cfg.dim, vp(b["ffn_norm"]), M, cfg.dim,
                  np.float32(cfg.eps), None, 0, vp(self.x8.q), vp(self.x8.s), vp(self.x8.qs))
@@ -150,7 +173,34 @@ class QwenModel:
             self._mm(b["down"], self.mid8, M, self.ffn, cfg.dim)
         call("gx_norm_quant", ctx, vp(self.xs), cfg.dim, vp(self.ffn), cfg.dim, vp(self.output_norm), M, cfg.dim,
              np.float32(cfg.eps), vp(self.hidden), cfg.dim, None, None, None)
-        return self.hidden[:M]
+
+    def _decode_step(self):
+        """One greedy step read entirely from the device: token self.tokens[0]
+        at position self.pos64.  Leaves the next token in self.tokens[0] and
+        in self.history[position + 1], and advances the position."""
+        self.positions[:1].copy_(self.pos64)
+        self._blocks(1, self.cfg.max_context - 1)
+        self.next_token(0)
+        self.history.index_copy_(0, self.pos64 + 1, self.next_id)
+        self.tokens[:1].copy_(self.next_id)
+        self.pos64.add_(1)
+
+    def capture_decode(self):
+        """Records _decode_step into a HIP graph (once).  The library's stream
+        is the capture stream while recording."""
+        if self.graph is not None:
+            return
+        torch.cuda.synchronize()
+        stream = torch.cuda.Stream()
+        graph = torch.cuda.CUDAGraph()
+        self._call("gx_set_stream", self.ctx.ptr, ctypes.c_void_p(stream.cuda_stream))
+        try:
+            with torch.cuda.graph(graph, stream=stream):
+                self._decode_step()
+        finally:
+            self._call("gx_set_stream", self.ctx.ptr, None)
+        torch.cuda.synchronize()
+        self.graph = graph
 
     def logits(self, row):
         """Logits of hidden state `row` (of the last forward): QuantizeK and
@@ -169,13 +219,22 @@ class QwenModel:
                    self._vp(self.next_id))
         return self.next_id
 
-    def greedy(self, prompt, steps):
+    def greedy(self, prompt, steps, graph=False):
         """The prompt in one batch, then `steps` greedy tokens, each fed back
-        from the device.  Returns the ids (host list)."""
+        from the device (graph: the decode steps as replays of the captured
+        step).  Returns the ids (host list)."""
+        if len(prompt) + steps - 1 > self.cfg.max_context:
+            raise ValueError(f"qwen: {steps} tokens after {len(prompt)} exceed the context {self.cfg.max_context}")
         self.reset()
         self.forward(prompt, 0)
-        ids = []
         tok = self.next_token(len(prompt) - 1)
+        if graph:
+            self.capture_decode()
+            self.start_decode(tok, len(prompt))
+            for _ in range(steps - 1):
+                self.graph.replay()
+            return self.decoded(tok, len(prompt), steps)
+        ids = []
         pos = len(prompt)
         for s in range(steps):
             ids.append(tok.clone())
@@ -184,6 +243,19 @@ class QwenModel:
                 tok = self.next_token(0)
                 pos += 1
         return [int(t.item()) for t in ids]
+
+    def start_decode(self, tok, pos):
+        """Seeds the captured step: token `tok` (device) at position `pos`."""
+        if pos >= self.cfg.max_context:
+            raise ValueError(f"qwen: position {pos} is past the context {self.cfg.max_context}")
+        self.tokens[:1].copy_(tok)
+        self.pos64.fill_(pos)
+
+    def decoded(self, tok, pos, steps):
+        """The ids of `steps` greedy tokens: `tok`, then those the replays
+        started at `pos` left in the history."""
+        rest = self.history[pos + 1:pos + steps].cpu().tolist() if steps > 1 else []
+        return [int(tok.item())] + [int(t) for t in rest]
 
     def free(self):
         for b in self.blocks:

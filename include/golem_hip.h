@@ -244,22 +244,31 @@ int gx_norm_quant(gx_ctx *ctx, float *x, int ldx, const float *add, int lda, con
  * by rope_cos/rope_sin[positions[m]] ([context][head_dim/2] floats: golem's
  * RoPETable.Prepare values) and rounded to fp16 into qh [M][heads*head_dim];
  * key heads are normed by k_norm and rotated, and key and value are stored
- * rounded to fp16 into the layer's caches kcache/vcache at
- * [positions[m]][kv_head][head_dim] (LayerCache.Store, qwen/cache.go:52-60).
- * All device pointers; positions: M int32. */
+ * rounded to fp16 into the layer's caches (LayerCache.Store,
+ * qwen/cache.go:52-60), a cache of `context` positions: the key at
+ * kcache[positions[m]][kv_head][head_dim], the value transposed at
+ * vcache[kv_head][head_dim][positions[m]] (a value row holds one element of
+ * a head over all positions).  positions[m] < context.  All device
+ * pointers; positions: M int32. */
 int gx_qwen_qk_rope(gx_ctx *ctx, const float *qkv, int ldqkv, int M, int heads, int kv_heads, int head_dim,
                     const int32_t *positions, const float *q_norm, const float *k_norm, const float *rope_cos,
-                    const float *rope_sin, float eps, uint16_t *qh, uint16_t *kcache, uint16_t *vcache);
+                    const float *rope_sin, float eps, uint16_t *qh, uint16_t *kcache, uint16_t *vcache, int context);
+
+/* Device bytes of the workspace gx_qwen_attention needs for M positions of
+ * `heads` query heads whose positions are at most max_pos. */
+int gx_qwen_attention_workspace_bytes(int M, int heads, int max_pos, size_t *bytes);
 
 /* The attention proper (qwen/attention.go:86-124) for M positions: every
- * query head of position m against the layer's cache over positions
+ * query head of position m against the layer's cache (the layouts of
+ * gx_qwen_qk_rope; context a multiple of 8 above max_pos) over positions
  * 0 .. positions[m] (max_pos bounds them all): scores (1/sqrt(head_dim)) *
  * DotF32, SoftmaxInPlace, probabilities rounded to fp16, values summed by
  * Axpy in position order; the heads' outputs [M][heads*head_dim] quantised to
- * Q8_0 into q/scales/qsum for the output projection. */
+ * Q8_0 into q/scales/qsum for the output projection.  workspace: 256-byte
+ * aligned device memory of gx_qwen_attention_workspace_bytes. */
 int gx_qwen_attention(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int kv_heads, int head_dim, int max_pos,
-                      const int32_t *positions, const uint16_t *kcache, const uint16_t *vcache, int8_t *q,
-                      float *scales, int32_t *qsum);
+                      const int32_t *positions, const uint16_t *kcache, const uint16_t *vcache, int context,
+                      int8_t *q, float *scales, int32_t *qsum, void *workspace, size_t workspace_bytes);
 
 /* SwiGLURange (nn/swiglu.go:77-82) and the Q8_0 of the result: gu[m] holds
  * position m's gate (ffn floats) then up (ffn floats); q/scales/qsum receive

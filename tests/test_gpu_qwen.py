@@ -99,6 +99,38 @@ def test_batch_equals_one_at_a_time(dev, name):
     model.free()
 
 
+@pytest.mark.parametrize("name", list(CONFIGS))
+def test_graph_decode_matches_eager(dev, name):
+    """The captured decode step, replayed: the token after every replay, and at
+    the end the caches and the last hidden state, bit for bit those of the
+    eager steps.  Each replay is followed by eager work (the check) and a
+    synchronisation; a second prompt reuses the same graph."""
+    cfg, model, _ = models(dev, name, False)
+    steps = 9
+    for seed in (21, 22):
+        prompt = [int(t) for t in synth.rng(seed).integers(0, cfg.vocab, 11 + seed % 2)]
+        want = model.greedy(prompt, steps)
+        kc = [k.clone() for k in model.kc]
+        vc = [v.clone() for v in model.vc]
+        hidden = model.hidden[0].clone()
+        model.reset()
+        model.forward(prompt, 0)
+        tok = model.next_token(len(prompt) - 1)
+        model.capture_decode()
+        model.start_decode(tok, len(prompt))
+        for s in range(steps - 1):
+            model.graph.replay()
+            torch.cuda.synchronize()
+            assert int(model.tokens[0].item()) == want[s + 1], f"replay {s}"
+        assert model.decoded(tok, len(prompt), steps) == want
+        for layer in range(cfg.layers):
+            assert torch.equal(kc[layer], model.kc[layer]) and torch.equal(vc[layer], model.vc[layer])
+        assert torch.equal(hidden.view(torch.int32), model.hidden[0].view(torch.int32))
+        assert model.greedy(prompt, steps, graph=True) == want
+    log(f"  {name}: graph replays match the eager steps")
+    model.free()
+
+
 def test_bad_shapes_are_refused(dev):
     from golem_amd import capi
     cfg, model, _ = models(dev, "hd64", False)
@@ -155,12 +187,12 @@ def test_qk_rope_and_cache_bit_exact(dev, orc, hd, heads, kv):
     pos = np.array([0, 1, 5, 17, 38, 39], np.int32)
     qh = dev.empty((M, heads * hd), np.int16)
     kc = torch.zeros((ctx_len, kv, hd), dtype=torch.int16, device="cuda")
-    vc = torch.zeros((ctx_len, kv, hd), dtype=torch.int16, device="cuda")
+    vc = torch.zeros((kv, hd, ctx_len), dtype=torch.int16, device="cuda")  # values transposed
     # every input held by a name until the kernel has run (capi.vp keeps only the address)
     ins = [dev.put(a) for a in (qkv, pos, qn, kn, cos, sin)]
     capi.call("gx_qwen_qk_rope", dev.ctx.ptr, capi.vp(ins[0]), width, M, heads, kv, hd, capi.vp(ins[1]),
               capi.vp(ins[2]), capi.vp(ins[3]), capi.vp(ins[4]), capi.vp(ins[5]), np.float32(1e-6), capi.vp(qh),
-              capi.vp(kc), capi.vp(vc))
+              capi.vp(kc), capi.vp(vc), ctx_len)
     got_q = dev.get(qh).view(np.float16).astype(np.float32)
     got_k = kc.cpu().numpy().view(np.float16).astype(np.float32)
     got_v = vc.cpu().numpy().view(np.float16).astype(np.float32)
@@ -178,25 +210,43 @@ def test_qk_rope_and_cache_bit_exact(dev, orc, hd, heads, kv):
             vh = qkv[t, (heads + kv + h) * hd:(heads + kv + h + 1) * hd]
             want_v = np.array([lib.orc_round_half(float(v)) for v in vh], np.float32)
             np.testing.assert_array_equal(got_k[pos[t], h].view(np.uint32), want_k.view(np.uint32))
-            np.testing.assert_array_equal(got_v[pos[t], h].view(np.uint32), want_v.view(np.uint32))
+            np.testing.assert_array_equal(got_v[h, :, pos[t]].view(np.uint32), want_v.view(np.uint32))
 
 
-@pytest.mark.parametrize("hd,heads,kv,ctx_len", [(128, 8, 2, 70), (64, 4, 2, 300), (128, 32, 8, 640)])
-def test_attention_bit_exact(dev, orc, hd, heads, kv, ctx_len):
+ATTENTION = [(128, 8, 2, 70), (64, 4, 2, 300), (128, 32, 8, 640),
+             (64, 2, 1, 2100),  # past the values pass's LDS chunk and the softmax's
+             (32, 8, 1, 95), (96, 4, 4, 130)]
+
+
+@pytest.mark.parametrize("batch", ["prompt", "one", "three"])
+@pytest.mark.parametrize("hd,heads,kv,ctx_len", ATTENTION)
+def test_attention_bit_exact(dev, orc, hd, heads, kv, ctx_len, batch):
     """Every query of a batch at its own position (the last sees the whole
-    cache): scores, softmax, fp16 probabilities, values, Q8_0 of the heads."""
-    g = synth.rng(63 + ctx_len)
-    pos = np.array([0, 1, ctx_len // 3, ctx_len - 2, ctx_len - 1], np.int32)
+    cache): scores, softmax, fp16 probabilities, values, Q8_0 of the heads.  A
+    prompt (more than 4 positions) and a decode step (one position, or three)
+    take differently shaped launches."""
+    g = synth.rng(63 + ctx_len + hd)
+    if batch == "prompt":
+        pos = np.array([0, 1, ctx_len // 3, ctx_len // 2, ctx_len // 2 + 1, ctx_len - 2, ctx_len - 1], np.int32)
+    elif batch == "one":
+        pos = np.array([ctx_len - 1], np.int32)
+    else:
+        pos = np.array([5, ctx_len - 9, ctx_len - 1], np.int32)
     M = len(pos)
+    context = (ctx_len + 7) // 8 * 8
     kcf = g.standard_normal((ctx_len, kv, hd)).astype(np.float16)
     vcf = (g.standard_normal((ctx_len, kv, hd)) * 2).astype(np.float16)
     qf = (g.standard_normal((M, heads * hd)) * 1.5).astype(np.float16)
+    vt = np.zeros((kv, hd, context), np.float16)  # the device's value layout
+    vt[:, :, :ctx_len] = vcf.transpose(1, 2, 0)
     q8 = dev.empty((M, heads * hd), np.int8)
     sc = dev.empty((M, heads * hd // 32), np.float32)
     qs = dev.empty((M, heads * hd // 32), np.int32)
-    ins = [dev.put(a) for a in (qf.view(np.int16), pos, kcf.view(np.int16), vcf.view(np.int16))]
+    n = capi.size_out("gx_qwen_attention_workspace_bytes", M, heads, int(pos.max()))
+    ws = dev.empty((n,), np.uint8)
+    ins = [dev.put(a) for a in (qf.view(np.int16), pos, kcf.view(np.int16), vt.view(np.int16))]
     capi.call("gx_qwen_attention", dev.ctx.ptr, capi.vp(ins[0]), M, heads, kv, hd, int(pos.max()), capi.vp(ins[1]),
-              capi.vp(ins[2]), capi.vp(ins[3]), capi.vp(q8), capi.vp(sc), capi.vp(qs))
+              capi.vp(ins[2]), capi.vp(ins[3]), context, capi.vp(q8), capi.vp(sc), capi.vp(qs), capi.vp(ws), n)
     lib = orc.load()
     K32, V32 = np.ascontiguousarray(kcf.astype(np.float32)), np.ascontiguousarray(vcf.astype(np.float32))
     scale = np.float32(1 / math.sqrt(float(hd)))
@@ -213,6 +263,21 @@ def test_attention_bit_exact(dev, orc, hd, heads, kv, ctx_len):
     np.testing.assert_array_equal(dev.get(q8), b.q_rows())
     np.testing.assert_array_equal(dev.get(sc).view(np.uint32), b.scales_rows().view(np.uint32))
     np.testing.assert_array_equal(dev.get(qs), b.qsum_rows())
+
+
+def test_attention_refuses_bad_caches(dev):
+    M, heads, kv, hd = 1, 4, 2, 64
+    n = capi.size_out("gx_qwen_attention_workspace_bytes", M, heads, 15)
+    ws = dev.empty((n,), np.uint8)
+    buf = dev.empty((4096,), np.int16)
+    args = [capi.vp(buf), M, heads, kv, hd, 15, capi.vp(buf), capi.vp(buf), capi.vp(buf)]
+    outs = [capi.vp(buf), capi.vp(buf), capi.vp(buf), capi.vp(ws)]
+    with pytest.raises(capi.GxError):  # a context that is not a multiple of 8
+        capi.call("gx_qwen_attention", dev.ctx.ptr, *args, 20, *outs, n)
+    with pytest.raises(capi.GxError):  # max_pos beyond the context
+        capi.call("gx_qwen_attention", dev.ctx.ptr, *args, 8, *outs, n)
+    with pytest.raises(capi.GxError):  # a workspace too small
+        capi.call("gx_qwen_attention", dev.ctx.ptr, *args, 16, *outs, n - 256)
 
 
 def test_swiglu_quant_bit_exact(dev, orc):
