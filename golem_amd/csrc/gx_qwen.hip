@@ -136,8 +136,13 @@ constexpr int kHeadMax = 256;  // head_dim limit (two values per lane)
 // position's Q rows, then K rows, then V rows.  rope_cos/sin are [context][hd/2].
 // Query heads: normed, rotated, rounded to fp16 into qh [M][heads*hd].  Key-
 // value heads: the key normed and rotated, both rounded to fp16 into the
-// layer's caches: the key at [pos][kvh][hd], the value at [kvh][hd][pos] of a
-// cache of `context` positions.
+// layer's caches of `context` positions: the key in 16-byte pieces,
+// [kvh][hd/8][pos][8] (a wavefront reading piece i of 64 consecutive
+// positions reads 1 KiB in one run), the value at [kvh][hd][pos].
+__device__ __forceinline__ void kcache_put(uint16_t *kt, int context, int e, uint16_t v) {
+    kt[(size_t)(e >> 3) * context * 8 + (e & 7)] = v;
+}
+
 __global__ __launch_bounds__(64) void qwen_qk_rope_kernel(const float *__restrict__ qkv, int ldqkv, int heads,
                                                           int kv_heads, int hd, const int32_t *__restrict__ positions,
                                                           const float *__restrict__ q_norm,
@@ -173,9 +178,10 @@ __global__ __launch_bounds__(64) void qwen_qk_rope_kernel(const float *__restric
             qh[(size_t)t * heads * hd + u * hd + i] = (uint16_t)float_to_half_bits(a);
             qh[(size_t)t * heads * hd + u * hd + i + half] = (uint16_t)float_to_half_bits(b);
         } else {
-            const size_t o = ((size_t)pos * kv_heads + (u - heads)) * hd;
-            kcache[o + i] = (uint16_t)float_to_half_bits(a);
-            kcache[o + i + half] = (uint16_t)float_to_half_bits(b);
+            // [kvh][hd/8][context][8]: piece e/8 of a key at position pos
+            uint16_t *kt = kcache + (size_t)(u - heads) * hd * context + (size_t)pos * 8;
+            kcache_put(kt, context, i, (uint16_t)float_to_half_bits(a));
+            kcache_put(kt, context, i + half, (uint16_t)float_to_half_bits(b));
         }
     }
     if (!is_q) {
@@ -209,7 +215,23 @@ __device__ __forceinline__ float half_lo(uint32_t w) {
 }
 __device__ __forceinline__ float half_hi(uint32_t w) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16)); }
 
+// lo/hi(a) * lo/hi(b) + c for fp16 pairs a and b, as one v_fma_mix: written
+// out so that a key row reused for several heads stays in its packed form
+// (the compiler would otherwise widen it to 128 floats once and run out of
+// registers).
+__device__ __forceinline__ float fma_mix_lo(uint32_t a, uint32_t b, float c) {
+    float r;
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,1,0]" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+__device__ __forceinline__ float fma_mix_hi(uint32_t a, uint32_t b, float c) {
+    float r;
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,1,0] op_sel_hi:[1,1,0]" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+
 constexpr int kTile = 64;  // positions per scores wavefront
+typedef float v4f_lds __attribute__((ext_vector_type(4)));
 
 // grid (S/64 position tiles, heads/GH head groups, ceil(M/TT) token tiles),
 // one wavefront.  Lane = cached position p; its key row is held in registers
@@ -218,7 +240,7 @@ constexpr int kTile = 64;  // positions per scores wavefront
 template <int HD>
 __global__ __launch_bounds__(64) void attn_scores_kernel(const uint16_t *__restrict__ qh, int M, int heads, int G,
                                                          int GH, int TT, const int32_t *__restrict__ positions, int limit,
-                                                         const uint16_t *__restrict__ kcache, int kv_heads,
+                                                         const uint16_t *__restrict__ kcache, int context,
                                                          float scale, int S, float *__restrict__ sc,
                                                          float *__restrict__ tmax) {
     const int lane = threadIdx.x, tile = blockIdx.x;
@@ -231,11 +253,11 @@ __global__ __launch_bounds__(64) void attn_scores_kernel(const uint16_t *__restr
     if (tile * kTile > last)
         return;  // the whole wavefront: nothing visible here
     const int p = tile * kTile + lane;
-    const v4u_stream *kr = (const v4u_stream *)(kcache + ((size_t)min(p, last) * kv_heads + kvh) * HD);
+    const v4u_stream *kr = (const v4u_stream *)(kcache + (size_t)kvh * HD * context) + min(p, last);
     v4u_stream k[HD / 8];
 #pragma unroll
     for (int i = 0; i < HD / 8; i++)
-        k[i] = kr[i];
+        k[i] = kr[(size_t)i * context];
     for (int tt = 0; tt < tn; tt++) {
         const int t = t0 + tt;
         const int n = min(positions[t] + 1, limit);
@@ -274,34 +296,47 @@ __global__ __launch_bounds__(64) void attn_scores_kernel(const uint16_t *__restr
 constexpr int kSoftChunk = 2048;  // exponentials per pass through LDS
 
 // Sum e[0 .. n) into `total` one value at a time, in order: two register sets
-// of 16 so that the next set's LDS reads overlap this set's additions.
+// of 16, the next set's LDS reads under this set's additions.  e is 16-byte
+// aligned and readable to e[n + 15] (the reads of a set may pass n; those
+// values are never added).
 __device__ __forceinline__ float serial_sum(const float *e, int n, float total) {
+    const v4f_lds *e4 = (const v4f_lds *)e;
+    v4f_lds a[4], b[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++)
+        a[u] = e4[u];
     int j = 0;
-    if (n >= 16) {
-        float a[16], b[16];
+    for (; j + 32 <= n; j += 32) {
 #pragma unroll
-        for (int u = 0; u < 16; u++)
-            a[u] = e[u];
-        for (; j + 32 <= n; j += 32) {
+        for (int u = 0; u < 4; u++)
+            b[u] = e4[(j + 16) / 4 + u];
 #pragma unroll
-            for (int u = 0; u < 16; u++)
-                b[u] = e[j + 16 + u];
-#pragma unroll
-            for (int u = 0; u < 16; u++)
-                total += a[u];
-#pragma unroll
-            for (int u = 0; u < 16; u++)
-                a[u] = e[min(j + 32 + u, n - 1)];
-#pragma unroll
-            for (int u = 0; u < 16; u++)
-                total += b[u];
+        for (int u = 0; u < 4; u++) {
+            total += a[u].x;
+            total += a[u].y;
+            total += a[u].z;
+            total += a[u].w;
         }
-        if (j + 16 <= n) {
 #pragma unroll
-            for (int u = 0; u < 16; u++)
-                total += a[u];
-            j += 16;
+        for (int u = 0; u < 4; u++)
+            a[u] = e4[(j + 32) / 4 + u];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            total += b[u].x;
+            total += b[u].y;
+            total += b[u].z;
+            total += b[u].w;
         }
+    }
+    if (j + 16 <= n) {  // a holds e[j .. j + 16)
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            total += a[u].x;
+            total += a[u].y;
+            total += a[u].z;
+            total += a[u].w;
+        }
+        j += 16;
     }
     for (; j < n; j++)
         total += e[j];
@@ -314,7 +349,7 @@ __global__ __launch_bounds__(64) void attn_softmax_kernel(int heads, const int32
                                                           int S,
                                                           float *__restrict__ sc, const float *__restrict__ tmax,
                                                           uint16_t *__restrict__ prob) {
-    __shared__ float e[kSoftChunk];
+    __shared__ __align__(16) float e[kSoftChunk + 16];  // serial_sum reads to n + 15
     __shared__ float total_sh;
     const int lane = threadIdx.x, h = blockIdx.x, t = blockIdx.y;
     const size_t row = (size_t)t * heads + h;
@@ -453,6 +488,209 @@ __global__ __launch_bounds__(NT) void attn_values_kernel(int M, int heads, int G
     }
 }
 
+// Decode attention in one kernel (M <= 4 positions, prefixes of at most
+// kDecodeMax positions): grid (kv_heads * hd/32 slices, M), 512 threads.  A
+// workgroup computes, for the G query heads of key-value head kvh, the
+// scores over the whole prefix (a thread per position, its key rows in
+// registers, the queries in LDS), the softmax and the probabilities, then the
+// 32 value chains of its slice for each head -- the same arithmetic, in the
+// same order, as the three passes above.  Its slice of the value rows and its
+// key rows are loaded first, so that the loads overlap; the slices'
+// workgroups repeat the scores and softmax of their heads.
+constexpr int kDecodeMax = 768;
+constexpr int kDecodeThreads = 512;
+constexpr int kDecodeStride = kDecodeMax + 8;  // value and probability rows, in halves
+constexpr int kDecodeRegs = kValSlice * (kDecodeMax / 8) / kDecodeThreads;  // value pieces per thread
+constexpr int kDecodeRows = (kDecodeMax + kDecodeThreads - 1) / kDecodeThreads;  // positions per thread
+constexpr int kScoreStride = kDecodeMax + 20;  // score rows 20 banks apart (conflict-free serial sums), read to n + 15
+
+template <int HD, int G>
+__global__ __launch_bounds__(kDecodeThreads) void attn_decode_kernel(
+    const uint16_t *__restrict__ qh, int heads, int kv_heads, const int32_t *__restrict__ positions, int limit,
+    const uint16_t *__restrict__ kcache, const uint16_t *__restrict__ vcache, int context, float scale,
+    int8_t *__restrict__ q, float *__restrict__ scales, int32_t *__restrict__ qsum) {
+    // LDS: region A holds the scores [G][kScoreStride] floats, later the value
+    // slice [32][kDecodeStride] halves; then the probabilities [G][kDecodeStride]
+    // halves and the queries [G][HD] halves.
+    // (+128 bytes: the chains' last reads may pass the end of the rows)
+    __shared__ __align__(16) uint8_t lds[kValSlice * kDecodeStride * 2 + G * kDecodeStride * 2 + G * HD * 2 + 128];
+    static_assert(G * kScoreStride * 4 + 64 <= kValSlice * kDecodeStride * 2, "scores fit region A");
+    __shared__ float red[kDecodeThreads / 64][G];
+    __shared__ float total[G];
+    float *sc = (float *)lds;
+    uint16_t *vs = (uint16_t *)lds;
+    uint16_t *ps = (uint16_t *)(lds + kValSlice * kDecodeStride * 2);
+    uint32_t *ql = (uint32_t *)(lds + kValSlice * kDecodeStride * 2 + G * kDecodeStride * 2);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    constexpr int slices = HD / kValSlice;
+    const int kvh = blockIdx.x / slices, d0 = (blockIdx.x - kvh * slices) * kValSlice;
+    const int t = blockIdx.y;
+    const int n = min(positions[t] + 1, limit);
+    const int groups = (n + 7) / 8, pieces = kValSlice * groups;
+
+    // The G queries (adjacent heads of the row) first, then the key pieces of
+    // this thread's positions, then the value slice (32 rows of positions,
+    // 16 bytes = 8 positions a piece): the queries can be stored while the
+    // rest is in flight.
+    const uint32_t *qg = (const uint32_t *)(qh + ((size_t)t * heads + kvh * G) * HD);
+    uint32_t qr = qg[min(tid, G * HD / 2 - 1)];
+    v4u_stream k[kDecodeRows][HD / 8];
+    const v4u_stream *kbase = (const v4u_stream *)(kcache + (size_t)kvh * HD * context);
+#pragma unroll
+    for (int r = 0; r < kDecodeRows; r++) {
+        const int p = min(tid + r * kDecodeThreads, n - 1);
+#pragma unroll
+        for (int i = 0; i < HD / 8; i++)
+            k[r][i] = kbase[(size_t)i * context + p];
+    }
+    const uint16_t *vrow = vcache + ((size_t)kvh * HD + d0) * context;
+    v4u_stream vr[kDecodeRegs];
+#pragma unroll
+    for (int u = 0; u < kDecodeRegs; u++) {
+        const int i = min(tid + u * kDecodeThreads, pieces - 1);
+        const int rr = i / groups, c = i - rr * groups;
+        vr[u] = *(const v4u_stream *)(vrow + (size_t)rr * context + 8 * c);
+    }
+    static_assert(G * HD / 2 <= kDecodeThreads, "one query dword per thread");
+    if (tid < G * HD / 2)
+        ql[tid] = qr;
+    __syncthreads();
+
+    // scores, DotF32's four chains: element e of a head goes to chain e % 4
+    float mx[G];
+#pragma unroll
+    for (int g = 0; g < G; g++)
+        mx[g] = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < kDecodeRows; r++) {
+        const int p = tid + r * kDecodeThreads;
+        if (r * kDecodeThreads + wave * 64 >= n)
+            break;  // the wavefront's positions are all past the prefix
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            const v4u_stream *qv = (const v4u_stream *)(ql + g * HD / 2);
+            float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+#pragma unroll
+            for (int i = 0; i < HD / 8; i++) {
+                const v4u_stream qq = qv[i], kk = k[r][i];
+                s0 = fma_mix_lo(qq.x, kk.x, s0);
+                s1 = fma_mix_hi(qq.x, kk.x, s1);
+                s2 = fma_mix_lo(qq.y, kk.y, s2);
+                s3 = fma_mix_hi(qq.y, kk.y, s3);
+                s0 = fma_mix_lo(qq.z, kk.z, s0);
+                s1 = fma_mix_hi(qq.z, kk.z, s1);
+                s2 = fma_mix_lo(qq.w, kk.w, s2);
+                s3 = fma_mix_hi(qq.w, kk.w, s3);
+            }
+            const float v = scale * ((s0 + s1) + (s2 + s3));
+            if (p < n) {
+                sc[g * kScoreStride + p] = v;
+                mx[g] = fmaxf(mx[g], v);
+            }
+        }
+    }
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1)
+            mx[g] = fmaxf(mx[g], __shfl_xor(mx[g], off, 64));
+        if (lane == 0)
+            red[wave][g] = mx[g];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        float m = red[0][g];
+#pragma unroll
+        for (int w = 1; w < kDecodeThreads / 64; w++)
+            m = fmaxf(m, red[w][g]);
+        for (int p = tid; p < n; p += kDecodeThreads)
+            sc[g * kScoreStride + p] = (float)exp((double)(sc[g * kScoreStride + p] - m));
+    }
+    __syncthreads();
+    if (tid < G)
+        total[tid] = serial_sum(sc + tid * kScoreStride, n, 0.0f);
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < G; g++)
+        for (int p = tid; p < groups * 8; p += kDecodeThreads)
+            ps[g * kDecodeStride + p] =
+                p < n ? (uint16_t)float_to_half_bits(__fdiv_rn(sc[g * kScoreStride + p], total[g])) : (uint16_t)0;
+    __syncthreads();  // the scores are dead: region A takes the value slice
+#pragma unroll
+    for (int u = 0; u < kDecodeRegs; u++) {
+        const int i = tid + u * kDecodeThreads;
+        if (i < pieces) {
+            const int rr = i / groups, c = i - rr * groups;
+            *(v4u_stream *)(vs + rr * kDecodeStride + 8 * c) = vr[u];
+        }
+    }
+    __syncthreads();
+    if (tid < G * kValSlice) {
+        const int dd = tid % kValSlice, g = tid / kValSlice;
+        const uint16_t *vrr = vs + dd * kDecodeStride, *pr = ps + g * kDecodeStride;
+        float acc = 0.0f;
+        // 32 positions a set, the next set's LDS reads under this set's fmas
+        // (a set may read past n, inside the LDS array; those are not used)
+        v4u_stream av[4], ap[4], bv[4], bp[4];
+#define GX_DEC_LOAD(sv, sp, at)                                                                                      \
+    _Pragma("unroll") for (int u = 0; u < 4; u++) {                                                                  \
+        sv[u] = *(const v4u_stream *)(vrr + (at) + 8 * u);                                                           \
+        sp[u] = *(const v4u_stream *)(pr + (at) + 8 * u);                                                            \
+    }
+#define GX_DEC_FMA(sv, sp)                                                                                           \
+    _Pragma("unroll") for (int u = 0; u < 4; u++) {                                                                  \
+        acc = __builtin_fmaf(half_lo(sp[u].x), half_lo(sv[u].x), acc);                                               \
+        acc = __builtin_fmaf(half_hi(sp[u].x), half_hi(sv[u].x), acc);                                               \
+        acc = __builtin_fmaf(half_lo(sp[u].y), half_lo(sv[u].y), acc);                                               \
+        acc = __builtin_fmaf(half_hi(sp[u].y), half_hi(sv[u].y), acc);                                               \
+        acc = __builtin_fmaf(half_lo(sp[u].z), half_lo(sv[u].z), acc);                                               \
+        acc = __builtin_fmaf(half_hi(sp[u].z), half_hi(sv[u].z), acc);                                               \
+        acc = __builtin_fmaf(half_lo(sp[u].w), half_lo(sv[u].w), acc);                                               \
+        acc = __builtin_fmaf(half_hi(sp[u].w), half_hi(sv[u].w), acc);                                               \
+    }
+        int j = 0;
+        GX_DEC_LOAD(av, ap, 0);
+        for (; j + 64 <= n; j += 64) {
+            GX_DEC_LOAD(bv, bp, j + 32);
+            GX_DEC_FMA(av, ap);
+            GX_DEC_LOAD(av, ap, j + 64);
+            GX_DEC_FMA(bv, bp);
+        }
+        if (j + 32 <= n) {  // av holds positions j .. j + 32
+            GX_DEC_FMA(av, ap);
+            j += 32;
+        }
+#undef GX_DEC_FMA
+#undef GX_DEC_LOAD
+        for (; j + 8 <= n; j += 8) {
+            const v4u_stream vv = *(const v4u_stream *)(vrr + j);
+            const v4u_stream pp = *(const v4u_stream *)(pr + j);
+            acc = __builtin_fmaf(half_lo(pp.x), half_lo(vv.x), acc);
+            acc = __builtin_fmaf(half_hi(pp.x), half_hi(vv.x), acc);
+            acc = __builtin_fmaf(half_lo(pp.y), half_lo(vv.y), acc);
+            acc = __builtin_fmaf(half_hi(pp.y), half_hi(vv.y), acc);
+            acc = __builtin_fmaf(half_lo(pp.z), half_lo(vv.z), acc);
+            acc = __builtin_fmaf(half_hi(pp.z), half_hi(vv.z), acc);
+            acc = __builtin_fmaf(half_lo(pp.w), half_lo(vv.w), acc);
+            acc = __builtin_fmaf(half_hi(pp.w), half_hi(vv.w), acc);
+        }
+        for (; j < n; j++)
+            acc = __builtin_fmaf((float)__builtin_bit_cast(_Float16, pr[j]),
+                                 (float)__builtin_bit_cast(_Float16, vrr[j]), acc);
+        float stored;
+        int32_t sm;
+        const int32_t nq = q8_0_lane(acc, &stored, &sm);
+        const int width = heads * HD, B = width >> 5;
+        const int col = (kvh * G + g) * HD + d0 + dd;
+        q[(size_t)t * width + col] = (int8_t)nq;
+        if (dd == 0) {
+            scales[(size_t)t * B + (col >> 5)] = stored;
+            qsum[(size_t)t * B + (col >> 5)] = sm;
+        }
+    }
+}
+
 // expf (ggml_v_expf one value at a time), nn/swiglu.go:31-74.
 __device__ __forceinline__ float ggml_expf(float x) {
     const float shift = 0x1.8p23f;
@@ -564,7 +802,8 @@ int launch_qwen_qk_rope(gx_ctx *ctx, const float *qkv, int ldqkv, int M, int hea
                         const int32_t *positions, const float *q_norm, const float *k_norm, const float *rope_cos,
                         const float *rope_sin, float eps, uint16_t *qh, uint16_t *kcache, uint16_t *vcache,
                         int context) {
-    GX_CHECK(hd <= kHeadMax && hd % 2 == 0, "gx: head width %d unsupported (even, at most %d)", hd, kHeadMax);
+    GX_CHECK(hd <= kHeadMax && hd % 8 == 0, "gx: head width %d unsupported (a multiple of 8, at most %d)", hd,
+             kHeadMax);
     qwen_qk_rope_kernel<<<dim3((unsigned)M, (unsigned)(heads + kv_heads)), 64, 0, ctx->stream>>>(
         qkv, ldqkv, heads, kv_heads, hd, positions, q_norm, k_norm, rope_cos, rope_sin, eps, qh, kcache, vcache,
         context);
@@ -592,6 +831,34 @@ int launch_qwen_attention(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int
     float *tmax = (float *)(workspace + up(rows * S * sizeof(float)));
     uint16_t *prob = (uint16_t *)(workspace + up(rows * S * sizeof(float)) + up(rows * (S / kTile) * sizeof(float)));
 
+    if (M <= 4 && limit <= kDecodeMax) {
+#define GX_DECODE(HH, GG)                                                                                            \
+    attn_decode_kernel<HH, GG><<<dim3((unsigned)(kv_heads * (HH / kValSlice)), (unsigned)M), kDecodeThreads, 0,      \
+                                 ctx->stream>>>(qh, heads, kv_heads, positions, limit, kcache, vcache, context,      \
+                                                scale, q, scales, qsum)
+#define GX_DECODE_G(HH)                                                                                              \
+    do {                                                                                                             \
+        if (G == 1)                                                                                                  \
+            GX_DECODE(HH, 1);                                                                                        \
+        else if (G == 2)                                                                                             \
+            GX_DECODE(HH, 2);                                                                                        \
+        else if (G == 4)                                                                                             \
+            GX_DECODE(HH, 4);                                                                                        \
+        else                                                                                                         \
+            GX_DECODE(HH, 8);                                                                                        \
+    } while (0)
+        if (hd == 32)
+            GX_DECODE_G(32);
+        else if (hd == 64)
+            GX_DECODE_G(64);
+        else if (hd == 96)
+            GX_DECODE_G(96);
+        else
+            GX_DECODE_G(128);
+#undef GX_DECODE_G
+#undef GX_DECODE
+        return check_launch("qwen_attention decode");
+    }
     // Scores: decode spreads the heads of a group over wavefronts (the key
     // rows are re-read from L2); a batch shares each key row among the group's
     // heads and 8 tokens.
@@ -599,7 +866,7 @@ int launch_qwen_attention(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int
     const dim3 sgrid((unsigned)(S / kTile), (unsigned)(heads / GH), (unsigned)((M + TT - 1) / TT));
 #define GX_SCORES(HH)                                                                                                \
     attn_scores_kernel<HH><<<sgrid, 64, 0, ctx->stream>>>(qh, M, heads, G, GH, TT, positions, limit, kcache,       \
-                                                          kv_heads, scale, S, sc, tmax)
+                                                          context, scale, S, sc, tmax)
     if (hd == 32)
         GX_SCORES(32);
     else if (hd == 64)

@@ -88,9 +88,10 @@ class QwenModel:
         self.output_norm = dev(weights["output_norm"])
         cos, sin = rope_tables(cfg.head_dim, cfg.max_context, cfg.rope_base)
         self.rope_cos, self.rope_sin = dev(cos), dev(sin)
-        # keys [context][kv_head][head_dim]; values transposed, [kv_head][head_dim][context]
+        # keys in 16-byte pieces [kv_head][head_dim/8][context][8]; values
+        # transposed, [kv_head][head_dim][context]
         self.context = (cfg.max_context + 7) // 8 * 8
-        kshape = (self.context, cfg.kv_heads, cfg.head_dim)
+        kshape = (cfg.kv_heads, cfg.head_dim // 8, self.context, 8)
         vshape = (cfg.kv_heads, cfg.head_dim, self.context)
         self.kc = [torch.zeros(kshape, dtype=torch.int16, device="cuda") for _ in range(cfg.layers)]
         self.vc = [torch.zeros(vshape, dtype=torch.int16, device="cuda") for _ in range(cfg.layers)]

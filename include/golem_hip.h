@@ -245,11 +245,12 @@ int gx_norm_quant(gx_ctx *ctx, float *x, int ldx, const float *add, int lda, con
  * RoPETable.Prepare values) and rounded to fp16 into qh [M][heads*head_dim];
  * key heads are normed by k_norm and rotated, and key and value are stored
  * rounded to fp16 into the layer's caches (LayerCache.Store,
- * qwen/cache.go:52-60), a cache of `context` positions: the key at
- * kcache[positions[m]][kv_head][head_dim], the value transposed at
- * vcache[kv_head][head_dim][positions[m]] (a value row holds one element of
- * a head over all positions).  positions[m] < context.  All device
- * pointers; positions: M int32. */
+ * qwen/cache.go:52-60), a cache of `context` positions: element e of the key
+ * at kcache[kv_head][e / 8][positions[m]][e % 8] (16-byte pieces, a piece of
+ * consecutive positions contiguous), the value transposed at
+ * vcache[kv_head][e][positions[m]] (a value row holds one element of a head
+ * over all positions).  positions[m] < context; head_dim a multiple of 8.
+ * All device pointers; positions: M int32. */
 int gx_qwen_qk_rope(gx_ctx *ctx, const float *qkv, int ldqkv, int M, int heads, int kv_heads, int head_dim,
                     const int32_t *positions, const float *q_norm, const float *k_norm, const float *rope_cos,
                     const float *rope_sin, float eps, uint16_t *qh, uint16_t *kcache, uint16_t *vcache, int context);

@@ -186,7 +186,7 @@ def test_qk_rope_and_cache_bit_exact(dev, orc, hd, heads, kv):
     kn = (1 + 0.02 * g.standard_normal(hd)).astype(np.float32)
     pos = np.array([0, 1, 5, 17, 38, 39], np.int32)
     qh = dev.empty((M, heads * hd), np.int16)
-    kc = torch.zeros((ctx_len, kv, hd), dtype=torch.int16, device="cuda")
+    kc = torch.zeros((kv, hd // 8, ctx_len, 8), dtype=torch.int16, device="cuda")  # keys in 16-byte pieces
     vc = torch.zeros((kv, hd, ctx_len), dtype=torch.int16, device="cuda")  # values transposed
     # every input held by a name until the kernel has run (capi.vp keeps only the address)
     ins = [dev.put(a) for a in (qkv, pos, qn, kn, cos, sin)]
@@ -209,7 +209,7 @@ def test_qk_rope_and_cache_bit_exact(dev, orc, hd, heads, kv):
             want_k = np.array([lib.orc_round_half(float(v)) for v in kh], np.float32)
             vh = qkv[t, (heads + kv + h) * hd:(heads + kv + h + 1) * hd]
             want_v = np.array([lib.orc_round_half(float(v)) for v in vh], np.float32)
-            np.testing.assert_array_equal(got_k[pos[t], h].view(np.uint32), want_k.view(np.uint32))
+            np.testing.assert_array_equal(got_k[h, :, pos[t], :].reshape(-1).view(np.uint32), want_k.view(np.uint32))
             np.testing.assert_array_equal(got_v[h, :, pos[t]].view(np.uint32), want_v.view(np.uint32))
 
 
@@ -239,12 +239,14 @@ def test_attention_bit_exact(dev, orc, hd, heads, kv, ctx_len, batch):
     qf = (g.standard_normal((M, heads * hd)) * 1.5).astype(np.float16)
     vt = np.zeros((kv, hd, context), np.float16)  # the device's value layout
     vt[:, :, :ctx_len] = vcf.transpose(1, 2, 0)
+    kt = np.zeros((kv, hd // 8, context, 8), np.float16)  # and its key layout
+    kt[:, :, :ctx_len, :] = kcf.reshape(ctx_len, kv, hd // 8, 8).transpose(1, 2, 0, 3)
     q8 = dev.empty((M, heads * hd), np.int8)
     sc = dev.empty((M, heads * hd // 32), np.float32)
     qs = dev.empty((M, heads * hd // 32), np.int32)
     n = capi.size_out("gx_qwen_attention_workspace_bytes", M, heads, int(pos.max()))
     ws = dev.empty((n,), np.uint8)
-    ins = [dev.put(a) for a in (qf.view(np.int16), pos, kcf.view(np.int16), vt.view(np.int16))]
+    ins = [dev.put(a) for a in (qf.view(np.int16), pos, kt.view(np.int16), vt.view(np.int16))]
     capi.call("gx_qwen_attention", dev.ctx.ptr, capi.vp(ins[0]), M, heads, kv, hd, int(pos.max()), capi.vp(ins[1]),
               capi.vp(ins[2]), capi.vp(ins[3]), context, capi.vp(q8), capi.vp(sc), capi.vp(qs), capi.vp(ws), n)
     lib = orc.load()
