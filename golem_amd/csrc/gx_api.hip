@@ -396,6 +396,43 @@ int gx_matmul_q4_0(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const float
     return q4_0_product(ctx, w, 0, q, scales, qsum, q16, M, row_start, row_end, bias, y, ldy);
 }
 
+int gx_norm_matmul_q4_0(gx_ctx *ctx, const gx_weight *w, const float *x, const float *add, const float *gain,
+                        float eps, float *x_out, int row_start, int row_end, float *y) {
+    if (int rc = use(ctx))
+        return rc;
+    if (int rc = check_product(w, GX_Q4_0, 1, row_start, row_end, y, row_end))
+        return rc;
+    GX_CHECK(w->count == 1, "gx: a fused product takes a single matrix");
+    GX_CHECK(x && gain, "gx: missing argument");
+    GX_CHECK(((uintptr_t)gain & 15) == 0, "gx: gain must be 16-byte aligned");
+    GX_CHECK(x_out == nullptr || (x_out != x && x_out != add),
+             "gx: x_out must not alias x or add (other workgroups still read them)");
+    if (row_start == row_end)
+        return ok();
+    if (int rc = gx::launch_q4_0_matvec_fused(ctx, w, 0, row_start, row_end, y, x, add, gain, eps, x_out, nullptr,
+                                              nullptr, nullptr))
+        return rc;
+    return ok();
+}
+
+int gx_norm_swiglu_q4_0(gx_ctx *ctx, const gx_weight *w, const float *x, const float *add, const float *gain,
+                        float eps, float *x_out, int8_t *q, float *scales, int32_t *qsum) {
+    if (int rc = use(ctx))
+        return rc;
+    if (int rc = check_product(w, GX_Q4_0, 1, 0, w ? w->rows : 0, q, 0))
+        return rc;
+    GX_CHECK(w->count == 1, "gx: a fused product takes a single matrix");
+    GX_CHECK(w->rows % 64 == 0, "gx: gate and up interleaved by 32 need a multiple of 64 rows, not %d", w->rows);
+    GX_CHECK(x && gain && scales && qsum, "gx: missing argument");
+    GX_CHECK(((uintptr_t)gain & 15) == 0, "gx: gain must be 16-byte aligned");
+    GX_CHECK(x_out == nullptr || (x_out != x && x_out != add),
+             "gx: x_out must not alias x or add (other workgroups still read them)");
+    if (int rc = gx::launch_q4_0_matvec_fused(ctx, w, 1, 0, w->rows, nullptr, x, add, gain, eps, x_out, q, scales,
+                                              qsum))
+        return rc;
+    return ok();
+}
+
 int gx_matmul_q4_0_expert(gx_ctx *ctx, const gx_weight *w, int expert, const int8_t *q, const float *scales,
                           const int32_t *qsum, const uint16_t *q16, int M, int row_start, int row_end, float *y,
                           int ldy) {
@@ -565,15 +602,17 @@ int gx_qwen_attention(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int kv_
     return ok();
 }
 
-int gx_swiglu_quant(gx_ctx *ctx, const float *gu, int ldgu, int M, int ffn, int8_t *q, float *scales, int32_t *qsum) {
+int gx_swiglu_quant(gx_ctx *ctx, const float *gu, int ldgu, int M, int ffn, int group, int8_t *q, float *scales,
+                    int32_t *qsum) {
     if (int rc = use(ctx))
         return rc;
     GX_CHECK(ffn > 0 && ffn % 32 == 0, "nn: activation length must be a multiple of the block size");
     GX_CHECK(M >= 0 && ldgu >= 2 * ffn, "gx: bad batch shape");
+    GX_CHECK(group == 0 || group == 32, "gx: gate and up come in halves (0) or by 32 (32), not by %d", group);
     GX_CHECK(gu && q && scales && qsum, "gx: missing argument");
     if (M == 0)
         return ok();
-    if (int rc = gx::launch_qwen_swiglu_quant(ctx, gu, ldgu, M, ffn, q, scales, qsum))
+    if (int rc = gx::launch_qwen_swiglu_quant(ctx, gu, ldgu, M, ffn, group, q, scales, qsum))
         return rc;
     return ok();
 }

@@ -41,6 +41,63 @@ __device__ __forceinline__ int32_t nearest_int(float f) {
     return (int32_t)(__float_as_uint(s) & 0x007fffffu) - 0x00400000;
 }
 
+// expf (ggml_v_expf one value at a time), nn/swiglu.go:31-74.
+__device__ __forceinline__ float ggml_expf(float x) {
+    const float shift = 0x1.8p23f;
+    const float log2e = 0x1.715476p+0f;
+    const float ln2hi = 0x1.62e4p-1f;
+    const float ln2lo = 0x1.7f7d1cp-20f;
+    const float c0 = 0x1.ffffecp-1f;
+    const float c1 = 0x1.fffdb6p-2f;
+    const float c2 = 0x1.555e66p-3f;
+    const float c3 = 0x1.573e2ep-5f;
+    const float c4 = 0x1.0e4020p-7f;
+    const float z = x * log2e + shift;
+    const float n = z - shift;
+    if (n > 126.0f || n < -126.0f)
+        return (float)exp((double)x);
+    const float b = x - n * ln2hi - n * ln2lo;
+    const float k = __uint_as_float((__float_as_uint(z) << 23) + __float_as_uint(1.0f));
+    const float u = b * b;
+    const float j = ((c4 * b + c3) * u + (c2 * b + c1)) * u + c0 * b;
+    return j * k + k;
+}
+
+// Q8_0 (Batch.quantizeBlock, nn/batch.go:109-143) of a 32-value block held
+// four values a lane by eight consecutive lanes (lanes 8k .. 8k+7 of a
+// wavefront, values in order): the same arithmetic as q8_0_lane.  Returns the
+// lane's four int8 packed in order; the block's fp16-rounded scale and sum of
+// q come back in *stored and *sum (valid in all eight lanes).
+__device__ __forceinline__ uint32_t q8_0_quad(const float v[4], float *stored, int32_t *sum) {
+    float peak = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+#pragma unroll
+    for (int off = 4; off > 0; off >>= 1)
+        peak = fmaxf(peak, __shfl_xor(peak, off, 8));
+    if (peak == 0.0f) {
+        *stored = 0.0f;
+        *sum = 0;
+        return 0u;
+    }
+    const float scale = __fdiv_rn(peak, 127.0f);
+    const float inverse = __fdiv_rn(127.0f, peak);
+    *stored = half_bits_to_float(float_to_half_bits(scale));
+    uint32_t packed = 0;
+    int32_t s = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const float prod = v[k] * inverse;
+        int32_t n = nearest_int(prod);
+        n = n > 127 ? 127 : (n < -128 ? -128 : n);
+        s += n;
+        packed |= ((uint32_t)n & 0xFFu) << (8 * k);
+    }
+#pragma unroll
+    for (int off = 4; off > 0; off >>= 1)
+        s += __shfl_xor(s, off, 8);
+    *sum = s;
+    return packed;
+}
+
 // Four signed byte products added to c (v_dot4_i32_i8).
 __device__ __forceinline__ int32_t dot4(uint32_t a, uint32_t b, int32_t c) {
     return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);

@@ -108,6 +108,9 @@ int launch_q4_0_gemm_f16(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, co
                          int32_t *dots);
 int launch_q4_0_matvec_units(gx_ctx *ctx, const gx_weight *w, const int32_t *unit_expert, int units, int act_div,
                               const int8_t *q, const float *scales, const int32_t *qsum, float *y, int ldy);
+int launch_q4_0_matvec_fused(gx_ctx *ctx, const gx_weight *w, int epi, int row_start, int row_end, float *y,
+                              const float *x, const float *add, const float *gain, float eps, float *x_out,
+                              int8_t *q, float *scales, int32_t *qsum);
 int launch_q4_0_block_dots_matvec(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const int32_t *qsum, int M,
                                   int row_start, int row_end, int32_t *out);
 int launch_q6_k_matvec(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const float *kscales,
@@ -130,8 +133,8 @@ size_t qwen_attention_workspace(int M, int heads, int max_pos);
 int launch_qwen_attention(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int kv_heads, int hd, int max_pos,
                           const int32_t *positions, const uint16_t *kcache, const uint16_t *vcache, int context,
                           float scale, int8_t *q, float *scales, int32_t *qsum, uint8_t *workspace);
-int launch_qwen_swiglu_quant(gx_ctx *ctx, const float *gu, int ldgu, int M, int ffn, int8_t *q, float *scales,
-                             int32_t *qsum);
+int launch_qwen_swiglu_quant(gx_ctx *ctx, const float *gu, int ldgu, int M, int ffn, int group, int8_t *q,
+                             float *scales, int32_t *qsum);
 int launch_argmax(gx_ctx *ctx, const float *x, int ldx, int M, int n, int32_t *out);
 int launch_f32_matvec(gx_ctx *ctx, const gx_weight *w, const float *x, int ldx, int M, int row_start, int row_end,
                       float *y, int ldy);

@@ -157,6 +157,196 @@ int launch_nc(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, const int8_t 
     return check_launch("q4_0_matvec");
 }
 
+
+// One position (M = 1) whose activation is produced by the product itself:
+// x (+ add) -> RMSNormPlain(gain, eps) -> Q8_0, a block's pre-norm
+// (qwen/block.go:45-52, 59-68), so that the norm needs no kernel of its own.
+// Every workgroup stages x + add in LDS and computes the norm's float64 sum
+// of squares with the same 512-partial tree as the separate norm kernel;
+// workgroup 0 writes x + add to x_out.  Each wavefront quantises the 256
+// values of the stretch it multiplies (four a lane, a Q8_0 block per eight
+// lanes) and moves them to SGPRs with readlane, which is where the plain
+// kernel's activation sits.  The values, and so the products, are the
+// separate kernels' bit for bit.
+//   EPI 0: y[row] for rows [row_start, row_end).
+//   EPI 1: the rows are gate and up interleaved by 32 (tile t holds gate rows
+//          32t .. 32t+31, then the same up rows): the tile's 32 outputs
+//          silu(gate) * up (SwiGLURange, nn/swiglu.go:77-82) go straight to
+//          their Q8_0 block t in q/scales/qsum, the down projection's input.
+constexpr int kFusedRegs = 8;  // staged values per thread: K <= 8 * threads
+
+// DB: two stretch slots a wavefront (double-buffered); without it a
+// wavefront has one slot and half the registers, so that two workgroups fit
+// a CU.
+template <int EPI, bool DB>
+__global__ __launch_bounds__(1024) void q4_0_matvec_fused_kernel(
+    const uint8_t *__restrict__ W, size_t plane0_bytes, int B, int DC, int K, int tile0, int row_start, int row_end,
+    float *__restrict__ y, const float *__restrict__ x, const float *__restrict__ add,
+    const float *__restrict__ gain, float eps, float *__restrict__ x_out, int8_t *__restrict__ q,
+    float *__restrict__ scales, int32_t *__restrict__ qsum) {
+    extern __shared__ __align__(16) float lds[];  // part [S][64], then xs [K]
+    __shared__ double red[512];
+    __shared__ float scale_sh;
+    const int S = (B + kStretch - 1) / kStretch;
+    float *part = lds;
+    float *xs = lds + S * kTileRows;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nwaves = blockDim.x >> 6;
+    const int tile = tile0 + blockIdx.x;
+    const uint8_t *qs_row = W + ((size_t)tile * B * kTileRows + lane) * kChunk;
+    const uint8_t *d_row = W + plane0_bytes + ((size_t)tile * DC * kTileRows + lane) * kChunk;
+
+    // x (+ add) into registers first, then the weights of the wavefront's
+    // first two stretch slots, so that the staging waits only for x and add.
+    float xv[kFusedRegs];
+#pragma unroll
+    for (int r = 0; r < kFusedRegs; r++) {
+        const int i = min(tid + r * (int)blockDim.x, K - 1);
+        xv[r] = add ? x[i] + add[i] : x[i];
+    }
+    // A wavefront's slot k is stretch wave + k*nwaves; every wavefront runs
+    // the same number of slots (a slot past S loads stretch S - 1 again and
+    // computes nothing), two register sets, a slot's loads issued a slot
+    // ahead under one uniform condition, so the wait counts stay exact.
+    const int slots = DB ? (S + nwaves - 1) / nwaves : 1;
+    uint4 wa[kStretch], wb[DB ? kStretch : 1], da, db;
+    float4 ga, gb;
+#define GX_FU_LOAD(wq, dch, gq, st)                                                                                  \
+    do {                                                                                                             \
+        const int sc_ = min((st), S - 1);                                                                            \
+        _Pragma("unroll") for (int j = 0; j < kStretch; j++)                                                         \
+            wq[j] = load_stream(qs_row + (size_t)min(sc_ * kStretch + j, B - 1) * kTileRows * kChunk);               \
+        dch = *(const uint4 *)(d_row + (size_t)sc_ * kTileRows * kChunk);                                            \
+        gq = *(const float4 *)(gain + min(sc_ * kStretch * kQ4Block + 4 * lane, K - 4));                             \
+    } while (0)
+    GX_FU_LOAD(wa, da, ga, wave);
+    if (DB && slots > 1)
+        GX_FU_LOAD(wb, db, gb, wave + nwaves);
+#pragma unroll
+    for (int r = 0; r < kFusedRegs; r++) {
+        const int i = tid + r * (int)blockDim.x;
+        if (i < K) {
+            xs[i] = xv[r];
+            if (blockIdx.x == 0 && x_out)
+                x_out[i] = xv[r];
+        }
+    }
+    __syncthreads();
+    // RMSNormPlain's sum: partial t = elements t, t + 512, ... in order, then
+    // halved pairwise, exactly as the separate norm kernel.
+    for (int pt = tid; pt < 512; pt += blockDim.x) {
+        double acc = 0.0;
+        for (int i = pt; i < K; i += 512) {
+            const float v = xs[i];
+            const float sq = v * v;
+            acc += (double)sq;
+        }
+        red[pt] = acc;
+    }
+    __syncthreads();
+    for (int w = 256; w >= 64; w >>= 1) {
+        for (int i = tid; i < w; i += blockDim.x)
+            red[i] = red[i] + red[i + w];
+        __syncthreads();
+    }
+    if (tid < 64) {
+        double t = red[tid];
+        for (int w = 32; w > 0; w >>= 1) {
+            const double o = __shfl_down(t, w, 64);
+            if (tid < w)
+                t = t + o;
+        }
+        if (tid == 0)
+            scale_sh = norm_scale(t, K, eps);
+    }
+    __syncthreads();
+    const float sc = scale_sh;
+
+    // The stretch's activation (values b0*32 + 4*lane .. + 3), its Q8_0 in
+    // SGPRs, and the product of the 64 rows with it.
+#define GX_FU_STRETCH(wq, dch, gq, st)                                                                               \
+    do {                                                                                                             \
+        const int b0 = (st) * kStretch;                                                                              \
+        const int nb = min(kStretch, B - b0);                                                                        \
+        const float4 xq = *(const float4 *)(xs + min(b0 * kQ4Block + 4 * lane, K - 4));                              \
+        const float xa[4] = {xq.x, xq.y, xq.z, xq.w}, gg[4] = {gq.x, gq.y, gq.z, gq.w};                              \
+        float v[4];                                                                                                  \
+        _Pragma("unroll") for (int k = 0; k < 4; k++) {                                                              \
+            const float nv = xa[k] * sc;                                                                             \
+            v[k] = nv * gg[k];                                                                                       \
+        }                                                                                                            \
+        float bstored;                                                                                               \
+        int32_t bsum;                                                                                                \
+        const uint32_t aq = q8_0_quad(v, &bstored, &bsum);                                                           \
+        float p = 0.0f;                                                                                              \
+        _Pragma("unroll") for (int j = 0; j < kStretch; j++) {                                                       \
+            if (j < nb) {                                                                                            \
+                int4 a0, a1;                                                                                         \
+                a0.x = __builtin_amdgcn_readlane((int)aq, 8 * j + 0);                                                \
+                a0.y = __builtin_amdgcn_readlane((int)aq, 8 * j + 1);                                                \
+                a0.z = __builtin_amdgcn_readlane((int)aq, 8 * j + 2);                                                \
+                a0.w = __builtin_amdgcn_readlane((int)aq, 8 * j + 3);                                                \
+                a1.x = __builtin_amdgcn_readlane((int)aq, 8 * j + 4);                                                \
+                a1.y = __builtin_amdgcn_readlane((int)aq, 8 * j + 5);                                                \
+                a1.z = __builtin_amdgcn_readlane((int)aq, 8 * j + 6);                                                \
+                a1.w = __builtin_amdgcn_readlane((int)aq, 8 * j + 7);                                                \
+                const int32_t qs = __builtin_amdgcn_readlane(bsum, 8 * j);                                           \
+                const float sa = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bstored), 8 * j));          \
+                const int32_t isum = q4_0_block_isum(wq[j], a0, a1, qs);                                             \
+                const float scl = chunk_half(dch, j) * sa;                                                           \
+                p = fmaf((float)isum, scl, p);                                                                       \
+            }                                                                                                        \
+        }                                                                                                            \
+        part[(st) * kTileRows + lane] = p;                                                                           \
+    } while (0)
+    if (DB) {
+        for (int k = 0; k < slots; k += 2) {
+            const int s = wave + k * nwaves;
+            if (s < S)
+                GX_FU_STRETCH(wa, da, ga, s);
+            if (k + 2 < slots)
+                GX_FU_LOAD(wa, da, ga, s + 2 * nwaves);
+            if (k + 1 < slots && s + nwaves < S)
+                GX_FU_STRETCH(wb, db, gb, s + nwaves);
+            if (k + 3 < slots)
+                GX_FU_LOAD(wb, db, gb, s + 3 * nwaves);
+        }
+    } else if (wave < S) {
+        GX_FU_STRETCH(wa, da, ga, wave);
+    }
+#undef GX_FU_STRETCH
+#undef GX_FU_LOAD
+    __syncthreads();
+    const int row = tile * kTileRows + lane;
+    if (wave == 0) {
+        float acc = 0.0f;
+        for (int s = 0; s < S; s++)
+            acc = acc + part[s * kTileRows + lane];
+        if (EPI == 0) {
+            if (row >= row_start && row < row_end)
+                y[row] = acc;
+        } else {
+            // lane l < 32: gate 32*tile + l; lane l + 32: its up
+            const float u = __shfl_down(acc, 32, 64);
+            const float g = acc;
+            const float ex = ggml_expf(-g);
+            const float den = 1.0f + ex;
+            const float sl = g / den;
+            const float v = sl * u;
+            float stored;
+            int32_t sm;
+            const int32_t nq = q8_0_lane(v, &stored, &sm);
+            if (lane < 32) {
+                q[(size_t)tile * 32 + lane] = (int8_t)nq;
+                if (lane == 0) {
+                    scales[tile] = stored;
+                    qsum[tile] = sm;
+                }
+            }
+        }
+    }
+}
 }  // namespace
 
 int launch_q4_0_matvec(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, const int8_t *q, const float *scales,
@@ -208,6 +398,34 @@ int launch_q4_0_matvec_units(gx_ctx *ctx, const gx_weight *w, const int32_t *uni
         w->dev, w->plane0_bytes, B, w->dchunks, q, scales, qsum, w->cols, 0, 0, w->rows, nullptr, y, ldy,
         unit_expert, w->matrix_bytes, act_div, w->count);
     return check_launch("q4_0_matvec_units");
+}
+
+int launch_q4_0_matvec_fused(gx_ctx *ctx, const gx_weight *w, int epi, int row_start, int row_end, float *y,
+                              const float *x, const float *add, const float *gain, float eps, float *x_out,
+                              int8_t *q, float *scales, int32_t *qsum) {
+    const int B = w->blocks, K = w->cols;
+    const int S = (B + kStretch - 1) / kStretch;
+    const int waves = min(S, 16);
+    GX_CHECK(K <= kFusedRegs * 64 * waves, "gx: a %d-input row is too wide for the fused norm", K);
+    const size_t lds = ((size_t)S * kTileRows + K) * sizeof(float);
+    GX_CHECK(lds <= 56 * 1024, "gx: a %d-input Q4_0 row is wider than this kernel's LDS", K);
+    const int tile0 = row_start / kTileRows;
+    const int grid = (row_end + kTileRows - 1) / kTileRows - tile0;
+#define GX_FUSED(E, D)                                                                                               \
+    q4_0_matvec_fused_kernel<E, D><<<grid, 64 * waves, lds, ctx->stream>>>(                                          \
+        w->dev, w->plane0_bytes, B, w->dchunks, K, tile0, row_start, row_end, y, x, add, gain, eps, x_out, q, scales, \
+        qsum)
+    const bool db = S > waves;
+    if (epi == 0 && !db)
+        GX_FUSED(0, false);
+    else if (epi == 0)
+        GX_FUSED(0, true);
+    else if (!db)
+        GX_FUSED(1, false);
+    else
+        GX_FUSED(1, true);
+#undef GX_FUSED
+    return check_launch("q4_0_matvec_fused");
 }
 
 int launch_q4_0_block_dots_matvec(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const int32_t *qsum, int M,

@@ -691,39 +691,23 @@ __global__ __launch_bounds__(kDecodeThreads) void attn_decode_kernel(
     }
 }
 
-// expf (ggml_v_expf one value at a time), nn/swiglu.go:31-74.
-__device__ __forceinline__ float ggml_expf(float x) {
-    const float shift = 0x1.8p23f;
-    const float log2e = 0x1.715476p+0f;
-    const float ln2hi = 0x1.62e4p-1f;
-    const float ln2lo = 0x1.7f7d1cp-20f;
-    const float c0 = 0x1.ffffecp-1f;
-    const float c1 = 0x1.fffdb6p-2f;
-    const float c2 = 0x1.555e66p-3f;
-    const float c3 = 0x1.573e2ep-5f;
-    const float c4 = 0x1.0e4020p-7f;
-    const float z = x * log2e + shift;
-    const float n = z - shift;
-    if (n > 126.0f || n < -126.0f)
-        return (float)exp((double)x);
-    const float b = x - n * ln2hi - n * ln2lo;
-    const float k = __uint_as_float((__float_as_uint(z) << 23) + __float_as_uint(1.0f));
-    const float u = b * b;
-    const float j = ((c4 * b + c3) * u + (c2 * b + c1)) * u + c0 * b;
-    return j * k + k;
-}
 
 // grid (ceil(ffn/256), M): gu [M][ldgu] holds each position's gate then up
-// (ffn each).  mid = silu(gate) * up (SwiGLURange, nn/swiglu.go:77-82), Q8_0.
+// (ffn each), or gates and ups interleaved by 32 (group 32).  mid =
+// silu(gate) * up (SwiGLURange, nn/swiglu.go:77-82), Q8_0.
 __global__ __launch_bounds__(256) void qwen_swiglu_quant_kernel(const float *__restrict__ gu, int ldgu, int ffn,
-                                                                int8_t *__restrict__ q, float *__restrict__ scales,
+                                                                int group, int8_t *__restrict__ q,
+                                                                float *__restrict__ scales,
                                                                 int32_t *__restrict__ qsum) {
     const int t = blockIdx.y;
     const int i = blockIdx.x * 256 + threadIdx.x;
     if (i >= ffn)
         return;  // ffn % 32 == 0: whole groups
-    const float g = gu[(size_t)t * ldgu + i];
-    const float u = gu[(size_t)t * ldgu + ffn + i];
+    // group 0: gate [ffn] then up [ffn]; group 32: 32 gates then their 32 ups
+    const size_t gi = group ? (size_t)(i >> 5) * 64 + (i & 31) : (size_t)i;
+    const size_t ui = group ? gi + 32 : (size_t)ffn + i;
+    const float g = gu[(size_t)t * ldgu + gi];
+    const float u = gu[(size_t)t * ldgu + ui];
     const float e = ggml_expf(-g);
     const float den = 1.0f + e;
     const float sl = g / den;
@@ -905,10 +889,10 @@ int launch_qwen_attention(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int
     return check_launch("qwen_attention values");
 }
 
-int launch_qwen_swiglu_quant(gx_ctx *ctx, const float *gu, int ldgu, int M, int ffn, int8_t *q, float *scales,
-                             int32_t *qsum) {
+int launch_qwen_swiglu_quant(gx_ctx *ctx, const float *gu, int ldgu, int M, int ffn, int group, int8_t *q,
+                             float *scales, int32_t *qsum) {
     qwen_swiglu_quant_kernel<<<dim3((unsigned)((ffn + 255) / 256), (unsigned)M), 256, 0, ctx->stream>>>(
-        gu, ldgu, ffn, q, scales, qsum);
+        gu, ldgu, ffn, group, q, scales, qsum);
     return check_launch("qwen_swiglu_quant");
 }
 

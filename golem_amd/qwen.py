@@ -10,7 +10,7 @@ the embedding rows (TokenEmbd.Row, a Q6_K dequantisation), then per block
     gx_qwen_attention  scores, softmax, values; Q8_0 of the heads
     gx_matmul_q4_0     O
     gx_norm_quant      x += attention; RMSNormPlain(ffn_norm); Q8_0
-    gx_matmul_q4_0     Gate and Up, stacked by rows
+    gx_matmul_q4_0     Gate and Up, stacked with rows interleaved by 32
     gx_swiglu_quant    silu(gate) * up; Q8_0
     gx_matmul_q4_0     Down
 
@@ -18,6 +18,11 @@ and the final norm (the last block's residual folded in).  Logits
 (qwen/model.go:181-194) is QuantizeK plus the tied Q6_K head; greedy picks the
 largest logit, the lower id on ties.  Stacking Q/K/V and Gate/Up changes no
 result: every output row is its own product.
+
+One position (a decode step) takes fewer launches: each pre-norm runs inside
+the product after it (gx_norm_matmul_q4_0 for Q|K|V), and the FFN's norm,
+Gate|Up product, SwiGLU and Q8_0 are one kernel (gx_norm_swiglu_q4_0), the
+same values bit for bit.
 
 Every kernel treats a position on its own, so a prompt read in one batch
 gives, bit for bit, what the same tokens give one at a time (golem's
@@ -55,6 +60,16 @@ def rope_tables(dims, context, base):
     return cos, sin
 
 
+def interleave_rows(gate, up, rows, cols):
+    """Gate and Up (Q4_0, rows x cols each) stacked into one matrix with
+    their rows interleaved by 32: 32 gate rows, the same 32 up rows, and so
+    on.  A 64-row tile then holds both halves of 32 SwiGLU outputs."""
+    rb = cols // 32 * 18
+    g = np.asarray(gate, np.uint8).reshape(rows // 32, 32 * rb)
+    u = np.asarray(up, np.uint8).reshape(rows // 32, 32 * rb)
+    return np.ascontiguousarray(np.concatenate([g, u], axis=1)).reshape(-1)
+
+
 class _Q8:
     """A Q8_0 batch on the device: q [M][K], scales and qsum [M][K/32]."""
 
@@ -79,7 +94,8 @@ class QwenModel:
             self.blocks.append({
                 "qkv": capi.Weight(ctx, np.concatenate([b["q"], b["k"], b["v"]]), capi.Q4_0, qd + 2 * kvd, cfg.dim),
                 "o": capi.Weight(ctx, b["o"], capi.Q4_0, cfg.dim, qd),
-                "gu": capi.Weight(ctx, np.concatenate([b["gate"], b["up"]]), capi.Q4_0, 2 * cfg.ffn, cfg.dim),
+                "gu": capi.Weight(ctx, interleave_rows(b["gate"], b["up"], cfg.ffn, cfg.dim), capi.Q4_0,
+                                  2 * cfg.ffn, cfg.dim),
                 "down": capi.Weight(ctx, b["down"], capi.Q4_0, cfg.dim, cfg.ffn),
                 "attn_norm": dev(b["attn_norm"]), "ffn_norm": dev(b["ffn_norm"]),
                 "q_norm": dev(b["q_norm"]), "k_norm": dev(b["k_norm"]),
@@ -98,6 +114,7 @@ class QwenModel:
 
         M = max_batch
         self.xs = torch.empty((M, cfg.dim), dtype=torch.float32, device="cuda")
+        self.xs2 = torch.empty((1, cfg.dim), dtype=torch.float32, device="cuda")  # the fused steps' other residual
         self.x8 = _Q8(M, cfg.dim)
         self.qkv = torch.empty((M, qd + 2 * kvd), dtype=torch.float32, device="cuda")
         self.qh = torch.empty((M, qd), dtype=torch.int16, device="cuda")
@@ -153,6 +170,8 @@ class QwenModel:
         and positions already in self.tokens / self.positions."""
         cfg, vp, call, ctx = self.cfg, self._vp, self._call, self.ctx.ptr
         call("gx_weight_rows", ctx, self.embd.ptr, 0, vp(self.tokens), M, vp(self.xs))
+        if M == 1:
+            return self._blocks_one(max_pos)
         qd, kvd = self.qd, self.kvd
         for i, b in enumerate(self.blocks):
             add = None if i == 0 else vp(self.ffn)
@@ -169,11 +188,42 @@ class QwenModel:
             call("gx_norm_quant", ctx, vp(self.xs), cfg.dim, vp(self.attn), cfg.dim, vp(b["ffn_norm"]), M, cfg.dim,
                  np.float32(cfg.eps), None, 0, vp(self.x8.q), vp(self.x8.s), vp(self.x8.qs))
             self._mm(b["gu"], self.x8, M, self.gu, 2 * cfg.ffn)
-            call("gx_swiglu_quant", ctx, vp(self.gu), 2 * cfg.ffn, M, cfg.ffn, vp(self.mid8.q), vp(self.mid8.s),
-                 vp(self.mid8.qs))
+            call("gx_swiglu_quant", ctx, vp(self.gu), 2 * cfg.ffn, M, cfg.ffn, 32, vp(self.mid8.q),
+                 vp(self.mid8.s), vp(self.mid8.qs))
             self._mm(b["down"], self.mid8, M, self.ffn, cfg.dim)
         call("gx_norm_quant", ctx, vp(self.xs), cfg.dim, vp(self.ffn), cfg.dim, vp(self.output_norm), M, cfg.dim,
              np.float32(cfg.eps), vp(self.hidden), cfg.dim, None, None, None)
+
+    def _blocks_one(self, max_pos):
+        """The blocks for one position, with each pre-norm fused into the
+        product after it, and the SwiGLU with its Q8_0 into the Gate/Up
+        product (the same values bit for bit).  The residual moves between two buffers, since a
+        fused product's workgroups all read it while one writes x + add."""
+        cfg, vp, call, ctx = self.cfg, self._vp, self._call, self.ctx.ptr
+        qd, kvd = self.qd, self.kvd
+        eps = np.float32(cfg.eps)
+        cur, other = self.xs, self.xs2
+        for i, b in enumerate(self.blocks):
+            if i == 0:
+                call("gx_norm_matmul_q4_0", ctx, b["qkv"].ptr, vp(cur), None, vp(b["attn_norm"]), eps, None, 0,
+                     b["qkv"].rows, vp(self.qkv))
+            else:
+                call("gx_norm_matmul_q4_0", ctx, b["qkv"].ptr, vp(cur), vp(self.ffn), vp(b["attn_norm"]), eps,
+                     vp(other), 0, b["qkv"].rows, vp(self.qkv))
+                cur, other = other, cur
+            call("gx_qwen_qk_rope", ctx, vp(self.qkv), qd + 2 * kvd, 1, cfg.heads, cfg.kv_heads, cfg.head_dim,
+                 vp(self.positions), vp(b["q_norm"]), vp(b["k_norm"]), vp(self.rope_cos), vp(self.rope_sin),
+                 eps, vp(self.qh), vp(self.kc[i]), vp(self.vc[i]), self.context)
+            call("gx_qwen_attention", ctx, vp(self.qh), 1, cfg.heads, cfg.kv_heads, cfg.head_dim,
+                 max_pos, vp(self.positions), vp(self.kc[i]), vp(self.vc[i]), self.context,
+                 vp(self.set8.q), vp(self.set8.s), vp(self.set8.qs), vp(self.attn_ws), self.attn_ws.numel())
+            self._mm(b["o"], self.set8, 1, self.attn, cfg.dim)
+            call("gx_norm_swiglu_q4_0", ctx, b["gu"].ptr, vp(cur), vp(self.attn), vp(b["ffn_norm"]), eps,
+                 vp(other), vp(self.mid8.q), vp(self.mid8.s), vp(self.mid8.qs))
+            cur, other = other, cur
+            self._mm(b["down"], self.mid8, 1, self.ffn, cfg.dim)
+        call("gx_norm_quant", ctx, vp(cur), cfg.dim, vp(self.ffn), cfg.dim, vp(self.output_norm), 1, cfg.dim,
+             eps, vp(self.hidden), cfg.dim, None, None, None)
 
     def _decode_step(self):
         """One greedy step read entirely from the device: token self.tokens[0]

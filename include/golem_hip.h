@@ -271,10 +271,33 @@ int gx_qwen_attention(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int kv_
                       const int32_t *positions, const uint16_t *kcache, const uint16_t *vcache, int context,
                       int8_t *q, float *scales, int32_t *qsum, void *workspace, size_t workspace_bytes);
 
+/* One position's RMSNormPlain + Q8_0 fused into the Q4_0 product that reads
+ * it (M = 1): y[row] for rows [row_start, row_end) of w times
+ * Q8_0(RMSNormPlain(x + add, gain, eps)), bit for bit gx_norm_quant followed
+ * by gx_matmul_q4_0 (qwen/block.go:45-56, 59-72: a block's pre-norm and the
+ * projection after it).  add may be NULL; x_out, when given, receives x + add
+ * (the residual) and must not alias x or add.  x, add, gain (16-byte
+ * aligned), x_out: device floats [w->cols]; y: device floats [w->rows]. */
+int gx_norm_matmul_q4_0(gx_ctx *ctx, const gx_weight *w, const float *x, const float *add, const float *gain,
+                        float eps, float *x_out, int row_start, int row_end, float *y);
+
+/* The FFN's first half for one position (M = 1), fused: RMSNormPlain + Q8_0
+ * of x + add as gx_norm_matmul_q4_0, the Gate and Up products of w, whose
+ * rows are gate and up interleaved by 32 (rows 64k .. 64k+31 are gate rows
+ * 32k .. 32k+31, the next 32 the same up rows), and silu(gate) * up with its
+ * Q8_0 into q/scales/qsum [w->rows / 2] -- bit for bit gx_norm_quant,
+ * gx_matmul_q4_0 and gx_swiglu_quant (group 32) (qwen/block.go:59-90,
+ * nn/swiglu.go:77-82). */
+int gx_norm_swiglu_q4_0(gx_ctx *ctx, const gx_weight *w, const float *x, const float *add, const float *gain,
+                        float eps, float *x_out, int8_t *q, float *scales, int32_t *qsum);
+
 /* SwiGLURange (nn/swiglu.go:77-82) and the Q8_0 of the result: gu[m] holds
- * position m's gate (ffn floats) then up (ffn floats); q/scales/qsum receive
- * Q8_0(silu(gate) * up) [M][ffn].  ffn a multiple of 32. */
-int gx_swiglu_quant(gx_ctx *ctx, const float *gu, int ldgu, int M, int ffn, int8_t *q, float *scales, int32_t *qsum);
+ * position m's gate (ffn floats) then up (ffn floats) when group is 0, or
+ * gates and ups interleaved by 32 (32 gates, then their 32 ups, ...) when
+ * group is 32; q/scales/qsum receive Q8_0(silu(gate) * up) [M][ffn].  ffn a
+ * multiple of 32. */
+int gx_swiglu_quant(gx_ctx *ctx, const float *gu, int ldgu, int M, int ffn, int group, int8_t *q, float *scales,
+                    int32_t *qsum);
 
 /* Greedy choice: ids[m] = the index of the largest of x[m][0..n), the lower
  * index on ties (qwen/model_test.go:118-126). */

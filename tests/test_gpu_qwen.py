@@ -139,7 +139,7 @@ def test_bad_shapes_are_refused(dev):
     with pytest.raises(ValueError):
         model.forward([1, 2], cfg.max_context - 1)  # past the context
     with pytest.raises(capi.GxError):
-        capi.call("gx_swiglu_quant", dev.ctx.ptr, capi.vp(model.gu), 2 * cfg.ffn, 1, 100, capi.vp(model.mid8.q),
+        capi.call("gx_swiglu_quant", dev.ctx.ptr, capi.vp(model.gu), 2 * cfg.ffn, 1, 100, 0, capi.vp(model.mid8.q),
                   capi.vp(model.mid8.s), capi.vp(model.mid8.qs))  # 100 is not a multiple of 32
     model.free()
 
@@ -282,6 +282,103 @@ def test_attention_refuses_bad_caches(dev):
         capi.call("gx_qwen_attention", dev.ctx.ptr, *args, 16, *outs, n - 256)
 
 
+@pytest.mark.parametrize("rows,K,span", [(6144, 2560, None), (19456, 2560, None), (200, 2080, (3, 131)),
+                                         (64, 256, None), (192, 4608, None), (130, 8192, (0, 130))])
+@pytest.mark.parametrize("with_add", [True, False])
+def test_norm_fused_product_bit_exact(dev, rows, K, span, with_add):
+    """gx_norm_matmul_q4_0 against gx_norm_quant then gx_matmul_q4_0: the
+    product, and x + add written to x_out, bit for bit (K = 2080 ends on a
+    one-block stretch; K = 256 is a workgroup of one wavefront; K = 4608 and
+    8192 give a wavefront two stretches or more)."""
+    g = synth.rng(70 + K + rows)
+    w = synth.q4_0_weights(g, rows, K)
+    wd = dev.weight(w, capi.Q4_0, rows, K)
+    x = (g.standard_normal(K) * 3).astype(np.float32)
+    add = g.standard_normal(K).astype(np.float32)
+    gain = (1 + 0.02 * g.standard_normal(K)).astype(np.float32)
+    start, end = span or (0, rows)
+    xd, ad, gd = dev.put(x[None]), dev.put(add[None]), dev.put(gain)
+    xo = dev.empty((1, K), np.float32)
+    y = dev.full((1, rows), float("nan"))
+    capi.call("gx_norm_matmul_q4_0", dev.ctx.ptr, wd.ptr, capi.vp(xd), capi.vp(ad) if with_add else None,
+              capi.vp(gd), np.float32(1e-6), capi.vp(xo) if with_add else None, start, end, capi.vp(y))
+    # the separate kernels on a copy
+    xr = dev.put(x[None])
+    q = dev.empty((1, K), np.int8)
+    sc = dev.empty((1, K // 32), np.float32)
+    qs = dev.empty((1, K // 32), np.int32)
+    capi.call("gx_norm_quant", dev.ctx.ptr, capi.vp(xr), K, capi.vp(ad) if with_add else None, K, capi.vp(gd), 1, K,
+              np.float32(1e-6), None, 0, capi.vp(q), capi.vp(sc), capi.vp(qs))
+    want = dev.full((1, rows), float("nan"))
+    capi.call("gx_matmul_q4_0", dev.ctx.ptr, wd.ptr, capi.vp(q), capi.vp(sc), capi.vp(qs), None, 1, start, end,
+              None, capi.vp(want), rows)
+    np.testing.assert_array_equal(dev.get(y).view(np.uint32), dev.get(want).view(np.uint32))
+    if with_add:
+        np.testing.assert_array_equal(dev.get(xo).view(np.uint32), dev.get(xr).view(np.uint32))
+    np.testing.assert_array_equal(dev.get(xd).view(np.uint32), x[None].view(np.uint32))  # x itself untouched
+    wd.free()
+
+
+@pytest.mark.parametrize("ffn,K", [(9728, 2560), (1056, 2080), (32, 256), (96, 4608)])
+def test_norm_swiglu_fused_bit_exact(dev, ffn, K):
+    """gx_norm_swiglu_q4_0 on gate and up interleaved by 32, against
+    gx_norm_quant, gx_matmul_q4_0 of the plainly stacked [gate; up] and
+    gx_swiglu_quant (group 0); and gx_swiglu_quant (group 32) on the
+    interleaved product's floats gives the same Q8_0."""
+    from golem_amd.qwen import interleave_rows
+    g = synth.rng(90 + ffn)
+    gate = synth.q4_0_weights(g, ffn, K)
+    up = synth.q4_0_weights(g, ffn, K)
+    stacked = dev.weight(np.concatenate([gate, up]), capi.Q4_0, 2 * ffn, K)
+    inter = dev.weight(interleave_rows(gate, up, ffn, K), capi.Q4_0, 2 * ffn, K)
+    x = (g.standard_normal((1, K)) * 3).astype(np.float32)
+    add = g.standard_normal((1, K)).astype(np.float32)
+    gain = (1 + 0.02 * g.standard_normal(K)).astype(np.float32)
+    xd, ad, gd = dev.put(x), dev.put(add), dev.put(gain)
+    xo = dev.empty((1, K), np.float32)
+    q = dev.empty((1, ffn), np.int8)
+    sc = dev.empty((1, ffn // 32), np.float32)
+    qs = dev.empty((1, ffn // 32), np.int32)
+    capi.call("gx_norm_swiglu_q4_0", dev.ctx.ptr, inter.ptr, capi.vp(xd), capi.vp(ad), capi.vp(gd), np.float32(1e-6),
+              capi.vp(xo), capi.vp(q), capi.vp(sc), capi.vp(qs))
+    # separately
+    xr = dev.put(x)
+    aq = dev.empty((1, K), np.int8)
+    asc = dev.empty((1, K // 32), np.float32)
+    aqs = dev.empty((1, K // 32), np.int32)
+    capi.call("gx_norm_quant", dev.ctx.ptr, capi.vp(xr), K, capi.vp(ad), K, capi.vp(gd), 1, K, np.float32(1e-6),
+              None, 0, capi.vp(aq), capi.vp(asc), capi.vp(aqs))
+    outs = []
+    for w, group in ((stacked, 0), (inter, 32)):
+        gu = dev.empty((1, 2 * ffn), np.float32)
+        capi.call("gx_matmul_q4_0", dev.ctx.ptr, w.ptr, capi.vp(aq), capi.vp(asc), capi.vp(aqs), None, 1, 0,
+                  2 * ffn, None, capi.vp(gu), 2 * ffn)
+        q2 = dev.empty((1, ffn), np.int8)
+        sc2 = dev.empty((1, ffn // 32), np.float32)
+        qs2 = dev.empty((1, ffn // 32), np.int32)
+        capi.call("gx_swiglu_quant", dev.ctx.ptr, capi.vp(gu), 2 * ffn, 1, ffn, group, capi.vp(q2), capi.vp(sc2),
+                  capi.vp(qs2))
+        outs.append((q2, sc2, qs2))
+    for q2, sc2, qs2 in outs:
+        np.testing.assert_array_equal(dev.get(q), dev.get(q2))
+        np.testing.assert_array_equal(dev.get(sc).view(np.uint32), dev.get(sc2).view(np.uint32))
+        np.testing.assert_array_equal(dev.get(qs), dev.get(qs2))
+    np.testing.assert_array_equal(dev.get(xo).view(np.uint32), dev.get(xr).view(np.uint32))
+    stacked.free()
+    inter.free()
+
+
+def test_fused_products_refuse_aliasing(dev):
+    K, rows = 256, 64
+    wd = dev.weight(synth.q4_0_weights(synth.rng(1), rows, K), capi.Q4_0, rows, K)
+    x = dev.full((1, K), 1.0)
+    y = dev.empty((1, rows), np.float32)
+    with pytest.raises(capi.GxError):
+        capi.call("gx_norm_matmul_q4_0", dev.ctx.ptr, wd.ptr, capi.vp(x), None, capi.vp(x), np.float32(1e-6),
+                  capi.vp(x), 0, rows, capi.vp(y))
+    wd.free()
+
+
 def test_swiglu_quant_bit_exact(dev, orc):
     g = synth.rng(64)
     M, ffn = 3, 9728
@@ -291,7 +388,7 @@ def test_swiglu_quant_bit_exact(dev, orc):
     sc = dev.empty((M, ffn // 32), np.float32)
     qs = dev.empty((M, ffn // 32), np.int32)
     gud = dev.put(gu)
-    capi.call("gx_swiglu_quant", dev.ctx.ptr, capi.vp(gud), 2 * ffn, M, ffn, capi.vp(q8), capi.vp(sc),
+    capi.call("gx_swiglu_quant", dev.ctx.ptr, capi.vp(gud), 2 * ffn, M, ffn, 0, capi.vp(q8), capi.vp(sc),
               capi.vp(qs))
     lib = orc.load()
     mid = np.zeros((M, ffn), np.float32)
