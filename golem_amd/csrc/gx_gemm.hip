@@ -26,6 +26,8 @@
 // buffered: the next stretch's global loads are in flight while this one's
 // MFMAs run.  The weights' nibbles are widened to signed int8 (n - 8) in
 // registers as they are read.
+#include <type_traits>
+
 #include "gx_device.hpp"
 #include "gx_internal.hpp"
 
@@ -520,6 +522,258 @@ __global__ __launch_bounds__(64 * NWT) void q4_0_gemm_f16_kernel(
     }
 }
 
+
+// ---- the int8 product, loads straight into LDS -------------------------
+//
+// The default kernel for the Q4_0 x Q8_0 product (the one above serves the
+// DOTS and GROUPED forms).  Every stage's operands come in by direct
+// global-to-LDS loads (global_load_lds_dwordx4 / _dword): no registers stage
+// them, and three stages live in an LDS ring, two in flight while one is
+// multiplied.  A workgroup owns 128 rows (two R64 tiles) x 64 tokens; each of
+// its eight wavefronts one 32x32 MFMA tile (rows 32*(w&3), tokens
+// 32*(w>>2)), at four wavefronts per SIMD (two workgroups per CU).  Per stage
+// (4 blocks) each wavefront issues exactly three loads, so `s_waitcnt
+// vmcnt(3)` before the stage's barrier means "this stage has landed" for
+// every wavefront; the barrier is the bare s_barrier (the fence of
+// __syncthreads would wait for every load in flight).  Slot layout (bytes):
+//   [0, 8192)       nibbles  [block 4][row 128][16]
+//   [8192, 16384)   int8     [block 4][half 2][token 64][16]
+//   [16384, 17408)  act. scales (fp32) [block 4][token 64]
+//   [17408, 18432)  weight scales (fp16) [row 128][block 4]
+constexpr int kDmaTok = 64;
+constexpr int kDmaSlot = 18432;
+constexpr int kDmaRing = 3;
+// The integer products run on a biased chain.  The weights enter the MFMA as
+// 16 * (n - 8) (the nibble in a byte's high half, its top bit flipped), and
+// each block's MFMA adds its 16 * isum to the previous block's output; a
+// stretch's chain starts from the bits of 1.5 * 2^19.  Read as fp32, every
+// output is then 1.5 * 2^19 plus the stretch's running isum, exactly: the
+// ulp in [2^19, 2^20) is 1/16, and the running sum of a stretch is at most
+// 8 blocks * 32 * 8 * 128 = 2^18 in magnitude, whose two ends (bits
+// 0x49000000 and 0x49800000) are exactly 2^19 and 2^20.  The difference of
+// two consecutive outputs is the block's isum as an fp32 -- one full-rate
+// subtraction instead of a quarter-rate int->float conversion -- and feeds
+// golem's fma unchanged.
+constexpr int kChainBias = 0x49400000;  // 786432.0f
+typedef __attribute__((address_space(3))) void *lds_ptr;
+
+// One block's operands from LDS (nibbles, activations, weight scale,
+// activation scale), issued without a wait.  Written out so that the
+// compiler sees no LDS load: it would otherwise make each one wait for every
+// load-to-LDS in flight, the next stages' included.  The caller waits
+// (lgkmcnt) before it uses the four registers.
+template <int OW, int OA, int OD, int OS>
+__device__ __forceinline__ void lds_read_block(uint32_t aw, uint32_t aa, uint32_t ad, uint32_t as, v4u &rw, v4i &ra,
+                                               uint32_t &rdw, float &rda) {
+    asm volatile(
+        "ds_read_b128 %0, %4 offset:%8\n\t"
+        "ds_read_b128 %1, %5 offset:%9\n\t"
+        "ds_read_u16 %2, %6 offset:%10\n\t"
+        "ds_read_b32 %3, %7 offset:%11"
+        : "=&v"(rw), "=&v"(ra), "=&v"(rdw), "=&v"(rda)
+        : "v"(aw), "v"(aa), "v"(ad), "v"(as), "i"(OW), "i"(OA), "i"(OD), "i"(OS));
+}
+
+template <int J, int N, typename F>
+__device__ __forceinline__ void unroll(F &&f) {  // f(integral_constant<int, J>) for J in [J, N)
+    if constexpr (J < N) {
+        f(std::integral_constant<int, J>{});
+        unroll<J + 1, N>(f);
+    }
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {  // vmcnt <= N; expcnt, lgkmcnt unconstrained
+    static_assert(N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+__global__ __launch_bounds__(512, 4) void q4_0_gemm_dma_kernel(const uint8_t *__restrict__ W, size_t plane0_bytes,
+                                                            int B, int DC, const int8_t *__restrict__ q,
+                                                            const float *__restrict__ scales, int K, int M,
+                                                            int tiles, int tile0, int row_start, int row_end,
+                                                            const float *__restrict__ bias, float *__restrict__ y,
+                                                            int ldy) {
+    __shared__ __align__(16) uint8_t ring_lds[kDmaRing * kDmaSlot];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wv = tid >> 6;
+    const int T0 = tile0 + 2 * blockIdx.x;        // the workgroup's first R64 tile
+    const int rg = wv & 3, tg = wv >> 2;          // this wavefront's 32 rows and 32 tokens
+    const int li = lane & 31, g = lane >> 5;
+    const uint32_t sh = 4u * g;
+    // Stages, two to a stretch.  An odd count gets one more stage: the second
+    // half of the last stretch, all of whose blocks lie past the row, with
+    // weight scales 0 from the plane's padding.
+    const int Hp = ((B + kStage - 1) / kStage + 1) & ~1;
+    const int first = blockIdx.y * kDmaTok, count = min(kDmaTok, M - first);
+
+    // This lane's sources, fixed for the product.  Loads past the matrix, the
+    // batch or the second tile read in-bounds neighbours; their values are
+    // never used (weight scale 0, or not stored).
+    const int wj = wv & 3, wh = wv >> 2;          // nibble load: block wj, rows 64*wh + lane
+    const int wt = min(T0 + wh, tiles - 1);
+    const uint8_t *wsrc = W + ((size_t)wt * B * kTileRows + lane) * kChunk;
+    const int aj = wv >> 1, ag = wv & 1;          // activation load: block aj, half ag, token lane
+    const int8_t *asrc = q + (size_t)(first + min(lane, count - 1)) * K + 16 * ag;
+    // The third load is a dword for every wavefront: waves 0..3 an activation
+    // scale (block wv, token lane), waves 4..7 a pair of weight scales (row
+    // r = idx / 2 of the workgroup's 128, blocks 2 * (idx & 1) + {0, 1} of the
+    // stage, idx = 64 * (wv - 4) + lane), so that every wavefront issues the
+    // same three instructions.
+    const uint8_t *ssrc;
+    if (wv < 4) {
+        ssrc = (const uint8_t *)(scales + (size_t)(first + min(lane, count - 1)) * B);
+    } else {
+        const int idx = 64 * (wv - 4) + lane, r = idx >> 1;
+        const int dt = min(T0 + (r >> 6), tiles - 1);
+        ssrc = W + plane0_bytes + ((size_t)dt * DC * kTileRows + (r & 63)) * kChunk + 4 * (idx & 1);
+    }
+
+    auto ring = [&](auto slot_tag) -> uint8_t * { return ring_lds + decltype(slot_tag)::value * kDmaSlot; };
+    auto issue = [&](auto slot_tag, int h) {
+        h = min(h, Hp - 1);  // past the last stage: the last stage again, into the free slot
+        uint8_t *slot = ring(slot_tag);
+        const int b0 = h * kStage;
+        __builtin_amdgcn_global_load_lds(wsrc + (size_t)min(b0 + wj, B - 1) * kTileRows * kChunk,
+                                         (lds_ptr)(slot + (wj * 128 + 64 * wh) * 16), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(asrc + (size_t)min(b0 + aj, B - 1) * kQ4Block,
+                                         (lds_ptr)(slot + 8192 + wv * 1024), 16, 0, 0);
+        const size_t soff = wv < 4 ? (size_t)min(b0 + wv, B - 1) * 4
+                                   : (size_t)(b0 >> 3) * kTileRows * kChunk + 8 * ((b0 >> 2) & 1);
+        __builtin_amdgcn_global_load_lds(ssrc + soff, (lds_ptr)(slot + 16384 + wv * 256), 4, 0, 0);
+    };
+
+    v16f acc, tot;
+    v16i chain;
+#pragma unroll
+    for (int e = 0; e < 16; e++)
+        tot[e] = 0.0f;
+    const v16f zero_f = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    const uint32_t wsh = 4u * (1 - g);  // g = 0 takes the low nibbles: up into the byte's high half
+    // This lane's LDS read addresses in slot 0 (the slot and block go in the
+    // reads' immediate offsets).
+    const uint32_t lds_base = (uint32_t)(uintptr_t)(lds_ptr)ring_lds;
+    const uint32_t lds_w = lds_base + (32 * rg + li) * 16;
+    const uint32_t lds_a = lds_base + 8192 + (g * 64 + 32 * tg + li) * 16;
+    const uint32_t lds_dw = lds_base + 17408 + (32 * rg + li) * 8;
+    const uint32_t lds_da = lds_base + 16384 + (32 * tg + li) * 4;
+
+    // One stage: four blocks.  kFirst marks a stretch's first stage, whose
+    // first block starts the chain from the bias and the stretch sum from
+    // its product (x * s == fma(x, s, 0) but for the sign of a zero, which
+    // the total's 0 + P cannot show).
+    auto stage = [&](auto slot_tag, auto first_tag, int h) {
+        constexpr int kSlot = decltype(slot_tag)::value;
+        constexpr bool kFirst = decltype(first_tag)::value;
+        wait_vmcnt<3>();  // stage h has landed (stage h + 1 may be in flight)
+        __builtin_amdgcn_s_barrier();
+        // into the slot stage h - 1 used; every wavefront is past it
+        issue(std::integral_constant<int, (kSlot + 2) % kDmaRing>{}, h + 2);
+        constexpr int so = kSlot * kDmaSlot;
+        // The operands of block j + 1 are read while block j is multiplied.
+        v4u wq_n;
+        v4i Bv_n;
+        uint32_t dwh_n;
+        float da_n;
+        auto read = [&](auto j_tag) {
+            constexpr int j = decltype(j_tag)::value;
+            lds_read_block<so + j * 2048, so + j * 2048, so + 2 * j, so + j * 256>(lds_w, lds_a, lds_dw, lds_da, wq_n,
+                                                                                 Bv_n, dwh_n, da_n);
+        };
+        read(std::integral_constant<int, 0>{});
+        unroll<0, kStage>([&](auto j_tag) {
+            constexpr int j = decltype(j_tag)::value;
+            // the previous block's work stays above this block's wait
+            __builtin_amdgcn_sched_barrier(0);
+            // the reads land; the registers pass through the wait so that
+            // nothing touches them before it
+            asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(wq_n), "+v"(Bv_n), "+v"(dwh_n), "+v"(da_n));
+            const v4u wq = wq_n;
+            const v4i Bv = Bv_n;
+            const uint32_t dwh = dwh_n;
+            const float da = da_n;
+            if constexpr (j + 1 < kStage)
+                read(std::integral_constant<int, j + 1>{});
+            v4i A;
+            A.x = (int)(((wq.x << wsh) & 0xF0F0F0F0u) ^ 0x80808080u);
+            A.y = (int)(((wq.y << wsh) & 0xF0F0F0F0u) ^ 0x80808080u);
+            A.z = (int)(((wq.z << wsh) & 0xF0F0F0F0u) ^ 0x80808080u);
+            A.w = (int)(((wq.w << wsh) & 0xF0F0F0F0u) ^ 0x80808080u);
+            constexpr bool start = kFirst && j == 0;
+            v16i prev;
+            if constexpr (start) {
+                // written afresh each stretch (a resident copy would cost 16
+                // registers and the fourth wavefront per SIMD)
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    int bias;
+                    asm volatile("v_mov_b32 %0, %1" : "=v"(bias) : "i"(kChainBias));
+                    prev[e] = bias;
+                }
+            } else {
+                prev = chain;
+            }
+            const v16i next = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, Bv, prev, 0, 0, 0);
+            // a block past the row has weight scale 0 (the padding is zero):
+            // fma(x, 0, acc) == acc
+            const v16f S = __builtin_amdgcn_mfma_f32_32x32x8f16(k0_operand(dwh, g == 0),
+                                                                k0_operand(float_to_half_bits(da), g == 0),
+                                                                zero_f, 0, 0, 0);
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const int nb = next[e], pb = prev[e];
+                const float x = __int_as_float(nb) - __int_as_float(pb);  // the block's isum, exactly
+                acc[e] = start ? x * S[e] : fmaf(x, S[e], acc[e]);
+            }
+            chain = next;
+        });
+        // the stage's sums are complete here, not sunk past the next barrier
+#pragma unroll
+        for (int e = 0; e < 16; e++)
+            asm volatile("" : "+v"(acc[e]));
+    };
+
+    auto fold = [&]() {  // a stretch is two stages
+#pragma unroll
+        for (int e = 0; e < 16; e++)
+            tot[e] = tot[e] + acc[e];
+    };
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    using S2 = std::integral_constant<int, 2>;
+    issue(S0{}, 0);
+    issue(S1{}, 1);
+    for (int h = 0;; h += 6) {  // three stretches: the ring comes round to slot 0
+        stage(S0{}, std::true_type{}, h);
+        stage(S1{}, std::false_type{}, h + 1);
+        fold();
+        if (h + 2 >= Hp)
+            break;
+        stage(S2{}, std::true_type{}, h + 2);
+        stage(S0{}, std::false_type{}, h + 3);
+        fold();
+        if (h + 4 >= Hp)
+            break;
+        stage(S1{}, std::true_type{}, h + 4);
+        stage(S2{}, std::false_type{}, h + 5);
+        fold();
+        if (h + 6 >= Hp)
+            break;
+    }
+    wait_vmcnt<0>();  // the trailing loads land before the workgroup ends
+    const int t = 32 * tg + li;
+    if (t < count) {
+        float *yr = y + (size_t)(first + t) * ldy;
+        const int nb = T0 * kTileRows + 32 * rg;  // the wavefront's first row
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+            const int n = nb + 8 * (e >> 2) + 4 * g + (e & 3);
+            if (n >= row_start && n < row_end)
+                yr[n] = bias ? tot[e] + bias[n] : tot[e];
+        }
+    }
+}
+
 }  // namespace
 
 int launch_q4_0_gemm(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, const int8_t *q, const float *scales,
@@ -534,9 +788,9 @@ int launch_q4_0_gemm(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, const 
                                                                      scales, w->cols, M, tile0, row_start, row_end,
                                                                      bias, y, ldy, dots, none);
     else
-        q4_0_gemm_kernel<false, false><<<grid, 256, 0, ctx->stream>>>(mat, w->plane0_bytes, w->blocks, w->dchunks, q,
-                                                                      scales, w->cols, M, tile0, row_start, row_end,
-                                                                      bias, y, ldy, dots, none);
+        q4_0_gemm_dma_kernel<<<dim3((grid.x + 1) / 2, (M + kDmaTok - 1) / kDmaTok), 512, 0, ctx->stream>>>(
+            mat, w->plane0_bytes, w->blocks, w->dchunks, q, scales, w->cols, M, w->tiles, tile0, row_start, row_end,
+            bias, y, ldy);
     return check_launch("q4_0_gemm");
 }
 
