@@ -347,7 +347,7 @@ def bench_c3(ctx, torch):
     for s in range(steps - 1):
         model.graph.replay()
     decode_ms = ctx.timer_stop()
-    ids = model.decoded(tok, len(prompt), steps)
+    ids = model.decoded(len(prompt), steps)
     q4 = lambda r, c: r * (c // 32) * 18
     qd, kvd = cfg.heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim
     layer_bytes = (q4(qd + 2 * kvd, cfg.dim) + q4(cfg.dim, qd) + q4(2 * cfg.ffn, cfg.dim) + q4(cfg.dim, cfg.ffn))

@@ -69,6 +69,21 @@ _SIGNATURES = {
     "gx_norm_matmul_q4_0": [_vp, _vp, _vp, _vp, _vp, ctypes.c_float, _vp, _c_int, _c_int, _vp],
     "gx_norm_swiglu_q4_0": [_vp, _vp, _vp, _vp, _vp, ctypes.c_float, _vp, _vp, _vp, _vp],
     "gx_argmax": [_vp, _vp, _c_int, _c_int, _c_int, _vp],
+    "gx_gguf_open": [ctypes.c_char_p, _pp],
+    "gx_gguf_close": [_vp],
+    "gx_gguf_tensor_count": [_vp, ctypes.POINTER(_c_int)],
+    "gx_gguf_tensor_name": [_vp, _c_int, ctypes.POINTER(ctypes.c_char_p)],
+    "gx_gguf_tensor": [_vp, ctypes.c_char_p, ctypes.POINTER(_c_int), ctypes.POINTER(_c_int),
+                       ctypes.POINTER(ctypes.c_int64), _pp, ctypes.POINTER(_c_size)],
+    "gx_gguf_meta_count": [_vp, ctypes.POINTER(_c_int)],
+    "gx_gguf_meta_key": [_vp, _c_int, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(_c_int)],
+    "gx_gguf_meta_string": [_vp, ctypes.c_char_p, _pp, ctypes.POINTER(_c_size)],
+    "gx_gguf_meta_bool": [_vp, ctypes.c_char_p, ctypes.POINTER(_c_int)],
+    "gx_gguf_meta_f32": [_vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_float)],
+    "gx_gguf_meta_u32": [_vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_uint32)],
+    "gx_gguf_meta_u32s": [_vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_uint32), _c_size, ctypes.POINTER(_c_size)],
+    "gx_gguf_meta_bools": [_vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_uint8), _c_size, ctypes.POINTER(_c_size)],
+    "gx_gguf_meta_strings": [_vp, ctypes.c_char_p, _c_size, _pp, ctypes.POINTER(_c_size), ctypes.POINTER(_c_size)],
 }
 _RESTYPE = {"gx_last_error": ctypes.c_char_p}
 

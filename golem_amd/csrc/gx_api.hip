@@ -28,6 +28,11 @@ int fail(int code, const char *fmt, ...) {
     return code;
 }
 
+int succeed() {
+    g_error.clear();
+    return GX_OK;
+}
+
 int check_launch(const char *what) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess)

@@ -50,6 +50,7 @@ __host__ __device__ inline size_t q16_offset(int t, int k, int blocks) {
 }
 
 int fail(int code, const char *fmt, ...);
+int succeed();  // clears the thread's error message; GX_OK
 int check_launch(const char *what);
 
 }  // namespace gx

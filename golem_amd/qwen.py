@@ -100,7 +100,11 @@ class QwenModel:
                 "attn_norm": dev(b["attn_norm"]), "ffn_norm": dev(b["ffn_norm"]),
                 "q_norm": dev(b["q_norm"]), "k_norm": dev(b["k_norm"]),
             })
-        self.embd = capi.Weight(ctx, weights["token_embd"], capi.Q6_K, cfg.vocab, cfg.dim)
+        # the tied embedding / head: Q6_K (config 3) or Q4_0 (a pure Q4_0 checkpoint)
+        self.head_quant = weights.get("token_embd_quant", capi.Q6_K)
+        if self.head_quant not in (capi.Q6_K, capi.Q4_0):
+            raise ValueError("qwen: the tied head must be Q6_K or Q4_0")
+        self.embd = capi.Weight(ctx, weights["token_embd"], self.head_quant, cfg.vocab, cfg.dim)
         self.output_norm = dev(weights["output_norm"])
         cos, sin = rope_tables(cfg.head_dim, cfg.max_context, cfg.rope_base)
         self.rope_cos, self.rope_sin = dev(cos), dev(sin)
@@ -254,10 +258,17 @@ class QwenModel:
         self.graph = graph
 
     def logits(self, row):
-        """Logits of hidden state `row` (of the last forward): QuantizeK and
-        the tied Q6_K head; the device logits [vocab] (reused storage)."""
+        """Logits of hidden state `row` (of the last forward): the tied head
+        (qwen/model.go:181-194), Q6_K over the Q8_K form or Q4_0 over the Q8_0
+        form; the device logits [vocab] (reused storage)."""
         cfg, vp, call, ctx = self.cfg, self._vp, self._call, self.ctx.ptr
         h = self.hidden[row:row + 1]
+        if self.head_quant == capi.Q4_0:
+            a = self.x8  # free once the blocks are done
+            call("gx_quantize_q8_0", ctx, vp(h), cfg.dim, 1, cfg.dim, vp(a.q), vp(a.s), vp(a.qs), None, None)
+            call("gx_matmul_q4_0", ctx, self.embd.ptr, vp(a.q), vp(a.s), vp(a.qs), None, 1, 0, cfg.vocab, None,
+                 vp(self.logit), cfg.vocab)
+            return self.logit[0]
         call("gx_quantize_q8_k", ctx, vp(h), cfg.dim, 1, cfg.dim, vp(self.k8), vp(self.ks), vp(self.bs))
         call("gx_matmul_q6_k", ctx, self.embd.ptr, vp(self.k8), vp(self.ks), vp(self.bs), 1, 0, cfg.vocab, None,
              vp(self.logit), cfg.vocab)
@@ -284,7 +295,7 @@ class QwenModel:
             self.start_decode(tok, len(prompt))
             for _ in range(steps - 1):
                 self.graph.replay()
-            return self.decoded(tok, len(prompt), steps)
+            return self.decoded(len(prompt), steps)
         ids = []
         pos = len(prompt)
         for s in range(steps):
@@ -296,17 +307,18 @@ class QwenModel:
         return [int(t.item()) for t in ids]
 
     def start_decode(self, tok, pos):
-        """Seeds the captured step: token `tok` (device) at position `pos`."""
+        """Seeds the captured step: token `tok` (device) at position `pos`,
+        also recorded as the history's entry `pos`."""
         if pos >= self.cfg.max_context:
             raise ValueError(f"qwen: position {pos} is past the context {self.cfg.max_context}")
         self.tokens[:1].copy_(tok)
+        self.history[pos:pos + 1].copy_(tok)
         self.pos64.fill_(pos)
 
-    def decoded(self, tok, pos, steps):
-        """The ids of `steps` greedy tokens: `tok`, then those the replays
-        started at `pos` left in the history."""
-        rest = self.history[pos + 1:pos + steps].cpu().tolist() if steps > 1 else []
-        return [int(tok.item())] + [int(t) for t in rest]
+    def decoded(self, pos, steps):
+        """The ids of `steps` greedy tokens from position `pos`: the seed
+        and those the replays left in the history."""
+        return [int(t) for t in self.history[pos:pos + steps].cpu().tolist()]
 
     def free(self):
         for b in self.blocks:

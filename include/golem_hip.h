@@ -303,6 +303,52 @@ int gx_swiglu_quant(gx_ctx *ctx, const float *gu, int ldgu, int M, int ffn, int 
  * index on ties (qwen/model_test.go:118-126). */
 int gx_argmax(gx_ctx *ctx, const float *x, int ldx, int M, int n, int32_t *ids);
 
+/* ---- GGUF checkpoints (host only; no GPU needed) ----------------------- */
+
+/* An opened GGUF file: mapped whole, read in place (tensors/gguf.go:33-41,
+ * tensors/mmap.go).  Tensor data pointers point into the mapping and stay
+ * valid until gx_gguf_close; gx_weight_upload(on_device = 0) takes them
+ * directly.  Tensor types are ggml's numbers (0 F32, 1 F16, 2 Q4_0, 8 Q8_0,
+ * 14 Q6_K, 30 BF16); metadata value types are GGUF's (0 uint8 ... 12
+ * float64, 8 string, 9 array). */
+typedef struct gx_gguf gx_gguf;
+
+/* OpenGGUF (tensors/gguf.go:164-175): maps the file and reads the header,
+ * metadata and tensor table, with golem's checks and messages ("not a GGUF
+ * file", "GGUF version N, only 2 and 3 are read", "truncated at byte N",
+ * "tensor \"x\" has N dimensions", "unsupported ggml type", a row that does not
+ * divide into blocks, an alignment that is not a power of two, a tensor past
+ * the end of the file), each prefixed with the path. */
+int gx_gguf_open(const char *path, gx_gguf **out);
+/* Close (tensors/gguf.go:314): unmaps; every pointer into the file dies. */
+int gx_gguf_close(gx_gguf *g);
+
+/* The tensor table (GGUF.Tensors): count, the name of entry i (file order,
+ * a repeated name keeping its last entry), and Get (tensors/gguf.go:305):
+ * type, dimensions (shape[0] is the row length), shape[4] (0 past ndims),
+ * the data in the mapping and its size.  Any output may be NULL. */
+int gx_gguf_tensor_count(const gx_gguf *g, int *count);
+int gx_gguf_tensor_name(const gx_gguf *g, int index, const char **name);
+int gx_gguf_tensor(const gx_gguf *g, const char *name, int *ggml_type, int *ndims, int64_t *shape,
+                   const void **data, size_t *bytes);
+
+/* The metadata (GGUF.Meta) and its typed accessors (tensors/gguf_meta.go):
+ * String :18, Bool :30, Float32 :42 (float32 or float64), Uint32 :79 (any
+ * integer width, converted as Go converts), Uint32Slice :88 and BoolSlice
+ * (an array, or a scalar as an array of one), Strings (an array of strings;
+ * string `index` of it when s is not NULL).  The *_s forms write at most
+ * cap values and always the full count. */
+int gx_gguf_meta_count(const gx_gguf *g, int *count);
+int gx_gguf_meta_key(const gx_gguf *g, int index, const char **key, int *type);
+int gx_gguf_meta_string(const gx_gguf *g, const char *key, const char **s, size_t *len);
+int gx_gguf_meta_bool(const gx_gguf *g, const char *key, int *out);
+int gx_gguf_meta_f32(const gx_gguf *g, const char *key, float *out);
+int gx_gguf_meta_u32(const gx_gguf *g, const char *key, uint32_t *out);
+int gx_gguf_meta_u32s(const gx_gguf *g, const char *key, uint32_t *out, size_t cap, size_t *count);
+int gx_gguf_meta_bools(const gx_gguf *g, const char *key, uint8_t *out, size_t cap, size_t *count);
+int gx_gguf_meta_strings(const gx_gguf *g, const char *key, size_t index, const char **s, size_t *len,
+                         size_t *count);
+
 #ifdef __cplusplus
 }
 #endif

@@ -12,8 +12,10 @@ residual adds).  The structure follows golem:
   Block                        qwen/block.go:32-102
   Attention                    qwen/attention.go:34-127
   LayerCache.Store             qwen/cache.go:52-60 (entries rounded through fp16)
-  Embed                        qwen/model.go:107-109 (TokenEmbd.Row, DequantizeQ6_K)
-  Logits                       qwen/model.go:181-194 (QuantizeK, MatVecQ6_K)
+  Embed                        qwen/model.go:107-109 (TokenEmbd.Row: DequantizeQ6_K, or
+                               dequantizeQ4_0Row for a Q4_0 table)
+  Logits                       qwen/model.go:181-194 (QuantizeK + MatVecQ6_K, or the
+                               Q8_0 form + Matrix.rows for a Q4_0 head)
 
 Dense matrices are repacked as golem repacks them at load (Matrix.Repack,
 nn/matrix.go:40-46) and multiplied through Matrix.rows' packed path.
@@ -22,8 +24,8 @@ import math
 
 import numpy as np
 
-from . import (Batch, Q4_0, _p, dequantize_q6_k, load, mat_vec_q6_k_rows, matrix_rows, pack_q4_0,
-               rms_norm_plain)
+from . import (Batch, Q4_0, Q6_K, _p, dequantize_q4_0_row, dequantize_q6_k, load, mat_vec_q6_k_rows,
+               matrix_rows, pack_q4_0, rms_norm_plain)
 
 
 class QwenOracle:
@@ -35,7 +37,9 @@ class QwenOracle:
         self.packed = [{n: pack_q4_0(b[n], *self.shapes[n]) for n in self.shapes} for b in weights["blocks"]]
         self.K = [np.zeros((cfg.max_context, cfg.kv_heads, cfg.head_dim), np.float32) for _ in range(cfg.layers)]
         self.V = [np.zeros_like(k) for k in self.K]
-        self.row_bytes = cfg.dim // 256 * 210
+        # the tied embedding / head: Q6_K (config 3) or Q4_0 (a pure Q4_0 file)
+        self.head_quant = weights.get("token_embd_quant", Q6_K)
+        self.row_bytes = cfg.dim // 256 * 210 if self.head_quant == Q6_K else cfg.dim // 32 * 18
 
     def reset(self):
         for k, v in zip(self.K, self.V):
@@ -56,6 +60,8 @@ class QwenOracle:
 
     def embed(self, token):
         row = self.w["token_embd"][token * self.row_bytes:(token + 1) * self.row_bytes]
+        if self.head_quant == Q4_0:
+            return dequantize_q4_0_row(row, self.cfg.dim)
         return dequantize_q6_k(row, self.cfg.dim)
 
     def forward(self, tokens, start_pos):
@@ -116,7 +122,11 @@ class QwenOracle:
         return self._mat(layer, "o", Batch(out).quantize())
 
     def logits(self, hidden):
-        """Logits for one hidden state: the tied Q6_K head over its Q8_K form."""
+        """Logits for one hidden state: the tied head, Q6_K over the Q8_K form
+        or Q4_0 over the Q8_0 form (the embedding is never repacked)."""
+        if self.head_quant == Q4_0:
+            b = Batch(np.asarray(hidden, np.float32)[None, :]).quantize()
+            return matrix_rows(Q4_0, self.w["token_embd"], self.cfg.vocab, self.cfg.dim, b)[0]
         b = Batch(np.asarray(hidden, np.float32)[None, :]).quantize_k()
         return mat_vec_q6_k_rows(self.w["token_embd"], b, self.cfg.vocab)[0]
 
