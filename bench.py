@@ -430,6 +430,37 @@ def bench_c4(ctx, torch, dev):
     for gu, dn in stacks:
         gu.free()
         dn.free()
+    res.update(bench_c4_moe_half(ctx, torch, dev))
+    return res
+
+
+def bench_c4_moe_half(ctx, torch, dev):
+    """The whole feed-forward half of the mixture block (moeHalf): the shared
+    dense branch, the router and experts, and the three post-norms, config
+    4's experts and router.  Config 4 gives no width for the shared branch;
+    the hidden width (2816) is used.  Decode (M = 1) and a 256-position
+    prefill; the residual norm under ffn_norm is included."""
+    from golem_amd import synth
+    from golem_amd.gemma import MoEConfig, MoEHalf, moe_weights
+    cfg = MoEConfig(2816, 2816, 128, 8, 704)
+    g = synth.rng(4)
+    w = moe_weights(cfg, g)
+    blk = MoEHalf(ctx, cfg, w, max_batch=256)
+    res = {}
+    for label, M, npos in (("decode", 1, 64), ("prefill256", 256, 2)):
+        xs = [dev(synth.activations(g, M, cfg.dim)) for _ in range(npos)]
+        out = torch.empty((M, cfg.dim), dtype=torch.float32, device="cuda")
+        for i in range(4):
+            blk.forward(xs[i % npos], out)
+        torch.cuda.synchronize()
+        reps = 64 if M == 1 else 10
+        ctx.timer_start()
+        for i in range(reps):
+            blk.forward(xs[i % npos], out)
+        ms = ctx.timer_stop() / reps
+        res[f"c4_moe_half_{label}"] = {"M": M, "ms_per_layer": round(ms, 4),
+                                       "positions_per_s": round(M / (ms * 1e-3), 1), "shared_ffn": cfg.ffn}
+    blk.free()
     return res
 
 

@@ -69,6 +69,9 @@ _SIGNATURES = {
     "gx_norm_matmul_q4_0": [_vp, _vp, _vp, _vp, _vp, ctypes.c_float, _vp, _c_int, _c_int, _vp],
     "gx_norm_swiglu_q4_0": [_vp, _vp, _vp, _vp, _vp, ctypes.c_float, _vp, _vp, _vp, _vp],
     "gx_argmax": [_vp, _vp, _c_int, _c_int, _c_int, _vp],
+    "gx_geglu_quant": [_vp, _vp, _c_int, _c_int, _c_int, _vp, _vp, _vp],
+    "gx_moe_join": [_vp, _vp, _c_int, _vp, _c_int, _vp, _c_int, _vp, _vp, _vp, _c_int, _c_int, ctypes.c_float, _vp,
+                    _c_int],
     "gx_gguf_open": [ctypes.c_char_p, _pp],
     "gx_gguf_close": [_vp],
     "gx_gguf_tensor_count": [_vp, ctypes.POINTER(_c_int)],

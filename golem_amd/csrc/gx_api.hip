@@ -622,6 +622,32 @@ int gx_swiglu_quant(gx_ctx *ctx, const float *gu, int ldgu, int M, int ffn, int 
     return ok();
 }
 
+int gx_geglu_quant(gx_ctx *ctx, const float *gu, int ldgu, int M, int ffn, int8_t *q, float *scales,
+                   int32_t *qsum) {
+    if (int rc = use(ctx))
+        return rc;
+    GX_CHECK(ffn > 0 && ffn % 32 == 0, "nn: activation length must be a multiple of the block size");
+    GX_CHECK(M >= 0 && ldgu >= 2 * ffn, "gx: bad batch shape");
+    GX_CHECK(gu && q && scales && qsum, "gx: missing argument");
+    if (int rc = gx::launch_geglu_quant(ctx, gu, ldgu, M, ffn, q, scales, qsum))
+        return rc;
+    return ok();
+}
+
+int gx_moe_join(gx_ctx *ctx, float *shared, int lds, float *experts, int lde, const float *resid, int ldr,
+                const float *post1, const float *post2, const float *post, int M, int K, float eps, float *out,
+                int ldo) {
+    if (int rc = use(ctx))
+        return rc;
+    GX_CHECK(K > 0 && M >= 0 && lds >= K && lde >= K && ldr >= K && ldo >= K, "gx: bad shape");
+    GX_CHECK(shared && experts && resid && post1 && post2 && post && out, "gx: missing argument");
+    GX_CHECK(shared != experts, "gx: the two branches must be separate buffers");
+    if (int rc = gx::launch_moe_join(ctx, shared, lds, experts, lde, resid, ldr, post1, post2, post, M, K, eps, out,
+                                     ldo))
+        return rc;
+    return ok();
+}
+
 int gx_argmax(gx_ctx *ctx, const float *x, int ldx, int M, int n, int32_t *ids) {
     if (int rc = use(ctx))
         return rc;

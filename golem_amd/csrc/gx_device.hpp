@@ -224,6 +224,49 @@ __device__ __forceinline__ float norm_scale(double sum, int D, float eps) {
     return (float)(1.0 / sqrt((double)(mean + eps)));
 }
 
+// The float64 sum of squares of K floats in LDS, by a workgroup of at least
+// 512 threads, in the order every whole-row RMSNormPlain here uses: 512
+// strided partials, then a pairwise tree down to one.  red: 512 doubles of
+// LDS; the sum comes back in every thread through *bcast (LDS).
+__device__ __forceinline__ double block_sum_squares(const float *xs, int K, double *red, double *bcast) {
+    const int tid = threadIdx.x;
+    if (tid < 512) {
+        double part = 0.0;
+        for (int i = tid; i < K; i += 512) {
+            const float v = xs[i];
+            const float sq = v * v;
+            part += (double)sq;
+        }
+        red[tid] = part;
+    }
+    __syncthreads();
+    double s = 0.0;
+    if (tid < 256)
+        s = red[tid] + red[tid + 256];
+    __syncthreads();
+    if (tid < 256)
+        red[tid] = s;
+    __syncthreads();
+    if (tid < 128)
+        s = s + red[tid + 128];
+    __syncthreads();
+    if (tid < 128)
+        red[tid] = s;
+    __syncthreads();
+    if (tid < 64) {
+        s = s + red[tid + 64];
+        for (int w = 32; w > 0; w >>= 1) {
+            const double o = __shfl_down(s, w, 64);
+            if (tid < w)
+                s = s + o;
+        }
+        if (tid == 0)
+            *bcast = s;
+    }
+    __syncthreads();
+    return *bcast;
+}
+
 
 // Q8_0 of one element per lane of a 32-lane group (Batch.quantizeBlock,
 // nn/batch.go:109-143): returns q; the group's fp16-rounded scale and sum of

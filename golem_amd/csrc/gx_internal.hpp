@@ -119,6 +119,11 @@ int launch_q6_k_matvec(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const f
                        int ldy, int32_t *dots);
 int moe_workspace_bytes(int M, int k, int D, int F, int E, size_t *bytes);
 int launch_gelu_table(gx_ctx *ctx, float *table);
+int launch_geglu_quant(gx_ctx *ctx, const float *gu, int ldgu, int M, int ffn, int8_t *q, float *scales,
+                       int32_t *qsum);
+int launch_moe_join(gx_ctx *ctx, float *shared, int lds_, float *experts, int lde, const float *resid, int ldr,
+                    const float *post1, const float *post2, const float *post, int M, int K, float eps, float *out,
+                    int ldo);
 int launch_moe_route(gx_ctx *ctx, const gx_weight *router, const float *router_scale, const float *resid, int ldr,
                      int M, int k, float eps, float *logits, int32_t *ids, float *weights);
 int launch_moe_experts(gx_ctx *ctx, const gx_weight *gate_up, const gx_weight *down, const float *down_scale,

@@ -334,17 +334,18 @@ __global__ __launch_bounds__(64) void moe_topk_kernel(const float *__restrict__ 
 }
 
 // mid = GELUTable(gate) * up for one unit per workgroup row, then its Q8_0
-// form (Batch.quantizeBlock): gate_up is [U][2F], mid_q [U][F].
-__global__ __launch_bounds__(256) void moe_gelu_mul_quant_kernel(const float *__restrict__ gate_up, int F, int U,
-                                                                  const float *__restrict__ table,
+// form (Batch.quantizeBlock): gate_up is [U][ld] with each row's F gates then
+// its F ups, mid_q [U][F].
+__global__ __launch_bounds__(256) void moe_gelu_mul_quant_kernel(const float *__restrict__ gate_up, int ld, int F,
+                                                                  int U, const float *__restrict__ table,
                                                                   int8_t *__restrict__ q, float *__restrict__ scales,
                                                                   int32_t *__restrict__ qsum) {
     const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (gid >= (size_t)U * F)
         return;  // U*F is a multiple of 32: whole 32-lane groups drop out
     const int u = (int)(gid / F), i = (int)(gid % F);
-    const float gate = gate_up[(size_t)u * 2 * F + i];
-    const float up = gate_up[(size_t)u * 2 * F + F + i];
+    const float gate = gate_up[(size_t)u * ld + i];
+    const float up = gate_up[(size_t)u * ld + F + i];
     // GELUTable (nn/gelu_table.go:40-52)
     float gl;
     if (gate <= -10.0f)
@@ -382,6 +383,47 @@ __global__ __launch_bounds__(256) void moe_gelu_mul_quant_kernel(const float *__
         scales[index] = half_bits_to_float(float_to_half_bits(scale));
         qsum[index] = sum;
     }
+}
+
+// The join of moeHalf (gemma/block.go:195-205), one position per workgroup:
+// shared = RMSNormPlain(shared, post1) and experts = RMSNormPlain(experts,
+// post2), both written back (golem's buffers hold them so afterwards);
+// combined = shared + experts; RMSNormPlain(combined, post); out = resid +
+// combined.  Each norm is a float64 sum of squares in the order of the other
+// residual norms, then (v * scale) * gain in float32.
+constexpr int kJoinThreads = 1024;
+__global__ __launch_bounds__(kJoinThreads) void moe_join_kernel(float *__restrict__ shared, int lds_,
+                                                               float *__restrict__ experts, int lde,
+                                                               const float *__restrict__ resid, int ldr,
+                                                               const float *__restrict__ post1,
+                                                               const float *__restrict__ post2,
+                                                               const float *__restrict__ post, int K, float eps,
+                                                               float *__restrict__ out, int ldo) {
+    extern __shared__ float join[];  // shared, experts: K floats each
+    float *sh = join, *ex = join + K;
+    __shared__ double red[512];
+    __shared__ double total;
+    const int tid = threadIdx.x, t = blockIdx.x;
+    float *sr = shared + (size_t)t * lds_, *er = experts + (size_t)t * lde;
+    for (int i = tid; i < K; i += kJoinThreads) {
+        sh[i] = sr[i];
+        ex[i] = er[i];
+    }
+    __syncthreads();
+    const float s1 = norm_scale(block_sum_squares(sh, K, red, &total), K, eps);
+    const float s2 = norm_scale(block_sum_squares(ex, K, red, &total), K, eps);
+    for (int i = tid; i < K; i += kJoinThreads) {
+        const float a = sh[i] * s1 * post1[i], b = ex[i] * s2 * post2[i];
+        sr[i] = a;
+        er[i] = b;
+        sh[i] = a + b;  // combined, in place of the shared values
+    }
+    __syncthreads();
+    const float s3 = norm_scale(block_sum_squares(sh, K, red, &total), K, eps);
+    const float *rr = resid + (size_t)t * ldr;
+    float *orow = out + (size_t)t * ldo;
+    for (int i = tid; i < K; i += kJoinThreads)
+        orow[i] = rr[i] + sh[i] * s3 * post[i];
 }
 
 // The expert sum: out[t][i] = 0, then out += (w_k * DownScale[id_k]) *
@@ -513,6 +555,29 @@ int moe_workspace_bytes(int M, int k, int D, int F, int E, size_t *bytes) {
     return GX_OK;
 }
 
+int launch_geglu_quant(gx_ctx *ctx, const float *gu, int ldgu, int M, int ffn, int8_t *q, float *scales,
+                       int32_t *qsum) {
+    const size_t n = (size_t)M * ffn;
+    if (n == 0)
+        return GX_OK;
+    moe_gelu_mul_quant_kernel<<<(unsigned)((n + 255) / 256), 256, 0, ctx->stream>>>(gu, ldgu, ffn, M,
+                                                                                    ctx->gelu_table, q, scales,
+                                                                                    qsum);
+    return check_launch("geglu_quant");
+}
+
+int launch_moe_join(gx_ctx *ctx, float *shared, int lds_, float *experts, int lde, const float *resid, int ldr,
+                    const float *post1, const float *post2, const float *post, int M, int K, float eps, float *out,
+                    int ldo) {
+    if (M == 0)
+        return GX_OK;
+    const size_t lds = 2 * (size_t)K * sizeof(float);
+    GX_CHECK(lds <= 64 * 1024, "gx: a %d-wide residual does not fit the join's LDS", K);
+    moe_join_kernel<<<M, kJoinThreads, lds, ctx->stream>>>(shared, lds_, experts, lde, resid, ldr, post1, post2,
+                                                           post, K, eps, out, ldo);
+    return check_launch("moe_join");
+}
+
 int launch_gelu_table(gx_ctx *ctx, float *table) {
     gelu_table_kernel<<<256, 256, 0, ctx->stream>>>(table);
     return check_launch("gelu_table");
@@ -582,8 +647,8 @@ int launch_moe_experts(gx_ctx *ctx, const gx_weight *gate_up, const gx_weight *d
             return rc;
     }
     const size_t n = (size_t)U * F;
-    moe_gelu_mul_quant_kernel<<<(unsigned)((n + 255) / 256), 256, 0, ctx->stream>>>(gu, F, U, gelu_table, mq, ms,
-                                                                                    mqs);
+    moe_gelu_mul_quant_kernel<<<(unsigned)((n + 255) / 256), 256, 0, ctx->stream>>>(gu, 2 * F, F, U, gelu_table,
+                                                                                    mq, ms, mqs);
     if (int rc = check_launch("moe_gelu_mul_quant"))
         return rc;
     if (grouped) {

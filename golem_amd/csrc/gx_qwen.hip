@@ -59,39 +59,10 @@ __global__ __launch_bounds__(kQNormThreads) void qwen_norm_quant_kernel(float *_
     if (ar)  // the residual, written back
         for (int i = tid; i < K; i += kQNormThreads)
             xr[i] = xs[i];
-    if (tid < 512) {
-        double part = 0.0;
-        for (int i = tid; i < K; i += 512) {
-            const float v = xs[i];
-            const float sq = v * v;
-            part += (double)sq;
-        }
-        red[tid] = part;
-    }
-    __syncthreads();
-    double s = 0.0;
-    if (tid < 256)
-        s = red[tid] + red[tid + 256];  // w = 256
-    __syncthreads();
-    if (tid < 256)
-        red[tid] = s;
-    __syncthreads();
-    if (tid < 128)
-        s = s + red[tid + 128];
-    __syncthreads();
-    if (tid < 128)
-        red[tid] = s;
-    __syncthreads();
-    if (tid < 64) {
-        s = s + red[tid + 64];
-        for (int w = 32; w > 0; w >>= 1) {
-            const double o = __shfl_down(s, w, 64);
-            if (tid < w)
-                s = s + o;
-        }
-        if (tid == 0)
-            scale_sh = norm_scale(s, K, eps);
-    }
+    __shared__ double total;
+    const double sum = block_sum_squares(xs, K, red, &total);
+    if (tid == 0)
+        scale_sh = norm_scale(sum, K, eps);
     __syncthreads();
     const float sc = scale_sh;
     // Element i = j*1024 + tid: a 32-lane group covers one Q8_0 block.

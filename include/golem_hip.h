@@ -226,6 +226,22 @@ int gx_moe_experts(gx_ctx *ctx, const gx_weight *gate_up, const gx_weight *down,
                    const float *x, int ldx, int M, int top_k, const int32_t *ids, const float *weights, float *out,
                    int ldo, void *workspace, size_t workspace_bytes);
 
+/* The shared expert's activation (gemma/block.go:163-174, the dense feed
+ * forward's): gu [M][ldgu] holds each position's ffn gates then its ffn ups;
+ * q/scales/qsum receive Q8_0(GELUTable(gate) * up) [M][ffn] (nn/gelu_table.go
+ * :40-52, the table of gx_gelu_table).  ffn a multiple of 32. */
+int gx_geglu_quant(gx_ctx *ctx, const float *gu, int ldgu, int M, int ffn, int8_t *q, float *scales,
+                   int32_t *qsum);
+
+/* The join of moeHalf (gemma/block.go:195-205) for M positions of width K:
+ * shared[m] = RMSNormPlain(shared[m], post1) and experts[m] =
+ * RMSNormPlain(experts[m], post2), both written back in place; then
+ * out[m] = resid[m] + RMSNormPlain(shared[m] + experts[m], post).  All device
+ * floats; out may be resid. */
+int gx_moe_join(gx_ctx *ctx, float *shared, int lds, float *experts, int lde, const float *resid, int ldr,
+                const float *post1, const float *post2, const float *post, int M, int K, float eps, float *out,
+                int ldo);
+
 /* ---- the Qwen3 dense block around the products (qwen/) --------------- */
 
 /* x[m] += add[m] (add may be NULL: no residual), then RMSNormPlain(x[m], gain,

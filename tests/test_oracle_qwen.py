@@ -80,3 +80,22 @@ def test_oracle_batch_equals_one_at_a_time():
     np.testing.assert_array_equal(batch.view(np.uint32), alone.view(np.uint32))
     for a, b in zip(k_batch, o.K):
         np.testing.assert_array_equal(a, b)
+
+
+def test_oracle_moe_half_adds_both_branches():
+    """golem's TestMoEHalfAddsBothBranches (gemma/moe_test.go:273-322) on the
+    oracle's moeHalf: both branches contribute, they differ, and the output
+    is the residual plus post_ffw_norm of their sum."""
+    from golem_amd.gemma import MoEConfig, moe_weights
+    from oracle.gemma import moe_half
+    cfg = MoEConfig(64, 64, 6, 2, 64)
+    g = synth.rng(70)
+    w = moe_weights(cfg, g)
+    resid = synth.activations(g, 2, cfg.dim)
+    out, shared, experts, ids, _ = moe_half(cfg, w, resid)
+    for t in range(2):
+        assert np.any(shared[t] != 0) and np.any(experts[t] != 0)
+        assert not np.array_equal(shared[t], experts[t])
+        assert len(set(ids[t].tolist())) == cfg.used
+        want = resid[t] + oracle.rms_norm_plain(shared[t] + experts[t], w["post_ffw_norm"], cfg.eps)
+        np.testing.assert_array_equal(out[t].view(np.uint32), want.astype(np.float32).view(np.uint32))
