@@ -356,8 +356,31 @@ def bench_c3(ctx, torch):
     kv_bytes = cfg.layers * mean_ctx * cfg.kv_heads * cfg.head_dim * 2 * 2
     token_bytes = cfg.layers * layer_bytes + head_bytes + kv_bytes
     per_tok = decode_ms / (steps - 1)
+
+    # Eight conversations decoded in lock step (slots): one pass over the
+    # weights and one head read per step for all eight.
+    nconv, slot_prompt, slot_steps = 8, 64, 16
+    model.set_slots(nconv)
+    firsts = []
+    for i in range(nconv):
+        model.use_slot(i)
+        model.forward(prompt[i * slot_prompt:(i + 1) * slot_prompt], 0)
+        firsts.append(int(model.next_token(slot_prompt - 1).item()))
+    model.start_slots(firsts, [slot_prompt] * nconv)
+    model.slots_step(nconv)  # warm
+    model.start_slots(firsts, [slot_prompt] * nconv)
+    torch.cuda.synchronize()
+    ctx.timer_start()
+    for _ in range(slot_steps):
+        model.slots_step(nconv)
+    slots_ms = ctx.timer_stop()
+    slot_step_ms = slots_ms / slot_steps
     model.free()
-    return {"c3_qwen3_4b": {
+    return {"c3_qwen3_4b_slots": {
+        "conversations": nconv, "prompt_each": slot_prompt, "steps": slot_steps,
+        "ms_per_step": round(slot_step_ms, 3), "tok_per_s": round(nconv * 1e3 / slot_step_ms, 1),
+        "eager": True},
+        "c3_qwen3_4b": {
         "prefill_tokens": len(prompt), "prefill_ms": round(prefill_ms, 2),
         "prefill_tok_per_s": round(len(prompt) / (prefill_ms * 1e-3), 1),
         "decode_steps": steps, "decode_ms_per_token": round(per_tok, 3),

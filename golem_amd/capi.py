@@ -61,10 +61,10 @@ _SIGNATURES = {
     "gx_moe_experts": [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _vp, _vp, _c_int, _vp, _c_size],
     "gx_norm_quant": [_vp, _vp, _c_int, _vp, _c_int, _vp, _c_int, _c_int, ctypes.c_float, _vp, _c_int, _vp, _vp, _vp],
     "gx_qwen_qk_rope": [_vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _vp, ctypes.c_float,
-                        _vp, _vp, _vp, _c_int],
+                        _vp, _vp, _vp, _c_int, _vp, _c_int],
     "gx_qwen_attention_workspace_bytes": [_c_int, _c_int, _c_int, ctypes.POINTER(_c_size)],
     "gx_qwen_attention": [_vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _c_int, _vp, _vp, _vp,
-                          _vp, _c_size],
+                          _vp, _c_size, _vp, _c_int],
     "gx_swiglu_quant": [_vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp],
     "gx_norm_matmul_q4_0": [_vp, _vp, _vp, _vp, _vp, ctypes.c_float, _vp, _c_int, _c_int, _vp],
     "gx_norm_swiglu_q4_0": [_vp, _vp, _vp, _vp, _vp, ctypes.c_float, _vp, _vp, _vp, _vp],

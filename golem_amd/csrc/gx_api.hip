@@ -560,7 +560,8 @@ int gx_norm_quant(gx_ctx *ctx, float *x, int ldx, const float *add, int lda, con
 
 int gx_qwen_qk_rope(gx_ctx *ctx, const float *qkv, int ldqkv, int M, int heads, int kv_heads, int head_dim,
                     const int32_t *positions, const float *q_norm, const float *k_norm, const float *rope_cos,
-                    const float *rope_sin, float eps, uint16_t *qh, uint16_t *kcache, uint16_t *vcache, int context) {
+                    const float *rope_sin, float eps, uint16_t *qh, uint16_t *kcache, uint16_t *vcache, int context,
+                    const int32_t *slots, int nslots) {
     if (int rc = use(ctx))
         return rc;
     GX_CHECK(heads > 0 && kv_heads > 0 && heads % kv_heads == 0, "gx: %d query heads over %d key-value heads", heads,
@@ -568,10 +569,11 @@ int gx_qwen_qk_rope(gx_ctx *ctx, const float *qkv, int ldqkv, int M, int heads, 
     GX_CHECK(M >= 0 && ldqkv >= (heads + 2 * kv_heads) * head_dim && context > 0, "gx: bad batch shape");
     GX_CHECK(qkv && positions && q_norm && k_norm && rope_cos && rope_sin && qh && kcache && vcache,
              "gx: missing argument");
+    GX_CHECK(!slots || nslots > 0, "gx: %d slots", nslots);
     if (M == 0)
         return ok();
     if (int rc = gx::launch_qwen_qk_rope(ctx, qkv, ldqkv, M, heads, kv_heads, head_dim, positions, q_norm, k_norm,
-                                         rope_cos, rope_sin, eps, qh, kcache, vcache, context))
+                                         rope_cos, rope_sin, eps, qh, kcache, vcache, context, slots, nslots))
         return rc;
     return ok();
 }
@@ -584,7 +586,8 @@ int gx_qwen_attention_workspace_bytes(int M, int heads, int max_pos, size_t *byt
 
 int gx_qwen_attention(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int kv_heads, int head_dim, int max_pos,
                       const int32_t *positions, const uint16_t *kcache, const uint16_t *vcache, int context,
-                      int8_t *q, float *scales, int32_t *qsum, void *workspace, size_t workspace_bytes) {
+                      int8_t *q, float *scales, int32_t *qsum, void *workspace, size_t workspace_bytes,
+                      const int32_t *slots, int nslots) {
     if (int rc = use(ctx))
         return rc;
     GX_CHECK(heads > 0 && kv_heads > 0 && heads % kv_heads == 0, "gx: %d query heads over %d key-value heads", heads,
@@ -595,6 +598,7 @@ int gx_qwen_attention(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int kv_
     GX_CHECK(qh && positions && kcache && vcache && q && scales && qsum && workspace, "gx: missing argument");
     GX_CHECK(((uintptr_t)vcache & 15) == 0, "gx: the value cache must be 16-byte aligned");
     GX_CHECK(((uintptr_t)workspace & 255) == 0, "gx: the workspace must be 256-byte aligned");
+    GX_CHECK(!slots || nslots > 0, "gx: %d slots", nslots);
     if (M == 0)
         return ok();
     const size_t need = gx::qwen_attention_workspace(M, heads, max_pos);
@@ -602,7 +606,8 @@ int gx_qwen_attention(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int kv_
     // llama.cpp's 1/sqrt(head_dim), taken in float64 and rounded (qwen/attention.go:90-93)
     const float scale = (float)(1.0 / sqrt((double)head_dim));
     if (int rc = gx::launch_qwen_attention(ctx, qh, M, heads, kv_heads, head_dim, max_pos, positions, kcache, vcache,
-                                           context, scale, q, scales, qsum, (uint8_t *)workspace))
+                                           context, scale, q, scales, qsum, (uint8_t *)workspace, slots,
+                                           nslots))
         return rc;
     return ok();
 }

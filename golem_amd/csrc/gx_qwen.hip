@@ -121,11 +121,26 @@ __global__ __launch_bounds__(64) void qwen_qk_rope_kernel(const float *__restric
                                                           const float *__restrict__ rope_cos,
                                                           const float *__restrict__ rope_sin, float eps,
                                                           uint16_t *__restrict__ qh, uint16_t *__restrict__ kcache,
-                                                          uint16_t *__restrict__ vcache, int context) {
+                                                          uint16_t *__restrict__ vcache, int context,
+                                                          const int32_t *__restrict__ slots, int nslots) {
     __shared__ float h[kHeadMax];
     __shared__ float sc_sh;
     const int lane = threadIdx.x, t = blockIdx.x, u = blockIdx.y;
     const int pos = positions[t];
+    if (slots) {  // the token's own conversation: its slot of the caches
+        const int slot = slots[t];
+        if (slot < 0 || slot >= nslots) {
+            // no such conversation: nothing is stored, and the query is NaN,
+            // which the attention and everything after carry to the output
+            if (u < heads)
+                for (int i = lane; i < hd; i += 64)
+                    qh[(size_t)t * heads * hd + u * hd + i] = 0x7E00;
+            return;
+        }
+        const size_t at = (size_t)slot * kv_heads * hd * context;
+        kcache += at;
+        vcache += at;
+    }
     const int half = hd >> 1;
     const bool is_q = u < heads;
     const int col = is_q ? u * hd : heads * hd + (u - heads) * hd;
@@ -213,10 +228,13 @@ __global__ __launch_bounds__(64) void attn_scores_kernel(const uint16_t *__restr
                                                          int GH, int TT, const int32_t *__restrict__ positions, int limit,
                                                          const uint16_t *__restrict__ kcache, int context,
                                                          float scale, int S, float *__restrict__ sc,
-                                                         float *__restrict__ tmax) {
+                                                         float *__restrict__ tmax, const int32_t *__restrict__ slots,
+                                                         int nslots, int kv_heads) {
     const int lane = threadIdx.x, tile = blockIdx.x;
     const int h0 = blockIdx.y * GH, t0 = blockIdx.z * TT;
     const int kvh = h0 / G, tiles = S / kTile;
+    if (slots)  // with slots, a token tile is one token (TT = 1); reads stay inside the caches
+        kcache += (size_t)min(max(slots[t0], 0), nslots - 1) * kv_heads * HD * context;
     const int tn = min(TT, M - t0);
     int last = -1;
     for (int tt = 0; tt < tn; tt++)
@@ -378,7 +396,8 @@ __global__ __launch_bounds__(NT) void attn_values_kernel(int M, int heads, int G
                                                          const uint16_t *__restrict__ vcache, int context,
                                                          int kv_heads, int S, const uint16_t *__restrict__ prob,
                                                          int8_t *__restrict__ q, float *__restrict__ scales,
-                                                         int32_t *__restrict__ qsum) {
+                                                         int32_t *__restrict__ qsum, const int32_t *__restrict__ slots,
+                                                         int nslots) {
     constexpr int rows = NT / kValSlice;  // (tt, g) pairs
     __shared__ __align__(16) uint16_t vs[kValSlice * kValStride];
     __shared__ __align__(16) uint16_t ps[rows * kValStride];
@@ -393,6 +412,8 @@ __global__ __launch_bounds__(NT) void attn_values_kernel(int M, int heads, int G
     int nmax = 0;
     for (int i = 0; i < tn; i++)
         nmax = max(nmax, min(positions[t0 + i] + 1, limit));
+    if (slots)  // with slots, a token tile is one token (TT = 1); reads stay inside the caches
+        vcache += (size_t)min(max(slots[t0], 0), nslots - 1) * kv_heads * hd * context;
     const uint16_t *vrow = vcache + ((size_t)kvh * hd + d0) * context;
     float acc = 0.0f;
     for (int c0 = 0; c0 < nmax; c0 += kValChunk) {
@@ -479,7 +500,8 @@ template <int HD, int G>
 __global__ __launch_bounds__(kDecodeThreads) void attn_decode_kernel(
     const uint16_t *__restrict__ qh, int heads, int kv_heads, const int32_t *__restrict__ positions, int limit,
     const uint16_t *__restrict__ kcache, const uint16_t *__restrict__ vcache, int context, float scale,
-    int8_t *__restrict__ q, float *__restrict__ scales, int32_t *__restrict__ qsum) {
+    int8_t *__restrict__ q, float *__restrict__ scales, int32_t *__restrict__ qsum,
+    const int32_t *__restrict__ slots, int nslots) {
     // LDS: region A holds the scores [G][kScoreStride] floats, later the value
     // slice [32][kDecodeStride] halves; then the probabilities [G][kDecodeStride]
     // halves and the queries [G][HD] halves.
@@ -498,6 +520,11 @@ __global__ __launch_bounds__(kDecodeThreads) void attn_decode_kernel(
     const int t = blockIdx.y;
     const int n = min(positions[t] + 1, limit);
     const int groups = (n + 7) / 8, pieces = kValSlice * groups;
+    if (slots) {  // the token's own conversation; reads stay inside the caches
+        const size_t at = (size_t)min(max(slots[t], 0), nslots - 1) * kv_heads * HD * context;
+        kcache += at;
+        vcache += at;
+    }
 
     // The G queries (adjacent heads of the row) first, then the key pieces of
     // this thread's positions, then the value slice (32 rows of positions,
@@ -756,12 +783,12 @@ int launch_qwen_norm_quant(gx_ctx *ctx, float *x, int ldx, const float *add, int
 int launch_qwen_qk_rope(gx_ctx *ctx, const float *qkv, int ldqkv, int M, int heads, int kv_heads, int hd,
                         const int32_t *positions, const float *q_norm, const float *k_norm, const float *rope_cos,
                         const float *rope_sin, float eps, uint16_t *qh, uint16_t *kcache, uint16_t *vcache,
-                        int context) {
+                        int context, const int32_t *slots, int nslots) {
     GX_CHECK(hd <= kHeadMax && hd % 8 == 0, "gx: head width %d unsupported (a multiple of 8, at most %d)", hd,
              kHeadMax);
     qwen_qk_rope_kernel<<<dim3((unsigned)M, (unsigned)(heads + kv_heads)), 64, 0, ctx->stream>>>(
         qkv, ldqkv, heads, kv_heads, hd, positions, q_norm, k_norm, rope_cos, rope_sin, eps, qh, kcache, vcache,
-        context);
+        context, slots, nslots);
     return check_launch("qwen_qk_rope");
 }
 
@@ -774,7 +801,8 @@ size_t qwen_attention_workspace(int M, int heads, int max_pos) {
 
 int launch_qwen_attention(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int kv_heads, int hd, int max_pos,
                           const int32_t *positions, const uint16_t *kcache, const uint16_t *vcache, int context,
-                          float scale, int8_t *q, float *scales, int32_t *qsum, uint8_t *workspace) {
+                          float scale, int8_t *q, float *scales, int32_t *qsum, uint8_t *workspace,
+                          const int32_t *slots, int nslots) {
     const int G = heads / kv_heads;
     GX_CHECK(hd == 32 || hd == 64 || hd == 96 || hd == 128, "gx: attention supports head widths 32, 64, 96 and 128");
     GX_CHECK(G == 1 || G == 2 || G == 4 || G == 8, "gx: %d query heads per key-value head unsupported", G);
@@ -786,11 +814,13 @@ int launch_qwen_attention(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int
     float *tmax = (float *)(workspace + up(rows * S * sizeof(float)));
     uint16_t *prob = (uint16_t *)(workspace + up(rows * S * sizeof(float)) + up(rows * (S / kTile) * sizeof(float)));
 
-    if (M <= 4 && limit <= kDecodeMax) {
+    // One workgroup per token: a few tokens of one conversation, or tokens of
+    // several conversations (slots), whose caches share nothing.
+    if ((M <= 4 || slots) && limit <= kDecodeMax) {
 #define GX_DECODE(HH, GG)                                                                                            \
     attn_decode_kernel<HH, GG><<<dim3((unsigned)(kv_heads * (HH / kValSlice)), (unsigned)M), kDecodeThreads, 0,      \
                                  ctx->stream>>>(qh, heads, kv_heads, positions, limit, kcache, vcache, context,      \
-                                                scale, q, scales, qsum)
+                                                scale, q, scales, qsum, slots, nslots)
 #define GX_DECODE_G(HH)                                                                                              \
     do {                                                                                                             \
         if (G == 1)                                                                                                  \
@@ -817,11 +847,11 @@ int launch_qwen_attention(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int
     // Scores: decode spreads the heads of a group over wavefronts (the key
     // rows are re-read from L2); a batch shares each key row among the group's
     // heads and 8 tokens.
-    const int GH = M <= 4 ? 1 : G, TT = M <= 4 ? 1 : 8;
+    const int GH = M <= 4 ? 1 : G, TT = M <= 4 || slots ? 1 : 8;
     const dim3 sgrid((unsigned)(S / kTile), (unsigned)(heads / GH), (unsigned)((M + TT - 1) / TT));
 #define GX_SCORES(HH)                                                                                                \
     attn_scores_kernel<HH><<<sgrid, 64, 0, ctx->stream>>>(qh, M, heads, G, GH, TT, positions, limit, kcache,       \
-                                                          context, scale, S, sc, tmax)
+                                                          context, scale, S, sc, tmax, slots, nslots, kv_heads)
     if (hd == 32)
         GX_SCORES(32);
     else if (hd == 64)
@@ -843,11 +873,13 @@ int launch_qwen_attention(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int
         NT *= 2;
     if (M > 4 && NT < 256)
         NT *= 2;
+    if (slots)  // a token tile is one token: its cache is its own
+        NT = G * kValSlice;
     const int TT2 = NT / (G * kValSlice);
     const dim3 vgrid((unsigned)(kv_heads * (hd / kValSlice)), (unsigned)((M + TT2 - 1) / TT2));
 #define GX_VALUES(N)                                                                                                 \
     attn_values_kernel<N><<<vgrid, N, 0, ctx->stream>>>(M, heads, G, hd, positions, limit, vcache, context,         \
-                                                        kv_heads, S, prob, q, scales, qsum)
+                                                        kv_heads, S, prob, q, scales, qsum, slots, nslots)
     if (NT == 32)
         GX_VALUES(32);
     else if (NT == 64)

@@ -108,13 +108,8 @@ class QwenModel:
         self.output_norm = dev(weights["output_norm"])
         cos, sin = rope_tables(cfg.head_dim, cfg.max_context, cfg.rope_base)
         self.rope_cos, self.rope_sin = dev(cos), dev(sin)
-        # keys in 16-byte pieces [kv_head][head_dim/8][context][8]; values
-        # transposed, [kv_head][head_dim][context]
-        self.context = (cfg.max_context + 7) // 8 * 8
-        kshape = (cfg.kv_heads, cfg.head_dim // 8, self.context, 8)
-        vshape = (cfg.kv_heads, cfg.head_dim, self.context)
-        self.kc = [torch.zeros(kshape, dtype=torch.int16, device="cuda") for _ in range(cfg.layers)]
-        self.vc = [torch.zeros(vshape, dtype=torch.int16, device="cuda") for _ in range(cfg.layers)]
+        # one conversation until set_slots says otherwise
+        self._make_caches(1)
 
         M = max_batch
         self.xs = torch.empty((M, cfg.dim), dtype=torch.float32, device="cuda")
@@ -129,12 +124,13 @@ class QwenModel:
         self.ffn = torch.empty((M, cfg.dim), dtype=torch.float32, device="cuda")
         self.hidden = torch.empty((M, cfg.dim), dtype=torch.float32, device="cuda")
         self.positions = torch.empty((M,), dtype=torch.int32, device="cuda")
+        self.slot_ids = torch.zeros((M,), dtype=torch.int32, device="cuda")  # each token's conversation
         self.tokens = torch.empty((M,), dtype=torch.int32, device="cuda")
-        self.k8 = torch.empty((1, cfg.dim), dtype=torch.int8, device="cuda")
-        self.ks = torch.empty((1, cfg.dim // 256), dtype=torch.float32, device="cuda")
-        self.bs = torch.empty((1, cfg.dim // 16), dtype=torch.int16, device="cuda")
-        self.logit = torch.empty((1, cfg.vocab), dtype=torch.float32, device="cuda")
-        self.next_id = torch.empty((1,), dtype=torch.int32, device="cuda")
+        self.k8 = torch.empty((M, cfg.dim), dtype=torch.int8, device="cuda")
+        self.ks = torch.empty((M, cfg.dim // 256), dtype=torch.float32, device="cuda")
+        self.bs = torch.empty((M, cfg.dim // 16), dtype=torch.int16, device="cuda")
+        self.logit = torch.empty((M, cfg.vocab), dtype=torch.float32, device="cuda")
+        self.next_id = torch.empty((M,), dtype=torch.int32, device="cuda")
         self.pos64 = torch.zeros((1,), dtype=torch.int64, device="cuda")  # the graph's position counter
         self.history = torch.zeros((cfg.max_context + 1,), dtype=torch.int32, device="cuda")
         self.graph = None
@@ -142,8 +138,39 @@ class QwenModel:
         self.attn_ws = torch.empty((n + 255) // 256 * 256, dtype=torch.uint8, device="cuda")
         self._vp, self._call = vp, call
 
+    def _make_caches(self, n):
+        """n conversations of max_context // n positions each (SetSlots,
+        qwen/slots.go:19-37).  Per layer, keys in 16-byte pieces
+        [slot][kv_head][head_dim/8][context][8] and values transposed
+        [slot][kv_head][head_dim][context]."""
+        cfg = self.cfg
+        self.nslots, self.slot = n, 0
+        self.slot_context = cfg.max_context // n
+        self.context = (self.slot_context + 7) // 8 * 8
+        kshape = (n, cfg.kv_heads, cfg.head_dim // 8, self.context, 8)
+        vshape = (n, cfg.kv_heads, cfg.head_dim, self.context)
+        self.kc = self.vc = None
+        self.kc = [torch.zeros(kshape, dtype=torch.int16, device="cuda") for _ in range(cfg.layers)]
+        self.vc = [torch.zeros(vshape, dtype=torch.int16, device="cuda") for _ in range(cfg.layers)]
+
+    def set_slots(self, n):
+        """SetSlots (qwen/slots.go:19-37): n independent conversations, each
+        holding max_context // n positions; replaces whatever was cached."""
+        if n < 1:
+            raise ValueError(f"qwen: {n} slots")
+        if self.cfg.max_context // n < 1:
+            raise ValueError(f"qwen: a context of {self.cfg.max_context} cut into {n} slots leaves no position each")
+        self.graph = None  # a captured step addressed the caches being replaced
+        self._make_caches(n)
+
+    def use_slot(self, i):
+        """UseSlot (qwen/slots.go:62-78): forward() goes to conversation i."""
+        if not 0 <= i < self.nslots:
+            raise IndexError(f"qwen: slot {i} of {self.nslots}")
+        self.slot = i
+
     def reset(self):
-        """Forget the conversation (Model.Reset): the caches are cleared."""
+        """Forget the conversations (Model.Reset): the caches are cleared."""
         for k, v in zip(self.kc, self.vc):
             k.zero_()
             v.zero_()
@@ -161,12 +188,34 @@ class QwenModel:
         if not torch.is_tensor(tokens):
             tokens = torch.tensor(np.asarray(tokens, dtype=np.int32), device="cuda")
         M = int(tokens.shape[0])
-        if M > self.max_batch or start_pos + M > cfg.max_context:
+        if M > self.max_batch or start_pos + M > self.slot_context:
             raise ValueError(f"qwen: {M} positions from {start_pos} exceed the batch {self.max_batch} "
-                             f"or the context {cfg.max_context}")
+                             f"or the context {self.slot_context}")
         self.tokens[:M].copy_(tokens)
         torch.arange(start_pos, start_pos + M, dtype=torch.int32, out=self.positions[:M])
+        if self.nslots > 1:
+            self.slot_ids[:M].fill_(self.slot)
         self._blocks(M, start_pos + M - 1)
+        return self.hidden[:M]
+
+    def forward_slots(self, tokens, slots, positions):
+        """ForwardSlots (qwen/place.go:33-41): token i at position
+        positions[i] of conversation slots[i], all in one pass over the
+        weights; each token's arithmetic is what it would be alone.  Returns
+        the device hidden states [M][dim] after the final norm."""
+        M = len(tokens)
+        if not (len(slots) == len(positions) == M) or M > self.max_batch or M == 0:
+            raise ValueError(f"qwen: {M} tokens, {len(slots)} slots, {len(positions)} positions "
+                             f"(batch {self.max_batch})")
+        for sl, pos in zip(slots, positions):
+            if not 0 <= sl < self.nslots:
+                raise IndexError(f"qwen: slot {sl} of {self.nslots}")
+            if not 0 <= pos < self.slot_context:
+                raise ValueError(f"qwen: position {pos} is past a slot's {self.slot_context}")
+        self.tokens[:M].copy_(torch.tensor(np.asarray(tokens, dtype=np.int32)))
+        self.positions[:M].copy_(torch.tensor(np.asarray(positions, dtype=np.int32)))
+        self.slot_ids[:M].copy_(torch.tensor(np.asarray(slots, dtype=np.int32)))
+        self._blocks(M, int(max(positions)))
         return self.hidden[:M]
 
     def _blocks(self, M, max_pos):
@@ -177,6 +226,7 @@ class QwenModel:
         if M == 1:
             return self._blocks_one(max_pos)
         qd, kvd = self.qd, self.kvd
+        sl = vp(self.slot_ids) if self.nslots > 1 else None
         for i, b in enumerate(self.blocks):
             add = None if i == 0 else vp(self.ffn)
             call("gx_norm_quant", ctx, vp(self.xs), cfg.dim, add, cfg.dim, vp(b["attn_norm"]), M, cfg.dim,
@@ -184,10 +234,11 @@ class QwenModel:
             self._mm(b["qkv"], self.x8, M, self.qkv, qd + 2 * kvd)
             call("gx_qwen_qk_rope", ctx, vp(self.qkv), qd + 2 * kvd, M, cfg.heads, cfg.kv_heads, cfg.head_dim,
                  vp(self.positions), vp(b["q_norm"]), vp(b["k_norm"]), vp(self.rope_cos), vp(self.rope_sin),
-                 np.float32(cfg.eps), vp(self.qh), vp(self.kc[i]), vp(self.vc[i]), self.context)
+                 np.float32(cfg.eps), vp(self.qh), vp(self.kc[i]), vp(self.vc[i]), self.context, sl, self.nslots)
             call("gx_qwen_attention", ctx, vp(self.qh), M, cfg.heads, cfg.kv_heads, cfg.head_dim,
                  max_pos, vp(self.positions), vp(self.kc[i]), vp(self.vc[i]), self.context,
-                 vp(self.set8.q), vp(self.set8.s), vp(self.set8.qs), vp(self.attn_ws), self.attn_ws.numel())
+                 vp(self.set8.q), vp(self.set8.s), vp(self.set8.qs), vp(self.attn_ws), self.attn_ws.numel(), sl,
+                 self.nslots)
             self._mm(b["o"], self.set8, M, self.attn, cfg.dim)
             call("gx_norm_quant", ctx, vp(self.xs), cfg.dim, vp(self.attn), cfg.dim, vp(b["ffn_norm"]), M, cfg.dim,
                  np.float32(cfg.eps), None, 0, vp(self.x8.q), vp(self.x8.s), vp(self.x8.qs))
@@ -205,6 +256,7 @@ class QwenModel:
         fused product's workgroups all read it while one writes x + add."""
         cfg, vp, call, ctx = self.cfg, self._vp, self._call, self.ctx.ptr
         qd, kvd = self.qd, self.kvd
+        sl = vp(self.slot_ids) if self.nslots > 1 else None
         eps = np.float32(cfg.eps)
         cur, other = self.xs, self.xs2
         for i, b in enumerate(self.blocks):
@@ -217,10 +269,11 @@ class QwenModel:
                 cur, other = other, cur
             call("gx_qwen_qk_rope", ctx, vp(self.qkv), qd + 2 * kvd, 1, cfg.heads, cfg.kv_heads, cfg.head_dim,
                  vp(self.positions), vp(b["q_norm"]), vp(b["k_norm"]), vp(self.rope_cos), vp(self.rope_sin),
-                 eps, vp(self.qh), vp(self.kc[i]), vp(self.vc[i]), self.context)
+                 eps, vp(self.qh), vp(self.kc[i]), vp(self.vc[i]), self.context, sl, self.nslots)
             call("gx_qwen_attention", ctx, vp(self.qh), 1, cfg.heads, cfg.kv_heads, cfg.head_dim,
                  max_pos, vp(self.positions), vp(self.kc[i]), vp(self.vc[i]), self.context,
-                 vp(self.set8.q), vp(self.set8.s), vp(self.set8.qs), vp(self.attn_ws), self.attn_ws.numel())
+                 vp(self.set8.q), vp(self.set8.s), vp(self.set8.qs), vp(self.attn_ws), self.attn_ws.numel(), sl,
+                 self.nslots)
             self._mm(b["o"], self.set8, 1, self.attn, cfg.dim)
             call("gx_norm_swiglu_q4_0", ctx, b["gu"].ptr, vp(cur), vp(self.attn), vp(b["ffn_norm"]), eps,
                  vp(other), vp(self.mid8.q), vp(self.mid8.s), vp(self.mid8.qs))
@@ -234,10 +287,10 @@ class QwenModel:
         at position self.pos64.  Leaves the next token in self.tokens[0] and
         in self.history[position + 1], and advances the position."""
         self.positions[:1].copy_(self.pos64)
-        self._blocks(1, self.cfg.max_context - 1)
+        self._blocks(1, self.slot_context - 1)
         self.next_token(0)
-        self.history.index_copy_(0, self.pos64 + 1, self.next_id)
-        self.tokens[:1].copy_(self.next_id)
+        self.history.index_copy_(0, self.pos64 + 1, self.next_id[:1])
+        self.tokens[:1].copy_(self.next_id[:1])
         self.pos64.add_(1)
 
     def capture_decode(self):
@@ -245,6 +298,8 @@ class QwenModel:
         is the capture stream while recording."""
         if self.graph is not None:
             return
+        if self.nslots > 1:
+            raise ValueError("qwen: the captured decode step serves one conversation")
         torch.cuda.synchronize()
         stream = torch.cuda.Stream()
         graph = torch.cuda.CUDAGraph()
@@ -274,12 +329,78 @@ class QwenModel:
              vp(self.logit), cfg.vocab)
         return self.logit[0]
 
+    def start_slots(self, tokens, positions):
+        """Seeds lock-step decoding of conversations 0 .. n-1: token i (a
+        host id, or a device int32 tensor of n ids) at position positions[i]
+        of slot i."""
+        n = len(positions)
+        if not 0 < n <= min(self.nslots, self.max_batch):
+            raise ValueError(f"qwen: {n} conversations for {self.nslots} slots")
+        if max(positions) >= self.slot_context:
+            raise ValueError(f"qwen: position {max(positions)} is past a slot's {self.slot_context}")
+        t = tokens if torch.is_tensor(tokens) else torch.tensor(np.asarray(tokens, dtype=np.int32))
+        self.tokens[:n].copy_(t)
+        self.positions[:n].copy_(torch.tensor(np.asarray(positions, dtype=np.int32)))
+        if self.nslots > 1:
+            self.slot_ids[:n].copy_(torch.arange(n, dtype=torch.int32))
+        self._slot_pos = list(positions)
+
+    def slots_step(self, n):
+        """One lock-step decode step of conversations 0 .. n-1 from the
+        tokens and positions on the device (the server's batch of slots,
+        cmd/golem-server/runner.go:233-297): one pass over the weights and one
+        head read for all n; the next ids replace the tokens (and stay in
+        next_id[:n]) and every position advances."""
+        top = max(self._slot_pos)
+        if top >= self.slot_context:
+            raise ValueError(f"qwen: position {top} is past a slot's {self.slot_context}")
+        self._blocks(n, top)
+        self.next_tokens(range(n))
+        self.tokens[:n].copy_(self.next_id[:n])
+        self.positions[:n].add_(1)
+        self._slot_pos = [p + 1 for p in self._slot_pos]
+        return self.next_id[:n]
+
+    def logits_batch(self, rows):
+        """LogitsBatch (qwen/model.go:200-214): the logits of several hidden
+        states of the last forward in one read of the head; device [n][vocab]
+        (reused storage), each row what logits() gives it alone."""
+        cfg, vp, call, ctx = self.cfg, self._vp, self._call, self.ctx.ptr
+        rows = list(rows)
+        n = len(rows)
+        if not 0 < n <= self.max_batch:
+            raise ValueError(f"qwen: {n} states for a batch of {self.max_batch}")
+        if rows == list(range(rows[0], rows[0] + n)):
+            h = self.hidden[rows[0]:rows[0] + n]
+        else:
+            h = self.attn[:n]  # free once the blocks are done
+            h.copy_(self.hidden[rows])
+        if self.head_quant == capi.Q4_0:
+            a = self.x8
+            call("gx_quantize_q8_0", ctx, vp(h), cfg.dim, n, cfg.dim, vp(a.q), vp(a.s), vp(a.qs), None, None)
+            call("gx_matmul_q4_0", ctx, self.embd.ptr, vp(a.q), vp(a.s), vp(a.qs), None, n, 0, cfg.vocab, None,
+                 vp(self.logit), cfg.vocab)
+        else:
+            call("gx_quantize_q8_k", ctx, vp(h), cfg.dim, n, cfg.dim, vp(self.k8), vp(self.ks), vp(self.bs))
+            call("gx_matmul_q6_k", ctx, self.embd.ptr, vp(self.k8), vp(self.ks), vp(self.bs), n, 0, cfg.vocab, None,
+                 vp(self.logit), cfg.vocab)
+        return self.logit[:n]
+
+    def next_tokens(self, rows):
+        """The greedy ids after several hidden states (one head read), left
+        on the device: next_id[:n]."""
+        n = len(list(rows))
+        self.logits_batch(rows)
+        self._call("gx_argmax", self.ctx.ptr, self._vp(self.logit), self.cfg.vocab, n, self.cfg.vocab,
+                   self._vp(self.next_id))
+        return self.next_id[:n]
+
     def next_token(self, row):
         """The greedy id after hidden state `row`, left on the device."""
         self.logits(row)
         self._call("gx_argmax", self.ctx.ptr, self._vp(self.logit), self.cfg.vocab, 1, self.cfg.vocab,
                    self._vp(self.next_id))
-        return self.next_id
+        return self.next_id[:1]
 
     def greedy(self, prompt, steps, graph=False):
         """The prompt in one batch, then `steps` greedy tokens, each fed back

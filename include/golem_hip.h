@@ -266,10 +266,17 @@ int gx_norm_quant(gx_ctx *ctx, float *x, int ldx, const float *add, int lda, con
  * consecutive positions contiguous), the value transposed at
  * vcache[kv_head][e][positions[m]] (a value row holds one element of a head
  * over all positions).  positions[m] < context; head_dim a multiple of 8.
- * All device pointers; positions: M int32. */
+ * All device pointers; positions: M int32.
+ * Slots (qwen/slots.go, qwen/place.go): with `slots` (M device int32) the
+ * caches hold nslots conversations of `context` positions one after another
+ * ([slot][kv_head]... of the layouts above) and position m belongs to
+ * conversation slots[m] -- golem's Place{Cache: Slot(slots[m]), Pos}.  A slot
+ * out of range stores nothing and leaves the position's query NaN.  NULL:
+ * one conversation. */
 int gx_qwen_qk_rope(gx_ctx *ctx, const float *qkv, int ldqkv, int M, int heads, int kv_heads, int head_dim,
                     const int32_t *positions, const float *q_norm, const float *k_norm, const float *rope_cos,
-                    const float *rope_sin, float eps, uint16_t *qh, uint16_t *kcache, uint16_t *vcache, int context);
+                    const float *rope_sin, float eps, uint16_t *qh, uint16_t *kcache, uint16_t *vcache, int context,
+                    const int32_t *slots, int nslots);
 
 /* Device bytes of the workspace gx_qwen_attention needs for M positions of
  * `heads` query heads whose positions are at most max_pos. */
@@ -282,10 +289,13 @@ int gx_qwen_attention_workspace_bytes(int M, int heads, int max_pos, size_t *byt
  * DotF32, SoftmaxInPlace, probabilities rounded to fp16, values summed by
  * Axpy in position order; the heads' outputs [M][heads*head_dim] quantised to
  * Q8_0 into q/scales/qsum for the output projection.  workspace: 256-byte
- * aligned device memory of gx_qwen_attention_workspace_bytes. */
+ * aligned device memory of gx_qwen_attention_workspace_bytes.  slots /
+ * nslots as for gx_qwen_qk_rope: position m reads only conversation
+ * slots[m]'s cache (ForwardMixed, qwen/model.go:131-172). */
 int gx_qwen_attention(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int kv_heads, int head_dim, int max_pos,
                       const int32_t *positions, const uint16_t *kcache, const uint16_t *vcache, int context,
-                      int8_t *q, float *scales, int32_t *qsum, void *workspace, size_t workspace_bytes);
+                      int8_t *q, float *scales, int32_t *qsum, void *workspace, size_t workspace_bytes,
+                      const int32_t *slots, int nslots);
 
 /* One position's RMSNormPlain + Q8_0 fused into the Q4_0 product that reads
  * it (M = 1): y[row] for rows [row_start, row_end) of w times

@@ -192,7 +192,7 @@ def test_qk_rope_and_cache_bit_exact(dev, orc, hd, heads, kv):
     ins = [dev.put(a) for a in (qkv, pos, qn, kn, cos, sin)]
     capi.call("gx_qwen_qk_rope", dev.ctx.ptr, capi.vp(ins[0]), width, M, heads, kv, hd, capi.vp(ins[1]),
               capi.vp(ins[2]), capi.vp(ins[3]), capi.vp(ins[4]), capi.vp(ins[5]), np.float32(1e-6), capi.vp(qh),
-              capi.vp(kc), capi.vp(vc), ctx_len)
+              capi.vp(kc), capi.vp(vc), ctx_len, None, 0)
     got_q = dev.get(qh).view(np.float16).astype(np.float32)
     got_k = kc.cpu().numpy().view(np.float16).astype(np.float32)
     got_v = vc.cpu().numpy().view(np.float16).astype(np.float32)
@@ -248,7 +248,8 @@ def test_attention_bit_exact(dev, orc, hd, heads, kv, ctx_len, batch):
     ws = dev.empty((n,), np.uint8)
     ins = [dev.put(a) for a in (qf.view(np.int16), pos, kt.view(np.int16), vt.view(np.int16))]
     capi.call("gx_qwen_attention", dev.ctx.ptr, capi.vp(ins[0]), M, heads, kv, hd, int(pos.max()), capi.vp(ins[1]),
-              capi.vp(ins[2]), capi.vp(ins[3]), context, capi.vp(q8), capi.vp(sc), capi.vp(qs), capi.vp(ws), n)
+              capi.vp(ins[2]), capi.vp(ins[3]), context, capi.vp(q8), capi.vp(sc), capi.vp(qs), capi.vp(ws), n,
+              None, 0)
     lib = orc.load()
     K32, V32 = np.ascontiguousarray(kcf.astype(np.float32)), np.ascontiguousarray(vcf.astype(np.float32))
     scale = np.float32(1 / math.sqrt(float(hd)))
@@ -275,11 +276,13 @@ def test_attention_refuses_bad_caches(dev):
     args = [capi.vp(buf), M, heads, kv, hd, 15, capi.vp(buf), capi.vp(buf), capi.vp(buf)]
     outs = [capi.vp(buf), capi.vp(buf), capi.vp(buf), capi.vp(ws)]
     with pytest.raises(capi.GxError):  # a context that is not a multiple of 8
-        capi.call("gx_qwen_attention", dev.ctx.ptr, *args, 20, *outs, n)
+        capi.call("gx_qwen_attention", dev.ctx.ptr, *args, 20, *outs, n, None, 0)
     with pytest.raises(capi.GxError):  # max_pos beyond the context
-        capi.call("gx_qwen_attention", dev.ctx.ptr, *args, 8, *outs, n)
+        capi.call("gx_qwen_attention", dev.ctx.ptr, *args, 8, *outs, n, None, 0)
     with pytest.raises(capi.GxError):  # a workspace too small
-        capi.call("gx_qwen_attention", dev.ctx.ptr, *args, 16, *outs, n - 256)
+        capi.call("gx_qwen_attention", dev.ctx.ptr, *args, 16, *outs, n - 256, None, 0)
+    with pytest.raises(capi.GxError):  # slots without a count
+        capi.call("gx_qwen_attention", dev.ctx.ptr, *args, 16, *outs, n, capi.vp(buf), 0)
 
 
 @pytest.mark.parametrize("rows,K,span", [(6144, 2560, None), (19456, 2560, None), (200, 2080, (3, 131)),
