@@ -123,6 +123,114 @@ __global__ __launch_bounds__(1024) void q4_0_matvec_kernel(
     }
 }
 
+// One column (M = 1) of a matrix with few tiles, spread over more CUs: grid
+// (tiles, splits), each workgroup kSplitWaves wavefronts taking one stretch
+// each (stretch s = split * kSplitWaves + wave).  The stretch sums go to the
+// context's workspace [tile][S][64]; a tile's last workgroup to arrive (a
+// counter per tile, returned to 0 by that workgroup) adds them in stretch
+// order from 0 -- the single-workgroup kernel's sum, bit for bit.  The sums
+// travel as agent-scope (write-through, L2-bypassing) stores and loads.
+constexpr int kSplitWaves = 8;
+__global__ __launch_bounds__(64 * kSplitWaves) void q4_0_matvec_split_kernel(
+    const uint8_t *__restrict__ W, size_t plane0_bytes, int B, int DC, const int8_t *__restrict__ q,
+    const float *__restrict__ scales, const int32_t *__restrict__ qsum, int tile0, int row_start, int row_end,
+    const float *__restrict__ bias, float *__restrict__ y, float *__restrict__ ws, uint32_t *__restrict__ count) {
+    __shared__ uint32_t ticket;
+    const int S = (B + kStretch - 1) / kStretch;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int tile = tile0 + blockIdx.x;
+    const int s = blockIdx.y * kSplitWaves + wave;
+    float *wst = ws + (size_t)blockIdx.x * S * kTileRows;
+    if (s < S) {
+        const uint8_t *qs_row = W + ((size_t)tile * B * kTileRows + lane) * kChunk;
+        const uint8_t *d_row = W + plane0_bytes + ((size_t)tile * DC * kTileRows + lane) * kChunk;
+        const int b0 = s * kStretch;
+        const int nb = min(kStretch, B - b0);
+        uint4 wq[kStretch];
+#pragma unroll
+        for (int j = 0; j < kStretch; j++)
+            wq[j] = load_stream(qs_row + (size_t)min(b0 + j, B - 1) * kTileRows * kChunk);
+        const uint4 dch = *(const uint4 *)(d_row + (size_t)s * kTileRows * kChunk);
+        float p = 0.0f;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            int4 a0[4], a1[4];
+            int32_t qs[4];
+            float sa[4];
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) {
+                const int b = min(b0 + 4 * h + jj, B - 1);
+                const int4 *a = (const int4 *)(q + (size_t)b * kQ4Block);
+                a0[jj] = a[0];
+                a1[jj] = a[1];
+                qs[jj] = qsum[b];
+                sa[jj] = scales[b];
+            }
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) {
+                const int j = 4 * h + jj;
+                if (j < nb) {
+                    const int32_t isum = q4_0_block_isum(wq[j], a0[jj], a1[jj], qs[jj]);
+                    const float sc = chunk_half(dch, j) * sa[jj];
+                    p = fmaf((float)isum, sc, p);
+                }
+            }
+        }
+        // written through to the agent's coherence point (an agent-scope store)
+        __hip_atomic_store(&wst[(size_t)s * kTileRows + lane], p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    // The stores have completed (vmcnt 0) before the workgroup counts itself.
+    // A release fence would also write back the whole L2, which costs more
+    // than the product; every value published here is already written through.
+    __builtin_amdgcn_s_waitcnt((0 & 15) | (7 << 4) | (15 << 8));
+    __syncthreads();
+    if (threadIdx.x == 0)
+        ticket = __hip_atomic_fetch_add(&count[blockIdx.x], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (ticket != gridDim.y - 1)
+        return;
+    // The last workgroup: its wavefronts bring every split's sums into LDS,
+    // eight stretches each per round, with loads carrying the agent scope bit
+    // (sc1, coherent like the stores; written out, since the compiler keeps
+    // atomic loads one at a time).  Reads past S land in the workspace's
+    // padding and are not used.
+    extern __shared__ float sums[];  // [S][64]
+    for (int t0 = wave * 8; t0 < S; t0 += kSplitWaves * 8) {
+        const float *src = wst + (size_t)t0 * kTileRows + lane;
+        float v0, v1, v2, v3, v4, v5, v6, v7;
+        asm volatile(
+            "global_load_dword %0, %8, off sc1\n\t"
+            "global_load_dword %1, %8, off offset:256 sc1\n\t"
+            "global_load_dword %2, %8, off offset:512 sc1\n\t"
+            "global_load_dword %3, %8, off offset:768 sc1\n\t"
+            "global_load_dword %4, %8, off offset:1024 sc1\n\t"
+            "global_load_dword %5, %8, off offset:1280 sc1\n\t"
+            "global_load_dword %6, %8, off offset:1536 sc1\n\t"
+            "global_load_dword %7, %8, off offset:1792 sc1\n\t"
+            "s_waitcnt vmcnt(0)"
+            : "=&v"(v0), "=&v"(v1), "=&v"(v2), "=&v"(v3), "=&v"(v4), "=&v"(v5), "=&v"(v6), "=&v"(v7)
+            : "v"(src)
+            : "memory");
+        const float v[8] = {v0, v1, v2, v3, v4, v5, v6, v7};
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            if (t0 + j < S)
+                sums[(t0 + j) * kTileRows + lane] = v[j];
+    }
+    __syncthreads();
+    if (wave != 0)
+        return;
+    const int row = tile * kTileRows + lane;
+    float acc = 0.0f;
+    for (int t = 0; t < S; t++)  // stretch order, from 0
+        acc = acc + sums[t * kTileRows + lane];
+    if (row >= row_start && row < row_end)
+        y[row] = bias ? acc + bias[row] : acc;
+    if (lane == 0)
+        __hip_atomic_store(&count[blockIdx.x], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // The per-block integers of the kernel above, for the parity tests: one
 // thread per (m, row, block), through the same q4_0_block_isum.
 __global__ void q4_0_block_dots_kernel(const uint8_t *__restrict__ W, int B, const int8_t *__restrict__ q,
@@ -352,6 +460,24 @@ __global__ __launch_bounds__(1024) void q4_0_matvec_fused_kernel(
 int launch_q4_0_matvec(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, const int8_t *q, const float *scales,
                        const int32_t *qsum, int M, int row_start, int row_end, const float *bias, float *y,
                        int ldy) {
+    // One column of a matrix with few tiles and long rows: the stretches of a
+    // tile over several workgroups, so that more CUs pull weights.
+    {
+        const int B = w->blocks, S = (B + kStretch - 1) / kStretch;
+        const int tile0 = row_start / kTileRows;
+        const int tiles = (row_end + kTileRows - 1) / kTileRows - tile0;
+        const int splits = (S + kSplitWaves - 1) / kSplitWaves;
+        // worth it once a single workgroup's wavefronts would each take more
+        // than one stretch
+        if (M == 1 && S > 16 && tiles * 4 <= ctx->cu_count && tiles <= kSplitTiles &&
+            (size_t)tiles * S * kTileRows <= kSplitWsFloats && S * kTileRows * sizeof(float) <= 64 * 1024) {
+            q4_0_matvec_split_kernel<<<dim3((unsigned)tiles, (unsigned)splits), 64 * kSplitWaves,
+                                       (size_t)S * kTileRows * sizeof(float), ctx->stream>>>(
+                mat, w->plane0_bytes, B, w->dchunks, q, scales, qsum, tile0, row_start, row_end, bias, y,
+                ctx->split_ws, ctx->split_count);
+            return check_launch("q4_0_matvec_split");
+        }
+    }
     // Columns in groups of 8, 4, 2, 1, each group reading the weights once;
     // the per-column arithmetic is the same whatever the group.  Very wide
     // rows keep the group narrow enough for the stretch sums to fit in LDS.

@@ -182,3 +182,23 @@ def test_errors_are_golem_panics(dev):
     act = dev.quantize_q8_0(synth.activations(g, 1, 64), with_corr=False)
     with pytest.raises(capi.GxError, match="out of"):
         dev.matmul_q4_0(wd, act, 1, 0, 5)
+
+
+@pytest.mark.parametrize("rows,cols", [(2560, 9728), (200, 8192), (64, 4352)])
+def test_split_matvec_equals_one_workgroup(dev, rows, cols):
+    """A long row of few tiles, one column, runs split over several
+    workgroups whose stretch sums meet through the workspace (the tile's last
+    workgroup adds them).  Launched again and again (the arrival counters go
+    back to 0 each time), every result equals, bit for bit, column 0 of a
+    two-column product, which one workgroup per tile computes."""
+    g = synth.rng(300 + rows)
+    w = synth.q4_0_weights(g, rows, cols)
+    wd = dev.weight(w, capi.Q4_0, rows, cols)
+    log(f"split matvec rows={rows} cols={cols}")
+    for it in range(40):
+        x = synth.activations(g, 2, cols)
+        act = dev.quantize_q8_0(x, with_corr=False)
+        one = dev.get(dev.matmul_q4_0(wd, [a[:1] for a in act[:3]] + [None], 1))
+        two = dev.get(dev.matmul_q4_0(wd, act, 2))
+        np.testing.assert_array_equal(one[0].view(np.uint32), two[0].view(np.uint32), err_msg=f"launch {it}")
+    wd.free()
