@@ -63,6 +63,8 @@ _SIGNATURES = {
     "gx_qwen_qk_rope": [_vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _vp, ctypes.c_float,
                         _vp, _vp, _vp, _c_int, _vp, _c_int],
     "gx_qwen_attention_workspace_bytes": [_c_int, _c_int, _c_int, ctypes.POINTER(_c_size)],
+    "gx_qwen_rope_attention": [_vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _vp,
+                               ctypes.c_float, _vp, _vp, _c_int, _vp, _vp, _vp, _vp, _c_int],
     "gx_qwen_attention": [_vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _c_int, _vp, _vp, _vp,
                           _vp, _c_size, _vp, _c_int],
     "gx_swiglu_quant": [_vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp],

@@ -590,6 +590,30 @@ int gx_qwen_qk_rope(gx_ctx *ctx, const float *qkv, int ldqkv, int M, int heads, 
     return ok();
 }
 
+int gx_qwen_rope_attention(gx_ctx *ctx, const float *qkv, int ldqkv, int heads, int kv_heads, int head_dim,
+                           int max_pos, const int32_t *positions, const float *q_norm, const float *k_norm,
+                           const float *rope_cos, const float *rope_sin, float eps, uint16_t *kcache,
+                           uint16_t *vcache, int context, int8_t *q, float *scales, int32_t *qsum,
+                           const int32_t *slots, int nslots) {
+    if (int rc = use(ctx))
+        return rc;
+    GX_CHECK(heads > 0 && kv_heads > 0 && heads % kv_heads == 0, "gx: %d query heads over %d key-value heads", heads,
+             kv_heads);
+    GX_CHECK(ldqkv >= (heads + 2 * kv_heads) * head_dim && max_pos >= 0, "gx: bad batch shape");
+    GX_CHECK(context % 8 == 0 && max_pos < context, "gx: a cache of %d positions (a multiple of 8) cannot hold %d",
+             context, max_pos);
+    GX_CHECK(qkv && positions && q_norm && k_norm && rope_cos && rope_sin && kcache && vcache && q && scales && qsum,
+             "gx: missing argument");
+    GX_CHECK(((uintptr_t)vcache & 15) == 0, "gx: the value cache must be 16-byte aligned");
+    GX_CHECK(!slots || nslots > 0, "gx: %d slots", nslots);
+    const float scale = (float)(1.0 / sqrt((double)head_dim));
+    if (int rc = gx::launch_qwen_rope_attention(ctx, qkv, ldqkv, heads, kv_heads, head_dim, max_pos, positions, q_norm,
+                                                k_norm, rope_cos, rope_sin, eps, kcache, vcache, context, scale, q,
+                                                scales, qsum, slots, nslots))
+        return rc;
+    return ok();
+}
+
 int gx_qwen_attention_workspace_bytes(int M, int heads, int max_pos, size_t *bytes) {
     GX_CHECK(M >= 0 && heads > 0 && max_pos >= 0 && bytes, "gx: bad attention shape");
     *bytes = gx::qwen_attention_workspace(M, heads, max_pos);

@@ -307,11 +307,18 @@ __global__ __launch_bounds__(1024) void q4_0_matvec_fused_kernel(
 
     // x (+ add) into registers first, then the weights of the wavefront's
     // first two stretch slots, so that the staging waits only for x and add.
-    float xv[kFusedRegs];
+    // All sixteen loads are issued before the first wait: x and add in
+    // separate unconditional loops (add is uniform), so that staging costs
+    // one cache round trip rather than one per element.  Then the weight
+    // loads are issued, and only then is the sum formed.
+    float xv[kFusedRegs], av[kFusedRegs];
 #pragma unroll
-    for (int r = 0; r < kFusedRegs; r++) {
-        const int i = min(tid + r * (int)blockDim.x, K - 1);
-        xv[r] = add ? x[i] + add[i] : x[i];
+    for (int r = 0; r < kFusedRegs; r++)
+        xv[r] = x[min(tid + r * (int)blockDim.x, K - 1)];
+    if (add) {
+#pragma unroll
+        for (int r = 0; r < kFusedRegs; r++)
+            av[r] = add[min(tid + r * (int)blockDim.x, K - 1)];
     }
     // A wavefront's slot k is stretch wave + k*nwaves; every wavefront runs
     // the same number of slots (a slot past S loads stretch S - 1 again and
@@ -331,6 +338,11 @@ __global__ __launch_bounds__(1024) void q4_0_matvec_fused_kernel(
     GX_FU_LOAD(wa, da, ga, wave);
     if (DB && slots > 1)
         GX_FU_LOAD(wb, db, gb, wave + nwaves);
+    if (add) {
+#pragma unroll
+        for (int r = 0; r < kFusedRegs; r++)
+            xv[r] = xv[r] + av[r];
+    }
 #pragma unroll
     for (int r = 0; r < kFusedRegs; r++) {
         const int i = tid + r * (int)blockDim.x;

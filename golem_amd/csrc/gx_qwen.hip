@@ -496,12 +496,30 @@ constexpr int kDecodeRegs = kValSlice * (kDecodeMax / 8) / kDecodeThreads;  // v
 constexpr int kDecodeRows = (kDecodeMax + kDecodeThreads - 1) / kDecodeThreads;  // positions per thread
 constexpr int kScoreStride = kDecodeMax + 20;  // score rows 20 banks apart (conflict-free serial sums), read to n + 15
 
-template <int HD, int G>
+//
+// FUSE (one position, M = 1): the kernel also does qwen_qk_rope_kernel's work
+// for that position.  Every workgroup stages its G query heads and its key
+// head from the Q|K|V product, takes each head's norm (head_norm_scale, a
+// lane per head) and rotates it with the same expressions, so the fp16 query
+// and key are qwen_qk_rope_kernel's bit for bit; the query goes straight to
+// LDS.  The new key and value are stored to the caches (the key by the
+// head's first slice, each slice its 32 value elements) for later
+// positions, and this position's own score and value term use the computed
+// copies, never the cache entries being written.
+struct QkRope {
+    const float *qkv;
+    int ldqkv;
+    const float *q_norm, *k_norm, *rope_cos, *rope_sin;
+    float eps;
+    uint16_t *kcache, *vcache;  // the caches the position is stored into
+};
+
+template <int HD, int G, bool FUSE>
 __global__ __launch_bounds__(kDecodeThreads) void attn_decode_kernel(
     const uint16_t *__restrict__ qh, int heads, int kv_heads, const int32_t *__restrict__ positions, int limit,
-    const uint16_t *__restrict__ kcache, const uint16_t *__restrict__ vcache, int context, float scale,
+    const uint16_t *kcache, const uint16_t *vcache, int context, float scale,
     int8_t *__restrict__ q, float *__restrict__ scales, int32_t *__restrict__ qsum,
-    const int32_t *__restrict__ slots, int nslots) {
+    const int32_t *__restrict__ slots, int nslots, QkRope fz) {
     // LDS: region A holds the scores [G][kScoreStride] floats, later the value
     // slice [32][kDecodeStride] halves; then the probabilities [G][kDecodeStride]
     // halves and the queries [G][HD] halves.
@@ -518,12 +536,19 @@ __global__ __launch_bounds__(kDecodeThreads) void attn_decode_kernel(
     constexpr int slices = HD / kValSlice;
     const int kvh = blockIdx.x / slices, d0 = (blockIdx.x - kvh * slices) * kValSlice;
     const int t = blockIdx.y;
-    const int n = min(positions[t] + 1, limit);
+    const int pos = positions[t];
+    const int n = min(pos + 1, limit);
     const int groups = (n + 7) / 8, pieces = kValSlice * groups;
+    bool store = true;  // FUSE: the position belongs to a conversation and is stored
     if (slots) {  // the token's own conversation; reads stay inside the caches
         const size_t at = (size_t)min(max(slots[t], 0), nslots - 1) * kv_heads * HD * context;
         kcache += at;
         vcache += at;
+        if (FUSE) {
+            store = slots[t] >= 0 && slots[t] < nslots;
+            fz.kcache += at;
+            fz.vcache += at;
+        }
     }
 
     // The G queries (adjacent heads of the row) first, then the key pieces of
@@ -531,7 +556,7 @@ __global__ __launch_bounds__(kDecodeThreads) void attn_decode_kernel(
     // 16 bytes = 8 positions a piece): the queries can be stored while the
     // rest is in flight.
     const uint32_t *qg = (const uint32_t *)(qh + ((size_t)t * heads + kvh * G) * HD);
-    uint32_t qr = qg[min(tid, G * HD / 2 - 1)];
+    const uint32_t qr = FUSE ? 0u : qg[min(tid, G * HD / 2 - 1)];
     v4u_stream k[kDecodeRows][HD / 8];
     const v4u_stream *kbase = (const v4u_stream *)(kcache + (size_t)kvh * HD * context);
 #pragma unroll
@@ -550,9 +575,79 @@ __global__ __launch_bounds__(kDecodeThreads) void attn_decode_kernel(
         vr[u] = *(const v4u_stream *)(vrow + (size_t)rr * context + 8 * c);
     }
     static_assert(G * HD / 2 <= kDecodeThreads, "one query dword per thread");
-    if (tid < G * HD / 2)
-        ql[tid] = qr;
-    __syncthreads();
+    // FUSE: the new key, fp16, at the end of region A (scores use its front)
+    uint16_t *nk = (uint16_t *)(lds + kValSlice * kDecodeStride * 2 - HD * 2);
+    float nv = 0.0f;  // FUSE: this thread's value element (tid < 32)
+    if (FUSE) {
+        static_assert(G * kScoreStride * 4 + 64 <= kValSlice * kDecodeStride * 2 - HD * 2, "scores clear the key");
+        static_assert((G + 1) * HD * 4 <= kValSlice * kDecodeStride * 2 - HD * 2, "staged heads fit region A");
+        // the G query heads and the key head (fp32) into region A, all loads
+        // before the first store; the slice's value elements into registers
+        float *hh = (float *)lds;
+        __shared__ float hs[G + 1];
+        const float *row = fz.qkv + (size_t)t * fz.ldqkv;
+        constexpr int kRounds = ((G + 1) * HD + kDecodeThreads - 1) / kDecodeThreads;
+        float hv[kRounds];
+#pragma unroll
+        for (int r = 0; r < kRounds; r++) {
+            const int i = min(tid + r * kDecodeThreads, (G + 1) * HD - 1);
+            hv[r] = row[i < G * HD ? kvh * G * HD + i : heads * HD + kvh * HD + (i - G * HD)];
+        }
+        nv = row[(heads + kv_heads) * HD + kvh * HD + d0 + (tid & (kValSlice - 1))];
+#pragma unroll
+        for (int r = 0; r < kRounds; r++)
+            hh[min(tid + r * kDecodeThreads, (G + 1) * HD - 1)] = hv[r];
+        __syncthreads();
+        if (tid <= G)
+            hs[tid] = head_norm_scale(hh + tid * HD, HD, fz.eps);
+        __syncthreads();
+        // normed, then rotated in pairs (i, i + HD/2): RoPETable.Apply,
+        // nn/rope.go:62-73, as qwen_qk_rope_kernel
+        constexpr int half = HD / 2;
+        uint16_t *qlh = (uint16_t *)ql;
+        for (int i = tid; i < (G + 1) * half; i += kDecodeThreads) {
+            const int w = i / half, j = i - w * half;
+            const float sc = hs[w];
+            const float *gain = w < G ? fz.q_norm : fz.k_norm;
+            const float re0 = hh[w * HD + j], im0 = hh[w * HD + j + half];
+            const float re = (re0 * sc) * gain[j], im = (im0 * sc) * gain[j + half];
+            const float c = fz.rope_cos[(size_t)pos * half + j], sn = fz.rope_sin[(size_t)pos * half + j];
+            const float a = re * c - im * sn;
+            const float b = re * sn + im * c;
+            uint16_t ha = (uint16_t)float_to_half_bits(a), hb = (uint16_t)float_to_half_bits(b);
+            if (w < G) {
+                if (!store)  // no conversation: the query is NaN
+                    ha = hb = 0x7E00;
+                qlh[w * HD + j] = ha;
+                qlh[w * HD + j + half] = hb;
+            } else {
+                nk[j] = ha;
+                nk[j + half] = hb;
+                if (store && d0 == 0) {
+                    uint16_t *kt = fz.kcache + (size_t)kvh * HD * context + (size_t)pos * 8;
+                    kcache_put(kt, context, j, ha);
+                    kcache_put(kt, context, j + half, hb);
+                }
+            }
+        }
+        if (store && tid < kValSlice)
+            fz.vcache[((size_t)kvh * HD + d0 + tid) * context + pos] = (uint16_t)float_to_half_bits(nv);
+        __syncthreads();
+        // this position's key from the copy, not the cache entry being written
+        if (pos == n - 1) {
+#pragma unroll
+            for (int r = 0; r < kDecodeRows; r++)
+                if (tid + r * kDecodeThreads == pos) {
+#pragma unroll
+                    for (int i = 0; i < HD / 8; i++)
+                        k[r][i] = ((const v4u_stream *)nk)[i];
+                }
+        }
+    } else {
+        if (tid < G * HD / 2)
+            ql[tid] = qr;
+        __syncthreads();
+    }
 
     // scores, DotF32's four chains: element e of a head goes to chain e % 4
     float mx[G];
@@ -622,6 +717,11 @@ __global__ __launch_bounds__(kDecodeThreads) void attn_decode_kernel(
             const int rr = i / groups, c = i - rr * groups;
             *(v4u_stream *)(vs + rr * kDecodeStride + 8 * c) = vr[u];
         }
+    }
+    if (FUSE && pos == n - 1) {
+        __syncthreads();  // the staged pieces first, then this position's values over them
+        if (tid < kValSlice)
+            vs[tid * kDecodeStride + pos] = (uint16_t)float_to_half_bits(nv);
     }
     __syncthreads();
     if (tid < G * kValSlice) {
@@ -818,9 +918,9 @@ int launch_qwen_attention(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int
     // several conversations (slots), whose caches share nothing.
     if ((M <= 4 || slots) && limit <= kDecodeMax) {
 #define GX_DECODE(HH, GG)                                                                                            \
-    attn_decode_kernel<HH, GG><<<dim3((unsigned)(kv_heads * (HH / kValSlice)), (unsigned)M), kDecodeThreads, 0,      \
-                                 ctx->stream>>>(qh, heads, kv_heads, positions, limit, kcache, vcache, context,      \
-                                                scale, q, scales, qsum, slots, nslots)
+    attn_decode_kernel<HH, GG, false><<<dim3((unsigned)(kv_heads * (HH / kValSlice)), (unsigned)M), kDecodeThreads,  \
+                                        0, ctx->stream>>>(qh, heads, kv_heads, positions, limit, kcache, vcache,      \
+                                                          context, scale, q, scales, qsum, slots, nslots, QkRope{})
 #define GX_DECODE_G(HH)                                                                                              \
     do {                                                                                                             \
         if (G == 1)                                                                                                  \
@@ -890,6 +990,45 @@ int launch_qwen_attention(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int
         GX_VALUES(256);
 #undef GX_VALUES
     return check_launch("qwen_attention values");
+}
+
+int launch_qwen_rope_attention(gx_ctx *ctx, const float *qkv, int ldqkv, int heads, int kv_heads, int hd,
+                               int max_pos, const int32_t *positions, const float *q_norm, const float *k_norm,
+                               const float *rope_cos, const float *rope_sin, float eps, uint16_t *kcache,
+                               uint16_t *vcache, int context, float scale, int8_t *q, float *scales, int32_t *qsum,
+                               const int32_t *slots, int nslots) {
+    const int G = heads / kv_heads;
+    GX_CHECK(hd == 32 || hd == 64 || hd == 96 || hd == 128, "gx: attention supports head widths 32, 64, 96 and 128");
+    GX_CHECK(G == 1 || G == 2 || G == 4 || G == 8, "gx: %d query heads per key-value head unsupported", G);
+    const int limit = max_pos + 1;
+    GX_CHECK(limit <= kDecodeMax, "gx: the fused attention reads at most %d positions, not %d", kDecodeMax, limit);
+    const QkRope fz{qkv, ldqkv, q_norm, k_norm, rope_cos, rope_sin, eps, kcache, vcache};
+#define GX_FUSED(HH, GG)                                                                                             \
+    attn_decode_kernel<HH, GG, true><<<dim3((unsigned)(kv_heads * (HH / kValSlice)), 1u), kDecodeThreads, 0,         \
+                                       ctx->stream>>>(nullptr, heads, kv_heads, positions, limit, kcache, vcache,    \
+                                                      context, scale, q, scales, qsum, slots, nslots, fz)
+#define GX_FUSED_G(HH)                                                                                               \
+    do {                                                                                                             \
+        if (G == 1)                                                                                                  \
+            GX_FUSED(HH, 1);                                                                                         \
+        else if (G == 2)                                                                                             \
+            GX_FUSED(HH, 2);                                                                                         \
+        else if (G == 4)                                                                                             \
+            GX_FUSED(HH, 4);                                                                                         \
+        else                                                                                                         \
+            GX_FUSED(HH, 8);                                                                                         \
+    } while (0)
+    if (hd == 32)
+        GX_FUSED_G(32);
+    else if (hd == 64)
+        GX_FUSED_G(64);
+    else if (hd == 96)
+        GX_FUSED_G(96);
+    else
+        GX_FUSED_G(128);
+#undef GX_FUSED_G
+#undef GX_FUSED
+    return check_launch("qwen_rope_attention");
 }
 
 int launch_qwen_swiglu_quant(gx_ctx *ctx, const float *gu, int ldgu, int M, int ffn, int group, int8_t *q,

@@ -21,8 +21,9 @@ result: every output row is its own product.
 
 One position (a decode step) takes fewer launches: each pre-norm runs inside
 the product after it (gx_norm_matmul_q4_0 for Q|K|V), and the FFN's norm,
-Gate|Up product, SwiGLU and Q8_0 are one kernel (gx_norm_swiglu_q4_0), the
-same values bit for bit.
+Gate|Up product, SwiGLU and Q8_0 are one kernel (gx_norm_swiglu_q4_0), and
+the head norms, RoPE, cache store and attention are one kernel
+(gx_qwen_rope_attention), the same values bit for bit.
 
 Every kernel treats a position on its own, so a prompt read in one batch
 gives, bit for bit, what the same tokens give one at a time (golem's
@@ -42,6 +43,10 @@ import numpy as np
 import torch
 
 from . import capi
+
+# gx_qwen_rope_attention reads at most this many cached positions (the
+# one-kernel decode attention's limit); longer prefixes take the two calls.
+FUSED_ATTENTION_MAX = 767
 
 
 def rope_tables(dims, context, base):
@@ -267,13 +272,20 @@ class QwenModel:
                 call("gx_norm_matmul_q4_0", ctx, b["qkv"].ptr, vp(cur), vp(self.ffn), vp(b["attn_norm"]), eps,
                      vp(other), 0, b["qkv"].rows, vp(self.qkv))
                 cur, other = other, cur
-            call("gx_qwen_qk_rope", ctx, vp(self.qkv), qd + 2 * kvd, 1, cfg.heads, cfg.kv_heads, cfg.head_dim,
-                 vp(self.positions), vp(b["q_norm"]), vp(b["k_norm"]), vp(self.rope_cos), vp(self.rope_sin),
-                 eps, vp(self.qh), vp(self.kc[i]), vp(self.vc[i]), self.context, sl, self.nslots)
-            call("gx_qwen_attention", ctx, vp(self.qh), 1, cfg.heads, cfg.kv_heads, cfg.head_dim,
-                 max_pos, vp(self.positions), vp(self.kc[i]), vp(self.vc[i]), self.context,
-                 vp(self.set8.q), vp(self.set8.s), vp(self.set8.qs), vp(self.attn_ws), self.attn_ws.numel(), sl,
-                 self.nslots)
+            if max_pos < FUSED_ATTENTION_MAX:  # head norms + RoPE + cache store + attention, one kernel
+                call("gx_qwen_rope_attention", ctx, vp(self.qkv), qd + 2 * kvd, cfg.heads, cfg.kv_heads,
+                     cfg.head_dim, max_pos, vp(self.positions), vp(b["q_norm"]), vp(b["k_norm"]),
+                     vp(self.rope_cos), vp(self.rope_sin), eps, vp(self.kc[i]), vp(self.vc[i]), self.context,
+                     vp(self.set8.q), vp(self.set8.s), vp(self.set8.qs), sl, self.nslots)
+            else:
+                call("gx_qwen_qk_rope", ctx, vp(self.qkv), qd + 2 * kvd, 1, cfg.heads, cfg.kv_heads,
+                     cfg.head_dim, vp(self.positions), vp(b["q_norm"]), vp(b["k_norm"]), vp(self.rope_cos),
+                     vp(self.rope_sin), eps, vp(self.qh), vp(self.kc[i]), vp(self.vc[i]), self.context, sl,
+                     self.nslots)
+                call("gx_qwen_attention", ctx, vp(self.qh), 1, cfg.heads, cfg.kv_heads, cfg.head_dim,
+                     max_pos, vp(self.positions), vp(self.kc[i]), vp(self.vc[i]), self.context,
+                     vp(self.set8.q), vp(self.set8.s), vp(self.set8.qs), vp(self.attn_ws), self.attn_ws.numel(),
+                     sl, self.nslots)
             self._mm(b["o"], self.set8, 1, self.attn, cfg.dim)
             call("gx_norm_swiglu_q4_0", ctx, b["gu"].ptr, vp(cur), vp(self.attn), vp(b["ffn_norm"]), eps,
                  vp(other), vp(self.mid8.q), vp(self.mid8.s), vp(self.mid8.qs))

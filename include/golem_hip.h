@@ -297,6 +297,20 @@ int gx_qwen_attention(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int kv_
                       int8_t *q, float *scales, int32_t *qsum, void *workspace, size_t workspace_bytes,
                       const int32_t *slots, int nslots);
 
+/* gx_qwen_qk_rope followed by gx_qwen_attention for ONE position
+ * (qwen/attention.go:57-124 at batch 1, the decode step), in one kernel: the
+ * head norms and RoPE of the Q|K|V row qkv (ldqkv as for gx_qwen_qk_rope),
+ * the key and value stored into the caches at positions[0], and the
+ * attention over positions 0 .. positions[0] (max_pos bounds it; at most 767),
+ * quantised to Q8_0 into q/scales/qsum.  The caches and q/scales/qsum come
+ * out bit for bit as the two calls leave them (the fp16 query is not written
+ * anywhere).  slots / nslots as for gx_qwen_qk_rope, with one position. */
+int gx_qwen_rope_attention(gx_ctx *ctx, const float *qkv, int ldqkv, int heads, int kv_heads, int head_dim,
+                           int max_pos, const int32_t *positions, const float *q_norm, const float *k_norm,
+                           const float *rope_cos, const float *rope_sin, float eps, uint16_t *kcache,
+                           uint16_t *vcache, int context, int8_t *q, float *scales, int32_t *qsum,
+                           const int32_t *slots, int nslots);
+
 /* One position's RMSNormPlain + Q8_0 fused into the Q4_0 product that reads
  * it (M = 1): y[row] for rows [row_start, row_end) of w times
  * Q8_0(RMSNormPlain(x + add, gain, eps)), bit for bit gx_norm_quant followed

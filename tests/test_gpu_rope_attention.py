@@ -1,0 +1,90 @@
+"""gx_qwen_rope_attention, the decode step's head norms + RoPE + cache store
++ attention in one kernel, against the two calls it replaces
+(gx_qwen_qk_rope then gx_qwen_attention, qwen/attention.go:57-124 at batch
+1), bit for bit: the Q8_0 of the heads (values, scales, sums) and both caches
+after the call.
+
+The caches are filled with random entries first, so that the position's own
+key and value -- which the fused kernel takes from its computed copies, not
+from the entries it is writing -- meet a full prefix.  Cases: golem's head of
+128 with four query heads per key-value head (config 3), the other head widths
+and group sizes, the first position, a middle one and the last, max_pos at the
+position and at the end of the cache (the captured decode graph's launch), and
+the slots form: a conversation's own caches, and a position in no
+conversation (its output NaN-derived, nothing stored)."""
+import numpy as np
+import pytest
+import torch
+
+from golem_amd import capi, synth
+
+CASES = [(128, 32, 8, 640), (128, 16, 8, 200), (64, 4, 2, 304), (32, 8, 1, 96), (96, 4, 4, 136),
+         (64, 8, 1, 768)]
+
+
+def run_case(dev, hd, heads, kv, context, pos, max_pos, slots=None, nslots=1, seed=0):
+    g = synth.rng(seed + 7 * pos + hd)
+    width = (heads + 2 * kv) * hd
+    qkv = (g.standard_normal((1, width)) * 3).astype(np.float32)
+    qn = (1 + 0.02 * g.standard_normal(hd)).astype(np.float32)
+    kn = (1 + 0.02 * g.standard_normal(hd)).astype(np.float32)
+    cos = g.uniform(-1, 1, (context, hd // 2)).astype(np.float32)
+    sin = g.uniform(-1, 1, (context, hd // 2)).astype(np.float32)
+    kc0 = (g.standard_normal((nslots, kv, hd // 8, context, 8))).astype(np.float16)
+    vc0 = (g.standard_normal((nslots, kv, hd, context)) * 2).astype(np.float16)
+    ins = [dev.put(a) for a in (qkv, np.array([pos], np.int32), qn, kn, cos, sin)]
+    sl = dev.put(np.array([slots], np.int32)) if slots is not None else None
+    eps = np.float32(1e-6)
+    outs = []
+    for fused in (False, True):
+        kc = dev.put(kc0.view(np.int16))
+        vc = dev.put(vc0.view(np.int16))
+        q8 = dev.empty((1, heads * hd), np.int8)
+        sc = dev.empty((1, heads * hd // 32), np.float32)
+        qs = dev.empty((1, heads * hd // 32), np.int32)
+        if fused:
+            capi.call("gx_qwen_rope_attention", dev.ctx.ptr, capi.vp(ins[0]), width, heads, kv, hd, max_pos,
+                      capi.vp(ins[1]), capi.vp(ins[2]), capi.vp(ins[3]), capi.vp(ins[4]), capi.vp(ins[5]), eps,
+                      capi.vp(kc), capi.vp(vc), context, capi.vp(q8), capi.vp(sc), capi.vp(qs),
+                      capi.vp(sl) if sl is not None else None, nslots)
+        else:
+            qh = dev.empty((1, heads * hd), np.int16)
+            capi.call("gx_qwen_qk_rope", dev.ctx.ptr, capi.vp(ins[0]), width, 1, heads, kv, hd, capi.vp(ins[1]),
+                      capi.vp(ins[2]), capi.vp(ins[3]), capi.vp(ins[4]), capi.vp(ins[5]), eps, capi.vp(qh),
+                      capi.vp(kc), capi.vp(vc), context, capi.vp(sl) if sl is not None else None, nslots)
+            n = capi.size_out("gx_qwen_attention_workspace_bytes", 1, heads, max_pos)
+            ws = dev.empty((n,), np.uint8)
+            capi.call("gx_qwen_attention", dev.ctx.ptr, capi.vp(qh), 1, heads, kv, hd, max_pos, capi.vp(ins[1]),
+                      capi.vp(kc), capi.vp(vc), context, capi.vp(q8), capi.vp(sc), capi.vp(qs), capi.vp(ws), n,
+                      capi.vp(sl) if sl is not None else None, nslots)
+        dev.ctx.sync()
+        outs.append([dev.get(a) for a in (q8, sc, qs, kc, vc)])
+    for name, a, b in zip(("q", "scales", "sums", "key cache", "value cache"), *outs):
+        assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), \
+            f"{name} differs (hd {hd}, heads {heads}/{kv}, pos {pos}, max_pos {max_pos}, slot {slots})"
+    return outs[1]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("hd,heads,kv,context", CASES)
+def test_rope_attention_matches_two_calls(dev, hd, heads, kv, context):
+    for pos in (0, context // 2 + 3, context - 1):
+        run_case(dev, hd, heads, kv, context, pos, pos)
+    run_case(dev, hd, heads, kv, context, context // 3, context - 1)
+
+
+@pytest.mark.gpu
+def test_rope_attention_slots(dev):
+    hd, heads, kv, context = 128, 32, 8, 256
+    run_case(dev, hd, heads, kv, context, 100, context - 1, slots=2, nslots=3)
+    run_case(dev, hd, heads, kv, context, 50, context - 1, slots=5, nslots=3)
+
+
+@pytest.mark.gpu
+def test_rope_attention_refuses_long_prefix(dev):
+    hd, heads, kv, context = 64, 4, 2, 1024
+    z = dev.empty((1 << 16,), np.float32)
+    with pytest.raises(capi.GxError, match="at most 768"):
+        capi.call("gx_qwen_rope_attention", dev.ctx.ptr, capi.vp(z), (heads + 2 * kv) * hd, heads, kv, hd, 800,
+                  capi.vp(z), capi.vp(z), capi.vp(z), capi.vp(z), capi.vp(z), np.float32(1e-6), capi.vp(z),
+                  capi.vp(z), context, capi.vp(z), capi.vp(z), capi.vp(z), None, 1)
