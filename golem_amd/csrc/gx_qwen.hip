@@ -551,6 +551,37 @@ __global__ __launch_bounds__(kDecodeThreads) void attn_decode_kernel(
         }
     }
 
+    // FUSE: the position's G query heads and its key head (fp32, from the
+    // Q|K|V row) and this thread's value element first, so that the norms
+    // and rotations wait only for them, not for the cache reads after them.
+    constexpr int kRounds = ((G + 1) * HD + kDecodeThreads - 1) / kDecodeThreads;
+    float hv[kRounds];
+    float nv = 0.0f;  // FUSE: this thread's value element (tid < 32)
+    if (FUSE) {
+        const float *row = fz.qkv + (size_t)t * fz.ldqkv;
+#pragma unroll
+        for (int r = 0; r < kRounds; r++) {
+            const int i = min(tid + r * kDecodeThreads, (G + 1) * HD - 1);
+            hv[r] = row[i < G * HD ? kvh * G * HD + i : heads * HD + kvh * HD + (i - G * HD)];
+        }
+        nv = row[(heads + kv_heads) * HD + kvh * HD + d0 + (tid & (kValSlice - 1))];
+    }
+    // and the norm gains and rotation of this thread's pairs (i, i + HD/2)
+    constexpr int kHalf = HD / 2, kRopeRounds = ((G + 1) * kHalf + kDecodeThreads - 1) / kDecodeThreads;
+    float rg0[kRopeRounds], rg1[kRopeRounds], rc[kRopeRounds], rs[kRopeRounds];
+    if (FUSE) {
+#pragma unroll
+        for (int r = 0; r < kRopeRounds; r++) {
+            const int i = min(tid + r * kDecodeThreads, (G + 1) * kHalf - 1);
+            const int w = i / kHalf, j = i - w * kHalf;
+            const float *gain = w < G ? fz.q_norm : fz.k_norm;
+            rg0[r] = gain[j];
+            rg1[r] = gain[j + kHalf];
+            rc[r] = fz.rope_cos[(size_t)pos * kHalf + j];
+            rs[r] = fz.rope_sin[(size_t)pos * kHalf + j];
+        }
+    }
+
     // The G queries (adjacent heads of the row) first, then the key pieces of
     // this thread's positions, then the value slice (32 rows of positions,
     // 16 bytes = 8 positions a piece): the queries can be stored while the
@@ -577,23 +608,12 @@ __global__ __launch_bounds__(kDecodeThreads) void attn_decode_kernel(
     static_assert(G * HD / 2 <= kDecodeThreads, "one query dword per thread");
     // FUSE: the new key, fp16, at the end of region A (scores use its front)
     uint16_t *nk = (uint16_t *)(lds + kValSlice * kDecodeStride * 2 - HD * 2);
-    float nv = 0.0f;  // FUSE: this thread's value element (tid < 32)
     if (FUSE) {
         static_assert(G * kScoreStride * 4 + 64 <= kValSlice * kDecodeStride * 2 - HD * 2, "scores clear the key");
         static_assert((G + 1) * HD * 4 <= kValSlice * kDecodeStride * 2 - HD * 2, "staged heads fit region A");
-        // the G query heads and the key head (fp32) into region A, all loads
-        // before the first store; the slice's value elements into registers
+        // the G query heads and the key head (fp32) into region A
         float *hh = (float *)lds;
         __shared__ float hs[G + 1];
-        const float *row = fz.qkv + (size_t)t * fz.ldqkv;
-        constexpr int kRounds = ((G + 1) * HD + kDecodeThreads - 1) / kDecodeThreads;
-        float hv[kRounds];
-#pragma unroll
-        for (int r = 0; r < kRounds; r++) {
-            const int i = min(tid + r * kDecodeThreads, (G + 1) * HD - 1);
-            hv[r] = row[i < G * HD ? kvh * G * HD + i : heads * HD + kvh * HD + (i - G * HD)];
-        }
-        nv = row[(heads + kv_heads) * HD + kvh * HD + d0 + (tid & (kValSlice - 1))];
 #pragma unroll
         for (int r = 0; r < kRounds; r++)
             hh[min(tid + r * kDecodeThreads, (G + 1) * HD - 1)] = hv[r];
@@ -603,15 +623,18 @@ __global__ __launch_bounds__(kDecodeThreads) void attn_decode_kernel(
         __syncthreads();
         // normed, then rotated in pairs (i, i + HD/2): RoPETable.Apply,
         // nn/rope.go:62-73, as qwen_qk_rope_kernel
-        constexpr int half = HD / 2;
+        constexpr int half = kHalf;
         uint16_t *qlh = (uint16_t *)ql;
-        for (int i = tid; i < (G + 1) * half; i += kDecodeThreads) {
+#pragma unroll
+        for (int r = 0; r < kRopeRounds; r++) {
+            const int i = tid + r * kDecodeThreads;
+            if (i >= (G + 1) * half)
+                break;
             const int w = i / half, j = i - w * half;
             const float sc = hs[w];
-            const float *gain = w < G ? fz.q_norm : fz.k_norm;
             const float re0 = hh[w * HD + j], im0 = hh[w * HD + j + half];
-            const float re = (re0 * sc) * gain[j], im = (im0 * sc) * gain[j + half];
-            const float c = fz.rope_cos[(size_t)pos * half + j], sn = fz.rope_sin[(size_t)pos * half + j];
+            const float re = (re0 * sc) * rg0[r], im = (im0 * sc) * rg1[r];
+            const float c = rc[r], sn = rs[r];
             const float a = re * c - im * sn;
             const float b = re * sn + im * c;
             uint16_t ha = (uint16_t)float_to_half_bits(a), hb = (uint16_t)float_to_half_bits(b);
