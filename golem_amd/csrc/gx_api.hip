@@ -82,12 +82,8 @@ int gx_init(int device, gx_ctx **out) {
         return gx::fail(GX_ERR_HIP, "hipEventCreate failed");
     }
     ctx->gelu_table = nullptr;
-    ctx->split_ws = nullptr;
-    ctx->split_count = nullptr;
     auto undo = [ctx]() {
         (void)hipFree(ctx->gelu_table);
-        (void)hipFree(ctx->split_ws);
-        (void)hipFree(ctx->split_count);
         (void)hipEventDestroy(ctx->t0);
         (void)hipEventDestroy(ctx->t1);
         delete ctx;
@@ -95,12 +91,6 @@ int gx_init(int device, gx_ctx **out) {
     if (hipMalloc(&ctx->gelu_table, 65536 * sizeof(float)) != hipSuccess) {
         undo();
         return gx::fail(GX_ERR_NOMEM, "gx: cannot allocate the GELU table");
-    }
-    if (hipMalloc(&ctx->split_ws, (kSplitWsFloats + kSplitWsPad) * sizeof(float)) != hipSuccess ||
-        hipMalloc(&ctx->split_count, kSplitTiles * sizeof(uint32_t)) != hipSuccess ||
-        hipMemset(ctx->split_count, 0, kSplitTiles * sizeof(uint32_t)) != hipSuccess) {
-        undo();
-        return gx::fail(GX_ERR_NOMEM, "gx: cannot allocate the split product's workspace");
     }
     if (int rc = gx::launch_gelu_table(ctx, ctx->gelu_table)) {
         undo();
@@ -121,8 +111,6 @@ int gx_free(gx_ctx *ctx) {
     (void)hipEventDestroy(ctx->t0);
     (void)hipEventDestroy(ctx->t1);
     (void)hipFree(ctx->gelu_table);
-    (void)hipFree(ctx->split_ws);
-    (void)hipFree(ctx->split_count);
     delete ctx;
     return ok();
 }

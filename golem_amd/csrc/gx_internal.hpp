@@ -61,13 +61,8 @@ struct gx_ctx {
     hipEvent_t t0, t1;
     int cu_count;
     float *gelu_table;  // golem's 65536-entry GELU table, built on the device at init
-    float *split_ws;    // stretch sums of the split matrix-vector product (kSplitWsFloats)
-    uint32_t *split_count;  // its per-tile arrival counters (kSplitTiles), zero between launches
 };
 
-constexpr size_t kSplitWsFloats = (size_t)1 << 19;  // 2 MiB
-constexpr size_t kSplitWsPad = 8 * 64;             // what the final sum's batched reads may pass the end by
-constexpr int kSplitTiles = 4096;
 
 struct gx_weight {
     gx_ctx *ctx;

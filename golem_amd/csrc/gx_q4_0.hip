@@ -123,112 +123,89 @@ __global__ __launch_bounds__(1024) void q4_0_matvec_kernel(
     }
 }
 
-// One column (M = 1) of a matrix with few tiles, spread over more CUs: grid
-// (tiles, splits), each workgroup kSplitWaves wavefronts taking one stretch
-// each (stretch s = split * kSplitWaves + wave).  The stretch sums go to the
-// context's workspace [tile][S][64]; a tile's last workgroup to arrive (a
-// counter per tile, returned to 0 by that workgroup) adds them in stretch
-// order from 0 -- the single-workgroup kernel's sum, bit for bit.  The sums
-// travel as agent-scope (write-through, L2-bypassing) stores and loads.
-constexpr int kSplitWaves = 8;
-__global__ __launch_bounds__(64 * kSplitWaves) void q4_0_matvec_split_kernel(
+// One column (M = 1) of a matrix with few tiles, over more workgroups
+// without a cross-workgroup sum: a workgroup owns R rows (a quarter or half
+// of a tile) and all their stretches.  Lane l of a wavefront is row l % R of
+// the group and stretch slot l / R, so one wavefront covers 64 / R
+// stretches; its 16-byte loads are 64 / R runs of R*16 contiguous bytes of
+// the R64 layout.  The stretches of a wavefront differ, so the activation
+// comes from an LDS copy staged first (every load in flight together)
+// rather than from SGPRs.  The stretch sums meet in LDS and are added in
+// stretch order from 0: the one-tile kernel's sum, bit for bit.
+constexpr int kStageRegs = 4;  // staged 16-byte activation pieces per thread
+
+template <int R>
+__global__ __launch_bounds__(1024) void q4_0_matvec_rg_kernel(
     const uint8_t *__restrict__ W, size_t plane0_bytes, int B, int DC, const int8_t *__restrict__ q,
-    const float *__restrict__ scales, const int32_t *__restrict__ qsum, int tile0, int row_start, int row_end,
-    const float *__restrict__ bias, float *__restrict__ y, float *__restrict__ ws, uint32_t *__restrict__ count) {
-    __shared__ uint32_t ticket;
+    const float *__restrict__ scales, const int32_t *__restrict__ qsum, int group0, int row_start, int row_end,
+    const float *__restrict__ bias, float *__restrict__ y) {
+    constexpr int kSlots = kTileRows / R;
+    extern __shared__ __align__(16) float rg_lds[];  // part [S][R], then q [K], scales [B], sums [B]
     const int S = (B + kStretch - 1) / kStretch;
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int tile = tile0 + blockIdx.x;
-    const int s = blockIdx.y * kSplitWaves + wave;
-    float *wst = ws + (size_t)blockIdx.x * S * kTileRows;
-    if (s < S) {
-        const uint8_t *qs_row = W + ((size_t)tile * B * kTileRows + lane) * kChunk;
-        const uint8_t *d_row = W + plane0_bytes + ((size_t)tile * DC * kTileRows + lane) * kChunk;
-        const int b0 = s * kStretch;
-        const int nb = min(kStretch, B - b0);
-        uint4 wq[kStretch];
+    const int K = B * kQ4Block;
+    float *part = rg_lds;
+    int8_t *qa = (int8_t *)(rg_lds + ((S * R + 3) & ~3));
+    float *sa = (float *)(qa + K);
+    int32_t *qsa = (int32_t *)(sa + B);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int g = group0 + blockIdx.x;
+    const int tile = g / kSlots, r = (g - tile * kSlots) * R + lane % R;
+    const int s = wave * kSlots + lane / R;  // this lane's stretch
+    const int sc = min(s, S - 1);
+    // the activation: all loads in flight, then the weights, then the barrier
+    {
+        const int tid = threadIdx.x, nt = blockDim.x, n16 = K / 16;
+        int4 v[kStageRegs];
+        float sv[kStageRegs];
+        int32_t qv[kStageRegs];
 #pragma unroll
-        for (int j = 0; j < kStretch; j++)
-            wq[j] = load_stream(qs_row + (size_t)min(b0 + j, B - 1) * kTileRows * kChunk);
-        const uint4 dch = *(const uint4 *)(d_row + (size_t)s * kTileRows * kChunk);
-        float p = 0.0f;
+        for (int k = 0; k < kStageRegs; k++)
+            v[k] = ((const int4 *)q)[min(tid + k * nt, n16 - 1)];
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
-            int4 a0[4], a1[4];
-            int32_t qs[4];
-            float sa[4];
-#pragma unroll
-            for (int jj = 0; jj < 4; jj++) {
-                const int b = min(b0 + 4 * h + jj, B - 1);
-                const int4 *a = (const int4 *)(q + (size_t)b * kQ4Block);
-                a0[jj] = a[0];
-                a1[jj] = a[1];
-                qs[jj] = qsum[b];
-                sa[jj] = scales[b];
-            }
-#pragma unroll
-            for (int jj = 0; jj < 4; jj++) {
-                const int j = 4 * h + jj;
-                if (j < nb) {
-                    const int32_t isum = q4_0_block_isum(wq[j], a0[jj], a1[jj], qs[jj]);
-                    const float sc = chunk_half(dch, j) * sa[jj];
-                    p = fmaf((float)isum, sc, p);
-                }
-            }
+        for (int k = 0; k < kStageRegs; k++) {
+            sv[k] = scales[min(tid + k * nt, B - 1)];
+            qv[k] = qsum[min(tid + k * nt, B - 1)];
         }
-        // written through to the agent's coherence point (an agent-scope store)
-        __hip_atomic_store(&wst[(size_t)s * kTileRows + lane], p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    // The stores have completed (vmcnt 0) before the workgroup counts itself.
-    // A release fence would also write back the whole L2, which costs more
-    // than the product; every value published here is already written through.
-    __builtin_amdgcn_s_waitcnt((0 & 15) | (7 << 4) | (15 << 8));
-    __syncthreads();
-    if (threadIdx.x == 0)
-        ticket = __hip_atomic_fetch_add(&count[blockIdx.x], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __syncthreads();
-    if (ticket != gridDim.y - 1)
-        return;
-    // The last workgroup: its wavefronts bring every split's sums into LDS,
-    // eight stretches each per round, with loads carrying the agent scope bit
-    // (sc1, coherent like the stores; written out, since the compiler keeps
-    // atomic loads one at a time).  Reads past S land in the workspace's
-    // padding and are not used.
-    extern __shared__ float sums[];  // [S][64]
-    for (int t0 = wave * 8; t0 < S; t0 += kSplitWaves * 8) {
-        const float *src = wst + (size_t)t0 * kTileRows + lane;
-        float v0, v1, v2, v3, v4, v5, v6, v7;
-        asm volatile(
-            "global_load_dword %0, %8, off sc1\n\t"
-            "global_load_dword %1, %8, off offset:256 sc1\n\t"
-            "global_load_dword %2, %8, off offset:512 sc1\n\t"
-            "global_load_dword %3, %8, off offset:768 sc1\n\t"
-            "global_load_dword %4, %8, off offset:1024 sc1\n\t"
-            "global_load_dword %5, %8, off offset:1280 sc1\n\t"
-            "global_load_dword %6, %8, off offset:1536 sc1\n\t"
-            "global_load_dword %7, %8, off offset:1792 sc1\n\t"
-            "s_waitcnt vmcnt(0)"
-            : "=&v"(v0), "=&v"(v1), "=&v"(v2), "=&v"(v3), "=&v"(v4), "=&v"(v5), "=&v"(v6), "=&v"(v7)
-            : "v"(src)
-            : "memory");
-        const float v[8] = {v0, v1, v2, v3, v4, v5, v6, v7};
 #pragma unroll
-        for (int j = 0; j < 8; j++)
-            if (t0 + j < S)
-                sums[(t0 + j) * kTileRows + lane] = v[j];
+        for (int k = 0; k < kStageRegs; k++)
+            ((int4 *)qa)[min(tid + k * nt, n16 - 1)] = v[k];
+#pragma unroll
+        for (int k = 0; k < kStageRegs; k++) {
+            sa[min(tid + k * nt, B - 1)] = sv[k];
+            qsa[min(tid + k * nt, B - 1)] = qv[k];
+        }
     }
+    const uint8_t *qs_row = W + ((size_t)tile * B * kTileRows + r) * kChunk;
+    const uint8_t *d_row = W + plane0_bytes + ((size_t)tile * DC * kTileRows + r) * kChunk;
+    const int b0 = sc * kStretch;
+    const int nb = s < S ? min(kStretch, B - b0) : 0;
+    uint4 wq[kStretch];
+#pragma unroll
+    for (int j = 0; j < kStretch; j++)
+        wq[j] = load_stream(qs_row + (size_t)min(b0 + j, B - 1) * kTileRows * kChunk);
+    const uint4 dch = *(const uint4 *)(d_row + (size_t)sc * kTileRows * kChunk);
     __syncthreads();
-    if (wave != 0)
-        return;
-    const int row = tile * kTileRows + lane;
-    float acc = 0.0f;
-    for (int t = 0; t < S; t++)  // stretch order, from 0
-        acc = acc + sums[t * kTileRows + lane];
-    if (row >= row_start && row < row_end)
+    float p = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kStretch; j++) {
+        if (j < nb) {
+            const int b = b0 + j;
+            const int4 *a = (const int4 *)(qa + (size_t)b * kQ4Block);
+            const int32_t isum = q4_0_block_isum(wq[j], a[0], a[1], qsa[b]);
+            const float scl = chunk_half(dch, j) * sa[b];
+            p = fmaf((float)isum, scl, p);
+        }
+    }
+    if (s < S)
+        part[s * R + lane % R] = p;
+    __syncthreads();
+    const int row = tile * kTileRows + r;
+    if (wave == 0 && lane < R && row >= row_start && row < row_end) {
+        float acc = 0.0f;
+        for (int t = 0; t < S; t++)  // stretch order, from 0
+            acc = acc + part[t * R + lane];
         y[row] = bias ? acc + bias[row] : acc;
-    if (lane == 0)
-        __hip_atomic_store(&count[blockIdx.x], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 }
 
 // The per-block integers of the kernel above, for the parity tests: one
@@ -473,22 +450,20 @@ __global__ __launch_bounds__(1024) void q4_0_matvec_fused_kernel(
 int launch_q4_0_matvec(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, const int8_t *q, const float *scales,
                        const int32_t *qsum, int M, int row_start, int row_end, const float *bias, float *y,
                        int ldy) {
-    // One column of a matrix with few tiles and long rows: the stretches of a
-    // tile over several workgroups, so that more CUs pull weights.
+    // One column of a matrix with few tiles (at most a quarter as many as
+    // CUs): quarter tiles, so that four times as many workgroups pull
+    // weights (O 5.6 -> 4.2 us, Down 9.7 -> 6.5 us back to back).
     {
         const int B = w->blocks, S = (B + kStretch - 1) / kStretch;
         const int tile0 = row_start / kTileRows;
         const int tiles = (row_end + kTileRows - 1) / kTileRows - tile0;
-        const int splits = (S + kSplitWaves - 1) / kSplitWaves;
-        // worth it once a single workgroup's wavefronts would each take more
-        // than one stretch
-        if (M == 1 && S > 16 && tiles * 4 <= ctx->cu_count && tiles <= kSplitTiles &&
-            (size_t)tiles * S * kTileRows <= kSplitWsFloats && S * kTileRows * sizeof(float) <= 64 * 1024) {
-            q4_0_matvec_split_kernel<<<dim3((unsigned)tiles, (unsigned)splits), 64 * kSplitWaves,
-                                       (size_t)S * kTileRows * sizeof(float), ctx->stream>>>(
-                mat, w->plane0_bytes, B, w->dchunks, q, scales, qsum, tile0, row_start, row_end, bias, y,
-                ctx->split_ws, ctx->split_count);
-            return check_launch("q4_0_matvec_split");
+        constexpr int R = 16, kSlots = kTileRows / R;
+        const int waves = (S + kSlots - 1) / kSlots;
+        const size_t lds = (size_t)((S * R + 3) & ~3) * sizeof(float) + (size_t)w->cols + (size_t)B * 8;
+        if (M == 1 && tiles * 4 <= ctx->cu_count && waves <= 16 && lds <= 64 * 1024) {
+            q4_0_matvec_rg_kernel<R><<<(unsigned)(tiles * kSlots), 64 * waves, lds, ctx->stream>>>(
+                mat, w->plane0_bytes, B, w->dchunks, q, scales, qsum, tile0 * kSlots, row_start, row_end, bias, y);
+            return check_launch("q4_0_matvec_rg");
         }
     }
     // Columns in groups of 8, 4, 2, 1, each group reading the weights once;

@@ -184,21 +184,30 @@ def test_errors_are_golem_panics(dev):
         dev.matmul_q4_0(wd, act, 1, 0, 5)
 
 
-@pytest.mark.parametrize("rows,cols", [(2560, 9728), (200, 8192), (64, 4352)])
-def test_split_matvec_equals_one_workgroup(dev, rows, cols):
-    """A long row of few tiles, one column, runs split over several
-    workgroups whose stretch sums meet through the workspace (the tile's last
-    workgroup adds them).  Launched again and again (the arrival counters go
-    back to 0 each time), every result equals, bit for bit, column 0 of a
-    two-column product, which one workgroup per tile computes."""
+@pytest.mark.parametrize("rows,cols", [(2560, 9728), (2560, 4096), (200, 8192), (64, 4352), (100, 16640)])
+def test_quarter_tile_matvec_equals_one_workgroup(dev, rows, cols):
+    """One column of a matrix with few tiles runs on quarter tiles (a
+    workgroup per 16 rows, a lane per (row, stretch)); more than 64 stretches
+    (16640 inputs) fall back to whole tiles.  Every result equals, bit for
+    bit, column 0 of a two-column product, which one workgroup per tile
+    computes; so do row ranges that cut the quarters, with and without a
+    bias, and rows outside the range keep their sentinels."""
     g = synth.rng(300 + rows)
     w = synth.q4_0_weights(g, rows, cols)
     wd = dev.weight(w, capi.Q4_0, rows, cols)
-    log(f"split matvec rows={rows} cols={cols}")
-    for it in range(40):
+    bias = g.standard_normal(rows).astype(np.float32)
+    log(f"quarter-tile matvec rows={rows} cols={cols}")
+    for it in range(8):
         x = synth.activations(g, 2, cols)
         act = dev.quantize_q8_0(x, with_corr=False)
         one = dev.get(dev.matmul_q4_0(wd, [a[:1] for a in act[:3]] + [None], 1))
         two = dev.get(dev.matmul_q4_0(wd, act, 2))
         np.testing.assert_array_equal(one[0].view(np.uint32), two[0].view(np.uint32), err_msg=f"launch {it}")
+    start, end = 7, rows - 5
+    y = dev.put(np.full((1, rows), np.nan, np.float32))
+    dev.matmul_q4_0(wd, [a[:1] for a in act[:3]] + [None], 1, start, end, bias=bias, y=y)
+    got = dev.get(y)[0]
+    want = two[0] + bias
+    np.testing.assert_array_equal(got[start:end].view(np.uint32), want[start:end].view(np.uint32))
+    assert np.isnan(got[:start]).all() and np.isnan(got[end:]).all()
     wd.free()
