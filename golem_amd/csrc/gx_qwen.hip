@@ -480,14 +480,15 @@ __global__ __launch_bounds__(NT) void attn_values_kernel(int M, int heads, int G
     }
 }
 
-// Decode attention in one kernel (M <= 4 positions, prefixes of at most
-// kDecodeMax positions): grid (kv_heads * hd/32 slices, M), 512 threads.  A
-// workgroup computes, for the G query heads of key-value head kvh, the
-// scores over the whole prefix (a thread per position, its key rows in
-// registers, the queries in LDS), the softmax and the probabilities, then the
-// 32 value chains of its slice for each head -- the same arithmetic, in the
-// same order, as the three passes above.  Its slice of the value rows and its
-// key rows are loaded first, so that the loads overlap; the slices'
+// Decode attention in one kernel (M <= 4 positions, or one position per
+// conversation, prefixes of at most kDecodeMax positions): grid
+// (heads / G * hd/32 slices, M), 512 threads.  A workgroup computes, for G
+// query heads of key-value head kvh (G = 1, or the whole group of heads that
+// share kvh), the scores over the whole prefix (a thread per position, its key
+// rows in registers, the queries in LDS), the softmax and the probabilities,
+// then the 32 value chains of its slice for each head -- the same arithmetic,
+// in the same order, as the three passes above.  Its slice of the value rows
+// and its key rows are loaded first, so that the loads overlap; the slices'
 // workgroups repeat the scores and softmax of their heads.
 constexpr int kDecodeMax = 768;
 constexpr int kDecodeThreads = 512;
@@ -534,7 +535,14 @@ __global__ __launch_bounds__(kDecodeThreads) void attn_decode_kernel(
     uint32_t *ql = (uint32_t *)(lds + kValSlice * kDecodeStride * 2 + G * kDecodeStride * 2);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     constexpr int slices = HD / kValSlice;
-    const int kvh = blockIdx.x / slices, d0 = (blockIdx.x - kvh * slices) * kValSlice;
+    // Workgroup b: key-value head b % kv_heads (so that the workgroups of one
+    // key-value head share an XCD's L2), and within it query heads
+    // h0 .. h0 + G - 1 and value slice d0.
+    const int group = heads / kv_heads;  // query heads per key-value head
+    const int kvh = blockIdx.x % kv_heads, rb = blockIdx.x / kv_heads;
+    const int hl = rb / slices, d0 = (rb - hl * slices) * kValSlice;
+    const int h0 = kvh * group + hl * G;
+    const bool first = hl == 0;  // the head group that stores the position (FUSE)
     const int t = blockIdx.y;
     const int pos = positions[t];
     const int n = min(pos + 1, limit);
@@ -562,7 +570,7 @@ __global__ __launch_bounds__(kDecodeThreads) void attn_decode_kernel(
 #pragma unroll
         for (int r = 0; r < kRounds; r++) {
             const int i = min(tid + r * kDecodeThreads, (G + 1) * HD - 1);
-            hv[r] = row[i < G * HD ? kvh * G * HD + i : heads * HD + kvh * HD + (i - G * HD)];
+            hv[r] = row[i < G * HD ? h0 * HD + i : heads * HD + kvh * HD + (i - G * HD)];
         }
         nv = row[(heads + kv_heads) * HD + kvh * HD + d0 + (tid & (kValSlice - 1))];
     }
@@ -586,7 +594,7 @@ __global__ __launch_bounds__(kDecodeThreads) void attn_decode_kernel(
     // this thread's positions, then the value slice (32 rows of positions,
     // 16 bytes = 8 positions a piece): the queries can be stored while the
     // rest is in flight.
-    const uint32_t *qg = (const uint32_t *)(qh + ((size_t)t * heads + kvh * G) * HD);
+    const uint32_t *qg = (const uint32_t *)(qh + ((size_t)t * heads + h0) * HD);
     const uint32_t qr = FUSE ? 0u : qg[min(tid, G * HD / 2 - 1)];
     v4u_stream k[kDecodeRows][HD / 8];
     const v4u_stream *kbase = (const v4u_stream *)(kcache + (size_t)kvh * HD * context);
@@ -646,14 +654,14 @@ __global__ __launch_bounds__(kDecodeThreads) void attn_decode_kernel(
             } else {
                 nk[j] = ha;
                 nk[j + half] = hb;
-                if (store && d0 == 0) {
+                if (store && first && d0 == 0) {
                     uint16_t *kt = fz.kcache + (size_t)kvh * HD * context + (size_t)pos * 8;
                     kcache_put(kt, context, j, ha);
                     kcache_put(kt, context, j + half, hb);
                 }
             }
         }
-        if (store && tid < kValSlice)
+        if (store && first && tid < kValSlice)
             fz.vcache[((size_t)kvh * HD + d0 + tid) * context + pos] = (uint16_t)float_to_half_bits(nv);
         __syncthreads();
         // this position's key from the copy, not the cache entry being written
@@ -803,7 +811,7 @@ __global__ __launch_bounds__(kDecodeThreads) void attn_decode_kernel(
         int32_t sm;
         const int32_t nq = q8_0_lane(acc, &stored, &sm);
         const int width = heads * HD, B = width >> 5;
-        const int col = (kvh * G + g) * HD + d0 + dd;
+        const int col = (h0 + g) * HD + d0 + dd;
         q[(size_t)t * width + col] = (int8_t)nq;
         if (dd == 0) {
             scales[(size_t)t * B + (col >> 5)] = stored;
@@ -940,13 +948,19 @@ int launch_qwen_attention(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int
     // One workgroup per token: a few tokens of one conversation, or tokens of
     // several conversations (slots), whose caches share nothing.
     if ((M <= 4 || slots) && limit <= kDecodeMax) {
+// One query head per workgroup when that fills at most two workgroups per CU
+// (128 workgroups for config 3's decode rather than 32): the scores,
+// exponentials and divisions a workgroup repeats for its value slice shrink
+// by the group size; the key rows are read by more workgroups, from the L2
+// their key-value head's workgroups share.  Larger batches keep a group of
+// query heads per workgroup.
 #define GX_DECODE(HH, GG)                                                                                            \
-    attn_decode_kernel<HH, GG, false><<<dim3((unsigned)(kv_heads * (HH / kValSlice)), (unsigned)M), kDecodeThreads,  \
+    attn_decode_kernel<HH, GG, false><<<dim3((unsigned)(heads / GG * (HH / kValSlice)), (unsigned)M), kDecodeThreads,\
                                         0, ctx->stream>>>(qh, heads, kv_heads, positions, limit, kcache, vcache,      \
                                                           context, scale, q, scales, qsum, slots, nslots, QkRope{})
 #define GX_DECODE_G(HH)                                                                                              \
     do {                                                                                                             \
-        if (G == 1)                                                                                                  \
+        if ((size_t)M * heads * (HH / kValSlice) <= 2 * (size_t)ctx->cu_count || G == 1)                             \
             GX_DECODE(HH, 1);                                                                                        \
         else if (G == 2)                                                                                             \
             GX_DECODE(HH, 2);                                                                                        \
@@ -1026,30 +1040,18 @@ int launch_qwen_rope_attention(gx_ctx *ctx, const float *qkv, int ldqkv, int hea
     const int limit = max_pos + 1;
     GX_CHECK(limit <= kDecodeMax, "gx: the fused attention reads at most %d positions, not %d", kDecodeMax, limit);
     const QkRope fz{qkv, ldqkv, q_norm, k_norm, rope_cos, rope_sin, eps, kcache, vcache};
-#define GX_FUSED(HH, GG)                                                                                             \
-    attn_decode_kernel<HH, GG, true><<<dim3((unsigned)(kv_heads * (HH / kValSlice)), 1u), kDecodeThreads, 0,         \
-                                       ctx->stream>>>(nullptr, heads, kv_heads, positions, limit, kcache, vcache,    \
-                                                      context, scale, q, scales, qsum, slots, nslots, fz)
-#define GX_FUSED_G(HH)                                                                                               \
-    do {                                                                                                             \
-        if (G == 1)                                                                                                  \
-            GX_FUSED(HH, 1);                                                                                         \
-        else if (G == 2)                                                                                             \
-            GX_FUSED(HH, 2);                                                                                         \
-        else if (G == 4)                                                                                             \
-            GX_FUSED(HH, 4);                                                                                         \
-        else                                                                                                         \
-            GX_FUSED(HH, 8);                                                                                         \
-    } while (0)
+#define GX_FUSED(HH)                                                                                                 \
+    attn_decode_kernel<HH, 1, true><<<dim3((unsigned)(heads * (HH / kValSlice)), 1u), kDecodeThreads, 0,             \
+                                      ctx->stream>>>(nullptr, heads, kv_heads, positions, limit, kcache, vcache,     \
+                                                     context, scale, q, scales, qsum, slots, nslots, fz)
     if (hd == 32)
-        GX_FUSED_G(32);
+        GX_FUSED(32);
     else if (hd == 64)
-        GX_FUSED_G(64);
+        GX_FUSED(64);
     else if (hd == 96)
-        GX_FUSED_G(96);
+        GX_FUSED(96);
     else
-        GX_FUSED_G(128);
-#undef GX_FUSED_G
+        GX_FUSED(128);
 #undef GX_FUSED
     return check_launch("qwen_rope_attention");
 }
