@@ -559,30 +559,25 @@ __global__ __launch_bounds__(kDecodeThreads) void attn_decode_kernel(
         }
     }
 
-    // FUSE: the position's G query heads and its key head (fp32, from the
-    // Q|K|V row) and this thread's value element first, so that the norms
-    // and rotations wait only for them, not for the cache reads after them.
-    constexpr int kRounds = ((G + 1) * HD + kDecodeThreads - 1) / kDecodeThreads;
-    float hv[kRounds];
-    float nv = 0.0f;  // FUSE: this thread's value element (tid < 32)
-    if (FUSE) {
+    // FUSE (G = 1): wavefront 0 alone prepares the position -- its query head
+    // and key head (fp32, from the Q|K|V row, four values a lane), the
+    // slice's value elements, and the norm gains and rotation of the HD pairs
+    // (i, i + HD/2), two a lane -- with these loads issued before its cache
+    // reads, while the other wavefronts go straight to theirs.
+    static_assert(!FUSE || G == 1, "the fused prologue serves one query head per workgroup");
+    constexpr int kHalf = HD / 2;
+    float4 hx = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    float nv = 0.0f, rg0[2], rg1[2], rc[2], rs[2];
+    if (FUSE && wave == 0) {
         const float *row = fz.qkv + (size_t)t * fz.ldqkv;
+        const int e = min(4 * lane, 2 * HD - 4);  // query elements, then key elements
+        hx = *(const float4 *)(row + (e < HD ? h0 * HD + e : heads * HD + kvh * HD + (e - HD)));
+        nv = row[(heads + kv_heads) * HD + kvh * HD + d0 + (lane & (kValSlice - 1))];
 #pragma unroll
-        for (int r = 0; r < kRounds; r++) {
-            const int i = min(tid + r * kDecodeThreads, (G + 1) * HD - 1);
-            hv[r] = row[i < G * HD ? h0 * HD + i : heads * HD + kvh * HD + (i - G * HD)];
-        }
-        nv = row[(heads + kv_heads) * HD + kvh * HD + d0 + (tid & (kValSlice - 1))];
-    }
-    // and the norm gains and rotation of this thread's pairs (i, i + HD/2)
-    constexpr int kHalf = HD / 2, kRopeRounds = ((G + 1) * kHalf + kDecodeThreads - 1) / kDecodeThreads;
-    float rg0[kRopeRounds], rg1[kRopeRounds], rc[kRopeRounds], rs[kRopeRounds];
-    if (FUSE) {
-#pragma unroll
-        for (int r = 0; r < kRopeRounds; r++) {
-            const int i = min(tid + r * kDecodeThreads, (G + 1) * kHalf - 1);
+        for (int r = 0; r < 2; r++) {
+            const int i = min(lane + 64 * r, HD - 1);  // pair i: head i / (HD/2)
             const int w = i / kHalf, j = i - w * kHalf;
-            const float *gain = w < G ? fz.q_norm : fz.k_norm;
+            const float *gain = w == 0 ? fz.q_norm : fz.k_norm;
             rg0[r] = gain[j];
             rg1[r] = gain[j + kHalf];
             rc[r] = fz.rope_cos[(size_t)pos * kHalf + j];
@@ -618,51 +613,67 @@ __global__ __launch_bounds__(kDecodeThreads) void attn_decode_kernel(
     uint16_t *nk = (uint16_t *)(lds + kValSlice * kDecodeStride * 2 - HD * 2);
     if (FUSE) {
         static_assert(G * kScoreStride * 4 + 64 <= kValSlice * kDecodeStride * 2 - HD * 2, "scores clear the key");
-        static_assert((G + 1) * HD * 4 <= kValSlice * kDecodeStride * 2 - HD * 2, "staged heads fit region A");
-        // the G query heads and the key head (fp32) into region A
-        float *hh = (float *)lds;
-        __shared__ float hs[G + 1];
+        static_assert(2 * HD * 12 <= kValSlice * kDecodeStride * 2 - HD * 2, "staged heads fit region A");
+        __shared__ float hs[2];
+        if (wave == 0) {
+            // The two heads and their squares (float32, widened) in region A;
+            // lanes 0 and 1 then add a head's squares in order in float64:
+            // head_norm_scale's sum, bit for bit, with its reads in flight.
+            float *hh = (float *)lds;
+            double *sq = (double *)(lds + 2 * HD * 4);
+            if (4 * lane < 2 * HD) {
+                *(float4 *)(hh + 4 * lane) = hx;
+                const float x4[4] = {hx.x, hx.y, hx.z, hx.w};
 #pragma unroll
-        for (int r = 0; r < kRounds; r++)
-            hh[min(tid + r * kDecodeThreads, (G + 1) * HD - 1)] = hv[r];
-        __syncthreads();
-        if (tid <= G)
-            hs[tid] = head_norm_scale(hh + tid * HD, HD, fz.eps);
-        __syncthreads();
-        // normed, then rotated in pairs (i, i + HD/2): RoPETable.Apply,
-        // nn/rope.go:62-73, as qwen_qk_rope_kernel
-        constexpr int half = kHalf;
-        uint16_t *qlh = (uint16_t *)ql;
-#pragma unroll
-        for (int r = 0; r < kRopeRounds; r++) {
-            const int i = tid + r * kDecodeThreads;
-            if (i >= (G + 1) * half)
-                break;
-            const int w = i / half, j = i - w * half;
-            const float sc = hs[w];
-            const float re0 = hh[w * HD + j], im0 = hh[w * HD + j + half];
-            const float re = (re0 * sc) * rg0[r], im = (im0 * sc) * rg1[r];
-            const float c = rc[r], sn = rs[r];
-            const float a = re * c - im * sn;
-            const float b = re * sn + im * c;
-            uint16_t ha = (uint16_t)float_to_half_bits(a), hb = (uint16_t)float_to_half_bits(b);
-            if (w < G) {
-                if (!store)  // no conversation: the query is NaN
-                    ha = hb = 0x7E00;
-                qlh[w * HD + j] = ha;
-                qlh[w * HD + j + half] = hb;
-            } else {
-                nk[j] = ha;
-                nk[j + half] = hb;
-                if (store && first && d0 == 0) {
-                    uint16_t *kt = fz.kcache + (size_t)kvh * HD * context + (size_t)pos * 8;
-                    kcache_put(kt, context, j, ha);
-                    kcache_put(kt, context, j + half, hb);
+                for (int k = 0; k < 4; k++) {
+                    const float v = x4[k];
+                    const float sqf = v * v;
+                    sq[4 * lane + k] = (double)sqf;
                 }
             }
+            if (lane < 2) {
+                const double *sh = sq + lane * HD;
+                double acc = 0.0;
+#pragma unroll 16
+                for (int i = 0; i < HD; i++)
+                    acc += sh[i];
+                const float mean = (float)(acc / (double)HD);
+                hs[lane] = (float)(1.0 / sqrt((double)(mean + fz.eps)));
+            }
+            // normed, then rotated in pairs (i, i + HD/2): RoPETable.Apply,
+            // nn/rope.go:62-73, as qwen_qk_rope_kernel
+            uint16_t *qlh = (uint16_t *)ql;
+#pragma unroll
+            for (int r = 0; r < 2; r++) {
+                const int i = lane + 64 * r;
+                if (i >= HD)
+                    break;
+                const int w = i / kHalf, j = i - w * kHalf;
+                const float sc = hs[w];
+                const float re0 = hh[w * HD + j], im0 = hh[w * HD + j + kHalf];
+                const float re = (re0 * sc) * rg0[r], im = (im0 * sc) * rg1[r];
+                const float c = rc[r], sn = rs[r];
+                const float a = re * c - im * sn;
+                const float b = re * sn + im * c;
+                uint16_t ha = (uint16_t)float_to_half_bits(a), hb = (uint16_t)float_to_half_bits(b);
+                if (w == 0) {
+                    if (!store)  // no conversation: the query is NaN
+                        ha = hb = 0x7E00;
+                    qlh[j] = ha;
+                    qlh[j + kHalf] = hb;
+                } else {
+                    nk[j] = ha;
+                    nk[j + kHalf] = hb;
+                    if (store && first && d0 == 0) {
+                        uint16_t *kt = fz.kcache + (size_t)kvh * HD * context + (size_t)pos * 8;
+                        kcache_put(kt, context, j, ha);
+                        kcache_put(kt, context, j + kHalf, hb);
+                    }
+                }
+            }
+            if (store && first && lane < kValSlice)
+                fz.vcache[((size_t)kvh * HD + d0 + lane) * context + pos] = (uint16_t)float_to_half_bits(nv);
         }
-        if (store && first && tid < kValSlice)
-            fz.vcache[((size_t)kvh * HD + d0 + tid) * context + pos] = (uint16_t)float_to_half_bits(nv);
         __syncthreads();
         // this position's key from the copy, not the cache entry being written
         if (pos == n - 1) {
