@@ -82,8 +82,12 @@ int gx_init(int device, gx_ctx **out) {
         return gx::fail(GX_ERR_HIP, "hipEventCreate failed");
     }
     ctx->gelu_table = nullptr;
+    ctx->argmax_v = nullptr;
+    ctx->argmax_i = nullptr;
     auto undo = [ctx]() {
         (void)hipFree(ctx->gelu_table);
+        (void)hipFree(ctx->argmax_v);
+        (void)hipFree(ctx->argmax_i);
         (void)hipEventDestroy(ctx->t0);
         (void)hipEventDestroy(ctx->t1);
         delete ctx;
@@ -91,6 +95,11 @@ int gx_init(int device, gx_ctx **out) {
     if (hipMalloc(&ctx->gelu_table, 65536 * sizeof(float)) != hipSuccess) {
         undo();
         return gx::fail(GX_ERR_NOMEM, "gx: cannot allocate the GELU table");
+    }
+    if (hipMalloc(&ctx->argmax_v, kArgmaxRows * kArgmaxParts * sizeof(float)) != hipSuccess ||
+        hipMalloc(&ctx->argmax_i, kArgmaxRows * kArgmaxParts * sizeof(int32_t)) != hipSuccess) {
+        undo();
+        return gx::fail(GX_ERR_NOMEM, "gx: cannot allocate the greedy pick's workspace");
     }
     if (int rc = gx::launch_gelu_table(ctx, ctx->gelu_table)) {
         undo();
@@ -111,6 +120,8 @@ int gx_free(gx_ctx *ctx) {
     (void)hipEventDestroy(ctx->t0);
     (void)hipEventDestroy(ctx->t1);
     (void)hipFree(ctx->gelu_table);
+    (void)hipFree(ctx->argmax_v);
+    (void)hipFree(ctx->argmax_i);
     delete ctx;
     return ok();
 }
@@ -684,7 +695,18 @@ int gx_argmax(gx_ctx *ctx, const float *x, int ldx, int M, int n, int32_t *ids) 
     GX_CHECK(x && ids, "gx: missing argument");
     if (M == 0)
         return ok();
-    if (int rc = gx::launch_argmax(ctx, x, ldx, M, n, ids))
+    if (int rc = gx::launch_argmax(ctx, x, ldx, M, n, ids, nullptr, 0, nullptr, nullptr))
+        return rc;
+    return ok();
+}
+
+int gx_argmax_step(gx_ctx *ctx, const float *x, int n, int32_t *ids, int32_t *history, int history_len,
+                   int32_t *pos, int32_t *positions) {
+    if (int rc = use(ctx))
+        return rc;
+    GX_CHECK(n > 0 && history_len > 0, "gx: bad shape");
+    GX_CHECK(x && ids && history && pos && positions, "gx: missing argument");
+    if (int rc = gx::launch_argmax(ctx, x, n, 1, n, ids, history, history_len, pos, positions))
         return rc;
     return ok();
 }

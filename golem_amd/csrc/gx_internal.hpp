@@ -61,8 +61,13 @@ struct gx_ctx {
     hipEvent_t t0, t1;
     int cu_count;
     float *gelu_table;  // golem's 65536-entry GELU table, built on the device at init
+    float *argmax_v;    // the greedy pick's part maxima [kArgmaxRows][kArgmaxParts]
+    int32_t *argmax_i;  // and their indices
 };
 
+
+constexpr int kArgmaxParts = 128;  // workgroups per row of the greedy pick
+constexpr int kArgmaxRows = 64;    // rows per launch pair
 
 struct gx_weight {
     gx_ctx *ctx;
@@ -148,7 +153,8 @@ int launch_qwen_attention(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int
                           const int32_t *slots, int nslots);
 int launch_qwen_swiglu_quant(gx_ctx *ctx, const float *gu, int ldgu, int M, int ffn, int group, int8_t *q,
                              float *scales, int32_t *qsum);
-int launch_argmax(gx_ctx *ctx, const float *x, int ldx, int M, int n, int32_t *out);
+int launch_argmax(gx_ctx *ctx, const float *x, int ldx, int M, int n, int32_t *out, int32_t *history,
+                  int history_len, int32_t *pos, int32_t *positions);
 int launch_f32_matvec(gx_ctx *ctx, const gx_weight *w, const float *x, int ldx, int M, int row_start, int row_end,
                       float *y, int ldy);
 }  // namespace gx

@@ -17,7 +17,8 @@
 //   swiglu_quant    silu(gate) * up with ggml's expf, Q8_0 (block.go:82-90,
 //                   nn/swiglu.go:31-82)
 //   Down product; its residual add opens the next block's norm_quant.
-// argmax_kernel is the greedy pick over logits (ties to the lower id).
+// argmax_part_kernel + argmax_final_kernel are the greedy pick over logits
+// (ties to the lower id).
 //
 // The per-head RMSNormPlain sums its 128 squares left to right in float64, as
 // golem does; the width-wide one uses the fixed tree of gx_device.hpp.
@@ -862,53 +863,105 @@ __global__ __launch_bounds__(256) void qwen_swiglu_quant_kernel(const float *__r
     }
 }
 
-// One row per workgroup: the index of the largest value, the lower index on
-// ties (NaN never wins).  Each thread scans a strided set of float4s, then the
-// workgroup reduces (value, index) pairs.
-constexpr int kArgmaxThreads = 1024;
-__global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float *__restrict__ x, int ldx, int n,
-                                                                int32_t *__restrict__ out) {
-    __shared__ float bv_sh[kArgmaxThreads];
-    __shared__ int bi_sh[kArgmaxThreads];
-    const int tid = threadIdx.x;
-    const float *r = x + (size_t)blockIdx.x * ldx;
+// Greedy choice in two launches: kArgmaxParts workgroups per row each take
+// a contiguous part and leave the part's largest value and the lowest index
+// holding it (none if the part is all NaN: NaN never wins); one wavefront per
+// row then merges the parts.  "Larger value, else lower index" is a total
+// order, so the result is the index of the largest value, the lower index on
+// ties, whatever the split (0 when every value is NaN).
+constexpr int kArgmaxThreads = 256;
+constexpr int kNone = 0x7fffffff;
+
+__device__ __forceinline__ void argmax_merge(float &bv, int &bi, float ov, int oi) {
+    if (oi != kNone && (bi == kNone || ov > bv || (ov == bv && oi < bi))) {
+        bv = ov;
+        bi = oi;
+    }
+}
+
+// grid (kArgmaxParts, M)
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_part_kernel(const float *__restrict__ x, int ldx, int n,
+                                                                     float *__restrict__ part_v,
+                                                                     int32_t *__restrict__ part_i) {
+    __shared__ float bv_sh[kArgmaxThreads / 64];
+    __shared__ int bi_sh[kArgmaxThreads / 64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const float *r = x + (size_t)blockIdx.y * ldx;
+    const int chunk = ((n + kArgmaxParts - 1) / kArgmaxParts + 3) & ~3;
+    const int lo = min(n, (int)blockIdx.x * chunk), hi = min(n, lo + chunk);
     float bv = -INFINITY;
-    int bi = 0x7fffffff;
+    int bi = kNone;
     auto take = [&](float v, int i) {
-        if (v > bv || (bi == 0x7fffffff && v == v)) {  // scanned in rising order: equal values keep the first
+        if (v > bv || (bi == kNone && v == v)) {  // rising order: equal values keep the first
             bv = v;
             bi = i;
         }
     };
-    const bool vec = ((uintptr_t)r & 15) == 0;
-    const int n4 = vec ? n / 4 : 0;
+    if (((uintptr_t)r & 15) == 0) {
+        const int q0 = lo / 4, q1 = hi / 4;  // lo is a multiple of 4
 #pragma unroll 4
-    for (int q = tid; q < n4; q += kArgmaxThreads) {
-        const float4 v = *(const float4 *)(r + 4 * q);
-        take(v.x, 4 * q);
-        take(v.y, 4 * q + 1);
-        take(v.z, 4 * q + 2);
-        take(v.w, 4 * q + 3);
-    }
-    for (int i = 4 * n4 + tid; i < n; i += kArgmaxThreads)
-        take(r[i], i);
-    bv_sh[tid] = bv;
-    bi_sh[tid] = bi;
-    __syncthreads();
-    for (int w = kArgmaxThreads / 2; w > 0; w >>= 1) {
-        if (tid < w) {
-            const float ov = bv_sh[tid + w];
-            const int oi = bi_sh[tid + w];
-            if (oi != 0x7fffffff && (bi_sh[tid] == 0x7fffffff || ov > bv_sh[tid] ||
-                                     (ov == bv_sh[tid] && oi < bi_sh[tid]))) {
-                bv_sh[tid] = ov;
-                bi_sh[tid] = oi;
-            }
+        for (int q = q0 + tid; q < q1; q += kArgmaxThreads) {
+            const float4 v = *(const float4 *)(r + 4 * q);
+            take(v.x, 4 * q);
+            take(v.y, 4 * q + 1);
+            take(v.z, 4 * q + 2);
+            take(v.w, 4 * q + 3);
         }
-        __syncthreads();
+        for (int i = 4 * q1 + tid; i < hi; i += kArgmaxThreads)
+            take(r[i], i);
+    } else {
+        for (int i = lo + tid; i < hi; i += kArgmaxThreads)
+            take(r[i], i);
     }
-    if (tid == 0)
-        out[blockIdx.x] = bi_sh[0] == 0x7fffffff ? 0 : bi_sh[0];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(bv, off, 64);
+        const int oi = __shfl_xor(bi, off, 64);
+        argmax_merge(bv, bi, ov, oi);
+    }
+    if (lane == 0) {
+        bv_sh[wave] = bv;
+        bi_sh[wave] = bi;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < kArgmaxThreads / 64; w++)
+            argmax_merge(bv, bi, bv_sh[w], bi_sh[w]);
+        part_v[(size_t)blockIdx.y * kArgmaxParts + blockIdx.x] = bv;
+        part_i[(size_t)blockIdx.y * kArgmaxParts + blockIdx.x] = bi;
+    }
+}
+
+// grid (M), one wavefront.  With `history` (M = 1, a captured decode step):
+// also history[*pos + 1] = id, *pos += 1, positions[0] = the new *pos.
+__global__ __launch_bounds__(64) void argmax_final_kernel(const float *__restrict__ part_v,
+                                                          const int32_t *__restrict__ part_i,
+                                                          int32_t *__restrict__ out, int32_t *__restrict__ history,
+                                                          int history_len, int32_t *__restrict__ pos,
+                                                          int32_t *__restrict__ positions) {
+    const int lane = threadIdx.x;
+    float bv = -INFINITY;
+    int bi = kNone;
+    for (int p = lane; p < kArgmaxParts; p += 64)
+        argmax_merge(bv, bi, part_v[(size_t)blockIdx.x * kArgmaxParts + p],
+                     part_i[(size_t)blockIdx.x * kArgmaxParts + p]);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(bv, off, 64);
+        const int oi = __shfl_xor(bi, off, 64);
+        argmax_merge(bv, bi, ov, oi);
+    }
+    if (lane == 0) {
+        const int id = bi == kNone ? 0 : bi;
+        out[blockIdx.x] = id;
+        if (history) {
+            const int next = pos[0] + 1;
+            if (next < history_len)
+                history[next] = id;
+            pos[0] = next;
+            positions[0] = next;
+        }
+    }
 }
 
 }  // namespace
@@ -1074,9 +1127,18 @@ int launch_qwen_swiglu_quant(gx_ctx *ctx, const float *gu, int ldgu, int M, int 
     return check_launch("qwen_swiglu_quant");
 }
 
-int launch_argmax(gx_ctx *ctx, const float *x, int ldx, int M, int n, int32_t *out) {
-    argmax_kernel<<<M, kArgmaxThreads, 0, ctx->stream>>>(x, ldx, n, out);
-    return check_launch("argmax");
+int launch_argmax(gx_ctx *ctx, const float *x, int ldx, int M, int n, int32_t *out, int32_t *history,
+                  int history_len, int32_t *pos, int32_t *positions) {
+    for (int m0 = 0; m0 < M; m0 += kArgmaxRows) {
+        const int rows = min(kArgmaxRows, M - m0);
+        argmax_part_kernel<<<dim3(kArgmaxParts, (unsigned)rows), kArgmaxThreads, 0, ctx->stream>>>(
+            x + (size_t)m0 * ldx, ldx, n, ctx->argmax_v, ctx->argmax_i);
+        argmax_final_kernel<<<rows, 64, 0, ctx->stream>>>(ctx->argmax_v, ctx->argmax_i, out + m0, history,
+                                                          history_len, pos, positions);
+        if (int rc = check_launch("argmax"))
+            return rc;
+    }
+    return GX_OK;
 }
 
 }  // namespace gx

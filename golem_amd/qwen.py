@@ -136,7 +136,7 @@ class QwenModel:
         self.bs = torch.empty((M, cfg.dim // 16), dtype=torch.int16, device="cuda")
         self.logit = torch.empty((M, cfg.vocab), dtype=torch.float32, device="cuda")
         self.next_id = torch.empty((M,), dtype=torch.int32, device="cuda")
-        self.pos64 = torch.zeros((1,), dtype=torch.int64, device="cuda")  # the graph's position counter
+        self.pos_dev = torch.zeros((1,), dtype=torch.int32, device="cuda")  # the graph's position counter
         self.history = torch.zeros((cfg.max_context + 1,), dtype=torch.int32, device="cuda")
         self.graph = None
         n = capi.size_out("gx_qwen_attention_workspace_bytes", M, cfg.heads, cfg.max_context - 1)
@@ -296,14 +296,14 @@ class QwenModel:
 
     def _decode_step(self):
         """One greedy step read entirely from the device: token self.tokens[0]
-        at position self.pos64.  Leaves the next token in self.tokens[0] and
+        at position self.pos_dev.  Leaves the next token in self.tokens[0] and
         in self.history[position + 1], and advances the position."""
-        self.positions[:1].copy_(self.pos64)
         self._blocks(1, self.slot_context - 1)
-        self.next_token(0)
-        self.history.index_copy_(0, self.pos64 + 1, self.next_id[:1])
-        self.tokens[:1].copy_(self.next_id[:1])
-        self.pos64.add_(1)
+        self.logits(0)
+        # the argmax, straight into the next step's token, and the history
+        # entry, counter and position of the next step, in one launch pair
+        self._call("gx_argmax_step", self.ctx.ptr, self._vp(self.logit), self.cfg.vocab, self._vp(self.tokens),
+                   self._vp(self.history), self.history.numel(), self._vp(self.pos_dev), self._vp(self.positions))
 
     def capture_decode(self):
         """Records _decode_step into a HIP graph (once).  The library's stream
@@ -446,7 +446,8 @@ class QwenModel:
             raise ValueError(f"qwen: position {pos} is past the context {self.cfg.max_context}")
         self.tokens[:1].copy_(tok)
         self.history[pos:pos + 1].copy_(tok)
-        self.pos64.fill_(pos)
+        self.pos_dev.fill_(pos)
+        self.positions[:1].fill_(pos)
 
     def decoded(self, pos, steps):
         """The ids of `steps` greedy tokens from position `pos`: the seed

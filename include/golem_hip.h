@@ -343,6 +343,15 @@ int gx_swiglu_quant(gx_ctx *ctx, const float *gu, int ldgu, int M, int ffn, int 
  * index on ties (qwen/model_test.go:118-126). */
 int gx_argmax(gx_ctx *ctx, const float *x, int ldx, int M, int n, int32_t *ids);
 
+/* One greedy step of a decode loop kept on the device (what golem's
+ * generation loop does on the host after Logits, qwen/model.go): ids[0] =
+ * gx_argmax of x[0..n); then history[*pos + 1] = ids[0] (when *pos + 1 <
+ * history_len), *pos += 1 and positions[0] = the new *pos, so that a captured
+ * decode step reads its next token and position from the device.  pos,
+ * positions, history, ids: device int32. */
+int gx_argmax_step(gx_ctx *ctx, const float *x, int n, int32_t *ids, int32_t *history, int history_len,
+                   int32_t *pos, int32_t *positions);
+
 /* ---- GGUF checkpoints (host only; no GPU needed) ----------------------- */
 
 /* An opened GGUF file: mapped whole, read in place (tensors/gguf.go:33-41,

@@ -415,3 +415,55 @@ def test_argmax_ties_to_lower_id(dev):
     xd = dev.put(x)
     capi.call("gx_argmax", dev.ctx.ptr, capi.vp(xd), x.shape[1], 3, x.shape[1], capi.vp(ids))
     assert dev.get(ids).tolist() == [77, 151935, 9]
+
+
+def _argmax_want(row):
+    """The greedy pick: the largest non-NaN value, the lower index on ties;
+    0 when every value is NaN."""
+    ok = ~np.isnan(row)
+    if not ok.any():
+        return 0
+    best = row[ok].max()
+    return int(np.flatnonzero(ok & (row == best))[0])
+
+
+@pytest.mark.parametrize("n", [1, 5, 511, 513, 4097, 151936])
+def test_argmax_parts_merge_in_order(dev, n):
+    """The two-level pick (parts of a row, then their merge) against the
+    rule itself, on rows whose maxima repeat across parts (ties to the lower
+    id), rows of NaN and -inf, an unaligned row stride, and more rows than
+    one launch pair takes (70 > 64)."""
+    g = synth.rng(900 + n)
+    M, ld = 70, n + 3
+    x = np.full((M, ld), -np.inf, np.float32)
+    x[:, :n] = g.integers(-50, 50, (M, n)).astype(np.float32)  # many equal values
+    x[1, :n] = np.nan
+    x[2, :n] = -np.inf
+    x[3, :n] = 7.0
+    x[4, :n] = np.where(g.random(n) < 0.5, np.nan, x[4, :n])
+    ids = dev.empty((M,), np.int32)
+    xd = dev.put(x)
+    capi.call("gx_argmax", dev.ctx.ptr, capi.vp(xd), ld, M, n, capi.vp(ids))
+    got = dev.get(ids).tolist()
+    assert got == [_argmax_want(x[m, :n]) for m in range(M)]
+
+
+def test_argmax_step_bookkeeping(dev):
+    """gx_argmax_step: the id lands in ids[0] and at history[pos + 1]; the
+    counter and positions[0] advance by one; past the history's end nothing
+    is written there."""
+    n = 151936
+    x = np.zeros((1, n), np.float32)
+    x[0, 4321] = 9.0
+    xd = dev.put(x)
+    ids = dev.put(np.array([-1], np.int32))
+    hist = dev.put(np.full((10,), -5, np.int32))
+    pos = dev.put(np.array([6], np.int32))
+    positions = dev.put(np.array([6, 77], np.int32))
+    for step in range(4):
+        capi.call("gx_argmax_step", dev.ctx.ptr, capi.vp(xd), n, capi.vp(ids), capi.vp(hist), 10, capi.vp(pos),
+                  capi.vp(positions))
+    assert dev.get(ids).tolist() == [4321]
+    assert dev.get(hist).tolist() == [-5] * 7 + [4321] * 3  # positions 7, 8, 9; 10 is past the end
+    assert dev.get(pos).tolist() == [10]
+    assert dev.get(positions).tolist() == [10, 77]
