@@ -73,20 +73,22 @@ __global__ __launch_bounds__(kLogitsThreads) void moe_logits_one_kernel(const fl
     const float *rg = router + (size_t)e * D;
     const float *xg = resid + (size_t)t * ldr;
     const int n4 = D / 4;
-    float4 rv[kLogitsOneF4 + 1], xv[kLogitsOneF4 + 1];
+    // Clamped indices and clamped stores (a thread past the end stores the
+    // last piece's own value again): every load is issued before the first
+    // wait, with no branch for a load to sink into.
+    float4 rv[kLogitsOneF4 + 1], xv[kLogitsOneF4 + 1], sv[kLogitsOneF4 + 1];
 #pragma unroll
-    for (int f = 0; f <= kLogitsOneF4; f++) {  // clamped: every load issued, no branch
+    for (int f = 0; f <= kLogitsOneF4; f++) {
         const int q = min(tid + f * kLogitsThreads, n4 - 1);
         rv[f] = *(const float4 *)(rg + 4 * q);
         xv[f] = *(const float4 *)(xg + 4 * q);
+        sv[f] = router_scale ? *(const float4 *)(router_scale + 4 * q) : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
     }
 #pragma unroll
     for (int f = 0; f <= kLogitsOneF4; f++) {
-        const int q = tid + f * kLogitsThreads;
-        if (q < n4) {
-            *(float4 *)(row + 4 * q) = rv[f];
-            *(float4 *)(xr + 4 * q) = xv[f];
-        }
+        const int q = min(tid + f * kLogitsThreads, n4 - 1);
+        *(float4 *)(row + 4 * q) = rv[f];
+        *(float4 *)(xr + 4 * q) = xv[f];
     }
     __syncthreads();
     double p0, p1;
@@ -97,10 +99,19 @@ __global__ __launch_bounds__(kLogitsThreads) void moe_logits_one_kernel(const fl
     __syncthreads();
     const float sc = scale_sh;
     const float inv_sqrt_dim = (float)(1.0 / sqrt((double)D));
-    for (int i = tid; i < D; i += kLogitsThreads) {
-        const float normed = xr[i] * sc;
-        const float factor = inv_sqrt_dim * (router_scale ? router_scale[i] : 1.0f);
-        xr[i] = normed * factor;
+    // x * scale * ((1/sqrt(D)) * RouterScale[i]), from the registers
+#pragma unroll
+    for (int f = 0; f <= kLogitsOneF4; f++) {
+        const int q = min(tid + f * kLogitsThreads, n4 - 1);
+        const float x4[4] = {xv[f].x, xv[f].y, xv[f].z, xv[f].w}, s4[4] = {sv[f].x, sv[f].y, sv[f].z, sv[f].w};
+        float o4[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const float normed = x4[c] * sc;
+            const float factor = inv_sqrt_dim * s4[c];
+            o4[c] = normed * factor;
+        }
+        *(float4 *)(xr + 4 * q) = make_float4(o4[0], o4[1], o4[2], o4[3]);
     }
     __syncthreads();
     if (tid < 64) {
