@@ -53,7 +53,9 @@ _SIGNATURES = {
     "gx_matmul_q4_0_expert": [_vp, _vp, _c_int, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _c_int],
     "gx_matmul_q6_k": [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _vp, _c_int],
     "gx_matmul_f32": [_vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _c_int],
-    "gx_q4_0_block_dots": [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp],
+    "gx_q4_0_block_dots": [_vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp],
+    "gx_q4_0_fused_block_dots": [_vp, _vp, _c_int, _vp, _vp, _vp, ctypes.c_float, _c_int, _c_int, _vp, _vp, _vp,
+                                 _vp],
     "gx_q6_k_block_dots": [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp],
     "gx_gelu_table": [_vp, _vp],
     "gx_moe_workspace_bytes": [_c_int, _c_int, _c_int, _c_int, _c_int, ctypes.POINTER(_c_size)],
@@ -67,6 +69,11 @@ _SIGNATURES = {
                                ctypes.c_float, _vp, _vp, _c_int, _vp, _vp, _vp, _vp, _c_int],
     "gx_qwen_attention": [_vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _c_int, _vp, _vp, _vp,
                           _vp, _c_size, _vp, _c_int],
+    "gx_qwen_attention_parallel": [_vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _c_int, _vp, _vp,
+                                   _vp, _vp, _c_size, _vp, _c_int],
+    "gx_qwen_rope_attention_parallel": [_vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _vp,
+                                        ctypes.c_float, _vp, _vp, _c_int, _vp, _vp, _vp, _vp, _c_int],
+    "gx_qwen_attention_heads": [_vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _c_int, _vp],
     "gx_swiglu_quant": [_vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp],
     "gx_norm_matmul_q4_0": [_vp, _vp, _vp, _vp, _vp, ctypes.c_float, _vp, _c_int, _c_int, _vp],
     "gx_norm_swiglu_q4_0": [_vp, _vp, _vp, _vp, _vp, ctypes.c_float, _vp, _vp, _vp, _vp],

@@ -397,11 +397,11 @@ static int q4_0_product(gx_ctx *ctx, const gx_weight *w, int expert, const int8_
     GX_CHECK(((uintptr_t)q16 & 15) == 0, "gx: q16 must be 16-byte aligned");
     int rc;
     if (M <= 8)
-        rc = gx::launch_q4_0_matvec(ctx, w, mat, q, scales, qsum, M, row_start, row_end, bias, y, ldy);
+        rc = gx::launch_q4_0_matvec(ctx, w, mat, q, scales, qsum, M, row_start, row_end, bias, y, ldy, nullptr, -1);
     else if (q16)
         rc = gx::launch_q4_0_gemm_f16(ctx, w, mat, q16, scales, M, row_start, row_end, bias, y, ldy, nullptr);
     else
-        rc = gx::launch_q4_0_gemm(ctx, w, mat, q, scales, qsum, M, row_start, row_end, bias, y, ldy, nullptr);
+        rc = gx::launch_q4_0_gemm(ctx, w, mat, q, scales, M, row_start, row_end, bias, y, ldy, nullptr);
     if (rc)
         return rc;
     return ok();
@@ -426,7 +426,7 @@ int gx_norm_matmul_q4_0(gx_ctx *ctx, const gx_weight *w, const float *x, const f
     if (row_start == row_end)
         return ok();
     if (int rc = gx::launch_q4_0_matvec_fused(ctx, w, 0, row_start, row_end, y, x, add, gain, eps, x_out, nullptr,
-                                              nullptr, nullptr))
+                                              nullptr, nullptr, nullptr))
         return rc;
     return ok();
 }
@@ -444,7 +444,27 @@ int gx_norm_swiglu_q4_0(gx_ctx *ctx, const gx_weight *w, const float *x, const f
     GX_CHECK(x_out == nullptr || (x_out != x && x_out != add),
              "gx: x_out must not alias x or add (other workgroups still read them)");
     if (int rc = gx::launch_q4_0_matvec_fused(ctx, w, 1, 0, w->rows, nullptr, x, add, gain, eps, x_out, q, scales,
-                                              qsum))
+                                              qsum, nullptr))
+        return rc;
+    return ok();
+}
+
+int gx_q4_0_fused_block_dots(gx_ctx *ctx, const gx_weight *w, int swiglu, const float *x, const float *add,
+                             const float *gain, float eps, int row_start, int row_end, int8_t *q, float *scales,
+                             int32_t *qsum, int32_t *out) {
+    if (int rc = use(ctx))
+        return rc;
+    if (int rc = check_product(w, GX_Q4_0, 1, row_start, row_end, out, row_end))
+        return rc;
+    GX_CHECK(w->count == 1, "gx: a fused product takes a single matrix");
+    GX_CHECK(x && gain && out, "gx: missing argument");
+    GX_CHECK(((uintptr_t)gain & 15) == 0, "gx: gain must be 16-byte aligned");
+    GX_CHECK(swiglu == 0 || (row_start == 0 && row_end == w->rows && w->rows % 64 == 0 && q && scales && qsum),
+             "gx: the SwiGLU form takes every row (a multiple of 64) and its Q8_0 outputs");
+    if (row_start == row_end)
+        return ok();
+    if (int rc = gx::launch_q4_0_matvec_fused(ctx, w, swiglu ? 1 : 0, row_start, row_end, nullptr, x, add, gain, eps,
+                                              nullptr, q, scales, qsum, out))
         return rc;
     return ok();
 }
@@ -484,23 +504,26 @@ int gx_matmul_f32(gx_ctx *ctx, const gx_weight *w, const float *x, int ldx, int 
     return ok();
 }
 
-int gx_q4_0_block_dots(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const int32_t *qsum, const uint16_t *q16,
-                       int M, int row_start, int row_end, int path, int32_t *out) {
+int gx_q4_0_block_dots(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const float *scales, const int32_t *qsum,
+                       const uint16_t *q16, int M, int row_start, int row_end, int path, int32_t *out) {
     if (int rc = use(ctx))
         return rc;
     if (int rc = check_product(w, GX_Q4_0, M, row_start, row_end, out, row_end))
         return rc;
-    GX_CHECK(q && qsum, "gx: missing activation");
+    GX_CHECK(q && qsum && scales, "gx: missing activation");
     GX_CHECK(((uintptr_t)q & 15) == 0, "gx: q must be 16-byte aligned");
-    GX_CHECK(path >= 0 && path <= 2, "gx: path must be 0 (matrix-vector), 1 (int8 MFMA) or 2 (fp16 MFMA)");
+    GX_CHECK(path >= 0 && path <= 3,
+             "gx: path must be 0 (matrix-vector), 1 (int8 MFMA), 2 (fp16 MFMA) or 3 (one-column matrix-vector)");
     GX_CHECK(path != 2 || (q16 && ((uintptr_t)q16 & 15) == 0), "gx: path 2 needs a 16-byte aligned q16");
+    GX_CHECK(path != 3 || M == 1, "gx: path 3 takes one column, not %d", M);
     if (M == 0 || row_start == row_end)
         return ok();
     int rc;
-    if (path == 0)
-        rc = gx::launch_q4_0_block_dots_matvec(ctx, w, q, qsum, M, row_start, row_end, out);
+    if (path == 0 || path == 3)
+        rc = gx::launch_q4_0_matvec(ctx, w, w->dev, q, scales, qsum, M, row_start, row_end, nullptr, nullptr, 0, out,
+                                    path == 0 ? 0 : 1);
     else if (path == 1)
-        rc = gx::launch_q4_0_gemm(ctx, w, w->dev, q, nullptr, qsum, M, row_start, row_end, nullptr, nullptr, 0, out);
+        rc = gx::launch_q4_0_gemm(ctx, w, w->dev, q, scales, M, row_start, row_end, nullptr, nullptr, 0, out);
     else
         rc = gx::launch_q4_0_gemm_f16(ctx, w, w->dev, q16, nullptr, M, row_start, row_end, nullptr, nullptr, 0, out);
     if (rc)
@@ -589,11 +612,11 @@ int gx_qwen_qk_rope(gx_ctx *ctx, const float *qkv, int ldqkv, int M, int heads, 
     return ok();
 }
 
-int gx_qwen_rope_attention(gx_ctx *ctx, const float *qkv, int ldqkv, int heads, int kv_heads, int head_dim,
-                           int max_pos, const int32_t *positions, const float *q_norm, const float *k_norm,
-                           const float *rope_cos, const float *rope_sin, float eps, uint16_t *kcache,
-                           uint16_t *vcache, int context, int8_t *q, float *scales, int32_t *qsum,
-                           const int32_t *slots, int nslots) {
+static int rope_attention(gx_ctx *ctx, const float *qkv, int ldqkv, int heads, int kv_heads, int head_dim,
+                          int max_pos, const int32_t *positions, const float *q_norm, const float *k_norm,
+                          const float *rope_cos, const float *rope_sin, float eps, uint16_t *kcache, uint16_t *vcache,
+                          int context, int8_t *q, float *scales, int32_t *qsum, const int32_t *slots, int nslots,
+                          int parallel) {
     if (int rc = use(ctx))
         return rc;
     GX_CHECK(heads > 0 && kv_heads > 0 && heads % kv_heads == 0, "gx: %d query heads over %d key-value heads", heads,
@@ -608,9 +631,27 @@ int gx_qwen_rope_attention(gx_ctx *ctx, const float *qkv, int ldqkv, int heads, 
     const float scale = (float)(1.0 / sqrt((double)head_dim));
     if (int rc = gx::launch_qwen_rope_attention(ctx, qkv, ldqkv, heads, kv_heads, head_dim, max_pos, positions, q_norm,
                                                 k_norm, rope_cos, rope_sin, eps, kcache, vcache, context, scale, q,
-                                                scales, qsum, slots, nslots))
+                                                scales, qsum, slots, nslots, parallel))
         return rc;
     return ok();
+}
+
+int gx_qwen_rope_attention(gx_ctx *ctx, const float *qkv, int ldqkv, int heads, int kv_heads, int head_dim,
+                           int max_pos, const int32_t *positions, const float *q_norm, const float *k_norm,
+                           const float *rope_cos, const float *rope_sin, float eps, uint16_t *kcache,
+                           uint16_t *vcache, int context, int8_t *q, float *scales, int32_t *qsum,
+                           const int32_t *slots, int nslots) {
+    return rope_attention(ctx, qkv, ldqkv, heads, kv_heads, head_dim, max_pos, positions, q_norm, k_norm, rope_cos,
+                          rope_sin, eps, kcache, vcache, context, q, scales, qsum, slots, nslots, 0);
+}
+
+int gx_qwen_rope_attention_parallel(gx_ctx *ctx, const float *qkv, int ldqkv, int heads, int kv_heads,
+                                    int head_dim, int max_pos, const int32_t *positions, const float *q_norm,
+                                    const float *k_norm, const float *rope_cos, const float *rope_sin, float eps,
+                                    uint16_t *kcache, uint16_t *vcache, int context, int8_t *q, float *scales,
+                                    int32_t *qsum, const int32_t *slots, int nslots) {
+    return rope_attention(ctx, qkv, ldqkv, heads, kv_heads, head_dim, max_pos, positions, q_norm, k_norm, rope_cos,
+                          rope_sin, eps, kcache, vcache, context, q, scales, qsum, slots, nslots, 1);
 }
 
 int gx_qwen_attention_workspace_bytes(int M, int heads, int max_pos, size_t *bytes) {
@@ -619,10 +660,10 @@ int gx_qwen_attention_workspace_bytes(int M, int heads, int max_pos, size_t *byt
     return ok();
 }
 
-int gx_qwen_attention(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int kv_heads, int head_dim, int max_pos,
-                      const int32_t *positions, const uint16_t *kcache, const uint16_t *vcache, int context,
-                      int8_t *q, float *scales, int32_t *qsum, void *workspace, size_t workspace_bytes,
-                      const int32_t *slots, int nslots) {
+static int attention(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int kv_heads, int head_dim, int max_pos,
+                     const int32_t *positions, const uint16_t *kcache, const uint16_t *vcache, int context, int8_t *q,
+                     float *scales, int32_t *qsum, void *workspace, size_t workspace_bytes, const int32_t *slots,
+                     int nslots, int parallel) {
     if (int rc = use(ctx))
         return rc;
     GX_CHECK(heads > 0 && kv_heads > 0 && heads % kv_heads == 0, "gx: %d query heads over %d key-value heads", heads,
@@ -642,9 +683,47 @@ int gx_qwen_attention(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int kv_
     const float scale = (float)(1.0 / sqrt((double)head_dim));
     if (int rc = gx::launch_qwen_attention(ctx, qh, M, heads, kv_heads, head_dim, max_pos, positions, kcache, vcache,
                                            context, scale, q, scales, qsum, (uint8_t *)workspace, slots,
-                                           nslots))
+                                           nslots, parallel, nullptr))
         return rc;
     return ok();
+}
+
+int gx_qwen_attention(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int kv_heads, int head_dim, int max_pos,
+                      const int32_t *positions, const uint16_t *kcache, const uint16_t *vcache, int context,
+                      int8_t *q, float *scales, int32_t *qsum, void *workspace, size_t workspace_bytes,
+                      const int32_t *slots, int nslots) {
+    return attention(ctx, qh, M, heads, kv_heads, head_dim, max_pos, positions, kcache, vcache, context, q, scales,
+                     qsum, workspace, workspace_bytes, slots, nslots, 0);
+}
+
+int gx_qwen_attention_heads(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int kv_heads, int head_dim,
+                            int max_pos, const int32_t *positions, const uint16_t *kcache, const uint16_t *vcache,
+                            int context, float *out) {
+    if (int rc = use(ctx))
+        return rc;
+    GX_CHECK(heads > 0 && kv_heads > 0 && heads % kv_heads == 0, "gx: %d query heads over %d key-value heads", heads,
+             kv_heads);
+    GX_CHECK(M > 0 && M <= 4 && max_pos >= 0 && max_pos < 768, "gx: the head outputs are for a decode step (M <= 4, "
+                                                                "prefixes to 768)");
+    GX_CHECK(head_dim == 32 || head_dim == 64 || head_dim == 96 || head_dim == 128,
+             "gx: attention supports head widths 32, 64, 96 and 128");
+    GX_CHECK(context % 8 == 0 && max_pos < context, "gx: a cache of %d positions (a multiple of 8) cannot hold %d",
+             context, max_pos);
+    GX_CHECK(qh && positions && kcache && vcache && out, "gx: missing argument");
+    GX_CHECK(((uintptr_t)vcache & 15) == 0, "gx: the value cache must be 16-byte aligned");
+    const float scale = (float)(1.0 / sqrt((double)head_dim));
+    if (int rc = gx::launch_qwen_attention(ctx, qh, M, heads, kv_heads, head_dim, max_pos, positions, kcache, vcache,
+                                           context, scale, nullptr, nullptr, nullptr, nullptr, nullptr, 0, 1, out))
+        return rc;
+    return ok();
+}
+
+int gx_qwen_attention_parallel(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int kv_heads, int head_dim,
+                               int max_pos, const int32_t *positions, const uint16_t *kcache,
+                               const uint16_t *vcache, int context, int8_t *q, float *scales, int32_t *qsum,
+                               void *workspace, size_t workspace_bytes, const int32_t *slots, int nslots) {
+    return attention(ctx, qh, M, heads, kv_heads, head_dim, max_pos, positions, kcache, vcache, context, q, scales,
+                     qsum, workspace, workspace_bytes, slots, nslots, 1);
 }
 
 int gx_swiglu_quant(gx_ctx *ctx, const float *gu, int ldgu, int M, int ffn, int group, int8_t *q, float *scales,

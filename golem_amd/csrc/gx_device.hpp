@@ -19,6 +19,16 @@ __device__ __forceinline__ uint32_t float_to_half_bits(float f) {
     return (uint32_t)__half_as_ushort(__float2half_rn(f));
 }
 
+// A workgroup barrier that orders LDS only: it waits for this wavefront's
+// LDS operations (lgkmcnt), not for its global loads or stores in flight
+// (__syncthreads' fence waits for those too once a global store precedes
+// it).  Global memory written before it is not made visible by it.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // The j-th of the eight fp16 values packed in a 16-byte chunk.
 __device__ __forceinline__ float chunk_half(const uint4 &c, int j) {
     const uint32_t word = (j >> 1) == 0 ? c.x : (j >> 1) == 1 ? c.y : (j >> 1) == 2 ? c.z : c.w;

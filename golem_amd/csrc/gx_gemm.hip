@@ -588,12 +588,16 @@ __device__ __forceinline__ void wait_vmcnt() {  // vmcnt <= N; expcnt, lgkmcnt u
     __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
+// DOTS: the same kernel, also writing every block's integer (the chain
+// difference x below) to dots[t][n - row_start][b]; the scales are then not
+// needed, and their loads read the activation instead (in bounds).
+template <bool DOTS>
 __global__ __launch_bounds__(512, 4) void q4_0_gemm_dma_kernel(const uint8_t *__restrict__ W, size_t plane0_bytes,
                                                             int B, int DC, const int8_t *__restrict__ q,
                                                             const float *__restrict__ scales, int K, int M,
                                                             int tiles, int tile0, int row_start, int row_end,
                                                             const float *__restrict__ bias, float *__restrict__ y,
-                                                            int ldy) {
+                                                            int ldy, int32_t *__restrict__ dots) {
     __shared__ __align__(16) uint8_t ring_lds[kDmaRing * kDmaSlot];
     const int tid = threadIdx.x;
     const int lane = tid & 63, wv = tid >> 6;
@@ -622,7 +626,8 @@ __global__ __launch_bounds__(512, 4) void q4_0_gemm_dma_kernel(const uint8_t *__
     // same three instructions.
     const uint8_t *ssrc;
     if (wv < 4) {
-        ssrc = (const uint8_t *)(scales + (size_t)(first + min(lane, count - 1)) * B);
+        ssrc = DOTS ? (const uint8_t *)(q + (size_t)(first + min(lane, count - 1)) * B * 4)
+                    : (const uint8_t *)(scales + (size_t)(first + min(lane, count - 1)) * B);
     } else {
         const int idx = 64 * (wv - 4) + lane, r = idx >> 1;
         const int dt = min(T0 + (r >> 6), tiles - 1);
@@ -724,6 +729,12 @@ __global__ __launch_bounds__(512, 4) void q4_0_gemm_dma_kernel(const uint8_t *__
                 const int nb = next[e], pb = prev[e];
                 const float x = __int_as_float(nb) - __int_as_float(pb);  // the block's isum, exactly
                 acc[e] = start ? x * S[e] : fmaf(x, S[e], acc[e]);
+                if constexpr (DOTS) {
+                    const int b = h * kStage + j, tt = 32 * tg + li;
+                    const int n = T0 * kTileRows + 32 * rg + 8 * (e >> 2) + 4 * g + (e & 3);
+                    if (b < B && tt < count && n >= row_start && n < row_end)
+                        dots[((size_t)(first + tt) * (row_end - row_start) + (n - row_start)) * B + b] = (int)x;
+                }
             }
             chain = next;
         });
@@ -762,7 +773,7 @@ __global__ __launch_bounds__(512, 4) void q4_0_gemm_dma_kernel(const uint8_t *__
     }
     wait_vmcnt<0>();  // the trailing loads land before the workgroup ends
     const int t = 32 * tg + li;
-    if (t < count) {
+    if (!DOTS && t < count) {
         float *yr = y + (size_t)(first + t) * ldy;
         const int nb = T0 * kTileRows + 32 * rg;  // the wavefront's first row
 #pragma unroll
@@ -777,20 +788,19 @@ __global__ __launch_bounds__(512, 4) void q4_0_gemm_dma_kernel(const uint8_t *__
 }  // namespace
 
 int launch_q4_0_gemm(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, const int8_t *q, const float *scales,
-                     const int32_t *qsum, int M, int row_start, int row_end, const float *bias, float *y, int ldy,
-                     int32_t *dots) {
-    (void)qsum;  // the widened weights are signed: no recentring term
+                     int M, int row_start, int row_end, const float *bias, float *y, int ldy, int32_t *dots) {
+    // the widened weights are signed: no recentring term, so no qsum
     const int tile0 = row_start / kTileRows;
-    dim3 grid((row_end + kTileRows - 1) / kTileRows - tile0, (M + kTokTile - 1) / kTokTile);
-    const Groups none{nullptr, nullptr, 1, 0};
+    const int tiles = (row_end + kTileRows - 1) / kTileRows - tile0;
+    const dim3 grid((unsigned)((tiles + 1) / 2), (unsigned)((M + kDmaTok - 1) / kDmaTok));
     if (dots)
-        q4_0_gemm_kernel<true, false><<<grid, 256, 0, ctx->stream>>>(mat, w->plane0_bytes, w->blocks, w->dchunks, q,
-                                                                     scales, w->cols, M, tile0, row_start, row_end,
-                                                                     bias, y, ldy, dots, none);
+        q4_0_gemm_dma_kernel<true><<<grid, 512, 0, ctx->stream>>>(mat, w->plane0_bytes, w->blocks, w->dchunks, q,
+                                                                  scales, w->cols, M, w->tiles, tile0, row_start,
+                                                                  row_end, bias, y, ldy, dots);
     else
-        q4_0_gemm_dma_kernel<<<dim3((grid.x + 1) / 2, (M + kDmaTok - 1) / kDmaTok), 512, 0, ctx->stream>>>(
-            mat, w->plane0_bytes, w->blocks, w->dchunks, q, scales, w->cols, M, w->tiles, tile0, row_start, row_end,
-            bias, y, ldy);
+        q4_0_gemm_dma_kernel<false><<<grid, 512, 0, ctx->stream>>>(mat, w->plane0_bytes, w->blocks, w->dchunks, q,
+                                                                   scales, w->cols, M, w->tiles, tile0, row_start,
+                                                                   row_end, bias, y, ldy, nullptr);
     return check_launch("q4_0_gemm");
 }
 

@@ -101,12 +101,14 @@ int launch_quantize_q8_0(gx_ctx *ctx, const float *x, int ldx, int M, int K, int
                          int32_t *qsum, float *corr, uint16_t *q16);
 int launch_quantize_q8_k(gx_ctx *ctx, const float *x, int ldx, int M, int K, int8_t *q, float *kscales,
                          int16_t *bsums);
+// form: -1 the product's own choice, 0 the SGPR-activation kernel, 1 the
+// one-column LDS kernel (M = 1).  dots: null, or the per-block integers
+// [M][row_end - row_start][K/32] of the kernel that runs.
 int launch_q4_0_matvec(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, const int8_t *q, const float *scales,
                        const int32_t *qsum, int M, int row_start, int row_end, const float *bias, float *y,
-                       int ldy);
+                       int ldy, int32_t *dots, int form);
 int launch_q4_0_gemm(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, const int8_t *q, const float *scales,
-                     const int32_t *qsum, int M, int row_start, int row_end, const float *bias, float *y, int ldy,
-                     int32_t *dots);
+                     int M, int row_start, int row_end, const float *bias, float *y, int ldy, int32_t *dots);
 int launch_q4_0_gemm_grouped(gx_ctx *ctx, const gx_weight *w, const int32_t *work, int max_items,
                              const int32_t *sorted, int act_div, const int8_t *q, const float *scales, float *y,
                              int ldy);
@@ -114,12 +116,11 @@ int launch_q4_0_gemm_f16(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, co
                          const float *scales, int M, int row_start, int row_end, const float *bias, float *y, int ldy,
                          int32_t *dots);
 int launch_q4_0_matvec_units(gx_ctx *ctx, const gx_weight *w, const int32_t *unit_expert, int units, int act_div,
-                              const int8_t *q, const float *scales, const int32_t *qsum, float *y, int ldy);
+                              const int8_t *q, const float *scales, const int32_t *qsum, float *y, int ldy,
+                              int32_t *dots);
 int launch_q4_0_matvec_fused(gx_ctx *ctx, const gx_weight *w, int epi, int row_start, int row_end, float *y,
                               const float *x, const float *add, const float *gain, float eps, float *x_out,
-                              int8_t *q, float *scales, int32_t *qsum);
-int launch_q4_0_block_dots_matvec(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const int32_t *qsum, int M,
-                                  int row_start, int row_end, int32_t *out);
+                              int8_t *q, float *scales, int32_t *qsum, int32_t *dots);
 int launch_q6_k_matvec(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const float *kscales,
                        const int16_t *bsums, int M, int row_start, int row_end, const float *bias, float *y,
                        int ldy, int32_t *dots);
@@ -146,11 +147,11 @@ int launch_qwen_rope_attention(gx_ctx *ctx, const float *qkv, int ldqkv, int hea
                                int max_pos, const int32_t *positions, const float *q_norm, const float *k_norm,
                                const float *rope_cos, const float *rope_sin, float eps, uint16_t *kcache,
                                uint16_t *vcache, int context, float scale, int8_t *q, float *scales, int32_t *qsum,
-                               const int32_t *slots, int nslots);
+                               const int32_t *slots, int nslots, int parallel);
 int launch_qwen_attention(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int kv_heads, int hd, int max_pos,
                           const int32_t *positions, const uint16_t *kcache, const uint16_t *vcache, int context,
                           float scale, int8_t *q, float *scales, int32_t *qsum, uint8_t *workspace,
-                          const int32_t *slots, int nslots);
+                          const int32_t *slots, int nslots, int parallel, float *heads_f);
 int launch_qwen_swiglu_quant(gx_ctx *ctx, const float *gu, int ldgu, int M, int ffn, int group, int8_t *q,
                              float *scales, int32_t *qsum);
 int launch_argmax(gx_ctx *ctx, const float *x, int ldx, int M, int n, int32_t *out, int32_t *history,

@@ -654,7 +654,7 @@ int launch_moe_experts(gx_ctx *ctx, const gx_weight *gate_up, const gx_weight *d
         if (int rc = launch_q4_0_gemm_grouped(ctx, gate_up, work, s.max_items, sorted, k, xq, xs, gu, 2 * F))
             return rc;
     } else {
-        if (int rc = launch_q4_0_matvec_units(ctx, gate_up, ids, U, k, xq, xs, xqs, gu, 2 * F))
+        if (int rc = launch_q4_0_matvec_units(ctx, gate_up, ids, U, k, xq, xs, xqs, gu, 2 * F, nullptr))
             return rc;
     }
     const size_t n = (size_t)U * F;
@@ -666,7 +666,7 @@ int launch_moe_experts(gx_ctx *ctx, const gx_weight *gate_up, const gx_weight *d
         if (int rc = launch_q4_0_gemm_grouped(ctx, down, work, s.max_items, sorted, 1, mq, ms, part, D))
             return rc;
     } else {
-        if (int rc = launch_q4_0_matvec_units(ctx, down, ids, U, 1, mq, ms, mqs, part, D))
+        if (int rc = launch_q4_0_matvec_units(ctx, down, ids, U, 1, mq, ms, mqs, part, D, nullptr))
             return rc;
     }
     const size_t no = (size_t)M * D;

@@ -3,9 +3,9 @@
 // This is golem's matVecPackedQ4_0Rows / matVecQ4_0Rows (nn/pack_q4_0.go:
 // 159-221, nn/dot_q4_0.go:168-270) rebuilt for a bandwidth-bound GPU kernel.
 //
-// Canonical order.  Every Q4_0 kernel in this library (this one and the
-// MFMA product) computes a row's value the same way, so that a column's
-// result does not depend on how many columns were in the batch:
+// Canonical order.  Every Q4_0 kernel in this library (these and the MFMA
+// products) computes a row's value the same way, so that a column's result
+// does not depend on how many columns were in the batch or which kernel ran:
 //   isum_b = sum_j (n_j - 8) * q_j                      exact int32
 //   s_b    = d_w[b] * d_a[b]                             one fp32 product
 //   P_s    = fma(float(isum_b), s_b, P_s) for the blocks b of stretch s,
@@ -14,13 +14,40 @@
 // golem sums the same integers with an unsigned nibble and a cancelling
 // correction term (nn/dot_q4_0.go:64-66); the two agree to rounding.
 //
-// Decomposition.  A workgroup owns one 64-row tile of the R64 layout; each
-// wavefront takes whole stretches, and a lane is one row of the tile.  The
-// wavefront's 16-byte loads of a stretch's chunks are 1 KiB contiguous, and
-// the activation of a stretch is the same for all 64 lanes, so it is read
-// with scalar loads into SGPRs and fed to v_dot4 from there: the vector
-// memory path carries weights only.  The stretch sums meet in LDS and one
-// wavefront adds them in order.
+// Three kernels:
+//   q4_0_matvec_kernel<NC, UNITS>  a workgroup owns one 64-row tile, a
+//       wavefront whole stretches, a lane one row.  The stretch's activation
+//       is the same for all 64 lanes, so it is read with scalar loads into
+//       SGPRs and fed to v_dot4 from there.  NC columns (8, 4, 2, 1) share
+//       one weight read; UNITS runs one expert of a stack per unit (MoE).
+//   q4_0_matvec_lds_kernel<R, IT>  one column (M = 1) of a matrix with few
+//       tiles: a workgroup owns R rows (a quarter tile) and all their
+//       stretches, lane l being row l % R and stretch slot l / R, so that
+//       four times as many workgroups pull weights with no cross-workgroup
+//       sum.  The stretches of a wavefront differ, so the activation is
+//       staged in LDS first.
+//   q4_0_matvec_fused_kernel<EPI, DB>  one position whose activation the
+//       product makes itself: x + add, RMSNormPlain(gain, eps) and Q8_0 (a
+//       block's pre-norm, qwen/block.go:45-52, 59-68), each wavefront
+//       quantising the stretch it multiplies into SGPRs; EPI 1 applies
+//       SwiGLU to a tile of gate and up rows interleaved by 32 and writes the
+//       Q8_0 block of its 32 outputs (qwen/block.go:82-90, nn/swiglu.go:
+//       77-82).
+//
+// Where the weight loads go out.  Measured on the box (a HIP graph of
+// launches over rotating weight copies, config 3's shapes): issuing every
+// weight load at a kernel's start, ahead of its prologue, is slower, not
+// faster -- Gate|Up with the norm 11.0 -> 15.7 us: a workgroup dispatched
+// late finds its activation loads queued behind the weight streams of the
+// workgroups dispatched before it.  So each kernel fetches what its prologue
+// needs first and the weights after the prologue's loads have landed.
+//
+// Per-block integer export: each kernel is compiled twice from the same
+// source, DOTS false for the product and DOTS true for the parity checks,
+// which also writes the isum of every (column, row, block) it computes to
+// dots[c][r - row_start][b] and stores no output row.  (A run-time switch
+// instead -- one uniform branch per block -- cost the product 0.2-0.5 us a
+// launch on the box.)
 #include "gx_device.hpp"
 #include "gx_internal.hpp"
 
@@ -30,18 +57,20 @@ namespace {
 // With UNITS, blockIdx.y is a unit of a mixture-of-experts batch: unit u
 // multiplies expert unit_expert[u] of a stack (matrices matrix_bytes apart)
 // by activation row u / act_div, into output row u.
-template <int NC, bool UNITS>
+template <int NC, bool UNITS, bool DOTS>
 __global__ __launch_bounds__(1024) void q4_0_matvec_kernel(
     const uint8_t *__restrict__ W, size_t plane0_bytes, int B, int DC, const int8_t *__restrict__ q,
     const float *__restrict__ scales, const int32_t *__restrict__ qsum, int K, int tile0, int row_start,
     int row_end, const float *__restrict__ bias, float *__restrict__ y, int ldy,
-    const int32_t *__restrict__ unit_expert, size_t matrix_bytes, int act_div, int experts) {
+    const int32_t *__restrict__ unit_expert, size_t matrix_bytes, int act_div, int experts,
+    int32_t *__restrict__ dots) {
     extern __shared__ float part[];  // [S][NC][64]
     const int S = (B + kStretch - 1) / kStretch;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nwaves = blockDim.x >> 6;
     const int tile = tile0 + blockIdx.x;
+    const int nrows = row_end - row_start;
     if (UNITS) {
         const int u = blockIdx.y;
         const int e = unit_expert[u];
@@ -57,6 +86,8 @@ __global__ __launch_bounds__(1024) void q4_0_matvec_kernel(
         scales += (size_t)a * B;
         qsum += (size_t)a * B;
         y += (size_t)u * ldy;
+        if (DOTS)
+            dots += (size_t)u * nrows * B;
     }
     const uint8_t *qs_row = W + ((size_t)tile * B * kTileRows + lane) * kChunk;
     const uint8_t *d_row = W + plane0_bytes + ((size_t)tile * DC * kTileRows + lane) * kChunk;
@@ -100,6 +131,11 @@ __global__ __launch_bounds__(1024) void q4_0_matvec_kernel(
                         const int32_t isum = q4_0_block_isum(wq[j], a0[jj], a1[jj], qs[jj]);
                         const float sc = chunk_half(dch, j) * sa[jj];
                         p[c] = fmaf((float)isum, sc, p[c]);
+                        if (DOTS) {
+                            const int row = tile * kTileRows + lane;
+                            if (row >= row_start && row < row_end)
+                                dots[((size_t)c * nrows + (row - row_start)) * B + b0 + j] = isum;
+                        }
                     }
                 }
             }
@@ -118,130 +154,119 @@ __global__ __launch_bounds__(1024) void q4_0_matvec_kernel(
                 acc = acc + part[(s * NC + c) * kTileRows + lane];
             if (bias)
                 acc = acc + bias[row];
-            y[(size_t)c * ldy + row] = acc;
+            if (!DOTS)
+                y[(size_t)c * ldy + row] = acc;
         }
     }
 }
 
-// One column (M = 1) of a matrix with few tiles, over more workgroups
-// without a cross-workgroup sum: a workgroup owns R rows (a quarter or half
-// of a tile) and all their stretches.  Lane l of a wavefront is row l % R of
-// the group and stretch slot l / R, so one wavefront covers 64 / R
-// stretches; its 16-byte loads are 64 / R runs of R*16 contiguous bytes of
-// the R64 layout.  The stretches of a wavefront differ, so the activation
-// comes from an LDS copy staged first (every load in flight together)
-// rather than from SGPRs.  The stretch sums meet in LDS and are added in
-// stretch order from 0: the one-tile kernel's sum, bit for bit.
-constexpr int kStageRegs = 4;  // staged 16-byte activation pieces per thread
+// ---- one column, activation in LDS ------------------------------------------
 
-template <int R>
-__global__ __launch_bounds__(1024) void q4_0_matvec_rg_kernel(
+constexpr int kActRegs = 4;  // staged 16-byte activation pieces per thread
+
+// LDS layout (bytes): part [S*R] floats, q [K] int8, scales [B], qsum [B].
+__host__ __device__ inline size_t lds_part_bytes(int S, int R) { return ((size_t)S * R * 4 + 15) & ~(size_t)15; }
+__host__ __device__ inline size_t lds_act_bytes(int K, int B) { return ((size_t)K + (size_t)B * 8 + 15) & ~(size_t)15; }
+
+// IT stretches a lane (IT = 2 when one pass of at most 16 wavefronts does
+// not cover the row).
+template <int R, int IT, bool DOTS>
+__global__ __launch_bounds__(1024) void q4_0_matvec_lds_kernel(
     const uint8_t *__restrict__ W, size_t plane0_bytes, int B, int DC, const int8_t *__restrict__ q,
     const float *__restrict__ scales, const int32_t *__restrict__ qsum, int group0, int row_start, int row_end,
-    const float *__restrict__ bias, float *__restrict__ y) {
-    constexpr int kSlots = kTileRows / R;
-    extern __shared__ __align__(16) float rg_lds[];  // part [S][R], then q [K], scales [B], sums [B]
-    const int S = (B + kStretch - 1) / kStretch;
+    const float *__restrict__ bias, float *__restrict__ y, int32_t *__restrict__ dots) {
+    constexpr int kSlots = kTileRows / R;  // stretch slots per wavefront
+    extern __shared__ __align__(16) uint8_t lds_raw[];
     const int K = B * kQ4Block;
-    float *part = rg_lds;
-    int8_t *qa = (int8_t *)(rg_lds + ((S * R + 3) & ~3));
+    const int S = (B + kStretch - 1) / kStretch;
+    float *part = (float *)lds_raw;
+    int8_t *qa = (int8_t *)(lds_raw + lds_part_bytes(S, R));
     float *sa = (float *)(qa + K);
     int32_t *qsa = (int32_t *)(sa + B);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int tid = threadIdx.x, nt = blockDim.x;
+    const int lane = tid & 63, wave = tid >> 6, nwaves = nt >> 6;
     const int g = group0 + blockIdx.x;
     const int tile = g / kSlots, r = (g - tile * kSlots) * R + lane % R;
-    const int s = wave * kSlots + lane / R;  // this lane's stretch
-    const int sc = min(s, S - 1);
-    // the activation: all loads in flight, then the weights, then the barrier
+    const int row = tile * kTileRows + r;
+    const bool in_range = row >= row_start && row < row_end;
+
+    // The activation: every load in flight together (indices past the end
+    // clamped, the values never stored), then into LDS.
     {
-        const int tid = threadIdx.x, nt = blockDim.x, n16 = K / 16;
-        int4 v[kStageRegs];
-        float sv[kStageRegs];
-        int32_t qv[kStageRegs];
+        const int n16 = K / 16;
+        int4 qv[kActRegs];
+        float sv[kActRegs];
+        int32_t qsv[kActRegs];
 #pragma unroll
-        for (int k = 0; k < kStageRegs; k++)
-            v[k] = ((const int4 *)q)[min(tid + k * nt, n16 - 1)];
+        for (int k = 0; k < kActRegs; k++)
+            qv[k] = ((const int4 *)q)[min(tid + k * nt, n16 - 1)];
 #pragma unroll
-        for (int k = 0; k < kStageRegs; k++) {
+        for (int k = 0; k < kActRegs; k++) {
             sv[k] = scales[min(tid + k * nt, B - 1)];
-            qv[k] = qsum[min(tid + k * nt, B - 1)];
+            qsv[k] = qsum[min(tid + k * nt, B - 1)];
         }
 #pragma unroll
-        for (int k = 0; k < kStageRegs; k++)
-            ((int4 *)qa)[min(tid + k * nt, n16 - 1)] = v[k];
-#pragma unroll
-        for (int k = 0; k < kStageRegs; k++) {
-            sa[min(tid + k * nt, B - 1)] = sv[k];
-            qsa[min(tid + k * nt, B - 1)] = qv[k];
+        for (int k = 0; k < kActRegs; k++) {
+            const int i = tid + k * nt;
+            if (i < n16)
+                ((int4 *)qa)[i] = qv[k];
+            if (i < B) {
+                sa[i] = sv[k];
+                qsa[i] = qsv[k];
+            }
         }
     }
+    // The weights: IT stretches, 8 nibble chunks and one scale chunk each
+    // (past the last block: the last one again).
     const uint8_t *qs_row = W + ((size_t)tile * B * kTileRows + r) * kChunk;
     const uint8_t *d_row = W + plane0_bytes + ((size_t)tile * DC * kTileRows + r) * kChunk;
-    const int b0 = sc * kStretch;
-    const int nb = s < S ? min(kStretch, B - b0) : 0;
-    uint4 wq[kStretch];
+    int st[IT];
+    uint4 wq[IT][kStretch], dch[IT];
 #pragma unroll
-    for (int j = 0; j < kStretch; j++)
-        wq[j] = load_stream(qs_row + (size_t)min(b0 + j, B - 1) * kTileRows * kChunk);
-    const uint4 dch = *(const uint4 *)(d_row + (size_t)sc * kTileRows * kChunk);
-    __syncthreads();
-    float p = 0.0f;
+    for (int it = 0; it < IT; it++) {
+        st[it] = it * nwaves * kSlots + wave * kSlots + lane / R;
+        const int sc = min(st[it], S - 1);
 #pragma unroll
-    for (int j = 0; j < kStretch; j++) {
-        if (j < nb) {
-            const int b = b0 + j;
-            const int4 *a = (const int4 *)(qa + (size_t)b * kQ4Block);
-            const int32_t isum = q4_0_block_isum(wq[j], a[0], a[1], qsa[b]);
-            const float scl = chunk_half(dch, j) * sa[b];
-            p = fmaf((float)isum, scl, p);
+        for (int j = 0; j < kStretch; j++)
+            wq[it][j] = load_stream(qs_row + (size_t)min(sc * kStretch + j, B - 1) * kTileRows * kChunk);
+        dch[it] = *(const uint4 *)(d_row + (size_t)sc * kTileRows * kChunk);
+    }
+    lds_barrier();
+
+    // Each lane's stretches, summed from +0 in block order.
+#pragma unroll
+    for (int it = 0; it < IT; it++) {
+        const int s = st[it];
+        if (s < S) {
+            const int b0 = s * kStretch;
+            const int nb = min(kStretch, B - b0);
+            float p = 0.0f;
+#pragma unroll
+            for (int j = 0; j < kStretch; j++) {
+                if (j < nb) {
+                    const int b = b0 + j;
+                    const int4 *ap = (const int4 *)(qa + (size_t)b * kQ4Block);
+                    const int32_t isum = q4_0_block_isum(wq[it][j], ap[0], ap[1], qsa[b]);
+                    const float scl = chunk_half(dch[it], j) * sa[b];
+                    p = fmaf((float)isum, scl, p);
+                    if (DOTS && in_range)
+                        dots[(size_t)(row - row_start) * B + b] = isum;
+                }
+            }
+            part[s * R + lane % R] = p;
         }
     }
-    if (s < S)
-        part[s * R + lane % R] = p;
-    __syncthreads();
-    const int row = tile * kTileRows + r;
-    if (wave == 0 && lane < R && row >= row_start && row < row_end) {
+    lds_barrier();
+
+    // The stretch sums in stretch order from 0: the one-tile kernel's sum,
+    // bit for bit.
+    if (!DOTS && wave == 0 && lane < R && in_range) {
         float acc = 0.0f;
-        for (int t = 0; t < S; t++)  // stretch order, from 0
+        for (int t = 0; t < S; t++)
             acc = acc + part[t * R + lane];
         y[row] = bias ? acc + bias[row] : acc;
     }
 }
-
-// The per-block integers of the kernel above, for the parity tests: one
-// thread per (m, row, block), through the same q4_0_block_isum.
-__global__ void q4_0_block_dots_kernel(const uint8_t *__restrict__ W, int B, const int8_t *__restrict__ q,
-                                       const int32_t *__restrict__ qsum, int K, int M, int row_start, int nrows,
-                                       int32_t *__restrict__ out) {
-    const size_t id = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (id >= (size_t)M * nrows * B)
-        return;
-    const int b = (int)(id % B);
-    const int r = (int)((id / B) % nrows);
-    const int m = (int)(id / ((size_t)B * nrows));
-    const int row = row_start + r;
-    const int tile = row >> 6, rr = row & 63;
-    const uint4 w = *(const uint4 *)(W + (((size_t)tile * B + b) * kTileRows + rr) * kChunk);
-    const int4 *a = (const int4 *)(q + (size_t)m * K + (size_t)b * kQ4Block);
-    out[id] = q4_0_block_isum(w, a[0], a[1], qsum[(size_t)m * B + b]);
-}
-
-template <int NC>
-int launch_nc(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, const int8_t *q, const float *scales,
-              const int32_t *qsum, int row_start, int row_end, const float *bias, float *y, int ldy) {
-    const int B = w->blocks;
-    const int S = (B + kStretch - 1) / kStretch;
-    const int waves = min(S, 16);
-    const size_t lds = (size_t)S * NC * kTileRows * sizeof(float);
-    GX_CHECK(lds <= 64 * 1024, "gx: a %d-input Q4_0 row is wider than this kernel's LDS", w->cols);
-    const int tile0 = row_start / kTileRows;
-    const int grid = (row_end + kTileRows - 1) / kTileRows - tile0;
-    q4_0_matvec_kernel<NC, false><<<grid, 64 * waves, lds, ctx->stream>>>(
-        mat, w->plane0_bytes, B, w->dchunks, q, scales, qsum, w->cols, tile0, row_start, row_end, bias, y, ldy,
-        nullptr, 0, 1, 0);
-    return check_launch("q4_0_matvec");
-}
-
 
 // One position (M = 1) whose activation is produced by the product itself:
 // x (+ add) -> RMSNormPlain(gain, eps) -> Q8_0, a block's pre-norm
@@ -263,12 +288,12 @@ constexpr int kFusedRegs = 8;  // staged values per thread: K <= 8 * threads
 // DB: two stretch slots a wavefront (double-buffered); without it a
 // wavefront has one slot and half the registers, so that two workgroups fit
 // a CU.
-template <int EPI, bool DB>
+template <int EPI, bool DB, bool DOTS>
 __global__ __launch_bounds__(1024) void q4_0_matvec_fused_kernel(
     const uint8_t *__restrict__ W, size_t plane0_bytes, int B, int DC, int K, int tile0, int row_start, int row_end,
     float *__restrict__ y, const float *__restrict__ x, const float *__restrict__ add,
     const float *__restrict__ gain, float eps, float *__restrict__ x_out, int8_t *__restrict__ q,
-    float *__restrict__ scales, int32_t *__restrict__ qsum) {
+    float *__restrict__ scales, int32_t *__restrict__ qsum, int32_t *__restrict__ dots) {
     extern __shared__ __align__(16) float lds[];  // part [S][64], then xs [K]
     __shared__ double red[512];
     __shared__ float scale_sh;
@@ -279,6 +304,8 @@ __global__ __launch_bounds__(1024) void q4_0_matvec_fused_kernel(
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int nwaves = blockDim.x >> 6;
     const int tile = tile0 + blockIdx.x;
+    const int row = tile * kTileRows + lane;
+    const bool in_range = row >= row_start && row < row_end;
     const uint8_t *qs_row = W + ((size_t)tile * B * kTileRows + lane) * kChunk;
     const uint8_t *d_row = W + plane0_bytes + ((size_t)tile * DC * kTileRows + lane) * kChunk;
 
@@ -394,6 +421,8 @@ __global__ __launch_bounds__(1024) void q4_0_matvec_fused_kernel(
                 const int32_t isum = q4_0_block_isum(wq[j], a0, a1, qs);                                             \
                 const float scl = chunk_half(dch, j) * sa;                                                           \
                 p = fmaf((float)isum, scl, p);                                                                       \
+                if (DOTS && in_range)                                                                                \
+                    dots[(size_t)(row - row_start) * B + b0 + j] = isum;                                             \
             }                                                                                                        \
         }                                                                                                            \
         part[(st) * kTileRows + lane] = p;                                                                           \
@@ -416,13 +445,12 @@ __global__ __launch_bounds__(1024) void q4_0_matvec_fused_kernel(
 #undef GX_FU_STRETCH
 #undef GX_FU_LOAD
     __syncthreads();
-    const int row = tile * kTileRows + lane;
     if (wave == 0) {
         float acc = 0.0f;
         for (int s = 0; s < S; s++)
             acc = acc + part[s * kTileRows + lane];
         if (EPI == 0) {
-            if (row >= row_start && row < row_end)
+            if (!DOTS && in_range)
                 y[row] = acc;
         } else {
             // lane l < 32: gate 32*tile + l; lane l + 32: its up
@@ -445,26 +473,83 @@ __global__ __launch_bounds__(1024) void q4_0_matvec_fused_kernel(
         }
     }
 }
+
+template <int NC>
+int launch_nc(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, const int8_t *q, const float *scales,
+              const int32_t *qsum, int row_start, int row_end, const float *bias, float *y, int ldy,
+              int32_t *dots) {
+    const int B = w->blocks;
+    const int S = (B + kStretch - 1) / kStretch;
+    const int waves = min(S, 16);
+    const size_t lds = (size_t)S * NC * kTileRows * sizeof(float);
+    GX_CHECK(lds <= 64 * 1024, "gx: a %d-input Q4_0 row is wider than this kernel's LDS", w->cols);
+    const int tile0 = row_start / kTileRows;
+    const int grid = (row_end + kTileRows - 1) / kTileRows - tile0;
+    if (dots)
+        q4_0_matvec_kernel<NC, false, true><<<grid, 64 * waves, lds, ctx->stream>>>(
+            mat, w->plane0_bytes, B, w->dchunks, q, scales, qsum, w->cols, tile0, row_start, row_end, bias, y, ldy,
+            nullptr, 0, 1, 0, dots);
+    else
+        q4_0_matvec_kernel<NC, false, false><<<grid, 64 * waves, lds, ctx->stream>>>(
+            mat, w->plane0_bytes, B, w->dchunks, q, scales, qsum, w->cols, tile0, row_start, row_end, bias, y, ldy,
+            nullptr, 0, 1, 0, nullptr);
+    return check_launch("q4_0_matvec");
+}
+
+// The one-column LDS kernel runs a quarter tile a workgroup, its
+// wavefronts covering the row's stretches in one pass (IT = 1) or two.
+constexpr int kLdsRows = 16;
+
+bool lds_fits(const gx_weight *w, int *it, int *waves, size_t *lds) {
+    const int B = w->blocks, K = w->cols, S = (B + kStretch - 1) / kStretch;
+    constexpr int slots = kTileRows / kLdsRows;
+    for (int IT = 1; IT <= 2; IT++) {
+        const int wv = (S + slots * IT - 1) / (slots * IT);
+        const int nt = 64 * wv;
+        const size_t bytes = lds_part_bytes(S, kLdsRows) + lds_act_bytes(K, B);
+        if (wv <= 16 && K / 16 <= kActRegs * nt && B <= kActRegs * nt && bytes <= 64 * 1024) {
+            *it = IT;
+            *waves = wv;
+            *lds = bytes;
+            return true;
+        }
+    }
+    return false;
+}
+
 }  // namespace
 
 int launch_q4_0_matvec(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, const int8_t *q, const float *scales,
                        const int32_t *qsum, int M, int row_start, int row_end, const float *bias, float *y,
-                       int ldy) {
+                       int ldy, int32_t *dots, int form) {
+    const int tile0 = row_start / kTileRows;
+    const int tiles = (row_end + kTileRows - 1) / kTileRows - tile0;
     // One column of a matrix with few tiles (at most a quarter as many as
-    // CUs): quarter tiles, so that four times as many workgroups pull
-    // weights (O 5.6 -> 4.2 us, Down 9.7 -> 6.5 us back to back).
-    {
-        const int B = w->blocks, S = (B + kStretch - 1) / kStretch;
-        const int tile0 = row_start / kTileRows;
-        const int tiles = (row_end + kTileRows - 1) / kTileRows - tile0;
-        constexpr int R = 16, kSlots = kTileRows / R;
-        const int waves = (S + kSlots - 1) / kSlots;
-        const size_t lds = (size_t)((S * R + 3) & ~3) * sizeof(float) + (size_t)w->cols + (size_t)B * 8;
-        if (M == 1 && tiles * 4 <= ctx->cu_count && waves <= 16 && lds <= 64 * 1024) {
-            q4_0_matvec_rg_kernel<R><<<(unsigned)(tiles * kSlots), 64 * waves, lds, ctx->stream>>>(
-                mat, w->plane0_bytes, B, w->dchunks, q, scales, qsum, tile0 * kSlots, row_start, row_end, bias, y);
-            return check_launch("q4_0_matvec_rg");
+    // CUs), or when asked (form 1): quarter tiles.  Measured in a graph of
+    // launches over rotating copies: O 2560 x 4096 5.7 -> 4.5 us, Down
+    // 2560 x 9728 9.8 -> 6.8 us; with 152 tiles (config 0) the whole-tile
+    // kernel stays ahead (5.4 against 6.1 us).
+    if (M == 1 && form != 0 && (form == 1 || tiles * 4 <= ctx->cu_count)) {
+        int IT, waves;
+        size_t lds;
+        if (lds_fits(w, &IT, &waves, &lds)) {
+            constexpr int slots = kTileRows / kLdsRows;
+            const unsigned grid = (unsigned)(tiles * slots), threads = (unsigned)(64 * waves);
+#define GX_LDS(II, DD)                                                                                               \
+    q4_0_matvec_lds_kernel<kLdsRows, II, DD><<<grid, threads, lds, ctx->stream>>>(                                   \
+        mat, w->plane0_bytes, w->blocks, w->dchunks, q, scales, qsum, tile0 * slots, row_start, row_end, bias, y, dots)
+            if (IT == 1 && !dots)
+                GX_LDS(1, false);
+            else if (IT == 1)
+                GX_LDS(1, true);
+            else if (!dots)
+                GX_LDS(2, false);
+            else
+                GX_LDS(2, true);
+#undef GX_LDS
+            return check_launch("q4_0_matvec_lds");
         }
+        GX_CHECK(form != 1, "gx: a %d-input Q4_0 row does not fit the one-column kernel", w->cols);
     }
     // Columns in groups of 8, 4, 2, 1, each group reading the weights once;
     // the per-column arithmetic is the same whatever the group.  Very wide
@@ -474,24 +559,26 @@ int launch_q4_0_matvec(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, cons
     const size_t per_column = (size_t)((B + kStretch - 1) / kStretch) * kTileRows * sizeof(float);
     const int widest = per_column * 8 <= 64 * 1024 ? 8 : per_column * 4 <= 64 * 1024 ? 4
                      : per_column * 2 <= 64 * 1024 ? 2 : 1;
+    const size_t nrows = (size_t)(row_end - row_start);
     while (c < M) {
         const int left = M - c;
         const int8_t *qc = q + (size_t)c * K;
         const float *sc = scales + (size_t)c * B;
         const int32_t *qs = qsum + (size_t)c * B;
-        float *yc = y + (size_t)c * ldy;
+        float *yc = y ? y + (size_t)c * ldy : nullptr;
+        int32_t *dc = dots ? dots + (size_t)c * nrows * B : nullptr;
         int rc;
         if (left >= 8 && widest >= 8) {
-            rc = launch_nc<8>(ctx, w, mat, qc, sc, qs, row_start, row_end, bias, yc, ldy);
+            rc = launch_nc<8>(ctx, w, mat, qc, sc, qs, row_start, row_end, bias, yc, ldy, dc);
             c += 8;
         } else if (left >= 4 && widest >= 4) {
-            rc = launch_nc<4>(ctx, w, mat, qc, sc, qs, row_start, row_end, bias, yc, ldy);
+            rc = launch_nc<4>(ctx, w, mat, qc, sc, qs, row_start, row_end, bias, yc, ldy, dc);
             c += 4;
         } else if (left >= 2 && widest >= 2) {
-            rc = launch_nc<2>(ctx, w, mat, qc, sc, qs, row_start, row_end, bias, yc, ldy);
+            rc = launch_nc<2>(ctx, w, mat, qc, sc, qs, row_start, row_end, bias, yc, ldy, dc);
             c += 2;
         } else {
-            rc = launch_nc<1>(ctx, w, mat, qc, sc, qs, row_start, row_end, bias, yc, ldy);
+            rc = launch_nc<1>(ctx, w, mat, qc, sc, qs, row_start, row_end, bias, yc, ldy, dc);
             c += 1;
         }
         if (rc)
@@ -501,22 +588,28 @@ int launch_q4_0_matvec(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, cons
 }
 
 int launch_q4_0_matvec_units(gx_ctx *ctx, const gx_weight *w, const int32_t *unit_expert, int units, int act_div,
-                              const int8_t *q, const float *scales, const int32_t *qsum, float *y, int ldy) {
+                              const int8_t *q, const float *scales, const int32_t *qsum, float *y, int ldy,
+                              int32_t *dots) {
     const int B = w->blocks;
     const int S = (B + kStretch - 1) / kStretch;
     const int waves = min(S, 16);
     const size_t lds = (size_t)S * kTileRows * sizeof(float);
     GX_CHECK(lds <= 64 * 1024, "gx: a %d-input Q4_0 row is wider than this kernel's LDS", w->cols);
     dim3 grid(w->tiles, units);
-    q4_0_matvec_kernel<1, true><<<grid, 64 * waves, lds, ctx->stream>>>(
-        w->dev, w->plane0_bytes, B, w->dchunks, q, scales, qsum, w->cols, 0, 0, w->rows, nullptr, y, ldy,
-        unit_expert, w->matrix_bytes, act_div, w->count);
+    if (dots)
+        q4_0_matvec_kernel<1, true, true><<<grid, 64 * waves, lds, ctx->stream>>>(
+            w->dev, w->plane0_bytes, B, w->dchunks, q, scales, qsum, w->cols, 0, 0, w->rows, nullptr, y, ldy,
+            unit_expert, w->matrix_bytes, act_div, w->count, dots);
+    else
+        q4_0_matvec_kernel<1, true, false><<<grid, 64 * waves, lds, ctx->stream>>>(
+            w->dev, w->plane0_bytes, B, w->dchunks, q, scales, qsum, w->cols, 0, 0, w->rows, nullptr, y, ldy,
+            unit_expert, w->matrix_bytes, act_div, w->count, nullptr);
     return check_launch("q4_0_matvec_units");
 }
 
 int launch_q4_0_matvec_fused(gx_ctx *ctx, const gx_weight *w, int epi, int row_start, int row_end, float *y,
                               const float *x, const float *add, const float *gain, float eps, float *x_out,
-                              int8_t *q, float *scales, int32_t *qsum) {
+                              int8_t *q, float *scales, int32_t *qsum, int32_t *dots) {
     const int B = w->blocks, K = w->cols;
     const int S = (B + kStretch - 1) / kStretch;
     const int waves = min(S, 16);
@@ -525,31 +618,29 @@ int launch_q4_0_matvec_fused(gx_ctx *ctx, const gx_weight *w, int epi, int row_s
     GX_CHECK(lds <= 56 * 1024, "gx: a %d-input Q4_0 row is wider than this kernel's LDS", K);
     const int tile0 = row_start / kTileRows;
     const int grid = (row_end + kTileRows - 1) / kTileRows - tile0;
-#define GX_FUSED(E, D)                                                                                               \
-    q4_0_matvec_fused_kernel<E, D><<<grid, 64 * waves, lds, ctx->stream>>>(                                          \
+#define GX_FUSED(E, D, DD)                                                                                           \
+    q4_0_matvec_fused_kernel<E, D, DD><<<grid, 64 * waves, lds, ctx->stream>>>(                                      \
         w->dev, w->plane0_bytes, B, w->dchunks, K, tile0, row_start, row_end, y, x, add, gain, eps, x_out, q, scales, \
-        qsum)
+        qsum, dots)
+#define GX_FUSED_D(E, D)                                                                                             \
+    do {                                                                                                             \
+        if (dots)                                                                                                    \
+            GX_FUSED(E, D, true);                                                                                    \
+        else                                                                                                         \
+            GX_FUSED(E, D, false);                                                                                   \
+    } while (0)
     const bool db = S > waves;
     if (epi == 0 && !db)
-        GX_FUSED(0, false);
+        GX_FUSED_D(0, false);
     else if (epi == 0)
-        GX_FUSED(0, true);
+        GX_FUSED_D(0, true);
     else if (!db)
-        GX_FUSED(1, false);
+        GX_FUSED_D(1, false);
     else
-        GX_FUSED(1, true);
+        GX_FUSED_D(1, true);
+#undef GX_FUSED_D
 #undef GX_FUSED
     return check_launch("q4_0_matvec_fused");
-}
-
-int launch_q4_0_block_dots_matvec(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const int32_t *qsum, int M,
-                                  int row_start, int row_end, int32_t *out) {
-    const int nrows = row_end - row_start;
-    const size_t total = (size_t)M * nrows * w->blocks;
-    const int threads = 256;
-    q4_0_block_dots_kernel<<<(unsigned)((total + threads - 1) / threads), threads, 0, ctx->stream>>>(
-        w->dev, w->blocks, q, qsum, w->cols, M, row_start, nrows, out);
-    return check_launch("q4_0_block_dots");
 }
 
 }  // namespace gx

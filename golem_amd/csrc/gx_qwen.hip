@@ -128,17 +128,18 @@ __global__ __launch_bounds__(64) void qwen_qk_rope_kernel(const float *__restric
     __shared__ float sc_sh;
     const int lane = threadIdx.x, t = blockIdx.x, u = blockIdx.y;
     const int pos = positions[t];
+    // A position past the cache, or a slot that names no conversation, has
+    // no place: nothing is stored, and the query is NaN, which the attention
+    // and everything after carry to the output.
+    const bool placed = pos >= 0 && pos < context && (!slots || (slots[t] >= 0 && slots[t] < nslots));
+    if (!placed) {
+        if (u < heads)
+            for (int i = lane; i < hd; i += 64)
+                qh[(size_t)t * heads * hd + u * hd + i] = 0x7E00;
+        return;
+    }
     if (slots) {  // the token's own conversation: its slot of the caches
-        const int slot = slots[t];
-        if (slot < 0 || slot >= nslots) {
-            // no such conversation: nothing is stored, and the query is NaN,
-            // which the attention and everything after carry to the output
-            if (u < heads)
-                for (int i = lane; i < hd; i += 64)
-                    qh[(size_t)t * heads * hd + u * hd + i] = 0x7E00;
-            return;
-        }
-        const size_t at = (size_t)slot * kv_heads * hd * context;
+        const size_t at = (size_t)slots[t] * kv_heads * hd * context;
         kcache += at;
         vcache += at;
     }
@@ -546,15 +547,21 @@ __global__ __launch_bounds__(kDecodeThreads) void attn_decode_kernel(
     const bool first = hl == 0;  // the head group that stores the position (FUSE)
     const int t = blockIdx.y;
     const int pos = positions[t];
-    const int n = min(pos + 1, limit);
+    const int n = min(max(pos, 0) + 1, limit);
+    // FUSE: a position outside the cache has no place in it: it stores
+    // nothing, its query is NaN, and the rotation tables are read at the
+    // cache's last position instead (in bounds).  One past max_pos but inside
+    // the cache is stored and attends positions 0 .. max_pos, as
+    // qwen_qk_rope_kernel and this kernel without FUSE do.
+    const int rpos = min(max(pos, 0), context - 1);
     const int groups = (n + 7) / 8, pieces = kValSlice * groups;
-    bool store = true;  // FUSE: the position belongs to a conversation and is stored
+    bool store = pos >= 0 && pos < context;  // FUSE: the position has a place and is stored
     if (slots) {  // the token's own conversation; reads stay inside the caches
         const size_t at = (size_t)min(max(slots[t], 0), nslots - 1) * kv_heads * HD * context;
         kcache += at;
         vcache += at;
         if (FUSE) {
-            store = slots[t] >= 0 && slots[t] < nslots;
+            store = store && slots[t] >= 0 && slots[t] < nslots;
             fz.kcache += at;
             fz.vcache += at;
         }
@@ -581,8 +588,8 @@ __global__ __launch_bounds__(kDecodeThreads) void attn_decode_kernel(
             const float *gain = w == 0 ? fz.q_norm : fz.k_norm;
             rg0[r] = gain[j];
             rg1[r] = gain[j + kHalf];
-            rc[r] = fz.rope_cos[(size_t)pos * kHalf + j];
-            rs[r] = fz.rope_sin[(size_t)pos * kHalf + j];
+            rc[r] = fz.rope_cos[(size_t)rpos * kHalf + j];
+            rs[r] = fz.rope_sin[(size_t)rpos * kHalf + j];
         }
     }
 
@@ -833,6 +840,367 @@ __global__ __launch_bounds__(kDecodeThreads) void attn_decode_kernel(
 }
 
 
+// ---- decode attention, sums in a parallel order -----------------------------
+//
+// The same attention as attn_decode_kernel (G = 1: a workgroup per (query
+// head, 32-wide value slice), positions of one token, prefixes of at most
+// kDecodeMax), with its two serial sums taken in parallel: SoftmaxInPlace's
+// total (nn/ops.go:59-73) as a tree of the threads' exponentials, and each
+// value element's Axpy over the positions (nn/kernel.go:221-233) as runs of
+// consecutive positions added afterwards in run order.  The scores, their
+// maximum, each exponential (float64 exp), the division and the fp16
+// rounding of each probability are golem's; only the order of the two sums
+// differs.  The value sums' reordering moves the outputs by about 1e-7; the
+// total's, when it moves the total by an ulp, moves any probability sitting
+// on an fp16 rounding boundary by one fp16 step (2^-11 of itself), which is
+// up to a few 1e-5 of a head's RMS.  Every thread takes a share of both sums, where
+// the serial kernel leaves them to one thread per head and 32 per slice.
+// Loads: the cached keys and values of the whole extent (max_pos + 1) are
+// requested first, before the token's position (itself a load) is known --
+// the key rows a lane per position, the value pieces of thread (run g,
+// element d) 8 positions to 16 bytes -- and positions past the prefix are
+// read but left out of every sum.  With FUSE, wavefront 0 only runs the
+// prologue (head norms, RoPE, the position's cache store), issuing the Q|K|V
+// row and norm gains first and the rotation tables once the position is
+// known, so that it waits for nothing but its own loads; the other seven
+// wavefronts do the cache work.  Barriers wait for LDS only, so the
+// prologue's cache stores and the value loads stay in flight across them.
+// With FUSE wavefront 0 does the prologue alone and the other seven the
+// cache work; without it all eight do.
+template <bool FUSE>
+struct ParShape {
+    static constexpr int kW0 = FUSE ? 1 : 0;                           // wavefronts out of the cache work
+    static constexpr int kCT = kDecodeThreads - 64 * kW0;              // cache threads
+    static constexpr int kRuns = kCT / kValSlice;                      // position runs of the value sums
+    static constexpr int kPieces = (kDecodeMax + 8 * kRuns - 1) / (8 * kRuns) + 1;  // value pieces a thread holds
+    static constexpr int kRows = (kDecodeMax + kCT - 1) / kCT;         // positions a thread scores
+};
+constexpr int kParProbs = kDecodeMax + 64;  // probabilities in LDS: up to the end of the last run
+
+template <int HD, bool FUSE>
+__global__ __launch_bounds__(kDecodeThreads) void attn_par_kernel(
+    const uint16_t *__restrict__ qh, int heads, int kv_heads, const int32_t *__restrict__ positions, int limit,
+    const uint16_t *kcache, const uint16_t *vcache, int context, float scale,
+    int8_t *__restrict__ q, float *__restrict__ scales, int32_t *__restrict__ qsum,
+    const int32_t *__restrict__ slots, int nslots, QkRope fz, float *__restrict__ heads_f) {
+    __shared__ __align__(16) uint32_t ql[HD / 2];                // the query, fp16 pairs
+    __shared__ __align__(16) uint16_t nk[HD];                   // FUSE: this position's key
+    __shared__ uint16_t nvl[kValSlice];                         // FUSE: this position's values of the slice
+    using Sh = ParShape<FUSE>;
+    static_assert(Sh::kRuns * (((kDecodeMax + Sh::kRuns - 1) / Sh::kRuns + 7) & ~7) <= kParProbs, "runs fit");
+    static_assert(Sh::kRows * Sh::kCT >= kParProbs - 8, "the probability rows are covered");
+    __shared__ __align__(16) uint16_t ps[kParProbs];            // probabilities, fp16
+    __shared__ float redm[kDecodeThreads / 64], reds[kDecodeThreads / 64];
+    __shared__ float vpart[Sh::kRuns][kValSlice + 1];
+    __shared__ __align__(16) float hh[2 * HD];                  // FUSE: the query and key heads, fp32
+    __shared__ __align__(16) double sq[2 * HD];                 // and their squares
+    __shared__ float hs[2];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    constexpr int slices = HD / kValSlice;
+    const int group = heads / kv_heads;
+    const int kvh = blockIdx.x % kv_heads, rb = blockIdx.x / kv_heads;
+    const int hl = rb / slices, d0 = (rb - hl * slices) * kValSlice;
+    const int h0 = kvh * group + hl;
+    const bool first = hl == 0;  // the query head whose workgroups store the position (FUSE)
+    const int t = blockIdx.y;
+    // The loads of the cached keys and values are issued for the whole
+    // extent max_pos + 1 (`limit`), before this token's position is known:
+    // the position is a load of its own (the captured decode step reads it
+    // from the device), and waiting for it would hold every load back by a
+    // memory round trip.  Positions past the token's prefix are read and
+    // left out of every sum.  Wavefront 0 (FUSE) first issues what its
+    // prologue needs -- the Q|K|V row and the norm gains, then, with the
+    // position, the rotation tables -- and its share of the cache loads
+    // after those, so that its prologue waits for its own loads only.
+    const int* pos_src = positions + t;
+    const int32_t* slot_src = slots ? slots + t : nullptr;
+    constexpr int kHalf = HD / 2;
+    // (no initial values: only wavefront 0 sets and reads them, and a value
+    // for the others would make wavefront 0 wait here for its loads)
+    float4 hx;
+    float nv, rg0[2], rg1[2], rc[2], rs[2];
+    if (FUSE && wave == 0) {
+        const float *row = fz.qkv + (size_t)t * fz.ldqkv;
+        const int e = min(4 * lane, 2 * HD - 4);  // query elements, then key elements
+        hx = *(const float4 *)(row + (e < HD ? h0 * HD + e : heads * HD + kvh * HD + (e - HD)));
+        nv = row[(heads + kv_heads) * HD + kvh * HD + d0 + (lane & (kValSlice - 1))];
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+            const int i = min(lane + 64 * r, HD - 1);
+            const int w = i / kHalf, j = i - w * kHalf;
+            const float *gain = w == 0 ? fz.q_norm : fz.k_norm;
+            rg0[r] = gain[j];
+            rg1[r] = gain[j + kHalf];
+        }
+    }
+    // without FUSE the query comes first: one dword a thread
+    const uint32_t qr = FUSE ? 0u : ((const uint32_t *)(qh + ((size_t)t * heads + h0) * HD))[min(tid, HD / 2 - 1)];
+    // a conversation's own caches: the slot decides the addresses
+    if (slots) {
+        const size_t at = (size_t)min(max(*slot_src, 0), nslots - 1) * kv_heads * HD * context;
+        kcache += at;
+        vcache += at;
+    }
+    v4u_stream k[Sh::kRows][HD / 8];
+    v4u_stream vr[Sh::kPieces];
+    const bool cw = !(FUSE && wave == 0);                 // a cache wavefront
+    const int ct = tid - 64 * Sh::kW0, cwave = wave - Sh::kW0;  // its thread and wavefront among them
+    const int gi = ct / kValSlice, dd = ct % kValSlice;
+    const int xchunk = ((limit + Sh::kRuns - 1) / Sh::kRuns + 7) & ~7;  // positions per value run
+    if (cw) {
+        // key rows: position ct + kCT r, a row only in wavefronts that reach it
+        const v4u_stream *kbase = (const v4u_stream *)(kcache + (size_t)kvh * HD * context);
+#pragma unroll
+        for (int r = 0; r < Sh::kRows; r++) {
+            if (r == 0 || r * Sh::kCT + cwave * 64 < limit) {
+                const int p = min(ct + r * Sh::kCT, limit - 1);
+#pragma unroll
+                for (int i = 0; i < HD / 8; i++)
+                    k[r][i] = kbase[(size_t)i * context + p];
+            }
+        }
+        // value pieces: run gi of xchunk positions (a multiple of 8), element dd
+        const uint16_t *vrow = vcache + ((size_t)kvh * HD + d0 + dd) * context;
+#pragma unroll
+        for (int u = 0; u < Sh::kPieces; u++) {
+            if (8 * u < xchunk) {
+                const int p0 = min(gi * xchunk + 8 * u, (limit - 1) & ~7);
+                vr[u] = *(const v4u_stream *)(vrow + p0);
+            }
+        }
+    }
+    const int pos = *pos_src;
+    const int n = min(max(pos, 0) + 1, limit);
+    const int rpos = min(max(pos, 0), context - 1);  // outside the cache: the tables' last row, nothing stored
+    bool store = pos >= 0 && pos < context;
+    if (FUSE && slots) {
+        const size_t at = (size_t)min(max(*slot_src, 0), nslots - 1) * kv_heads * HD * context;
+        store = store && *slot_src >= 0 && *slot_src < nslots;
+        fz.kcache += at;
+        fz.vcache += at;
+    }
+    if (FUSE && wave == 0) {
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+            const int i = min(lane + 64 * r, HD - 1);
+            const int j = i % kHalf;
+            rc[r] = fz.rope_cos[(size_t)rpos * kHalf + j];
+            rs[r] = fz.rope_sin[(size_t)rpos * kHalf + j];
+        }
+    }
+    if (FUSE) {
+        if (wave == 0) {
+            // the two heads' norms: the squares in parallel, each head's
+            // float64 sum in order in one lane (head_norm_scale's, bit for bit)
+            if (4 * lane < 2 * HD) {
+                *(float4 *)(hh + 4 * lane) = hx;
+                const float x4[4] = {hx.x, hx.y, hx.z, hx.w};
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    const float v = x4[c];
+                    const float sqf = v * v;
+                    sq[4 * lane + c] = (double)sqf;
+                }
+            }
+            if (lane < 2) {
+                const double *sh = sq + lane * HD;
+                double acc = 0.0;
+#pragma unroll 16
+                for (int i = 0; i < HD; i++)
+                    acc += sh[i];
+                const float mean = (float)(acc / (double)HD);
+                hs[lane] = (float)(1.0 / sqrt((double)(mean + fz.eps)));
+            }
+            uint16_t *qlh = (uint16_t *)ql;
+#pragma unroll
+            for (int r = 0; r < 2; r++) {
+                const int i = lane + 64 * r;
+                if (i >= HD)
+                    break;
+                const int w = i / kHalf, j = i - w * kHalf;
+                const float sc = hs[w];
+                const float re0 = hh[w * HD + j], im0 = hh[w * HD + j + kHalf];
+                const float re = (re0 * sc) * rg0[r], im = (im0 * sc) * rg1[r];
+                const float c = rc[r], sn = rs[r];
+                const float a = re * c - im * sn;
+                const float b = re * sn + im * c;
+                uint16_t ha = (uint16_t)float_to_half_bits(a), hb = (uint16_t)float_to_half_bits(b);
+                if (w == 0) {
+                    if (!store)  // no place in the cache: the query is NaN
+                        ha = hb = 0x7E00;
+                    qlh[j] = ha;
+                    qlh[j + kHalf] = hb;
+                } else {
+                    nk[j] = ha;
+                    nk[j + kHalf] = hb;
+                    if (store && first && d0 == 0) {
+                        uint16_t *kt = fz.kcache + (size_t)kvh * HD * context + (size_t)pos * 8;
+                        kcache_put(kt, context, j, ha);
+                        kcache_put(kt, context, j + kHalf, hb);
+                    }
+                }
+            }
+            if (lane < kValSlice) {
+                asm volatile("" : "+v"(nv));  // converted here, not hoisted up to its load
+                const uint16_t vb = (uint16_t)float_to_half_bits(nv);
+                nvl[lane] = vb;
+                if (store && first)
+                    fz.vcache[((size_t)kvh * HD + d0 + lane) * context + pos] = vb;
+            }
+        }
+    } else {
+        if (tid < HD / 2)
+            ql[tid] = qr;
+    }
+    lds_barrier();
+    if (FUSE && pos == n - 1 && cw) {  // this position's key from the copy, not the cache entry being written
+#pragma unroll
+        for (int r = 0; r < Sh::kRows; r++)
+            if (ct + r * Sh::kCT == pos) {
+#pragma unroll
+                for (int i = 0; i < HD / 8; i++)
+                    k[r][i] = ((const v4u_stream *)nk)[i];
+            }
+    }
+
+    // scores (DotF32's four chains, as the serial kernel) and their maximum
+    float s[Sh::kRows];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < Sh::kRows; r++) {
+        s[r] = -INFINITY;
+        if (!cw || r * Sh::kCT + cwave * 64 >= n)
+            continue;
+        const int p = ct + r * Sh::kCT;
+        const v4u_stream *qv = (const v4u_stream *)ql;
+        float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < HD / 8; i++) {
+            const v4u_stream qq = qv[i], kk = k[r][i];
+            s0 = fma_mix_lo(qq.x, kk.x, s0);
+            s1 = fma_mix_hi(qq.x, kk.x, s1);
+            s2 = fma_mix_lo(qq.y, kk.y, s2);
+            s3 = fma_mix_hi(qq.y, kk.y, s3);
+            s0 = fma_mix_lo(qq.z, kk.z, s0);
+            s1 = fma_mix_hi(qq.z, kk.z, s1);
+            s2 = fma_mix_lo(qq.w, kk.w, s2);
+            s3 = fma_mix_hi(qq.w, kk.w, s3);
+        }
+        const float v = scale * ((s0 + s1) + (s2 + s3));
+        if (p < n) {
+            s[r] = v;
+            mx = fmaxf(mx, v);
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1)
+        mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    if (lane == 0)
+        redm[wave] = mx;
+    lds_barrier();
+    float m = redm[0];
+#pragma unroll
+    for (int w = 1; w < kDecodeThreads / 64; w++)
+        m = fmaxf(m, redm[w]);
+    // exponentials (float64 exp, as SoftmaxInPlace), and their total as a tree
+    float e[Sh::kRows];
+    float tsum = 0.0f;
+#pragma unroll
+    for (int r = 0; r < Sh::kRows; r++) {
+        e[r] = cw && ct + r * Sh::kCT < n ? (float)exp((double)(s[r] - m)) : 0.0f;
+        tsum = tsum + e[r];
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1)
+        tsum = tsum + __shfl_xor(tsum, off, 64);
+    if (lane == 0)
+        reds[wave] = tsum;
+    lds_barrier();
+    float total = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kDecodeThreads / 64; w++)
+        total = total + reds[w];
+    // probabilities, rounded through fp16; zeros past the prefix to the end
+    // of the last run
+    if (cw) {
+#pragma unroll
+        for (int r = 0; r < Sh::kRows; r++) {
+            const int p = ct + r * Sh::kCT;
+            if (p < n)
+                ps[p] = (uint16_t)float_to_half_bits(__fdiv_rn(e[r], total));
+            else if (p < Sh::kRuns * xchunk)
+                ps[p] = 0;
+        }
+    }
+    lds_barrier();
+
+    // the value element's run of positions, then the runs in group order
+    float acc = 0.0f;
+#pragma unroll
+    for (int u = 0; u < Sh::kPieces; u++) {
+        const int p0 = gi * xchunk + 8 * u;
+        if (cw && 8 * u < xchunk && p0 < n) {
+            const v4u_stream pp = *(const v4u_stream *)(ps + p0);
+            v4u_stream vv = vr[u];
+            if (FUSE && pos >= p0 && pos < p0 + 8) {  // this position's value from the copy
+                const int e8 = pos - p0;
+                uint32_t wd[4] = {vv.x, vv.y, vv.z, vv.w};
+                const uint32_t nb = nvl[dd];
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    if (e8 == 2 * c)
+                        wd[c] = (wd[c] & 0xFFFF0000u) | nb;
+                    if (e8 == 2 * c + 1)
+                        wd[c] = (wd[c] & 0x0000FFFFu) | (nb << 16);
+                }
+                vv.x = wd[0];
+                vv.y = wd[1];
+                vv.z = wd[2];
+                vv.w = wd[3];
+            }
+            if (p0 + 8 <= n) {
+                acc = fma_mix_lo(pp.x, vv.x, acc);
+                acc = fma_mix_hi(pp.x, vv.x, acc);
+                acc = fma_mix_lo(pp.y, vv.y, acc);
+                acc = fma_mix_hi(pp.y, vv.y, acc);
+                acc = fma_mix_lo(pp.z, vv.z, acc);
+                acc = fma_mix_hi(pp.z, vv.z, acc);
+                acc = fma_mix_lo(pp.w, vv.w, acc);
+                acc = fma_mix_hi(pp.w, vv.w, acc);
+            } else {  // the prefix ends inside this piece: nothing past it is read
+                const uint32_t pw[4] = {pp.x, pp.y, pp.z, pp.w}, vw[4] = {vv.x, vv.y, vv.z, vv.w};
+#pragma unroll
+                for (int c = 0; c < 8; c++)
+                    if (p0 + c < n)
+                        acc = (c & 1) ? fma_mix_hi(pw[c >> 1], vw[c >> 1], acc) : fma_mix_lo(pw[c >> 1], vw[c >> 1], acc);
+            }
+        }
+    }
+    if (cw)
+        vpart[gi][dd] = acc;
+    lds_barrier();
+    if (tid < kValSlice) {
+        float o = 0.0f;
+#pragma unroll
+        for (int g = 0; g < Sh::kRuns; g++)
+            o = o + vpart[g][tid];
+        float stored;
+        int32_t sm;
+        const int32_t nq = q8_0_lane(o, &stored, &sm);
+        const int width = heads * HD, B = width >> 5;
+        const int col = h0 * HD + d0 + tid;
+        if (heads_f)  // the head outputs themselves, for parity checks
+            heads_f[(size_t)t * width + col] = o;
+        if (q) {
+            q[(size_t)t * width + col] = (int8_t)nq;
+            if (tid == 0) {
+                scales[(size_t)t * B + (col >> 5)] = stored;
+                qsum[(size_t)t * B + (col >> 5)] = sm;
+            }
+        }
+    }
+}
+
 // grid (ceil(ffn/256), M): gu [M][ldgu] holds each position's gate then up
 // (ffn each), or gates and ups interleaved by 32 (group 32).  mid =
 // silu(gate) * up (SwiGLURange, nn/swiglu.go:77-82), Q8_0.
@@ -865,10 +1233,14 @@ __global__ __launch_bounds__(256) void qwen_swiglu_quant_kernel(const float *__r
 
 // Greedy choice in two launches: kArgmaxParts workgroups per row each take
 // a contiguous part and leave the part's largest value and the lowest index
-// holding it (none if the part is all NaN: NaN never wins); one wavefront per
-// row then merges the parts.  "Larger value, else lower index" is a total
-// order, so the result is the index of the largest value, the lower index on
-// ties, whatever the split (0 when every value is NaN).
+// holding it (none if the part is all NaN); one wavefront per row then merges
+// the parts.  "Larger value, else lower index" is a total order, so the
+// result is the index of the largest non-NaN value, the lower index on ties,
+// whatever the split.  golem's Argmax (gemma/model.go:288-296,
+// qwen/model_test.go:118-126) starts from index 0 and moves only to a value
+// greater than the current best, so a NaN anywhere but at index 0 never wins,
+// and a NaN at index 0 wins outright (nothing compares greater): the merge
+// returns 0 when x[0] is NaN, and 0 when every value is NaN.
 constexpr int kArgmaxThreads = 256;
 constexpr int kNone = 0x7fffffff;
 
@@ -933,8 +1305,11 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_part_kernel(const float
 }
 
 // grid (M), one wavefront.  With `history` (M = 1, a captured decode step):
-// also history[*pos + 1] = id, *pos += 1, positions[0] = the new *pos.
-__global__ __launch_bounds__(64) void argmax_final_kernel(const float *__restrict__ part_v,
+// also, while *pos + 1 < history_len, history[*pos + 1] = id, *pos += 1 and
+// positions[0] = the new *pos; at the history's end the counter stops there,
+// so a step replayed past the end never addresses past it.
+__global__ __launch_bounds__(64) void argmax_final_kernel(const float *__restrict__ x, int ldx,
+                                                          const float *__restrict__ part_v,
                                                           const int32_t *__restrict__ part_i,
                                                           int32_t *__restrict__ out, int32_t *__restrict__ history,
                                                           int history_len, int32_t *__restrict__ pos,
@@ -952,14 +1327,16 @@ __global__ __launch_bounds__(64) void argmax_final_kernel(const float *__restric
         argmax_merge(bv, bi, ov, oi);
     }
     if (lane == 0) {
-        const int id = bi == kNone ? 0 : bi;
+        const float x0 = x[(size_t)blockIdx.x * ldx];
+        const int id = (bi == kNone || x0 != x0) ? 0 : bi;
         out[blockIdx.x] = id;
         if (history) {
             const int next = pos[0] + 1;
-            if (next < history_len)
+            if (next < history_len) {
                 history[next] = id;
-            pos[0] = next;
-            positions[0] = next;
+                pos[0] = next;
+                positions[0] = next;
+            }
         }
     }
 }
@@ -997,7 +1374,7 @@ size_t qwen_attention_workspace(int M, int heads, int max_pos) {
 int launch_qwen_attention(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int kv_heads, int hd, int max_pos,
                           const int32_t *positions, const uint16_t *kcache, const uint16_t *vcache, int context,
                           float scale, int8_t *q, float *scales, int32_t *qsum, uint8_t *workspace,
-                          const int32_t *slots, int nslots) {
+                          const int32_t *slots, int nslots, int parallel, float *heads_f) {
     const int G = heads / kv_heads;
     GX_CHECK(hd == 32 || hd == 64 || hd == 96 || hd == 128, "gx: attention supports head widths 32, 64, 96 and 128");
     GX_CHECK(G == 1 || G == 2 || G == 4 || G == 8, "gx: %d query heads per key-value head unsupported", G);
@@ -1011,6 +1388,22 @@ int launch_qwen_attention(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int
 
     // One workgroup per token: a few tokens of one conversation, or tokens of
     // several conversations (slots), whose caches share nothing.
+    if (parallel && (M <= 4 || slots) && limit <= kDecodeMax) {
+#define GX_PAR(HH)                                                                                                   \
+    attn_par_kernel<HH, false><<<dim3((unsigned)(heads * (HH / kValSlice)), (unsigned)M), kDecodeThreads, 0,       \
+                                 ctx->stream>>>(qh, heads, kv_heads, positions, limit, kcache, vcache, context,      \
+                                                scale, q, scales, qsum, slots, nslots, QkRope{}, heads_f)
+        if (hd == 32)
+            GX_PAR(32);
+        else if (hd == 64)
+            GX_PAR(64);
+        else if (hd == 96)
+            GX_PAR(96);
+        else
+            GX_PAR(128);
+#undef GX_PAR
+        return check_launch("qwen_attention parallel");
+    }
     if ((M <= 4 || slots) && limit <= kDecodeMax) {
 // One query head per workgroup when that fills at most two workgroups per CU
 // (128 workgroups for config 3's decode rather than 32): the scores,
@@ -1097,13 +1490,29 @@ int launch_qwen_rope_attention(gx_ctx *ctx, const float *qkv, int ldqkv, int hea
                                int max_pos, const int32_t *positions, const float *q_norm, const float *k_norm,
                                const float *rope_cos, const float *rope_sin, float eps, uint16_t *kcache,
                                uint16_t *vcache, int context, float scale, int8_t *q, float *scales, int32_t *qsum,
-                               const int32_t *slots, int nslots) {
+                               const int32_t *slots, int nslots, int parallel) {
     const int G = heads / kv_heads;
     GX_CHECK(hd == 32 || hd == 64 || hd == 96 || hd == 128, "gx: attention supports head widths 32, 64, 96 and 128");
     GX_CHECK(G == 1 || G == 2 || G == 4 || G == 8, "gx: %d query heads per key-value head unsupported", G);
     const int limit = max_pos + 1;
     GX_CHECK(limit <= kDecodeMax, "gx: the fused attention reads at most %d positions, not %d", kDecodeMax, limit);
     const QkRope fz{qkv, ldqkv, q_norm, k_norm, rope_cos, rope_sin, eps, kcache, vcache};
+    if (parallel) {
+#define GX_PAR(HH)                                                                                                   \
+    attn_par_kernel<HH, true><<<dim3((unsigned)(heads * (HH / kValSlice)), 1u), kDecodeThreads, 0, ctx->stream>>>(  \
+        nullptr, heads, kv_heads, positions, limit, kcache, vcache, context, scale, q, scales, qsum, slots, nslots, fz, \
+        nullptr)
+        if (hd == 32)
+            GX_PAR(32);
+        else if (hd == 64)
+            GX_PAR(64);
+        else if (hd == 96)
+            GX_PAR(96);
+        else
+            GX_PAR(128);
+#undef GX_PAR
+        return check_launch("qwen_rope_attention parallel");
+    }
 #define GX_FUSED(HH)                                                                                                 \
     attn_decode_kernel<HH, 1, true><<<dim3((unsigned)(heads * (HH / kValSlice)), 1u), kDecodeThreads, 0,             \
                                       ctx->stream>>>(nullptr, heads, kv_heads, positions, limit, kcache, vcache,     \
@@ -1133,8 +1542,8 @@ int launch_argmax(gx_ctx *ctx, const float *x, int ldx, int M, int n, int32_t *o
         const int rows = min(kArgmaxRows, M - m0);
         argmax_part_kernel<<<dim3(kArgmaxParts, (unsigned)rows), kArgmaxThreads, 0, ctx->stream>>>(
             x + (size_t)m0 * ldx, ldx, n, ctx->argmax_v, ctx->argmax_i);
-        argmax_final_kernel<<<rows, 64, 0, ctx->stream>>>(ctx->argmax_v, ctx->argmax_i, out + m0, history,
-                                                          history_len, pos, positions);
+        argmax_final_kernel<<<rows, 64, 0, ctx->stream>>>(x + (size_t)m0 * ldx, ldx, ctx->argmax_v, ctx->argmax_i,
+                                                          out + m0, history, history_len, pos, positions);
         if (int rc = check_launch("argmax"))
             return rc;
     }

@@ -85,8 +85,18 @@ class _Q8:
 
 
 class QwenModel:
-    def __init__(self, ctx, cfg, weights, max_batch):
+    """attention: "parallel" runs decode steps' attention with its softmax
+    total and value sums in a parallel order (gx_qwen_rope_attention_parallel
+    / gx_qwen_attention_parallel: golem's values within float rounding);
+    "golem" keeps golem's serial order bit for bit.  Prompts (more than four
+    positions) take the serial kernels either way."""
+
+    def __init__(self, ctx, cfg, weights, max_batch, attention="parallel"):
+        if attention not in ("parallel", "golem"):
+            raise ValueError(f"qwen: attention order {attention!r}")
         self.ctx, self.cfg, self.max_batch = ctx, cfg, max_batch
+        self.graph = None
+        self.set_attention(attention)
         vp, call = capi.vp, capi.call
         qd, kvd = cfg.heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim
         self.qd, self.kvd = qd, kvd
@@ -111,7 +121,9 @@ class QwenModel:
             raise ValueError("qwen: the tied head must be Q6_K or Q4_0")
         self.embd = capi.Weight(ctx, weights["token_embd"], self.head_quant, cfg.vocab, cfg.dim)
         self.output_norm = dev(weights["output_norm"])
-        cos, sin = rope_tables(cfg.head_dim, cfg.max_context, cfg.rope_base)
+        # a row for every position of the cache (a multiple of 8), as the
+        # kernels' contract has it
+        cos, sin = rope_tables(cfg.head_dim, (cfg.max_context + 7) // 8 * 8, cfg.rope_base)
         self.rope_cos, self.rope_sin = dev(cos), dev(sin)
         # one conversation until set_slots says otherwise
         self._make_caches(1)
@@ -157,6 +169,15 @@ class QwenModel:
         self.kc = self.vc = None
         self.kc = [torch.zeros(kshape, dtype=torch.int16, device="cuda") for _ in range(cfg.layers)]
         self.vc = [torch.zeros(vshape, dtype=torch.int16, device="cuda") for _ in range(cfg.layers)]
+
+    def set_attention(self, attention):
+        """Switch the decode steps' attention order ("parallel" or "golem");
+        a captured step is dropped."""
+        if attention not in ("parallel", "golem"):
+            raise ValueError(f"qwen: attention order {attention!r}")
+        sfx = "_parallel" if attention == "parallel" else ""
+        self._rope_attention, self._attention = "gx_qwen_rope_attention" + sfx, "gx_qwen_attention" + sfx
+        self.graph = None
 
     def set_slots(self, n):
         """SetSlots (qwen/slots.go:19-37): n independent conversations, each
@@ -223,9 +244,28 @@ class QwenModel:
         self._blocks(M, int(max(positions)))
         return self.hidden[:M]
 
-    def _blocks(self, M, max_pos):
+    def residual(self, tokens, start_pos, blocks):
+        """The residual stream of M >= 2 consecutive tokens after the first
+        `blocks` blocks (0: the embedding rows), as ForwardBatch computes it
+        before the final norm: a host [M][dim] float32 copy.  For checking a
+        deep model block by block."""
+        M = len(tokens)
+        if M < 2 or M > self.max_batch or start_pos + M > self.slot_context:
+            raise ValueError(f"qwen: {M} positions from {start_pos} for a block-by-block residual")
+        self.tokens[:M].copy_(torch.tensor(np.asarray(tokens, dtype=np.int32)))
+        torch.arange(start_pos, start_pos + M, dtype=torch.int32, out=self.positions[:M])
+        if self.nslots > 1:
+            self.slot_ids[:M].fill_(self.slot)
+        self._blocks(M, start_pos + M - 1, blocks)
+        self.ctx.sync()
+        if blocks == 0:
+            return self.xs[:M].cpu().numpy().copy()
+        return (self.xs[:M] + self.ffn[:M]).cpu().numpy()  # the last block's residual add
+
+    def _blocks(self, M, max_pos, blocks=None):
         """The embedding rows, every block and the final norm for the M tokens
-        and positions already in self.tokens / self.positions."""
+        and positions already in self.tokens / self.positions (with `blocks`:
+        only the first that many blocks, and no final norm)."""
         cfg, vp, call, ctx = self.cfg, self._vp, self._call, self.ctx.ptr
         call("gx_weight_rows", ctx, self.embd.ptr, 0, vp(self.tokens), M, vp(self.xs))
         if M == 1:
@@ -233,6 +273,8 @@ class QwenModel:
         qd, kvd = self.qd, self.kvd
         sl = vp(self.slot_ids) if self.nslots > 1 else None
         for i, b in enumerate(self.blocks):
+            if blocks is not None and i >= blocks:
+                return
             add = None if i == 0 else vp(self.ffn)
             call("gx_norm_quant", ctx, vp(self.xs), cfg.dim, add, cfg.dim, vp(b["attn_norm"]), M, cfg.dim,
                  np.float32(cfg.eps), None, 0, vp(self.x8.q), vp(self.x8.s), vp(self.x8.qs))
@@ -240,7 +282,7 @@ class QwenModel:
             call("gx_qwen_qk_rope", ctx, vp(self.qkv), qd + 2 * kvd, M, cfg.heads, cfg.kv_heads, cfg.head_dim,
                  vp(self.positions), vp(b["q_norm"]), vp(b["k_norm"]), vp(self.rope_cos), vp(self.rope_sin),
                  np.float32(cfg.eps), vp(self.qh), vp(self.kc[i]), vp(self.vc[i]), self.context, sl, self.nslots)
-            call("gx_qwen_attention", ctx, vp(self.qh), M, cfg.heads, cfg.kv_heads, cfg.head_dim,
+            call(self._attention, ctx, vp(self.qh), M, cfg.heads, cfg.kv_heads, cfg.head_dim,
                  max_pos, vp(self.positions), vp(self.kc[i]), vp(self.vc[i]), self.context,
                  vp(self.set8.q), vp(self.set8.s), vp(self.set8.qs), vp(self.attn_ws), self.attn_ws.numel(), sl,
                  self.nslots)
@@ -251,6 +293,8 @@ class QwenModel:
             call("gx_swiglu_quant", ctx, vp(self.gu), 2 * cfg.ffn, M, cfg.ffn, 32, vp(self.mid8.q),
                  vp(self.mid8.s), vp(self.mid8.qs))
             self._mm(b["down"], self.mid8, M, self.ffn, cfg.dim)
+        if blocks is not None:
+            return
         call("gx_norm_quant", ctx, vp(self.xs), cfg.dim, vp(self.ffn), cfg.dim, vp(self.output_norm), M, cfg.dim,
              np.float32(cfg.eps), vp(self.hidden), cfg.dim, None, None, None)
 
@@ -273,7 +317,7 @@ class QwenModel:
                      vp(other), 0, b["qkv"].rows, vp(self.qkv))
                 cur, other = other, cur
             if max_pos < FUSED_ATTENTION_MAX:  # head norms + RoPE + cache store + attention, one kernel
-                call("gx_qwen_rope_attention", ctx, vp(self.qkv), qd + 2 * kvd, cfg.heads, cfg.kv_heads,
+                call(self._rope_attention, ctx, vp(self.qkv), qd + 2 * kvd, cfg.heads, cfg.kv_heads,
                      cfg.head_dim, max_pos, vp(self.positions), vp(b["q_norm"]), vp(b["k_norm"]),
                      vp(self.rope_cos), vp(self.rope_sin), eps, vp(self.kc[i]), vp(self.vc[i]), self.context,
                      vp(self.set8.q), vp(self.set8.s), vp(self.set8.qs), sl, self.nslots)
@@ -282,7 +326,7 @@ class QwenModel:
                      cfg.head_dim, vp(self.positions), vp(b["q_norm"]), vp(b["k_norm"]), vp(self.rope_cos),
                      vp(self.rope_sin), eps, vp(self.qh), vp(self.kc[i]), vp(self.vc[i]), self.context, sl,
                      self.nslots)
-                call("gx_qwen_attention", ctx, vp(self.qh), 1, cfg.heads, cfg.kv_heads, cfg.head_dim,
+                call(self._attention, ctx, vp(self.qh), 1, cfg.heads, cfg.kv_heads, cfg.head_dim,
                      max_pos, vp(self.positions), vp(self.kc[i]), vp(self.vc[i]), self.context,
                      vp(self.set8.q), vp(self.set8.s), vp(self.set8.qs), vp(self.attn_ws), self.attn_ws.numel(),
                      sl, self.nslots)

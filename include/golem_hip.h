@@ -179,12 +179,31 @@ int gx_matmul_f32(gx_ctx *ctx, const gx_weight *w, const float *x, int ldx, int 
 /* ---- per-block integers (parity instrumentation) --------------------- */
 
 /* The signed per-block integer each product uses, sum_j (n_j - 8) * q_j, for
- * every (m, r, block): out[m][r - row_start][K/32] (device int32).  path 0 is
- * the matrix-vector kernel's arithmetic, path 1 the int8-MFMA product's,
- * path 2 the fp16-MFMA product's (needs q16).  golem's dotQ4_0Go accumulator
- * (nn/dot_q4_0.go:58-63) is this plus 8*qsum. */
-int gx_q4_0_block_dots(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const int32_t *qsum, const uint16_t *q16,
-                       int M, int row_start, int row_end, int path, int32_t *out);
+ * every (m, r, block): out[m][r - row_start][K/32] (device int32), exported
+ * by the very kernel that computes the product (its per-block integer
+ * output switched on; nothing else changes).  path 0: the matrix-vector
+ * kernel with the activation in scalar registers (M <= 8 as the product
+ * groups the columns, 8/4/2/1 a launch, and any larger M the same way);
+ * path 1: the int8-MFMA product (the direct-to-LDS kernel every M > 8
+ * product without q16 runs); path 2: the fp16-MFMA product (needs q16);
+ * path 3: the one-column matrix-vector kernel with the activation in LDS
+ * (M = 1, the whole/half/quarter-tile shape the product picks for this
+ * matrix).  golem's dotQ4_0Go accumulator (nn/dot_q4_0.go:58-63) is this plus
+ * 8*qsum.  No counterpart in golem: parity instrumentation. */
+int gx_q4_0_block_dots(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const float *scales, const int32_t *qsum,
+                       const uint16_t *q16, int M, int row_start, int row_end, int path, int32_t *out);
+
+/* The per-block integers of the fused one-position products
+ * (gx_norm_matmul_q4_0 when swiglu is 0, gx_norm_swiglu_q4_0 when it is 1),
+ * from the same kernel: x + add is normed (RMSNormPlain(gain, eps)) and
+ * quantised to Q8_0 inside it, and out[r - row_start][K/32] receives each
+ * block's sum_j (n_j - 8) * q_j against that Q8_0 form.  swiglu 1 needs
+ * every row and writes the SwiGLU Q8_0 into q/scales/qsum as
+ * gx_norm_swiglu_q4_0 does.  No counterpart in golem: parity
+ * instrumentation. */
+int gx_q4_0_fused_block_dots(gx_ctx *ctx, const gx_weight *w, int swiglu, const float *x, const float *add,
+                             const float *gain, float eps, int row_start, int row_end, int8_t *q, float *scales,
+                             int32_t *qsum, int32_t *out);
 
 /* dotQ6_KGo's per-superblock integer sum - 32*shift (nn/dot_q6_k.go:31-51)
  * for every (m, r, superblock): out[m][r - row_start][K/256]. */
@@ -272,7 +291,8 @@ int gx_norm_quant(gx_ctx *ctx, float *x, int ldx, const float *add, int lda, con
  * ([slot][kv_head]... of the layouts above) and position m belongs to
  * conversation slots[m] -- golem's Place{Cache: Slot(slots[m]), Pos}.  A slot
  * out of range stores nothing and leaves the position's query NaN.  NULL:
- * one conversation. */
+ * one conversation.  A position outside [0, context) is treated as such a
+ * slot: nothing stored, query NaN. */
 int gx_qwen_qk_rope(gx_ctx *ctx, const float *qkv, int ldqkv, int M, int heads, int kv_heads, int head_dim,
                     const int32_t *positions, const float *q_norm, const float *k_norm, const float *rope_cos,
                     const float *rope_sin, float eps, uint16_t *qh, uint16_t *kcache, uint16_t *vcache, int context,
@@ -304,12 +324,50 @@ int gx_qwen_attention(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int kv_
  * attention over positions 0 .. positions[0] (max_pos bounds it; at most 767),
  * quantised to Q8_0 into q/scales/qsum.  The caches and q/scales/qsum come
  * out bit for bit as the two calls leave them (the fp16 query is not written
- * anywhere).  slots / nslots as for gx_qwen_qk_rope, with one position. */
+ * anywhere).  slots / nslots as for gx_qwen_qk_rope, with one position.
+ * A position outside [0, context) stores nothing and its query is NaN (the
+ * rotation tables are then read at context - 1), so a replayed step whose
+ * counter has reached the end of the context stays inside the caches; one
+ * past max_pos but inside the cache is stored and attends positions
+ * 0 .. max_pos, as the two calls do. */
 int gx_qwen_rope_attention(gx_ctx *ctx, const float *qkv, int ldqkv, int heads, int kv_heads, int head_dim,
                            int max_pos, const int32_t *positions, const float *q_norm, const float *k_norm,
                            const float *rope_cos, const float *rope_sin, float eps, uint16_t *kcache,
                            uint16_t *vcache, int context, int8_t *q, float *scales, int32_t *qsum,
                            const int32_t *slots, int nslots);
+
+/* gx_qwen_attention and gx_qwen_rope_attention with their two serial sums
+ * taken in parallel, for decode steps (M <= 4 positions of one conversation,
+ * or one position per conversation with slots; prefixes of at most 768):
+ * SoftmaxInPlace's total (nn/ops.go:59-73) as a tree over the positions, and
+ * each head element's Axpy over the positions (nn/kernel.go:221-233) as 16
+ * runs of consecutive positions added in run order.  The scores, maximum,
+ * exponentials, division and fp16 probabilities are golem's; only the order
+ * of those two sums differs, so the head outputs are golem's within float
+ * rounding -- within 1e-4 of RMS against the oracle, since a probability
+ * that sits on an fp16 rounding boundary moves one fp16 step when the total
+ * does by an ulp -- and their Q8_0 form matches golem's except where a value
+ * sits on a rounding boundary.  Every
+ * thread of a workgroup takes a share of both sums, where golem's order
+ * leaves them to one lane per head and one per head element.  Same
+ * arguments, caches and outputs as the serial forms; the caches come out bit
+ * for bit the same.  Larger batches fall back to the serial kernels. */
+int gx_qwen_attention_parallel(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int kv_heads, int head_dim,
+                               int max_pos, const int32_t *positions, const uint16_t *kcache,
+                               const uint16_t *vcache, int context, int8_t *q, float *scales, int32_t *qsum,
+                               void *workspace, size_t workspace_bytes, const int32_t *slots, int nslots);
+int gx_qwen_rope_attention_parallel(gx_ctx *ctx, const float *qkv, int ldqkv, int heads, int kv_heads,
+                                    int head_dim, int max_pos, const int32_t *positions, const float *q_norm,
+                                    const float *k_norm, const float *rope_cos, const float *rope_sin, float eps,
+                                    uint16_t *kcache, uint16_t *vcache, int context, int8_t *q, float *scales,
+                                    int32_t *qsum, const int32_t *slots, int nslots);
+
+/* The head outputs of gx_qwen_attention_parallel before their Q8_0, out
+ * [M][heads*head_dim] (device floats), M <= 4.  No counterpart in golem:
+ * parity instrumentation for the parallel order. */
+int gx_qwen_attention_heads(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int kv_heads, int head_dim,
+                            int max_pos, const int32_t *positions, const uint16_t *kcache, const uint16_t *vcache,
+                            int context, float *out);
 
 /* One position's RMSNormPlain + Q8_0 fused into the Q4_0 product that reads
  * it (M = 1): y[row] for rows [row_start, row_end) of w times
@@ -340,15 +398,27 @@ int gx_swiglu_quant(gx_ctx *ctx, const float *gu, int ldgu, int M, int ffn, int 
                     int32_t *qsum);
 
 /* Greedy choice: ids[m] = the index of the largest of x[m][0..n), the lower
- * index on ties (qwen/model_test.go:118-126). */
+ * index on ties, by golem's rule (gemma/model.go:288-296,
+ * qwen/model_test.go:118-126: start at index 0, move only to a greater
+ * value): a NaN never wins except at index 0, where it wins outright, so the
+ * pick is 0 when x[m][0] is NaN.
+ * Workspace: the pick keeps its per-row partial results in scratch memory of
+ * the context (allocated by gx_init).  Every gx_argmax / gx_argmax_step of one
+ * context, including those recorded in a captured graph and replayed, must
+ * therefore be ordered on one stream; two of them in flight at once on
+ * different streams race on that scratch. */
 int gx_argmax(gx_ctx *ctx, const float *x, int ldx, int M, int n, int32_t *ids);
 
 /* One greedy step of a decode loop kept on the device (what golem's
  * generation loop does on the host after Logits, qwen/model.go): ids[0] =
- * gx_argmax of x[0..n); then history[*pos + 1] = ids[0] (when *pos + 1 <
- * history_len), *pos += 1 and positions[0] = the new *pos, so that a captured
- * decode step reads its next token and position from the device.  pos,
- * positions, history, ids: device int32. */
+ * gx_argmax of x[0..n); then, while *pos + 1 < history_len,
+ * history[*pos + 1] = ids[0], *pos += 1 and positions[0] = the new *pos, so
+ * that a captured decode step reads its next token and position from the
+ * device.  At the history's end the counter stops (only ids[0] is written):
+ * a step replayed past the end of the context never addresses past the
+ * history, and gx_qwen_rope_attention stores nothing for a position outside
+ * its cache.  pos, positions, history, ids: device int32.  The same workspace
+ * rule as gx_argmax. */
 int gx_argmax_step(gx_ctx *ctx, const float *x, int n, int32_t *ids, int32_t *history, int history_len,
                    int32_t *pos, int32_t *positions);
 

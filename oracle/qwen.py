@@ -29,12 +29,18 @@ from . import (Batch, Q4_0, Q6_K, _p, dequantize_q4_0_row, dequantize_q6_k, load
 
 
 class QwenOracle:
-    def __init__(self, cfg, weights):
+    """repacked=False multiplies the dense matrices in golem's row layout
+    (Matrix.rows without Repack: matVecQ4_0Rows, dotQ4_0Go) instead of the
+    8-row packed form golem's loader builds -- golem's other generic form of
+    the same product, equal to it up to float rounding."""
+
+    def __init__(self, cfg, weights, repacked=True):
         self.cfg, self.w = cfg, weights
         qd, kvd = cfg.heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim
         self.shapes = {"q": (qd, cfg.dim), "k": (kvd, cfg.dim), "v": (kvd, cfg.dim), "o": (cfg.dim, qd),
                        "gate": (cfg.ffn, cfg.dim), "up": (cfg.ffn, cfg.dim), "down": (cfg.dim, cfg.ffn)}
-        self.packed = [{n: pack_q4_0(b[n], *self.shapes[n]) for n in self.shapes} for b in weights["blocks"]]
+        self.packed = [{n: pack_q4_0(b[n], *self.shapes[n]) if repacked else None for n in self.shapes}
+                       for b in weights["blocks"]]
         self.K = [np.zeros((cfg.max_context, cfg.kv_heads, cfg.head_dim), np.float32) for _ in range(cfg.layers)]
         self.V = [np.zeros_like(k) for k in self.K]
         # the tied embedding / head: Q6_K (config 3) or Q4_0 (a pure Q4_0 file)
@@ -73,26 +79,42 @@ class QwenOracle:
             self.block(layer, xs, pos)
         return np.stack([rms_norm_plain(x, self.w["output_norm"], cfg.eps) for x in xs])
 
+    def norm(self, layer, xs, which):
+        """A block's pre-norm (qwen/block.go:45-52, 59-68): RMSNormPlain of
+        every position with the block's attn_norm or ffn_norm gain, and the
+        Q8_0 form of the result."""
+        gain = self.w["blocks"][layer][which]
+        return Batch(np.stack([rms_norm_plain(x, gain, self.cfg.eps) for x in xs])).quantize()
+
+    def swiglu(self, gate, up):
+        """SwiGLURange (nn/swiglu.go:77-82) of every position: silu(gate) * up."""
+        lib, mid = load(), np.array(gate, dtype=np.float32)
+        for t in range(len(mid)):
+            g, u = np.ascontiguousarray(mid[t]), np.ascontiguousarray(up[t], dtype=np.float32)
+            lib.orc_swiglu_range(_p(g), _p(u), 0, self.cfg.ffn)
+            mid[t] = g
+        return mid
+
     def block(self, layer, xs, pos):
-        cfg, bw = self.cfg, self.w["blocks"][layer]
-        normed = Batch(np.stack([rms_norm_plain(x, bw["attn_norm"], cfg.eps) for x in xs])).quantize()
+        normed = self.norm(layer, xs, "attn_norm")
         attn = self.attention(layer, normed, pos)
         xs += attn
-        normed = Batch(np.stack([rms_norm_plain(x, bw["ffn_norm"], cfg.eps) for x in xs])).quantize()
-        gate = self._mat(layer, "gate", normed)
-        up = self._mat(layer, "up", normed)
-        lib = load()
-        for t in range(len(xs)):
-            g, u = np.ascontiguousarray(gate[t]), np.ascontiguousarray(up[t])
-            lib.orc_swiglu_range(_p(g), _p(u), 0, cfg.ffn)
-            gate[t] = g
-        ffn = self._mat(layer, "down", Batch(gate).quantize())
+        normed = self.norm(layer, xs, "ffn_norm")
+        mid = self.swiglu(self._mat(layer, "gate", normed), self._mat(layer, "up", normed))
+        ffn = self._mat(layer, "down", Batch(mid).quantize())
         xs += ffn
 
     def attention(self, layer, normed, pos):
-        cfg, bw, lib = self.cfg, self.w["blocks"][layer], load()
-        hd, batch = cfg.head_dim, normed.size
         q, k, v = (self._mat(layer, n, normed) for n in ("q", "k", "v"))
+        return self._mat(layer, "o", Batch(self.attend(layer, q, k, v, pos)).quantize())
+
+    def attend(self, layer, q, k, v, pos):
+        """Attention's head-by-head part and the attention proper
+        (qwen/attention.go:57-124) from the Q, K and V projections of the
+        batch: per-head norms, RoPE, fp16 query and cache entries, then every
+        head's output (the floats the O projection's Q8_0 is made from)."""
+        cfg, bw, lib = self.cfg, self.w["blocks"][layer], load()
+        hd, batch = cfg.head_dim, len(q)
         qh = np.zeros_like(q)
         cos = np.zeros(hd // 2, np.float32)
         sin = np.zeros(hd // 2, np.float32)
@@ -119,7 +141,7 @@ class QwenOracle:
                 lib.orc_attend(_p(query), _p(Kl), _p(Vl), cfg.kv_heads, hd, h // per_kv, pos[t] + 1, scale,
                                _p(scores), _p(dst))
                 out[t, h * hd:(h + 1) * hd] = dst
-        return self._mat(layer, "o", Batch(out).quantize())
+        return out
 
     def logits(self, hidden):
         """Logits for one hidden state: the tied head, Q6_K over the Q8_K form

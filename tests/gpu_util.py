@@ -98,8 +98,8 @@ class Device:
     def q4_0_block_dots(self, w, act, M, start, end, path):
         q, sc, qs, q16 = act[:4]
         out = self.empty((M, end - start, w.cols // 32), np.int32)
-        capi.call("gx_q4_0_block_dots", self.ctx.ptr, w.ptr, capi.vp(q), capi.vp(qs), capi.vp(q16), M, start, end,
-                  path, capi.vp(out))
+        capi.call("gx_q4_0_block_dots", self.ctx.ptr, w.ptr, capi.vp(q), capi.vp(sc), capi.vp(qs), capi.vp(q16), M,
+                  start, end, path, capi.vp(out))
         return self.get(out)
 
     def q6_k_block_dots(self, w, act, M, start, end):

@@ -52,9 +52,14 @@ def test_device_matches_golden(dev, gold):
     q, sc, qs, _, co = (None if a is None else dev.get(a) for a in act)
     assert same_bits(q, gold["c0_q"]) and same_bits(sc, gold["c0_scales"]) and same_bits(co, gold["c0_corr"])
     w0 = dev.weight(gold["c0_w"], capi.Q4_0, ROWS, 2560)
-    isum = dev.q4_0_block_dots(w0, act, 1, 0, ROWS, 0)  # sum (n - 8) q, the device's integer
     qsum = gold["c0_q"].reshape(1, 1, 80, 32).astype(np.int64).sum(axis=3)
-    np.testing.assert_array_equal(isum.astype(np.int64) + 8 * qsum, gold["c0_acc"].astype(np.int64))
+    # sum (n - 8) q as the shipped kernels compute it: path 3 is the
+    # one-column kernel this M = 1 product runs, path 0 the SGPR kernel of
+    # small batches, path 1 the int8-MFMA product
+    for path in (3, 0, 1):
+        isum = dev.q4_0_block_dots(w0, act, 1, 0, ROWS, path)
+        np.testing.assert_array_equal(isum.astype(np.int64) + 8 * qsum, gold["c0_acc"].astype(np.int64),
+                                      err_msg=f"path {path}")
     y0 = dev.get(dev.matmul_q4_0(w0, act, 1))
     rel, at = oracle.compare_floats(y0[0], gold["c0_y"][0])
     assert rel <= 1e-5, f"Q4_0 rows: {rel:.3g} of RMS at {at}"

@@ -209,6 +209,37 @@ def test_config4_decode_and_prefill(dev, orc):
     log("config 4: decode and grouped prefill agree")
 
 
+def test_config4_prefill_256(dev, orc):
+    """Config 4's prefill at its configured size: 256 positions, 2048
+    (position, slot) units grouped by expert.  Expert ids bit for bit against
+    the oracle for every position (with the 8th/9th logit margin logged);
+    outputs of sampled positions within 2e-5 of RMS of golem through the
+    oracle; and sampled positions bit-identical to the same position run
+    alone (moe_test.go:164-205)."""
+    D, F, E, k = 2816, 704, 128, 8
+    moe = Moe(dev, D, F, E, k, 4)
+    M = 256
+    x = synth.activations(moe.g, M, D)
+    logits, ids, w = moe.route(x)
+    idh, wh = dev.get(ids), dev.get(w)
+    margins = []
+    for t in range(M):
+        ol, oi, ow = orc.route_one(x[t], moe.router, k)
+        np.testing.assert_array_equal(idh[t], oi, err_msg=f"position {t}")
+        srt = np.sort(ol)[::-1]
+        margins.append(float(srt[k - 1] - srt[k]))
+    log(f"config 4 prefill: ids identical at 256 positions; smallest 8th/9th margin {min(margins):.3g}")
+    batch = dev.get(moe.experts(x, ids, w))
+    sample = [0, 1, 100, 200, 255]
+    want = moe.oracle(orc, x[sample], idh[sample], wh[sample])
+    for i, t in enumerate(sample):
+        rel, at = orc.compare_floats(batch[t], want[i])
+        assert rel <= TOL, f"position {t}: {rel:.3g} of RMS at {at}"
+    for t in (0, 128, 255):
+        one = dev.get(moe.experts(x[t:t + 1], ids[t:t + 1], w[t:t + 1]))
+        np.testing.assert_array_equal(one[0].view(np.uint32), batch[t].view(np.uint32))
+
+
 def test_bad_expert_id_poisons_its_position(dev):
     D, F, E, k = 256, 64, 4, 2
     moe = Moe(dev, D, F, E, k, 60)

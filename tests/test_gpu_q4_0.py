@@ -1,8 +1,11 @@
 """The Q4_0 products against the oracle.
 
 Integers: every per-block sum the GPU uses equals golem's dotQ4_0Go
-accumulator minus 8*sum(q) (nn/dot_q4_0.go:58-63), for both the
-matrix-vector kernel and the MFMA product, bit for bit.
+accumulator minus 8*sum(q) (nn/dot_q4_0.go:58-63), bit for bit, exported by
+the kernels that ship (gx_q4_0_block_dots: the SGPR-activation matrix-vector
+kernel, the direct-to-LDS int8-MFMA product, the fp16-MFMA product and the
+one-column LDS kernel in each of its tile shapes; gx_q4_0_fused_block_dots:
+the fused norm products of the decode step).
 Floats: golem's compareFloats bar (nn/quants_reference_test.go:96-120),
 max |got - want| / RMS(want) <= 1e-5, against both of golem's generic forms
 (row layout dotQ4_0Go and the 8-row packed dotPackedQ4_0Go) through
@@ -52,9 +55,12 @@ def test_dequantized_rows_cover_every_half(dev, orc):
     np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
-@pytest.mark.parametrize("rows,cols,M", [(64, 256, 1), (200, 2560, 3), (96, 704, 9), (130, 2816, 40)])
-@pytest.mark.parametrize("path", [0, 1, 2])
+@pytest.mark.parametrize("rows,cols,M", [(64, 256, 1), (200, 2560, 3), (96, 704, 9), (130, 2816, 40),
+                                         (300, 2560, 1)])
+@pytest.mark.parametrize("path", [0, 1, 2, 3])
 def test_block_integers_bit_exact(dev, orc, rows, cols, M, path):
+    if path == 3 and M != 1:
+        pytest.skip("the one-column kernel takes M = 1")
     log(f"q4_0 block dots rows={rows} cols={cols} M={M} path={path}")
     w, b, wd, act = setup(dev, orc, rows, cols, M, 100 + rows)
     start, end = (0, rows) if rows < 100 else (5, rows - 3)
@@ -62,6 +68,81 @@ def test_block_integers_bit_exact(dev, orc, rows, cols, M, path):
     acc = orc.q4_0_block_acc(w, b, rows)[:, start:end, :]
     qsum = b.qsum_rows()[:, None, :]
     np.testing.assert_array_equal(got, acc - 8 * qsum)
+
+
+@pytest.mark.parametrize("rows,cols,span", [
+    (2560, 9728, (0, 2560)),      # Down: 10 wavefronts a workgroup
+    (2560, 4096, (17, 2500)),     # O, a range that cuts quarter tiles
+    (9728, 2560, (0, 9728)),      # config 0's matrix (the product runs whole tiles there)
+    (16448, 2560, (3, 16441)),    # 257 tiles
+    (100, 16640, (0, 100)),       # 65 stretches: two stretches a lane
+])
+def test_one_column_integers_every_shape(dev, orc, rows, cols, span):
+    """Path 3 -- the quarter-tile one-column kernel the decode's O and Down
+    products run -- bit for bit against golem's accumulator, and its outputs
+    equal the SGPR kernel's (path 0's) bit for bit."""
+    log(f"one-column dots rows={rows} cols={cols} span={span}")
+    w, b, wd, act = setup(dev, orc, rows, cols, 1, 700 + rows)
+    start, end = span
+    got = dev.q4_0_block_dots(wd, act, 1, start, end, 3)
+    acc = orc.q4_0_block_acc(w, b, rows)[:, start:end, :]
+    np.testing.assert_array_equal(got, acc - 8 * b.qsum_rows()[:, None, :])
+    y = dev.get(dev.matmul_q4_0(wd, act, 1, start, end))[0]
+    q, sc, qs = act[:3]
+    y2 = dev.full((2, rows), float("nan"))
+    # two columns, the second a copy of the first: the SGPR kernel computes both
+    q2, sc2, qs2 = (torch_cat2(dev, t) for t in (q, sc, qs))
+    capi.call("gx_matmul_q4_0", dev.ctx.ptr, wd.ptr, capi.vp(q2), capi.vp(sc2), capi.vp(qs2), None, 2, start, end,
+              None, capi.vp(y2), rows)
+    y2 = dev.get(y2)
+    np.testing.assert_array_equal(y[start:end].view(np.uint32), y2[0, start:end].view(np.uint32))
+    np.testing.assert_array_equal(y[start:end].view(np.uint32), y2[1, start:end].view(np.uint32))
+
+
+def torch_cat2(dev, t):
+    """Two rows of the same activation (a [1][n] device tensor)."""
+    return dev.torch.cat([t, t], 0).contiguous()
+
+
+def _fused_case(orc, g, rows, cols, with_add):
+    w = synth.q4_0_weights(g, rows, cols)
+    x = g.standard_normal(cols).astype(np.float32)
+    add = g.standard_normal(cols).astype(np.float32) if with_add else None
+    gain = (1.0 + 0.02 * g.standard_normal(cols)).astype(np.float32)
+    xa = x + add if with_add else x.copy()
+    normed = orc.rms_norm_plain(xa, gain, 1e-6)
+    b = orc.Batch(normed[None, :]).quantize()
+    return w, x, add, gain, b
+
+
+@pytest.mark.parametrize("rows,cols,swiglu,span", [
+    (6144, 2560, 0, (0, 6144)),    # config 3's Q|K|V
+    (19456, 2560, 1, (0, 19456)),  # config 3's Gate|Up with the SwiGLU epilogue
+    (1536, 512, 0, (5, 1500)),     # a small model's Q|K|V, a cut range
+    (128, 8192, 1, (0, 128)),      # a long row: two stretch slots a wavefront
+])
+def test_fused_norm_integers(dev, orc, rows, cols, swiglu, span):
+    """The fused one-position products (pre-norm + Q8_0 inside the kernel)
+    export the integers of the Q8_0 form they made: golem's accumulator over
+    Q8_0(RMSNormPlain(x + add, gain)) minus 8*sum(q), bit for bit."""
+    g = synth.rng(800 + rows + swiglu)
+    for with_add in (True, False):
+        log(f"fused dots rows={rows} cols={cols} swiglu={swiglu} add={with_add}")
+        w, x, add, gain, b = _fused_case(orc, g, rows, cols, with_add)
+        wd = dev.weight(w, capi.Q4_0, rows, cols)
+        xd, gd = dev.put(x), dev.put(gain)
+        ad = dev.put(add) if with_add else None
+        start, end = span
+        out = dev.empty((end - start, cols // 32), np.int32)
+        q8 = dev.empty((rows // 2,), np.int8) if swiglu else None
+        s8 = dev.empty((rows // 64,), np.float32) if swiglu else None
+        qs8 = dev.empty((rows // 64,), np.int32) if swiglu else None
+        capi.call("gx_q4_0_fused_block_dots", dev.ctx.ptr, wd.ptr, swiglu, capi.vp(xd), capi.vp(ad), capi.vp(gd),
+                  np.float32(1e-6), start, end, capi.vp(q8), capi.vp(s8), capi.vp(qs8), capi.vp(out))
+        got = dev.get(out)
+        acc = orc.q4_0_block_acc(w, b, rows)[0, start:end, :]
+        np.testing.assert_array_equal(got, acc - 8 * b.qsum_rows()[0][None, :])
+        wd.free()
 
 
 def test_block_acc_oracle_agrees_with_c_loop(orc):
@@ -156,7 +237,7 @@ def test_batch_equals_one_at_a_time(dev, orc, rows, cols, f16):
 
 
 @pytest.mark.parametrize("f16", [True, False])
-@pytest.mark.parametrize("M", [64, 512])
+@pytest.mark.parametrize("M", [64, 512, 2048])
 def test_gemm_against_golem(dev, orc, M, f16):
     rows, cols = 9728, 2560
     log(f"q4_0 gemm M={M} f16={f16}")
@@ -172,6 +253,26 @@ def test_gemm_against_golem(dev, orc, M, f16):
     for i, c in enumerate(cols_sel):
         rel, at = orc.compare_floats(got[c, sel_rows], want[i])
         assert rel <= TOL, f"column {c}: {rel:.3g} at {at}"
+
+
+def test_gemm_integers_config_2(dev, orc):
+    """Config 2 at M = 2048: the int8-MFMA product's own per-block integers
+    (direct-to-LDS kernel, biased chain) for 64 rows of every token, bit for
+    bit against golem's accumulator; and its outputs for those rows against
+    one token at a time through the matrix-vector kernel, bit for bit."""
+    rows, cols, M = 9728, 2560, 2048
+    w, b, wd, act = setup(dev, orc, rows, cols, M, 2)
+    start, end = 4032, 4096
+    log("config 2 M=2048 block dots, int8 MFMA")
+    got = dev.q4_0_block_dots(wd, act, M, start, end, 1)
+    wsub = w.reshape(rows, -1)[start:end].reshape(-1)
+    acc = orc.q4_0_block_acc(wsub, b, end - start)
+    np.testing.assert_array_equal(got, acc - 8 * b.qsum_rows()[:, None, :])
+    y = dev.get(dev.matmul_q4_0(wd, act, M, f16=False))
+    for c in (0, 1023, 2047):
+        one = dev.quantize_q8_0(b.F[c:c + 1], with_corr=False)
+        alone = dev.get(dev.matmul_q4_0(wd, one, 1))
+        np.testing.assert_array_equal(alone[0].view(np.uint32), y[c].view(np.uint32))
 
 
 def test_errors_are_golem_panics(dev):

@@ -268,6 +268,78 @@ def test_attention_bit_exact(dev, orc, hd, heads, kv, ctx_len, batch):
     np.testing.assert_array_equal(dev.get(qs), b.qsum_rows())
 
 
+PARALLEL = [(128, 32, 8, 640), (128, 8, 2, 70), (64, 4, 2, 300), (32, 8, 1, 95), (96, 4, 4, 130),
+            (128, 4, 1, 768), (64, 2, 1, 513), (128, 4, 4, 1), (64, 4, 2, 9)]
+
+
+@pytest.mark.parametrize("batch", ["one", "three"])
+@pytest.mark.parametrize("hd,heads,kv,ctx_len", PARALLEL)
+def test_attention_parallel_against_golem(dev, orc, hd, heads, kv, ctx_len, batch):
+    """The parallel-order decode attention against golem's (orc_attend,
+    qwen/attention.go:96-124): every head's output floats within 1e-4 of RMS
+    (gx_qwen_attention_heads), and the Q8_0 of the heads
+    (gx_qwen_attention_parallel) equal to golem's but for values on a
+    rounding boundary, which move one step.  Prefixes of 1 to 768 positions,
+    including those that end inside a 16-byte piece and at a run's edge.
+    Why 1e-4 and not the products' 1e-5: golem rounds every probability to
+    fp16 (attention.go:112-114), so when the softmax total, summed in another
+    order, moves by an ulp, a probability sitting on an fp16 rounding
+    boundary moves by 2^-11 of itself -- up to ~3e-5 of RMS seen on a head
+    whose probabilities are concentrated.  The value sums' own reordering
+    stays near 1e-7."""
+    g = synth.rng(163 + ctx_len + hd)
+    if batch == "one":
+        pos = np.array([ctx_len - 1], np.int32)
+    else:
+        pos = np.array([0, ctx_len // 2, ctx_len - 1], np.int32)
+    M = len(pos)
+    context = (ctx_len + 7) // 8 * 8
+    kcf = g.standard_normal((ctx_len, kv, hd)).astype(np.float16)
+    vcf = (g.standard_normal((ctx_len, kv, hd)) * 2).astype(np.float16)
+    qf = (g.standard_normal((M, heads * hd)) * 1.5).astype(np.float16)
+    vt = np.zeros((kv, hd, context), np.float16)
+    vt[:, :, :ctx_len] = vcf.transpose(1, 2, 0)
+    kt = np.zeros((kv, hd // 8, context, 8), np.float16)
+    kt[:, :, :ctx_len, :] = kcf.reshape(ctx_len, kv, hd // 8, 8).transpose(1, 2, 0, 3)
+    ins = [dev.put(a) for a in (qf.view(np.int16), pos, kt.view(np.int16), vt.view(np.int16))]
+    heads_f = dev.empty((M, heads * hd), np.float32)
+    capi.call("gx_qwen_attention_heads", dev.ctx.ptr, capi.vp(ins[0]), M, heads, kv, hd, int(pos.max()),
+              capi.vp(ins[1]), capi.vp(ins[2]), capi.vp(ins[3]), context, capi.vp(heads_f))
+    q8 = dev.empty((M, heads * hd), np.int8)
+    sc = dev.empty((M, heads * hd // 32), np.float32)
+    qs = dev.empty((M, heads * hd // 32), np.int32)
+    n = capi.size_out("gx_qwen_attention_workspace_bytes", M, heads, int(pos.max()))
+    ws = dev.empty((n,), np.uint8)
+    capi.call("gx_qwen_attention_parallel", dev.ctx.ptr, capi.vp(ins[0]), M, heads, kv, hd, int(pos.max()),
+              capi.vp(ins[1]), capi.vp(ins[2]), capi.vp(ins[3]), context, capi.vp(q8), capi.vp(sc), capi.vp(qs),
+              capi.vp(ws), n, None, 0)
+    lib = orc.load()
+    K32, V32 = np.ascontiguousarray(kcf.astype(np.float32)), np.ascontiguousarray(vcf.astype(np.float32))
+    scale = np.float32(1 / math.sqrt(float(hd)))
+    out = np.zeros((M, heads * hd), np.float32)
+    scores = np.zeros(ctx_len, np.float32)
+    for t in range(M):
+        for h in range(heads):
+            query = np.ascontiguousarray(qf[t, h * hd:(h + 1) * hd].astype(np.float32))
+            dst = np.zeros(hd, np.float32)
+            lib.orc_attend(orc._p(query), orc._p(K32), orc._p(V32), kv, hd, h // (heads // kv), int(pos[t]) + 1,
+                           scale, orc._p(scores), orc._p(dst))
+            out[t, h * hd:(h + 1) * hd] = dst
+    got = dev.get(heads_f)
+    worst = 0.0
+    for t in range(M):
+        for h in range(heads):
+            rel, at = orc.compare_floats(got[t, h * hd:(h + 1) * hd], out[t, h * hd:(h + 1) * hd])
+            worst = max(worst, rel)
+            assert rel <= 1e-4, f"position {pos[t]} head {h}: {rel:.3g} of RMS at {at}"
+    b = orc.Batch(out).quantize()
+    dq = dev.get(q8).astype(np.int32) - b.q_rows().astype(np.int32)
+    moved = int(np.count_nonzero(dq))
+    log(f"  parallel attention hd={hd} heads={heads}/{kv} n={ctx_len} {batch}: worst {worst:.2g} of RMS, "
+        f"{moved} of {dq.size} Q8_0 values one step off")
+    assert np.abs(dq).max() <= 1 and moved <= max(2, dq.size // 100)
+
+
 def test_attention_refuses_bad_caches(dev):
     M, heads, kv, hd = 1, 4, 2, 64
     n = capi.size_out("gx_qwen_attention_workspace_bytes", M, heads, 15)
@@ -405,26 +477,51 @@ def test_swiglu_quant_bit_exact(dev, orc):
 
 
 def test_argmax_ties_to_lower_id(dev):
-    x = np.zeros((3, 151936), np.float32)
+    """golem's Argmax (gemma/model.go:288-296): ties to the lower id, a NaN
+    past index 0 never wins, a NaN at index 0 wins outright."""
+    x = np.zeros((4, 151936), np.float32)
     x[0, 77] = x[0, 150000] = 5.0
     x[1, :] = -1.0
     x[1, 151935] = 2.0
     x[2, 1000] = np.nan
     x[2, 9] = 3.0
-    ids = dev.empty((3,), np.int32)
+    x[3, 0] = np.nan
+    x[3, 5000] = 8.0
+    ids = dev.empty((4,), np.int32)
     xd = dev.put(x)
-    capi.call("gx_argmax", dev.ctx.ptr, capi.vp(xd), x.shape[1], 3, x.shape[1], capi.vp(ids))
-    assert dev.get(ids).tolist() == [77, 151935, 9]
+    capi.call("gx_argmax", dev.ctx.ptr, capi.vp(xd), x.shape[1], 4, x.shape[1], capi.vp(ids))
+    assert dev.get(ids).tolist() == [77, 151935, 9, 0]
+
+
+def _golem_argmax(row):
+    """golem's loop itself (qwen/model_test.go:118-126), for short rows."""
+    best = 0
+    for i in range(1, len(row)):
+        if row[i] > row[best]:
+            best = i
+    return best
 
 
 def _argmax_want(row):
-    """The greedy pick: the largest non-NaN value, the lower index on ties;
-    0 when every value is NaN."""
-    ok = ~np.isnan(row)
-    if not ok.any():
+    """golem's pick in closed form: 0 when x[0] is NaN (nothing compares
+    greater), else the lower index of the largest non-NaN value."""
+    if np.isnan(row[0]):
         return 0
+    ok = ~np.isnan(row)
     best = row[ok].max()
     return int(np.flatnonzero(ok & (row == best))[0])
+
+
+def test_argmax_closed_form_is_golems_loop():
+    """The closed form the GPU tests use agrees with golem's loop on rows
+    with NaN (at 0 and elsewhere), -inf and repeated maxima (CPU)."""
+    g = synth.rng(77)
+    for trial in range(300):
+        n = int(g.integers(1, 40))
+        row = g.integers(-3, 3, n).astype(np.float32)
+        row[g.random(n) < 0.2] = np.nan
+        row[g.random(n) < 0.1] = -np.inf
+        assert _argmax_want(row) == _golem_argmax(row), row
 
 
 @pytest.mark.parametrize("n", [1, 5, 511, 513, 4097, 151936])
@@ -441,6 +538,7 @@ def test_argmax_parts_merge_in_order(dev, n):
     x[2, :n] = -np.inf
     x[3, :n] = 7.0
     x[4, :n] = np.where(g.random(n) < 0.5, np.nan, x[4, :n])
+    x[5, 0] = np.nan  # golem's pick is then 0 whatever follows
     ids = dev.empty((M,), np.int32)
     xd = dev.put(x)
     capi.call("gx_argmax", dev.ctx.ptr, capi.vp(xd), ld, M, n, capi.vp(ids))
@@ -450,8 +548,9 @@ def test_argmax_parts_merge_in_order(dev, n):
 
 def test_argmax_step_bookkeeping(dev):
     """gx_argmax_step: the id lands in ids[0] and at history[pos + 1]; the
-    counter and positions[0] advance by one; past the history's end nothing
-    is written there."""
+    counter and positions[0] advance by one; at the history's end the counter
+    stops (nothing past it is written, and the position a replayed step would
+    read stays inside the history)."""
     n = 151936
     x = np.zeros((1, n), np.float32)
     x[0, 4321] = 9.0
@@ -465,5 +564,5 @@ def test_argmax_step_bookkeeping(dev):
                   capi.vp(positions))
     assert dev.get(ids).tolist() == [4321]
     assert dev.get(hist).tolist() == [-5] * 7 + [4321] * 3  # positions 7, 8, 9; 10 is past the end
-    assert dev.get(pos).tolist() == [10]
-    assert dev.get(positions).tolist() == [10, 77]
+    assert dev.get(pos).tolist() == [9]
+    assert dev.get(positions).tolist() == [9, 77]

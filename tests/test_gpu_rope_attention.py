@@ -22,7 +22,7 @@ CASES = [(128, 32, 8, 640), (128, 16, 8, 200), (64, 4, 2, 304), (32, 8, 1, 96), 
          (64, 8, 1, 768)]
 
 
-def run_case(dev, hd, heads, kv, context, pos, max_pos, slots=None, nslots=1, seed=0):
+def run_case(dev, hd, heads, kv, context, pos, max_pos, slots=None, nslots=1, seed=0, parallel=False):
     g = synth.rng(seed + 7 * pos + hd)
     width = (heads + 2 * kv) * hd
     qkv = (g.standard_normal((1, width)) * 3).astype(np.float32)
@@ -42,8 +42,9 @@ def run_case(dev, hd, heads, kv, context, pos, max_pos, slots=None, nslots=1, se
         q8 = dev.empty((1, heads * hd), np.int8)
         sc = dev.empty((1, heads * hd // 32), np.float32)
         qs = dev.empty((1, heads * hd // 32), np.int32)
+        sfx = "_parallel" if parallel else ""
         if fused:
-            capi.call("gx_qwen_rope_attention", dev.ctx.ptr, capi.vp(ins[0]), width, heads, kv, hd, max_pos,
+            capi.call("gx_qwen_rope_attention" + sfx, dev.ctx.ptr, capi.vp(ins[0]), width, heads, kv, hd, max_pos,
                       capi.vp(ins[1]), capi.vp(ins[2]), capi.vp(ins[3]), capi.vp(ins[4]), capi.vp(ins[5]), eps,
                       capi.vp(kc), capi.vp(vc), context, capi.vp(q8), capi.vp(sc), capi.vp(qs),
                       capi.vp(sl) if sl is not None else None, nslots)
@@ -54,30 +55,47 @@ def run_case(dev, hd, heads, kv, context, pos, max_pos, slots=None, nslots=1, se
                       capi.vp(kc), capi.vp(vc), context, capi.vp(sl) if sl is not None else None, nslots)
             n = capi.size_out("gx_qwen_attention_workspace_bytes", 1, heads, max_pos)
             ws = dev.empty((n,), np.uint8)
-            capi.call("gx_qwen_attention", dev.ctx.ptr, capi.vp(qh), 1, heads, kv, hd, max_pos, capi.vp(ins[1]),
+            capi.call("gx_qwen_attention" + sfx, dev.ctx.ptr, capi.vp(qh), 1, heads, kv, hd, max_pos, capi.vp(ins[1]),
                       capi.vp(kc), capi.vp(vc), context, capi.vp(q8), capi.vp(sc), capi.vp(qs), capi.vp(ws), n,
                       capi.vp(sl) if sl is not None else None, nslots)
         dev.ctx.sync()
         outs.append([dev.get(a) for a in (q8, sc, qs, kc, vc)])
     for name, a, b in zip(("q", "scales", "sums", "key cache", "value cache"), *outs):
         assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), \
-            f"{name} differs (hd {hd}, heads {heads}/{kv}, pos {pos}, max_pos {max_pos}, slot {slots})"
-    return outs[1]
+            f"{name} differs (hd {hd}, heads {heads}/{kv}, pos {pos}, max_pos {max_pos}, slot {slots}, " \
+            f"parallel {parallel})"
+    return outs[1] + [kc0.view(np.int16), vc0.view(np.int16)]
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("parallel", [False, True])
 @pytest.mark.parametrize("hd,heads,kv,context", CASES)
-def test_rope_attention_matches_two_calls(dev, hd, heads, kv, context):
-    for pos in (0, context // 2 + 3, context - 1):
-        run_case(dev, hd, heads, kv, context, pos, pos)
-    run_case(dev, hd, heads, kv, context, context // 3, context - 1)
+def test_rope_attention_matches_two_calls(dev, hd, heads, kv, context, parallel):
+    for pos in (0, 7, 8, context // 2 + 3, context - 1):
+        run_case(dev, hd, heads, kv, context, pos, pos, parallel=parallel)
+    run_case(dev, hd, heads, kv, context, context // 3, context - 1, parallel=parallel)
 
 
 @pytest.mark.gpu
-def test_rope_attention_slots(dev):
+@pytest.mark.parametrize("parallel", [False, True])
+def test_rope_attention_slots(dev, parallel):
     hd, heads, kv, context = 128, 32, 8, 256
-    run_case(dev, hd, heads, kv, context, 100, context - 1, slots=2, nslots=3)
-    run_case(dev, hd, heads, kv, context, 50, context - 1, slots=5, nslots=3)
+    run_case(dev, hd, heads, kv, context, 100, context - 1, slots=2, nslots=3, parallel=parallel)
+    run_case(dev, hd, heads, kv, context, 50, context - 1, slots=5, nslots=3, parallel=parallel)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("parallel", [False, True])
+def test_rope_attention_outside_the_prefix(dev, parallel):
+    """A position past max_pos but inside the cache is stored and attends
+    positions 0 .. max_pos; one at the cache's end (a replayed step whose
+    counter reached the end of the context) stores nothing -- both caches
+    come out as they went in -- and its query is NaN; in both cases the
+    fused kernel agrees with the two calls bit for bit."""
+    hd, heads, kv, context = 64, 4, 2, 64
+    run_case(dev, hd, heads, kv, context, 40, 30, parallel=parallel)
+    q8, sc, qs, kc, vc, kc0, vc0 = run_case(dev, hd, heads, kv, context, context, context - 1, parallel=parallel)
+    assert np.array_equal(kc, kc0) and np.array_equal(vc, vc0)
 
 
 @pytest.mark.gpu
