@@ -61,6 +61,7 @@ _SIGNATURES = {
     "gx_moe_workspace_bytes": [_c_int, _c_int, _c_int, _c_int, _c_int, ctypes.POINTER(_c_size)],
     "gx_moe_route": [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, ctypes.c_float, _vp, _vp, _vp],
     "gx_moe_experts": [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _vp, _vp, _c_int, _vp, _c_size],
+    "gx_moe_experts_noalloc": [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _vp, _vp, _c_int],
     "gx_norm_quant": [_vp, _vp, _c_int, _vp, _c_int, _vp, _c_int, _c_int, ctypes.c_float, _vp, _c_int, _vp, _vp, _vp],
     "gx_qwen_qk_rope": [_vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _vp, ctypes.c_float,
                         _vp, _vp, _vp, _c_int, _vp, _c_int],

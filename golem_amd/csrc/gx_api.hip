@@ -14,6 +14,16 @@
 
 namespace {
 thread_local std::string g_error;
+
+// The scratch of the entry points that allocate nothing (gx_moe_experts_noalloc):
+// device memory of fixed size that the library holds on every GPU it runs
+// on until the process ends.  Host code never passes `scratch` itself to a
+// kernel -- on the host the name is only a stand-in -- but the address
+// hipGetSymbolAddress gives for it on the context's device, kept in the
+// context at gx_init.  Every call on one GPU shares it: calls that overlap
+// on one GPU race, and each call finds what the last one left there.
+constexpr size_t kScratchBytes = (size_t)16 << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
 }
 
 namespace gx {
@@ -84,6 +94,7 @@ int gx_init(int device, gx_ctx **out) {
     ctx->gelu_table = nullptr;
     ctx->argmax_v = nullptr;
     ctx->argmax_i = nullptr;
+    ctx->scratch = nullptr;
     auto undo = [ctx]() {
         (void)hipFree(ctx->gelu_table);
         (void)hipFree(ctx->argmax_v);
@@ -100,6 +111,16 @@ int gx_init(int device, gx_ctx **out) {
         hipMalloc(&ctx->argmax_i, kArgmaxRows * kArgmaxParts * sizeof(int32_t)) != hipSuccess) {
         undo();
         return gx::fail(GX_ERR_NOMEM, "gx: cannot allocate the greedy pick's workspace");
+    }
+    {
+        // this device's address of the static scratch (the device is current)
+        void *sp = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || sp == nullptr) {
+            undo();
+            return gx::fail(GX_ERR_HIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+        }
+        ctx->scratch = (uint8_t *)sp;
     }
     if (int rc = gx::launch_gelu_table(ctx, ctx->gelu_table)) {
         undo();
@@ -790,9 +811,9 @@ int gx_argmax_step(gx_ctx *ctx, const float *x, int n, int32_t *ids, int32_t *hi
     return ok();
 }
 
-int gx_moe_experts(gx_ctx *ctx, const gx_weight *gate_up, const gx_weight *down, const float *down_scale,
-                   const float *x, int ldx, int M, int top_k, const int32_t *ids, const float *weights, float *out,
-                   int ldo, void *workspace, size_t workspace_bytes) {
+static int moe_experts(gx_ctx *ctx, const gx_weight *gate_up, const gx_weight *down, const float *down_scale,
+                       const float *x, int ldx, int M, int top_k, const int32_t *ids, const float *weights, float *out,
+                       int ldo, void *workspace, size_t workspace_bytes, bool noalloc) {
     if (int rc = use(ctx))
         return rc;
     GX_CHECK(gate_up && down && gate_up->quant == GX_Q4_0 && down->quant == GX_Q4_0,
@@ -807,6 +828,11 @@ int gx_moe_experts(gx_ctx *ctx, const gx_weight *gate_up, const gx_weight *down,
     GX_CHECK(((uintptr_t)workspace & 255) == 0, "gx: the workspace must be 256-byte aligned");
     size_t need = 0;
     gx::moe_workspace_bytes(M, top_k, gate_up->cols, down->cols, gate_up->count, &need);
+    if (noalloc)
+        GX_CHECK(need <= workspace_bytes,
+                 "gx: %d positions of %d experts need %zu bytes of scratch; gx_moe_experts_noalloc holds %zu (use "
+                 "gx_moe_experts with a workspace, or fewer positions a call)",
+                 M, top_k, need, workspace_bytes);
     GX_CHECK(workspace_bytes >= need, "gx: the workspace holds %zu bytes, %zu needed", workspace_bytes, need);
     if (M == 0)
         return ok();
@@ -814,6 +840,23 @@ int gx_moe_experts(gx_ctx *ctx, const gx_weight *gate_up, const gx_weight *down,
                                         (uint8_t *)workspace, ctx->gelu_table))
         return rc;
     return ok();
+}
+
+int gx_moe_experts(gx_ctx *ctx, const gx_weight *gate_up, const gx_weight *down, const float *down_scale,
+                   const float *x, int ldx, int M, int top_k, const int32_t *ids, const float *weights, float *out,
+                   int ldo, void *workspace, size_t workspace_bytes) {
+    return moe_experts(ctx, gate_up, down, down_scale, x, ldx, M, top_k, ids, weights, out, ldo, workspace,
+                       workspace_bytes, false);
+}
+
+int gx_moe_experts_noalloc(gx_ctx *ctx, const gx_weight *gate_up, const gx_weight *down, const float *down_scale,
+                           const float *x, int ldx, int M, int top_k, const int32_t *ids, const float *weights,
+                           float *out, int ldo) {
+    if (int rc = use(ctx))
+        return rc;
+    // the scratch's address on this device (from gx_init), never the symbol
+    return moe_experts(ctx, gate_up, down, down_scale, x, ldx, M, top_k, ids, weights, out, ldo, ctx->scratch,
+                       kScratchBytes, true);
 }
 
 }  // extern "C"

@@ -63,6 +63,7 @@ struct gx_ctx {
     float *gelu_table;  // golem's 65536-entry GELU table, built on the device at init
     float *argmax_v;    // the greedy pick's part maxima [kArgmaxRows][kArgmaxParts]
     int32_t *argmax_i;  // and their indices
+    uint8_t *scratch;   // this device's copy of the no-alloc entry points' static scratch (gx_api.hip)
 };
 
 

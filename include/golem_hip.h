@@ -245,6 +245,21 @@ int gx_moe_experts(gx_ctx *ctx, const gx_weight *gate_up, const gx_weight *down,
                    const float *x, int ldx, int M, int top_k, const int32_t *ids, const float *weights, float *out,
                    int ldo, void *workspace, size_t workspace_bytes);
 
+/* gx_moe_experts without the workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid allocation).  No counterpart in golem.  Its
+ * scratch is a fixed 16 MiB of device memory the library holds on every GPU
+ * it runs on until the process ends; a call whose workspace
+ * (gx_moe_workspace_bytes) would exceed it is refused with GX_ERR_INVALID,
+ * before any work is queued.  The call allocates nothing and queues the same
+ * kernels as gx_moe_experts, so the outputs are the same bit for bit.  All
+ * calls on one GPU share that scratch, which keeps the last call's contents:
+ * calls that overlap on one GPU (several streams, several contexts, or
+ * several host threads) race; order them on one stream. */
+int gx_moe_experts_noalloc(gx_ctx *ctx, const gx_weight *gate_up, const gx_weight *down, const float *down_scale,
+                           const float *x, int ldx, int M, int top_k, const int32_t *ids, const float *weights,
+                           float *out, int ldo);
+
 /* The shared expert's activation (gemma/block.go:163-174, the dense feed
  * forward's): gu [M][ldgu] holds each position's ffn gates then its ffn ups;
  * q/scales/qsum receive Q8_0(GELUTable(gate) * up) [M][ffn] (nn/gelu_table.go
