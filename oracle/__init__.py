@@ -70,7 +70,7 @@ def load():
         "orc_axpy": (None, [V, V, I, F]),
         "orc_choose_experts": (None, [V, I, I, V, V]),
         "orc_route_one": (None, [V, I, V, V, I, I, F, V, V, V, V]),
-        "orc_expert_unit": (None, [V, V, V, I, I, V]),
+        "orc_expert_unit": (None, [I, V, V, V, I, I, V]),
         "orc_expert_reduce": (None, [V, V, V, V, I, I, V]),
     }
     for name, (res, args) in sig.items():
@@ -299,10 +299,13 @@ def route_one(resid, router, used, eps=1e-6, router_scale=None):
     return logits, ids, weights
 
 
-def expert_unit(gate_up_w, down_w, x, dim, ffn):
+def expert_unit(gate_up_w, down_w, x, dim, ffn, quant=None):
+    """One (position, expert) unit of ExpertFFN; quant Q4_0 (default) or F32
+    stacks."""
     partial = np.zeros(dim, dtype=np.float32)
-    load().orc_expert_unit(_p(np.ascontiguousarray(gate_up_w)), _p(np.ascontiguousarray(down_w)),
-                           _p(np.ascontiguousarray(x, dtype=np.float32)), dim, ffn, _p(partial))
+    load().orc_expert_unit(Q4_0 if quant is None else quant, _p(np.ascontiguousarray(gate_up_w)),
+                           _p(np.ascontiguousarray(down_w)), _p(np.ascontiguousarray(x, dtype=np.float32)), dim, ffn,
+                           _p(partial))
     return partial
 
 

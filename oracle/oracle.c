@@ -778,14 +778,20 @@ void orc_route_one(const float *resid, int dim, const float *router /*[experts][
     orc_choose_experts(logits, experts, used, ids, weights);
 }
 
-/* One (position, expert) unit of ExpertFFN, gemma/moe.go:137-162, on the row
- * layout (ExpertStack.At, gemma/weights.go:67-72; never repacked):
- *   x (dim floats) is quantised to Q8_0 as one contiguous column,
- *   gate_up = GateUp[id] * x (2*ffn rows, gate first then up),
- *   gate = GELUTable(gate); mid = gate * up; mid quantised (ffn inputs),
- *   partial = Down[id] * mid (dim rows).
- * gate_up_w is one expert's 2*ffn x dim Q4_0 rows, down_w its dim x ffn rows. */
-void orc_expert_unit(const uint8_t *gate_up_w, const uint8_t *down_w, const float *x, int dim, int ffn,
+/* One (position, expert) unit of ExpertFFN, gemma/moe.go:119-162, on the row
+ * layout (ExpertStack.At, gemma/weights.go:67-72; never repacked), both
+ * products through Matrix.rows (MatVecRows, nn/matrix.go:87-131) of the
+ * stack's format:
+ *   x (dim floats) is quantised to Q8_0 as one contiguous column
+ *     (moe.go:119-125),
+ *   gate_up = GateUp[id] . x (2*ffn rows, gate first then up, moe.go:142-147),
+ *   gate = GELUTable(gate); mid = gate * up (moe.go:149-152); mid quantised,
+ *   partial = Down[id] . mid (dim rows, moe.go:154-156).
+ * quant is ORC_Q4_0 (the configs' stacks: Q8_0 products) or ORC_F32 (golem's
+ * own test stacks, gemma/moe_test.go:21-56: DotF32 of each row with the
+ * floats; the Q8_0 forms are made but unread).  gate_up_w is one expert's
+ * 2*ffn x dim rows, down_w its dim x ffn rows. */
+void orc_expert_unit(int quant, const uint8_t *gate_up_w, const uint8_t *down_w, const float *x, int dim, int ffn,
                      float *partial)
 {
     int8_t *q = malloc(dim);
@@ -796,12 +802,14 @@ void orc_expert_unit(const uint8_t *gate_up_w, const uint8_t *down_w, const floa
     float *msc = malloc(sizeof(float) * (ffn / 32)), *mco = malloc(sizeof(float) * (ffn / 32));
 
     orc_quantize_column_range(x, dim, 1, q, sc, co, 0, 0, dim);
-    orc_mat_vec_q4_0_rows(gate_up_w, q, sc, co, 1, 1, dim, gu, 2 * ffn, 0, 2 * ffn);
+    orc_matrix_rows(quant, gate_up_w, NULL, 2 * ffn, dim, NULL, 0, x, q, sc, co, NULL, NULL, NULL, 1, 1, gu, 2 * ffn,
+                    0, 2 * ffn);
     orc_gelu_table(gu, ffn);
     for (int i = 0; i < ffn; i++)
         mid[i] = gu[i] * gu[ffn + i];
     orc_quantize_column_range(mid, ffn, 1, mq, msc, mco, 0, 0, ffn);
-    orc_mat_vec_q4_0_rows(down_w, mq, msc, mco, 1, 1, ffn, partial, dim, 0, dim);
+    orc_matrix_rows(quant, down_w, NULL, dim, ffn, NULL, 0, mid, mq, msc, mco, NULL, NULL, NULL, 1, 1, partial, dim, 0,
+                    dim);
 
     free(q); free(sc); free(co); free(gu); free(mid); free(mq); free(msc); free(mco);
 }
