@@ -410,9 +410,11 @@ def bench_c4(ctx, torch, dev):
     """Config 4: router (128 x 2816 fp32) + top-8 + 8 GELU-gated Q4_0 experts
     per position (gate_up 1408 x 2816, down 2816 x 704), seed 4. Decode (one
     position) and a 256-position prefill grouped by expert, each timed as
-    route + experts with HIP events. Two copies of the expert stacks (856 MB,
-    beyond the 256 MB last-level cache) alternate between steps, and decode
-    walks 64 different positions, so the experts a step reads are not cached."""
+    route + experts with HIP events (decode also as replays of a captured
+    graph of 16 steps, the figure reported; the eager figure beside it). Two
+    copies of the expert stacks (856 MB, beyond the 256 MB last-level cache)
+    alternate between steps, and decode walks 64 different positions, so the
+    experts a step reads are not cached."""
     from golem_amd import capi, synth
     import ctypes
     call, vp = capi.call, capi.vp
@@ -458,12 +460,37 @@ def bench_c4(ctx, torch, dev):
         for i in range(reps):
             step(i)
         ms = ctx.timer_stop() / reps
+        eager_ms = ms
+        if M == 1:
+            # Decode as a serving loop runs it: the layer's launches captured
+            # once (16 steps over rotating inputs and stacks) and replayed.
+            gsteps = 16
+            torch.cuda.synchronize()
+            stream = torch.cuda.Stream()
+            graph = torch.cuda.CUDAGraph()
+            call("gx_set_stream", ctx.ptr, ctypes.c_void_p(stream.cuda_stream))
+            try:
+                with torch.cuda.graph(graph, stream=stream):
+                    for i in range(gsteps):
+                        step(i)
+            finally:
+                call("gx_set_stream", ctx.ptr, None)
+            for _ in range(2):
+                graph.replay()
+            torch.cuda.synchronize()
+            greps = 8
+            ctx.timer_start()
+            for _ in range(greps):
+                graph.replay()
+            ms = ctx.timer_stop() / (greps * gsteps)
+            del graph
         mean_touched = float(np.mean(touched))
         by = mean_touched * expert_bytes + E * D * 4 + M * D * 4 * 2
         res[f"c4_moe_{label}"] = {
             "M": M, "ms_per_layer": round(ms, 4), "positions_per_s": round(M / (ms * 1e-3), 1),
             "experts_read": round(mean_touched, 2), "bytes_per_layer": int(by),
-            "GB/s": round(by / (ms * 1e-3) / 1e9, 1), "hbm_frac": round(by / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+            "GB/s": round(by / (ms * 1e-3) / 1e9, 1), "hbm_frac": round(by / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "graph": M == 1, "eager_ms_per_layer": round(eager_ms, 4)}
     wr.free()
     for gu, dn in stacks:
         gu.free()

@@ -95,7 +95,9 @@ int gx_init(int device, gx_ctx **out) {
     ctx->argmax_v = nullptr;
     ctx->argmax_i = nullptr;
     ctx->scratch = nullptr;
+    ctx->route_count = nullptr;
     auto undo = [ctx]() {
+        (void)hipFree(ctx->route_count);
         (void)hipFree(ctx->gelu_table);
         (void)hipFree(ctx->argmax_v);
         (void)hipFree(ctx->argmax_i);
@@ -111,6 +113,11 @@ int gx_init(int device, gx_ctx **out) {
         hipMalloc(&ctx->argmax_i, kArgmaxRows * kArgmaxParts * sizeof(int32_t)) != hipSuccess) {
         undo();
         return gx::fail(GX_ERR_NOMEM, "gx: cannot allocate the greedy pick's workspace");
+    }
+    if (hipMalloc(&ctx->route_count, kRouteMaxPos * sizeof(unsigned)) != hipSuccess ||
+        hipMemset(ctx->route_count, 0, kRouteMaxPos * sizeof(unsigned)) != hipSuccess) {
+        undo();
+        return gx::fail(GX_ERR_NOMEM, "gx: cannot allocate the router's counters");
     }
     {
         // this device's address of the static scratch (the device is current)
@@ -143,6 +150,7 @@ int gx_free(gx_ctx *ctx) {
     (void)hipFree(ctx->gelu_table);
     (void)hipFree(ctx->argmax_v);
     (void)hipFree(ctx->argmax_i);
+    (void)hipFree(ctx->route_count);
     delete ctx;
     return ok();
 }
@@ -548,6 +556,30 @@ int gx_q4_0_block_dots(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const f
     else
         rc = gx::launch_q4_0_gemm_f16(ctx, w, w->dev, q16, nullptr, M, row_start, row_end, nullptr, nullptr, 0, out);
     if (rc)
+        return rc;
+    return ok();
+}
+
+int gx_moe_unit_dots(gx_ctx *ctx, const gx_weight *gate_up, const gx_weight *down, const float *x, int ldx, int M,
+                     int top_k, const int32_t *ids, const int8_t *mid_q, const float *mid_scales,
+                     const int32_t *mid_qsum, int32_t *dots_gate_up, int32_t *dots_down) {
+    if (int rc = use(ctx))
+        return rc;
+    GX_CHECK(gate_up && down && gate_up->quant == GX_Q4_0 && down->quant == GX_Q4_0,
+             "gx: the expert stacks are Q4_0 matrices");
+    GX_CHECK(gate_up->count == down->count, "gx: %d gate_up experts but %d down experts", gate_up->count, down->count);
+    GX_CHECK(gate_up->rows == 2 * down->cols && down->rows == gate_up->cols,
+             "gx: gate_up is %dx%d and down %dx%d: want 2F x D and D x F", gate_up->rows, gate_up->cols, down->rows,
+             down->cols);
+    GX_CHECK(top_k > 0 && top_k <= gate_up->count, "gx: top_k %d out of range", top_k);
+    GX_CHECK(M >= 0 && M <= 4, "gx: the few-position expert kernels take at most 4 positions, not %d", M);
+    GX_CHECK(ids && (!dots_gate_up || (x && ldx >= gate_up->cols)) &&
+                 (!dots_down || (mid_q && mid_scales && mid_qsum)),
+             "gx: missing argument");
+    if (M == 0)
+        return ok();
+    if (int rc = gx::launch_moe_unit_dots(ctx, gate_up, down, x, ldx, M, top_k, ids, mid_q, mid_scales, mid_qsum,
+                                          dots_gate_up, dots_down))
         return rc;
     return ok();
 }

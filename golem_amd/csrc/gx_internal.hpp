@@ -64,11 +64,13 @@ struct gx_ctx {
     float *argmax_v;    // the greedy pick's part maxima [kArgmaxRows][kArgmaxParts]
     int32_t *argmax_i;  // and their indices
     uint8_t *scratch;   // this device's copy of the no-alloc entry points' static scratch (gx_api.hip)
+    unsigned *route_count;  // the one-launch router's per-position counters [kRouteMaxPos], zero between calls
 };
 
 
 constexpr int kArgmaxParts = 128;  // workgroups per row of the greedy pick
 constexpr int kArgmaxRows = 64;    // rows per launch pair
+constexpr int kRouteMaxPos = 4;    // positions routed by the one-launch router kernel
 
 struct gx_weight {
     gx_ctx *ctx;
@@ -137,6 +139,9 @@ int launch_moe_route(gx_ctx *ctx, const gx_weight *router, const float *router_s
 int launch_moe_experts(gx_ctx *ctx, const gx_weight *gate_up, const gx_weight *down, const float *down_scale,
                        const float *x, int ldx, int M, int k, const int32_t *ids, const float *weights, float *out,
                        int ldo, uint8_t *ws, const float *gelu_table);
+int launch_moe_unit_dots(gx_ctx *ctx, const gx_weight *gate_up, const gx_weight *down, const float *x, int ldx,
+                         int M, int k, const int32_t *ids, const int8_t *mid_q, const float *mid_scales,
+                         const int32_t *mid_qsum, int32_t *dots_gate_up, int32_t *dots_down);
 int launch_qwen_norm_quant(gx_ctx *ctx, float *x, int ldx, const float *add, int lda, const float *gain, int M, int K,
                            float eps, float *out, int ldo, int8_t *q, float *scales, int32_t *qsum);
 int launch_qwen_qk_rope(gx_ctx *ctx, const float *qkv, int ldqkv, int M, int heads, int kv_heads, int hd,

@@ -48,34 +48,149 @@ __global__ void gelu_table_kernel(float *__restrict__ table) {
 // rare ties.  The normalised input is (x * scale) * ((1/sqrt(D)) *
 // RouterScale[i]), as Route forms it (gemma/moe.go:34-53).
 //
-//   moe_logits_one_kernel: one workgroup per (expert, position); the row and
-//     the position's input sit in LDS, every load issued at once.  Few
-//     positions (decode), where the cost is latency.
+//   moe_route_one_kernel: one workgroup per (expert, position) for few
+//     positions (decode), where the cost is latency: the row and the input
+//     are read with every load issued at once, the products are formed by
+//     all threads into LDS chain by chain, and four lanes run the chains.
+//     The workgroup that finishes a position's last logit (a counter per
+//     position, kept by the context) then chooses its experts, so routing
+//     is one launch.
 //   moe_logits_kernel<EW>: EW experts x 64/EW positions per workgroup; rows and
 //     inputs pass through LDS a 64-input chunk at a time, fetched from a ring
-//     of registers kLogitsDepth chunks ahead.  Many positions.
+//     of registers kLogitsDepth chunks ahead.  Many positions; the choosing
+//     is moe_topk_kernel.
 constexpr int kLogitsThreads = 256;
 constexpr int kLogitsChunk = 64;     // inputs per chunk
 constexpr int kLogitsChunkPad = 68;  // chunk row stride in LDS (bank spread)
 constexpr int kLogitsDepth = 8;      // chunks fetched ahead
-constexpr int kLogitsOneMaxD = 7168; // row + input in LDS: 57 KB
+constexpr int kLogitsOneMaxD = 7168; // input + products in LDS: 57 KB
 constexpr int kLogitsOneF4 = kLogitsOneMaxD / 4 / kLogitsThreads;
+constexpr int kTopkMaxPerLane = 16;  // E <= 1024
+constexpr int kTopkMax = 64;         // k <= 64
+constexpr int kUnitMaxPos = 4;       // positions whose units run as matrix-vector products
 
-__global__ __launch_bounds__(kLogitsThreads) void moe_logits_one_kernel(const float *__restrict__ router, int D,
-                                                                        int E, const float *__restrict__ router_scale,
-                                                                        const float *__restrict__ resid, int ldr,
-                                                                        float eps, float *__restrict__ logits) {
-    extern __shared__ float lds[];
-    float *row = lds, *xr = lds + D;
+// chooseExperts (gemma/moe.go:62-88) for one position whose E logits sit in
+// LDS (lg, padded with -inf to a multiple of 4), by a whole workgroup of at
+// least 64 threads.  golem takes k rounds of an argmax that scans in index
+// order and replaces its best only on a strictly greater logit.  Without a
+// NaN the rounds take the logits by value, largest first and equal values
+// lower index first, so logit i is taken in round
+//     r = #{j : l_j > l_i} + #{j < i : l_j == l_i},
+// which each thread computes for its logits at once (a -inf pad is never
+// greater than a logit, and never equal at a lower index).  A NaN is taken
+// only as the first logit not yet chosen (no comparison with it is ever
+// true); with any NaN present wavefront 0 runs the rounds as golem does.
+// Weights: exp(l - top) in float64 of the float32 difference, rounded to
+// float32, summed in slot order, divided by the sum.
+__device__ void choose_experts(const float *lg, int E, int k, float *sel_l, int32_t *sel_i, float *wv,
+                               int32_t *__restrict__ ids, float *__restrict__ weights) {
+    const int tid = threadIdx.x, nt = blockDim.x;
+    bool nan_here = false;
+    for (int i = tid; i < E; i += nt)
+        nan_here |= lg[i] != lg[i];
+    if (!__syncthreads_or(nan_here)) {
+        const int E4 = (E + 3) & ~3;
+        for (int i = tid; i < E; i += nt) {
+            const float v = lg[i];
+            int r = 0;
+            for (int j = 0; j < E4; j += 4) {
+                const float4 w = *(const float4 *)(lg + j);
+                r += (int)((w.x > v) | ((w.x == v) & (j + 0 < i)));
+                r += (int)((w.y > v) | ((w.y == v) & (j + 1 < i)));
+                r += (int)((w.z > v) | ((w.z == v) & (j + 2 < i)));
+                r += (int)((w.w > v) | ((w.w == v) & (j + 3 < i)));
+            }
+            if (r < k) {
+                sel_l[r] = v;
+                sel_i[r] = i;
+            }
+        }
+    } else if (tid < 64) {
+        const int lane = tid;
+        float v[kTopkMaxPerLane];
+        unsigned taken = 0;  // bit j: logit lane + 64 j is chosen or absent
+#pragma unroll
+        for (int j = 0; j < kTopkMaxPerLane; j++) {
+            const int e = lane + 64 * j;
+            v[j] = lg[min(e, E - 1)];
+            taken |= (e >= E ? 1u : 0u) << j;
+        }
+        for (int round = 0; round < k; round++) {
+            // the first logit not yet chosen wins the round if it is a NaN
+            int first = 0x7fffffff;
+            const unsigned open = ~taken & ((1u << kTopkMaxPerLane) - 1);
+            if (open)
+                first = lane + 64 * __builtin_ctz(open);
+            for (int w = 32; w > 0; w >>= 1)
+                first = min(first, __shfl_xor(first, w, 64));
+            int best = lg[first] != lg[first] ? first : 0x7fffffff;
+            if (best == 0x7fffffff) {
+                // otherwise the largest non-NaN logit not yet chosen, the
+                // lowest index among equals
+                float bv = 0.0f;
+                int bi = 0x7fffffff;
+#pragma unroll
+                for (int j = 0; j < kTopkMaxPerLane; j++) {
+                    const int e = lane + 64 * j;
+                    if (((taken >> j) & 1u) || v[j] != v[j])
+                        continue;
+                    if (bi == 0x7fffffff || v[j] > bv) {  // e rises with j: equal values keep the lower index
+                        bv = v[j];
+                        bi = e;
+                    }
+                }
+                for (int w = 32; w > 0; w >>= 1) {
+                    const float ov = __shfl_xor(bv, w, 64);
+                    const int oi = __shfl_xor(bi, w, 64);
+                    if (oi != 0x7fffffff && (bi == 0x7fffffff || ov > bv || (ov == bv && oi < bi))) {
+                        bv = ov;
+                        bi = oi;
+                    }
+                }
+                best = bi;
+            }
+            if ((best & 63) == lane)
+                taken |= 1u << (best >> 6);
+            if (lane == 0) {
+                sel_i[round] = best;
+                sel_l[round] = lg[best];
+            }
+        }
+    }
+    __syncthreads();
+    if (tid < k) {
+        ids[tid] = sel_i[tid];
+        wv[tid] = (float)exp((double)(sel_l[tid] - sel_l[0]));
+    }
+    __syncthreads();
+    if (tid < k) {
+        float total = 0.0f;
+        for (int j = 0; j < k; j++)
+            total += wv[j];
+        weights[tid] = wv[tid] / total;
+    }
+}
+
+__global__ __launch_bounds__(kLogitsThreads) void moe_route_one_kernel(
+    const float *__restrict__ router, int D, int E, const float *__restrict__ router_scale,
+    const float *__restrict__ resid, int ldr, float eps, int k, float *__restrict__ logits,
+    int32_t *__restrict__ ids, float *__restrict__ weights, unsigned *__restrict__ count) {
+    extern __shared__ __align__(16) float lds[];  // the input [max(D, E4)], then the products [4][D/4 + 4]
     __shared__ double red[kLogitsThreads];
     __shared__ float scale_sh;
+    __shared__ int last_sh;
+    __shared__ float sel_l[kTopkMax], wv[kTopkMax];
+    __shared__ int32_t sel_i[kTopkMax];
     const int tid = threadIdx.x, e = blockIdx.x, t = blockIdx.y;
+    const int E4 = (E + 3) & ~3;
+    float *xr = lds;
+    float *P = lds + max(D, E4);
+    const int cs = D / 4 + 4;  // a chain's stride: the four chains start in different banks
     const float *rg = router + (size_t)e * D;
     const float *xg = resid + (size_t)t * ldr;
     const int n4 = D / 4;
-    // Clamped indices and clamped stores (a thread past the end stores the
-    // last piece's own value again): every load is issued before the first
-    // wait, with no branch for a load to sink into.
+    // Clamped indices: every load is issued before the first wait, with no
+    // branch for a load to sink into.
     float4 rv[kLogitsOneF4 + 1], xv[kLogitsOneF4 + 1], sv[kLogitsOneF4 + 1];
 #pragma unroll
     for (int f = 0; f <= kLogitsOneF4; f++) {
@@ -86,9 +201,9 @@ __global__ __launch_bounds__(kLogitsThreads) void moe_logits_one_kernel(const fl
     }
 #pragma unroll
     for (int f = 0; f <= kLogitsOneF4; f++) {
-        const int q = min(tid + f * kLogitsThreads, n4 - 1);
-        *(float4 *)(row + 4 * q) = rv[f];
-        *(float4 *)(xr + 4 * q) = xv[f];
+        const int q = tid + f * kLogitsThreads;
+        if (q < n4)
+            *(float4 *)(xr + 4 * q) = xv[f];
     }
     __syncthreads();
     double p0, p1;
@@ -99,43 +214,71 @@ __global__ __launch_bounds__(kLogitsThreads) void moe_logits_one_kernel(const fl
     __syncthreads();
     const float sc = scale_sh;
     const float inv_sqrt_dim = (float)(1.0 / sqrt((double)D));
-    // x * scale * ((1/sqrt(D)) * RouterScale[i]), from the registers
+    // The products row[i] * ((x[i] * scale) * ((1/sqrt(D)) * RouterScale[i])),
+    // element 4j + c at P[c * cs + j].
 #pragma unroll
     for (int f = 0; f <= kLogitsOneF4; f++) {
-        const int q = min(tid + f * kLogitsThreads, n4 - 1);
+        const int q = tid + f * kLogitsThreads;
         const float x4[4] = {xv[f].x, xv[f].y, xv[f].z, xv[f].w}, s4[4] = {sv[f].x, sv[f].y, sv[f].z, sv[f].w};
-        float o4[4];
+        const float r4[4] = {rv[f].x, rv[f].y, rv[f].z, rv[f].w};
+        if (q < n4) {
 #pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const float normed = x4[c] * sc;
-            const float factor = inv_sqrt_dim * s4[c];
-            o4[c] = normed * factor;
+            for (int c = 0; c < 4; c++) {
+                const float normed = x4[c] * sc;
+                const float factor = inv_sqrt_dim * s4[c];
+                const float xn = normed * factor;
+                P[c * cs + q] = r4[c] * xn;
+            }
         }
-        *(float4 *)(xr + 4 * q) = make_float4(o4[0], o4[1], o4[2], o4[3]);
     }
     __syncthreads();
     if (tid < 64) {
-        const int c = tid & 3;
         float acc = 0.0f;
         if (tid < 4) {
-            for (int i0 = c; i0 < D; i0 += 64) {  // D % 64 == 0: 16 steps per pass
-                float a[16], b[16];
+            // chain tid: its products in order, 16 at a time, the next 16
+            // read while these are added
+            const float4 *pc = (const float4 *)(P + tid * cs);
+            const int n = D / 16;  // float4s per chain, a multiple of 4
+            float4 cur[4], nxt[4];
 #pragma unroll
-                for (int j = 0; j < 16; j++) {
-                    a[j] = row[i0 + 4 * j];
-                    b[j] = xr[i0 + 4 * j];
+            for (int u = 0; u < 4; u++)
+                cur[u] = pc[u];
+            for (int j = 0; j < n; j += 4) {
+                if (j + 4 < n) {
+#pragma unroll
+                    for (int u = 0; u < 4; u++)
+                        nxt[u] = pc[j + 4 + u];
                 }
 #pragma unroll
-                for (int j = 0; j < 16; j++) {
-                    const float prod = a[j] * b[j];
-                    acc = acc + prod;
+                for (int u = 0; u < 4; u++) {
+                    acc = acc + cur[u].x;
+                    acc = acc + cur[u].y;
+                    acc = acc + cur[u].z;
+                    acc = acc + cur[u].w;
                 }
+#pragma unroll
+                for (int u = 0; u < 4; u++)
+                    cur[u] = nxt[u];
             }
         }
         const float s1 = __shfl_down(acc, 1, 64), s2 = __shfl_down(acc, 2, 64), s3 = __shfl_down(acc, 3, 64);
-        if (tid == 0)
+        if (tid == 0) {
             logits[(size_t)t * E + e] = (acc + s1) + (s2 + s3);
+            // the logit is visible device-wide before it is counted; the
+            // counter wraps to 0 on the last count, ready for the next launch
+            __threadfence();
+            last_sh = atomicInc(count + t, (unsigned)(E - 1)) == (unsigned)(E - 1);
+        }
     }
+    __syncthreads();
+    if (!last_sh)
+        return;
+    // The position's last logit: every other workgroup's is visible now.
+    __threadfence();
+    for (int i = tid; i < E4; i += kLogitsThreads)
+        xr[i] = i < E ? logits[(size_t)t * E + i] : -__builtin_inff();
+    __syncthreads();
+    choose_experts(xr, E, k, sel_l, sel_i, wv, ids + (size_t)t * k, weights + (size_t)t * k);
 }
 
 template <int EW>
@@ -255,109 +398,28 @@ __global__ __launch_bounds__(kLogitsThreads) void moe_logits_kernel(const float 
         logits[(size_t)(t0 + p) * E + e0 + e] = (acc + s1) + (s2 + s3);
 }
 
-// chooseExperts (gemma/moe.go:62-88) for one position per wavefront: k rounds
-// of argmax over the logits not yet chosen.  golem scans in index order and
-// replaces its best on a strictly greater logit, so ties go to the lower
-// index and a NaN is taken only when it is the first logit not yet chosen
-// (no comparison with it is ever true); the wavefront reduction keeps exactly
-// that rule.  Weights: exp(l - top) in float64, rounded to float32, summed in
-// slot order, divided by the sum.
-constexpr int kTopkMaxPerLane = 16;  // E <= 1024
-constexpr int kTopkMax = 64;         // k <= 64
-
-__global__ __launch_bounds__(64) void moe_topk_kernel(const float *__restrict__ logits, int E, int k,
-                                                      int32_t *__restrict__ ids, float *__restrict__ weights) {
-    __shared__ float chosen_l[kTopkMax];
-    __shared__ float wv[kTopkMax];
-    __shared__ float lg[64 * kTopkMaxPerLane];
-    const int t = blockIdx.x, lane = threadIdx.x;
-    const float *lgg = logits + (size_t)t * E;
-    float v[kTopkMaxPerLane];
-    unsigned taken = 0;  // bit j: logit lane + 64 j is chosen or absent
-#pragma unroll
-    for (int j = 0; j < kTopkMaxPerLane; j++) {
-        const int e = lane + 64 * j;
-        v[j] = lgg[min(e, E - 1)];
-        lg[e] = v[j];
-        taken |= (e >= E ? 1u : 0u) << j;
-    }
+// chooseExperts for many positions: one workgroup a position.
+__global__ __launch_bounds__(256) void moe_topk_kernel(const float *__restrict__ logits, int E, int k,
+                                                       int32_t *__restrict__ ids, float *__restrict__ weights) {
+    __shared__ __align__(16) float lg[64 * kTopkMaxPerLane];
+    __shared__ float sel_l[kTopkMax], wv[kTopkMax];
+    __shared__ int32_t sel_i[kTopkMax];
+    const int t = blockIdx.x, E4 = (E + 3) & ~3;
+    for (int i = threadIdx.x; i < E4; i += blockDim.x)
+        lg[i] = i < E ? logits[(size_t)t * E + i] : -__builtin_inff();
     __syncthreads();
-    // A NaN logit is taken only as the first logit not yet chosen; without
-    // any, a round is a plain argmax (greater value, then lower index).
-    bool nan_here = false;
-#pragma unroll
-    for (int j = 0; j < kTopkMaxPerLane; j++)
-        nan_here |= lane + 64 * j < E && v[j] != v[j];
-    const bool any_nan = __any(nan_here);
-    for (int round = 0; round < k; round++) {
-        int best = 0x7fffffff;
-        if (any_nan) {
-            int first = 0x7fffffff;
-            const unsigned open = ~taken & ((1u << kTopkMaxPerLane) - 1);
-            if (open)
-                first = lane + 64 * __builtin_ctz(open);
-            for (int w = 32; w > 0; w >>= 1)
-                first = min(first, __shfl_xor(first, w, 64));
-            if (lg[first] != lg[first])
-                best = first;
-        }
-        if (best == 0x7fffffff) {
-            // largest non-NaN value not yet chosen, lowest index among equals
-            float bv = 0.0f;
-            int bi = 0x7fffffff;
-#pragma unroll
-            for (int j = 0; j < kTopkMaxPerLane; j++) {
-                const int e = lane + 64 * j;
-                if (((taken >> j) & 1u) || v[j] != v[j])
-                    continue;
-                if (bi == 0x7fffffff || v[j] > bv) {  // e rises with j: equal values keep the lower index
-                    bv = v[j];
-                    bi = e;
-                }
-            }
-            for (int w = 32; w > 0; w >>= 1) {
-                const float ov = __shfl_xor(bv, w, 64);
-                const int oi = __shfl_xor(bi, w, 64);
-                if (oi != 0x7fffffff && (bi == 0x7fffffff || ov > bv || (ov == bv && oi < bi))) {
-                    bv = ov;
-                    bi = oi;
-                }
-            }
-            best = bi;
-        }
-        if ((best & 63) == lane)
-            taken |= 1u << (best >> 6);
-        if (lane == 0) {
-            ids[(size_t)t * k + round] = best;
-            chosen_l[round] = lg[best];
-        }
-    }
-    __syncthreads();
-    // exp(l - top) in float64 for every slot at once; the sum in slot order.
-    if (lane < k)
-        wv[lane] = (float)exp((double)(chosen_l[lane] - chosen_l[0]));
-    __syncthreads();
-    float total = 0.0f;
-    for (int j = 0; j < k; j++)
-        total += wv[j];
-    if (lane < k)
-        weights[(size_t)t * k + lane] = wv[lane] / total;
+    choose_experts(lg, E, k, sel_l, sel_i, wv, ids + (size_t)t * k, weights + (size_t)t * k);
 }
 
-// mid = GELUTable(gate) * up for one unit per workgroup row, then its Q8_0
-// form (Batch.quantizeBlock): gate_up is [U][ld] with each row's F gates then
-// its F ups, mid_q [U][F].
-__global__ __launch_bounds__(256) void moe_gelu_mul_quant_kernel(const float *__restrict__ gate_up, int ld, int F,
-                                                                  int U, const float *__restrict__ table,
-                                                                  int8_t *__restrict__ q, float *__restrict__ scales,
-                                                                  int32_t *__restrict__ qsum) {
-    const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (gid >= (size_t)U * F)
-        return;  // U*F is a multiple of 32: whole 32-lane groups drop out
-    const int u = (int)(gid / F), i = (int)(gid % F);
-    const float gate = gate_up[(size_t)u * ld + i];
-    const float up = gate_up[(size_t)u * ld + F + i];
-    // GELUTable (nn/gelu_table.go:40-52)
+// mid = GELUTable(gate) * up for the 32 values of one Q8_0 block, one value a
+// lane on lanes 0..31 (all of them active), then the block's Q8_0
+// (Batch.quantizeBlock, nn/batch.go:109-143, as gx_quant.hip's kernel):
+// lane l writes q[l]; lane 0 the scale (through fp16) and the sum of q.
+// GELUTable (nn/gelu_table.go:40-52): 0 at or below -10, the input at or
+// above 10, the table at the input's fp16 bits between.
+__device__ __forceinline__ void gelu_mul_q8_0(float gate, float up, const float *__restrict__ table, int8_t *q,
+                                              float *scale_out, int32_t *qsum_out) {
+    const int l = threadIdx.x & 31;
     float gl;
     if (gate <= -10.0f)
         gl = 0.0f;
@@ -366,17 +428,15 @@ __global__ __launch_bounds__(256) void moe_gelu_mul_quant_kernel(const float *__
     else
         gl = table[float_to_half_bits(gate)];
     const float v = gl * up;
-    // quantizeBlock (nn/batch.go:109-143), as gx_quant.hip's kernel
     float peak = fabsf(v);
 #pragma unroll
     for (int off = 16; off > 0; off >>= 1)
         peak = fmaxf(peak, __shfl_xor(peak, off, 32));
-    const size_t index = (size_t)u * (F >> 5) + (i >> 5);
     if (peak == 0.0f) {
-        q[gid] = 0;
-        if ((i & 31) == 0) {
-            scales[index] = 0.0f;
-            qsum[index] = 0;
+        q[l] = 0;
+        if (l == 0) {
+            *scale_out = 0.0f;
+            *qsum_out = 0;
         }
         return;
     }
@@ -385,14 +445,258 @@ __global__ __launch_bounds__(256) void moe_gelu_mul_quant_kernel(const float *__
     const float prod = v * inverse;
     int32_t n = nearest_int(prod);
     n = n > 127 ? 127 : (n < -128 ? -128 : n);
-    q[gid] = (int8_t)n;
+    q[l] = (int8_t)n;
     int32_t sum = n;
 #pragma unroll
     for (int off = 16; off > 0; off >>= 1)
         sum += __shfl_xor(sum, off, 32);
-    if ((i & 31) == 0) {
-        scales[index] = half_bits_to_float(float_to_half_bits(scale));
-        qsum[index] = sum;
+    if (l == 0) {
+        *scale_out = half_bits_to_float(float_to_half_bits(scale));
+        *qsum_out = sum;
+    }
+}
+
+// mid = GELUTable(gate) * up for one unit per workgroup row, then its Q8_0
+// form: gate_up is [U][ld] with each row's F gates then its F ups, mid_q
+// [U][F].  (The grouped path; few positions fuse this into the product.)
+__global__ __launch_bounds__(256) void moe_gelu_mul_quant_kernel(const float *__restrict__ gate_up, int ld, int F,
+                                                                  int U, const float *__restrict__ table,
+                                                                  int8_t *__restrict__ q, float *__restrict__ scales,
+                                                                  int32_t *__restrict__ qsum) {
+    const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= (size_t)U * F)
+        return;  // U*F is a multiple of 32: whole 32-lane groups drop out
+    const int u = (int)(gid / F), i = (int)(gid % F);
+    const size_t index = (size_t)u * (F >> 5) + (i >> 5);
+    gelu_mul_q8_0(gate_up[(size_t)u * ld + i], gate_up[(size_t)u * ld + F + i], table, q + (gid & ~(size_t)31),
+                  scales + index, qsum + index);
+}
+
+// ---- few positions: the units as matrix-vector products ---------------------
+//
+// Two kernels after the router, each reading its expert matrices once per
+// unit (moe.go:127-163):
+//   moe_gate_up_kernel: unit u = blockIdx.y (position u / k, expert ids[u]).
+//     Its position's input is quantised to Q8_0 by each wavefront for the
+//     stretch it multiplies (q8_0_quad: the separate quantiser's values) and
+//     moved to SGPRs, as in the fused norm products.  A workgroup owns gate
+//     rows 32h .. 32h+31 (lanes 0..31) and the same up rows F + 32h ..
+//     (lanes 32..63), each lane reading its row where the R64 layout keeps it,
+//     so that its 32 results are one Q8_0 block of mid: GELUTable(gate) * up
+//     and the block's Q8_0 are its epilogue.
+//   moe_down_reduce_kernel: position t = blockIdx.y; a workgroup owns 16 rows
+//     (a quarter of an R64 tile) of all k units' down products, and sums them
+//     with the routing weights in slot order -- golem's Axpy (out = 0, out +=
+//     (w_j * DownScale[id_j]) * value_j, a rounded product then a rounded sum)
+//     -- so no partial leaves the workgroup.
+// A unit's row value is the canonical one of every Q4_0 kernel here (block
+// products fma'd within a stretch from +0, stretch sums in order from +0).
+// An id outside [0, E) reads nothing: its unit's value is NaN, and so is its
+// position's output.
+//
+// DOTS: the same kernels writing each (unit, row, block) integer, gate_up
+// into dots[u][row][b] for its 2F rows in golem's order, down into
+// dots[t*k + j][row][b]; they then store no output.
+
+template <bool DOTS>
+__global__ __launch_bounds__(1024) void moe_gate_up_kernel(
+    const uint8_t *__restrict__ W, size_t plane0_bytes, size_t matrix_bytes, int B, int DC, int F, int experts,
+    const float *__restrict__ x, int ldx, int k, const int32_t *__restrict__ ids, const float *__restrict__ table,
+    int8_t *__restrict__ mq, float *__restrict__ ms, int32_t *__restrict__ mqs, int32_t *__restrict__ dots) {
+    extern __shared__ float part[];  // [S][64]
+    const int K = B * kQ4Block, S = (B + kStretch - 1) / kStretch;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nwaves = blockDim.x >> 6;
+    const int h = blockIdx.x, u = blockIdx.y;
+    const int e = ids[u];
+    const size_t mb = (size_t)u * (F / kQ4Block) + h;  // the mid block this workgroup makes
+    if (e < 0 || e >= experts) {
+        if (!DOTS && threadIdx.x < 32) {
+            mq[mb * kQ4Block + threadIdx.x] = 0;
+            if (threadIdx.x == 0) {
+                ms[mb] = __builtin_nanf("");
+                mqs[mb] = 0;
+            }
+        }
+        return;
+    }
+    W += (size_t)e * matrix_bytes;
+    const float *xa = x + (size_t)(u / k) * ldx;
+    const int rowg = lane < 32 ? 32 * h + lane : F + 32 * h + (lane - 32);  // golem's row of this lane
+    const int tile = rowg >> 6, rin = rowg & 63;
+    const uint8_t *qs_row = W + ((size_t)tile * B * kTileRows + rin) * kChunk;
+    const uint8_t *d_row = W + plane0_bytes + ((size_t)tile * DC * kTileRows + rin) * kChunk;
+
+    for (int s = wave; s < S; s += nwaves) {
+        const int b0 = s * kStretch;
+        const int nb = min(kStretch, B - b0);
+        // The stretch's inputs first (values 32 b0 + 4 lane .. + 3; past the
+        // row the last four again, never used), then its weights.
+        float v[4];
+        const int i0 = min(b0 * kQ4Block + 4 * lane, K - 4);
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+            v[c] = xa[i0 + c];
+        uint4 wq[kStretch];
+#pragma unroll
+        for (int j = 0; j < kStretch; j++)
+            wq[j] = load_stream(qs_row + (size_t)min(b0 + j, B - 1) * kTileRows * kChunk);
+        const uint4 dch = *(const uint4 *)(d_row + (size_t)s * kTileRows * kChunk);
+        float bstored;
+        int32_t bsum;
+        const uint32_t aq = q8_0_quad(v, &bstored, &bsum);
+        float p = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kStretch; j++) {
+            if (j < nb) {
+                int4 a0, a1;
+                a0.x = __builtin_amdgcn_readlane((int)aq, 8 * j + 0);
+                a0.y = __builtin_amdgcn_readlane((int)aq, 8 * j + 1);
+                a0.z = __builtin_amdgcn_readlane((int)aq, 8 * j + 2);
+                a0.w = __builtin_amdgcn_readlane((int)aq, 8 * j + 3);
+                a1.x = __builtin_amdgcn_readlane((int)aq, 8 * j + 4);
+                a1.y = __builtin_amdgcn_readlane((int)aq, 8 * j + 5);
+                a1.z = __builtin_amdgcn_readlane((int)aq, 8 * j + 6);
+                a1.w = __builtin_amdgcn_readlane((int)aq, 8 * j + 7);
+                const int32_t qs = __builtin_amdgcn_readlane(bsum, 8 * j);
+                const float sa = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bstored), 8 * j));
+                const int32_t isum = q4_0_block_isum(wq[j], a0, a1, qs);
+                const float scl = chunk_half(dch, j) * sa;
+                p = fmaf((float)isum, scl, p);
+                if (DOTS)
+                    dots[((size_t)u * 2 * F + rowg) * B + b0 + j] = isum;
+            }
+        }
+        part[s * kTileRows + lane] = p;
+    }
+    __syncthreads();
+    if (!DOTS && wave == 0) {
+        float acc = 0.0f;
+        for (int s = 0; s < S; s++)
+            acc = acc + part[s * kTileRows + lane];
+        const float up = __shfl_down(acc, 32, 64);
+        if (lane < 32)
+            gelu_mul_q8_0(acc, up, table, mq + mb * kQ4Block, ms + mb, mqs + mb);
+    }
+}
+
+constexpr int kDownRows = 16;   // rows of a down workgroup
+constexpr int kDownActRegs = 4; // staged 16-byte activation pieces per thread
+
+__host__ __device__ inline size_t down_part_bytes(int pairs) { return ((size_t)pairs * kDownRows * 4 + 15) & ~(size_t)15; }
+
+template <bool DOTS>
+__global__ __launch_bounds__(1024) void moe_down_reduce_kernel(
+    const uint8_t *__restrict__ W, size_t plane0_bytes, size_t matrix_bytes, int B, int DC, int experts,
+    const int8_t *__restrict__ mq, const float *__restrict__ ms, const int32_t *__restrict__ mqs, int k,
+    const int32_t *__restrict__ ids, const float *__restrict__ weights, const float *__restrict__ down_scale,
+    float *__restrict__ out, int ldo, int D, int32_t *__restrict__ dots) {
+    // LDS: the pairs' stretch sums [k*S][16] floats, then the position's k
+    // activations: q [k][F] int8, scales [k][B] float, sums [k][B] int32.
+    extern __shared__ __align__(16) uint8_t lds_raw[];
+    const int F = B * kQ4Block, S = (B + kStretch - 1) / kStretch, P = k * S;
+    float *part = (float *)lds_raw;
+    int8_t *qa = (int8_t *)(lds_raw + down_part_bytes(P));
+    float *sa = (float *)(qa + (size_t)k * F);
+    int32_t *qsa = (int32_t *)(sa + (size_t)k * B);
+    const int tid = threadIdx.x, nt = blockDim.x;
+    const int lane = tid & 63, wave = tid >> 6, nwaves = nt >> 6;
+    const int t = blockIdx.y;
+    const int tile = blockIdx.x >> 2, r = (blockIdx.x & 3) * kDownRows + (lane & 15);
+    const int row = tile * kTileRows + r;
+    const int32_t *idt = ids + (size_t)t * k;
+
+    // The activations: every load in flight together (indices past the end
+    // clamped, the values never stored), then into LDS below.
+    const int n16 = k * F / 16, nb = k * B;
+    const int4 *qsrc = (const int4 *)(mq + (size_t)t * k * F);
+    const float *ssrc = ms + (size_t)t * k * B;
+    const int32_t *qssrc = mqs + (size_t)t * k * B;
+    int4 qv[kDownActRegs];
+    float sv[kDownActRegs];
+    int32_t qsv[kDownActRegs];
+#pragma unroll
+    for (int a = 0; a < kDownActRegs; a++)
+        qv[a] = qsrc[min(tid + a * nt, n16 - 1)];
+#pragma unroll
+    for (int a = 0; a < kDownActRegs; a++) {
+        sv[a] = ssrc[min(tid + a * nt, nb - 1)];
+        qsv[a] = qssrc[min(tid + a * nt, nb - 1)];
+    }
+    // This lane's pair p = j * S + s (slot j, stretch s): pairs wave * 4 +
+    // lane / 16, then nwaves * 4 further on.
+    int p = wave * 4 + (lane >> 4);
+    uint4 wq[kStretch], dch;
+    bool bad = false;
+    auto load_pair = [&](int pp) {
+        const int pc = min(pp, P - 1);
+        const int j = pc / S, s = pc - j * S;
+        const int e = idt[j];
+        bad = e < 0 || e >= experts;
+        const uint8_t *We = W + (size_t)(bad ? 0 : e) * matrix_bytes;
+        const uint8_t *qs_row = We + ((size_t)tile * B * kTileRows + r) * kChunk;
+        const uint8_t *d_row = We + plane0_bytes + ((size_t)tile * DC * kTileRows + r) * kChunk;
+#pragma unroll
+        for (int jj = 0; jj < kStretch; jj++)
+            wq[jj] = load_stream(qs_row + (size_t)min(s * kStretch + jj, B - 1) * kTileRows * kChunk);
+        dch = *(const uint4 *)(d_row + (size_t)s * kTileRows * kChunk);
+    };
+    load_pair(p);
+#pragma unroll
+    for (int a = 0; a < kDownActRegs; a++) {
+        const int i = tid + a * nt;
+        if (i < n16)
+            ((int4 *)qa)[i] = qv[a];
+        if (i < nb) {
+            sa[i] = sv[a];
+            qsa[i] = qsv[a];
+        }
+    }
+    lds_barrier();
+
+    for (int base = wave * 4;;) {
+        if (p < P) {
+            const int j = p / S, s = p - j * S;
+            const int b0 = s * kStretch;
+            const int n = min(kStretch, B - b0);
+            const int8_t *aj = qa + (size_t)j * F;
+            float acc = 0.0f;
+#pragma unroll
+            for (int jj = 0; jj < kStretch; jj++) {
+                if (jj < n) {
+                    const int b = b0 + jj;
+                    const int4 *ap = (const int4 *)(aj + (size_t)b * kQ4Block);
+                    const int32_t isum = q4_0_block_isum(wq[jj], ap[0], ap[1], qsa[j * B + b]);
+                    const float scl = chunk_half(dch, jj) * sa[j * B + b];
+                    acc = fmaf((float)isum, scl, acc);
+                    if (DOTS && !bad)
+                        dots[(((size_t)t * k + j) * D + row) * B + b] = isum;
+                }
+            }
+            part[p * kDownRows + (lane & 15)] = bad ? __builtin_nanf("") : acc;
+        }
+        base += nwaves * 4;
+        if (base >= P)
+            break;
+        p += nwaves * 4;
+        load_pair(p);
+    }
+    lds_barrier();
+
+    if (!DOTS && wave == 0 && lane < kDownRows) {
+        float o = 0.0f;
+        for (int j = 0; j < k; j++) {
+            float v = 0.0f;
+            for (int s = 0; s < S; s++)
+                v = v + part[(j * S + s) * kDownRows + lane];
+            const int e = idt[j];
+            const float ds = !down_scale ? 1.0f : (e >= 0 && e < experts) ? down_scale[e] : __builtin_nanf("");
+            const float a = weights[(size_t)t * k + j] * ds;
+            const float pr = a * v;
+            o = o + pr;
+        }
+        out[(size_t)t * ldo + row] = o;
     }
 }
 
@@ -440,7 +744,7 @@ __global__ __launch_bounds__(kJoinThreads) void moe_join_kernel(float *__restric
 // The expert sum: out[t][i] = 0, then out += (w_k * DownScale[id_k]) *
 // partial_k for k in slot order, each step a rounded product then a rounded
 // sum (golem's generic Axpy).
-__global__ void moe_reduce_kernel(const float *__restrict__ partial, int D, int M, int k,
+__global__ void moe_reduce_kernel(const float *__restrict__ partial, int D, int M, int k, int E,
                                   const int32_t *__restrict__ ids, const float *__restrict__ weights,
                                   const float *__restrict__ down_scale, float *__restrict__ out, int ldo) {
     const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -450,7 +754,9 @@ __global__ void moe_reduce_kernel(const float *__restrict__ partial, int D, int 
     float acc = 0.0f;
     for (int j = 0; j < k; j++) {
         const int u = t * k + j;
-        const float a = weights[u] * (down_scale ? down_scale[ids[u]] : 1.0f);
+        const int e = ids[u];
+        const float ds = !down_scale ? 1.0f : (e >= 0 && e < E) ? down_scale[e] : __builtin_nanf("");
+        const float a = weights[u] * ds;
         const float p = a * partial[(size_t)u * D + i];
         acc = acc + p;
     }
@@ -602,21 +908,48 @@ int launch_moe_route(gx_ctx *ctx, const gx_weight *router, const float *router_s
     GX_CHECK(k <= kTopkMax, "gx: top_k %d exceeds %d", k, kTopkMax);
     GX_CHECK(((uintptr_t)resid & 15) == 0 && ldr % 4 == 0, "gx: resid must be 16-byte aligned with ldr %% 4 == 0");
     const float *rw = (const float *)router->dev;
-    if (M <= 4 && D <= kLogitsOneMaxD) {
-        const size_t lds = 2 * sizeof(float) * (size_t)D;
-        moe_logits_one_kernel<<<dim3((unsigned)E, (unsigned)M), kLogitsThreads, lds, ctx->stream>>>(
-            rw, D, E, router_scale, resid, ldr, eps, logits);
-    } else {
-        constexpr int EW = 4, P = 64 / EW;
-        const dim3 grid((unsigned)((E + EW - 1) / EW), (unsigned)((M + P - 1) / P));
-        moe_logits_kernel<EW><<<grid, kLogitsThreads, 0, ctx->stream>>>(rw, D, E, router_scale, resid, ldr, M, eps,
-                                                                         logits);
+    if (M <= kRouteMaxPos && D <= kLogitsOneMaxD) {
+        const size_t lds = sizeof(float) * ((size_t)max(D, (E + 3) & ~3) + 4 * ((size_t)D / 4 + 4));
+        moe_route_one_kernel<<<dim3((unsigned)E, (unsigned)M), kLogitsThreads, lds, ctx->stream>>>(
+            rw, D, E, router_scale, resid, ldr, eps, k, logits, ids, weights, ctx->route_count);
+        return check_launch("moe_route_one");
     }
+    constexpr int EW = 4, P = 64 / EW;
+    const dim3 grid((unsigned)((E + EW - 1) / EW), (unsigned)((M + P - 1) / P));
+    moe_logits_kernel<EW><<<grid, kLogitsThreads, 0, ctx->stream>>>(rw, D, E, router_scale, resid, ldr, M, eps,
+                                                                     logits);
     if (int rc = check_launch("moe_logits"))
         return rc;
-    moe_topk_kernel<<<M, 64, 0, ctx->stream>>>(logits, E, k, ids, weights);
+    moe_topk_kernel<<<M, E <= 64 ? 64 : E <= 128 ? 128 : 256, 0, ctx->stream>>>(logits, E, k, ids, weights);
     return check_launch("moe_topk");
 }
+
+namespace {
+
+// The few-position kernels' launch shapes (gate_up: one stretch a wavefront
+// or more; down: four pairs a wavefront, at most 16 wavefronts).
+struct UnitShape {
+    int gu_waves, dn_waves;
+    size_t gu_lds, dn_lds;
+};
+
+int unit_shape(const gx_weight *gate_up, const gx_weight *down, int k, UnitShape *sh) {
+    const int Sg = (gate_up->blocks + kStretch - 1) / kStretch;
+    sh->gu_waves = min(Sg, 16);
+    sh->gu_lds = (size_t)Sg * kTileRows * sizeof(float);
+    const int B = down->blocks, F = down->cols, Sd = (B + kStretch - 1) / kStretch, pairs = k * Sd;
+    sh->dn_waves = min((pairs + 3) / 4, 16);
+    const int nt = 64 * sh->dn_waves;
+    sh->dn_lds = down_part_bytes(pairs) + (size_t)k * F + (size_t)k * B * 8;
+    GX_CHECK(sh->gu_lds <= 64 * 1024, "gx: a %d-input expert row is wider than the gate_up kernel's LDS",
+             gate_up->cols);
+    GX_CHECK(sh->dn_lds <= 64 * 1024 && k * F / 16 <= kDownActRegs * nt && k * B <= kDownActRegs * nt,
+             "gx: %d units of %d-input down rows do not fit the down kernel", k, F);
+    GX_CHECK(down->rows % kDownRows == 0, "gx: %d down rows are not a multiple of %d", down->rows, kDownRows);
+    return GX_OK;
+}
+
+}  // namespace
 
 int launch_moe_experts(gx_ctx *ctx, const gx_weight *gate_up, const gx_weight *down, const float *down_scale,
                        const float *x, int ldx, int M, int k, const int32_t *ids, const float *weights, float *out,
@@ -624,55 +957,88 @@ int launch_moe_experts(gx_ctx *ctx, const gx_weight *gate_up, const gx_weight *d
     const int D = gate_up->cols, F = down->cols, E = gate_up->count;
     const MoeSpace s = moe_space(M, k, D, F, E);
     const int U = s.units;
+    int8_t *mq = (int8_t *)(ws + s.mq);
+    float *ms = (float *)(ws + s.ms);
+    int32_t *mqs = (int32_t *)(ws + s.mqs);
+
+    if (M <= kUnitMaxPos) {
+        // Few positions: two kernels, each unit a matrix-vector product.
+        UnitShape sh;
+        if (int rc = unit_shape(gate_up, down, k, &sh))
+            return rc;
+        moe_gate_up_kernel<false><<<dim3((unsigned)(F / kQ4Block), (unsigned)U), 64 * sh.gu_waves, sh.gu_lds,
+                                    ctx->stream>>>(gate_up->dev, gate_up->plane0_bytes, gate_up->matrix_bytes,
+                                                   gate_up->blocks, gate_up->dchunks, F, E, x, ldx, k, ids, gelu_table,
+                                                   mq, ms, mqs, nullptr);
+        if (int rc = check_launch("moe_gate_up"))
+            return rc;
+        moe_down_reduce_kernel<false><<<dim3((unsigned)(D / kDownRows), (unsigned)M), 64 * sh.dn_waves, sh.dn_lds,
+                                        ctx->stream>>>(down->dev, down->plane0_bytes, down->matrix_bytes,
+                                                       down->blocks, down->dchunks, E, mq, ms, mqs, k, ids, weights,
+                                                       down_scale, out, ldo, D, nullptr);
+        return check_launch("moe_down_reduce");
+    }
+
     int8_t *xq = (int8_t *)(ws + s.xq);
     float *xs = (float *)(ws + s.xs);
     int32_t *xqs = (int32_t *)(ws + s.xqs);
     float *gu = (float *)(ws + s.gu);
-    int8_t *mq = (int8_t *)(ws + s.mq);
-    float *ms = (float *)(ws + s.ms);
-    int32_t *mqs = (int32_t *)(ws + s.mqs);
     float *part = (float *)(ws + s.part);
     int32_t *sorted = (int32_t *)(ws + s.sorted);
     int32_t *work = (int32_t *)(ws + s.work);
-
     // Each position's input, quantised once for its k units (moe.go:119-125).
     if (int rc = launch_quantize_q8_0(ctx, x, ldx, M, D, xq, xs, xqs, nullptr, nullptr))
         return rc;
-    const bool grouped = M > 4;
-    if (grouped) {
-        // A unit whose expert id is out of range is in no group: its sums
-        // stay NaN, and so does its position's output.
-        const size_t n = (size_t)U * 2 * F;
-        fill_nan_kernel<<<(unsigned)((n + 255) / 256), 256, 0, ctx->stream>>>(gu, n);
-        const size_t np = (size_t)U * D;
-        fill_nan_kernel<<<(unsigned)((np + 255) / 256), 256, 0, ctx->stream>>>(part, np);
-        const size_t lds = (size_t)(3 * E + kSortThreads) * sizeof(int32_t);
-        GX_CHECK(lds <= 64 * 1024, "gx: %d experts do not fit the sort's LDS", E);
-        moe_sort_kernel<<<1, kSortThreads, lds, ctx->stream>>>(ids, U, E, 128, s.max_items, sorted, work);
-        if (int rc = check_launch("moe_sort"))
-            return rc;
-        if (int rc = launch_q4_0_gemm_grouped(ctx, gate_up, work, s.max_items, sorted, k, xq, xs, gu, 2 * F))
-            return rc;
-    } else {
-        if (int rc = launch_q4_0_matvec_units(ctx, gate_up, ids, U, k, xq, xs, xqs, gu, 2 * F, nullptr))
-            return rc;
-    }
-    const size_t n = (size_t)U * F;
-    moe_gelu_mul_quant_kernel<<<(unsigned)((n + 255) / 256), 256, 0, ctx->stream>>>(gu, 2 * F, F, U, gelu_table,
-                                                                                    mq, ms, mqs);
+    // A unit whose expert id is out of range is in no group: its sums stay
+    // NaN, and so does its position's output.
+    const size_t n = (size_t)U * 2 * F;
+    fill_nan_kernel<<<(unsigned)((n + 255) / 256), 256, 0, ctx->stream>>>(gu, n);
+    const size_t np = (size_t)U * D;
+    fill_nan_kernel<<<(unsigned)((np + 255) / 256), 256, 0, ctx->stream>>>(part, np);
+    const size_t lds = (size_t)(3 * E + kSortThreads) * sizeof(int32_t);
+    GX_CHECK(lds <= 64 * 1024, "gx: %d experts do not fit the sort's LDS", E);
+    moe_sort_kernel<<<1, kSortThreads, lds, ctx->stream>>>(ids, U, E, 128, s.max_items, sorted, work);
+    if (int rc = check_launch("moe_sort"))
+        return rc;
+    if (int rc = launch_q4_0_gemm_grouped(ctx, gate_up, work, s.max_items, sorted, k, xq, xs, gu, 2 * F))
+        return rc;
+    const size_t nm = (size_t)U * F;
+    moe_gelu_mul_quant_kernel<<<(unsigned)((nm + 255) / 256), 256, 0, ctx->stream>>>(gu, 2 * F, F, U, gelu_table,
+                                                                                     mq, ms, mqs);
     if (int rc = check_launch("moe_gelu_mul_quant"))
         return rc;
-    if (grouped) {
-        if (int rc = launch_q4_0_gemm_grouped(ctx, down, work, s.max_items, sorted, 1, mq, ms, part, D))
-            return rc;
-    } else {
-        if (int rc = launch_q4_0_matvec_units(ctx, down, ids, U, 1, mq, ms, mqs, part, D, nullptr))
-            return rc;
-    }
+    if (int rc = launch_q4_0_gemm_grouped(ctx, down, work, s.max_items, sorted, 1, mq, ms, part, D))
+        return rc;
     const size_t no = (size_t)M * D;
-    moe_reduce_kernel<<<(unsigned)((no + 255) / 256), 256, 0, ctx->stream>>>(part, D, M, k, ids, weights,
+    moe_reduce_kernel<<<(unsigned)((no + 255) / 256), 256, 0, ctx->stream>>>(part, D, M, k, E, ids, weights,
                                                                              down_scale, out, ldo);
     return check_launch("moe_reduce");
+}
+
+int launch_moe_unit_dots(gx_ctx *ctx, const gx_weight *gate_up, const gx_weight *down, const float *x, int ldx,
+                         int M, int k, const int32_t *ids, const int8_t *mid_q, const float *mid_scales,
+                         const int32_t *mid_qsum, int32_t *dots_gate_up, int32_t *dots_down) {
+    const int D = gate_up->cols, F = down->cols, E = gate_up->count;
+    UnitShape sh;
+    if (int rc = unit_shape(gate_up, down, k, &sh))
+        return rc;
+    if (dots_gate_up) {
+        moe_gate_up_kernel<true><<<dim3((unsigned)(F / kQ4Block), (unsigned)(M * k)), 64 * sh.gu_waves, sh.gu_lds,
+                                   ctx->stream>>>(gate_up->dev, gate_up->plane0_bytes, gate_up->matrix_bytes,
+                                                  gate_up->blocks, gate_up->dchunks, F, E, x, ldx, k, ids,
+                                                  ctx->gelu_table, nullptr, nullptr, nullptr, dots_gate_up);
+        if (int rc = check_launch("moe_gate_up dots"))
+            return rc;
+    }
+    if (dots_down) {
+        moe_down_reduce_kernel<true><<<dim3((unsigned)(D / kDownRows), (unsigned)M), 64 * sh.dn_waves, sh.dn_lds,
+                                       ctx->stream>>>(down->dev, down->plane0_bytes, down->matrix_bytes, down->blocks,
+                                                      down->dchunks, E, mid_q, mid_scales, mid_qsum, k, ids, nullptr,
+                                                      nullptr, nullptr, 0, D, dots_down);
+        if (int rc = check_launch("moe_down_reduce dots"))
+            return rc;
+    }
+    return GX_OK;
 }
 
 }  // namespace gx

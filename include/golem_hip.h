@@ -205,6 +205,19 @@ int gx_q4_0_fused_block_dots(gx_ctx *ctx, const gx_weight *w, int swiglu, const 
                              const float *gain, float eps, int row_start, int row_end, int8_t *q, float *scales,
                              int32_t *qsum, int32_t *out);
 
+/* The per-block integers of the few-position expert kernels (gx_moe_experts
+ * at M <= 4), from those kernels with their integer output switched on:
+ * dots_gate_up [M*top_k][2*ffn][dim/32] receives, for unit u (position
+ * u / top_k, expert ids[u]), each gate|up row's block sums against Q8_0(x[u /
+ * top_k]) as the kernel quantises it; dots_down [M*top_k][dim][ffn/32] each
+ * down row's block sums against the unit's Q8_0 input given in mid_q
+ * [M*top_k][ffn], mid_scales and mid_qsum [M*top_k][ffn/32].  Either output
+ * may be NULL (then its inputs may be too).  A unit whose id is out of range
+ * writes nothing.  No counterpart in golem: parity instrumentation. */
+int gx_moe_unit_dots(gx_ctx *ctx, const gx_weight *gate_up, const gx_weight *down, const float *x, int ldx, int M,
+                     int top_k, const int32_t *ids, const int8_t *mid_q, const float *mid_scales,
+                     const int32_t *mid_qsum, int32_t *dots_gate_up, int32_t *dots_down);
+
 /* dotQ6_KGo's per-superblock integer sum - 32*shift (nn/dot_q6_k.go:31-51)
  * for every (m, r, superblock): out[m][r - row_start][K/256]. */
 int gx_q6_k_block_dots(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const int16_t *bsums, int M,
@@ -226,7 +239,10 @@ int gx_moe_workspace_bytes(int M, int top_k, int dim, int ffn, int experts, size
  * RMSNormPlain without a gain (eps), scaled by (1/sqrt(dim)) *
  * router_scale[i] (router_scale may be NULL: ones), and multiplied by the F32
  * router (experts x dim) in DotF32's generic order.  Outputs (device):
- * logits [M][experts], ids [M][top_k], weights [M][top_k]. */
+ * logits [M][experts], ids [M][top_k], weights [M][top_k].  For M <= 4 this
+ * is one kernel launch, whose last workgroup per position chooses the
+ * experts; it keeps a counter per position in the context, so calls on one
+ * context are ordered on its stream (as all calls on a context are). */
 int gx_moe_route(gx_ctx *ctx, const gx_weight *router, const float *router_scale, const float *resid, int ldr, int M,
                  int top_k, float eps, float *logits, int32_t *ids, float *weights);
 
@@ -236,8 +252,10 @@ int gx_moe_route(gx_ctx *ctx, const gx_weight *router, const float *router_scale
  * tensor of gemma/README.md:276-278) and down (dim x ffn) computes
  * Down[e] . Q8_0(GELUTable(gate) * up) with gate|up = GateUp[e] . Q8_0(x[m]);
  * out[m] = sum_k (weights[m][k] * down_scale[e]) * that (down_scale may be
- * NULL: ones).  Few positions run each unit as a matrix-vector product; more
- * are sorted by expert and run as ragged MFMA batches, one per expert.  The
+ * NULL: ones).  Few positions (M <= 4) run as two kernels: gate|up with
+ * the input's Q8_0, GELU * up and the mid's Q8_0 fused, then down with the
+ * weighted sum fused.  More are sorted by expert and run as ragged MFMA
+ * batches, one per expert.  The
  * workspace (device, 256-byte aligned, gx_moe_workspace_bytes) is the
  * scratch golem keeps in its Scratch; no call allocates.  An id out of range
  * makes its position's output NaN. */

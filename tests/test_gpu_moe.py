@@ -251,3 +251,115 @@ def test_bad_expert_id_poisons_its_position(dev):
         out = dev.get(moe.experts(x, dev.put(ids), dev.put(w)))
         assert np.all(np.isnan(out[0]))
         assert not np.any(np.isnan(out[1:]))
+
+
+def test_unit_integers_bit_exact(dev, orc):
+    """The few-position expert kernels' per-block integers (gx_moe_unit_dots)
+    at config 4's shape, every unit of two positions: gate|up against the
+    Q8_0 of its position's input as the kernel quantises it, down against a
+    given Q8_0 input, each equal to golem's accumulator less 8 * sum(q)
+    (nn/dot_q4_0.go:58-63)."""
+    from oracle import Batch
+    D, F, E, k = 2816, 704, 128, 8
+    moe = Moe(dev, D, F, E, k, 4)
+    M = 2
+    x = synth.activations(moe.g, M, D)
+    ids = np.stack([moe.g.choice(E, k, replace=False) for _ in range(M)]).astype(np.int32)
+    mid = synth.activations(moe.g, M * k, F)
+    mb = Batch(mid).quantize()
+    dgu = dev.empty((M * k, 2 * F, D // 32), np.int32)
+    ddn = dev.empty((M * k, D, F // 32), np.int32)
+    mq, ms, mqs = dev.put(mb.q_rows()), dev.put(mb.scales_rows()), dev.put(mb.qsum_rows())
+    xd, idd = dev.put(x), dev.put(ids)  # held until the kernels have read them
+    capi.call("gx_moe_unit_dots", dev.ctx.ptr, moe.wgu.ptr, moe.wdn.ptr, capi.vp(xd), D, M, k,
+              capi.vp(idd), capi.vp(mq), capi.vp(ms), capi.vp(mqs), capi.vp(dgu), capi.vp(ddn))
+    dgu, ddn = dev.get(dgu), dev.get(ddn)
+    for u in range(M * k):
+        t, e = u // k, int(ids[u // k, u % k])
+        xb = Batch(x[t:t + 1]).quantize()
+        acc = orc.q4_0_block_acc(moe.expert_bytes(moe.gate_up, 2 * F, D, e), xb, 2 * F)[0]
+        np.testing.assert_array_equal(dgu[u], acc - 8 * xb.qsum_rows()[0][None, :], err_msg=f"gate_up unit {u}")
+        ub = Batch(mid[u:u + 1]).quantize()
+        acc = orc.q4_0_block_acc(moe.expert_bytes(moe.down, D, F, e), ub, D)[0]
+        np.testing.assert_array_equal(ddn[u], acc - 8 * ub.qsum_rows()[0][None, :], err_msg=f"down unit {u}")
+
+
+def test_route_one_launch_repeats(dev, orc):
+    """The one-launch router (at most four positions) counts each position's
+    logits in the context and the last workgroup chooses; the counter wraps
+    to zero for the next call.  Consecutive calls of 1..4 positions, each
+    bit for bit against the oracle."""
+    D, E, k = 2816, 128, 8
+    m = Moe.__new__(Moe)
+    g = synth.rng(77)
+    m.D, m.E, m.k, m.dev = D, E, k, dev
+    m.router = (g.standard_normal((E, D)) * 0.02).astype(np.float32)
+    m.wr = dev.weight(m.router, capi.F32, E, D)
+    for M in (1, 4, 2, 3, 1, 1, 4):
+        x = synth.activations(g, M, D)
+        logits, ids, w = m.route(x)
+        logits, ids, w = dev.get(logits), dev.get(ids), dev.get(w)
+        for t in range(M):
+            ol, oi, ow = orc.route_one(x[t], m.router, k)
+            np.testing.assert_array_equal(logits[t].view(np.uint32), ol.view(np.uint32))
+            np.testing.assert_array_equal(ids[t], oi)
+            np.testing.assert_allclose(w[t], ow, rtol=1e-6, atol=0)
+
+
+def test_decode_graph_replays_match_eager(dev, orc):
+    """Config 4's decode (route + experts, three launches) captured once into
+    a HIP graph and replayed on new inputs, with eager work and
+    synchronisations between the replays: every replay's output bit-identical
+    to the eager call's, which is within 2e-5 of RMS of golem."""
+    import ctypes
+    import torch
+    D, F, E, k = 2816, 704, 128, 8
+    moe = Moe(dev, D, F, E, k, 4)
+    n = ctypes.c_size_t()
+    capi.call("gx_moe_workspace_bytes", 1, k, D, F, E, ctypes.byref(n))
+    ws = dev.empty((n.value,), np.uint8)
+    xs = dev.empty((1, D), np.float32)
+    logits = dev.empty((1, E), np.float32)
+    ids = dev.empty((1, k), np.int32)
+    w = dev.empty((1, k), np.float32)
+    out = dev.empty((1, D), np.float32)
+
+    def step():
+        capi.call("gx_moe_route", dev.ctx.ptr, moe.wr.ptr, None, capi.vp(xs), D, 1, k, np.float32(1e-6),
+                  capi.vp(logits), capi.vp(ids), capi.vp(w))
+        capi.call("gx_moe_experts", dev.ctx.ptr, moe.wgu.ptr, moe.wdn.ptr, None, capi.vp(xs), D, 1, k,
+                  capi.vp(ids), capi.vp(w), capi.vp(out), D, capi.vp(ws), n.value)
+
+    inputs = [synth.activations(moe.g, 1, D) for _ in range(4)]
+    eager = []
+    for x in inputs:
+        xs.copy_(dev.put(x))
+        step()
+        eager.append((dev.get(ids).copy(), dev.get(out).copy()))
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    capi.call("gx_set_stream", dev.ctx.ptr, ctypes.c_void_p(stream.cuda_stream))
+    try:
+        with torch.cuda.graph(graph, stream=stream):
+            step()
+    finally:
+        capi.call("gx_set_stream", dev.ctx.ptr, None)
+    torch.cuda.synchronize()
+    for rep in range(2):
+        for i, x in enumerate(inputs):
+            xs.copy_(dev.put(x))
+            graph.replay()
+            torch.cuda.synchronize()
+            np.testing.assert_array_equal(dev.get(ids), eager[i][0])
+            np.testing.assert_array_equal(dev.get(out).view(np.uint32), eager[i][1].view(np.uint32))
+            # eager work between replays
+            step()
+            torch.cuda.synchronize()
+            np.testing.assert_array_equal(dev.get(out).view(np.uint32), eager[i][1].view(np.uint32))
+    ol, oi, ow = orc.route_one(inputs[0][0], moe.router, k)
+    np.testing.assert_array_equal(eager[0][0][0], oi)
+    want = moe.oracle(orc, inputs[0], oi[None, :], ow[None, :])
+    rel, at = orc.compare_floats(eager[0][1][0], want[0])
+    assert rel <= TOL, f"{rel:.3g} of RMS at {at}"
+    del graph
