@@ -21,20 +21,6 @@
 namespace gx {
 namespace {
 
-// golem's GELU table (nn/gelu_table.go:25-38): for every fp16 input,
-// fp16(float32(geluTanh(float64(input)))), held as float.
-__global__ void gelu_table_kernel(float *__restrict__ table) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= 65536)
-        return;
-    const double x = (double)half_bits_to_float((uint32_t)i);
-    const double sqrt2_over_pi = 0.79788456080286535587989211986876;
-    const double coef_a = 0.044715;
-    const double inner = sqrt2_over_pi * x * (1.0 + coef_a * x * x);
-    const double g = 0.5 * x * (1.0 + tanh(inner));
-    table[i] = half_bits_to_float(float_to_half_bits((float)g));
-}
-
 // The router.
 //
 // Logits: DotF32 (nn/dot_f32.go:13-33) is four serial chains -- chain c adds
@@ -69,39 +55,74 @@ constexpr int kTopkMaxPerLane = 16;  // E <= 1024
 constexpr int kTopkMax = 64;         // k <= 64
 constexpr int kUnitMaxPos = 4;       // positions whose units run as matrix-vector products
 
-// chooseExperts (gemma/moe.go:62-88) for one position whose E logits sit in
-// LDS (lg, padded with -inf to a multiple of 4), by a whole workgroup of at
-// least 64 threads.  golem takes k rounds of an argmax that scans in index
-// order and replaces its best only on a strictly greater logit.  Without a
-// NaN the rounds take the logits by value, largest first and equal values
-// lower index first, so logit i is taken in round
+// chooseExperts (gemma/moe.go:62-88) for one position, by a whole workgroup
+// of at least 64 threads.  golem takes k rounds of an argmax that scans in
+// index order and replaces its best only on a strictly greater logit.
+// Without a NaN the rounds take the logits by value, largest first and
+// equal values lower index first, so logit i is taken in round
 //     r = #{j : l_j > l_i} + #{j < i : l_j == l_i},
-// which each thread computes for its logits at once (a -inf pad is never
-// greater than a logit, and never equal at a lower index).  A NaN is taken
-// only as the first logit not yet chosen (no comparison with it is ever
-// true); with any NaN present wavefront 0 runs the rounds as golem does.
-// Weights: exp(l - top) in float64 of the float32 difference, rounded to
-// float32, summed in slot order, divided by the sum.
-__device__ void choose_experts(const float *lg, int E, int k, float *sel_l, int32_t *sel_i, float *wv,
-                               int32_t *__restrict__ ids, float *__restrict__ weights) {
-    const int tid = threadIdx.x, nt = blockDim.x;
+// which every thread computes for its logit at once, one unsigned compare a
+// logit, on keys that order (value, -index) as one 64-bit integer
+// (rank_key).  A NaN is taken only as the first logit not yet chosen (no
+// comparison with it is ever true); with any NaN present wavefront 0 runs
+// the rounds as golem does.  Weights: exp(l - top) in float64 of the float32
+// difference, rounded to float32, summed in slot order, divided by the sum.
+//
+// The caller stages the logits in LDS first (stage_logits): lg holds them
+// as floats and comp their keys, both padded to a multiple of 32 (keys 0,
+// below every logit's), and any_nan says whether one is a NaN.
+
+// The order of a non-NaN float as an unsigned integer (-0 taken as +0, as
+// golem's comparisons take it), above it the index reversed: a larger key
+// is a larger logit, or an equal one at a lower index.
+__device__ __forceinline__ uint64_t rank_key(float v, int i) {
+    const uint32_t u = __float_as_uint(v == 0.0f ? 0.0f : v);
+    const uint32_t key = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((uint64_t)key << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)i);
+}
+
+// Logits [0, E) from `src` (read by `load`) into lg and comp; returns, in
+// every thread, whether any is a NaN (the barrier that publishes them).
+template <typename Load>
+__device__ __forceinline__ bool stage_logits(int E, float *lg, uint64_t *comp, Load &&load) {
+    const int E32 = (E + 31) & ~31;
     bool nan_here = false;
-    for (int i = tid; i < E; i += nt)
-        nan_here |= lg[i] != lg[i];
-    if (!__syncthreads_or(nan_here)) {
-        const int E4 = (E + 3) & ~3;
-        for (int i = tid; i < E; i += nt) {
-            const float v = lg[i];
+    for (int i = threadIdx.x; i < E32; i += blockDim.x) {
+        const float v = i < E ? load(i) : -__builtin_inff();
+        lg[i] = v;
+        comp[i] = i < E ? rank_key(v, i) : 0;
+        nan_here |= v != v;
+    }
+    return __syncthreads_or(nan_here);
+}
+
+__device__ void choose_experts(const float *lg, const uint64_t *comp, bool any_nan, int E, int k, float *sel_l,
+                               int32_t *sel_i, float *wv, int32_t *__restrict__ ids, float *__restrict__ weights) {
+    const int tid = threadIdx.x, nt = blockDim.x;
+    if (!any_nan) {
+        // Two threads a logit when the workgroup has them (adjacent lanes,
+        // each half of the keys), their counts added by a lane swap.
+        const int E32 = (E + 31) & ~31;
+        const int split = nt >= 2 * E32 ? 2 : 1;
+        const int span = E32 / split, per = nt / split;
+        for (int i0 = 0; i0 < E; i0 += per) {  // the same trip count in every thread
+            const int i = i0 + tid / split, h = tid % split;
+            const uint64_t c = comp[min(i, E - 1)];
+            const uint64_t *cj = comp + h * span;
             int r = 0;
-            for (int j = 0; j < E4; j += 4) {
-                const float4 w = *(const float4 *)(lg + j);
-                r += (int)((w.x > v) | ((w.x == v) & (j + 0 < i)));
-                r += (int)((w.y > v) | ((w.y == v) & (j + 1 < i)));
-                r += (int)((w.z > v) | ((w.z == v) & (j + 2 < i)));
-                r += (int)((w.w > v) | ((w.w == v) & (j + 3 < i)));
+            for (int j = 0; j < span; j += 16) {
+                uint64_t w[16];  // 16 keys in flight at once
+#pragma unroll
+                for (int u = 0; u < 16; u++)
+                    w[u] = cj[j + u];
+#pragma unroll
+                for (int u = 0; u < 16; u++)
+                    r += (int)(w[u] > c);
             }
-            if (r < k) {
-                sel_l[r] = v;
+            if (split == 2)
+                r += __shfl_xor(r, 1, 64);
+            if (i < E && h == 0 && r < k) {
+                sel_l[r] = lg[i];
                 sel_i[r] = i;
             }
         }
@@ -175,17 +196,20 @@ __global__ __launch_bounds__(kLogitsThreads) void moe_route_one_kernel(
     const float *__restrict__ router, int D, int E, const float *__restrict__ router_scale,
     const float *__restrict__ resid, int ldr, float eps, int k, float *__restrict__ logits,
     int32_t *__restrict__ ids, float *__restrict__ weights, unsigned *__restrict__ count) {
-    extern __shared__ __align__(16) float lds[];  // the input [max(D, E4)], then the products [4][D/4 + 4]
+    // LDS: the input [max(D, E32)], then the chains' products [4][cs] (later
+    // the logits' keys [E32] as uint64)
+    extern __shared__ __align__(16) float lds[];
     __shared__ double red[kLogitsThreads];
     __shared__ float scale_sh;
     __shared__ int last_sh;
     __shared__ float sel_l[kTopkMax], wv[kTopkMax];
     __shared__ int32_t sel_i[kTopkMax];
     const int tid = threadIdx.x, e = blockIdx.x, t = blockIdx.y;
-    const int E4 = (E + 3) & ~3;
+    const int E32 = (E + 31) & ~31;
     float *xr = lds;
-    float *P = lds + max(D, E4);
-    const int cs = D / 4 + 4;  // a chain's stride: the four chains start in different banks
+    float *P = lds + max(D, E32);
+    const int cn = (D / 16 + 7) & ~7;  // float4s of a chain, padded to a multiple of 8
+    const int cs = 4 * cn + 4;         // a chain's stride in floats: the four chains start in different banks
     const float *rg = router + (size_t)e * D;
     const float *xg = resid + (size_t)t * ldr;
     const int n4 = D / 4;
@@ -229,56 +253,86 @@ __global__ __launch_bounds__(kLogitsThreads) void moe_route_one_kernel(
                 const float xn = normed * factor;
                 P[c * cs + q] = r4[c] * xn;
             }
+        } else if (q < 4 * cn) {
+#pragma unroll
+            for (int c = 0; c < 4; c++)
+                P[c * cs + q] = 0.0f;
         }
     }
     __syncthreads();
     if (tid < 64) {
         float acc = 0.0f;
         if (tid < 4) {
-            // chain tid: its products in order, 16 at a time, the next 16
-            // read while these are added
+            // Chain tid: its products in order, 32 at a time from two
+            // buffers, each refilled while the other is added (a copy from
+            // one to the other would wait for the refill), so the LDS
+            // latency stays behind the dependent adds.  The chain is padded
+            // with +0 products to a multiple of 32, which leave a sum that
+            // starts from +0 unchanged.
             const float4 *pc = (const float4 *)(P + tid * cs);
-            const int n = D / 16;  // float4s per chain, a multiple of 4
-            float4 cur[4], nxt[4];
+            float4 A[8], Bq[8];
 #pragma unroll
-            for (int u = 0; u < 4; u++)
-                cur[u] = pc[u];
-            for (int j = 0; j < n; j += 4) {
-                if (j + 4 < n) {
+            for (int u = 0; u < 8; u++)
+                A[u] = pc[u];
+            for (int j = 0;; j += 16) {
+                const bool more = j + 8 < cn;
+                if (more) {
 #pragma unroll
-                    for (int u = 0; u < 4; u++)
-                        nxt[u] = pc[j + 4 + u];
+                    for (int u = 0; u < 8; u++)
+                        Bq[u] = pc[j + 8 + u];
                 }
 #pragma unroll
-                for (int u = 0; u < 4; u++) {
-                    acc = acc + cur[u].x;
-                    acc = acc + cur[u].y;
-                    acc = acc + cur[u].z;
-                    acc = acc + cur[u].w;
+                for (int u = 0; u < 8; u++) {
+                    acc = acc + A[u].x;
+                    acc = acc + A[u].y;
+                    acc = acc + A[u].z;
+                    acc = acc + A[u].w;
+                }
+                if (!more)
+                    break;
+                const bool more2 = j + 16 < cn;
+                if (more2) {
+#pragma unroll
+                    for (int u = 0; u < 8; u++)
+                        A[u] = pc[j + 16 + u];
                 }
 #pragma unroll
-                for (int u = 0; u < 4; u++)
-                    cur[u] = nxt[u];
+                for (int u = 0; u < 8; u++) {
+                    acc = acc + Bq[u].x;
+                    acc = acc + Bq[u].y;
+                    acc = acc + Bq[u].z;
+                    acc = acc + Bq[u].w;
+                }
+                if (!more2)
+                    break;
             }
         }
         const float s1 = __shfl_down(acc, 1, 64), s2 = __shfl_down(acc, 2, 64), s3 = __shfl_down(acc, 3, 64);
         if (tid == 0) {
-            logits[(size_t)t * E + e] = (acc + s1) + (s2 + s3);
-            // the logit is visible device-wide before it is counted; the
-            // counter wraps to 0 on the last count, ready for the next launch
-            __threadfence();
+            // The logit is stored at device scope (through to the level all
+            // XCDs share, not held in this XCD's L2) and the store has
+            // completed before it is counted, so no device-wide release
+            // (an L2 write-back per workgroup) is needed.  The counter wraps
+            // to 0 on the position's last count, ready for the next launch.
+            __hip_atomic_store(logits + (size_t)t * E + e, (acc + s1) + (s2 + s3), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+            __builtin_amdgcn_s_waitcnt(0);
             last_sh = atomicInc(count + t, (unsigned)(E - 1)) == (unsigned)(E - 1);
         }
     }
     __syncthreads();
     if (!last_sh)
         return;
-    // The position's last logit: every other workgroup's is visible now.
-    __threadfence();
-    for (int i = tid; i < E4; i += kLogitsThreads)
-        xr[i] = i < E ? logits[(size_t)t * E + i] : -__builtin_inff();
-    __syncthreads();
-    choose_experts(xr, E, k, sel_l, sel_i, wv, ids + (size_t)t * k, weights + (size_t)t * k);
+    // The position's last logit: every other workgroup's has completed at
+    // device scope; they are read at device scope after this XCD's caches
+    // are invalidated.
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    const float *lt = logits + (size_t)t * E;
+    uint64_t *comp = (uint64_t *)P;  // the products are spent
+    const bool any_nan = stage_logits(E, xr, comp, [&](int i) {
+        return __hip_atomic_load(lt + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    });
+    choose_experts(xr, comp, any_nan, E, k, sel_l, sel_i, wv, ids + (size_t)t * k, weights + (size_t)t * k);
 }
 
 template <int EW>
@@ -402,21 +456,40 @@ __global__ __launch_bounds__(kLogitsThreads) void moe_logits_kernel(const float 
 __global__ __launch_bounds__(256) void moe_topk_kernel(const float *__restrict__ logits, int E, int k,
                                                        int32_t *__restrict__ ids, float *__restrict__ weights) {
     __shared__ __align__(16) float lg[64 * kTopkMaxPerLane];
+    __shared__ __align__(16) uint64_t comp[64 * kTopkMaxPerLane];
     __shared__ float sel_l[kTopkMax], wv[kTopkMax];
     __shared__ int32_t sel_i[kTopkMax];
-    const int t = blockIdx.x, E4 = (E + 3) & ~3;
-    for (int i = threadIdx.x; i < E4; i += blockDim.x)
-        lg[i] = i < E ? logits[(size_t)t * E + i] : -__builtin_inff();
-    __syncthreads();
-    choose_experts(lg, E, k, sel_l, sel_i, wv, ids + (size_t)t * k, weights + (size_t)t * k);
+    const int t = blockIdx.x;
+    const float *lt = logits + (size_t)t * E;
+    const bool any_nan = stage_logits(E, lg, comp, [&](int i) { return lt[i]; });
+    choose_experts(lg, comp, any_nan, E, k, sel_l, sel_i, wv, ids + (size_t)t * k, weights + (size_t)t * k);
 }
 
 // mid = GELUTable(gate) * up for the 32 values of one Q8_0 block, one value a
 // lane on lanes 0..31 (all of them active), then the block's Q8_0
 // (Batch.quantizeBlock, nn/batch.go:109-143, as gx_quant.hip's kernel):
 // lane l writes q[l]; lane 0 the scale (through fp16) and the sum of q.
+// golem's GELU table (nn/gelu_table.go:25-38): for every fp16 input,
+// fp16(float32(geluTanh(float64(input)))), held as float.
 // GELUTable (nn/gelu_table.go:40-52): 0 at or below -10, the input at or
-// above 10, the table at the input's fp16 bits between.
+// above 10, the table at the input's fp16 bits between -- read from the
+// table, or (table null) the table's entry computed in place by the
+// table's own arithmetic, which saves a dependent global load.
+__device__ __forceinline__ float gelu_entry(uint32_t h) {
+    const double x = (double)half_bits_to_float(h);
+    const double sqrt2_over_pi = 0.79788456080286535587989211986876;
+    const double coef_a = 0.044715;
+    const double inner = sqrt2_over_pi * x * (1.0 + coef_a * x * x);
+    const double g = 0.5 * x * (1.0 + tanh(inner));
+    return half_bits_to_float(float_to_half_bits((float)g));
+}
+
+__global__ void gelu_table_kernel(float *__restrict__ table) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < 65536)
+        table[i] = gelu_entry((uint32_t)i);
+}
+
 __device__ __forceinline__ void gelu_mul_q8_0(float gate, float up, const float *__restrict__ table, int8_t *q,
                                               float *scale_out, int32_t *qsum_out) {
     const int l = threadIdx.x & 31;
@@ -426,7 +499,7 @@ __device__ __forceinline__ void gelu_mul_q8_0(float gate, float up, const float 
     else if (gate >= 10.0f)
         gl = gate;
     else
-        gl = table[float_to_half_bits(gate)];
+        gl = table ? table[float_to_half_bits(gate)] : gelu_entry(float_to_half_bits(gate));
     const float v = gl * up;
     float peak = fabsf(v);
 #pragma unroll
@@ -573,8 +646,16 @@ __global__ __launch_bounds__(1024) void moe_gate_up_kernel(
     __syncthreads();
     if (!DOTS && wave == 0) {
         float acc = 0.0f;
-        for (int s = 0; s < S; s++)
-            acc = acc + part[s * kTileRows + lane];
+        for (int s0 = 0; s0 < S; s0 += 8) {
+            float pv[8];  // eight stretch sums in flight at once, added in order
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+                pv[u] = part[min(s0 + u, S - 1) * kTileRows + lane];
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+                if (s0 + u < S)
+                    acc = acc + pv[u];
+        }
         const float up = __shfl_down(acc, 32, 64);
         if (lane < 32)
             gelu_mul_q8_0(acc, up, table, mq + mb * kQ4Block, ms + mb, mqs + mb);
@@ -606,6 +687,16 @@ __global__ __launch_bounds__(1024) void moe_down_reduce_kernel(
     const int tile = blockIdx.x >> 2, r = (blockIdx.x & 3) * kDownRows + (lane & 15);
     const int row = tile * kTileRows + r;
     const int32_t *idt = ids + (size_t)t * k;
+    // The routing factors w_j * DownScale[id_j]: lane j of wavefront 0 loads
+    // slot j's id and weight ahead of everything, its scale behind the
+    // weights (so that no wait for it holds them up), and forms the factor
+    // once the products are done; the sum reads it from that lane.
+    int e_reg = 0;
+    float w_reg = 0.0f;
+    if (!DOTS && wave == 0 && lane < k) {
+        e_reg = idt[lane];
+        w_reg = weights[(size_t)t * k + lane];
+    }
 
     // The activations: every load in flight together (indices past the end
     // clamped, the values never stored), then into LDS below.
@@ -643,6 +734,9 @@ __global__ __launch_bounds__(1024) void moe_down_reduce_kernel(
         dch = *(const uint4 *)(d_row + (size_t)s * kTileRows * kChunk);
     };
     load_pair(p);
+    float ds_reg = 1.0f;
+    if (!DOTS && wave == 0 && lane < k && down_scale)
+        ds_reg = e_reg >= 0 && e_reg < experts ? down_scale[e_reg] : __builtin_nanf("");
 #pragma unroll
     for (int a = 0; a < kDownActRegs; a++) {
         const int i = tid + a * nt;
@@ -682,19 +776,33 @@ __global__ __launch_bounds__(1024) void moe_down_reduce_kernel(
         p += nwaves * 4;
         load_pair(p);
     }
+    const float a_reg = w_reg * ds_reg;  // slot `lane`'s factor (lanes < k of wavefront 0)
     lds_barrier();
 
     if (!DOTS && wave == 0 && lane < kDownRows) {
-        float o = 0.0f;
-        for (int j = 0; j < k; j++) {
-            float v = 0.0f;
-            for (int s = 0; s < S; s++)
-                v = v + part[(j * S + s) * kDownRows + lane];
-            const int e = idt[j];
-            const float ds = !down_scale ? 1.0f : (e >= 0 && e < experts) ? down_scale[e] : __builtin_nanf("");
-            const float a = weights[(size_t)t * k + j] * ds;
-            const float pr = a * v;
-            o = o + pr;
+        // The pairs' sums in order, eight in flight at once: each slot's
+        // stretch sums from +0, then o += factor * value, slot by slot.
+        float o = 0.0f, v = 0.0f;
+        int s = 0, j = 0;  // the same in every lane
+        for (int p0 = 0; p0 < P; p0 += 8) {
+            float pv[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+                pv[u] = part[min(p0 + u, P - 1) * kDownRows + lane];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                if (p0 + u < P) {
+                    v = v + pv[u];
+                    if (++s == S) {
+                        const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a_reg), j));
+                        const float pr = a * v;
+                        o = o + pr;
+                        v = 0.0f;
+                        s = 0;
+                        j++;
+                    }
+                }
+            }
         }
         out[(size_t)t * ldo + row] = o;
     }
@@ -909,7 +1017,10 @@ int launch_moe_route(gx_ctx *ctx, const gx_weight *router, const float *router_s
     GX_CHECK(((uintptr_t)resid & 15) == 0 && ldr % 4 == 0, "gx: resid must be 16-byte aligned with ldr %% 4 == 0");
     const float *rw = (const float *)router->dev;
     if (M <= kRouteMaxPos && D <= kLogitsOneMaxD) {
-        const size_t lds = sizeof(float) * ((size_t)max(D, (E + 3) & ~3) + 4 * ((size_t)D / 4 + 4));
+        const size_t cn = ((size_t)D / 16 + 7) & ~(size_t)7;  // the kernel's chain layout
+        const size_t E32 = (size_t)((E + 31) & ~31);
+        const size_t lds = sizeof(float) * (max((size_t)D, E32) + max(4 * (4 * cn + 4), 2 * E32));
+        GX_CHECK(lds <= 64 * 1024, "gx: the router's %d inputs do not fit the one-launch kernel", D);
         moe_route_one_kernel<<<dim3((unsigned)E, (unsigned)M), kLogitsThreads, lds, ctx->stream>>>(
             rw, D, E, router_scale, resid, ldr, eps, k, logits, ids, weights, ctx->route_count);
         return check_launch("moe_route_one");
