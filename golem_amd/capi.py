@@ -57,7 +57,8 @@ _SIGNATURES = {
     "gx_q4_0_fused_block_dots": [_vp, _vp, _c_int, _vp, _vp, _vp, ctypes.c_float, _c_int, _c_int, _vp, _vp, _vp,
                                  _vp],
     "gx_q6_k_block_dots": [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp],
-    "gx_moe_unit_dots": [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _vp, _vp],
+    "gx_moe_block_dots": [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _vp, ctypes.c_size_t,
+                          _vp, _vp],
     "gx_gelu_table": [_vp, _vp],
     "gx_moe_workspace_bytes": [_c_int, _c_int, _c_int, _c_int, _c_int, ctypes.POINTER(_c_size)],
     "gx_moe_route": [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, ctypes.c_float, _vp, _vp, _vp],

@@ -560,9 +560,10 @@ int gx_q4_0_block_dots(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const f
     return ok();
 }
 
-int gx_moe_unit_dots(gx_ctx *ctx, const gx_weight *gate_up, const gx_weight *down, const float *x, int ldx, int M,
-                     int top_k, const int32_t *ids, const int8_t *mid_q, const float *mid_scales,
-                     const int32_t *mid_qsum, int32_t *dots_gate_up, int32_t *dots_down) {
+int gx_moe_block_dots(gx_ctx *ctx, const gx_weight *gate_up, const gx_weight *down, const float *x, int ldx, int M,
+                      int top_k, const int32_t *ids, const int8_t *mid_q, const float *mid_scales,
+                      const int32_t *mid_qsum, void *workspace, size_t workspace_bytes, int32_t *dots_gate_up,
+                      int32_t *dots_down) {
     if (int rc = use(ctx))
         return rc;
     GX_CHECK(gate_up && down && gate_up->quant == GX_Q4_0 && down->quant == GX_Q4_0,
@@ -572,14 +573,20 @@ int gx_moe_unit_dots(gx_ctx *ctx, const gx_weight *gate_up, const gx_weight *dow
              "gx: gate_up is %dx%d and down %dx%d: want 2F x D and D x F", gate_up->rows, gate_up->cols, down->rows,
              down->cols);
     GX_CHECK(top_k > 0 && top_k <= gate_up->count, "gx: top_k %d out of range", top_k);
-    GX_CHECK(M >= 0 && M <= 4, "gx: the few-position expert kernels take at most 4 positions, not %d", M);
+    GX_CHECK(M >= 0, "gx: bad batch shape");
     GX_CHECK(ids && (!dots_gate_up || (x && ldx >= gate_up->cols)) &&
                  (!dots_down || (mid_q && mid_scales && mid_qsum)),
              "gx: missing argument");
+    if (M > 4) {
+        size_t need = 0;
+        gx::moe_workspace_bytes(M, top_k, gate_up->cols, down->cols, gate_up->count, &need);
+        GX_CHECK(workspace && ((uintptr_t)workspace & 255) == 0 && workspace_bytes >= need,
+                 "gx: more than 4 positions need the experts' workspace (%zu bytes, 256-byte aligned)", need);
+    }
     if (M == 0)
         return ok();
-    if (int rc = gx::launch_moe_unit_dots(ctx, gate_up, down, x, ldx, M, top_k, ids, mid_q, mid_scales, mid_qsum,
-                                          dots_gate_up, dots_down))
+    if (int rc = gx::launch_moe_block_dots(ctx, gate_up, down, x, ldx, M, top_k, ids, mid_q, mid_scales, mid_qsum,
+                                           (uint8_t *)workspace, dots_gate_up, dots_down))
         return rc;
     return ok();
 }

@@ -19,13 +19,10 @@
 // 11-bit by 11-bit product fits fp32).  The vector ALU is left with one
 // conversion and one fma per element per block.
 //
-// Tile: a workgroup of four wavefronts owns 64 rows (one R64 tile) x 128
-// tokens; each wavefront 32 rows x 64 tokens, i.e. two 32x32 MFMA tiles that
-// share the weight operand.  Half a stretch (4 blocks) of the tile's nibbles, its
-// tokens' int8 activations and both sides' scales are staged in LDS, double
-// buffered: the next stretch's global loads are in flight while this one's
-// MFMAs run.  The weights' nibbles are widened to signed int8 (n - 8) in
-// registers as they are read.
+// Two kernels: the int8 one below (loads straight into LDS, every Q4_0
+// product of more than a few tokens, dense or grouped by expert) and an fp16
+// one for callers that hold the activation's fp16 copy.  The weights'
+// nibbles are widened to signed int8 (n - 8) in registers as they are read.
 #include <type_traits>
 
 #include "gx_device.hpp"
@@ -40,21 +37,6 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 typedef unsigned v4u __attribute__((ext_vector_type(4)));
 
-// Nibbles 0..15 in each byte -> (n - 8) as int8: n + 120 stays below 256
-// without a carry, and flipping the top bit subtracts 128.
-__device__ __forceinline__ uint32_t widen_nibbles(uint32_t n) { return (n + 0x78787878u) ^ 0x80808080u; }
-
-// The signed weights of one block for this lane's k-half: g = 0 takes the
-// low nibbles (weights 0..15), g = 1 the high nibbles (weights 16..31).
-__device__ __forceinline__ v4i weight_operand(const uint4 &wq, uint32_t sh) {
-    v4i A;
-    A.x = (int)widen_nibbles((wq.x >> sh) & 0x0F0F0F0Fu);
-    A.y = (int)widen_nibbles((wq.y >> sh) & 0x0F0F0F0Fu);
-    A.z = (int)widen_nibbles((wq.z >> sh) & 0x0F0F0F0Fu);
-    A.w = (int)widen_nibbles((wq.w >> sh) & 0x0F0F0F0Fu);
-    return A;
-}
-
 // A 32x32x8 f16 operand holding the fp16 bits `h` at k = 0 (lanes 0..31,
 // element 0) and zeros everywhere else.
 __device__ __forceinline__ v4h k0_operand(uint32_t h, bool first_half) {
@@ -62,73 +44,9 @@ __device__ __forceinline__ v4h k0_operand(uint32_t h, bool first_half) {
     return __builtin_bit_cast(v4h, bits);
 }
 
-// The fp16 bits of the j-th of the eight values packed in a chunk (j may be
-// a run-time index).
-__device__ __forceinline__ uint32_t chunk_half_bits(const uint4 &c, int j) {
-    const uint32_t lo = (j & 2) ? c.y : c.x, hi = (j & 2) ? c.w : c.z;
-    const uint32_t word = (j & 4) ? hi : lo;
-    return (j & 1) ? (word >> 16) : (word & 0xFFFFu);
-}
 
-// LDS layout of one pipeline stage: half a stretch, 4 blocks.
-constexpr int kStage = 4;                         // blocks per stage
-constexpr int kTokTile = 128;                     // tokens per workgroup
-constexpr int kActRow = kStage * kQ4Block + 16;   // one token's stage, padded (144 B)
-struct Stage {
-    uint8_t w[kStage][kTileRows][kChunk];         // nibbles, block-major, R64 order (4 KiB)
-    uint8_t a[kTokTile][kActRow];                 // int8 activations (18 KiB)
-    uint16_t dw[kStage][kTileRows];               // weight scales, fp16 bits
-    uint16_t da[kStage][kTokTile];                // activation scales, fp16 bits
-};
-
-// One thread's share of a stage: the global loads, then the writes into LDS.
-// Weights: chunk tid of the 256 (block tid / 64, row tid % 64).  Activations:
-// chunks c = tid + 256 k (k < 4) of the 1024 (token c / 8, 16-byte part
-// c % 8).  Weight scales: threads 0..63, the 8 bytes of row tid's chunk that
-// hold this stage's 4 blocks.  Activation scales: token tid / 2, blocks
-// 2 (tid % 2) .. + 2.  Indices past the matrix or the batch are clamped to
-// the last valid one (in bounds; such values are never used: a block past
-// the row gets weight scale 0, a token past the batch is not stored).
-struct Fetch {
-    v4u w, a[4];
-    unsigned dw0, dw1;
-    float da[2];
-};
-
-// The activation rows a thread stages are fixed for the whole product: its
-// four chunks belong to tokens tid/8 + 32 k, its scales to token tid/2.  They
-// are resolved once (through the expert groups' gather list when grouped).
-struct Rows {
-    const int8_t *a[4];
-    const float *s;
-};
-
-template <bool DOTS>
-__device__ __forceinline__ void fetch_stage(Fetch &f, const uint8_t *__restrict__ W, size_t plane0_bytes, int B,
-                                            int DC, const Rows &rows, int tile, int h, int tid) {
-    const int b0 = h * kStage;
-    {
-        const int b = min(b0 + (tid >> 6), B - 1);
-        f.w = *(const v4u *)(W + (((size_t)tile * B + b) * kTileRows + (tid & 63)) * kChunk);
-    }
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        const int c = tid + 256 * k;
-        const int b = min(b0 + ((c & 7) >> 1), B - 1);
-        f.a[k] = *(const v4u *)(rows.a[k] + (size_t)b * kQ4Block + 16 * (c & 1));
-    }
-    if (!DOTS) {
-        if (tid < 64) {
-            const unsigned *chunk = (const unsigned *)(W + plane0_bytes +
-                                                       (((size_t)tile * DC + (b0 >> 3)) * kTileRows + tid) * kChunk);
-            f.dw0 = chunk[(b0 & 7) >> 1];
-            f.dw1 = chunk[((b0 & 7) >> 1) + 1];
-        }
-#pragma unroll
-        for (int k = 0; k < 2; k++)
-            f.da[k] = rows.s[min(b0 + 2 * (tid & 1) + k, B - 1)];
-    }
-}
+// Blocks a pipeline stage holds (half a stretch).
+constexpr int kStage = 4;
 
 // A mixture-of-experts product runs grouped: workgroup row y of the grid is
 // work item y, {expert, first, count}, covering units sorted[first ..
@@ -140,148 +58,6 @@ struct Groups {
     int act_div;
     size_t matrix_bytes;
 };
-
-template <bool DOTS>
-__device__ __forceinline__ void commit_stage(const Fetch &f, Stage &t, int nb, int tid) {
-    *(v4u *)t.w[tid >> 6][tid & 63] = f.w;
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        const int c = tid + 256 * k;
-        *(v4u *)&t.a[c >> 3][(c & 7) * 16] = f.a[k];
-    }
-    if (!DOTS) {
-        if (tid < 64) {
-            const unsigned words[2] = {f.dw0, f.dw1};
-#pragma unroll
-            for (int j = 0; j < kStage; j++)  // a block past the row gets scale 0
-                t.dw[j][tid] = j < nb ? (uint16_t)(words[j >> 1] >> (16 * (j & 1))) : (uint16_t)0;
-        }
-#pragma unroll
-        for (int k = 0; k < 2; k++)
-            t.da[2 * (tid & 1) + k][tid >> 1] = (uint16_t)float_to_half_bits(f.da[k]);
-    }
-}
-
-template <bool DOTS, bool GROUPED>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 8))) void q4_0_gemm_kernel(
-    const uint8_t *__restrict__ W, size_t plane0_bytes, int B, int DC, const int8_t *__restrict__ q,
-    const float *__restrict__ scales, int K, int M, int tile0, int row_start, int row_end,
-    const float *__restrict__ bias, float *__restrict__ y, int ldy, int32_t *__restrict__ dots, Groups grp) {
-    __shared__ Stage st[2];
-    const int tid = threadIdx.x;
-    const int lane = tid & 63, wv = tid >> 6;
-    const int tile = tile0 + blockIdx.x;
-    const int n0 = tile * kTileRows;
-    const int nw = 32 * (wv & 1), mw = 64 * (wv >> 1);
-    const int li = lane & 31, g = lane >> 5;
-    const uint32_t sh = 4u * g;
-    const int H = (B + kStage - 1) / kStage;  // stages; two make a stretch
-    const int nrows = row_end - row_start;
-
-    // Local token t of this workgroup -> activation row and output row.
-    int first = blockIdx.y * kTokTile, count = min(kTokTile, M - first);
-    if (GROUPED) {
-        const int *item = grp.work + 4 * blockIdx.y;
-        count = item[2];
-        if (count <= 0)
-            return;
-        W += (size_t)item[0] * grp.matrix_bytes;
-        first = item[1];
-    }
-    auto act_row = [&](int t) -> int {
-        t = min(t, count - 1);
-        return GROUPED ? grp.sorted[first + t] / grp.act_div : first + t;
-    };
-    auto out_row = [&](int t) -> int { return t < count ? (GROUPED ? grp.sorted[first + t] : first + t) : -1; };
-    Rows rows;
-#pragma unroll
-    for (int k = 0; k < 4; k++)
-        rows.a[k] = q + (size_t)act_row((tid >> 3) + 32 * k) * K;
-    rows.s = DOTS ? nullptr : scales + (size_t)act_row(tid >> 1) * B;
-    const int bm0 = out_row(mw + li), bm1 = out_row(mw + 32 + li);
-    const bool v0 = bm0 >= 0, v1 = bm1 >= 0;
-
-    v16f acc0, acc1, tot0, tot1;
-#pragma unroll
-    for (int e = 0; e < 16; e++)
-        acc0[e] = acc1[e] = tot0[e] = tot1[e] = 0.0f;
-    const v16i zero_i = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-    const v16f zero_f = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-
-    Fetch f;
-    fetch_stage<DOTS>(f, W, plane0_bytes, B, DC, rows, tile, 0, tid);
-    commit_stage<DOTS>(f, st[0], min(kStage, B), tid);
-    __syncthreads();
-    for (int h = 0; h < H; h++) {
-        Stage &cur = st[h & 1];
-        if (h + 1 < H)  // in flight during this stage's arithmetic
-            fetch_stage<DOTS>(f, W, plane0_bytes, B, DC, rows, tile, h + 1, tid);
-        const int nb = min(kStage, B - h * kStage);
-#pragma unroll 2
-        for (int j = 0; j < kStage; j++) {
-            const v4i A = weight_operand(*(const uint4 *)cur.w[j][nw + li], sh);
-            const v4i B0 = *(const v4i *)&cur.a[mw + li][j * kQ4Block + 16 * g];
-            const v4i B1 = *(const v4i *)&cur.a[mw + 32 + li][j * kQ4Block + 16 * g];
-            const v16i C0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B0, zero_i, 0, 0, 0);
-            const v16i C1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B1, zero_i, 0, 0, 0);
-            if (DOTS) {
-                if (j < nb) {
-                    const int b = h * kStage + j;
-#pragma unroll
-                    for (int e = 0; e < 16; e++) {
-                        const int n = n0 + nw + 8 * (e >> 2) + 4 * g + (e & 3);
-                        if (n >= row_start && n < row_end) {
-                            if (v0)
-                                dots[((size_t)bm0 * nrows + (n - row_start)) * B + b] = C0[e];
-                            if (v1)
-                                dots[((size_t)bm1 * nrows + (n - row_start)) * B + b] = C1[e];
-                        }
-                    }
-                }
-            } else {
-                // Past the last block the weight scale is 0: the product adds
-                // fma(c, 0, acc) == acc.
-                const v4h As = k0_operand(cur.dw[j][nw + li], g == 0);
-                const v16f S0 = __builtin_amdgcn_mfma_f32_32x32x8f16(As, k0_operand(cur.da[j][mw + li], g == 0),
-                                                                     zero_f, 0, 0, 0);
-                const v16f S1 = __builtin_amdgcn_mfma_f32_32x32x8f16(As, k0_operand(cur.da[j][mw + 32 + li], g == 0),
-                                                                     zero_f, 0, 0, 0);
-#pragma unroll
-                for (int e = 0; e < 16; e++) {
-                    acc0[e] = fmaf((float)C0[e], S0[e], acc0[e]);
-                    acc1[e] = fmaf((float)C1[e], S1[e], acc1[e]);
-                }
-            }
-        }
-        // A stretch is two stages: after the second (or the row's last stage)
-        // the stretch sum joins the total.
-        if (!DOTS && ((h & 1) || h + 1 == H)) {
-#pragma unroll
-            for (int e = 0; e < 16; e++) {
-                tot0[e] = tot0[e] + acc0[e];
-                tot1[e] = tot1[e] + acc1[e];
-                acc0[e] = 0.0f;
-                acc1[e] = 0.0f;
-            }
-        }
-        if (h + 1 < H)
-            commit_stage<DOTS>(f, st[(h + 1) & 1], min(kStage, B - (h + 1) * kStage), tid);
-        __syncthreads();
-    }
-    if (DOTS)
-        return;
-#pragma unroll
-    for (int e = 0; e < 16; e++) {
-        const int n = n0 + nw + 8 * (e >> 2) + 4 * g + (e & 3);
-        if (n >= row_start && n < row_end) {
-            const float bn = bias ? bias[n] : 0.0f;
-            if (v0)
-                y[(size_t)bm0 * ldy + n] = bias ? tot0[e] + bn : tot0[e];
-            if (v1)
-                y[(size_t)bm1 * ldy + n] = bias ? tot1[e] + bn : tot1[e];
-        }
-    }
-}
 
 // ---- the fp16 product ------------------------------------------------------
 //
@@ -525,8 +301,7 @@ __global__ __launch_bounds__(64 * NWT) void q4_0_gemm_f16_kernel(
 
 // ---- the int8 product, loads straight into LDS -------------------------
 //
-// The default kernel for the Q4_0 x Q8_0 product (the one above serves the
-// DOTS and GROUPED forms).  Every stage's operands come in by direct
+// The kernel for the Q4_0 x Q8_0 product of a batch.  Every stage's operands come in by direct
 // global-to-LDS loads (global_load_lds_dwordx4 / _dword): no registers stage
 // them, and three stages live in an LDS ring, two in flight while one is
 // multiplied.  A workgroup owns 128 rows (two R64 tiles) x 64 tokens; each of
@@ -541,7 +316,6 @@ __global__ __launch_bounds__(64 * NWT) void q4_0_gemm_f16_kernel(
 //   [16384, 17408)  act. scales (fp32) [block 4][token 64]
 //   [17408, 18432)  weight scales (fp16) [row 128][block 4]
 constexpr int kDmaTok = 64;
-constexpr int kDmaSlot = 18432;
 constexpr int kDmaRing = 3;
 // The integer products run on a biased chain.  The weights enter the MFMA as
 // 16 * (n - 8) (the nibble in a byte's high half, its top bit flipped), and
@@ -588,64 +362,153 @@ __device__ __forceinline__ void wait_vmcnt() {  // vmcnt <= N; expcnt, lgkmcnt u
     __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
+// The two tile shapes of the direct-to-LDS product.  Both: a workgroup owns
+// 128 rows (two R64 tiles), a wavefront one 32x32 MFMA tile (rows 32*(w&3),
+// tokens 32*(w>>2)).
+//   TOK 64: eight wavefronts; three loads a wavefront a stage.  Slot bytes:
+//     [0, 8192) nibbles [block 4][row 128][16]
+//     [8192, 16384) int8 [block 4][half 2][token 64][16]
+//     [16384, 17408) act. scales (fp32) [block 4][token 64]
+//     [17408, 18432) weight scales (fp16) [row 128][block 4]
+//   TOK 32: four wavefronts (for batches of few tokens: an expert's share of
+//     a prompt); five loads a wavefront a stage -- two of nibbles, one of
+//     int8, two dwords of scales (the last of wavefronts 2 and 3 a dummy, so
+//     that every wavefront issues the same count).  Slot bytes:
+//     [0, 8192) nibbles [block 4][row 128][16]
+//     [8192, 12288) int8 [block 4][half 2][token 32][16]
+//     [12288, 12800) act. scales (fp32) [block 4][token 32]
+//     [12800, 13824) weight scales (fp16) [row 128][block 4]
+//     [13824, 14080) the dummy dwords
+template <int TOK>
+struct DmaShape;
+template <>
+struct DmaShape<64> {
+    static constexpr int kWaves = 8, kLoads = 3, kSlot = 18432, kOcc = 4;  // two workgroups a CU
+    static constexpr int kAct = 8192, kActScale = 16384, kWScale = 17408;
+};
+template <>
+struct DmaShape<32> {
+    static constexpr int kWaves = 4, kLoads = 5, kSlot = 14336, kOcc = 3;  // three workgroups a CU (LDS)
+    static constexpr int kAct = 8192, kActScale = 12288, kWScale = 12800, kDummy = 13824;
+};
+
+// GROUPED: blockIdx.y is an item of the expert work list (grp.work[item] =
+// {expert, first, count <= TOK, 0}; count 0 past the last item): the item's
+// tokens are units sorted[first ..], token t reading activation row
+// sorted[first + t] / act_div and writing output row sorted[first + t], all
+// against expert grp.work[item].x of the stack (matrices matrix_bytes
+// apart).  Otherwise tokens TOK * blockIdx.y .. of the batch.
+//
 // DOTS: the same kernel, also writing every block's integer (the chain
-// difference x below) to dots[t][n - row_start][b]; the scales are then not
-// needed, and their loads read the activation instead (in bounds).
-template <bool DOTS>
-__global__ __launch_bounds__(512, 4) void q4_0_gemm_dma_kernel(const uint8_t *__restrict__ W, size_t plane0_bytes,
-                                                            int B, int DC, const int8_t *__restrict__ q,
-                                                            const float *__restrict__ scales, int K, int M,
-                                                            int tiles, int tile0, int row_start, int row_end,
-                                                            const float *__restrict__ bias, float *__restrict__ y,
-                                                            int ldy, int32_t *__restrict__ dots) {
-    __shared__ __align__(16) uint8_t ring_lds[kDmaRing * kDmaSlot];
+// difference x below) to dots[out row][n - row_start][b]; the scales are then
+// not needed, and their loads read the activation instead (in bounds).
+template <int TOK, bool GROUPED, bool DOTS>
+__global__ __launch_bounds__(64 * DmaShape<TOK>::kWaves, DmaShape<TOK>::kOcc) void q4_0_gemm_dma_kernel(
+    const uint8_t *__restrict__ W, size_t plane0_bytes, int B, int DC, const int8_t *__restrict__ q,
+    const float *__restrict__ scales, int K, int M, int tiles, int tile0, int row_start, int row_end,
+    const float *__restrict__ bias, float *__restrict__ y, int ldy, int32_t *__restrict__ dots, Groups grp) {
+    using Sh = DmaShape<TOK>;
+    constexpr int kSlotB = Sh::kSlot;
+    __shared__ __align__(16) uint8_t ring_lds[kDmaRing * kSlotB];
     const int tid = threadIdx.x;
     const int lane = tid & 63, wv = tid >> 6;
     const int T0 = tile0 + 2 * blockIdx.x;        // the workgroup's first R64 tile
     const int rg = wv & 3, tg = wv >> 2;          // this wavefront's 32 rows and 32 tokens
     const int li = lane & 31, g = lane >> 5;
-    const uint32_t sh = 4u * g;
+    int first, count;
+    if (GROUPED) {
+        const int4 item = ((const int4 *)grp.work)[blockIdx.y];
+        count = item.z;
+        if (count <= 0)
+            return;  // past the last item: the whole workgroup
+        W += (size_t)item.x * grp.matrix_bytes;
+        first = item.y;
+    } else {
+        first = blockIdx.y * TOK;
+        count = min(TOK, M - first);
+    }
+    // token t's activation row and output row
+    auto arow = [&](int t) -> int { return GROUPED ? grp.sorted[first + t] / grp.act_div : first + t; };
+    auto orow = [&](int t) -> int { return GROUPED ? grp.sorted[first + t] : first + t; };
     // Stages, two to a stretch.  An odd count gets one more stage: the second
     // half of the last stretch, all of whose blocks lie past the row, with
     // weight scales 0 from the plane's padding.
     const int Hp = ((B + kStage - 1) / kStage + 1) & ~1;
-    const int first = blockIdx.y * kDmaTok, count = min(kDmaTok, M - first);
 
     // This lane's sources, fixed for the product.  Loads past the matrix, the
     // batch or the second tile read in-bounds neighbours; their values are
     // never used (weight scale 0, or not stored).
-    const int wj = wv & 3, wh = wv >> 2;          // nibble load: block wj, rows 64*wh + lane
-    const int wt = min(T0 + wh, tiles - 1);
-    const uint8_t *wsrc = W + ((size_t)wt * B * kTileRows + lane) * kChunk;
-    const int aj = wv >> 1, ag = wv & 1;          // activation load: block aj, half ag, token lane
-    const int8_t *asrc = q + (size_t)(first + min(lane, count - 1)) * K + 16 * ag;
-    // The third load is a dword for every wavefront: waves 0..3 an activation
-    // scale (block wv, token lane), waves 4..7 a pair of weight scales (row
-    // r = idx / 2 of the workgroup's 128, blocks 2 * (idx & 1) + {0, 1} of the
-    // stage, idx = 64 * (wv - 4) + lane), so that every wavefront issues the
-    // same three instructions.
-    const uint8_t *ssrc;
-    if (wv < 4) {
-        ssrc = DOTS ? (const uint8_t *)(q + (size_t)(first + min(lane, count - 1)) * B * 4)
-                    : (const uint8_t *)(scales + (size_t)(first + min(lane, count - 1)) * B);
-    } else {
-        const int idx = 64 * (wv - 4) + lane, r = idx >> 1;
+    auto wpair_src = [&](int pidx) -> const uint8_t * {  // weight-scale pair pidx of the 256
+        const int r = pidx >> 1;
         const int dt = min(T0 + (r >> 6), tiles - 1);
-        ssrc = W + plane0_bytes + ((size_t)dt * DC * kTileRows + (r & 63)) * kChunk + 4 * (idx & 1);
+        return W + plane0_bytes + ((size_t)dt * DC * kTileRows + (r & 63)) * kChunk + 4 * (pidx & 1);
+    };
+    const uint8_t *wsrc0, *wsrc1 = nullptr, *ssrc, *ssrc2 = nullptr;
+    const int8_t *asrc;
+    int wj, wh;
+    if constexpr (TOK == 64) {
+        wj = wv & 3, wh = wv >> 2;                // nibble load: block wj, rows 64*wh + lane
+        wsrc0 = W + ((size_t)min(T0 + wh, tiles - 1) * B * kTileRows + lane) * kChunk;
+        const int ag = wv & 1;                    // activation load: block wv >> 1, half ag, token lane
+        asrc = q + (size_t)arow(min(lane, count - 1)) * K + 16 * ag;
+        // The third load is a dword for every wavefront: waves 0..3 an
+        // activation scale (block wv, token lane), waves 4..7 a pair of
+        // weight scales (pair 64 * (wv - 4) + lane).
+        if (wv < 4)
+            ssrc = DOTS ? (const uint8_t *)(q + (size_t)arow(min(lane, count - 1)) * K)
+                        : (const uint8_t *)(scales + (size_t)arow(min(lane, count - 1)) * B);
+        else
+            ssrc = wpair_src(64 * (wv - 4) + lane);
+    } else {
+        wj = wv, wh = 0;                          // nibble loads: block wv, rows lane and 64 + lane
+        wsrc0 = W + ((size_t)min(T0, tiles - 1) * B * kTileRows + lane) * kChunk;
+        wsrc1 = W + ((size_t)min(T0 + 1, tiles - 1) * B * kTileRows + lane) * kChunk;
+        asrc = q + (size_t)arow(min(li, count - 1)) * K + 16 * g;  // block wv, half g, token li
+        // Dword A: waves 0, 1 activation scale idx = 64 wv + lane (block
+        // idx / 32, token idx % 32); waves 2, 3 weight-scale pair 64 (wv - 2)
+        // + lane.  Dword B: waves 0, 1 pair 128 + 64 wv + lane; waves 2, 3 a
+        // dummy (the pair of lane again, into the dummy dwords).
+        if (wv < 2) {
+            const int t = (64 * wv + lane) & 31;
+            ssrc = DOTS ? (const uint8_t *)(q + (size_t)arow(min(t, count - 1)) * K)
+                        : (const uint8_t *)(scales + (size_t)arow(min(t, count - 1)) * B);
+            ssrc2 = wpair_src(128 + 64 * wv + lane);
+        } else {
+            ssrc = wpair_src(64 * (wv - 2) + lane);
+            ssrc2 = ssrc;
+        }
     }
 
-    auto ring = [&](auto slot_tag) -> uint8_t * { return ring_lds + decltype(slot_tag)::value * kDmaSlot; };
+    auto ring = [&](auto slot_tag) -> uint8_t * { return ring_lds + decltype(slot_tag)::value * kSlotB; };
     auto issue = [&](auto slot_tag, int h) {
         h = min(h, Hp - 1);  // past the last stage: the last stage again, into the free slot
         uint8_t *slot = ring(slot_tag);
         const int b0 = h * kStage;
-        __builtin_amdgcn_global_load_lds(wsrc + (size_t)min(b0 + wj, B - 1) * kTileRows * kChunk,
-                                         (lds_ptr)(slot + (wj * 128 + 64 * wh) * 16), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds(asrc + (size_t)min(b0 + aj, B - 1) * kQ4Block,
-                                         (lds_ptr)(slot + 8192 + wv * 1024), 16, 0, 0);
-        const size_t soff = wv < 4 ? (size_t)min(b0 + wv, B - 1) * 4
-                                   : (size_t)(b0 >> 3) * kTileRows * kChunk + 8 * ((b0 >> 2) & 1);
-        __builtin_amdgcn_global_load_lds(ssrc + soff, (lds_ptr)(slot + 16384 + wv * 256), 4, 0, 0);
+        const size_t woff = (size_t)min(b0 + wj, B - 1) * kTileRows * kChunk;
+        const size_t pair_off = (size_t)(b0 >> 3) * kTileRows * kChunk + 8 * ((b0 >> 2) & 1);
+        if constexpr (TOK == 64) {
+            __builtin_amdgcn_global_load_lds(wsrc0 + woff, (lds_ptr)(slot + (wj * 128 + 64 * wh) * 16), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(asrc + (size_t)min(b0 + (wv >> 1), B - 1) * kQ4Block,
+                                             (lds_ptr)(slot + Sh::kAct + wv * 1024), 16, 0, 0);
+            const size_t soff = wv < 4 ? (size_t)min(b0 + wv, B - 1) * 4 : pair_off;
+            __builtin_amdgcn_global_load_lds(ssrc + soff, (lds_ptr)(slot + Sh::kActScale + wv * 256), 4, 0, 0);
+        } else {
+            __builtin_amdgcn_global_load_lds(wsrc0 + woff, (lds_ptr)(slot + (wj * 128) * 16), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(wsrc1 + woff, (lds_ptr)(slot + (wj * 128 + 64) * 16), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(asrc + (size_t)min(b0 + wv, B - 1) * kQ4Block,
+                                             (lds_ptr)(slot + Sh::kAct + wv * 1024), 16, 0, 0);
+            if (wv < 2) {
+                const int blk = (64 * wv + lane) >> 5;
+                __builtin_amdgcn_global_load_lds(ssrc + (size_t)min(b0 + blk, B - 1) * 4,
+                                                 (lds_ptr)(slot + Sh::kActScale + wv * 256), 4, 0, 0);
+                __builtin_amdgcn_global_load_lds(ssrc2 + pair_off, (lds_ptr)(slot + Sh::kWScale + 512 + wv * 256),
+                                                 4, 0, 0);
+            } else {
+                __builtin_amdgcn_global_load_lds(ssrc + pair_off, (lds_ptr)(slot + Sh::kWScale + (wv - 2) * 256),
+                                                 4, 0, 0);
+                __builtin_amdgcn_global_load_lds(ssrc2 + pair_off, (lds_ptr)(slot + Sh::kDummy), 4, 0, 0);
+            }
+        }
     };
 
     v16f acc, tot;
@@ -659,9 +522,9 @@ __global__ __launch_bounds__(512, 4) void q4_0_gemm_dma_kernel(const uint8_t *__
     // reads' immediate offsets).
     const uint32_t lds_base = (uint32_t)(uintptr_t)(lds_ptr)ring_lds;
     const uint32_t lds_w = lds_base + (32 * rg + li) * 16;
-    const uint32_t lds_a = lds_base + 8192 + (g * 64 + 32 * tg + li) * 16;
-    const uint32_t lds_dw = lds_base + 17408 + (32 * rg + li) * 8;
-    const uint32_t lds_da = lds_base + 16384 + (32 * tg + li) * 4;
+    const uint32_t lds_a = lds_base + Sh::kAct + (g * TOK + 32 * tg + li) * 16;
+    const uint32_t lds_dw = lds_base + Sh::kWScale + (32 * rg + li) * 8;
+    const uint32_t lds_da = lds_base + Sh::kActScale + (32 * tg + li) * 4;
 
     // One stage: four blocks.  kFirst marks a stretch's first stage, whose
     // first block starts the chain from the bias and the stretch sum from
@@ -670,11 +533,11 @@ __global__ __launch_bounds__(512, 4) void q4_0_gemm_dma_kernel(const uint8_t *__
     auto stage = [&](auto slot_tag, auto first_tag, int h) {
         constexpr int kSlot = decltype(slot_tag)::value;
         constexpr bool kFirst = decltype(first_tag)::value;
-        wait_vmcnt<3>();  // stage h has landed (stage h + 1 may be in flight)
+        wait_vmcnt<Sh::kLoads>();  // stage h has landed (stage h + 1 may be in flight)
         __builtin_amdgcn_s_barrier();
         // into the slot stage h - 1 used; every wavefront is past it
         issue(std::integral_constant<int, (kSlot + 2) % kDmaRing>{}, h + 2);
-        constexpr int so = kSlot * kDmaSlot;
+        constexpr int so = kSlot * kSlotB;
         // The operands of block j + 1 are read while block j is multiplied.
         v4u wq_n;
         v4i Bv_n;
@@ -682,8 +545,8 @@ __global__ __launch_bounds__(512, 4) void q4_0_gemm_dma_kernel(const uint8_t *__
         float da_n;
         auto read = [&](auto j_tag) {
             constexpr int j = decltype(j_tag)::value;
-            lds_read_block<so + j * 2048, so + j * 2048, so + 2 * j, so + j * 256>(lds_w, lds_a, lds_dw, lds_da, wq_n,
-                                                                                 Bv_n, dwh_n, da_n);
+            lds_read_block<so + j * 2048, so + j * 2 * TOK * 16, so + 2 * j, so + j * TOK * 4>(
+                lds_w, lds_a, lds_dw, lds_da, wq_n, Bv_n, dwh_n, da_n);
         };
         read(std::integral_constant<int, 0>{});
         unroll<0, kStage>([&](auto j_tag) {
@@ -733,7 +596,7 @@ __global__ __launch_bounds__(512, 4) void q4_0_gemm_dma_kernel(const uint8_t *__
                     const int b = h * kStage + j, tt = 32 * tg + li;
                     const int n = T0 * kTileRows + 32 * rg + 8 * (e >> 2) + 4 * g + (e & 3);
                     if (b < B && tt < count && n >= row_start && n < row_end)
-                        dots[((size_t)(first + tt) * (row_end - row_start) + (n - row_start)) * B + b] = (int)x;
+                        dots[((size_t)orow(tt) * (row_end - row_start) + (n - row_start)) * B + b] = (int)x;
                 }
             }
             chain = next;
@@ -774,7 +637,7 @@ __global__ __launch_bounds__(512, 4) void q4_0_gemm_dma_kernel(const uint8_t *__
     wait_vmcnt<0>();  // the trailing loads land before the workgroup ends
     const int t = 32 * tg + li;
     if (!DOTS && t < count) {
-        float *yr = y + (size_t)(first + t) * ldy;
+        float *yr = y + (size_t)orow(t) * ldy;
         const int nb = T0 * kTileRows + 32 * rg;  // the wavefront's first row
 #pragma unroll
         for (int e = 0; e < 16; e++) {
@@ -793,28 +656,34 @@ int launch_q4_0_gemm(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, const 
     const int tile0 = row_start / kTileRows;
     const int tiles = (row_end + kTileRows - 1) / kTileRows - tile0;
     const dim3 grid((unsigned)((tiles + 1) / 2), (unsigned)((M + kDmaTok - 1) / kDmaTok));
+    const Groups none{nullptr, nullptr, 1, 0};
     if (dots)
-        q4_0_gemm_dma_kernel<true><<<grid, 512, 0, ctx->stream>>>(mat, w->plane0_bytes, w->blocks, w->dchunks, q,
-                                                                  scales, w->cols, M, w->tiles, tile0, row_start,
-                                                                  row_end, bias, y, ldy, dots);
+        q4_0_gemm_dma_kernel<64, false, true><<<grid, 512, 0, ctx->stream>>>(
+            mat, w->plane0_bytes, w->blocks, w->dchunks, q, scales, w->cols, M, w->tiles, tile0, row_start, row_end,
+            bias, y, ldy, dots, none);
     else
-        q4_0_gemm_dma_kernel<false><<<grid, 512, 0, ctx->stream>>>(mat, w->plane0_bytes, w->blocks, w->dchunks, q,
-                                                                   scales, w->cols, M, w->tiles, tile0, row_start,
-                                                                   row_end, bias, y, ldy, nullptr);
+        q4_0_gemm_dma_kernel<64, false, false><<<grid, 512, 0, ctx->stream>>>(
+            mat, w->plane0_bytes, w->blocks, w->dchunks, q, scales, w->cols, M, w->tiles, tile0, row_start, row_end,
+            bias, y, ldy, nullptr, none);
     return check_launch("q4_0_gemm");
 }
 
 int launch_q4_0_gemm_grouped(gx_ctx *ctx, const gx_weight *w, const int32_t *work, int max_items,
                              const int32_t *sorted, int act_div, const int8_t *q, const float *scales, float *y,
-                             int ldy) {
-    dim3 grid(w->tiles, max_items);
+                             int ldy, int32_t *dots) {
+    // Items of at most kGroupTok units (the sort's tile), 32 tokens a workgroup.
+    const dim3 grid((unsigned)((w->tiles + 1) / 2), (unsigned)max_items);
     const Groups grp{work, sorted, act_div, w->matrix_bytes};
-    q4_0_gemm_kernel<false, true><<<grid, 256, 0, ctx->stream>>>(w->dev, w->plane0_bytes, w->blocks, w->dchunks, q,
-                                                                 scales, w->cols, 0, 0, 0, w->rows, nullptr, y, ldy,
-                                                                 nullptr, grp);
+    if (dots)
+        q4_0_gemm_dma_kernel<32, true, true><<<grid, 256, 0, ctx->stream>>>(
+            w->dev, w->plane0_bytes, w->blocks, w->dchunks, q, scales, w->cols, 0, w->tiles, 0, 0, w->rows, nullptr,
+            y, ldy, dots, grp);
+    else
+        q4_0_gemm_dma_kernel<32, true, false><<<grid, 256, 0, ctx->stream>>>(
+            w->dev, w->plane0_bytes, w->blocks, w->dchunks, q, scales, w->cols, 0, w->tiles, 0, 0, w->rows, nullptr,
+            y, ldy, nullptr, grp);
     return check_launch("q4_0_gemm_grouped");
 }
-
 }  // namespace gx
 
 namespace gx {

@@ -112,9 +112,12 @@ int launch_q4_0_matvec(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, cons
                        int ldy, int32_t *dots, int form);
 int launch_q4_0_gemm(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, const int8_t *q, const float *scales,
                      int M, int row_start, int row_end, const float *bias, float *y, int ldy, int32_t *dots);
+// The expert-grouped product: work items {expert, first, count <= 32, 0}
+// over the units sorted by expert (gx_moe.hip's sort); dots as above, by
+// output (unit) row.
 int launch_q4_0_gemm_grouped(gx_ctx *ctx, const gx_weight *w, const int32_t *work, int max_items,
                              const int32_t *sorted, int act_div, const int8_t *q, const float *scales, float *y,
-                             int ldy);
+                             int ldy, int32_t *dots);
 int launch_q4_0_gemm_f16(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, const uint16_t *q16,
                          const float *scales, int M, int row_start, int row_end, const float *bias, float *y, int ldy,
                          int32_t *dots);
@@ -139,9 +142,9 @@ int launch_moe_route(gx_ctx *ctx, const gx_weight *router, const float *router_s
 int launch_moe_experts(gx_ctx *ctx, const gx_weight *gate_up, const gx_weight *down, const float *down_scale,
                        const float *x, int ldx, int M, int k, const int32_t *ids, const float *weights, float *out,
                        int ldo, uint8_t *ws, const float *gelu_table);
-int launch_moe_unit_dots(gx_ctx *ctx, const gx_weight *gate_up, const gx_weight *down, const float *x, int ldx,
-                         int M, int k, const int32_t *ids, const int8_t *mid_q, const float *mid_scales,
-                         const int32_t *mid_qsum, int32_t *dots_gate_up, int32_t *dots_down);
+int launch_moe_block_dots(gx_ctx *ctx, const gx_weight *gate_up, const gx_weight *down, const float *x, int ldx,
+                          int M, int k, const int32_t *ids, const int8_t *mid_q, const float *mid_scales,
+                          const int32_t *mid_qsum, uint8_t *ws, int32_t *dots_gate_up, int32_t *dots_down);
 int launch_qwen_norm_quant(gx_ctx *ctx, float *x, int ldx, const float *add, int lda, const float *gain, int M, int K,
                            float eps, float *out, int ldo, int8_t *q, float *scales, int32_t *qsum);
 int launch_qwen_qk_rope(gx_ctx *ctx, const float *qkv, int ldqkv, int M, int heads, int kv_heads, int hd,

@@ -54,6 +54,7 @@ constexpr int kLogitsOneF4 = kLogitsOneMaxD / 4 / kLogitsThreads;
 constexpr int kTopkMaxPerLane = 16;  // E <= 1024
 constexpr int kTopkMax = 64;         // k <= 64
 constexpr int kUnitMaxPos = 4;       // positions whose units run as matrix-vector products
+constexpr int kGroupTok = 32;        // units of a grouped product's work item (its token tile)
 
 // chooseExperts (gemma/moe.go:62-88) for one position, by a whole workgroup
 // of at least 64 threads.  golem takes k rounds of an argmax that scans in
@@ -863,8 +864,11 @@ __global__ void moe_reduce_kernel(const float *__restrict__ partial, int D, int 
     for (int j = 0; j < k; j++) {
         const int u = t * k + j;
         const int e = ids[u];
-        const float ds = !down_scale ? 1.0f : (e >= 0 && e < E) ? down_scale[e] : __builtin_nanf("");
-        const float a = weights[u] * ds;
+        if (e < 0 || e >= E) {  // in no group: its partial row was never written
+            acc = __builtin_nanf("");
+            continue;
+        }
+        const float a = weights[u] * (down_scale ? down_scale[e] : 1.0f);
         const float p = a * partial[(size_t)u * D + i];
         acc = acc + p;
     }
@@ -873,71 +877,124 @@ __global__ void moe_reduce_kernel(const float *__restrict__ partial, int D, int 
 
 // Stable counting sort of the U = M*k units by expert, in one workgroup, and
 // the work list of the grouped product.  Units with an id outside [0, E) are
-// left out of every group (their partial sums stay NaN).
+// left out of every group (the sum gives their positions NaN).
 //   sorted[0..U): units, expert by expert, each expert's in unit order
 //   work[item] = {expert, first, count, 0}, items of up to `tile` units,
 //   expert by expert; the items past the last are {0, 0, 0, 0}.
+// Counts per expert first (their exclusive scan is each expert's first
+// place), then the units kSortThreads at a time: a unit's place is its
+// expert's first place, plus that expert's units in earlier chunks (a
+// running count), in earlier wavefronts of this chunk (per-wavefront counts
+// summed in wavefront order), and in lower lanes of its own wavefront (its
+// rank, from the wavefront's 64 ids in LDS).  Counting with LDS atomics is
+// order-free, so the places do not depend on scheduling.
 constexpr int kSortThreads = 1024;
+constexpr int kSortWaves = kSortThreads / 64;
+
+// Exclusive prefix sums of a and b over the workgroup's threads in thread
+// order (kSortThreads threads); tmp: 2 * kSortWaves ints of LDS.
+__device__ __forceinline__ void scan2_exclusive(int a, int b, int &ea, int &eb, int *tmp) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int ia = a, ib = b;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int ua = __shfl_up(ia, d, 64), ub = __shfl_up(ib, d, 64);
+        if (lane >= d) {
+            ia += ua;
+            ib += ub;
+        }
+    }
+    if (lane == 63) {
+        tmp[wave] = ia;
+        tmp[kSortWaves + wave] = ib;
+    }
+    __syncthreads();
+    int wa = 0, wb = 0;
+    for (int w = 0; w < wave; w++) {
+        wa += tmp[w];
+        wb += tmp[kSortWaves + w];
+    }
+    ea = wa + ia - a;
+    eb = wb + ib - b;
+    __syncthreads();
+}
+
 __global__ __launch_bounds__(kSortThreads) void moe_sort_kernel(const int32_t *__restrict__ ids, int U, int E,
                                                                 int tile, int max_items,
                                                                 int32_t *__restrict__ sorted,
                                                                 int32_t *__restrict__ work) {
-    extern __shared__ int32_t sh[];  // counts[E], offsets[E], placed[E], chunk ids[kSortThreads]
-    int32_t *counts = sh, *offsets = sh + E, *placed = sh + 2 * E, *chunk = sh + 3 * E;
-    const int tid = threadIdx.x;
+    // LDS: the chunk's ids [kSortThreads] (16-byte aligned), first[E],
+    // run[E], cnt[kSortWaves][E]
+    extern __shared__ __align__(16) int32_t sh[];
+    __shared__ int32_t tmp[2 * kSortWaves];
+    int32_t *chunk = sh, *first = sh + kSortThreads, *run = first + E, *cnt = run + E;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     for (int e = tid; e < E; e += kSortThreads)
-        counts[e] = 0, placed[e] = 0;
-    for (int i = tid; i < max_items; i += kSortThreads) {
-        work[4 * i] = 0, work[4 * i + 1] = 0, work[4 * i + 2] = 0, work[4 * i + 3] = 0;
-    }
+        run[e] = 0;
+    for (int i = tid; i < 4 * max_items; i += kSortThreads)
+        work[i] = 0;
     __syncthreads();
     for (int u = tid; u < U; u += kSortThreads) {
         const int e = ids[u];
         if (e >= 0 && e < E)
-            atomicAdd(&counts[e], 1);
+            atomicAdd(&run[e], 1);
     }
     __syncthreads();
-    if (tid == 0) {
-        int acc = 0, item = 0;
-        for (int e = 0; e < E; e++) {
-            offsets[e] = acc;
-            for (int f = 0; f < counts[e]; f += tile) {
-                if (item < max_items) {
-                    work[4 * item] = e;
-                    work[4 * item + 1] = acc + f;
-                    work[4 * item + 2] = min(tile, counts[e] - f);
-                }
-                item++;
+    // Each expert's first place and first item (E <= kSortThreads).
+    {
+        const int c = tid < E ? run[tid] : 0;
+        const int ni = (c + tile - 1) / tile;
+        int fp, fi;
+        scan2_exclusive(c, ni, fp, fi, tmp);
+        if (tid < E) {
+            first[tid] = fp;
+            for (int f = 0; f < ni && fi + f < max_items; f++) {
+                work[4 * (fi + f)] = tid;
+                work[4 * (fi + f) + 1] = fp + f * tile;
+                work[4 * (fi + f) + 2] = min(tile, c - f * tile);
             }
-            acc += counts[e];
+            run[tid] = 0;
         }
     }
-    __syncthreads();
-    // Units in chunks of kSortThreads, in order: a unit's place is its
-    // expert's offset, plus the units of that expert in earlier chunks, plus
-    // those before it in this chunk.
     for (int base = 0; base < U; base += kSortThreads) {
         const int u = base + tid;
-        const int e = u < U ? ids[u] : -1;
+        int e = u < U ? ids[u] : -1;
+        const bool valid = e >= 0 && e < E;
+        if (!valid)
+            e = -1;
         chunk[tid] = e;
+        for (int i = tid; i < kSortWaves * E; i += kSortThreads)
+            cnt[i] = 0;
         __syncthreads();
-        if (e >= 0 && e < E) {
-            int before = 0;
-            for (int j = 0; j < tid; j++)
-                before += chunk[j] == e;
-            sorted[offsets[e] + placed[e] + before] = u;
+        // this unit's rank among the lanes below it with the same expert
+        const int4 *cw = (const int4 *)(chunk + 64 * wave);
+        int r = 0;
+#pragma unroll
+        for (int q = 0; q < 16; q++) {
+            const int4 c4 = cw[q];
+            r += (int)((c4.x == e) & (4 * q + 0 < lane));
+            r += (int)((c4.y == e) & (4 * q + 1 < lane));
+            r += (int)((c4.z == e) & (4 * q + 2 < lane));
+            r += (int)((c4.w == e) & (4 * q + 3 < lane));
+        }
+        if (valid)
+            atomicAdd(&cnt[wave * E + e], 1);
+        __syncthreads();
+        // per expert: the running count before each wavefront of the chunk
+        for (int x = tid; x < E; x += kSortThreads) {
+            int acc = run[x];
+            for (int w = 0; w < kSortWaves; w++) {
+                const int c = cnt[w * E + x];
+                cnt[w * E + x] = acc;
+                acc += c;
+            }
+            run[x] = acc;
         }
         __syncthreads();
-        if (e >= 0 && e < E)
-            atomicAdd(&placed[e], 1);
+        if (valid)
+            sorted[first[e] + cnt[wave * E + e] + r] = u;
         __syncthreads();
     }
-}
-
-__global__ void fill_nan_kernel(float *__restrict__ p, size_t n) {
-    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n)
-        p[i] = __builtin_nanf("");
 }
 
 constexpr size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
@@ -952,7 +1009,7 @@ MoeSpace moe_space(int M, int k, int D, int F, int E) {
     MoeSpace s{};
     const size_t U = (size_t)M * k;
     s.units = (int)U;
-    s.max_items = E + (int)((U + 127) / 128);
+    s.max_items = E + (int)((U + kGroupTok - 1) / kGroupTok);
     size_t at = 0;
     auto take = [&](size_t bytes) {
         const size_t here = at;
@@ -1062,6 +1119,17 @@ int unit_shape(const gx_weight *gate_up, const gx_weight *down, int k, UnitShape
 
 }  // namespace
 
+namespace {
+
+int launch_sort(gx_ctx *ctx, const int32_t *ids, int U, int E, const MoeSpace &s, int32_t *sorted, int32_t *work) {
+    const size_t lds = (size_t)((2 + kSortWaves) * E + kSortThreads) * sizeof(int32_t);
+    GX_CHECK(E <= kSortThreads && lds <= 64 * 1024, "gx: %d experts do not fit the sort's LDS", E);
+    moe_sort_kernel<<<1, kSortThreads, lds, ctx->stream>>>(ids, U, E, kGroupTok, s.max_items, sorted, work);
+    return check_launch("moe_sort");
+}
+
+}  // namespace
+
 int launch_moe_experts(gx_ctx *ctx, const gx_weight *gate_up, const gx_weight *down, const float *down_scale,
                        const float *x, int ldx, int M, int k, const int32_t *ids, const float *weights, float *out,
                        int ldo, uint8_t *ws, const float *gelu_table) {
@@ -1100,25 +1168,18 @@ int launch_moe_experts(gx_ctx *ctx, const gx_weight *gate_up, const gx_weight *d
     // Each position's input, quantised once for its k units (moe.go:119-125).
     if (int rc = launch_quantize_q8_0(ctx, x, ldx, M, D, xq, xs, xqs, nullptr, nullptr))
         return rc;
-    // A unit whose expert id is out of range is in no group: its sums stay
-    // NaN, and so does its position's output.
-    const size_t n = (size_t)U * 2 * F;
-    fill_nan_kernel<<<(unsigned)((n + 255) / 256), 256, 0, ctx->stream>>>(gu, n);
-    const size_t np = (size_t)U * D;
-    fill_nan_kernel<<<(unsigned)((np + 255) / 256), 256, 0, ctx->stream>>>(part, np);
-    const size_t lds = (size_t)(3 * E + kSortThreads) * sizeof(int32_t);
-    GX_CHECK(lds <= 64 * 1024, "gx: %d experts do not fit the sort's LDS", E);
-    moe_sort_kernel<<<1, kSortThreads, lds, ctx->stream>>>(ids, U, E, 128, s.max_items, sorted, work);
-    if (int rc = check_launch("moe_sort"))
+    // A unit whose expert id is out of range is in no group: its rows are
+    // never written, and the sum makes its position's output NaN.
+    if (int rc = launch_sort(ctx, ids, U, E, s, sorted, work))
         return rc;
-    if (int rc = launch_q4_0_gemm_grouped(ctx, gate_up, work, s.max_items, sorted, k, xq, xs, gu, 2 * F))
+    if (int rc = launch_q4_0_gemm_grouped(ctx, gate_up, work, s.max_items, sorted, k, xq, xs, gu, 2 * F, nullptr))
         return rc;
     const size_t nm = (size_t)U * F;
     moe_gelu_mul_quant_kernel<<<(unsigned)((nm + 255) / 256), 256, 0, ctx->stream>>>(gu, 2 * F, F, U, gelu_table,
                                                                                      mq, ms, mqs);
     if (int rc = check_launch("moe_gelu_mul_quant"))
         return rc;
-    if (int rc = launch_q4_0_gemm_grouped(ctx, down, work, s.max_items, sorted, 1, mq, ms, part, D))
+    if (int rc = launch_q4_0_gemm_grouped(ctx, down, work, s.max_items, sorted, 1, mq, ms, part, D, nullptr))
         return rc;
     const size_t no = (size_t)M * D;
     moe_reduce_kernel<<<(unsigned)((no + 255) / 256), 256, 0, ctx->stream>>>(part, D, M, k, E, ids, weights,
@@ -1126,27 +1187,54 @@ int launch_moe_experts(gx_ctx *ctx, const gx_weight *gate_up, const gx_weight *d
     return check_launch("moe_reduce");
 }
 
-int launch_moe_unit_dots(gx_ctx *ctx, const gx_weight *gate_up, const gx_weight *down, const float *x, int ldx,
-                         int M, int k, const int32_t *ids, const int8_t *mid_q, const float *mid_scales,
-                         const int32_t *mid_qsum, int32_t *dots_gate_up, int32_t *dots_down) {
+int launch_moe_block_dots(gx_ctx *ctx, const gx_weight *gate_up, const gx_weight *down, const float *x, int ldx,
+                          int M, int k, const int32_t *ids, const int8_t *mid_q, const float *mid_scales,
+                          const int32_t *mid_qsum, uint8_t *ws, int32_t *dots_gate_up, int32_t *dots_down) {
     const int D = gate_up->cols, F = down->cols, E = gate_up->count;
-    UnitShape sh;
-    if (int rc = unit_shape(gate_up, down, k, &sh))
+    if (M <= kUnitMaxPos) {
+        UnitShape sh;
+        if (int rc = unit_shape(gate_up, down, k, &sh))
+            return rc;
+        if (dots_gate_up) {
+            moe_gate_up_kernel<true><<<dim3((unsigned)(F / kQ4Block), (unsigned)(M * k)), 64 * sh.gu_waves,
+                                       sh.gu_lds, ctx->stream>>>(gate_up->dev, gate_up->plane0_bytes,
+                                                                 gate_up->matrix_bytes, gate_up->blocks,
+                                                                 gate_up->dchunks, F, E, x, ldx, k, ids,
+                                                                 ctx->gelu_table, nullptr, nullptr, nullptr,
+                                                                 dots_gate_up);
+            if (int rc = check_launch("moe_gate_up dots"))
+                return rc;
+        }
+        if (dots_down) {
+            moe_down_reduce_kernel<true><<<dim3((unsigned)(D / kDownRows), (unsigned)M), 64 * sh.dn_waves,
+                                           sh.dn_lds, ctx->stream>>>(down->dev, down->plane0_bytes,
+                                                                     down->matrix_bytes, down->blocks, down->dchunks,
+                                                                     E, mid_q, mid_scales, mid_qsum, k, ids, nullptr,
+                                                                     nullptr, nullptr, 0, D, dots_down);
+            if (int rc = check_launch("moe_down_reduce dots"))
+                return rc;
+        }
+        return GX_OK;
+    }
+    // More positions: the grouped products over the same sort as the product's.
+    const MoeSpace s = moe_space(M, k, D, F, E);
+    int8_t *xq = (int8_t *)(ws + s.xq);
+    float *xs = (float *)(ws + s.xs);
+    int32_t *xqs = (int32_t *)(ws + s.xqs);
+    int32_t *sorted = (int32_t *)(ws + s.sorted);
+    int32_t *work = (int32_t *)(ws + s.work);
+    if (int rc = launch_sort(ctx, ids, s.units, E, s, sorted, work))
         return rc;
     if (dots_gate_up) {
-        moe_gate_up_kernel<true><<<dim3((unsigned)(F / kQ4Block), (unsigned)(M * k)), 64 * sh.gu_waves, sh.gu_lds,
-                                   ctx->stream>>>(gate_up->dev, gate_up->plane0_bytes, gate_up->matrix_bytes,
-                                                  gate_up->blocks, gate_up->dchunks, F, E, x, ldx, k, ids,
-                                                  ctx->gelu_table, nullptr, nullptr, nullptr, dots_gate_up);
-        if (int rc = check_launch("moe_gate_up dots"))
+        if (int rc = launch_quantize_q8_0(ctx, x, ldx, M, D, xq, xs, xqs, nullptr, nullptr))
+            return rc;
+        if (int rc = launch_q4_0_gemm_grouped(ctx, gate_up, work, s.max_items, sorted, k, xq, xs, nullptr, 0,
+                                              dots_gate_up))
             return rc;
     }
     if (dots_down) {
-        moe_down_reduce_kernel<true><<<dim3((unsigned)(D / kDownRows), (unsigned)M), 64 * sh.dn_waves, sh.dn_lds,
-                                       ctx->stream>>>(down->dev, down->plane0_bytes, down->matrix_bytes, down->blocks,
-                                                      down->dchunks, E, mid_q, mid_scales, mid_qsum, k, ids, nullptr,
-                                                      nullptr, nullptr, 0, D, dots_down);
-        if (int rc = check_launch("moe_down_reduce dots"))
+        if (int rc = launch_q4_0_gemm_grouped(ctx, down, work, s.max_items, sorted, 1, mid_q, mid_scales, nullptr, 0,
+                                              dots_down))
             return rc;
     }
     return GX_OK;

@@ -205,18 +205,22 @@ int gx_q4_0_fused_block_dots(gx_ctx *ctx, const gx_weight *w, int swiglu, const 
                              const float *gain, float eps, int row_start, int row_end, int8_t *q, float *scales,
                              int32_t *qsum, int32_t *out);
 
-/* The per-block integers of the few-position expert kernels (gx_moe_experts
- * at M <= 4), from those kernels with their integer output switched on:
- * dots_gate_up [M*top_k][2*ffn][dim/32] receives, for unit u (position
- * u / top_k, expert ids[u]), each gate|up row's block sums against Q8_0(x[u /
- * top_k]) as the kernel quantises it; dots_down [M*top_k][dim][ffn/32] each
- * down row's block sums against the unit's Q8_0 input given in mid_q
- * [M*top_k][ffn], mid_scales and mid_qsum [M*top_k][ffn/32].  Either output
- * may be NULL (then its inputs may be too).  A unit whose id is out of range
- * writes nothing.  No counterpart in golem: parity instrumentation. */
-int gx_moe_unit_dots(gx_ctx *ctx, const gx_weight *gate_up, const gx_weight *down, const float *x, int ldx, int M,
-                     int top_k, const int32_t *ids, const int8_t *mid_q, const float *mid_scales,
-                     const int32_t *mid_qsum, int32_t *dots_gate_up, int32_t *dots_down);
+/* The per-block integers of the expert products gx_moe_experts runs, from
+ * those kernels with their integer output switched on: for M <= 4 the
+ * fused matrix-vector kernels, for more positions the grouped int8-MFMA
+ * product over the same sort by expert.  dots_gate_up [M*top_k][2*ffn][dim/32]
+ * receives, for unit u (position u / top_k, expert ids[u]), each gate|up
+ * row's block sums against Q8_0(x[u / top_k]); dots_down [M*top_k][dim]
+ * [ffn/32] each down row's block sums against the unit's Q8_0 input given in
+ * mid_q [M*top_k][ffn], mid_scales and mid_qsum [M*top_k][ffn/32].  Either
+ * output may be NULL (then its inputs may be too).  More than 4 positions
+ * need gx_moe_experts' workspace (it may be NULL otherwise).  A unit whose
+ * id is out of range writes nothing.  No counterpart in golem: parity
+ * instrumentation. */
+int gx_moe_block_dots(gx_ctx *ctx, const gx_weight *gate_up, const gx_weight *down, const float *x, int ldx, int M,
+                      int top_k, const int32_t *ids, const int8_t *mid_q, const float *mid_scales,
+                      const int32_t *mid_qsum, void *workspace, size_t workspace_bytes, int32_t *dots_gate_up,
+                      int32_t *dots_down);
 
 /* dotQ6_KGo's per-superblock integer sum - 32*shift (nn/dot_q6_k.go:31-51)
  * for every (m, r, superblock): out[m][r - row_start][K/256]. */

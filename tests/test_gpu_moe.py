@@ -253,28 +253,37 @@ def test_bad_expert_id_poisons_its_position(dev):
         assert not np.any(np.isnan(out[1:]))
 
 
-def test_unit_integers_bit_exact(dev, orc):
-    """The few-position expert kernels' per-block integers (gx_moe_unit_dots)
-    at config 4's shape, every unit of two positions: gate|up against the
-    Q8_0 of its position's input as the kernel quantises it, down against a
-    given Q8_0 input, each equal to golem's accumulator less 8 * sum(q)
-    (nn/dot_q4_0.go:58-63)."""
+@pytest.mark.parametrize("M,spread", [(2, 128), (40, 128), (40, 8)])
+def test_expert_integers_bit_exact(dev, orc, M, spread):
+    """The expert products' per-block integers (gx_moe_block_dots) at config
+    4's shape, from the kernels gx_moe_experts runs: the fused
+    matrix-vector kernels for 2 positions, the grouped int8-MFMA product for
+    40 (experts drawn from all 128, and from only 8 so that an expert's 40
+    units span several 32-unit items).  gate|up against the Q8_0 of each
+    position's input, down against a given Q8_0 input, each equal to golem's
+    accumulator less 8 * sum(q) (nn/dot_q4_0.go:58-63), for every unit of 2
+    positions and a sample of the 320 units."""
+    import ctypes
     from oracle import Batch
     D, F, E, k = 2816, 704, 128, 8
     moe = Moe(dev, D, F, E, k, 4)
-    M = 2
     x = synth.activations(moe.g, M, D)
-    ids = np.stack([moe.g.choice(E, k, replace=False) for _ in range(M)]).astype(np.int32)
+    pool = moe.g.choice(E, spread, replace=False)
+    ids = np.stack([moe.g.choice(pool, k, replace=False) for _ in range(M)]).astype(np.int32)
     mid = synth.activations(moe.g, M * k, F)
     mb = Batch(mid).quantize()
     dgu = dev.empty((M * k, 2 * F, D // 32), np.int32)
     ddn = dev.empty((M * k, D, F // 32), np.int32)
     mq, ms, mqs = dev.put(mb.q_rows()), dev.put(mb.scales_rows()), dev.put(mb.qsum_rows())
     xd, idd = dev.put(x), dev.put(ids)  # held until the kernels have read them
-    capi.call("gx_moe_unit_dots", dev.ctx.ptr, moe.wgu.ptr, moe.wdn.ptr, capi.vp(xd), D, M, k,
-              capi.vp(idd), capi.vp(mq), capi.vp(ms), capi.vp(mqs), capi.vp(dgu), capi.vp(ddn))
+    n = ctypes.c_size_t()
+    capi.call("gx_moe_workspace_bytes", M, k, D, F, E, ctypes.byref(n))
+    ws = dev.empty((n.value,), np.uint8)
+    capi.call("gx_moe_block_dots", dev.ctx.ptr, moe.wgu.ptr, moe.wdn.ptr, capi.vp(xd), D, M, k, capi.vp(idd),
+              capi.vp(mq), capi.vp(ms), capi.vp(mqs), capi.vp(ws), n.value, capi.vp(dgu), capi.vp(ddn))
     dgu, ddn = dev.get(dgu), dev.get(ddn)
-    for u in range(M * k):
+    units = range(M * k) if M * k <= 16 else sorted(set(synth.rng(M).choice(M * k, 20, replace=False)) | {0, M * k - 1})
+    for u in units:
         t, e = u // k, int(ids[u // k, u % k])
         xb = Batch(x[t:t + 1]).quantize()
         acc = orc.q4_0_block_acc(moe.expert_bytes(moe.gate_up, 2 * F, D, e), xb, 2 * F)[0]
