@@ -96,8 +96,10 @@ int gx_init(int device, gx_ctx **out) {
     ctx->argmax_i = nullptr;
     ctx->scratch = nullptr;
     ctx->route_count = nullptr;
+    ctx->route_scale = nullptr;
     auto undo = [ctx]() {
         (void)hipFree(ctx->route_count);
+        (void)hipFree(ctx->route_scale);
         (void)hipFree(ctx->gelu_table);
         (void)hipFree(ctx->argmax_v);
         (void)hipFree(ctx->argmax_i);
@@ -115,7 +117,8 @@ int gx_init(int device, gx_ctx **out) {
         return gx::fail(GX_ERR_NOMEM, "gx: cannot allocate the greedy pick's workspace");
     }
     if (hipMalloc(&ctx->route_count, kRouteMaxPos * sizeof(unsigned)) != hipSuccess ||
-        hipMemset(ctx->route_count, 0, kRouteMaxPos * sizeof(unsigned)) != hipSuccess) {
+        hipMemset(ctx->route_count, 0, kRouteMaxPos * sizeof(unsigned)) != hipSuccess ||
+        hipMalloc(&ctx->route_scale, kRouteScaleMax * sizeof(float)) != hipSuccess) {
         undo();
         return gx::fail(GX_ERR_NOMEM, "gx: cannot allocate the router's counters");
     }
@@ -151,6 +154,7 @@ int gx_free(gx_ctx *ctx) {
     (void)hipFree(ctx->argmax_v);
     (void)hipFree(ctx->argmax_i);
     (void)hipFree(ctx->route_count);
+    (void)hipFree(ctx->route_scale);
     delete ctx;
     return ok();
 }

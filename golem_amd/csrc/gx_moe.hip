@@ -41,14 +41,13 @@ namespace {
 //     The workgroup that finishes a position's last logit (a counter per
 //     position, kept by the context) then chooses its experts, so routing
 //     is one launch.
-//   moe_logits_kernel<EW>: EW experts x 64/EW positions per workgroup; rows and
-//     inputs pass through LDS a 64-input chunk at a time, fetched from a ring
-//     of registers kLogitsDepth chunks ahead.  Many positions; the choosing
-//     is moe_topk_kernel.
+//   moe_norm_scale_kernel + moe_logits_kernel: the norm scales once per
+//     position, then 4 experts x 8 positions per workgroup, a lane one
+//     chain; rows and inputs pass through LDS 512 inputs at a time,
+//     transposed chain by chain.  Many positions; the choosing is
+//     moe_topk_kernel.
 constexpr int kLogitsThreads = 256;
-constexpr int kLogitsChunk = 64;     // inputs per chunk
-constexpr int kLogitsChunkPad = 68;  // chunk row stride in LDS (bank spread)
-constexpr int kLogitsDepth = 8;      // chunks fetched ahead
+constexpr int kLogitsChunk = 64;     // the router's width is a multiple of this
 constexpr int kLogitsOneMaxD = 7168; // input + products in LDS: 57 KB
 constexpr int kLogitsOneF4 = kLogitsOneMaxD / 4 / kLogitsThreads;
 constexpr int kTopkMaxPerLane = 16;  // E <= 1024
@@ -336,118 +335,165 @@ __global__ __launch_bounds__(kLogitsThreads) void moe_route_one_kernel(
     choose_experts(xr, comp, any_nan, E, k, sel_l, sel_i, wv, ids + (size_t)t * k, weights + (size_t)t * k);
 }
 
-template <int EW>
-__global__ __launch_bounds__(kLogitsThreads) void moe_logits_kernel(const float *__restrict__ router, int D, int E,
-                                                                    const float *__restrict__ router_scale,
-                                                                    const float *__restrict__ resid, int ldr, int M,
-                                                                    float eps, float *__restrict__ logits) {
-    constexpr int P = 64 / EW;                       // positions per workgroup
-    constexpr int XF4 = P * 16 / kLogitsThreads;     // input float4 per thread per chunk
-    constexpr int RT = EW * 16;                      // threads holding a row float4 per chunk
-    constexpr int BUF = (EW + P) * kLogitsChunkPad;  // a chunk in LDS: rows, then inputs
-    __shared__ float buf[2 * BUF];
-    __shared__ float scale[P];
-    __shared__ double red[kLogitsThreads];
-    const int tid = threadIdx.x;
-    const int e0 = blockIdx.x * EW, t0 = blockIdx.y * P;
+// Many positions: the norm scales first, one wavefront a position
+// (moe_norm_scale_kernel, every load of a position in flight at once), then
+// the logits.
+//
+// RMSNormPlain's scale of one position with exactly the sums of
+// norm_partials + norm_tree: lane l holds partials l + 64 m (m < 8),
+// partial t summing elements t, t + 512, ... in order; then the same
+// pairwise halving (t + 256, t + 128, t + 64 within the lane, then across
+// lanes).
+constexpr int kNormRounds = 8;  // 512-element rounds of loads in flight at once
 
-    // The norm's scale for each position, the workgroup together.
-    for (int p = 0; p < P && t0 + p < M; p++) {
-        double p0, p1;
-        norm_partials(resid + (size_t)(t0 + p) * ldr, D, p0, p1);
-        const double sum = norm_tree(p0, p1, red);
-        if (tid == 0)
-            scale[p] = norm_scale(sum, D, eps);
-        __syncthreads();
+__global__ __launch_bounds__(256) void moe_norm_scale_kernel(const float *__restrict__ resid, int ldr, int M, int D,
+                                                             float eps, float *__restrict__ scale) {
+    const int l = threadIdx.x & 63, t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= M)
+        return;  // whole wavefronts
+    const float *x = resid + (size_t)t * ldr;
+    double p[8];
+#pragma unroll
+    for (int m = 0; m < 8; m++)
+        p[m] = 0.0;
+    for (int base = 0; base < D; base += 512 * kNormRounds) {
+        float v[kNormRounds][8];
+#pragma unroll
+        for (int u = 0; u < kNormRounds; u++)
+#pragma unroll
+            for (int m = 0; m < 8; m++)
+                v[u][m] = x[min(base + 512 * u + l + 64 * m, D - 1)];
+#pragma unroll
+        for (int u = 0; u < kNormRounds; u++)
+#pragma unroll
+            for (int m = 0; m < 8; m++) {
+                const float a = base + 512 * u + l + 64 * m < D ? v[u][m] : 0.0f;
+                const float sq = a * a;
+                p[m] += (double)sq;
+            }
     }
+    double q[4], r[2];
+#pragma unroll
+    for (int m = 0; m < 4; m++)
+        q[m] = p[m] + p[m + 4];
+#pragma unroll
+    for (int m = 0; m < 2; m++)
+        r[m] = q[m] + q[m + 2];
+    double s = r[0] + r[1];
+    for (int w = 32; w > 0; w >>= 1) {
+        const double o = __shfl_down(s, w, 64);
+        if (l < w)
+            s = s + o;
+    }
+    if (l == 0)
+        scale[t] = norm_scale(s, D, eps);
+}
 
+// The logits: 4 experts x P positions a workgroup (16 P threads), a lane one
+// chain (lane = chain c + 4 (expert + 4 position)).  The inputs pass through
+// LDS CH at a time, transposed so that each chain's CH/4 elements of a chunk
+// are contiguous (one 16-byte read per lane for four of its steps), double
+// buffered: the next chunk's global loads are in flight while this one is
+// summed.
+constexpr int kLgEW = 4;
+
+template <int P, int CH>
+__global__ __launch_bounds__(16 * P) void moe_logits_kernel(const float *__restrict__ router, int D, int E,
+                                                           const float *__restrict__ router_scale,
+                                                           const float *__restrict__ resid, int ldr, int M,
+                                                           const float *__restrict__ scales,
+                                                           float *__restrict__ logits) {
+    constexpr int NT = 16 * P, ST = CH / 4, PAD = ST + 4;
+    constexpr int RF4 = (kLgEW * ST + NT - 1) / NT, XF4 = P * ST / NT;  // staged float4 per thread per chunk
+    static_assert(P * ST % NT == 0, "chunk shape");
+    __shared__ __align__(16) float Rs[2][kLgEW][4][PAD];
+    __shared__ __align__(16) float Xs[2][P][4][PAD];
+    const int tid = threadIdx.x;
+    const int e0 = blockIdx.x * kLgEW, t0 = blockIdx.y * P;
+    const int c = tid & 3, e = (tid >> 2) & 3, p = tid >> 4;  // this lane's chain
     const float inv_sqrt_dim = (float)(1.0 / sqrt((double)D));
-    const int re = (tid % RT) >> 4, rq = tid & 15;  // this thread's row float4 of a chunk
-    const float *rsrc = router + (size_t)min(e0 + re, E - 1) * D + 4 * rq;
-    float xs[kLogitsDepth][XF4 * 4], rs[kLogitsDepth][4];
-    const int c = tid & 3, e = (tid >> 2) % EW, p = (tid >> 2) / EW;  // lane = (p, e, c)
-    float acc = 0.0f;
-    const int chunks = D / kLogitsChunk;
 
-#define GX_LOGITS_FETCH(k, slot)                                                                                     \
-    do {                                                                                                             \
-        for (int f = 0; f < XF4; f++) {                                                                              \
-            const int idx = tid + f * kLogitsThreads;                                                                \
-            const int tt = min(t0 + (idx >> 4), M - 1);                                                              \
-            const float4 v = *(const float4 *)(resid + (size_t)tt * ldr + (k) * kLogitsChunk + 4 * (idx & 15));     \
-            xs[slot][4 * f + 0] = v.x;                                                                               \
-            xs[slot][4 * f + 1] = v.y;                                                                               \
-            xs[slot][4 * f + 2] = v.z;                                                                               \
-            xs[slot][4 * f + 3] = v.w;                                                                               \
-        }                                                                                                            \
-        const float4 r = *(const float4 *)(rsrc + (k) * kLogitsChunk);                                               \
-        rs[slot][0] = r.x;                                                                                           \
-        rs[slot][1] = r.y;                                                                                           \
-        rs[slot][2] = r.z;                                                                                           \
-        rs[slot][3] = r.w;                                                                                           \
-    } while (0)
-
-#define GX_LOGITS_PUT(k, slot)                                                                                       \
-    do {                                                                                                             \
-        float *b = buf + ((k) & 1) * BUF;                                                                            \
-        if (tid < RT)                                                                                                \
-            for (int j = 0; j < 4; j++)                                                                              \
-                b[re * kLogitsChunkPad + 4 * rq + j] = rs[slot][j];                                                  \
-        float *bx = b + EW * kLogitsChunkPad;                                                                        \
-        for (int f = 0; f < XF4; f++) {                                                                              \
-            const int idx = tid + f * kLogitsThreads;                                                                \
-            const int pp = idx >> 4, q = idx & 15;                                                                   \
-            const float sc = scale[pp];                                                                              \
-            const int i0 = (k) * kLogitsChunk + 4 * q;                                                               \
-            for (int j = 0; j < 4; j++) {                                                                            \
-                const float normed = xs[slot][4 * f + j] * sc;                                                       \
-                const float factor = inv_sqrt_dim * (router_scale ? router_scale[i0 + j] : 1.0f);                    \
-                bx[pp * kLogitsChunkPad + 4 * q + j] = normed * factor;                                              \
-            }                                                                                                        \
-        }                                                                                                            \
-    } while (0)
-
+    // This thread's staging: row pieces idx = tid + NT f (expert idx / ST,
+    // float4 idx % ST of the chunk) and input pieces likewise (position
+    // idx / ST); past D the pieces are zero.
+    float4 rv[RF4], xv[XF4], sv[XF4];
+    float sc[XF4];
 #pragma unroll
-    for (int u = 0; u < kLogitsDepth; u++)
-        if (u < chunks)
-            GX_LOGITS_FETCH(u, u);
-    GX_LOGITS_PUT(0, 0);
-    if (kLogitsDepth < chunks)
-        GX_LOGITS_FETCH(kLogitsDepth, 0);
-    __syncthreads();
-    for (int kb = 0; kb < chunks; kb += kLogitsDepth) {
+    for (int f = 0; f < XF4; f++)
+        sc[f] = scales[min(t0 + (tid + NT * f) / ST, M - 1)];
+    auto fetch = [&](int k) {
+        const int i0 = k * CH;
 #pragma unroll
-        for (int u = 0; u < kLogitsDepth; u++) {
-            const int k = kb + u;
-            if (k < chunks) {
-                const float *b = buf + (k & 1) * BUF;
-                const float *rk = b + e * kLogitsChunkPad + c;
-                const float *xr = b + EW * kLogitsChunkPad + p * kLogitsChunkPad + c;
-                float av[16], bv[16];
+        for (int f = 0; f < RF4; f++) {
+            const int idx = tid + NT * f, i = i0 + 4 * (idx % ST);
+            const float *rsrc = router + (size_t)min(e0 + min(idx / ST, kLgEW - 1), E - 1) * D;
+            rv[f] = i < D ? *(const float4 *)(rsrc + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
 #pragma unroll
-                for (int j = 0; j < 16; j++) {
-                    av[j] = rk[4 * j];
-                    bv[j] = xr[4 * j];
-                }
+        for (int f = 0; f < XF4; f++) {
+            const int idx = tid + NT * f, i = i0 + 4 * (idx % ST);
+            const float *xr = resid + (size_t)min(t0 + idx / ST, M - 1) * ldr;
+            xv[f] = i < D ? *(const float4 *)(xr + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            sv[f] = router_scale && i < D ? *(const float4 *)(router_scale + i) : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+        }
+    };
+    auto put = [&](int buf) {
 #pragma unroll
-                for (int j = 0; j < 16; j++) {
-                    const float prod = av[j] * bv[j];
-                    acc = acc + prod;
-                }
-                // chunk k + 1 into the other buffer (last read at chunk k - 1);
-                // its ring slot then takes chunk k + 1 + depth
-                const int nu = (u + 1) % kLogitsDepth;  // a constant once unrolled
-                if (k + 1 < chunks) {
-                    GX_LOGITS_PUT(k + 1, nu);
-                    if (k + 1 + kLogitsDepth < chunks)
-                        GX_LOGITS_FETCH(k + 1 + kLogitsDepth, nu);
-                }
-                __syncthreads();
+        for (int f = 0; f < RF4; f++) {
+            const int idx = tid + NT * f, ee = idx / ST, q = idx % ST;
+            const float r4[4] = {rv[f].x, rv[f].y, rv[f].z, rv[f].w};
+            if (idx < kLgEW * ST) {
+#pragma unroll
+                for (int cc = 0; cc < 4; cc++)
+                    Rs[buf][ee][cc][q] = r4[cc];
             }
         }
+#pragma unroll
+        for (int f = 0; f < XF4; f++) {
+            const int idx = tid + NT * f, pp = idx / ST, q = idx % ST;
+            const float x4[4] = {xv[f].x, xv[f].y, xv[f].z, xv[f].w}, s4[4] = {sv[f].x, sv[f].y, sv[f].z, sv[f].w};
+#pragma unroll
+            for (int cc = 0; cc < 4; cc++) {
+                const float normed = x4[cc] * sc[f];
+                const float factor = inv_sqrt_dim * s4[cc];
+                Xs[buf][pp][cc][q] = normed * factor;
+            }
+        }
+    };
+
+    const int chunks = (D + CH - 1) / CH;
+    fetch(0);
+    put(0);
+    __syncthreads();
+    float acc = 0.0f;
+    for (int k = 0; k < chunks; k++) {
+        const int buf = k & 1;
+        if (k + 1 < chunks)
+            fetch(k + 1);
+        const float4 *rr = (const float4 *)Rs[buf][e][c];
+        const float4 *xx = (const float4 *)Xs[buf][p][c];
+        // the chunk's steps in order; past D the products are +0, which
+        // leave a sum that starts from +0 unchanged
+        for (int q4 = 0; q4 < ST / 4; q4 += 4) {
+            float4 a[4], b[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                a[u] = rr[q4 + u];
+                b[u] = xx[q4 + u];
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const float p0 = a[u].x * b[u].x, p1 = a[u].y * b[u].y, p2 = a[u].z * b[u].z, p3 = a[u].w * b[u].w;
+                acc = acc + p0;
+                acc = acc + p1;
+                acc = acc + p2;
+                acc = acc + p3;
+            }
+        }
+        if (k + 1 < chunks)
+            put(buf ^ 1);  // the other buffer was last read in chunk k - 1
+        __syncthreads();
     }
-#undef GX_LOGITS_FETCH
-#undef GX_LOGITS_PUT
     const float s1 = __shfl_down(acc, 1, 64), s2 = __shfl_down(acc, 2, 64), s3 = __shfl_down(acc, 3, 64);
     if (c == 0 && t0 + p < M && e0 + e < E)
         logits[(size_t)(t0 + p) * E + e0 + e] = (acc + s1) + (s2 + s3);
@@ -1082,12 +1128,20 @@ int launch_moe_route(gx_ctx *ctx, const gx_weight *router, const float *router_s
             rw, D, E, router_scale, resid, ldr, eps, k, logits, ids, weights, ctx->route_count);
         return check_launch("moe_route_one");
     }
-    constexpr int EW = 4, P = 64 / EW;
-    const dim3 grid((unsigned)((E + EW - 1) / EW), (unsigned)((M + P - 1) / P));
-    moe_logits_kernel<EW><<<grid, kLogitsThreads, 0, ctx->stream>>>(rw, D, E, router_scale, resid, ldr, M, eps,
-                                                                     logits);
-    if (int rc = check_launch("moe_logits"))
-        return rc;
+    // Positions in runs of at most kRouteScaleMax (the context's scales).
+    for (int m0 = 0; m0 < M; m0 += kRouteScaleMax) {
+        const int m = min(kRouteScaleMax, M - m0);
+        const float *rr = resid + (size_t)m0 * ldr;
+        moe_norm_scale_kernel<<<(unsigned)((m + 3) / 4), 256, 0, ctx->stream>>>(rr, ldr, m, D, eps, ctx->route_scale);
+        if (int rc = check_launch("moe_norm_scale"))
+            return rc;
+        constexpr int P = 16, CH = 256;
+        const dim3 grid((unsigned)((E + kLgEW - 1) / kLgEW), (unsigned)((m + P - 1) / P));
+        moe_logits_kernel<P, CH><<<grid, 16 * P, 0, ctx->stream>>>(rw, D, E, router_scale, rr, ldr, m,
+                                                                    ctx->route_scale, logits + (size_t)m0 * E);
+        if (int rc = check_launch("moe_logits"))
+            return rc;
+    }
     moe_topk_kernel<<<M, E <= 64 ? 64 : E <= 128 ? 128 : 256, 0, ctx->stream>>>(logits, E, k, ids, weights);
     return check_launch("moe_topk");
 }
