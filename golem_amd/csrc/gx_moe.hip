@@ -592,6 +592,44 @@ __global__ __launch_bounds__(256) void moe_gelu_mul_quant_kernel(const float *__
                   scales + index, qsum + index);
 }
 
+// The same, four values a lane (eight lanes a Q8_0 block, q8_0_quad's
+// arithmetic, which is gelu_mul_q8_0's): for 16-byte aligned rows.
+__global__ __launch_bounds__(256) void moe_gelu_mul_quant4_kernel(const float *__restrict__ gate_up, int ld, int F,
+                                                                   int U, const float *__restrict__ table,
+                                                                   int8_t *__restrict__ q,
+                                                                   float *__restrict__ scales,
+                                                                   int32_t *__restrict__ qsum) {
+    const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int F4 = F / 4;
+    if (gid >= (size_t)U * F4)
+        return;  // U*F/4 is a multiple of 8: whole 8-lane groups drop out
+    const int u = (int)(gid / F4), i = 4 * (int)(gid % F4);
+    const float4 g4 = *(const float4 *)(gate_up + (size_t)u * ld + i);
+    const float4 u4 = *(const float4 *)(gate_up + (size_t)u * ld + F + i);
+    const float gate[4] = {g4.x, g4.y, g4.z, g4.w}, up[4] = {u4.x, u4.y, u4.z, u4.w};
+    float v[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        float gl;
+        if (gate[c] <= -10.0f)
+            gl = 0.0f;
+        else if (gate[c] >= 10.0f)
+            gl = gate[c];
+        else
+            gl = table[float_to_half_bits(gate[c])];
+        v[c] = gl * up[c];
+    }
+    float stored;
+    int32_t sum;
+    const uint32_t packed = q8_0_quad(v, &stored, &sum);
+    *(uint32_t *)(q + (size_t)u * F + i) = packed;
+    if ((gid & 7) == 0) {
+        const size_t index = (size_t)u * (F >> 5) + (i >> 5);
+        scales[index] = stored;
+        qsum[index] = sum;
+    }
+}
+
 // ---- few positions: the units as matrix-vector products ---------------------
 //
 // Two kernels after the router, each reading its expert matrices once per
@@ -921,6 +959,39 @@ __global__ void moe_reduce_kernel(const float *__restrict__ partial, int D, int 
     out[(size_t)t * ldo + i] = acc;
 }
 
+// The same, four outputs a thread (16-byte aligned rows).
+__global__ __launch_bounds__(256) void moe_reduce4_kernel(const float *__restrict__ partial, int D, int M, int k,
+                                                          int E, const int32_t *__restrict__ ids,
+                                                          const float *__restrict__ weights,
+                                                          const float *__restrict__ down_scale,
+                                                          float *__restrict__ out, int ldo) {
+    const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int D4 = D / 4;
+    if (gid >= (size_t)M * D4)
+        return;
+    const int t = (int)(gid / D4), i = 4 * (int)(gid % D4);
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = 0; j < k; j++) {
+        const int u = t * k + j;
+        const int e = ids[u];
+        if (e < 0 || e >= E) {  // in no group: its partial row was never written
+#pragma unroll
+            for (int c = 0; c < 4; c++)
+                acc[c] = __builtin_nanf("");
+            continue;
+        }
+        const float a = weights[u] * (down_scale ? down_scale[e] : 1.0f);
+        const float4 p4 = *(const float4 *)(partial + (size_t)u * D + i);
+        const float pv[4] = {p4.x, p4.y, p4.z, p4.w};
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const float p = a * pv[c];
+            acc[c] = acc[c] + p;
+        }
+    }
+    *(float4 *)(out + (size_t)t * ldo + i) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+}
+
 // Stable counting sort of the U = M*k units by expert, in one workgroup, and
 // the work list of the grouped product.  Units with an id outside [0, E) are
 // left out of every group (the sum gives their positions NaN).
@@ -936,6 +1007,7 @@ __global__ void moe_reduce_kernel(const float *__restrict__ partial, int D, int 
 // order-free, so the places do not depend on scheduling.
 constexpr int kSortThreads = 1024;
 constexpr int kSortWaves = kSortThreads / 64;
+constexpr int kSortHeld = 4;  // ids a thread keeps in registers (U <= 4096 read once)
 
 // Exclusive prefix sums of a and b over the workgroup's threads in thread
 // order (kSortThreads threads); tmp: 2 * kSortWaves ints of LDS.
@@ -980,7 +1052,17 @@ __global__ __launch_bounds__(kSortThreads) void moe_sort_kernel(const int32_t *_
     for (int i = tid; i < 4 * max_items; i += kSortThreads)
         work[i] = 0;
     __syncthreads();
-    for (int u = tid; u < U; u += kSortThreads) {
+    // This thread's first kSortHeld ids stay in registers for the placing
+    // below (read once).
+    int held[kSortHeld];
+#pragma unroll
+    for (int h = 0; h < kSortHeld; h++)
+        held[h] = tid + h * kSortThreads < U ? ids[tid + h * kSortThreads] : -1;
+#pragma unroll
+    for (int h = 0; h < kSortHeld; h++)
+        if (held[h] >= 0 && held[h] < E)
+            atomicAdd(&run[held[h]], 1);
+    for (int u = tid + kSortHeld * kSortThreads; u < U; u += kSortThreads) {
         const int e = ids[u];
         if (e >= 0 && e < E)
             atomicAdd(&run[e], 1);
@@ -1002,9 +1084,15 @@ __global__ __launch_bounds__(kSortThreads) void moe_sort_kernel(const int32_t *_
             run[tid] = 0;
         }
     }
-    for (int base = 0; base < U; base += kSortThreads) {
+    for (int base = 0, h = 0; base < U; base += kSortThreads, h++) {
         const int u = base + tid;
-        int e = u < U ? ids[u] : -1;
+        int e = -1;
+#pragma unroll
+        for (int hh = 0; hh < kSortHeld; hh++)
+            if (hh == h)
+                e = held[hh];
+        if (h >= kSortHeld)
+            e = u < U ? ids[u] : -1;
         const bool valid = e >= 0 && e < E;
         if (!valid)
             e = -1;
@@ -1088,9 +1176,13 @@ int launch_geglu_quant(gx_ctx *ctx, const float *gu, int ldgu, int M, int ffn, i
     const size_t n = (size_t)M * ffn;
     if (n == 0)
         return GX_OK;
-    moe_gelu_mul_quant_kernel<<<(unsigned)((n + 255) / 256), 256, 0, ctx->stream>>>(gu, ldgu, ffn, M,
-                                                                                    ctx->gelu_table, q, scales,
-                                                                                    qsum);
+    if (((uintptr_t)gu & 15) == 0 && ldgu % 4 == 0)
+        moe_gelu_mul_quant4_kernel<<<(unsigned)((n / 4 + 255) / 256), 256, 0, ctx->stream>>>(
+            gu, ldgu, ffn, M, ctx->gelu_table, q, scales, qsum);
+    else
+        moe_gelu_mul_quant_kernel<<<(unsigned)((n + 255) / 256), 256, 0, ctx->stream>>>(gu, ldgu, ffn, M,
+                                                                                        ctx->gelu_table, q, scales,
+                                                                                        qsum);
     return check_launch("geglu_quant");
 }
 
@@ -1228,16 +1320,22 @@ int launch_moe_experts(gx_ctx *ctx, const gx_weight *gate_up, const gx_weight *d
         return rc;
     if (int rc = launch_q4_0_gemm_grouped(ctx, gate_up, work, s.max_items, sorted, k, xq, xs, gu, 2 * F, nullptr))
         return rc;
-    const size_t nm = (size_t)U * F;
-    moe_gelu_mul_quant_kernel<<<(unsigned)((nm + 255) / 256), 256, 0, ctx->stream>>>(gu, 2 * F, F, U, gelu_table,
-                                                                                     mq, ms, mqs);
+    const size_t nm4 = (size_t)U * F / 4;  // gu is the workspace's (aligned), F a multiple of 32
+    moe_gelu_mul_quant4_kernel<<<(unsigned)((nm4 + 255) / 256), 256, 0, ctx->stream>>>(gu, 2 * F, F, U, gelu_table,
+                                                                                       mq, ms, mqs);
     if (int rc = check_launch("moe_gelu_mul_quant"))
         return rc;
     if (int rc = launch_q4_0_gemm_grouped(ctx, down, work, s.max_items, sorted, 1, mq, ms, part, D, nullptr))
         return rc;
-    const size_t no = (size_t)M * D;
-    moe_reduce_kernel<<<(unsigned)((no + 255) / 256), 256, 0, ctx->stream>>>(part, D, M, k, E, ids, weights,
-                                                                             down_scale, out, ldo);
+    if (((uintptr_t)out & 15) == 0 && ldo % 4 == 0) {
+        const size_t no4 = (size_t)M * D / 4;
+        moe_reduce4_kernel<<<(unsigned)((no4 + 255) / 256), 256, 0, ctx->stream>>>(part, D, M, k, E, ids, weights,
+                                                                                   down_scale, out, ldo);
+    } else {
+        const size_t no = (size_t)M * D;
+        moe_reduce_kernel<<<(unsigned)((no + 255) / 256), 256, 0, ctx->stream>>>(part, D, M, k, E, ids, weights,
+                                                                                 down_scale, out, ldo);
+    }
     return check_launch("moe_reduce");
 }
 
