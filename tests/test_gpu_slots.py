@@ -178,3 +178,49 @@ def test_a_slot_out_of_range_stores_nothing(dev):
     assert not np.any(kcn[0]) and not np.any(vcn[0]), "slot 0 was written"
     assert np.any(kcn[1][:, :, 3, :]) and np.any(vcn[1][:, :, 3]), "token 0's key and value are missing"
     assert not np.any(kcn[1][:, :, 5, :]) and not np.any(vcn[1][:, :, 5]), "the stray token was stored"
+
+
+@pytest.mark.parametrize("nconv", [3, 6])
+def test_slots_against_golem(dev, orc, nconv):
+    """Each conversation of a lock-step batch against golem's engine run alone
+    on that conversation (oracle/qwen.py): at every step its hidden state
+    within 5e-2 of RMS (the bar of the one-conversation tests, test_gpu_qwen)
+    and its greedy ids identical -- qwen/place_test.go:8-50 checked against
+    golem rather than against this build's own single-conversation path."""
+    from oracle.qwen import QwenOracle
+    loose = 5e-2
+    cfg = synth.QwenConfig(256, 512, 2, 4, 2, 64, 1024, 16 * nconv)  # 16 positions a conversation
+    w = synth.qwen_weights(cfg, 83, symmetric=True)
+    om = QwenOracle(cfg, w)
+    g = synth.rng(190 + nconv)
+    prompts = [[int(t) for t in g.integers(0, cfg.vocab, 3 + i)] for i in range(nconv)]
+    steps = 5
+    want = [om.greedy(p, steps)[0] for p in prompts]
+    m = QwenModel(dev.ctx, cfg, w, max_batch=16)
+    m.set_slots(nconv)
+    seqs, toks, worst = [], [], 0.0
+    for i, p in enumerate(prompts):
+        m.use_slot(i)
+        got = dev.get(m.forward(p, 0))[-1].copy()
+        om.reset()
+        rel = orc.compare_floats(got, om.forward(p, 0)[-1])[0]
+        assert rel <= loose, f"conversation {i} prompt: {rel:.3g} of RMS"
+        worst = max(worst, rel)
+        toks.append(int(m.next_token(len(p) - 1).item()))
+        seqs.append(list(p) + [toks[-1]])
+    pos = [len(p) for p in prompts]
+    for _ in range(steps - 1):
+        hidden = dev.get(m.forward_slots(toks, list(range(nconv)), pos)).copy()
+        for i in range(nconv):
+            om.reset()
+            rel = orc.compare_floats(hidden[i], om.forward(seqs[i], 0)[-1])[0]
+            assert rel <= loose, f"conversation {i} at position {pos[i]}: {rel:.3g} of RMS"
+            worst = max(worst, rel)
+        toks = [int(t) for t in m.next_tokens(range(nconv)).cpu().tolist()]
+        for i in range(nconv):
+            seqs[i].append(toks[i])
+        pos = [p + 1 for p in pos]
+    got_ids = [s[len(p):] for s, p in zip(seqs, prompts)]
+    log(f"  {nconv} conversations against golem: hidden within {worst:.2g} of RMS; ids {got_ids}")
+    assert got_ids == want
+    m.free()
