@@ -179,10 +179,15 @@ def main():
                 graph.replay()
             ms0 = ctx.timer_stop() / reps
             b0 = r0 * (c0 // 32) * 18 + c0 + 8 * (c0 // 32) + 4 * r0
+            gbs0 = b0 / (ms0 * 1e-3) / 1e9
             extra["c0_q4_0_matvec"] = {"shape": [r0, c0], "M": 1, "kernel_us": round(ms0 * 1e3, 3),
-                                       "GB/s": round(b0 / (ms0 * 1e-3) / 1e9, 1),
-                                       "hbm_frac": round(b0 / (ms0 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                                       "bytes_per_launch": b0, "weight_copies": n_copies}
+                                       "GB/s": round(gbs0, 1), "hbm_frac": round(gbs0 / HBM_PEAK_GBS, 4),
+                                       "bytes_per_launch": b0, "weight_copies": n_copies,
+                                       "roofline": {"bound": "hbm", "achieved": round(gbs0, 1),
+                                                    "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                                    "frac": round(gbs0 / HBM_PEAK_GBS, 4),
+                                                    "traffic": read_traffic("q4_0_matvec_c0_traffic.txt"),
+                                                    "kernel": "q4_0_matvec_kernel"}}
             for w_ in w0s:
                 w_.free()
             if args.only == "c0":
@@ -219,7 +224,10 @@ def main():
                 by = r0 * (c0 // 32) * 18 + M * (c0 + 8 * (c0 // 32)) + 4 * M * r0
                 extra[f"c2_q4_0_gemm_m{M}_{label}"] = {
                     "shape": [M, r0, c0], "kernel_us": round(ms2 * 1e3, 2), "TOP/s": round(tops, 2),
-                    "int8_mfma_frac": round(tops / INT8_PEAK_TOPS, 4), "GB/s": round(by / (ms2 * 1e-3) / 1e9, 1)}
+                    "GMAC/s": round(tops * 1e3 / 2, 1),
+                    "int8_mfma_frac": round(tops / INT8_PEAK_TOPS, 4), "GB/s": round(by / (ms2 * 1e-3) / 1e9, 1),
+                    "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": INT8_PEAK_TOPS,
+                                 "unit": "TOP/s", "frac": round(tops / INT8_PEAK_TOPS, 4)}}
         w0d.free()
         if args.only == "c2":
             print(json.dumps(extra))
@@ -280,7 +288,8 @@ def cpu_baseline(w6, x, rows, cols, step_bytes, step, y, torch, no_extra):
     rotating weight copies (640 MB, past the last-level cache) for ~10 s on
     every allowed thread and ~3 s on one; the GPU's logits are checked bit for
     bit against it.  Config 0 (Q4_0, dotQ4_0AVX2 under matVecQ4_0Rows) is
-    timed the same way for ~3 s."""
+    timed the same way for ~3 s, and config 2's matrix through golem's packed
+    path (dotPackedQ4_0x4AVX2) for ~3 s at each of M = 64 and 512."""
     import oracle
     threads = oracle.host_threads()
     oracle.cpu_lib(threads)
@@ -322,6 +331,18 @@ def cpu_baseline(w6, x, rows, cols, step_bytes, step, y, torch, no_extra):
         by0 = r0 * (c0 // 32) * 18 + c0 + 8 * (c0 // 32) + 4 * r0
         out["c0_q4_0_matvec"] = {"GB/s": round(n0 * by0 / t0 / 1e9, 2), "us_per_pass": round(t0 / n0 * 1e6, 1),
                                  "cores": threads, "passes": n0}
+        # Config 2 (Q4_0 9728 x 2560 against M tokens) through golem's packed
+        # path (PackQ4_0's eight-row groups, dotPackedQ4_0x4AVX2 under
+        # matVecPackedQ4_0Rows): ~3 s each at M = 64 and 512.
+        packed = oracle.pack_q4_0(w0, r0, c0)
+        g2 = synth.rng(2)
+        for M in (64, 512):
+            b2 = oracle.Batch(synth.activations(g2, M, c0)).quantize()
+            y2 = np.zeros((M, r0), dtype=np.float32)
+            n2, t2 = timed(lambda i: oracle.cpu_mat_vec_packed_q4_0(packed, b2, r0, threads, y2), 3.0)
+            macs = float(M) * r0 * c0
+            out[f"c2_q4_0_packed_m{M}"] = {"GMAC/s": round(n2 * macs / t2 / 1e9, 2),
+                                           "ms_per_pass": round(t2 / n2 * 1e3, 2), "cores": threads, "passes": n2}
     return out
 
 
@@ -403,6 +424,10 @@ def bench_c3(ctx, torch):
         "decode_bytes_per_token": int(token_bytes),
         "decode_GB/s": round(token_bytes / (per_tok * 1e-3) / 1e9, 1),
         "decode_hbm_frac": round(token_bytes / (per_tok * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "roofline": {"bound": "hbm", "achieved": round(token_bytes / (per_tok * 1e-3) / 1e9, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(token_bytes / (per_tok * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                     "scope": "a whole decode step (every kernel), bytes a token reads"},
         "greedy_ids_head": ids[:8], "setup_s": round(setup_s, 1)}}
 
 
@@ -490,7 +515,10 @@ def bench_c4(ctx, torch, dev):
             "M": M, "ms_per_layer": round(ms, 4), "positions_per_s": round(M / (ms * 1e-3), 1),
             "experts_read": round(mean_touched, 2), "bytes_per_layer": int(by),
             "GB/s": round(by / (ms * 1e-3) / 1e9, 1), "hbm_frac": round(by / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            "graph": M == 1, "eager_ms_per_layer": round(eager_ms, 4)}
+            "graph": M == 1, "eager_ms_per_layer": round(eager_ms, 4),
+            "roofline": {"bound": "hbm", "achieved": round(by / (ms * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(by / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                         "scope": "the layer's launches (route + experts), bytes of the experts read"}}
     wr.free()
     for gu, dn in stacks:
         gu.free()

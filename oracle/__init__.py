@@ -369,6 +369,7 @@ def cpu_lib(threads=None):
         "cpu_pool_threads": (I, []),
         "cpu_mat_vec_q6_k": (I, [V, V, V, V, I, I, I, V, I, I]),
         "cpu_mat_vec_q4_0": (I, [V, V, V, V, I, I, I, V, I, I]),
+        "cpu_mat_vec_packed_q4_0": (I, [V, V, V, V, I, I, I, V, I, I]),
         "cpu_dot_q4_0": (None, [V, V, V, V, I, I, I, I, V, I, I]),
         "cpu_dot_q6_k": (F, [V, V, V, V, I]),
     }.items():
@@ -396,6 +397,17 @@ def cpu_mat_vec_q4_0(w, batch, rows, threads, ys=None):
         ys = np.full((batch.size, rows), np.nan, dtype=np.float32)
     rc = cpu_lib().cpu_mat_vec_q4_0(_p(w), _p(batch.Q), _p(batch.Scales), _p(batch.Corr), rows, batch.width,
                                     batch.size, _p(ys), ys.shape[1], threads)
+    assert rc == 0
+    return ys
+
+
+def cpu_mat_vec_packed_q4_0(packed, batch, rows, threads, ys=None):
+    """matVecPackedQ4_0Rows (whole groups of eight rows) through golem's AVX2
+    x4/x1 packed kernels, from pack_q4_0's layout."""
+    if ys is None:
+        ys = np.full((batch.size, rows), np.nan, dtype=np.float32)
+    rc = cpu_lib().cpu_mat_vec_packed_q4_0(_p(packed), _p(batch.Q), _p(batch.Scales), _p(batch.Corr), rows,
+                                           batch.width, batch.size, _p(ys), ys.shape[1], threads)
     assert rc == 0
     return ys
 

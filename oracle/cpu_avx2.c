@@ -448,6 +448,122 @@ int cpu_mat_vec_q4_0(const uint8_t *w, const int8_t *Q, const float *S, const fl
     return 0;
 }
 
+/* ---- the packed product (nn/pack_q4_0.go, nn/pack_q4_0_amd64.s) ----------
+ *
+ * Eight rows interleaved per group of blocks (144 bytes a block: the rows'
+ * eight fp16 scales, then four 32-byte chunks of eight inputs; byte s*8+j of
+ * chunk g holds row {0,1,4,5}[s] in its low nibble and row {2,3,6,7}[s] in
+ * its high one, at input 8g+j).  dotPackedQ4_0x4AVX2 (:99-160) multiplies a
+ * group against four columns: per block the nibbles are split into eight
+ * registers once; per column the eight activation bytes of a chunk are
+ * broadcast to its four slots, VPMADDUBSW'd against the low and the high
+ * nibbles, the int16 pairs summed over the four chunks, widened by VPMADDWD
+ * against ones and folded by one VPHADDD into the eight rows in order; then
+ * acc += float(sums) * (act_scale * row_scale) and acc -= corr * row_scale,
+ * both fused.  dotPackedQ4_0AVX2 is the same for one column. */
+static inline void packed_unpack(const uint8_t *blk, __m256i nib[8], __m256 *rs) {
+    *rs = _mm256_cvtph_ps(_mm_loadu_si128((const __m128i *)blk));
+    const __m256i mask = _mm256_set1_epi8(0x0F);
+    for (int g = 0; g < 4; g++) {
+        const __m256i c = _mm256_loadu_si256((const __m256i *)(blk + 16 + 32 * g));
+        nib[2 * g] = _mm256_and_si256(c, mask);
+        nib[2 * g + 1] = _mm256_and_si256(_mm256_srli_epi16(c, 4), mask);
+    }
+}
+
+static inline __m256 packed_sums(const __m256i nib[8], const int8_t *q) {
+    __m256i lo = _mm256_setzero_si256(), hi = _mm256_setzero_si256();
+    for (int g = 0; g < 4; g++) {
+        const __m256i a = _mm256_set1_epi64x(*(const long long *)(q + 8 * g));
+        const __m256i l = _mm256_maddubs_epi16(nib[2 * g], a), h = _mm256_maddubs_epi16(nib[2 * g + 1], a);
+        lo = g == 0 ? l : _mm256_add_epi16(lo, l);
+        hi = g == 0 ? h : _mm256_add_epi16(hi, h);
+    }
+    const __m256i ones = _mm256_set1_epi16(1);
+    return _mm256_cvtepi32_ps(_mm256_hadd_epi32(_mm256_madd_epi16(lo, ones), _mm256_madd_epi16(hi, ones)));
+}
+
+/* One group of eight rows against `cols` (4 or 1) columns from column c,
+ * over n inputs from `block`; state: cols x 8 running sums. */
+static void packed_kernel(const uint8_t *w, const int8_t *Q, const float *S, const float *C, int stride, int block,
+                          int c, int n, float *state, int mode, int cols) {
+    __m256 acc[4];
+    for (int j = 0; j < cols; j++)
+        acc[j] = (mode & BEGIN) ? _mm256_setzero_ps() : _mm256_loadu_ps(state + 8 * j);
+    for (int b = 0; b < n / 32; b++) {
+        __m256i nib[8];
+        __m256 rs;
+        packed_unpack(w + (size_t)b * 144, nib, &rs);
+        const size_t at = (size_t)(block + b) * stride + c;
+        for (int j = 0; j < cols; j++) {
+            const __m256 sums = packed_sums(nib, Q + (at + j) * 32);
+            const __m256 sc = _mm256_mul_ps(_mm256_set1_ps(S[at + j]), rs);
+            acc[j] = _mm256_fmadd_ps(sums, sc, acc[j]);
+            acc[j] = _mm256_fnmadd_ps(_mm256_set1_ps(C[at + j]), rs, acc[j]);
+        }
+    }
+    for (int j = 0; j < cols; j++)
+        _mm256_storeu_ps(state + 8 * j, acc[j]);
+}
+
+struct packed_args {
+    const uint8_t *w;
+    const int8_t *Q;
+    const float *S, *C;
+    int size, inputs, ldy;
+    float *y;
+};
+
+enum { MAX_GROUP_TILE = 8 }; /* nn/pack_q4_0.go:147-152 */
+
+/* matVecPackedQ4_0Rows (nn/pack_q4_0.go:153-221): rows [start, end), a
+ * group computed whole and written in part. */
+static void packed_rows(void *p, int start, int end) {
+    const struct packed_args *a = p;
+    const size_t group_bytes = (size_t)a->inputs / 32 * 144;
+    const int first = start / 8, last = (end + 7) / 8;
+    const int steps = K_TILE < a->inputs ? K_TILE : a->inputs;
+    const int step_bytes = steps / 32 * 144;
+    int tile = ROW_TILE_BYTES / step_bytes;
+    tile = tile < 1 ? 1 : tile > MAX_GROUP_TILE ? MAX_GROUP_TILE : tile;
+    float four[MAX_GROUP_TILE][32], one[MAX_GROUP_TILE][8];
+    for (int from = first; from < last; from += tile) {
+        const int to = from + tile < last ? from + tile : last;
+        int c = 0;
+        for (int wi = 0; wi < 2; wi++) {
+            const int cols = wi == 0 ? 4 : 1;
+            for (; c + cols <= a->size; c += cols) {
+                for (int k = 0; k < a->inputs; k += steps) {
+                    const int block = k / 32, n = a->inputs - k < steps ? a->inputs - k : steps;
+                    const int mode = (k == 0 ? BEGIN : 0) | (k + n >= a->inputs ? FINISH : 0);
+                    for (int g = from; g < to; g++)
+                        packed_kernel(a->w + (size_t)g * group_bytes + (size_t)block * 144, a->Q, a->S, a->C,
+                                      a->size, block, c, n, cols == 4 ? four[g - from] : one[g - from], mode, cols);
+                }
+                for (int g = from; g < to; g++)
+                    for (int j = 0; j < cols; j++)
+                        for (int r = 0; r < 8; r++) {
+                            const int row = 8 * g + r;
+                            if (row >= start && row < end)
+                                a->y[(size_t)(c + j) * a->ldy + row] =
+                                    (cols == 4 ? four[g - from] : one[g - from])[8 * j + r];
+                        }
+            }
+        }
+    }
+}
+
+/* The packed product of golem's loader (whole groups of eight rows) over a
+ * batch in golem's interleaved layout, on at most `threads` threads. */
+int cpu_mat_vec_packed_q4_0(const uint8_t *packed, const int8_t *Q, const float *S, const float *C, int rows,
+                            int inputs, int size, float *y, int ldy, int threads) {
+    if (inputs % 32 || rows % 8 || !pool.count)
+        return -1;
+    struct packed_args a = {packed, Q, S, C, size, inputs, ldy, y};
+    in_parallel(rows, (long)rows * inputs * size, threads, packed_rows, &a);
+    return 0;
+}
+
 /* The single kernels, for the tests: one row against columns [c, c+cols). */
 void cpu_dot_q4_0(const uint8_t *w, const int8_t *Q, const float *S, const float *C, int stride, int block, int c,
                   int n, float *state, int mode, int cols) {

@@ -118,3 +118,31 @@ def test_q6_k_extreme_scales():
     b = oracle.Batch(x).quantize_k()
     np.testing.assert_array_equal(oracle.cpu_mat_vec_q6_k(w, b, rows, 1).view(np.uint32),
                                   oracle.mat_vec_q6_k_rows(w, b, rows).view(np.uint32))
+
+
+@pytest.mark.parametrize("rows,cols,size", [(64, 2560, 7), (40, 4096, 4), (16, 9728, 5)])
+def test_packed_q4_0_against_portable(rows, cols, size):
+    """The packed x4/x1 kernels (dotPackedQ4_0x4AVX2 and dotPackedQ4_0AVX2
+    restated) against dotPackedQ4_0Go through matVecPackedQ4_0Rows (the
+    oracle): golem states they agree to rounding, not to the bit
+    (nn/pack_q4_0.go:128-133), so within 1e-5 of RMS per column; a batch's
+    column is bit-identical to the same column alone (the x1 kernel is the x4
+    kernel for one column) and to any thread count.  Sizes cover columns past
+    the last group of four and rows past one 2048-input tile (K_TILE)."""
+    g = synth.rng(rows + cols + size)
+    w = np.concatenate([golem_like_rows(g, cols) for _ in range(rows)])
+    packed = oracle.pack_q4_0(w, rows, cols)
+    b = oracle.Batch(synth.activations(g, size, cols)).quantize()
+    threads = oracle.host_threads()
+    oracle.cpu_lib(threads)
+    got = oracle.cpu_mat_vec_packed_q4_0(packed, b, rows, threads)
+    want = oracle.mat_vec_packed_q4_0_rows(packed, b, rows)
+    for c in range(size):
+        rel, at = oracle.compare_floats(got[c], want[c])
+        assert rel <= 1e-5, f"column {c}: {rel:.3g} of RMS at {at}"
+    one = oracle.cpu_mat_vec_packed_q4_0(packed, b, rows, 1)
+    np.testing.assert_array_equal(got.view(np.uint32), one.view(np.uint32))
+    for c in (0, size - 1):
+        bc = oracle.Batch(b.F[c:c + 1]).quantize()
+        alone = oracle.cpu_mat_vec_packed_q4_0(packed, bc, rows, threads)
+        np.testing.assert_array_equal(alone[0].view(np.uint32), got[c].view(np.uint32))
