@@ -229,6 +229,57 @@ __device__ __forceinline__ double norm_tree(double p0, double p1, double *red) {
     return s;
 }
 
+// x (+ add) of K values staged for a fused pre-norm: each value into xs
+// (LDS) and, when x_out is given, x_out; partial t of the tree (t < 512)
+// into red[t] (LDS).  Eight elements of a partial are loaded at a time, so a
+// thread waits for one round trip per 4096 values.
+__device__ __forceinline__ void norm_stage(const float *x, const float *add, int K, float *xs, float *x_out,
+                                           double *red) {
+    for (int pt = threadIdx.x; pt < 512; pt += blockDim.x) {
+        double acc = 0.0;
+        for (int base = 0; base < K; base += 8 * 512) {
+            float v[8], a[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+                v[u] = x[min(base + pt + 512 * u, K - 1)];
+            if (add) {
+#pragma unroll
+                for (int u = 0; u < 8; u++)
+                    a[u] = add[min(base + pt + 512 * u, K - 1)];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int i = base + pt + 512 * u;
+                if (i < K) {
+                    const float s = add ? v[u] + a[u] : v[u];
+                    xs[i] = s;
+                    if (x_out)
+                        x_out[i] = s;
+                    const float sq = s * s;
+                    acc += (double)sq;
+                }
+            }
+        }
+        red[pt] = acc;
+    }
+}
+
+// The tree over red[512] (LDS) by one wavefront: lane l pairs partials
+// l + 64 m itself (t + 256, then t + 128, then t + 64), then the shuffle
+// tree across lanes.  The sum is valid in lane 0.
+__device__ __forceinline__ double norm_tree_wave(const double *red) {
+    const int l = threadIdx.x & 63;
+    const double a = red[l] + red[l + 256], b = red[l + 64] + red[l + 320];
+    const double c = red[l + 128] + red[l + 384], d = red[l + 192] + red[l + 448];
+    double s = (a + c) + (b + d);
+    for (int w = 32; w > 0; w >>= 1) {
+        const double o = __shfl_down(s, w, 64);
+        if (l < w)
+            s = s + o;
+    }
+    return s;
+}
+
 __device__ __forceinline__ float norm_scale(double sum, int D, float eps) {
     const float mean = (float)(sum / (double)D);
     return (float)(1.0 / sqrt((double)(mean + eps)));

@@ -14,7 +14,7 @@
 // golem sums the same integers with an unsigned nibble and a cancelling
 // correction term (nn/dot_q4_0.go:64-66); the two agree to rounding.
 //
-// Three kernels:
+// Four kernels:
 //   q4_0_matvec_kernel<NC, UNITS>  a workgroup owns one 64-row tile, a
 //       wavefront whole stretches, a lane one row.  The stretch's activation
 //       is the same for all 64 lanes, so it is read with scalar loads into
@@ -33,6 +33,13 @@
 //       SwiGLU to a tile of gate and up rows interleaved by 32 and writes the
 //       Q8_0 block of its 32 outputs (qwen/block.go:82-90, nn/swiglu.go:
 //       77-82).
+//   q4_0_matvec_fused_lds_kernel<R>  the same pre-norm product without the
+//       SwiGLU epilogue on sub-tiles of R rows (lanes as in the LDS kernel),
+//       for a matrix whose whole tiles would leave most CUs idle.
+//
+// The norm's prologue is norm_stage + norm_tree_wave (gx_device.hpp): two
+// barriers where a tree halved through LDS took five (Q|K|V 6.82 -> 6.56 us,
+// Gate|Up 11.11 -> 10.78 us in a graph of launches over rotating copies).
 //
 // Where the weight loads go out.  Measured on the box (a HIP graph of
 // launches over rotating weight copies, config 3's shapes): issuing every
@@ -283,7 +290,6 @@ __global__ __launch_bounds__(1024) void q4_0_matvec_lds_kernel(
 //          32t .. 32t+31, then the same up rows): the tile's 32 outputs
 //          silu(gate) * up (SwiGLURange, nn/swiglu.go:77-82) go straight to
 //          their Q8_0 block t in q/scales/qsum, the down projection's input.
-constexpr int kFusedRegs = 8;  // staged values per thread: K <= 8 * threads
 
 // DB: two stretch slots a wavefront (double-buffered); without it a
 // wavefront has one slot and half the registers, so that two workgroups fit
@@ -309,18 +315,14 @@ __global__ __launch_bounds__(1024) void q4_0_matvec_fused_kernel(
     const uint8_t *qs_row = W + ((size_t)tile * B * kTileRows + lane) * kChunk;
     const uint8_t *d_row = W + plane0_bytes + ((size_t)tile * DC * kTileRows + lane) * kChunk;
 
-    // x (+ add) into registers first.  All sixteen loads are issued before
-    // the first wait: x and add in
-    // separate unconditional loops (add is uniform), so that staging costs
-    // one cache round trip rather than one per element.
-    float xv[kFusedRegs], av[kFusedRegs];
-#pragma unroll
-    for (int r = 0; r < kFusedRegs; r++)
-        xv[r] = x[min(tid + r * (int)blockDim.x, K - 1)];
-    if (add) {
-#pragma unroll
-        for (int r = 0; r < kFusedRegs; r++)
-            av[r] = add[min(tid + r * (int)blockDim.x, K - 1)];
+    // x (+ add) into LDS and the norm's partials (norm_stage), then its tree
+    // in wavefront 0: two barriers.
+    norm_stage(x, add, K, xs, blockIdx.x == 0 ? x_out : nullptr, red);
+    __syncthreads();
+    if (wave == 0) {
+        const double total = norm_tree_wave(red);
+        if (tid == 0)
+            scale_sh = norm_scale(total, K, eps);
     }
     // A wavefront's slot k is stretch wave + k*nwaves; every wavefront runs
     // the same number of slots (a slot past S loads stretch S - 1 again and
@@ -337,48 +339,6 @@ __global__ __launch_bounds__(1024) void q4_0_matvec_fused_kernel(
         dch = *(const uint4 *)(d_row + (size_t)sc_ * kTileRows * kChunk);                                            \
         gq = *(const float4 *)(gain + min(sc_ * kStretch * kQ4Block + 4 * lane, K - 4));                             \
     } while (0)
-    if (add) {
-#pragma unroll
-        for (int r = 0; r < kFusedRegs; r++)
-            xv[r] = xv[r] + av[r];
-    }
-#pragma unroll
-    for (int r = 0; r < kFusedRegs; r++) {
-        const int i = tid + r * (int)blockDim.x;
-        if (i < K) {
-            xs[i] = xv[r];
-            if (blockIdx.x == 0 && x_out)
-                x_out[i] = xv[r];
-        }
-    }
-    __syncthreads();
-    // RMSNormPlain's sum: partial t = elements t, t + 512, ... in order, then
-    // halved pairwise, exactly as the separate norm kernel.
-    for (int pt = tid; pt < 512; pt += blockDim.x) {
-        double acc = 0.0;
-        for (int i = pt; i < K; i += 512) {
-            const float v = xs[i];
-            const float sq = v * v;
-            acc += (double)sq;
-        }
-        red[pt] = acc;
-    }
-    __syncthreads();
-    for (int w = 256; w >= 64; w >>= 1) {
-        for (int i = tid; i < w; i += blockDim.x)
-            red[i] = red[i] + red[i + w];
-        __syncthreads();
-    }
-    if (tid < 64) {
-        double t = red[tid];
-        for (int w = 32; w > 0; w >>= 1) {
-            const double o = __shfl_down(t, w, 64);
-            if (tid < w)
-                t = t + o;
-        }
-        if (tid == 0)
-            scale_sh = norm_scale(t, K, eps);
-    }
     __syncthreads();
     const float sc = scale_sh;
     // The weights go out only now: with them in flight the norm's LDS steps
@@ -471,6 +431,113 @@ __global__ __launch_bounds__(1024) void q4_0_matvec_fused_kernel(
                 }
             }
         }
+    }
+}
+
+// The fused pre-norm product (EPI 0) on sub-tiles of R rows, so that a matrix
+// of few tiles spreads its weights over more CUs: a CU fetches only a few
+// tens of GB/s, so Q|K|V's 96 whole tiles on 96 of 256 CUs wait on their
+// CUs, not on HBM.  Each workgroup makes the whole activation (x + add, the
+// norm, Q8_0 of every block, four values a thread from its own float4) into
+// LDS and then multiplies as q4_0_matvec_lds_kernel does: lane l is row
+// l % R and stretch slot l / R.  Values, and so products, are the whole-tile
+// kernel's bit for bit.
+template <int R, bool DOTS>
+__global__ __launch_bounds__(1024) void q4_0_matvec_fused_lds_kernel(
+    const uint8_t *__restrict__ W, size_t plane0_bytes, int B, int DC, int group0, int row_start, int row_end,
+    float *__restrict__ y, const float *__restrict__ x, const float *__restrict__ add,
+    const float *__restrict__ gain, float eps, float *__restrict__ x_out, int32_t *__restrict__ dots) {
+    constexpr int kSlots = kTileRows / R;
+    extern __shared__ __align__(16) uint8_t lds_raw[];
+    __shared__ double red[512];
+    __shared__ float scale_sh;
+    const int K = B * kQ4Block;
+    const int S = (B + kStretch - 1) / kStretch;
+    float *part = (float *)lds_raw;
+    float *xs = (float *)(lds_raw + lds_part_bytes(S, R));
+    int8_t *qa = (int8_t *)(xs + K);
+    float *sa = (float *)(qa + K);
+    int32_t *qsa = (int32_t *)(sa + B);
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int g = group0 + blockIdx.x;
+    const int tile = g / kSlots, r = (g - tile * kSlots) * R + lane % R;
+    const int row = tile * kTileRows + r;
+    const bool in_range = row >= row_start && row < row_end;
+
+    // x (+ add) into LDS and the norm's partials, then its tree in
+    // wavefront 0 (as q4_0_matvec_fused_kernel)
+    const int n4 = K / 4;
+    const float4 gv = ((const float4 *)gain)[min(tid, n4 - 1)];
+    norm_stage(x, add, K, xs, blockIdx.x == 0 ? x_out : nullptr, red);
+    __syncthreads();
+    if (wave == 0) {
+        const double total = norm_tree_wave(red);
+        if (tid == 0)
+            scale_sh = norm_scale(total, K, eps);
+    }
+    __syncthreads();
+    const float sc = scale_sh;
+    // The weights go out now, behind the activation's loads.
+    const uint8_t *qs_row = W + ((size_t)tile * B * kTileRows + r) * kChunk;
+    const uint8_t *d_row = W + plane0_bytes + ((size_t)tile * DC * kTileRows + r) * kChunk;
+    const int st = wave * kSlots + lane / R;
+    uint4 wq[kStretch], dch;
+    if (wave * kSlots < S) {  // wavefronts past the last stretch load nothing
+        const int s = min(st, S - 1);
+#pragma unroll
+        for (int j = 0; j < kStretch; j++)
+            wq[j] = load_stream(qs_row + (size_t)min(s * kStretch + j, B - 1) * kTileRows * kChunk);
+        dch = *(const uint4 *)(d_row + (size_t)s * kTileRows * kChunk);
+    }
+    // Q8_0: thread i quantises values 4i .. 4i+3, eight threads a block.
+    {
+        const float4 xv = ((const float4 *)xs)[min(tid, n4 - 1)];
+        const float xa[4] = {xv.x, xv.y, xv.z, xv.w}, ga[4] = {gv.x, gv.y, gv.z, gv.w};
+        float v[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const float nv = xa[k] * sc;
+            v[k] = nv * ga[k];
+        }
+        float bstored;
+        int32_t bsum;
+        const uint32_t aq = q8_0_quad(v, &bstored, &bsum);
+        if (tid < n4) {
+            ((uint32_t *)qa)[tid] = aq;
+            if ((tid & 7) == 0) {
+                sa[tid >> 3] = bstored;
+                qsa[tid >> 3] = bsum;
+            }
+        }
+    }
+    lds_barrier();
+
+    // The lane's stretch, from +0 in block order.
+    if (st < S) {
+        const int b0 = st * kStretch;
+        const int nb = min(kStretch, B - b0);
+        float p = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kStretch; j++) {
+            if (j < nb) {
+                const int b = b0 + j;
+                const int4 *ap = (const int4 *)(qa + (size_t)b * kQ4Block);
+                const int32_t isum = q4_0_block_isum(wq[j], ap[0], ap[1], qsa[b]);
+                const float scl = chunk_half(dch, j) * sa[b];
+                p = fmaf((float)isum, scl, p);
+                if (DOTS && in_range)
+                    dots[(size_t)(row - row_start) * B + b] = isum;
+            }
+        }
+        part[st * R + lane % R] = p;
+    }
+    lds_barrier();
+    if (!DOTS && wave == 0 && lane < R && in_range) {
+        float acc = 0.0f;
+        for (int t = 0; t < S; t++)
+            acc = acc + part[t * R + lane];
+        y[row] = acc;
     }
 }
 
@@ -612,12 +679,32 @@ int launch_q4_0_matvec_fused(gx_ctx *ctx, const gx_weight *w, int epi, int row_s
                               int8_t *q, float *scales, int32_t *qsum, int32_t *dots) {
     const int B = w->blocks, K = w->cols;
     const int S = (B + kStretch - 1) / kStretch;
-    const int waves = min(S, 16);
-    GX_CHECK(K <= kFusedRegs * 64 * waves, "gx: a %d-input row is too wide for the fused norm", K);
-    const size_t lds = ((size_t)S * kTileRows + K) * sizeof(float);
-    GX_CHECK(lds <= 56 * 1024, "gx: a %d-input Q4_0 row is wider than this kernel's LDS", K);
     const int tile0 = row_start / kTileRows;
     const int grid = (row_end + kTileRows - 1) / kTileRows - tile0;
+    // Without the SwiGLU epilogue, a matrix whose whole tiles would fill at
+    // most half the CUs runs on half tiles (measured in a graph of launches
+    // over rotating copies, config 3's Q|K|V: 6.56 -> 6.29 us; quarter tiles
+    // 6.97, eighth tiles 9.8: every workgroup makes the whole activation).
+    {
+        constexpr int R = 32, slots = kTileRows / R;
+        const int waves = max((K / 4 + 63) / 64, (S + slots - 1) / slots);
+        const size_t lds = lds_part_bytes(S, R) + (size_t)K * sizeof(float) + lds_act_bytes(K, B);
+        if (epi == 0 && grid * slots <= ctx->cu_count && waves <= 16 && lds <= 56 * 1024 &&
+            ((uintptr_t)w->dev & 15) == 0 && ((uintptr_t)gain & 15) == 0) {
+            if (dots)
+                q4_0_matvec_fused_lds_kernel<R, true><<<grid * slots, 64 * waves, lds, ctx->stream>>>(
+                    w->dev, w->plane0_bytes, B, w->dchunks, tile0 * slots, row_start, row_end, y, x, add, gain, eps,
+                    x_out, dots);
+            else
+                q4_0_matvec_fused_lds_kernel<R, false><<<grid * slots, 64 * waves, lds, ctx->stream>>>(
+                    w->dev, w->plane0_bytes, B, w->dchunks, tile0 * slots, row_start, row_end, y, x, add, gain, eps,
+                    x_out, nullptr);
+            return check_launch("q4_0_matvec_fused_lds");
+        }
+    }
+    const int waves = min(S, 16);
+    const size_t lds = ((size_t)S * kTileRows + K) * sizeof(float);
+    GX_CHECK(lds <= 56 * 1024, "gx: a %d-input Q4_0 row is wider than this kernel's LDS", K);
 #define GX_FUSED(E, D, DD)                                                                                           \
     q4_0_matvec_fused_kernel<E, D, DD><<<grid, 64 * waves, lds, ctx->stream>>>(                                      \
         w->dev, w->plane0_bytes, B, w->dchunks, K, tile0, row_start, row_end, y, x, add, gain, eps, x_out, q, scales, \
