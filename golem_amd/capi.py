@@ -53,6 +53,9 @@ _SIGNATURES = {
     "gx_matmul_q4_0_expert": [_vp, _vp, _c_int, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _c_int],
     "gx_matmul_q6_k": [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _vp, _c_int],
     "gx_matmul_f32": [_vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _c_int],
+    "gx_matvec_rows_q4_0": [_vp, _vp, _vp, _vp, _vp, _c_int, ctypes.c_uint64, _c_int, _c_int, _vp, _c_int],
+    "gx_matvec_rows_q6_k": [_vp, _vp, _vp, _vp, _vp, _c_int, ctypes.c_uint64, _c_int, _c_int, _vp, _c_int],
+    "gx_matvec_rows_stats": [_vp, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)],
     "gx_q4_0_block_dots": [_vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp],
     "gx_q4_0_fused_block_dots": [_vp, _vp, _c_int, _vp, _vp, _vp, ctypes.c_float, _c_int, _c_int, _vp, _vp, _vp,
                                  _vp],

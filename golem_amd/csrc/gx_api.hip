@@ -8,6 +8,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
 #include <string>
 
 #include "gx_internal.hpp"
@@ -63,6 +64,99 @@ static int use(gx_ctx *ctx) {
     return GX_OK;
 }
 
+// The coalesced MatVecRows products (gx_matvec_rows_*): golem's engines call
+// MatVecRows on small row slices from pool workers (qwen/block.go:82-90,
+// qwen/attention.go:57-84, gemma/moe.go:151-161).  The first call of a
+// (matrix, activation, generation, M) computes every row once on the device
+// and copies the product to pinned host memory; every call then copies its
+// own rows from there.  A few products are kept, least recently used out.
+struct gx_rows_entry {
+    const gx_weight *w = nullptr;
+    const void *act = nullptr;
+    uint64_t generation = 0;
+    int M = 0;
+    bool valid = false;
+    uint64_t last_use = 0;
+    float *dev = nullptr;   // [M][rows], device
+    float *host = nullptr;  // its copy, pinned host memory
+    size_t cap = 0;         // floats each holds
+};
+constexpr int kRowsEntries = 16;
+struct gx_rows {
+    std::mutex mu;
+    gx_rows_entry e[kRowsEntries];
+    uint64_t clock = 0, products = 0, served = 0;
+};
+
+static void rows_release(gx_rows *r) {
+    if (r == nullptr)
+        return;
+    for (gx_rows_entry &e : r->e) {
+        (void)hipFree(e.dev);
+        (void)hipHostFree(e.host);
+    }
+    delete r;
+}
+
+// Serves rows [row_start, row_end) of every column of w's product with an
+// activation named by (act, generation, M); `product` writes the whole
+// product into a device buffer of M x rows floats.
+template <typename F>
+static int rows_serve(gx_ctx *ctx, const gx_weight *w, const void *act, uint64_t generation, int M, int row_start,
+                      int row_end, float *ys, int ldys, F &&product) {
+    gx_rows *r = ctx->rows;
+    std::lock_guard<std::mutex> lock(r->mu);
+    gx_rows_entry *hit = nullptr;
+    for (gx_rows_entry &e : r->e)
+        if (e.valid && e.w == w && e.act == act && e.generation == generation && e.M == M)
+            hit = &e;
+    if (hit == nullptr) {
+        hit = &r->e[0];
+        for (gx_rows_entry &e : r->e)
+            if (!e.valid || e.last_use < hit->last_use)
+                hit = &e;
+        hit->valid = false;
+        const size_t need = (size_t)M * w->rows;
+        if (hit->cap < need) {
+            (void)hipFree(hit->dev);
+            (void)hipHostFree(hit->host);
+            hit->dev = nullptr;
+            hit->host = nullptr;
+            hit->cap = 0;
+            GX_HIP(hipMalloc(&hit->dev, need * sizeof(float)));
+            GX_HIP(hipHostMalloc(&hit->host, need * sizeof(float), hipHostMallocDefault));
+            hit->cap = need;
+        }
+        if (int rc = product(hit->dev))
+            return rc;
+        GX_HIP(hipMemcpyAsync(hit->host, hit->dev, need * sizeof(float), hipMemcpyDeviceToHost, ctx->stream));
+        GX_HIP(hipStreamSynchronize(ctx->stream));
+        hit->w = w;
+        hit->act = act;
+        hit->generation = generation;
+        hit->M = M;
+        hit->valid = true;
+        r->products++;
+    }
+    hit->last_use = ++r->clock;
+    const int n = row_end - row_start;
+    for (int m = 0; m < M && n > 0; m++)
+        memcpy(ys + (size_t)m * ldys + row_start, hit->host + (size_t)m * w->rows + row_start, (size_t)n * sizeof(float));
+    r->served++;
+    return GX_OK;
+}
+
+static int rows_check(const gx_weight *w, int quant, int M, int row_start, int row_end, const float *ys, int ldys) {
+    GX_CHECK(w != nullptr, "gx: no weights");
+    GX_CHECK(w->quant == quant, "gx: the matrix is not %s", quant == GX_Q4_0 ? "Q4_0" : "Q6_K");
+    GX_CHECK(w->count == 1, "gx: a row-slice product takes a single matrix");
+    GX_CHECK(M >= 1, "gx: M must be at least 1, not %d", M);
+    GX_CHECK(row_start >= 0 && row_start <= row_end && row_end <= w->rows,
+             "nn: rows [%d, %d) outside a %d-row matrix", row_start, row_end, w->rows);
+    GX_CHECK(ys != nullptr && ldys >= row_end, "gx: ys must hold rows up to %d a column (ldys %d)", row_end, ldys);
+    return GX_OK;
+}
+
 extern "C" {
 
 const char *gx_last_error(void) { return g_error.c_str(); }
@@ -97,7 +191,9 @@ int gx_init(int device, gx_ctx **out) {
     ctx->scratch = nullptr;
     ctx->route_count = nullptr;
     ctx->route_scale = nullptr;
+    ctx->rows = new gx_rows();
     auto undo = [ctx]() {
+        rows_release(ctx->rows);
         (void)hipFree(ctx->route_count);
         (void)hipFree(ctx->route_scale);
         (void)hipFree(ctx->gelu_table);
@@ -155,6 +251,7 @@ int gx_free(gx_ctx *ctx) {
     (void)hipFree(ctx->argmax_i);
     (void)hipFree(ctx->route_count);
     (void)hipFree(ctx->route_scale);
+    rows_release(ctx->rows);
     delete ctx;
     return ok();
 }
@@ -335,6 +432,12 @@ int gx_weight_free(gx_weight *w) {
     if (w == nullptr)
         return ok();
     (void)hipSetDevice(w->ctx->device);
+    {  // a later matrix at the same address must not find this one's products
+        std::lock_guard<std::mutex> lock(w->ctx->rows->mu);
+        for (gx_rows_entry &e : w->ctx->rows->e)
+            if (e.w == w)
+                e.valid = false;
+    }
     (void)hipFree(w->dev);
     delete w;
     return ok();
@@ -520,6 +623,44 @@ int gx_matmul_q6_k(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const float
         return ok();
     if (int rc = gx::launch_q6_k_matvec(ctx, w, q, kscales, bsums, M, row_start, row_end, bias, y, ldy, nullptr))
         return rc;
+    return ok();
+}
+
+int gx_matvec_rows_q4_0(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const float *scales, const int32_t *qsum,
+                        int M, uint64_t generation, int row_start, int row_end, float *ys, int ldys) {
+    if (int rc = use(ctx))
+        return rc;
+    if (int rc = rows_check(w, GX_Q4_0, M, row_start, row_end, ys, ldys))
+        return rc;
+    GX_CHECK(w->ctx == ctx, "gx: the matrix belongs to another context");
+    if (int rc = rows_serve(ctx, w, q, generation, M, row_start, row_end, ys, ldys, [&](float *dev) {
+            return q4_0_product(ctx, w, 0, q, scales, qsum, nullptr, M, 0, w->rows, nullptr, dev, w->rows);
+        }))
+        return rc;
+    return ok();
+}
+
+int gx_matvec_rows_q6_k(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const float *kscales, const int16_t *bsums,
+                        int M, uint64_t generation, int row_start, int row_end, float *ys, int ldys) {
+    if (int rc = use(ctx))
+        return rc;
+    if (int rc = rows_check(w, GX_Q6_K, M, row_start, row_end, ys, ldys))
+        return rc;
+    GX_CHECK(w->ctx == ctx, "gx: the matrix belongs to another context");
+    if (int rc = rows_serve(ctx, w, q, generation, M, row_start, row_end, ys, ldys, [&](float *dev) {
+            return gx_matmul_q6_k(ctx, w, q, kscales, bsums, M, 0, w->rows, nullptr, dev, w->rows);
+        }))
+        return rc;
+    return ok();
+}
+
+int gx_matvec_rows_stats(gx_ctx *ctx, uint64_t *products, uint64_t *served) {
+    GX_CHECK(ctx != nullptr, "gx: no context");
+    std::lock_guard<std::mutex> lock(ctx->rows->mu);
+    if (products)
+        *products = ctx->rows->products;
+    if (served)
+        *served = ctx->rows->served;
     return ok();
 }
 

@@ -66,6 +66,7 @@ struct gx_ctx {
     uint8_t *scratch;   // this device's copy of the no-alloc entry points' static scratch (gx_api.hip)
     unsigned *route_count;  // the one-launch router's per-position counters [kRouteMaxPos], zero between calls
     float *route_scale;     // the many-position router's norm scales [kRouteScaleMax]
+    struct gx_rows *rows;   // the coalesced MatVecRows products (gx_api.hip)
 };
 
 

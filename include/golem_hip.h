@@ -170,6 +170,31 @@ int gx_matmul_q4_0_expert(gx_ctx *ctx, const gx_weight *w, int expert, const int
 int gx_matmul_q6_k(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const float *kscales, const int16_t *bsums,
                    int M, int row_start, int row_end, const float *bias, float *y, int ldy);
 
+/* Matrix.MatVecRows for golem's fine-grained callers (nn/matrix.go:84-92):
+ * its engines call it on 32-row slices from pool workers (qwen/block.go:
+ * 82-90, qwen/attention.go:57-84), which as one product each would be
+ * thousands of launches a token.  Here the first call for a (matrix,
+ * activation q, generation, M) computes every row of the product once on the
+ * device (gx_matmul_q4_0 / gx_matmul_q6_k) and copies it to pinned host
+ * memory; every call, that one included, then copies rows [row_start,
+ * row_end) of each column into ys[m * ldys + r] (host floats; ys holds full
+ * columns, ldys >= row_end), as MatVecRows fills ys[c][start:end].
+ * `generation` names the activation's contents: the caller changes it
+ * whenever q changes (after each Batch.Quantize* of the batch).  Calls may
+ * come from several threads at once: they serialise on the context's lock
+ * and share one product per key; the bias stays with the caller, as
+ * Matrix.rows adds it (nn/matrix.go:126-130).  The 16 most recent products
+ * are kept (device + pinned host copies, allocated once per size);
+ * gx_weight_free forgets a matrix's.  q4_0 takes the Q8_0 form, q6_k the
+ * Q8_K form, as the products do. */
+int gx_matvec_rows_q4_0(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const float *scales, const int32_t *qsum,
+                        int M, uint64_t generation, int row_start, int row_end, float *ys, int ldys);
+int gx_matvec_rows_q6_k(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const float *kscales, const int16_t *bsums,
+                        int M, uint64_t generation, int row_start, int row_end, float *ys, int ldys);
+/* Products computed and slices served so far by the two calls above (for
+ * checks).  No counterpart in golem. */
+int gx_matvec_rows_stats(gx_ctx *ctx, uint64_t *products, uint64_t *served);
+
 /* y[m][r] = DotF32(W[r], x[m]) for an F32 matrix (Matrix.rows' F32 case,
  * nn/matrix.go:113-120), in the generic DotF32 order (nn/dot_f32.go:13-33):
  * four interleaved accumulators, then (s0+s1)+(s2+s3). */
