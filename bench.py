@@ -402,20 +402,22 @@ def bench_c3(ctx, torch):
         model.use_slot(i)
         model.forward(prompt[i * slot_prompt:(i + 1) * slot_prompt], 0)
         firsts.append(int(model.next_token(slot_prompt - 1).item()))
-    model.start_slots(firsts, [slot_prompt] * nconv)
-    model.slots_step(nconv)  # warm
-    model.start_slots(firsts, [slot_prompt] * nconv)
-    torch.cuda.synchronize()
-    ctx.timer_start()
-    for _ in range(slot_steps):
-        model.slots_step(nconv)
-    slots_ms = ctx.timer_stop()
-    slot_step_ms = slots_ms / slot_steps
+    slot_ms = {}
+    for graph in (False, True):  # eager steps, then replays of the captured step
+        model.start_slots(firsts, [slot_prompt] * nconv)
+        model.slots_step(nconv, graph=graph)  # warm (and, for the graph, its capture)
+        model.start_slots(firsts, [slot_prompt] * nconv)
+        torch.cuda.synchronize()
+        ctx.timer_start()
+        for _ in range(slot_steps):
+            model.slots_step(nconv, graph=graph)
+        slot_ms[graph] = ctx.timer_stop() / slot_steps
+    slot_step_ms = slot_ms[True]
     model.free()
     return {"c3_qwen3_4b_slots": {
         "conversations": nconv, "prompt_each": slot_prompt, "steps": slot_steps,
         "ms_per_step": round(slot_step_ms, 3), "tok_per_s": round(nconv * 1e3 / slot_step_ms, 1),
-        "eager": True},
+        "graph": True, "eager_ms_per_step": round(slot_ms[False], 3)},
         "c3_qwen3_4b": {
         "prefill_tokens": len(prompt), "prefill_ms": round(prefill_ms, 2),
         "prefill_tok_per_s": round(len(prompt) / (prefill_ms * 1e-3), 1),

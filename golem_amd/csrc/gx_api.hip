@@ -686,16 +686,17 @@ int gx_q4_0_block_dots(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const f
         return rc;
     GX_CHECK(q && qsum && scales, "gx: missing activation");
     GX_CHECK(((uintptr_t)q & 15) == 0, "gx: q must be 16-byte aligned");
-    GX_CHECK(path >= 0 && path <= 3,
-             "gx: path must be 0 (matrix-vector), 1 (int8 MFMA), 2 (fp16 MFMA) or 3 (one-column matrix-vector)");
+    GX_CHECK(path >= 0 && path <= 4,
+             "gx: path must be 0 (matrix-vector), 1 (int8 MFMA), 2 (fp16 MFMA), 3 (one-column matrix-vector) or 4 "
+             "(multi-column matrix-vector)");
     GX_CHECK(path != 2 || (q16 && ((uintptr_t)q16 & 15) == 0), "gx: path 2 needs a 16-byte aligned q16");
     GX_CHECK(path != 3 || M == 1, "gx: path 3 takes one column, not %d", M);
     if (M == 0 || row_start == row_end)
         return ok();
     int rc;
-    if (path == 0 || path == 3)
+    if (path == 0 || path == 3 || path == 4)
         rc = gx::launch_q4_0_matvec(ctx, w, w->dev, q, scales, qsum, M, row_start, row_end, nullptr, nullptr, 0, out,
-                                    path == 0 ? 0 : 1);
+                                    path == 0 ? 0 : path == 3 ? 1 : 2);
     else if (path == 1)
         rc = gx::launch_q4_0_gemm(ctx, w, w->dev, q, scales, M, row_start, row_end, nullptr, nullptr, 0, out);
     else

@@ -14,7 +14,7 @@
 // golem sums the same integers with an unsigned nibble and a cancelling
 // correction term (nn/dot_q4_0.go:64-66); the two agree to rounding.
 //
-// Four kernels:
+// Five kernels:
 //   q4_0_matvec_kernel<NC, UNITS>  a workgroup owns one 64-row tile, a
 //       wavefront whole stretches, a lane one row.  The stretch's activation
 //       is the same for all 64 lanes, so it is read with scalar loads into
@@ -33,6 +33,8 @@
 //       SwiGLU to a tile of gate and up rows interleaved by 32 and writes the
 //       Q8_0 block of its 32 outputs (qwen/block.go:82-90, nn/swiglu.go:
 //       77-82).
+//   q4_0_matvec_cols_kernel<R, NC>  2..8 columns: every column's
+//       activation staged in LDS at once, on whole, half or quarter tiles.
 //   q4_0_matvec_fused_lds_kernel<R>  the same pre-norm product without the
 //       SwiGLU epilogue on sub-tiles of R rows (lanes as in the LDS kernel),
 //       for a matrix whose whole tiles would leave most CUs idle.
@@ -272,6 +274,119 @@ __global__ __launch_bounds__(1024) void q4_0_matvec_lds_kernel(
         for (int t = 0; t < S; t++)
             acc = acc + part[t * R + lane];
         y[row] = bias ? acc + bias[row] : acc;
+    }
+}
+
+// NC columns (2 <= M <= 8 as the product groups them) on tiles of R rows:
+// the whole activation of the NC columns is staged in LDS first (one round
+// trip; the whole-tile kernel's per-block scalar loads, NC of them in a row
+// per stretch, were a chain of cache round trips), and the R-row shape
+// spreads a matrix of few tiles over more CUs (golem's lock-step slots read
+// O and Down, 40 tiles each, at M = 8).  Lane l is row l % R and stretch
+// slot l / R; it sums its stretch for every column from +0 in block order,
+// and thread (c, r) then adds column c's stretch sums of row r in order:
+// each column is the one-column kernels' bit for bit.
+constexpr int kColRegs = 8;  // staged 16-byte activation pieces per thread per pass
+
+__host__ __device__ inline size_t cols_lds_bytes(int S, int R, int NC, int K, int B) {
+    return lds_part_bytes(S * NC, R) + lds_act_bytes(NC * K, NC * B);
+}
+
+template <int R, int NC, bool DOTS>
+__global__ __launch_bounds__(1024) void q4_0_matvec_cols_kernel(
+    const uint8_t *__restrict__ W, size_t plane0_bytes, int B, int DC, const int8_t *__restrict__ q,
+    const float *__restrict__ scales, const int32_t *__restrict__ qsum, int group0, int row_start, int row_end,
+    const float *__restrict__ bias, float *__restrict__ y, int ldy, int32_t *__restrict__ dots) {
+    constexpr int kSlots = kTileRows / R;
+    extern __shared__ __align__(16) uint8_t lds_raw[];
+    const int K = B * kQ4Block;
+    const int S = (B + kStretch - 1) / kStretch;
+    float *part = (float *)lds_raw;  // [S][NC][R]
+    int8_t *qa = (int8_t *)(lds_raw + lds_part_bytes(S * NC, R));  // [NC][K]
+    float *sa = (float *)(qa + (size_t)NC * K);                     // [NC][B]
+    int32_t *qsa = (int32_t *)(sa + NC * B);                         // [NC][B]
+    const int tid = threadIdx.x, nt = blockDim.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int g = group0 + blockIdx.x;
+    const int tile = g / kSlots, r = (g - tile * kSlots) * R + lane % R;
+    const int row = tile * kTileRows + r;
+    const bool in_range = row >= row_start && row < row_end;
+    const int st = wave * kSlots + lane / R;  // this lane's stretch
+
+    // The weights first (they do not depend on the activation), then the
+    // activation of the NC columns (rows q[c] are consecutive), every load of
+    // a pass in flight together, into LDS.
+    const uint8_t *qs_row = W + ((size_t)tile * B * kTileRows + r) * kChunk;
+    const uint8_t *d_row = W + plane0_bytes + ((size_t)tile * DC * kTileRows + r) * kChunk;
+    uint4 wq[kStretch], dch;
+    if (wave * kSlots < S) {  // wavefronts past the last stretch load nothing
+        const int sc = min(st, S - 1);
+#pragma unroll
+        for (int j = 0; j < kStretch; j++)
+            wq[j] = load_stream(qs_row + (size_t)min(sc * kStretch + j, B - 1) * kTileRows * kChunk);
+        dch = *(const uint4 *)(d_row + (size_t)sc * kTileRows * kChunk);
+    }
+    const int n16 = NC * K / 16, nb = NC * B;
+    for (int base = 0; base < max(n16, nb); base += kColRegs * nt) {
+        int4 qv[kColRegs];
+        float sv[kColRegs];
+        int32_t qsv[kColRegs];
+#pragma unroll
+        for (int k = 0; k < kColRegs; k++) {
+            const int i = base + tid + k * nt;
+            qv[k] = ((const int4 *)q)[min(i, n16 - 1)];
+            sv[k] = scales[min(i, nb - 1)];
+            qsv[k] = qsum[min(i, nb - 1)];
+        }
+#pragma unroll
+        for (int k = 0; k < kColRegs; k++) {
+            const int i = base + tid + k * nt;
+            if (i < n16)
+                ((int4 *)qa)[i] = qv[k];
+            if (i < nb) {
+                sa[i] = sv[k];
+                qsa[i] = qsv[k];
+            }
+        }
+    }
+    lds_barrier();
+
+    if (st < S) {
+        const int b0 = st * kStretch;
+        const int nbk = min(kStretch, B - b0);
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            const int8_t *qc = qa + (size_t)c * K;
+            float p = 0.0f;
+#pragma unroll
+            for (int j = 0; j < kStretch; j++) {
+                if (j < nbk) {
+                    const int b = b0 + j;
+                    const int4 *ap = (const int4 *)(qc + (size_t)b * kQ4Block);
+                    const int32_t isum = q4_0_block_isum(wq[j], ap[0], ap[1], qsa[c * B + b]);
+                    const float scl = chunk_half(dch, j) * sa[c * B + b];
+                    p = fmaf((float)isum, scl, p);
+                    if (DOTS && in_range)
+                        dots[((size_t)c * (row_end - row_start) + (row - row_start)) * B + b] = isum;
+                }
+            }
+            part[(st * NC + c) * R + lane % R] = p;
+        }
+    }
+    lds_barrier();
+    if (!DOTS) {
+        for (int pr = tid; pr < NC * R; pr += nt) {
+            const int c = pr / R, rr = pr - c * R;
+            const int orow = tile * kTileRows + (g - tile * kSlots) * R + rr;
+            if (orow >= row_start && orow < row_end) {
+                float acc = 0.0f;
+                for (int t = 0; t < S; t++)
+                    acc = acc + part[(t * NC + c) * R + rr];
+                if (bias)
+                    acc = acc + bias[orow];
+                y[(size_t)c * ldy + orow] = acc;
+            }
+        }
     }
 }
 
@@ -584,6 +699,58 @@ bool lds_fits(const gx_weight *w, int *it, int *waves, size_t *lds) {
     return false;
 }
 
+// The multi-column kernel's shape for NC columns: whole tiles when they
+// give enough workgroups to keep most CUs fetching, else half or quarter
+// tiles; every stretch in one pass of at most 16 wavefronts; LDS within
+// 64 KiB.
+bool cols_shape(const gx_ctx *ctx, const gx_weight *w, int tiles, int NC, int *R, int *waves, size_t *lds) {
+    const int B = w->blocks, K = w->cols, S = (B + kStretch - 1) / kStretch;
+    const int want = ctx->cu_count * 3 / 5;
+    const int rs[3] = {64, 32, 16};
+    for (int i = 0; i < 3; i++) {
+        const int r = rs[i], slots = kTileRows / r;
+        const int wv = (S + slots - 1) / slots;
+        const size_t bytes = cols_lds_bytes(S, r, NC, K, B);
+        if (wv > 16 || bytes > 64 * 1024)
+            continue;
+        if (tiles * slots >= want || r == 16) {
+            *R = r;
+            *waves = wv;
+            *lds = bytes;
+            return true;
+        }
+    }
+    return false;
+}
+
+template <int NC>
+int launch_cols(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, const int8_t *q, const float *scales,
+                const int32_t *qsum, int R, int waves, size_t lds, int row_start, int row_end, const float *bias,
+                float *y, int ldy, int32_t *dots) {
+    const int tile0 = row_start / kTileRows;
+    const int tiles = (row_end + kTileRows - 1) / kTileRows - tile0;
+    const int slots = kTileRows / R;
+    const unsigned grid = (unsigned)(tiles * slots), threads = (unsigned)(64 * waves);
+#define GX_COLS(RR, DD)                                                                                              \
+    q4_0_matvec_cols_kernel<RR, NC, DD><<<grid, threads, lds, ctx->stream>>>(                                        \
+        mat, w->plane0_bytes, w->blocks, w->dchunks, q, scales, qsum, tile0 * slots, row_start, row_end, bias, y,    \
+        ldy, dots)
+    if (R == 64 && dots)
+        GX_COLS(64, true);
+    else if (R == 64)
+        GX_COLS(64, false);
+    else if (R == 32 && dots)
+        GX_COLS(32, true);
+    else if (R == 32)
+        GX_COLS(32, false);
+    else if (dots)
+        GX_COLS(16, true);
+    else
+        GX_COLS(16, false);
+#undef GX_COLS
+    return check_launch("q4_0_matvec_cols");
+}
+
 }  // namespace
 
 int launch_q4_0_matvec(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, const int8_t *q, const float *scales,
@@ -618,15 +785,64 @@ int launch_q4_0_matvec(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, cons
         }
         GX_CHECK(form != 1, "gx: a %d-input Q4_0 row does not fit the one-column kernel", w->cols);
     }
-    // Columns in groups of 8, 4, 2, 1, each group reading the weights once;
-    // the per-column arithmetic is the same whatever the group.  Very wide
-    // rows keep the group narrow enough for the stretch sums to fit in LDS.
-    int c = 0;
     const int K = w->cols, B = w->blocks;
+    const size_t nrows = (size_t)(row_end - row_start);
+    // Two to eight columns (or form 2): the LDS-staged kernel, columns in
+    // groups of 8, 4, 2, 1 as its LDS allows, each group reading the weights
+    // once.  Measured at config 3's shapes and M = 8 (eight lock-step
+    // conversations, kernel trace), against the whole-tile kernel: Down
+    // 2 x 21.6 -> 2 x 11.7 us, O 17.7 -> 12.4, Q|K|V 15.8 -> 13.7, Gate|Up
+    // 27.8 -> 28.7 (whole tiles either way).
+    if ((M >= 2 && form != 0) || form == 2) {
+        int c = 0;
+        while (c < M) {
+            const int left = M - c;
+            int NC = 0, R = 0, waves = 0;
+            size_t lds = 0;
+            const int widths[4] = {8, 4, 2, 1};
+            for (int i = 0; i < 4 && NC == 0; i++)
+                if (widths[i] <= left && cols_shape(ctx, w, tiles, widths[i], &R, &waves, &lds))
+                    NC = widths[i];
+            if (NC == 0)
+                break;  // too wide for the LDS: the whole-tile kernel below
+            const int8_t *qc = q + (size_t)c * K;
+            const float *sc = scales + (size_t)c * B;
+            const int32_t *qs = qsum + (size_t)c * B;
+            float *yc = y ? y + (size_t)c * ldy : nullptr;
+            int32_t *dc = dots ? dots + (size_t)c * nrows * B : nullptr;
+            int rc;
+            if (NC == 8)
+                rc = launch_cols<8>(ctx, w, mat, qc, sc, qs, R, waves, lds, row_start, row_end, bias, yc, ldy, dc);
+            else if (NC == 4)
+                rc = launch_cols<4>(ctx, w, mat, qc, sc, qs, R, waves, lds, row_start, row_end, bias, yc, ldy, dc);
+            else if (NC == 2)
+                rc = launch_cols<2>(ctx, w, mat, qc, sc, qs, R, waves, lds, row_start, row_end, bias, yc, ldy, dc);
+            else
+                rc = launch_cols<1>(ctx, w, mat, qc, sc, qs, R, waves, lds, row_start, row_end, bias, yc, ldy, dc);
+            if (rc)
+                return rc;
+            c += NC;
+        }
+        if (c == M)
+            return GX_OK;
+        GX_CHECK(form != 2, "gx: a %d-input Q4_0 row does not fit the multi-column kernel", w->cols);
+        q += (size_t)c * K;
+        scales += (size_t)c * B;
+        qsum += (size_t)c * B;
+        if (y)
+            y += (size_t)c * ldy;
+        if (dots)
+            dots += (size_t)c * nrows * B;
+        M -= c;
+    }
+    // Columns in groups of 8, 4, 2, 1 on whole tiles with the activation in
+    // scalar registers, each group reading the weights once; the per-column
+    // arithmetic is the same whatever the group.  Very wide rows keep the
+    // group narrow enough for the stretch sums to fit in LDS.
+    int c = 0;
     const size_t per_column = (size_t)((B + kStretch - 1) / kStretch) * kTileRows * sizeof(float);
     const int widest = per_column * 8 <= 64 * 1024 ? 8 : per_column * 4 <= 64 * 1024 ? 4
                      : per_column * 2 <= 64 * 1024 ? 2 : 1;
-    const size_t nrows = (size_t)(row_end - row_start);
     while (c < M) {
         const int left = M - c;
         const int8_t *qc = q + (size_t)c * K;

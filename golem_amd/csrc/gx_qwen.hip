@@ -867,12 +867,17 @@ __global__ __launch_bounds__(kDecodeThreads) void attn_decode_kernel(
 // prologue's cache stores and the value loads stay in flight across them.
 // With FUSE wavefront 0 does the prologue alone and the other seven the
 // cache work; without it all eight do.
+// The value runs are fixed (kRuns runs of kXChunk positions, whatever the
+// launch's extent and in both forms), so that a token's result depends on
+// its prefix only: a step replayed from a graph launched for the whole cache
+// equals the same step launched for its own prefix, bit for bit.
 template <bool FUSE>
 struct ParShape {
     static constexpr int kW0 = FUSE ? 1 : 0;                           // wavefronts out of the cache work
     static constexpr int kCT = kDecodeThreads - 64 * kW0;              // cache threads
-    static constexpr int kRuns = kCT / kValSlice;                      // position runs of the value sums
-    static constexpr int kPieces = (kDecodeMax + 8 * kRuns - 1) / (8 * kRuns) + 1;  // value pieces a thread holds
+    static constexpr int kRuns = (kDecodeThreads - 64) / kValSlice;    // position runs of the value sums
+    static constexpr int kXChunk = ((kDecodeMax + kRuns - 1) / kRuns + 7) & ~7;  // positions a run
+    static constexpr int kPieces = kXChunk / 8;                        // value pieces a thread holds
     static constexpr int kRows = (kDecodeMax + kCT - 1) / kCT;         // positions a thread scores
 };
 constexpr int kParProbs = kDecodeMax + 64;  // probabilities in LDS: up to the end of the last run
@@ -887,7 +892,7 @@ __global__ __launch_bounds__(kDecodeThreads) void attn_par_kernel(
     __shared__ __align__(16) uint16_t nk[HD];                   // FUSE: this position's key
     __shared__ uint16_t nvl[kValSlice];                         // FUSE: this position's values of the slice
     using Sh = ParShape<FUSE>;
-    static_assert(Sh::kRuns * (((kDecodeMax + Sh::kRuns - 1) / Sh::kRuns + 7) & ~7) <= kParProbs, "runs fit");
+    static_assert(Sh::kRuns * Sh::kXChunk <= kParProbs && Sh::kRuns * Sh::kXChunk >= kDecodeMax, "runs fit");
     static_assert(Sh::kRows * Sh::kCT >= kParProbs - 8, "the probability rows are covered");
     __shared__ __align__(16) uint16_t ps[kParProbs];            // probabilities, fp16
     __shared__ float redm[kDecodeThreads / 64], reds[kDecodeThreads / 64];
@@ -946,7 +951,8 @@ __global__ __launch_bounds__(kDecodeThreads) void attn_par_kernel(
     const bool cw = !(FUSE && wave == 0);                 // a cache wavefront
     const int ct = tid - 64 * Sh::kW0, cwave = wave - Sh::kW0;  // its thread and wavefront among them
     const int gi = ct / kValSlice, dd = ct % kValSlice;
-    const int xchunk = ((limit + Sh::kRuns - 1) / Sh::kRuns + 7) & ~7;  // positions per value run
+    constexpr int xchunk = Sh::kXChunk;                  // positions per value run
+    const bool vrun = cw && gi < Sh::kRuns;              // a thread of a value run
     if (cw) {
         // key rows: position ct + kCT r, a row only in wavefronts that reach it
         const v4u_stream *kbase = (const v4u_stream *)(kcache + (size_t)kvh * HD * context);
@@ -961,9 +967,9 @@ __global__ __launch_bounds__(kDecodeThreads) void attn_par_kernel(
         }
         // value pieces: run gi of xchunk positions (a multiple of 8), element dd
         const uint16_t *vrow = vcache + ((size_t)kvh * HD + d0 + dd) * context;
+        if (vrun) {
 #pragma unroll
-        for (int u = 0; u < Sh::kPieces; u++) {
-            if (8 * u < xchunk) {
+            for (int u = 0; u < Sh::kPieces; u++) {
                 const int p0 = min(gi * xchunk + 8 * u, (limit - 1) & ~7);
                 vr[u] = *(const v4u_stream *)(vrow + p0);
             }
@@ -1139,7 +1145,7 @@ __global__ __launch_bounds__(kDecodeThreads) void attn_par_kernel(
 #pragma unroll
     for (int u = 0; u < Sh::kPieces; u++) {
         const int p0 = gi * xchunk + 8 * u;
-        if (cw && 8 * u < xchunk && p0 < n) {
+        if (vrun && p0 < n) {
             const v4u_stream pp = *(const v4u_stream *)(ps + p0);
             v4u_stream vv = vr[u];
             if (FUSE && pos >= p0 && pos < p0 + 8) {  // this position's value from the copy
@@ -1176,7 +1182,7 @@ __global__ __launch_bounds__(kDecodeThreads) void attn_par_kernel(
             }
         }
     }
-    if (cw)
+    if (vrun)
         vpart[gi][dd] = acc;
     lds_barrier();
     if (tid < kValSlice) {

@@ -96,6 +96,7 @@ class QwenModel:
             raise ValueError(f"qwen: attention order {attention!r}")
         self.ctx, self.cfg, self.max_batch = ctx, cfg, max_batch
         self.graph = None
+        self.slot_graphs = {}  # captured lock-step slot steps, by conversation count
         self.set_attention(attention)
         vp, call = capi.vp, capi.call
         qd, kvd = cfg.heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim
@@ -151,6 +152,7 @@ class QwenModel:
         self.pos_dev = torch.zeros((1,), dtype=torch.int32, device="cuda")  # the graph's position counter
         self.history = torch.zeros((cfg.max_context + 1,), dtype=torch.int32, device="cuda")
         self.graph = None
+        self.slot_graphs = {}
         n = capi.size_out("gx_qwen_attention_workspace_bytes", M, cfg.heads, cfg.max_context - 1)
         self.attn_ws = torch.empty((n + 255) // 256 * 256, dtype=torch.uint8, device="cuda")
         self._vp, self._call = vp, call
@@ -178,6 +180,7 @@ class QwenModel:
         sfx = "_parallel" if attention == "parallel" else ""
         self._rope_attention, self._attention = "gx_qwen_rope_attention" + sfx, "gx_qwen_attention" + sfx
         self.graph = None
+        self.slot_graphs = {}
 
     def set_slots(self, n):
         """SetSlots (qwen/slots.go:19-37): n independent conversations, each
@@ -187,6 +190,7 @@ class QwenModel:
         if self.cfg.max_context // n < 1:
             raise ValueError(f"qwen: a context of {self.cfg.max_context} cut into {n} slots leaves no position each")
         self.graph = None  # a captured step addressed the caches being replaced
+        self.slot_graphs = {}
         self._make_caches(n)
 
     def use_slot(self, i):
@@ -401,21 +405,51 @@ class QwenModel:
             self.slot_ids[:n].copy_(torch.arange(n, dtype=torch.int32))
         self._slot_pos = list(positions)
 
-    def slots_step(self, n):
+    def slots_step(self, n, graph=False):
         """One lock-step decode step of conversations 0 .. n-1 from the
         tokens and positions on the device (the server's batch of slots,
         cmd/golem-server/runner.go:233-297): one pass over the weights and one
         head read for all n; the next ids replace the tokens (and stay in
-        next_id[:n]) and every position advances."""
+        next_id[:n]) and every position advances.  graph: the step as a
+        replay of its captured form (capture_slots), the same values bit for
+        bit."""
         top = max(self._slot_pos)
         if top >= self.slot_context:
             raise ValueError(f"qwen: position {top} is past a slot's {self.slot_context}")
-        self._blocks(n, top)
+        if graph:
+            self.capture_slots(n)
+            self.slot_graphs[n].replay()
+        else:
+            self._slots_device_step(n, top)
+        self._slot_pos = [p + 1 for p in self._slot_pos]
+        return self.next_id[:n]
+
+    def _slots_device_step(self, n, max_pos):
+        self._blocks(n, max_pos)
         self.next_tokens(range(n))
         self.tokens[:n].copy_(self.next_id[:n])
         self.positions[:n].add_(1)
-        self._slot_pos = [p + 1 for p in self._slot_pos]
-        return self.next_id[:n]
+
+    def capture_slots(self, n):
+        """Records the device work of slots_step(n) into a HIP graph (once per
+        n): the attention is launched for a slot's whole context and each
+        token stops at its own prefix, read from the device, so one recording
+        serves every step."""
+        if self.slot_graphs.get(n) is not None:
+            return
+        if not 0 < n <= min(self.nslots, self.max_batch):
+            raise ValueError(f"qwen: {n} conversations for {self.nslots} slots")
+        torch.cuda.synchronize()
+        stream = torch.cuda.Stream()
+        graph = torch.cuda.CUDAGraph()
+        self._call("gx_set_stream", self.ctx.ptr, ctypes.c_void_p(stream.cuda_stream))
+        try:
+            with torch.cuda.graph(graph, stream=stream):
+                self._slots_device_step(n, self.slot_context - 1)
+        finally:
+            self._call("gx_set_stream", self.ctx.ptr, None)
+        torch.cuda.synchronize()
+        self.slot_graphs[n] = graph
 
     def logits_batch(self, rows):
         """LogitsBatch (qwen/model.go:200-214): the logits of several hidden

@@ -17,7 +17,9 @@
  * unless gx_set_stream chose another); calls return once it is enqueued.
  * gx_sync waits for it.  A context is not meant to be driven by several host
  * threads at once: golem serialises its parallel sections with a mutex
- * (nn/parallel.go:163-191) and a shim does the same.
+ * (nn/parallel.go:163-191) and a shim does the same.  The row-slice products
+ * (gx_matvec_rows_*) are the exception: they take the context's lock
+ * themselves, for golem's pool workers.
  *
  * Layouts on the device.
  *   Q8_0 activations (golem's Batch.Q/Scales/Corr, nn/batch.go:17-27), one
@@ -149,8 +151,10 @@ int gx_quantize_q8_k(gx_ctx *ctx, const float *x, int ldx, int M, int K, int8_t 
  * rows r in [row_start, row_end) of a Q4_0 matrix: Matrix.MatVecBatch and
  * MatVecRows for Q4_0 (nn/matrix.go:78-104), and MatVecQ4_0
  * (nn/dot_q4_0.go:117-124) when the range is all rows.  bias is NULL or
- * rows floats (device).  M <= 8 runs the bandwidth-bound matrix-vector
- * kernel; larger M runs an MFMA product: on fp16 MFMA when q16 is given,
+ * rows floats (device).  M <= 8 runs a bandwidth-bound matrix-vector
+ * kernel (one column: activation in scalar registers, or in LDS on quarter
+ * tiles for a matrix of few tiles; 2..8 columns: activations in LDS, on whole,
+ * half or quarter tiles); larger M runs an MFMA product: on fp16 MFMA when q16 is given,
  * else on int8 MFMA.  All of them sum every row's blocks in the same order
  * from the same exact per-block integers, so a column's result does not
  * depend on M or on the kernel. */
@@ -213,8 +217,11 @@ int gx_matmul_f32(gx_ctx *ctx, const gx_weight *w, const float *x, int ldx, int 
  * product without q16 runs); path 2: the fp16-MFMA product (needs q16);
  * path 3: the one-column matrix-vector kernel with the activation in LDS
  * (M = 1, the whole/half/quarter-tile shape the product picks for this
- * matrix).  golem's dotQ4_0Go accumulator (nn/dot_q4_0.go:58-63) is this plus
- * 8*qsum.  No counterpart in golem: parity instrumentation. */
+ * matrix); path 4: the multi-column matrix-vector kernel with the
+ * activations in LDS (what products of 2 <= M <= 8 run, in the column groups
+ * and tile shape the product picks).  golem's dotQ4_0Go accumulator
+ * (nn/dot_q4_0.go:58-63) is this plus 8*qsum.  No counterpart in golem:
+ * parity instrumentation. */
 int gx_q4_0_block_dots(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const float *scales, const int32_t *qsum,
                        const uint16_t *q16, int M, int row_start, int row_end, int path, int32_t *out);
 

@@ -57,7 +57,7 @@ def test_dequantized_rows_cover_every_half(dev, orc):
 
 @pytest.mark.parametrize("rows,cols,M", [(64, 256, 1), (200, 2560, 3), (96, 704, 9), (130, 2816, 40),
                                          (300, 2560, 1)])
-@pytest.mark.parametrize("path", [0, 1, 2, 3])
+@pytest.mark.parametrize("path", [0, 1, 2, 3, 4])
 def test_block_integers_bit_exact(dev, orc, rows, cols, M, path):
     if path == 3 and M != 1:
         pytest.skip("the one-column kernel takes M = 1")
@@ -68,6 +68,35 @@ def test_block_integers_bit_exact(dev, orc, rows, cols, M, path):
     acc = orc.q4_0_block_acc(w, b, rows)[:, start:end, :]
     qsum = b.qsum_rows()[:, None, :]
     np.testing.assert_array_equal(got, acc - 8 * qsum)
+
+
+@pytest.mark.parametrize("rows,cols,M,span", [
+    (2560, 9728, 8, (0, 2560)),     # Down at 8 columns: two groups of 4 on quarter tiles
+    (2560, 4096, 5, (17, 2500)),    # O: a group of 4 and one column, a range that cuts quarter tiles
+    (6144, 2560, 8, (0, 6144)),     # Q|K|V: half tiles
+    (19456, 2560, 3, (64, 19456)),  # Gate|Up: whole tiles
+    (9728, 2560, 2, (0, 9728)),     # config 0's matrix
+])
+def test_multi_column_integers_every_shape(dev, orc, rows, cols, M, span):
+    """Path 4 -- the multi-column kernel golem's lock-step slots run (2 to 8
+    columns) -- bit for bit against golem's accumulator, and every column of
+    its product equal to that column's one-column product bit for bit
+    (golem's batch == one at a time, nn/dot_q4_0.go:143-146)."""
+    log(f"multi-column dots rows={rows} cols={cols} M={M} span={span}")
+    w, b, wd, act = setup(dev, orc, rows, cols, M, 900 + rows + M)
+    start, end = span
+    got = dev.q4_0_block_dots(wd, act, M, start, end, 4)
+    acc = orc.q4_0_block_acc(w, b, rows)[:, start:end, :]
+    np.testing.assert_array_equal(got, acc - 8 * b.qsum_rows()[:, None, :])
+    y = dev.get(dev.matmul_q4_0(wd, act, M, start, end))
+    q, sc, qs = act[:3]
+    for m in range(M):
+        y1 = dev.full((1, rows), float("nan"))
+        capi.call("gx_matmul_q4_0", dev.ctx.ptr, wd.ptr, capi.vp(q[m:m + 1]), capi.vp(sc[m:m + 1]),
+                  capi.vp(qs[m:m + 1]), None, 1, start, end, None, capi.vp(y1), rows)
+        y1 = dev.get(y1)[0]
+        np.testing.assert_array_equal(y[m, start:end].view(np.uint32), y1[start:end].view(np.uint32))
+    assert np.isnan(y[:, :start]).all() and np.isnan(y[:, end:]).all()
 
 
 @pytest.mark.parametrize("rows,cols,span", [
@@ -90,7 +119,7 @@ def test_one_column_integers_every_shape(dev, orc, rows, cols, span):
     y = dev.get(dev.matmul_q4_0(wd, act, 1, start, end))[0]
     q, sc, qs = act[:3]
     y2 = dev.full((2, rows), float("nan"))
-    # two columns, the second a copy of the first: the SGPR kernel computes both
+    # two columns, the second a copy of the first: the multi-column kernel computes both
     q2, sc2, qs2 = (torch_cat2(dev, t) for t in (q, sc, qs))
     capi.call("gx_matmul_q4_0", dev.ctx.ptr, wd.ptr, capi.vp(q2), capi.vp(sc2), capi.vp(qs2), None, 2, start, end,
               None, capi.vp(y2), rows)

@@ -154,6 +154,52 @@ def test_lock_step_decode_draws_each_conversations_tokens(dev, nconv):
     m.free()
 
 
+@pytest.mark.parametrize("nconv", [3, 6])
+def test_captured_slot_steps_match_eager(dev, nconv):
+    """slots_step as replays of its captured form (capture_slots): the ids
+    after every step, and at the end every cache and the hidden states, bit
+    for bit those of the eager steps.  An eager step launches the attention
+    for its own longest prefix, the captured one for the whole slot; each
+    token stops at its own prefix and the parallel attention's value runs
+    are fixed, so the two agree.  (A small random model repeats its ids; the
+    caches, which hold every step's keys and values, and the hidden states
+    carry the check.)  Each replay is followed by eager work (the check) and
+    a synchronisation."""
+    cfg = synth.QwenConfig(256, 512, 2, 4, 2, 64, 1024, 16 * nconv)
+    w = synth.qwen_weights(cfg, 83, symmetric=False)
+    m = QwenModel(dev.ctx, cfg, w, max_batch=16)
+    m.set_slots(nconv)
+    g = synth.rng(95 + nconv)
+    prompts = [[int(t) for t in g.integers(0, cfg.vocab, 2 + i)] for i in range(nconv)]
+    steps = 6
+
+    def seed():
+        m.reset()
+        toks = []
+        for i, p in enumerate(prompts):
+            m.use_slot(i)
+            m.forward(p, 0)
+            toks.append(int(m.next_token(len(p) - 1).item()))
+        m.start_slots(toks, [len(p) for p in prompts])
+
+    seed()
+    eager = [m.slots_step(nconv).cpu().tolist() for _ in range(steps)]
+    kc = [k.clone() for k in m.kc]
+    vc = [v.clone() for v in m.vc]
+    hidden = m.hidden[:nconv].clone()
+    seed()
+    got = []
+    for _ in range(steps):
+        got.append(m.slots_step(nconv, graph=True).cpu().tolist())
+        torch.cuda.synchronize()
+    log(f"  {nconv} conversations, captured steps: {got}")
+    assert got == eager
+    for layer in range(cfg.layers):
+        assert torch.equal(kc[layer], m.kc[layer]) and torch.equal(vc[layer], m.vc[layer]), f"layer {layer}"
+    assert torch.equal(hidden.view(torch.int32), m.hidden[:nconv].view(torch.int32))
+    m.free()
+
+
 def test_a_slot_out_of_range_stores_nothing(dev):
     """gx_qwen_qk_rope with a token in no conversation: nothing lands in any
     cache, and its query heads are NaN."""
