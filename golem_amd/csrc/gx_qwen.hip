@@ -871,18 +871,22 @@ __global__ __launch_bounds__(kDecodeThreads) void attn_decode_kernel(
 // launch's extent and in both forms), so that a token's result depends on
 // its prefix only: a step replayed from a graph launched for the whole cache
 // equals the same step launched for its own prefix, bit for bit.
-template <bool FUSE>
+// ROWS: key rows a thread scores -- one when the extent fits the cache
+// threads (half the registers: two workgroups a CU), else enough for
+// kDecodeMax.  The runs do not depend on it.
+template <bool FUSE, int ROWS>
 struct ParShape {
     static constexpr int kW0 = FUSE ? 1 : 0;                           // wavefronts out of the cache work
     static constexpr int kCT = kDecodeThreads - 64 * kW0;              // cache threads
     static constexpr int kRuns = (kDecodeThreads - 64) / kValSlice;    // position runs of the value sums
     static constexpr int kXChunk = ((kDecodeMax + kRuns - 1) / kRuns + 7) & ~7;  // positions a run
     static constexpr int kPieces = kXChunk / 8;                        // value pieces a thread holds
-    static constexpr int kRows = (kDecodeMax + kCT - 1) / kCT;         // positions a thread scores
+    static constexpr int kRows = ROWS;                                 // positions a thread scores
+    static constexpr int kMaxRows = (kDecodeMax + kCT - 1) / kCT;
 };
 constexpr int kParProbs = kDecodeMax + 64;  // probabilities in LDS: up to the end of the last run
 
-template <int HD, bool FUSE>
+template <int HD, bool FUSE, int ROWS>
 __global__ __launch_bounds__(kDecodeThreads) void attn_par_kernel(
     const uint16_t *__restrict__ qh, int heads, int kv_heads, const int32_t *__restrict__ positions, int limit,
     const uint16_t *kcache, const uint16_t *vcache, int context, float scale,
@@ -891,9 +895,10 @@ __global__ __launch_bounds__(kDecodeThreads) void attn_par_kernel(
     __shared__ __align__(16) uint32_t ql[HD / 2];                // the query, fp16 pairs
     __shared__ __align__(16) uint16_t nk[HD];                   // FUSE: this position's key
     __shared__ uint16_t nvl[kValSlice];                         // FUSE: this position's values of the slice
-    using Sh = ParShape<FUSE>;
+    using Sh = ParShape<FUSE, ROWS>;
     static_assert(Sh::kRuns * Sh::kXChunk <= kParProbs && Sh::kRuns * Sh::kXChunk >= kDecodeMax, "runs fit");
-    static_assert(Sh::kRows * Sh::kCT >= kParProbs - 8, "the probability rows are covered");
+    static_assert(Sh::kMaxRows * Sh::kCT >= kParProbs - 8, "the probability rows are covered");
+    static_assert(ROWS == 1 || ROWS == Sh::kMaxRows, "one row a thread, or as many as kDecodeMax needs");
     __shared__ __align__(16) uint16_t ps[kParProbs];            // probabilities, fp16
     __shared__ float redm[kDecodeThreads / 64], reds[kDecodeThreads / 64];
     __shared__ float vpart[Sh::kRuns][kValSlice + 1];
@@ -1395,18 +1400,26 @@ int launch_qwen_attention(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int
     // One workgroup per token: a few tokens of one conversation, or tokens of
     // several conversations (slots), whose caches share nothing.
     if (parallel && (M <= 4 || slots) && limit <= kDecodeMax) {
-#define GX_PAR(HH)                                                                                                   \
-    attn_par_kernel<HH, false><<<dim3((unsigned)(heads * (HH / kValSlice)), (unsigned)M), kDecodeThreads, 0,       \
-                                 ctx->stream>>>(qh, heads, kv_heads, positions, limit, kcache, vcache, context,      \
-                                                scale, q, scales, qsum, slots, nslots, QkRope{}, heads_f)
+#define GX_PAR(HH, RR)                                                                                               \
+    attn_par_kernel<HH, false, RR><<<dim3((unsigned)(heads * (HH / kValSlice)), (unsigned)M), kDecodeThreads, 0,   \
+                                     ctx->stream>>>(qh, heads, kv_heads, positions, limit, kcache, vcache, context,  \
+                                                    scale, q, scales, qsum, slots, nslots, QkRope{}, heads_f)
+#define GX_PAR_R(HH)                                                                                                 \
+    do {                                                                                                             \
+        if (limit <= ParShape<false, 1>::kCT)                                                                        \
+            GX_PAR(HH, 1);                                                                                           \
+        else                                                                                                         \
+            GX_PAR(HH, (ParShape<false, 1>::kMaxRows));                                                              \
+    } while (0)
         if (hd == 32)
-            GX_PAR(32);
+            GX_PAR_R(32);
         else if (hd == 64)
-            GX_PAR(64);
+            GX_PAR_R(64);
         else if (hd == 96)
-            GX_PAR(96);
+            GX_PAR_R(96);
         else
-            GX_PAR(128);
+            GX_PAR_R(128);
+#undef GX_PAR_R
 #undef GX_PAR
         return check_launch("qwen_attention parallel");
     }
@@ -1504,18 +1517,26 @@ int launch_qwen_rope_attention(gx_ctx *ctx, const float *qkv, int ldqkv, int hea
     GX_CHECK(limit <= kDecodeMax, "gx: the fused attention reads at most %d positions, not %d", kDecodeMax, limit);
     const QkRope fz{qkv, ldqkv, q_norm, k_norm, rope_cos, rope_sin, eps, kcache, vcache};
     if (parallel) {
-#define GX_PAR(HH)                                                                                                   \
-    attn_par_kernel<HH, true><<<dim3((unsigned)(heads * (HH / kValSlice)), 1u), kDecodeThreads, 0, ctx->stream>>>(  \
-        nullptr, heads, kv_heads, positions, limit, kcache, vcache, context, scale, q, scales, qsum, slots, nslots, fz, \
-        nullptr)
+#define GX_PAR(HH, RR)                                                                                               \
+    attn_par_kernel<HH, true, RR><<<dim3((unsigned)(heads * (HH / kValSlice)), 1u), kDecodeThreads, 0,             \
+                                    ctx->stream>>>(nullptr, heads, kv_heads, positions, limit, kcache, vcache,       \
+                                                   context, scale, q, scales, qsum, slots, nslots, fz, nullptr)
+#define GX_PAR_R(HH)                                                                                                 \
+    do {                                                                                                             \
+        if (limit <= ParShape<true, 1>::kCT)                                                                         \
+            GX_PAR(HH, 1);                                                                                           \
+        else                                                                                                         \
+            GX_PAR(HH, (ParShape<true, 1>::kMaxRows));                                                               \
+    } while (0)
         if (hd == 32)
-            GX_PAR(32);
+            GX_PAR_R(32);
         else if (hd == 64)
-            GX_PAR(64);
+            GX_PAR_R(64);
         else if (hd == 96)
-            GX_PAR(96);
+            GX_PAR_R(96);
         else
-            GX_PAR(128);
+            GX_PAR_R(128);
+#undef GX_PAR_R
 #undef GX_PAR
         return check_launch("qwen_rope_attention parallel");
     }
