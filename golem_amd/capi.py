@@ -79,6 +79,8 @@ _SIGNATURES = {
                                    _vp, _vp, _c_size, _vp, _c_int],
     "gx_qwen_rope_attention_parallel": [_vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _vp,
                                         ctypes.c_float, _vp, _vp, _c_int, _vp, _vp, _vp, _vp, _c_int],
+    "gx_qwen_rope_attention_slots": [_vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp,
+                                     _vp, ctypes.c_float, _vp, _vp, _c_int, _vp, _vp, _vp, _vp, _c_int, _c_int],
     "gx_qwen_attention_heads": [_vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _c_int, _vp],
     "gx_swiglu_quant": [_vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp],
     "gx_norm_matmul_q4_0": [_vp, _vp, _vp, _vp, _vp, ctypes.c_float, _vp, _c_int, _c_int, _vp],

@@ -818,7 +818,7 @@ int gx_qwen_qk_rope(gx_ctx *ctx, const float *qkv, int ldqkv, int M, int heads, 
     return ok();
 }
 
-static int rope_attention(gx_ctx *ctx, const float *qkv, int ldqkv, int heads, int kv_heads, int head_dim,
+static int rope_attention(gx_ctx *ctx, const float *qkv, int ldqkv, int M, int heads, int kv_heads, int head_dim,
                           int max_pos, const int32_t *positions, const float *q_norm, const float *k_norm,
                           const float *rope_cos, const float *rope_sin, float eps, uint16_t *kcache, uint16_t *vcache,
                           int context, int8_t *q, float *scales, int32_t *qsum, const int32_t *slots, int nslots,
@@ -834,8 +834,12 @@ static int rope_attention(gx_ctx *ctx, const float *qkv, int ldqkv, int heads, i
              "gx: missing argument");
     GX_CHECK(((uintptr_t)vcache & 15) == 0, "gx: the value cache must be 16-byte aligned");
     GX_CHECK(!slots || nslots > 0, "gx: %d slots", nslots);
+    GX_CHECK(M == 1 || (M > 1 && slots), "gx: %d tokens of one conversation: the fused attention takes one token, "
+             "or one token per conversation", M);
+    if (M == 0)
+        return ok();
     const float scale = (float)(1.0 / sqrt((double)head_dim));
-    if (int rc = gx::launch_qwen_rope_attention(ctx, qkv, ldqkv, heads, kv_heads, head_dim, max_pos, positions, q_norm,
+    if (int rc = gx::launch_qwen_rope_attention(ctx, qkv, ldqkv, M, heads, kv_heads, head_dim, max_pos, positions, q_norm,
                                                 k_norm, rope_cos, rope_sin, eps, kcache, vcache, context, scale, q,
                                                 scales, qsum, slots, nslots, parallel))
         return rc;
@@ -847,7 +851,7 @@ int gx_qwen_rope_attention(gx_ctx *ctx, const float *qkv, int ldqkv, int heads, 
                            const float *rope_cos, const float *rope_sin, float eps, uint16_t *kcache,
                            uint16_t *vcache, int context, int8_t *q, float *scales, int32_t *qsum,
                            const int32_t *slots, int nslots) {
-    return rope_attention(ctx, qkv, ldqkv, heads, kv_heads, head_dim, max_pos, positions, q_norm, k_norm, rope_cos,
+    return rope_attention(ctx, qkv, ldqkv, 1, heads, kv_heads, head_dim, max_pos, positions, q_norm, k_norm, rope_cos,
                           rope_sin, eps, kcache, vcache, context, q, scales, qsum, slots, nslots, 0);
 }
 
@@ -856,8 +860,19 @@ int gx_qwen_rope_attention_parallel(gx_ctx *ctx, const float *qkv, int ldqkv, in
                                     const float *k_norm, const float *rope_cos, const float *rope_sin, float eps,
                                     uint16_t *kcache, uint16_t *vcache, int context, int8_t *q, float *scales,
                                     int32_t *qsum, const int32_t *slots, int nslots) {
-    return rope_attention(ctx, qkv, ldqkv, heads, kv_heads, head_dim, max_pos, positions, q_norm, k_norm, rope_cos,
+    return rope_attention(ctx, qkv, ldqkv, 1, heads, kv_heads, head_dim, max_pos, positions, q_norm, k_norm, rope_cos,
                           rope_sin, eps, kcache, vcache, context, q, scales, qsum, slots, nslots, 1);
+}
+
+int gx_qwen_rope_attention_slots(gx_ctx *ctx, const float *qkv, int ldqkv, int M, int heads, int kv_heads,
+                                 int head_dim, int max_pos, const int32_t *positions, const float *q_norm,
+                                 const float *k_norm, const float *rope_cos, const float *rope_sin, float eps,
+                                 uint16_t *kcache, uint16_t *vcache, int context, int8_t *q, float *scales,
+                                 int32_t *qsum, const int32_t *slots, int nslots, int parallel) {
+    GX_CHECK(slots != nullptr, "gx: the fused attention of several tokens needs their conversations (slots)");
+    GX_CHECK(M >= 0, "gx: bad batch shape");
+    return rope_attention(ctx, qkv, ldqkv, M, heads, kv_heads, head_dim, max_pos, positions, q_norm, k_norm, rope_cos,
+                          rope_sin, eps, kcache, vcache, context, q, scales, qsum, slots, nslots, parallel ? 1 : 0);
 }
 
 int gx_qwen_attention_workspace_bytes(int M, int heads, int max_pos, size_t *bytes) {

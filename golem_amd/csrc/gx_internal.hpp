@@ -155,7 +155,7 @@ int launch_qwen_qk_rope(gx_ctx *ctx, const float *qkv, int ldqkv, int M, int hea
                         const float *rope_sin, float eps, uint16_t *qh, uint16_t *kcache, uint16_t *vcache,
                         int context, const int32_t *slots, int nslots);
 size_t qwen_attention_workspace(int M, int heads, int max_pos);
-int launch_qwen_rope_attention(gx_ctx *ctx, const float *qkv, int ldqkv, int heads, int kv_heads, int hd,
+int launch_qwen_rope_attention(gx_ctx *ctx, const float *qkv, int ldqkv, int M, int heads, int kv_heads, int hd,
                                int max_pos, const int32_t *positions, const float *q_norm, const float *k_norm,
                                const float *rope_cos, const float *rope_sin, float eps, uint16_t *kcache,
                                uint16_t *vcache, int context, float scale, int8_t *q, float *scales, int32_t *qsum,

@@ -1505,7 +1505,7 @@ int launch_qwen_attention(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int
     return check_launch("qwen_attention values");
 }
 
-int launch_qwen_rope_attention(gx_ctx *ctx, const float *qkv, int ldqkv, int heads, int kv_heads, int hd,
+int launch_qwen_rope_attention(gx_ctx *ctx, const float *qkv, int ldqkv, int M, int heads, int kv_heads, int hd,
                                int max_pos, const int32_t *positions, const float *q_norm, const float *k_norm,
                                const float *rope_cos, const float *rope_sin, float eps, uint16_t *kcache,
                                uint16_t *vcache, int context, float scale, int8_t *q, float *scales, int32_t *qsum,
@@ -1518,7 +1518,7 @@ int launch_qwen_rope_attention(gx_ctx *ctx, const float *qkv, int ldqkv, int hea
     const QkRope fz{qkv, ldqkv, q_norm, k_norm, rope_cos, rope_sin, eps, kcache, vcache};
     if (parallel) {
 #define GX_PAR(HH, RR)                                                                                               \
-    attn_par_kernel<HH, true, RR><<<dim3((unsigned)(heads * (HH / kValSlice)), 1u), kDecodeThreads, 0,             \
+    attn_par_kernel<HH, true, RR><<<dim3((unsigned)(heads * (HH / kValSlice)), (unsigned)M), kDecodeThreads, 0,             \
                                     ctx->stream>>>(nullptr, heads, kv_heads, positions, limit, kcache, vcache,       \
                                                    context, scale, q, scales, qsum, slots, nslots, fz, nullptr)
 #define GX_PAR_R(HH)                                                                                                 \
@@ -1541,7 +1541,7 @@ int launch_qwen_rope_attention(gx_ctx *ctx, const float *qkv, int ldqkv, int hea
         return check_launch("qwen_rope_attention parallel");
     }
 #define GX_FUSED(HH)                                                                                                 \
-    attn_decode_kernel<HH, 1, true><<<dim3((unsigned)(heads * (HH / kValSlice)), 1u), kDecodeThreads, 0,             \
+    attn_decode_kernel<HH, 1, true><<<dim3((unsigned)(heads * (HH / kValSlice)), (unsigned)M), kDecodeThreads, 0,             \
                                       ctx->stream>>>(nullptr, heads, kv_heads, positions, limit, kcache, vcache,     \
                                                      context, scale, q, scales, qsum, slots, nslots, fz)
     if (hd == 32)

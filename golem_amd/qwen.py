@@ -266,10 +266,13 @@ class QwenModel:
             return self.xs[:M].cpu().numpy().copy()
         return (self.xs[:M] + self.ffn[:M]).cpu().numpy()  # the last block's residual add
 
-    def _blocks(self, M, max_pos, blocks=None):
+    def _blocks(self, M, max_pos, blocks=None, one_per_slot=False):
         """The embedding rows, every block and the final norm for the M tokens
         and positions already in self.tokens / self.positions (with `blocks`:
-        only the first that many blocks, and no final norm)."""
+        only the first that many blocks, and no final norm).  one_per_slot:
+        the M tokens belong to M different conversations (a lock-step step),
+        so the head norms, RoPE, cache stores and attention run as one
+        kernel."""
         cfg, vp, call, ctx = self.cfg, self._vp, self._call, self.ctx.ptr
         call("gx_weight_rows", ctx, self.embd.ptr, 0, vp(self.tokens), M, vp(self.xs))
         if M == 1:
@@ -283,13 +286,20 @@ class QwenModel:
             call("gx_norm_quant", ctx, vp(self.xs), cfg.dim, add, cfg.dim, vp(b["attn_norm"]), M, cfg.dim,
                  np.float32(cfg.eps), None, 0, vp(self.x8.q), vp(self.x8.s), vp(self.x8.qs))
             self._mm(b["qkv"], self.x8, M, self.qkv, qd + 2 * kvd)
-            call("gx_qwen_qk_rope", ctx, vp(self.qkv), qd + 2 * kvd, M, cfg.heads, cfg.kv_heads, cfg.head_dim,
-                 vp(self.positions), vp(b["q_norm"]), vp(b["k_norm"]), vp(self.rope_cos), vp(self.rope_sin),
-                 np.float32(cfg.eps), vp(self.qh), vp(self.kc[i]), vp(self.vc[i]), self.context, sl, self.nslots)
-            call(self._attention, ctx, vp(self.qh), M, cfg.heads, cfg.kv_heads, cfg.head_dim,
-                 max_pos, vp(self.positions), vp(self.kc[i]), vp(self.vc[i]), self.context,
-                 vp(self.set8.q), vp(self.set8.s), vp(self.set8.qs), vp(self.attn_ws), self.attn_ws.numel(), sl,
-                 self.nslots)
+            if one_per_slot and max_pos < FUSED_ATTENTION_MAX:
+                call("gx_qwen_rope_attention_slots", ctx, vp(self.qkv), qd + 2 * kvd, M, cfg.heads, cfg.kv_heads,
+                     cfg.head_dim, max_pos, vp(self.positions), vp(b["q_norm"]), vp(b["k_norm"]),
+                     vp(self.rope_cos), vp(self.rope_sin), np.float32(cfg.eps), vp(self.kc[i]), vp(self.vc[i]),
+                     self.context, vp(self.set8.q), vp(self.set8.s), vp(self.set8.qs), sl, self.nslots,
+                     1 if self._attention.endswith("_parallel") else 0)
+            else:
+                call("gx_qwen_qk_rope", ctx, vp(self.qkv), qd + 2 * kvd, M, cfg.heads, cfg.kv_heads, cfg.head_dim,
+                     vp(self.positions), vp(b["q_norm"]), vp(b["k_norm"]), vp(self.rope_cos), vp(self.rope_sin),
+                     np.float32(cfg.eps), vp(self.qh), vp(self.kc[i]), vp(self.vc[i]), self.context, sl, self.nslots)
+                call(self._attention, ctx, vp(self.qh), M, cfg.heads, cfg.kv_heads, cfg.head_dim,
+                     max_pos, vp(self.positions), vp(self.kc[i]), vp(self.vc[i]), self.context,
+                     vp(self.set8.q), vp(self.set8.s), vp(self.set8.qs), vp(self.attn_ws), self.attn_ws.numel(),
+                     sl, self.nslots)
             self._mm(b["o"], self.set8, M, self.attn, cfg.dim)
             call("gx_norm_quant", ctx, vp(self.xs), cfg.dim, vp(self.attn), cfg.dim, vp(b["ffn_norm"]), M, cfg.dim,
                  np.float32(cfg.eps), None, 0, vp(self.x8.q), vp(self.x8.s), vp(self.x8.qs))
@@ -425,7 +435,7 @@ class QwenModel:
         return self.next_id[:n]
 
     def _slots_device_step(self, n, max_pos):
-        self._blocks(n, max_pos)
+        self._blocks(n, max_pos, one_per_slot=self.nslots > 1)
         self.next_tokens(range(n))
         self.tokens[:n].copy_(self.next_id[:n])
         self.positions[:n].add_(1)

@@ -431,6 +431,20 @@ int gx_qwen_rope_attention_parallel(gx_ctx *ctx, const float *qkv, int ldqkv, in
                                     uint16_t *kcache, uint16_t *vcache, int context, int8_t *q, float *scales,
                                     int32_t *qsum, const int32_t *slots, int nslots);
 
+/* gx_qwen_rope_attention (parallel 0) or _parallel (parallel 1) for M tokens
+ * of M different conversations at once: token t's Q|K|V row qkv[t*ldqkv],
+ * position positions[t] of conversation slots[t] (slots required), its
+ * Q8_0 heads at row t of q/scales/qsum -- the lock-step decode of several
+ * conversations (qwen/place.go:33-41, one token a slot, as the server's
+ * batch of slots).  Each token's values are those of the one-token call bit
+ * for bit.  Two tokens of one conversation in one call are not allowed: a
+ * token would not see the other's new cache entry. */
+int gx_qwen_rope_attention_slots(gx_ctx *ctx, const float *qkv, int ldqkv, int M, int heads, int kv_heads,
+                                 int head_dim, int max_pos, const int32_t *positions, const float *q_norm,
+                                 const float *k_norm, const float *rope_cos, const float *rope_sin, float eps,
+                                 uint16_t *kcache, uint16_t *vcache, int context, int8_t *q, float *scales,
+                                 int32_t *qsum, const int32_t *slots, int nslots, int parallel);
+
 /* The head outputs of gx_qwen_attention_parallel before their Q8_0, out
  * [M][heads*head_dim] (device floats), M <= 4.  No counterpart in golem:
  * parity instrumentation for the parallel order. */

@@ -106,3 +106,54 @@ def test_rope_attention_refuses_long_prefix(dev):
         capi.call("gx_qwen_rope_attention", dev.ctx.ptr, capi.vp(z), (heads + 2 * kv) * hd, heads, kv, hd, 800,
                   capi.vp(z), capi.vp(z), capi.vp(z), capi.vp(z), capi.vp(z), np.float32(1e-6), capi.vp(z),
                   capi.vp(z), context, capi.vp(z), capi.vp(z), capi.vp(z), None, 1)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("parallel", [False, True])
+@pytest.mark.parametrize("hd,heads,kv,context,M", [(128, 32, 8, 80, 8), (64, 4, 2, 304, 3), (128, 16, 8, 520, 5)])
+def test_rope_attention_slots_equal_one_at_a_time(dev, hd, heads, kv, context, M, parallel):
+    """gx_qwen_rope_attention_slots: M tokens of M conversations in one call
+    (the lock-step step) give, token by token, what the one-token call gives
+    for that token alone -- Q8_0 heads and both caches bit for bit."""
+    g = synth.rng(400 + M + hd)
+    nslots = M + 1
+    width = (heads + 2 * kv) * hd
+    qkv = (g.standard_normal((M, width)) * 3).astype(np.float32)
+    qn = (1 + 0.02 * g.standard_normal(hd)).astype(np.float32)
+    kn = (1 + 0.02 * g.standard_normal(hd)).astype(np.float32)
+    cos = g.uniform(-1, 1, (context, hd // 2)).astype(np.float32)
+    sin = g.uniform(-1, 1, (context, hd // 2)).astype(np.float32)
+    kc0 = g.standard_normal((nslots, kv, hd // 8, context, 8)).astype(np.float16)
+    vc0 = (g.standard_normal((nslots, kv, hd, context)) * 2).astype(np.float16)
+    pos = g.integers(0, context, M).astype(np.int32)
+    slots = g.permutation(nslots)[:M].astype(np.int32)  # M different conversations
+    max_pos = context - 1
+    eps = np.float32(1e-6)
+    ins = [dev.put(a) for a in (qkv, pos, qn, kn, cos, sin, slots)]
+    kc, vc = dev.put(kc0.view(np.int16)), dev.put(vc0.view(np.int16))
+    q8 = dev.empty((M, heads * hd), np.int8)
+    sc = dev.empty((M, heads * hd // 32), np.float32)
+    qs = dev.empty((M, heads * hd // 32), np.int32)
+    capi.call("gx_qwen_rope_attention_slots", dev.ctx.ptr, capi.vp(ins[0]), width, M, heads, kv, hd, max_pos,
+              capi.vp(ins[1]), capi.vp(ins[2]), capi.vp(ins[3]), capi.vp(ins[4]), capi.vp(ins[5]), eps, capi.vp(kc),
+              capi.vp(vc), context, capi.vp(q8), capi.vp(sc), capi.vp(qs), capi.vp(ins[6]), nslots,
+              1 if parallel else 0)
+    got = [dev.get(a) for a in (q8, sc, qs, kc, vc)]
+    kc1, vc1 = dev.put(kc0.view(np.int16)), dev.put(vc0.view(np.int16))
+    name = "gx_qwen_rope_attention_parallel" if parallel else "gx_qwen_rope_attention"
+    for t in range(M):
+        q1 = dev.empty((1, heads * hd), np.int8)
+        s1 = dev.empty((1, heads * hd // 32), np.float32)
+        u1 = dev.empty((1, heads * hd // 32), np.int32)
+        capi.call(name, dev.ctx.ptr, capi.vp(ins[0][t:t + 1]), width, heads, kv, hd, max_pos, capi.vp(ins[1][t:t + 1]),
+                  capi.vp(ins[2]), capi.vp(ins[3]), capi.vp(ins[4]), capi.vp(ins[5]), eps, capi.vp(kc1), capi.vp(vc1),
+                  context, capi.vp(q1), capi.vp(s1), capi.vp(u1), capi.vp(ins[6][t:t + 1]), nslots)
+        for nm, a, b in (("q", got[0][t], dev.get(q1)[0]), ("scales", got[1][t], dev.get(s1)[0]),
+                         ("sums", got[2][t], dev.get(u1)[0])):
+            assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), f"token {t}: {nm}"
+    assert np.array_equal(got[3].view(np.uint8), dev.get(kc1).view(np.uint8)), "key cache"
+    assert np.array_equal(got[4].view(np.uint8), dev.get(vc1).view(np.uint8)), "value cache"
+    with pytest.raises(capi.GxError):
+        capi.call("gx_qwen_rope_attention_slots", dev.ctx.ptr, capi.vp(ins[0]), width, M, heads, kv, hd, max_pos,
+                  capi.vp(ins[1]), capi.vp(ins[2]), capi.vp(ins[3]), capi.vp(ins[4]), capi.vp(ins[5]), eps,
+                  capi.vp(kc), capi.vp(vc), context, capi.vp(q8), capi.vp(sc), capi.vp(qs), None, nslots, 1)
