@@ -389,34 +389,38 @@ __global__ __launch_bounds__(256) void moe_norm_scale_kernel(const float *__rest
         scale[t] = norm_scale(s, D, eps);
 }
 
-// The logits: 4 experts x P positions a workgroup (16 P threads), a lane one
-// chain (lane = chain c + 4 (expert + 4 position)).  The inputs pass through
-// LDS CH at a time, transposed so that each chain's CH/4 elements of a chunk
-// are contiguous (one 16-byte read per lane for four of its steps), double
-// buffered: the next chunk's global loads are in flight while this one is
-// summed.
-constexpr int kLgEW = 4;
+// The logits: EW experts x P positions a workgroup (4 EW P threads), a lane
+// one chain (lane = chain c + 4 (expert + EW position)).  The inputs pass
+// through LDS CH at a time, transposed so that each chain's CH/4 elements of
+// a chunk are contiguous (one 16-byte read per lane for four of its steps),
+// double buffered: the next chunk's global loads are in flight while this
+// one is summed.  Eight experts a workgroup read each position's inputs for
+// twice the chains of four, and a thread's router-scale piece is the same
+// for every position it stages (its chunk offset is tid % (CH/4)): one load
+// (EW 4 with a load per staged piece moved ~36 KB a chunk through each
+// workgroup for 1,024 chains, 18 us at config 4's 256 positions).
+constexpr int kLgEW = 8;
 
 template <int P, int CH>
-__global__ __launch_bounds__(16 * P) void moe_logits_kernel(const float *__restrict__ router, int D, int E,
-                                                           const float *__restrict__ router_scale,
-                                                           const float *__restrict__ resid, int ldr, int M,
-                                                           const float *__restrict__ scales,
-                                                           float *__restrict__ logits) {
-    constexpr int NT = 16 * P, ST = CH / 4, PAD = ST + 4;
+__global__ __launch_bounds__(4 * kLgEW * P) void moe_logits_kernel(const float *__restrict__ router, int D, int E,
+                                                                  const float *__restrict__ router_scale,
+                                                                  const float *__restrict__ resid, int ldr, int M,
+                                                                  const float *__restrict__ scales,
+                                                                  float *__restrict__ logits) {
+    constexpr int NT = 4 * kLgEW * P, ST = CH / 4, PAD = ST + 4;
     constexpr int RF4 = (kLgEW * ST + NT - 1) / NT, XF4 = P * ST / NT;  // staged float4 per thread per chunk
-    static_assert(P * ST % NT == 0, "chunk shape");
+    static_assert(P * ST % NT == 0 && NT % ST == 0, "chunk shape");
     __shared__ __align__(16) float Rs[2][kLgEW][4][PAD];
     __shared__ __align__(16) float Xs[2][P][4][PAD];
     const int tid = threadIdx.x;
     const int e0 = blockIdx.x * kLgEW, t0 = blockIdx.y * P;
-    const int c = tid & 3, e = (tid >> 2) & 3, p = tid >> 4;  // this lane's chain
+    const int c = tid & 3, e = (tid >> 2) % kLgEW, p = tid / (4 * kLgEW);  // this lane's chain
     const float inv_sqrt_dim = (float)(1.0 / sqrt((double)D));
 
     // This thread's staging: row pieces idx = tid + NT f (expert idx / ST,
     // float4 idx % ST of the chunk) and input pieces likewise (position
     // idx / ST); past D the pieces are zero.
-    float4 rv[RF4], xv[XF4], sv[XF4];
+    float4 rv[RF4], xv[XF4], sv;
     float sc[XF4];
 #pragma unroll
     for (int f = 0; f < XF4; f++)
@@ -434,8 +438,9 @@ __global__ __launch_bounds__(16 * P) void moe_logits_kernel(const float *__restr
             const int idx = tid + NT * f, i = i0 + 4 * (idx % ST);
             const float *xr = resid + (size_t)min(t0 + idx / ST, M - 1) * ldr;
             xv[f] = i < D ? *(const float4 *)(xr + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            sv[f] = router_scale && i < D ? *(const float4 *)(router_scale + i) : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
         }
+        const int is = i0 + 4 * (tid % ST);  // every staged piece's offset in the chunk (NT % ST == 0)
+        sv = router_scale && is < D ? *(const float4 *)(router_scale + is) : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
     };
     auto put = [&](int buf) {
 #pragma unroll
@@ -451,7 +456,7 @@ __global__ __launch_bounds__(16 * P) void moe_logits_kernel(const float *__restr
 #pragma unroll
         for (int f = 0; f < XF4; f++) {
             const int idx = tid + NT * f, pp = idx / ST, q = idx % ST;
-            const float x4[4] = {xv[f].x, xv[f].y, xv[f].z, xv[f].w}, s4[4] = {sv[f].x, sv[f].y, sv[f].z, sv[f].w};
+            const float x4[4] = {xv[f].x, xv[f].y, xv[f].z, xv[f].w}, s4[4] = {sv.x, sv.y, sv.z, sv.w};
 #pragma unroll
             for (int cc = 0; cc < 4; cc++) {
                 const float normed = x4[cc] * sc[f];
@@ -1229,7 +1234,7 @@ int launch_moe_route(gx_ctx *ctx, const gx_weight *router, const float *router_s
             return rc;
         constexpr int P = 16, CH = 256;
         const dim3 grid((unsigned)((E + kLgEW - 1) / kLgEW), (unsigned)((m + P - 1) / P));
-        moe_logits_kernel<P, CH><<<grid, 16 * P, 0, ctx->stream>>>(rw, D, E, router_scale, rr, ldr, m,
+        moe_logits_kernel<P, CH><<<grid, 4 * kLgEW * P, 0, ctx->stream>>>(rw, D, E, router_scale, rr, ldr, m,
                                                                     ctx->route_scale, logits + (size_t)m0 * E);
         if (int rc = check_launch("moe_logits"))
             return rc;
