@@ -655,8 +655,24 @@ int launch_q4_0_gemm(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, const 
     // the widened weights are signed: no recentring term, so no qsum
     const int tile0 = row_start / kTileRows;
     const int tiles = (row_end + kTileRows - 1) / kTileRows - tile0;
-    const dim3 grid((unsigned)((tiles + 1) / 2), (unsigned)((M + kDmaTok - 1) / kDmaTok));
     const Groups none{nullptr, nullptr, 1, 0};
+    // Up to 1024 tokens, 32-token workgroups: twice as many of them to fill
+    // the CUs (config 2's 9728 x 2560 in a graph over rotating copies: M = 64
+    // 25.0 -> 20.1 us, M = 512 62.0 -> 56.1 us; M = 2048 195 against 198 us
+    // keeps 64).  The per-token arithmetic is the same either way.
+    if (M <= 1024) {
+        const dim3 grid((unsigned)((tiles + 1) / 2), (unsigned)((M + 31) / 32));
+        if (dots)
+            q4_0_gemm_dma_kernel<32, false, true><<<grid, 256, 0, ctx->stream>>>(
+                mat, w->plane0_bytes, w->blocks, w->dchunks, q, scales, w->cols, M, w->tiles, tile0, row_start,
+                row_end, bias, y, ldy, dots, none);
+        else
+            q4_0_gemm_dma_kernel<32, false, false><<<grid, 256, 0, ctx->stream>>>(
+                mat, w->plane0_bytes, w->blocks, w->dchunks, q, scales, w->cols, M, w->tiles, tile0, row_start,
+                row_end, bias, y, ldy, nullptr, none);
+        return check_launch("q4_0_gemm");
+    }
+    const dim3 grid((unsigned)((tiles + 1) / 2), (unsigned)((M + kDmaTok - 1) / kDmaTok));
     if (dots)
         q4_0_gemm_dma_kernel<64, false, true><<<grid, 512, 0, ctx->stream>>>(
             mat, w->plane0_bytes, w->blocks, w->dchunks, q, scales, w->cols, M, w->tiles, tile0, row_start, row_end,
