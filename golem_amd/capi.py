@@ -83,6 +83,7 @@ _SIGNATURES = {
                                      _vp, ctypes.c_float, _vp, _vp, _c_int, _vp, _vp, _vp, _vp, _c_int, _c_int],
     "gx_qwen_attention_heads": [_vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _c_int, _vp],
     "gx_swiglu_quant": [_vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp],
+    "gx_matmul_swiglu_q4_0": [_vp, _vp, _vp, _vp, _vp, _c_int, _vp, _vp, _vp],
     "gx_norm_matmul_q4_0": [_vp, _vp, _vp, _vp, _vp, ctypes.c_float, _vp, _c_int, _c_int, _vp],
     "gx_norm_swiglu_q4_0": [_vp, _vp, _vp, _vp, _vp, ctypes.c_float, _vp, _vp, _vp, _vp],
     "gx_argmax_step": [_vp, _vp, _c_int, _vp, _vp, _c_int, _vp, _vp],

@@ -626,6 +626,25 @@ int gx_matmul_q6_k(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const float
     return ok();
 }
 
+int gx_matmul_swiglu_q4_0(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const float *scales,
+                          const int32_t *qsum, int M, int8_t *mid_q, float *mid_scales, int32_t *mid_qsum) {
+    if (int rc = use(ctx))
+        return rc;
+    if (int rc = check_product(w, GX_Q4_0, M, 0, w ? w->rows : 0, mid_q, w ? w->rows : 0))
+        return rc;
+    GX_CHECK(w->count == 1, "gx: a SwiGLU product takes a single matrix");
+    GX_CHECK(w->rows % 64 == 0,
+             "gx: the SwiGLU form needs gate and up rows interleaved by 32 (rows a multiple of 64, not %d)", w->rows);
+    GX_CHECK(M >= 0 && M <= 8, "gx: the SwiGLU product takes 1 to 8 columns, not %d", M);
+    GX_CHECK(q && scales && qsum && mid_q && mid_scales && mid_qsum, "gx: missing argument");
+    GX_CHECK(((uintptr_t)q & 15) == 0, "gx: q must be 16-byte aligned");
+    if (M == 0)
+        return ok();
+    if (int rc = gx::launch_q4_0_matvec_swiglu(ctx, w, q, scales, qsum, M, mid_q, mid_scales, mid_qsum))
+        return rc;
+    return ok();
+}
+
 int gx_matvec_rows_q4_0(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const float *scales, const int32_t *qsum,
                         int M, uint64_t generation, int row_start, int row_end, float *ys, int ldys) {
     if (int rc = use(ctx))

@@ -127,6 +127,8 @@ int launch_q4_0_gemm_f16(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, co
 int launch_q4_0_matvec_units(gx_ctx *ctx, const gx_weight *w, const int32_t *unit_expert, int units, int act_div,
                               const int8_t *q, const float *scales, const int32_t *qsum, float *y, int ldy,
                               int32_t *dots);
+int launch_q4_0_matvec_swiglu(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const float *scales,
+                               const int32_t *qsum, int M, int8_t *mq, float *ms, int32_t *mqs);
 int launch_q4_0_matvec_fused(gx_ctx *ctx, const gx_weight *w, int epi, int row_start, int row_end, float *y,
                               const float *x, const float *add, const float *gain, float eps, float *x_out,
                               int8_t *q, float *scales, int32_t *qsum, int32_t *dots);

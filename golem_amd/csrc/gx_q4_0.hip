@@ -292,11 +292,18 @@ __host__ __device__ inline size_t cols_lds_bytes(int S, int R, int NC, int K, in
     return lds_part_bytes(S * NC, R) + lds_act_bytes(NC * K, NC * B);
 }
 
-template <int R, int NC, bool DOTS>
+// EPI 1 (R = 64, every row): the rows are gate and up interleaved by 32 as
+// for q4_0_matvec_fused_kernel<1>; wavefront w takes column c = w (then
+// w + nwaves ..): lane l sums its row, and the tile's 32 outputs
+// silu(gate) * up go to their Q8_0 block in mq/ms/mqs [NC][rows / 2], the
+// fused kernel's epilogue bit for bit.
+template <int R, int NC, bool DOTS, int EPI = 0>
 __global__ __launch_bounds__(1024) void q4_0_matvec_cols_kernel(
     const uint8_t *__restrict__ W, size_t plane0_bytes, int B, int DC, const int8_t *__restrict__ q,
     const float *__restrict__ scales, const int32_t *__restrict__ qsum, int group0, int row_start, int row_end,
-    const float *__restrict__ bias, float *__restrict__ y, int ldy, int32_t *__restrict__ dots) {
+    const float *__restrict__ bias, float *__restrict__ y, int ldy, int32_t *__restrict__ dots,
+    int8_t *__restrict__ mq = nullptr, float *__restrict__ ms = nullptr, int32_t *__restrict__ mqs = nullptr) {
+    static_assert(EPI == 0 || R == kTileRows, "the SwiGLU epilogue takes whole tiles");
     constexpr int kSlots = kTileRows / R;
     extern __shared__ __align__(16) uint8_t lds_raw[];
     const int K = B * kQ4Block;
@@ -375,7 +382,31 @@ __global__ __launch_bounds__(1024) void q4_0_matvec_cols_kernel(
         }
     }
     lds_barrier();
-    if (!DOTS) {
+    if (!DOTS && EPI == 1) {
+        const int F = row_end / 2;  // the SwiGLU's width: gate and up rows in equal number
+        for (int c = wave; c < NC; c += nt >> 6) {
+            float acc = 0.0f;
+            for (int t = 0; t < S; t++)
+                acc = acc + part[(t * NC + c) * kTileRows + lane];
+            // lane l < 32: gate 32 * tile + l; lane l + 32: its up
+            const float u = __shfl_down(acc, 32, 64);
+            const float gt = acc;
+            const float ex = ggml_expf(-gt);
+            const float den = 1.0f + ex;
+            const float sl = gt / den;
+            const float v = sl * u;
+            float stored;
+            int32_t sm;
+            const int32_t nq = q8_0_lane(v, &stored, &sm);
+            if (lane < 32) {
+                mq[(size_t)c * F + (size_t)tile * 32 + lane] = (int8_t)nq;
+                if (lane == 0) {
+                    ms[(size_t)c * (F / kQ4Block) + tile] = stored;
+                    mqs[(size_t)c * (F / kQ4Block) + tile] = sm;
+                }
+            }
+        }
+    } else if (!DOTS) {
         for (int pr = tid; pr < NC * R; pr += nt) {
             const int c = pr / R, rr = pr - c * R;
             const int orow = tile * kTileRows + (g - tile * kSlots) * R + rr;
@@ -752,6 +783,15 @@ int launch_cols(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, const int8_
     return check_launch("q4_0_matvec_cols");
 }
 
+template <int NC>
+int launch_cols_swiglu(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const float *scales, const int32_t *qsum,
+                       int waves, size_t lds, int8_t *mq, float *ms, int32_t *mqs) {
+    q4_0_matvec_cols_kernel<kTileRows, NC, false, 1><<<w->tiles, 64 * waves, lds, ctx->stream>>>(
+        w->dev, w->plane0_bytes, w->blocks, w->dchunks, q, scales, qsum, 0, 0, w->rows, nullptr, nullptr, 0, nullptr,
+        mq, ms, mqs);
+    return check_launch("q4_0_matvec_cols_swiglu");
+}
+
 }  // namespace
 
 int launch_q4_0_matvec(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, const int8_t *q, const float *scales,
@@ -867,6 +907,46 @@ int launch_q4_0_matvec(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, cons
         }
         if (rc)
             return rc;
+    }
+    return GX_OK;
+}
+
+int launch_q4_0_matvec_swiglu(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const float *scales,
+                               const int32_t *qsum, int M, int8_t *mq, float *ms, int32_t *mqs) {
+    const int K = w->cols, B = w->blocks, S = (B + kStretch - 1) / kStretch, F = w->rows / 2;
+    GX_CHECK(S <= 16, "gx: a %d-input row is too wide for the multi-column SwiGLU product", K);
+    int c = 0;
+    while (c < M) {
+        const int left = M - c;
+        const int widths[4] = {8, 4, 2, 1};
+        int NC = 0;
+        size_t lds = 0;
+        for (int i = 0; i < 4 && NC == 0; i++) {
+            const size_t bytes = cols_lds_bytes(S, kTileRows, widths[i], K, B);
+            if (widths[i] <= left && bytes <= 64 * 1024) {
+                NC = widths[i];
+                lds = bytes;
+            }
+        }
+        GX_CHECK(NC > 0, "gx: a %d-input row does not fit the multi-column SwiGLU product", K);
+        const int8_t *qc = q + (size_t)c * K;
+        const float *sc = scales + (size_t)c * B;
+        const int32_t *qs = qsum + (size_t)c * B;
+        int8_t *mqc = mq + (size_t)c * F;
+        float *msc = ms + (size_t)c * (F / kQ4Block);
+        int32_t *mqsc = mqs + (size_t)c * (F / kQ4Block);
+        int rc;
+        if (NC == 8)
+            rc = launch_cols_swiglu<8>(ctx, w, qc, sc, qs, S, lds, mqc, msc, mqsc);
+        else if (NC == 4)
+            rc = launch_cols_swiglu<4>(ctx, w, qc, sc, qs, S, lds, mqc, msc, mqsc);
+        else if (NC == 2)
+            rc = launch_cols_swiglu<2>(ctx, w, qc, sc, qs, S, lds, mqc, msc, mqsc);
+        else
+            rc = launch_cols_swiglu<1>(ctx, w, qc, sc, qs, S, lds, mqc, msc, mqsc);
+        if (rc)
+            return rc;
+        c += NC;
     }
     return GX_OK;
 }

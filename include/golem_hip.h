@@ -472,6 +472,17 @@ int gx_norm_matmul_q4_0(gx_ctx *ctx, const gx_weight *w, const float *x, const f
 int gx_norm_swiglu_q4_0(gx_ctx *ctx, const gx_weight *w, const float *x, const float *add, const float *gain,
                         float eps, float *x_out, int8_t *q, float *scales, int32_t *qsum);
 
+/* gx_matmul_q4_0 over every row of a Gate|Up matrix whose gate and up rows
+ * are interleaved by 32 (rows 64k .. 64k+31 gate rows 32k .., the next 32
+ * the same up rows), then silu(gate) * up and its Q8_0 into mid_q
+ * [M][rows/2], mid_scales and mid_qsum [M][rows/64] -- bit for bit
+ * gx_matmul_q4_0 followed by gx_swiglu_quant (group 32) (qwen/block.go:
+ * 82-90, nn/swiglu.go:77-82), in one kernel a group of columns: for 1 to 8
+ * positions (golem's lock-step slots, short batches).  No counterpart in
+ * golem as one call. */
+int gx_matmul_swiglu_q4_0(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const float *scales,
+                          const int32_t *qsum, int M, int8_t *mid_q, float *mid_scales, int32_t *mid_qsum);
+
 /* SwiGLURange (nn/swiglu.go:77-82) and the Q8_0 of the result: gu[m] holds
  * position m's gate (ffn floats) then up (ffn floats) when group is 0, or
  * gates and ups interleaved by 32 (32 gates, then their 32 ups, ...) when

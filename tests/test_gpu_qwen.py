@@ -443,6 +443,57 @@ def test_norm_swiglu_fused_bit_exact(dev, ffn, K):
     inter.free()
 
 
+@pytest.mark.parametrize("ffn,K", [(9728, 2560), (1056, 2080), (32, 256)])
+def test_matmul_swiglu_columns_bit_exact(dev, ffn, K):
+    """gx_matmul_swiglu_q4_0 (the product of 1 to 8 columns with SwiGLU and
+    Q8_0 in its epilogue) against gx_matmul_q4_0 of the same interleaved
+    matrix then gx_swiglu_quant (group 32), column by column, bit for bit."""
+    from golem_amd.qwen import interleave_rows
+    g = synth.rng(190 + ffn)
+    gate = synth.q4_0_weights(g, ffn, K)
+    up = synth.q4_0_weights(g, ffn, K)
+    inter = dev.weight(interleave_rows(gate, up, ffn, K), capi.Q4_0, 2 * ffn, K)
+    for M in (1, 2, 3, 5, 8):
+        log(f"matmul swiglu ffn={ffn} K={K} M={M}")
+        act = dev.quantize_q8_0((synth.activations(g, M, K) * 2).astype(np.float32), with_corr=False,
+                                with_q16=False)
+        q = dev.empty((M, ffn), np.int8)
+        sc = dev.empty((M, ffn // 32), np.float32)
+        qs = dev.empty((M, ffn // 32), np.int32)
+        capi.call("gx_matmul_swiglu_q4_0", dev.ctx.ptr, inter.ptr, capi.vp(act[0]), capi.vp(act[1]),
+                  capi.vp(act[2]), M, capi.vp(q), capi.vp(sc), capi.vp(qs))
+        gu = dev.empty((M, 2 * ffn), np.float32)
+        capi.call("gx_matmul_q4_0", dev.ctx.ptr, inter.ptr, capi.vp(act[0]), capi.vp(act[1]), capi.vp(act[2]),
+                  None, M, 0, 2 * ffn, None, capi.vp(gu), 2 * ffn)
+        q2 = dev.empty((M, ffn), np.int8)
+        sc2 = dev.empty((M, ffn // 32), np.float32)
+        qs2 = dev.empty((M, ffn // 32), np.int32)
+        capi.call("gx_swiglu_quant", dev.ctx.ptr, capi.vp(gu), 2 * ffn, M, ffn, 32, capi.vp(q2), capi.vp(sc2),
+                  capi.vp(qs2))
+        np.testing.assert_array_equal(dev.get(q), dev.get(q2))
+        np.testing.assert_array_equal(dev.get(sc).view(np.uint32), dev.get(sc2).view(np.uint32))
+        np.testing.assert_array_equal(dev.get(qs), dev.get(qs2))
+    inter.free()
+
+
+def test_matmul_swiglu_refuses_what_it_cannot_take(dev):
+    g = synth.rng(3)
+    act = dev.quantize_q8_0(synth.activations(g, 9, 4608), with_corr=False, with_q16=False)
+    q = dev.empty((9, 4608), np.int8)
+    sc = dev.empty((9, 4608 // 32), np.float32)
+    qs = dev.empty((9, 4608 // 32), np.int32)
+    wide = dev.weight(synth.q4_0_weights(g, 64, 4608), capi.Q4_0, 64, 4608)  # 18 stretches a row
+    odd = dev.weight(synth.q4_0_weights(g, 96, 256), capi.Q4_0, 96, 256)  # rows not a multiple of 64
+    fine = dev.weight(synth.q4_0_weights(g, 64, 256), capi.Q4_0, 64, 256)
+    for w, M in ((wide, 1), (odd, 1), (fine, 9)):  # 9 columns: more than the kernel takes
+        with pytest.raises(capi.GxError):
+            capi.call("gx_matmul_swiglu_q4_0", dev.ctx.ptr, w.ptr, capi.vp(act[0]), capi.vp(act[1]),
+                      capi.vp(act[2]), M, capi.vp(q), capi.vp(sc), capi.vp(qs))
+    wide.free()
+    odd.free()
+    fine.free()
+
+
 def test_fused_products_refuse_aliasing(dev):
     K, rows = 256, 64
     wd = dev.weight(synth.q4_0_weights(synth.rng(1), rows, K), capi.Q4_0, rows, K)
