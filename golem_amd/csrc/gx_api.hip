@@ -532,7 +532,7 @@ static int q4_0_product(gx_ctx *ctx, const gx_weight *w, int expert, const int8_
     const uint8_t *mat = w->dev + (size_t)expert * w->matrix_bytes;
     GX_CHECK(((uintptr_t)q16 & 15) == 0, "gx: q16 must be 16-byte aligned");
     int rc;
-    if (M <= 8)
+    if (M <= 16)
         rc = gx::launch_q4_0_matvec(ctx, w, mat, q, scales, qsum, M, row_start, row_end, bias, y, ldy, nullptr, -1);
     else if (q16)
         rc = gx::launch_q4_0_gemm_f16(ctx, w, mat, q16, scales, M, row_start, row_end, bias, y, ldy, nullptr);
@@ -635,7 +635,7 @@ int gx_matmul_swiglu_q4_0(gx_ctx *ctx, const gx_weight *w, const int8_t *q, cons
     GX_CHECK(w->count == 1, "gx: a SwiGLU product takes a single matrix");
     GX_CHECK(w->rows % 64 == 0,
              "gx: the SwiGLU form needs gate and up rows interleaved by 32 (rows a multiple of 64, not %d)", w->rows);
-    GX_CHECK(M >= 0 && M <= 8, "gx: the SwiGLU product takes 1 to 8 columns, not %d", M);
+    GX_CHECK(M >= 0 && M <= 16, "gx: the SwiGLU product takes 1 to 16 columns, not %d", M);
     GX_CHECK(q && scales && qsum && mid_q && mid_scales && mid_qsum, "gx: missing argument");
     GX_CHECK(((uintptr_t)q & 15) == 0, "gx: q must be 16-byte aligned");
     if (M == 0)
@@ -705,17 +705,17 @@ int gx_q4_0_block_dots(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const f
         return rc;
     GX_CHECK(q && qsum && scales, "gx: missing activation");
     GX_CHECK(((uintptr_t)q & 15) == 0, "gx: q must be 16-byte aligned");
-    GX_CHECK(path >= 0 && path <= 4,
-             "gx: path must be 0 (matrix-vector), 1 (int8 MFMA), 2 (fp16 MFMA), 3 (one-column matrix-vector) or 4 "
-             "(multi-column matrix-vector)");
+    GX_CHECK(path >= 0 && path <= 5,
+             "gx: path must be 0 (matrix-vector), 1 (int8 MFMA), 2 (fp16 MFMA), 3 (one-column matrix-vector), 4 "
+             "(multi-column matrix-vector) or 5 (few-column MFMA)");
     GX_CHECK(path != 2 || (q16 && ((uintptr_t)q16 & 15) == 0), "gx: path 2 needs a 16-byte aligned q16");
     GX_CHECK(path != 3 || M == 1, "gx: path 3 takes one column, not %d", M);
     if (M == 0 || row_start == row_end)
         return ok();
     int rc;
-    if (path == 0 || path == 3 || path == 4)
+    if (path == 0 || path >= 3)
         rc = gx::launch_q4_0_matvec(ctx, w, w->dev, q, scales, qsum, M, row_start, row_end, nullptr, nullptr, 0, out,
-                                    path == 0 ? 0 : path == 3 ? 1 : 2);
+                                    path == 0 ? 0 : path - 2);
     else if (path == 1)
         rc = gx::launch_q4_0_gemm(ctx, w, w->dev, q, scales, M, row_start, row_end, nullptr, nullptr, 0, out);
     else

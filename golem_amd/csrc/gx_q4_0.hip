@@ -422,6 +422,345 @@ __global__ __launch_bounds__(1024) void q4_0_matvec_cols_kernel(
     }
 }
 
+// ---- few columns on the matrix cores ---------------------------------------
+//
+// 2..16 columns (lock-step decode of several conversations, short batches):
+// the per-block integers come from v_mfma_i32_16x16x32_i8, 16 weight rows
+// against the same block of 16 columns, instead of from per-lane dot
+// products -- the multi-column kernel above spends ~25 vector instructions
+// per (row, column, block) and is VALU-bound from about 4 columns on
+// (config 3's Gate|Up at 8 columns: 28 MB in 26.8 us).
+//
+// Operands (one 16x16x32 MFMA a block): lane l holds row/column l % 16 and
+// inputs 8 (l / 16) .. 8 (l / 16) + 7 of the block.  A Q4_0 chunk holds
+// inputs 0..15 in the low nibbles of bytes 0..15 and 16..31 in the high
+// ones, so lane group k = l / 16 reads bytes 8 (k & 1) .. + 7 of its row's
+// chunk and takes the low (k < 2) or high nibbles, widened in place to
+// 16 (n - 8) as a signed byte.  The accumulators chain through a stretch
+// from the bits of kMfmaChainBias: read as fp32, each output is that bias plus
+// the stretch's running isum exactly (the ulp in [2^19, 2^20) is 1/16 and a
+// stretch's running sum is at most 8 * 32 * 8 * 128 = 2^18 in magnitude),
+// so the block's isum is the difference of two consecutive outputs, one
+// full-rate subtraction.  The scale product d_w * d_a of the tile is an
+// outer product of two fp16 vectors, exact in fp32: v_mfma_f32_16x16x16f16
+// with the two vectors at input 0 and zeros elsewhere.  The vector ALU is
+// left with one subtraction and one fma per output per block, in the
+// canonical order, so a column's values are those of every other kernel
+// bit for bit.
+//
+// Work: a workgroup owns RG row groups of 16 rows (R = 16 RG rows of one
+// tile); a unit is (row group, stretch), and wavefront w takes units w,
+// w + nwaves, ...  Each unit's stretch sum P_s for its 16 rows x 16 columns
+// goes to LDS part[s][c][r]; the sums over s in order follow a barrier.
+//   EPI 0: y[c][row] for rows [row_start, row_end), columns c < M.
+//   EPI 1 (RG = 4, whole tiles of gate and up interleaved by 32): the
+//          SwiGLU and Q8_0 epilogue of q4_0_matvec_cols_kernel<64, NC, .., 1>
+//          per column.
+typedef int v4i_mf __attribute__((ext_vector_type(4)));
+typedef float v4f_mf __attribute__((ext_vector_type(4)));
+typedef _Float16 v4h_mf __attribute__((ext_vector_type(4)));
+typedef unsigned v2u_mf __attribute__((ext_vector_type(2)));
+constexpr int kMfmaChainBias = 0x49400000;  // 1.5 * 2^19 as fp32 bits
+constexpr int kMfmaCols = 16;
+
+template <int RG, int EPI, bool DOTS>
+__global__ __launch_bounds__(1024) void q4_0_mfma_cols_kernel(
+    const uint8_t *__restrict__ W, size_t plane0_bytes, int B, int DC, const int8_t *__restrict__ q,
+    const float *__restrict__ scales, int M, int group0, int row_start, int row_end,
+    const float *__restrict__ bias, float *__restrict__ y, int ldy, int32_t *__restrict__ dots,
+    int8_t *__restrict__ mq, float *__restrict__ ms, int32_t *__restrict__ mqs) {
+    constexpr int R = 16 * RG, kSlots = kTileRows / R;
+    static_assert(EPI == 0 || RG == 4, "the SwiGLU epilogue takes whole tiles");
+    extern __shared__ __align__(16) float part[];  // [S][M][R]
+    const int K = B * kQ4Block;
+    const int S = (B + kStretch - 1) / kStretch;
+    const int tid = threadIdx.x, nt = blockDim.x;
+    const int lane = tid & 63, wave = tid >> 6, nw = nt >> 6;
+    const int g = group0 + blockIdx.x;
+    const int tile = g / kSlots, r0 = (g - tile * kSlots) * R;  // the group's first row within its tile
+    const int i = lane & 15, kb = lane >> 4;
+    const uint32_t wsh = kb < 2 ? 4u : 0u;  // low nibbles move up into the byte's high half
+    const bool col_ok = i < M;
+    const int8_t *qcol = q + (size_t)min(i, M - 1) * K + 8 * kb;
+    const float *scol = scales + (size_t)min(i, M - 1) * B;
+
+    for (int u = wave; u < RG * S; u += nw) {
+        const int rg = u / S, s = u - rg * S;
+        const int b0 = s * kStretch, nbk = min(kStretch, B - b0);
+        const int rl = r0 + 16 * rg + i;  // lane's row (as the A operand's row) within the tile
+        const uint8_t *wp = W + ((size_t)(tile * B + b0) * kTileRows + rl) * kChunk + 8 * (kb & 1);
+        // the unit's loads: the columns' inputs first, then the weights
+        long av[kStretch];
+        v2u_mf wv[kStretch];
+        float da[kStretch];
+        uint4 dch = make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+        for (int j = 0; j < kStretch; j++) {
+            av[j] = 0;
+            da[j] = 0.0f;
+            if (j < nbk && col_ok)
+                av[j] = *(const long *)(qcol + (size_t)(b0 + j) * kQ4Block);
+            if (j < nbk && col_ok && kb == 0)
+                da[j] = scol[b0 + j];
+        }
+#pragma unroll
+        for (int j = 0; j < kStretch; j++)
+            if (j < nbk)
+                wv[j] = __builtin_nontemporal_load((const v2u_mf *)(wp + (size_t)j * kTileRows * kChunk));
+        if (kb == 0)
+            dch = *(const uint4 *)(W + plane0_bytes + ((size_t)(tile * DC + s) * kTileRows + rl) * kChunk);
+
+        v4i_mf prev;
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            prev[e] = kMfmaChainBias;
+        const v4f_mf zero = {0.0f, 0.0f, 0.0f, 0.0f};
+        v4f_mf p = zero;
+#pragma unroll
+        for (int j = 0; j < kStretch; j++) {
+            if (j < nbk) {
+                const uint32_t lo = ((wv[j].x << wsh) & 0xF0F0F0F0u) ^ 0x80808080u;
+                const uint32_t hi = ((wv[j].y << wsh) & 0xF0F0F0F0u) ^ 0x80808080u;
+                const long A = (long)(((unsigned long)hi << 32) | lo);
+                const v4i_mf next = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, av[j], prev, 0, 0, 0);
+                const uint32_t dw = ((j >> 1) == 0 ? dch.x : (j >> 1) == 1 ? dch.y : (j >> 1) == 2 ? dch.z : dch.w);
+                const uint32_t dwh = (j & 1) ? (dw >> 16) : (dw & 0xFFFFu);
+                const v4h_mf wa = __builtin_bit_cast(v4h_mf, make_uint2(dwh, 0u));
+                const v4h_mf ca = __builtin_bit_cast(v4h_mf, make_uint2(float_to_half_bits(da[j]), 0u));
+                const v4f_mf sc = __builtin_amdgcn_mfma_f32_16x16x16f16(wa, ca, zero, 0, 0, 0);
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const float x = __int_as_float(next[e]) - __int_as_float(prev[e]);  // the block's isum
+                    p[e] = fmaf(x, sc[e], p[e]);
+                    if (DOTS) {
+                        const int row = tile * kTileRows + r0 + 16 * rg + 4 * kb + e;
+                        if (col_ok && row >= row_start && row < row_end)
+                            dots[((size_t)i * (row_end - row_start) + (row - row_start)) * B + b0 + j] = (int)x;
+                    }
+                }
+                prev = next;
+            }
+        }
+        if (col_ok)
+            *(float4 *)&part[((size_t)s * M + i) * R + 16 * rg + 4 * kb] = make_float4(p[0], p[1], p[2], p[3]);
+    }
+    if (DOTS)
+        return;
+    lds_barrier();
+    if (EPI == 1) {
+        const int F = row_end / 2;  // the SwiGLU's width: gate and up rows in equal number
+        for (int c = wave; c < M; c += nw) {
+            float acc = 0.0f;
+            for (int t = 0; t < S; t++)
+                acc = acc + part[((size_t)t * M + c) * kTileRows + lane];
+            // lane l < 32: gate 32 * tile + l; lane l + 32: its up
+            const float u = __shfl_down(acc, 32, 64);
+            const float gt = acc;
+            const float ex = ggml_expf(-gt);
+            const float den = 1.0f + ex;
+            const float sl = gt / den;
+            const float v = sl * u;
+            float stored;
+            int32_t sm;
+            const int32_t nq = q8_0_lane(v, &stored, &sm);
+            if (lane < 32) {
+                mq[(size_t)c * F + (size_t)tile * 32 + lane] = (int8_t)nq;
+                if (lane == 0) {
+                    ms[(size_t)c * (F / kQ4Block) + tile] = stored;
+                    mqs[(size_t)c * (F / kQ4Block) + tile] = sm;
+                }
+            }
+        }
+    } else {
+        for (int pr = tid; pr < M * R; pr += nt) {
+            const int c = pr / R, rr = pr - c * R;
+            const int orow = tile * kTileRows + r0 + rr;
+            if (orow >= row_start && orow < row_end) {
+                float acc = 0.0f;
+                for (int t = 0; t < S; t++)
+                    acc = acc + part[((size_t)t * M + c) * R + rr];
+                if (bias)
+                    acc = acc + bias[orow];
+                y[(size_t)c * ldy + orow] = acc;
+            }
+        }
+    }
+}
+
+// The same product with the columns' inputs and scales staged in LDS once
+// per workgroup (16-byte loads, every load of a pass in flight together)
+// and each wavefront's stretch multiplied for RG row groups against the
+// same B operands.  Reading the B operands straight from global memory
+// (q4_0_mfma_cols_kernel) costs a scattered 8-byte load per lane and block
+// and the whole activation again for every 16 rows: at config 3's shapes
+// and 8 columns that traffic, not the weights', set the time (Q|K|V
+// 8.1 us, of which the weights' loads alone 4.7).  Rows of the staged
+// activation are K + 16 bytes apart and its scales B + 1 floats apart, so
+// that the 16 columns x 4 lane groups of a B-operand read fall in distinct
+// LDS banks.  The stretch sums then reuse the activation's LDS (after a
+// barrier).  Takes S <= 16 stretches (one a wavefront).
+__host__ __device__ inline size_t mfma_lds_act_bytes(int M, int K, int B) {
+    return (((size_t)M * (K + 16) + 15) & ~(size_t)15) + (size_t)M * (B + 1) * sizeof(float);
+}
+
+template <int RG, int EPI, bool DOTS>
+__global__ __launch_bounds__(1024) void q4_0_mfma_cols_lds_kernel(
+    const uint8_t *__restrict__ W, size_t plane0_bytes, int B, int DC, const int8_t *__restrict__ q,
+    const float *__restrict__ scales, int M, int group0, int row_start, int row_end,
+    const float *__restrict__ bias, float *__restrict__ y, int ldy, int32_t *__restrict__ dots,
+    int8_t *__restrict__ mq, float *__restrict__ ms, int32_t *__restrict__ mqs) {
+    constexpr int R = 16 * RG, kSlots = kTileRows / R;
+    static_assert(EPI == 0 || RG == 4, "the SwiGLU epilogue takes whole tiles");
+    extern __shared__ __align__(16) uint8_t lds_raw[];
+    const int K = B * kQ4Block, ldq = K + 16, lds_b = B + 1;
+    const int S = (B + kStretch - 1) / kStretch;
+    int8_t *qa = (int8_t *)lds_raw;                                                 // [M][K + 16]
+    float *sa = (float *)(lds_raw + (((size_t)M * ldq + 15) & ~(size_t)15));       // [M][B + 1]
+    float *part = (float *)lds_raw;                                                 // [S][M][R], after the barrier
+    const int tid = threadIdx.x, nt = blockDim.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int g = group0 + blockIdx.x;
+    const int tile = g / kSlots, r0 = (g - tile * kSlots) * R;
+    const int i = lane & 15, kb = lane >> 4;
+    const uint32_t wsh = kb < 2 ? 4u : 0u;
+    const bool col_ok = i < M;
+
+    // the columns' inputs and scales into LDS, every load of a pass in flight
+    const int n16 = K / 16, p16 = M * n16, nb = M * B;
+    for (int base = 0; base < max(p16, nb); base += kColRegs * nt) {
+        int4 qv[kColRegs];
+        float sv[kColRegs];
+#pragma unroll
+        for (int k = 0; k < kColRegs; k++) {
+            const int e = base + tid + k * nt;
+            qv[k] = ((const int4 *)q)[min(e, p16 - 1)];
+            sv[k] = scales[min(e, nb - 1)];
+        }
+#pragma unroll
+        for (int k = 0; k < kColRegs; k++) {
+            const int e = base + tid + k * nt;
+            if (e < p16) {
+                const int c = e / n16;
+                *(int4 *)(qa + (size_t)c * ldq + (size_t)(e - c * n16) * 16) = qv[k];
+            }
+            if (e < nb) {
+                const int c = e / B;
+                sa[c * lds_b + (e - c * B)] = sv[k];
+            }
+        }
+    }
+    // then this wavefront's stretch of the RG row groups
+    const int s = wave, b0 = s * kStretch, nbk = min(kStretch, B - b0);
+    v2u_mf wv[RG][kStretch];
+    uint4 dch[RG];
+#pragma unroll
+    for (int rg = 0; rg < RG; rg++) {
+        const int rl = r0 + 16 * rg + i;
+        const uint8_t *wp = W + ((size_t)(tile * B + b0) * kTileRows + rl) * kChunk + 8 * (kb & 1);
+#pragma unroll
+        for (int j = 0; j < kStretch; j++)
+            if (j < nbk)
+                wv[rg][j] = __builtin_nontemporal_load((const v2u_mf *)(wp + (size_t)j * kTileRows * kChunk));
+        dch[rg] = make_uint4(0u, 0u, 0u, 0u);
+        if (kb == 0)
+            dch[rg] = *(const uint4 *)(W + plane0_bytes + ((size_t)(tile * DC + s) * kTileRows + rl) * kChunk);
+    }
+    lds_barrier();
+
+    const v4f_mf zero = {0.0f, 0.0f, 0.0f, 0.0f};
+    v4i_mf prev[RG];
+    v4f_mf p[RG];
+#pragma unroll
+    for (int rg = 0; rg < RG; rg++) {
+        p[rg] = zero;
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            prev[rg][e] = kMfmaChainBias;
+    }
+    const int8_t *qrow = qa + (size_t)min(i, M - 1) * ldq + 8 * kb;
+    const float *srow = sa + min(i, M - 1) * lds_b;
+#pragma unroll
+    for (int j = 0; j < kStretch; j++) {
+        if (j < nbk) {
+            const int b = b0 + j;
+            const long bop = col_ok ? *(const long *)(qrow + (size_t)b * kQ4Block) : 0;
+            const float da = (col_ok && kb == 0) ? srow[b] : 0.0f;
+            const v4h_mf ca = __builtin_bit_cast(v4h_mf, make_uint2(float_to_half_bits(da), 0u));
+#pragma unroll
+            for (int rg = 0; rg < RG; rg++) {
+                const uint32_t lo = ((wv[rg][j].x << wsh) & 0xF0F0F0F0u) ^ 0x80808080u;
+                const uint32_t hi = ((wv[rg][j].y << wsh) & 0xF0F0F0F0u) ^ 0x80808080u;
+                const long A = (long)(((unsigned long)hi << 32) | lo);
+                const v4i_mf next = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, bop, prev[rg], 0, 0, 0);
+                const uint32_t dw = (j >> 1) == 0 ? dch[rg].x : (j >> 1) == 1 ? dch[rg].y
+                                  : (j >> 1) == 2 ? dch[rg].z : dch[rg].w;
+                const uint32_t dwh = (j & 1) ? (dw >> 16) : (dw & 0xFFFFu);
+                const v4h_mf wa = __builtin_bit_cast(v4h_mf, make_uint2(dwh, 0u));
+                const v4f_mf sc = __builtin_amdgcn_mfma_f32_16x16x16f16(wa, ca, zero, 0, 0, 0);
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const float x = __int_as_float(next[e]) - __int_as_float(prev[rg][e]);  // the block's isum
+                    p[rg][e] = fmaf(x, sc[e], p[rg][e]);
+                    if (DOTS) {
+                        const int row = tile * kTileRows + r0 + 16 * rg + 4 * kb + e;
+                        if (col_ok && row >= row_start && row < row_end)
+                            dots[((size_t)i * (row_end - row_start) + (row - row_start)) * B + b] = (int)x;
+                    }
+                }
+                prev[rg] = next;
+            }
+        }
+    }
+    if (DOTS)
+        return;
+    lds_barrier();  // every wavefront is done with the staged activation
+    if (col_ok) {
+#pragma unroll
+        for (int rg = 0; rg < RG; rg++)
+            *(float4 *)&part[((size_t)s * M + i) * R + 16 * rg + 4 * kb] =
+                make_float4(p[rg][0], p[rg][1], p[rg][2], p[rg][3]);
+    }
+    lds_barrier();
+    if (EPI == 1) {
+        const int F = row_end / 2;
+        for (int c = wave; c < M; c += nt >> 6) {
+            float acc = 0.0f;
+            for (int t = 0; t < S; t++)
+                acc = acc + part[((size_t)t * M + c) * kTileRows + lane];
+            // lane l < 32: gate 32 * tile + l; lane l + 32: its up
+            const float u = __shfl_down(acc, 32, 64);
+            const float gt = acc;
+            const float ex = ggml_expf(-gt);
+            const float den = 1.0f + ex;
+            const float sl = gt / den;
+            const float v = sl * u;
+            float stored;
+            int32_t sm;
+            const int32_t nq = q8_0_lane(v, &stored, &sm);
+            if (lane < 32) {
+                mq[(size_t)c * F + (size_t)tile * 32 + lane] = (int8_t)nq;
+                if (lane == 0) {
+                    ms[(size_t)c * (F / kQ4Block) + tile] = stored;
+                    mqs[(size_t)c * (F / kQ4Block) + tile] = sm;
+                }
+            }
+        }
+    } else {
+        for (int pr = tid; pr < M * R; pr += nt) {
+            const int c = pr / R, rr = pr - c * R;
+            const int orow = tile * kTileRows + r0 + rr;
+            if (orow >= row_start && orow < row_end) {
+                float acc = 0.0f;
+                for (int t = 0; t < S; t++)
+                    acc = acc + part[((size_t)t * M + c) * R + rr];
+                if (bias)
+                    acc = acc + bias[orow];
+                y[(size_t)c * ldy + orow] = acc;
+            }
+        }
+    }
+}
+
 // One position (M = 1) whose activation is produced by the product itself:
 // x (+ add) -> RMSNormPlain(gain, eps) -> Q8_0, a block's pre-norm
 // (qwen/block.go:45-52, 59-68), so that the norm needs no kernel of its own.
@@ -792,6 +1131,56 @@ int launch_cols_swiglu(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const f
     return check_launch("q4_0_matvec_cols_swiglu");
 }
 
+// The few-column MFMA product: R = 16 rows a workgroup (EPI 0) or whole
+// tiles (EPI 1), a wavefront a (row group, stretch) unit at a time.
+size_t mfma_cols_lds(const gx_weight *w, int M, int R) {
+    const int S = (w->blocks + kStretch - 1) / kStretch;
+    return (size_t)S * M * R * sizeof(float);
+}
+
+int launch_mfma_cols(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, const int8_t *q, const float *scales, int M,
+                     int row_start, int row_end, const float *bias, float *y, int ldy, int32_t *dots) {
+    const int B = w->blocks, S = (B + kStretch - 1) / kStretch;
+    const int tile0 = row_start / kTileRows;
+    const int tiles = (row_end + kTileRows - 1) / kTileRows - tile0;
+    // The LDS-staged form when a wavefront a stretch covers the row and the
+    // columns fit: 32-row workgroups when that still gives a workgroup a CU
+    // (config 3 at 8 columns, graph of launches over rotating copies:
+    // Gate|Up 17.7 -> 16.0 us, Q|K|V 8.1 -> 7.7, O 6.7 -> 6.3), else 16.
+    const int RG = tiles * 2 >= ctx->cu_count ? 2 : 1;
+    const size_t staged = std::max(mfma_lds_act_bytes(M, w->cols, B), mfma_cols_lds(w, M, 16 * RG));
+    if (S <= 16 && staged <= 64 * 1024) {
+        const int slots = kTileRows / (16 * RG);
+        const unsigned grid = (unsigned)(tiles * slots), threads = (unsigned)(64 * S);
+#define GX_MF(RR, DD)                                                                                                \
+    q4_0_mfma_cols_lds_kernel<RR, 0, DD><<<grid, threads, staged, ctx->stream>>>(                                    \
+        mat, w->plane0_bytes, B, w->dchunks, q, scales, M, tile0 * slots, row_start, row_end, bias, y, ldy, dots,    \
+        nullptr, nullptr, nullptr)
+        if (RG == 2 && dots)
+            GX_MF(2, true);
+        else if (RG == 2)
+            GX_MF(2, false);
+        else if (dots)
+            GX_MF(1, true);
+        else
+            GX_MF(1, false);
+#undef GX_MF
+        return check_launch("q4_0_mfma_cols_lds");
+    }
+    constexpr int kSlots = kTileRows / 16;
+    const unsigned grid = (unsigned)(tiles * kSlots), threads = (unsigned)(64 * min(S, 16));
+    const size_t lds = mfma_cols_lds(w, M, 16);
+    if (dots)
+        q4_0_mfma_cols_kernel<1, 0, true><<<grid, threads, lds, ctx->stream>>>(
+            mat, w->plane0_bytes, w->blocks, w->dchunks, q, scales, M, tile0 * kSlots, row_start, row_end, bias, y,
+            ldy, dots, nullptr, nullptr, nullptr);
+    else
+        q4_0_mfma_cols_kernel<1, 0, false><<<grid, threads, lds, ctx->stream>>>(
+            mat, w->plane0_bytes, w->blocks, w->dchunks, q, scales, M, tile0 * kSlots, row_start, row_end, bias, y,
+            ldy, nullptr, nullptr, nullptr, nullptr);
+    return check_launch("q4_0_mfma_cols");
+}
+
 }  // namespace
 
 int launch_q4_0_matvec(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, const int8_t *q, const float *scales,
@@ -834,6 +1223,10 @@ int launch_q4_0_matvec(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, cons
     // conversations, kernel trace), against the whole-tile kernel: Down
     // 2 x 21.6 -> 2 x 11.7 us, O 17.7 -> 12.4, Q|K|V 15.8 -> 13.7, Gate|Up
     // 27.8 -> 28.7 (whole tiles either way).
+    // 2..16 columns (or form 3): the per-block integers on the matrix cores.
+    if (((M >= 2 && form < 0) || form == 3) && M <= kMfmaCols && mfma_cols_lds(w, M, 16) <= 64 * 1024)
+        return launch_mfma_cols(ctx, w, mat, q, scales, M, row_start, row_end, bias, y, ldy, dots);
+    GX_CHECK(form != 3, "gx: %d columns of %d inputs do not fit the few-column MFMA kernel", M, w->cols);
     if ((M >= 2 && form != 0) || form == 2) {
         int c = 0;
         while (c < M) {
@@ -914,6 +1307,20 @@ int launch_q4_0_matvec(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, cons
 int launch_q4_0_matvec_swiglu(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const float *scales,
                                const int32_t *qsum, int M, int8_t *mq, float *ms, int32_t *mqs) {
     const int K = w->cols, B = w->blocks, S = (B + kStretch - 1) / kStretch, F = w->rows / 2;
+    const size_t staged = std::max(mfma_lds_act_bytes(M, K, B), mfma_cols_lds(w, M, kTileRows));
+    if (M <= kMfmaCols && S <= 16 && staged <= 64 * 1024) {
+        q4_0_mfma_cols_lds_kernel<4, 1, false><<<w->tiles, 64 * S, staged, ctx->stream>>>(
+            w->dev, w->plane0_bytes, B, w->dchunks, q, scales, M, 0, 0, w->rows, nullptr, nullptr, 0, nullptr, mq, ms,
+            mqs);
+        return check_launch("q4_0_mfma_cols_lds_swiglu");
+    }
+    if (M <= kMfmaCols && mfma_cols_lds(w, M, kTileRows) <= 64 * 1024) {
+        q4_0_mfma_cols_kernel<4, 1, false><<<w->tiles, 64 * min(4 * S, 16), mfma_cols_lds(w, M, kTileRows),
+                                              ctx->stream>>>(w->dev, w->plane0_bytes, B, w->dchunks, q, scales, M,
+                                                             0, 0, w->rows, nullptr, nullptr, 0, nullptr, mq, ms,
+                                                             mqs);
+        return check_launch("q4_0_mfma_cols_swiglu");
+    }
     GX_CHECK(S <= 16, "gx: a %d-input row is too wide for the multi-column SwiGLU product", K);
     int c = 0;
     while (c < M) {

@@ -151,11 +151,12 @@ int gx_quantize_q8_k(gx_ctx *ctx, const float *x, int ldx, int M, int K, int8_t 
  * rows r in [row_start, row_end) of a Q4_0 matrix: Matrix.MatVecBatch and
  * MatVecRows for Q4_0 (nn/matrix.go:78-104), and MatVecQ4_0
  * (nn/dot_q4_0.go:117-124) when the range is all rows.  bias is NULL or
- * rows floats (device).  M <= 8 runs a bandwidth-bound matrix-vector
- * kernel (one column: activation in scalar registers, or in LDS on quarter
- * tiles for a matrix of few tiles; 2..8 columns: activations in LDS, on whole,
- * half or quarter tiles); larger M runs an MFMA product: on fp16 MFMA when q16 is given,
- * else on int8 MFMA.  All of them sum every row's blocks in the same order
+ * rows floats (device).  One column runs a bandwidth-bound matrix-vector
+ * kernel (activation in scalar registers, or in LDS on quarter tiles for a
+ * matrix of few tiles); 2..16 columns the few-column int8-MFMA kernel
+ * (16 rows against 16 columns a block); larger M a tiled MFMA product: on
+ * fp16 MFMA when q16 is given, else on int8 MFMA.  All of them sum every
+ * row's blocks in the same order
  * from the same exact per-block integers, so a column's result does not
  * depend on M or on the kernel. */
 int gx_matmul_q4_0(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const float *scales, const int32_t *qsum,
@@ -218,8 +219,9 @@ int gx_matmul_f32(gx_ctx *ctx, const gx_weight *w, const float *x, int ldx, int 
  * path 3: the one-column matrix-vector kernel with the activation in LDS
  * (M = 1, the whole/half/quarter-tile shape the product picks for this
  * matrix); path 4: the multi-column matrix-vector kernel with the
- * activations in LDS (what products of 2 <= M <= 8 run, in the column groups
- * and tile shape the product picks).  golem's dotQ4_0Go accumulator
+ * activations in LDS (2..8 columns a launch, in the column groups and tile
+ * shape it picks); path 5: the few-column int8-MFMA kernel (what products of
+ * 2 <= M <= 16 run).  golem's dotQ4_0Go accumulator
  * (nn/dot_q4_0.go:58-63) is this plus 8*qsum.  No counterpart in golem:
  * parity instrumentation. */
 int gx_q4_0_block_dots(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const float *scales, const int32_t *qsum,
@@ -477,8 +479,8 @@ int gx_norm_swiglu_q4_0(gx_ctx *ctx, const gx_weight *w, const float *x, const f
  * the same up rows), then silu(gate) * up and its Q8_0 into mid_q
  * [M][rows/2], mid_scales and mid_qsum [M][rows/64] -- bit for bit
  * gx_matmul_q4_0 followed by gx_swiglu_quant (group 32) (qwen/block.go:
- * 82-90, nn/swiglu.go:77-82), in one kernel a group of columns: for 1 to 8
- * positions (golem's lock-step slots, short batches).  No counterpart in
+ * 82-90, nn/swiglu.go:77-82), in one kernel: for 1 to 16 positions
+ * (golem's lock-step slots, short batches).  No counterpart in
  * golem as one call. */
 int gx_matmul_swiglu_q4_0(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const float *scales,
                           const int32_t *qsum, int M, int8_t *mid_q, float *mid_scales, int32_t *mid_qsum);

@@ -57,10 +57,12 @@ def test_dequantized_rows_cover_every_half(dev, orc):
 
 @pytest.mark.parametrize("rows,cols,M", [(64, 256, 1), (200, 2560, 3), (96, 704, 9), (130, 2816, 40),
                                          (300, 2560, 1)])
-@pytest.mark.parametrize("path", [0, 1, 2, 3, 4])
+@pytest.mark.parametrize("path", [0, 1, 2, 3, 4, 5])
 def test_block_integers_bit_exact(dev, orc, rows, cols, M, path):
     if path == 3 and M != 1:
         pytest.skip("the one-column kernel takes M = 1")
+    if path == 5 and M > 16:
+        pytest.skip("the few-column MFMA kernel takes at most 16 columns")
     log(f"q4_0 block dots rows={rows} cols={cols} M={M} path={path}")
     w, b, wd, act = setup(dev, orc, rows, cols, M, 100 + rows)
     start, end = (0, rows) if rows < 100 else (5, rows - 3)
@@ -76,16 +78,20 @@ def test_block_integers_bit_exact(dev, orc, rows, cols, M, path):
     (6144, 2560, 8, (0, 6144)),     # Q|K|V: half tiles
     (19456, 2560, 3, (64, 19456)),  # Gate|Up: whole tiles
     (9728, 2560, 2, (0, 9728)),     # config 0's matrix
+    (2560, 9728, 16, (3, 2557)),    # Down at 16 columns (path 4 in groups of 8)
+    (200, 2816, 11, (0, 200)),      # a ragged last tile
 ])
-def test_multi_column_integers_every_shape(dev, orc, rows, cols, M, span):
-    """Path 4 -- the multi-column kernel golem's lock-step slots run (2 to 8
-    columns) -- bit for bit against golem's accumulator, and every column of
-    its product equal to that column's one-column product bit for bit
-    (golem's batch == one at a time, nn/dot_q4_0.go:143-146)."""
-    log(f"multi-column dots rows={rows} cols={cols} M={M} span={span}")
+@pytest.mark.parametrize("path", [4, 5])
+def test_multi_column_integers_every_shape(dev, orc, rows, cols, M, span, path):
+    """Path 4 (the multi-column matrix-vector kernel) and path 5 (the
+    few-column MFMA kernel golem's lock-step slots run, 2 to 16 columns), bit
+    for bit against golem's accumulator, and every column of the product
+    equal to that column's one-column product bit for bit (golem's batch ==
+    one at a time, nn/dot_q4_0.go:143-146)."""
+    log(f"multi-column dots rows={rows} cols={cols} M={M} span={span} path={path}")
     w, b, wd, act = setup(dev, orc, rows, cols, M, 900 + rows + M)
     start, end = span
-    got = dev.q4_0_block_dots(wd, act, M, start, end, 4)
+    got = dev.q4_0_block_dots(wd, act, M, start, end, path)
     acc = orc.q4_0_block_acc(w, b, rows)[:, start:end, :]
     np.testing.assert_array_equal(got, acc - 8 * b.qsum_rows()[:, None, :])
     y = dev.get(dev.matmul_q4_0(wd, act, M, start, end))
@@ -235,9 +241,9 @@ def test_row_ranges_and_bias(dev, orc, span):
 @pytest.mark.parametrize("f16", [True, False])
 @pytest.mark.parametrize("rows,cols", [(9728, 2560), (2560, 9728), (2816, 704), (200, 2816)])
 def test_batch_equals_one_at_a_time(dev, orc, rows, cols, f16):
-    """Every column of a batch -- M in 1..8 on the matrix-vector kernel, larger
-    M on the fp16-MFMA (f16) or int8-MFMA kernel -- is bit-identical to the
-    same column computed alone."""
+    """Every column of a batch -- one column on the matrix-vector kernel, 2..16
+    on the few-column MFMA kernel, larger M on the fp16-MFMA (f16) or
+    int8-MFMA kernel -- is bit-identical to the same column computed alone."""
     M = 70
     g = synth.rng(400 + rows)
     w = synth.q4_0_weights(g, rows, cols)
@@ -256,7 +262,7 @@ def test_batch_equals_one_at_a_time(dev, orc, rows, cols, f16):
     # Each sub-batch is quantised on its own (the fp16 copy is panel-ordered,
     # so a prefix of tokens is not a prefix of the buffer; the quantiser is
     # exact per token, which test_gpu_quant pins).
-    for m in (1, 2, 3, 5, 8, 9, 33):
+    for m in (1, 2, 3, 5, 8, 9, 16, 17, 33):
         part = dev.get(dev.matmul_q4_0(wd, dev.quantize_q8_0(x[:m], with_corr=False), m, f16=f16))
         np.testing.assert_array_equal(part.view(np.uint32), whole[:m].view(np.uint32))
     for c in (0, 17, 69):

@@ -443,9 +443,9 @@ def test_norm_swiglu_fused_bit_exact(dev, ffn, K):
     inter.free()
 
 
-@pytest.mark.parametrize("ffn,K", [(9728, 2560), (1056, 2080), (32, 256)])
+@pytest.mark.parametrize("ffn,K", [(9728, 2560), (1056, 2080), (32, 256), (96, 4608)])
 def test_matmul_swiglu_columns_bit_exact(dev, ffn, K):
-    """gx_matmul_swiglu_q4_0 (the product of 1 to 8 columns with SwiGLU and
+    """gx_matmul_swiglu_q4_0 (the product of 1 to 16 columns with SwiGLU and
     Q8_0 in its epilogue) against gx_matmul_q4_0 of the same interleaved
     matrix then gx_swiglu_quant (group 32), column by column, bit for bit."""
     from golem_amd.qwen import interleave_rows
@@ -453,7 +453,8 @@ def test_matmul_swiglu_columns_bit_exact(dev, ffn, K):
     gate = synth.q4_0_weights(g, ffn, K)
     up = synth.q4_0_weights(g, ffn, K)
     inter = dev.weight(interleave_rows(gate, up, ffn, K), capi.Q4_0, 2 * ffn, K)
-    for M in (1, 2, 3, 5, 8):
+    # K = 4608 (18 stretches) takes the form without staging, up to 8 columns
+    for M in ((1, 2, 3, 5, 8, 16) if K <= 4096 else (1, 2, 8)):
         log(f"matmul swiglu ffn={ffn} K={K} M={M}")
         act = dev.quantize_q8_0((synth.activations(g, M, K) * 2).astype(np.float32), with_corr=False,
                                 with_q16=False)
@@ -478,17 +479,20 @@ def test_matmul_swiglu_columns_bit_exact(dev, ffn, K):
 
 def test_matmul_swiglu_refuses_what_it_cannot_take(dev):
     g = synth.rng(3)
-    act = dev.quantize_q8_0(synth.activations(g, 9, 4608), with_corr=False, with_q16=False)
-    q = dev.empty((9, 4608), np.int8)
-    sc = dev.empty((9, 4608 // 32), np.float32)
-    qs = dev.empty((9, 4608 // 32), np.int32)
-    wide = dev.weight(synth.q4_0_weights(g, 64, 4608), capi.Q4_0, 64, 4608)  # 18 stretches a row
+    M, K = 17, 8192
+    act = dev.quantize_q8_0(synth.activations(g, M, K), with_corr=False, with_q16=False)
+    q = dev.empty((M, K), np.int8)
+    sc = dev.empty((M, K // 32), np.float32)
+    qs = dev.empty((M, K // 32), np.int32)
+    # 16 columns of 32 stretches: more stretch sums than the LDS holds, and
+    # more stretches than the multi-column kernel's wavefronts
+    wide = dev.weight(synth.q4_0_weights(g, 64, K), capi.Q4_0, 64, K)
     odd = dev.weight(synth.q4_0_weights(g, 96, 256), capi.Q4_0, 96, 256)  # rows not a multiple of 64
     fine = dev.weight(synth.q4_0_weights(g, 64, 256), capi.Q4_0, 64, 256)
-    for w, M in ((wide, 1), (odd, 1), (fine, 9)):  # 9 columns: more than the kernel takes
+    for w, m in ((wide, 16), (odd, 1), (fine, 17)):  # 17 columns: more than the kernel takes
         with pytest.raises(capi.GxError):
             capi.call("gx_matmul_swiglu_q4_0", dev.ctx.ptr, w.ptr, capi.vp(act[0]), capi.vp(act[1]),
-                      capi.vp(act[2]), M, capi.vp(q), capi.vp(sc), capi.vp(qs))
+                      capi.vp(act[2]), m, capi.vp(q), capi.vp(sc), capi.vp(qs))
     wide.free()
     odd.free()
     fine.free()
