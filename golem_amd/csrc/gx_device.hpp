@@ -29,6 +29,17 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// An LDS pointer, for the direct global-to-LDS loads.
+typedef __attribute__((address_space(3))) void *lds_ptr;
+
+// Wait until at most N vector-memory operations of this wavefront are in
+// flight (expcnt and lgkmcnt unconstrained).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
 // The j-th of the eight fp16 values packed in a 16-byte chunk.
 __device__ __forceinline__ float chunk_half(const uint4 &c, int j) {
     const uint32_t word = (j >> 1) == 0 ? c.x : (j >> 1) == 1 ? c.y : (j >> 1) == 2 ? c.z : c.w;

@@ -329,7 +329,6 @@ constexpr int kDmaRing = 3;
 // subtraction instead of a quarter-rate int->float conversion -- and feeds
 // golem's fma unchanged.
 constexpr int kChainBias = 0x49400000;  // 786432.0f
-typedef __attribute__((address_space(3))) void *lds_ptr;
 
 // One block's operands from LDS (nibbles, activations, weight scale,
 // activation scale), issued without a wait.  Written out so that the
@@ -356,11 +355,6 @@ __device__ __forceinline__ void unroll(F &&f) {  // f(integral_constant<int, J>)
     }
 }
 
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {  // vmcnt <= N; expcnt, lgkmcnt unconstrained
-    static_assert(N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
-}
 
 // The two tile shapes of the direct-to-LDS product.  Both: a workgroup owns
 // 128 rows (two R64 tiles), a wavefront one 32x32 MFMA tile (rows 32*(w&3),

@@ -462,6 +462,7 @@ typedef _Float16 v4h_mf __attribute__((ext_vector_type(4)));
 typedef unsigned v2u_mf __attribute__((ext_vector_type(2)));
 constexpr int kMfmaChainBias = 0x49400000;  // 1.5 * 2^19 as fp32 bits
 constexpr int kMfmaCols = 16;
+constexpr size_t kLdsMax = 160 * 1024;  // a gfx950 workgroup's LDS
 
 template <int RG, int EPI, bool DOTS>
 __global__ __launch_bounds__(1024) void q4_0_mfma_cols_kernel(
@@ -588,23 +589,200 @@ __global__ __launch_bounds__(1024) void q4_0_mfma_cols_kernel(
 }
 
 // The same product with the columns' inputs and scales staged in LDS once
-// per workgroup (16-byte loads, every load of a pass in flight together)
-// and each wavefront's stretch multiplied for RG row groups against the
-// same B operands.  Reading the B operands straight from global memory
-// (q4_0_mfma_cols_kernel) costs a scattered 8-byte load per lane and block
-// and the whole activation again for every 16 rows: at config 3's shapes
-// and 8 columns that traffic, not the weights', set the time (Q|K|V
-// 8.1 us, of which the weights' loads alone 4.7).  Rows of the staged
-// activation are K + 16 bytes apart and its scales B + 1 floats apart, so
-// that the 16 columns x 4 lane groups of a B-operand read fall in distinct
-// LDS banks.  The stretch sums then reuse the activation's LDS (after a
-// barrier).  Takes S <= 16 stretches (one a wavefront).
+// per workgroup (16-byte loads, every load of a pass in flight together).
+// Reading the B operands straight from global memory (q4_0_mfma_cols_kernel)
+// costs a scattered 8-byte load per lane and block and the whole activation
+// again for every 16 rows: at config 3's shapes and 8 columns that traffic,
+// not the weights', set the time (Q|K|V 8.1 us, of which the weights' loads
+// alone 4.7).  Rows of the staged activation are K + 16 bytes apart and its
+// scales B + 1 floats apart, so that the 16 columns x 4 lane groups of a
+// B-operand read fall in distinct LDS banks.  The stretch sums then reuse
+// the activation's LDS (after a barrier).  This form (16 rows a workgroup)
+// serves rows of 17 to 48 stretches: wavefront w takes stretches w, w + 16,
+// .. (SW of them at most), their weights all requested into registers
+// before the barrier; rows of at most 16 stretches take the form below,
+// whose weights arrive through LDS.
 __host__ __device__ inline size_t mfma_lds_act_bytes(int M, int K, int B) {
     return (((size_t)M * (K + 16) + 15) & ~(size_t)15) + (size_t)M * (B + 1) * sizeof(float);
 }
 
-template <int RG, int EPI, bool DOTS>
+template <int SW, bool DOTS>
 __global__ __launch_bounds__(1024) void q4_0_mfma_cols_lds_kernel(
+    const uint8_t *__restrict__ W, size_t plane0_bytes, int B, int DC, const int8_t *__restrict__ q,
+    const float *__restrict__ scales, int M, int group0, int row_start, int row_end,
+    const float *__restrict__ bias, float *__restrict__ y, int ldy, int32_t *__restrict__ dots) {
+    constexpr int RG = 1, R = 16, kSlots = kTileRows / R;
+    extern __shared__ __align__(16) uint8_t lds_raw[];
+    const int K = B * kQ4Block, ldq = K + 16, lds_b = B + 1;
+    const int S = (B + kStretch - 1) / kStretch;
+    int8_t *qa = (int8_t *)lds_raw;                                                 // [M][K + 16]
+    float *sa = (float *)(lds_raw + (((size_t)M * ldq + 15) & ~(size_t)15));       // [M][B + 1]
+    float *part = (float *)lds_raw;                                                 // [S][M][R], after the barrier
+    const int tid = threadIdx.x, nt = blockDim.x;
+    const int lane = tid & 63, wave = tid >> 6, nw = nt >> 6;
+    const int g = group0 + blockIdx.x;
+    const int tile = g / kSlots, r0 = (g - tile * kSlots) * R;
+    const int i = lane & 15, kb = lane >> 4;
+    const uint32_t wsh = kb < 2 ? 4u : 0u;
+    const bool col_ok = i < M;
+
+    // The columns' inputs and scales into LDS, every load of a pass in
+    // flight together, and only then this wavefront's weights.  (Weights
+    // requested before the staging loads have landed are slower: config 3's
+    // Down at 8 columns 12.2 -> 13.8 us, Gate|Up 16.0 -> 19.2 us.)
+    const int n16 = K / 16, p16 = M * n16, nb = M * B;
+    for (int base = 0; base < max(p16, nb); base += kColRegs * nt) {
+        int4 qv[kColRegs];
+        float sv[kColRegs];
+#pragma unroll
+        for (int k = 0; k < kColRegs; k++) {
+            const int e = base + tid + k * nt;
+            qv[k] = ((const int4 *)q)[min(e, p16 - 1)];
+            sv[k] = scales[min(e, nb - 1)];
+        }
+#pragma unroll
+        for (int k = 0; k < kColRegs; k++) {
+            const int e = base + tid + k * nt;
+            if (e < p16) {
+                const int c = e / n16;
+                *(int4 *)(qa + (size_t)c * ldq + (size_t)(e - c * n16) * 16) = qv[k];
+            }
+            if (e < nb) {
+                const int c = e / B;
+                sa[c * lds_b + (e - c * B)] = sv[k];
+            }
+        }
+    }
+    // this wavefront's stretches wave, wave + nw, .. (SW of them at most) of
+    // the RG row groups, every load in flight together
+    v2u_mf wv[SW][RG][kStretch];
+    uint4 dch[SW][RG];
+#pragma unroll
+    for (int k = 0; k < SW; k++) {
+        const int s = wave + k * nw, b0 = s * kStretch, nbk = min(kStretch, B - b0);
+#pragma unroll
+        for (int rg = 0; rg < RG; rg++) {
+            const int rl = r0 + 16 * rg + i;
+            const uint8_t *wp = W + ((size_t)(tile * B + b0) * kTileRows + rl) * kChunk + 8 * (kb & 1);
+#pragma unroll
+            for (int j = 0; j < kStretch; j++)
+                if (j < nbk)
+                    wv[k][rg][j] = __builtin_nontemporal_load((const v2u_mf *)(wp + (size_t)j * kTileRows * kChunk));
+            dch[k][rg] = make_uint4(0u, 0u, 0u, 0u);
+            if (kb == 0 && s < S)
+                dch[k][rg] = *(const uint4 *)(W + plane0_bytes + ((size_t)(tile * DC + s) * kTileRows + rl) * kChunk);
+        }
+    }
+    lds_barrier();
+
+    const v4f_mf zero = {0.0f, 0.0f, 0.0f, 0.0f};
+    v4f_mf p[SW][RG];
+    const int8_t *qrow = qa + (size_t)min(i, M - 1) * ldq + 8 * kb;
+    const float *srow = sa + min(i, M - 1) * lds_b;
+    // stretch by stretch: the first one's blocks are multiplied while the
+    // later stretches' weights still arrive (interleaving the stretches'
+    // blocks instead, for independent MFMA chains, waits for every stretch
+    // first: config 3's Down at 8 columns 12.2 -> 14.0 us)
+#pragma unroll
+    for (int k = 0; k < SW; k++) {
+        const int s = wave + k * nw, b0 = s * kStretch, nbk = min(kStretch, B - b0);  // nbk <= 0 past the row
+        v4i_mf prev[RG];
+#pragma unroll
+        for (int rg = 0; rg < RG; rg++) {
+            p[k][rg] = zero;
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                prev[rg][e] = kMfmaChainBias;
+        }
+#pragma unroll
+        for (int j = 0; j < kStretch; j++) {
+            if (j < nbk) {
+                const int b = b0 + j;
+                const long bop = col_ok ? *(const long *)(qrow + (size_t)b * kQ4Block) : 0;
+                const float da = (col_ok && kb == 0) ? srow[b] : 0.0f;
+                const v4h_mf ca = __builtin_bit_cast(v4h_mf, make_uint2(float_to_half_bits(da), 0u));
+#pragma unroll
+                for (int rg = 0; rg < RG; rg++) {
+                    const uint32_t lo = ((wv[k][rg][j].x << wsh) & 0xF0F0F0F0u) ^ 0x80808080u;
+                    const uint32_t hi = ((wv[k][rg][j].y << wsh) & 0xF0F0F0F0u) ^ 0x80808080u;
+                    const long A = (long)(((unsigned long)hi << 32) | lo);
+                    const v4i_mf next = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, bop, prev[rg], 0, 0, 0);
+                    const uint4 &dc = dch[k][rg];
+                    const uint32_t dw = (j >> 1) == 0 ? dc.x : (j >> 1) == 1 ? dc.y : (j >> 1) == 2 ? dc.z : dc.w;
+                    const uint32_t dwh = (j & 1) ? (dw >> 16) : (dw & 0xFFFFu);
+                    const v4h_mf wa = __builtin_bit_cast(v4h_mf, make_uint2(dwh, 0u));
+                    const v4f_mf sc = __builtin_amdgcn_mfma_f32_16x16x16f16(wa, ca, zero, 0, 0, 0);
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const float x = __int_as_float(next[e]) - __int_as_float(prev[rg][e]);  // the block's isum
+                        p[k][rg][e] = fmaf(x, sc[e], p[k][rg][e]);
+                        if (DOTS) {
+                            const int row = tile * kTileRows + r0 + 16 * rg + 4 * kb + e;
+                            if (col_ok && row >= row_start && row < row_end)
+                                dots[((size_t)i * (row_end - row_start) + (row - row_start)) * B + b] = (int)x;
+                        }
+                    }
+                    prev[rg] = next;
+                }
+            }
+        }
+    }
+    if (DOTS)
+        return;
+    lds_barrier();  // every wavefront is done with the staged activation
+    if (col_ok) {
+#pragma unroll
+        for (int k = 0; k < SW; k++) {
+            const int s = wave + k * nw;
+            if (s < S) {
+#pragma unroll
+                for (int rg = 0; rg < RG; rg++)
+                    *(float4 *)&part[((size_t)s * M + i) * R + 16 * rg + 4 * kb] =
+                        make_float4(p[k][rg][0], p[k][rg][1], p[k][rg][2], p[k][rg][3]);
+            }
+        }
+    }
+    lds_barrier();
+    for (int pr = tid; pr < M * R; pr += nt) {
+        const int c = pr / R, rr = pr - c * R;
+        const int orow = tile * kTileRows + r0 + rr;
+        if (orow >= row_start && orow < row_end) {
+            float acc = 0.0f;
+            for (int t = 0; t < S; t++)
+                acc = acc + part[((size_t)t * M + c) * R + rr];
+            if (bias)
+                acc = acc + bias[orow];
+            y[(size_t)c * ldy + orow] = acc;
+        }
+    }
+}
+
+// The LDS-staged product with the weights arriving in LDS too: each
+// wavefront's row groups go global -> LDS as whole 16-byte chunks (lane l:
+// row l % 16 of the group, blocks l / 16 and 4 + l / 16 of the stretch), two
+// row groups in flight in a ring of two 2 KiB slots, and the A operands are
+// read back in the MFMA's layout (8 bytes a lane).  Against 8-byte loads
+// straight into registers this halves the weights' load instructions and
+// frees the registers that held them (64 for four row groups).  The compute
+// phase reads LDS through inline asm only: the compiler would otherwise make
+// every LDS read wait for all global-to-LDS loads in flight.
+constexpr int kMfmaSlotB = 2048;  // one row group's stretch: 16 rows x 8 blocks x 16 bytes
+
+template <int OFF>
+__device__ __forceinline__ void ds_read_u64(uint32_t addr, v2u_mf &r) {
+    asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
+}
+template <int OFF>
+__device__ __forceinline__ void ds_read_f32(uint32_t addr, float &r) {
+    asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
+}
+
+__host__ __device__ inline size_t mfma_dma_ring_offset(int M, int K, int B) {
+    return (mfma_lds_act_bytes(M, K, B) + 15) & ~(size_t)15;
+}
+
+template <int RG, int EPI, bool DOTS>
+__global__ __launch_bounds__(1024) void q4_0_mfma_cols_dma_kernel(
     const uint8_t *__restrict__ W, size_t plane0_bytes, int B, int DC, const int8_t *__restrict__ q,
     const float *__restrict__ scales, int M, int group0, int row_start, int row_end,
     const float *__restrict__ bias, float *__restrict__ y, int ldy, int32_t *__restrict__ dots,
@@ -619,11 +797,13 @@ __global__ __launch_bounds__(1024) void q4_0_mfma_cols_lds_kernel(
     float *part = (float *)lds_raw;                                                 // [S][M][R], after the barrier
     const int tid = threadIdx.x, nt = blockDim.x;
     const int lane = tid & 63, wave = tid >> 6;
+    uint8_t *ring = lds_raw + mfma_dma_ring_offset(M, K, B) + (size_t)wave * 2 * kMfmaSlotB;
     const int g = group0 + blockIdx.x;
     const int tile = g / kSlots, r0 = (g - tile * kSlots) * R;
     const int i = lane & 15, kb = lane >> 4;
     const uint32_t wsh = kb < 2 ? 4u : 0u;
     const bool col_ok = i < M;
+    const int s = wave, b0 = s * kStretch, nbk = min(kStretch, B - b0);
 
     // the columns' inputs and scales into LDS, every load of a pass in flight
     const int n16 = K / 16, p16 = M * n16, nb = M * B;
@@ -649,68 +829,121 @@ __global__ __launch_bounds__(1024) void q4_0_mfma_cols_lds_kernel(
             }
         }
     }
-    // then this wavefront's stretch of the RG row groups
-    const int s = wave, b0 = s * kStretch, nbk = min(kStretch, B - b0);
-    v2u_mf wv[RG][kStretch];
+    // the row groups' weight scales, then their chunks (two groups in flight)
     uint4 dch[RG];
 #pragma unroll
     for (int rg = 0; rg < RG; rg++) {
-        const int rl = r0 + 16 * rg + i;
-        const uint8_t *wp = W + ((size_t)(tile * B + b0) * kTileRows + rl) * kChunk + 8 * (kb & 1);
-#pragma unroll
-        for (int j = 0; j < kStretch; j++)
-            if (j < nbk)
-                wv[rg][j] = __builtin_nontemporal_load((const v2u_mf *)(wp + (size_t)j * kTileRows * kChunk));
         dch[rg] = make_uint4(0u, 0u, 0u, 0u);
         if (kb == 0)
-            dch[rg] = *(const uint4 *)(W + plane0_bytes + ((size_t)(tile * DC + s) * kTileRows + rl) * kChunk);
+            dch[rg] = *(const uint4 *)(W + plane0_bytes + ((size_t)(tile * DC + s) * kTileRows + r0 + 16 * rg + i) *
+                                                             kChunk);
     }
-    lds_barrier();
+    const uint8_t *wsrc = W + ((size_t)tile * B * kTileRows + r0 + i) * kChunk;
+#define GX_MFMA_ISSUE(RGI, SLOT)                                                                                     \
+    do {                                                                                                             \
+        _Pragma("unroll") for (int h = 0; h < 2; h++) {                                                              \
+            const int b = min(b0 + 4 * h + kb, B - 1);                                                               \
+            __builtin_amdgcn_global_load_lds(wsrc + ((size_t)b * kTileRows + 16 * (RGI)) * kChunk,                   \
+                                             (lds_ptr)(ring + (SLOT) * kMfmaSlotB + h * 1024), 16, 0, 0);            \
+        }                                                                                                            \
+    } while (0)
+    GX_MFMA_ISSUE(0, 0);
+    if (RG > 1)
+        GX_MFMA_ISSUE(1, 1);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this thread's staging stores
+    __builtin_amdgcn_s_barrier();
 
-    const v4f_mf zero = {0.0f, 0.0f, 0.0f, 0.0f};
-    v4i_mf prev[RG];
-    v4f_mf p[RG];
-#pragma unroll
-    for (int rg = 0; rg < RG; rg++) {
-        p[rg] = zero;
-#pragma unroll
-        for (int e = 0; e < 4; e++)
-            prev[rg][e] = kMfmaChainBias;
-    }
-    const int8_t *qrow = qa + (size_t)min(i, M - 1) * ldq + 8 * kb;
-    const float *srow = sa + min(i, M - 1) * lds_b;
+    // the stretch's B operands and activation scales (asm reads, no wait on
+    // the weights in flight)
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_ptr)lds_raw;
+    const uint32_t qaddr = lds0 + (uint32_t)(min(i, M - 1) * ldq + 8 * kb + b0 * kQ4Block);
+    const uint32_t saddr = (uint32_t)(uintptr_t)(lds_ptr)sa + (uint32_t)((min(i, M - 1) * lds_b + b0) * 4);
+    v2u_mf bq[kStretch];
+    float das[kStretch];
+    ds_read_u64<0 * kQ4Block>(qaddr, bq[0]);
+    ds_read_u64<1 * kQ4Block>(qaddr, bq[1]);
+    ds_read_u64<2 * kQ4Block>(qaddr, bq[2]);
+    ds_read_u64<3 * kQ4Block>(qaddr, bq[3]);
+    ds_read_u64<4 * kQ4Block>(qaddr, bq[4]);
+    ds_read_u64<5 * kQ4Block>(qaddr, bq[5]);
+    ds_read_u64<6 * kQ4Block>(qaddr, bq[6]);
+    ds_read_u64<7 * kQ4Block>(qaddr, bq[7]);
+    ds_read_f32<0>(saddr, das[0]);
+    ds_read_f32<4>(saddr, das[1]);
+    ds_read_f32<8>(saddr, das[2]);
+    ds_read_f32<12>(saddr, das[3]);
+    ds_read_f32<16>(saddr, das[4]);
+    ds_read_f32<20>(saddr, das[5]);
+    ds_read_f32<24>(saddr, das[6]);
+    ds_read_f32<28>(saddr, das[7]);
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(bq[0]), "+v"(bq[1]), "+v"(bq[2]), "+v"(bq[3]), "+v"(bq[4]), "+v"(bq[5]), "+v"(bq[6]),
+                   "+v"(bq[7]), "+v"(das[0]), "+v"(das[1]), "+v"(das[2]), "+v"(das[3]), "+v"(das[4]), "+v"(das[5]),
+                   "+v"(das[6]), "+v"(das[7]));
+    v4h_mf ca[kStretch];
+    long bop[kStretch];
 #pragma unroll
     for (int j = 0; j < kStretch; j++) {
-        if (j < nbk) {
-            const int b = b0 + j;
-            const long bop = col_ok ? *(const long *)(qrow + (size_t)b * kQ4Block) : 0;
-            const float da = (col_ok && kb == 0) ? srow[b] : 0.0f;
-            const v4h_mf ca = __builtin_bit_cast(v4h_mf, make_uint2(float_to_half_bits(da), 0u));
+        bop[j] = col_ok ? (long)(((unsigned long)bq[j].y << 32) | bq[j].x) : 0;
+        ca[j] = __builtin_bit_cast(v4h_mf, make_uint2(col_ok && kb == 0 ? float_to_half_bits(das[j]) : 0u, 0u));
+    }
+
+    const v4f_mf zero = {0.0f, 0.0f, 0.0f, 0.0f};
+    v4f_mf p[RG];
+    const uint32_t abase = (uint32_t)(uintptr_t)(lds_ptr)ring + (uint32_t)(i * 16 + 8 * (kb & 1));
 #pragma unroll
-            for (int rg = 0; rg < RG; rg++) {
-                const uint32_t lo = ((wv[rg][j].x << wsh) & 0xF0F0F0F0u) ^ 0x80808080u;
-                const uint32_t hi = ((wv[rg][j].y << wsh) & 0xF0F0F0F0u) ^ 0x80808080u;
+    for (int rg = 0; rg < RG; rg++) {
+        if (rg + 1 < RG)
+            wait_vmcnt<2>();  // this group's chunks have landed (the next group's may be in flight)
+        else
+            wait_vmcnt<0>();
+        v2u_mf wa[kStretch];
+        const uint32_t aslot = abase + (uint32_t)((rg & 1) * kMfmaSlotB);
+        ds_read_u64<0 * 256>(aslot, wa[0]);
+        ds_read_u64<1 * 256>(aslot, wa[1]);
+        ds_read_u64<2 * 256>(aslot, wa[2]);
+        ds_read_u64<3 * 256>(aslot, wa[3]);
+        ds_read_u64<1024 + 0 * 256>(aslot, wa[4]);
+        ds_read_u64<1024 + 1 * 256>(aslot, wa[5]);
+        ds_read_u64<1024 + 2 * 256>(aslot, wa[6]);
+        ds_read_u64<1024 + 3 * 256>(aslot, wa[7]);
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(wa[0]), "+v"(wa[1]), "+v"(wa[2]), "+v"(wa[3]), "+v"(wa[4]), "+v"(wa[5]), "+v"(wa[6]),
+                       "+v"(wa[7]));
+        if (rg + 2 < RG)
+            GX_MFMA_ISSUE(rg + 2, rg & 1);  // into the slot just read
+        v4i_mf prev;
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            prev[e] = kMfmaChainBias;
+        p[rg] = zero;
+#pragma unroll
+        for (int j = 0; j < kStretch; j++) {
+            if (j < nbk) {
+                const uint32_t lo = ((wa[j].x << wsh) & 0xF0F0F0F0u) ^ 0x80808080u;
+                const uint32_t hi = ((wa[j].y << wsh) & 0xF0F0F0F0u) ^ 0x80808080u;
                 const long A = (long)(((unsigned long)hi << 32) | lo);
-                const v4i_mf next = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, bop, prev[rg], 0, 0, 0);
-                const uint32_t dw = (j >> 1) == 0 ? dch[rg].x : (j >> 1) == 1 ? dch[rg].y
-                                  : (j >> 1) == 2 ? dch[rg].z : dch[rg].w;
+                const v4i_mf next = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, bop[j], prev, 0, 0, 0);
+                const uint4 &dc = dch[rg];
+                const uint32_t dw = (j >> 1) == 0 ? dc.x : (j >> 1) == 1 ? dc.y : (j >> 1) == 2 ? dc.z : dc.w;
                 const uint32_t dwh = (j & 1) ? (dw >> 16) : (dw & 0xFFFFu);
-                const v4h_mf wa = __builtin_bit_cast(v4h_mf, make_uint2(dwh, 0u));
-                const v4f_mf sc = __builtin_amdgcn_mfma_f32_16x16x16f16(wa, ca, zero, 0, 0, 0);
+                const v4h_mf wh = __builtin_bit_cast(v4h_mf, make_uint2(dwh, 0u));
+                const v4f_mf sc = __builtin_amdgcn_mfma_f32_16x16x16f16(wh, ca[j], zero, 0, 0, 0);
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
-                    const float x = __int_as_float(next[e]) - __int_as_float(prev[rg][e]);  // the block's isum
+                    const float x = __int_as_float(next[e]) - __int_as_float(prev[e]);  // the block's isum
                     p[rg][e] = fmaf(x, sc[e], p[rg][e]);
                     if (DOTS) {
                         const int row = tile * kTileRows + r0 + 16 * rg + 4 * kb + e;
                         if (col_ok && row >= row_start && row < row_end)
-                            dots[((size_t)i * (row_end - row_start) + (row - row_start)) * B + b] = (int)x;
+                            dots[((size_t)i * (row_end - row_start) + (row - row_start)) * B + b0 + j] = (int)x;
                     }
                 }
-                prev[rg] = next;
+                prev = next;
             }
         }
     }
+#undef GX_MFMA_ISSUE
     if (DOTS)
         return;
     lds_barrier();  // every wavefront is done with the staged activation
@@ -1143,27 +1376,50 @@ int launch_mfma_cols(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, const 
     const int B = w->blocks, S = (B + kStretch - 1) / kStretch;
     const int tile0 = row_start / kTileRows;
     const int tiles = (row_end + kTileRows - 1) / kTileRows - tile0;
-    // The LDS-staged form when a wavefront a stretch covers the row and the
-    // columns fit: 32-row workgroups when that still gives a workgroup a CU
-    // (config 3 at 8 columns, graph of launches over rotating copies:
-    // Gate|Up 17.7 -> 16.0 us, Q|K|V 8.1 -> 7.7, O 6.7 -> 6.3), else 16.
-    const int RG = tiles * 2 >= ctx->cu_count ? 2 : 1;
-    const size_t staged = std::max(mfma_lds_act_bytes(M, w->cols, B), mfma_cols_lds(w, M, 16 * RG));
-    if (S <= 16 && staged <= 64 * 1024) {
-        const int slots = kTileRows / (16 * RG);
-        const unsigned grid = (unsigned)(tiles * slots), threads = (unsigned)(64 * S);
-#define GX_MF(RR, DD)                                                                                                \
-    q4_0_mfma_cols_lds_kernel<RR, 0, DD><<<grid, threads, staged, ctx->stream>>>(                                    \
+    // One stretch a wavefront: the form with the weights through LDS, 32-row
+    // workgroups for a matrix of 64 tiles or more (config 3 at 8 columns,
+    // graph of launches over rotating copies: Q|K|V 8.1 -> 6.6 us, Gate|Up
+    // 17.6 -> 13.7, O 6.7 -> 6.4).
+    if (S <= 16) {
+        const int RG = tiles >= 64 ? 2 : 1;
+        const size_t bytes = std::max(mfma_dma_ring_offset(M, w->cols, B) + (size_t)S * 2 * kMfmaSlotB,
+                                      mfma_cols_lds(w, M, 16 * RG));
+        if (bytes <= kLdsMax) {
+            const int slots = kTileRows / (16 * RG);
+            const unsigned grid = (unsigned)(tiles * slots), threads = (unsigned)(64 * S);
+#define GX_MD(RR, DD)                                                                                                \
+    q4_0_mfma_cols_dma_kernel<RR, 0, DD><<<grid, threads, bytes, ctx->stream>>>(                                     \
         mat, w->plane0_bytes, B, w->dchunks, q, scales, M, tile0 * slots, row_start, row_end, bias, y, ldy, dots,    \
         nullptr, nullptr, nullptr)
-        if (RG == 2 && dots)
+            if (RG == 2 && dots)
+                GX_MD(2, true);
+            else if (RG == 2)
+                GX_MD(2, false);
+            else if (dots)
+                GX_MD(1, true);
+            else
+                GX_MD(1, false);
+#undef GX_MD
+            return check_launch("q4_0_mfma_cols_dma");
+        }
+    }
+    // Up to three stretches a wavefront: weights into registers (config 3's
+    // Down at 8 columns 13.7 -> 12.2 us against the unstaged form).
+    const int SW = (S + 15) / 16;
+    const size_t staged = std::max(mfma_lds_act_bytes(M, w->cols, B), mfma_cols_lds(w, M, 16));
+    if (SW <= 3 && staged <= kLdsMax) {
+        const unsigned grid = (unsigned)(tiles * 4), threads = (unsigned)(64 * min(S, 16));
+#define GX_MF(SS, DD)                                                                                                \
+    q4_0_mfma_cols_lds_kernel<SS, DD><<<grid, threads, staged, ctx->stream>>>(                                       \
+        mat, w->plane0_bytes, B, w->dchunks, q, scales, M, tile0 * 4, row_start, row_end, bias, y, ldy, dots)
+        if (SW <= 2 && dots)
             GX_MF(2, true);
-        else if (RG == 2)
+        else if (SW <= 2)
             GX_MF(2, false);
         else if (dots)
-            GX_MF(1, true);
+            GX_MF(3, true);
         else
-            GX_MF(1, false);
+            GX_MF(3, false);
 #undef GX_MF
         return check_launch("q4_0_mfma_cols_lds");
     }
@@ -1307,12 +1563,15 @@ int launch_q4_0_matvec(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, cons
 int launch_q4_0_matvec_swiglu(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const float *scales,
                                const int32_t *qsum, int M, int8_t *mq, float *ms, int32_t *mqs) {
     const int K = w->cols, B = w->blocks, S = (B + kStretch - 1) / kStretch, F = w->rows / 2;
-    const size_t staged = std::max(mfma_lds_act_bytes(M, K, B), mfma_cols_lds(w, M, kTileRows));
-    if (M <= kMfmaCols && S <= 16 && staged <= 64 * 1024) {
-        q4_0_mfma_cols_lds_kernel<4, 1, false><<<w->tiles, 64 * S, staged, ctx->stream>>>(
+    const size_t ringed = std::max(mfma_dma_ring_offset(M, K, B) + (size_t)S * 2 * kMfmaSlotB,
+                                   mfma_cols_lds(w, M, kTileRows));
+    if (M <= kMfmaCols && S <= 16 && ringed <= kLdsMax) {
+        // (config 3's Gate|Up at 8 columns: 22.0 us with the weights in
+        // registers, 17.0 through LDS)
+        q4_0_mfma_cols_dma_kernel<4, 1, false><<<w->tiles, 64 * S, ringed, ctx->stream>>>(
             w->dev, w->plane0_bytes, B, w->dchunks, q, scales, M, 0, 0, w->rows, nullptr, nullptr, 0, nullptr, mq, ms,
             mqs);
-        return check_launch("q4_0_mfma_cols_lds_swiglu");
+        return check_launch("q4_0_mfma_cols_dma_swiglu");
     }
     if (M <= kMfmaCols && mfma_cols_lds(w, M, kTileRows) <= 64 * 1024) {
         q4_0_mfma_cols_kernel<4, 1, false><<<w->tiles, 64 * min(4 * S, 16), mfma_cols_lds(w, M, kTileRows),
