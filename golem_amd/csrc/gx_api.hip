@@ -810,6 +810,7 @@ int gx_norm_quant(gx_ctx *ctx, float *x, int ldx, const float *add, int lda, con
     GX_CHECK(K > 0 && K % 32 == 0, "nn: activation length must be a multiple of the block size");
     GX_CHECK(M >= 0 && ldx >= K && (!add || lda >= K) && (!out || ldo >= K), "gx: bad batch shape");
     GX_CHECK(x && gain && (out || q) && (!q || (scales && qsum)), "gx: missing argument");
+    GX_CHECK(((uintptr_t)q & 3) == 0, "gx: q must be 4-byte aligned");
     if (M == 0)
         return ok();
     if (int rc = gx::launch_qwen_norm_quant(ctx, x, ldx, add, lda, gain, M, K, eps, out, ldo, q, scales, qsum))

@@ -146,11 +146,13 @@ def test_bad_shapes_are_refused(dev):
 
 # ---- kernel by kernel, bit for bit -------------------------------------------
 
-def test_norm_quant_bit_exact(dev, orc):
-    g = synth.rng(61)
-    M, K = 5, 2560
+@pytest.mark.parametrize("M,K", [(5, 2560), (8, 2816), (3, 9728), (2, 32), (4, 96)])
+def test_norm_quant_bit_exact(dev, orc, M, K):
+    g = synth.rng(61 + K)
     x = (g.standard_normal((M, K)) * 3).astype(np.float32)
+    x[M - 1, : min(K, 64)] = 0.0  # whole zero blocks: scale 0, q 0
     add = g.standard_normal((M, K)).astype(np.float32)
+    add[M - 1, : min(K, 64)] = 0.0
     gain = (1 + 0.02 * g.standard_normal(K)).astype(np.float32)
     xd, ad, gd = dev.put(x), dev.put(add), dev.put(gain)
     q = dev.empty((M, K), np.int8)

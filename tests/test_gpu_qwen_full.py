@@ -60,6 +60,9 @@ def check_block(model, om, orc, prompt, layer):
         return t[:M].cpu().numpy().copy()
 
     qkv, set_q, set_s, attn = dev(model.qkv), dev(model.set8.q), dev(model.set8.s), dev(model.attn)
+    # up to 16 positions the block's Gate|Up product hands SwiGLU's Q8_0 on
+    # without its floats: the product of the device's own pre-norm, again
+    model._mm(model.blocks[layer]["gu"], model.x8, M, model.gu, 2 * cfg.ffn)
     x8_q, x8_s, gu = dev(model.x8.q), dev(model.x8.s), dev(model.gu)
     mid_q, mid_s, ffn = dev(model.mid8.q), dev(model.mid8.s), dev(model.ffn)
 
