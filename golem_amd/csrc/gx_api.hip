@@ -1036,8 +1036,9 @@ static int moe_experts(gx_ctx *ctx, const gx_weight *gate_up, const gx_weight *d
                        int ldo, void *workspace, size_t workspace_bytes, bool noalloc) {
     if (int rc = use(ctx))
         return rc;
-    GX_CHECK(gate_up && down && gate_up->quant == GX_Q4_0 && down->quant == GX_Q4_0,
-             "gx: the expert stacks are Q4_0 matrices");
+    GX_CHECK(gate_up && down && gate_up->quant == down->quant &&
+                 (gate_up->quant == GX_Q4_0 || gate_up->quant == GX_F32),
+             "gx: the expert stacks are Q4_0 matrices or F32 matrices, both the same");
     GX_CHECK(gate_up->count == down->count, "gx: %d gate_up experts but %d down experts", gate_up->count, down->count);
     GX_CHECK(gate_up->rows == 2 * down->cols && down->rows == gate_up->cols,
              "gx: gate_up is %dx%d and down %dx%d: want 2F x D and D x F", gate_up->rows, gate_up->cols, down->rows,

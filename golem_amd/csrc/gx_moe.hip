@@ -997,6 +997,70 @@ __global__ __launch_bounds__(256) void moe_reduce4_kernel(const float *__restric
     *(float4 *)(out + (size_t)t * ldo + i) = make_float4(acc[0], acc[1], acc[2], acc[3]);
 }
 
+// ---- F32 expert stacks ------------------------------------------------------
+//
+// golem's ExpertStack carries any nn.Quant (gemma/weights.go:59-72).  With F32
+// stacks, Matrix.rows' F32 case (nn/matrix.go:113-120) multiplies the Batch's
+// floats in DotF32's generic order, so the position's input and mid enter
+// unquantised (the Batch's Q8_0 form, which QuantizeColumnRange also fills,
+// is never read by an F32 matrix): gate|up = DotF32(GateUp[e] row, x_t),
+// GELUTable(gate) * up in place of the gate, partial = DotF32(Down[e] row,
+// mid), then the same weighted sum.  Four lanes a dot, as f32_matvec_kernel.
+// A unit whose id is out of range writes nothing; the sum makes its
+// position's output NaN.
+__global__ __launch_bounds__(256) void moe_f32_units_kernel(const float *__restrict__ W, size_t matrix_floats,
+                                                            int rows, int cols, const float *__restrict__ x, int ldx,
+                                                            int act_div, int U, const int32_t *__restrict__ ids,
+                                                            int E, float *__restrict__ y, int ldy) {
+    const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t dot = gid >> 2;
+    const int j = (int)(gid & 3);
+    const bool in = dot < (size_t)U * rows;
+    const int u = in ? (int)(dot / rows) : 0;
+    const int row = in ? (int)(dot % rows) : 0;
+    const int e = ids[u];
+    const bool live = in && e >= 0 && e < E;
+    const float *a = W + (size_t)(live ? e : 0) * matrix_floats + (size_t)row * cols;
+    const float *b = x + (size_t)(u / act_div) * ldx;
+    float s = 0.0f;
+    if (live) {
+        const int whole = cols & ~3;
+        for (int i = j; i < whole; i += 4) {
+            const float p = a[i] * b[i];
+            s = s + p;
+        }
+        if (j == 0)
+            for (int i = whole; i < cols; i++) {
+                const float p = a[i] * b[i];
+                s = s + p;
+            }
+    }
+    // (s0 + s1) + (s2 + s3)
+    const float pair = s + __shfl_xor(s, 1, 4);
+    const float other = __shfl_xor(pair, 2, 4);
+    if (live && j == 0)
+        y[(size_t)u * ldy + row] = pair + other;
+}
+
+// mid = GELUTable(gate) * up, in place of the gate: gu [U][ld], gate then up.
+__global__ __launch_bounds__(256) void moe_gelu_mul_f32_kernel(float *__restrict__ gu, int ld, int F, int U,
+                                                               const float *__restrict__ table) {
+    const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= (size_t)U * F)
+        return;
+    const int u = (int)(gid / F), i = (int)(gid % F);
+    float *row = gu + (size_t)u * ld;
+    const float gate = row[i];
+    float gl;
+    if (gate <= -10.0f)
+        gl = 0.0f;
+    else if (gate >= 10.0f)
+        gl = gate;
+    else
+        gl = table[float_to_half_bits(gate)];
+    row[i] = gl * row[F + i];
+}
+
 // Stable counting sort of the U = M*k units by expert, in one workgroup, and
 // the work list of the grouped product.  Units with an id outside [0, E) are
 // left out of every group (the sum gives their positions NaN).
@@ -1287,6 +1351,27 @@ int launch_moe_experts(gx_ctx *ctx, const gx_weight *gate_up, const gx_weight *d
     const int D = gate_up->cols, F = down->cols, E = gate_up->count;
     const MoeSpace s = moe_space(M, k, D, F, E);
     const int U = s.units;
+    if (gate_up->quant == GX_F32) {
+        // F32 stacks (both): DotF32 products of the unquantised input and mid
+        float *gu = (float *)(ws + s.gu);
+        float *part = (float *)(ws + s.part);
+        const size_t g_lanes = (size_t)U * 2 * F * 4, d_lanes = (size_t)U * D * 4, nm = (size_t)U * F;
+        moe_f32_units_kernel<<<(unsigned)((g_lanes + 255) / 256), 256, 0, ctx->stream>>>(
+            (const float *)gate_up->dev, gate_up->matrix_bytes / 4, 2 * F, D, x, ldx, k, U, ids, E, gu, 2 * F);
+        if (int rc = check_launch("moe_f32_gate_up"))
+            return rc;
+        moe_gelu_mul_f32_kernel<<<(unsigned)((nm + 255) / 256), 256, 0, ctx->stream>>>(gu, 2 * F, F, U, gelu_table);
+        if (int rc = check_launch("moe_gelu_mul_f32"))
+            return rc;
+        moe_f32_units_kernel<<<(unsigned)((d_lanes + 255) / 256), 256, 0, ctx->stream>>>(
+            (const float *)down->dev, down->matrix_bytes / 4, D, F, gu, 2 * F, 1, U, ids, E, part, D);
+        if (int rc = check_launch("moe_f32_down"))
+            return rc;
+        const size_t no = (size_t)M * D;
+        moe_reduce_kernel<<<(unsigned)((no + 255) / 256), 256, 0, ctx->stream>>>(part, D, M, k, E, ids, weights,
+                                                                                 down_scale, out, ldo);
+        return check_launch("moe_reduce");
+    }
     int8_t *mq = (int8_t *)(ws + s.mq);
     float *ms = (float *)(ws + s.ms);
     int32_t *mqs = (int32_t *)(ws + s.mqs);

@@ -293,7 +293,9 @@ int gx_moe_route(gx_ctx *ctx, const gx_weight *router, const float *router_scale
  * NULL: ones).  Few positions (M <= 4) run as two kernels: gate|up with
  * the input's Q8_0, GELU * up and the mid's Q8_0 fused, then down with the
  * weighted sum fused.  More are sorted by expert and run as ragged MFMA
- * batches, one per expert.  The
+ * batches, one per expert.  F32 stacks (both gate_up and down F32, as
+ * golem's own MoE test holds them) take the input and mid unquantised into
+ * DotF32 products (nn/matrix.go:113-120), bit for bit.  The
  * workspace (device, 256-byte aligned, gx_moe_workspace_bytes) is the
  * scratch golem keeps in its Scratch; no call allocates.  An id out of range
  * makes its position's output NaN. */

@@ -372,3 +372,49 @@ def test_decode_graph_replays_match_eager(dev, orc):
     rel, at = orc.compare_floats(eager[0][1][0], want[0])
     assert rel <= TOL, f"{rel:.3g} of RMS at {at}"
     del graph
+
+
+@pytest.mark.parametrize("M", [1, 3, 9])
+def test_f32_expert_stacks_bit_exact(dev, orc, M):
+    """F32 expert stacks (golem's ExpertStack takes any nn.Quant,
+    gemma/weights.go:59-72; its own MoE oracle test runs on F32 stacks,
+    gemma/moe_test.go:36-42): the input and mid enter the DotF32 products
+    unquantised (nn/matrix.go:113-120), GELUTable * up between them, the
+    weighted sum with DownScale -- bit for bit against the oracle's unit and
+    reduction (oracle.expert_unit with quant F32, pinned on golem's dense
+    oracle in test_oracle_composition).  An out-of-range id makes only its
+    position NaN; stacks of two formats are refused."""
+    D, F, E, k = 512, 128, 16, 4
+    g = synth.rng(70 + M)
+    gu = (g.standard_normal((E, 2 * F, D)) * 0.05).astype(np.float32)
+    dn = (g.standard_normal((E, D, F)) * 0.05).astype(np.float32)
+    wgu = dev.weight(gu, capi.F32, 2 * F, D, count=E)
+    wdn = dev.weight(dn, capi.F32, D, F, count=E)
+    ds = (1 + 0.1 * g.standard_normal(E)).astype(np.float32)
+    x = (g.standard_normal((M, D)) * 2).astype(np.float32)
+    ids = np.stack([g.choice(E, k, replace=False) for _ in range(M)]).astype(np.int32)
+    if M > 1:
+        ids[1, 2] = E + 5  # out of range: position 1 is NaN, the others are not touched
+    w = g.random((M, k)).astype(np.float32)
+    w /= w.sum(axis=1, keepdims=True)
+    import ctypes
+    n = ctypes.c_size_t()
+    capi.call("gx_moe_workspace_bytes", M, k, D, F, E, ctypes.byref(n))
+    ws = dev.empty((n.value + 256,), np.uint8)
+    out = dev.full((M, D), float("nan"))
+    dsd, xd, idd, wd = dev.put(ds), dev.put(x), dev.put(ids), dev.put(w)  # held until the calls are done
+    capi.call("gx_moe_experts", dev.ctx.ptr, wgu.ptr, wdn.ptr, capi.vp(dsd), capi.vp(xd), D, M, k, capi.vp(idd),
+              capi.vp(wd), capi.vp(out), D, capi.vp(ws), n.value)
+    got = dev.get(out)
+    for t in range(M):
+        if M > 1 and t == 1:
+            assert np.all(np.isnan(got[t]))
+            continue
+        parts = np.stack([orc.expert_unit(gu[e], dn[e], x[t], D, F, quant=orc.F32)
+                          for e in ids[t]])
+        want = orc.expert_reduce(parts, ids[t], w[t], D, down_scale=ds)
+        np.testing.assert_array_equal(got[t].view(np.uint32), want.view(np.uint32))
+    mixed = dev.weight(synth.q4_0_weights(g, E * D, F), capi.Q4_0, D, F, count=E)
+    with pytest.raises(capi.GxError):
+        capi.call("gx_moe_experts", dev.ctx.ptr, wgu.ptr, mixed.ptr, None, capi.vp(xd), D, M, k, capi.vp(idd),
+                  capi.vp(wd), capi.vp(out), D, capi.vp(ws), n.value)
