@@ -288,8 +288,9 @@ def cpu_baseline(w6, x, rows, cols, step_bytes, step, y, torch, no_extra):
     rotating weight copies (640 MB, past the last-level cache) for ~10 s on
     every allowed thread and ~3 s on one; the GPU's logits are checked bit for
     bit against it.  Config 0 (Q4_0, dotQ4_0AVX2 under matVecQ4_0Rows) is
-    timed the same way for ~3 s, and config 2's matrix through golem's packed
-    path (dotPackedQ4_0x4AVX2) for ~3 s at each of M = 64 and 512."""
+    timed the same way for ~3 s, config 2's matrix through golem's packed
+    path (dotPackedQ4_0x4AVX2) for ~3 s at each of M = 64 and 512, and the
+    products of config 3's decode token for ~5 s (cpu_c3_decode)."""
     import oracle
     threads = oracle.host_threads()
     oracle.cpu_lib(threads)
@@ -343,7 +344,38 @@ def cpu_baseline(w6, x, rows, cols, step_bytes, step, y, torch, no_extra):
             macs = float(M) * r0 * c0
             out[f"c2_q4_0_packed_m{M}"] = {"GMAC/s": round(n2 * macs / t2 / 1e9, 2),
                                            "ms_per_pass": round(t2 / n2 * 1e3, 2), "cores": threads, "passes": n2}
+        out["c3_decode_products"] = cpu_c3_decode(oracle, synth, w6, timed, threads)
     return out
+
+
+def cpu_c3_decode(oracle, synth, w6, timed, threads):
+    """Config 3's decode token on the CPU, its products only: per block
+    Q|K|V (6144 x 2560), O (2560 x 4096), Gate|Up (19456 x 2560) and Down
+    (2560 x 9728) through golem's packed Q4_0 path (matVecPackedQ4_0Rows over
+    PackQ4_0's layout, dotPackedQ4_0x4AVX2 restated), 36 blocks with their own
+    copies of the weights (2 GB, past the last-level cache), then the Q6_K
+    head (config 1's matrix).  Attention, norms and SwiGLU are left out, so
+    the rate is an upper bound on golem's CPU decode at this shape."""
+    g = synth.rng(3)
+    shapes = [(6144, 2560), (2560, 4096), (19456, 2560), (2560, 9728)]
+    layer = [oracle.pack_q4_0(synth.q4_0_weights(g, r, c), r, c) for r, c in shapes]
+    blocks = [layer] + [[m.copy() for m in layer] for _ in range(35)]
+    acts = {c: oracle.Batch(synth.activations(g, 1, c)).quantize() for c in (2560, 4096, 9728)}
+    ys = {r: np.zeros((1, r), dtype=np.float32) for r, _ in shapes}
+    bh = oracle.Batch(synth.activations(g, 1, 2560)).quantize_k()
+    head_rows = 151936
+    yh = np.zeros((1, head_rows), dtype=np.float32)
+
+    def token(i):
+        for blk in blocks:
+            for (r, c), m in zip(shapes, blk):
+                oracle.cpu_mat_vec_packed_q4_0(m, acts[c], r, threads, ys[r])
+        oracle.cpu_mat_vec_q6_k(w6, bh, head_rows, threads, yh)
+
+    n, t = timed(token, 5.0)
+    del blocks
+    return {"tok_per_s": round(n / t, 2), "ms_per_token": round(t / n * 1e3, 1), "cores": threads, "tokens": n,
+            "scope": "the products of a decode token only (36 blocks + Q6_K head), golem's AVX2 packed path"}
 
 
 def bench_c3(ctx, torch):
