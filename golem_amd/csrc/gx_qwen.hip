@@ -880,11 +880,21 @@ __global__ __launch_bounds__(kDecodeThreads) void attn_decode_kernel(
 // ROWS: key rows a thread scores -- one when the extent fits the cache
 // threads (half the registers: two workgroups a CU), else enough for
 // kDecodeMax.  The runs do not depend on it.
-template <bool FUSE, int ROWS>
+// VW: value elements a workgroup (kValSlice: a head's 32-element slice, the
+// long-extent form; HD: the whole head, one workgroup a query head, for
+// extents of at most kShortRuns runs).  The position runs of the value sums
+// are the same in both (kRuns runs of kXChunk positions, combined in run
+// order), so both give the same bits; the short form has threads for its
+// first kShortRuns runs only and adds the rest's +0 as one +0.
+constexpr int kShortRuns = 2;
+
+template <bool FUSE, int ROWS, int VW = kValSlice>
 struct ParShape {
     static constexpr int kW0 = FUSE ? 1 : 0;                           // wavefronts out of the cache work
-    static constexpr int kCT = kDecodeThreads - 64 * kW0;              // cache threads
+    static constexpr int kNT = VW == kValSlice ? kDecodeThreads : 64 * kW0 + kShortRuns * VW;  // threads
+    static constexpr int kCT = kNT - 64 * kW0;                         // cache threads
     static constexpr int kRuns = (kDecodeThreads - 64) / kValSlice;    // position runs of the value sums
+    static constexpr int kRunThr = kCT / VW;                           // runs that have threads
     static constexpr int kXChunk = ((kDecodeMax + kRuns - 1) / kRuns + 7) & ~7;  // positions a run
     static constexpr int kPieces = kXChunk / 8;                        // value pieces a thread holds
     static constexpr int kRows = ROWS;                                 // positions a thread scores
@@ -892,30 +902,32 @@ struct ParShape {
 };
 constexpr int kParProbs = kDecodeMax + 64;  // probabilities in LDS: up to the end of the last run
 
-template <int HD, bool FUSE, int ROWS>
-__global__ __launch_bounds__(kDecodeThreads) void attn_par_kernel(
+template <int HD, bool FUSE, int ROWS, int VW = kValSlice>
+__global__ __launch_bounds__((ParShape<FUSE, ROWS, VW>::kNT)) void attn_par_kernel(
     const uint16_t *__restrict__ qh, int heads, int kv_heads, const int32_t *__restrict__ positions, int limit,
     const uint16_t *kcache, const uint16_t *vcache, int context, float scale,
     int8_t *__restrict__ q, float *__restrict__ scales, int32_t *__restrict__ qsum,
     const int32_t *__restrict__ slots, int nslots, QkRope fz, float *__restrict__ heads_f) {
+    using Sh = ParShape<FUSE, ROWS, VW>;
+    constexpr int kNT = Sh::kNT;
     __shared__ __align__(16) uint32_t ql[HD / 2];                // the query, fp16 pairs
     __shared__ __align__(16) uint16_t nk[HD];                   // FUSE: this position's key
-    __shared__ uint16_t nvl[kValSlice];                         // FUSE: this position's values of the slice
-    using Sh = ParShape<FUSE, ROWS>;
+    __shared__ uint16_t nvl[VW];                                // FUSE: this position's values of the slice
     static_assert(Sh::kRuns * Sh::kXChunk <= kParProbs && Sh::kRuns * Sh::kXChunk >= kDecodeMax, "runs fit");
-    static_assert(Sh::kMaxRows * Sh::kCT >= kParProbs - 8, "the probability rows are covered");
+    static_assert(VW != kValSlice || Sh::kMaxRows * Sh::kCT >= kParProbs - 8, "the probability rows are covered");
     static_assert(ROWS == 1 || ROWS == Sh::kMaxRows, "one row a thread, or as many as kDecodeMax needs");
+    static_assert(VW == kValSlice || (ROWS == 1 && VW == HD && Sh::kRunThr == kShortRuns), "the short form");
     __shared__ __align__(16) uint16_t ps[kParProbs];            // probabilities, fp16
-    __shared__ float redm[kDecodeThreads / 64], reds[kDecodeThreads / 64];
-    __shared__ float vpart[Sh::kRuns][kValSlice + 1];
+    __shared__ float redm[kNT / 64], reds[kNT / 64];
+    __shared__ float vpart[Sh::kRuns][VW + 1];
     __shared__ __align__(16) float hh[2 * HD];                  // FUSE: the query and key heads, fp32
     __shared__ __align__(16) double sq[2 * HD];                 // and their squares
     __shared__ float hs[2];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    constexpr int slices = HD / kValSlice;
+    constexpr int slices = HD / VW;
     const int group = heads / kv_heads;
     const int kvh = blockIdx.x % kv_heads, rb = blockIdx.x / kv_heads;
-    const int hl = rb / slices, d0 = (rb - hl * slices) * kValSlice;
+    const int hl = rb / slices, d0 = (rb - hl * slices) * VW;
     const int h0 = kvh * group + hl;
     const bool first = hl == 0;  // the query head whose workgroups store the position (FUSE)
     const int t = blockIdx.y;
@@ -933,13 +945,16 @@ __global__ __launch_bounds__(kDecodeThreads) void attn_par_kernel(
     constexpr int kHalf = HD / 2;
     // (no initial values: only wavefront 0 sets and reads them, and a value
     // for the others would make wavefront 0 wait here for its loads)
+    constexpr int kNv = (VW + 63) / 64;  // this position's values a lane
     float4 hx;
-    float nv, rg0[2], rg1[2], rc[2], rs[2];
+    float nv[kNv], rg0[2], rg1[2], rc[2], rs[2];
     if (FUSE && wave == 0) {
         const float *row = fz.qkv + (size_t)t * fz.ldqkv;
         const int e = min(4 * lane, 2 * HD - 4);  // query elements, then key elements
         hx = *(const float4 *)(row + (e < HD ? h0 * HD + e : heads * HD + kvh * HD + (e - HD)));
-        nv = row[(heads + kv_heads) * HD + kvh * HD + d0 + (lane & (kValSlice - 1))];
+#pragma unroll
+        for (int r = 0; r < kNv; r++)
+            nv[r] = row[(heads + kv_heads) * HD + kvh * HD + d0 + ((lane + 64 * r) % VW)];
 #pragma unroll
         for (int r = 0; r < 2; r++) {
             const int i = min(lane + 64 * r, HD - 1);
@@ -961,7 +976,7 @@ __global__ __launch_bounds__(kDecodeThreads) void attn_par_kernel(
     v4u_stream vr[Sh::kPieces];
     const bool cw = !(FUSE && wave == 0);                 // a cache wavefront
     const int ct = tid - 64 * Sh::kW0, cwave = wave - Sh::kW0;  // its thread and wavefront among them
-    const int gi = ct / kValSlice, dd = ct % kValSlice;
+    const int gi = ct / VW, dd = ct % VW;
     constexpr int xchunk = Sh::kXChunk;                  // positions per value run
     const bool vrun = cw && gi < Sh::kRuns;              // a thread of a value run
     if (cw) {
@@ -1057,12 +1072,16 @@ __global__ __launch_bounds__(kDecodeThreads) void attn_par_kernel(
                     }
                 }
             }
-            if (lane < kValSlice) {
-                asm volatile("" : "+v"(nv));  // converted here, not hoisted up to its load
-                const uint16_t vb = (uint16_t)float_to_half_bits(nv);
-                nvl[lane] = vb;
-                if (store && first)
-                    fz.vcache[((size_t)kvh * HD + d0 + lane) * context + pos] = vb;
+#pragma unroll
+            for (int r = 0; r < kNv; r++) {
+                const int l = lane + 64 * r;
+                if (l < VW) {
+                    asm volatile("" : "+v"(nv[r]));  // converted here, not hoisted up to its load
+                    const uint16_t vb = (uint16_t)float_to_half_bits(nv[r]);
+                    nvl[l] = vb;
+                    if (store && first)
+                        fz.vcache[((size_t)kvh * HD + d0 + l) * context + pos] = vb;
+                }
             }
         }
     } else {
@@ -1117,7 +1136,7 @@ __global__ __launch_bounds__(kDecodeThreads) void attn_par_kernel(
     lds_barrier();
     float m = redm[0];
 #pragma unroll
-    for (int w = 1; w < kDecodeThreads / 64; w++)
+    for (int w = 1; w < kNT / 64; w++)
         m = fmaxf(m, redm[w]);
     // exponentials (float64 exp, as SoftmaxInPlace), and their total as a tree
     float e[Sh::kRows];
@@ -1135,7 +1154,7 @@ __global__ __launch_bounds__(kDecodeThreads) void attn_par_kernel(
     lds_barrier();
     float total = 0.0f;
 #pragma unroll
-    for (int w = 0; w < kDecodeThreads / 64; w++)
+    for (int w = 0; w < kNT / 64; w++)
         total = total + reds[w];
     // probabilities, rounded through fp16; zeros past the prefix to the end
     // of the last run
@@ -1196,11 +1215,13 @@ __global__ __launch_bounds__(kDecodeThreads) void attn_par_kernel(
     if (vrun)
         vpart[gi][dd] = acc;
     lds_barrier();
-    if (tid < kValSlice) {
+    if (tid < VW) {
         float o = 0.0f;
 #pragma unroll
-        for (int g = 0; g < Sh::kRuns; g++)
+        for (int g = 0; g < Sh::kRunThr && g < Sh::kRuns; g++)
             o = o + vpart[g][tid];
+        if (Sh::kRunThr < Sh::kRuns)  // the empty runs' +0 sums
+            o = o + 0.0f;
         float stored;
         int32_t sm;
         const int32_t nq = q8_0_lane(o, &stored, &sm);
@@ -1210,7 +1231,7 @@ __global__ __launch_bounds__(kDecodeThreads) void attn_par_kernel(
             heads_f[(size_t)t * width + col] = o;
         if (q) {
             q[(size_t)t * width + col] = (int8_t)nq;
-            if (tid == 0) {
+            if ((tid & 31) == 0) {  // a Q8_0 block a 32-lane group
                 scales[(size_t)t * B + (col >> 5)] = stored;
                 qsum[(size_t)t * B + (col >> 5)] = sm;
             }
@@ -1406,16 +1427,19 @@ int launch_qwen_attention(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int
     // One workgroup per token: a few tokens of one conversation, or tokens of
     // several conversations (slots), whose caches share nothing.
     if (parallel && (M <= 4 || slots) && limit <= kDecodeMax) {
-#define GX_PAR(HH, RR)                                                                                               \
-    attn_par_kernel<HH, false, RR><<<dim3((unsigned)(heads * (HH / kValSlice)), (unsigned)M), kDecodeThreads, 0,   \
-                                     ctx->stream>>>(qh, heads, kv_heads, positions, limit, kcache, vcache, context,  \
-                                                    scale, q, scales, qsum, slots, nslots, QkRope{}, heads_f)
+#define GX_PAR(HH, RR, VV)                                                                                           \
+    attn_par_kernel<HH, false, RR, VV><<<dim3((unsigned)(heads * (HH / VV)), (unsigned)M),                          \
+                                         ParShape<false, RR, VV>::kNT, 0, ctx->stream>>>(                           \
+        qh, heads, kv_heads, positions, limit, kcache, vcache, context, scale, q, scales, qsum, slots, nslots,      \
+        QkRope{}, heads_f)
 #define GX_PAR_R(HH)                                                                                                 \
     do {                                                                                                             \
-        if (limit <= ParShape<false, 1>::kCT)                                                                        \
-            GX_PAR(HH, 1);                                                                                           \
+        if (HH > kValSlice && limit <= kShortRuns * ParShape<false, 1>::kXChunk)                                     \
+            GX_PAR(HH, 1, HH);                                                                                       \
+        else if (limit <= ParShape<false, 1>::kCT)                                                                   \
+            GX_PAR(HH, 1, kValSlice);                                                                                \
         else                                                                                                         \
-            GX_PAR(HH, (ParShape<false, 1>::kMaxRows));                                                              \
+            GX_PAR(HH, (ParShape<false, 1>::kMaxRows), kValSlice);                                                   \
     } while (0)
         if (hd == 32)
             GX_PAR_R(32);
@@ -1523,16 +1547,22 @@ int launch_qwen_rope_attention(gx_ctx *ctx, const float *qkv, int ldqkv, int M, 
     GX_CHECK(limit <= kDecodeMax, "gx: the fused attention reads at most %d positions, not %d", kDecodeMax, limit);
     const QkRope fz{qkv, ldqkv, q_norm, k_norm, rope_cos, rope_sin, eps, kcache, vcache};
     if (parallel) {
-#define GX_PAR(HH, RR)                                                                                               \
-    attn_par_kernel<HH, true, RR><<<dim3((unsigned)(heads * (HH / kValSlice)), (unsigned)M), kDecodeThreads, 0,             \
-                                    ctx->stream>>>(nullptr, heads, kv_heads, positions, limit, kcache, vcache,       \
-                                                   context, scale, q, scales, qsum, slots, nslots, fz, nullptr)
+#define GX_PAR(HH, RR, VV)                                                                                           \
+    attn_par_kernel<HH, true, RR, VV><<<dim3((unsigned)(heads * (HH / VV)), (unsigned)M),                           \
+                                        ParShape<true, RR, VV>::kNT, 0, ctx->stream>>>(                             \
+        nullptr, heads, kv_heads, positions, limit, kcache, vcache, context, scale, q, scales, qsum, slots, nslots, \
+        fz, nullptr)
+// Extents of at most two value runs (112 positions): one workgroup a query
+// head, the whole head's values (a quarter of the workgroups; eight
+// conversations at config 3's shape fit the CUs in one round).
 #define GX_PAR_R(HH)                                                                                                 \
     do {                                                                                                             \
-        if (limit <= ParShape<true, 1>::kCT)                                                                         \
-            GX_PAR(HH, 1);                                                                                           \
+        if (HH > kValSlice && limit <= kShortRuns * ParShape<true, 1>::kXChunk)                                      \
+            GX_PAR(HH, 1, HH);                                                                                       \
+        else if (limit <= ParShape<true, 1>::kCT)                                                                    \
+            GX_PAR(HH, 1, kValSlice);                                                                                \
         else                                                                                                         \
-            GX_PAR(HH, (ParShape<true, 1>::kMaxRows));                                                               \
+            GX_PAR(HH, (ParShape<true, 1>::kMaxRows), kValSlice);                                                    \
     } while (0)
         if (hd == 32)
             GX_PAR_R(32);

@@ -157,3 +157,20 @@ def test_rope_attention_slots_equal_one_at_a_time(dev, hd, heads, kv, context, M
         capi.call("gx_qwen_rope_attention_slots", dev.ctx.ptr, capi.vp(ins[0]), width, M, heads, kv, hd, max_pos,
                   capi.vp(ins[1]), capi.vp(ins[2]), capi.vp(ins[3]), capi.vp(ins[4]), capi.vp(ins[5]), eps,
                   capi.vp(kc), capi.vp(vc), context, capi.vp(q8), capi.vp(sc), capi.vp(qs), None, nslots, 1)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("hd,heads,kv", [(128, 32, 8), (64, 8, 2), (96, 4, 4)])
+def test_parallel_short_extent_form_equals_long(dev, hd, heads, kv):
+    """Extents of at most two value runs (112 positions) take the parallel
+    kernel's short form (one workgroup a query head); the same token through
+    the long form (an extent past 112, one key row a thread, and past 448,
+    several) gives the same bits: the value runs, the softmax tree and the
+    run order are the same in both."""
+    context = 640
+    for pos in (0, 50, 55, 56, 111):
+        short = run_case(dev, hd, heads, kv, context, pos, max(pos, 111), parallel=True)
+        for max_pos in (300, context - 1):
+            long = run_case(dev, hd, heads, kv, context, pos, max_pos, parallel=True)
+            for name, a, b in zip(("q", "scales", "sums", "key cache", "value cache"), short[:5], long[:5]):
+                assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), f"{name}: pos {pos} max_pos {max_pos}"
