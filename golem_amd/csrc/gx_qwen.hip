@@ -488,6 +488,183 @@ __global__ __launch_bounds__(NT) void attn_values_kernel(int M, int heads, int G
     }
 }
 
+// The same value chains for a prompt's tokens.  A wavefront owns 64 value
+// elements (lane d) of one head g for TC tokens: the tokens' probability
+// rows are wavefront-uniform, loaded one step ahead as wavefront-wide vector
+// loads of one address, while the value rows of the slice pass through LDS
+// once per workgroup (TT = TGW*TC tokens of the group's G heads share them).
+// Each lane runs TC chains, one a token, each in position order with its own
+// accumulator: attn_values_kernel's fma order, so the same bits.  (That
+// kernel staged the probabilities in LDS too and read them per lane: at 512
+// tokens its LDS traffic and its two tokens a workgroup set the time.)
+constexpr int kSpDims = 64;     // value elements a wavefront
+constexpr int kSpChunk = 512;   // positions a pass through LDS
+constexpr int kSpStride = kSpChunk + 8;
+
+template <int TC, int G, int TGW>
+__global__ __launch_bounds__(64 * TGW * G) void attn_values_sp_kernel(int M, int heads, int hd,
+                                                                      const int32_t *__restrict__ positions,
+                                                                      int limit, const uint16_t *__restrict__ vcache,
+                                                                      int context, int kv_heads, int S,
+                                                                      const uint16_t *__restrict__ prob,
+                                                                      int8_t *__restrict__ q,
+                                                                      float *__restrict__ scales,
+                                                                      int32_t *__restrict__ qsum) {
+    constexpr int NT = 64 * TGW * G, TT = TGW * TC;
+    extern __shared__ __align__(16) uint16_t vs[];  // [kSpDims][kSpStride]
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int tg = wave / G, g = wave - tg * G;
+    const int slices = hd / kSpDims;
+    const int kvh = blockIdx.x / slices, d0 = (blockIdx.x - kvh * slices) * kSpDims;
+    const int t0 = blockIdx.y * TT, tn = min(TT, M - t0);
+    int n[TC];
+    const uint16_t *prow[TC];
+#pragma unroll
+    for (int c = 0; c < TC; c++) {
+        const int tt = tg * TC + c;
+        n[c] = tt < tn ? min(positions[t0 + tt] + 1, limit) : 0;
+        prow[c] = prob + ((size_t)(t0 + min(tt, tn - 1)) * heads + kvh * G + g) * S;
+    }
+    int nmax = 0;
+    for (int i = 0; i < tn; i++)
+        nmax = max(nmax, min(positions[t0 + i] + 1, limit));
+    const uint16_t *vrow = vcache + ((size_t)kvh * hd + d0) * context;
+    float acc[TC];
+#pragma unroll
+    for (int c = 0; c < TC; c++)
+        acc[c] = 0.0f;
+    for (int c0 = 0; c0 < nmax; c0 += kSpChunk) {
+        const int groups = (min(kSpChunk, nmax - c0) + 7) / 8;  // 8-position pieces of a row
+        const int pieces = kSpDims * groups;
+        __syncthreads();  // the previous chunk's chains are done with the rows
+        for (int base = 0; base < pieces; base += NT * 4) {
+            v4u_stream r[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int i = min(base + tid + u * NT, pieces - 1);
+                const int rr = i / groups, c = i - rr * groups;
+                r[u] = *(const v4u_stream *)(vrow + (size_t)rr * context + c0 + 8 * c);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int i = base + tid + u * NT;
+                if (i < pieces) {
+                    const int rr = i / groups, c = i - rr * groups;
+                    *(v4u_stream *)(vs + rr * kSpStride + 8 * c) = r[u];
+                }
+            }
+        }
+        __syncthreads();
+        const uint16_t *vr = vs + lane * kSpStride;
+        int ln[TC], lmin = kSpChunk;
+#pragma unroll
+        for (int c = 0; c < TC; c++) {
+            ln[c] = min(kSpChunk, n[c] - c0);
+            lmin = min(lmin, ln[c]);
+        }
+        // 16 positions a step, every chain whole; the probabilities come in
+        // as wavefront-wide vector loads of one address (the offset is held
+        // in a VGPR: scalar loads return out of order, so the next step's
+        // could not be in flight while this step's are used), one step ahead.
+        int j = 0;
+        v4u_stream pa[TC][2], pb[TC][2];
+#define GX_SP_LOAD(DST, JJ)                                                                                          \
+    do {                                                                                                             \
+        _Pragma("unroll") for (int c = 0; c < TC; c++) {                                                            \
+            _Pragma("unroll") for (int u = 0; u < 2; u++) {                                                         \
+                int off = c0 + (JJ) + 8 * u;                                                                         \
+                asm volatile("" : "+v"(off));                                                                        \
+                DST[c][u] = *(const v4u_stream *)(prow[c] + off);                                                    \
+            }                                                                                                        \
+        }                                                                                                            \
+    } while (0)
+#define GX_SP_STEP(SRC, JJ)                                                                                          \
+    do {                                                                                                             \
+        _Pragma("unroll") for (int u = 0; u < 2; u++) {                                                             \
+            const v4u_stream vv = *(const v4u_stream *)(vr + (JJ) + 8 * u);                                          \
+            _Pragma("unroll") for (int c = 0; c < TC; c++) {                                                        \
+                const v4u_stream pp = SRC[c][u];                                                                     \
+                float a = acc[c];                                                                                    \
+                a = fma_mix_lo(pp.x, vv.x, a);                                                                       \
+                a = fma_mix_hi(pp.x, vv.x, a);                                                                       \
+                a = fma_mix_lo(pp.y, vv.y, a);                                                                       \
+                a = fma_mix_hi(pp.y, vv.y, a);                                                                       \
+                a = fma_mix_lo(pp.z, vv.z, a);                                                                       \
+                a = fma_mix_hi(pp.z, vv.z, a);                                                                       \
+                a = fma_mix_lo(pp.w, vv.w, a);                                                                       \
+                a = fma_mix_hi(pp.w, vv.w, a);                                                                       \
+                acc[c] = a;                                                                                          \
+            }                                                                                                        \
+        }                                                                                                            \
+    } while (0)
+        if (16 <= lmin)
+            GX_SP_LOAD(pa, 0);
+        while (j + 16 <= lmin) {
+            if (j + 32 <= lmin)
+                GX_SP_LOAD(pb, j + 16);
+            GX_SP_STEP(pa, j);
+            j += 16;
+            if (j + 16 > lmin)
+                break;
+            if (j + 32 <= lmin)
+                GX_SP_LOAD(pa, j + 16);
+            GX_SP_STEP(pb, j);
+            j += 16;
+        }
+#undef GX_SP_STEP
+#undef GX_SP_LOAD
+        // the chains' tails, 24 positions a round (three 8-position pieces
+        // of every chain requested together), position by position within
+        int lmax = 0;
+#pragma unroll
+        for (int c = 0; c < TC; c++)
+            lmax = max(lmax, ln[c]);
+        for (; j < lmax; j += 24) {
+            v4u_stream pt[TC][3];
+#pragma unroll
+            for (int c = 0; c < TC; c++)
+#pragma unroll
+                for (int u = 0; u < 3; u++) {
+                    int off = min(c0 + j + 8 * u, S - 8);  // past the prefix: read, never used
+                    asm volatile("" : "+v"(off));
+                    pt[c][u] = *(const v4u_stream *)(prow[c] + off);
+                }
+#pragma unroll
+            for (int u = 0; u < 3; u++) {
+                const int jp = j + 8 * u;
+                const v4u_stream vv = *(const v4u_stream *)(vr + min(jp, kSpChunk - 8));
+                const uint32_t vw[4] = {vv.x, vv.y, vv.z, vv.w};
+#pragma unroll
+                for (int c = 0; c < TC; c++) {
+                    const uint32_t pw[4] = {pt[c][u].x, pt[c][u].y, pt[c][u].z, pt[c][u].w};
+#pragma unroll
+                    for (int e = 0; e < 8; e++)
+                        if (jp + e < ln[c])
+                            acc[c] = (e & 1) ? fma_mix_hi(pw[e >> 1], vw[e >> 1], acc[c])
+                                             : fma_mix_lo(pw[e >> 1], vw[e >> 1], acc[c]);
+                }
+            }
+        }
+    }
+    const int width = heads * hd, B = width >> 5;
+#pragma unroll
+    for (int c = 0; c < TC; c++) {
+        float stored;
+        int32_t sm;
+        const int32_t nq = q8_0_lane(acc[c], &stored, &sm);  // a Q8_0 block a 32-lane half
+        const int tt = tg * TC + c;
+        if (tt < tn) {
+            const int t = t0 + tt, col = (kvh * G + g) * hd + d0 + lane;
+            q[(size_t)t * width + col] = (int8_t)nq;
+            if ((lane & 31) == 0) {
+                scales[(size_t)t * B + (col >> 5)] = stored;
+                qsum[(size_t)t * B + (col >> 5)] = sm;
+            }
+        }
+    }
+}
+
 // Decode attention in one kernel (M <= 4 positions, or one position per
 // conversation, prefixes of at most kDecodeMax positions): grid
 // (heads / G * hd/32 slices, M), 512 threads.  A workgroup computes, for G
@@ -1510,6 +1687,32 @@ int launch_qwen_attention(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int
                                                                                      sc, tmax, prob);
     if (int rc = check_launch("qwen_attention softmax"))
         return rc;
+    // Values for a prompt (head widths of whole 64-element wavefronts): the
+    // probabilities as wavefront-wide operands, 16 wavefronts a workgroup,
+    // four tokens a wavefront.  Config 3's 512-token prefill: 106 -> 64 us a
+    // layer (counters: the VALU ~11 % busy, a third of the wave cycles
+    // waiting -- every probability reaches all 64 lanes of a wavefront).
+    if (M > 4 && !slots && G <= 4 && hd % kSpDims == 0) {
+        constexpr int kTC = 4;
+        const size_t lds = (size_t)kSpDims * kSpStride * sizeof(uint16_t);
+#define GX_VSP(GG)                                                                                                   \
+    do {                                                                                                             \
+        constexpr int TGW = 16 / GG, TT = TGW * kTC;                                                                 \
+        attn_values_sp_kernel<kTC, GG, TGW><<<dim3((unsigned)(kv_heads * (hd / kSpDims)),                            \
+                                                   (unsigned)((M + TT - 1) / TT)),                                   \
+                                              64 * TGW * GG, lds, ctx->stream>>>(M, heads, hd, positions, limit,     \
+                                                                                 vcache, context, kv_heads, S, prob, \
+                                                                                 q, scales, qsum);                   \
+    } while (0)
+        if (G == 1)
+            GX_VSP(1);
+        else if (G == 2)
+            GX_VSP(2);
+        else
+            GX_VSP(4);
+#undef GX_VSP
+        return check_launch("qwen_attention values");
+    }
     // Values: TT tokens of G heads per workgroup, 32 chains each (NT <= 256).
     int NT = G * kValSlice;
     while (NT < 128 && NT * 2 <= G * kValSlice * M)
