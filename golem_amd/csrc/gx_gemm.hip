@@ -44,6 +44,19 @@ __device__ __forceinline__ v4h k0_operand(uint32_t h, bool first_half) {
     return __builtin_bit_cast(v4h, bits);
 }
 
+// The same operand in both halves of the wavefront (k = 0 and k = 4): the
+// outer product then holds every d_w[i] * d_a[j] twice, 2 d_w d_a, exactly.
+// `h` has its upper 16 bits clear (a u16 LDS read, or a VOP1 fp16 result).
+__device__ __forceinline__ v4h k04_operand(uint32_t h) {
+    return __builtin_bit_cast(v4h, make_uint2(h, 0u));
+}
+
+// {fp16(f), +0} as one dword, in one instruction.  Exact for a value that fp16
+// holds, whatever the rounding (the Q8_0 activation scales are fp16 values).
+__device__ __forceinline__ uint32_t half2_bits_rtz(float f) {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(f, 0.0f));
+}
+
 
 // Blocks a pipeline stage holds (half a stretch).
 constexpr int kStage = 4;
@@ -320,31 +333,43 @@ constexpr int kDmaRing = 3;
 // The integer products run on a biased chain.  The weights enter the MFMA as
 // 16 * (n - 8) (the nibble in a byte's high half, its top bit flipped), and
 // each block's MFMA adds its 16 * isum to the previous block's output; a
-// stretch's chain starts from the bits of 1.5 * 2^19.  Read as fp32, every
-// output is then 1.5 * 2^19 plus the stretch's running isum, exactly: the
-// ulp in [2^19, 2^20) is 1/16, and the running sum of a stretch is at most
-// 8 blocks * 32 * 8 * 128 = 2^18 in magnitude, whose two ends (bits
-// 0x49000000 and 0x49800000) are exactly 2^19 and 2^20.  The difference of
-// two consecutive outputs is the block's isum as an fp32 -- one full-rate
-// subtraction instead of a quarter-rate int->float conversion -- and feeds
-// golem's fma unchanged.
-constexpr int kChainBias = 0x49400000;  // 786432.0f
+// stretch's chain starts from the bits of 1.5 * 2^18.  Read as fp32, every
+// output is then 1.5 * 2^18 plus half the stretch's running isum, exactly:
+// the ulp in [2^18, 2^19) is 1/32, and the running sum of a stretch is at
+// most 8 blocks * 32 * 8 * 128 = 2^18 in magnitude, 2^22 ulps either side of
+// the middle of the binade, whose ends (bits 0x48800000 and 0x49000000) are
+// exactly 2^18 and 2^19.  The difference of two consecutive outputs is half
+// the block's isum as an fp32 -- one full-rate subtraction instead of a
+// conversion -- and the scale outer product is 2 d_w d_a (k04_operand), so
+// fma(isum / 2, 2 d_w d_a, acc) is golem's fma(isum, d_w d_a, acc) bit for
+// bit: the two products are the same real number, rounded once.
+constexpr int kChainBias = 0x48C00000;  // 393216.0f
 
 // One block's operands from LDS (nibbles, activations, weight scale,
 // activation scale), issued without a wait.  Written out so that the
 // compiler sees no LDS load: it would otherwise make each one wait for every
 // load-to-LDS in flight, the next stages' included.  The caller waits
 // (lgkmcnt) before it uses the four registers.
-template <int OW, int OA, int OD, int OS>
-__device__ __forceinline__ void lds_read_block(uint32_t aw, uint32_t aa, uint32_t ad, uint32_t as, v4u &rw, v4i &ra,
-                                               uint32_t &rdw, float &rda) {
+//
+// Lane (row or token l % 32, half g = l / 32) reads 8 bytes of its row's
+// nibble chunk, bytes 8g .. 8g + 7, and takes both nibbles of each: its MFMA
+// slots are k = 16 + 8g .. 16 + 8g + 7 (the high nibbles) then k = 8g ..
+// 8g + 7 (the low ones), and its activation operand holds the same k in the
+// same order: bytes 8g .. 8g + 7 of the block's second half (OA1), then of
+// its first half (OA0).  The integer sum does not depend on the order of k;
+// a lane widening a whole half-chunk's one nibble needed two instructions a
+// dword for the low half, and this takes six for the lane's sixteen.
+template <int OW, int OA1, int OA0, int OD, int OS>
+__device__ __forceinline__ void lds_read_block(uint32_t aw, uint32_t aa, uint32_t ad, uint32_t as, uint2 &rw,
+                                               uint2 &ra1, uint2 &ra0, uint32_t &rdw, float &rda) {
     asm volatile(
-        "ds_read_b128 %0, %4 offset:%8\n\t"
-        "ds_read_b128 %1, %5 offset:%9\n\t"
-        "ds_read_u16 %2, %6 offset:%10\n\t"
-        "ds_read_b32 %3, %7 offset:%11"
-        : "=&v"(rw), "=&v"(ra), "=&v"(rdw), "=&v"(rda)
-        : "v"(aw), "v"(aa), "v"(ad), "v"(as), "i"(OW), "i"(OA), "i"(OD), "i"(OS));
+        "ds_read_b64 %0, %5 offset:%9\n\t"
+        "ds_read_b64 %1, %6 offset:%10\n\t"
+        "ds_read_b64 %2, %6 offset:%11\n\t"
+        "ds_read_u16 %3, %7 offset:%12\n\t"
+        "ds_read_b32 %4, %8 offset:%13"
+        : "=&v"(rw), "=&v"(ra1), "=&v"(ra0), "=&v"(rdw), "=&v"(rda)
+        : "v"(aw), "v"(aa), "v"(ad), "v"(as), "i"(OW), "i"(OA1), "i"(OA0), "i"(OD), "i"(OS));
 }
 
 template <int J, int N, typename F>
@@ -400,25 +425,42 @@ template <int TOK, bool GROUPED, bool DOTS>
 __global__ __launch_bounds__(64 * DmaShape<TOK>::kWaves, DmaShape<TOK>::kOcc) void q4_0_gemm_dma_kernel(
     const uint8_t *__restrict__ W, size_t plane0_bytes, int B, int DC, const int8_t *__restrict__ q,
     const float *__restrict__ scales, int K, int M, int tiles, int tile0, int row_start, int row_end,
-    const float *__restrict__ bias, float *__restrict__ y, int ldy, int32_t *__restrict__ dots, Groups grp) {
+    const float *__restrict__ bias, float *__restrict__ y, int ldy, int32_t *__restrict__ dots, Groups grp,
+    int xcd_pairs) {
     using Sh = DmaShape<TOK>;
     constexpr int kSlotB = Sh::kSlot;
     __shared__ __align__(16) uint8_t ring_lds[kDmaRing * kSlotB];
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wv = tid >> 6;
-    const int T0 = tile0 + 2 * blockIdx.x;        // the workgroup's first R64 tile
+    const int lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // The workgroup's row pair bx and token group by.  With xcd_pairs > 0 the
+    // grid is one-dimensional in the dispatcher's XCD order (workgroup i runs
+    // on XCD i % 8): XCD x takes row pairs [x P / 8, (x + 1) P / 8) of the P
+    // and every token group, token group by token group, so that its L2
+    // holds its rows' weights while the tokens stream past once.  (A 2-D
+    // grid deals every XCD all row pairs: each L2 refetches the whole matrix
+    // many times over.)
+    int bx = blockIdx.x, by = blockIdx.y;
+    if (!GROUPED && xcd_pairs > 0) {
+        const int x = blockIdx.x & 7, local = blockIdx.x >> 3;
+        const int lo = x * xcd_pairs / 8, n = (x + 1) * xcd_pairs / 8 - lo;
+        if (local >= n * ((M + TOK - 1) / TOK))
+            return;  // this XCD's share is done: the whole workgroup
+        by = local / n;
+        bx = lo + (local - by * n);
+    }
+    const int T0 = tile0 + 2 * bx;                // the workgroup's first R64 tile
     const int rg = wv & 3, tg = wv >> 2;          // this wavefront's 32 rows and 32 tokens
     const int li = lane & 31, g = lane >> 5;
     int first, count;
     if (GROUPED) {
-        const int4 item = ((const int4 *)grp.work)[blockIdx.y];
+        const int4 item = ((const int4 *)grp.work)[by];
         count = item.z;
         if (count <= 0)
             return;  // past the last item: the whole workgroup
         W += (size_t)item.x * grp.matrix_bytes;
         first = item.y;
     } else {
-        first = blockIdx.y * TOK;
+        first = by * TOK;
         count = min(TOK, M - first);
     }
     // token t's activation row and output row
@@ -511,12 +553,11 @@ __global__ __launch_bounds__(64 * DmaShape<TOK>::kWaves, DmaShape<TOK>::kOcc) vo
     for (int e = 0; e < 16; e++)
         tot[e] = 0.0f;
     const v16f zero_f = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-    const uint32_t wsh = 4u * (1 - g);  // g = 0 takes the low nibbles: up into the byte's high half
-    // This lane's LDS read addresses in slot 0 (the slot and block go in the
-    // reads' immediate offsets).
+    // This lane's LDS read addresses in slot 0 (the slot, block and half go
+    // in the reads' immediate offsets).
     const uint32_t lds_base = (uint32_t)(uintptr_t)(lds_ptr)ring_lds;
-    const uint32_t lds_w = lds_base + (32 * rg + li) * 16;
-    const uint32_t lds_a = lds_base + Sh::kAct + (g * TOK + 32 * tg + li) * 16;
+    const uint32_t lds_w = lds_base + (32 * rg + li) * 16 + 8 * g;
+    const uint32_t lds_a = lds_base + Sh::kAct + (32 * tg + li) * 16 + 8 * g;
     const uint32_t lds_dw = lds_base + Sh::kWScale + (32 * rg + li) * 8;
     const uint32_t lds_da = lds_base + Sh::kActScale + (32 * tg + li) * 4;
 
@@ -533,14 +574,13 @@ __global__ __launch_bounds__(64 * DmaShape<TOK>::kWaves, DmaShape<TOK>::kOcc) vo
         issue(std::integral_constant<int, (kSlot + 2) % kDmaRing>{}, h + 2);
         constexpr int so = kSlot * kSlotB;
         // The operands of block j + 1 are read while block j is multiplied.
-        v4u wq_n;
-        v4i Bv_n;
+        uint2 wq_n, Bh_n, Bl_n;
         uint32_t dwh_n;
         float da_n;
         auto read = [&](auto j_tag) {
             constexpr int j = decltype(j_tag)::value;
-            lds_read_block<so + j * 2048, so + j * 2 * TOK * 16, so + 2 * j, so + j * TOK * 4>(
-                lds_w, lds_a, lds_dw, lds_da, wq_n, Bv_n, dwh_n, da_n);
+            lds_read_block<so + j * 2048, so + (2 * j + 1) * TOK * 16, so + 2 * j * TOK * 16, so + 2 * j,
+                           so + j * TOK * 4>(lds_w, lds_a, lds_dw, lds_da, wq_n, Bh_n, Bl_n, dwh_n, da_n);
         };
         read(std::integral_constant<int, 0>{});
         unroll<0, kStage>([&](auto j_tag) {
@@ -549,18 +589,30 @@ __global__ __launch_bounds__(64 * DmaShape<TOK>::kWaves, DmaShape<TOK>::kOcc) vo
             __builtin_amdgcn_sched_barrier(0);
             // the reads land; the registers pass through the wait so that
             // nothing touches them before it
-            asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(wq_n), "+v"(Bv_n), "+v"(dwh_n), "+v"(da_n));
-            const v4u wq = wq_n;
-            const v4i Bv = Bv_n;
+            asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(wq_n), "+v"(Bh_n), "+v"(Bl_n), "+v"(dwh_n), "+v"(da_n));
+            const uint2 wq = wq_n;
+            const v4i Bv = {(int)Bh_n.x, (int)Bh_n.y, (int)Bl_n.x, (int)Bl_n.y};
             const uint32_t dwh = dwh_n;
             const float da = da_n;
             if constexpr (j + 1 < kStage)
                 read(std::integral_constant<int, j + 1>{});
+            // The scale outer product goes to the matrix core first: it does
+            // not wait for the chain, and the integer MFMA queues behind it
+            // while the nibbles are widened.  (Issued after the integer MFMA,
+            // the compiler put the first chain difference ahead of it, so
+            // the scales waited for the integers: two MFMA latencies a
+            // block.)
+            // a block past the row has weight scale 0 (the padding is zero):
+            // fma(x, 0, acc) == acc
+            const v16f S = __builtin_amdgcn_mfma_f32_32x32x8f16(k04_operand(dwh), k04_operand(half2_bits_rtz(da)),
+                                                                zero_f, 0, 0, 0);
+            // 16 (n - 8) in every byte: the high nibbles in place, the low
+            // ones shifted up, the top bit flipped
             v4i A;
-            A.x = (int)(((wq.x << wsh) & 0xF0F0F0F0u) ^ 0x80808080u);
-            A.y = (int)(((wq.y << wsh) & 0xF0F0F0F0u) ^ 0x80808080u);
-            A.z = (int)(((wq.z << wsh) & 0xF0F0F0F0u) ^ 0x80808080u);
-            A.w = (int)(((wq.w << wsh) & 0xF0F0F0F0u) ^ 0x80808080u);
+            A.x = (int)((wq.x & 0xF0F0F0F0u) ^ 0x80808080u);
+            A.y = (int)((wq.y & 0xF0F0F0F0u) ^ 0x80808080u);
+            A.z = (int)(((wq.x << 4) & 0xF0F0F0F0u) ^ 0x80808080u);
+            A.w = (int)(((wq.y << 4) & 0xF0F0F0F0u) ^ 0x80808080u);
             constexpr bool start = kFirst && j == 0;
             v16i prev;
             if constexpr (start) {
@@ -576,21 +628,19 @@ __global__ __launch_bounds__(64 * DmaShape<TOK>::kWaves, DmaShape<TOK>::kOcc) vo
                 prev = chain;
             }
             const v16i next = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, Bv, prev, 0, 0, 0);
-            // a block past the row has weight scale 0 (the padding is zero):
-            // fma(x, 0, acc) == acc
-            const v16f S = __builtin_amdgcn_mfma_f32_32x32x8f16(k0_operand(dwh, g == 0),
-                                                                k0_operand(float_to_half_bits(da), g == 0),
-                                                                zero_f, 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int e = 0; e < 16; e++) {
-                const int nb = next[e], pb = prev[e];
-                const float x = __int_as_float(nb) - __int_as_float(pb);  // the block's isum, exactly
+                // half the block's isum, exactly (a stretch's first block
+                // subtracts the bias as a literal: its MFMA then runs in
+                // place, with no copy of the bias kept for the difference)
+                const float x = __int_as_float(next[e]) - (start ? __int_as_float(kChainBias) : __int_as_float(prev[e]));
                 acc[e] = start ? x * S[e] : fmaf(x, S[e], acc[e]);
                 if constexpr (DOTS) {
                     const int b = h * kStage + j, tt = 32 * tg + li;
                     const int n = T0 * kTileRows + 32 * rg + 8 * (e >> 2) + 4 * g + (e & 3);
                     if (b < B && tt < count && n >= row_start && n < row_end)
-                        dots[((size_t)orow(tt) * (row_end - row_start) + (n - row_start)) * B + b] = (int)x;
+                        dots[((size_t)orow(tt) * (row_end - row_start) + (n - row_start)) * B + b] = (int)(2.0f * x);
                 }
             }
             chain = next;
@@ -650,31 +700,29 @@ int launch_q4_0_gemm(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, const 
     const int tile0 = row_start / kTileRows;
     const int tiles = (row_end + kTileRows - 1) / kTileRows - tile0;
     const Groups none{nullptr, nullptr, 1, 0};
+    const int pairs = (tiles + 1) / 2;
     // Up to 1024 tokens, 32-token workgroups: twice as many of them to fill
     // the CUs (config 2's 9728 x 2560 in a graph over rotating copies: M = 64
     // 25.0 -> 20.1 us, M = 512 62.0 -> 56.1 us; M = 2048 195 against 198 us
     // keeps 64).  The per-token arithmetic is the same either way.
-    if (M <= 1024) {
-        const dim3 grid((unsigned)((tiles + 1) / 2), (unsigned)((M + 31) / 32));
-        if (dots)
-            q4_0_gemm_dma_kernel<32, false, true><<<grid, 256, 0, ctx->stream>>>(
-                mat, w->plane0_bytes, w->blocks, w->dchunks, q, scales, w->cols, M, w->tiles, tile0, row_start,
-                row_end, bias, y, ldy, dots, none);
-        else
-            q4_0_gemm_dma_kernel<32, false, false><<<grid, 256, 0, ctx->stream>>>(
-                mat, w->plane0_bytes, w->blocks, w->dchunks, q, scales, w->cols, M, w->tiles, tile0, row_start,
-                row_end, bias, y, ldy, nullptr, none);
-        return check_launch("q4_0_gemm");
-    }
-    const dim3 grid((unsigned)((tiles + 1) / 2), (unsigned)((M + kDmaTok - 1) / kDmaTok));
-    if (dots)
-        q4_0_gemm_dma_kernel<64, false, true><<<grid, 512, 0, ctx->stream>>>(
-            mat, w->plane0_bytes, w->blocks, w->dchunks, q, scales, w->cols, M, w->tiles, tile0, row_start, row_end,
-            bias, y, ldy, dots, none);
+    const int tok = M <= 1024 ? 32 : kDmaTok;
+    const int groups = (M + tok - 1) / tok;
+    // XCD order for matrices of at least eight row pairs (every XCD some).
+    const int xp = pairs >= 8 ? pairs : 0;
+    const dim3 grid = xp ? dim3((unsigned)(8 * ((pairs + 7) / 8) * groups)) : dim3((unsigned)pairs, (unsigned)groups);
+#define GX_DMA_LAUNCH(TK, NT, DD)                                                                                   \
+    q4_0_gemm_dma_kernel<TK, false, DD><<<grid, NT, 0, ctx->stream>>>(                                              \
+        mat, w->plane0_bytes, w->blocks, w->dchunks, q, scales, w->cols, M, w->tiles, tile0, row_start, row_end,     \
+        bias, y, ldy, DD ? dots : nullptr, none, xp)
+    if (tok == 32 && dots)
+        GX_DMA_LAUNCH(32, 256, true);
+    else if (tok == 32)
+        GX_DMA_LAUNCH(32, 256, false);
+    else if (dots)
+        GX_DMA_LAUNCH(64, 512, true);
     else
-        q4_0_gemm_dma_kernel<64, false, false><<<grid, 512, 0, ctx->stream>>>(
-            mat, w->plane0_bytes, w->blocks, w->dchunks, q, scales, w->cols, M, w->tiles, tile0, row_start, row_end,
-            bias, y, ldy, nullptr, none);
+        GX_DMA_LAUNCH(64, 512, false);
+#undef GX_DMA_LAUNCH
     return check_launch("q4_0_gemm");
 }
 
@@ -687,11 +735,11 @@ int launch_q4_0_gemm_grouped(gx_ctx *ctx, const gx_weight *w, const int32_t *wor
     if (dots)
         q4_0_gemm_dma_kernel<32, true, true><<<grid, 256, 0, ctx->stream>>>(
             w->dev, w->plane0_bytes, w->blocks, w->dchunks, q, scales, w->cols, 0, w->tiles, 0, 0, w->rows, nullptr,
-            y, ldy, dots, grp);
+            y, ldy, dots, grp, 0);
     else
         q4_0_gemm_dma_kernel<32, true, false><<<grid, 256, 0, ctx->stream>>>(
             w->dev, w->plane0_bytes, w->blocks, w->dchunks, q, scales, w->cols, 0, w->tiles, 0, 0, w->rows, nullptr,
-            y, ldy, nullptr, grp);
+            y, ldy, nullptr, grp, 0);
     return check_launch("q4_0_gemm_grouped");
 }
 }  // namespace gx
