@@ -187,11 +187,10 @@ __global__ __launch_bounds__(64) void qwen_qk_rope_kernel(const float *__restric
 }
 
 // The attention proper runs as three passes over a workspace: scores
-// sc [M][heads][S] floats, the maximum of every 64-position tile
-// tmax [M][heads][S/64], probabilities prob [M][heads][S] fp16, where S is the
-// deepest visible prefix rounded up to 64.
+// sc [M][heads][S] floats and probabilities prob [M][heads][S] fp16, where S
+// is the deepest visible prefix rounded up to 64.
 //   scores   a lane per cached position: scale * DotF32(query, key) in
-//            DotF32's four-chain order, and each tile's maximum
+//            DotF32's four-chain order
 //   softmax  a wavefront per (position, head): SoftmaxInPlace's maximum,
 //            exp in float64, the sum taken position by position, the
 //            division, the probability rounded through fp16
@@ -229,18 +228,22 @@ typedef float v4f_lds __attribute__((ext_vector_type(4)));
 
 // grid (S/64 position tiles, heads/GH head groups, ceil(M/TT) token tiles),
 // one wavefront.  Lane = cached position p; its key row is held in registers
-// for the GH heads (of one key-value head) of the TT tokens, whose queries
-// are uniform across the wavefront (scalar loads).
+// for the GH heads (of one key-value head) of the TT tokens.  Their TT x GH
+// queries are staged in LDS first, every load in flight at once, and read
+// back as broadcasts (all lanes one address).  (Read as scalar loads, one
+// query after another, each dot product waited for its own query; with the
+// tile maxima reduced here as well, config 3's 512-token prompt spent 65 us
+// a layer in this pass, now 43.)
 template <int HD>
 __global__ __launch_bounds__(64) void attn_scores_kernel(const uint16_t *__restrict__ qh, int M, int heads, int G,
                                                          int GH, int TT, const int32_t *__restrict__ positions, int limit,
                                                          const uint16_t *__restrict__ kcache, int context,
                                                          float scale, int S, float *__restrict__ sc,
-                                                         float *__restrict__ tmax, const int32_t *__restrict__ slots,
-                                                         int nslots, int kv_heads) {
+                                                         const int32_t *__restrict__ slots, int nslots, int kv_heads) {
+    extern __shared__ __align__(16) uint32_t qst[];  // [TT][GH][HD / 2] fp16 pairs
     const int lane = threadIdx.x, tile = blockIdx.x;
     const int h0 = blockIdx.y * GH, t0 = blockIdx.z * TT;
-    const int kvh = h0 / G, tiles = S / kTile;
+    const int kvh = h0 / G;
     if (slots)  // with slots, a token tile is one token (TT = 1); reads stay inside the caches
         kcache += (size_t)min(max(slots[t0], 0), nslots - 1) * kv_heads * HD * context;
     const int tn = min(TT, M - t0);
@@ -249,12 +252,33 @@ __global__ __launch_bounds__(64) void attn_scores_kernel(const uint16_t *__restr
         last = max(last, min(positions[t0 + tt], limit - 1));
     if (tile * kTile > last)
         return;  // the whole wavefront: nothing visible here
+    // The queries: 16-byte pieces c = (tt * GH + j) * HD / 8 + i, token rows
+    // past the batch clamped to its last (never used).
+    {
+        constexpr int kPer = HD / 8;  // pieces a query
+        const int pieces = TT * GH * kPer;
+        for (int c0 = 0; c0 < pieces; c0 += 8 * 64) {
+            v4u_stream v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int c = min(c0 + u * 64 + lane, pieces - 1);
+                const int qi = c / kPer, i = c - qi * kPer;
+                const int tt = qi / GH, j = qi - tt * GH;
+                v[u] = ((const v4u_stream *)(qh + ((size_t)min(t0 + tt, M - 1) * heads + h0 + j) * HD))[i];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+                if (c0 + u * 64 + lane < pieces)
+                    ((v4u_stream *)qst)[c0 + u * 64 + lane] = v[u];
+        }
+    }
     const int p = tile * kTile + lane;
     const v4u_stream *kr = (const v4u_stream *)(kcache + (size_t)kvh * HD * context) + min(p, last);
     v4u_stream k[HD / 8];
 #pragma unroll
     for (int i = 0; i < HD / 8; i++)
         k[i] = kr[(size_t)i * context];
+    __syncthreads();
     for (int tt = 0; tt < tn; tt++) {
         const int t = t0 + tt;
         const int n = min(positions[t] + 1, limit);
@@ -262,7 +286,7 @@ __global__ __launch_bounds__(64) void attn_scores_kernel(const uint16_t *__restr
             continue;
         for (int j = 0; j < GH; j++) {
             const int h = h0 + j;
-            const uint32_t *q = (const uint32_t *)(qh + ((size_t)t * heads + h) * HD);
+            const uint32_t *q = qst + (tt * GH + j) * (HD / 2);
             float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;  // elements 4i, 4i+1, 4i+2, 4i+3
 #pragma unroll
             for (int i = 0; i < HD / 8; i++) {
@@ -280,12 +304,6 @@ __global__ __launch_bounds__(64) void attn_scores_kernel(const uint16_t *__restr
             const size_t row = (size_t)t * heads + h;
             if (p < n)
                 sc[row * S + p] = v;
-            float m = p < n ? v : -INFINITY;
-#pragma unroll
-            for (int off = 32; off > 0; off >>= 1)
-                m = fmaxf(m, __shfl_xor(m, off, 64));
-            if (lane == 0)
-                tmax[row * tiles + tile] = m;
         }
     }
 }
@@ -344,20 +362,23 @@ __device__ __forceinline__ float serial_sum(const float *e, int n, float total) 
 // scores of (position t, head h), then RoundHalf of each probability.
 __global__ __launch_bounds__(64) void attn_softmax_kernel(int heads, const int32_t *__restrict__ positions, int limit,
                                                           int S,
-                                                          float *__restrict__ sc, const float *__restrict__ tmax,
-                                                          uint16_t *__restrict__ prob) {
+                                                          float *__restrict__ sc, uint16_t *__restrict__ prob) {
     __shared__ __align__(16) float e[kSoftChunk + 16];  // serial_sum reads to n + 15
     __shared__ float total_sh;
     const int lane = threadIdx.x, h = blockIdx.x, t = blockIdx.y;
     const size_t row = (size_t)t * heads + h;
-    const int n = min(positions[t] + 1, limit), tiles = (n + kTile - 1) / kTile;
-    float m = -INFINITY;  // the maximum is exact in any order
-    for (int i = lane; i < tiles; i += 64)
-        m = fmaxf(m, tmax[row * (S / kTile) + i]);
+    const int n = min(positions[t] + 1, limit);
+    float *s = sc + row * S;
+    // The maximum is exact in any order; it is taken here, once a row, from
+    // the scores themselves.  (Each scores wavefront reducing its tile's
+    // maximum across its lanes, one dot product after another, was a chain
+    // of six cross-lane round trips per product: most of the scores pass.)
+    float m = -INFINITY;
+    for (int j = lane; j < n; j += 64)
+        m = fmaxf(m, s[j]);
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1)
         m = fmaxf(m, __shfl_xor(m, off, 64));
-    float *s = sc + row * S;
     float total = 0.0f;  // lane 0's
     for (int c0 = 0; c0 < n; c0 += kSoftChunk) {
         const int cn = min(kSoftChunk, n - c0);
@@ -1583,7 +1604,7 @@ size_t qwen_attention_workspace(int M, int heads, int max_pos) {
     const size_t S = ((size_t)max_pos + kTile) / kTile * kTile;
     const size_t rows = (size_t)M * heads;
     auto up = [](size_t b) { return (b + 255) / 256 * 256; };
-    return up(rows * S * sizeof(float)) + up(rows * (S / kTile) * sizeof(float)) + up(rows * S * sizeof(uint16_t));
+    return up(rows * S * sizeof(float)) + up(rows * S * sizeof(uint16_t));
 }
 
 int launch_qwen_attention(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int kv_heads, int hd, int max_pos,
@@ -1598,8 +1619,7 @@ int launch_qwen_attention(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int
     const size_t rows = (size_t)M * heads;
     auto up = [](size_t b) { return (b + 255) / 256 * 256; };
     float *sc = (float *)workspace;
-    float *tmax = (float *)(workspace + up(rows * S * sizeof(float)));
-    uint16_t *prob = (uint16_t *)(workspace + up(rows * S * sizeof(float)) + up(rows * (S / kTile) * sizeof(float)));
+    uint16_t *prob = (uint16_t *)(workspace + up(rows * S * sizeof(float)));
 
     // One workgroup per token: a few tokens of one conversation, or tokens of
     // several conversations (slots), whose caches share nothing.
@@ -1670,8 +1690,8 @@ int launch_qwen_attention(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int
     const int GH = M <= 4 ? 1 : G, TT = M <= 4 || slots ? 1 : 8;
     const dim3 sgrid((unsigned)(S / kTile), (unsigned)(heads / GH), (unsigned)((M + TT - 1) / TT));
 #define GX_SCORES(HH)                                                                                                \
-    attn_scores_kernel<HH><<<sgrid, 64, 0, ctx->stream>>>(qh, M, heads, G, GH, TT, positions, limit, kcache,       \
-                                                          context, scale, S, sc, tmax, slots, nslots, kv_heads)
+    attn_scores_kernel<HH><<<sgrid, 64, (size_t)TT * GH * HH * 2, ctx->stream>>>(                               \
+        qh, M, heads, G, GH, TT, positions, limit, kcache, context, scale, S, sc, slots, nslots, kv_heads)
     if (hd == 32)
         GX_SCORES(32);
     else if (hd == 64)
@@ -1684,7 +1704,7 @@ int launch_qwen_attention(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int
     if (int rc = check_launch("qwen_attention scores"))
         return rc;
     attn_softmax_kernel<<<dim3((unsigned)heads, (unsigned)M), 64, 0, ctx->stream>>>(heads, positions, limit, S,
-                                                                                     sc, tmax, prob);
+                                                                                     sc, prob);
     if (int rc = check_launch("qwen_attention softmax"))
         return rc;
     // Values for a prompt (head widths of whole 64-element wavefronts): the
