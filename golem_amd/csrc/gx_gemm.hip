@@ -429,6 +429,11 @@ __global__ __launch_bounds__(64 * DmaShape<TOK>::kWaves, DmaShape<TOK>::kOcc) vo
     int xcd_pairs) {
     using Sh = DmaShape<TOK>;
     constexpr int kSlotB = Sh::kSlot;
+    // Software-pipelined blocks (one block's MFMAs ahead of the previous
+    // block's epilogue) need ~30 more registers: the 32-token form, at three
+    // workgroups a CU by its LDS, has them; the 64-token form would lose its
+    // fourth wavefront a SIMD.
+    constexpr bool kPipe = TOK == 32;
     __shared__ __align__(16) uint8_t ring_lds[kDmaRing * kSlotB];
     const int tid = threadIdx.x;
     const int lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -583,7 +588,12 @@ __global__ __launch_bounds__(64 * DmaShape<TOK>::kWaves, DmaShape<TOK>::kOcc) vo
                            so + j * TOK * 4>(lds_w, lds_a, lds_dw, lds_da, wq_n, Bh_n, Bl_n, dwh_n, da_n);
         };
         read(std::integral_constant<int, 0>{});
-        unroll<0, kStage>([&](auto j_tag) {
+        // front(j): block j's operands land, block j + 1's reads go out, and
+        // block j's two MFMAs are issued; back(j): block j's chain
+        // differences and fmas.
+        v16f Sr[kStage];
+        v16i Nr[kStage];
+        auto front = [&](auto j_tag) {
             constexpr int j = decltype(j_tag)::value;
             // the previous block's work stays above this block's wait
             __builtin_amdgcn_sched_barrier(0);
@@ -604,8 +614,8 @@ __global__ __launch_bounds__(64 * DmaShape<TOK>::kWaves, DmaShape<TOK>::kOcc) vo
             // block.)
             // a block past the row has weight scale 0 (the padding is zero):
             // fma(x, 0, acc) == acc
-            const v16f S = __builtin_amdgcn_mfma_f32_32x32x8f16(k04_operand(dwh), k04_operand(half2_bits_rtz(da)),
-                                                                zero_f, 0, 0, 0);
+            Sr[j] = __builtin_amdgcn_mfma_f32_32x32x8f16(k04_operand(dwh), k04_operand(half2_bits_rtz(da)), zero_f, 0,
+                                                          0, 0);
             // 16 (n - 8) in every byte: the high nibbles in place, the low
             // ones shifted up, the top bit flipped
             v4i A;
@@ -613,29 +623,40 @@ __global__ __launch_bounds__(64 * DmaShape<TOK>::kWaves, DmaShape<TOK>::kOcc) vo
             A.y = (int)((wq.y & 0xF0F0F0F0u) ^ 0x80808080u);
             A.z = (int)(((wq.x << 4) & 0xF0F0F0F0u) ^ 0x80808080u);
             A.w = (int)(((wq.y << 4) & 0xF0F0F0F0u) ^ 0x80808080u);
-            constexpr bool start = kFirst && j == 0;
             v16i prev;
-            if constexpr (start) {
+            if constexpr (kFirst && j == 0) {
                 // written afresh each stretch (a resident copy would cost 16
-                // registers and the fourth wavefront per SIMD)
+                // registers and a wavefront per SIMD)
 #pragma unroll
                 for (int e = 0; e < 16; e++) {
                     int bias;
                     asm volatile("v_mov_b32 %0, %1" : "=v"(bias) : "i"(kChainBias));
                     prev[e] = bias;
                 }
-            } else {
+            } else if constexpr (j == 0) {
                 prev = chain;
+            } else {
+                prev = Nr[j - 1];
             }
-            const v16i next = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, Bv, prev, 0, 0, 0);
-            __builtin_amdgcn_sched_barrier(0);
+            Nr[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, Bv, prev, 0, 0, 0);
+        };
+        auto back = [&](auto j_tag) {
+            constexpr int j = decltype(j_tag)::value;
+            constexpr bool start = kFirst && j == 0;
 #pragma unroll
             for (int e = 0; e < 16; e++) {
                 // half the block's isum, exactly (a stretch's first block
                 // subtracts the bias as a literal: its MFMA then runs in
                 // place, with no copy of the bias kept for the difference)
-                const float x = __int_as_float(next[e]) - (start ? __int_as_float(kChainBias) : __int_as_float(prev[e]));
-                acc[e] = start ? x * S[e] : fmaf(x, S[e], acc[e]);
+                int pb;
+                if constexpr (start)
+                    pb = kChainBias;
+                else if constexpr (j == 0)
+                    pb = chain[e];
+                else
+                    pb = Nr[j - 1][e];
+                const float x = __int_as_float(Nr[j][e]) - __int_as_float(pb);
+                acc[e] = start ? x * Sr[j][e] : fmaf(x, Sr[j][e], acc[e]);
                 if constexpr (DOTS) {
                     const int b = h * kStage + j, tt = 32 * tg + li;
                     const int n = T0 * kTileRows + 32 * rg + 8 * (e >> 2) + 4 * g + (e & 3);
@@ -643,8 +664,26 @@ __global__ __launch_bounds__(64 * DmaShape<TOK>::kWaves, DmaShape<TOK>::kOcc) vo
                         dots[((size_t)orow(tt) * (row_end - row_start) + (n - row_start)) * B + b] = (int)(2.0f * x);
                 }
             }
-            chain = next;
-        });
+        };
+        if constexpr (kPipe) {
+            // block j + 1's MFMAs go out before block j's differences, which
+            // then run while the matrix core works on them
+            front(std::integral_constant<int, 0>{});
+            unroll<0, kStage>([&](auto j_tag) {
+                constexpr int j = decltype(j_tag)::value;
+                if constexpr (j + 1 < kStage)
+                    front(std::integral_constant<int, j + 1>{});
+                __builtin_amdgcn_sched_barrier(0);
+                back(j_tag);
+            });
+        } else {
+            unroll<0, kStage>([&](auto j_tag) {
+                front(j_tag);
+                __builtin_amdgcn_sched_barrier(0);
+                back(j_tag);
+            });
+        }
+        chain = Nr[kStage - 1];
         // the stage's sums are complete here, not sunk past the next barrier
 #pragma unroll
         for (int e = 0; e < 16; e++)
