@@ -358,14 +358,24 @@ __device__ __forceinline__ float serial_sum(const float *e, int n, float total) 
     return total;
 }
 
-// grid (heads, M), one wavefront: SoftmaxInPlace (nn/ops.go:59-73) of the
-// scores of (position t, head h), then RoundHalf of each probability.
-__global__ __launch_bounds__(64) void attn_softmax_kernel(int heads, const int32_t *__restrict__ positions, int limit,
-                                                          int S,
-                                                          float *__restrict__ sc, uint16_t *__restrict__ prob) {
-    __shared__ __align__(16) float e[kSoftChunk + 16];  // serial_sum reads to n + 15
-    __shared__ float total_sh;
-    const int lane = threadIdx.x, h = blockIdx.x, t = blockIdx.y;
+// grid (ceil(heads / kSoftRows), M), a wavefront per (position t, head h):
+// SoftmaxInPlace (nn/ops.go:59-73) of the row's scores, then RoundHalf of
+// each probability.  The wavefronts of a workgroup share nothing (each has
+// its own `cap` + 16 floats of LDS, cap = min(kSoftChunk, S)), so a CU holds
+// twice as many rows at once as with one-wavefront workgroups: the row's
+// total is a serial chain on one lane, and more rows in flight cover it.
+// (Config 3's 512-token prompt: 25 us a layer with one row a workgroup.)
+constexpr int kSoftRows = 4;
+__global__ __launch_bounds__(64 * kSoftRows) void attn_softmax_kernel(int heads, const int32_t *__restrict__ positions,
+                                                                      int limit, int S, int cap,
+                                                                      float *__restrict__ sc,
+                                                                      uint16_t *__restrict__ prob) {
+    extern __shared__ __align__(16) float esh[];  // [kSoftRows][cap + 16]: serial_sum reads to n + 15
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int h = blockIdx.x * kSoftRows + w, t = blockIdx.y;
+    if (h >= heads)
+        return;  // the whole wavefront; no workgroup barrier follows
+    float *e = esh + w * (cap + 16);
     const size_t row = (size_t)t * heads + h;
     const int n = min(positions[t] + 1, limit);
     float *s = sc + row * S;
@@ -380,25 +390,24 @@ __global__ __launch_bounds__(64) void attn_softmax_kernel(int heads, const int32
     for (int off = 32; off > 0; off >>= 1)
         m = fmaxf(m, __shfl_xor(m, off, 64));
     float total = 0.0f;  // lane 0's
-    for (int c0 = 0; c0 < n; c0 += kSoftChunk) {
-        const int cn = min(kSoftChunk, n - c0);
+    for (int c0 = 0; c0 < n; c0 += cap) {
+        const int cn = min(cap, n - c0);
         for (int j = lane; j < cn; j += 64) {
             const float v = (float)exp((double)(s[c0 + j] - m));
             e[j] = v;
-            if (n > kSoftChunk)
+            if (n > cap)
                 s[c0 + j] = v;  // kept for the division
         }
-        __syncthreads();
+        // one wavefront: its LDS accesses complete in order; the wait keeps
+        // the compiler from moving lane 0's reads above the stores
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         if (lane == 0)
             total = serial_sum(e, cn, total);
-        __syncthreads();
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     }
-    if (lane == 0)
-        total_sh = total;
-    __syncthreads();
-    total = total_sh;
+    total = __shfl(total, 0, 64);
     uint16_t *pr = prob + row * S;
-    if (n <= kSoftChunk) {
+    if (n <= cap) {
         for (int j = lane; j < n; j += 64)
             pr[j] = (uint16_t)float_to_half_bits(__fdiv_rn(e[j], total));
     } else {
@@ -1703,8 +1712,12 @@ int launch_qwen_attention(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int
 #undef GX_SCORES
     if (int rc = check_launch("qwen_attention scores"))
         return rc;
-    attn_softmax_kernel<<<dim3((unsigned)heads, (unsigned)M), 64, 0, ctx->stream>>>(heads, positions, limit, S,
-                                                                                     sc, prob);
+    {
+        const int cap = min(kSoftChunk, S);
+        attn_softmax_kernel<<<dim3((unsigned)((heads + kSoftRows - 1) / kSoftRows), (unsigned)M), 64 * kSoftRows,
+                              (size_t)kSoftRows * (cap + 16) * sizeof(float), ctx->stream>>>(heads, positions, limit, S,
+                                                                                             cap, sc, prob);
+    }
     if (int rc = check_launch("qwen_attention softmax"))
         return rc;
     // Values for a prompt (head widths of whole 64-element wavefronts): the
