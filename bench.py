@@ -46,7 +46,8 @@ def parse():
     p.add_argument("--no-extra", action="store_true", help="skip the config 0 / config 2 measurements")
     p.add_argument("--only", default="",
                    help="profiling: run only this leg (c1, c0, c2, c3, c4) and exit; 'copy' runs the 256 MiB "
-                        "device copy that scales the FETCH_SIZE / WRITE_SIZE counters")
+                        "device copy that scales the FETCH_SIZE / WRITE_SIZE counters; 'c3prefill' reads "
+                        "config 3's 512-token prompt four times (a kernel trace of the prefill alone)")
     p.add_argument("--c2-m", type=int, default=0, help="profiling: config 2 at this M only")
     p.add_argument("--c2-path", default="", help="profiling: config 2 on this kernel only (f16, i8)")
     return p.parse_args()
@@ -233,6 +234,10 @@ def main():
             print(json.dumps(extra))
             return
 
+    if args.only == "c3prefill":
+        print(json.dumps(bench_c3_prefill(ctx, torch)))
+        return
+
     # ---- config 3: Qwen3-4B-shaped decoder, prefill 512 + 128 greedy steps ----
     if not args.no_extra and args.only in ("", "c3"):
         extra.update(bench_c3(ctx, torch))
@@ -376,6 +381,28 @@ def cpu_c3_decode(oracle, synth, w6, timed, threads):
     del blocks
     return {"tok_per_s": round(n / t, 2), "ms_per_token": round(t / n * 1e3, 1), "cores": threads, "tokens": n,
             "scope": "the products of a decode token only (36 blocks + Q6_K head), golem's AVX2 packed path"}
+
+
+def bench_c3_prefill(ctx, torch):
+    """Profiling leg: config 3's model and 512-token prompt (as bench_c3),
+    the prompt read four times from an empty cache, each timed with HIP
+    events through its first token."""
+    from golem_amd import synth
+    from golem_amd.qwen import QwenModel
+    cfg = synth.qwen3_4b(640)
+    w = synth.qwen_weights(cfg, 3)
+    model = QwenModel(ctx, cfg, w, max_batch=512)
+    del w
+    prompt = synth.rng(3).integers(0, cfg.vocab, 512).astype(np.int32)
+    ms = []
+    for _ in range(4):
+        model.reset()
+        torch.cuda.synchronize()
+        ctx.timer_start()
+        model.forward(prompt, 0)
+        model.next_token(len(prompt) - 1)
+        ms.append(round(ctx.timer_stop(), 3))
+    return {"c3_prefill_ms": ms}
 
 
 def bench_c3(ctx, torch):
