@@ -519,10 +519,13 @@ __global__ __launch_bounds__(NT) void attn_values_kernel(int M, int heads, int G
 }
 
 // The same value chains for a prompt's tokens.  A wavefront owns 64 value
-// elements (lane d) of one head g for TC tokens: the tokens' probability
-// rows are wavefront-uniform, loaded one step ahead as wavefront-wide vector
-// loads of one address, while the value rows of the slice pass through LDS
-// once per workgroup (TT = TGW*TC tokens of the group's G heads share them).
+// elements (lane d) of one head g for TC tokens.  Per chunk of kSpChunk
+// positions the workgroup stages the slice's value rows (TT = TGW*TC tokens
+// of the group's G heads share them) and its TT*G probability rows in LDS;
+// a wavefront's probabilities are uniform, read one step ahead as broadcasts
+// (all lanes one address).  (Read as wavefront-wide vector loads of one
+// address straight from the workspace, one step ahead did not cover their
+// latency: 64 us a layer at config 3's 512-token prompt.)
 // Each lane runs TC chains, one a token, each in position order with its own
 // accumulator: attn_values_kernel's fma order, so the same bits.  (That
 // kernel staged the probabilities in LDS too and read them per lane: at 512
@@ -541,7 +544,8 @@ __global__ __launch_bounds__(64 * TGW * G) void attn_values_sp_kernel(int M, int
                                                                       float *__restrict__ scales,
                                                                       int32_t *__restrict__ qsum) {
     constexpr int NT = 64 * TGW * G, TT = TGW * TC;
-    extern __shared__ __align__(16) uint16_t vs[];  // [kSpDims][kSpStride]
+    extern __shared__ __align__(16) uint16_t vs[];  // [kSpDims][kSpStride], then ps [TT * G][kSpStride]
+    uint16_t *ps = vs + kSpDims * kSpStride;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int tg = wave / G, g = wave - tg * G;
@@ -549,12 +553,10 @@ __global__ __launch_bounds__(64 * TGW * G) void attn_values_sp_kernel(int M, int
     const int kvh = blockIdx.x / slices, d0 = (blockIdx.x - kvh * slices) * kSpDims;
     const int t0 = blockIdx.y * TT, tn = min(TT, M - t0);
     int n[TC];
-    const uint16_t *prow[TC];
 #pragma unroll
     for (int c = 0; c < TC; c++) {
         const int tt = tg * TC + c;
         n[c] = tt < tn ? min(positions[t0 + tt] + 1, limit) : 0;
-        prow[c] = prob + ((size_t)(t0 + min(tt, tn - 1)) * heads + kvh * G + g) * S;
     }
     int nmax = 0;
     for (int i = 0; i < tn; i++)
@@ -585,28 +587,50 @@ __global__ __launch_bounds__(64 * TGW * G) void attn_values_sp_kernel(int M, int
                 }
             }
         }
+        {
+            // probability row pr = token tt * G + head gg (tokens past the
+            // batch read its last token's row; positions past a token's
+            // prefix are staged and never used)
+            const int ppieces = TT * G * groups;
+            for (int base = 0; base < ppieces; base += NT * 4) {
+                v4u_stream r[4];
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const int i = min(base + tid + u * NT, ppieces - 1);
+                    const int pr = i / groups, c = i - pr * groups;
+                    const int tt = pr / G, gg = pr - tt * G;
+                    r[u] = *(const v4u_stream *)(prob + ((size_t)(t0 + min(tt, tn - 1)) * heads + kvh * G + gg) * S +
+                                                 c0 + 8 * c);
+                }
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const int i = base + tid + u * NT;
+                    if (i < ppieces) {
+                        const int pr = i / groups, c = i - pr * groups;
+                        *(v4u_stream *)(ps + pr * kSpStride + 8 * c) = r[u];
+                    }
+                }
+            }
+        }
         __syncthreads();
         const uint16_t *vr = vs + lane * kSpStride;
         int ln[TC], lmin = kSpChunk;
+        const uint16_t *prl[TC];  // this wavefront's probability rows in LDS
 #pragma unroll
         for (int c = 0; c < TC; c++) {
             ln[c] = min(kSpChunk, n[c] - c0);
             lmin = min(lmin, ln[c]);
+            prl[c] = ps + ((tg * TC + c) * G + g) * kSpStride;
         }
-        // 16 positions a step, every chain whole; the probabilities come in
-        // as wavefront-wide vector loads of one address (the offset is held
-        // in a VGPR: scalar loads return out of order, so the next step's
-        // could not be in flight while this step's are used), one step ahead.
+        // 16 positions a step, every chain whole; the probabilities come
+        // from LDS as broadcasts, one step ahead.
         int j = 0;
         v4u_stream pa[TC][2], pb[TC][2];
 #define GX_SP_LOAD(DST, JJ)                                                                                          \
     do {                                                                                                             \
         _Pragma("unroll") for (int c = 0; c < TC; c++) {                                                            \
-            _Pragma("unroll") for (int u = 0; u < 2; u++) {                                                         \
-                int off = c0 + (JJ) + 8 * u;                                                                         \
-                asm volatile("" : "+v"(off));                                                                        \
-                DST[c][u] = *(const v4u_stream *)(prow[c] + off);                                                    \
-            }                                                                                                        \
+            _Pragma("unroll") for (int u = 0; u < 2; u++)                                                           \
+                DST[c][u] = *(const v4u_stream *)(prl[c] + (JJ) + 8 * u);                                          \
         }                                                                                                            \
     } while (0)
 #define GX_SP_STEP(SRC, JJ)                                                                                          \
@@ -655,11 +679,8 @@ __global__ __launch_bounds__(64 * TGW * G) void attn_values_sp_kernel(int M, int
 #pragma unroll
             for (int c = 0; c < TC; c++)
 #pragma unroll
-                for (int u = 0; u < 3; u++) {
-                    int off = min(c0 + j + 8 * u, S - 8);  // past the prefix: read, never used
-                    asm volatile("" : "+v"(off));
-                    pt[c][u] = *(const v4u_stream *)(prow[c] + off);
-                }
+                for (int u = 0; u < 3; u++)  // past the prefix: read, never used
+                    pt[c][u] = *(const v4u_stream *)(prl[c] + min(j + 8 * u, kSpChunk - 8));
 #pragma unroll
             for (int u = 0; u < 3; u++) {
                 const int jp = j + 8 * u;
@@ -1727,10 +1748,10 @@ int launch_qwen_attention(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int
     // waiting -- every probability reaches all 64 lanes of a wavefront).
     if (M > 4 && !slots && G <= 4 && hd % kSpDims == 0) {
         constexpr int kTC = 4;
-        const size_t lds = (size_t)kSpDims * kSpStride * sizeof(uint16_t);
 #define GX_VSP(GG)                                                                                                   \
     do {                                                                                                             \
         constexpr int TGW = 16 / GG, TT = TGW * kTC;                                                                 \
+        const size_t lds = (size_t)(kSpDims + TT * GG) * kSpStride * sizeof(uint16_t);                               \
         attn_values_sp_kernel<kTC, GG, TGW><<<dim3((unsigned)(kv_heads * (hd / kSpDims)),                            \
                                                    (unsigned)((M + TT - 1) / TT)),                                   \
                                               64 * TGW * GG, lds, ctx->stream>>>(M, heads, hd, positions, limit,     \
