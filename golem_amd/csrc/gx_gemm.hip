@@ -16,8 +16,10 @@
 // vectors (golem stores d_a, the Q8_0 scale, already rounded through fp16),
 // so it comes from the matrix core too: v_mfma_f32_32x32x8_f16 with the two
 // vectors in k = 0 and zeros elsewhere gives every product exactly (an
-// 11-bit by 11-bit product fits fp32).  The vector ALU is left with one
-// conversion and one fma per element per block.
+// 11-bit by 11-bit product fits fp32; the int8 kernel puts them in k = 0 and
+// k = 4 and takes 2 d_w d_a against half the integer).  The vector ALU is
+// left with one conversion (a subtraction) and one fma per element per
+// block.
 //
 // Two kernels: the int8 one below (loads straight into LDS, every Q4_0
 // product of more than a few tokens, dense or grouped by expert) and an fp16
