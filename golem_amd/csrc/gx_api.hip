@@ -635,12 +635,15 @@ int gx_matmul_swiglu_q4_0(gx_ctx *ctx, const gx_weight *w, const int8_t *q, cons
     GX_CHECK(w->count == 1, "gx: a SwiGLU product takes a single matrix");
     GX_CHECK(w->rows % 64 == 0,
              "gx: the SwiGLU form needs gate and up rows interleaved by 32 (rows a multiple of 64, not %d)", w->rows);
-    GX_CHECK(M >= 0 && M <= 16, "gx: the SwiGLU product takes 1 to 16 columns, not %d", M);
+    GX_CHECK(M >= 0, "gx: %d columns", M);
     GX_CHECK(q && scales && qsum && mid_q && mid_scales && mid_qsum, "gx: missing argument");
     GX_CHECK(((uintptr_t)q & 15) == 0, "gx: q must be 16-byte aligned");
     if (M == 0)
         return ok();
-    if (int rc = gx::launch_q4_0_matvec_swiglu(ctx, w, q, scales, qsum, M, mid_q, mid_scales, mid_qsum))
+    // 1..16 columns on the matrix-vector kernels, more on the int8 batch
+    // product with the same epilogue
+    if (int rc = M <= 16 ? gx::launch_q4_0_matvec_swiglu(ctx, w, q, scales, qsum, M, mid_q, mid_scales, mid_qsum)
+                         : gx::launch_q4_0_gemm_swiglu(ctx, w, q, scales, M, mid_q, mid_scales, mid_qsum))
         return rc;
     return ok();
 }

@@ -423,12 +423,20 @@ struct DmaShape<32> {
 // DOTS: the same kernel, also writing every block's integer (the chain
 // difference x below) to dots[out row][n - row_start][b]; the scales are then
 // not needed, and their loads read the activation instead (in bounds).
-template <int TOK, bool GROUPED, bool DOTS>
+//
+// EPI 1 (dense, whole matrix): the rows are gate and up interleaved by 32 (a
+// tile's rows 0..31 gate, 32..63 up, for the same 32 outputs), and the
+// product ends in silu(gate) * up and its Q8_0 (qwen_swiglu_quant_kernel's
+// arithmetic, element for element) into mq / ms / mqs [M][rows / 2]: the
+// wavefront of a tile's up rows passes its sums through LDS to the
+// wavefront of the gate rows, whose lane pair (l, l + 32) holds one token's
+// 32 outputs, one Q8_0 block.
+template <int TOK, bool GROUPED, bool DOTS, int EPI = 0>
 __global__ __launch_bounds__(64 * DmaShape<TOK>::kWaves, DmaShape<TOK>::kOcc) void q4_0_gemm_dma_kernel(
     const uint8_t *__restrict__ W, size_t plane0_bytes, int B, int DC, const int8_t *__restrict__ q,
     const float *__restrict__ scales, int K, int M, int tiles, int tile0, int row_start, int row_end,
     const float *__restrict__ bias, float *__restrict__ y, int ldy, int32_t *__restrict__ dots, Groups grp,
-    int xcd_pairs) {
+    int xcd_pairs, int8_t *__restrict__ mq, float *__restrict__ ms, int32_t *__restrict__ mqs) {
     using Sh = DmaShape<TOK>;
     constexpr int kSlotB = Sh::kSlot;
     // Software-pipelined blocks (one block's MFMAs ahead of the previous
@@ -721,7 +729,71 @@ __global__ __launch_bounds__(64 * DmaShape<TOK>::kWaves, DmaShape<TOK>::kOcc) vo
     }
     wait_vmcnt<0>();  // the trailing loads land before the workgroup ends
     const int t = 32 * tg + li;
-    if (!DOTS && t < count) {
+    if constexpr (EPI == 1) {
+        __syncthreads();  // every wavefront is past its last operand reads
+        float *xch = (float *)ring_lds;  // [wavefront pair][lane][17]
+        const int pair = wv >> 1;
+        if (rg & 1) {
+#pragma unroll
+            for (int e = 0; e < 16; e++)
+                xch[(pair * 64 + lane) * 17 + e] = tot[e];
+        }
+        __syncthreads();
+        const int tile = T0 + (rg >> 1);
+        if (!(rg & 1) && tile * kTileRows < row_end) {
+            const int F = row_end >> 1;  // outputs a token
+            float v[16];
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const float gt = tot[e], u = xch[(pair * 64 + lane) * 17 + e];
+                const float ex = ggml_expf(-gt);
+                const float den = 1.0f + ex;
+                const float sl = gt / den;
+                v[e] = sl * u;
+            }
+            float peak = fabsf(v[0]);
+#pragma unroll
+            for (int e = 1; e < 16; e++)
+                peak = fmaxf(peak, fabsf(v[e]));
+            peak = fmaxf(peak, __shfl_xor(peak, 32, 64));  // the token's other 16 outputs
+            int32_t n[16];
+            float stored = 0.0f;
+            if (peak == 0.0f) {
+#pragma unroll
+                for (int e = 0; e < 16; e++)
+                    n[e] = 0;
+            } else {
+                const float scale = __fdiv_rn(peak, 127.0f);
+                const float inverse = __fdiv_rn(127.0f, peak);
+                stored = half_bits_to_float(float_to_half_bits(scale));
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    const int32_t k = nearest_int(v[e] * inverse);
+                    n[e] = k > 127 ? 127 : (k < -128 ? -128 : k);
+                }
+            }
+            int32_t sum = 0;
+#pragma unroll
+            for (int e = 0; e < 16; e++)
+                sum += n[e];
+            sum += __shfl_xor(sum, 32, 64);
+            if (t < count) {
+                const int row = orow(t);
+                // element e is output 8 (e / 4) + 4 g + e % 4 of the tile's 32
+#pragma unroll
+                for (int e4 = 0; e4 < 4; e4++) {
+                    const uint32_t w = (uint32_t)(n[4 * e4] & 0xFF) | ((uint32_t)(n[4 * e4 + 1] & 0xFF) << 8) |
+                                       ((uint32_t)(n[4 * e4 + 2] & 0xFF) << 16) |
+                                       ((uint32_t)(n[4 * e4 + 3] & 0xFF) << 24);
+                    *(uint32_t *)(mq + (size_t)row * F + tile * 32 + 8 * e4 + 4 * g) = w;
+                }
+                if (g == 0) {
+                    ms[(size_t)row * (F >> 5) + tile] = stored;
+                    mqs[(size_t)row * (F >> 5) + tile] = sum;
+                }
+            }
+        }
+    } else if (!DOTS && t < count) {
         float *yr = y + (size_t)orow(t) * ldy;
         const int nb = T0 * kTileRows + 32 * rg;  // the wavefront's first row
 #pragma unroll
@@ -735,8 +807,13 @@ __global__ __launch_bounds__(64 * DmaShape<TOK>::kWaves, DmaShape<TOK>::kOcc) vo
 
 }  // namespace
 
-int launch_q4_0_gemm(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, const int8_t *q, const float *scales,
-                     int M, int row_start, int row_end, const float *bias, float *y, int ldy, int32_t *dots) {
+namespace {
+// The dense product's grid and launch (EPI 0: y = the product; EPI 1: the
+// SwiGLU + Q8_0 epilogue into mq / ms / mqs).
+template <int EPI>
+int launch_dense(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, const int8_t *q, const float *scales, int M,
+                 int row_start, int row_end, const float *bias, float *y, int ldy, int32_t *dots, int8_t *mq,
+                 float *ms, int32_t *mqs) {
     // the widened weights are signed: no recentring term, so no qsum
     const int tile0 = row_start / kTileRows;
     const int tiles = (row_end + kTileRows - 1) / kTileRows - tile0;
@@ -752,19 +829,38 @@ int launch_q4_0_gemm(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, const 
     const int xp = pairs >= 8 ? pairs : 0;
     const dim3 grid = xp ? dim3((unsigned)(8 * ((pairs + 7) / 8) * groups)) : dim3((unsigned)pairs, (unsigned)groups);
 #define GX_DMA_LAUNCH(TK, NT, DD)                                                                                   \
-    q4_0_gemm_dma_kernel<TK, false, DD><<<grid, NT, 0, ctx->stream>>>(                                              \
+    q4_0_gemm_dma_kernel<TK, false, DD, EPI><<<grid, NT, 0, ctx->stream>>>(                                         \
         mat, w->plane0_bytes, w->blocks, w->dchunks, q, scales, w->cols, M, w->tiles, tile0, row_start, row_end,     \
-        bias, y, ldy, DD ? dots : nullptr, none, xp)
-    if (tok == 32 && dots)
-        GX_DMA_LAUNCH(32, 256, true);
-    else if (tok == 32)
-        GX_DMA_LAUNCH(32, 256, false);
-    else if (dots)
-        GX_DMA_LAUNCH(64, 512, true);
-    else
-        GX_DMA_LAUNCH(64, 512, false);
+        bias, y, ldy, DD ? dots : nullptr, none, xp, mq, ms, mqs)
+    if constexpr (EPI == 1) {
+        if (tok == 32)
+            GX_DMA_LAUNCH(32, 256, false);
+        else
+            GX_DMA_LAUNCH(64, 512, false);
+    } else {
+        if (tok == 32 && dots)
+            GX_DMA_LAUNCH(32, 256, true);
+        else if (tok == 32)
+            GX_DMA_LAUNCH(32, 256, false);
+        else if (dots)
+            GX_DMA_LAUNCH(64, 512, true);
+        else
+            GX_DMA_LAUNCH(64, 512, false);
+    }
 #undef GX_DMA_LAUNCH
     return check_launch("q4_0_gemm");
+}
+}  // namespace
+
+int launch_q4_0_gemm(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, const int8_t *q, const float *scales,
+                     int M, int row_start, int row_end, const float *bias, float *y, int ldy, int32_t *dots) {
+    return launch_dense<0>(ctx, w, mat, q, scales, M, row_start, row_end, bias, y, ldy, dots, nullptr, nullptr,
+                           nullptr);
+}
+
+int launch_q4_0_gemm_swiglu(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const float *scales, int M,
+                            int8_t *mq, float *ms, int32_t *mqs) {
+    return launch_dense<1>(ctx, w, w->dev, q, scales, M, 0, w->rows, nullptr, nullptr, 0, nullptr, mq, ms, mqs);
 }
 
 int launch_q4_0_gemm_grouped(gx_ctx *ctx, const gx_weight *w, const int32_t *work, int max_items,
@@ -776,11 +872,11 @@ int launch_q4_0_gemm_grouped(gx_ctx *ctx, const gx_weight *w, const int32_t *wor
     if (dots)
         q4_0_gemm_dma_kernel<32, true, true><<<grid, 256, 0, ctx->stream>>>(
             w->dev, w->plane0_bytes, w->blocks, w->dchunks, q, scales, w->cols, 0, w->tiles, 0, 0, w->rows, nullptr,
-            y, ldy, dots, grp, 0);
+            y, ldy, dots, grp, 0, nullptr, nullptr, nullptr);
     else
         q4_0_gemm_dma_kernel<32, true, false><<<grid, 256, 0, ctx->stream>>>(
             w->dev, w->plane0_bytes, w->blocks, w->dchunks, q, scales, w->cols, 0, w->tiles, 0, 0, w->rows, nullptr,
-            y, ldy, nullptr, grp, 0);
+            y, ldy, nullptr, grp, 0, nullptr, nullptr, nullptr);
     return check_launch("q4_0_gemm_grouped");
 }
 }  // namespace gx

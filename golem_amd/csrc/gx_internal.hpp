@@ -115,6 +115,8 @@ int launch_q4_0_matvec(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, cons
                        int ldy, int32_t *dots, int form);
 int launch_q4_0_gemm(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, const int8_t *q, const float *scales,
                      int M, int row_start, int row_end, const float *bias, float *y, int ldy, int32_t *dots);
+int launch_q4_0_gemm_swiglu(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const float *scales, int M,
+                            int8_t *mq, float *ms, int32_t *mqs);
 // The expert-grouped product: work items {expert, first, count <= 32, 0}
 // over the units sorted by expert (gx_moe.hip's sort); dots as above, by
 // output (unit) row.

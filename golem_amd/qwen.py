@@ -303,13 +303,9 @@ class QwenModel:
             self._mm(b["o"], self.set8, M, self.attn, cfg.dim)
             call("gx_norm_quant", ctx, vp(self.xs), cfg.dim, vp(self.attn), cfg.dim, vp(b["ffn_norm"]), M, cfg.dim,
                  np.float32(cfg.eps), None, 0, vp(self.x8.q), vp(self.x8.s), vp(self.x8.qs))
-            if M <= 16:  # the product and SwiGLU + Q8_0 in one kernel
-                call("gx_matmul_swiglu_q4_0", ctx, b["gu"].ptr, vp(self.x8.q), vp(self.x8.s), vp(self.x8.qs), M,
-                     vp(self.mid8.q), vp(self.mid8.s), vp(self.mid8.qs))
-            else:
-                self._mm(b["gu"], self.x8, M, self.gu, 2 * cfg.ffn)
-                call("gx_swiglu_quant", ctx, vp(self.gu), 2 * cfg.ffn, M, cfg.ffn, 32, vp(self.mid8.q),
-                     vp(self.mid8.s), vp(self.mid8.qs))
+            # the product and SwiGLU + Q8_0 in one kernel (its epilogue)
+            call("gx_matmul_swiglu_q4_0", ctx, b["gu"].ptr, vp(self.x8.q), vp(self.x8.s), vp(self.x8.qs), M,
+                 vp(self.mid8.q), vp(self.mid8.s), vp(self.mid8.qs))
             self._mm(b["down"], self.mid8, M, self.ffn, cfg.dim)
         if blocks is not None:
             return

@@ -481,9 +481,10 @@ int gx_norm_swiglu_q4_0(gx_ctx *ctx, const gx_weight *w, const float *x, const f
  * the same up rows), then silu(gate) * up and its Q8_0 into mid_q
  * [M][rows/2], mid_scales and mid_qsum [M][rows/64] -- bit for bit
  * gx_matmul_q4_0 followed by gx_swiglu_quant (group 32) (qwen/block.go:
- * 82-90, nn/swiglu.go:77-82), in one kernel: for 1 to 16 positions
- * (golem's lock-step slots, short batches).  No counterpart in
- * golem as one call. */
+ * 82-90, nn/swiglu.go:77-82), in one kernel: 1 to 16 positions on the
+ * matrix-vector kernels (golem's lock-step slots, short batches), more on
+ * the int8 batch product with the same epilogue (a prompt).  No counterpart
+ * in golem as one call. */
 int gx_matmul_swiglu_q4_0(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const float *scales,
                           const int32_t *qsum, int M, int8_t *mid_q, float *mid_scales, int32_t *mid_qsum);
 

@@ -447,8 +447,9 @@ def test_norm_swiglu_fused_bit_exact(dev, ffn, K):
 
 @pytest.mark.parametrize("ffn,K", [(9728, 2560), (1056, 2080), (32, 256), (96, 4608)])
 def test_matmul_swiglu_columns_bit_exact(dev, ffn, K):
-    """gx_matmul_swiglu_q4_0 (the product of 1 to 16 columns with SwiGLU and
-    Q8_0 in its epilogue) against gx_matmul_q4_0 of the same interleaved
+    """gx_matmul_swiglu_q4_0 (the product with SwiGLU and Q8_0 in its
+    epilogue: 1 to 16 columns on the matrix-vector kernels, more on the int8
+    batch product) against gx_matmul_q4_0 of the same interleaved
     matrix then gx_swiglu_quant (group 32), column by column, bit for bit."""
     from golem_amd.qwen import interleave_rows
     g = synth.rng(190 + ffn)
@@ -456,7 +457,9 @@ def test_matmul_swiglu_columns_bit_exact(dev, ffn, K):
     up = synth.q4_0_weights(g, ffn, K)
     inter = dev.weight(interleave_rows(gate, up, ffn, K), capi.Q4_0, 2 * ffn, K)
     # K = 4608 (18 stretches) takes the form without staging, up to 8 columns
-    for M in ((1, 2, 3, 5, 8, 16) if K <= 4096 else (1, 2, 8)):
+    # 17 and more columns: the int8 batch product's epilogue (32-token
+    # workgroups up to 1024 tokens, 64 beyond)
+    for M in ((1, 2, 3, 5, 8, 16, 17, 70, 1030) if K <= 4096 else (1, 2, 8, 40)):
         log(f"matmul swiglu ffn={ffn} K={K} M={M}")
         act = dev.quantize_q8_0((synth.activations(g, M, K) * 2).astype(np.float32), with_corr=False,
                                 with_q16=False)
@@ -490,14 +493,12 @@ def test_matmul_swiglu_refuses_what_it_cannot_take(dev):
     # more stretches than the multi-column kernel's wavefronts
     wide = dev.weight(synth.q4_0_weights(g, 64, K), capi.Q4_0, 64, K)
     odd = dev.weight(synth.q4_0_weights(g, 96, 256), capi.Q4_0, 96, 256)  # rows not a multiple of 64
-    fine = dev.weight(synth.q4_0_weights(g, 64, 256), capi.Q4_0, 64, 256)
-    for w, m in ((wide, 16), (odd, 1), (fine, 17)):  # 17 columns: more than the kernel takes
+    for w, m in ((wide, 16), (odd, 1), (odd, 17)):  # odd rows refused on either path
         with pytest.raises(capi.GxError):
             capi.call("gx_matmul_swiglu_q4_0", dev.ctx.ptr, w.ptr, capi.vp(act[0]), capi.vp(act[1]),
                       capi.vp(act[2]), m, capi.vp(q), capi.vp(sc), capi.vp(qs))
     wide.free()
     odd.free()
-    fine.free()
 
 
 def test_fused_products_refuse_aliasing(dev):
