@@ -39,6 +39,7 @@ def load():
         "orc_half_to_float": (F, [ctypes.c_uint16]),
         "orc_float_to_half": (ctypes.c_uint16, [F]),
         "orc_round_half": (F, [F]),
+        "orc_round_half_n": (None, [V, I]),
         "orc_nearest_int": (ctypes.c_int32, [F]),
         "orc_quantize_range": (I, [V, I, I, I, V, V, V, I, I]),
         "orc_quantize_column_range": (None, [V, I, I, V, V, V, I, I, I]),

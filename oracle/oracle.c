@@ -110,6 +110,14 @@ uint16_t orc_float_to_half(float f)
 /* RoundHalf, nn/half.go:48 */
 float orc_round_half(float v) { return orc_half_to_float(orc_float_to_half(v)); }
 
+/* RoundHalf over n values in place (the cache entries and queries of a
+ * head, qwen/attention.go:67, qwen/cache.go:52-60). */
+void orc_round_half_n(float *x, int n)
+{
+    for (int i = 0; i < n; i++)
+        x[i] = orc_round_half(x[i]);
+}
+
 /* nearestInt, nn/batch.go:221-224: adding 1.5*2^23 leaves the rounded
  * integer in the low mantissa bits (valid for |f| < 2^22). */
 int32_t orc_nearest_int(float f)

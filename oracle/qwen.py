@@ -58,10 +58,8 @@ class QwenOracle:
 
     @staticmethod
     def _round_half(x):
-        lib = load()
         out = np.array(x, dtype=np.float32).reshape(-1)
-        for i in range(len(out)):
-            out[i] = lib.orc_round_half(float(out[i]))
+        load().orc_round_half_n(_p(out), len(out))
         return out.reshape(np.shape(x))
 
     def embed(self, token):
@@ -108,19 +106,23 @@ class QwenOracle:
         q, k, v = (self._mat(layer, n, normed) for n in ("q", "k", "v"))
         return self._mat(layer, "o", Batch(self.attend(layer, q, k, v, pos)).quantize())
 
-    def attend(self, layer, q, k, v, pos):
+    def attend(self, layer, q, k, v, pos, only=None):
         """Attention's head-by-head part and the attention proper
         (qwen/attention.go:57-124) from the Q, K and V projections of the
         batch: per-head norms, RoPE, fp16 query and cache entries, then every
-        head's output (the floats the O projection's Q8_0 is made from)."""
+        head's output (the floats the O projection's Q8_0 is made from).
+        only: the batch rows whose outputs are wanted (every row's keys and
+        values still go into the cache); the result then has one row each."""
         cfg, bw, lib = self.cfg, self.w["blocks"][layer], load()
         hd, batch = cfg.head_dim, len(q)
+        rows = list(range(batch)) if only is None else [int(t) for t in only]
+        wanted = set(rows)
         qh = np.zeros_like(q)
         cos = np.zeros(hd // 2, np.float32)
         sin = np.zeros(hd // 2, np.float32)
         for t in range(batch):
             lib.orc_rope_prepare(hd, pos[t], cfg.rope_base, _p(cos), _p(sin))
-            for h in range(cfg.heads):
+            for h in range(cfg.heads if t in wanted else 0):
                 head = rms_norm_plain(q[t, h * hd:(h + 1) * hd], bw["q_norm"], cfg.eps)
                 lib.orc_rope_apply(_p(head), hd, _p(cos), _p(sin))
                 qh[t, h * hd:(h + 1) * hd] = self._round_half(head)
@@ -131,16 +133,16 @@ class QwenOracle:
                 self.V[layer][pos[t], h] = self._round_half(v[t, h * hd:(h + 1) * hd])
         per_kv = cfg.heads // cfg.kv_heads
         scale = np.float32(1 / math.sqrt(float(hd)))
-        out = np.zeros((batch, cfg.heads * hd), np.float32)
+        out = np.zeros((len(rows), cfg.heads * hd), np.float32)
         scores = np.zeros(cfg.max_context, np.float32)
         Kl, Vl = self.K[layer], self.V[layer]
-        for t in range(batch):
+        for i, t in enumerate(rows):
             for h in range(cfg.heads):
                 query = np.ascontiguousarray(qh[t, h * hd:(h + 1) * hd])
                 dst = np.zeros(hd, np.float32)
                 lib.orc_attend(_p(query), _p(Kl), _p(Vl), cfg.kv_heads, hd, h // per_kv, pos[t] + 1, scale,
                                _p(scores), _p(dst))
-                out[t, h * hd:(h + 1) * hd] = dst
+                out[i, h * hd:(h + 1) * hd] = dst
         return out
 
     def logits(self, hidden):

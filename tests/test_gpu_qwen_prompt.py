@@ -1,0 +1,192 @@
+"""Config 3's prompt path at its configured length: a 512-token prefill at the
+full width (2560, FFN 9728, 32/8 heads of 128) on the device against the
+oracle's restatement of golem's engine (oracle/qwen.py).
+
+A prompt of more than 16 positions runs kernels a short prompt never
+reaches: the 64-token int8 MFMA product (Q|K|V, O, Down), the same product
+with the SwiGLU + Q8_0 epilogue (Gate|Up), the head-norm/RoPE pass at
+M = 512, and the prompt attention's three passes (scores, softmax, values in
+16-token workgroups).  golem reads such a prompt through ForwardBatch
+(qwen/model.go:127-175) and Attention (qwen/attention.go:86-124).
+
+- the attention alone at config 3's heads over a 512-position prompt: the
+  Q8_0 of every head of one or more tokens of each 16-token group, bit for
+  bit against golem's orc_attend;
+- two full-width blocks over a 512-token prompt, stage by stage on sampled
+  positions of every token group (each stage fed the device's own inputs,
+  as in test_gpu_qwen_full.py), plus every key and value cache entry of
+  all 512 positions bit for bit;
+- a 48-token prompt read in one batch equal, bit for bit, to the same
+  tokens one at a time at full width (TestBatchAgreesWithOneAtATime,
+  qwen/model_test.go:78).
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from golem_amd import capi, synth
+from golem_amd.qwen import QwenModel
+from tests.gpu_util import log
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+PROMPT = 512
+# one token of every 16-token group of the values pass (at a different
+# offset in each), and the groups' edges at both ends and the middle
+SAMPLE = sorted(set([16 * g + (7 * g) % 16 for g in range(PROMPT // 16)]
+                    + [0, 1, 15, 16, 17, 255, 256, 510, 511]))
+
+
+def _bits(a):
+    return np.ascontiguousarray(a).view(np.uint32)
+
+
+def _config3(layers, context):
+    return synth.QwenConfig(2560, 9728, layers, 32, 8, 128, 151936, context)
+
+
+def test_prompt_attention_config3_heads_512(dev, orc):
+    """gx_qwen_attention over a 512-position prompt (every position a query
+    at its own position, the last seeing all 512) at config 3's heads."""
+    hd, heads, kv = 128, 32, 8
+    g = synth.rng(512)
+    M = PROMPT
+    pos = np.arange(M, dtype=np.int32)
+    context = M
+    kcf = g.standard_normal((M, kv, hd)).astype(np.float16)
+    vcf = (g.standard_normal((M, kv, hd)) * 2).astype(np.float16)
+    qf = (g.standard_normal((M, heads * hd)) * 1.5).astype(np.float16)
+    vt = np.ascontiguousarray(vcf.transpose(1, 2, 0))  # [kv][hd][context]
+    kt = np.ascontiguousarray(kcf.reshape(M, kv, hd // 8, 8).transpose(1, 2, 0, 3))  # [kv][hd/8][context][8]
+    q8 = dev.empty((M, heads * hd), np.int8)
+    sc = dev.empty((M, heads * hd // 32), np.float32)
+    qs = dev.empty((M, heads * hd // 32), np.int32)
+    n = capi.size_out("gx_qwen_attention_workspace_bytes", M, heads, M - 1)
+    ws = dev.empty((n,), np.uint8)
+    ins = [dev.put(a) for a in (qf.view(np.int16), pos, kt.view(np.int16), vt.view(np.int16))]
+    log(f"prompt attention {heads}/{kv} heads x {hd}, {M} positions")
+    capi.call("gx_qwen_attention", dev.ctx.ptr, capi.vp(ins[0]), M, heads, kv, hd, M - 1, capi.vp(ins[1]),
+              capi.vp(ins[2]), capi.vp(ins[3]), context, capi.vp(q8), capi.vp(sc), capi.vp(qs), capi.vp(ws), n,
+              None, 0)
+    lib = orc.load()
+    K32, V32 = np.ascontiguousarray(kcf.astype(np.float32)), np.ascontiguousarray(vcf.astype(np.float32))
+    scale = np.float32(1 / math.sqrt(float(hd)))
+    out = np.zeros((len(SAMPLE), heads * hd), np.float32)
+    scores = np.zeros(M, np.float32)
+    for i, t in enumerate(SAMPLE):
+        for h in range(heads):
+            query = np.ascontiguousarray(qf[t, h * hd:(h + 1) * hd].astype(np.float32))
+            dst = np.zeros(hd, np.float32)
+            lib.orc_attend(orc._p(query), orc._p(K32), orc._p(V32), kv, hd, h // (heads // kv), t + 1, scale,
+                           orc._p(scores), orc._p(dst))
+            out[i, h * hd:(h + 1) * hd] = dst
+    b = orc.Batch(out).quantize()
+    got_q, got_s, got_qs = dev.get(q8)[SAMPLE], dev.get(sc)[SAMPLE], dev.get(qs)[SAMPLE]
+    for i, t in enumerate(SAMPLE):
+        assert np.array_equal(got_q[i], b.q_rows()[i]), f"token {t} (group {t // 16}): head Q8_0"
+        assert np.array_equal(_bits(got_s[i]), _bits(b.scales_rows()[i])), f"token {t}: head scales"
+        assert np.array_equal(got_qs[i], b.qsum_rows()[i]), f"token {t}: head sums"
+    log(f"  {len(SAMPLE)} tokens from {len(set(t // 16 for t in SAMPLE))} token groups bit for bit")
+
+
+def check_block_sampled(model, om, orc, prompt, layer):
+    """One block of a long prompt, stage by stage, on the SAMPLE positions;
+    every stage fed the device's own inputs so nothing accumulates."""
+    from oracle import Batch
+    cfg, M, S = model.cfg, len(prompt), SAMPLE
+    pos = list(range(M))
+    xin = model.residual(prompt, 0, layer)
+    xout = model.residual(prompt, 0, layer + 1)
+
+    def dev(t):
+        return t[:M].cpu().numpy().copy()
+
+    qkv, set_q, set_s, attn = dev(model.qkv), dev(model.set8.q), dev(model.set8.s), dev(model.attn)
+    mid_q, mid_s, ffn = dev(model.mid8.q), dev(model.mid8.s), dev(model.ffn)
+    kc, vc = model.kc[layer].cpu().numpy(), model.vc[layer].cpu().numpy()
+    # the Gate|Up floats of the device's own pre-norm (the block hands SwiGLU's
+    # Q8_0 on from the product's epilogue without them)
+    model._mm(model.blocks[layer]["gu"], model.x8, M, model.gu, 2 * cfg.ffn)
+    x8_q, x8_s, gu = dev(model.x8.q), dev(model.x8.s), dev(model.gu)
+
+    def rel(got, want):
+        return max(orc.compare_floats(got[i], want[i])[0] for i in range(len(want)))
+
+    qd, kvd, hd = model.qd, model.kvd, cfg.head_dim
+    worst = {}
+    nA = om.norm(layer, xin[S], "attn_norm")
+    q, k, v = (om._mat(layer, n, nA) for n in ("q", "k", "v"))
+    worst["qkv"] = rel(qkv[S], np.concatenate([q, k, v], axis=1))
+    # head norms + RoPE + cache entries of every position, then the attention
+    # of the sampled tokens over the device's Q|K|V rows
+    out = om.attend(layer, qkv[:, :qd], qkv[:, qd:qd + kvd], qkv[:, qd + kvd:], pos, only=S)
+    got_k = kc[0].view(np.float16).astype(np.float32)  # [kv][hd/8][context][8]
+    got_k = got_k[:, :, :M, :].transpose(2, 0, 1, 3).reshape(M, cfg.kv_heads, hd)
+    got_v = vc[0].view(np.float16).astype(np.float32)[:, :, :M].transpose(2, 0, 1)  # [kv][hd][context]
+    assert np.array_equal(_bits(got_k), _bits(om.K[layer][:M])), f"block {layer}: key cache"
+    assert np.array_equal(_bits(got_v), _bits(om.V[layer][:M])), f"block {layer}: value cache"
+    heads = Batch(out).quantize()
+    for i, t in enumerate(S):
+        assert np.array_equal(set_q[t], heads.q_rows()[i]), f"block {layer} token {t}: attention Q8_0"
+        assert np.array_equal(_bits(set_s[t]), _bits(heads.scales_rows()[i])), f"block {layer} token {t}: scales"
+    worst["o"] = rel(attn[S], om._mat(layer, "o", heads))
+    xs = xin[S] + attn[S]
+    nF = om.norm(layer, xs, "ffn_norm")
+    assert np.array_equal(x8_q[S], nF.q_rows()), f"block {layer}: FFN pre-norm Q8_0"
+    assert np.array_equal(_bits(x8_s[S]), _bits(nF.scales_rows())), f"block {layer}: FFN pre-norm scales"
+    g4 = gu[S].reshape(len(S), -1, 64)  # gate and up rows interleaved by 32
+    gate, up = g4[:, :, :32].reshape(len(S), -1), g4[:, :, 32:].reshape(len(S), -1)
+    worst["gate"] = rel(gate, om._mat(layer, "gate", nF))
+    worst["up"] = rel(up, om._mat(layer, "up", nF))
+    mid = Batch(om.swiglu(gate, up)).quantize()
+    assert np.array_equal(mid_q[S], mid.q_rows()), f"block {layer}: SwiGLU Q8_0"
+    assert np.array_equal(_bits(mid_s[S]), _bits(mid.scales_rows())), f"block {layer}: SwiGLU scales"
+    worst["down"] = rel(ffn[S], om._mat(layer, "down", mid))
+    assert np.array_equal(_bits(xout[S]), _bits(xs + ffn[S])), f"block {layer}: residual adds"
+    for stage, r in worst.items():
+        assert r <= TOL, f"block {layer} {stage}: {r:.3g} of RMS"
+    log(f"  block {layer}: " + ", ".join(f"{k} {v:.2g}" for k, v in worst.items()) + " of RMS")
+    return max(worst.values())
+
+
+@pytest.mark.parametrize("symmetric", [False, True])
+def test_prompt_512_two_blocks_stage_by_stage(dev, orc, symmetric):
+    from oracle.qwen import QwenOracle
+    cfg = _config3(2, PROMPT)
+    log(f"config 3 width, 2 blocks, {PROMPT}-token prompt, symmetric={symmetric}: drawing weights")
+    w = synth.qwen_weights(cfg, 3 + symmetric, symmetric=symmetric)
+    model = QwenModel(dev.ctx, cfg, w, max_batch=PROMPT, attention="golem")
+    om = QwenOracle(cfg, w)
+    prompt = [int(t) for t in synth.rng(3).integers(0, cfg.vocab, PROMPT)]
+    for layer in range(cfg.layers):
+        check_block_sampled(model, om, orc, prompt, layer)
+    log(f"  {len(SAMPLE)} sampled positions from {len(set(t // 16 for t in SAMPLE))} token groups")
+    model.free()
+
+
+def test_prompt_48_batch_equals_one_at_a_time_full_width(dev):
+    """golem's TestBatchAgreesWithOneAtATime (qwen/model_test.go:78) at
+    config 3's width: 48 tokens in one batch (the 64-token int8 product,
+    the prompt attention's three passes over three token groups) against the
+    same tokens one position at a time (the decode kernels), hidden states
+    and caches bit for bit, in golem's attention order."""
+    cfg = _config3(2, 64)
+    w = synth.qwen_weights(cfg, 35, symmetric=True)
+    model = QwenModel(dev.ctx, cfg, w, max_batch=48, attention="golem")
+    prompt = [int(t) for t in synth.rng(35).integers(0, cfg.vocab, 48)]
+    log(f"config 3 width, 2 blocks: {len(prompt)} tokens in one batch against one at a time")
+    model.reset()
+    batch = dev.get(model.forward(prompt, 0)).copy()
+    kb = [k.cpu().numpy().copy() for k in model.kc]
+    vb = [v.cpu().numpy().copy() for v in model.vc]
+    model.reset()
+    alone = np.stack([dev.get(model.forward([t], i))[0].copy() for i, t in enumerate(prompt)])
+    np.testing.assert_array_equal(_bits(batch), _bits(alone))
+    for layer in range(cfg.layers):
+        np.testing.assert_array_equal(kb[layer], model.kc[layer].cpu().numpy())
+        np.testing.assert_array_equal(vb[layer], model.vc[layer].cpu().numpy())
+    torch.cuda.synchronize()
+    model.free()
