@@ -84,6 +84,86 @@ __device__ __forceinline__ float ggml_expf(float x) {
     return j * k + k;
 }
 
+// A lane's neighbour's value through DPP, for wavefront reductions without an
+// LDS round trip: CTRL 0xB1 = quad_perm [1,0,3,2] (lane l ^ 1), 0x4E =
+// quad_perm [2,3,0,1] (l ^ 2), 0x141 = row_half_mirror (7 - l within 8
+// lanes), 0x140 = row_mirror (15 - l within 16 lanes).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// The pairwise sum of a wavefront's 64 values, every lane getting the same
+// bits: lane l adds lane l ^ 1's value, then l ^ 2's, l ^ 4's, l ^ 8's, l ^
+// 16's and l ^ 32's (each step a commutative add of two equal-structured
+// partial sums), i.e. ((v0 + v1) + (v2 + v3)) + ... as a balanced tree in lane
+// order.  Once a quad (eight, sixteen lanes) holds equal values, the mirror
+// permutations pick a lane of the partner group, which holds the same value
+// as lane l ^ 4 (l ^ 8); rows are combined through readlane.
+__device__ __forceinline__ float wave_pairwise_sum(float v) {
+    v = v + dpp_f32<0xB1>(v);
+    v = v + dpp_f32<0x4E>(v);
+    v = v + dpp_f32<0x141>(v);
+    v = v + dpp_f32<0x140>(v);
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return (r0 + r1) + (r2 + r3);
+}
+
+// The maximum of a wavefront's 64 values (fmaxf: NaNs ignored), in every lane.
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp_f32<0xB1>(v));
+    v = fmaxf(v, dpp_f32<0x4E>(v));
+    v = fmaxf(v, dpp_f32<0x141>(v));
+    v = fmaxf(v, dpp_f32<0x140>(v));
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
+template <int CTRL>
+__device__ __forceinline__ int32_t dpp_i32(int32_t v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+
+// The maximum and the integer sum over each aligned group of 8 lanes
+// (lane l with l ^ 1, l ^ 2, then the other quad of the eight), every lane
+// of the group getting the result.  Order-free: max and integer addition
+// are exact in any order.
+__device__ __forceinline__ float group8_max(float v) {
+    v = fmaxf(v, dpp_f32<0xB1>(v));
+    v = fmaxf(v, dpp_f32<0x4E>(v));
+    return fmaxf(v, dpp_f32<0x141>(v));
+}
+__device__ __forceinline__ int32_t group8_sum(int32_t v) {
+    v += dpp_i32<0xB1>(v);
+    v += dpp_i32<0x4E>(v);
+    return v + dpp_i32<0x141>(v);
+}
+
+// The same over each aligned group of 32 lanes (a wavefront's halves): rows
+// of 16 through DPP, the two rows of a half through readlane.
+__device__ __forceinline__ float group32_max(float v) {
+    v = group8_max(v);
+    v = fmaxf(v, dpp_f32<0x140>(v));
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return (__lane_id() < 32) ? fmaxf(r0, r1) : fmaxf(r2, r3);
+}
+__device__ __forceinline__ int32_t group32_sum(int32_t v) {
+    v = group8_sum(v);
+    v += dpp_i32<0x140>(v);
+    const int32_t r0 = __builtin_amdgcn_readlane(v, 0), r1 = __builtin_amdgcn_readlane(v, 16);
+    const int32_t r2 = __builtin_amdgcn_readlane(v, 32), r3 = __builtin_amdgcn_readlane(v, 48);
+    return (__lane_id() < 32) ? r0 + r1 : r2 + r3;
+}
+
 // Q8_0 (Batch.quantizeBlock, nn/batch.go:109-143) of a 32-value block held
 // four values a lane by eight consecutive lanes (lanes 8k .. 8k+7 of a
 // wavefront, values in order): the same arithmetic as q8_0_lane.  Returns the
@@ -91,9 +171,7 @@ __device__ __forceinline__ float ggml_expf(float x) {
 // q come back in *stored and *sum (valid in all eight lanes).
 __device__ __forceinline__ uint32_t q8_0_quad(const float v[4], float *stored, int32_t *sum) {
     float peak = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-#pragma unroll
-    for (int off = 4; off > 0; off >>= 1)
-        peak = fmaxf(peak, __shfl_xor(peak, off, 8));
+    peak = group8_max(peak);
     if (peak == 0.0f) {
         *stored = 0.0f;
         *sum = 0;
@@ -112,10 +190,7 @@ __device__ __forceinline__ uint32_t q8_0_quad(const float v[4], float *stored, i
         s += n;
         packed |= ((uint32_t)n & 0xFFu) << (8 * k);
     }
-#pragma unroll
-    for (int off = 4; off > 0; off >>= 1)
-        s += __shfl_xor(s, off, 8);
-    *sum = s;
+    *sum = group8_sum(s);
     return packed;
 }
 
@@ -344,10 +419,7 @@ __device__ __forceinline__ double block_sum_squares(const float *xs, int K, doub
 // nn/batch.go:109-143): returns q; the group's fp16-rounded scale and sum of
 // q come back in *stored and *sum (valid in every lane).
 __device__ __forceinline__ int32_t q8_0_lane(float v, float *stored, int32_t *sum) {
-    float peak = fabsf(v);
-#pragma unroll
-    for (int off = 16; off > 0; off >>= 1)
-        peak = fmaxf(peak, __shfl_xor(peak, off, 32));
+    const float peak = group32_max(fabsf(v));
     if (peak == 0.0f) {
         *stored = 0.0f;
         *sum = 0;
@@ -359,11 +431,7 @@ __device__ __forceinline__ int32_t q8_0_lane(float v, float *stored, int32_t *su
     const float prod = v * inverse;
     int32_t n = nearest_int(prod);
     n = n > 127 ? 127 : (n < -128 ? -128 : n);
-    int32_t s = n;
-#pragma unroll
-    for (int off = 16; off > 0; off >>= 1)
-        s += __shfl_xor(s, off, 32);
-    *sum = s;
+    *sum = group32_sum(n);
     return n;
 }
 

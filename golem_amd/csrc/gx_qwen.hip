@@ -1076,80 +1076,77 @@ __global__ __launch_bounds__(kDecodeThreads) void attn_decode_kernel(
 
 // ---- decode attention, sums in a parallel order -----------------------------
 //
-// The same attention as attn_decode_kernel (G = 1: a workgroup per (query
-// head, 32-wide value slice), positions of one token, prefixes of at most
-// kDecodeMax), with its two serial sums taken in parallel: SoftmaxInPlace's
-// total (nn/ops.go:59-73) as a tree of the threads' exponentials, and each
-// value element's Axpy over the positions (nn/kernel.go:221-233) as runs of
-// consecutive positions added afterwards in run order.  The scores, their
-// maximum, each exponential (float64 exp), the division and the fp16
-// rounding of each probability are golem's; only the order of the two sums
-// differs.  The value sums' reordering moves the outputs by about 1e-7; the
-// total's, when it moves the total by an ulp, moves any probability sitting
-// on an fp16 rounding boundary by one fp16 step (2^-11 of itself), which is
-// up to a few 1e-5 of a head's RMS.  Every thread takes a share of both sums, where
-// the serial kernel leaves them to one thread per head and 32 per slice.
-// Loads: the cached keys and values of the whole extent (max_pos + 1) are
-// requested first, before the token's position (itself a load) is known --
-// the key rows a lane per position, the value pieces of thread (run g,
-// element d) 8 positions to 16 bytes -- and positions past the prefix are
-// read but left out of every sum.  With FUSE, wavefront 0 only runs the
-// prologue (head norms, RoPE, the position's cache store), issuing the Q|K|V
-// row and norm gains first and the rotation tables once the position is
-// known, so that it waits for nothing but its own loads; the other seven
-// wavefronts do the cache work.  Barriers wait for LDS only, so the
-// prologue's cache stores and the value loads stay in flight across them.
-// With FUSE wavefront 0 does the prologue alone and the other seven the
-// cache work; without it all eight do.
-// The value runs are fixed (kRuns runs of kXChunk positions, whatever the
-// launch's extent and in both forms), so that a token's result depends on
-// its prefix only: a step replayed from a graph launched for the whole cache
-// equals the same step launched for its own prefix, bit for bit.
-// ROWS: key rows a thread scores -- one when the extent fits the cache
-// threads (half the registers: two workgroups a CU), else enough for
-// kDecodeMax.  The runs do not depend on it.
-// VW: value elements a workgroup (kValSlice: a head's 32-element slice, the
-// long-extent form; HD: the whole head, one workgroup a query head, for
-// extents of at most kShortRuns runs).  The position runs of the value sums
-// are the same in both (kRuns runs of kXChunk positions, combined in run
-// order), so both give the same bits; the short form has threads for its
-// first kShortRuns runs only and adds the rest's +0 as one +0.
-constexpr int kShortRuns = 2;
+// The decode step's default attention (M <= 4 positions, or one position per
+// conversation, prefixes of at most kDecodeMax): grid (heads * hd/VW, M), a
+// workgroup per (query head, VW-element value slice, token), 1024 threads.
+// The same scores, maximum, float64 exponentials, division and fp16 rounding
+// of each probability as golem's SoftmaxInPlace and Axpy (qwen/attention.go:
+// 96-114, nn/ops.go:59-73), with the two serial sums taken in a fixed parallel
+// order that does not depend on the launch's extent (so that a step replayed
+// from a graph launched for the whole cache equals the same step launched for
+// its own prefix) nor on the workgroup's shape:
+//   total  = ((0 + B_0) + B_1) + ...   B_b the pairwise sum of block b's 64
+//            exponentials (lane = p % 64; lane l adds l ^ 1, then l ^ 2, ...,
+//            l ^ 32: wave_pairwise_sum), zeros past the prefix;
+//   out[d] = ((0 + R_0) + R_1) + ...   R_r the fma chain of run r's 32
+//            probability * value products in position order, from +0.
+// The reordered total moves a probability on an fp16 rounding boundary by one
+// step now and then (head values within a few 1e-5 of RMS of golem's), the
+// reordered value sums by about 1e-7.
+//
+// Loads: the whole extent's key rows (a lane per position: a wavefront reads
+// 1 KiB of a key piece) and the value slice (its VW rows are contiguous: each
+// wavefront load reads a 1 KiB run, staged through LDS) are requested before
+// the token's position (itself a load) is known; positions past the prefix
+// are read and left out of every sum.  With FUSE, wavefront 0 first runs the
+// prologue (head norms, RoPE, the position's cache store) on loads it issues
+// ahead of its share of the cache loads.  Barriers wait for LDS only, so the
+// prologue's stores and the cache loads stay in flight across them.
+// VW: kValSlice (a head's 32-element slice, the long form, extents up to
+// kDecodeMax) or HD (the whole head, one workgroup a query head, extents up
+// to kParShortMax: a quarter of the workgroups, for the lock-step
+// conversations' short prefixes).  ROWS: key rows a cache thread scores.
+constexpr int kParThreads = 1024;
+constexpr int kParBlock = 64;      // positions a block of the softmax total
+constexpr int kParRun = 32;        // positions a run of the value sums
+constexpr int kParShortMax = 128;  // the extents the whole-head form holds
+constexpr int kParMaxRuns = kDecodeMax / kParRun;      // 24
+constexpr int kParMaxBlocks = kDecodeMax / kParBlock;  // 12
 
-template <bool FUSE, int ROWS, int VW = kValSlice>
+template <int VW, bool FUSE>
 struct ParShape {
-    static constexpr int kW0 = FUSE ? 1 : 0;                           // wavefronts out of the cache work
-    static constexpr int kNT = VW == kValSlice ? kDecodeThreads : 64 * kW0 + kShortRuns * VW;  // threads
-    static constexpr int kCT = kNT - 64 * kW0;                         // cache threads
-    static constexpr int kRuns = (kDecodeThreads - 64) / kValSlice;    // position runs of the value sums
-    static constexpr int kRunThr = kCT / VW;                           // runs that have threads
-    static constexpr int kXChunk = ((kDecodeMax + kRuns - 1) / kRuns + 7) & ~7;  // positions a run
-    static constexpr int kPieces = kXChunk / 8;                        // value pieces a thread holds
-    static constexpr int kRows = ROWS;                                 // positions a thread scores
-    static constexpr int kMaxRows = (kDecodeMax + kCT - 1) / kCT;
+    static constexpr int kCap = VW == kValSlice ? kDecodeMax : kParShortMax;  // positions the form holds
+    static constexpr int kStride = kCap + 8;               // halves a staged value row (rows 4 banks apart)
+    static constexpr int kPieces = kCap / 8;               // 16-byte pieces a staged row
+    static constexpr int kVLoads = VW * kPieces / kParThreads;  // value pieces a thread stages
+    static constexpr int kSlots = kParThreads / VW;        // run slots
+    static constexpr int kRunsPer = (kCap / kParRun + kSlots - 1) / kSlots;  // runs a thread sums
+    static constexpr int kW0 = FUSE ? 1 : 0;               // wavefronts out of the cache work
+    static constexpr int kCT = kParThreads - 64 * kW0;     // cache threads
+    static constexpr int kMaxRows = (kCap + kCT - 1) / kCT;  // key rows a cache thread may score
 };
-constexpr int kParProbs = kDecodeMax + 64;  // probabilities in LDS: up to the end of the last run
 
-template <int HD, bool FUSE, int ROWS, int VW = kValSlice>
-__global__ __launch_bounds__((ParShape<FUSE, ROWS, VW>::kNT)) void attn_par_kernel(
+template <int HD, bool FUSE, int ROWS, int VW>
+__global__ __launch_bounds__(kParThreads) void attn_par_kernel(
     const uint16_t *__restrict__ qh, int heads, int kv_heads, const int32_t *__restrict__ positions, int limit,
     const uint16_t *kcache, const uint16_t *vcache, int context, float scale,
     int8_t *__restrict__ q, float *__restrict__ scales, int32_t *__restrict__ qsum,
     const int32_t *__restrict__ slots, int nslots, QkRope fz, float *__restrict__ heads_f) {
-    using Sh = ParShape<FUSE, ROWS, VW>;
-    constexpr int kNT = Sh::kNT;
-    __shared__ __align__(16) uint32_t ql[HD / 2];                // the query, fp16 pairs
-    __shared__ __align__(16) uint16_t nk[HD];                   // FUSE: this position's key
-    __shared__ uint16_t nvl[VW];                                // FUSE: this position's values of the slice
-    static_assert(Sh::kRuns * Sh::kXChunk <= kParProbs && Sh::kRuns * Sh::kXChunk >= kDecodeMax, "runs fit");
-    static_assert(VW != kValSlice || Sh::kMaxRows * Sh::kCT >= kParProbs - 8, "the probability rows are covered");
-    static_assert(ROWS == 1 || ROWS == Sh::kMaxRows, "one row a thread, or as many as kDecodeMax needs");
-    static_assert(VW == kValSlice || (ROWS == 1 && VW == HD && Sh::kRunThr == kShortRuns), "the short form");
-    __shared__ __align__(16) uint16_t ps[kParProbs];            // probabilities, fp16
-    __shared__ float redm[kNT / 64], reds[kNT / 64];
-    __shared__ float vpart[Sh::kRuns][VW + 1];
-    __shared__ __align__(16) float hh[2 * HD];                  // FUSE: the query and key heads, fp32
-    __shared__ __align__(16) double sq[2 * HD];                 // and their squares
+    using Sh = ParShape<VW, FUSE>;
+    constexpr int kCT = Sh::kCT, kCWaves = kCT / 64, kHalf = HD / 2;
+    static_assert(VW * Sh::kPieces % kParThreads == 0 && kParThreads % VW == 0, "whole pieces and run slots");
+    static_assert(Sh::kRunsPer * Sh::kSlots * kParRun >= Sh::kCap, "the runs are covered");
+    static_assert(ROWS == 1 || ROWS == Sh::kMaxRows, "one key row a thread, or as many as the form holds");
+    __shared__ __align__(16) uint32_t ql[HD / 2];                 // the query, fp16 pairs
+    __shared__ __align__(16) uint16_t nk[HD];                    // FUSE: this position's key
+    __shared__ __align__(16) uint16_t nvl[VW];                   // FUSE: this position's values of the slice
+    __shared__ __align__(16) uint16_t vs[VW * Sh::kStride];      // the value slice, fp16
+    __shared__ __align__(16) uint16_t ps[Sh::kCap];              // probabilities, fp16
+    __shared__ float redm[kParThreads / 64];
+    __shared__ float bsum[kParMaxBlocks];
+    __shared__ float vpart[Sh::kCap / kParRun][VW + 1];
+    __shared__ __align__(16) float hh[2 * HD];                   // FUSE: the query and key heads, fp32
+    __shared__ __align__(16) double sq[2 * HD];                  // and their squares
     __shared__ float hs[2];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     constexpr int slices = HD / VW;
@@ -1159,21 +1156,14 @@ __global__ __launch_bounds__((ParShape<FUSE, ROWS, VW>::kNT)) void attn_par_kern
     const int h0 = kvh * group + hl;
     const bool first = hl == 0;  // the query head whose workgroups store the position (FUSE)
     const int t = blockIdx.y;
-    // The loads of the cached keys and values are issued for the whole
-    // extent max_pos + 1 (`limit`), before this token's position is known:
-    // the position is a load of its own (the captured decode step reads it
-    // from the device), and waiting for it would hold every load back by a
-    // memory round trip.  Positions past the token's prefix are read and
-    // left out of every sum.  Wavefront 0 (FUSE) first issues what its
-    // prologue needs -- the Q|K|V row and the norm gains, then, with the
-    // position, the rotation tables -- and its share of the cache loads
-    // after those, so that its prologue waits for its own loads only.
-    const int* pos_src = positions + t;
-    const int32_t* slot_src = slots ? slots + t : nullptr;
-    constexpr int kHalf = HD / 2;
-    // (no initial values: only wavefront 0 sets and reads them, and a value
-    // for the others would make wavefront 0 wait here for its loads)
-    constexpr int kNv = (VW + 63) / 64;  // this position's values a lane
+    if (hl >= group)  // a grid wider than the heads: nothing of this workgroup's exists
+        return;
+    const int *pos_src = positions + t;
+    const int32_t *slot_src = slots ? slots + t : nullptr;
+    // FUSE, wavefront 0: the Q|K|V row's query and key heads, this position's
+    // values of the slice and the norm gains first (no initial values: a
+    // value for the other wavefronts would make wavefront 0 wait here)
+    constexpr int kNv = (VW + 63) / 64;
     float4 hx;
     float nv[kNv], rg0[2], rg1[2], rc[2], rs[2];
     if (FUSE && wave == 0) {
@@ -1195,46 +1185,45 @@ __global__ __launch_bounds__((ParShape<FUSE, ROWS, VW>::kNT)) void attn_par_kern
     // without FUSE the query comes first: one dword a thread
     const uint32_t qr = FUSE ? 0u : ((const uint32_t *)(qh + ((size_t)t * heads + h0) * HD))[min(tid, HD / 2 - 1)];
     // a conversation's own caches: the slot decides the addresses
-    if (slots) {
-        const size_t at = (size_t)min(max(*slot_src, 0), nslots - 1) * kv_heads * HD * context;
-        kcache += at;
-        vcache += at;
-    }
-    v4u_stream k[Sh::kRows][HD / 8];
-    v4u_stream vr[Sh::kPieces];
-    const bool cw = !(FUSE && wave == 0);                 // a cache wavefront
+    size_t at = 0;
+    if (slots)
+        at = (size_t)min(max(*slot_src, 0), nslots - 1) * kv_heads * HD * context;
+    // the key rows of the cache threads' positions ct + kCT r
+    v4u_stream k[ROWS][HD / 8];
+    const bool cw = !(FUSE && wave == 0);                       // a cache wavefront
     const int ct = tid - 64 * Sh::kW0, cwave = wave - Sh::kW0;  // its thread and wavefront among them
-    const int gi = ct / VW, dd = ct % VW;
-    constexpr int xchunk = Sh::kXChunk;                  // positions per value run
-    const bool vrun = cw && gi < Sh::kRuns;              // a thread of a value run
     if (cw) {
-        // key rows: position ct + kCT r, a row only in wavefronts that reach it
-        const v4u_stream *kbase = (const v4u_stream *)(kcache + (size_t)kvh * HD * context);
+        const v4u_stream *kbase = (const v4u_stream *)(kcache + at + (size_t)kvh * HD * context);
 #pragma unroll
-        for (int r = 0; r < Sh::kRows; r++) {
-            if (r == 0 || r * Sh::kCT + cwave * 64 < limit) {
-                const int p = min(ct + r * Sh::kCT, limit - 1);
+        for (int r = 0; r < ROWS; r++) {
+            if (r == 0 || r * kCT + cwave * 64 < limit) {
+                const int p = min(ct + r * kCT, limit - 1);
 #pragma unroll
                 for (int i = 0; i < HD / 8; i++)
                     k[r][i] = kbase[(size_t)i * context + p];
             }
         }
-        // value pieces: run gi of xchunk positions (a multiple of 8), element dd
-        const uint16_t *vrow = vcache + ((size_t)kvh * HD + d0 + dd) * context;
-        if (vrun) {
-#pragma unroll
-            for (int u = 0; u < Sh::kPieces; u++) {
-                const int p0 = min(gi * xchunk + 8 * u, (limit - 1) & ~7);
-                vr[u] = *(const v4u_stream *)(vrow + p0);
-            }
-        }
     }
+    // the value slice: VW contiguous rows, 16-byte pieces of the extent (with
+    // FUSE, wavefront 0 issues its share after the rotation tables: loads
+    // return in order, and the prologue waits for the tables)
+    const uint16_t *vslice = vcache + at + ((size_t)kvh * HD + d0) * context;
+    const int lastp = (limit - 1) >> 3;
+    v4u_stream vr[Sh::kVLoads];
+    auto load_values = [&]() {
+#pragma unroll
+        for (int c = 0; c < Sh::kVLoads; c++) {
+            const int j = tid + kParThreads * c, row = j / Sh::kPieces, col = j - row * Sh::kPieces;
+            vr[c] = *(const v4u_stream *)(vslice + (size_t)row * context + 8 * min(col, lastp));
+        }
+    };
+    if (cw)
+        load_values();
     const int pos = *pos_src;
     const int n = min(max(pos, 0) + 1, limit);
     const int rpos = min(max(pos, 0), context - 1);  // outside the cache: the tables' last row, nothing stored
     bool store = pos >= 0 && pos < context;
     if (FUSE && slots) {
-        const size_t at = (size_t)min(max(*slot_src, 0), nslots - 1) * kv_heads * HD * context;
         store = store && *slot_src >= 0 && *slot_src < nslots;
         fz.kcache += at;
         fz.vcache += at;
@@ -1247,6 +1236,7 @@ __global__ __launch_bounds__((ParShape<FUSE, ROWS, VW>::kNT)) void attn_par_kern
             rc[r] = fz.rope_cos[(size_t)rpos * kHalf + j];
             rs[r] = fz.rope_sin[(size_t)rpos * kHalf + j];
         }
+        load_values();
     }
     if (FUSE) {
         if (wave == 0) {
@@ -1319,23 +1309,24 @@ __global__ __launch_bounds__((ParShape<FUSE, ROWS, VW>::kNT)) void attn_par_kern
     lds_barrier();
     if (FUSE && pos == n - 1 && cw) {  // this position's key from the copy, not the cache entry being written
 #pragma unroll
-        for (int r = 0; r < Sh::kRows; r++)
-            if (ct + r * Sh::kCT == pos) {
+        for (int r = 0; r < ROWS; r++)
+            if (ct + r * kCT == pos) {
 #pragma unroll
                 for (int i = 0; i < HD / 8; i++)
                     k[r][i] = ((const v4u_stream *)nk)[i];
             }
     }
 
-    // scores (DotF32's four chains, as the serial kernel) and their maximum
-    float s[Sh::kRows];
+    // scores (DotF32's four chains: element e of the head goes to chain e % 4)
+    // and their maximum
+    float s[ROWS];
     float mx = -INFINITY;
 #pragma unroll
-    for (int r = 0; r < Sh::kRows; r++) {
+    for (int r = 0; r < ROWS; r++) {
         s[r] = -INFINITY;
-        if (!cw || r * Sh::kCT + cwave * 64 >= n)
+        if (!cw || r * kCT + cwave * 64 >= n)
             continue;
-        const int p = ct + r * Sh::kCT;
+        const int p = ct + r * kCT;
         const v4u_stream *qv = (const v4u_stream *)ql;
         float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
 #pragma unroll
@@ -1356,73 +1347,86 @@ __global__ __launch_bounds__((ParShape<FUSE, ROWS, VW>::kNT)) void attn_par_kern
             mx = fmaxf(mx, v);
         }
     }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1)
-        mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    mx = wave_max(mx);
     if (lane == 0)
         redm[wave] = mx;
     lds_barrier();
     float m = redm[0];
 #pragma unroll
-    for (int w = 1; w < kNT / 64; w++)
+    for (int w = 1; w < kParThreads / 64; w++)
         m = fmaxf(m, redm[w]);
-    // exponentials (float64 exp, as SoftmaxInPlace), and their total as a tree
-    float e[Sh::kRows];
-    float tsum = 0.0f;
+    // exponentials (float64 exp, as SoftmaxInPlace); each 64-position block's
+    // pairwise sum (a cache wavefront's lanes are one block's positions)
+    float e[ROWS];
 #pragma unroll
-    for (int r = 0; r < Sh::kRows; r++) {
-        e[r] = cw && ct + r * Sh::kCT < n ? (float)exp((double)(s[r] - m)) : 0.0f;
-        tsum = tsum + e[r];
-    }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1)
-        tsum = tsum + __shfl_xor(tsum, off, 64);
-    if (lane == 0)
-        reds[wave] = tsum;
-    lds_barrier();
-    float total = 0.0f;
-#pragma unroll
-    for (int w = 0; w < kNT / 64; w++)
-        total = total + reds[w];
-    // probabilities, rounded through fp16; zeros past the prefix to the end
-    // of the last run
-    if (cw) {
-#pragma unroll
-        for (int r = 0; r < Sh::kRows; r++) {
-            const int p = ct + r * Sh::kCT;
-            if (p < n)
-                ps[p] = (uint16_t)float_to_half_bits(__fdiv_rn(e[r], total));
-            else if (p < Sh::kRuns * xchunk)
-                ps[p] = 0;
+    for (int r = 0; r < ROWS; r++) {
+        e[r] = cw && ct + r * kCT < n ? (float)exp((double)(s[r] - m)) : 0.0f;
+        if (cw && r * kCT + cwave * 64 < n) {
+            const float b = wave_pairwise_sum(e[r]);
+            if (lane == 0)
+                bsum[cwave + kCWaves * r] = b;
         }
     }
     lds_barrier();
-
-    // the value element's run of positions, then the runs in group order
-    float acc = 0.0f;
+    // the total, blocks in order; the probabilities, rounded through fp16,
+    // zeros past the prefix to the end of the last run
+    const int nblocks = (n + kParBlock - 1) / kParBlock, nruns = (n + kParRun - 1) / kParRun;
+    float total = 0.0f;
+    for (int b = 0; b < nblocks; b++)
+        total = total + bsum[b];
+    if (cw) {
 #pragma unroll
-    for (int u = 0; u < Sh::kPieces; u++) {
-        const int p0 = gi * xchunk + 8 * u;
-        if (vrun && p0 < n) {
-            const v4u_stream pp = *(const v4u_stream *)(ps + p0);
-            v4u_stream vv = vr[u];
-            if (FUSE && pos >= p0 && pos < p0 + 8) {  // this position's value from the copy
-                const int e8 = pos - p0;
-                uint32_t wd[4] = {vv.x, vv.y, vv.z, vv.w};
-                const uint32_t nb = nvl[dd];
+        for (int r = 0; r < ROWS; r++) {
+            const int p = ct + r * kCT;
+            if (p < n)
+                ps[p] = (uint16_t)float_to_half_bits(__fdiv_rn(e[r], total));
+            else if (p < nruns * kParRun)
+                ps[p] = 0;
+        }
+    }
+    // the value slice into LDS (with FUSE this position's values from the
+    // copy, not the cache entries being written)
 #pragma unroll
-                for (int c = 0; c < 4; c++) {
-                    if (e8 == 2 * c)
-                        wd[c] = (wd[c] & 0xFFFF0000u) | nb;
-                    if (e8 == 2 * c + 1)
-                        wd[c] = (wd[c] & 0x0000FFFFu) | (nb << 16);
-                }
-                vv.x = wd[0];
-                vv.y = wd[1];
-                vv.z = wd[2];
-                vv.w = wd[3];
+    for (int c = 0; c < Sh::kVLoads; c++) {
+        const int j = tid + kParThreads * c, row = j / Sh::kPieces, col = j - row * Sh::kPieces;
+        v4u_stream vv = vr[c];
+        if (FUSE && pos == n - 1 && col == (pos >> 3)) {
+            const int e8 = pos & 7;
+            uint32_t wd[4] = {vv.x, vv.y, vv.z, vv.w};
+            const uint32_t nb = nvl[row];
+#pragma unroll
+            for (int h = 0; h < 4; h++) {
+                if (e8 == 2 * h)
+                    wd[h] = (wd[h] & 0xFFFF0000u) | nb;
+                if (e8 == 2 * h + 1)
+                    wd[h] = (wd[h] & 0x0000FFFFu) | (nb << 16);
             }
-            if (p0 + 8 <= n) {
+            vv.x = wd[0];
+            vv.y = wd[1];
+            vv.z = wd[2];
+            vv.w = wd[3];
+        }
+        *(v4u_stream *)(&vs[row * Sh::kStride + 8 * col]) = vv;
+    }
+    lds_barrier();
+
+    // the runs' fma chains: whole 8-position pieces, then the piece the prefix
+    // ends in, position by position (nothing past the prefix is read)
+    const int dd = tid % VW, js = tid / VW;  // the thread's element and run slot
+#pragma unroll
+    for (int i = 0; i < Sh::kRunsPer; i++) {
+        const int r = js + Sh::kSlots * i;
+        if (r >= nruns)
+            break;
+        const int whole = min((n - r * kParRun) >> 3, kParRun / 8);
+        const uint16_t *vrow = vs + dd * Sh::kStride + r * kParRun;
+        const uint16_t *prow = ps + r * kParRun;
+        float acc = 0.0f;
+#pragma unroll
+        for (int u = 0; u < kParRun / 8; u++) {
+            if (u < whole) {
+                const v4u_stream vv = *(const v4u_stream *)(vrow + 8 * u);
+                const v4u_stream pp = *(const v4u_stream *)(prow + 8 * u);
                 acc = fma_mix_lo(pp.x, vv.x, acc);
                 acc = fma_mix_hi(pp.x, vv.x, acc);
                 acc = fma_mix_lo(pp.y, vv.y, acc);
@@ -1431,25 +1435,24 @@ __global__ __launch_bounds__((ParShape<FUSE, ROWS, VW>::kNT)) void attn_par_kern
                 acc = fma_mix_hi(pp.z, vv.z, acc);
                 acc = fma_mix_lo(pp.w, vv.w, acc);
                 acc = fma_mix_hi(pp.w, vv.w, acc);
-            } else {  // the prefix ends inside this piece: nothing past it is read
-                const uint32_t pw[4] = {pp.x, pp.y, pp.z, pp.w}, vw[4] = {vv.x, vv.y, vv.z, vv.w};
-#pragma unroll
-                for (int c = 0; c < 8; c++)
-                    if (p0 + c < n)
-                        acc = (c & 1) ? fma_mix_hi(pw[c >> 1], vw[c >> 1], acc) : fma_mix_lo(pw[c >> 1], vw[c >> 1], acc);
             }
         }
+        const int p0 = r * kParRun + 8 * whole;
+        if (whole < kParRun / 8 && p0 < n) {
+            const v4u_stream vv = *(const v4u_stream *)(vrow + 8 * whole);
+            const v4u_stream pp = *(const v4u_stream *)(prow + 8 * whole);
+            const uint32_t vw[4] = {vv.x, vv.y, vv.z, vv.w}, pw[4] = {pp.x, pp.y, pp.z, pp.w};
+            for (int c = 0; c < n - p0; c++)
+                acc = (c & 1) ? fma_mix_hi(pw[c >> 1], vw[c >> 1], acc) : fma_mix_lo(pw[c >> 1], vw[c >> 1], acc);
+        }
+        vpart[r][dd] = acc;
     }
-    if (vrun)
-        vpart[gi][dd] = acc;
     lds_barrier();
+    // runs in order, then the slice's Q8_0 blocks (a 32-lane group a block)
     if (tid < VW) {
         float o = 0.0f;
-#pragma unroll
-        for (int g = 0; g < Sh::kRunThr && g < Sh::kRuns; g++)
-            o = o + vpart[g][tid];
-        if (Sh::kRunThr < Sh::kRuns)  // the empty runs' +0 sums
-            o = o + 0.0f;
+        for (int r = 0; r < nruns; r++)
+            o = o + vpart[r][tid];
         float stored;
         int32_t sm;
         const int32_t nq = q8_0_lane(o, &stored, &sm);
@@ -1459,7 +1462,7 @@ __global__ __launch_bounds__((ParShape<FUSE, ROWS, VW>::kNT)) void attn_par_kern
             heads_f[(size_t)t * width + col] = o;
         if (q) {
             q[(size_t)t * width + col] = (int8_t)nq;
-            if ((tid & 31) == 0) {  // a Q8_0 block a 32-lane group
+            if ((tid & 31) == 0) {
                 scales[(size_t)t * B + (col >> 5)] = stored;
                 qsum[(size_t)t * B + (col >> 5)] = sm;
             }
@@ -1607,6 +1610,42 @@ __global__ __launch_bounds__(64) void argmax_final_kernel(const float *__restric
     }
 }
 
+// The parallel-order decode attention (attn_par_kernel): the whole-head form
+// (VW = HD, a workgroup a query head) for extents of at most kParShortMax
+// positions with whole-wavefront head widths, else 32-element slices; one key
+// row a cache thread when the extent fits the cache threads (half the key
+// registers), else as many as kDecodeMax needs.
+template <bool FUSE>
+int launch_par(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int kv_heads, int hd, int limit,
+               const int32_t *positions, const uint16_t *kcache, const uint16_t *vcache, int context, float scale,
+               int8_t *q, float *scales, int32_t *qsum, const int32_t *slots, int nslots, const QkRope &fz,
+               float *heads_f) {
+#define GX_PAR(HH, RR, VV)                                                                                           \
+    attn_par_kernel<HH, FUSE, RR, VV><<<dim3((unsigned)(heads * (HH / VV)), (unsigned)M), kParThreads, 0,            \
+                                        ctx->stream>>>(qh, heads, kv_heads, positions, limit, kcache, vcache,       \
+                                                       context, scale, q, scales, qsum, slots, nslots, fz, heads_f)
+#define GX_PAR_R(HH, SHORT)                                                                                          \
+    do {                                                                                                             \
+        if (SHORT && limit <= kParShortMax)                                                                          \
+            GX_PAR(HH, 1, (SHORT ? HH : kValSlice));                                                                 \
+        else if (limit <= ParShape<kValSlice, FUSE>::kCT)                                                            \
+            GX_PAR(HH, 1, kValSlice);                                                                                \
+        else                                                                                                         \
+            GX_PAR(HH, (ParShape<kValSlice, FUSE>::kMaxRows), kValSlice);                                            \
+    } while (0)
+    if (hd == 32)
+        GX_PAR_R(32, false);
+    else if (hd == 64)
+        GX_PAR_R(64, true);
+    else if (hd == 96)
+        GX_PAR_R(96, false);
+    else
+        GX_PAR_R(128, true);
+#undef GX_PAR_R
+#undef GX_PAR
+    return check_launch("qwen_attention parallel");
+}
+
 }  // namespace
 
 int launch_qwen_norm_quant(gx_ctx *ctx, float *x, int ldx, const float *add, int lda, const float *gain, int M, int K,
@@ -1653,33 +1692,9 @@ int launch_qwen_attention(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int
 
     // One workgroup per token: a few tokens of one conversation, or tokens of
     // several conversations (slots), whose caches share nothing.
-    if (parallel && (M <= 4 || slots) && limit <= kDecodeMax) {
-#define GX_PAR(HH, RR, VV)                                                                                           \
-    attn_par_kernel<HH, false, RR, VV><<<dim3((unsigned)(heads * (HH / VV)), (unsigned)M),                          \
-                                         ParShape<false, RR, VV>::kNT, 0, ctx->stream>>>(                           \
-        qh, heads, kv_heads, positions, limit, kcache, vcache, context, scale, q, scales, qsum, slots, nslots,      \
-        QkRope{}, heads_f)
-#define GX_PAR_R(HH)                                                                                                 \
-    do {                                                                                                             \
-        if (HH > kValSlice && limit <= kShortRuns * ParShape<false, 1>::kXChunk)                                     \
-            GX_PAR(HH, 1, HH);                                                                                       \
-        else if (limit <= ParShape<false, 1>::kCT)                                                                   \
-            GX_PAR(HH, 1, kValSlice);                                                                                \
-        else                                                                                                         \
-            GX_PAR(HH, (ParShape<false, 1>::kMaxRows), kValSlice);                                                   \
-    } while (0)
-        if (hd == 32)
-            GX_PAR_R(32);
-        else if (hd == 64)
-            GX_PAR_R(64);
-        else if (hd == 96)
-            GX_PAR_R(96);
-        else
-            GX_PAR_R(128);
-#undef GX_PAR_R
-#undef GX_PAR
-        return check_launch("qwen_attention parallel");
-    }
+    if (parallel && (M <= 4 || slots) && limit <= kDecodeMax)
+        return launch_par<false>(ctx, qh, M, heads, kv_heads, hd, limit, positions, kcache, vcache, context, scale,
+                                 q, scales, qsum, slots, nslots, QkRope{}, heads_f);
     if ((M <= 4 || slots) && limit <= kDecodeMax) {
 // One query head per workgroup when that fills at most two workgroups per CU
 // (128 workgroups for config 3's decode rather than 32): the scores,
@@ -1803,36 +1818,9 @@ int launch_qwen_rope_attention(gx_ctx *ctx, const float *qkv, int ldqkv, int M, 
     const int limit = max_pos + 1;
     GX_CHECK(limit <= kDecodeMax, "gx: the fused attention reads at most %d positions, not %d", kDecodeMax, limit);
     const QkRope fz{qkv, ldqkv, q_norm, k_norm, rope_cos, rope_sin, eps, kcache, vcache};
-    if (parallel) {
-#define GX_PAR(HH, RR, VV)                                                                                           \
-    attn_par_kernel<HH, true, RR, VV><<<dim3((unsigned)(heads * (HH / VV)), (unsigned)M),                           \
-                                        ParShape<true, RR, VV>::kNT, 0, ctx->stream>>>(                             \
-        nullptr, heads, kv_heads, positions, limit, kcache, vcache, context, scale, q, scales, qsum, slots, nslots, \
-        fz, nullptr)
-// Extents of at most two value runs (112 positions): one workgroup a query
-// head, the whole head's values (a quarter of the workgroups; eight
-// conversations at config 3's shape fit the CUs in one round).
-#define GX_PAR_R(HH)                                                                                                 \
-    do {                                                                                                             \
-        if (HH > kValSlice && limit <= kShortRuns * ParShape<true, 1>::kXChunk)                                      \
-            GX_PAR(HH, 1, HH);                                                                                       \
-        else if (limit <= ParShape<true, 1>::kCT)                                                                    \
-            GX_PAR(HH, 1, kValSlice);                                                                                \
-        else                                                                                                         \
-            GX_PAR(HH, (ParShape<true, 1>::kMaxRows), kValSlice);                                                    \
-    } while (0)
-        if (hd == 32)
-            GX_PAR_R(32);
-        else if (hd == 64)
-            GX_PAR_R(64);
-        else if (hd == 96)
-            GX_PAR_R(96);
-        else
-            GX_PAR_R(128);
-#undef GX_PAR_R
-#undef GX_PAR
-        return check_launch("qwen_rope_attention parallel");
-    }
+    if (parallel)
+        return launch_par<true>(ctx, nullptr, M, heads, kv_heads, hd, limit, positions, kcache, vcache, context,
+                                scale, q, scales, qsum, slots, nslots, fz, nullptr);
 #define GX_FUSED(HH)                                                                                                 \
     attn_decode_kernel<HH, 1, true><<<dim3((unsigned)(heads * (HH / kValSlice)), (unsigned)M), kDecodeThreads, 0,             \
                                       ctx->stream>>>(nullptr, heads, kv_heads, positions, limit, kcache, vcache,     \

@@ -61,6 +61,7 @@ def load():
         "orc_rope_prepare": (None, [I, I, ctypes.c_double, V, V]),
         "orc_rope_apply": (None, [V, I, V, V]),
         "orc_attend": (None, [V, V, V, I, I, I, I, F, V, V]),
+        "orc_attend_parallel": (None, [V, V, V, I, I, I, I, F, V, V]),
         "orc_matrix_rows": (I, [I, V, V, I, I, V, I, V, V, V, V, V, V, V, I, I, V, I, I, I]),
         "orc_rms_norm_plain": (None, [V, I, V, F]),
         "orc_gelu_table_build": (None, [V]),

@@ -738,6 +738,58 @@ void orc_attend(const float *query, const float *K, const float *V, int kvheads,
         orc_axpy(dst, V + ((size_t)p * kvheads + kv) * hd, hd, scores[p]);
 }
 
+/* The decode attention in this build's parallel order -- NOT golem's: the
+ * device's default decode attention (golem_amd/csrc/gx_qwen.hip,
+ * attn_par_kernel), restated so that the kernel can be checked bit for bit;
+ * golem's own order is orc_attend.
+ * golem's scores, maximum, float64 exponentials, division and fp16 rounding
+ * of each probability (qwen/attention.go:96-114, nn/ops.go:59-73), with the
+ * two sums taken in a fixed parallel order:
+ *   total  = ((0 + B_0) + B_1) + ... over blocks of 64 positions, B_b the
+ *            pairwise sum of the block's exponentials (zeros past n): lane
+ *            l = p % 64 holds e_p, then every lane adds lane l ^ 1's value,
+ *            then l ^ 2's, ..., then l ^ 32's; B_b is lane 0's result;
+ *   dst[d] = ((0 + R_0) + R_1) + ... over runs of 32 positions, R_r the
+ *            chain acc = fma(prob_p, value_p[d], acc) from 0 over the run's
+ *            positions below n in order.
+ * The maximum ignores NaN scores as fmaxf does.  scores holds n floats and
+ * is left holding the fp16-rounded probabilities. */
+void orc_attend_parallel(const float *query, const float *K, const float *V, int kvheads, int hd, int kv, int n,
+                      float scale, float *scores, float *dst)
+{
+    float m = -INFINITY;
+    for (int p = 0; p < n; p++) {
+        scores[p] = scale * orc_dot_f32(query, K + ((size_t)p * kvheads + kv) * hd, hd);
+        m = fmaxf(m, scores[p]);
+    }
+    for (int p = 0; p < n; p++)
+        scores[p] = (float)exp((double)(scores[p] - m));
+    float total = 0;
+    for (int b = 0; b * 64 < n; b++) {
+        float lanes[64], next[64];
+        for (int l = 0; l < 64; l++)
+            lanes[l] = b * 64 + l < n ? scores[b * 64 + l] : 0.0f;
+        for (int off = 1; off < 64; off <<= 1) {
+            for (int l = 0; l < 64; l++)
+                next[l] = lanes[l] + lanes[l ^ off];
+            memcpy(lanes, next, sizeof(lanes));
+        }
+        total = total + lanes[0];
+    }
+    for (int p = 0; p < n; p++)
+        scores[p] = orc_round_half(scores[p] / total);
+    for (int d = 0; d < hd; d++) {
+        float o = 0;
+        for (int r = 0; r * 32 < n; r++) {
+            float acc = 0;
+            for (int p = r * 32; p < r * 32 + 32 && p < n; p++)
+                acc = fmaf(scores[p], V[((size_t)p * kvheads + kv) * hd + d], acc);
+            o = o + acc;
+        }
+        dst[d] = o;
+    }
+}
+
 /* ---- mixture of experts ------------------------------------------------- */
 
 /* chooseExperts, gemma/moe.go:62-88: repeated argmax (strict >, ties to the

@@ -281,7 +281,9 @@ def test_attention_parallel_against_golem(dev, orc, hd, heads, kv, ctx_len, batc
     qwen/attention.go:96-124): every head's output floats within 1e-4 of RMS
     (gx_qwen_attention_heads), and the Q8_0 of the heads
     (gx_qwen_attention_parallel) equal to golem's but for values on a
-    rounding boundary, which move one step.  Prefixes of 1 to 768 positions,
+    rounding boundary, which move one step.  Against the oracle's
+    restatement of the parallel order (orc_attend_parallel) the head floats and
+    their Q8_0 are bit for bit.  Prefixes of 1 to 768 positions,
     including those that end inside a 16-byte piece and at a run's edge.
     Why 1e-4 and not the products' 1e-5: golem rounds every probability to
     fp16 (attention.go:112-114), so when the softmax total, summed in another
@@ -334,6 +336,19 @@ def test_attention_parallel_against_golem(dev, orc, hd, heads, kv, ctx_len, batc
             rel, at = orc.compare_floats(got[t, h * hd:(h + 1) * hd], out[t, h * hd:(h + 1) * hd])
             worst = max(worst, rel)
             assert rel <= 1e-4, f"position {pos[t]} head {h}: {rel:.3g} of RMS at {at}"
+    # bit for bit against the oracle's restatement of the parallel order itself
+    par = np.zeros_like(out)
+    for t in range(M):
+        for h in range(heads):
+            query = np.ascontiguousarray(qf[t, h * hd:(h + 1) * hd].astype(np.float32))
+            dst = np.zeros(hd, np.float32)
+            lib.orc_attend_parallel(orc._p(query), orc._p(K32), orc._p(V32), kv, hd, h // (heads // kv),
+                                 int(pos[t]) + 1, scale, orc._p(scores), orc._p(dst))
+            par[t, h * hd:(h + 1) * hd] = dst
+    np.testing.assert_array_equal(got.view(np.uint32), par.view(np.uint32))
+    bs = orc.Batch(par).quantize()
+    np.testing.assert_array_equal(dev.get(q8), bs.q_rows())
+    np.testing.assert_array_equal(dev.get(sc).view(np.uint32), bs.scales_rows().view(np.uint32))
     b = orc.Batch(out).quantize()
     dq = dev.get(q8).astype(np.int32) - b.q_rows().astype(np.int32)
     moved = int(np.count_nonzero(dq))

@@ -160,17 +160,21 @@ def test_rope_attention_slots_equal_one_at_a_time(dev, hd, heads, kv, context, M
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("hd,heads,kv", [(128, 32, 8), (64, 8, 2), (96, 4, 4)])
-def test_parallel_short_extent_form_equals_long(dev, hd, heads, kv):
-    """Extents of at most two value runs (112 positions) take the parallel
-    kernel's short form (one workgroup a query head); the same token through
-    the long form (an extent past 112, one key row a thread, and past 448,
-    several) gives the same bits: the value runs, the softmax tree and the
-    run order are the same in both."""
+@pytest.mark.parametrize("hd,heads,kv", [(128, 32, 8), (64, 8, 2), (96, 4, 4), (32, 8, 1)])
+def test_parallel_extent_independent(dev, hd, heads, kv):
+    """The parallel order does not depend on the launch's extent: a token
+    launched for its own prefix (max_pos = its position) and for longer
+    extents (as a captured decode step, launched for the whole cache, runs
+    it) gives the same bits -- the 64-position blocks of the softmax total
+    and the 32-position runs of the value sums are fixed, whichever form
+    (one key row a thread or two; a 32-element value slice or the whole head
+    a workgroup, below 129 positions) the launch takes."""
     context = 640
-    for pos in (0, 50, 55, 56, 111):
-        short = run_case(dev, hd, heads, kv, context, pos, max(pos, 111), parallel=True)
-        for max_pos in (300, context - 1):
-            long = run_case(dev, hd, heads, kv, context, pos, max_pos, parallel=True)
-            for name, a, b in zip(("q", "scales", "sums", "key cache", "value cache"), short[:5], long[:5]):
+    for pos in (0, 31, 32, 63, 64, 111, 300, 511):
+        own = run_case(dev, hd, heads, kv, context, pos, pos, parallel=True)
+        for max_pos in sorted({min(pos + 33, context - 1), 400, context - 1} - {pos}):
+            if max_pos < pos:
+                continue
+            other = run_case(dev, hd, heads, kv, context, pos, max_pos, parallel=True)
+            for name, a, b in zip(("q", "scales", "sums", "key cache", "value cache"), own[:5], other[:5]):
                 assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), f"{name}: pos {pos} max_pos {max_pos}"

@@ -99,3 +99,63 @@ def test_oracle_moe_half_adds_both_branches():
         assert len(set(ids[t].tolist())) == cfg.used
         want = resid[t] + oracle.rms_norm_plain(shared[t] + experts[t], w["post_ffw_norm"], cfg.eps)
         np.testing.assert_array_equal(out[t].view(np.uint32), want.astype(np.float32).view(np.uint32))
+
+
+def _parallel(lib, q, K, V, kv, hd, n, scale):
+    scores = np.zeros(max(n, 1), np.float32)
+    dst = np.zeros(hd, np.float32)
+    lib.orc_attend_parallel(oracle._p(q), oracle._p(K), oracle._p(V), K.shape[1], hd, kv, n, scale,
+                         oracle._p(scores), oracle._p(dst))
+    return dst, scores
+
+
+def test_parallel_order_attention_closed_forms():
+    """orc_attend_parallel (the decode attention's parallel order, this build's,
+    not golem's): one position gives its value exactly; n identical keys give
+    every position probability fp16(1/n) and the values' average; a total of
+    exactly representable exponentials (all scores equal) is n whatever the
+    order."""
+    lib = oracle.load()
+    hd, kv = 64, 2
+    g = synth.rng(30)
+    n = 200
+    K = g.standard_normal((n, kv, hd)).astype(np.float16).astype(np.float32)
+    V = g.standard_normal((n, kv, hd)).astype(np.float16).astype(np.float32)
+    q = g.standard_normal(hd).astype(np.float16).astype(np.float32)
+    dst, _ = _parallel(lib, q, K, V, 1, hd, 1, np.float32(0.125))
+    np.testing.assert_array_equal(dst, V[0, 1])
+    K[:, 0] = K[0, 0]  # every key of head 0 equal: probabilities fp16(1/n)
+    dst, probs = _parallel(lib, q, K, V, 0, hd, n, np.float32(0.125))
+    p = np.float32(np.float16(np.float32(1) / np.float32(n)))
+    assert np.all(probs[:n] == p)
+    want = np.float64(p) * V[:n, 0].astype(np.float64).sum(axis=0)
+    np.testing.assert_allclose(dst, want, rtol=0, atol=1e-5)
+
+
+def test_parallel_order_attention_near_golem():
+    """The parallel order against golem's serial order (orc_attend) and a
+    float64 evaluation: its head values within 1e-4 of RMS of golem's and of
+    the exact softmax-weighted sum of the fp16-rounded probabilities -- a
+    dropped run, a block summed twice, a probability of the wrong position or
+    a value of the wrong element fails by far more."""
+    lib = oracle.load()
+    g = synth.rng(31)
+    for hd, kv, n in ((128, 8, 640), (64, 2, 97), (32, 1, 33), (128, 4, 513)):
+        K = g.standard_normal((n, kv, hd)).astype(np.float16).astype(np.float32)
+        V = (g.standard_normal((n, kv, hd)) * 2).astype(np.float16).astype(np.float32)
+        q = (g.standard_normal(hd) * 1.5).astype(np.float16).astype(np.float32)
+        scale = np.float32(1 / math.sqrt(hd))
+        h = kv - 1
+        got, probs = _parallel(lib, q, K, V, h, hd, n, scale)
+        scores = np.zeros(n, np.float32)
+        serial = np.zeros(hd, np.float32)
+        lib.orc_attend(oracle._p(q), oracle._p(K), oracle._p(V), kv, hd, h, n, scale, oracle._p(scores),
+                       oracle._p(serial))
+        rel, _ = oracle.compare_floats(got, serial)
+        assert rel <= 1e-4, (hd, n, rel)
+        s = (K[:, h].astype(np.float64) @ q.astype(np.float64)) * float(scale)
+        e = np.exp(s - s.max())
+        np.testing.assert_allclose(probs[:n], np.float16(e / e.sum()).astype(np.float32), rtol=2e-3, atol=1e-7)
+        exact = probs[:n].astype(np.float64) @ V[:, h].astype(np.float64)
+        rel, _ = oracle.compare_floats(got, exact.astype(np.float32))
+        assert rel <= 1e-5, (hd, n, rel)
