@@ -415,6 +415,66 @@ __device__ __forceinline__ double block_sum_squares(const float *xs, int K, doub
 }
 
 
+// The minimum of an integer over a wavefront, in every lane.
+__device__ __forceinline__ int32_t wave_min_i32(int32_t v) {
+    v = min(v, dpp_i32<0xB1>(v));
+    v = min(v, dpp_i32<0x4E>(v));
+    v = min(v, dpp_i32<0x141>(v));
+    v = min(v, dpp_i32<0x140>(v));
+    const int32_t r0 = __builtin_amdgcn_readlane(v, 0), r1 = __builtin_amdgcn_readlane(v, 16);
+    const int32_t r2 = __builtin_amdgcn_readlane(v, 32), r3 = __builtin_amdgcn_readlane(v, 48);
+    return min(min(r0, r1), min(r2, r3));
+}
+
+// Batch.QuantizeK of one 256-element superblock by one wavefront
+// (nn/batch.go:159-213), lane l holding elements 4l .. 4l+3: extreme = the
+// signed value of the first element of largest magnitude, inverse =
+// -128 / extreme, q = min(127, nearestInt(x * inverse)), kscale =
+// 1 / inverse; a superblock of zeros gives zeros.  Returns the lane's four q
+// packed in a dword; *gsum receives the sum of its 16-element group in every
+// lane of the group's quad (lanes 4g .. 4g+3), *kscale the superblock's
+// scale (every lane).  NaNs never win the magnitude comparison, as in
+// golem's loop.
+__device__ __forceinline__ uint32_t q8_k_wave(const float v[4], int lane, int32_t *gsum, float *kscale) {
+    float peak = 0.0f;
+    int at = 256;  // the lane's first element of its largest magnitude
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float a = fabsf(v[i]);
+        if (a > peak) {
+            peak = a;
+            at = 4 * lane + i;
+        }
+    }
+    const float top = wave_max(peak);
+    if (top == 0.0f) {
+        *gsum = 0;
+        *kscale = 0.0f;
+        return 0u;
+    }
+    // the lowest index of the largest magnitude: every lane's own first
+    // occurrence, the lowest of those that reach the wavefront's maximum
+    const int first = wave_min_i32(peak == top ? at : 256);
+    const float mine = (first & 3) == 0 ? v[0] : (first & 3) == 1 ? v[1] : (first & 3) == 2 ? v[2] : v[3];
+    const float extreme = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), first >> 2));
+    const float inverse = __fdiv_rn(-128.0f, extreme);
+    uint32_t packed = 0;
+    int32_t sum = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float prod = v[i] * inverse;
+        int32_t n = nearest_int(prod);
+        n = n > 127 ? 127 : n;
+        packed |= ((uint32_t)(uint8_t)(int8_t)n) << (8 * i);
+        sum += n;
+    }
+    sum += dpp_i32<0xB1>(sum);
+    sum += dpp_i32<0x4E>(sum);
+    *gsum = sum;
+    *kscale = __fdiv_rn(1.0f, inverse);
+    return packed;
+}
+
 // Q8_0 of one element per lane of a 32-lane group (Batch.quantizeBlock,
 // nn/batch.go:109-143): returns q; the group's fp16-rounded scale and sum of
 // q come back in *stored and *sum (valid in every lane).

@@ -84,56 +84,14 @@ __global__ __launch_bounds__(256) void quantize_q8_k_kernel(const float *__restr
     const int m = (int)(sb / nsb), b = (int)(sb % nsb);
     const float4 v4 = *(const float4 *)(x + (size_t)m * ldx + (size_t)b * kSuper + 4 * lane);
     const float v[4] = {v4.x, v4.y, v4.z, v4.w};
-    // The first element of strictly largest magnitude, as golem's loop finds
-    // it: a larger magnitude wins, an equal one keeps the lower index.
-    float peak = 0.0f;
-    int at = -1;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const float a = fabsf(v[i]);
-        if (a > peak) {
-            peak = a;
-            at = 4 * lane + i;
-        }
-    }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        const float op = __shfl_xor(peak, off, 64);
-        const int oa = __shfl_xor(at, off, 64);
-        if (op > peak || (op == peak && oa >= 0 && (at < 0 || oa < at))) {
-            peak = op;
-            at = oa;
-        }
-    }
-    int8_t *qo = q + (size_t)m * K + (size_t)b * kSuper;
-    int16_t *so = bsums + (size_t)m * (K / 16) + (size_t)b * 16;
-    if (peak == 0.0f) {
-        *(uint32_t *)(qo + 4 * lane) = 0u;
-        if (lane == 0)
-            kscales[(size_t)m * nsb + b] = 0.0f;
-        if ((lane & 3) == 0)
-            so[lane >> 2] = 0;
-        return;
-    }
-    const float extreme = x[(size_t)m * ldx + (size_t)b * kSuper + at];
-    const float inverse = __fdiv_rn(-128.0f, extreme);
-    uint32_t packed = 0;
-    int32_t sum = 0;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const float prod = v[i] * inverse;
-        int32_t n = nearest_int(prod);
-        n = n > 127 ? 127 : n;
-        packed |= ((uint32_t)(uint8_t)(int8_t)n) << (8 * i);
-        sum += n;
-    }
-    *(uint32_t *)(qo + 4 * lane) = packed;
-    sum += __shfl_xor(sum, 1, 64);
-    sum += __shfl_xor(sum, 2, 64);
+    int32_t gsum;
+    float ks;
+    const uint32_t packed = q8_k_wave(v, lane, &gsum, &ks);
+    *(uint32_t *)(q + (size_t)m * K + (size_t)b * kSuper + 4 * lane) = packed;
     if ((lane & 3) == 0)
-        so[lane >> 2] = (int16_t)sum;
+        bsums[(size_t)m * (K / 16) + (size_t)b * 16 + (lane >> 2)] = (int16_t)gsum;
     if (lane == 0)
-        kscales[(size_t)m * nsb + b] = __fdiv_rn(1.0f, inverse);
+        kscales[(size_t)m * nsb + b] = ks;
 }
 
 }  // namespace
