@@ -45,7 +45,7 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-extra", action="store_true", help="skip the config 0 / config 2 measurements")
     p.add_argument("--only", default="",
-                   help="profiling: run only this leg (c1, c0, c2, c3, c4) and exit; 'copy' runs the 256 MiB "
+                   help="profiling: run only this leg (c1, c0, c0floor, c2, c3, c3prefill, c4, valu) and exit; 'copy' runs the 256 MiB "
                         "device copy that scales the FETCH_SIZE / WRITE_SIZE counters; 'c3prefill' reads "
                         "config 3's 512-token prompt four times (a kernel trace of the prefill alone)")
     p.add_argument("--c2-m", type=int, default=0, help="profiling: config 2 at this M only")
@@ -142,12 +142,12 @@ def main():
 
     # ---- config 0 and config 2 (secondary) --------------------------------
     extra = {}
-    if not args.no_extra and args.only in ("", "c0", "c2"):
+    if not args.no_extra and args.only in ("", "c0", "c0floor", "c2"):
         r0, c0 = 9728, 2560
         g0 = synth.rng(0)
         w0 = synth.q4_0_weights(g0, r0, c0)
         x0 = synth.activations(g0, 1, c0)
-        if args.only in ("", "c0"):
+        if args.only in ("", "c0", "c0floor"):
             n_copies = 20
             w0s = [capi.Weight(ctx, w0, capi.Q4_0, r0, c0) for _ in range(n_copies)]
             x0d = dev(x0)
@@ -189,9 +189,11 @@ def main():
                                                     "frac": round(gbs0 / HBM_PEAK_GBS, 4),
                                                     "traffic": read_traffic("q4_0_matvec_c0_traffic.txt"),
                                                     "kernel": "q4_0_matvec_kernel"}}
+            if args.only == "c0floor":
+                extra["c0_floor"] = bench_c0_floor(ctx, torch, graph, n_copies, b0)
             for w_ in w0s:
                 w_.free()
-            if args.only == "c0":
+            if args.only in ("c0", "c0floor"):
                 print(json.dumps(extra))
                 return
         w0d = capi.Weight(ctx, w0, capi.Q4_0, r0, c0)
@@ -234,6 +236,9 @@ def main():
             print(json.dumps(extra))
             return
 
+    if args.only == "valu":
+        print(json.dumps(bench_valu(ctx, torch)))
+        return
     if args.only == "c3prefill":
         print(json.dumps(bench_c3_prefill(ctx, torch)))
         return
@@ -285,6 +290,81 @@ def main():
     for w_ in copies:
         w_.free()
     ctx.close()
+
+
+def bench_c0_floor(ctx, torch, c0_graph, n_copies, b0):
+    """Profiling leg (--only c0floor): config 0's product beside the floors a
+    launch of its size meets on this GPU, each a graph of 20 launches
+    replayed back to back (as the C0 figure is taken): an empty kernel of 1
+    and of 256 workgroups, and a plain 16-byte non-temporal read of C0's
+    bytes (rounded to 16) from 20 rotating copies at 152, 304 and 608
+    workgroups (the product runs 152, one a 64-row tile).  Per-launch
+    microseconds by HIP events; the same leg under rocprofv3 --kernel-trace
+    gives the per-dispatch durations."""
+    from golem_amd import capi
+    import ctypes
+    call, vp = capi.call, capi.vp
+    nbytes = b0 // 16 * 16
+    bufs = [torch.empty((nbytes,), dtype=torch.uint8, device="cuda").fill_(i + 1) for i in range(n_copies)]
+    sink = torch.zeros((4096,), dtype=torch.int32, device="cuda")
+    stream = torch.cuda.current_stream()
+
+    def captured(launch):
+        torch.cuda.synchronize()
+        cap = torch.cuda.Stream()
+        g = torch.cuda.CUDAGraph()
+        call("gx_set_stream", ctx.ptr, ctypes.c_void_p(cap.cuda_stream))
+        try:
+            with torch.cuda.graph(g, stream=cap):
+                for i in range(n_copies):
+                    launch(i)
+        finally:
+            call("gx_set_stream", ctx.ptr, ctypes.c_void_p(stream.cuda_stream))
+        return g
+
+    def per_launch(g, replays=50):
+        for _ in range(3):
+            g.replay()
+        torch.cuda.synchronize()
+        ctx.timer_start()
+        for _ in range(replays):
+            g.replay()
+        return ctx.timer_stop() / (replays * n_copies) * 1e3
+
+    out = {"c0_product_us": round(per_launch(c0_graph), 3)}
+    for wgs in (1, 256):
+        out[f"empty_{wgs}wg_us"] = round(per_launch(captured(lambda i, w=wgs: call("gx_calib_empty", ctx.ptr, w))), 3)
+    for wgs in (152, 304, 608):
+        us = per_launch(captured(lambda i, w=wgs: call("gx_calib_read", ctx.ptr, vp(bufs[i]), nbytes, w, vp(sink))))
+        out[f"read_{wgs}wg_us"] = round(us, 3)
+        out[f"read_{wgs}wg_GB/s"] = round(nbytes / (us * 1e-6) / 1e9, 1)
+    out["read_bytes"] = nbytes
+    out["c0_product_us"] = round(per_launch(c0_graph), 3)  # again, after the others
+    return out
+
+
+def bench_valu(ctx, torch):
+    """Profiling leg (--only valu): the VALU-saturating calibration kernel
+    (8 independent v_fmac_f32 chains a lane, 2048 workgroups of 256
+    threads, 4096 steps), for reading SQ_INSTS_VALU / SQ_ACTIVE_INST_VALU /
+    SQ_BUSY_CYCLES of the products against the counters' value at
+    saturation."""
+    from golem_amd import capi
+    call, vp = capi.call, capi.vp
+    sink = torch.zeros((4096,), dtype=torch.float32, device="cuda")
+    wgs, iters = 2048, 4096
+    for _ in range(3):
+        call("gx_calib_valu", ctx.ptr, wgs, iters, vp(sink))
+    torch.cuda.synchronize()
+    ctx.timer_start()
+    reps = 10
+    for _ in range(reps):
+        call("gx_calib_valu", ctx.ptr, wgs, iters, vp(sink))
+    ms = ctx.timer_stop() / reps
+    fmas = 8.0 * iters * 256 * wgs
+    return {"valu": {"workgroups": wgs, "threads": 256, "fmac_per_lane": 8 * iters, "kernel_us": round(ms * 1e3, 2),
+                     "wave64_fmac_per_cycle_per_cu_at_2.4GHz": round(fmas / 64 / (ms * 1e-3) / 2.4e9 / 256, 3),
+                     "fp32_TFLOP/s": round(2 * fmas / (ms * 1e-3) / 1e12, 1)}}
 
 
 def cpu_baseline(w6, x, rows, cols, step_bytes, step, y, torch, no_extra):

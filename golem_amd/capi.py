@@ -48,6 +48,9 @@ _SIGNATURES = {
                        ctypes.POINTER(_c_int), ctypes.POINTER(_c_size)],
     "gx_weight_rows": [_vp, _vp, _c_int, _vp, _c_int, _vp],
     "gx_quantize_q8_0": [_vp, _vp, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _vp],
+    "gx_calib_empty": [_vp, _c_int],
+    "gx_calib_read": [_vp, _vp, _c_size, _c_int, _vp],
+    "gx_calib_valu": [_vp, _c_int, _c_int, _vp],
     "gx_quantize_q8_k": [_vp, _vp, _c_int, _c_int, _c_int, _vp, _vp, _vp],
     "gx_matmul_q4_0": [_vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _vp, _c_int],
     "gx_matmul_q4_0_expert": [_vp, _vp, _c_int, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _c_int],

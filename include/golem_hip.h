@@ -521,6 +521,22 @@ int gx_argmax(gx_ctx *ctx, const float *x, int ldx, int M, int n, int32_t *ids);
 int gx_argmax_step(gx_ctx *ctx, const float *x, int n, int32_t *ids, int32_t *history, int history_len,
                    int32_t *pos, int32_t *positions);
 
+/* ---- calibration (measurement only) ----------------------------------- */
+
+/* No counterpart in golem; no product calls these.  They give the
+ * measurements beside the products their floors and ceilings on this GPU:
+ * gx_calib_empty launches an empty kernel of `workgroups` workgroups (the
+ * per-dispatch floor); gx_calib_read reads `bytes` (16-byte aligned, a
+ * multiple of 16) with 16-byte non-temporal loads, each of `workgroups`
+ * 512-thread workgroups a contiguous share (moving a product's bytes alone at
+ * its grid), `sink` one word per workgroup, practically never written;
+ * gx_calib_valu runs 8 * iters independent v_fmac_f32 per lane in 256-thread
+ * workgroups (the VALU issue rate at saturation, for reading the SQ counters
+ * of the products against). */
+int gx_calib_empty(gx_ctx *ctx, int workgroups);
+int gx_calib_read(gx_ctx *ctx, const void *src, size_t bytes, int workgroups, uint32_t *sink);
+int gx_calib_valu(gx_ctx *ctx, int workgroups, int iters, float *sink);
+
 /* ---- GGUF checkpoints (host only; no GPU needed) ----------------------- */
 
 /* An opened GGUF file: mapped whole, read in place (tensors/gguf.go:33-41,
