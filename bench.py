@@ -374,8 +374,9 @@ def cpu_baseline(w6, x, rows, cols, step_bytes, step, y, torch, no_extra):
     every allowed thread and ~3 s on one; the GPU's logits are checked bit for
     bit against it.  Config 0 (Q4_0, dotQ4_0AVX2 under matVecQ4_0Rows) is
     timed the same way for ~3 s, config 2's matrix through golem's packed
-    path (dotPackedQ4_0x4AVX2) for ~3 s at each of M = 64 and 512, and the
-    products of config 3's decode token for ~5 s (cpu_c3_decode)."""
+    path (dotPackedQ4_0x4AVX2) for ~3 s at each of M = 64, 512 and 2048,
+    config 3's whole decode token for ~6 s (cpu_c3_decode) and config 4's
+    MoE layer, decode and prefill, ~3 s each (cpu_c4)."""
     import oracle
     threads = oracle.host_threads()
     oracle.cpu_lib(threads)
@@ -422,45 +423,76 @@ def cpu_baseline(w6, x, rows, cols, step_bytes, step, y, torch, no_extra):
         # matVecPackedQ4_0Rows): ~3 s each at M = 64 and 512.
         packed = oracle.pack_q4_0(w0, r0, c0)
         g2 = synth.rng(2)
-        for M in (64, 512):
+        for M in (64, 512, 2048):
             b2 = oracle.Batch(synth.activations(g2, M, c0)).quantize()
             y2 = np.zeros((M, r0), dtype=np.float32)
             n2, t2 = timed(lambda i: oracle.cpu_mat_vec_packed_q4_0(packed, b2, r0, threads, y2), 3.0)
             macs = float(M) * r0 * c0
             out[f"c2_q4_0_packed_m{M}"] = {"GMAC/s": round(n2 * macs / t2 / 1e9, 2),
                                            "ms_per_pass": round(t2 / n2 * 1e3, 2), "cores": threads, "passes": n2}
-        out["c3_decode_products"] = cpu_c3_decode(oracle, synth, w6, timed, threads)
+        out["c3_decode_token"] = cpu_c3_decode(oracle, synth, w6, timed, threads)
+        out.update(cpu_c4(oracle, synth, timed, threads))
     return out
 
 
 def cpu_c3_decode(oracle, synth, w6, timed, threads):
-    """Config 3's decode token on the CPU, its products only: per block
-    Q|K|V (6144 x 2560), O (2560 x 4096), Gate|Up (19456 x 2560) and Down
-    (2560 x 9728) through golem's packed Q4_0 path (matVecPackedQ4_0Rows over
-    PackQ4_0's layout, dotPackedQ4_0x4AVX2 restated), 36 blocks with their own
-    copies of the weights (2 GB, past the last-level cache), then the Q6_K
-    head (config 1's matrix).  Attention, norms and SwiGLU are left out, so
-    the rate is an upper bound on golem's CPU decode at this shape."""
+    """Config 3's whole decode token on the CPU, golem's x86 engine restated
+    (oracle/cpu_avx2.c cpu_qwen_token: per block the pre-norms and their
+    Q8_0, the head section -- Q/K/V rows through matVecPackedQ4_0Rows, head
+    norms, RoPE, fp16 rounding, the cache store --, the attention section --
+    dotF32AVX2 scores, SoftmaxInPlace, fp16 probabilities, Axpy, the heads'
+    Q8_0 --, O, the FFN section -- Gate and Up rows, SwiGLU, Q8_0 --, Down,
+    the residual adds; then the final norm, QuantizeK and the Q6_K head),
+    36 blocks with their own packed weights (2 GB, past the last-level
+    cache), caches of fp16-rounded values, positions 576 .. 639 in turn."""
+    from golem_amd.qwen import rope_tables
+    cfg = synth.qwen3_4b(640)
     g = synth.rng(3)
-    shapes = [(6144, 2560), (2560, 4096), (19456, 2560), (2560, 9728)]
-    layer = [oracle.pack_q4_0(synth.q4_0_weights(g, r, c), r, c) for r, c in shapes]
-    blocks = [layer] + [[m.copy() for m in layer] for _ in range(35)]
-    acts = {c: oracle.Batch(synth.activations(g, 1, c)).quantize() for c in (2560, 4096, 9728)}
-    ys = {r: np.zeros((1, r), dtype=np.float32) for r, _ in shapes}
-    bh = oracle.Batch(synth.activations(g, 1, 2560)).quantize_k()
-    head_rows = 151936
-    yh = np.zeros((1, head_rows), dtype=np.float32)
+    one = synth.qwen_weights(synth.QwenConfig(cfg.dim, cfg.ffn, 1, cfg.heads, cfg.kv_heads, cfg.head_dim, 256,
+                                              cfg.max_context), 3)
+    w = {"blocks": [one["blocks"][0]] * cfg.layers, "output_norm": one["output_norm"], "token_embd": w6}
+    cpu = oracle.CpuQwen(cfg, w)
+    for kc, vc in cpu.caches:
+        kc[:] = g.standard_normal(kc.shape).astype(np.float16)
+        vc[:] = g.standard_normal(vc.shape).astype(np.float16)
+    cos, sin = rope_tables(cfg.head_dim, cfg.max_context, cfg.rope_base)
+    x0 = synth.activations(g, 1, cfg.dim)[0]
 
     def token(i):
-        for blk in blocks:
-            for (r, c), m in zip(shapes, blk):
-                oracle.cpu_mat_vec_packed_q4_0(m, acts[c], r, threads, ys[r])
-        oracle.cpu_mat_vec_q6_k(w6, bh, head_rows, threads, yh)
+        pos = 576 + i % 64
+        cpu.token(x0.copy(), pos, cos[pos], sin[pos], threads)
 
-    n, t = timed(token, 5.0)
-    del blocks
+    n, t = timed(token, 6.0)
+    del cpu
     return {"tok_per_s": round(n / t, 2), "ms_per_token": round(t / n * 1e3, 1), "cores": threads, "tokens": n,
-            "scope": "the products of a decode token only (36 blocks + Q6_K head), golem's AVX2 packed path"}
+            "scope": "a whole decode token (36 blocks: norms, products, head norms, RoPE, cache, attention over "
+                     "577..640 positions, SwiGLU; final norm and Q6_K head), golem's x86 engine restated"}
+
+
+def cpu_c4(oracle, synth, timed, threads):
+    """Config 4 on the CPU: gemma's Route + ExpertFFN through golem's x86
+    kernels (oracle/cpu_avx2.c cpu_moe_ffn: dotF32AVX2 router, the
+    worker-pool sections over positions and (position, slot) units, the
+    expert stacks in the row layout through matVecQ4_0Rows), decode (one
+    position, 64 different inputs in turn) and the 256-position prefill, on
+    config 4's seeded weights (428 MB of experts)."""
+    D, F, E, k = 2816, 704, 128, 8
+    g = synth.rng(4)
+    router = (g.standard_normal((E, D)) * 0.02).astype(np.float32)
+    gate_up = synth.q4_0_weights(g, E * 2 * F, D)
+    down = synth.q4_0_weights(g, E * D, F)
+    expert_bytes = (2 * F * (D // 32) + D * (F // 32)) * 18
+    out = {}
+    for label, M, npos in (("decode", 1, 64), ("prefill256", 256, 2)):
+        xs = [synth.activations(g, M, D) for _ in range(npos)]
+        moe = oracle.CpuMoE(router, gate_up, down, D, F, E, k, M)
+        touched = [len(np.unique(moe.run(x, threads)[1])) for x in xs]
+        n, t = timed(lambda i: moe.run(xs[i % npos], threads), 3.0)
+        ms = t / n * 1e3
+        by = float(np.mean(touched)) * expert_bytes + E * D * 4
+        out[f"c4_moe_{label}"] = {"ms_per_layer": round(ms, 3), "positions_per_s": round(M / (ms * 1e-3), 1),
+                                  "GB/s": round(by / (ms * 1e-3) / 1e9, 2), "cores": threads, "passes": n}
+    return out
 
 
 def bench_c3_prefill(ctx, torch):

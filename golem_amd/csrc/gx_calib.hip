@@ -26,6 +26,7 @@ __global__ __launch_bounds__(512) void calib_read_kernel(const uint8_t *__restri
     const size_t per = (chunks + gridDim.x - 1) / gridDim.x;  // 16-byte chunks a workgroup
     const size_t c0 = (size_t)blockIdx.x * per, c1 = min(c0 + per, chunks);
     uint32_t acc = 0;
+#pragma unroll 16
     for (size_t c = c0 + threadIdx.x; c < c1; c += blockDim.x) {
         const uint4 v = load_stream(src + c * 16);
         acc ^= v.x ^ v.y ^ v.z ^ v.w;

@@ -372,6 +372,8 @@ def cpu_lib(threads=None):
         "cpu_mat_vec_q6_k": (I, [V, V, V, V, I, I, I, V, I, I]),
         "cpu_mat_vec_q4_0": (I, [V, V, V, V, I, I, I, V, I, I]),
         "cpu_mat_vec_packed_q4_0": (I, [V, V, V, V, I, I, I, V, I, I]),
+        "cpu_moe_ffn": (I, [V, V, V, V, I, I, I, I, I, V, V, V, V, V, V, V, V, V, V, V, V, V, V, I]),
+        "cpu_qwen_token": (I, [V, I, I, I, I, I, I, I, I, F, V, V, V, V, I, V, V, I]),
         "cpu_dot_q4_0": (None, [V, V, V, V, I, I, I, I, V, I, I]),
         "cpu_dot_q6_k": (F, [V, V, V, V, I]),
     }.items():
@@ -412,6 +414,80 @@ def cpu_mat_vec_packed_q4_0(packed, batch, rows, threads, ys=None):
                                            batch.width, batch.size, _p(ys), ys.shape[1], threads)
     assert rc == 0
     return ys
+
+
+class CpuMoE:
+    """gemma's Route + ExpertFFN (gemma/moe.go:34-180) through golem's x86
+    kernels (cpu_avx2.c: dotF32AVX2, matVecQ4_0Rows over the row-layout
+    expert stacks, the worker pool's sections), with its scratch for `batch`
+    positions.  run() returns (out [batch][D], ids [batch][k], weights)."""
+
+    def __init__(self, router, gate_up, down, D, F, E, k, batch):
+        self.router = np.ascontiguousarray(router, np.float32)
+        self.gate_up, self.down = np.ascontiguousarray(gate_up), np.ascontiguousarray(down)
+        self.D, self.F, self.E, self.k, self.batch = D, F, E, k, batch
+        self.gelu = gelu_table_build()
+        u = batch * k
+        z = lambda shape, dt=np.float32: np.zeros(shape, dt)
+        self.rin, self.logits = z((batch, D)), z((batch, E))
+        self.ids, self.weights = z((batch, k), np.int32), z((batch, k))
+        self.xq, self.xs, self.xc = z((batch, D), np.int8), z((batch, D // 32)), z((batch, D // 32))
+        self.gu = z((u, 2 * F))
+        self.mq, self.ms, self.mc = z((u, F), np.int8), z((u, F // 32)), z((u, F // 32))
+        self.partial, self.out = z((u, D)), z((batch, D))
+
+    def run(self, resid, threads):
+        resid = np.ascontiguousarray(resid, np.float32)
+        assert resid.shape == (self.batch, self.D)
+        rc = cpu_lib().cpu_moe_ffn(_p(self.router), _p(self.gate_up), _p(self.down), _p(self.gelu), self.D, self.F,
+                                   self.E, self.k, self.batch, _p(resid), _p(self.rin), _p(self.logits), _p(self.ids),
+                                   _p(self.weights), _p(self.xq), _p(self.xs), _p(self.xc), _p(self.gu), _p(self.mq),
+                                   _p(self.ms), _p(self.mc), _p(self.partial), _p(self.out), threads)
+        assert rc == 0
+        return self.out, self.ids, self.weights
+
+
+class CpuQwen:
+    """golem's Qwen3 decode token (qwen/block.go:32-102, attention.go:34-127,
+    model.go:181-194) through its x86 kernels (cpu_avx2.c): the dense
+    matrices in PackQ4_0's layout (golem's loader repacks them), the fp32
+    caches of golem's LayerCache, the Q6_K tied head.  `layers` is a list of
+    weight dicts as synth.qwen_weights builds them."""
+
+    KEYS = ("q", "k", "v", "o", "gate", "up", "down")
+
+    def __init__(self, cfg, weights, layers=None):
+        self.cfg = cfg
+        blocks = weights["blocks"] if layers is None else layers
+        shapes = {"q": (cfg.heads * cfg.head_dim, cfg.dim), "k": (cfg.kv_heads * cfg.head_dim, cfg.dim),
+                  "v": (cfg.kv_heads * cfg.head_dim, cfg.dim), "o": (cfg.dim, cfg.heads * cfg.head_dim),
+                  "gate": (cfg.ffn, cfg.dim), "up": (cfg.ffn, cfg.dim), "down": (cfg.dim, cfg.ffn)}
+        self.keep = []
+        ptrs = []
+        for b in blocks:
+            mats = [pack_q4_0(b[n], *shapes[n]) for n in self.KEYS]
+            norms = [np.ascontiguousarray(b[n], np.float32) for n in ("attn_norm", "ffn_norm", "q_norm", "k_norm")]
+            caches = [np.zeros((cfg.max_context, cfg.kv_heads, cfg.head_dim), np.float32) for _ in range(2)]
+            self.keep += mats + norms + caches
+            ptrs += [a.ctypes.data for a in mats + norms + caches]
+        self.ptrs = np.array(ptrs, dtype=np.uint64)
+        self.caches = [(self.keep[i + 11], self.keep[i + 12]) for i in range(0, len(self.keep), 13)]
+        self.output_norm = np.ascontiguousarray(weights["output_norm"], np.float32)
+        self.head = np.ascontiguousarray(weights["token_embd"])
+        self.logits = np.zeros(cfg.vocab, np.float32)
+
+    def token(self, x, pos, cos, sin, threads):
+        """x: the embedding row (float32 [dim], updated to the final-normed
+        hidden state); cos / sin: RoPETable's row for pos.  Returns the
+        logits."""
+        cfg = self.cfg
+        rc = cpu_lib().cpu_qwen_token(ctypes.c_void_p(self.ptrs.ctypes.data), len(self.caches), cfg.dim, cfg.ffn,
+                                      cfg.heads, cfg.kv_heads, cfg.head_dim, cfg.max_context, pos, cfg.eps,
+                                      _p(np.ascontiguousarray(cos, np.float32)),
+                                      _p(np.ascontiguousarray(sin, np.float32)), _p(self.output_norm),
+                                      _p(self.head), cfg.vocab, _p(x), _p(self.logits), threads)
+        assert rc == 0
+        return self.logits
 
 
 def cpu_dot_q4_0(w_row, batch, block, column, n, state, mode, cols):

@@ -573,3 +573,477 @@ void cpu_dot_q4_0(const uint8_t *w, const int8_t *Q, const float *S, const float
 float cpu_dot_q6_k(const uint8_t *w, const int8_t *q, const int16_t *bsums, const float *kscales, int n) {
     return dot_q6_k_avx2(w, q, bsums, kscales, n);
 }
+
+/* ---- gemma's MoE feed-forward (gemma/moe.go:34-180) ------------------------
+ *
+ * Route and ExpertFFN as golem runs them on x86, for config 4's CPU figure:
+ *   Route          per position RMSNormPlain (nn/ops.go:195-214, the float64
+ *                  sum left to right) times 1/sqrt(Dim) (RouterScale ones),
+ *                  then the F32 router through Matrix.rows' F32 case --
+ *                  dotF32AVX2 (nn/dot_f32_amd64.s:43-113: four accumulators
+ *                  of eight lanes, the eights, the remainder, nothing fused)
+ *                  in a section over the router's rows -- then
+ *                  chooseExperts (gemma/moe.go:62-88);
+ *   ExpertFFN      a section over positions quantising each input
+ *                  (Batch.quantizeBlock, nn/batch.go:109-143), a section over
+ *                  the (position, slot) units -- the expert's gate|up rows
+ *                  through matVecQ4_0Rows (the row layout: expert stacks are
+ *                  not repacked), GELUTable(gate) * up, its Q8_0, the down
+ *                  rows -- and a section over positions summing the units
+ *                  with Axpy (the FMA form, nn/kernel_amd64.s:134-197),
+ *                  DownScale ones. */
+
+/* dotF32AVX2 */
+static float dot_f32_avx2(const float *a, const float *b, int n) {
+    __m256 y0 = _mm256_setzero_ps(), y1 = _mm256_setzero_ps(), y2 = _mm256_setzero_ps(), y3 = _mm256_setzero_ps();
+    int i = 0;
+    for (; i + 32 <= n; i += 32) {
+        y0 = _mm256_add_ps(y0, _mm256_mul_ps(_mm256_loadu_ps(a + i), _mm256_loadu_ps(b + i)));
+        y1 = _mm256_add_ps(y1, _mm256_mul_ps(_mm256_loadu_ps(a + i + 8), _mm256_loadu_ps(b + i + 8)));
+        y2 = _mm256_add_ps(y2, _mm256_mul_ps(_mm256_loadu_ps(a + i + 16), _mm256_loadu_ps(b + i + 16)));
+        y3 = _mm256_add_ps(y3, _mm256_mul_ps(_mm256_loadu_ps(a + i + 24), _mm256_loadu_ps(b + i + 24)));
+    }
+    y0 = _mm256_add_ps(y0, y1);
+    y2 = _mm256_add_ps(y2, y3);
+    y0 = _mm256_add_ps(y0, y2);
+    for (; i + 8 <= n; i += 8)
+        y0 = _mm256_add_ps(y0, _mm256_mul_ps(_mm256_loadu_ps(a + i), _mm256_loadu_ps(b + i)));
+    __m128 x = _mm_add_ps(_mm256_castps256_ps128(y0), _mm256_extractf128_ps(y0, 1));
+    x = _mm_add_ps(x, _mm_movehl_ps(x, x));
+    x = _mm_add_ss(x, _mm_shuffle_ps(x, x, 0x01));
+    float s = _mm_cvtss_f32(x);
+    for (; i < n; i++)
+        s += a[i] * b[i];
+    return s;
+}
+
+/* Batch.quantizeBlock for one column's n inputs (golem's generic Go: the
+ * only form it has). */
+static inline int32_t nearest(float f) {
+    float s = f + 12582912.0f;
+    int32_t u;
+    memcpy(&u, &s, 4);
+    return (u & 0x007fffff) - 0x00400000;
+}
+static void quantize_column(const float *x, int n, int8_t *q, float *scales, float *corr) {
+    for (int b = 0; b < n / 32; b++) {
+        const float *v = x + 32 * b;
+        float peak = 0;
+        for (int i = 0; i < 32; i++) {
+            const float a = v[i] < 0 ? -v[i] : v[i];
+            if (a > peak)
+                peak = a;
+        }
+        if (peak == 0) {
+            scales[b] = corr[b] = 0;
+            memset(q + 32 * b, 0, 32);
+            continue;
+        }
+        const float scale = peak / 127, inverse = 127 / peak;
+        scales[b] = _cvtsh_ss(_cvtss_sh(scale, _MM_FROUND_TO_NEAREST_INT));
+        int32_t sum = 0;
+        for (int i = 0; i < 32; i++) {
+            int32_t k = nearest(v[i] * inverse);
+            k = k > 127 ? 127 : k < -128 ? -128 : k;
+            q[32 * b + i] = (int8_t)k;
+            sum += k;
+        }
+        corr[b] = 8 * scales[b] * (float)sum;
+    }
+}
+
+struct moe_cpu {
+    const float *router;              /* [E][D] */
+    const uint8_t *gate_up, *down;    /* row-layout Q4_0 stacks */
+    const float *gelu;                /* golem's 65536-entry table, indexed by the fp16 bits */
+    int D, F, E, k, batch;
+    const float *resid;               /* [batch][D]: the router's and the experts' input */
+    float *rin;                       /* [batch][D] scratch */
+    float *logits;                    /* [batch][E] */
+    int32_t *ids;                     /* [batch][k] */
+    float *weights;                   /* [batch][k] */
+    int8_t *xq;                       /* [batch][D], scales / corr [batch][D/32] */
+    float *xs, *xc;
+    float *gu;                        /* [units][2F] */
+    int8_t *mq;                       /* [units][F], scales / corr [units][F/32] */
+    float *ms, *mc;
+    float *partial;                   /* [units][D] */
+    float *out;                       /* [batch][D] */
+};
+
+static void moe_norm_section(void *p, int start, int end) {
+    struct moe_cpu *m = p;
+    const float scale = (float)(1 / __builtin_sqrt((double)m->D));
+    for (int t = start; t < end; t++) {
+        float *x = m->rin + (size_t)t * m->D;
+        memcpy(x, m->resid + (size_t)t * m->D, sizeof(float) * m->D);
+        double s = 0;
+        for (int i = 0; i < m->D; i++)
+            s += (double)(x[i] * x[i]);
+        const float mean = (float)(s / (double)m->D);
+        const float r = (float)(1 / __builtin_sqrt((double)(mean + 1e-6f)));
+        for (int i = 0; i < m->D; i++)
+            x[i] = (x[i] * r) * (scale * 1.0f);
+        /* the router's input is quantised too (its F32 product reads the floats) */
+        quantize_column(x, m->D, m->xq + (size_t)t * m->D, m->xs + (size_t)t * m->D / 32,
+                        m->xc + (size_t)t * m->D / 32);
+    }
+}
+
+static void moe_router_section(void *p, int start, int end) {
+    struct moe_cpu *m = p;
+    for (int t = 0; t < m->batch; t++)
+        for (int e = start; e < end; e++)
+            m->logits[(size_t)t * m->E + e] =
+                dot_f32_avx2(m->router + (size_t)e * m->D, m->rin + (size_t)t * m->D, m->D);
+}
+
+static void moe_choose(struct moe_cpu *m) {
+    for (int t = 0; t < m->batch; t++) {
+        const float *l = m->logits + (size_t)t * m->E;
+        int32_t *ids = m->ids + (size_t)t * m->k;
+        float *w = m->weights + (size_t)t * m->k;
+        for (int k = 0; k < m->k; k++) {
+            int best = -1;
+            for (int e = 0; e < m->E; e++) {
+                int taken = 0;
+                for (int j = 0; j < k; j++)
+                    taken |= ids[j] == e;
+                if (!taken && (best < 0 || l[e] > l[best]))
+                    best = e;
+            }
+            ids[k] = best;
+        }
+        const float top = l[ids[0]];
+        float total = 0;
+        for (int k = 0; k < m->k; k++) {
+            w[k] = (float)__builtin_exp((double)(l[ids[k]] - top));
+            total += w[k];
+        }
+        for (int k = 0; k < m->k; k++)
+            w[k] /= total;
+    }
+}
+
+static void moe_quantize_section(void *p, int start, int end) {
+    struct moe_cpu *m = p;
+    for (int t = start; t < end; t++)
+        quantize_column(m->resid + (size_t)t * m->D, m->D, m->xq + (size_t)t * m->D, m->xs + (size_t)t * m->D / 32,
+                        m->xc + (size_t)t * m->D / 32);
+}
+
+static inline float gelu_lookup(const float *table, float x) {
+    if (x <= -10.0f)
+        return 0.0f;
+    if (x >= 10.0f)
+        return x;
+    return table[_cvtss_sh(x, _MM_FROUND_TO_NEAREST_INT)];
+}
+
+static void moe_units_section(void *p, int start, int end) {
+    struct moe_cpu *m = p;
+    const int D = m->D, F = m->F;
+    const size_t gu_bytes = (size_t)2 * F * (D / 32) * 18, dn_bytes = (size_t)D * (F / 32) * 18;
+    for (int u = start; u < end; u++) {
+        const int t = u / m->k, id = m->ids[u];
+        float *gu = m->gu + (size_t)u * 2 * F;
+        struct q4_args a = {m->gate_up + (size_t)id * gu_bytes, m->xq + (size_t)t * D, m->xs + (size_t)t * D / 32,
+                            m->xc + (size_t)t * D / 32, 1, 1, D, 2 * F, gu};
+        q4_rows(&a, 0, 2 * F);
+        float *mid = gu;  /* gate, then gate * up in place */
+        for (int i = 0; i < F; i++)
+            mid[i] = gelu_lookup(m->gelu, gu[i]) * gu[F + i];
+        int8_t *mq = m->mq + (size_t)u * F;
+        float *ms = m->ms + (size_t)u * F / 32, *mc = m->mc + (size_t)u * F / 32;
+        quantize_column(mid, F, mq, ms, mc);
+        struct q4_args b = {m->down + (size_t)id * dn_bytes, mq, ms, mc, 1, 1, F, D, m->partial + (size_t)u * D};
+        q4_rows(&b, 0, D);
+    }
+}
+
+static void moe_reduce_section(void *p, int start, int end) {
+    struct moe_cpu *m = p;
+    for (int t = start; t < end; t++) {
+        float *o = m->out + (size_t)t * m->D;
+        memset(o, 0, sizeof(float) * m->D);
+        for (int k = 0; k < m->k; k++) {
+            const __m256 w = _mm256_set1_ps(m->weights[(size_t)t * m->k + k] * 1.0f);
+            const float *src = m->partial + ((size_t)t * m->k + k) * m->D;
+            int i = 0;
+            for (; i + 8 <= m->D; i += 8)
+                _mm256_storeu_ps(o + i, _mm256_fmadd_ps(w, _mm256_loadu_ps(src + i), _mm256_loadu_ps(o + i)));
+            for (; i < m->D; i++)
+                o[i] += m->weights[(size_t)t * m->k + k] * src[i];
+        }
+    }
+}
+
+/* Route + ExpertFFN for `batch` positions on at most `threads` threads;
+ * scratch is caller-owned (sizes as the struct says). */
+int cpu_moe_ffn(const float *router, const uint8_t *gate_up, const uint8_t *down, const float *gelu, int D, int F,
+                int E, int k, int batch, const float *resid, float *rin, float *logits, int32_t *ids, float *weights,
+                int8_t *xq, float *xs, float *xc, float *gu, int8_t *mq, float *ms, float *mc, float *partial,
+                float *out, int threads) {
+    if (!pool.count || D % 32 || F % 32)
+        return -1;
+    struct moe_cpu m = {router, gate_up, down, gelu, D, F, E, k, batch, resid, rin, logits, ids, weights,
+                        xq, xs, xc, gu, mq, ms, mc, partial, out};
+    enum { PER_POSITION = 24 }; /* gemma/block.go:104 */
+    in_parallel(batch, (long)batch * D * PER_POSITION, threads, moe_norm_section, &m);
+    in_parallel(E, (long)batch * E * D, threads, moe_router_section, &m);
+    moe_choose(&m);
+    in_parallel(batch, (long)batch * D * PER_POSITION, threads, moe_quantize_section, &m);
+    const int units = batch * k;
+    in_parallel(units, (long)units * F * D * 2, threads, moe_units_section, &m);
+    in_parallel(batch, (long)batch * k * D, threads, moe_reduce_section, &m);
+    return 0;
+}
+
+/* ---- qwen's decode token (qwen/block.go:32-102, qwen/attention.go:34-127) --
+ *
+ * One position through every block and the tied Q6_K head, as golem runs it
+ * on x86: the pre-norms (RMSNormPlain with the block's gain, then the Q8_0
+ * form), the head section (a unit a query head or a key-value head: its 128
+ * rows of the packed products through matVecPackedQ4_0Rows, the head norm,
+ * RoPE, fp16 rounding, the cache store), the attention section (a unit a
+ * query head: DotF32 scores through dotF32AVX2, SoftmaxInPlace in float64
+ * exp, fp16 probabilities, Axpy of the cached values, the head's Q8_0), O,
+ * the FFN section (a unit a 32-row stretch of Gate and of Up, SwiGLU with
+ * ggml's expf (nn/swiglu.go:31-82) and the stretch's Q8_0), Down, the
+ * residual adds; then the final norm, QuantizeK and MatVecQ6_K. */
+
+static void rms_norm(float *x, const float *gain, int n, float eps) {
+    double s = 0;
+    for (int i = 0; i < n; i++)
+        s += (double)(x[i] * x[i]);
+    const float mean = (float)(s / (double)n);
+    const float r = (float)(1 / __builtin_sqrt((double)(mean + eps)));
+    for (int i = 0; i < n; i++)
+        x[i] = gain ? (x[i] * r) * gain[i] : x[i] * r;
+}
+
+static inline float round_half(float v) { return _cvtsh_ss(_cvtss_sh(v, _MM_FROUND_TO_NEAREST_INT)); }
+
+/* ggml's expf as golem restates it (nn/swiglu.go:31-74) */
+static float ggml_expf(float x) {
+    const float shift = 0x1.8p23f, log2e = 0x1.715476p+0f, ln2hi = 0x1.62e4p-1f, ln2lo = 0x1.7f7d1cp-20f;
+    const float c0 = 0x1.ffffecp-1f, c1 = 0x1.fffdb6p-2f, c2 = 0x1.555e66p-3f, c3 = 0x1.573e2ep-5f,
+                c4 = 0x1.0e4020p-7f;
+    const float z = x * log2e + shift, n = z - shift;
+    if (n > 126 || n < -126)
+        return (float)__builtin_exp((double)x);
+    const float b = x - n * ln2hi - n * ln2lo;
+    uint32_t zu, one;
+    const float onef = 1.0f;
+    memcpy(&zu, &z, 4);
+    memcpy(&one, &onef, 4);
+    const uint32_t ku = (zu << 23) + one;
+    float k;
+    memcpy(&k, &ku, 4);
+    const float u = b * b;
+    const float j = ((c4 * b + c3) * u + (c2 * b + c1)) * u + c0 * b;
+    return j * k + k;
+}
+
+/* Batch.QuantizeK (nn/batch.go:159-213) of one column */
+static void quantize_k(const float *x, int n, int8_t *q, float *kscales, int16_t *bsums) {
+    for (int b = 0; b < n / 256; b++) {
+        const float *v = x + 256 * b;
+        float peak = 0, extreme = 0;
+        for (int i = 0; i < 256; i++) {
+            const float a = v[i] < 0 ? -v[i] : v[i];
+            if (a > peak) {
+                peak = a;
+                extreme = v[i];
+            }
+        }
+        if (peak == 0) {
+            kscales[b] = 0;
+            memset(q + 256 * b, 0, 256);
+            for (int g = 0; g < 16; g++)
+                bsums[16 * b + g] = 0;
+            continue;
+        }
+        const float inverse = -128 / extreme;
+        for (int g = 0; g < 16; g++) {
+            int32_t s = 0;
+            for (int i = 16 * g; i < 16 * g + 16; i++) {
+                int32_t k = nearest(v[i] * inverse);
+                k = k > 127 ? 127 : k;
+                q[256 * b + i] = (int8_t)k;
+                s += k;
+            }
+            bsums[16 * b + g] = (int16_t)s;
+        }
+        kscales[b] = 1 / inverse;
+    }
+}
+
+enum { QL_Q, QL_K, QL_V, QL_O, QL_GATE, QL_UP, QL_DOWN, QL_ATTN_NORM, QL_FFN_NORM, QL_Q_NORM, QL_K_NORM, QL_KC, QL_VC,
+       QL_COUNT };
+
+struct qwen_cpu {
+    void *const *layer;  /* [layers][QL_COUNT] */
+    int D, F, H, KV, HD, ctx, pos;
+    float eps, scale;
+    const float *cos, *sin;  /* the rotation at pos, [HD/2] */
+    int8_t *nq; float *ns, *nc;          /* the normed input's Q8_0 [D] */
+    float *qh;                           /* [H][HD] rounded queries */
+    float *hk, *hv;                      /* [KV][HD] scratch for the projections */
+    int8_t *sq; float *ss, *sc;          /* the heads' Q8_0 [H * HD] */
+    float *set;                          /* [H * HD] */
+    float *scores;                       /* [H][ctx] */
+    float *gate, *up;                    /* [F] */
+    int8_t *mq; float *msc, *mc;         /* mid's Q8_0 [F] */
+    int L;
+};
+
+static void packed_range(const uint8_t *w, const int8_t *Q, const float *S, const float *C, int inputs, float *y,
+                         int start, int end) {
+    struct packed_args a = {w, Q, S, C, 1, inputs, 0, y};
+    packed_rows(&a, start, end);
+}
+
+static void qwen_heads_section(void *p, int start, int end) {
+    struct qwen_cpu *m = p;
+    void *const *lw = m->layer + (size_t)m->L * QL_COUNT;
+    const int HD = m->HD, half = HD / 2;
+    for (int u = start; u < end; u++) {
+        const int is_q = u < m->H, h = is_q ? u : u - m->H;
+        float *head = is_q ? m->qh + (size_t)h * HD : m->hk + (size_t)h * HD;
+        /* the head's rows; golem's scratch rows are indexed by the matrix row */
+        packed_range(lw[is_q ? QL_Q : QL_K], m->nq, m->ns, m->nc, m->D, head - (size_t)h * HD, h * HD, (h + 1) * HD);
+        rms_norm(head, lw[is_q ? QL_Q_NORM : QL_K_NORM], HD, m->eps);
+        for (int i = 0; i < half; i++) {
+            const float re = head[i], im = head[i + half];
+            head[i] = re * m->cos[i] - im * m->sin[i];
+            head[i + half] = re * m->sin[i] + im * m->cos[i];
+        }
+        for (int i = 0; i < HD; i++)
+            head[i] = round_half(head[i]);
+        if (!is_q) {
+            float *vh = m->hv + (size_t)h * HD;
+            packed_range(lw[QL_V], m->nq, m->ns, m->nc, m->D, vh - (size_t)h * HD, h * HD, (h + 1) * HD);
+            float *kc = (float *)lw[QL_KC] + ((size_t)m->pos * m->KV + h) * HD;
+            float *vc = (float *)lw[QL_VC] + ((size_t)m->pos * m->KV + h) * HD;
+            for (int i = 0; i < HD; i++) {
+                kc[i] = head[i];
+                vc[i] = round_half(vh[i]);
+            }
+        }
+    }
+}
+
+static void qwen_attend_section(void *p, int start, int end) {
+    struct qwen_cpu *m = p;
+    void *const *lw = m->layer + (size_t)m->L * QL_COUNT;
+    const int HD = m->HD, n = m->pos + 1;
+    const float *kc = lw[QL_KC], *vc = lw[QL_VC];
+    for (int h = start; h < end; h++) {
+        const int kv = h / (m->H / m->KV);
+        float *s = m->scores + (size_t)h * m->ctx;
+        const float *q = m->qh + (size_t)h * HD;
+        float mx = -__builtin_inff();
+        for (int p2 = 0; p2 < n; p2++) {
+            s[p2] = m->scale * dot_f32_avx2(q, kc + ((size_t)p2 * m->KV + kv) * HD, HD);
+            if (s[p2] > mx)
+                mx = s[p2];
+        }
+        float total = 0;
+        for (int p2 = 0; p2 < n; p2++) {
+            s[p2] = (float)__builtin_exp((double)(s[p2] - mx));
+            total += s[p2];
+        }
+        for (int p2 = 0; p2 < n; p2++)
+            s[p2] = round_half(s[p2] / total);
+        float *dst = m->set + (size_t)h * HD;
+        memset(dst, 0, sizeof(float) * HD);
+        for (int p2 = 0; p2 < n; p2++) {
+            const __m256 a = _mm256_set1_ps(s[p2]);
+            const float *src = vc + ((size_t)p2 * m->KV + kv) * HD;
+            for (int i = 0; i < HD; i += 8)
+                _mm256_storeu_ps(dst + i, _mm256_fmadd_ps(a, _mm256_loadu_ps(src + i), _mm256_loadu_ps(dst + i)));
+        }
+        quantize_column(dst, HD, m->sq + (size_t)h * HD, m->ss + (size_t)h * HD / 32, m->sc + (size_t)h * HD / 32);
+    }
+}
+
+static void qwen_ffn_section(void *p, int start, int end) {
+    struct qwen_cpu *m = p;
+    void *const *lw = m->layer + (size_t)m->L * QL_COUNT;
+    const int from = 32 * start, to = 32 * end;
+    packed_range(lw[QL_GATE], m->nq, m->ns, m->nc, m->D, m->gate, from, to);
+    packed_range(lw[QL_UP], m->nq, m->ns, m->nc, m->D, m->up, from, to);
+    for (int i = from; i < to; i++) {
+        const float g = m->gate[i];
+        m->gate[i] = g / (1 + ggml_expf(-g)) * m->up[i];
+    }
+    quantize_column(m->gate + from, to - from, m->mq + from, m->msc + from / 32, m->mc + from / 32);
+}
+
+static void qwen_rows_o(void *p, int start, int end) {
+    struct qwen_cpu *m = p;
+    void *const *lw = m->layer + (size_t)m->L * QL_COUNT;
+    packed_range(lw[QL_O], m->sq, m->ss, m->sc, m->H * m->HD, m->gate /* attn out, D <= F */, start, end);
+}
+
+static void qwen_rows_down(void *p, int start, int end) {
+    struct qwen_cpu *m = p;
+    void *const *lw = m->layer + (size_t)m->L * QL_COUNT;
+    packed_range(lw[QL_DOWN], m->mq, m->msc, m->mc, m->F, m->up /* ffn out, D <= F */, start, end);
+}
+
+/* One decode token: x [D] is the embedding row in and the hidden state after
+ * the final norm out; logits [vocab] through the Q6_K head. */
+int cpu_qwen_token(void *const *layers, int nlayers, int D, int F, int H, int KV, int HD, int ctx, int pos, float eps,
+                   const float *cos, const float *sin, const float *output_norm, const uint8_t *head, int vocab,
+                   float *x, float *logits, int threads) {
+    if (!pool.count || pos >= ctx || D > F || H * HD > F)
+        return -1;
+    enum { PER_POSITION = 24 }; /* qwen/block.go:30 */
+    const int QD = H * HD;
+    struct qwen_cpu m = {0};
+    m.layer = layers;
+    m.D = D, m.F = F, m.H = H, m.KV = KV, m.HD = HD, m.ctx = ctx, m.pos = pos;
+    m.eps = eps;
+    m.scale = (float)(1 / __builtin_sqrt((double)HD));
+    m.cos = cos, m.sin = sin;
+    float *normed = malloc(sizeof(float) * D);
+    m.nq = malloc(D), m.ns = malloc(sizeof(float) * D / 32), m.nc = malloc(sizeof(float) * D / 32);
+    m.qh = malloc(sizeof(float) * QD), m.hk = malloc(sizeof(float) * KV * HD), m.hv = malloc(sizeof(float) * KV * HD);
+    m.sq = malloc(QD), m.ss = malloc(sizeof(float) * QD / 32), m.sc = malloc(sizeof(float) * QD / 32);
+    m.set = malloc(sizeof(float) * QD), m.scores = malloc(sizeof(float) * H * ctx);
+    m.gate = malloc(sizeof(float) * F), m.up = malloc(sizeof(float) * F);
+    m.mq = malloc(F), m.msc = malloc(sizeof(float) * F / 32), m.mc = malloc(sizeof(float) * F / 32);
+    for (int L = 0; L < nlayers; L++) {
+        void *const *lw = layers + (size_t)L * QL_COUNT;
+        m.L = L;
+        memcpy(normed, x, sizeof(float) * D);
+        rms_norm(normed, lw[QL_ATTN_NORM], D, eps);
+        quantize_column(normed, D, m.nq, m.ns, m.nc);
+        in_parallel(H + KV, (long)(H + KV) * HD * D, threads, qwen_heads_section, &m);
+        in_parallel(H, 2L * H * (pos + 1) * HD, threads, qwen_attend_section, &m);
+        in_parallel(D, (long)D * QD, threads, qwen_rows_o, &m);  /* O.MatVecBatch */
+        for (int i = 0; i < D; i++)
+            x[i] += m.gate[i];
+        memcpy(normed, x, sizeof(float) * D);
+        rms_norm(normed, lw[QL_FFN_NORM], D, eps);
+        quantize_column(normed, D, m.nq, m.ns, m.nc);
+        in_parallel(F / 32, 2L * F * D, threads, qwen_ffn_section, &m);
+        in_parallel(D, (long)D * F, threads, qwen_rows_down, &m);  /* Down.MatVecBatch */
+        for (int i = 0; i < D; i++)
+            x[i] += m.up[i];
+        (void)PER_POSITION;  /* a batch of one: the per-position sections run on the caller */
+    }
+    rms_norm(x, output_norm, D, eps);
+    int8_t *kq = malloc(D);
+    float *ks = malloc(sizeof(float) * D / 256);
+    int16_t *bs = malloc(sizeof(int16_t) * D / 16);
+    quantize_k(x, D, kq, ks, bs);
+    struct q6_args a = {head, kq, bs, ks, D, 1, vocab, logits};
+    in_parallel(vocab, (long)vocab * D, threads, q6_rows, &a);
+    free(kq), free(ks), free(bs), free(normed);
+    free(m.nq), free(m.ns), free(m.nc), free(m.qh), free(m.hk), free(m.hv), free(m.sq), free(m.ss), free(m.sc);
+    free(m.set), free(m.scores), free(m.gate), free(m.up), free(m.mq), free(m.msc), free(m.mc);
+    return 0;
+}

@@ -146,3 +146,72 @@ def test_packed_q4_0_against_portable(rows, cols, size):
         bc = oracle.Batch(b.F[c:c + 1]).quantize()
         alone = oracle.cpu_mat_vec_packed_q4_0(packed, bc, rows, threads)
         np.testing.assert_array_equal(alone[0].view(np.uint32), got[c].view(np.uint32))
+
+
+def test_moe_ffn_against_portable():
+    """Route + ExpertFFN through golem's x86 kernels (the CPU baseline of
+    config 4) against the oracle's generic restatement: the same experts
+    and routing weights (the logits differ only in DotF32's summation order:
+    dotF32AVX2 against the generic four chains), and the output within 1e-3
+    of RMS (golem's own AVX2-against-Go bar, dot_q4_0_avx2_test.go:68)."""
+    D, F, E, k, batch = 256, 64, 16, 4, 3
+    g = synth.rng(440)
+    router = (g.standard_normal((E, D)) * 0.02).astype(np.float32)
+    gate_up = synth.q4_0_weights(g, E * 2 * F, D)
+    down = synth.q4_0_weights(g, E * D, F)
+    resid = synth.activations(g, batch, D)
+    moe = oracle.CpuMoE(router, gate_up, down, D, F, E, k, batch)
+    out, ids, wts = moe.run(resid, 2)
+    gu_b, dn_b = 2 * F * (D // 32) * 18, D * (F // 32) * 18
+    for t in range(batch):
+        _, want_ids, want_w = oracle.route_one(resid[t], router, k)
+        assert list(ids[t]) == list(want_ids), (t, ids[t], want_ids)
+        np.testing.assert_allclose(wts[t], want_w, rtol=1e-5)
+        parts = [oracle.expert_unit(gate_up[i * gu_b:(i + 1) * gu_b], down[i * dn_b:(i + 1) * dn_b], resid[t], D, F)
+                 for i in want_ids]
+        want = oracle.expert_reduce(np.stack(parts), want_ids, want_w, D)
+        rel, at = oracle.compare_floats(out[t], want)
+        assert rel <= 1e-3, f"position {t}: {rel:.3g} of RMS at {at}"
+    # every thread count gives the same bits (the sections' splits change nothing)
+    one, _, _ = moe.run(resid, 1)
+    one = one.copy()
+    many, _, _ = moe.run(resid, 8)
+    np.testing.assert_array_equal(one.view(np.uint32), many.view(np.uint32))
+
+
+def test_qwen_token_against_portable():
+    """golem's Qwen3 decode token through its x86 kernels (the CPU baseline of
+    config 3) against the oracle's generic restatement of the engine, fed the
+    same caches: the hidden state after the final norm within 1e-3 of RMS
+    (golem's AVX2-against-Go bar; DotF32's and Axpy's orders differ) and the
+    logits' greedy id equal; two thread counts give the same bits."""
+    import math
+    from oracle.qwen import QwenOracle
+    cfg = synth.QwenConfig(256, 512, 2, 4, 2, 64, 1024, 16)
+    w = synth.qwen_weights(cfg, 450, symmetric=True)
+    om = QwenOracle(cfg, w)
+    prompt = [int(t) for t in synth.rng(451).integers(0, cfg.vocab, 6)]
+    om.reset()
+    om.forward(prompt, 0)
+    cpu = oracle.CpuQwen(cfg, w)
+    for L, (kc, vc) in enumerate(cpu.caches):
+        kc[:] = om.K[L]
+        vc[:] = om.V[L]
+    tok, pos = 17, len(prompt)
+    lib = oracle.load()
+    cos, sin = np.zeros(cfg.head_dim // 2, np.float32), np.zeros(cfg.head_dim // 2, np.float32)
+    lib.orc_rope_prepare(cfg.head_dim, pos, cfg.rope_base, oracle._p(cos), oracle._p(sin))
+    x = om.embed(tok).astype(np.float32).copy()
+    logits = cpu.token(x, pos, cos, sin, 2).copy()
+    want = om.forward([tok], pos)[0]
+    rel, at = oracle.compare_floats(x, want)
+    assert rel <= 1e-3, f"hidden state {rel:.3g} of RMS at {at}"
+    want_logits = om.logits(want)
+    assert int(np.argmax(logits)) == int(np.argmax(want_logits))
+    # the caches hold the position's key and value as golem stores them
+    for L, (kc, vc) in enumerate(cpu.caches):
+        assert oracle.compare_floats(kc[pos], om.K[L][pos])[0] <= 1e-3
+    x2 = om.embed(tok).astype(np.float32).copy()
+    cpu.token(x2, pos, cos, sin, 8)
+    np.testing.assert_array_equal(x.view(np.uint32), x2.view(np.uint32))
+    assert math.isfinite(float(logits.max()))
