@@ -2,8 +2,9 @@
 //
 // ExpertFFN (gemma/moe.go:112-180) for M positions:
 //   Route (gemma/moe.go:34-53): x = RMSNormPlain(resid) * (1/sqrt(Dim)) *
-//     RouterScale, router logits = DotF32(router row, x) in golem's generic
-//     order, chooseExperts (moe.go:62-88): top_k by repeated argmax (strict >,
+//     RouterScale, router logits = DotF32(router row, x) in the order golem
+//     runs it on x86 (dotF32AVX2), chooseExperts (moe.go:62-88): top_k by
+//     repeated argmax (strict >,
 //     ties to the lower index), weights exp(l - top) in float64, renormalised.
 //   Units (position t, slot k): gate_up = GateUp[id] . Q8_0(x_t) (2*ffn rows,
 //     gate first), mid = GELUTable(gate) * up, quantised to Q8_0,
@@ -23,10 +24,15 @@ namespace {
 
 // The router.
 //
-// Logits: DotF32 (nn/dot_f32.go:13-33) is four serial chains -- chain c adds
-// the products of elements c, c+4, c+8, ... in order -- that meet as
-// (s0 + s1) + (s2 + s3).  A lane runs one chain in that order, so the logits
-// are golem's bits.  RMSNormPlain (nn/ops.go:195-214) squares in float32 and
+// Logits: DotF32 on an amd64 host with AVX2 (nn/dot_f32.go:18-20) is
+// dotF32AVX2 (nn/dot_f32_amd64.s:43-113): 32 chains -- lane j of its four
+// eight-lane registers adds the product of element 32g + j of every group of
+// 32, each product rounded before the add -- then lanes j + 8 onto j and j +
+// 24 onto j + 16, those two, lanes j + 4, pairs (0, 2) and (1, 3), and the
+// last two (dot_f32_avx2_combine).  A lane runs one chain, so the logits are
+// golem's x86 bits, from chains of D/32 steps where the generic form's four
+// chains take D/4.  (The router's width is a multiple of 64: no eights, no
+// tail.)  RMSNormPlain (nn/ops.go:195-214) squares in float32 and
 // sums in float64, here in a fixed tree: 512 partial sums, partial t holding
 // elements t, t+512, t+1024, ... in order, then halved pairwise (t + w for
 // w = 256 .. 1).  golem sums left to right; the two float64 sums differ by a
@@ -37,15 +43,14 @@ namespace {
 //   moe_route_one_kernel: one workgroup per (expert, position) for few
 //     positions (decode), where the cost is latency: the row and the input
 //     are read with every load issued at once, the products are formed by
-//     all threads into LDS chain by chain, and four lanes run the chains.
+//     all threads into LDS, and 32 lanes run the chains.
 //     The workgroup that finishes a position's last logit (a counter per
 //     position, kept by the context) then chooses its experts, so routing
 //     is one launch.
 //   moe_norm_scale_kernel + moe_logits_kernel: the norm scales once per
-//     position, then 4 experts x 8 positions per workgroup, a lane one
-//     chain; rows and inputs pass through LDS 512 inputs at a time,
-//     transposed chain by chain.  Many positions; the choosing is
-//     moe_topk_kernel.
+//     position, then 8 experts x 16 positions per workgroup, a lane one
+//     chain of four positions' logits; rows and inputs pass through LDS 256
+//     inputs at a time.  Many positions; the choosing is moe_topk_kernel.
 constexpr int kLogitsThreads = 256;
 constexpr int kLogitsChunk = 64;     // the router's width is a multiple of this
 constexpr int kLogitsOneMaxD = 7168; // input + products in LDS: 57 KB
@@ -54,6 +59,18 @@ constexpr int kTopkMaxPerLane = 16;  // E <= 1024
 constexpr int kTopkMax = 64;         // k <= 64
 constexpr int kUnitMaxPos = 4;       // positions whose units run as matrix-vector products
 constexpr int kGroupTok = 32;        // units of a grouped product's work item (its token tile)
+
+// dotF32AVX2's end (nn/dot_f32_amd64.s:79-99) over the 32 chains held by the
+// lanes of an aligned 32-lane group (chain j in lane j): Y0 + Y1 and Y2 + Y3
+// lane by lane, then their sum, then lanes j and j + 4, then (0, 2) and
+// (1, 3), then the two.  The result is in the group's first lane.
+__device__ __forceinline__ float dot_f32_avx2_combine(float acc) {
+    const float t = acc + __shfl_down(acc, 8, 32);   // lanes 0..7: Y0 + Y1; 16..23: Y2 + Y3
+    const float v = t + __shfl_down(t, 16, 32);      // lanes 0..7: (Y0 + Y1) + (Y2 + Y3)
+    const float w = v + __shfl_down(v, 4, 32);       // lanes 0..3
+    const float x = w + __shfl_down(w, 2, 32);       // lanes 0..1
+    return x + __shfl_down(x, 1, 32);                // lane 0
+}
 
 // chooseExperts (gemma/moe.go:62-88) for one position, by a whole workgroup
 // of at least 64 threads.  golem takes k rounds of an argmax that scans in
@@ -196,8 +213,8 @@ __global__ __launch_bounds__(kLogitsThreads) void moe_route_one_kernel(
     const float *__restrict__ router, int D, int E, const float *__restrict__ router_scale,
     const float *__restrict__ resid, int ldr, float eps, int k, float *__restrict__ logits,
     int32_t *__restrict__ ids, float *__restrict__ weights, unsigned *__restrict__ count) {
-    // LDS: the input [max(D, E32)], then the chains' products [4][cs] (later
-    // the logits' keys [E32] as uint64)
+    // LDS: the input [max(D, E32)], then the products [D] in element order
+    // (later the logits' keys [E32] as uint64)
     extern __shared__ __align__(16) float lds[];
     __shared__ double red[kLogitsThreads];
     __shared__ float scale_sh;
@@ -208,8 +225,6 @@ __global__ __launch_bounds__(kLogitsThreads) void moe_route_one_kernel(
     const int E32 = (E + 31) & ~31;
     float *xr = lds;
     float *P = lds + max(D, E32);
-    const int cn = (D / 16 + 7) & ~7;  // float4s of a chain, padded to a multiple of 8
-    const int cs = 4 * cn + 4;         // a chain's stride in floats: the four chains start in different banks
     const float *rg = router + (size_t)e * D;
     const float *xg = resid + (size_t)t * ldr;
     const int n4 = D / 4;
@@ -239,93 +254,66 @@ __global__ __launch_bounds__(kLogitsThreads) void moe_route_one_kernel(
     const float sc = scale_sh;
     const float inv_sqrt_dim = (float)(1.0 / sqrt((double)D));
     // The products row[i] * ((x[i] * scale) * ((1/sqrt(D)) * RouterScale[i])),
-    // element 4j + c at P[c * cs + j].
+    // in element order.
 #pragma unroll
     for (int f = 0; f <= kLogitsOneF4; f++) {
         const int q = tid + f * kLogitsThreads;
         const float x4[4] = {xv[f].x, xv[f].y, xv[f].z, xv[f].w}, s4[4] = {sv[f].x, sv[f].y, sv[f].z, sv[f].w};
         const float r4[4] = {rv[f].x, rv[f].y, rv[f].z, rv[f].w};
         if (q < n4) {
+            float4 pv;
+            float *pp = (float *)&pv;
 #pragma unroll
             for (int c = 0; c < 4; c++) {
                 const float normed = x4[c] * sc;
                 const float factor = inv_sqrt_dim * s4[c];
                 const float xn = normed * factor;
-                P[c * cs + q] = r4[c] * xn;
+                pp[c] = r4[c] * xn;
             }
-        } else if (q < 4 * cn) {
-#pragma unroll
-            for (int c = 0; c < 4; c++)
-                P[c * cs + q] = 0.0f;
+            *(float4 *)(P + 4 * q) = pv;
         }
     }
     __syncthreads();
     if (tid < 64) {
+        // chain tid (lanes 0..31): products tid, tid + 32, ... in order, eight
+        // read ahead of the dependent adds
         float acc = 0.0f;
-        if (tid < 4) {
-            // Chain tid: its products in order, 32 at a time from two
-            // buffers, each refilled while the other is added (a copy from
-            // one to the other would wait for the refill), so the LDS
-            // latency stays behind the dependent adds.  The chain is padded
-            // with +0 products to a multiple of 32, which leave a sum that
-            // starts from +0 unchanged.
-            const float4 *pc = (const float4 *)(P + tid * cs);
-            float4 A[8], Bq[8];
+        const int steps = D / 32;
+        const float *pc = P + (tid & 31);
+        float a[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            a[u] = pc[32 * min(u, steps - 1)];
+        for (int g = 0; g < steps; g += 8) {
+            float b[8];
 #pragma unroll
             for (int u = 0; u < 8; u++)
-                A[u] = pc[u];
-            for (int j = 0;; j += 16) {
-                const bool more = j + 8 < cn;
-                if (more) {
+                b[u] = pc[32 * min(g + 8 + u, steps - 1)];
 #pragma unroll
-                    for (int u = 0; u < 8; u++)
-                        Bq[u] = pc[j + 8 + u];
-                }
+            for (int u = 0; u < 8; u++)
+                if (g + u < steps)
+                    acc = acc + a[u];
 #pragma unroll
-                for (int u = 0; u < 8; u++) {
-                    acc = acc + A[u].x;
-                    acc = acc + A[u].y;
-                    acc = acc + A[u].z;
-                    acc = acc + A[u].w;
-                }
-                if (!more)
-                    break;
-                const bool more2 = j + 16 < cn;
-                if (more2) {
-#pragma unroll
-                    for (int u = 0; u < 8; u++)
-                        A[u] = pc[j + 16 + u];
-                }
-#pragma unroll
-                for (int u = 0; u < 8; u++) {
-                    acc = acc + Bq[u].x;
-                    acc = acc + Bq[u].y;
-                    acc = acc + Bq[u].z;
-                    acc = acc + Bq[u].w;
-                }
-                if (!more2)
-                    break;
-            }
+            for (int u = 0; u < 8; u++)
+                a[u] = b[u];
         }
-        const float s1 = __shfl_down(acc, 1, 64), s2 = __shfl_down(acc, 2, 64), s3 = __shfl_down(acc, 3, 64);
+        const float logit = dot_f32_avx2_combine(acc);
         if (tid == 0) {
-            // The logit is stored at device scope (through to the level all
-            // XCDs share, not held in this XCD's L2) and the store has
-            // completed before it is counted, so no device-wide release
-            // (an L2 write-back per workgroup) is needed.  The counter wraps
+            // The logit is stored at device scope, then counted with a
+            // device-scope release: the counter's increments form a release
+            // sequence, so the workgroup that takes the last count (and
+            // issues the acquire below) sees every logit.  The counter wraps
             // to 0 on the position's last count, ready for the next launch.
-            __hip_atomic_store(logits + (size_t)t * E + e, (acc + s1) + (s2 + s3), __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-            __builtin_amdgcn_s_waitcnt(0);
-            last_sh = atomicInc(count + t, (unsigned)(E - 1)) == (unsigned)(E - 1);
+            __hip_atomic_store(logits + (size_t)t * E + e, logit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            last_sh = __builtin_amdgcn_atomic_inc32(count + t, (unsigned)(E - 1), __ATOMIC_RELEASE, "agent") ==
+                      (unsigned)(E - 1);
         }
     }
     __syncthreads();
     if (!last_sh)
         return;
-    // The position's last logit: every other workgroup's has completed at
-    // device scope; they are read at device scope after this XCD's caches
-    // are invalidated.
+    // The position's last logit: the acquire pairs with every workgroup's
+    // release of its count; the logits are read at device scope.
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     const float *lt = logits + (size_t)t * E;
     uint64_t *comp = (uint64_t *)P;  // the products are spent
@@ -389,79 +377,77 @@ __global__ __launch_bounds__(256) void moe_norm_scale_kernel(const float *__rest
         scale[t] = norm_scale(s, D, eps);
 }
 
-// The logits: EW experts x P positions a workgroup (4 EW P threads), a lane
-// one chain (lane = chain c + 4 (expert + EW position)).  The inputs pass
-// through LDS CH at a time, transposed so that each chain's CH/4 elements of
-// a chunk are contiguous (one 16-byte read per lane for four of its steps),
-// double buffered: the next chunk's global loads are in flight while this
-// one is summed.  Eight experts a workgroup read each position's inputs for
-// twice the chains of four, and a thread's router-scale piece is the same
-// for every position it stages (its chunk offset is tid % (CH/4)): one load
-// (EW 4 with a load per staged piece moved ~36 KB a chunk through each
-// workgroup for 1,024 chains, 18 us at config 4's 256 positions).
+// The logits: EW experts x P positions a workgroup (32 EW G threads), a lane
+// one of the 32 chains of P / G logits (lane = chain j + 32 (expert + EW
+// group)): group g holds positions g, g + G, ... so that each router element
+// read from LDS serves P / G positions.  Rows and inputs pass through LDS CH
+// at a time, double buffered (the next chunk's global loads are in flight
+// while this one is summed); chain j adds the products of the chunk's
+// elements j, j + 32, ... in order, and a logit's 32 lanes meet as
+// dotF32AVX2 ends.
 constexpr int kLgEW = 8;
 
-template <int P, int CH>
-__global__ __launch_bounds__(4 * kLgEW * P) void moe_logits_kernel(const float *__restrict__ router, int D, int E,
-                                                                  const float *__restrict__ router_scale,
-                                                                  const float *__restrict__ resid, int ldr, int M,
-                                                                  const float *__restrict__ scales,
-                                                                  float *__restrict__ logits) {
-    constexpr int NT = 4 * kLgEW * P, ST = CH / 4, PAD = ST + 4;
-    constexpr int RF4 = (kLgEW * ST + NT - 1) / NT, XF4 = P * ST / NT;  // staged float4 per thread per chunk
-    static_assert(P * ST % NT == 0 && NT % ST == 0, "chunk shape");
-    __shared__ __align__(16) float Rs[2][kLgEW][4][PAD];
-    __shared__ __align__(16) float Xs[2][P][4][PAD];
+template <int P, int G, int CH>
+__global__ __launch_bounds__(32 * kLgEW * G) void moe_logits_kernel(const float *__restrict__ router, int D, int E,
+                                                                   const float *__restrict__ router_scale,
+                                                                   const float *__restrict__ resid, int ldr, int M,
+                                                                   const float *__restrict__ scales,
+                                                                   float *__restrict__ logits) {
+    constexpr int NT = 32 * kLgEW * G, Q = CH / 4, PG = P / G;  // threads; float4s of a row's chunk
+    constexpr int RF = (kLgEW * Q + NT - 1) / NT, XF = (P * Q + NT - 1) / NT;  // staged float4s a thread
+    static_assert(CH % 32 == 0 && P % G == 0, "whole groups of 32 a chunk, whole position groups");
+    __shared__ __align__(16) float Rs[2][kLgEW][CH];
+    __shared__ __align__(16) float Xs[2][P][CH];
     const int tid = threadIdx.x;
     const int e0 = blockIdx.x * kLgEW, t0 = blockIdx.y * P;
-    const int c = tid & 3, e = (tid >> 2) % kLgEW, p = tid / (4 * kLgEW);  // this lane's chain
+    const int j = tid & 31, e = (tid >> 5) % kLgEW, g = tid / (32 * kLgEW);  // this lane's chains
     const float inv_sqrt_dim = (float)(1.0 / sqrt((double)D));
 
-    // This thread's staging: row pieces idx = tid + NT f (expert idx / ST,
-    // float4 idx % ST of the chunk) and input pieces likewise (position
-    // idx / ST); past D the pieces are zero.
-    float4 rv[RF4], xv[XF4], sv;
-    float sc[XF4];
+    // This thread's staging: row piece idx = tid + NT f (expert idx / Q,
+    // float4 idx % Q of the chunk), input piece likewise (position idx / Q);
+    // past D the pieces are zero.
+    float4 rv[RF], xv[XF], sv[XF];
+    float sc[XF];
 #pragma unroll
-    for (int f = 0; f < XF4; f++)
-        sc[f] = scales[min(t0 + (tid + NT * f) / ST, M - 1)];
+    for (int f = 0; f < XF; f++)
+        sc[f] = scales[min(t0 + min((tid + NT * f) / Q, P - 1), M - 1)];
     auto fetch = [&](int k) {
         const int i0 = k * CH;
 #pragma unroll
-        for (int f = 0; f < RF4; f++) {
-            const int idx = tid + NT * f, i = i0 + 4 * (idx % ST);
-            const float *rsrc = router + (size_t)min(e0 + min(idx / ST, kLgEW - 1), E - 1) * D;
+        for (int f = 0; f < RF; f++) {
+            const int idx = tid + NT * f, i = i0 + 4 * (idx % Q);
+            const float *rsrc = router + (size_t)min(e0 + min(idx / Q, kLgEW - 1), E - 1) * D;
             rv[f] = i < D ? *(const float4 *)(rsrc + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         }
 #pragma unroll
-        for (int f = 0; f < XF4; f++) {
-            const int idx = tid + NT * f, i = i0 + 4 * (idx % ST);
-            const float *xr = resid + (size_t)min(t0 + idx / ST, M - 1) * ldr;
+        for (int f = 0; f < XF; f++) {
+            const int idx = tid + NT * f, i = i0 + 4 * (idx % Q);
+            const float *xr = resid + (size_t)min(t0 + min(idx / Q, P - 1), M - 1) * ldr;
             xv[f] = i < D ? *(const float4 *)(xr + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            sv[f] = router_scale && i < D ? *(const float4 *)(router_scale + i) : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
         }
-        const int is = i0 + 4 * (tid % ST);  // every staged piece's offset in the chunk (NT % ST == 0)
-        sv = router_scale && is < D ? *(const float4 *)(router_scale + is) : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
     };
     auto put = [&](int buf) {
 #pragma unroll
-        for (int f = 0; f < RF4; f++) {
-            const int idx = tid + NT * f, ee = idx / ST, q = idx % ST;
-            const float r4[4] = {rv[f].x, rv[f].y, rv[f].z, rv[f].w};
-            if (idx < kLgEW * ST) {
-#pragma unroll
-                for (int cc = 0; cc < 4; cc++)
-                    Rs[buf][ee][cc][q] = r4[cc];
-            }
+        for (int f = 0; f < RF; f++) {
+            const int idx = tid + NT * f;
+            if (idx < kLgEW * Q)
+                *(float4 *)&Rs[buf][idx / Q][4 * (idx % Q)] = rv[f];
         }
 #pragma unroll
-        for (int f = 0; f < XF4; f++) {
-            const int idx = tid + NT * f, pp = idx / ST, q = idx % ST;
-            const float x4[4] = {xv[f].x, xv[f].y, xv[f].z, xv[f].w}, s4[4] = {sv.x, sv.y, sv.z, sv.w};
+        for (int f = 0; f < XF; f++) {
+            const int idx = tid + NT * f;
+            if (idx < P * Q) {
+                const float x4[4] = {xv[f].x, xv[f].y, xv[f].z, xv[f].w}, s4[4] = {sv[f].x, sv[f].y, sv[f].z, sv[f].w};
+                float4 o;
+                float *op = (float *)&o;
 #pragma unroll
-            for (int cc = 0; cc < 4; cc++) {
-                const float normed = x4[cc] * sc[f];
-                const float factor = inv_sqrt_dim * s4[cc];
-                Xs[buf][pp][cc][q] = normed * factor;
+                for (int cc = 0; cc < 4; cc++) {
+                    const float normed = x4[cc] * sc[f];
+                    const float factor = inv_sqrt_dim * s4[cc];
+                    op[cc] = normed * factor;
+                }
+                *(float4 *)&Xs[buf][idx / Q][4 * (idx % Q)] = o;
             }
         }
     };
@@ -470,38 +456,38 @@ __global__ __launch_bounds__(4 * kLgEW * P) void moe_logits_kernel(const float *
     fetch(0);
     put(0);
     __syncthreads();
-    float acc = 0.0f;
+    float acc[PG];
+#pragma unroll
+    for (int c = 0; c < PG; c++)
+        acc[c] = 0.0f;
     for (int k = 0; k < chunks; k++) {
         const int buf = k & 1;
         if (k + 1 < chunks)
             fetch(k + 1);
-        const float4 *rr = (const float4 *)Rs[buf][e][c];
-        const float4 *xx = (const float4 *)Xs[buf][p][c];
+        const float *rr = Rs[buf][e] + j;
+        const float *xx = Xs[buf][g] + j;
         // the chunk's steps in order; past D the products are +0, which
         // leave a sum that starts from +0 unchanged
-        for (int q4 = 0; q4 < ST / 4; q4 += 4) {
-            float4 a[4], b[4];
 #pragma unroll
-            for (int u = 0; u < 4; u++) {
-                a[u] = rr[q4 + u];
-                b[u] = xx[q4 + u];
-            }
+        for (int s = 0; s < CH / 32; s++) {
+            const float r = rr[32 * s];
 #pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const float p0 = a[u].x * b[u].x, p1 = a[u].y * b[u].y, p2 = a[u].z * b[u].z, p3 = a[u].w * b[u].w;
-                acc = acc + p0;
-                acc = acc + p1;
-                acc = acc + p2;
-                acc = acc + p3;
+            for (int c = 0; c < PG; c++) {
+                const float prod = r * xx[G * CH * c + 32 * s];
+                acc[c] = acc[c] + prod;
             }
         }
         if (k + 1 < chunks)
             put(buf ^ 1);  // the other buffer was last read in chunk k - 1
         __syncthreads();
     }
-    const float s1 = __shfl_down(acc, 1, 64), s2 = __shfl_down(acc, 2, 64), s3 = __shfl_down(acc, 3, 64);
-    if (c == 0 && t0 + p < M && e0 + e < E)
-        logits[(size_t)(t0 + p) * E + e0 + e] = (acc + s1) + (s2 + s3);
+#pragma unroll
+    for (int c = 0; c < PG; c++) {
+        const int p = g + G * c;
+        const float logit = dot_f32_avx2_combine(acc[c]);
+        if (j == 0 && t0 + p < M && e0 + e < E)
+            logits[(size_t)(t0 + p) * E + e0 + e] = logit;
+    }
 }
 
 // chooseExperts for many positions: one workgroup a position.
@@ -1281,9 +1267,8 @@ int launch_moe_route(gx_ctx *ctx, const gx_weight *router, const float *router_s
     GX_CHECK(((uintptr_t)resid & 15) == 0 && ldr % 4 == 0, "gx: resid must be 16-byte aligned with ldr %% 4 == 0");
     const float *rw = (const float *)router->dev;
     if (M <= kRouteMaxPos && D <= kLogitsOneMaxD) {
-        const size_t cn = ((size_t)D / 16 + 7) & ~(size_t)7;  // the kernel's chain layout
         const size_t E32 = (size_t)((E + 31) & ~31);
-        const size_t lds = sizeof(float) * (max((size_t)D, E32) + max(4 * (4 * cn + 4), 2 * E32));
+        const size_t lds = sizeof(float) * (max((size_t)D, E32) + max((size_t)D, 2 * E32));
         GX_CHECK(lds <= 64 * 1024, "gx: the router's %d inputs do not fit the one-launch kernel", D);
         moe_route_one_kernel<<<dim3((unsigned)E, (unsigned)M), kLogitsThreads, lds, ctx->stream>>>(
             rw, D, E, router_scale, resid, ldr, eps, k, logits, ids, weights, ctx->route_count);
@@ -1296,10 +1281,10 @@ int launch_moe_route(gx_ctx *ctx, const gx_weight *router, const float *router_s
         moe_norm_scale_kernel<<<(unsigned)((m + 3) / 4), 256, 0, ctx->stream>>>(rr, ldr, m, D, eps, ctx->route_scale);
         if (int rc = check_launch("moe_norm_scale"))
             return rc;
-        constexpr int P = 16, CH = 256;
+        constexpr int P = 16, G = 4, CH = 256;
         const dim3 grid((unsigned)((E + kLgEW - 1) / kLgEW), (unsigned)((m + P - 1) / P));
-        moe_logits_kernel<P, CH><<<grid, 4 * kLgEW * P, 0, ctx->stream>>>(rw, D, E, router_scale, rr, ldr, m,
-                                                                    ctx->route_scale, logits + (size_t)m0 * E);
+        moe_logits_kernel<P, G, CH><<<grid, 32 * kLgEW * G, 0, ctx->stream>>>(rw, D, E, router_scale, rr, ldr, m,
+                                                                        ctx->route_scale, logits + (size_t)m0 * E);
         if (int rc = check_launch("moe_logits"))
             return rc;
     }

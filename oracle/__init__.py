@@ -58,6 +58,7 @@ def load():
         "orc_mat_vec_q6_k_rows": (None, [V, V, V, V, I, I, I, V, I, I, I]),
         "orc_dequantize_q6_k": (None, [V, I, V]),
         "orc_dot_f32": (F, [V, V, I]),
+        "orc_dot_f32_avx2": (F, [V, V, I]),
         "orc_rope_prepare": (None, [I, I, ctypes.c_double, V, V]),
         "orc_rope_apply": (None, [V, I, V, V]),
         "orc_attend": (None, [V, V, V, I, I, I, I, F, V, V]),
@@ -254,6 +255,13 @@ def dot_f32(a, b):
     return load().orc_dot_f32(_p(a), _p(b), min(len(a), len(b)))
 
 
+def dot_f32_avx2(a, b):
+    """DotF32 in dotF32AVX2's order (the form golem runs on amd64)."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    return load().orc_dot_f32_avx2(_p(a), _p(b), min(len(a), len(b)))
+
+
 def rms_norm_plain(x, gain=None, eps=1e-6):
     x = np.array(x, dtype=np.float32)
     g = None if gain is None else np.ascontiguousarray(gain, dtype=np.float32)
@@ -376,6 +384,7 @@ def cpu_lib(threads=None):
         "cpu_qwen_token": (I, [V, I, I, I, I, I, I, I, I, F, V, V, V, V, I, V, V, I]),
         "cpu_dot_q4_0": (None, [V, V, V, V, I, I, I, I, V, I, I]),
         "cpu_dot_q6_k": (F, [V, V, V, V, I]),
+        "cpu_dot_f32": (F, [V, V, I]),
     }.items():
         fn = getattr(lib, name)
         fn.restype, fn.argtypes = res, args

@@ -1047,3 +1047,6 @@ int cpu_qwen_token(void *const *layers, int nlayers, int D, int F, int H, int KV
     free(m.set), free(m.scores), free(m.gate), free(m.up), free(m.mq), free(m.msc), free(m.mc);
     return 0;
 }
+
+/* dotF32AVX2, for the tests */
+float cpu_dot_f32(const float *a, const float *b, int n) { return n == 0 ? 0.0f : dot_f32_avx2(a, b, n); }

@@ -10,7 +10,7 @@ Test infrastructure only: the device path never calls it.
   out     = resid + RMSNormPlain(shared + experts, post_ffw_norm)
 
 The products are golem's Matrix.rows over Q8_0 batches (matrix_rows), the
-router golem's generic DotF32 order (route_one), the expert units and their
+router in DotF32's x86 (dotF32AVX2) order (route_one), the expert units and their
 sum orc_expert_unit / orc_expert_reduce.
 """
 import numpy as np

@@ -820,9 +820,51 @@ void orc_choose_experts(const float *logits, int experts, int used, int32_t *ids
         weights[k] /= total;
 }
 
+/* DotF32 as it runs on an amd64 host with AVX2 (nn/dot_f32.go:18-20):
+ * dotF32AVX2's order (nn/dot_f32_amd64.s:43-113).  Four registers of eight
+ * lanes, lane j of register r adding the product of element 32g + 8r + j of
+ * every whole group of 32 (each product rounded, then added: nothing fused);
+ * then Y0 + Y1 and Y2 + Y3, then their sum; then the remaining whole groups
+ * of eight into those eight lanes; then lanes j and j + 4, then pairs 0,2 and
+ * 1,3, then the two; then the remaining elements one at a time. */
+float orc_dot_f32_avx2(const float *a, const float *b, int n)
+{
+    if (n == 0)
+        return 0;
+    float y[32] = {0};
+    int i = 0;
+    for (; i + 32 <= n; i += 32)
+        for (int j = 0; j < 32; j++) {
+            float p = a[i + j] * b[i + j];
+            y[j] = y[j] + p;
+        }
+    float v[8];
+    for (int j = 0; j < 8; j++) {
+        float y01 = y[j] + y[j + 8];
+        float y23 = y[j + 16] + y[j + 24];
+        v[j] = y01 + y23;
+    }
+    for (; i + 8 <= n; i += 8)
+        for (int j = 0; j < 8; j++) {
+            float p = a[i + j] * b[i + j];
+            v[j] = v[j] + p;
+        }
+    float w[4];
+    for (int j = 0; j < 4; j++)
+        w[j] = v[j] + v[j + 4];
+    float x0 = w[0] + w[2], x1 = w[1] + w[3];
+    float s = x0 + x1;
+    for (; i < n; i++) {
+        float p = a[i] * b[i];
+        s = s + p;
+    }
+    return s;
+}
+
 /* Route, gemma/moe.go:34-53, for one position: RMSNormPlain without a gain,
  * times (1/sqrt(Dim)) * RouterScale[i], then the F32 router rows through
- * DotF32 (Matrix.rows F32 case, nn/matrix.go:113-120), then chooseExperts.
+ * DotF32 (Matrix.rows F32 case, nn/matrix.go:113-120) in the order golem
+ * runs it on x86 (orc_dot_f32_avx2), then chooseExperts.
  * router_scale may be NULL (all ones).  logits receives `experts` values. */
 void orc_route_one(const float *resid, int dim, const float *router /*[experts][dim]*/, const float *router_scale,
                    int experts, int used, float eps, float *scratch /*dim*/, float *logits, int32_t *ids,
@@ -834,7 +876,7 @@ void orc_route_one(const float *resid, int dim, const float *router /*[experts][
     for (int i = 0; i < dim; i++)
         scratch[i] *= scale * (router_scale ? router_scale[i] : 1.0f);
     for (int e = 0; e < experts; e++)
-        logits[e] = orc_dot_f32(router + (size_t)e * dim, scratch, dim);
+        logits[e] = orc_dot_f32_avx2(router + (size_t)e * dim, scratch, dim);
     orc_choose_experts(logits, experts, used, ids, weights);
 }
 

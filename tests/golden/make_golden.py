@@ -4,7 +4,7 @@ to the device path shows up against fixed vectors.
 
 golem's own quant fixtures (testdata/gemma/quants) are absent from the
 reference, so these vectors come from this project's oracle (the C
-restatement of golem's generic Go path, oracle/oracle.c), whose functions are
+restatement of golem's engine, oracle/oracle.c), whose functions are
 pinned by golem's known answers and by closed forms in
 tests/test_oracle_*.py.  Inputs are drawn exactly as bench.py draws configs
 0, 1 and 4 (golem_amd/synth.py), then cut:
@@ -13,7 +13,8 @@ tests/test_oracle_*.py.  Inputs are drawn exactly as bench.py draws configs
       its activation: Q8_0 form, golem's per-block accumulators, y
   c1  the first 64 rows of config 1's Q6_K head (151936 x 2560, seed 1) and
       its activation: Q8_K form, per-superblock integers, y
-  c4  a router of 128 experts over 256 inputs (seed 4): logits, the top 8
+  c4  a router of 128 experts over 256 inputs (seed 4): logits in golem's
+      x86 DotF32 order (dotF32AVX2), the top 8
       and their weights (Route / chooseExperts)
 
 Run from the repository root: python tests/golden/make_golden.py"""

@@ -151,9 +151,9 @@ def test_packed_q4_0_against_portable(rows, cols, size):
 def test_moe_ffn_against_portable():
     """Route + ExpertFFN through golem's x86 kernels (the CPU baseline of
     config 4) against the oracle's generic restatement: the same experts
-    and routing weights (the logits differ only in DotF32's summation order:
-    dotF32AVX2 against the generic four chains), and the output within 1e-3
-    of RMS (golem's own AVX2-against-Go bar, dot_q4_0_avx2_test.go:68)."""
+    and routing weights bit for bit (both route through DotF32's x86 order,
+    dotF32AVX2), and the output within 1e-3 of RMS (golem's own
+    AVX2-against-Go bar, dot_q4_0_avx2_test.go:68)."""
     D, F, E, k, batch = 256, 64, 16, 4, 3
     g = synth.rng(440)
     router = (g.standard_normal((E, D)) * 0.02).astype(np.float32)
@@ -166,7 +166,7 @@ def test_moe_ffn_against_portable():
     for t in range(batch):
         _, want_ids, want_w = oracle.route_one(resid[t], router, k)
         assert list(ids[t]) == list(want_ids), (t, ids[t], want_ids)
-        np.testing.assert_allclose(wts[t], want_w, rtol=1e-5)
+        np.testing.assert_array_equal(np.asarray(wts[t]).view(np.uint32), np.asarray(want_w).view(np.uint32))
         parts = [oracle.expert_unit(gate_up[i * gu_b:(i + 1) * gu_b], down[i * dn_b:(i + 1) * dn_b], resid[t], D, F)
                  for i in want_ids]
         want = oracle.expert_reduce(np.stack(parts), want_ids, want_w, D)
@@ -215,3 +215,17 @@ def test_qwen_token_against_portable():
     cpu.token(x2, pos, cos, sin, 8)
     np.testing.assert_array_equal(x.view(np.uint32), x2.view(np.uint32))
     assert math.isfinite(float(logits.max()))
+
+
+@pytest.mark.parametrize("n", [1, 7, 8, 9, 31, 32, 33, 40, 64, 100, 703, 704, 2816, 4099])
+def test_dot_f32_avx2_order_against_the_instructions(n):
+    """orc_dot_f32_avx2 (the router's DotF32, restated as scalar C in
+    dotF32AVX2's order) against the AVX2 instructions themselves
+    (cpu_avx2.c: VMULPS / VADDPS in the kernel's register order): bit for
+    bit, every length class -- whole groups of 32, eights, a tail."""
+    g = synth.rng(460 + n)
+    a = (g.standard_normal(n) * 3).astype(np.float32)
+    b = (g.standard_normal(n) * 0.02).astype(np.float32)
+    want = np.float32(oracle.cpu_lib().cpu_dot_f32(oracle._p(a), oracle._p(b), n))
+    got = np.float32(oracle.dot_f32_avx2(a, b))
+    assert got.view(np.uint32) == want.view(np.uint32), (n, got, want)

@@ -1,7 +1,7 @@
 """The expert branch of golem's mixture of experts (gemma/moe.go:34-180)
 against the oracle.
 
-Selection: router logits bit for bit (golem's generic DotF32 order) and the
+Selection: router logits bit for bit (golem's x86 DotF32 order, dotF32AVX2) and the
 chosen experts identical; the 8th/9th logit margin is logged, as
 gemma/moe_reference_test.go:117-136 does for its greedy ties.
 Outputs: within 2e-5 of RMS (the benchmark's bar for config 4), for the

@@ -181,3 +181,21 @@ def test_dot_f32_generic_order(orc):
         exact = float(np.dot(a.astype(np.float64), b.astype(np.float64)))
         bound = n * 2 ** -23 * float(np.sum(np.abs(a.astype(np.float64) * b)))
         assert abs(got - exact) <= bound + 1e-30
+
+
+def test_dot_f32_avx2_order_bounds(orc):
+    """dotF32AVX2's order (the router's DotF32) against float64: within the
+    standard bound n * eps * sum|a b| of a float32 sum; exact on small
+    integers; and it is not the generic order's chain (a mistake that summed
+    in the generic order would pass the bound but not the instructions' bits,
+    test_cpu_baseline.py)."""
+    g = np.random.default_rng(5)
+    for n in (5, 64, 2816, 3000):
+        a = (g.standard_normal(n) * 3).astype(np.float32)
+        b = (g.standard_normal(n) * 0.02).astype(np.float32)
+        exact = float(np.dot(a.astype(np.float64), b.astype(np.float64)))
+        bound = n * 2.0 ** -24 * float(np.sum(np.abs(a.astype(np.float64) * b)))
+        assert abs(orc.dot_f32_avx2(a, b) - exact) <= bound
+    a = np.arange(1, 97, dtype=np.float32)
+    b = np.ones(96, dtype=np.float32)
+    assert orc.dot_f32_avx2(a, b) == float(96 * 97 // 2)
