@@ -531,11 +531,13 @@ static int q4_0_product(gx_ctx *ctx, const gx_weight *w, int expert, const int8_
         return ok();
     const uint8_t *mat = w->dev + (size_t)expert * w->matrix_bytes;
     GX_CHECK(((uintptr_t)q16 & 15) == 0, "gx: q16 must be 16-byte aligned");
+    // Every batch runs on int8 MFMA, q16 or not: the fp16-MFMA kernel is
+    // slower at every M measured (config 2, M = 64 / 512 / 2048: 34.5 / 96.9
+    // / 269.8 us against 16.7 / 55.5 / 186.0) and moves 2.6x its bytes; it
+    // stays reachable for the parity checks (gx_q4_0_block_dots path 2).
     int rc;
     if (M <= 16)
         rc = gx::launch_q4_0_matvec(ctx, w, mat, q, scales, qsum, M, row_start, row_end, bias, y, ldy, nullptr, -1);
-    else if (q16)
-        rc = gx::launch_q4_0_gemm_f16(ctx, w, mat, q16, scales, M, row_start, row_end, bias, y, ldy, nullptr);
     else
         rc = gx::launch_q4_0_gemm(ctx, w, mat, q, scales, M, row_start, row_end, bias, y, ldy, nullptr);
     if (rc)

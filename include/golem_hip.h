@@ -154,8 +154,9 @@ int gx_quantize_q8_k(gx_ctx *ctx, const float *x, int ldx, int M, int K, int8_t 
  * rows floats (device).  One column runs a bandwidth-bound matrix-vector
  * kernel (activation in scalar registers, or in LDS on quarter tiles for a
  * matrix of few tiles); 2..16 columns the few-column int8-MFMA kernel
- * (16 rows against 16 columns a block); larger M a tiled MFMA product: on
- * fp16 MFMA when q16 is given, else on int8 MFMA.  All of them sum every
+ * (16 rows against 16 columns a block); larger M a tiled product on int8
+ * MFMA.  q16 may be NULL and is not read: the fp16-MFMA form is slower at
+ * every M and runs only as gx_q4_0_block_dots path 2.  All of them sum every
  * row's blocks in the same order
  * from the same exact per-block integers, so a column's result does not
  * depend on M or on the kernel. */

@@ -75,7 +75,7 @@ class Device:
 
     def matmul_q4_0(self, w, act, M, start=0, end=None, bias=None, y=None, f16=True):
         """act is quantize_q8_0's tuple (or its first four entries, sliced);
-        f16=False withholds q16 so that a batch runs the int8-MFMA kernel."""
+        f16=False withholds q16 (the product runs on int8 MFMA either way)."""
         q, sc, qs, q16 = act[:4]
         end = w.rows if end is None else end
         if y is None:

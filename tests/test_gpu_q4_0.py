@@ -246,8 +246,9 @@ def test_row_ranges_and_bias(dev, orc, span):
 @pytest.mark.parametrize("rows,cols", [(9728, 2560), (2560, 9728), (2816, 704), (200, 2816)])
 def test_batch_equals_one_at_a_time(dev, orc, rows, cols, f16):
     """Every column of a batch -- one column on the matrix-vector kernel, 2..16
-    on the few-column MFMA kernel, larger M on the fp16-MFMA (f16) or
-    int8-MFMA kernel -- is bit-identical to the same column computed alone."""
+    on the few-column MFMA kernel, larger M on the int8-MFMA kernel, with the
+    fp16 copy given (f16) or withheld: the product reads only the int8 form
+    either way -- is bit-identical to the same column computed alone."""
     M = 70
     g = synth.rng(400 + rows)
     w = synth.q4_0_weights(g, rows, cols)
