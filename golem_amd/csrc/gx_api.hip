@@ -949,8 +949,8 @@ int gx_qwen_attention_heads(gx_ctx *ctx, const uint16_t *qh, int M, int heads, i
         return rc;
     GX_CHECK(heads > 0 && kv_heads > 0 && heads % kv_heads == 0, "gx: %d query heads over %d key-value heads", heads,
              kv_heads);
-    GX_CHECK(M > 0 && M <= 4 && max_pos >= 0 && max_pos < 768, "gx: the head outputs are for a decode step (M <= 4, "
-                                                                "prefixes to 768)");
+    GX_CHECK(M > 0 && max_pos >= 0 && max_pos < (M <= 4 ? 768 : 1024),
+             "gx: the head outputs are for a decode step (M <= 4, prefixes to 768) or a prompt (prefixes to 1024)");
     GX_CHECK(head_dim == 32 || head_dim == 64 || head_dim == 96 || head_dim == 128,
              "gx: attention supports head widths 32, 64, 96 and 128");
     GX_CHECK(context % 8 == 0 && max_pos < context, "gx: a cache of %d positions (a multiple of 8) cannot hold %d",

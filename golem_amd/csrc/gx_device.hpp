@@ -62,6 +62,73 @@ __device__ __forceinline__ int32_t nearest_int(float f) {
     return (int32_t)(__float_as_uint(s) & 0x007fffffu) - 0x00400000;
 }
 
+// (float)exp((double)d) for d <= 0 (a softmax's s - max, as SoftmaxInPlace
+// takes it, nn/ops.go:59-73), as straight-line float64 arithmetic so that
+// several exponentials interleave: n = rint(d log2 e), r = d - n ln2 (ln2
+// split hi + lo, the first product exact), e^r by Horner's rule on the Taylor
+// series to r^13 (|r| <= 0.347: truncation below 1e-17), scaled by 2^n, then
+// rounded to float.  Below -110 (under float's least subnormal) and at -inf
+// the result is +0; a NaN stays NaN.  Over every float in [-110, 0] it
+// equals (float)exp((double)d) of a correctly rounded float64 exp, bit for
+// bit (checked exhaustively on the host against the C library); the same
+// steps in C are the oracle's orc_exp_neg.
+__device__ __forceinline__ float exp_neg(float df) {
+    const double d = (double)df;
+    const double n = __builtin_rint(d * 1.4426950408889634);
+    double r = __builtin_fma(-n, 6.93147180369123816490e-01, d);
+    r = __builtin_fma(-n, 1.90821492927058770002e-10, r);
+    double p = 1.0 / 6227020800.0;
+    p = __builtin_fma(p, r, 1.0 / 479001600.0);
+    p = __builtin_fma(p, r, 1.0 / 39916800.0);
+    p = __builtin_fma(p, r, 1.0 / 3628800.0);
+    p = __builtin_fma(p, r, 1.0 / 362880.0);
+    p = __builtin_fma(p, r, 1.0 / 40320.0);
+    p = __builtin_fma(p, r, 1.0 / 5040.0);
+    p = __builtin_fma(p, r, 1.0 / 720.0);
+    p = __builtin_fma(p, r, 1.0 / 120.0);
+    p = __builtin_fma(p, r, 1.0 / 24.0);
+    p = __builtin_fma(p, r, 1.0 / 6.0);
+    p = __builtin_fma(p, r, 0.5);
+    p = __builtin_fma(p, r, 1.0);
+    p = __builtin_fma(p, r, 1.0);
+    const float out = (float)__builtin_ldexp(p, (int)n);
+    return d < -110.0 ? 0.0f : out;
+}
+
+// exp_neg of N values, the steps written for all N in turn: N independent
+// float64 chains side by side, each value's bits exp_neg's.
+template <int N>
+__device__ __forceinline__ void exp_neg_n(const float *df, float *out) {
+    constexpr double c[12] = {1.0 / 479001600.0, 1.0 / 39916800.0, 1.0 / 3628800.0, 1.0 / 362880.0,
+                              1.0 / 40320.0,     1.0 / 5040.0,     1.0 / 720.0,     1.0 / 120.0,
+                              1.0 / 24.0,        1.0 / 6.0,        0.5,             1.0};
+    double d[N], n[N], r[N], p[N];
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+        d[i] = (double)df[i];
+        n[i] = __builtin_rint(d[i] * 1.4426950408889634);
+    }
+#pragma unroll
+    for (int i = 0; i < N; i++)
+        r[i] = __builtin_fma(-n[i], 6.93147180369123816490e-01, d[i]);
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+        r[i] = __builtin_fma(-n[i], 1.90821492927058770002e-10, r[i]);
+        p[i] = 1.0 / 6227020800.0;
+    }
+#pragma unroll
+    for (int k = 0; k < 12; k++)
+#pragma unroll
+        for (int i = 0; i < N; i++)
+            p[i] = __builtin_fma(p[i], r[i], c[k]);
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+        p[i] = __builtin_fma(p[i], r[i], 1.0);
+        const float v = (float)__builtin_ldexp(p[i], (int)n[i]);
+        out[i] = d[i] < -110.0 ? 0.0f : v;
+    }
+}
+
 // expf (ggml_v_expf one value at a time), nn/swiglu.go:31-74.
 __device__ __forceinline__ float ggml_expf(float x) {
     const float shift = 0x1.8p23f;

@@ -1355,12 +1355,13 @@ __global__ __launch_bounds__(kParThreads) void attn_par_kernel(
 #pragma unroll
     for (int w = 1; w < kParThreads / 64; w++)
         m = fmaxf(m, redm[w]);
-    // exponentials (float64 exp, as SoftmaxInPlace); each 64-position block's
+    // exponentials (exp_neg: SoftmaxInPlace's float64 exp rounded to float,
+    // bit for bit); each 64-position block's
     // pairwise sum (a cache wavefront's lanes are one block's positions)
     float e[ROWS];
 #pragma unroll
     for (int r = 0; r < ROWS; r++) {
-        e[r] = cw && ct + r * kCT < n ? (float)exp((double)(s[r] - m)) : 0.0f;
+        e[r] = cw && ct + r * kCT < n ? exp_neg(s[r] - m) : 0.0f;
         if (cw && r * kCT + cwave * 64 < n) {
             const float b = wave_pairwise_sum(e[r]);
             if (lane == 0)
@@ -1468,6 +1469,297 @@ __global__ __launch_bounds__(kParThreads) void attn_par_kernel(
             }
         }
     }
+}
+
+// ---- prompt attention on the matrix cores -----------------------------------
+//
+// The parallel form for a prompt (M > 4 tokens of one conversation, prefixes
+// of at most kPmMax): grid (ceil(M / 32), heads), a workgroup per (query head,
+// 32-token tile), eight wavefronts.  Per token, over its positions 0 .. pos:
+//   scores  s_p = scale * (q . k_p): v_mfma_f32_32x32x16_f16 over the head
+//           (fp16 operands, exact products, fp32 sums in the matrix core's
+//           order), 32 tokens x 32 positions a tile, into LDS;
+//   maximum, exponentials (exp_neg: the float64 exp of the float
+//           difference, as SoftmaxInPlace), total and fp16 probabilities as the
+//           decode's parallel order takes them: the total is ((0 + B_0) +
+//           B_1) + ..., B_b the pairwise sum (wave_pairwise_sum) of 64-position
+//           block b;
+//   values  out[d] = sum_p prob_p * v_p[d]: the same MFMA, the probabilities
+//           as the 32 x 16 operand (tokens x positions), the value rows as
+//           the 16 x 32 one (positions x head elements); the positions in two
+//           halves (a wavefront each), the first half's sum plus the second's.
+// Positions past a token's own are +0 probabilities; value elements past the
+// tile's last position are zeroed before they enter the product, so a cache
+// entry not yet written (any bits) never reaches a sum.  The matrix cores'
+// order of the two dot products is the only difference from the decode
+// form: the head values are golem's within float rounding (checked at 1e-4 of
+// RMS, as the decode's parallel order).
+constexpr int kPmTok = 32;       // tokens a workgroup: one MFMA tile of rows
+constexpr int kPmWaves = 8;
+constexpr int kPmThreads = 64 * kPmWaves;
+constexpr int kPmMax = 1024;     // positions the form holds (scores in LDS)
+constexpr int kPmPre = 8;        // value pieces a lane keeps in flight
+
+typedef _Float16 pm_v8h __attribute__((ext_vector_type(8)));
+typedef float pm_v16f __attribute__((ext_vector_type(16)));
+
+__host__ __device__ inline int pm_stride(int limit) { return ((limit + 63) & ~63) + 4; }  // floats a score row
+
+template <int HD>
+__global__ __launch_bounds__(kPmThreads, 4) void attn_prompt_mfma_kernel(
+    const uint16_t *__restrict__ qh, int M, int heads, int kv_heads, const int32_t *__restrict__ positions,
+    int limit, const uint16_t *__restrict__ kcache, const uint16_t *__restrict__ vcache, int context, float scale,
+    int8_t *__restrict__ q, float *__restrict__ scales, int32_t *__restrict__ qsum, float *__restrict__ heads_f) {
+    static_assert(HD % 32 == 0, "whole 32-element head blocks");
+    constexpr int KS = HD / 16;  // the head in MFMA k-steps
+    extern __shared__ __align__(16) float sl[];  // [kPmTok][stride]: scores, then exponentials
+    __shared__ int nrow[kPmTok];
+    __shared__ float mrow[kPmTok], trow[kPmTok];
+    __shared__ float bsum[kPmTok][kPmMax / 64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, li = lane & 31, g = lane >> 5;
+    const int h = blockIdx.y, t0 = blockIdx.x * kPmTok;
+    const int kvh = h / (heads / kv_heads);
+    const int stride = pm_stride(limit);
+
+    // this lane's query operands first: token t0 + li, elements 16 s + 8 g ..
+    pm_v8h aq[KS];
+    {
+        const uint16_t *qr = qh + ((size_t)min(t0 + li, M - 1) * heads + h) * HD + 8 * g;
+#pragma unroll
+        for (int s = 0; s < KS; s++)
+            aq[s] = *(const pm_v8h *)(qr + 16 * s);
+    }
+    if (tid < kPmTok)
+        nrow[tid] = t0 + tid < M ? min(max(positions[t0 + tid], 0) + 1, limit) : 0;
+    lds_barrier();
+    int nmax = 0;
+#pragma unroll 8
+    for (int r = 0; r < kPmTok; r++)
+        nmax = max(nmax, nrow[r]);
+    const int np = (nmax + 63) & ~63;  // whole 64-position blocks
+
+    // scores: wavefront w takes the 32-position tiles w, w + 4, ...; key
+    // pieces past nmax repeat the last one (in bounds, never used)
+    // (the next tile's keys are requested before this one's products: all
+    // of a tile's loads in flight at once)
+    const uint16_t *kb = kcache + (size_t)kvh * HD * context;
+    auto kload = [&](int j, pm_v8h *bk) {
+        const int p = min(32 * j + li, nmax - 1);
+#pragma unroll
+        for (int s = 0; s < KS; s++)
+            bk[s] = *(const pm_v8h *)(kb + ((size_t)(2 * s + g) * context + p) * 8);
+    };
+    pm_v8h bk[KS];
+    kload(wave, bk);
+    for (int j = wave; j < np / 32; j += kPmWaves) {
+        pm_v8h cur[KS];
+#pragma unroll
+        for (int s = 0; s < KS; s++)
+            cur[s] = bk[s];
+        if (j + kPmWaves < np / 32)
+            kload(j + kPmWaves, bk);
+        pm_v16f acc = {};
+#pragma unroll
+        for (int s = 0; s < KS; s++)
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(aq[s], cur[s], acc, 0, 0, 0);
+#pragma unroll
+        for (int e = 0; e < 16; e++)
+            sl[(8 * (e >> 2) + 4 * g + (e & 3)) * stride + 32 * j + li] = scale * acc[e];
+    }
+    lds_barrier();
+
+    // The values: wavefront w takes head block db = w % 4 (elements 32 db ..
+    // 32 db + 31) over half hf = w / 4 of the k-steps (16 positions each);
+    // its first kPmPre value pieces go out now, to land while the softmax
+    // runs (its barriers wait for LDS only): lane (li, g) holds positions
+    // 16 i + 8 g .. + 7 of element 32 db + li.
+    const int db = wave & 3, hf = wave >> 2;
+    const bool pv = db < HD / 32;
+    const int nsteps = np / 16, half = (nsteps + 1) / 2;
+    const int i_lo = hf ? half : 0, i_hi = hf ? nsteps : half;
+    const uint16_t *vrow = vcache + ((size_t)kvh * HD + 32 * db + li) * context;
+    auto vload = [&](int i) -> v4u_stream {
+        return *(const v4u_stream *)(vrow + min(16 * i + 8 * g, context - 8));  // a multiple of 8, as the context is
+    };
+    v4u_stream vr[kPmPre];
+    if (pv) {
+#pragma unroll
+        for (int u = 0; u < kPmPre; u++)
+            vr[u] = vload(min(i_lo + u, i_hi - 1));
+    }
+
+    // each token's maximum over its own positions: a wavefront a token, lane
+    // l holding positions 64 b + l
+    for (int r = wave; r < kPmTok; r += kPmWaves) {
+        const int n = nrow[r];
+        const float *row = sl + r * stride;
+        const int nbr = (n + 63) >> 6;
+        float m = -INFINITY;
+        for (int b0 = 0; b0 < nbr; b0 += 4) {  // four reads in flight
+            float v[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+                v[u] = row[64 * min(b0 + u, nbr - 1) + lane];
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+                m = 64 * (b0 + u) + lane < n ? fmaxf(m, v[u]) : m;
+        }
+        m = wave_max(m);
+        if (lane == 0)
+            mrow[r] = m;
+    }
+    lds_barrier();
+    // exponentials in place and each 64-position block's pairwise sum, a
+    // wavefront a token, four blocks at once (independent float64 chains,
+    // every lane computing; positions past the token's own become +0)
+    for (int r = wave; r < kPmTok; r += kPmWaves) {
+        const int n = nrow[r], nbr = (n + 63) >> 6;
+        const float m = mrow[r];
+        float *row = sl + r * stride;
+        for (int b0 = 0; b0 < nbr; b0 += 4) {
+            float d[4], ev[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+                d[u] = row[64 * min(b0 + u, nbr - 1) + lane] - m;
+            exp_neg_n<4>(d, ev);
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+                ev[u] = 64 * (b0 + u) + lane < n ? ev[u] : 0.0f;
+            float bs[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+                bs[u] = wave_pairwise_sum(ev[u]);
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                if (b0 + u < nbr) {
+                    row[64 * (b0 + u) + lane] = ev[u];
+                    if (lane == 0)
+                        bsum[r][b0 + u] = bs[u];
+                }
+            }
+        }
+    }
+    lds_barrier();
+    if (tid < kPmTok) {
+        float total = 0.0f;
+        const int nbr = (nrow[tid] + 63) >> 6;
+        for (int b = 0; b < nbr; b++)
+            total = total + bsum[tid][b];
+        trow[tid] = total;
+    }
+    lds_barrier();
+    // the probabilities fp16(e / total) in place (+0 past the token's own
+    // positions): sixteen lanes a token, 128 positions a step; a step's
+    // halves overwrite floats of its own or an earlier step, already read (a
+    // wavefront's LDS accesses keep their order)
+    {
+        const int r = tid >> 4, sub = tid & 15;
+        const float tot = trow[r];
+        const int n = nrow[r];
+        float *row = sl + r * stride;
+        uint16_t *hrow = (uint16_t *)row;
+        for (int c = 0; 128 * c < np; c++) {
+            const int p0 = 128 * c + 8 * sub;
+            if (p0 < np) {
+                const float4 e0 = *(const float4 *)(row + p0), e1 = *(const float4 *)(row + p0 + 4);
+                const float ev[8] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};
+                uint32_t hv[8];
+#pragma unroll
+                for (int k = 0; k < 8; k++)
+                    hv[k] = p0 + k < n ? float_to_half_bits(__fdiv_rn(ev[k], tot)) : 0u;
+                *(v4u_stream *)(hrow + p0) = (v4u_stream){hv[0] | (hv[1] << 16), hv[2] | (hv[3] << 16),
+                                                          hv[4] | (hv[5] << 16), hv[6] | (hv[7] << 16)};
+            }
+        }
+    }
+    lds_barrier();
+
+    // values: the probabilities as the row operand, the value pieces as the
+    // column operand; piece i + kPmPre is requested as piece i is used
+    const uint16_t *pr = (const uint16_t *)(sl + li * stride) + 8 * g;
+    pm_v16f acc = {};
+    if (pv) {
+        for (int i0 = i_lo; i0 < i_hi; i0 += kPmPre) {
+#pragma unroll
+            for (int u = 0; u < kPmPre; u++) {
+                const int i = i0 + u;
+                if (i < i_hi) {
+                    v4u_stream vv = vr[u];
+                    if (i + kPmPre < i_hi)
+                        vr[u] = vload(i + kPmPre);
+                    const int p0 = 16 * i + 8 * g;
+                    if (p0 + 8 > nmax) {  // the piece the tile's positions end in, or past them: zeros from nmax
+#pragma unroll
+                        for (int k = 0; k < 4; k++) {
+                            const uint32_t keep = (p0 + 2 * k < nmax ? 0x0000FFFFu : 0u) |
+                                                  (p0 + 2 * k + 1 < nmax ? 0xFFFF0000u : 0u);
+                            vv[k] &= keep;
+                        }
+                    }
+                    const pm_v8h ap = *(const pm_v8h *)(pr + 16 * i);
+                    acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ap, __builtin_bit_cast(pm_v8h, vv), acc, 0, 0, 0);
+                }
+            }
+        }
+    }
+    // the two halves' sums added, first half first: the second half's
+    // wavefronts leave theirs in LDS (the probabilities are spent)
+    lds_barrier();
+    float *part = sl + db * 16 * 64 + lane;
+    if (pv && hf) {
+#pragma unroll
+        for (int e = 0; e < 16; e++)
+            part[64 * e] = acc[e];
+    }
+    lds_barrier();
+    if (pv && !hf) {
+#pragma unroll
+        for (int e = 0; e < 16; e++)
+            acc[e] = acc[e] + part[64 * e];
+        // acc[e]: token 8 (e / 4) + 4 g + e % 4, head element 32 db + li; each
+        // token's 32 elements sit in one 32-lane group: its Q8_0 block
+        const int width = heads * HD, B = width >> 5;
+        const int col = h * HD + 32 * db + li;
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+            const int t = t0 + 8 * (e >> 2) + 4 * g + (e & 3);
+            float stored;
+            int32_t sm;
+            const int32_t nq = q8_0_lane(acc[e], &stored, &sm);
+            if (t < M) {
+                if (heads_f)
+                    heads_f[(size_t)t * width + col] = acc[e];
+                if (q) {
+                    q[(size_t)t * width + col] = (int8_t)nq;
+                    if (li == 0) {
+                        scales[(size_t)t * B + (col >> 5)] = stored;
+                        qsum[(size_t)t * B + (col >> 5)] = sm;
+                    }
+                }
+            }
+        }
+    }
+}
+
+int launch_prompt_mfma(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int kv_heads, int hd, int limit,
+                       const int32_t *positions, const uint16_t *kcache, const uint16_t *vcache, int context,
+                       float scale, int8_t *q, float *scales, int32_t *qsum, float *heads_f) {
+    // the scores; later the second half's value sums, 4 x 16 x 64 floats
+    const size_t lds = sizeof(float) * std::max((size_t)kPmTok * pm_stride(limit), (size_t)4 * 16 * 64);
+    const dim3 grid((unsigned)((M + kPmTok - 1) / kPmTok), (unsigned)heads);
+#define GX_PM(HH)                                                                                                    \
+    attn_prompt_mfma_kernel<HH><<<grid, kPmThreads, lds, ctx->stream>>>(                                             \
+        qh, M, heads, kv_heads, positions, limit, kcache, vcache, context, scale, q, scales, qsum, heads_f)
+    if (hd == 32)
+        GX_PM(32);
+    else if (hd == 64)
+        GX_PM(64);
+    else if (hd == 96)
+        GX_PM(96);
+    else
+        GX_PM(128);
+#undef GX_PM
+    return check_launch("qwen_attention prompt mfma");
 }
 
 // grid (ceil(ffn/256), M): gu [M][ldgu] holds each position's gate then up
@@ -1695,6 +1987,10 @@ int launch_qwen_attention(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int
     if (parallel && (M <= 4 || slots) && limit <= kDecodeMax)
         return launch_par<false>(ctx, qh, M, heads, kv_heads, hd, limit, positions, kcache, vcache, context, scale,
                                  q, scales, qsum, slots, nslots, QkRope{}, heads_f);
+    // A prompt of one conversation in the parallel order: the matrix cores.
+    if (parallel && !slots && limit <= kPmMax)
+        return launch_prompt_mfma(ctx, qh, M, heads, kv_heads, hd, limit, positions, kcache, vcache, context, scale,
+                                  q, scales, qsum, heads_f);
     if ((M <= 4 || slots) && limit <= kDecodeMax) {
 // One query head per workgroup when that fills at most two workgroups per CU
 // (128 workgroups for config 3's decode rather than 32): the scores,

@@ -87,9 +87,11 @@ class _Q8:
 class QwenModel:
     """attention: "parallel" runs decode steps' attention with its softmax
     total and value sums in a parallel order (gx_qwen_rope_attention_parallel
-    / gx_qwen_attention_parallel: golem's values within float rounding);
-    "golem" keeps golem's serial order bit for bit.  Prompts (more than four
-    positions) take the serial kernels either way."""
+    / gx_qwen_attention_parallel) and prompts (more than four positions) on
+    the matrix cores: golem's values within float rounding, so a prompt read
+    in one batch and the same tokens read one at a time agree only to that
+    rounding.  "golem" keeps golem's serial order bit for bit, and with it
+    golem's batch == one at a time."""
 
     def __init__(self, ctx, cfg, weights, max_batch, attention="parallel"):
         if attention not in ("parallel", "golem"):
@@ -225,7 +227,7 @@ class QwenModel:
         torch.arange(start_pos, start_pos + M, dtype=torch.int32, out=self.positions[:M])
         if self.nslots > 1:
             self.slot_ids[:M].fill_(self.slot)
-        self._blocks(M, start_pos + M - 1)
+        self._blocks(M, start_pos + M - 1, own_slot=True)
         return self.hidden[:M]
 
     def forward_slots(self, tokens, slots, positions):
@@ -260,19 +262,21 @@ class QwenModel:
         torch.arange(start_pos, start_pos + M, dtype=torch.int32, out=self.positions[:M])
         if self.nslots > 1:
             self.slot_ids[:M].fill_(self.slot)
-        self._blocks(M, start_pos + M - 1, blocks)
+        self._blocks(M, start_pos + M - 1, blocks, own_slot=True)
         self.ctx.sync()
         if blocks == 0:
             return self.xs[:M].cpu().numpy().copy()
         return (self.xs[:M] + self.ffn[:M]).cpu().numpy()  # the last block's residual add
 
-    def _blocks(self, M, max_pos, blocks=None, one_per_slot=False):
+    def _blocks(self, M, max_pos, blocks=None, one_per_slot=False, own_slot=False):
         """The embedding rows, every block and the final norm for the M tokens
         and positions already in self.tokens / self.positions (with `blocks`:
         only the first that many blocks, and no final norm).  one_per_slot:
         the M tokens belong to M different conversations (a lock-step step),
         so the head norms, RoPE, cache stores and attention run as one
-        kernel."""
+        kernel.  own_slot: the M tokens are the current conversation's
+        (forward), whose caches the attention then reads as a lone
+        conversation's."""
         cfg, vp, call, ctx = self.cfg, self._vp, self._call, self.ctx.ptr
         call("gx_weight_rows", ctx, self.embd.ptr, 0, vp(self.tokens), M, vp(self.xs))
         if M == 1:
@@ -296,10 +300,17 @@ class QwenModel:
                 call("gx_qwen_qk_rope", ctx, vp(self.qkv), qd + 2 * kvd, M, cfg.heads, cfg.kv_heads, cfg.head_dim,
                      vp(self.positions), vp(b["q_norm"]), vp(b["k_norm"]), vp(self.rope_cos), vp(self.rope_sin),
                      np.float32(cfg.eps), vp(self.qh), vp(self.kc[i]), vp(self.vc[i]), self.context, sl, self.nslots)
+                if sl is None or not own_slot:
+                    kca, vca, sla = self.kc[i], self.vc[i], sl
+                else:
+                    # a prompt of the current conversation reads that slot's
+                    # caches as a lone conversation's: the same kernels, and
+                    # so the same values, as the model without slots
+                    kca, vca, sla = self.kc[i][self.slot], self.vc[i][self.slot], None
                 call(self._attention, ctx, vp(self.qh), M, cfg.heads, cfg.kv_heads, cfg.head_dim,
-                     max_pos, vp(self.positions), vp(self.kc[i]), vp(self.vc[i]), self.context,
+                     max_pos, vp(self.positions), vp(kca), vp(vca), self.context,
                      vp(self.set8.q), vp(self.set8.s), vp(self.set8.qs), vp(self.attn_ws), self.attn_ws.numel(),
-                     sl, self.nslots)
+                     sla, self.nslots if sla is not None else 0)
             self._mm(b["o"], self.set8, M, self.attn, cfg.dim)
             call("gx_norm_quant", ctx, vp(self.xs), cfg.dim, vp(self.attn), cfg.dim, vp(b["ffn_norm"]), M, cfg.dim,
                  np.float32(cfg.eps), None, 0, vp(self.x8.q), vp(self.x8.s), vp(self.x8.qs))

@@ -425,7 +425,12 @@ int gx_qwen_rope_attention(gx_ctx *ctx, const float *qkv, int ldqkv, int heads, 
  * thread of a workgroup takes a share of both sums, where golem's order
  * leaves them to one lane per head and one per head element.  Same
  * arguments, caches and outputs as the serial forms; the caches come out bit
- * for bit the same.  Larger batches fall back to the serial kernels. */
+ * for bit the same.  A prompt (M > 4 tokens of one conversation, prefixes
+ * of at most 1024) runs on the matrix cores instead: the scores and the
+ * value sums are fp16 MFMA products (exact products, fp32 sums in the
+ * matrix core's order), the maximum, exponentials, total and fp16
+ * probabilities as above; the head outputs stay within 1e-4 of RMS of
+ * golem's.  Longer prompts and batches with slots take the serial kernels. */
 int gx_qwen_attention_parallel(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int kv_heads, int head_dim,
                                int max_pos, const int32_t *positions, const uint16_t *kcache,
                                const uint16_t *vcache, int context, int8_t *q, float *scales, int32_t *qsum,
@@ -451,8 +456,9 @@ int gx_qwen_rope_attention_slots(gx_ctx *ctx, const float *qkv, int ldqkv, int M
                                  int32_t *qsum, const int32_t *slots, int nslots, int parallel);
 
 /* The head outputs of gx_qwen_attention_parallel before their Q8_0, out
- * [M][heads*head_dim] (device floats), M <= 4.  No counterpart in golem:
- * parity instrumentation for the parallel order. */
+ * [M][heads*head_dim] (device floats): a decode step (M <= 4, prefixes to
+ * 768) or a prompt (prefixes to 1024).  No counterpart in golem: parity
+ * instrumentation for the parallel order. */
 int gx_qwen_attention_heads(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int kv_heads, int head_dim,
                             int max_pos, const int32_t *positions, const uint16_t *kcache, const uint16_t *vcache,
                             int context, float *out);

@@ -63,6 +63,8 @@ def load():
         "orc_rope_apply": (None, [V, I, V, V]),
         "orc_attend": (None, [V, V, V, I, I, I, I, F, V, V]),
         "orc_attend_parallel": (None, [V, V, V, I, I, I, I, F, V, V]),
+        "orc_exp_neg": (F, [F]),
+        "orc_exp_neg_check": (ctypes.c_long, [V, ctypes.c_long, V]),
         "orc_matrix_rows": (I, [I, V, V, I, I, V, I, V, V, V, V, V, V, V, I, I, V, I, I, I]),
         "orc_rms_norm_plain": (None, [V, I, V, F]),
         "orc_gelu_table_build": (None, [V]),

@@ -719,6 +719,51 @@ void orc_rope_apply(float *vec, int dims, const float *c, const float *s)
     }
 }
 
+/* The device's exp_neg (golem_amd/csrc/gx_device.hpp): (float)exp((double)d)
+ * for d <= 0 as straight-line float64 arithmetic -- n = rint(d log2 e), r = d
+ * - n ln2 (hi + lo), Horner on the Taylor series to r^13, times 2^n, rounded
+ * to float; +0 below -110.  Test infrastructure: tests check it against the
+ * C library's exp over floats of [-110, 0] (it is the exponential of
+ * SoftmaxInPlace, nn/ops.go:59-73, which golem takes in float64). */
+float orc_exp_neg(float df) {
+    const double d = (double)df;
+    const double n = rint(d * 1.4426950408889634);
+    double r = fma(-n, 6.93147180369123816490e-01, d);
+    r = fma(-n, 1.90821492927058770002e-10, r);
+    double p = 1.0 / 6227020800.0;
+    p = fma(p, r, 1.0 / 479001600.0);
+    p = fma(p, r, 1.0 / 39916800.0);
+    p = fma(p, r, 1.0 / 3628800.0);
+    p = fma(p, r, 1.0 / 362880.0);
+    p = fma(p, r, 1.0 / 40320.0);
+    p = fma(p, r, 1.0 / 5040.0);
+    p = fma(p, r, 1.0 / 720.0);
+    p = fma(p, r, 1.0 / 120.0);
+    p = fma(p, r, 1.0 / 24.0);
+    p = fma(p, r, 1.0 / 6.0);
+    p = fma(p, r, 0.5);
+    p = fma(p, r, 1.0);
+    p = fma(p, r, 1.0);
+    const float out = (float)ldexp(p, (int)n);
+    return d < -110.0 ? 0.0f : out;
+}
+
+/* Many at once (test helper): out[i] = orc_exp_neg(x[i]) and the count of
+ * i where it differs from (float)exp((double)x[i]) in bits. */
+long orc_exp_neg_check(const float *x, long n, float *out) {
+    long bad = 0;
+    for (long i = 0; i < n; i++) {
+        const float a = orc_exp_neg(x[i]), b = (float)exp((double)x[i]);
+        uint32_t ua, ub;
+        memcpy(&ua, &a, 4);
+        memcpy(&ub, &b, 4);
+        bad += ua != ub;
+        if (out)
+            out[i] = a;
+    }
+    return bad;
+}
+
 /* One query head of one position, qwen/attention.go:96-124: against the first
  * n positions of a layer cache (K, V as [position][kvheads][hd] floats, already
  * rounded through fp16), scores = scale * DotF32(query, key), SoftmaxInPlace,

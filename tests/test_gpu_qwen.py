@@ -22,7 +22,7 @@ The whole model, on small models of the same structure:
   (qwen/model_test.go:118-126).
 - a prompt read in one batch is, bit for bit, the same tokens read one at a
   time -- hidden states and cache entries (TestBatchAgreesWithOneAtATime,
-  qwen/model_test.go:79).
+  qwen/model_test.go:79), in golem's attention order.
 
 The two geometries cover a head of 64 with two query heads per key-value head,
 and golem's real head of 128 with four per key-value head; each model is drawn
@@ -41,6 +41,7 @@ from tests.gpu_util import log
 pytestmark = pytest.mark.gpu
 
 LOOSE = 5e-2
+LOOSE_PARALLEL = 1e-1
 LOGITS = 0.25  # the head spreads a hidden state's shift over 150k dot products
 
 CONFIGS = {
@@ -49,26 +50,34 @@ CONFIGS = {
 }
 
 
-def models(dev, name, symmetric):
+def models(dev, name, symmetric, attention="parallel"):
     from oracle.qwen import QwenOracle
     cfg = CONFIGS[name]
     w = synth.qwen_weights(cfg, 7 + len(name), symmetric=symmetric)
-    return cfg, QwenModel(dev.ctx, cfg, w, max_batch=16), QwenOracle(cfg, w)
+    return cfg, QwenModel(dev.ctx, cfg, w, max_batch=16, attention=attention), QwenOracle(cfg, w)
 
 
+@pytest.mark.parametrize("attention", ["golem", "parallel"])
 @pytest.mark.parametrize("symmetric", [False, True])
 @pytest.mark.parametrize("name", list(CONFIGS))
-def test_prefill_and_greedy_against_golem(dev, orc, name, symmetric):
-    cfg, model, oracle_model = models(dev, name, symmetric)
+def test_prefill_and_greedy_against_golem(dev, orc, name, symmetric, attention):
+    """In golem's attention order every kernel is golem's bit for bit and the
+    hidden states stay within LOOSE; in the parallel order the prompt's
+    attention runs on the matrix cores, whose scores move a probability on an
+    fp16 rounding boundary now and then (a head by up to 2e-3 of RMS), and
+    each such move cascades through the Q8_0 of the products after it, so
+    the bar there is LOOSE_PARALLEL.  The greedy ids are golem's in both."""
+    cfg, model, oracle_model = models(dev, name, symmetric, attention)
+    bar = LOOSE if attention == "golem" else LOOSE_PARALLEL
     prompt = [int(t) for t in synth.rng(8).integers(0, cfg.vocab, 12)]
-    log(f"qwen {name} symmetric={symmetric}: prefill {len(prompt)}")
+    log(f"qwen {name} symmetric={symmetric} attention={attention}: prefill {len(prompt)}")
     oracle_model.reset()
     want = oracle_model.forward(prompt, 0)
     model.reset()
     got = dev.get(model.forward(prompt, 0))
     rels = [orc.compare_floats(got[t], want[t])[0] for t in range(len(prompt))]
     log(f"  hidden, of RMS per position: {[float('%.2g' % r) for r in rels]}")
-    assert max(rels) <= LOOSE, f"position {int(np.argmax(rels))}: {max(rels):.3g} of RMS"
+    assert max(rels) <= bar, f"position {int(np.argmax(rels))}: {max(rels):.3g} of RMS"
     lg = dev.get(model.logits(len(prompt) - 1))
     rel, at = orc.compare_floats(lg, oracle_model.logits(want[-1]))
     log(f"  last logits {rel:.3g} of RMS")
@@ -84,7 +93,11 @@ def test_prefill_and_greedy_against_golem(dev, orc, name, symmetric):
 
 @pytest.mark.parametrize("name", list(CONFIGS))
 def test_batch_equals_one_at_a_time(dev, name):
-    cfg, model, _ = models(dev, name, True)
+    """golem's invariant holds in golem's attention order: the prompt's serial
+    passes and the decode step's kernel sum in the same order (the parallel
+    forms -- a prompt on the matrix cores, a decode step in another parallel
+    order -- agree only to float rounding)."""
+    cfg, model, _ = models(dev, name, True, attention="golem")
     prompt = [int(t) for t in synth.rng(9).integers(0, cfg.vocab, 13)]
     model.reset()
     batch = dev.get(model.forward(prompt, 0)).copy()

@@ -190,3 +190,121 @@ def test_prompt_48_batch_equals_one_at_a_time_full_width(dev):
         np.testing.assert_array_equal(vb[layer], model.vc[layer].cpu().numpy())
     torch.cuda.synchronize()
     model.free()
+
+
+# (head width, heads, key-value heads, prompt length M, first position, context)
+PROMPT_PARALLEL = [(128, 32, 8, PROMPT, 0, 640), (64, 4, 2, 70, 0, 80), (128, 8, 2, 37, 100, 200),
+                   (32, 8, 1, 5, 0, 8), (96, 4, 4, 33, 31, 72), (128, 4, 1, 64, 960, 1024)]
+# One fp16 step of a probability near 1 (2^-11), times a value element of
+# ~3 RMS: what one probability that rounds the other way moves a head by.
+FP16_STEP = 2e-3
+
+
+def _prompt_case(dev, orc, hd, heads, kv, M, start, context, exact):
+    """A prompt's caches and queries (cache entries past the prompt hold NaN
+    bits), the MFMA form's head floats and Q8_0, and the rows compared.
+    exact: queries and keys on a grid of 1/4 (|q|, |k| <= 1/2), so that every
+    dot product is exact in any order and the scores are golem's bits."""
+    g = synth.rng(700 + M + hd + start + exact)
+    n = start + M
+    pos = np.arange(start, n, dtype=np.int32)
+    if exact:
+        kcf = (g.integers(-2, 3, (n, kv, hd)) * 0.25).astype(np.float16)
+        qf = (g.integers(-2, 3, (M, heads * hd)) * 0.25).astype(np.float16)
+    else:
+        kcf = g.standard_normal((n, kv, hd)).astype(np.float16)
+        qf = (g.standard_normal((M, heads * hd)) * 1.5).astype(np.float16)
+    vcf = (g.standard_normal((n, kv, hd)) * 2).astype(np.float16)
+    nan = np.array([0x7E00], np.uint16).view(np.float16)[0]
+    vt = np.full((kv, hd, context), nan, np.float16)
+    vt[:, :, :n] = vcf.transpose(1, 2, 0)
+    kt = np.full((kv, hd // 8, context, 8), nan, np.float16)
+    kt[:, :, :n, :] = kcf.reshape(n, kv, hd // 8, 8).transpose(1, 2, 0, 3)
+    ins = [dev.put(a) for a in (qf.view(np.int16), pos, kt.view(np.int16), vt.view(np.int16))]
+    log(f"prompt attention (MFMA) hd={hd} heads={heads}/{kv} M={M} from {start}, context {context}, exact={exact}")
+    heads_f = dev.empty((M, heads * hd), np.float32)
+    capi.call("gx_qwen_attention_heads", dev.ctx.ptr, capi.vp(ins[0]), M, heads, kv, hd, n - 1, capi.vp(ins[1]),
+              capi.vp(ins[2]), capi.vp(ins[3]), context, capi.vp(heads_f))
+    q8 = dev.empty((M, heads * hd), np.int8)
+    sc = dev.empty((M, heads * hd // 32), np.float32)
+    qs = dev.empty((M, heads * hd // 32), np.int32)
+    nw = capi.size_out("gx_qwen_attention_workspace_bytes", M, heads, n - 1)
+    ws = dev.empty((nw,), np.uint8)
+    capi.call("gx_qwen_attention_parallel", dev.ctx.ptr, capi.vp(ins[0]), M, heads, kv, hd, n - 1, capi.vp(ins[1]),
+              capi.vp(ins[2]), capi.vp(ins[3]), context, capi.vp(q8), capi.vp(sc), capi.vp(qs), capi.vp(ws), nw,
+              None, 0)
+    rows = list(range(M)) if M <= 80 else SAMPLE
+    got = dev.get(heads_f)[rows]
+    # the Q8_0 output is the head floats' own, bit for bit
+    mine = orc.Batch(np.ascontiguousarray(got)).quantize()
+    gq = dev.get(q8)[rows]
+    np.testing.assert_array_equal(gq, mine.q_rows())
+    np.testing.assert_array_equal(_bits(dev.get(sc)[rows]), _bits(mine.scales_rows()))
+    np.testing.assert_array_equal(dev.get(qs)[rows], mine.qsum_rows())
+    return qf, kcf, vcf, pos, rows, got, gq
+
+
+def _oracle_heads(orc, fn, qf, kcf, vcf, pos, rows, hd, heads, kv):
+    lib = orc.load()
+    K32, V32 = np.ascontiguousarray(kcf.astype(np.float32)), np.ascontiguousarray(vcf.astype(np.float32))
+    scale = np.float32(1 / math.sqrt(float(hd)))
+    want = np.zeros((len(rows), heads * hd), np.float32)
+    scores = np.zeros(len(kcf), np.float32)
+    for i, t in enumerate(rows):
+        for h in range(heads):
+            query = np.ascontiguousarray(qf[t, h * hd:(h + 1) * hd].astype(np.float32))
+            dst = np.zeros(hd, np.float32)
+            getattr(lib, fn)(orc._p(query), orc._p(K32), orc._p(V32), kv, hd, h // (heads // kv), int(pos[t]) + 1,
+                             scale, orc._p(scores), orc._p(dst))
+            want[i, h * hd:(h + 1) * hd] = dst
+    return want
+
+
+def _compare(orc, got, want, gq, rows, pos, heads, hd, bar):
+    worst, over = 0.0, 0
+    for i, t in enumerate(rows):
+        for h in range(heads):
+            rel, at = orc.compare_floats(got[i, h * hd:(h + 1) * hd], want[i, h * hd:(h + 1) * hd])
+            worst = max(worst, rel)
+            over += rel > 1e-4
+            assert rel <= bar, f"token {t} (position {pos[t]}) head {h}: {rel:.3g} of RMS at {at}"
+    dq = gq.astype(np.int32) - orc.Batch(want).quantize().q_rows().astype(np.int32)
+    moved = int(np.count_nonzero(dq))
+    log(f"  {len(rows)} tokens: worst {worst:.2g} of RMS ({over} of {len(rows) * heads} heads above 1e-4), "
+        f"{moved} of {dq.size} Q8_0 values one step off")
+    assert np.abs(dq).max() <= 1 and moved <= max(2, dq.size // 100)
+
+
+@pytest.mark.parametrize("hd,heads,kv,M,start,context", PROMPT_PARALLEL)
+def test_prompt_attention_mfma_exact_scores(dev, orc, hd, heads, kv, M, start, context):
+    """The MFMA prompt form on scores that are exact in any order (queries and
+    keys on a grid of 1/4): everything up to the probabilities is then the
+    decode's parallel order bit for bit -- the same maximum, float64
+    exponentials, pairwise block totals and fp16 probabilities -- so against
+    its restatement (orc_attend_parallel) the heads differ only by the value
+    sums' order (the matrix core's against runs of 32 fma chains): within
+    1e-5 of RMS (about 1e-6 seen).  A wrong token, head, position bound or value element moves
+    a head by O(1).  Ragged token tiles, prompts that continue a cache, head
+    widths 32 to 128, prefixes up to the form's 1024; cache entries past the
+    prompt hold NaN bits, so a position no token attends never reaches a
+    sum."""
+    qf, kcf, vcf, pos, rows, got, gq = _prompt_case(dev, orc, hd, heads, kv, M, start, context, True)
+    want = _oracle_heads(orc, "orc_attend_parallel", qf, kcf, vcf, pos, rows, hd, heads, kv)
+    _compare(orc, got, want, gq, rows, pos, heads, hd, 1e-5)
+
+
+@pytest.mark.parametrize("hd,heads,kv,M,start,context", PROMPT_PARALLEL)
+def test_prompt_attention_mfma_against_golem(dev, orc, hd, heads, kv, M, start, context):
+    """The MFMA prompt form on random fp16 queries and keys against golem's
+    attention (orc_attend, qwen/attention.go:86-124).  The scores are now
+    golem's within an ulp or two, not bit for bit, and golem rounds every
+    probability to fp16 (attention.go:112-114): a probability that sits on a
+    rounding boundary goes the other way, and a short prefix's probabilities
+    are large, so a head can move by one fp16 step of its largest probability
+    times a value element -- up to FP16_STEP of RMS (4e-4 seen at a token of
+    18 positions).  The bar is that step; the heads above the decode form's
+    1e-4 are counted and logged, and the Q8_0 of the heads is golem's but for
+    values on a rounding boundary (one step, at most 1 % of them)."""
+    qf, kcf, vcf, pos, rows, got, gq = _prompt_case(dev, orc, hd, heads, kv, M, start, context, False)
+    want = _oracle_heads(orc, "orc_attend", qf, kcf, vcf, pos, rows, hd, heads, kv)
+    _compare(orc, got, want, gq, rows, pos, heads, hd, FP16_STEP)
