@@ -186,6 +186,141 @@ __global__ __launch_bounds__(64) void qwen_qk_rope_kernel(const float *__restric
     }
 }
 
+// The same for a batch: grid (ceil(M / kQkTok), heads + kv_heads), 256
+// threads, kQkTok tokens of one head a workgroup.  The tokens' heads are
+// staged in LDS; the 64 float64 sums of squares run side by side, one lane a
+// token, each left to right as head_norm_scale takes it; then the rotation,
+// each output element from the same operations as the one-token kernel, and
+// the fp16 stores laid out so that consecutive lanes take consecutive tokens
+// where the destination runs over positions: a key's 16-byte pieces (a
+// wavefront writes a piece of 64 positions, 1 KiB) and a value's elements
+// (128 bytes of one element row); a query's 16-byte pieces run along its
+// head.  The same bits as qwen_qk_rope_kernel.
+constexpr int kQkTok = 64;
+
+template <int HD>
+__global__ __launch_bounds__(256) void qwen_qk_rope_tile_kernel(
+    const float *__restrict__ qkv, int ldqkv, int M, int heads, int kv_heads, const int32_t *__restrict__ positions,
+    const float *__restrict__ q_norm, const float *__restrict__ k_norm, const float *__restrict__ rope_cos,
+    const float *__restrict__ rope_sin, float eps, uint16_t *__restrict__ qh, uint16_t *__restrict__ kcache,
+    uint16_t *__restrict__ vcache, int context, const int32_t *__restrict__ slots, int nslots) {
+    constexpr int half = HD / 2, P = HD / 8;  // rotation pairs; 16-byte pieces a head
+    __shared__ float hs[kQkTok][HD + 1];      // +1: a lane a token reads down a column without conflicts
+    __shared__ float scs[kQkTok];
+    __shared__ int pos_s[kQkTok];
+    __shared__ int place_s[kQkTok];           // placed: 1; no place: 0; past the batch: -1
+    __shared__ int slot_s[kQkTok];
+    const int tid = threadIdx.x, t0 = blockIdx.x * kQkTok, u = blockIdx.y;
+    const bool is_q = u < heads;
+    const int col = is_q ? u * HD : heads * HD + (u - heads) * HD;
+    if (tid < kQkTok) {
+        const int t = t0 + tid;
+        int pl = -1, pos = 0, sl = 0;
+        if (t < M) {
+            pos = positions[t];
+            sl = slots ? slots[t] : 0;
+            pl = pos >= 0 && pos < context && (!slots || (sl >= 0 && sl < nslots)) ? 1 : 0;
+        }
+        pos_s[tid] = pos;
+        place_s[tid] = pl;
+        slot_s[tid] = sl;
+    }
+    // the heads, a float4 a thread at a time (rows past the batch repeat the last)
+    for (int idx = tid; idx < kQkTok * (HD / 4); idx += 256) {
+        const int tk = idx / (HD / 4), c4 = idx - tk * (HD / 4);
+        const float4 v = *(const float4 *)(qkv + (size_t)min(t0 + tk, M - 1) * ldqkv + col + 4 * c4);
+        hs[tk][4 * c4] = v.x;
+        hs[tk][4 * c4 + 1] = v.y;
+        hs[tk][4 * c4 + 2] = v.z;
+        hs[tk][4 * c4 + 3] = v.w;
+    }
+    __syncthreads();
+    if (tid < kQkTok) {
+        // head_norm_scale's sum, left to right, sixteen values read ahead
+        const float *hr = hs[tid];
+        double acc = 0.0;
+        for (int i0 = 0; i0 < HD; i0 += 16) {
+            float v[16];
+#pragma unroll
+            for (int i = 0; i < 16; i++)
+                v[i] = hr[i0 + i];
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const float sq = v[i] * v[i];
+                acc += (double)sq;
+            }
+        }
+        const float mean = (float)(acc / (double)HD);
+        scs[tid] = (float)(1.0 / sqrt((double)(mean + eps)));
+    }
+    __syncthreads();
+    const float *gain = is_q ? q_norm : k_norm;
+    // (token, piece) items: queries with the piece fastest (a query's pieces
+    // are contiguous), keys with the token fastest (a piece's positions are).
+    // Element e of a rotated head: pair j = e % half, a = re c - im s (e <
+    // half), b = re s + im c (e >= half), re = x_j sc g_j, im = x_{j+half}
+    // sc g_{j+half}: RoPETable.Apply, nn/rope.go:62-73.  A piece's eight
+    // elements share one side, so their pairs are eight consecutive j.
+    for (int idx = tid; idx < kQkTok * P; idx += 256) {
+        const int tk = is_q ? idx / P : idx % kQkTok, pc = is_q ? idx % P : idx / kQkTok;
+        const int pl = place_s[tk];
+        if (pl < 0)
+            continue;
+        const int pos = pos_s[tk];
+        uint32_t w[4] = {0x7E007E00u, 0x7E007E00u, 0x7E007E00u, 0x7E007E00u};  // no place: a NaN query
+        if (pl) {
+            const bool lo = 8 * pc < half;
+            const int j0 = lo ? 8 * pc : 8 * pc - half;
+            const float4 c0 = *(const float4 *)(rope_cos + (size_t)pos * half + j0);
+            const float4 c1 = *(const float4 *)(rope_cos + (size_t)pos * half + j0 + 4);
+            const float4 s0 = *(const float4 *)(rope_sin + (size_t)pos * half + j0);
+            const float4 s1 = *(const float4 *)(rope_sin + (size_t)pos * half + j0 + 4);
+            const float cs[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+            const float sn[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+            const float sc = scs[tk];
+            uint32_t hb[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const int j = j0 + k;
+                const float re = (hs[tk][j] * sc) * gain[j], im = (hs[tk][j + half] * sc) * gain[j + half];
+                const float v = lo ? re * cs[k] - im * sn[k] : re * sn[k] + im * cs[k];
+                hb[k] = float_to_half_bits(v);
+            }
+#pragma unroll
+            for (int k = 0; k < 4; k++)
+                w[k] = hb[2 * k] | (hb[2 * k + 1] << 16);
+        }
+        const v4u_stream o = {w[0], w[1], w[2], w[3]};
+        if (is_q) {
+            *(v4u_stream *)(qh + (size_t)(t0 + tk) * heads * HD + u * HD + 8 * pc) = o;
+        } else if (pl) {
+            uint16_t *kt = kcache + (size_t)slot_s[tk] * kv_heads * HD * context + (size_t)(u - heads) * HD * context;
+            *(v4u_stream *)(kt + ((size_t)pc * context + pos) * 8) = o;
+        }
+    }
+    if (is_q)
+        return;
+    // the values: staged the same way, then a lane a token down each element row
+    __syncthreads();
+    const int vcol = (heads + kv_heads) * HD + (u - heads) * HD;
+    for (int idx = tid; idx < kQkTok * (HD / 4); idx += 256) {
+        const int tk = idx / (HD / 4), c4 = idx - tk * (HD / 4);
+        const float4 v = *(const float4 *)(qkv + (size_t)min(t0 + tk, M - 1) * ldqkv + vcol + 4 * c4);
+        hs[tk][4 * c4] = v.x;
+        hs[tk][4 * c4 + 1] = v.y;
+        hs[tk][4 * c4 + 2] = v.z;
+        hs[tk][4 * c4 + 3] = v.w;
+    }
+    __syncthreads();
+    for (int idx = tid; idx < kQkTok * HD; idx += 256) {
+        const int tk = idx % kQkTok, d = idx / kQkTok;
+        if (place_s[tk] > 0) {
+            uint16_t *vt = vcache + (size_t)slot_s[tk] * kv_heads * HD * context + (size_t)(u - heads) * HD * context;
+            vt[(size_t)d * context + pos_s[tk]] = (uint16_t)float_to_half_bits(hs[tk][d]);
+        }
+    }
+}
+
 // The attention proper runs as three passes over a workspace: scores
 // sc [M][heads][S] floats and probabilities prob [M][heads][S] fp16, where S
 // is the deepest visible prefix rounded up to 64.
@@ -1955,6 +2090,21 @@ int launch_qwen_qk_rope(gx_ctx *ctx, const float *qkv, int ldqkv, int M, int hea
                         int context, const int32_t *slots, int nslots) {
     GX_CHECK(hd <= kHeadMax && hd % 8 == 0, "gx: head width %d unsupported (a multiple of 8, at most %d)", hd,
              kHeadMax);
+    // A batch (and a head width the tiled kernel is built for, operands it
+    // can read 16 bytes at a time): 64 tokens of a head a workgroup.
+    const bool aligned = (((uintptr_t)qkv | (uintptr_t)rope_cos | (uintptr_t)rope_sin) & 15) == 0 && ldqkv % 4 == 0;
+    if (M >= 32 && (hd == 64 || hd == 128) && aligned) {
+        const dim3 grid((unsigned)((M + kQkTok - 1) / kQkTok), (unsigned)(heads + kv_heads));
+        if (hd == 64)
+            qwen_qk_rope_tile_kernel<64><<<grid, 256, 0, ctx->stream>>>(qkv, ldqkv, M, heads, kv_heads, positions,
+                                                                         q_norm, k_norm, rope_cos, rope_sin, eps, qh,
+                                                                         kcache, vcache, context, slots, nslots);
+        else
+            qwen_qk_rope_tile_kernel<128><<<grid, 256, 0, ctx->stream>>>(qkv, ldqkv, M, heads, kv_heads, positions,
+                                                                          q_norm, k_norm, rope_cos, rope_sin, eps, qh,
+                                                                          kcache, vcache, context, slots, nslots);
+        return check_launch("qwen_qk_rope tiles");
+    }
     qwen_qk_rope_kernel<<<dim3((unsigned)M, (unsigned)(heads + kv_heads)), 64, 0, ctx->stream>>>(
         qkv, ldqkv, heads, kv_heads, hd, positions, q_norm, k_norm, rope_cos, rope_sin, eps, qh, kcache, vcache,
         context, slots, nslots);

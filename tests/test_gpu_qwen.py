@@ -184,10 +184,14 @@ def test_norm_quant_bit_exact(dev, orc, M, K):
     np.testing.assert_array_equal(dev.get(qs), b.qsum_rows())
 
 
+@pytest.mark.parametrize("M", [6, 70])
 @pytest.mark.parametrize("hd,heads,kv", [(128, 8, 2), (64, 4, 4)])
-def test_qk_rope_and_cache_bit_exact(dev, orc, hd, heads, kv):
-    g = synth.rng(62 + hd)
-    M, ctx_len = 6, 40
+def test_qk_rope_and_cache_bit_exact(dev, orc, hd, heads, kv, M):
+    """A token at a time (M = 6) and 64-token tiles (M = 70: a full tile and
+    a ragged one, positions out of order, two tokens with no place in the
+    cache, whose queries are NaN and which store nothing)."""
+    g = synth.rng(62 + hd + M)
+    ctx_len = 40 if M == 6 else 100
     cos, sin = rope_tables(hd, ctx_len, 1e6)
     lib = orc.load()
     # the host tables are golem's RoPETable values through the same libm
@@ -199,7 +203,11 @@ def test_qk_rope_and_cache_bit_exact(dev, orc, hd, heads, kv):
     qkv = (g.standard_normal((M, width)) * 4).astype(np.float32)
     qn = (1 + 0.02 * g.standard_normal(hd)).astype(np.float32)
     kn = (1 + 0.02 * g.standard_normal(hd)).astype(np.float32)
-    pos = np.array([0, 1, 5, 17, 38, 39], np.int32)
+    if M == 6:
+        pos = np.array([0, 1, 5, 17, 38, 39], np.int32)
+    else:
+        pos = g.permutation(ctx_len)[:M].astype(np.int32)
+        pos[[3, 66]] = [-1, ctx_len]  # no place
     qh = dev.empty((M, heads * hd), np.int16)
     kc = torch.zeros((kv, hd // 8, ctx_len, 8), dtype=torch.int16, device="cuda")  # keys in 16-byte pieces
     vc = torch.zeros((kv, hd, ctx_len), dtype=torch.int16, device="cuda")  # values transposed
@@ -212,6 +220,9 @@ def test_qk_rope_and_cache_bit_exact(dev, orc, hd, heads, kv):
     got_k = kc.cpu().numpy().view(np.float16).astype(np.float32)
     got_v = vc.cpu().numpy().view(np.float16).astype(np.float32)
     for t in range(M):
+        if not 0 <= pos[t] < ctx_len:
+            assert np.isnan(got_q[t]).all()
+            continue
         lib.orc_rope_prepare(hd, int(pos[t]), 1e6, orc._p(c1), orc._p(s1))
         for h in range(heads):
             head = orc.rms_norm_plain(qkv[t, h * hd:(h + 1) * hd], qn, 1e-6)
@@ -226,6 +237,9 @@ def test_qk_rope_and_cache_bit_exact(dev, orc, hd, heads, kv):
             want_v = np.array([lib.orc_round_half(float(v)) for v in vh], np.float32)
             np.testing.assert_array_equal(got_k[h, :, pos[t], :].reshape(-1).view(np.uint32), want_k.view(np.uint32))
             np.testing.assert_array_equal(got_v[h, :, pos[t]].view(np.uint32), want_v.view(np.uint32))
+    # nothing else written: the positions no token holds are still zero
+    free = np.setdiff1d(np.arange(ctx_len), pos)
+    assert not got_k[:, :, free, :].any() and not got_v[:, :, free].any()
 
 
 ATTENTION = [(128, 8, 2, 70), (64, 4, 2, 300), (128, 32, 8, 640),
