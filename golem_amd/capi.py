@@ -90,6 +90,7 @@ _SIGNATURES = {
     "gx_norm_matmul_q4_0": [_vp, _vp, _vp, _vp, _vp, ctypes.c_float, _vp, _c_int, _c_int, _vp],
     "gx_norm_swiglu_q4_0": [_vp, _vp, _vp, _vp, _vp, ctypes.c_float, _vp, _vp, _vp, _vp],
     "gx_argmax_step": [_vp, _vp, _c_int, _vp, _vp, _c_int, _vp, _vp],
+    "gx_argmax_slots_step": [_vp, _vp, _c_int, _c_int, _c_int, _vp, _vp, _vp],
     "gx_argmax": [_vp, _vp, _c_int, _c_int, _c_int, _vp],
     "gx_geglu_quant": [_vp, _vp, _c_int, _c_int, _c_int, _vp, _vp, _vp],
     "gx_moe_join": [_vp, _vp, _c_int, _vp, _c_int, _vp, _c_int, _vp, _vp, _vp, _c_int, _c_int, ctypes.c_float, _vp,

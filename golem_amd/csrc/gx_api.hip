@@ -1036,6 +1036,19 @@ int gx_argmax_step(gx_ctx *ctx, const float *x, int n, int32_t *ids, int32_t *hi
     return ok();
 }
 
+int gx_argmax_slots_step(gx_ctx *ctx, const float *x, int ldx, int M, int n, int32_t *ids, int32_t *tokens,
+                         int32_t *positions) {
+    if (int rc = use(ctx))
+        return rc;
+    GX_CHECK(M >= 0 && n > 0 && ldx >= n, "gx: bad shape");
+    GX_CHECK(x && ids && tokens && positions, "gx: missing argument");
+    if (M == 0)
+        return ok();
+    if (int rc = gx::launch_argmax(ctx, x, ldx, M, n, ids, nullptr, 0, nullptr, nullptr, tokens, positions))
+        return rc;
+    return ok();
+}
+
 static int moe_experts(gx_ctx *ctx, const gx_weight *gate_up, const gx_weight *down, const float *down_scale,
                        const float *x, int ldx, int M, int top_k, const int32_t *ids, const float *weights, float *out,
                        int ldo, void *workspace, size_t workspace_bytes, bool noalloc) {

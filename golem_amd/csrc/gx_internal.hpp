@@ -171,7 +171,8 @@ int launch_qwen_attention(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int
 int launch_qwen_swiglu_quant(gx_ctx *ctx, const float *gu, int ldgu, int M, int ffn, int group, int8_t *q,
                              float *scales, int32_t *qsum);
 int launch_argmax(gx_ctx *ctx, const float *x, int ldx, int M, int n, int32_t *out, int32_t *history,
-                  int history_len, int32_t *pos, int32_t *positions);
+                  int history_len, int32_t *pos, int32_t *positions, int32_t *row_tokens = nullptr,
+                  int32_t *row_positions = nullptr);
 int launch_f32_matvec(gx_ctx *ctx, const gx_weight *w, const float *x, int ldx, int M, int row_start, int row_end,
                       float *y, int ldy);
 }  // namespace gx

@@ -2003,13 +2003,17 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_part_kernel(const float
 // grid (M), one wavefront.  With `history` (M = 1, a captured decode step):
 // also, while *pos + 1 < history_len, history[*pos + 1] = id, *pos += 1 and
 // positions[0] = the new *pos; at the history's end the counter stops there,
-// so a step replayed past the end never addresses past it.
+// so a step replayed past the end never addresses past it.  With
+// `row_tokens` (a lock-step step of M conversations): row_tokens[m] = id and
+// row_positions[m] += 1, each row's next input.
 __global__ __launch_bounds__(64) void argmax_final_kernel(const float *__restrict__ x, int ldx,
                                                           const float *__restrict__ part_v,
                                                           const int32_t *__restrict__ part_i,
                                                           int32_t *__restrict__ out, int32_t *__restrict__ history,
                                                           int history_len, int32_t *__restrict__ pos,
-                                                          int32_t *__restrict__ positions) {
+                                                          int32_t *__restrict__ positions,
+                                                          int32_t *__restrict__ row_tokens,
+                                                          int32_t *__restrict__ row_positions) {
     const int lane = threadIdx.x;
     float bv = -INFINITY;
     int bi = kNone;
@@ -2026,6 +2030,10 @@ __global__ __launch_bounds__(64) void argmax_final_kernel(const float *__restric
         const float x0 = x[(size_t)blockIdx.x * ldx];
         const int id = (bi == kNone || x0 != x0) ? 0 : bi;
         out[blockIdx.x] = id;
+        if (row_tokens) {
+            row_tokens[blockIdx.x] = id;
+            row_positions[blockIdx.x] += 1;
+        }
         if (history) {
             const int next = pos[0] + 1;
             if (next < history_len) {
@@ -2291,13 +2299,15 @@ int launch_qwen_swiglu_quant(gx_ctx *ctx, const float *gu, int ldgu, int M, int 
 }
 
 int launch_argmax(gx_ctx *ctx, const float *x, int ldx, int M, int n, int32_t *out, int32_t *history,
-                  int history_len, int32_t *pos, int32_t *positions) {
+                  int history_len, int32_t *pos, int32_t *positions, int32_t *row_tokens, int32_t *row_positions) {
     for (int m0 = 0; m0 < M; m0 += kArgmaxRows) {
         const int rows = min(kArgmaxRows, M - m0);
         argmax_part_kernel<<<dim3(kArgmaxParts, (unsigned)rows), kArgmaxThreads, 0, ctx->stream>>>(
             x + (size_t)m0 * ldx, ldx, n, ctx->argmax_v, ctx->argmax_i);
         argmax_final_kernel<<<rows, 64, 0, ctx->stream>>>(x + (size_t)m0 * ldx, ldx, ctx->argmax_v, ctx->argmax_i,
-                                                          out + m0, history, history_len, pos, positions);
+                                                          out + m0, history, history_len, pos, positions,
+                                                          row_tokens ? row_tokens + m0 : nullptr,
+                                                          row_positions ? row_positions + m0 : nullptr);
         if (int rc = check_launch("argmax"))
             return rc;
     }

@@ -447,9 +447,10 @@ class QwenModel:
 
     def _slots_device_step(self, n, max_pos):
         self._blocks(n, max_pos, one_per_slot=self.nslots > 1)
-        self.next_tokens(range(n))
-        self.tokens[:n].copy_(self.next_id[:n])
-        self.positions[:n].add_(1)
+        self.logits_batch(range(n))
+        # the picks, each row's next token and its position advanced, in one launch
+        self._call("gx_argmax_slots_step", self.ctx.ptr, self._vp(self.logit), self.cfg.vocab, n, self.cfg.vocab,
+                   self._vp(self.next_id), self._vp(self.tokens), self._vp(self.positions))
 
     def capture_slots(self, n):
         """Records the device work of slots_step(n) into a HIP graph (once per

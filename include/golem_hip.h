@@ -528,6 +528,16 @@ int gx_argmax(gx_ctx *ctx, const float *x, int ldx, int M, int n, int32_t *ids);
 int gx_argmax_step(gx_ctx *ctx, const float *x, int n, int32_t *ids, int32_t *history, int history_len,
                    int32_t *pos, int32_t *positions);
 
+/* The greedy step of M conversations decoded in lock step (the server's
+ * batch of slots, cmd/golem-server/runner.go:233-297, with the pick on the
+ * device): ids[m] = gx_argmax of row m of x, then tokens[m] = ids[m] and
+ * positions[m] += 1 -- row m's input to the next step -- in the same launch,
+ * so a captured lock-step step needs no other work between replays.
+ * tokens, positions, ids: device int32 [M].  The same workspace rule as
+ * gx_argmax. */
+int gx_argmax_slots_step(gx_ctx *ctx, const float *x, int ldx, int M, int n, int32_t *ids, int32_t *tokens,
+                         int32_t *positions);
+
 /* ---- calibration (measurement only) ----------------------------------- */
 
 /* No counterpart in golem; no product calls these.  They give the

@@ -666,3 +666,26 @@ def test_argmax_step_bookkeeping(dev):
     assert dev.get(hist).tolist() == [-5] * 7 + [4321] * 3  # positions 7, 8, 9; 10 is past the end
     assert dev.get(pos).tolist() == [9]
     assert dev.get(positions).tolist() == [9, 77]
+
+
+def test_argmax_slots_step_bookkeeping(dev):
+    """gx_argmax_slots_step: each row's pick in ids, the same id as the row's
+    next token, each row's position advanced by one -- three steps over
+    rows whose winners differ (one a NaN at index 0, which wins), the rows
+    past M untouched."""
+    n, M = 4099, 3
+    g = synth.rng(650)
+    x = g.standard_normal((M + 1, n)).astype(np.float32)
+    x[0, 17] = 50.0
+    x[1, 0] = np.nan
+    x[2, n - 1] = 40.0
+    xd = dev.put(x)
+    ids = dev.put(np.full((M + 1,), -1, np.int32))
+    tokens = dev.put(np.full((M + 1,), -2, np.int32))
+    positions = dev.put(np.array([5, 0, 100, 7], np.int32))
+    for _ in range(3):
+        capi.call("gx_argmax_slots_step", dev.ctx.ptr, capi.vp(xd), n, M, n, capi.vp(ids), capi.vp(tokens),
+                  capi.vp(positions))
+    assert dev.get(ids).tolist() == [17, 0, n - 1, -1]
+    assert dev.get(tokens).tolist() == [17, 0, n - 1, -2]
+    assert dev.get(positions).tolist() == [8, 3, 103, 7]
