@@ -210,9 +210,17 @@ def main():
             # the int8-MFMA product (every batch's kernel; the fp16-MFMA form
             # is a parity path only)
             for label, q16 in (("i8", None),):
-                for _ in range(5):
-                    call("gx_matmul_q4_0", ctx.ptr, w0d.ptr, vp(q2), vp(s2), vp(qs2), vp(q16), M, 0, r0, None,
-                         vp(y2), r0)
+                # warm until ~50 ms of launches have run: the clocks settle
+                # under sustained matrix-core load (a 1 ms warm-up left
+                # M = 2048 ~15 % slower than the same kernel after others)
+                t_w = time.perf_counter()
+                while True:
+                    for _ in range(5):
+                        call("gx_matmul_q4_0", ctx.ptr, w0d.ptr, vp(q2), vp(s2), vp(qs2), vp(q16), M, 0, r0, None,
+                             vp(y2), r0)
+                    torch.cuda.synchronize()
+                    if time.perf_counter() - t_w > 0.05:
+                        break
                 reps = 50
                 ctx.timer_start()
                 for _ in range(reps):
@@ -540,7 +548,13 @@ def bench_c3(ctx, torch):
         model.graph.replay()
     torch.cuda.synchronize()
 
+    # one untimed prefill first: the clocks settle under the products'
+    # sustained matrix-core load, and the timed one is the steady state
     model.reset()
+    model.forward(prompt, 0)
+    model.next_token(len(prompt) - 1)
+    model.reset()
+    torch.cuda.synchronize()
     ctx.timer_start()
     model.forward(prompt, 0)
     tok = model.next_token(len(prompt) - 1)
@@ -641,8 +655,13 @@ def bench_c4(ctx, torch, dev):
             call("gx_moe_experts", ctx.ptr, gu.ptr, dn.ptr, None, vp(x), D, M, k, vp(ids), vp(wts), vp(out), D,
                  vp(ws), n.value)
 
-        for i in range(6):
+        # warm until ~50 ms of steps have run (the clocks settle under load)
+        t_w, i = time.perf_counter(), 0
+        while i < 6 or time.perf_counter() - t_w < 0.05:
             step(i)
+            i += 1
+            if i % 8 == 0:
+                torch.cuda.synchronize()
         torch.cuda.synchronize()
         # distinct experts each position set reads, for the algorithmic bytes
         touched = []
