@@ -45,7 +45,7 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-extra", action="store_true", help="skip the config 0 / config 2 measurements")
     p.add_argument("--only", default="",
-                   help="profiling: run only this leg (c1, c0, c0floor, c2, c3, c3prefill, c4, valu) and exit; 'copy' runs the 256 MiB "
+                   help="profiling: run only this leg (c1, c0, c0floor, c2, c3, c3prefill, c3eager, c4, valu) and exit; 'copy' runs the 256 MiB "
                         "device copy that scales the FETCH_SIZE / WRITE_SIZE counters; 'c3prefill' reads "
                         "config 3's 512-token prompt four times (a kernel trace of the prefill alone)")
     p.add_argument("--c2-m", type=int, default=0, help="profiling: config 2 at this M only")
@@ -246,6 +246,9 @@ def main():
         return
     if args.only == "c3prefill":
         print(json.dumps(bench_c3_prefill(ctx, torch)))
+        return
+    if args.only == "c3eager":
+        print(json.dumps(bench_c3_eager(ctx, torch)))
         return
 
     # ---- config 3: Qwen3-4B-shaped decoder, prefill 512 + 128 greedy steps ----
@@ -520,6 +523,32 @@ def bench_c3_prefill(ctx, torch):
         model.next_token(len(prompt) - 1)
         ms.append(round(ctx.timer_stop(), 3))
     return {"c3_prefill_ms": ms}
+
+
+def bench_c3_eager(ctx, torch):
+    """Profiling leg for counter passes (rocprofv3 --pmc does not survive
+    this leg's graph capture): config 3's model and prompt, then 24 decode
+    steps launched eagerly, one position at a time -- the same kernels and
+    shapes as the captured step, each launch on its own."""
+    from golem_amd import synth
+    from golem_amd.qwen import QwenModel
+    cfg = synth.qwen3_4b(640)
+    w = synth.qwen_weights(cfg, 3)
+    model = QwenModel(ctx, cfg, w, max_batch=512)
+    del w
+    prompt = synth.rng(3).integers(0, cfg.vocab, 512).astype(np.int32)
+    model.reset()
+    model.forward(prompt, 0)
+    tok = int(model.next_token(len(prompt) - 1).item())
+    ids = [tok]
+    ctx.timer_start()
+    for s in range(24):
+        model.forward([tok], len(prompt) + s)
+        tok = int(model.next_token(0).item())
+        ids.append(tok)
+    ms = ctx.timer_stop() / 24
+    model.free()
+    return {"c3_eager_decode_ms_per_token": round(ms, 3), "ids": ids[:8]}
 
 
 def bench_c3(ctx, torch):
