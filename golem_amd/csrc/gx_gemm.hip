@@ -318,20 +318,31 @@ __global__ __launch_bounds__(64 * NWT) void q4_0_gemm_f16_kernel(
 //
 // The kernel for the Q4_0 x Q8_0 product of a batch.  Every stage's operands come in by direct
 // global-to-LDS loads (global_load_lds_dwordx4 / _dword): no registers stage
-// them, and three stages live in an LDS ring, two in flight while one is
-// multiplied.  A workgroup owns 128 rows (two R64 tiles) x 64 tokens; each of
-// its eight wavefronts one 32x32 MFMA tile (rows 32*(w&3), tokens
+// them, and the stages live in an LDS ring of kRing slots (four for the
+// 64-token form, three for the 32-token one), all but one in flight while one
+// is multiplied.  A workgroup owns 128 rows (two R64 tiles) x 64 tokens; each
+// of its eight wavefronts one 32x32 MFMA tile (rows 32*(w&3), tokens
 // 32*(w>>2)), at four wavefronts per SIMD (two workgroups per CU).  Per stage
-// (4 blocks) each wavefront issues exactly three loads, so `s_waitcnt
-// vmcnt(3)` before the stage's barrier means "this stage has landed" for
-// every wavefront; the barrier is the bare s_barrier (the fence of
+// (4 blocks) each wavefront issues exactly kLoads loads, so `s_waitcnt
+// vmcnt((kRing - 2) kLoads)` before the stage's barrier means "this stage has
+// landed" for every wavefront; the barrier is the bare s_barrier (the fence of
 // __syncthreads would wait for every load in flight).  Slot layout (bytes):
 //   [0, 8192)       nibbles  [block 4][row 128][16]
 //   [8192, 16384)   int8     [block 4][half 2][token 64][16]
 //   [16384, 17408)  act. scales (fp32) [block 4][token 64]
 //   [17408, 18432)  weight scales (fp16) [row 128][block 4]
 constexpr int kDmaTok = 64;
-constexpr int kDmaRing = 3;
+// LDS slots of the ring (stages in flight + 1).  The 64-token form takes
+// four (two workgroups a CU still fit: 2 x 72 KiB): config 2 at M = 2048
+// 180 -> 177 us; the 32-token form keeps three, which keep three
+// workgroups a CU (four slots: M = 512 50 -> 55 us, config 4's prefill
+// 181 -> 189 us).
+#ifndef GX_DMA_RING64
+#define GX_DMA_RING64 4
+#endif
+#ifndef GX_DMA_RING32
+#define GX_DMA_RING32 3
+#endif
 // The integer products run on a biased chain.  The weights enter the MFMA as
 // 16 * (n - 8) (the nibble in a byte's high half, its top bit flipped), and
 // each block's MFMA adds its 16 * isum to the previous block's output; a
@@ -405,11 +416,13 @@ struct DmaShape;
 template <>
 struct DmaShape<64> {
     static constexpr int kWaves = 8, kLoads = 3, kSlot = 18432, kOcc = 4;  // two workgroups a CU
+    static constexpr int kRing = GX_DMA_RING64;
     static constexpr int kAct = 8192, kActScale = 16384, kWScale = 17408;
 };
 template <>
 struct DmaShape<32> {
     static constexpr int kWaves = 4, kLoads = 5, kSlot = 14336, kOcc = 3;  // three workgroups a CU (LDS)
+    static constexpr int kRing = GX_DMA_RING32;
     static constexpr int kAct = 8192, kActScale = 12288, kWScale = 12800, kDummy = 13824;
 };
 
@@ -444,7 +457,8 @@ __global__ __launch_bounds__(64 * DmaShape<TOK>::kWaves, DmaShape<TOK>::kOcc) vo
     // workgroups a CU by its LDS, has them; the 64-token form would lose its
     // fourth wavefront a SIMD.
     constexpr bool kPipe = TOK == 32;
-    __shared__ __align__(16) uint8_t ring_lds[kDmaRing * kSlotB];
+    constexpr int kRing = Sh::kRing;
+    __shared__ __align__(16) uint8_t ring_lds[kRing * kSlotB];
     const int tid = threadIdx.x;
     const int lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     // The workgroup's row pair bx and token group by.  With xcd_pairs > 0 the
@@ -583,10 +597,10 @@ __global__ __launch_bounds__(64 * DmaShape<TOK>::kWaves, DmaShape<TOK>::kOcc) vo
     auto stage = [&](auto slot_tag, auto first_tag, int h) {
         constexpr int kSlot = decltype(slot_tag)::value;
         constexpr bool kFirst = decltype(first_tag)::value;
-        wait_vmcnt<Sh::kLoads>();  // stage h has landed (stage h + 1 may be in flight)
+        wait_vmcnt<(kRing - 2) * Sh::kLoads>();  // stage h has landed (stages h + 1 .. may be in flight)
         __builtin_amdgcn_s_barrier();
         // into the slot stage h - 1 used; every wavefront is past it
-        issue(std::integral_constant<int, (kSlot + 2) % kDmaRing>{}, h + 2);
+        issue(std::integral_constant<int, (kSlot + kRing - 1) % kRing>{}, h + kRing - 1);
         constexpr int so = kSlot * kSlotB;
         // The operands of block j + 1 are read while block j is multiplied.
         uint2 wq_n, Bh_n, Bl_n;
@@ -708,24 +722,43 @@ __global__ __launch_bounds__(64 * DmaShape<TOK>::kWaves, DmaShape<TOK>::kOcc) vo
     using S0 = std::integral_constant<int, 0>;
     using S1 = std::integral_constant<int, 1>;
     using S2 = std::integral_constant<int, 2>;
-    issue(S0{}, 0);
-    issue(S1{}, 1);
-    for (int h = 0;; h += 6) {  // three stretches: the ring comes round to slot 0
-        stage(S0{}, std::true_type{}, h);
-        stage(S1{}, std::false_type{}, h + 1);
-        fold();
-        if (h + 2 >= Hp)
-            break;
-        stage(S2{}, std::true_type{}, h + 2);
-        stage(S0{}, std::false_type{}, h + 3);
-        fold();
-        if (h + 4 >= Hp)
-            break;
-        stage(S1{}, std::true_type{}, h + 4);
-        stage(S2{}, std::false_type{}, h + 5);
-        fold();
-        if (h + 6 >= Hp)
-            break;
+    if constexpr (kRing == 3) {
+        issue(S0{}, 0);
+        issue(S1{}, 1);
+        for (int h = 0;; h += 6) {  // three stretches: the ring comes round to slot 0
+            stage(S0{}, std::true_type{}, h);
+            stage(S1{}, std::false_type{}, h + 1);
+            fold();
+            if (h + 2 >= Hp)
+                break;
+            stage(S2{}, std::true_type{}, h + 2);
+            stage(S0{}, std::false_type{}, h + 3);
+            fold();
+            if (h + 4 >= Hp)
+                break;
+            stage(S1{}, std::true_type{}, h + 4);
+            stage(S2{}, std::false_type{}, h + 5);
+            fold();
+            if (h + 6 >= Hp)
+                break;
+        }
+    } else {
+        using S3 = std::integral_constant<int, 3>;
+        issue(S0{}, 0);
+        issue(S1{}, 1);
+        issue(S2{}, 2);
+        for (int h = 0;; h += 4) {  // two stretches: the ring comes round to slot 0
+            stage(S0{}, std::true_type{}, h);
+            stage(S1{}, std::false_type{}, h + 1);
+            fold();
+            if (h + 2 >= Hp)
+                break;
+            stage(S2{}, std::true_type{}, h + 2);
+            stage(S3{}, std::false_type{}, h + 3);
+            fold();
+            if (h + 4 >= Hp)
+                break;
+        }
     }
     wait_vmcnt<0>();  // the trailing loads land before the workgroup ends
     const int t = 32 * tg + li;
