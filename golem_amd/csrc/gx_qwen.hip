@@ -187,9 +187,12 @@ __global__ __launch_bounds__(64) void qwen_qk_rope_kernel(const float *__restric
 }
 
 // The same for a batch: grid (ceil(M / kQkTok), heads + kv_heads), 256
-// threads, kQkTok tokens of one head a workgroup.  The tokens' heads are
-// staged in LDS; the 64 float64 sums of squares run side by side, one lane a
-// token, each left to right as head_norm_scale takes it; then the rotation,
+// threads, kQkTok tokens of one head a workgroup.  The tokens' heads and the
+// norm's gains are staged in LDS (a key-value head's value rows are loaded
+// at the same time, into registers, for later); the 64 float64 sums of
+// squares run side by side, one lane a token, each left to right as
+// head_norm_scale takes it, while every thread's rotation-table loads --
+// which wait only on the positions -- are in flight; then the rotation,
 // each output element from the same operations as the one-token kernel, and
 // the fp16 stores laid out so that consecutive lanes take consecutive tokens
 // where the destination runs over positions: a key's 16-byte pieces (a
@@ -204,8 +207,12 @@ __global__ __launch_bounds__(256) void qwen_qk_rope_tile_kernel(
     const float *__restrict__ q_norm, const float *__restrict__ k_norm, const float *__restrict__ rope_cos,
     const float *__restrict__ rope_sin, float eps, uint16_t *__restrict__ qh, uint16_t *__restrict__ kcache,
     uint16_t *__restrict__ vcache, int context, const int32_t *__restrict__ slots, int nslots) {
-    constexpr int half = HD / 2, P = HD / 8;  // rotation pairs; 16-byte pieces a head
+    constexpr int half = HD / 2, P = HD / 8;    // rotation pairs; 16-byte pieces a head
+    constexpr int kItems = kQkTok * P / 256;    // (token, piece) items a thread
+    constexpr int kRows4 = kQkTok * HD / 4 / 256;  // float4s of a head tile a thread
+    static_assert(kItems * 256 == kQkTok * P && kRows4 * 256 * 4 == kQkTok * HD, "whole items");
     __shared__ float hs[kQkTok][HD + 1];      // +1: a lane a token reads down a column without conflicts
+    __shared__ float gs[HD];
     __shared__ float scs[kQkTok];
     __shared__ int pos_s[kQkTok];
     __shared__ int place_s[kQkTok];           // placed: 1; no place: 0; past the batch: -1
@@ -213,6 +220,7 @@ __global__ __launch_bounds__(256) void qwen_qk_rope_tile_kernel(
     const int tid = threadIdx.x, t0 = blockIdx.x * kQkTok, u = blockIdx.y;
     const bool is_q = u < heads;
     const int col = is_q ? u * HD : heads * HD + (u - heads) * HD;
+    const float *gain = is_q ? q_norm : k_norm;
     if (tid < kQkTok) {
         const int t = t0 + tid;
         int pl = -1, pos = 0, sl = 0;
@@ -225,16 +233,43 @@ __global__ __launch_bounds__(256) void qwen_qk_rope_tile_kernel(
         place_s[tid] = pl;
         slot_s[tid] = sl;
     }
-    // the heads, a float4 a thread at a time (rows past the batch repeat the last)
-    for (int idx = tid; idx < kQkTok * (HD / 4); idx += 256) {
+    if (tid < HD)
+        gs[tid] = gain[tid];
+    // the heads, a float4 a thread at a time (rows past the batch repeat the
+    // last); a key-value head's value rows into registers alongside
+    const int vcol = (heads + kv_heads) * HD + (u - heads) * HD;
+    float4 vv[kRows4];
+#pragma unroll
+    for (int r = 0; r < kRows4; r++) {
+        const int idx = tid + 256 * r;
         const int tk = idx / (HD / 4), c4 = idx - tk * (HD / 4);
-        const float4 v = *(const float4 *)(qkv + (size_t)min(t0 + tk, M - 1) * ldqkv + col + 4 * c4);
+        const float *row = qkv + (size_t)min(t0 + tk, M - 1) * ldqkv;
+        const float4 v = *(const float4 *)(row + col + 4 * c4);
+        if (!is_q)
+            vv[r] = *(const float4 *)(row + vcol + 4 * c4);
         hs[tk][4 * c4] = v.x;
         hs[tk][4 * c4 + 1] = v.y;
         hs[tk][4 * c4 + 2] = v.z;
         hs[tk][4 * c4 + 3] = v.w;
     }
     __syncthreads();
+    // (token, piece) items: queries with the piece fastest (a query's pieces
+    // are contiguous), keys with the token fastest (a piece's positions are).
+    // Their rotation tables go out now, while the norms' sums run.
+    float4 c0[kItems], c1[kItems], s0[kItems], s1[kItems];
+#pragma unroll
+    for (int it = 0; it < kItems; it++) {
+        const int idx = tid + 256 * it;
+        const int tk = is_q ? idx / P : idx % kQkTok, pc = is_q ? idx % P : idx / kQkTok;
+        if (place_s[tk] > 0) {
+            const int pos = pos_s[tk];
+            const int j0 = 8 * pc < half ? 8 * pc : 8 * pc - half;
+            c0[it] = *(const float4 *)(rope_cos + (size_t)pos * half + j0);
+            c1[it] = *(const float4 *)(rope_cos + (size_t)pos * half + j0 + 4);
+            s0[it] = *(const float4 *)(rope_sin + (size_t)pos * half + j0);
+            s1[it] = *(const float4 *)(rope_sin + (size_t)pos * half + j0 + 4);
+        }
+    }
     if (tid < kQkTok) {
         // head_norm_scale's sum, left to right, sixteen values read ahead
         const float *hr = hs[tid];
@@ -254,14 +289,13 @@ __global__ __launch_bounds__(256) void qwen_qk_rope_tile_kernel(
         scs[tid] = (float)(1.0 / sqrt((double)(mean + eps)));
     }
     __syncthreads();
-    const float *gain = is_q ? q_norm : k_norm;
-    // (token, piece) items: queries with the piece fastest (a query's pieces
-    // are contiguous), keys with the token fastest (a piece's positions are).
     // Element e of a rotated head: pair j = e % half, a = re c - im s (e <
     // half), b = re s + im c (e >= half), re = x_j sc g_j, im = x_{j+half}
     // sc g_{j+half}: RoPETable.Apply, nn/rope.go:62-73.  A piece's eight
     // elements share one side, so their pairs are eight consecutive j.
-    for (int idx = tid; idx < kQkTok * P; idx += 256) {
+#pragma unroll
+    for (int it = 0; it < kItems; it++) {
+        const int idx = tid + 256 * it;
         const int tk = is_q ? idx / P : idx % kQkTok, pc = is_q ? idx % P : idx / kQkTok;
         const int pl = place_s[tk];
         if (pl < 0)
@@ -271,18 +305,14 @@ __global__ __launch_bounds__(256) void qwen_qk_rope_tile_kernel(
         if (pl) {
             const bool lo = 8 * pc < half;
             const int j0 = lo ? 8 * pc : 8 * pc - half;
-            const float4 c0 = *(const float4 *)(rope_cos + (size_t)pos * half + j0);
-            const float4 c1 = *(const float4 *)(rope_cos + (size_t)pos * half + j0 + 4);
-            const float4 s0 = *(const float4 *)(rope_sin + (size_t)pos * half + j0);
-            const float4 s1 = *(const float4 *)(rope_sin + (size_t)pos * half + j0 + 4);
-            const float cs[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
-            const float sn[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+            const float cs[8] = {c0[it].x, c0[it].y, c0[it].z, c0[it].w, c1[it].x, c1[it].y, c1[it].z, c1[it].w};
+            const float sn[8] = {s0[it].x, s0[it].y, s0[it].z, s0[it].w, s1[it].x, s1[it].y, s1[it].z, s1[it].w};
             const float sc = scs[tk];
             uint32_t hb[8];
 #pragma unroll
             for (int k = 0; k < 8; k++) {
                 const int j = j0 + k;
-                const float re = (hs[tk][j] * sc) * gain[j], im = (hs[tk][j + half] * sc) * gain[j + half];
+                const float re = (hs[tk][j] * sc) * gs[j], im = (hs[tk][j + half] * sc) * gs[j + half];
                 const float v = lo ? re * cs[k] - im * sn[k] : re * sn[k] + im * cs[k];
                 hb[k] = float_to_half_bits(v);
             }
@@ -300,16 +330,17 @@ __global__ __launch_bounds__(256) void qwen_qk_rope_tile_kernel(
     }
     if (is_q)
         return;
-    // the values: staged the same way, then a lane a token down each element row
+    // the values: from the registers into the staging rows, then a lane a
+    // token down each element row
     __syncthreads();
-    const int vcol = (heads + kv_heads) * HD + (u - heads) * HD;
-    for (int idx = tid; idx < kQkTok * (HD / 4); idx += 256) {
+#pragma unroll
+    for (int r = 0; r < kRows4; r++) {
+        const int idx = tid + 256 * r;
         const int tk = idx / (HD / 4), c4 = idx - tk * (HD / 4);
-        const float4 v = *(const float4 *)(qkv + (size_t)min(t0 + tk, M - 1) * ldqkv + vcol + 4 * c4);
-        hs[tk][4 * c4] = v.x;
-        hs[tk][4 * c4 + 1] = v.y;
-        hs[tk][4 * c4 + 2] = v.z;
-        hs[tk][4 * c4 + 3] = v.w;
+        hs[tk][4 * c4] = vv[r].x;
+        hs[tk][4 * c4 + 1] = vv[r].y;
+        hs[tk][4 * c4 + 2] = vv[r].z;
+        hs[tk][4 * c4 + 3] = vv[r].w;
     }
     __syncthreads();
     for (int idx = tid; idx < kQkTok * HD; idx += 256) {
