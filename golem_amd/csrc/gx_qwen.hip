@@ -1664,7 +1664,7 @@ constexpr int kPmTok = 32;       // tokens a workgroup: one MFMA tile of rows
 constexpr int kPmWaves = 8;
 constexpr int kPmThreads = 64 * kPmWaves;
 constexpr int kPmMax = 1024;     // positions the form holds (scores in LDS)
-constexpr int kPmPre = 8;        // value pieces a lane keeps in flight
+constexpr int kPmPre = 4;        // value pieces a lane keeps in flight
 
 typedef _Float16 pm_v8h __attribute__((ext_vector_type(8)));
 typedef float pm_v16f __attribute__((ext_vector_type(16)));
@@ -1682,18 +1682,18 @@ __global__ __launch_bounds__(kPmThreads, 4) void attn_prompt_mfma_kernel(
     __shared__ int nrow[kPmTok];
     __shared__ float mrow[kPmTok], trow[kPmTok];
     __shared__ float bsum[kPmTok][kPmMax / 64];
+    __shared__ __align__(16) uint16_t qs[kPmTok][HD + 8];  // the tile's queries (+8: rows 4 banks apart)
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, li = lane & 31, g = lane >> 5;
     const int h = blockIdx.y, t0 = blockIdx.x * kPmTok;
     const int kvh = h / (heads / kv_heads);
     const int stride = pm_stride(limit);
 
-    // this lane's query operands first: token t0 + li, elements 16 s + 8 g ..
-    pm_v8h aq[KS];
-    {
-        const uint16_t *qr = qh + ((size_t)min(t0 + li, M - 1) * heads + h) * HD + 8 * g;
-#pragma unroll
-        for (int s = 0; s < KS; s++)
-            aq[s] = *(const pm_v8h *)(qr + 16 * s);
+    // the tile's queries into LDS (read back as the operands: token t0 + li,
+    // elements 16 s + 8 g .., in registers they would crowd out the keys)
+    for (int i = tid; i < kPmTok * (HD / 8); i += kPmThreads) {
+        const int tk = i / (HD / 8), c = i - tk * (HD / 8);
+        *(v4u_stream *)&qs[tk][8 * c] =
+            *(const v4u_stream *)(qh + ((size_t)min(t0 + tk, M - 1) * heads + h) * HD + 8 * c);
     }
     if (tid < kPmTok)
         nrow[tid] = t0 + tid < M ? min(max(positions[t0 + tid], 0) + 1, limit) : 0;
@@ -1708,12 +1708,14 @@ __global__ __launch_bounds__(kPmThreads, 4) void attn_prompt_mfma_kernel(
     // pieces past nmax repeat the last one (in bounds, never used)
     // (the next tile's keys are requested before this one's products: all
     // of a tile's loads in flight at once)
-    const uint16_t *kb = kcache + (size_t)kvh * HD * context;
+    // (32-bit byte offsets from one uniform base: an address a piece
+    // costs one register, not two)
+    const char *kb = (const char *)(kcache + (size_t)kvh * HD * context);
     auto kload = [&](int j, pm_v8h *bk) {
         const int p = min(32 * j + li, nmax - 1);
 #pragma unroll
         for (int s = 0; s < KS; s++)
-            bk[s] = *(const pm_v8h *)(kb + ((size_t)(2 * s + g) * context + p) * 8);
+            bk[s] = *(const pm_v8h *)(kb + (uint32_t)(((2 * s + g) * context + p) * 16));
     };
     pm_v8h bk[KS];
     kload(wave, bk);
@@ -1726,8 +1728,10 @@ __global__ __launch_bounds__(kPmThreads, 4) void attn_prompt_mfma_kernel(
             kload(j + kPmWaves, bk);
         pm_v16f acc = {};
 #pragma unroll
-        for (int s = 0; s < KS; s++)
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(aq[s], cur[s], acc, 0, 0, 0);
+        for (int s = 0; s < KS; s++) {
+            const pm_v8h aq = *(const pm_v8h *)&qs[li][16 * s + 8 * g];
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(aq, cur[s], acc, 0, 0, 0);
+        }
 #pragma unroll
         for (int e = 0; e < 16; e++)
             sl[(8 * (e >> 2) + 4 * g + (e & 3)) * stride + 32 * j + li] = scale * acc[e];
@@ -1878,29 +1882,36 @@ __global__ __launch_bounds__(kPmThreads, 4) void attn_prompt_mfma_kernel(
             part[64 * e] = acc[e];
     }
     lds_barrier();
+    // the first half's wavefronts add the second's and lay the tile's head
+    // floats out token by token: acc[e] is token 8 (e / 4) + 4 g + e % 4,
+    // head element 32 db + li
+    constexpr int OS = HD + 4;  // floats a staged output row
+    float *ot = sl + 4 * 16 * 64;
     if (pv && !hf) {
 #pragma unroll
         for (int e = 0; e < 16; e++)
-            acc[e] = acc[e] + part[64 * e];
-        // acc[e]: token 8 (e / 4) + 4 g + e % 4, head element 32 db + li; each
-        // token's 32 elements sit in one 32-lane group: its Q8_0 block
-        const int width = heads * HD, B = width >> 5;
-        const int col = h * HD + 32 * db + li;
-#pragma unroll
-        for (int e = 0; e < 16; e++) {
-            const int t = t0 + 8 * (e >> 2) + 4 * g + (e & 3);
-            float stored;
-            int32_t sm;
-            const int32_t nq = q8_0_lane(acc[e], &stored, &sm);
-            if (t < M) {
-                if (heads_f)
-                    heads_f[(size_t)t * width + col] = acc[e];
-                if (q) {
-                    q[(size_t)t * width + col] = (int8_t)nq;
-                    if (li == 0) {
-                        scales[(size_t)t * B + (col >> 5)] = stored;
-                        qsum[(size_t)t * B + (col >> 5)] = sm;
-                    }
+            ot[(8 * (e >> 2) + 4 * g + (e & 3)) * OS + 32 * db + li] = acc[e] + part[64 * e];
+    }
+    lds_barrier();
+    // then every thread: four consecutive values of a token, eight lanes a
+    // Q8_0 block
+    const int width = heads * HD, B = width >> 5;
+    for (int i4 = tid; i4 < kPmTok * (HD / 4); i4 += kPmThreads) {
+        const int tk = i4 / (HD / 4), c4 = i4 - tk * (HD / 4), t = t0 + tk;
+        const float4 o = *(const float4 *)(ot + tk * OS + 4 * c4);
+        const float v[4] = {o.x, o.y, o.z, o.w};
+        float stored;
+        int32_t sm;
+        const uint32_t packed = q8_0_quad(v, &stored, &sm);
+        if (t < M) {
+            const int col = h * HD + 4 * c4;
+            if (heads_f)
+                *(float4 *)(heads_f + (size_t)t * width + col) = o;
+            if (q) {
+                *(uint32_t *)(q + (size_t)t * width + col) = packed;
+                if ((c4 & 7) == 0) {
+                    scales[(size_t)t * B + (col >> 5)] = stored;
+                    qsum[(size_t)t * B + (col >> 5)] = sm;
                 }
             }
         }
@@ -1911,7 +1922,9 @@ int launch_prompt_mfma(gx_ctx *ctx, const uint16_t *qh, int M, int heads, int kv
                        const int32_t *positions, const uint16_t *kcache, const uint16_t *vcache, int context,
                        float scale, int8_t *q, float *scales, int32_t *qsum, float *heads_f) {
     // the scores; later the second half's value sums, 4 x 16 x 64 floats
-    const size_t lds = sizeof(float) * std::max((size_t)kPmTok * pm_stride(limit), (size_t)4 * 16 * 64);
+    // the scores, later the half sums [4][16][64] and the output tile [32][hd + 4]
+    const size_t lds =
+        sizeof(float) * std::max((size_t)kPmTok * pm_stride(limit), (size_t)4 * 16 * 64 + (size_t)kPmTok * (hd + 4));
     const dim3 grid((unsigned)((M + kPmTok - 1) / kPmTok), (unsigned)heads);
 #define GX_PM(HH)                                                                                                    \
     attn_prompt_mfma_kernel<HH><<<grid, kPmThreads, lds, ctx->stream>>>(                                             \
