@@ -1684,7 +1684,12 @@ __global__ __launch_bounds__(kPmThreads, 4) void attn_prompt_mfma_kernel(
     __shared__ float bsum[kPmTok][kPmMax / 64];
     __shared__ __align__(16) uint16_t qs[kPmTok][HD + 8];  // the tile's queries (+8: rows 4 banks apart)
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, li = lane & 31, g = lane >> 5;
-    const int h = blockIdx.y, t0 = blockIdx.x * kPmTok;
+    // the second half of the heads takes the token tiles in reverse order:
+    // workgroups L and L + grid / 2, which tend to share a CU, then hold
+    // tiles i and n - 1 - i (light with heavy) rather than the same tile
+    const int h = blockIdx.y;
+    const int tile = 2 * blockIdx.y >= gridDim.y ? gridDim.x - 1 - blockIdx.x : blockIdx.x;
+    const int t0 = tile * kPmTok;
     const int kvh = h / (heads / kv_heads);
     const int stride = pm_stride(limit);
 
