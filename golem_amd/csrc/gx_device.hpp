@@ -64,69 +64,61 @@ __device__ __forceinline__ int32_t nearest_int(float f) {
 
 // (float)exp((double)d) for d <= 0 (a softmax's s - max, as SoftmaxInPlace
 // takes it, nn/ops.go:59-73), as straight-line float64 arithmetic so that
-// several exponentials interleave: n = rint(d log2 e), r = d - n ln2 (ln2
-// split hi + lo, the first product exact), e^r by Horner's rule on the Taylor
-// series to r^13 (|r| <= 0.347: truncation below 1e-17), scaled by 2^n, then
-// rounded to float.  Below -110 (under float's least subnormal) and at -inf
-// the result is +0; a NaN stays NaN.  Over every float in [-110, 0] it
-// equals (float)exp((double)d) of a correctly rounded float64 exp, bit for
-// bit (checked exhaustively on the host against the C library); the same
-// steps in C are the oracle's orc_exp_neg.
+// several exponentials interleave: n = rint(d 64 / ln2), r = d - n ln2 / 64
+// (ln2 / 64 split hi + lo, the first product exact: hi has 42 significant
+// bits and |n| < 2^14), e^r - 1 by Horner's rule on the Taylor series to r^5
+// (|r| <= ln2 / 128), then 2^(j/64) (1 + (e^r - 1)) with j = n mod 64 from a
+// table of the 64 float64 values 2^(j/64), correctly rounded, as one fma,
+// scaled by 2^(n div 64) and rounded to float.  Below -110 (under float's
+// least subnormal) and at -inf the result is +0; a NaN stays NaN.  Over every
+// float in [-110, 0] it equals (float)exp((double)d) of a correctly rounded
+// float64 exp, bit for bit (checked exhaustively on the host against the C
+// library; a Taylor series to r^4 is not enough: 9 floats differ); the same
+// steps in C are the oracle's orc_exp_neg.  Twelve float64 operations and a
+// table read, where the series to r^13 without a table took twenty-one.
+__constant__ double kExp2Sixtyfourths[64] = {
+    0x1p+0, 0x1.02c9a3e778061p+0, 0x1.059b0d3158574p+0, 0x1.0874518759bc8p+0,
+    0x1.0b5586cf9890fp+0, 0x1.0e3ec32d3d1a2p+0, 0x1.11301d0125b51p+0, 0x1.1429aaea92dep+0,
+    0x1.172b83c7d517bp+0, 0x1.1a35beb6fcb75p+0, 0x1.1d4873168b9aap+0, 0x1.2063b88628cd6p+0,
+    0x1.2387a6e756238p+0, 0x1.26b4565e27cddp+0, 0x1.29e9df51fdee1p+0, 0x1.2d285a6e4030bp+0,
+    0x1.306fe0a31b715p+0, 0x1.33c08b26416ffp+0, 0x1.371a7373aa9cbp+0, 0x1.3a7db34e59ff7p+0,
+    0x1.3dea64c123422p+0, 0x1.4160a21f72e2ap+0, 0x1.44e086061892dp+0, 0x1.486a2b5c13cdp+0,
+    0x1.4bfdad5362a27p+0, 0x1.4f9b2769d2ca7p+0, 0x1.5342b569d4f82p+0, 0x1.56f4736b527dap+0,
+    0x1.5ab07dd485429p+0, 0x1.5e76f15ad2148p+0, 0x1.6247eb03a5585p+0, 0x1.6623882552225p+0,
+    0x1.6a09e667f3bcdp+0, 0x1.6dfb23c651a2fp+0, 0x1.71f75e8ec5f74p+0, 0x1.75feb564267c9p+0,
+    0x1.7a11473eb0187p+0, 0x1.7e2f336cf4e62p+0, 0x1.82589994cce13p+0, 0x1.868d99b4492edp+0,
+    0x1.8ace5422aa0dbp+0, 0x1.8f1ae99157736p+0, 0x1.93737b0cdc5e5p+0, 0x1.97d829fde4e5p+0,
+    0x1.9c49182a3f09p+0, 0x1.a0c667b5de565p+0, 0x1.a5503b23e255dp+0, 0x1.a9e6b5579fdbfp+0,
+    0x1.ae89f995ad3adp+0, 0x1.b33a2b84f15fbp+0, 0x1.b7f76f2fb5e47p+0, 0x1.bcc1e904bc1d2p+0,
+    0x1.c199bdd85529cp+0, 0x1.c67f12e57d14bp+0, 0x1.cb720dcef9069p+0, 0x1.d072d4a07897cp+0,
+    0x1.d5818dcfba487p+0, 0x1.da9e603db3285p+0, 0x1.dfc97337b9b5fp+0, 0x1.e502ee78b3ff6p+0,
+    0x1.ea4afa2a490dap+0, 0x1.efa1bee615a27p+0, 0x1.f50765b6e454p+0, 0x1.fa7c1819e90d8p+0
+};
+
 __device__ __forceinline__ float exp_neg(float df) {
     const double d = (double)df;
-    const double n = __builtin_rint(d * 1.4426950408889634);
-    double r = __builtin_fma(-n, 6.93147180369123816490e-01, d);
-    r = __builtin_fma(-n, 1.90821492927058770002e-10, r);
-    double p = 1.0 / 6227020800.0;
-    p = __builtin_fma(p, r, 1.0 / 479001600.0);
-    p = __builtin_fma(p, r, 1.0 / 39916800.0);
-    p = __builtin_fma(p, r, 1.0 / 3628800.0);
-    p = __builtin_fma(p, r, 1.0 / 362880.0);
-    p = __builtin_fma(p, r, 1.0 / 40320.0);
-    p = __builtin_fma(p, r, 1.0 / 5040.0);
-    p = __builtin_fma(p, r, 1.0 / 720.0);
-    p = __builtin_fma(p, r, 1.0 / 120.0);
+    const double n = __builtin_rint(d * 0x1.71547652b82fep+6);
+    double r = __builtin_fma(-n, 0x1.62e42fefa38p-7, d);
+    r = __builtin_fma(-n, 0x1.ef358p-51, r);
+    double p = 1.0 / 120.0;
     p = __builtin_fma(p, r, 1.0 / 24.0);
     p = __builtin_fma(p, r, 1.0 / 6.0);
     p = __builtin_fma(p, r, 0.5);
     p = __builtin_fma(p, r, 1.0);
-    p = __builtin_fma(p, r, 1.0);
-    const float out = (float)__builtin_ldexp(p, (int)n);
+    p = p * r;
+    const int ni = (int)n;
+    const double t = kExp2Sixtyfourths[ni & 63];
+    const float out = (float)__builtin_ldexp(__builtin_fma(t, p, t), ni >> 6);
     return d < -110.0 ? 0.0f : out;
 }
 
-// exp_neg of N values, the steps written for all N in turn: N independent
-// float64 chains side by side, each value's bits exp_neg's.
+// exp_neg of N values: N independent float64 chains side by side, each
+// value's bits exp_neg's.
 template <int N>
 __device__ __forceinline__ void exp_neg_n(const float *df, float *out) {
-    constexpr double c[12] = {1.0 / 479001600.0, 1.0 / 39916800.0, 1.0 / 3628800.0, 1.0 / 362880.0,
-                              1.0 / 40320.0,     1.0 / 5040.0,     1.0 / 720.0,     1.0 / 120.0,
-                              1.0 / 24.0,        1.0 / 6.0,        0.5,             1.0};
-    double d[N], n[N], r[N], p[N];
-#pragma unroll
-    for (int i = 0; i < N; i++) {
-        d[i] = (double)df[i];
-        n[i] = __builtin_rint(d[i] * 1.4426950408889634);
-    }
 #pragma unroll
     for (int i = 0; i < N; i++)
-        r[i] = __builtin_fma(-n[i], 6.93147180369123816490e-01, d[i]);
-#pragma unroll
-    for (int i = 0; i < N; i++) {
-        r[i] = __builtin_fma(-n[i], 1.90821492927058770002e-10, r[i]);
-        p[i] = 1.0 / 6227020800.0;
-    }
-#pragma unroll
-    for (int k = 0; k < 12; k++)
-#pragma unroll
-        for (int i = 0; i < N; i++)
-            p[i] = __builtin_fma(p[i], r[i], c[k]);
-#pragma unroll
-    for (int i = 0; i < N; i++) {
-        p[i] = __builtin_fma(p[i], r[i], 1.0);
-        const float v = (float)__builtin_ldexp(p[i], (int)n[i]);
-        out[i] = d[i] < -110.0 ? 0.0f : v;
-    }
+        out[i] = exp_neg(df[i]);
 }
 
 // expf (ggml_v_expf one value at a time), nn/swiglu.go:31-74.
