@@ -855,8 +855,10 @@ int launch_dense(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, const int8
     // Up to 1024 tokens, 32-token workgroups: twice as many of them to fill
     // the CUs (config 2's 9728 x 2560 in a graph over rotating copies: M = 64
     // 25.0 -> 20.1 us, M = 512 62.0 -> 56.1 us; M = 2048 195 against 198 us
-    // keeps 64).  The per-token arithmetic is the same either way.
-    const int tok = M <= 1024 ? 32 : kDmaTok;
+    // keeps 64), unless the 64-token form has a thousand workgroups anyway
+    // (config 3's Gate|Up, 19456 rows, at a 512-token prompt: the prefill
+    // 9.93 -> 9.80 ms).  The per-token arithmetic is the same either way.
+    const int tok = (M <= 1024 && pairs * ((M + kDmaTok - 1) / kDmaTok) < 1000) ? 32 : kDmaTok;
     const int groups = (M + tok - 1) / tok;
     // XCD order for matrices of at least eight row pairs (every XCD some).
     const int xp = pairs >= 8 ? pairs : 0;
