@@ -1186,6 +1186,155 @@ __global__ __launch_bounds__(kSortThreads) void moe_sort_kernel(const int32_t *_
     }
 }
 
+// The same stable counting sort in one pass, for at most kSortSmallC chunks
+// of kSortThreads units and E * kSortSmallC * kSortWaves counters in LDS (a
+// prompt's units at a time), run by workgroup 0 of moe_sort_quant_kernel:
+// unit u = tid + kSortThreads c is counted in its (chunk, wavefront) group's
+// counter of its expert and ranked among the group's lower lanes; each
+// expert's counters are then prefixed in (chunk, wavefront) order by eight
+// lanes at once and the experts' first places and items by one scan, so a
+// unit's place first[e] + (earlier groups' count) + rank is the one the
+// chunked kernel above gives it: units of an expert in unit order.
+constexpr int kSortSmallC = 4;
+constexpr int kSortSmallCounters = 8192;
+
+__host__ __device__ inline bool sort_small_fits(int U, int E) {
+    const int C = (U + kSortThreads - 1) / kSortThreads;
+    return C <= kSortSmallC && E <= kSortThreads / 8 && C * kSortWaves * E <= kSortSmallCounters;
+}
+
+__device__ __forceinline__ void sort_small(const int32_t *__restrict__ ids, int U, int E, int tile, int max_items,
+                                           int32_t *__restrict__ sorted, int32_t *__restrict__ work, int32_t *sh,
+                                           int *tmp) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int C = (U + kSortThreads - 1) / kSortThreads, G = C * kSortWaves;  // (chunk, wavefront) groups
+    int32_t *cnt = sh;                                  // [G][E]: counts, then exclusive offsets
+    int32_t *ids_s = sh + kSortSmallCounters;           // [C][kSortThreads] (16-byte aligned)
+    int32_t *first = ids_s + kSortSmallC * kSortThreads;  // [E]
+    for (int i = tid; i < G * E; i += kSortThreads)
+        cnt[i] = 0;
+    for (int i = tid; i < 4 * max_items; i += kSortThreads)
+        work[i] = 0;
+    int ev[kSortSmallC];
+#pragma unroll
+    for (int c = 0; c < kSortSmallC; c++) {
+        const int u = tid + kSortThreads * c;
+        int e = c < C && u < U ? ids[u] : -1;
+        e = e >= 0 && e < E ? e : -1;
+        ev[c] = e;
+        if (c < C)
+            ids_s[kSortThreads * c + tid] = e;
+    }
+    __syncthreads();
+    int rank[kSortSmallC];
+#pragma unroll
+    for (int c = 0; c < kSortSmallC; c++) {
+        rank[c] = 0;
+        if (c < C) {
+            const int e = ev[c];
+            if (e >= 0)
+                atomicAdd(&cnt[(kSortWaves * c + wave) * E + e], 1);
+            // this unit's rank among the lanes below it with the same expert
+            const int4 *cw = (const int4 *)(ids_s + kSortThreads * c + 64 * wave);
+            int r = 0;
+#pragma unroll
+            for (int q = 0; q < 16; q++) {
+                const int4 c4 = cw[q];
+                r += (int)((c4.x == e) & (4 * q + 0 < lane));
+                r += (int)((c4.y == e) & (4 * q + 1 < lane));
+                r += (int)((c4.z == e) & (4 * q + 2 < lane));
+                r += (int)((c4.w == e) & (4 * q + 3 < lane));
+            }
+            rank[c] = r;
+        }
+    }
+    __syncthreads();
+    // each expert's groups in order: eight lanes an expert, G / 8 groups a lane
+    // (G is a multiple of 16), a serial prefix then a scan over the eight
+    int total = 0;
+    {
+        const int e = tid >> 3, j = tid & 7, per = G >> 3;
+        int run = 0;
+        if (e < E) {
+            for (int i = 0; i < per; i++) {
+                const int at = (j * per + i) * E + e;
+                const int v = cnt[at];
+                cnt[at] = run;
+                run += v;
+            }
+        }
+        int inc = run;
+#pragma unroll
+        for (int d = 1; d < 8; d <<= 1) {
+            const int o = __shfl_up(inc, d, 8);
+            if (j >= d)
+                inc += o;
+        }
+        const int before = inc - run;  // this lane's groups start after the lower lanes'
+        if (e < E) {
+            for (int i = 0; i < per; i++)
+                cnt[(j * per + i) * E + e] += before;
+        }
+        total = __shfl(inc, 7, 8);  // the expert's count, in each of its eight lanes
+    }
+    // the experts' totals to thread e (through first[], overwritten below
+    // after the scan's barriers), then their first places and first items
+    if ((tid & 7) == 0 && (tid >> 3) < E)
+        first[tid >> 3] = total;
+    __syncthreads();
+    const int ce = tid < E ? first[tid] : 0;
+    const int ni = (ce + tile - 1) / tile;
+    int fp, fi;
+    scan2_exclusive(ce, ni, fp, fi, tmp);
+    if (tid < E) {
+        first[tid] = fp;
+        for (int f = 0; f < ni && fi + f < max_items; f++) {
+            work[4 * (fi + f)] = tid;
+            work[4 * (fi + f) + 1] = fp + f * tile;
+            work[4 * (fi + f) + 2] = min(tile, ce - f * tile);
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < kSortSmallC; c++) {
+        const int e = ev[c];
+        if (c < C && e >= 0)
+            sorted[first[e] + cnt[(kSortWaves * c + wave) * E + e] + rank[c]] = tid + kSortThreads * c;
+    }
+}
+
+// The grouped path's first launch: workgroup 0 sorts the units (sort_small),
+// the others quantise each position's input to Q8_0 for its k units, four
+// values a thread (eight threads a block: q8_0_quad, Batch.quantizeBlock's
+// bits), as quantize_q8_0_kernel does one value a thread.
+__global__ __launch_bounds__(kSortThreads) void moe_sort_quant_kernel(
+    const int32_t *__restrict__ ids, int U, int E, int tile, int max_items, int32_t *__restrict__ sorted,
+    int32_t *__restrict__ work, const float *__restrict__ x, int ldx, int M, int D, int8_t *__restrict__ q,
+    float *__restrict__ scales, int32_t *__restrict__ qsum) {
+    extern __shared__ __align__(16) int32_t sort_sh[];
+    __shared__ int tmp[2 * kSortWaves];
+    if (blockIdx.x == 0) {
+        sort_small(ids, U, E, tile, max_items, sorted, work, sort_sh, tmp);
+        return;
+    }
+    const size_t i4 = (size_t)(blockIdx.x - 1) * kSortThreads + threadIdx.x;
+    const int n4 = D / 4;
+    if (i4 >= (size_t)M * n4)  // whole eight-lane groups: D % 32 == 0
+        return;
+    const int m = (int)(i4 / n4), c4 = (int)(i4 - (size_t)m * n4);
+    const float4 xv = *(const float4 *)(x + (size_t)m * ldx + 4 * c4);
+    const float v[4] = {xv.x, xv.y, xv.z, xv.w};
+    float stored;
+    int32_t sm;
+    const uint32_t packed = q8_0_quad(v, &stored, &sm);
+    *(uint32_t *)(q + (size_t)m * D + 4 * c4) = packed;
+    if ((c4 & 7) == 0) {
+        const size_t b = (size_t)m * (D >> 5) + (c4 >> 3);
+        scales[b] = stored;
+        qsum[b] = sm;
+    }
+}
+
 constexpr size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
 // Workspace layout for M positions, k slots, width D, expert width F.
@@ -1321,6 +1470,20 @@ int unit_shape(const gx_weight *gate_up, const gx_weight *down, int k, UnitShape
 
 namespace {
 
+// The sort and the input's Q8_0 in one launch, when the units fit the
+// one-pass sort and the input is whole float4s; false: nothing launched.
+bool launch_sort_quant(gx_ctx *ctx, const int32_t *ids, int U, int E, const MoeSpace &s, int32_t *sorted,
+                       int32_t *work, const float *x, int ldx, int M, int D, int8_t *xq, float *xs, int32_t *xqs) {
+    if (!sort_small_fits(U, E) || ((uintptr_t)x & 15) != 0 || ldx % 4 != 0 || D % 32 != 0)
+        return false;
+    const size_t lds = (size_t)(kSortSmallCounters + kSortSmallC * kSortThreads + E) * sizeof(int32_t);
+    const size_t n4 = (size_t)M * D / 4;
+    const unsigned grid = 1 + (unsigned)((n4 + kSortThreads - 1) / kSortThreads);
+    moe_sort_quant_kernel<<<grid, kSortThreads, lds, ctx->stream>>>(ids, U, E, kGroupTok, s.max_items, sorted, work,
+                                                                   x, ldx, M, D, xq, xs, xqs);
+    return true;
+}
+
 int launch_sort(gx_ctx *ctx, const int32_t *ids, int U, int E, const MoeSpace &s, int32_t *sorted, int32_t *work) {
     const size_t lds = (size_t)((2 + kSortWaves) * E + kSortThreads) * sizeof(int32_t);
     GX_CHECK(E <= kSortThreads && lds <= 64 * 1024, "gx: %d experts do not fit the sort's LDS", E);
@@ -1386,13 +1549,19 @@ int launch_moe_experts(gx_ctx *ctx, const gx_weight *gate_up, const gx_weight *d
     float *part = (float *)(ws + s.part);
     int32_t *sorted = (int32_t *)(ws + s.sorted);
     int32_t *work = (int32_t *)(ws + s.work);
-    // Each position's input, quantised once for its k units (moe.go:119-125).
-    if (int rc = launch_quantize_q8_0(ctx, x, ldx, M, D, xq, xs, xqs, nullptr, nullptr))
-        return rc;
-    // A unit whose expert id is out of range is in no group: its rows are
-    // never written, and the sum makes its position's output NaN.
-    if (int rc = launch_sort(ctx, ids, U, E, s, sorted, work))
-        return rc;
+    // Each position's input, quantised once for its k units (moe.go:119-125),
+    // and the units sorted by expert.  A unit whose expert id is out of range
+    // is in no group: its rows are never written, and the sum makes its
+    // position's output NaN.
+    if (launch_sort_quant(ctx, ids, U, E, s, sorted, work, x, ldx, M, D, xq, xs, xqs)) {
+        if (int rc = check_launch("moe_sort_quant"))
+            return rc;
+    } else {
+        if (int rc = launch_quantize_q8_0(ctx, x, ldx, M, D, xq, xs, xqs, nullptr, nullptr))
+            return rc;
+        if (int rc = launch_sort(ctx, ids, U, E, s, sorted, work))
+            return rc;
+    }
     if (int rc = launch_q4_0_gemm_grouped(ctx, gate_up, work, s.max_items, sorted, k, xq, xs, gu, 2 * F, nullptr))
         return rc;
     const size_t nm4 = (size_t)U * F / 4;  // gu is the workspace's (aligned), F a multiple of 32
