@@ -253,6 +253,58 @@ def test_bad_expert_id_poisons_its_position(dev):
         assert not np.any(np.isnan(out[1:]))
 
 
+def test_sort_forms_agree(dev):
+    """The grouped path sorts the units by expert in one of two forms: one
+    pass inside the launch that quantises the input (at most 4,096 units over
+    at most 128 experts, the input whole float4s), or the three-phase sort
+    after a quantising launch (more units, more experts, or a row stride not
+    a multiple of four).  A position's output does not depend on which ran:
+    1,100 positions x 4 (4,400 units: three-phase) against the same positions
+    in halves of 550 (2,200 units: one pass); the halves read through a row
+    stride of D + 1 (three-phase); and with 200 experts (three-phase at any
+    size) sampled positions against the same position alone."""
+    D, F, k = 256, 64, 4
+
+    def draw(moe, M):
+        ids = np.stack([moe.g.choice(moe.E, k, replace=False) for _ in range(M)]).astype(np.int32)
+        w = moe.g.uniform(0.05, 0.5, (M, k)).astype(np.float32)
+        return ids, w
+
+    moe = Moe(dev, D, F, 16, k, 70)
+    M = 1100
+    x = synth.activations(moe.g, M, D)
+    ids, w = draw(moe, M)
+    whole = dev.get(moe.experts(x, dev.put(ids), dev.put(w)))
+    assert not np.any(np.isnan(whole))
+    for h in (slice(0, 550), slice(550, 1100)):
+        half = dev.get(moe.experts(x[h], dev.put(ids[h]), dev.put(w[h])))
+        np.testing.assert_array_equal(half.view(np.uint32), whole[h].view(np.uint32), err_msg=f"half {h}")
+        # the same half read with a row stride of D + 1
+        import ctypes
+        Mh = half.shape[0]
+        xs = np.zeros((Mh, D + 1), np.float32)
+        xs[:, :D] = x[h]
+        n = ctypes.c_size_t()
+        capi.call("gx_moe_workspace_bytes", Mh, k, D, F, moe.E, ctypes.byref(n))
+        ws = dev.empty((n.value,), np.uint8)
+        xd, idd, wd = dev.put(xs), dev.put(ids[h]), dev.put(w[h])
+        out = dev.full((Mh, D), float("nan"))
+        capi.call("gx_moe_experts", dev.ctx.ptr, moe.wgu.ptr, moe.wdn.ptr, None, capi.vp(xd), D + 1, Mh, k,
+                  capi.vp(idd), capi.vp(wd), capi.vp(out), D, capi.vp(ws), n.value)
+        np.testing.assert_array_equal(dev.get(out).view(np.uint32), whole[h].view(np.uint32),
+                                      err_msg=f"half {h}, stride D + 1")
+    log("sort forms: 4,400 units (three-phase) == two halves of 2,200 (one pass) == strided halves")
+
+    moe = Moe(dev, D, F, 200, k, 71)
+    M = 300
+    x = synth.activations(moe.g, M, D)
+    ids, w = draw(moe, M)
+    batch = dev.get(moe.experts(x, dev.put(ids), dev.put(w)))
+    for t in (0, 1, 150, 299):
+        one = dev.get(moe.experts(x[t:t + 1], dev.put(ids[t:t + 1]), dev.put(w[t:t + 1])))
+        np.testing.assert_array_equal(one[0].view(np.uint32), batch[t].view(np.uint32), err_msg=f"position {t}")
+
+
 @pytest.mark.parametrize("M,spread", [(2, 128), (40, 128), (40, 8)])
 def test_expert_integers_bit_exact(dev, orc, M, spread):
     """The expert products' per-block integers (gx_moe_block_dots) at config
