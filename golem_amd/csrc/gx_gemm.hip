@@ -857,8 +857,15 @@ int launch_dense(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, const int8
     // 25.0 -> 20.1 us, M = 512 62.0 -> 56.1 us; M = 2048 195 against 198 us
     // keeps 64), unless the 64-token form has a thousand workgroups anyway
     // (config 3's Gate|Up, 19456 rows, at a 512-token prompt: the prefill
-    // 9.93 -> 9.80 ms).  The per-token arithmetic is the same either way.
-    const int tok = (M <= 1024 && pairs * ((M + kDmaTok - 1) / kDmaTok) < 1000) ? 32 : kDmaTok;
+    // 9.93 -> 9.80 ms).  Between 256 and 512 of them, though, some CUs take
+    // two 32-token workgroups to the others' one, where the 64-token form
+    // fits in one round (config 3's O and Down, 2560 rows, at a 512-token
+    // prompt: 35.1 -> 33.1 and 71.0 -> 63.6 us).  The per-token arithmetic
+    // is the same either way.
+    const int w32 = pairs * ((M + 31) / 32);
+    const int tok = (M <= 1024 && pairs * ((M + kDmaTok - 1) / kDmaTok) < 1000 && (w32 <= 256 || w32 > 512))
+                        ? 32
+                        : kDmaTok;
     const int groups = (M + tok - 1) / tok;
     // XCD order for matrices of at least eight row pairs (every XCD some).
     const int xp = pairs >= 8 ? pairs : 0;
