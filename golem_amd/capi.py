@@ -71,6 +71,8 @@ _SIGNATURES = {
     "gx_moe_experts": [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _vp, _vp, _c_int, _vp, _c_size],
     "gx_moe_experts_noalloc": [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _vp, _vp, _c_int],
     "gx_norm_quant": [_vp, _vp, _c_int, _vp, _c_int, _vp, _c_int, _c_int, ctypes.c_float, _vp, _c_int, _vp, _vp, _vp],
+    "gx_qwen_qkv_rope": [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _vp,
+                         ctypes.c_float, _vp, _vp, _vp, _c_int, _vp, _c_int, _vp],
     "gx_qwen_qk_rope": [_vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _vp, ctypes.c_float,
                         _vp, _vp, _vp, _c_int, _vp, _c_int],
     "gx_qwen_attention_workspace_bytes": [_c_int, _c_int, _c_int, ctypes.POINTER(_c_size)],

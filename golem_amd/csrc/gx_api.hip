@@ -843,6 +843,44 @@ int gx_qwen_qk_rope(gx_ctx *ctx, const float *qkv, int ldqkv, int M, int heads, 
     return ok();
 }
 
+int gx_qwen_qkv_rope(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const float *scales, const int32_t *qsum,
+                     int M, int heads, int kv_heads, int head_dim, const int32_t *positions, const float *q_norm,
+                     const float *k_norm, const float *rope_cos, const float *rope_sin, float eps, uint16_t *qh,
+                     uint16_t *kcache, uint16_t *vcache, int context, const int32_t *slots, int nslots,
+                     float *qkv) {
+    if (int rc = use(ctx))
+        return rc;
+    GX_CHECK(w != nullptr && w->quant == GX_Q4_0 && w->count == 1, "gx: the Q|K|V product takes one Q4_0 matrix");
+    GX_CHECK(heads > 0 && kv_heads > 0 && heads % kv_heads == 0, "gx: %d query heads over %d key-value heads", heads,
+             kv_heads);
+    GX_CHECK(head_dim > 0 && w->rows == (heads + 2 * kv_heads) * head_dim,
+             "gx: %d rows are not %d query and 2 x %d key-value heads of %d", w->rows, heads, kv_heads, head_dim);
+    GX_CHECK(M >= 0 && context > 0, "gx: bad batch shape");
+    GX_CHECK(q && scales && qsum && positions && q_norm && k_norm && rope_cos && rope_sin && qh && kcache && vcache,
+             "gx: missing argument");
+    GX_CHECK(((uintptr_t)q & 15) == 0, "gx: q must be 16-byte aligned");
+    GX_CHECK(!slots || nslots > 0, "gx: %d slots", nslots);
+    if (M == 0)
+        return ok();
+    const bool fused = M > 16 && (head_dim == 64 || head_dim == 128) &&
+                       (((uintptr_t)rope_cos | (uintptr_t)rope_sin) & 15) == 0;
+    if (fused) {
+        const gx::QkvRopeArgs a{positions, q_norm, k_norm, rope_cos, rope_sin, eps,  qh,
+                                kcache,    vcache, context, heads, kv_heads, head_dim, slots, nslots};
+        if (int rc = gx::launch_q4_0_gemm_qkv_rope(ctx, w, q, scales, M, a))
+            return rc;
+        return ok();
+    }
+    GX_CHECK(qkv != nullptr, "gx: %d positions of head width %d need the qkv buffer (the product, then the heads)", M,
+             head_dim);
+    if (int rc = q4_0_product(ctx, w, 0, q, scales, qsum, nullptr, M, 0, w->rows, nullptr, qkv, w->rows))
+        return rc;
+    if (int rc = gx::launch_qwen_qk_rope(ctx, qkv, w->rows, M, heads, kv_heads, head_dim, positions, q_norm, k_norm,
+                                         rope_cos, rope_sin, eps, qh, kcache, vcache, context, slots, nslots))
+        return rc;
+    return ok();
+}
+
 static int rope_attention(gx_ctx *ctx, const float *qkv, int ldqkv, int M, int heads, int kv_heads, int head_dim,
                           int max_pos, const int32_t *positions, const float *q_norm, const float *k_norm,
                           const float *rope_cos, const float *rope_sin, float eps, uint16_t *kcache, uint16_t *vcache,

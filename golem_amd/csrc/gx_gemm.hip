@@ -426,6 +426,144 @@ struct DmaShape<32> {
     static constexpr int kAct = 8192, kActScale = 12288, kWScale = 12800, kDummy = 13824;
 };
 
+// EPI 2's epilogue (see the kernel): 4 wavefronts, wavefront rg holding
+// rows 32 rg .. of the workgroup's 128 for tokens first + li.  Element e of
+// a rotated head: pair j = e % half, a = re c - im s (e < half), b = re s +
+// im c, re = x_j sc g_j, im = x_{j+half} sc g_{j+half} (RoPETable.Apply,
+// nn/rope.go:62-73; qwen/attention.go:57-84, qwen/cache.go:52-60).
+constexpr int kQkvStride = 129;  // a token's staged row: a lane a token reads down a column without conflicts
+
+__device__ __forceinline__ void qkv_rope_epilogue(const v16f &tot, uint8_t *lds, const QkvRopeArgs &qr, int T0,
+                                                  int rg, int li, int g, int first, int count) {
+    const int tid = threadIdx.x;
+    const int hd = qr.hd, half = hd >> 1, P = hd >> 3, hpw = 128 / hd;  // pieces a head; heads a workgroup
+    const int nheads = qr.heads + 2 * qr.kv_heads;
+    const int h0 = T0 * kTileRows / hd;  // the workgroup's first head
+    float *hs = (float *)lds;                       // [32 tokens][kQkvStride]
+    float *gs = hs + 32 * kQkvStride;               // [128]: each row's gain
+    float *scs = gs + 128;                          // [2][32] norm scales
+    int *pos_s = (int *)(scs + 64), *place_s = pos_s + 32, *slot_s = place_s + 32;
+    __syncthreads();  // every wavefront is past its last operand reads
+#pragma unroll
+    for (int e = 0; e < 16; e++)
+        hs[li * kQkvStride + 32 * rg + 8 * (e >> 2) + 4 * g + (e & 3)] = tot[e];
+    // section of head k of the workgroup: 0 query, 1 key, 2 value, 3 none
+    auto section = [&](int k) -> int {
+        const int hg = h0 + k;
+        return hg < qr.heads ? 0 : hg < qr.heads + qr.kv_heads ? 1 : hg < nheads ? 2 : 3;
+    };
+    if (tid < 32) {
+        int pl = -1, pos = 0, sl = 0;
+        if (tid < count) {
+            const int t = first + tid;
+            pos = qr.positions[t];
+            sl = qr.slots ? qr.slots[t] : 0;
+            pl = pos >= 0 && pos < qr.context && (!qr.slots || (sl >= 0 && sl < qr.nslots)) ? 1 : 0;
+        }
+        pos_s[tid] = pos;
+        place_s[tid] = pl;
+        slot_s[tid] = sl;
+    } else if (tid >= 64 && tid < 192) {
+        const int r = tid - 64, sec = section(r / hd);
+        gs[r] = sec == 0 ? qr.q_norm[r % hd] : sec == 1 ? qr.k_norm[r % hd] : 0.0f;
+    }
+    __syncthreads();
+    // (head, token, piece) items of the query and key heads, two a thread:
+    // a query's pieces fastest (contiguous in qh), a key's tokens fastest
+    // (a piece's positions are contiguous in the cache).  Their rotation
+    // tables go out now, while the norms' sums run.
+    float4 c0[2], c1[2], s0[2], s1[2];
+    int ik[2], itk[2], ipc[2], isec[2];
+#pragma unroll
+    for (int it = 0; it < 2; it++) {
+        const int idx = tid + 256 * it, k = idx / (32 * P), rem = idx - k * 32 * P;
+        const int sec = section(k);
+        const int tk = sec == 0 ? rem / P : rem & 31, pc = sec == 0 ? rem % P : rem >> 5;
+        ik[it] = k, itk[it] = tk, ipc[it] = pc, isec[it] = sec;
+        if (sec <= 1 && place_s[tk] > 0) {
+            const int pos = pos_s[tk];
+            const int j0 = 8 * pc < half ? 8 * pc : 8 * pc - half;
+            c0[it] = *(const float4 *)(qr.rope_cos + (size_t)pos * half + j0);
+            c1[it] = *(const float4 *)(qr.rope_cos + (size_t)pos * half + j0 + 4);
+            s0[it] = *(const float4 *)(qr.rope_sin + (size_t)pos * half + j0);
+            s1[it] = *(const float4 *)(qr.rope_sin + (size_t)pos * half + j0 + 4);
+        }
+    }
+    if (tid < 32 * hpw) {
+        // head_norm_scale's sum, left to right, sixteen values read ahead
+        const int k = tid >> 5, tk = tid & 31;
+        if (section(k) <= 1 && tk < count) {
+            const float *hr = hs + tk * kQkvStride + k * hd;
+            double acc = 0.0;
+            for (int i0 = 0; i0 < hd; i0 += 16) {
+                float v[16];
+#pragma unroll
+                for (int i = 0; i < 16; i++)
+                    v[i] = hr[i0 + i];
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    const float sq = v[i] * v[i];
+                    acc += (double)sq;
+                }
+            }
+            const float mean = (float)(acc / (double)hd);
+            scs[tid] = (float)(1.0 / sqrt((double)(mean + qr.eps)));
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int it = 0; it < 2; it++) {
+        const int k = ik[it], tk = itk[it], pc = ipc[it], sec = isec[it];
+        const int pl = place_s[tk];
+        if (sec > 1 || pl < 0)
+            continue;
+        const int pos = pos_s[tk], hg = h0 + k;
+        uint32_t w[4] = {0x7E007E00u, 0x7E007E00u, 0x7E007E00u, 0x7E007E00u};  // no place: a NaN query
+        if (pl) {
+            const bool lo = 8 * pc < half;
+            const int j0 = lo ? 8 * pc : 8 * pc - half;
+            const float cs[8] = {c0[it].x, c0[it].y, c0[it].z, c0[it].w, c1[it].x, c1[it].y, c1[it].z, c1[it].w};
+            const float sn[8] = {s0[it].x, s0[it].y, s0[it].z, s0[it].w, s1[it].x, s1[it].y, s1[it].z, s1[it].w};
+            const float sc = scs[k * 32 + tk];
+            const float *hr = hs + tk * kQkvStride + k * hd;
+            const float *gr = gs + k * hd;
+            uint32_t hb[8];
+#pragma unroll
+            for (int kk = 0; kk < 8; kk++) {
+                const int j = j0 + kk;
+                const float re = (hr[j] * sc) * gr[j], im = (hr[j + half] * sc) * gr[j + half];
+                const float v = lo ? re * cs[kk] - im * sn[kk] : re * sn[kk] + im * cs[kk];
+                hb[kk] = float_to_half_bits(v);
+            }
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++)
+                w[kk] = hb[2 * kk] | (hb[2 * kk + 1] << 16);
+        }
+        const v4u_stream o = {w[0], w[1], w[2], w[3]};
+        if (sec == 0) {
+            *(v4u_stream *)(qr.qh + (size_t)(first + tk) * qr.heads * hd + (size_t)hg * hd + 8 * pc) = o;
+        } else if (pl) {
+            uint16_t *kt = qr.kcache + (size_t)slot_s[tk] * qr.kv_heads * hd * qr.context +
+                           (size_t)(hg - qr.heads) * hd * qr.context;
+            *(v4u_stream *)(kt + ((size_t)pc * qr.context + pos) * 8) = o;
+        }
+    }
+    // the value heads: a lane a token down each element row
+    for (int k = 0; k < hpw; k++) {
+        if (section(k) != 2)
+            continue;
+        const int kvh = h0 + k - qr.heads - qr.kv_heads;
+        for (int idx = tid; idx < 32 * hd; idx += 256) {
+            const int tk = idx & 31, d = idx >> 5;
+            if (place_s[tk] > 0) {
+                uint16_t *vt = qr.vcache + (size_t)slot_s[tk] * qr.kv_heads * hd * qr.context +
+                               (size_t)kvh * hd * qr.context;
+                vt[(size_t)d * qr.context + pos_s[tk]] = (uint16_t)float_to_half_bits(hs[tk * kQkvStride + k * hd + d]);
+            }
+        }
+    }
+}
+
 // GROUPED: blockIdx.y is an item of the expert work list (grp.work[item] =
 // {expert, first, count <= TOK, 0}; count 0 past the last item): the item's
 // tokens are units sorted[first ..], token t reading activation row
@@ -444,12 +582,20 @@ struct DmaShape<32> {
 // wavefront of a tile's up rows passes its sums through LDS to the
 // wavefront of the gate rows, whose lane pair (l, l + 32) holds one token's
 // 32 outputs, one Q8_0 block.
+//
+// EPI 2 (dense, whole matrix, TOK 32): the rows are the query, key and value
+// heads stacked (hd = 64 or 128 rows a head, so a workgroup's 128 rows are
+// whole heads), and the product ends in qwen_qk_rope_tile_kernel's work for
+// its heads and 32 tokens, bit for bit: the sums staged in LDS by token, a
+// query or key head's RMSNormPlain (float64, left to right, a lane a token),
+// RoPE with golem's tables, fp16, the query into qr.qh and the key and value
+// into the caches -- without the [M][rows] float round trip.
 template <int TOK, bool GROUPED, bool DOTS, int EPI = 0>
 __global__ __launch_bounds__(64 * DmaShape<TOK>::kWaves, DmaShape<TOK>::kOcc) void q4_0_gemm_dma_kernel(
     const uint8_t *__restrict__ W, size_t plane0_bytes, int B, int DC, const int8_t *__restrict__ q,
     const float *__restrict__ scales, int K, int M, int tiles, int tile0, int row_start, int row_end,
     const float *__restrict__ bias, float *__restrict__ y, int ldy, int32_t *__restrict__ dots, Groups grp,
-    int xcd_pairs, int8_t *__restrict__ mq, float *__restrict__ ms, int32_t *__restrict__ mqs) {
+    int xcd_pairs, int8_t *__restrict__ mq, float *__restrict__ ms, int32_t *__restrict__ mqs, QkvRopeArgs qr) {
     using Sh = DmaShape<TOK>;
     constexpr int kSlotB = Sh::kSlot;
     // Software-pipelined blocks (one block's MFMAs ahead of the previous
@@ -826,6 +972,9 @@ __global__ __launch_bounds__(64 * DmaShape<TOK>::kWaves, DmaShape<TOK>::kOcc) vo
                 }
             }
         }
+    } else if constexpr (EPI == 2) {
+        static_assert(TOK == 32 && !GROUPED && !DOTS, "the Q|K|V epilogue is a dense 32-token form");
+        qkv_rope_epilogue(tot, ring_lds, qr, T0, rg, li, g, first, count);
     } else if (!DOTS && t < count) {
         float *yr = y + (size_t)orow(t) * ldy;
         const int nb = T0 * kTileRows + 32 * rg;  // the wavefront's first row
@@ -873,7 +1022,7 @@ int launch_dense(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, const int8
 #define GX_DMA_LAUNCH(TK, NT, DD)                                                                                   \
     q4_0_gemm_dma_kernel<TK, false, DD, EPI><<<grid, NT, 0, ctx->stream>>>(                                         \
         mat, w->plane0_bytes, w->blocks, w->dchunks, q, scales, w->cols, M, w->tiles, tile0, row_start, row_end,     \
-        bias, y, ldy, DD ? dots : nullptr, none, xp, mq, ms, mqs)
+        bias, y, ldy, DD ? dots : nullptr, none, xp, mq, ms, mqs, QkvRopeArgs{})
     if constexpr (EPI == 1) {
         if (tok == 32)
             GX_DMA_LAUNCH(32, 256, false);
@@ -905,6 +1054,19 @@ int launch_q4_0_gemm_swiglu(gx_ctx *ctx, const gx_weight *w, const int8_t *q, co
     return launch_dense<1>(ctx, w, w->dev, q, scales, M, 0, w->rows, nullptr, nullptr, 0, nullptr, mq, ms, mqs);
 }
 
+int launch_q4_0_gemm_qkv_rope(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const float *scales, int M,
+                              const QkvRopeArgs &a) {
+    // the 32-token form always (its epilogue's shape), in XCD order
+    const int pairs = (w->tiles + 1) / 2, groups = (M + 31) / 32;
+    const Groups none{nullptr, nullptr, 1, 0};
+    const int xp = pairs >= 8 ? pairs : 0;
+    const dim3 grid = xp ? dim3((unsigned)(8 * ((pairs + 7) / 8) * groups)) : dim3((unsigned)pairs, (unsigned)groups);
+    q4_0_gemm_dma_kernel<32, false, false, 2><<<grid, 256, 0, ctx->stream>>>(
+        w->dev, w->plane0_bytes, w->blocks, w->dchunks, q, scales, w->cols, M, w->tiles, 0, 0, w->rows, nullptr,
+        nullptr, 0, nullptr, none, xp, nullptr, nullptr, nullptr, a);
+    return check_launch("q4_0_gemm qkv_rope");
+}
+
 int launch_q4_0_gemm_grouped(gx_ctx *ctx, const gx_weight *w, const int32_t *work, int max_items,
                              const int32_t *sorted, int act_div, const int8_t *q, const float *scales, float *y,
                              int ldy, int32_t *dots) {
@@ -914,11 +1076,11 @@ int launch_q4_0_gemm_grouped(gx_ctx *ctx, const gx_weight *w, const int32_t *wor
     if (dots)
         q4_0_gemm_dma_kernel<32, true, true><<<grid, 256, 0, ctx->stream>>>(
             w->dev, w->plane0_bytes, w->blocks, w->dchunks, q, scales, w->cols, 0, w->tiles, 0, 0, w->rows, nullptr,
-            y, ldy, dots, grp, 0, nullptr, nullptr, nullptr);
+            y, ldy, dots, grp, 0, nullptr, nullptr, nullptr, QkvRopeArgs{});
     else
         q4_0_gemm_dma_kernel<32, true, false><<<grid, 256, 0, ctx->stream>>>(
             w->dev, w->plane0_bytes, w->blocks, w->dchunks, q, scales, w->cols, 0, w->tiles, 0, 0, w->rows, nullptr,
-            y, ldy, nullptr, grp, 0, nullptr, nullptr, nullptr);
+            y, ldy, nullptr, grp, 0, nullptr, nullptr, nullptr, QkvRopeArgs{});
     return check_launch("q4_0_gemm_grouped");
 }
 }  // namespace gx

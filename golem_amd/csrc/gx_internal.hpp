@@ -117,6 +117,20 @@ int launch_q4_0_gemm(gx_ctx *ctx, const gx_weight *w, const uint8_t *mat, const 
                      int M, int row_start, int row_end, const float *bias, float *y, int ldy, int32_t *dots);
 int launch_q4_0_gemm_swiglu(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const float *scales, int M,
                             int8_t *mq, float *ms, int32_t *mqs);
+// The Q|K|V product of a batch with the head norms, RoPE and the fp16
+// query and cache stores of qwen_qk_rope in its epilogue (rows: the query,
+// key and value heads stacked, hd 64 or 128).
+struct QkvRopeArgs {
+    const int32_t *positions;
+    const float *q_norm, *k_norm, *rope_cos, *rope_sin;
+    float eps;
+    uint16_t *qh, *kcache, *vcache;
+    int context, heads, kv_heads, hd;
+    const int32_t *slots;
+    int nslots;
+};
+int launch_q4_0_gemm_qkv_rope(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const float *scales, int M,
+                              const QkvRopeArgs &a);
 // The expert-grouped product: work items {expert, first, count <= 32, 0}
 // over the units sorted by expert (gx_moe.hip's sort); dots as above, by
 // output (unit) row.

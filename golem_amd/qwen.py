@@ -5,8 +5,10 @@ the embedding rows (TokenEmbd.Row, a Q6_K dequantisation), then per block
 (qwen/block.go:32-102):
 
     gx_norm_quant      x += previous FFN output; RMSNormPlain(attn_norm); Q8_0
-    gx_matmul_q4_0     Q, K and V, stacked by rows into one Q4_0 matrix
-    gx_qwen_qk_rope    head norms, RoPE, fp16 query, fp16 cache entries
+    gx_qwen_qkv_rope   Q, K and V, stacked by rows into one Q4_0 matrix, then
+                       head norms, RoPE, fp16 query, fp16 cache entries (for
+                       a batch in the product's epilogue: gx_matmul_q4_0 +
+                       gx_qwen_qk_rope bit for bit)
     gx_qwen_attention  scores, softmax, values; Q8_0 of the heads
     gx_matmul_q4_0     O
     gx_norm_quant      x += attention; RMSNormPlain(ffn_norm); Q8_0
@@ -289,17 +291,20 @@ class QwenModel:
             add = None if i == 0 else vp(self.ffn)
             call("gx_norm_quant", ctx, vp(self.xs), cfg.dim, add, cfg.dim, vp(b["attn_norm"]), M, cfg.dim,
                  np.float32(cfg.eps), None, 0, vp(self.x8.q), vp(self.x8.s), vp(self.x8.qs))
-            self._mm(b["qkv"], self.x8, M, self.qkv, qd + 2 * kvd)
             if one_per_slot and max_pos < FUSED_ATTENTION_MAX:
+                self._mm(b["qkv"], self.x8, M, self.qkv, qd + 2 * kvd)
                 call("gx_qwen_rope_attention_slots", ctx, vp(self.qkv), qd + 2 * kvd, M, cfg.heads, cfg.kv_heads,
                      cfg.head_dim, max_pos, vp(self.positions), vp(b["q_norm"]), vp(b["k_norm"]),
                      vp(self.rope_cos), vp(self.rope_sin), np.float32(cfg.eps), vp(self.kc[i]), vp(self.vc[i]),
                      self.context, vp(self.set8.q), vp(self.set8.s), vp(self.set8.qs), sl, self.nslots,
                      1 if self._attention.endswith("_parallel") else 0)
             else:
-                call("gx_qwen_qk_rope", ctx, vp(self.qkv), qd + 2 * kvd, M, cfg.heads, cfg.kv_heads, cfg.head_dim,
-                     vp(self.positions), vp(b["q_norm"]), vp(b["k_norm"]), vp(self.rope_cos), vp(self.rope_sin),
-                     np.float32(cfg.eps), vp(self.qh), vp(self.kc[i]), vp(self.vc[i]), self.context, sl, self.nslots)
+                # the product and the heads' norms, RoPE and stores (one
+                # kernel for a batch: the product's epilogue)
+                call("gx_qwen_qkv_rope", ctx, b["qkv"].ptr, vp(self.x8.q), vp(self.x8.s), vp(self.x8.qs), M,
+                     cfg.heads, cfg.kv_heads, cfg.head_dim, vp(self.positions), vp(b["q_norm"]), vp(b["k_norm"]),
+                     vp(self.rope_cos), vp(self.rope_sin), np.float32(cfg.eps), vp(self.qh), vp(self.kc[i]),
+                     vp(self.vc[i]), self.context, sl, self.nslots, vp(self.qkv))
                 if sl is None or not own_slot:
                     kca, vca, sla = self.kc[i], self.vc[i], sl
                 else:

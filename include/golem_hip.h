@@ -372,6 +372,26 @@ int gx_qwen_qk_rope(gx_ctx *ctx, const float *qkv, int ldqkv, int M, int heads, 
                     const float *rope_sin, float eps, uint16_t *qh, uint16_t *kcache, uint16_t *vcache, int context,
                     const int32_t *slots, int nslots);
 
+/* The Q|K|V product of M positions followed by gx_qwen_qk_rope, the same
+ * values bit for bit: golem's Attention from its three products through the
+ * cache stores (qwen/attention.go:34-84, qwen/cache.go:52-60), with
+ * Matrix.MatMul's product (nn/matrix.go) on the Q4_0 matrix w whose rows are
+ * the heads query heads, then the kv_heads key heads, then the kv_heads
+ * value heads, head_dim rows each (golem's three matrices stacked by rows).
+ * q / scales / qsum: the activation's Q8_0 form (gx_quantize_q8_0; q 16-byte
+ * aligned).  qh, the caches, positions, slots and the rest as for
+ * gx_qwen_qk_rope.  More than 16 positions at head widths 64 and 128 run as
+ * one kernel (the heads' norms, RoPE and stores in the product's epilogue,
+ * no float Q|K|V row written); otherwise qkv ([M][w->rows] floats, device)
+ * receives the product, which then goes through gx_qwen_qk_rope -- qkv may
+ * be NULL only when the single kernel applies.  No reference counterpart
+ * as one call: it replaces the pair gx_matmul_q4_0 + gx_qwen_qk_rope. */
+int gx_qwen_qkv_rope(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const float *scales, const int32_t *qsum,
+                     int M, int heads, int kv_heads, int head_dim, const int32_t *positions, const float *q_norm,
+                     const float *k_norm, const float *rope_cos, const float *rope_sin, float eps, uint16_t *qh,
+                     uint16_t *kcache, uint16_t *vcache, int context, const int32_t *slots, int nslots,
+                     float *qkv);
+
 /* Device bytes of the workspace gx_qwen_attention needs for M positions of
  * `heads` query heads whose positions are at most max_pos. */
 int gx_qwen_attention_workspace_bytes(int M, int heads, int max_pos, size_t *bytes);

@@ -242,6 +242,66 @@ def test_qk_rope_and_cache_bit_exact(dev, orc, hd, heads, kv, M):
     assert not got_k[:, :, free, :].any() and not got_v[:, :, free].any()
 
 
+@pytest.mark.parametrize("hd,heads,kv,K,M,slots", [
+    (128, 32, 8, 2560, 512, False),  # config 3 at its prompt length
+    (128, 8, 2, 512, 70, False),     # a ragged last token group, out-of-order and unplaced positions
+    (64, 4, 2, 256, 40, True),       # two heads a workgroup; slots, one out of range
+    (64, 2, 1, 256, 17, False),      # one workgroup of a query and a query head, one of a key and a value
+    (128, 2, 1, 256, 16, False),     # 16 positions: the product, then the heads
+    (96, 4, 2, 256, 40, False),      # a head width the single kernel does not take
+])
+def test_qkv_rope_matches_product_then_heads(dev, hd, heads, kv, K, M, slots):
+    """gx_qwen_qkv_rope (the Q|K|V product with the heads' norms, RoPE and
+    fp16 stores in its epilogue for more than 16 positions at head widths 64
+    and 128) against gx_matmul_q4_0 then gx_qwen_qk_rope: the queries and
+    every cache entry bit for bit (the pair is pinned to the oracle above)."""
+    g = synth.rng(90 + hd + M)
+    rows = (heads + 2 * kv) * hd
+    ctx_len = max(2 * M, 64)
+    nslots = 3 if slots else 0
+    w = synth.q4_0_weights(g, rows, K)
+    wd = dev.weight(w, capi.Q4_0, rows, K)
+    x = synth.activations(g, M, K)
+    xq, xs, xqs, _, _ = dev.quantize_q8_0(x)
+    cos, sin = rope_tables(hd, ctx_len, 1e6)
+    qn = (1 + 0.02 * g.standard_normal(hd)).astype(np.float32)
+    kn = (1 + 0.02 * g.standard_normal(hd)).astype(np.float32)
+    pos = g.permutation(ctx_len)[:M].astype(np.int32)
+    if M > 20:
+        pos[[3, M - 4]] = [-1, ctx_len]  # no place
+    sl = g.integers(0, nslots, M).astype(np.int32) if slots else None
+    if slots:
+        sl[5] = nslots  # out of range: nothing stored, query NaN
+    ins = [dev.put(a) for a in (pos, qn, kn, cos, sin)] + ([dev.put(sl)] if slots else [None])
+    ncache = max(nslots, 1)
+
+    def run(fused):
+        qh = dev.full((M, heads * hd), 0x1234, np.int16)
+        kc = torch.zeros((ncache, kv, hd // 8, ctx_len, 8), dtype=torch.int16, device="cuda")
+        vc = torch.zeros((ncache, kv, hd, ctx_len), dtype=torch.int16, device="cuda")
+        sp = capi.vp(ins[5]) if slots else None
+        if fused:
+            qkv = dev.empty((M, rows), np.float32) if (M <= 16 or hd not in (64, 128)) else None
+            capi.call("gx_qwen_qkv_rope", dev.ctx.ptr, wd.ptr, capi.vp(xq), capi.vp(xs), capi.vp(xqs), M, heads, kv,
+                      hd, capi.vp(ins[0]), capi.vp(ins[1]), capi.vp(ins[2]), capi.vp(ins[3]), capi.vp(ins[4]),
+                      np.float32(1e-6), capi.vp(qh), capi.vp(kc), capi.vp(vc), ctx_len, sp, nslots,
+                      capi.vp(qkv) if qkv is not None else None)
+        else:
+            qkv = dev.empty((M, rows), np.float32)
+            capi.call("gx_matmul_q4_0", dev.ctx.ptr, wd.ptr, capi.vp(xq), capi.vp(xs), capi.vp(xqs), None, M, 0,
+                      rows, None, capi.vp(qkv), rows)
+            capi.call("gx_qwen_qk_rope", dev.ctx.ptr, capi.vp(qkv), rows, M, heads, kv, hd, capi.vp(ins[0]),
+                      capi.vp(ins[1]), capi.vp(ins[2]), capi.vp(ins[3]), capi.vp(ins[4]), np.float32(1e-6),
+                      capi.vp(qh), capi.vp(kc), capi.vp(vc), ctx_len, sp, nslots)
+        return dev.get(qh), kc.cpu().numpy(), vc.cpu().numpy()
+
+    got, want = run(True), run(False)
+    for name, a, b in zip(("queries", "keys", "values"), got, want):
+        np.testing.assert_array_equal(a, b, err_msg=name)
+    assert np.count_nonzero(want[1]) > 0 and np.count_nonzero(want[2]) > 0
+    wd.free()
+
+
 ATTENTION = [(128, 8, 2, 70), (64, 4, 2, 300), (128, 32, 8, 640),
              (64, 2, 1, 2100),  # past the values pass's LDS chunk and the softmax's
              (32, 8, 1, 95), (96, 4, 4, 130)]

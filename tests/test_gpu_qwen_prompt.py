@@ -104,13 +104,27 @@ def check_block_sampled(model, om, orc, prompt, layer):
     def dev(t):
         return t[:M].cpu().numpy().copy()
 
-    qkv, set_q, set_s, attn = dev(model.qkv), dev(model.set8.q), dev(model.set8.s), dev(model.attn)
+    set_q, set_s, attn = dev(model.set8.q), dev(model.set8.s), dev(model.attn)
     mid_q, mid_s, ffn = dev(model.mid8.q), dev(model.mid8.s), dev(model.ffn)
     kc, vc = model.kc[layer].cpu().numpy(), model.vc[layer].cpu().numpy()
     # the Gate|Up floats of the device's own pre-norm (the block hands SwiGLU's
     # Q8_0 on from the product's epilogue without them)
     model._mm(model.blocks[layer]["gu"], model.x8, M, model.gu, 2 * cfg.ffn)
     x8_q, x8_s, gu = dev(model.x8.q), dev(model.x8.s), dev(model.gu)
+    # likewise the Q|K|V floats (the heads' norms, RoPE and cache stores run
+    # in the product's epilogue): the block input's attention pre-norm and
+    # Q8_0 again, then the product alone
+    b = model.blocks[layer]
+    xd = torch.from_numpy(np.ascontiguousarray(xin)).cuda()
+    aq = torch.empty((M, cfg.dim), dtype=torch.int8, device="cuda")
+    asc = torch.empty((M, cfg.dim // 32), dtype=torch.float32, device="cuda")
+    aqs = torch.empty((M, cfg.dim // 32), dtype=torch.int32, device="cuda")
+    capi.call("gx_norm_quant", model.ctx.ptr, capi.vp(xd), cfg.dim, None, cfg.dim, capi.vp(b["attn_norm"]), M,
+              cfg.dim, np.float32(cfg.eps), None, 0, capi.vp(aq), capi.vp(asc), capi.vp(aqs))
+    qkv_d = torch.empty((M, model.qd + 2 * model.kvd), dtype=torch.float32, device="cuda")
+    capi.call("gx_matmul_q4_0", model.ctx.ptr, b["qkv"].ptr, capi.vp(aq), capi.vp(asc), capi.vp(aqs), None, M, 0,
+              model.qd + 2 * model.kvd, None, capi.vp(qkv_d), model.qd + 2 * model.kvd)
+    qkv = qkv_d.cpu().numpy()
 
     def rel(got, want):
         return max(orc.compare_floats(got[i], want[i])[0] for i in range(len(want)))
