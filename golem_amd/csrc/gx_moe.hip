@@ -83,7 +83,9 @@ __device__ __forceinline__ float dot_f32_avx2_combine(float acc) {
 // (rank_key).  A NaN is taken only as the first logit not yet chosen (no
 // comparison with it is ever true); with any NaN present wavefront 0 runs
 // the rounds as golem does.  Weights: exp(l - top) in float64 of the float32
-// difference, rounded to float32, summed in slot order, divided by the sum.
+// difference, rounded to float32 (exp_neg: bit for bit that, on every
+// difference this can be, <= 0 or NaN), summed in slot order, divided by the
+// sum -- in wavefront 0's registers, the sum's terms by shuffles.
 //
 // The caller stages the logits in LDS first (stage_logits): lg holds them
 // as floats and comp their keys, both padded to a multiple of 32 (keys 0,
@@ -114,7 +116,7 @@ __device__ __forceinline__ bool stage_logits(int E, float *lg, uint64_t *comp, L
 }
 
 __device__ void choose_experts(const float *lg, const uint64_t *comp, bool any_nan, int E, int k, float *sel_l,
-                               int32_t *sel_i, float *wv, int32_t *__restrict__ ids, float *__restrict__ weights) {
+                               int32_t *sel_i, int32_t *__restrict__ ids, float *__restrict__ weights) {
     const int tid = threadIdx.x, nt = blockDim.x;
     if (!any_nan) {
         // Two threads a logit when the workgroup has them (adjacent lanes,
@@ -196,16 +198,15 @@ __device__ void choose_experts(const float *lg, const uint64_t *comp, bool any_n
         }
     }
     __syncthreads();
-    if (tid < k) {
-        ids[tid] = sel_i[tid];
-        wv[tid] = (float)exp((double)(sel_l[tid] - sel_l[0]));
-    }
-    __syncthreads();
-    if (tid < k) {
+    if (tid < 64) {
+        const float e = exp_neg(sel_l[min(tid, k - 1)] - sel_l[0]);
         float total = 0.0f;
         for (int j = 0; j < k; j++)
-            total += wv[j];
-        weights[tid] = wv[tid] / total;
+            total += __shfl(e, j, 64);
+        if (tid < k) {
+            ids[tid] = sel_i[tid];
+            weights[tid] = e / total;
+        }
     }
 }
 
@@ -219,7 +220,7 @@ __global__ __launch_bounds__(kLogitsThreads) void moe_route_one_kernel(
     __shared__ double red[kLogitsThreads];
     __shared__ float scale_sh;
     __shared__ int last_sh;
-    __shared__ float sel_l[kTopkMax], wv[kTopkMax];
+    __shared__ float sel_l[kTopkMax];
     __shared__ int32_t sel_i[kTopkMax];
     const int tid = threadIdx.x, e = blockIdx.x, t = blockIdx.y;
     const int E32 = (E + 31) & ~31;
@@ -320,7 +321,7 @@ __global__ __launch_bounds__(kLogitsThreads) void moe_route_one_kernel(
     const bool any_nan = stage_logits(E, xr, comp, [&](int i) {
         return __hip_atomic_load(lt + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     });
-    choose_experts(xr, comp, any_nan, E, k, sel_l, sel_i, wv, ids + (size_t)t * k, weights + (size_t)t * k);
+    choose_experts(xr, comp, any_nan, E, k, sel_l, sel_i, ids + (size_t)t * k, weights + (size_t)t * k);
 }
 
 // Many positions: the norm scales first, one wavefront a position
@@ -495,12 +496,12 @@ __global__ __launch_bounds__(256) void moe_topk_kernel(const float *__restrict__
                                                        int32_t *__restrict__ ids, float *__restrict__ weights) {
     __shared__ __align__(16) float lg[64 * kTopkMaxPerLane];
     __shared__ __align__(16) uint64_t comp[64 * kTopkMaxPerLane];
-    __shared__ float sel_l[kTopkMax], wv[kTopkMax];
+    __shared__ float sel_l[kTopkMax];
     __shared__ int32_t sel_i[kTopkMax];
     const int t = blockIdx.x;
     const float *lt = logits + (size_t)t * E;
     const bool any_nan = stage_logits(E, lg, comp, [&](int i) { return lt[i]; });
-    choose_experts(lg, comp, any_nan, E, k, sel_l, sel_i, wv, ids + (size_t)t * k, weights + (size_t)t * k);
+    choose_experts(lg, comp, any_nan, E, k, sel_l, sel_i, ids + (size_t)t * k, weights + (size_t)t * k);
 }
 
 // mid = GELUTable(gate) * up for the 32 values of one Q8_0 block, one value a
