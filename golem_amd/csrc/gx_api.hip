@@ -189,12 +189,10 @@ int gx_init(int device, gx_ctx **out) {
     ctx->argmax_v = nullptr;
     ctx->argmax_i = nullptr;
     ctx->scratch = nullptr;
-    ctx->route_count = nullptr;
     ctx->route_scale = nullptr;
     ctx->rows = new gx_rows();
     auto undo = [ctx]() {
         rows_release(ctx->rows);
-        (void)hipFree(ctx->route_count);
         (void)hipFree(ctx->route_scale);
         (void)hipFree(ctx->gelu_table);
         (void)hipFree(ctx->argmax_v);
@@ -212,11 +210,9 @@ int gx_init(int device, gx_ctx **out) {
         undo();
         return gx::fail(GX_ERR_NOMEM, "gx: cannot allocate the greedy pick's workspace");
     }
-    if (hipMalloc(&ctx->route_count, kRouteMaxPos * sizeof(unsigned)) != hipSuccess ||
-        hipMemset(ctx->route_count, 0, kRouteMaxPos * sizeof(unsigned)) != hipSuccess ||
-        hipMalloc(&ctx->route_scale, kRouteScaleMax * sizeof(float)) != hipSuccess) {
+    if (hipMalloc(&ctx->route_scale, kRouteScaleMax * sizeof(float)) != hipSuccess) {
         undo();
-        return gx::fail(GX_ERR_NOMEM, "gx: cannot allocate the router's counters");
+        return gx::fail(GX_ERR_NOMEM, "gx: cannot allocate the router's scales");
     }
     {
         // this device's address of the static scratch (the device is current)
@@ -249,7 +245,6 @@ int gx_free(gx_ctx *ctx) {
     (void)hipFree(ctx->gelu_table);
     (void)hipFree(ctx->argmax_v);
     (void)hipFree(ctx->argmax_i);
-    (void)hipFree(ctx->route_count);
     (void)hipFree(ctx->route_scale);
     rows_release(ctx->rows);
     delete ctx;

@@ -64,7 +64,6 @@ struct gx_ctx {
     float *argmax_v;    // the greedy pick's part maxima [kArgmaxRows][kArgmaxParts]
     int32_t *argmax_i;  // and their indices
     uint8_t *scratch;   // this device's copy of the no-alloc entry points' static scratch (gx_api.hip)
-    unsigned *route_count;  // the one-launch router's per-position counters [kRouteMaxPos], zero between calls
     float *route_scale;     // the many-position router's norm scales [kRouteScaleMax]
     struct gx_rows *rows;   // the coalesced MatVecRows products (gx_api.hip)
 };
@@ -72,7 +71,7 @@ struct gx_ctx {
 
 constexpr int kArgmaxParts = 128;  // workgroups per row of the greedy pick
 constexpr int kArgmaxRows = 64;    // rows per launch pair
-constexpr int kRouteMaxPos = 4;    // positions routed by the one-launch router kernel
+constexpr int kRouteMaxPos = 4;    // positions routed by the few-position router kernel
 constexpr int kRouteScaleMax = 4096;  // positions of one many-position router pass
 
 struct gx_weight {

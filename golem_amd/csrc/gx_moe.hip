@@ -43,10 +43,11 @@ namespace {
 //   moe_route_one_kernel: one workgroup per (expert, position) for few
 //     positions (decode), where the cost is latency: the row and the input
 //     are read with every load issued at once, the products are formed by
-//     all threads into LDS, and 32 lanes run the chains.
-//     The workgroup that finishes a position's last logit (a counter per
-//     position, kept by the context) then chooses its experts, so routing
-//     is one launch.
+//     all threads into LDS, and 32 lanes run the chains.  The choice is a
+//     second launch (moe_topk_kernel): handing the logits to the position's
+//     last workgroup inside the launch (a release count per logit, an
+//     acquire, the logits read back at device scope) cost more than the
+//     launch (config 4 decode 24.6 -> 22.7 us).
 //   moe_norm_scale_kernel + moe_logits_kernel: the norm scales once per
 //     position, then 8 experts x 16 positions per workgroup, a lane one
 //     chain of four positions' logits; rows and inputs pass through LDS 256
@@ -212,20 +213,14 @@ __device__ void choose_experts(const float *lg, const uint64_t *comp, bool any_n
 
 __global__ __launch_bounds__(kLogitsThreads) void moe_route_one_kernel(
     const float *__restrict__ router, int D, int E, const float *__restrict__ router_scale,
-    const float *__restrict__ resid, int ldr, float eps, int k, float *__restrict__ logits,
-    int32_t *__restrict__ ids, float *__restrict__ weights, unsigned *__restrict__ count) {
-    // LDS: the input [max(D, E32)], then the products [D] in element order
-    // (later the logits' keys [E32] as uint64)
+    const float *__restrict__ resid, int ldr, float eps, float *__restrict__ logits) {
+    // LDS: the input [D], then the products [D] in element order
     extern __shared__ __align__(16) float lds[];
     __shared__ double red[kLogitsThreads];
     __shared__ float scale_sh;
-    __shared__ int last_sh;
-    __shared__ float sel_l[kTopkMax];
-    __shared__ int32_t sel_i[kTopkMax];
     const int tid = threadIdx.x, e = blockIdx.x, t = blockIdx.y;
-    const int E32 = (E + 31) & ~31;
     float *xr = lds;
-    float *P = lds + max(D, E32);
+    float *P = lds + D;
     const float *rg = router + (size_t)e * D;
     const float *xg = resid + (size_t)t * ldr;
     const int n4 = D / 4;
@@ -299,29 +294,9 @@ __global__ __launch_bounds__(kLogitsThreads) void moe_route_one_kernel(
                 a[u] = b[u];
         }
         const float logit = dot_f32_avx2_combine(acc);
-        if (tid == 0) {
-            // The logit is stored at device scope, then counted with a
-            // device-scope release: the counter's increments form a release
-            // sequence, so the workgroup that takes the last count (and
-            // issues the acquire below) sees every logit.  The counter wraps
-            // to 0 on the position's last count, ready for the next launch.
-            __hip_atomic_store(logits + (size_t)t * E + e, logit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            last_sh = __builtin_amdgcn_atomic_inc32(count + t, (unsigned)(E - 1), __ATOMIC_RELEASE, "agent") ==
-                      (unsigned)(E - 1);
-        }
+        if (tid == 0)
+            logits[(size_t)t * E + e] = logit;
     }
-    __syncthreads();
-    if (!last_sh)
-        return;
-    // The position's last logit: the acquire pairs with every workgroup's
-    // release of its count; the logits are read at device scope.
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    const float *lt = logits + (size_t)t * E;
-    uint64_t *comp = (uint64_t *)P;  // the products are spent
-    const bool any_nan = stage_logits(E, xr, comp, [&](int i) {
-        return __hip_atomic_load(lt + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    });
-    choose_experts(xr, comp, any_nan, E, k, sel_l, sel_i, ids + (size_t)t * k, weights + (size_t)t * k);
 }
 
 // Many positions: the norm scales first, one wavefront a position
@@ -1417,12 +1392,14 @@ int launch_moe_route(gx_ctx *ctx, const gx_weight *router, const float *router_s
     GX_CHECK(((uintptr_t)resid & 15) == 0 && ldr % 4 == 0, "gx: resid must be 16-byte aligned with ldr %% 4 == 0");
     const float *rw = (const float *)router->dev;
     if (M <= kRouteMaxPos && D <= kLogitsOneMaxD) {
-        const size_t E32 = (size_t)((E + 31) & ~31);
-        const size_t lds = sizeof(float) * (max((size_t)D, E32) + max((size_t)D, 2 * E32));
-        GX_CHECK(lds <= 64 * 1024, "gx: the router's %d inputs do not fit the one-launch kernel", D);
+        const size_t lds = sizeof(float) * 2 * (size_t)D;
+        GX_CHECK(lds <= 64 * 1024, "gx: the router's %d inputs do not fit the few-position kernel", D);
         moe_route_one_kernel<<<dim3((unsigned)E, (unsigned)M), kLogitsThreads, lds, ctx->stream>>>(
-            rw, D, E, router_scale, resid, ldr, eps, k, logits, ids, weights, ctx->route_count);
-        return check_launch("moe_route_one");
+            rw, D, E, router_scale, resid, ldr, eps, logits);
+        if (int rc = check_launch("moe_route_one"))
+            return rc;
+        moe_topk_kernel<<<M, E <= 64 ? 64 : E <= 128 ? 128 : 256, 0, ctx->stream>>>(logits, E, k, ids, weights);
+        return check_launch("moe_topk");
     }
     // Positions in runs of at most kRouteScaleMax (the context's scales).
     for (int m0 = 0; m0 < M; m0 += kRouteScaleMax) {

@@ -345,11 +345,10 @@ def test_expert_integers_bit_exact(dev, orc, M, spread):
         np.testing.assert_array_equal(ddn[u], acc - 8 * ub.qsum_rows()[0][None, :], err_msg=f"down unit {u}")
 
 
-def test_route_one_launch_repeats(dev, orc):
-    """The one-launch router (at most four positions) counts each position's
-    logits in the context and the last workgroup chooses; the counter wraps
-    to zero for the next call.  Consecutive calls of 1..4 positions, each
-    bit for bit against the oracle."""
+def test_route_few_positions_repeats(dev, orc):
+    """The few-position router (at most four positions: a workgroup per
+    logit, then the choice): consecutive calls of 1..4 positions, each bit
+    for bit against the oracle."""
     D, E, k = 2816, 128, 8
     m = Moe.__new__(Moe)
     g = synth.rng(77)
@@ -368,7 +367,7 @@ def test_route_one_launch_repeats(dev, orc):
 
 
 def test_decode_graph_replays_match_eager(dev, orc):
-    """Config 4's decode (route + experts, three launches) captured once into
+    """Config 4's decode (route + experts, four launches) captured once into
     a HIP graph and replayed on new inputs, with eager work and
     synchronisations between the replays: every replay's output bit-identical
     to the eager call's, which is within 2e-5 of RMS of golem."""
