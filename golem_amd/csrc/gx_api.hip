@@ -857,8 +857,9 @@ int gx_qwen_qkv_rope(gx_ctx *ctx, const gx_weight *w, const int8_t *q, const flo
     GX_CHECK(!slots || nslots > 0, "gx: %d slots", nslots);
     if (M == 0)
         return ok();
+    // (the epilogue stores the queries and keys 16 bytes at a time)
     const bool fused = M > 16 && (head_dim == 64 || head_dim == 128) &&
-                       (((uintptr_t)rope_cos | (uintptr_t)rope_sin) & 15) == 0;
+                       (((uintptr_t)rope_cos | (uintptr_t)rope_sin | (uintptr_t)qh | (uintptr_t)kcache) & 15) == 0;
     if (fused) {
         const gx::QkvRopeArgs a{positions, q_norm, k_norm, rope_cos, rope_sin, eps,  qh,
                                 kcache,    vcache, context, heads, kv_heads, head_dim, slots, nslots};

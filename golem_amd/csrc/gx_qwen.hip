@@ -2149,7 +2149,9 @@ int launch_qwen_qk_rope(gx_ctx *ctx, const float *qkv, int ldqkv, int M, int hea
              kHeadMax);
     // A batch (and a head width the tiled kernel is built for, operands it
     // can read 16 bytes at a time): 64 tokens of a head a workgroup.
-    const bool aligned = (((uintptr_t)qkv | (uintptr_t)rope_cos | (uintptr_t)rope_sin) & 15) == 0 && ldqkv % 4 == 0;
+    const bool aligned =
+        (((uintptr_t)qkv | (uintptr_t)rope_cos | (uintptr_t)rope_sin | (uintptr_t)qh | (uintptr_t)kcache) & 15) == 0 &&
+        ldqkv % 4 == 0;
     if (M >= 32 && (hd == 64 || hd == 128) && aligned) {
         const dim3 grid((unsigned)((M + kQkTok - 1) / kQkTok), (unsigned)(heads + kv_heads));
         if (hd == 64)

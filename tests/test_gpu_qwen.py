@@ -302,6 +302,45 @@ def test_qkv_rope_matches_product_then_heads(dev, hd, heads, kv, K, M, slots):
     wd.free()
 
 
+def test_qkv_rope_unaligned_queries(dev):
+    """Queries 2 bytes off a 16-byte boundary: gx_qwen_qkv_rope and
+    gx_qwen_qk_rope take their element-store paths (the tiled and epilogue
+    forms store 16 bytes at a time) and still agree bit for bit."""
+    hd, heads, kv, K, M = 128, 4, 2, 256, 40
+    g = synth.rng(97)
+    rows = (heads + 2 * kv) * hd
+    ctx_len = 64
+    wd = dev.weight(synth.q4_0_weights(g, rows, K), capi.Q4_0, rows, K)
+    xq, xs, xqs, _, _ = dev.quantize_q8_0(synth.activations(g, M, K))
+    cos, sin = rope_tables(hd, ctx_len, 1e6)
+    qn = (1 + 0.02 * g.standard_normal(hd)).astype(np.float32)
+    kn = (1 + 0.02 * g.standard_normal(hd)).astype(np.float32)
+    pos = g.permutation(ctx_len)[:M].astype(np.int32)
+    ins = [dev.put(a) for a in (pos, qn, kn, cos, sin)]
+    outs = []
+    for fused in (True, False):
+        qbuf = dev.full((M * heads * hd + 8,), 0x1234, np.int16)
+        qh = qbuf[1:1 + M * heads * hd]  # 2 bytes past the allocation's 256-byte alignment
+        kc = torch.zeros((kv, hd // 8, ctx_len, 8), dtype=torch.int16, device="cuda")
+        vc = torch.zeros((kv, hd, ctx_len), dtype=torch.int16, device="cuda")
+        qkv = dev.empty((M, rows), np.float32)
+        if fused:
+            capi.call("gx_qwen_qkv_rope", dev.ctx.ptr, wd.ptr, capi.vp(xq), capi.vp(xs), capi.vp(xqs), M, heads, kv,
+                      hd, capi.vp(ins[0]), capi.vp(ins[1]), capi.vp(ins[2]), capi.vp(ins[3]), capi.vp(ins[4]),
+                      np.float32(1e-6), capi.vp(qh), capi.vp(kc), capi.vp(vc), ctx_len, None, 0, capi.vp(qkv))
+        else:
+            capi.call("gx_matmul_q4_0", dev.ctx.ptr, wd.ptr, capi.vp(xq), capi.vp(xs), capi.vp(xqs), None, M, 0,
+                      rows, None, capi.vp(qkv), rows)
+            capi.call("gx_qwen_qk_rope", dev.ctx.ptr, capi.vp(qkv), rows, M, heads, kv, hd, capi.vp(ins[0]),
+                      capi.vp(ins[1]), capi.vp(ins[2]), capi.vp(ins[3]), capi.vp(ins[4]), np.float32(1e-6),
+                      capi.vp(qh), capi.vp(kc), capi.vp(vc), ctx_len, None, 0)
+        outs.append((dev.get(qbuf), kc.cpu().numpy(), vc.cpu().numpy()))
+    for a, b in zip(*outs):
+        np.testing.assert_array_equal(a, b)
+    assert outs[0][0][0] == 0x1234 and np.all(outs[0][0][1 + M * heads * hd:] == 0x1234)  # nothing outside written
+    wd.free()
+
+
 ATTENTION = [(128, 8, 2, 70), (64, 4, 2, 300), (128, 32, 8, 640),
              (64, 2, 1, 2100),  # past the values pass's LDS chunk and the softmax's
              (32, 8, 1, 95), (96, 4, 4, 130)]
