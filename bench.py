@@ -69,7 +69,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only; --gpus {args.gpus} is not supported by this build "
-              "(the path shards by output rows; see DESIGN.md)", file=sys.stderr)
+              "(the products would shard by output rows, one shard a GPU)", file=sys.stderr)
         sys.exit(2)
 
     import torch

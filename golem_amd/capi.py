@@ -1,8 +1,8 @@
 """ctypes binding of the C ABI in include/golem_hip.h.
 
 This is how Python (the tests, bench.py, smoke) reaches the HIP library; a Go
-caller reaches the same entry points through the cgo shim shown in
-INTEGRATION.md.  Device pointers are passed as integers (for instance a torch
+caller reaches the same entry points through a cgo shim over the same
+header.  Device pointers are passed as integers (for instance a torch
 tensor's data_ptr()); the library itself never sees a torch type.
 
 Loading fails loudly when libgolem_hip.so is missing: there is no CPU
