@@ -244,6 +244,7 @@ def test_qk_rope_and_cache_bit_exact(dev, orc, hd, heads, kv, M):
 
 @pytest.mark.parametrize("hd,heads,kv,K,M,slots", [
     (128, 32, 8, 2560, 512, False),  # config 3 at its prompt length
+    (128, 32, 8, 2560, 1040, True),  # 33 token groups (a ragged last one), slots
     (128, 8, 2, 512, 70, False),     # a ragged last token group, out-of-order and unplaced positions
     (64, 4, 2, 256, 40, True),       # two heads a workgroup; slots, one out of range
     (64, 2, 1, 256, 17, False),      # one workgroup of a query and a query head, one of a key and a value
