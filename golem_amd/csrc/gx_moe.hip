@@ -1034,8 +1034,9 @@ __global__ __launch_bounds__(256) void moe_gelu_mul_f32_kernel(float *__restrict
 // expert's first place, plus that expert's units in earlier chunks (a
 // running count), in earlier wavefronts of this chunk (per-wavefront counts
 // summed in wavefront order), and in lower lanes of its own wavefront (its
-// rank, from the wavefront's 64 ids in LDS).  Counting with LDS atomics is
-// order-free, so the places do not depend on scheduling.
+// rank, from a ballot match).  The experts' totals are counted with LDS
+// atomics, which are order-free, and the wavefront counts written by one lane
+// each, so the places do not depend on scheduling.
 constexpr int kSortThreads = 1024;
 constexpr int kSortWaves = kSortThreads / 64;
 constexpr int kSortHeld = 4;  // ids a thread keeps in registers (U <= 4096 read once)
@@ -1068,16 +1069,31 @@ __device__ __forceinline__ void scan2_exclusive(int a, int b, int &ea, int &eb, 
     __syncthreads();
 }
 
+// This lane's rank among the lower lanes of its wavefront that hold the same
+// expert e, and in count how many lanes hold it (for valid lanes; every lane
+// of the wavefront calls it): a ballot on each of e's nb low bits keeps the
+// lanes that agree with it on that bit.
+__device__ __forceinline__ int wave_match_rank(int e, bool valid, int nb, int &count) {
+    uint64_t peers = __ballot(valid);
+    for (int b = 0; b < nb; b++) {
+        const bool bit = (e >> b) & 1;
+        const uint64_t set = __ballot(bit);
+        peers &= bit ? set : ~set;
+    }
+    count = __popcll(peers);
+    return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(peers >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)peers, 0u));
+}
+
 __global__ __launch_bounds__(kSortThreads) void moe_sort_kernel(const int32_t *__restrict__ ids, int U, int E,
                                                                 int tile, int max_items,
                                                                 int32_t *__restrict__ sorted,
                                                                 int32_t *__restrict__ work) {
-    // LDS: the chunk's ids [kSortThreads] (16-byte aligned), first[E],
-    // run[E], cnt[kSortWaves][E]
+    // LDS: first[E], run[E], cnt[kSortWaves][E]
     extern __shared__ __align__(16) int32_t sh[];
     __shared__ int32_t tmp[2 * kSortWaves];
-    int32_t *chunk = sh, *first = sh + kSortThreads, *run = first + E, *cnt = run + E;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    int32_t *first = sh, *run = first + E, *cnt = run + E;
+    const int tid = threadIdx.x, wave = tid >> 6;
+    const int nb = E > 1 ? 32 - __clz(E - 1) : 0;
     for (int e = tid; e < E; e += kSortThreads)
         run[e] = 0;
     for (int i = tid; i < 4 * max_items; i += kSortThreads)
@@ -1127,23 +1143,15 @@ __global__ __launch_bounds__(kSortThreads) void moe_sort_kernel(const int32_t *_
         const bool valid = e >= 0 && e < E;
         if (!valid)
             e = -1;
-        chunk[tid] = e;
         for (int i = tid; i < kSortWaves * E; i += kSortThreads)
             cnt[i] = 0;
+        // this unit's rank among the lanes below it with the same expert;
+        // the highest of them writes the wavefront's count of the expert
+        int count;
+        const int r = wave_match_rank(e, valid, nb, count);
         __syncthreads();
-        // this unit's rank among the lanes below it with the same expert
-        const int4 *cw = (const int4 *)(chunk + 64 * wave);
-        int r = 0;
-#pragma unroll
-        for (int q = 0; q < 16; q++) {
-            const int4 c4 = cw[q];
-            r += (int)((c4.x == e) & (4 * q + 0 < lane));
-            r += (int)((c4.y == e) & (4 * q + 1 < lane));
-            r += (int)((c4.z == e) & (4 * q + 2 < lane));
-            r += (int)((c4.w == e) & (4 * q + 3 < lane));
-        }
-        if (valid)
-            atomicAdd(&cnt[wave * E + e], 1);
+        if (valid && r == count - 1)
+            cnt[wave * E + e] = count;
         __syncthreads();
         // per expert: the running count before each wavefront of the chunk
         for (int x = tid; x < E; x += kSortThreads) {
@@ -1163,112 +1171,121 @@ __global__ __launch_bounds__(kSortThreads) void moe_sort_kernel(const int32_t *_
 }
 
 // The same stable counting sort in one pass, for at most kSortSmallC chunks
-// of kSortThreads units and E * kSortSmallC * kSortWaves counters in LDS (a
-// prompt's units at a time), run by workgroup 0 of moe_sort_quant_kernel:
-// unit u = tid + kSortThreads c is counted in its (chunk, wavefront) group's
-// counter of its expert and ranked among the group's lower lanes; each
-// expert's counters are then prefixed in (chunk, wavefront) order by eight
-// lanes at once and the experts' first places and items by one scan, so a
-// unit's place first[e] + (earlier groups' count) + rank is the one the
-// chunked kernel above gives it: units of an expert in unit order.
+// of kSortThreads units over at most kSortThreads / 8 experts (a prompt's
+// units at a time), run by workgroup 0 of moe_sort_quant_kernel.  Unit
+// u = tid + kSortThreads c belongs to group g = kSortWaves c + wave (its
+// wavefront's 64 units of chunk c, groups in unit order).  Its rank among
+// the group's lower lanes with the same expert comes from wave_match_rank,
+// and the highest such lane writes the group's count of the expert, so no
+// counter is shared.  Thread t = j E + e (j < 8) then prefixes expert e's
+// counts over its 2C groups from j 2C (group-major counters: consecutive
+// banks across a wavefront) and records their sum; after a barrier it adds
+// the lower j's sums while wavefront 0 scans the experts' totals into their
+// first places and work items.  A unit's place first[e] + (earlier groups'
+// count) + rank is the one the chunked kernel above gives it: units of an
+// expert in unit order.
 constexpr int kSortSmallC = 4;
-constexpr int kSortSmallCounters = 8192;
+constexpr int kSortSmallCounters = kSortSmallC * kSortWaves * (kSortThreads / 8);
 
 __host__ __device__ inline bool sort_small_fits(int U, int E) {
-    const int C = (U + kSortThreads - 1) / kSortThreads;
-    return C <= kSortSmallC && E <= kSortThreads / 8 && C * kSortWaves * E <= kSortSmallCounters;
+    return U <= kSortSmallC * kSortThreads && E <= kSortThreads / 8;
 }
 
+// LDS ints sort_small uses for E experts.
+__host__ __device__ inline int sort_small_lds_ints(int E) { return kSortSmallCounters + 9 * E; }
+
 __device__ __forceinline__ void sort_small(const int32_t *__restrict__ ids, int U, int E, int tile, int max_items,
-                                           int32_t *__restrict__ sorted, int32_t *__restrict__ work, int32_t *sh,
-                                           int *tmp) {
+                                           int32_t *__restrict__ sorted, int32_t *__restrict__ work, int32_t *sh) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int C = (U + kSortThreads - 1) / kSortThreads, G = C * kSortWaves;  // (chunk, wavefront) groups
-    int32_t *cnt = sh;                                  // [G][E]: counts, then exclusive offsets
-    int32_t *ids_s = sh + kSortSmallCounters;           // [C][kSortThreads] (16-byte aligned)
-    int32_t *first = ids_s + kSortSmallC * kSortThreads;  // [E]
+    const int C = (U + kSortThreads - 1) / kSortThreads, G = C * kSortWaves, per = G / 8;
+    int32_t *cnt = sh;                        // [G][E]: group counts, then places within the expert
+    int32_t *part = sh + kSortSmallCounters;  // [8][E]: each j's sum of counts
+    int32_t *first = part + 8 * E;            // [E]
+    int raw[kSortSmallC];
+#pragma unroll
+    for (int c = 0; c < kSortSmallC; c++) {
+        const int u = tid + kSortThreads * c;
+        raw[c] = c < C && u < U ? ids[u] : -1;
+    }
+    // the clearing overlaps the loads above
     for (int i = tid; i < G * E; i += kSortThreads)
         cnt[i] = 0;
     for (int i = tid; i < 4 * max_items; i += kSortThreads)
         work[i] = 0;
-    int ev[kSortSmallC];
+    const int nb = E > 1 ? 32 - __clz(E - 1) : 0;
+    int ev[kSortSmallC], rank[kSortSmallC], count[kSortSmallC];
 #pragma unroll
     for (int c = 0; c < kSortSmallC; c++) {
-        const int u = tid + kSortThreads * c;
-        int e = c < C && u < U ? ids[u] : -1;
-        e = e >= 0 && e < E ? e : -1;
-        ev[c] = e;
-        if (c < C)
-            ids_s[kSortThreads * c + tid] = e;
-    }
-    __syncthreads();
-    int rank[kSortSmallC];
-#pragma unroll
-    for (int c = 0; c < kSortSmallC; c++) {
+        ev[c] = raw[c] >= 0 && raw[c] < E ? raw[c] : -1;
         rank[c] = 0;
-        if (c < C) {
-            const int e = ev[c];
-            if (e >= 0)
-                atomicAdd(&cnt[(kSortWaves * c + wave) * E + e], 1);
-            // this unit's rank among the lanes below it with the same expert
-            const int4 *cw = (const int4 *)(ids_s + kSortThreads * c + 64 * wave);
-            int r = 0;
-#pragma unroll
-            for (int q = 0; q < 16; q++) {
-                const int4 c4 = cw[q];
-                r += (int)((c4.x == e) & (4 * q + 0 < lane));
-                r += (int)((c4.y == e) & (4 * q + 1 < lane));
-                r += (int)((c4.z == e) & (4 * q + 2 < lane));
-                r += (int)((c4.w == e) & (4 * q + 3 < lane));
-            }
-            rank[c] = r;
-        }
+        count[c] = 0;
+        if (c < C)  // uniform: every lane of the wavefront takes part in the match
+            rank[c] = wave_match_rank(ev[c], ev[c] >= 0, nb, count[c]);
     }
+    __syncthreads();  // the clearing before the counts
+#pragma unroll
+    for (int c = 0; c < kSortSmallC; c++)
+        if (c < C && ev[c] >= 0 && rank[c] == count[c] - 1)
+            cnt[(kSortWaves * c + wave) * E + ev[c]] = count[c];
     __syncthreads();
-    // each expert's groups in order: eight lanes an expert, G / 8 groups a lane
-    // (G is a multiple of 16), a serial prefix then a scan over the eight
-    int total = 0;
-    {
-        const int e = tid >> 3, j = tid & 7, per = G >> 3;
+    const int e8 = tid % E, j8 = tid / E;  // j8 < 8: thread t = j E + e walks expert e's groups from j 2C
+    int excl[2 * kSortSmallC];
+    if (j8 < 8) {
+        int v[2 * kSortSmallC];
+#pragma unroll
+        for (int i = 0; i < 2 * kSortSmallC; i++)
+            v[i] = i < per ? cnt[(j8 * per + i) * E + e8] : 0;
         int run = 0;
-        if (e < E) {
-            for (int i = 0; i < per; i++) {
-                const int at = (j * per + i) * E + e;
-                const int v = cnt[at];
-                cnt[at] = run;
-                run += v;
+#pragma unroll
+        for (int i = 0; i < 2 * kSortSmallC; i++) {
+            excl[i] = run;
+            run += v[i];
+        }
+        part[j8 * E + e8] = run;
+    }
+    __syncthreads();
+    if (j8 < 8) {
+        int before = 0;
+        for (int jj = 0; jj < j8; jj++)
+            before += part[jj * E + e8];
+#pragma unroll
+        for (int i = 0; i < 2 * kSortSmallC; i++)
+            if (i < per)
+                cnt[(j8 * per + i) * E + e8] = before + excl[i];
+    }
+    if (wave == 0) {
+        // experts 2 lane and 2 lane + 1 (E <= 128): totals, then their first
+        // places and first items by an inclusive scan over the lanes
+        const int ea = 2 * lane, eb = ea + 1;
+        int ta = 0, tb = 0;
+#pragma unroll
+        for (int jj = 0; jj < 8; jj++) {
+            ta += ea < E ? part[jj * E + ea] : 0;
+            tb += eb < E ? part[jj * E + eb] : 0;
+        }
+        const int na = (ta + tile - 1) / tile, nb2 = (tb + tile - 1) / tile;
+        int ic = ta + tb, in = na + nb2;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const int uc = __shfl_up(ic, d, 64), un = __shfl_up(in, d, 64);
+            if (lane >= d) {
+                ic += uc;
+                in += un;
             }
         }
-        int inc = run;
-#pragma unroll
-        for (int d = 1; d < 8; d <<= 1) {
-            const int o = __shfl_up(inc, d, 8);
-            if (j >= d)
-                inc += o;
-        }
-        const int before = inc - run;  // this lane's groups start after the lower lanes'
-        if (e < E) {
-            for (int i = 0; i < per; i++)
-                cnt[(j * per + i) * E + e] += before;
-        }
-        total = __shfl(inc, 7, 8);  // the expert's count, in each of its eight lanes
-    }
-    // the experts' totals to thread e (through first[], overwritten below
-    // after the scan's barriers), then their first places and first items
-    if ((tid & 7) == 0 && (tid >> 3) < E)
-        first[tid >> 3] = total;
-    __syncthreads();
-    const int ce = tid < E ? first[tid] : 0;
-    const int ni = (ce + tile - 1) / tile;
-    int fp, fi;
-    scan2_exclusive(ce, ni, fp, fi, tmp);
-    if (tid < E) {
-        first[tid] = fp;
-        for (int f = 0; f < ni && fi + f < max_items; f++) {
-            work[4 * (fi + f)] = tid;
-            work[4 * (fi + f) + 1] = fp + f * tile;
-            work[4 * (fi + f) + 2] = min(tile, ce - f * tile);
-        }
+        const int fa = ic - ta - tb, fia = in - na - nb2;
+        auto items = [&](int e, int fp, int fi, int ce, int ni) {
+            first[e] = fp;
+            for (int f = 0; f < ni && fi + f < max_items; f++) {
+                work[4 * (fi + f)] = e;
+                work[4 * (fi + f) + 1] = fp + f * tile;
+                work[4 * (fi + f) + 2] = min(tile, ce - f * tile);
+            }
+        };
+        if (ea < E)
+            items(ea, fa, fia, ta, na);
+        if (eb < E)
+            items(eb, fa + ta, fia + na, tb, nb2);
     }
     __syncthreads();
 #pragma unroll
@@ -1288,9 +1305,8 @@ __global__ __launch_bounds__(kSortThreads) void moe_sort_quant_kernel(
     int32_t *__restrict__ work, const float *__restrict__ x, int ldx, int M, int D, int8_t *__restrict__ q,
     float *__restrict__ scales, int32_t *__restrict__ qsum) {
     extern __shared__ __align__(16) int32_t sort_sh[];
-    __shared__ int tmp[2 * kSortWaves];
     if (blockIdx.x == 0) {
-        sort_small(ids, U, E, tile, max_items, sorted, work, sort_sh, tmp);
+        sort_small(ids, U, E, tile, max_items, sorted, work, sort_sh);
         return;
     }
     const size_t i4 = (size_t)(blockIdx.x - 1) * kSortThreads + threadIdx.x;
@@ -1454,7 +1470,7 @@ bool launch_sort_quant(gx_ctx *ctx, const int32_t *ids, int U, int E, const MoeS
                        int32_t *work, const float *x, int ldx, int M, int D, int8_t *xq, float *xs, int32_t *xqs) {
     if (!sort_small_fits(U, E) || ((uintptr_t)x & 15) != 0 || ldx % 4 != 0 || D % 32 != 0)
         return false;
-    const size_t lds = (size_t)(kSortSmallCounters + kSortSmallC * kSortThreads + E) * sizeof(int32_t);
+    const size_t lds = (size_t)sort_small_lds_ints(E) * sizeof(int32_t);
     const size_t n4 = (size_t)M * D / 4;
     const unsigned grid = 1 + (unsigned)((n4 + kSortThreads - 1) / kSortThreads);
     moe_sort_quant_kernel<<<grid, kSortThreads, lds, ctx->stream>>>(ids, U, E, kGroupTok, s.max_items, sorted, work,
@@ -1463,7 +1479,7 @@ bool launch_sort_quant(gx_ctx *ctx, const int32_t *ids, int U, int E, const MoeS
 }
 
 int launch_sort(gx_ctx *ctx, const int32_t *ids, int U, int E, const MoeSpace &s, int32_t *sorted, int32_t *work) {
-    const size_t lds = (size_t)((2 + kSortWaves) * E + kSortThreads) * sizeof(int32_t);
+    const size_t lds = (size_t)(2 + kSortWaves) * E * sizeof(int32_t);
     GX_CHECK(E <= kSortThreads && lds <= 64 * 1024, "gx: %d experts do not fit the sort's LDS", E);
     moe_sort_kernel<<<1, kSortThreads, lds, ctx->stream>>>(ids, U, E, kGroupTok, s.max_items, sorted, work);
     return check_launch("moe_sort");

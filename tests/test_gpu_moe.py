@@ -253,6 +253,88 @@ def test_bad_expert_id_poisons_its_position(dev):
         assert not np.any(np.isnan(out[1:]))
 
 
+def _moe_space(M, k, D, F, E):
+    """Offsets of the sorted units and the work list in gx_moe_experts'
+    workspace (its layout: each region rounded up to 256 bytes)."""
+    U = M * k
+    max_items = E + (U + 31) // 32
+    sizes = [M * D, M * (D // 32) * 4, M * (D // 32) * 4, U * 2 * F * 4, U * F, U * (F // 32) * 4,
+             U * (F // 32) * 4, U * D * 4, U * 4, max_items * 16]
+    offs, at = [], 0
+    for n in sizes:
+        offs.append(at)
+        at += (n + 255) & ~255
+    return offs[8], offs[9], max_items, at
+
+
+@pytest.mark.parametrize("M,k,E,bad,stride", [
+    (256, 8, 128, 0, 0),     # 2,048 units: the one-pass sort, two chunks
+    (512, 8, 128, 7, 0),     # 4,096 units, its largest; ids out of range
+    (5, 2, 16, 1, 0),        # a ragged first chunk
+    (300, 3, 100, 5, 0),     # experts not a power of two
+    (40, 1, 1, 0, 0),        # one expert: no id bits to match
+    (2000, 1, 8, 0, 0),      # almost every unit in one expert: many items
+    (1100, 4, 16, 3, 0),     # 4,400 units: the chunked sort
+    (50, 4, 200, 2, 0),      # 200 experts: the chunked sort
+    (256, 8, 128, 0, 1),     # a row stride of D + 1: the chunked sort
+])
+def test_sort_places_units_stably(dev, M, k, E, bad, stride):
+    """The units the experts' launch sorts (gemma/moe.go:120-141 runs a
+    position's experts in slot order; the grouped product gathers each
+    expert's units): sorted[] holds the valid units expert by expert, each
+    expert's in unit order (numpy's stable argsort), and work[] each expert's
+    items of up to 32 units {expert, first place, count, 0}, then zeros."""
+    import ctypes
+    D, F = 256, 64
+    g = synth.rng(1000 + M + E)
+    if k <= E:
+        ids = np.stack([g.choice(E, k, replace=False) for _ in range(M)]).astype(np.int32)
+    else:
+        ids = g.integers(0, E, (M, k)).astype(np.int32)
+    if M == 2000:
+        ids[:] = 3
+        ids[g.choice(M, 40, replace=False), 0] = g.integers(0, E, 40)
+    flat = ids.reshape(-1)
+    if bad:
+        at = g.choice(flat.size, bad, replace=False)
+        flat[at] = np.where(np.arange(bad) % 2 == 0, -1, E)
+    gu = synth.q4_0_weights(g, E * 2 * F, D)
+    dn = synth.q4_0_weights(g, E * D, F)
+    wgu, wdn = dev.weight(gu, capi.Q4_0, 2 * F, D, count=E), dev.weight(dn, capi.Q4_0, D, F, count=E)
+    x = synth.activations(g, M, D)
+    ld = D + stride
+    xs = np.zeros((M, ld), np.float32)
+    xs[:, :D] = x
+    w = g.uniform(0.05, 0.5, (M, k)).astype(np.float32)
+    n = ctypes.c_size_t()
+    capi.call("gx_moe_workspace_bytes", M, k, D, F, E, ctypes.byref(n))
+    s_off, w_off, max_items, total = _moe_space(M, k, D, F, E)
+    assert total == n.value
+    ws = dev.full((n.value // 4,), -7, np.int32)
+    out = dev.empty((M, D), np.float32)
+    xd, idd, wd = dev.put(xs), dev.put(ids), dev.put(w)  # held until the launch has run
+    capi.call("gx_moe_experts", dev.ctx.ptr, wgu.ptr, wdn.ptr, None, capi.vp(xd), ld, M, k, capi.vp(idd),
+              capi.vp(wd), capi.vp(out), D, capi.vp(ws), n.value)
+    wsh = dev.get(ws).view(np.uint8)
+    valid = (flat >= 0) & (flat < E)
+    want = np.argsort(np.where(valid, flat, E), kind="stable")[:int(valid.sum())].astype(np.int32)
+    got = wsh[s_off:s_off + 4 * flat.size].view(np.int32)[:want.size]
+    np.testing.assert_array_equal(got, want)
+    counts = np.bincount(flat[valid], minlength=E)
+    items, place = [], 0
+    for e in range(E):
+        for f in range(0, counts[e], 32):
+            items.append((e, place + f, min(32, counts[e] - f), 0))
+        place += counts[e]
+    want_w = np.zeros((max_items, 4), np.int32)
+    want_w[:len(items)] = items
+    np.testing.assert_array_equal(wsh[w_off:w_off + 16 * max_items].view(np.int32).reshape(max_items, 4), want_w)
+    wgu.free()
+    wdn.free()
+    log(f"sort: M={M} k={k} E={E} ({flat.size} units, {bad} out of range, stride D+{stride}) stable, "
+        f"{len(items)} items")
+
+
 def test_sort_forms_agree(dev):
     """The grouped path sorts the units by expert in one of two forms: one
     pass inside the launch that quantises the input (at most 4,096 units over
