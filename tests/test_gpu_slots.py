@@ -154,6 +154,48 @@ def test_lock_step_decode_draws_each_conversations_tokens(dev, nconv):
     m.free()
 
 
+@pytest.mark.parametrize("nconv", [3, 6, 8])
+def test_lock_step_hidden_states_equal_each_alone(dev, nconv):
+    """Every step of a lock-step batch gives each conversation, bit for bit,
+    the hidden state the same conversation gets run alone on the device with
+    the same tokens (qwen/model_test.go:78's batch-equals-one-at-a-time, per
+    slot): the products give each column its one-column result and the
+    attention's order does not depend on the launch, so a token routed to
+    another slot's cache or position, or a column crossed with another,
+    shows as a difference in the bits."""
+    cfg = synth.QwenConfig(256, 512, 2, 4, 2, 64, 1024, 16 * nconv)
+    w = synth.qwen_weights(cfg, 85, symmetric=True)
+    g = synth.rng(290 + nconv)
+    prompts = [[int(t) for t in g.integers(0, cfg.vocab, 2 + (5 * i) % 9)] for i in range(nconv)]
+    steps = 5
+    m = QwenModel(dev.ctx, cfg, w, max_batch=16)
+    m.set_slots(nconv)
+    toks = []
+    for i, p in enumerate(prompts):
+        m.use_slot(i)
+        m.forward(p, 0)
+        toks.append(int(m.next_token(len(p) - 1).item()))
+    fed = [[t] for t in toks]
+    pos = [len(p) for p in prompts]
+    hidden = []
+    for _ in range(steps):
+        hidden.append(_bits(m.forward_slots(toks, list(range(nconv)), pos)))
+        toks = [int(t) for t in m.next_tokens(range(nconv)).cpu().tolist()]
+        for i in range(nconv):
+            fed[i].append(toks[i])
+        pos = [p + 1 for p in pos]
+    m.free()
+    solo = QwenModel(dev.ctx, cfg, w, max_batch=16)
+    for i, p in enumerate(prompts):
+        solo.reset()
+        solo.forward(p, 0)
+        for s in range(steps):
+            want = _bits(solo.forward([fed[i][s]], len(p) + s)[0])
+            np.testing.assert_array_equal(hidden[s][i], want, err_msg=f"conversation {i}, step {s}")
+    log(f"  {nconv} conversations: every step's hidden states bit for bit those run alone")
+    solo.free()
+
+
 @pytest.mark.parametrize("nconv", [3, 6])
 def test_captured_slot_steps_match_eager(dev, nconv):
     """slots_step as replays of its captured form (capture_slots): the ids
